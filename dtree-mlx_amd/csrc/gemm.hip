@@ -1,0 +1,386 @@
+// Skinny bf16 GEMM for tree verification: Y[M<=128, N] = X[M, K] * W[N, K]^T.
+//
+// The verify step multiplies ~25 tree rows by every weight matrix of the
+// model, so each launch is a pure weight stream (26 FLOP/B, far under the
+// bf16 MFMA ridge): the design goal is HBM bandwidth, not MFMA throughput.
+//
+// Work split
+//   * An output column tile is 32 weight rows. A workgroup (4 waves) owns one
+//     tile and a K range; its waves interleave 64-wide K blocks so one
+//     iteration of the workgroup reads 512 contiguous bytes of every weight row.
+//   * Lane (c = lane%32, h = lane/32) loads 64 contiguous bytes of weight row
+//     c (K offset 32h within the block) with streaming loads, and the same K
+//     slice of activation row c. Element group j of both operands feeds MFMA j
+//     (v_mfma_f32_32x32x16_bf16), so A and B see the same K permutation and
+//     the 4 MFMAs sum exactly the 64 K values of the block.
+//   * Waves reduce through LDS in a fixed order. With split_k > 1 the K range
+//     is split over workgroups; each writes its partial tile, and the last to
+//     arrive (device-scope counter) sums all partials in split order, so the
+//     result does not depend on arrival order. All splits of a tile are
+//     mapped to one XCD (workgroups go round-robin over the 8 XCDs), so the
+//     partials stay in that XCD's L2.
+//   * Epilogues fuse the RMSNorm row scale (norm weight folded into the
+//     producer's bf16 X), residual add, SwiGLU, and the per-tile sum of
+//     squares the next RMSNorm needs.
+#include "common.h"
+
+namespace dtree {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+
+struct GemmParams {
+  const uint16_t* x; int ldx;
+  const uint16_t* w; int n, k;
+  int S, kb_per_split, ntiles;
+  const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
+  float* out_f32; int ld_out_f32;
+  uint16_t* out_bf16; int ld_out_bf16;
+  const uint16_t* next_norm;
+  float* ss_out;
+  uint16_t* hidden_out; int ld_hidden;
+  float* part; int* counters;
+};
+
+// Partial product of one 32-column tile over K blocks [kb0, kb1) into
+// red[wave][mb*1024 + row*32 + col]; then waves are summed into red[0..].
+template <int MB, int U>
+__device__ __forceinline__ void wg_tile(const uint16_t* __restrict__ x, int ldx,
+                                        const uint16_t* __restrict__ w, int K, int tile, int kb0,
+                                        int kb1, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, h = lane >> 5;
+  f32x16_t acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
+
+  const uint16_t* wp = w + (size_t)(tile * 32 + c) * K + 32 * h;
+  const uint16_t* xp = x + (size_t)c * ldx + 32 * h;
+  int kb = kb0 + wave;
+  for (; kb + kWaves * (U - 1) < kb1; kb += kWaves * U) {
+    u32x4_t wv[U][4];
+    u32x4_t xv[U][MB][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[u][i] = ld_u32x4_stream(wp + (size_t)(kb + kWaves * u) * 64 + 8 * i);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          xv[u][mb][i] = ld_u32x4(xp + (size_t)mb * 32 * ldx + (size_t)(kb + kWaves * u) * 64 + 8 * i);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32(xv[u][mb][i], wv[u][i], acc[mb]);
+  }
+  for (; kb < kb1; kb += kWaves) {
+    u32x4_t wv[4];
+    u32x4_t xv[MB][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wv[i] = ld_u32x4_stream(wp + (size_t)kb * 64 + 8 * i);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[mb][i] = ld_u32x4(xp + (size_t)mb * 32 * ldx + (size_t)kb * 64 + 8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32(xv[mb][i], wv[i], acc[mb]);
+  }
+
+  // Waves 1..3 park their tiles in LDS; wave 0 adds them in wave order, so
+  // the sum is independent of timing, then publishes the tile at red[0..).
+  if (wave > 0) {
+    float* my = red + (wave - 1) * MB * 1024;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) my[mb * 1024 + acc_row(r, h) * 32 + c] = acc[mb][r];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int wv = 0; wv < kWaves - 1; ++wv)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mb][r] += red[wv * MB * 1024 + mb * 1024 + acc_row(r, h) * 32 + c];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[mb * 1024 + acc_row(r, h) * 32 + c] = acc[mb][r];
+  }
+  __syncthreads();
+}
+
+template <int MB>
+__device__ __forceinline__ void row_scale(const float* ss_in, int ss_tiles, float inv_dim, float eps,
+                                          float* rs) {
+  constexpr int MP = MB * 32;
+  if (threadIdx.x < MP) {
+    float v = 1.f;
+    if (ss_in) {
+      float s = 0.f;
+      for (int t = 0; t < ss_tiles; ++t) s += ss_in[t * MP + threadIdx.x];
+      v = rsqrtf(s * inv_dim + eps);
+    }
+    rs[threadIdx.x] = v;
+  }
+}
+
+template <int MB, int U, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
+  constexpr int MP = MB * 32;
+  constexpr int TE = MB * 1024;  // tile elements
+  __shared__ float red[(kWaves - 1) * TE];
+  __shared__ float rs[MP];
+  __shared__ int is_last;
+
+  int tile, s;
+  if (p.S == 1) {
+    tile = blockIdx.x;
+    s = 0;
+  } else {
+    const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+    tile = (j / p.S) * 8 + xcd;
+    s = j % p.S;
+  }
+  if (tile >= p.ntiles) return;
+  const int nkb = p.k >> 6;
+  const int kb0 = s * p.kb_per_split;
+  const int kb1 = min(kb0 + p.kb_per_split, nkb);
+
+  wg_tile<MB, U>(p.x, p.ldx, p.w, p.k, tile, kb0, kb1, red);
+
+  if (p.S > 1) {
+    float* mine = p.part + ((size_t)tile * p.S + s) * TE;
+    for (int e = threadIdx.x; e < TE; e += kThreads) mine[e] = red[e];
+    fence_release();
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = (atomicAdd(&p.counters[tile], 1) == p.S - 1);
+    __syncthreads();
+    if (!is_last) return;
+    fence_acquire();
+    const float* all = p.part + (size_t)tile * p.S * TE;
+    for (int e = threadIdx.x; e < TE; e += kThreads) {
+      float v = 0.f;
+      for (int q = 0; q < p.S; ++q) v += __builtin_nontemporal_load(all + (size_t)q * TE + e);
+      red[e] = v;
+    }
+    if (threadIdx.x == 0) p.counters[tile] = 0;
+  }
+  row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs);
+  __syncthreads();
+
+  if constexpr (EPI == DTREE_EPI_STORE_F32) {
+    for (int e = threadIdx.x; e < TE; e += kThreads) {
+      const int m = e >> 5, n = e & 31;
+      p.out_f32[(size_t)m * p.ld_out_f32 + tile * 32 + n] = red[e] * rs[m];
+    }
+  } else if constexpr (EPI == DTREE_EPI_STORE_BF16) {
+    for (int e = threadIdx.x; e < TE; e += kThreads) {
+      const int m = e >> 5, n = e & 31;
+      p.out_bf16[(size_t)m * p.ld_out_bf16 + tile * 32 + n] = f2bf(red[e] * rs[m]);
+    }
+  } else if constexpr (EPI == DTREE_EPI_RESIDUAL) {
+    // Thread t handles column n = t%32 of rows t/32 + 8i: a row is owned by
+    // 32 consecutive lanes, so its sum of squares is a half-wave butterfly.
+    const int n = threadIdx.x & 31;
+    const int col = tile * 32 + n;
+    const float g = bf2f(p.next_norm[col]);
+    for (int e = threadIdx.x; e < TE; e += kThreads) {
+      const int m = e >> 5;
+      float* xp = p.out_f32 + (size_t)m * p.ld_out_f32 + col;
+      const float xv = *xp + red[e];
+      *xp = xv;
+      p.out_bf16[(size_t)m * p.ld_out_bf16 + col] = f2bf(xv * g);
+      if (p.hidden_out) p.hidden_out[(size_t)m * p.ld_hidden + col] = f2bf(xv);
+      float sq = xv * xv;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+      if (n == 0) p.ss_out[(size_t)tile * MP + m] = sq;
+    }
+  } else if constexpr (EPI == DTREE_EPI_SWIGLU) {
+    for (int e = threadIdx.x; e < MP * 16; e += kThreads) {
+      const int m = e >> 4, j = e & 15;
+      const float gt = red[m * 32 + j] * rs[m];
+      const float up = red[m * 32 + 16 + j] * rs[m];
+      p.out_bf16[(size_t)m * p.ld_out_bf16 + tile * 16 + j] = f2bf(silu_f(gt) * up);
+    }
+  }
+}
+
+// ---- LM head: persistent over vocab tiles, per-row running argmax --------
+struct LmParams {
+  const uint16_t* x; int ldx;
+  const uint16_t* w; int vocab, k;
+  int ntiles;
+  const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
+  float* logits;
+  int2* cand;  // [gridDim.x][MP] (value bits, index)
+};
+
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+template <int MB, int U>
+__global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
+  constexpr int MP = MB * 32;
+  constexpr int TE = MB * 1024;
+  constexpr int IT = TE / kThreads;  // rows handled per thread
+  __shared__ float red[(kWaves - 1) * TE];
+  __shared__ float rs[MP];
+  row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs);
+  float bv[IT];
+  int bi[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    bv[i] = -__builtin_huge_valf();
+    bi[i] = 0x7fffffff;
+  }
+  const int nkb = p.k >> 6;
+  const int n = threadIdx.x & 31;
+  for (int tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
+    __syncthreads();
+    wg_tile<MB, U>(p.x, p.ldx, p.w, p.k, tile, 0, nkb, red);
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int e = threadIdx.x + i * kThreads;
+      const int m = e >> 5;
+      float v = red[e] * rs[m];
+      int idx = tile * 32 + n;
+      if (p.logits) p.logits[(size_t)m * p.vocab + idx] = v;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(v, o);
+        const int oi = __shfl_xor(idx, o);
+        argmax_merge(v, idx, ov, oi);
+      }
+      argmax_merge(bv[i], bi[i], v, idx);
+    }
+  }
+  if (n == 0) {
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int m = (threadIdx.x + i * kThreads) >> 5;
+      p.cand[(size_t)blockIdx.x * MP + m] = make_int2(__float_as_int(bv[i]), bi[i]);
+    }
+  }
+}
+
+int lmhead_grid(int ntiles) { return ntiles < 1024 ? ntiles : 1024; }
+
+static int auto_split(int ntiles, int nkb) {
+  int s = 1;
+  while (s * 2 * ntiles <= 1024 && nkb / (s * 2) >= 4) s *= 2;
+  return s;
+}
+
+template <int MB, int U>
+static void launch_gemm(const GemmParams& p, int epi, int blocks, hipStream_t st) {
+  switch (epi) {
+    case DTREE_EPI_STORE_F32: gemm_kernel<MB, U, DTREE_EPI_STORE_F32><<<blocks, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: gemm_kernel<MB, U, DTREE_EPI_RESIDUAL><<<blocks, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: gemm_kernel<MB, U, DTREE_EPI_SWIGLU><<<blocks, kThreads, 0, st>>>(p); break;
+    default: gemm_kernel<MB, U, DTREE_EPI_STORE_BF16><<<blocks, kThreads, 0, st>>>(p); break;
+  }
+}
+
+}  // namespace dtree
+
+using namespace dtree;
+
+extern "C" size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int split_k) {
+  if (rows_padded <= 0 || n <= 0 || k <= 0) return 0;
+  const int ntiles = n / 32, nkb = k / 64;
+  const int S = split_k > 0 ? split_k : auto_split(ntiles, nkb);
+  const size_t nt8 = (size_t)((ntiles + 7) / 8) * 8;
+  return nt8 * sizeof(int) + (S > 1 ? nt8 * S * (size_t)rows_padded * 32 * sizeof(float) : 0) + 256;
+}
+
+extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
+  DTREE_REQUIRE(a, "gemm: null args");
+  DTREE_REQUIRE(a->x && a->w, "gemm: null x or w");
+  DTREE_REQUIRE(a->n > 0 && a->n % 32 == 0, "gemm: n must be a positive multiple of 32");
+  DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0, "gemm: k must be a positive multiple of 64");
+  DTREE_REQUIRE(a->rows_padded == 32 || a->rows_padded == 64 || a->rows_padded == 96 || a->rows_padded == 128,
+                "gemm: rows_padded must be 32, 64, 96 or 128");
+  DTREE_REQUIRE(a->ldx >= a->k && a->ldx % 8 == 0, "gemm: ldx must be >= k and a multiple of 8");
+  const int ntiles = a->n / 32, nkb = a->k / 64;
+  const int S = a->split_k > 0 ? a->split_k : auto_split(ntiles, nkb);
+  DTREE_REQUIRE(S <= nkb, "gemm: split_k larger than the number of 64-wide K blocks");
+  const int epi = a->epilogue;
+  DTREE_REQUIRE(epi >= 0 && epi <= 3, "gemm: unknown epilogue");
+  if (epi == DTREE_EPI_STORE_F32 || epi == DTREE_EPI_RESIDUAL)
+    DTREE_REQUIRE(a->out_f32 && a->ld_out_f32 >= a->n, "gemm: out_f32 missing or ld too small");
+  if (epi == DTREE_EPI_RESIDUAL)
+    DTREE_REQUIRE(a->out_bf16 && a->next_norm && a->ss_out && a->ld_out_bf16 >= a->n,
+                  "gemm: residual epilogue needs out_bf16, next_norm, ss_out");
+  if (epi == DTREE_EPI_SWIGLU)
+    DTREE_REQUIRE(a->out_bf16 && a->ld_out_bf16 >= a->n / 2, "gemm: swiglu needs out_bf16 (n/2 wide)");
+  if (epi == DTREE_EPI_STORE_BF16) DTREE_REQUIRE(a->out_bf16 && a->ld_out_bf16 >= a->n, "gemm: out_bf16");
+  if (a->hidden_out) DTREE_REQUIRE(a->ld_hidden >= a->n, "gemm: ld_hidden too small");
+  if (a->ss_in) DTREE_REQUIRE(a->ss_tiles > 0 && a->norm_dim > 0, "gemm: ss_in needs ss_tiles and norm_dim");
+  const size_t need = dtree_gemm_workspace_bytes(a->rows_padded, a->n, a->k, S);
+  DTREE_REQUIRE(a->workspace && a->workspace_bytes >= need, "gemm: workspace too small");
+
+  GemmParams p{};
+  p.x = a->x; p.ldx = a->ldx; p.w = a->w; p.n = a->n; p.k = a->k;
+  p.S = S; p.kb_per_split = (nkb + S - 1) / S; p.ntiles = ntiles;
+  p.ss_in = a->ss_in; p.ss_tiles = a->ss_tiles;
+  p.inv_norm_dim = a->norm_dim > 0 ? 1.0f / (float)a->norm_dim : 1.f; p.eps = a->eps;
+  p.out_f32 = a->out_f32; p.ld_out_f32 = a->ld_out_f32;
+  p.out_bf16 = a->out_bf16; p.ld_out_bf16 = a->ld_out_bf16;
+  p.next_norm = a->next_norm; p.ss_out = a->ss_out;
+  p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
+  const size_t nt8 = (size_t)((ntiles + 7) / 8) * 8;
+  p.counters = reinterpret_cast<int*>(a->workspace);
+  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + ((nt8 * sizeof(int) + 255) & ~(size_t)255));
+  const int blocks = S == 1 ? ntiles : (int)(nt8 * S);
+  switch (a->rows_padded) {
+    case 32: launch_gemm<1, 4>(p, epi, blocks, stream); break;
+    case 64: launch_gemm<2, 2>(p, epi, blocks, stream); break;
+    case 96: launch_gemm<3, 1>(p, epi, blocks, stream); break;
+    default: launch_gemm<4, 1>(p, epi, blocks, stream); break;
+  }
+  DTREE_LAUNCH_CHECK("gemm launch");
+  return DTREE_OK;
+}
+
+extern "C" size_t dtree_lmhead_candidates_bytes(int32_t rows_padded) {
+  return (size_t)1024 * rows_padded * sizeof(int2);
+}
+
+extern "C" int dtree_lmhead_argmax(const uint16_t* x, int32_t ldx, int32_t rows_padded, const uint16_t* emb,
+                                   int32_t vocab, int32_t hidden, const float* ss_in, int32_t ss_tiles,
+                                   float eps, float* logits, void* candidates, hipStream_t stream) {
+  DTREE_REQUIRE(x && emb && candidates, "lmhead: null pointer");
+  DTREE_REQUIRE(vocab > 0 && vocab % 32 == 0, "lmhead: vocab must be a multiple of 32");
+  DTREE_REQUIRE(hidden > 0 && hidden % 64 == 0 && ldx >= hidden, "lmhead: hidden must be a multiple of 64");
+  DTREE_REQUIRE(rows_padded == 32 || rows_padded == 64 || rows_padded == 96 || rows_padded == 128,
+                "lmhead: rows_padded must be 32, 64, 96 or 128");
+  LmParams p{};
+  p.x = x; p.ldx = ldx; p.w = emb; p.vocab = vocab; p.k = hidden; p.ntiles = vocab / 32;
+  p.ss_in = ss_in; p.ss_tiles = ss_tiles; p.inv_norm_dim = 1.0f / (float)hidden; p.eps = eps;
+  p.logits = logits; p.cand = reinterpret_cast<int2*>(candidates);
+  const int grid = lmhead_grid(p.ntiles);
+  switch (rows_padded) {
+    case 32: lmhead_kernel<1, 4><<<grid, kThreads, 0, stream>>>(p); break;
+    case 64: lmhead_kernel<2, 2><<<grid, kThreads, 0, stream>>>(p); break;
+    case 96: lmhead_kernel<3, 1><<<grid, kThreads, 0, stream>>>(p); break;
+    default: lmhead_kernel<4, 1><<<grid, kThreads, 0, stream>>>(p); break;
+  }
+  DTREE_LAUNCH_CHECK("lmhead launch");
+  return DTREE_OK;
+}

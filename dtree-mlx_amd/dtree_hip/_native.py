@@ -1,0 +1,132 @@
+"""ctypes binding of libdtree_hip.so (the C ABI declared in include/dtree_hip.h).
+
+The library is loaded from this package directory. There is no fallback: if
+it is missing or stale the import of any compute entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
+
+MAX_NODES = 128
+MASK_WORDS = 4
+PAGE = 64
+ABI_VERSION = 1
+
+EPI_STORE_F32 = 0
+EPI_RESIDUAL = 1
+EPI_SWIGLU = 2
+EPI_STORE_BF16 = 3
+
+
+class DtreeError(RuntimeError):
+    pass
+
+
+class StepDesc(C.Structure):
+    _fields_ = [
+        ("past_length", C.c_int32),
+        ("num_nodes", C.c_int32),
+        ("n_accepted", C.c_int32),
+        ("bonus_token", C.c_int32),
+        ("tokens", C.c_int32 * MAX_NODES),
+        ("positions", C.c_int32 * MAX_NODES),
+        ("parents", C.c_int32 * MAX_NODES),
+        ("ancestors", (C.c_uint32 * MASK_WORDS) * MAX_NODES),
+        ("accepted", C.c_int32 * MAX_NODES),
+        ("posterior", C.c_int32 * MAX_NODES),
+    ]
+
+
+class GemmArgs(C.Structure):
+    _fields_ = [
+        ("x", C.c_void_p), ("ldx", C.c_int32), ("rows_padded", C.c_int32),
+        ("w", C.c_void_p), ("n", C.c_int32), ("k", C.c_int32),
+        ("epilogue", C.c_int32), ("split_k", C.c_int32),
+        ("ss_in", C.c_void_p), ("ss_tiles", C.c_int32), ("norm_dim", C.c_int32), ("eps", C.c_float),
+        ("out_f32", C.c_void_p), ("ld_out_f32", C.c_int32),
+        ("out_bf16", C.c_void_p), ("ld_out_bf16", C.c_int32),
+        ("next_norm", C.c_void_p), ("ss_out", C.c_void_p),
+        ("hidden_out", C.c_void_p), ("ld_hidden", C.c_int32),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [
+        ("qkv", C.c_void_p), ("ld_qkv", C.c_int32),
+        ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("eps", C.c_float),
+        ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+        ("k_pages", C.c_void_p), ("v_pages", C.c_void_p), ("page_table", C.c_void_p),
+        ("desc", C.c_void_p),
+        ("out", C.c_void_p), ("ld_out", C.c_int32),
+        ("num_heads", C.c_int32), ("num_kv_heads", C.c_int32), ("head_dim", C.c_int32),
+        ("rows_padded", C.c_int32),
+        ("scale", C.c_float),
+        ("max_past_length", C.c_int32),
+        ("write_cache", C.c_int32),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+    ]
+
+
+_vp, _i32, _f32, _sz = C.c_void_p, C.c_int32, C.c_float, C.c_size_t
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "dtree_last_error": (C.c_char_p, []),
+    "dtree_abi_version": (C.c_int, []),
+    "dtree_step_desc_bytes": (_sz, []),
+    "dtree_gemm_workspace_bytes": (_sz, [C.c_int, C.c_int, C.c_int, C.c_int]),
+    "dtree_gemm_bf16": (C.c_int, [C.POINTER(GemmArgs), _vp]),
+    "dtree_embed": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _f32, _vp, _vp, _vp]),
+    "dtree_rope_table": (C.c_int, [_vp, _i32, _i32, _f32, _vp, _vp, _vp]),
+    "dtree_attention_workspace_bytes": (_sz, [_i32, _i32, _i32]),
+    "dtree_tree_attention": (C.c_int, [C.POINTER(AttnArgs), _vp]),
+    "dtree_lmhead_candidates_bytes": (_sz, [_i32]),
+    "dtree_lmhead_candidate_blocks": (C.c_int, [_i32]),
+    "dtree_lmhead_argmax": (C.c_int, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _f32, _vp, _vp, _vp]),
+    "dtree_accept_walk": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp]),
+    "dtree_compact": (C.c_int, [_vp, _vp, _vp, _sz, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "dtree_rownorm": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _i32, _vp]),
+    "dtree_graph_begin": (C.c_int, [_vp]),
+    "dtree_graph_end": (C.c_int, [_vp, C.POINTER(C.c_void_p)]),
+    "dtree_graph_launch": (C.c_int, [_vp, _vp]),
+    "dtree_graph_destroy": (C.c_int, [_vp]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+def lib() -> C.CDLL:
+    """Load the native library (raises if it is missing or has another ABI)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise DtreeError(
+            f"native library {LIB_PATH} is missing; build it with "
+            "`python dtree-mlx_amd/build_native.py` (or __graft_entry__.build())")
+    h = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(h, name)
+        fn.restype = res
+        fn.argtypes = args
+    if h.dtree_abi_version() != ABI_VERSION:
+        raise DtreeError("libdtree_hip.so ABI version mismatch; rebuild it")
+    if h.dtree_step_desc_bytes() != C.sizeof(StepDesc):
+        raise DtreeError("DtreeStepDesc layout mismatch between Python and the library")
+    _LIB = h
+    return h
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().dtree_last_error().decode(errors="replace")
+        raise DtreeError(f"{what or 'dtree call'} failed ({rc}): {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)

@@ -1,0 +1,110 @@
+"""Paged bf16 KV cache for the tree-verify kernels.
+
+Layout (all layers in one allocation each, so compaction is one launch):
+  k_pages [layers, n_pages, kv_heads, PAGE, head_dim]
+  v_pages [layers, n_pages, kv_heads, head_dim, PAGE]   (V^T inside a page, so
+          the P.V MFMA reads eight consecutive keys per 16-byte load)
+  page_table [n_pages] int32: logical page -> physical page.
+
+Logical position t of a layer lives in physical page page_table[t // PAGE] at
+slot t % PAGE. ``offset`` is the number of committed positions (the KVCache
+offset of mlx-lm that dtree_runtime / the adapters read).
+"""
+from __future__ import annotations
+
+import torch
+
+from ._native import PAGE
+
+
+class LayerCacheView:
+    """Per-layer handle with the fields the reference runtime reads (offset)."""
+
+    def __init__(self, cache: "PagedKVCache", layer: int):
+        self._c = cache
+        self.layer = layer
+
+    @property
+    def offset(self) -> int:
+        return self._c.offset
+
+    @property
+    def keys(self) -> torch.Tensor:
+        return self._c.logical_keys(self.layer)
+
+    @property
+    def values(self) -> torch.Tensor:
+        return self._c.logical_values(self.layer)
+
+
+class PagedKVCache:
+    def __init__(self, layers: int, kv_heads: int, head_dim: int, capacity: int, device="cuda",
+                 page_order: torch.Tensor | None = None):
+        self.layers = layers
+        self.kv_heads = kv_heads
+        self.head_dim = head_dim
+        self.n_pages = (capacity + PAGE - 1) // PAGE
+        self.capacity = self.n_pages * PAGE
+        dev = torch.device(device)
+        self.k_pages = torch.zeros(layers, self.n_pages, kv_heads, PAGE, head_dim, dtype=torch.bfloat16, device=dev)
+        self.v_pages = torch.zeros(layers, self.n_pages, kv_heads, head_dim, PAGE, dtype=torch.bfloat16, device=dev)
+        if page_order is None:
+            page_order = torch.arange(self.n_pages, dtype=torch.int32)
+        if sorted(page_order.tolist()) != list(range(self.n_pages)):
+            raise ValueError("page_order must be a permutation of the pages")
+        self.page_table = page_order.to(device=dev, dtype=torch.int32).contiguous()
+        self.offset = 0
+
+    @property
+    def layer_stride(self) -> int:
+        return self.n_pages * self.kv_heads * PAGE * self.head_dim
+
+    def k_ptr(self, layer: int) -> int:
+        return self.k_pages.data_ptr() + 2 * layer * self.layer_stride
+
+    def v_ptr(self, layer: int) -> int:
+        return self.v_pages.data_ptr() + 2 * layer * self.layer_stride
+
+    def __len__(self) -> int:
+        return self.layers
+
+    def __getitem__(self, i: int) -> LayerCacheView:
+        if not 0 <= i < self.layers:
+            raise IndexError(i)
+        return LayerCacheView(self, i)
+
+    def __iter__(self):
+        return (LayerCacheView(self, i) for i in range(self.layers))
+
+    # ---- logical views (tests, checkers, cache import) -------------------
+    def _pages_for(self, length: int) -> torch.Tensor:
+        n = (length + PAGE - 1) // PAGE
+        return self.page_table[:n].long()
+
+    def logical_keys(self, layer: int, length: int | None = None) -> torch.Tensor:
+        """[T, kv_heads, head_dim] bf16, logical order."""
+        T = self.offset if length is None else length
+        pg = self.k_pages[layer][self._pages_for(T)]  # [np, Hkv, PAGE, D]
+        return pg.permute(0, 2, 1, 3).reshape(-1, self.kv_heads, self.head_dim)[:T]
+
+    def logical_values(self, layer: int, length: int | None = None) -> torch.Tensor:
+        T = self.offset if length is None else length
+        pg = self.v_pages[layer][self._pages_for(T)]  # [np, Hkv, D, PAGE]
+        return pg.permute(0, 3, 1, 2).reshape(-1, self.kv_heads, self.head_dim)[:T]
+
+    def write_logical(self, layer: int, keys: torch.Tensor, values: torch.Tensor, start: int = 0) -> None:
+        """Store [T, kv_heads, head_dim] rows at logical positions start..start+T-1."""
+        T = keys.shape[0]
+        if start + T > self.capacity:
+            raise ValueError("cache capacity exceeded")
+        keys = keys.to(self.k_pages.device, torch.bfloat16)
+        values = values.to(self.v_pages.device, torch.bfloat16)
+        pos = torch.arange(start, start + T, device=self.k_pages.device)
+        page = self.page_table.long()[pos // PAGE]
+        slot = pos % PAGE
+        self.k_pages[layer][page, :, slot, :] = keys
+        # v_pages[layer][page, h, d, slot] = values[t, h, d]
+        self.v_pages[layer].permute(0, 3, 1, 2)[page, slot, :, :] = values
+
+    def reset(self, offset: int = 0) -> None:
+        self.offset = offset

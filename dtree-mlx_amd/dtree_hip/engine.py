@@ -1,0 +1,383 @@
+"""Qwen3 tree-verify executor: launches the HIP kernels of one verify step.
+
+One step (dtree_runtime.py:410-537 for the Qwen3 target):
+  embed(+input RMSNorm fold, RoPE table)
+  for every layer:
+    QKV GEMM (row scale = input RMSNorm)      -> qkv fp32
+    tree attention (q/k norm, RoPE, cache append, ancestor mask) -> attn bf16
+    O GEMM + residual (+ post-attention RMSNorm fold)
+    gate/up GEMM + SwiGLU (row scale = post-attention RMSNorm) -> act bf16
+    down GEMM + residual (+ next RMSNorm fold, optional hidden capture)
+  LM head + argmax candidates, argmax reduction + accept walk, KV/hidden compaction.
+
+The launch sequence only depends on device-resident step data (P, L, tree),
+so it can be captured once into a HIP graph and replayed for every step.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _native as N
+from .cache import PagedKVCache
+from .config import Qwen3Config
+from .weights import Qwen3Weights
+
+
+def ancestor_bitsets(parents) -> np.ndarray:
+    """[L, MASK_WORDS] uint32 ancestor-or-self bitsets (parents[i] < i, root -1)."""
+    L = len(parents)
+    if L > N.MAX_NODES:
+        raise ValueError(f"at most {N.MAX_NODES} tree nodes are supported, got {L}")
+    out = np.zeros((L, N.MASK_WORDS), dtype=np.uint32)
+    for i in range(L):
+        p = int(parents[i])
+        if i == 0:
+            if p != -1:
+                raise ValueError(f"tree root parent must be -1, got {p}")
+        elif p < 0 or p >= i:
+            raise ValueError(f"tree parent index must precede child, got parents[{i}]={p}")
+        else:
+            out[i] = out[p]
+        out[i, i // 32] |= np.uint32(1 << (i % 32))
+    return out
+
+
+def mask_to_parents(tree_mask: np.ndarray) -> list[int]:
+    """Parents from an ancestor-or-self visibility matrix [L, L] (rows topological)."""
+    L = tree_mask.shape[0]
+    parents = [-1]
+    for i in range(1, L):
+        anc = [j for j in range(i) if tree_mask[i, j]]
+        if not tree_mask[i, i]:
+            raise ValueError("tree visibility must include the diagonal")
+        if not anc:
+            raise ValueError(f"node {i} sees no ancestor; the root must be visible to every node")
+        p = max(anc)
+        expect = tree_mask[p, :i].copy()
+        expect[p] = True
+        if not np.array_equal(expect, tree_mask[i, :i]):
+            raise ValueError("tree visibility rows must be ancestor-or-self sets (parent row + self)")
+        parents.append(p)
+    return parents
+
+
+@dataclass
+class StepResult:
+    accepted: list[int]
+    bonus_token: int
+    posterior: list[int]
+
+
+class Qwen3TreeEngine:
+    def __init__(self, cfg: Qwen3Config, weights: Qwen3Weights, max_past: int, max_nodes: int = 32,
+                 layer_ids=(), split_k: dict | None = None):
+        cfg.validate()
+        if max_nodes > 32:
+            raise NotImplementedError("trees of up to 32 nodes (one 32-row MFMA block) for Qwen3 attention")
+        self.cfg = cfg
+        self.w = weights
+        self.lib = N.lib()
+        self.dev = weights.device
+        self.max_past = int(max_past)
+        self.max_nodes = max_nodes
+        self.MP = 32
+        self.layer_ids = list(layer_ids)
+        H, F, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+        MP, dev = self.MP, self.dev
+        f32, bf16 = torch.float32, torch.bfloat16
+        self.x = torch.zeros(MP, H, dtype=f32, device=dev)
+        self.xg = torch.zeros(MP, H, dtype=bf16, device=dev)
+        self.ss = torch.zeros(H // 32, MP, dtype=f32, device=dev)
+        self.qkv = torch.zeros(MP, cfg.qkv_dim, dtype=f32, device=dev)
+        self.attn = torch.zeros(MP, cfg.q_dim, dtype=bf16, device=dev)
+        self.act = torch.zeros(MP, F, dtype=bf16, device=dev)
+        self.rope_cos = torch.zeros(MP, cfg.head_dim // 2, dtype=f32, device=dev)
+        self.rope_sin = torch.zeros(MP, cfg.head_dim // 2, dtype=f32, device=dev)
+        self.norm_hidden = torch.zeros(MP, H, dtype=bf16, device=dev)
+        nh = max(1, len(self.layer_ids))
+        self.hidden = torch.zeros(MP, nh * H, dtype=bf16, device=dev)
+        self.hidden_sel = torch.zeros(MP, nh * H, dtype=bf16, device=dev)
+        self.logits = None
+        self.split_k = dict(split_k or {})
+        shapes = self._gemm_shapes()
+        ws = max(self.lib.dtree_gemm_workspace_bytes(MP, n, k, self.split_k.get(name, 0))
+                 for name, (n, k) in shapes.items())
+        self.gemm_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
+        aws = self.lib.dtree_attention_workspace_bytes(cfg.num_attention_heads, cfg.head_dim, self.max_past)
+        self.attn_ws = torch.zeros(aws, dtype=torch.uint8, device=dev)
+        self.n_cand = self.lib.dtree_lmhead_candidate_blocks(V)
+        self.cand = torch.zeros(self.lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=dev)
+        self.desc_host = N.StepDesc()
+        self.desc_pinned = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8).pin_memory()
+        self.desc = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8, device=dev)
+        self.desc_aux_pinned = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8).pin_memory()
+        self.desc_aux = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8, device=dev)
+        self._desc_event = torch.cuda.Event()
+        self._aux_event = torch.cuda.Event()
+        self._desc_event.record()
+        self._aux_event.record()
+        self.lm_in = torch.zeros(self.MP, H, dtype=bf16, device=dev)
+        self.result = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32, device=dev)
+        self.result_host = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32).pin_memory()
+        self._graphs: dict = {}
+
+    # ---- sizes ---------------------------------------------------------------
+    def _gemm_shapes(self):
+        c = self.cfg
+        H, F = c.hidden_size, c.intermediate_size
+        return {"qkv": (c.qkv_dim, H), "o": (H, c.q_dim), "gu": (2 * F, H), "down": (H, F)}
+
+    def new_cache(self, page_order=None) -> PagedKVCache:
+        c = self.cfg
+        return PagedKVCache(c.num_hidden_layers, c.num_key_value_heads, c.head_dim,
+                            self.max_past + self.max_nodes, device=self.dev, page_order=page_order)
+
+    @staticmethod
+    def stream_handle(stream=None) -> int:
+        s = torch.cuda.current_stream() if stream is None else stream
+        return s.cuda_stream
+
+    # ---- step descriptor -------------------------------------------------------
+    def set_step(self, tokens, positions, parents, past_length: int, stream=None, ancestors=None,
+                 aux: bool = False, accepted=None) -> None:
+        """Fill the device step descriptor (``aux`` selects the second one used by
+        stand-alone argmax / compaction calls, so the step's own stays intact)."""
+        L = len(tokens)
+        if not 1 <= L <= self.max_nodes:
+            raise ValueError(f"tree must have 1..{self.max_nodes} nodes, got {L}")
+        if len(positions) != L or len(parents) != L:
+            raise ValueError("tokens, positions and parents must have the same length")
+        if past_length < 0 or past_length > self.max_past:
+            raise ValueError(f"past_length {past_length} outside [0, {self.max_past}]")
+        anc = ancestor_bitsets(parents) if ancestors is None else np.asarray(ancestors, dtype=np.uint32)
+        d = self.desc_host
+        d.past_length = int(past_length)
+        d.num_nodes = L
+        d.n_accepted = 0 if accepted is None else len(accepted)
+        d.bonus_token = -1
+        if accepted is not None:
+            for i, a in enumerate(accepted):
+                d.accepted[i] = int(a)
+        for i in range(L):
+            tok = int(tokens[i])
+            if not 0 <= tok < self.cfg.vocab_size:
+                raise ValueError(f"token id {tok} outside the vocabulary")
+            d.tokens[i] = tok
+            d.positions[i] = int(positions[i])
+            d.parents[i] = int(parents[i])
+            for w in range(N.MASK_WORDS):
+                d.ancestors[i][w] = int(anc[i, w])
+        for i in range(L, N.MAX_NODES):
+            d.tokens[i] = 0
+            d.positions[i] = 0
+            d.parents[i] = -1
+            for w in range(N.MASK_WORDS):
+                d.ancestors[i][w] = 0
+        pinned, dst, ev = ((self.desc_aux_pinned, self.desc_aux, self._aux_event) if aux
+                           else (self.desc_pinned, self.desc, self._desc_event))
+        ev.synchronize()  # the previous upload from this pinned buffer has finished
+        C.memmove(pinned.data_ptr(), C.addressof(d), C.sizeof(d))
+        s = torch.cuda.current_stream() if stream is None else stream
+        with torch.cuda.stream(s):
+            dst.copy_(pinned, non_blocking=True)
+            ev.record(s)
+
+    # ---- launches ----------------------------------------------------------------
+    def gemm_args(self, name, x, ldx, w, epi, *, ss_in=None, out_f32=None, out_bf16=None, next_norm=None,
+                  ss_out=None, hidden_out=0, ld_hidden=0) -> N.GemmArgs:
+        n, k = w.shape
+        a = N.GemmArgs()
+        a.x = x.data_ptr(); a.ldx = ldx; a.rows_padded = self.MP
+        a.w = w.data_ptr(); a.n = n; a.k = k
+        a.epilogue = epi; a.split_k = self.split_k.get(name, 0)
+        a.ss_in = ss_in.data_ptr() if ss_in is not None else None
+        a.ss_tiles = self.cfg.hidden_size // 32 if ss_in is not None else 0
+        a.norm_dim = self.cfg.hidden_size; a.eps = self.cfg.rms_norm_eps
+        if out_f32 is not None:
+            a.out_f32 = out_f32.data_ptr(); a.ld_out_f32 = out_f32.shape[1]
+        if out_bf16 is not None:
+            a.out_bf16 = out_bf16.data_ptr(); a.ld_out_bf16 = out_bf16.shape[1]
+        a.next_norm = next_norm.data_ptr() if next_norm is not None else None
+        a.ss_out = ss_out.data_ptr() if ss_out is not None else None
+        a.hidden_out = hidden_out or None; a.ld_hidden = ld_hidden
+        a.workspace = self.gemm_ws.data_ptr(); a.workspace_bytes = self.gemm_ws.numel()
+        return a
+
+    def _gemm(self, name, x, ldx, w, epi, st, **kw):
+        a = self.gemm_args(name, x, ldx, w, epi, **kw)
+        N.check(self.lib.dtree_gemm_bf16(C.byref(a), st), f"gemm {name}")
+
+    def _attention(self, li, cache: PagedKVCache, st, write_cache=True):
+        c = self.cfg
+        lw = self.w.layers[li]
+        a = N.AttnArgs()
+        a.qkv = self.qkv.data_ptr(); a.ld_qkv = self.qkv.shape[1]
+        a.q_norm = lw.q_norm.data_ptr(); a.k_norm = lw.k_norm.data_ptr(); a.eps = c.rms_norm_eps
+        a.rope_cos = self.rope_cos.data_ptr(); a.rope_sin = self.rope_sin.data_ptr()
+        a.k_pages = cache.k_ptr(li); a.v_pages = cache.v_ptr(li); a.page_table = cache.page_table.data_ptr()
+        a.desc = self.desc.data_ptr()
+        a.out = self.attn.data_ptr(); a.ld_out = self.attn.shape[1]
+        a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
+        a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
+        a.max_past_length = self.max_past; a.write_cache = 1 if write_cache else 0
+        a.workspace = self.attn_ws.data_ptr(); a.workspace_bytes = self.attn_ws.numel()
+        N.check(self.lib.dtree_tree_attention(C.byref(a), st), "tree attention")
+
+    def launch_forward(self, cache: PagedKVCache, st: int, norm_hidden: bool = False) -> None:
+        """embed + all layers; tree K/V rows land in the cache at [P, P+L)."""
+        c = self.cfg
+        H = c.hidden_size
+        if cache.capacity < self.max_past + self.max_nodes:
+            raise ValueError("cache capacity is smaller than max_past + max_nodes")
+        N.check(self.lib.dtree_embed(
+            self.desc.data_ptr(), self.w.embed.data_ptr(), c.vocab_size, H, self.w.layers[0].input_norm.data_ptr(),
+            self.MP,
+            self.x.data_ptr(), self.xg.data_ptr(), self.ss.data_ptr(), c.head_dim, c.rope_theta,
+            self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
+        slot = {li: i for i, li in enumerate(self.layer_ids)}
+        nL = c.num_hidden_layers
+        for li in range(nL):
+            lw = self.w.layers[li]
+            nxt = self.w.layers[li + 1].input_norm if li + 1 < nL else self.w.final_norm
+            self._gemm("qkv", self.xg, H, lw.wqkv, N.EPI_STORE_F32, st, ss_in=self.ss, out_f32=self.qkv)
+            self._attention(li, cache, st)
+            self._gemm("o", self.attn, c.q_dim, lw.wo, N.EPI_RESIDUAL, st, out_f32=self.x, out_bf16=self.xg,
+                       next_norm=lw.post_norm, ss_out=self.ss)
+            self._gemm("gu", self.xg, H, lw.wgu, N.EPI_SWIGLU, st, ss_in=self.ss, out_bf16=self.act)
+            hid, ldh = 0, 0
+            if li in slot:
+                hid = self.hidden.data_ptr() + 2 * slot[li] * H
+                ldh = self.hidden.shape[1]
+            self._gemm("down", self.act, c.intermediate_size, lw.wd, N.EPI_RESIDUAL, st, out_f32=self.x,
+                       out_bf16=self.xg, next_norm=nxt, ss_out=self.ss, hidden_out=hid, ld_hidden=ldh)
+        if norm_hidden:
+            N.check(self.lib.dtree_rownorm(self.x.data_ptr(), H, self.MP, H, self.ss.data_ptr(), H // 32,
+                                           self.w.final_norm.data_ptr(), c.rms_norm_eps,
+                                           self.norm_hidden.data_ptr(), H, st), "rownorm")
+
+    def launch_lm_head(self, st: int, x=None, ss=True, want_logits=False) -> None:
+        c = self.cfg
+        logits_ptr = None
+        if want_logits:
+            if self.logits is None:
+                self.logits = torch.zeros(self.MP, c.vocab_size, dtype=torch.float32, device=self.dev)
+            logits_ptr = self.logits.data_ptr()
+        xin = self.xg if x is None else x
+        N.check(self.lib.dtree_lmhead_argmax(
+            xin.data_ptr(), xin.shape[1], self.MP, self.w.embed.data_ptr(), c.vocab_size, c.hidden_size,
+            self.ss.data_ptr() if ss else None, c.hidden_size // 32 if ss else 0, c.rms_norm_eps,
+            logits_ptr, self.cand.data_ptr(), st), "lm head")
+
+    def launch_walk(self, st: int, aux: bool = False) -> None:
+        d = self.desc_aux if aux else self.desc
+        N.check(self.lib.dtree_accept_walk(d.data_ptr(), self.cand.data_ptr(), self.n_cand, self.MP,
+                                           self.result.data_ptr(), st), "accept walk")
+
+    def launch_compact(self, cache: PagedKVCache, st: int, select_hidden: bool = True, aux: bool = False) -> None:
+        c = self.cfg
+        d = self.desc_aux if aux else self.desc
+        N.check(self.lib.dtree_compact(
+            d.data_ptr(), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(), cache.layer_stride,
+            c.num_hidden_layers, c.num_key_value_heads, c.head_dim, cache.page_table.data_ptr(),
+            self.hidden.data_ptr() if select_hidden else None, self.hidden.shape[1],
+            self.hidden_sel.data_ptr() if select_hidden else None, st), "compact")
+
+    def launch_verify(self, cache: PagedKVCache, st: int) -> None:
+        self.launch_forward(cache, st)
+        self.launch_lm_head(st)
+        self.launch_walk(st)
+        self.launch_compact(cache, st)
+
+    # ---- host-facing steps -----------------------------------------------------
+    def set_layer_ids(self, layer_ids) -> None:
+        ids = list(layer_ids)
+        if ids == self.layer_ids:
+            return
+        H = self.cfg.hidden_size
+        self.layer_ids = ids
+        nh = max(1, len(ids))
+        self.hidden = torch.zeros(self.MP, nh * H, dtype=torch.bfloat16, device=self.dev)
+        self.hidden_sel = torch.zeros(self.MP, nh * H, dtype=torch.bfloat16, device=self.dev)
+        self.release_graphs()
+
+    def read_result(self, stream=None) -> StepResult:
+        s = torch.cuda.current_stream() if stream is None else stream
+        with torch.cuda.stream(s):
+            self.result_host.copy_(self.result, non_blocking=True)
+        s.synchronize()
+        r = self.result_host.numpy()
+        n, bonus, L = int(r[0]), int(r[1]), int(r[2])
+        return StepResult(accepted=[int(v) for v in r[3:3 + n]], bonus_token=bonus,
+                          posterior=[int(v) for v in r[3 + N.MAX_NODES:3 + N.MAX_NODES + L]])
+
+    def verify(self, cache: PagedKVCache, tokens, positions, parents, use_graph: bool = True,
+               commit: bool = True) -> StepResult:
+        """Full verify step on the current stream; returns the walk result and
+        (commit=True) advances cache.offset by the accepted count."""
+        P = cache.offset
+        self.set_step(tokens, positions, parents, P)
+        st = self.stream_handle()
+        if use_graph:
+            self.graph_launch(cache, st)
+        else:
+            self.launch_verify(cache, st)
+        res = self.read_result()
+        if commit:
+            cache.offset = P + len(res.accepted)
+        return res
+
+    def forward_only(self, cache: PagedKVCache, tokens, positions, parents, norm_hidden=False) -> None:
+        self.set_step(tokens, positions, parents, cache.offset)
+        self.launch_forward(cache, self.stream_handle(), norm_hidden=norm_hidden)
+
+    def prefill(self, cache: PagedKVCache, tokens, chunk: int | None = None) -> None:
+        """Causal prefill through the tree path: chains of up to max_nodes tokens."""
+        chunk = chunk or self.max_nodes
+        toks = [int(t) for t in tokens]
+        for s in range(0, len(toks), chunk):
+            part = toks[s:s + chunk]
+            P = cache.offset
+            if P + len(part) > self.max_past:
+                raise ValueError("prefill beyond max_past")
+            self.forward_only(cache, part, [P + i for i in range(len(part))], [-1] + list(range(len(part) - 1)))
+            cache.offset = P + len(part)
+
+    # ---- HIP graph of the verify step ------------------------------------------
+    def graph_launch(self, cache: PagedKVCache, st: int) -> None:
+        key = id(cache)
+        g = self._graphs.get(key)
+        if g is None:
+            g = self.capture_verify(cache)
+        N.check(self.lib.dtree_graph_launch(C.c_void_p(g), st), "graph launch")
+
+    def capture_verify(self, cache: PagedKVCache) -> int:
+        side = torch.cuda.Stream(device=self.dev)
+        side.wait_stream(torch.cuda.current_stream())
+        h = side.cuda_stream
+        N.check(self.lib.dtree_graph_begin(h), "graph begin")
+        try:
+            self.launch_verify(cache, h)
+        except Exception:
+            ex = C.c_void_p()
+            self.lib.dtree_graph_end(h, C.byref(ex))
+            raise
+        ex = C.c_void_p()
+        N.check(self.lib.dtree_graph_end(h, C.byref(ex)), "graph end")
+        torch.cuda.current_stream().wait_stream(side)
+        self._graphs[id(cache)] = ex.value
+        return ex.value
+
+    def release_graphs(self) -> None:
+        for g in self._graphs.values():
+            self.lib.dtree_graph_destroy(C.c_void_p(g))
+        self._graphs.clear()
+
+    def __del__(self):
+        try:
+            self.release_graphs()
+        except Exception:
+            pass

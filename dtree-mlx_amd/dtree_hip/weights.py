@@ -1,0 +1,137 @@
+"""Qwen3 target weights in the device layout the verify kernels stream.
+
+Per layer (all bf16, nn.Linear [out, in] layout):
+  wqkv [q_dim + 2*kv_dim, H]   rows = q heads | k heads | v heads
+  wo   [H, q_dim]
+  wgu  [2F, H]                 gate / up interleaved in 16-row groups, so one
+                               32-row GEMM tile holds gate and up of the same
+                               16 FFN features (fused SwiGLU epilogue)
+  wd   [H, F]
+  input_norm, post_norm [H], q_norm, k_norm [head_dim]
+Global: embed [V, H] (tied LM head), final_norm [H].
+
+Random init follows the synthetic workload: linear and embedding weights
+N(0, 0.02) in bf16, norm weights 1.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .config import Qwen3Config
+
+
+def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    F, H = gate.shape
+    if F % 16:
+        raise ValueError("intermediate size must be a multiple of 16")
+    return torch.stack([gate.reshape(F // 16, 16, H), up.reshape(F // 16, 16, H)], dim=1).reshape(2 * F, H)
+
+
+def split_gate_up(wgu: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    F2, H = wgu.shape
+    v = wgu.reshape(F2 // 32, 2, 16, H)
+    return v[:, 0].reshape(F2 // 2, H), v[:, 1].reshape(F2 // 2, H)
+
+
+@dataclass
+class LayerWeights:
+    input_norm: torch.Tensor
+    wqkv: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    wo: torch.Tensor
+    post_norm: torch.Tensor
+    wgu: torch.Tensor
+    wd: torch.Tensor
+
+
+@dataclass
+class Qwen3Weights:
+    cfg: Qwen3Config
+    embed: torch.Tensor
+    final_norm: torch.Tensor
+    layers: list[LayerWeights] = field(default_factory=list)
+
+    @property
+    def device(self) -> torch.device:
+        return self.embed.device
+
+    @classmethod
+    def random(cls, cfg: Qwen3Config, seed: int = 0, device="cuda", std: float = 0.02,
+               norm_jitter: float = 0.0) -> "Qwen3Weights":
+        """Seeded random init on `device` (norm weights 1, or 1 + N(0, jitter))."""
+        cfg.validate()
+        dev = torch.device(device)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+
+        def lin(rows, cols):
+            t = torch.empty(rows, cols, dtype=torch.float32, device=dev)
+            t.normal_(0.0, std, generator=gen)
+            return t.to(torch.bfloat16)
+
+        def norm(n):
+            if norm_jitter == 0.0:
+                return torch.ones(n, dtype=torch.bfloat16, device=dev)
+            t = torch.empty(n, dtype=torch.float32, device=dev).normal_(0.0, norm_jitter, generator=gen)
+            return (1.0 + t).to(torch.bfloat16)
+
+        H, F, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+        embed = lin(cfg.vocab_size, H)
+        layers = []
+        for _ in range(cfg.num_hidden_layers):
+            wqkv = lin(cfg.qkv_dim, H)
+            wo = lin(H, cfg.q_dim)
+            gate = lin(F, H)
+            up = lin(F, H)
+            wd = lin(H, F)
+            layers.append(LayerWeights(
+                input_norm=norm(H), wqkv=wqkv, q_norm=norm(D), k_norm=norm(D), wo=wo,
+                post_norm=norm(H), wgu=interleave_gate_up(gate, up), wd=wd))
+            del gate, up
+        return cls(cfg=cfg, embed=embed, final_norm=norm(H), layers=layers)
+
+    def to(self, device) -> "Qwen3Weights":
+        mv = lambda t: t.to(device)  # noqa: E731
+        return Qwen3Weights(
+            cfg=self.cfg, embed=mv(self.embed), final_norm=mv(self.final_norm),
+            layers=[LayerWeights(**{k: mv(getattr(lw, k)) for k in LayerWeights.__dataclass_fields__})
+                    for lw in self.layers])
+
+    def nbytes_linear(self) -> int:
+        return sum(lw.wqkv.numel() + lw.wo.numel() + lw.wgu.numel() + lw.wd.numel()
+                   for lw in self.layers) * 2
+
+    def host_accessor(self):
+        """(layer, name) -> numpy bf16 bits, in nn.Linear layout, for a CPU checker."""
+        cfg = self.cfg
+        cache: dict = {}
+
+        def bits(t: torch.Tensor) -> np.ndarray:
+            return t.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16)
+
+        def get(layer, name):
+            key = (layer, name)
+            if key in cache:
+                return cache[key]
+            if layer is None:
+                out = bits({"embed": self.embed, "final_norm": self.final_norm}[name])
+                if name == "embed":
+                    cache[key] = out
+                return out
+            lw = self.layers[layer]
+            q, kv = cfg.q_dim, cfg.kv_dim
+            if name in ("q", "k", "v"):
+                lo = {"q": 0, "k": q, "v": q + kv}[name]
+                hi = lo + (q if name == "q" else kv)
+                return bits(lw.wqkv[lo:hi])
+            if name in ("gate", "up"):
+                g, u = split_gate_up(lw.wgu)
+                return bits(g if name == "gate" else u)
+            return bits({"input_norm": lw.input_norm, "q_norm": lw.q_norm, "k_norm": lw.k_norm,
+                         "o": lw.wo, "post_norm": lw.post_norm, "down": lw.wd}[name])
+
+        return get

@@ -1,0 +1,201 @@
+/*
+ * dtree_hip.h -- C ABI of the MI355X (gfx950) DTree tree-verify step.
+ *
+ * Every entry point takes plain device pointers, sizes and an explicit
+ * hipStream_t, launches asynchronously on that stream, and returns 0 on
+ * success or a negative DTREE_E* status; dtree_last_error() then holds a
+ * message for the calling thread. Nothing here allocates device memory:
+ * callers pass workspaces sized by the *_workspace_bytes queries.
+ *
+ * Reference citations are paths relative to the DrHB/dtree-mlx checkout.
+ */
+#ifndef DTREE_HIP_H
+#define DTREE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DTREE_ABI_VERSION 1
+
+#define DTREE_OK 0
+#define DTREE_E_ARG (-1)      /* bad shape / pointer / enum */
+#define DTREE_E_HIP (-2)      /* HIP runtime error */
+#define DTREE_E_TREE (-3)     /* non-topological parents, too many nodes */
+#define DTREE_E_WORKSPACE (-4) /* workspace too small */
+
+#define DTREE_MAX_NODES 128   /* tree nodes incl. root per verify step */
+#define DTREE_MASK_WORDS 4    /* 32-bit words of an ancestor bitset */
+#define DTREE_PAGE 64         /* KV positions per cache page */
+
+/*
+ * Device-resident description of one verify step. The host fills the input
+ * half (past_length .. ancestors) and copies it to device memory before the
+ * kernels run; kernels fill the output half. Keeping P and L in device memory
+ * lets one captured HIP graph serve every step.
+ *
+ * Mirrors the per-step values of dtree_runtime.py:166-192 (ids, positions =
+ * start + depth, mask = all prefix columns + ancestor-or-self tree columns)
+ * and the walk result of dtree_runtime.py:195-208 (accepted indices, bonus).
+ */
+typedef struct DtreeStepDesc {
+  int32_t past_length;                 /* P: cached positions before the tree */
+  int32_t num_nodes;                   /* L: root + draft nodes              */
+  int32_t n_accepted;                  /* out: len(accepted_indices)          */
+  int32_t bonus_token;                 /* out: posterior token after the walk */
+  int32_t tokens[DTREE_MAX_NODES];     /* node token ids (root first)         */
+  int32_t positions[DTREE_MAX_NODES];  /* RoPE positions                      */
+  int32_t parents[DTREE_MAX_NODES];    /* parent index, root = -1, parent < i */
+  uint32_t ancestors[DTREE_MAX_NODES][DTREE_MASK_WORDS]; /* ancestor-or-self */
+  int32_t accepted[DTREE_MAX_NODES];   /* out: accepted node indices          */
+  int32_t posterior[DTREE_MAX_NODES];  /* out: target argmax per node         */
+} DtreeStepDesc;
+
+/* GEMM epilogues (dtree_gemm_bf16). */
+#define DTREE_EPI_STORE_F32 0  /* out_f32[m][n] = rs[m] * acc                 */
+#define DTREE_EPI_RESIDUAL 1   /* x[m][n] += acc; xg = bf16(x*g_next); ss tile */
+#define DTREE_EPI_SWIGLU 2     /* act = bf16(silu(rs*gate) * rs*up), W rows
+                                  interleaved in 16-row gate/up groups         */
+#define DTREE_EPI_STORE_BF16 3 /* out_bf16[m][n] = bf16(rs[m] * acc)          */
+
+/*
+ * Skinny bf16 GEMM Y = X W^T for up to 128 rows (tree nodes), fp32 accumulate
+ * on gfx950 MFMA 32x32x16. rs[m] is the RMSNorm row scale
+ * rsqrt(sum_t ss_in[t][m] / norm_dim + eps) when ss_in != NULL, else 1.
+ * Replaces the nn.Linear projections of the tree block
+ * (qwen3_tree.py:50-52, 78, 82) with the RMSNorms of qwen3_tree.py:47, 81
+ * folded in (norm weight folded into the producer's bf16 X, row scale here).
+ */
+typedef struct DtreeGemmArgs {
+  const uint16_t* x;      /* bf16 [rows_padded][ldx], rows >= L are zero   */
+  int32_t ldx;
+  int32_t rows_padded;    /* 32, 64, 96 or 128                             */
+  const uint16_t* w;      /* bf16 [n][k] (nn.Linear layout)                */
+  int32_t n, k;           /* n % 32 == 0, k % 64 == 0                      */
+  int32_t epilogue;       /* DTREE_EPI_*                                   */
+  int32_t split_k;        /* >= 1; 0 = choose automatically                */
+  const float* ss_in;     /* [ss_tiles][rows_padded] or NULL               */
+  int32_t ss_tiles;
+  int32_t norm_dim;       /* divisor of the row mean square                */
+  float eps;
+  float* out_f32; int32_t ld_out_f32;      /* STORE_F32 out / RESIDUAL x   */
+  uint16_t* out_bf16; int32_t ld_out_bf16; /* RESIDUAL xg / SWIGLU / BF16  */
+  const uint16_t* next_norm;  /* RESIDUAL: weight of the following RMSNorm */
+  float* ss_out;              /* RESIDUAL: [n/32][rows_padded] sum of x^2  */
+  uint16_t* hidden_out; int32_t ld_hidden; /* RESIDUAL: optional bf16 copy */
+  void* workspace; size_t workspace_bytes; /* split-K partials + counters  */
+} DtreeGemmArgs;
+
+const char* dtree_last_error(void);
+int dtree_abi_version(void);
+size_t dtree_step_desc_bytes(void);
+
+/* Workspace for dtree_gemm_bf16 (partials + tile counters). Counters must be
+ * zero before the first call; every call leaves them zero again. */
+size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int split_k);
+int dtree_gemm_bf16(const DtreeGemmArgs* args, hipStream_t stream);
+
+/*
+ * Embedding gather + first RMSNorm fold (adapters.py:580, qwen3_tree.py:47):
+ * x[m] = E[tokens[m]] (fp32), xg = bf16(x * norm_w), ss[t][m] = sum of x^2
+ * over column tile t (32 columns); rows >= L and token ids outside
+ * [0, vocab) embed as zero. Also fills the RoPE
+ * table cos/sin [rows_padded][head_dim/2] for desc->positions
+ * (mlx nn.RoPE, traditional=False, per-token offsets, qwen3_tree.py:22-27).
+ */
+int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t vocab,
+                int32_t hidden, const uint16_t* norm_w, int32_t rows_padded, float* x, uint16_t* xg,
+                float* ss, int32_t head_dim, float rope_base, float* rope_cos,
+                float* rope_sin, hipStream_t stream);
+
+/* RoPE table only (used when q/k come from outside dtree_embed). */
+int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, int32_t head_dim,
+                     float rope_base, float* rope_cos, float* rope_sin, hipStream_t stream);
+
+/*
+ * Ancestor-masked GQA tree attention over a paged bf16 KV prefix
+ * (qwen3_tree.py:54-76 and the cache append at :146; mask semantics
+ * dtree_runtime.py:190-191). Reads raw q/k/v (fp32, row m = tree node m) from
+ * qkv[m][...] laid out as [q heads | k heads | v heads] * head_dim, applies
+ * q_norm / k_norm (RMSNorm over head_dim, NULL = none), RoPE from the table,
+ * writes the L new K/V rows into the cache at logical positions P..P+L-1,
+ * and writes softmax(scale * q k^T + mask) v as bf16 out[m][h*head_dim + d]
+ * (rows >= L zero). K pages: [page][kv_head][DTREE_PAGE][head_dim];
+ * V pages (transposed): [page][kv_head][head_dim][DTREE_PAGE].
+ * page_table maps logical page -> physical page.
+ */
+typedef struct DtreeAttnArgs {
+  const float* qkv; int32_t ld_qkv;
+  const uint16_t* q_norm; const uint16_t* k_norm; float eps;
+  const float* rope_cos; const float* rope_sin;
+  uint16_t* k_pages; uint16_t* v_pages; const int32_t* page_table;
+  const DtreeStepDesc* desc;
+  uint16_t* out; int32_t ld_out;
+  int32_t num_heads, num_kv_heads, head_dim, rows_padded;
+  float scale;
+  int32_t max_past_length;  /* grid is sized for this P */
+  int32_t write_cache;      /* 1: append the tree K/V rows to the cache */
+  void* workspace; size_t workspace_bytes;
+} DtreeAttnArgs;
+
+size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim,
+                                       int32_t max_past_length);
+int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
+
+/*
+ * Fused LM head + argmax (adapters.py:114-118, 489-492, first index on ties
+ * as adapters.py:78-81): per row m, argmax_v rs[m] * (x[m] . E[v]).
+ * Writes per-workgroup (value, index) candidates to `candidates`
+ * ([grid][rows_padded] float2-like pairs); dtree_accept_walk reduces them.
+ * logits (optional, [rows_padded][vocab] fp32) receives every logit.
+ */
+size_t dtree_lmhead_candidates_bytes(int32_t rows_padded);
+int dtree_lmhead_candidate_blocks(int32_t vocab);
+int dtree_lmhead_argmax(const uint16_t* x, int32_t ldx, int32_t rows_padded,
+                        const uint16_t* emb, int32_t vocab, int32_t hidden,
+                        const float* ss_in, int32_t ss_tiles, float eps,
+                        float* logits, void* candidates, hipStream_t stream);
+
+/*
+ * Final argmax reduction + greedy accept walk (dtree_runtime.py:195-208).
+ * Writes desc->posterior[0..L), accepted[], n_accepted, bonus_token, and the
+ * same values to the device buffer `result` when non-NULL
+ * ([3 + 2*DTREE_MAX_NODES] int32: n_accepted, bonus, L, accepted[MAX],
+ * posterior[MAX]). num_candidate_blocks = dtree_lmhead_candidate_blocks(vocab).
+ */
+int dtree_accept_walk(DtreeStepDesc* desc, const void* candidates,
+                      int32_t num_candidate_blocks, int32_t rows_padded,
+                      int32_t* result, hipStream_t stream);
+
+/*
+ * KV compaction (adapters.py:635-668) for `layers` layer caches whose page
+ * pools are `layer_stride` elements apart, plus the hidden-state select of
+ * dtree_runtime.py:520-521 (hidden_in rows accepted[j] -> hidden_out row j,
+ * optional). Reads accepted / n_accepted / P from desc.
+ */
+int dtree_compact(const DtreeStepDesc* desc, uint16_t* k_pages, uint16_t* v_pages,
+                  size_t layer_stride, int32_t layers, int32_t num_kv_heads,
+                  int32_t head_dim, const int32_t* page_table,
+                  const uint16_t* hidden_in, int32_t hidden_width, uint16_t* hidden_out,
+                  hipStream_t stream);
+
+/* Final RMSNorm output (norm_hidden of adapters.py:595): out = bf16(x*rs*w). */
+int dtree_rownorm(const float* x, int32_t ldx, int32_t rows_padded, int32_t hidden,
+                  const float* ss_in, int32_t ss_tiles, const uint16_t* w, float eps,
+                  uint16_t* out, int32_t ld_out, hipStream_t stream);
+
+/* HIP graph capture of a launch sequence (stands in for the mx.compile region
+ * of qwen3_tree.py:38 and the per-step eval of dtree_runtime.py:480). */
+int dtree_graph_begin(hipStream_t stream);
+int dtree_graph_end(hipStream_t stream, void** graph_exec);
+int dtree_graph_launch(void* graph_exec, hipStream_t stream);
+int dtree_graph_destroy(void* graph_exec);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DTREE_HIP_H */

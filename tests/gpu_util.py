@@ -1,0 +1,63 @@
+"""Helpers shared by the GPU parity tests (no kernels launched at import)."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from dtree_hip import _native as N
+from dtree_hip.engine import ancestor_bitsets
+
+
+def to_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_f32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def device_desc(tokens, positions, parents, past_length, device, accepted=None, ancestors=None) -> torch.Tensor:
+    d = N.StepDesc()
+    L = len(tokens)
+    anc = ancestor_bitsets(parents) if ancestors is None else ancestors
+    d.past_length = past_length
+    d.num_nodes = L
+    for i in range(L):
+        d.tokens[i] = int(tokens[i])
+        d.positions[i] = int(positions[i])
+        d.parents[i] = int(parents[i])
+        for w in range(N.MASK_WORDS):
+            d.ancestors[i][w] = int(anc[i, w])
+    if accepted is not None:
+        d.n_accepted = len(accepted)
+        for i, a in enumerate(accepted):
+            d.accepted[i] = int(a)
+    buf = (C.c_uint8 * C.sizeof(d)).from_buffer_copy(bytes(d))
+    host = torch.frombuffer(bytearray(bytes(buf)), dtype=torch.uint8)
+    return host.to(device)
+
+
+def read_desc(t: torch.Tensor) -> N.StepDesc:
+    raw = bytes(t.cpu().numpy().tobytes())
+    return N.StepDesc.from_buffer_copy(raw)
+
+
+def tree_mask(parents, P: int) -> np.ndarray:
+    L = len(parents)
+    anc = ancestor_bitsets(parents)
+    m = np.ones((L, P + L), bool)
+    for i in range(L):
+        for j in range(L):
+            m[i, P + j] = bool((int(anc[i, j // 32]) >> (j % 32)) & 1)
+    return m
+
+
+def random_tree(L: int, seed: int) -> list[int]:
+    g = np.random.default_rng(seed)
+    return [-1] + [int(g.integers(0, i)) for i in range(1, L)]
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream

@@ -1,0 +1,355 @@
+"""Kernel-level parity on the GPU through the C ABI, against the CPU oracle /
+fp32 references. Tolerances: fp32-accumulated GEMM outputs rtol 1e-4 (only
+the summation order differs); bf16 outputs within 1 bf16 ulp-ish (rtol 1e-2);
+attention vs the fp32 oracle within 2e-2 of the row scale (bf16 operands)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from dtree_hip import _native as N
+from dtree_hip.cache import PagedKVCache
+from oracle import qwen3 as oq
+from oracle import tree as otree
+
+from gpu_util import bf16_f32, device_desc, random_tree, read_desc, stream, tree_mask
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm(x, w, epi, split, ws, **kw):
+    a = N.GemmArgs()
+    a.x = x.data_ptr(); a.ldx = x.shape[1]; a.rows_padded = x.shape[0]
+    a.w = w.data_ptr(); a.n = w.shape[0]; a.k = w.shape[1]
+    a.epilogue = epi; a.split_k = split
+    ss = kw.get("ss_in")
+    a.ss_in = ss.data_ptr() if ss is not None else None
+    a.ss_tiles = ss.shape[0] if ss is not None else 0
+    a.norm_dim = kw.get("norm_dim", 1); a.eps = 1e-6
+    for name in ("out_f32", "out_bf16"):
+        t = kw.get(name)
+        if t is not None:
+            setattr(a, name, t.data_ptr()); setattr(a, "ld_" + name, t.shape[1])
+    nn = kw.get("next_norm")
+    a.next_norm = nn.data_ptr() if nn is not None else None
+    so = kw.get("ss_out")
+    a.ss_out = so.data_ptr() if so is not None else None
+    hid = kw.get("hidden_out")
+    if hid is not None:
+        a.hidden_out = hid.data_ptr(); a.ld_hidden = hid.shape[1]
+    a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+    N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "gemm")
+
+
+def _rows(MP, L, K, g, dev, scale=1.0):
+    x = torch.zeros(MP, K)
+    x[:L] = torch.from_numpy(g.standard_normal((L, K)).astype(np.float32)) * scale
+    return x.to(torch.bfloat16).to(dev)
+
+
+@pytest.mark.parametrize("MP,L", [(32, 25), (32, 32), (64, 40), (96, 65), (128, 128)])
+@pytest.mark.parametrize("split", [1, 3, 8])
+def test_gemm_store_f32_rowscale(gpu_device, MP, L, split):
+    g = np.random.default_rng(MP + split)
+    N_, K = 256, 1024
+    x = _rows(MP, L, K, g, gpu_device)
+    w = torch.from_numpy(g.standard_normal((N_, K)).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu_device)
+    ss = torch.from_numpy(np.abs(g.standard_normal((5, MP))).astype(np.float32)).to(gpu_device)
+    out = torch.zeros(MP, N_, device=gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, N_, K, split), dtype=torch.uint8, device=gpu_device)
+    _gemm(x, w, N.EPI_STORE_F32, split, ws, ss_in=ss, norm_dim=K, out_f32=out)
+    torch.cuda.synchronize()
+    rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(0) / K + 1e-6)
+    ref = (bf16_f32(x).astype(np.float64) @ bf16_f32(w).T.astype(np.float64)) * rs[:, None]
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+    assert int(ws[: (N_ // 32) * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
+    out2 = torch.zeros_like(out)
+    _gemm(x, w, N.EPI_STORE_F32, split, ws, ss_in=ss, norm_dim=K, out_f32=out2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)  # deterministic split-K reduction
+
+
+@pytest.mark.parametrize("split", [1, 4])
+def test_gemm_residual_epilogue(gpu_device, split):
+    g = np.random.default_rng(7)
+    MP, L, N_, K = 32, 25, 512, 768
+    x = _rows(MP, L, K, g, gpu_device)
+    w = torch.from_numpy(g.standard_normal((N_, K)).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu_device)
+    res = torch.zeros(MP, N_)
+    res[:L] = torch.from_numpy(g.standard_normal((L, N_)).astype(np.float32))
+    res = res.to(gpu_device)
+    res0 = res.clone()
+    gn = torch.from_numpy((1 + 0.1 * g.standard_normal(N_)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    xg = torch.zeros(MP, N_, dtype=torch.bfloat16, device=gpu_device)
+    ss = torch.zeros(N_ // 32, MP, device=gpu_device)
+    hid = torch.zeros(MP, 3 * N_, dtype=torch.bfloat16, device=gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, N_, K, split), dtype=torch.uint8, device=gpu_device)
+    _gemm(x, w, N.EPI_RESIDUAL, split, ws, out_f32=res, out_bf16=xg, next_norm=gn, ss_out=ss,
+          hidden_out=hid[:, N_:])
+    torch.cuda.synchronize()
+    ref = res0.cpu().numpy().astype(np.float64) + bf16_f32(x).astype(np.float64) @ bf16_f32(w).T.astype(np.float64)
+    got = res.cpu().numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+    assert np.all(got[L:] == 0)
+    exp_xg = (torch.from_numpy(got) * gn.float().cpu()).to(torch.bfloat16)
+    assert torch.equal(xg.cpu(), exp_xg)
+    exp_ss = (got.astype(np.float64) ** 2).reshape(MP, N_ // 32, 32).sum(-1).T
+    np.testing.assert_allclose(ss.cpu().numpy(), exp_ss, rtol=1e-5, atol=1e-5)
+    assert torch.equal(hid[:, N_:2 * N_].cpu(), torch.from_numpy(got).to(torch.bfloat16))
+    assert int(hid[:, :N_].float().abs().sum()) == 0 and int(hid[:, 2 * N_:].float().abs().sum()) == 0
+
+
+def test_gemm_swiglu_epilogue(gpu_device):
+    g = np.random.default_rng(9)
+    MP, L, F, K = 32, 25, 384, 512
+    x = _rows(MP, L, K, g, gpu_device)
+    gate = torch.from_numpy(g.standard_normal((F, K)).astype(np.float32) * 0.05).to(torch.bfloat16)
+    up = torch.from_numpy(g.standard_normal((F, K)).astype(np.float32) * 0.05).to(torch.bfloat16)
+    from dtree_hip.weights import interleave_gate_up
+    wgu = interleave_gate_up(gate, up).to(gpu_device)
+    ss = torch.from_numpy(np.abs(g.standard_normal((3, MP))).astype(np.float32) + 0.5).to(gpu_device)
+    act = torch.zeros(MP, F, dtype=torch.bfloat16, device=gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, 2 * F, K, 2), dtype=torch.uint8, device=gpu_device)
+    _gemm(x, wgu, N.EPI_SWIGLU, 2, ws, ss_in=ss, norm_dim=K, out_bf16=act)
+    torch.cuda.synchronize()
+    rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(0) / K + 1e-6)
+    xf = bf16_f32(x).astype(np.float64)
+    gt = (xf @ gate.float().numpy().T) * rs[:, None]
+    u = (xf @ up.float().numpy().T) * rs[:, None]
+    ref = gt / (1 + np.exp(-gt)) * u
+    np.testing.assert_allclose(bf16_f32(act), ref, rtol=1e-2, atol=1e-3)
+
+
+def _attention(qkv, cache, layer, desc, out, ws, Hq, Hkv, max_past, cos, sin, qn, kn, write=1):
+    a = N.AttnArgs()
+    a.qkv = qkv.data_ptr(); a.ld_qkv = qkv.shape[1]
+    a.q_norm = qn.data_ptr() if qn is not None else None
+    a.k_norm = kn.data_ptr() if kn is not None else None
+    a.eps = 1e-6
+    a.rope_cos = cos.data_ptr(); a.rope_sin = sin.data_ptr()
+    a.k_pages = cache.k_ptr(layer); a.v_pages = cache.v_ptr(layer); a.page_table = cache.page_table.data_ptr()
+    a.desc = desc.data_ptr(); a.out = out.data_ptr(); a.ld_out = out.shape[1]
+    a.num_heads = Hq; a.num_kv_heads = Hkv; a.head_dim = 128; a.rows_padded = 32
+    a.scale = 128 ** -0.5; a.max_past_length = max_past; a.write_cache = write
+    a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+    N.check(N.lib().dtree_tree_attention(C.byref(a), stream()), "attention")
+
+
+def _attention_case(dev, P, parents, Hq=32, Hkv=8, seed=0, permute_pages=True, max_past=None):
+    g = np.random.default_rng(seed)
+    D = 128
+    L = len(parents)
+    max_past = max(P, 64) if max_past is None else max_past
+    n_pages = (max_past + 32 + 63) // 64
+    order = torch.from_numpy(g.permutation(n_pages).astype(np.int32)) if permute_pages else None
+    cache = PagedKVCache(1, Hkv, D, max_past + 32, device=dev, page_order=order)
+    kpre = (g.standard_normal((P, Hkv, D)) * 0.5).astype(np.float32)
+    vpre = (g.standard_normal((P, Hkv, D)) * 0.5).astype(np.float32)
+    if P:
+        cache.write_logical(0, torch.from_numpy(kpre), torch.from_numpy(vpre))
+    cache.offset = P
+    qkv = np.zeros((32, (Hq + 2 * Hkv) * D), np.float32)
+    qkv[:L] = g.standard_normal((L, (Hq + 2 * Hkv) * D)).astype(np.float32)
+    qn = (1 + 0.1 * g.standard_normal(D)).astype(np.float32)
+    kn = (1 + 0.1 * g.standard_normal(D)).astype(np.float32)
+    depth = [0] * L
+    for i in range(1, L):
+        depth[i] = depth[parents[i]] + 1
+    pos = [P + d for d in depth]
+    desc = device_desc([0] * L, pos, parents, P, dev)
+    cos = torch.zeros(32, 64, device=dev)
+    sin = torch.zeros(32, 64, device=dev)
+    N.check(N.lib().dtree_rope_table(desc.data_ptr(), 32, D, 1e6, cos.data_ptr(), sin.data_ptr(), stream()))
+    qn_t = torch.from_numpy(qn).to(torch.bfloat16).to(dev)
+    kn_t = torch.from_numpy(kn).to(torch.bfloat16).to(dev)
+    out = torch.zeros(32, Hq * D, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(N.lib().dtree_attention_workspace_bytes(Hq, D, max_past), dtype=torch.uint8, device=dev)
+    qkv_t = torch.from_numpy(qkv).to(dev)
+    _attention(qkv_t, cache, 0, desc, out, ws, Hq, Hkv, max_past, cos, sin, qn_t, kn_t)
+    torch.cuda.synchronize()
+
+    # oracle: q/k norm (bf16 norm weights), RoPE, masked SDPA over [prefix ; tree]
+    qnf, knf = bf16_f32(qn_t), bf16_f32(kn_t)
+    q = oq.rms_norm(qkv[:L, : Hq * D].reshape(L, Hq, D), qnf, 1e-6)
+    k = oq.rms_norm(qkv[:L, Hq * D:(Hq + Hkv) * D].reshape(L, Hkv, D), knf, 1e-6)
+    v = qkv[:L, (Hq + Hkv) * D:].reshape(L, Hkv, D)
+    q = oq.rope(q, np.array(pos), 1e6)
+    k = oq.rope(k, np.array(pos), 1e6)
+    kp = oq.bf16_to_f32(oq.f32_to_bf16_bits(kpre))
+    vp = oq.bf16_to_f32(oq.f32_to_bf16_bits(vpre))
+    ref = oq.sdpa(q, np.concatenate([kp, k]), np.concatenate([vp, v]), tree_mask(parents, P), D ** -0.5)
+    return cache, out, ref.reshape(L, Hq * D), k, v, ws
+
+
+@pytest.mark.parametrize("P", [0, 1, 100, 128, 129, 512, 1000])
+@pytest.mark.parametrize("shape", ["chain25", "star25", "random25", "single", "chain32"])
+def test_tree_attention_matches_oracle(gpu_device, P, shape):
+    L = {"chain25": 25, "star25": 25, "random25": 25, "single": 1, "chain32": 32}[shape]
+    if shape.startswith("chain"):
+        parents = [-1] + list(range(L - 1))
+    elif shape == "star25":
+        parents = [-1] + [0] * (L - 1)
+    elif shape == "single":
+        parents = [-1]
+    else:
+        parents = random_tree(L, seed=P + 11)
+    cache, out, ref, k, v, ws = _attention_case(gpu_device, P, parents, seed=P + L)
+    got = bf16_f32(out)
+    scale = np.abs(ref).max()
+    assert np.abs(got[:L] - ref).max() <= 2e-2 * scale, np.abs(got[:L] - ref).max() / scale
+    assert np.all(got[L:] == 0)
+    # tree K/V appended at [P, P+L): K = bf16(rope(k_norm(k))), V = bf16(v)
+    kc = bf16_f32(cache.logical_keys(0, P + L))[P:]
+    vc = bf16_f32(cache.logical_values(0, P + L))[P:]
+    np.testing.assert_allclose(kc, k, rtol=1e-2, atol=1e-2)
+    np.testing.assert_array_equal(vc, oq.bf16_to_f32(oq.f32_to_bf16_bits(v)))
+    Hq = 32
+    assert int(ws[: Hq * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
+
+
+def test_tree_attention_gqa_small_and_deterministic(gpu_device):
+    parents = random_tree(25, seed=5)
+    cache, out, ref, *_ = _attention_case(gpu_device, 300, parents, Hq=8, Hkv=2, seed=4, max_past=2000)
+    got = bf16_f32(out)
+    assert np.abs(got[:25] - ref).max() <= 2e-2 * np.abs(ref).max()
+    cache2, out2, *_ = _attention_case(gpu_device, 300, parents, Hq=8, Hkv=2, seed=4, max_past=2000)
+    assert torch.equal(out, out2)
+
+
+def _lmhead(x, E, dev, logits=None, ss=None):
+    MP = x.shape[0]
+    lib = N.lib()
+    cand = torch.zeros(lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=dev)
+    N.check(lib.dtree_lmhead_argmax(x.data_ptr(), x.shape[1], MP, E.data_ptr(), E.shape[0], E.shape[1],
+                                    ss.data_ptr() if ss is not None else None, ss.shape[0] if ss is not None else 0,
+                                    1e-6, logits.data_ptr() if logits is not None else None, cand.data_ptr(),
+                                    stream()))
+    return cand, lib.dtree_lmhead_candidate_blocks(E.shape[0])
+
+
+def _walk(cand, nblocks, desc, dev):
+    res = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32, device=dev)
+    N.check(N.lib().dtree_accept_walk(desc.data_ptr(), cand.data_ptr(), nblocks, 32, res.data_ptr(), stream()))
+    torch.cuda.synchronize()
+    r = res.cpu().numpy()
+    n, bonus, L = int(r[0]), int(r[1]), int(r[2])
+    return list(r[3:3 + n]), bonus, list(r[3 + N.MAX_NODES:3 + N.MAX_NODES + L])
+
+
+@pytest.mark.parametrize("V", [4096, 151936])
+def test_lmhead_argmax_and_logits(gpu_device, V):
+    g = np.random.default_rng(V)
+    H, L = 2560, 25
+    x = _rows(32, L, H, g, gpu_device)
+    E = torch.from_numpy((g.standard_normal((V, H)) * 0.02).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    logits = torch.zeros(32, V, device=gpu_device)
+    cand, nb = _lmhead(x, E, gpu_device, logits=logits)
+    desc = device_desc([0] * L, [0] * L, [-1] + [0] * (L - 1), 0, gpu_device)
+    _, _, post = _walk(cand, nb, desc, gpu_device)
+    ref = bf16_f32(x)[:L] @ bf16_f32(E).T
+    np.testing.assert_allclose(logits.cpu().numpy()[:L], ref, rtol=1e-4, atol=1e-4)
+    srt = np.sort(ref, axis=-1)
+    margin = srt[:, -1] - srt[:, -2]
+    want = np.argmax(ref, axis=-1)
+    for m in range(L):
+        if margin[m] > 1e-3:
+            assert post[m] == want[m]
+    assert post == list(np.argmax(logits.cpu().numpy()[:L], axis=-1))
+
+
+def test_lmhead_first_index_on_tie(gpu_device):
+    # tests/test_adapters.py:51-81: rows 0 and 70 of the head equal -> index 0
+    V, H = 128, 64
+    E = torch.zeros(V, H)
+    E[0] = 1.0
+    E[70] = 1.0
+    E = E.to(torch.bfloat16).to(gpu_device)
+    x = torch.zeros(32, H, dtype=torch.bfloat16, device=gpu_device)
+    x[0] = 1.0
+    cand, nb = _lmhead(x, E, gpu_device)
+    desc = device_desc([0], [0], [-1], 0, gpu_device)
+    _, _, post = _walk(cand, nb, desc, gpu_device)
+    assert post == [0]
+    # tie across workgroups: 151936-wide vocab, equal rows at 5 and 151900
+    V = 151936
+    E = torch.zeros(V, H)
+    E[151900] = 1.0
+    E[5] = 1.0
+    E = E.to(torch.bfloat16).to(gpu_device)
+    cand, nb = _lmhead(x, E, gpu_device)
+    _, _, post = _walk(cand, nb, desc, gpu_device)
+    assert post == [5]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_walk_and_compaction_match_oracle(gpu_device, seed):
+    g = np.random.default_rng(seed)
+    L, V, H = 25, 64, 64
+    parents = random_tree(L, seed)
+    # distinct tokens among siblings
+    tokens = [int(g.integers(0, V))]
+    for i in range(1, L):
+        used = {tokens[j] for j in range(1, i) if parents[j] == parents[i]}
+        t = int(g.integers(0, V))
+        while t in used:
+            t = int(g.integers(0, V))
+        tokens.append(t)
+    child_maps = [dict() for _ in range(L)]
+    for i in range(1, L):
+        child_maps[parents[i]][tokens[i]] = i
+    # posterior: follow a random path by making argmax = some child token, then stop
+    post = [int(g.integers(0, V)) for _ in range(L)]
+    cur = 0
+    while True:
+        ch = [j for j in range(1, L) if parents[j] == cur]
+        if not ch or g.random() < 0.15:
+            break
+        nxt = ch[int(g.integers(0, len(ch)))]
+        post[cur] = tokens[nxt]
+        cur = nxt
+    # identity LM head: x rows one-hot at the posterior token
+    E = torch.eye(V, H).to(torch.bfloat16).to(gpu_device)
+    x = torch.zeros(32, H)
+    for m in range(L):
+        x[m, post[m]] = 1.0
+    x = x.to(torch.bfloat16).to(gpu_device)
+    cand, nb = _lmhead(x, E, gpu_device)
+    P = 70 + seed
+    depth = [0] * L
+    for i in range(1, L):
+        depth[i] = depth[parents[i]] + 1
+    desc = device_desc(tokens, [P + d for d in depth], parents, P, gpu_device)
+    acc, bonus, got_post = _walk(cand, nb, desc, gpu_device)
+    o_acc, o_bonus = otree.follow_verified_tree(child_maps, post)
+    assert got_post == post
+    assert acc == o_acc and bonus == o_bonus
+    d = read_desc(desc)
+    assert d.n_accepted == len(acc) and list(d.accepted[: len(acc)]) == acc
+
+    # compaction of 3 layers x 2 kv heads, permuted pages; hidden select
+    layers, Hkv, D = 3, 2, 128
+    order = torch.from_numpy(g.permutation(4).astype(np.int32))
+    cache = PagedKVCache(layers, Hkv, D, 256, device=gpu_device, page_order=order)
+    before_k, before_v = [], []
+    for li in range(layers):
+        k = torch.from_numpy(g.standard_normal((P + L, Hkv, D)).astype(np.float32))
+        v = torch.from_numpy(g.standard_normal((P + L, Hkv, D)).astype(np.float32))
+        cache.write_logical(li, k, v)
+        before_k.append(bf16_f32(cache.logical_keys(li, P + L)))
+        before_v.append(bf16_f32(cache.logical_values(li, P + L)))
+    hid = torch.from_numpy(g.standard_normal((32, 96)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    hsel = torch.zeros(32, 96, dtype=torch.bfloat16, device=gpu_device)
+    N.check(N.lib().dtree_compact(desc.data_ptr(), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(),
+                                  cache.layer_stride, layers, Hkv, D, cache.page_table.data_ptr(), hid.data_ptr(),
+                                  96, hsel.data_ptr(), stream()))
+    torch.cuda.synchronize()
+    n = len(acc)
+    for li in range(layers):
+        ek = oq.compact(before_k[li], P, acc)
+        ev = oq.compact(before_v[li], P, acc)
+        np.testing.assert_array_equal(bf16_f32(cache.logical_keys(li, P + n)), ek)
+        np.testing.assert_array_equal(bf16_f32(cache.logical_values(li, P + n)), ev)
+        # rows past the kept range are untouched unless overwritten by the move
+        np.testing.assert_array_equal(bf16_f32(cache.logical_keys(li, P + L))[P + n:], before_k[li][P + n:])
+    assert torch.equal(hsel[:n].cpu(), hid[acc].cpu())

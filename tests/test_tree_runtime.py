@@ -1,0 +1,139 @@
+"""Tree build / compile / walk: reference known-answer tests (ported from
+tests/test_dtree_runtime.py of DrHB/dtree-mlx) plus brute-force pinning of the
+best-first tree on tiny inputs. CPU only."""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from dtree_hip.dtree_runtime import (build_dtree_tree, compile_dtree_tree, follow_verified_tree,
+                                     lazy_follow_tree_exact)
+from oracle import tree as otree
+
+KAT_LOGITS = np.array([[5.0, 4.0, 1.0], [6.0, 2.0, 1.0], [7.0, 3.0, 1.0]], dtype=np.float32)
+
+
+@pytest.mark.parametrize("impl", ["product", "oracle"])
+def test_build_tree_returns_prefix_closed_visibility(impl):
+    # tests/test_dtree_runtime.py:15-40
+    if impl == "product":
+        ids, depths, parents, child_maps, vis, _ = build_dtree_tree(torch.from_numpy(KAT_LOGITS), budget=4)
+        vis = vis.numpy()
+    else:
+        ids, depths, parents, child_maps, vis = otree.build_tree(KAT_LOGITS, budget=4)
+    assert ids and len(ids) == len(depths)
+    assert parents[0] == -1
+    assert vis.shape[0] == 1 + len(ids)
+    assert bool(vis[0, 0])
+    for i in range(1, len(parents)):
+        p = parents[i]
+        assert p < i
+        assert child_maps[p][ids[i - 1]] == i
+        assert bool(vis[i, p]) and bool(vis[i, i])
+
+
+def test_build_tree_kat_exact_nodes():
+    # Hand-derived for the KAT logits, budget 4 (topk = min(budget, V) = 3):
+    # log-probs per row are sorted by token id here, row-0 best is token 0.
+    ids, depths, parents, _, _, _ = build_dtree_tree(torch.from_numpy(KAT_LOGITS), budget=4)
+    chosen, toks = otree.brute_force_tree(KAT_LOGITS, budget=4, topk=3)
+    assert ids == toks
+    assert depths == [len(r) for r in chosen]
+    # chain 0 -> 0 -> 0 has log-prob sum ~ -0.38 - 0.02 - 0.02; sibling token 1 at depth 1 ~ -1.38
+    assert ids[:3] == [0, 0, 0] and parents[:4] == [-1, 0, 1, 2]
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_build_tree_matches_brute_force(seed):
+    g = np.random.default_rng(seed)
+    D, V, k = int(g.integers(2, 5)), int(g.integers(4, 9)), int(g.integers(2, 4))
+    budget = int(g.integers(1, min(30, sum(k ** d for d in range(1, D + 1))) + 1))
+    logits = (g.standard_normal((D, V)) * 3).astype(np.float32)
+    chosen, toks = otree.brute_force_tree(logits, budget, k)
+    ids, depths, parents, child_maps, vis, _ = build_dtree_tree(torch.from_numpy(logits), budget, topk=k)
+    o_ids, o_depths, o_parents, _, o_vis = otree.build_tree(logits, budget, topk=k)
+    assert ids == toks == o_ids
+    assert depths == [len(r) for r in chosen] == o_depths
+    assert parents == o_parents
+    # parent of each node is the node whose rank tuple is its prefix
+    index = {r: i + 1 for i, r in enumerate(chosen)}
+    for i, r in enumerate(chosen):
+        assert parents[i + 1] == (0 if len(r) == 1 else index[r[:-1]])
+    assert np.array_equal(vis.numpy(), o_vis)
+    for i in range(len(parents)):
+        anc = set()
+        j = i
+        while j >= 0:
+            anc.add(j)
+            j = parents[j]
+        assert set(np.nonzero(o_vis[i])[0].tolist()) == anc
+
+
+def test_build_tree_empty_budget():
+    ids, depths, parents, child_maps, vis, _ = build_dtree_tree(torch.zeros(3, 5), budget=0)
+    assert ids == [] and parents == [-1] and vis.shape == (1, 1)
+
+
+@pytest.mark.parametrize("impl", ["product", "oracle"])
+def test_follow_verified_tree_walks_matching_children(impl):
+    # tests/test_dtree_runtime.py:43-52
+    child_maps = [{11: 1, 12: 2}, {21: 3}, {}, {}]
+    fn = follow_verified_tree if impl == "product" else otree.follow_verified_tree
+    accepted, nxt = fn(child_maps, [11, 21, 99, 0])
+    assert accepted == [0, 1, 3]
+    assert nxt == 0
+
+
+def test_build_node_lineages_returns_root_to_parent_paths():
+    # tests/test_dtree_runtime.py:55-64
+    assert otree.build_node_lineages([-1, 0, 0, 1, 3, 2]) == [[], [0], [0], [0, 1], [0, 1, 3], [0, 2]]
+    with pytest.raises(ValueError):
+        otree.build_node_lineages([-1, 1])
+    assert otree.tree_depth_groups([-1, 0, 0, 1, 3, 2]) == [[0], [1, 2], [3, 5], [4]]
+
+
+def test_lazy_follow_tree_exact_walks_only_the_taken_branch():
+    # tests/test_dtree_runtime.py:67-106, with torch tensors
+    class FakeTextModel:
+        def forward_dflash(self, inputs, cache, layer_ids):
+            token = int(inputs[0, 0].item())
+            return (torch.tensor([[[float(token)]]]), torch.tensor([[[float(token + 1000)]]]))
+
+    class FakeTarget:
+        def __init__(self):
+            self.adapter = SimpleNamespace(family="qwen3_5")
+            self.model = SimpleNamespace(language_model=SimpleNamespace(model=FakeTextModel()))
+
+        def lm_head_argmax(self, hidden_states):
+            token = int(hidden_states[0, 0, 0].item())
+            return torch.tensor([[{10: 100, 11: 300, 21: 999}[token]]])
+
+    accepted, nxt, vh = lazy_follow_tree_exact(
+        target=FakeTarget(), target_cache=[], layer_ids=[], tree_tokens=[10, 11, 12, 21],
+        child_maps=[{100: 1, 200: 2}, {300: 3}, {}, {}], temperature=0.0,
+        verify_mode="parallel-greedy-argmax", profile_times=None)
+    assert accepted == [0, 1, 3]
+    assert nxt == 999
+    assert vh.tolist() == [[[1010.0], [1011.0], [1021.0]]]
+
+
+def test_lazy_follow_rejects_other_families():
+    with pytest.raises(NotImplementedError):
+        lazy_follow_tree_exact(SimpleNamespace(adapter=SimpleNamespace(family="qwen3")), [], [], [1], [{}], 0.0,
+                               "parallel-greedy-argmax", None)
+
+
+def test_compile_tree_mask_semantics():
+    ids, depths, parents, child_maps, vis, _ = build_dtree_tree(torch.from_numpy(KAT_LOGITS), budget=4)
+    P = 5
+    ids_buf = torch.zeros(1, 5, dtype=torch.int64)
+    pos_buf = torch.zeros(1, 5, dtype=torch.int64)
+    mask_buf = torch.zeros(5, 20, dtype=torch.bool)  # deliberately not all-ones
+    vids, tokens, vpos, mask = compile_dtree_tree(42, P, ids, depths, vis, P, ids_buf, pos_buf, mask_buf)
+    o_ids, o_pos, o_mask = otree.compile_tree(42, P, ids, depths, vis.numpy(), P)
+    assert tokens == [42, *ids]
+    assert vids[0].tolist() == o_ids.tolist()
+    assert vpos[0].tolist() == o_pos.tolist() == [P, *[P + d for d in depths]]
+    assert np.array_equal(mask.numpy(), o_mask)
+    assert mask[:, :P].all()
