@@ -226,7 +226,7 @@ def main():
         "algorithmic_bytes_per_step": ab["total"],
         "tokens_per_s": round(steps_per_s * mean_acc, 2),
         "mean_accepted": mean_acc,
-        "roofline": {"kernel": "gemm_kernel<1,4,SWIGLU> (gate/up projection + SwiGLU, one layer)",
+        "roofline": {"kernel": "gemm_kernel<1,2,2,true,SWIGLU> (gate/up projection + SwiGLU, one layer)",
                      "bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "avg_launch_us": round(k_ms * 1e3, 2), "algorithmic_bytes_per_launch": k_bytes},

@@ -33,7 +33,7 @@ struct AttnParams {
   const float* rope_cos; const float* rope_sin;
   uint16_t* kp; uint16_t* vp; const int* page_table;
   const DtreeStepDesc* desc;
-  uint16_t* out; int ld_out;
+  uint16_t* out; uint16_t* out_lo; int ld_out;
   int Hq, Hkv, max_chunks;
   float scale_log2;
   int write_cache;
@@ -94,6 +94,32 @@ __device__ __forceinline__ void pack_frag(const float (&v)[D / 16][8], u32x4_t (
                    pack_bf2(v[j][6], v[j][7])};
 }
 
+// v = hi + lo with hi = bf16(v), lo = bf16(v - hi): about 16 significant bits
+// through two bf16 MFMAs.
+__device__ __forceinline__ void split8(const float* v, u32x4_t& hi, u32x4_t& lo) {
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = v[i] - bf2f(f2bf(v[i]));
+  hi = u32x4_t{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])};
+  lo = u32x4_t{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+}
+
+// P.V step s2 of a 32-key block: B operand = probabilities of registers
+// 8*s2 .. 8*s2+7 (split hi/lo), A operand = V^T fragments.
+template <int ND>
+__device__ __forceinline__ void pv_step(const f32x16_t& p, int s2, const u32x4_t (&va)[ND], f32x16_t (&o)[ND]) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = p[8 * s2 + i];
+  u32x4_t ph, pl;
+  split8(v, ph, pl);
+#pragma unroll
+  for (int db = 0; db < ND; ++db) {
+    o[db] = mfma32(va[db], ph, o[db]);
+    o[db] = mfma32(va[db], pl, o[db]);
+  }
+}
+
 // Online-softmax update for one 32-key block; s[] already scaled (log2 units).
 template <int ND>
 __device__ __forceinline__ void softmax_block(f32x16_t& s, float& m_run, float& l_run, f32x16_t (&o)[ND]) {
@@ -137,12 +163,13 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
   const int lane = threadIdx.x, c = lane & 31, h = lane >> 5;
   const int half_d = D / 2;
 
-  u32x4_t qf[NJ];
+  u32x4_t qf[NJ], ql[NJ];
   {
     float q[NJ][8];
     load_head_row<D>(p.qkv + (size_t)c * p.ld_qkv + hq * D, p.q_norm, p.eps, true, p.rope_cos + c * half_d,
                      p.rope_sin + c * half_d, h, q);
-    pack_frag<D>(q, qf);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) split8(q[j], qf[j], ql[j]);
   }
 
   float m_run = kNeg, l_run = 0.f;
@@ -195,6 +222,7 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
     for (int j = 0; j < NJ; ++j) {
       const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[kr_row * KS + 16 * j + 8 * h]);
       s = mfma32(a, qf[j], s);
+      s = mfma32(a, ql[j], s);
     }
     const uint32_t anc = p.desc->ancestors[c][0];
 #pragma unroll
@@ -206,13 +234,11 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
     softmax_block<ND>(s, m_run, l_run, o);
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
-      const u32x4_t pf = u32x4_t{pack_bf2(s[8 * s2 + 0], s[8 * s2 + 1]), pack_bf2(s[8 * s2 + 2], s[8 * s2 + 3]),
-                                 pack_bf2(s[8 * s2 + 4], s[8 * s2 + 5]), pack_bf2(s[8 * s2 + 6], s[8 * s2 + 7])};
+      u32x4_t va[ND];
 #pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&vt[(32 * db + c) * VS + 16 * s2 + 8 * h]);
-        o[db] = mfma32(a, pf, o[db]);
-      }
+      for (int db = 0; db < ND; ++db)
+        va[db] = *reinterpret_cast<const u32x4_t*>(&vt[(32 * db + c) * VS + 16 * s2 + 8 * h]);
+      pv_step<ND>(s, s2, va, o);
     }
   } else {
     const int k_begin = (chunk - 1) * kChunkKeys;
@@ -229,7 +255,10 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) s = mfma32(kf[j], qf[j], s);
+      for (int j = 0; j < NJ; ++j) {
+        s = mfma32(kf[j], qf[j], s);
+        s = mfma32(kf[j], ql[j], s);
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kb0 + 16 * (r >> 3) + 8 * h + (r & 7);
@@ -239,13 +268,10 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
       const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off0;
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const u32x4_t pf = u32x4_t{pack_bf2(s[8 * s2 + 0], s[8 * s2 + 1]), pack_bf2(s[8 * s2 + 2], s[8 * s2 + 3]),
-                                   pack_bf2(s[8 * s2 + 4], s[8 * s2 + 5]), pack_bf2(s[8 * s2 + 6], s[8 * s2 + 7])};
+        u32x4_t va[ND];
 #pragma unroll
-        for (int db = 0; db < ND; ++db) {
-          const u32x4_t a = ld_u32x4(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 16 * s2 + 8 * h);
-          o[db] = mfma32(a, pf, o[db]);
-        }
+        for (int db = 0; db < ND; ++db) va[db] = ld_u32x4(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 16 * s2 + 8 * h);
+        pv_step<ND>(s, s2, va, o);
       }
     }
   }
@@ -293,7 +319,10 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
       float acc = 0.f;
       if (q < L)
         for (int k = 0; k < nc; ++k) acc += wts[k * 32 + q] * __builtin_nontemporal_load(base + k * stride + (size_t)q * D + d);
-      p.out[(size_t)q * p.ld_out + hq * D + d] = f2bf(acc);
+      const size_t oi = (size_t)q * p.ld_out + hq * D + d;
+      const uint16_t hi = f2bf(acc);
+      p.out[oi] = hi;
+      if (p.out_lo) p.out_lo[oi] = f2bf(acc - bf2f(hi));
     }
   }
 }
@@ -330,7 +359,7 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   p.qkv = a->qkv; p.ld_qkv = a->ld_qkv; p.q_norm = a->q_norm; p.k_norm = a->k_norm; p.eps = a->eps;
   p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
   p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
-  p.out = a->out; p.ld_out = a->ld_out;
+  p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
   p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.max_chunks = max_chunks;
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.counters = reinterpret_cast<int*>(a->workspace);

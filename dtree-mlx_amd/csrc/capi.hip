@@ -31,11 +31,6 @@ extern "C" int dtree_abi_version(void) { return DTREE_ABI_VERSION; }
 
 extern "C" size_t dtree_step_desc_bytes(void) { return sizeof(DtreeStepDesc); }
 
-extern "C" int dtree_lmhead_candidate_blocks(int32_t vocab) {
-  const int ntiles = vocab / 32;
-  return ntiles < 1024 ? ntiles : 1024;
-}
-
 extern "C" int dtree_graph_begin(hipStream_t stream) {
   return hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
 }

@@ -5,14 +5,19 @@
 // bf16 MFMA ridge): the design goal is HBM bandwidth, not MFMA throughput.
 //
 // Work split
-//   * An output column tile is 32 weight rows. A workgroup (4 waves) owns one
-//     tile and a K range; its waves interleave 64-wide K blocks so one
-//     iteration of the workgroup reads 512 contiguous bytes of every weight row.
+//   * A column tile is 32*NB weight rows. A workgroup (4 waves) owns one tile
+//     and a K range; its waves interleave 64-wide K blocks so one iteration of
+//     the workgroup reads 512 contiguous bytes of every weight row.
 //   * Lane (c = lane%32, h = lane/32) loads 64 contiguous bytes of weight row
-//     c (K offset 32h within the block) with streaming loads, and the same K
-//     slice of activation row c. Element group j of both operands feeds MFMA j
-//     (v_mfma_f32_32x32x16_bf16), so A and B see the same K permutation and
-//     the 4 MFMAs sum exactly the 64 K values of the block.
+//     c of each of the NB 32-row blocks (K offset 32h within the block) with
+//     streaming loads, and the same K slice of activation row c. Element group
+//     j of both operands feeds MFMA j (v_mfma_f32_32x32x16_bf16), so A and B
+//     see the same K permutation and 4 MFMAs sum exactly the block's 64 K
+//     values. One activation fragment serves NB weight blocks.
+//   * Activations may arrive as a split pair x = hi + lo (both bf16, about
+//     16 significant bits together); both halves are multiplied with the same
+//     weight fragment. The weights stay bf16, so HBM traffic is unchanged and
+//     the MFMA work doubles, which the bandwidth-bound kernel absorbs.
 //   * Waves reduce through LDS in a fixed order. With split_k > 1 the K range
 //     is split over workgroups; each writes its partial tile, and the last to
 //     arrive (device-scope counter) sums all partials in split order, so the
@@ -20,8 +25,8 @@
 //     mapped to one XCD (workgroups go round-robin over the 8 XCDs), so the
 //     partials stay in that XCD's L2.
 //   * Epilogues fuse the RMSNorm row scale (norm weight folded into the
-//     producer's bf16 X), residual add, SwiGLU, and the per-tile sum of
-//     squares the next RMSNorm needs.
+//     producer's X), residual add, SwiGLU, and the per-32-column sum of
+//     squares the next RMSNorm needs; they emit split hi/lo outputs.
 #include "common.h"
 
 namespace dtree {
@@ -30,92 +35,119 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 
 struct GemmParams {
-  const uint16_t* x; int ldx;
+  const uint16_t* x; const uint16_t* x_lo; int ldx;
   const uint16_t* w; int n, k;
   int S, kb_per_split, ntiles;
   const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
   float* out_f32; int ld_out_f32;
-  uint16_t* out_bf16; int ld_out_bf16;
+  uint16_t* out_bf16; uint16_t* out_lo; int ld_out_bf16;
   const uint16_t* next_norm;
   float* ss_out;
   uint16_t* hidden_out; int ld_hidden;
   float* part; int* counters;
 };
 
-// Partial product of one 32-column tile over K blocks [kb0, kb1) into
-// red[wave][mb*1024 + row*32 + col]; then waves are summed into red[0..].
-template <int MB, int U>
-__device__ __forceinline__ void wg_tile(const uint16_t* __restrict__ x, int ldx,
-                                        const uint16_t* __restrict__ w, int K, int tile, int kb0,
-                                        int kb1, float* red) {
+// Split v into bf16 hi + bf16 lo (lo = bf16(v - hi)).
+__device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, size_t idx, float v) {
+  const uint16_t h = f2bf(v);
+  hi[idx] = h;
+  if (lo) lo[idx] = f2bf(v - bf2f(h));
+}
+
+// Partial product of one tile (32*NB columns) over K blocks [kb0, kb1); the
+// waves' tiles are summed into red[0 .. MB*32*32*NB) laid out [row][col].
+template <int MB, int NB, int U, bool LO>
+__device__ __forceinline__ void wg_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ xlo, int ldx,
+                                        const uint16_t* __restrict__ w, int K, int tile, int kb0, int kb1,
+                                        float* red) {
+  constexpr int TN = 32 * NB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 31, h = lane >> 5;
-  f32x16_t acc[MB];
+  f32x16_t acc[NB][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
-
-  const uint16_t* wp = w + (size_t)(tile * 32 + c) * K + 32 * h;
-  const uint16_t* xp = x + (size_t)c * ldx + 32 * h;
-  int kb = kb0 + wave;
-  for (; kb + kWaves * (U - 1) < kb1; kb += kWaves * U) {
-    u32x4_t wv[U][4];
-    u32x4_t xv[U][MB][4];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wv[u][i] = ld_u32x4_stream(wp + (size_t)(kb + kWaves * u) * 64 + 8 * i);
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          xv[u][mb][i] = ld_u32x4(xp + (size_t)mb * 32 * ldx + (size_t)(kb + kWaves * u) * 64 + 8 * i);
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32(xv[u][mb][i], wv[u][i], acc[mb]);
-  }
-  for (; kb < kb1; kb += kWaves) {
-    u32x4_t wv[4];
-    u32x4_t xv[MB][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wv[i] = ld_u32x4_stream(wp + (size_t)kb * 64 + 8 * i);
+  for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xv[mb][i] = ld_u32x4(xp + (size_t)mb * 32 * ldx + (size_t)kb * 64 + 8 * i);
+      for (int r = 0; r < 16; ++r) acc[nb][mb][r] = 0.f;
+
+  const uint16_t* wp = w + (size_t)(tile * TN + c) * K + 32 * h;
+  const size_t wnb = (size_t)32 * K;  // next 32-row weight block
+  const uint16_t* xp = x + (size_t)c * ldx + 32 * h;
+  const uint16_t* xq = LO ? xlo + (size_t)c * ldx + 32 * h : nullptr;
+  int kb = kb0 + wave;
+  for (; kb < kb1; kb += kWaves * U) {
+    u32x4_t wv[U][NB][4];
+    u32x4_t xv[U][MB][4];
+    u32x4_t xl[U][MB][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int u = 0; u < U; ++u) {
+      const int kk = kb + kWaves * u;
+      if (U == 1 || kk < kb1) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32(xv[mb][i], wv[i], acc[mb]);
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wv[u][nb][i] = ld_u32x4_stream(wp + nb * wnb + (size_t)kk * 64 + 8 * i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = kb + kWaves * u;
+      if (U == 1 || kk < kb1) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            xv[u][mb][i] = ld_u32x4(xp + (size_t)mb * 32 * ldx + (size_t)kk * 64 + 8 * i);
+            if (LO) xl[u][mb][i] = ld_u32x4(xq + (size_t)mb * 32 * ldx + (size_t)kk * 64 + 8 * i);
+          }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = kb + kWaves * u;
+      if (U == 1 || kk < kb1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+              acc[nb][mb] = mfma32(xv[u][mb][i], wv[u][nb][i], acc[nb][mb]);
+              if (LO) acc[nb][mb] = mfma32(xl[u][mb][i], wv[u][nb][i], acc[nb][mb]);
+            }
+      }
+    }
   }
 
   // Waves 1..3 park their tiles in LDS; wave 0 adds them in wave order, so
   // the sum is independent of timing, then publishes the tile at red[0..).
+  constexpr int TE = MB * 32 * TN;
   if (wave > 0) {
-    float* my = red + (wave - 1) * MB * 1024;
+    float* my = red + (wave - 1) * TE;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) my[mb * 1024 + acc_row(r, h) * 32 + c] = acc[mb][r];
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) my[(mb * 32 + acc_row(r, h)) * TN + nb * 32 + c] = acc[nb][mb][r];
   }
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
     for (int wv = 0; wv < kWaves - 1; ++wv)
 #pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[nb][mb][r] += red[wv * TE + (mb * 32 + acc_row(r, h)) * TN + nb * 32 + c];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[mb][r] += red[wv * MB * 1024 + mb * 1024 + acc_row(r, h) * 32 + c];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) red[mb * 1024 + acc_row(r, h) * 32 + c] = acc[mb][r];
+        for (int r = 0; r < 16; ++r) red[(mb * 32 + acc_row(r, h)) * TN + nb * 32 + c] = acc[nb][mb][r];
   }
   __syncthreads();
 }
@@ -135,10 +167,11 @@ __device__ __forceinline__ void row_scale(const float* ss_in, int ss_tiles, floa
   }
 }
 
-template <int MB, int U, int EPI>
+template <int MB, int NB, int U, bool LO, int EPI>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int MP = MB * 32;
-  constexpr int TE = MB * 1024;  // tile elements
+  constexpr int TN = 32 * NB;
+  constexpr int TE = MP * TN;  // tile elements
   __shared__ float red[(kWaves - 1) * TE];
   __shared__ float rs[MP];
   __shared__ int is_last;
@@ -157,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   const int kb0 = s * p.kb_per_split;
   const int kb1 = min(kb0 + p.kb_per_split, nkb);
 
-  wg_tile<MB, U>(p.x, p.ldx, p.w, p.k, tile, kb0, kb1, red);
+  wg_tile<MB, NB, U, LO>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, kb0, kb1, red);
 
   if (p.S > 1) {
     float* mine = p.part + ((size_t)tile * p.S + s) * TE;
@@ -179,47 +212,49 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs);
   __syncthreads();
 
+  // Element e of the tile: row e / TN, column e % TN. With TN in {32, 64} and
+  // 256 threads, a 32-column group of one row is held by 32 consecutive lanes.
   if constexpr (EPI == DTREE_EPI_STORE_F32) {
     for (int e = threadIdx.x; e < TE; e += kThreads) {
-      const int m = e >> 5, n = e & 31;
-      p.out_f32[(size_t)m * p.ld_out_f32 + tile * 32 + n] = red[e] * rs[m];
+      const int m = e / TN, n = e % TN;
+      p.out_f32[(size_t)m * p.ld_out_f32 + tile * TN + n] = red[e] * rs[m];
     }
   } else if constexpr (EPI == DTREE_EPI_STORE_BF16) {
     for (int e = threadIdx.x; e < TE; e += kThreads) {
-      const int m = e >> 5, n = e & 31;
-      p.out_bf16[(size_t)m * p.ld_out_bf16 + tile * 32 + n] = f2bf(red[e] * rs[m]);
+      const int m = e / TN, n = e % TN;
+      split_store(p.out_bf16, p.out_lo, (size_t)m * p.ld_out_bf16 + tile * TN + n, red[e] * rs[m]);
     }
   } else if constexpr (EPI == DTREE_EPI_RESIDUAL) {
-    // Thread t handles column n = t%32 of rows t/32 + 8i: a row is owned by
-    // 32 consecutive lanes, so its sum of squares is a half-wave butterfly.
-    const int n = threadIdx.x & 31;
-    const int col = tile * 32 + n;
+    const int n = threadIdx.x % TN;
+    const int col = tile * TN + n;
     const float g = bf2f(p.next_norm[col]);
     for (int e = threadIdx.x; e < TE; e += kThreads) {
-      const int m = e >> 5;
+      const int m = e / TN;
       float* xp = p.out_f32 + (size_t)m * p.ld_out_f32 + col;
       const float xv = *xp + red[e];
       *xp = xv;
-      p.out_bf16[(size_t)m * p.ld_out_bf16 + col] = f2bf(xv * g);
+      split_store(p.out_bf16, p.out_lo, (size_t)m * p.ld_out_bf16 + col, xv * g);
       if (p.hidden_out) p.hidden_out[(size_t)m * p.ld_hidden + col] = f2bf(xv);
       float sq = xv * xv;
 #pragma unroll
       for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
-      if (n == 0) p.ss_out[(size_t)tile * MP + m] = sq;
+      if ((n & 31) == 0) p.ss_out[(size_t)(col >> 5) * MP + m] = sq;
     }
   } else if constexpr (EPI == DTREE_EPI_SWIGLU) {
-    for (int e = threadIdx.x; e < MP * 16; e += kThreads) {
-      const int m = e >> 4, j = e & 15;
-      const float gt = red[m * 32 + j] * rs[m];
-      const float up = red[m * 32 + 16 + j] * rs[m];
-      p.out_bf16[(size_t)m * p.ld_out_bf16 + tile * 16 + j] = f2bf(silu_f(gt) * up);
+    // Each 32-column group = 16 gate rows then 16 up rows of 16 FFN features.
+    for (int e = threadIdx.x; e < MP * TN / 2; e += kThreads) {
+      const int m = e / (TN / 2), f = e % (TN / 2);
+      const int sb = f >> 4, j = f & 15;
+      const float gt = red[m * TN + sb * 32 + j] * rs[m];
+      const float up = red[m * TN + sb * 32 + 16 + j] * rs[m];
+      split_store(p.out_bf16, p.out_lo, (size_t)m * p.ld_out_bf16 + tile * (TN / 2) + f, silu_f(gt) * up);
     }
   }
 }
 
 // ---- LM head: persistent over vocab tiles, per-row running argmax --------
 struct LmParams {
-  const uint16_t* x; int ldx;
+  const uint16_t* x; const uint16_t* x_lo; int ldx;
   const uint16_t* w; int vocab, k;
   int ntiles;
   const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
@@ -234,10 +269,11 @@ __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi)
   }
 }
 
-template <int MB, int U>
+template <int MB, int NB, int U, bool LO>
 __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   constexpr int MP = MB * 32;
-  constexpr int TE = MB * 1024;
+  constexpr int TN = 32 * NB;
+  constexpr int TE = MP * TN;
   constexpr int IT = TE / kThreads;  // rows handled per thread
   __shared__ float red[(kWaves - 1) * TE];
   __shared__ float rs[MP];
@@ -250,19 +286,19 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
     bi[i] = 0x7fffffff;
   }
   const int nkb = p.k >> 6;
-  const int n = threadIdx.x & 31;
+  const int n = threadIdx.x % TN;
   for (int tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     __syncthreads();
-    wg_tile<MB, U>(p.x, p.ldx, p.w, p.k, tile, 0, nkb, red);
+    wg_tile<MB, NB, U, LO>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, 0, nkb, red);
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int e = threadIdx.x + i * kThreads;
-      const int m = e >> 5;
+      const int m = e / TN;
       float v = red[e] * rs[m];
-      int idx = tile * 32 + n;
+      int idx = tile * TN + n;
       if (p.logits) p.logits[(size_t)m * p.vocab + idx] = v;
 #pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) {
+      for (int o = TN / 2; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(v, o);
         const int oi = __shfl_xor(idx, o);
         argmax_merge(v, idx, ov, oi);
@@ -273,13 +309,23 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   if (n == 0) {
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
-      const int m = (threadIdx.x + i * kThreads) >> 5;
+      const int m = (threadIdx.x + i * kThreads) / TN;
       p.cand[(size_t)blockIdx.x * MP + m] = make_int2(__float_as_int(bv[i]), bi[i]);
     }
   }
 }
 
-int lmhead_grid(int ntiles) { return ntiles < 1024 ? ntiles : 1024; }
+// Tile width per row block count: two 32-row weight blocks share one
+// activation fragment for up to 64 rows; wider row blocks keep one.
+template <int MB> struct Cfg;
+template <> struct Cfg<1> { static constexpr int NB = 2, U = 2; };
+template <> struct Cfg<2> { static constexpr int NB = 2, U = 1; };
+template <> struct Cfg<3> { static constexpr int NB = 1, U = 1; };
+template <> struct Cfg<4> { static constexpr int NB = 1, U = 1; };
+
+static int tile_cols(int rows_padded) { return rows_padded <= 64 ? 64 : 32; }
+
+static int lmhead_grid(int ntiles) { return ntiles < 1024 ? ntiles : 1024; }
 
 static int auto_split(int ntiles, int nkb) {
   int s = 1;
@@ -287,15 +333,34 @@ static int auto_split(int ntiles, int nkb) {
   return s;
 }
 
-template <int MB, int U>
-static void launch_gemm(const GemmParams& p, int epi, int blocks, hipStream_t st) {
+template <int MB, bool LO>
+static void launch_gemm_lo(const GemmParams& p, int epi, int blocks, hipStream_t st) {
+  constexpr int NB = Cfg<MB>::NB, U = Cfg<MB>::U;
   switch (epi) {
-    case DTREE_EPI_STORE_F32: gemm_kernel<MB, U, DTREE_EPI_STORE_F32><<<blocks, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_RESIDUAL: gemm_kernel<MB, U, DTREE_EPI_RESIDUAL><<<blocks, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_SWIGLU: gemm_kernel<MB, U, DTREE_EPI_SWIGLU><<<blocks, kThreads, 0, st>>>(p); break;
-    default: gemm_kernel<MB, U, DTREE_EPI_STORE_BF16><<<blocks, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_STORE_F32: gemm_kernel<MB, NB, U, LO, DTREE_EPI_STORE_F32><<<blocks, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: gemm_kernel<MB, NB, U, LO, DTREE_EPI_RESIDUAL><<<blocks, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: gemm_kernel<MB, NB, U, LO, DTREE_EPI_SWIGLU><<<blocks, kThreads, 0, st>>>(p); break;
+    default: gemm_kernel<MB, NB, U, LO, DTREE_EPI_STORE_BF16><<<blocks, kThreads, 0, st>>>(p); break;
   }
 }
+
+template <int MB>
+static void launch_gemm(const GemmParams& p, int epi, int blocks, hipStream_t st) {
+  if (p.x_lo) launch_gemm_lo<MB, true>(p, epi, blocks, st);
+  else launch_gemm_lo<MB, false>(p, epi, blocks, st);
+}
+
+template <int MB>
+static void launch_lm(const LmParams& p, int grid, hipStream_t st) {
+  constexpr int NB = Cfg<MB>::NB, U = Cfg<MB>::U;
+  if (p.x_lo) lmhead_kernel<MB, NB, U, true><<<grid, kThreads, 0, st>>>(p);
+  else lmhead_kernel<MB, NB, U, false><<<grid, kThreads, 0, st>>>(p);
+}
+
+// Workspace = a fixed counter region (so GEMMs of different shapes can share
+// one workspace without one's partials landing on another's counters) followed
+// by the split-K partial tiles.
+constexpr size_t kCounterBytes = 65536;  // 16384 column tiles
 
 }  // namespace dtree
 
@@ -303,23 +368,26 @@ using namespace dtree;
 
 extern "C" size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int split_k) {
   if (rows_padded <= 0 || n <= 0 || k <= 0) return 0;
-  const int ntiles = n / 32, nkb = k / 64;
+  const int tn = tile_cols(rows_padded);
+  const int ntiles = (n + tn - 1) / tn, nkb = k / 64;
   const int S = split_k > 0 ? split_k : auto_split(ntiles, nkb);
   const size_t nt8 = (size_t)((ntiles + 7) / 8) * 8;
-  return nt8 * sizeof(int) + (S > 1 ? nt8 * S * (size_t)rows_padded * 32 * sizeof(float) : 0) + 256;
+  return kCounterBytes + (S > 1 ? nt8 * S * (size_t)rows_padded * tn * sizeof(float) : 0);
 }
 
 extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a, "gemm: null args");
   DTREE_REQUIRE(a->x && a->w, "gemm: null x or w");
-  DTREE_REQUIRE(a->n > 0 && a->n % 32 == 0, "gemm: n must be a positive multiple of 32");
-  DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0, "gemm: k must be a positive multiple of 64");
   DTREE_REQUIRE(a->rows_padded == 32 || a->rows_padded == 64 || a->rows_padded == 96 || a->rows_padded == 128,
                 "gemm: rows_padded must be 32, 64, 96 or 128");
+  const int tn = tile_cols(a->rows_padded);
+  DTREE_REQUIRE(a->n > 0 && a->n % tn == 0, "gemm: n must be a positive multiple of 64 (32 for > 64 rows)");
+  DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0, "gemm: k must be a positive multiple of 64");
   DTREE_REQUIRE(a->ldx >= a->k && a->ldx % 8 == 0, "gemm: ldx must be >= k and a multiple of 8");
-  const int ntiles = a->n / 32, nkb = a->k / 64;
+  const int ntiles = a->n / tn, nkb = a->k / 64;
   const int S = a->split_k > 0 ? a->split_k : auto_split(ntiles, nkb);
   DTREE_REQUIRE(S <= nkb, "gemm: split_k larger than the number of 64-wide K blocks");
+  DTREE_REQUIRE((size_t)ntiles * sizeof(int) <= kCounterBytes, "gemm: n too large for the tile counter region");
   const int epi = a->epilogue;
   DTREE_REQUIRE(epi >= 0 && epi <= 3, "gemm: unknown epilogue");
   if (epi == DTREE_EPI_STORE_F32 || epi == DTREE_EPI_RESIDUAL)
@@ -336,23 +404,23 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a->workspace && a->workspace_bytes >= need, "gemm: workspace too small");
 
   GemmParams p{};
-  p.x = a->x; p.ldx = a->ldx; p.w = a->w; p.n = a->n; p.k = a->k;
+  p.x = a->x; p.x_lo = a->x_lo; p.ldx = a->ldx; p.w = a->w; p.n = a->n; p.k = a->k;
   p.S = S; p.kb_per_split = (nkb + S - 1) / S; p.ntiles = ntiles;
   p.ss_in = a->ss_in; p.ss_tiles = a->ss_tiles;
   p.inv_norm_dim = a->norm_dim > 0 ? 1.0f / (float)a->norm_dim : 1.f; p.eps = a->eps;
   p.out_f32 = a->out_f32; p.ld_out_f32 = a->ld_out_f32;
-  p.out_bf16 = a->out_bf16; p.ld_out_bf16 = a->ld_out_bf16;
+  p.out_bf16 = a->out_bf16; p.out_lo = a->out_lo; p.ld_out_bf16 = a->ld_out_bf16;
   p.next_norm = a->next_norm; p.ss_out = a->ss_out;
   p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
   const size_t nt8 = (size_t)((ntiles + 7) / 8) * 8;
   p.counters = reinterpret_cast<int*>(a->workspace);
-  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + ((nt8 * sizeof(int) + 255) & ~(size_t)255));
+  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kCounterBytes);
   const int blocks = S == 1 ? ntiles : (int)(nt8 * S);
   switch (a->rows_padded) {
-    case 32: launch_gemm<1, 4>(p, epi, blocks, stream); break;
-    case 64: launch_gemm<2, 2>(p, epi, blocks, stream); break;
-    case 96: launch_gemm<3, 1>(p, epi, blocks, stream); break;
-    default: launch_gemm<4, 1>(p, epi, blocks, stream); break;
+    case 32: launch_gemm<1>(p, epi, blocks, stream); break;
+    case 64: launch_gemm<2>(p, epi, blocks, stream); break;
+    case 96: launch_gemm<3>(p, epi, blocks, stream); break;
+    default: launch_gemm<4>(p, epi, blocks, stream); break;
   }
   DTREE_LAUNCH_CHECK("gemm launch");
   return DTREE_OK;
@@ -362,24 +430,31 @@ extern "C" size_t dtree_lmhead_candidates_bytes(int32_t rows_padded) {
   return (size_t)1024 * rows_padded * sizeof(int2);
 }
 
-extern "C" int dtree_lmhead_argmax(const uint16_t* x, int32_t ldx, int32_t rows_padded, const uint16_t* emb,
-                                   int32_t vocab, int32_t hidden, const float* ss_in, int32_t ss_tiles,
-                                   float eps, float* logits, void* candidates, hipStream_t stream) {
+extern "C" int dtree_lmhead_candidate_blocks(int32_t vocab, int32_t rows_padded) {
+  const int tn = tile_cols(rows_padded);
+  return lmhead_grid(vocab / tn);
+}
+
+extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int32_t ldx, int32_t rows_padded,
+                                   const uint16_t* emb, int32_t vocab, int32_t hidden, const float* ss_in,
+                                   int32_t ss_tiles, float eps, float* logits, void* candidates,
+                                   hipStream_t stream) {
   DTREE_REQUIRE(x && emb && candidates, "lmhead: null pointer");
-  DTREE_REQUIRE(vocab > 0 && vocab % 32 == 0, "lmhead: vocab must be a multiple of 32");
-  DTREE_REQUIRE(hidden > 0 && hidden % 64 == 0 && ldx >= hidden, "lmhead: hidden must be a multiple of 64");
   DTREE_REQUIRE(rows_padded == 32 || rows_padded == 64 || rows_padded == 96 || rows_padded == 128,
                 "lmhead: rows_padded must be 32, 64, 96 or 128");
+  const int tn = tile_cols(rows_padded);
+  DTREE_REQUIRE(vocab > 0 && vocab % tn == 0, "lmhead: vocab must be a multiple of 64 (32 for > 64 rows)");
+  DTREE_REQUIRE(hidden > 0 && hidden % 64 == 0 && ldx >= hidden, "lmhead: hidden must be a multiple of 64");
   LmParams p{};
-  p.x = x; p.ldx = ldx; p.w = emb; p.vocab = vocab; p.k = hidden; p.ntiles = vocab / 32;
+  p.x = x; p.x_lo = x_lo; p.ldx = ldx; p.w = emb; p.vocab = vocab; p.k = hidden; p.ntiles = vocab / tn;
   p.ss_in = ss_in; p.ss_tiles = ss_tiles; p.inv_norm_dim = 1.0f / (float)hidden; p.eps = eps;
   p.logits = logits; p.cand = reinterpret_cast<int2*>(candidates);
   const int grid = lmhead_grid(p.ntiles);
   switch (rows_padded) {
-    case 32: lmhead_kernel<1, 4><<<grid, kThreads, 0, stream>>>(p); break;
-    case 64: lmhead_kernel<2, 2><<<grid, kThreads, 0, stream>>>(p); break;
-    case 96: lmhead_kernel<3, 1><<<grid, kThreads, 0, stream>>>(p); break;
-    default: lmhead_kernel<4, 1><<<grid, kThreads, 0, stream>>>(p); break;
+    case 32: launch_lm<1>(p, grid, stream); break;
+    case 64: launch_lm<2>(p, grid, stream); break;
+    case 96: launch_lm<3>(p, grid, stream); break;
+    default: launch_lm<4>(p, grid, stream); break;
   }
   DTREE_LAUNCH_CHECK("lmhead launch");
   return DTREE_OK;

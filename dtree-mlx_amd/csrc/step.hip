@@ -26,7 +26,8 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const DtreeStepDesc* de
 // x[m][:] = E[tokens[m]] (rows >= L zero), xg = bf16(x * g), ss[tile][m].
 // Blocks [0, H/256) gather; the remaining blocks fill the RoPE table.
 __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, const uint16_t* emb, int V, int H,
-                                                    const uint16_t* g, int MP, float* x, uint16_t* xg, float* ss,
+                                                    const uint16_t* g, int MP, float* x, uint16_t* xg,
+                                                    uint16_t* xg_lo, float* ss,
                                                     int half, float base, float* cos_out, float* sin_out,
                                                     int gather_blocks) {
   if ((int)blockIdx.x >= gather_blocks) {
@@ -46,7 +47,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
     }
     if (in) {
       x[(size_t)m * H + col] = v;
-      xg[(size_t)m * H + col] = f2bf(v * gw);
+      const float vg = v * gw;
+      const uint16_t hi = f2bf(vg);
+      xg[(size_t)m * H + col] = hi;
+      if (xg_lo) xg_lo[(size_t)m * H + col] = f2bf(vg - bf2f(hi));
     }
     float sq = v * v;
 #pragma unroll
@@ -205,8 +209,8 @@ extern "C" int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, 
 }
 
 extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t vocab, int32_t hidden,
-                           const uint16_t* norm_w,
-                           int32_t rows_padded, float* x, uint16_t* xg, float* ss, int32_t head_dim, float rope_base,
+                           const uint16_t* norm_w, int32_t rows_padded, float* x, uint16_t* xg, uint16_t* xg_lo,
+                           float* ss, int32_t head_dim, float rope_base,
                            float* rope_cos, float* rope_sin, hipStream_t stream) {
   DTREE_REQUIRE(desc && embed && norm_w && x && xg && ss, "embed: null pointer");
   DTREE_REQUIRE(hidden > 0 && hidden % 32 == 0, "embed: hidden must be a multiple of 32");
@@ -218,7 +222,7 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
     DTREE_REQUIRE(head_dim > 0 && head_dim % 2 == 0, "embed: head_dim");
     rope_blocks = (rows_padded * head_dim / 2 + 255) / 256;
   }
-  embed_kernel<<<gather + rope_blocks, 256, 0, stream>>>(desc, embed, vocab, hidden, norm_w, rows_padded, x, xg, ss,
+  embed_kernel<<<gather + rope_blocks, 256, 0, stream>>>(desc, embed, vocab, hidden, norm_w, rows_padded, x, xg, xg_lo, ss,
                                                           head_dim / 2, rope_base, rope_cos, rope_sin, gather);
   DTREE_LAUNCH_CHECK("embed launch");
   return DTREE_OK;

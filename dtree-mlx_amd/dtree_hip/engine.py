@@ -89,12 +89,13 @@ class Qwen3TreeEngine:
         H, F, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
         MP, dev = self.MP, self.dev
         f32, bf16 = torch.float32, torch.bfloat16
+        # GEMM inputs are split pairs [hi, lo] of bf16 planes (value = hi + lo).
         self.x = torch.zeros(MP, H, dtype=f32, device=dev)
-        self.xg = torch.zeros(MP, H, dtype=bf16, device=dev)
+        self.xg = torch.zeros(2, MP, H, dtype=bf16, device=dev)
         self.ss = torch.zeros(H // 32, MP, dtype=f32, device=dev)
         self.qkv = torch.zeros(MP, cfg.qkv_dim, dtype=f32, device=dev)
-        self.attn = torch.zeros(MP, cfg.q_dim, dtype=bf16, device=dev)
-        self.act = torch.zeros(MP, F, dtype=bf16, device=dev)
+        self.attn = torch.zeros(2, MP, cfg.q_dim, dtype=bf16, device=dev)
+        self.act = torch.zeros(2, MP, F, dtype=bf16, device=dev)
         self.rope_cos = torch.zeros(MP, cfg.head_dim // 2, dtype=f32, device=dev)
         self.rope_sin = torch.zeros(MP, cfg.head_dim // 2, dtype=f32, device=dev)
         self.norm_hidden = torch.zeros(MP, H, dtype=bf16, device=dev)
@@ -109,7 +110,7 @@ class Qwen3TreeEngine:
         self.gemm_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
         aws = self.lib.dtree_attention_workspace_bytes(cfg.num_attention_heads, cfg.head_dim, self.max_past)
         self.attn_ws = torch.zeros(aws, dtype=torch.uint8, device=dev)
-        self.n_cand = self.lib.dtree_lmhead_candidate_blocks(V)
+        self.n_cand = self.lib.dtree_lmhead_candidate_blocks(V, MP)
         self.cand = torch.zeros(self.lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=dev)
         self.desc_host = N.StepDesc()
         self.desc_pinned = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8).pin_memory()
@@ -191,7 +192,11 @@ class Qwen3TreeEngine:
                   ss_out=None, hidden_out=0, ld_hidden=0) -> N.GemmArgs:
         n, k = w.shape
         a = N.GemmArgs()
-        a.x = x.data_ptr(); a.ldx = ldx; a.rows_padded = self.MP
+        if x.dim() == 3:  # split pair [hi, lo]
+            a.x = x[0].data_ptr(); a.x_lo = x[1].data_ptr()
+        else:
+            a.x = x.data_ptr()
+        a.ldx = ldx; a.rows_padded = self.MP
         a.w = w.data_ptr(); a.n = n; a.k = k
         a.epilogue = epi; a.split_k = self.split_k.get(name, 0)
         a.ss_in = ss_in.data_ptr() if ss_in is not None else None
@@ -200,7 +205,11 @@ class Qwen3TreeEngine:
         if out_f32 is not None:
             a.out_f32 = out_f32.data_ptr(); a.ld_out_f32 = out_f32.shape[1]
         if out_bf16 is not None:
-            a.out_bf16 = out_bf16.data_ptr(); a.ld_out_bf16 = out_bf16.shape[1]
+            if out_bf16.dim() == 3:
+                a.out_bf16 = out_bf16[0].data_ptr(); a.out_lo = out_bf16[1].data_ptr()
+            else:
+                a.out_bf16 = out_bf16.data_ptr()
+            a.ld_out_bf16 = out_bf16.shape[-1]
         a.next_norm = next_norm.data_ptr() if next_norm is not None else None
         a.ss_out = ss_out.data_ptr() if ss_out is not None else None
         a.hidden_out = hidden_out or None; a.ld_hidden = ld_hidden
@@ -220,7 +229,7 @@ class Qwen3TreeEngine:
         a.rope_cos = self.rope_cos.data_ptr(); a.rope_sin = self.rope_sin.data_ptr()
         a.k_pages = cache.k_ptr(li); a.v_pages = cache.v_ptr(li); a.page_table = cache.page_table.data_ptr()
         a.desc = self.desc.data_ptr()
-        a.out = self.attn.data_ptr(); a.ld_out = self.attn.shape[1]
+        a.out = self.attn[0].data_ptr(); a.out_lo = self.attn[1].data_ptr(); a.ld_out = self.attn.shape[-1]
         a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
         a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
         a.max_past_length = self.max_past; a.write_cache = 1 if write_cache else 0
@@ -236,7 +245,7 @@ class Qwen3TreeEngine:
         N.check(self.lib.dtree_embed(
             self.desc.data_ptr(), self.w.embed.data_ptr(), c.vocab_size, H, self.w.layers[0].input_norm.data_ptr(),
             self.MP,
-            self.x.data_ptr(), self.xg.data_ptr(), self.ss.data_ptr(), c.head_dim, c.rope_theta,
+            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.ss.data_ptr(), c.head_dim, c.rope_theta,
             self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
         slot = {li: i for i, li in enumerate(self.layer_ids)}
         nL = c.num_hidden_layers
@@ -267,8 +276,9 @@ class Qwen3TreeEngine:
                 self.logits = torch.zeros(self.MP, c.vocab_size, dtype=torch.float32, device=self.dev)
             logits_ptr = self.logits.data_ptr()
         xin = self.xg if x is None else x
+        hi, lo = (xin[0].data_ptr(), xin[1].data_ptr()) if xin.dim() == 3 else (xin.data_ptr(), None)
         N.check(self.lib.dtree_lmhead_argmax(
-            xin.data_ptr(), xin.shape[1], self.MP, self.w.embed.data_ptr(), c.vocab_size, c.hidden_size,
+            hi, lo, xin.shape[-1], self.MP, self.w.embed.data_ptr(), c.vocab_size, c.hidden_size,
             self.ss.data_ptr() if ss else None, c.hidden_size // 32 if ss else 0, c.rms_norm_eps,
             logits_ptr, self.cand.data_ptr(), st), "lm head")
 

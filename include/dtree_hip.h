@@ -72,10 +72,11 @@ typedef struct DtreeStepDesc {
  */
 typedef struct DtreeGemmArgs {
   const uint16_t* x;      /* bf16 [rows_padded][ldx], rows >= L are zero   */
+  const uint16_t* x_lo;   /* optional low half: X = x + x_lo (both bf16)   */
   int32_t ldx;
   int32_t rows_padded;    /* 32, 64, 96 or 128                             */
   const uint16_t* w;      /* bf16 [n][k] (nn.Linear layout)                */
-  int32_t n, k;           /* n % 32 == 0, k % 64 == 0                      */
+  int32_t n, k;           /* k % 64 == 0; n % 64 == 0 (% 32 above 64 rows) */
   int32_t epilogue;       /* DTREE_EPI_*                                   */
   int32_t split_k;        /* >= 1; 0 = choose automatically                */
   const float* ss_in;     /* [ss_tiles][rows_padded] or NULL               */
@@ -83,7 +84,9 @@ typedef struct DtreeGemmArgs {
   int32_t norm_dim;       /* divisor of the row mean square                */
   float eps;
   float* out_f32; int32_t ld_out_f32;      /* STORE_F32 out / RESIDUAL x   */
-  uint16_t* out_bf16; int32_t ld_out_bf16; /* RESIDUAL xg / SWIGLU / BF16  */
+  uint16_t* out_bf16;     /* RESIDUAL xg / SWIGLU / BF16 output (hi half)  */
+  uint16_t* out_lo;       /* optional low half of out_bf16 (v - hi)        */
+  int32_t ld_out_bf16;
   const uint16_t* next_norm;  /* RESIDUAL: weight of the following RMSNorm */
   float* ss_out;              /* RESIDUAL: [n/32][rows_padded] sum of x^2  */
   uint16_t* hidden_out; int32_t ld_hidden; /* RESIDUAL: optional bf16 copy */
@@ -101,7 +104,8 @@ int dtree_gemm_bf16(const DtreeGemmArgs* args, hipStream_t stream);
 
 /*
  * Embedding gather + first RMSNorm fold (adapters.py:580, qwen3_tree.py:47):
- * x[m] = E[tokens[m]] (fp32), xg = bf16(x * norm_w), ss[t][m] = sum of x^2
+ * x[m] = E[tokens[m]] (fp32), xg = bf16(x * norm_w) (+ optional low half
+ * xg_lo = bf16(x * norm_w - xg)), ss[t][m] = sum of x^2
  * over column tile t (32 columns); rows >= L and token ids outside
  * [0, vocab) embed as zero. Also fills the RoPE
  * table cos/sin [rows_padded][head_dim/2] for desc->positions
@@ -109,7 +113,7 @@ int dtree_gemm_bf16(const DtreeGemmArgs* args, hipStream_t stream);
  */
 int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t vocab,
                 int32_t hidden, const uint16_t* norm_w, int32_t rows_padded, float* x, uint16_t* xg,
-                float* ss, int32_t head_dim, float rope_base, float* rope_cos,
+                uint16_t* xg_lo, float* ss, int32_t head_dim, float rope_base, float* rope_cos,
                 float* rope_sin, hipStream_t stream);
 
 /* RoPE table only (used when q/k come from outside dtree_embed). */
@@ -134,7 +138,7 @@ typedef struct DtreeAttnArgs {
   const float* rope_cos; const float* rope_sin;
   uint16_t* k_pages; uint16_t* v_pages; const int32_t* page_table;
   const DtreeStepDesc* desc;
-  uint16_t* out; int32_t ld_out;
+  uint16_t* out; uint16_t* out_lo; int32_t ld_out;  /* out_lo optional low half */
   int32_t num_heads, num_kv_heads, head_dim, rows_padded;
   float scale;
   int32_t max_past_length;  /* grid is sized for this P */
@@ -154,8 +158,8 @@ int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
  * logits (optional, [rows_padded][vocab] fp32) receives every logit.
  */
 size_t dtree_lmhead_candidates_bytes(int32_t rows_padded);
-int dtree_lmhead_candidate_blocks(int32_t vocab);
-int dtree_lmhead_argmax(const uint16_t* x, int32_t ldx, int32_t rows_padded,
+int dtree_lmhead_candidate_blocks(int32_t vocab, int32_t rows_padded);
+int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int32_t ldx, int32_t rows_padded,
                         const uint16_t* emb, int32_t vocab, int32_t hidden,
                         const float* ss_in, int32_t ss_tiles, float eps,
                         float* logits, void* candidates, hipStream_t stream);

@@ -30,14 +30,14 @@ def _gemm(x, w, epi, split, ws, **kw):
     for name in ("out_f32", "out_bf16"):
         t = kw.get(name)
         if t is not None:
-            setattr(a, name, t.data_ptr()); setattr(a, "ld_" + name, t.shape[1])
+            setattr(a, name, t.data_ptr()); setattr(a, "ld_" + name, t.stride(0))
     nn = kw.get("next_norm")
     a.next_norm = nn.data_ptr() if nn is not None else None
     so = kw.get("ss_out")
     a.ss_out = so.data_ptr() if so is not None else None
     hid = kw.get("hidden_out")
     if hid is not None:
-        a.hidden_out = hid.data_ptr(); a.ld_hidden = hid.shape[1]
+        a.hidden_out = hid.data_ptr(); a.ld_hidden = hid.stride(0)
     a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
     N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "gemm")
 
@@ -68,6 +68,56 @@ def test_gemm_store_f32_rowscale(gpu_device, MP, L, split):
     _gemm(x, w, N.EPI_STORE_F32, split, ws, ss_in=ss, norm_dim=K, out_f32=out2)
     torch.cuda.synchronize()
     assert torch.equal(out, out2)  # deterministic split-K reduction
+
+
+@pytest.mark.parametrize("MP", [32, 64, 128])
+def test_gemm_split_pair_input_and_output(gpu_device, MP):
+    """X = hi + lo (split bf16 pair) multiplies like an fp32 X; the split output
+    hi + lo carries the fp32 result to ~2^-16 relative."""
+    g = np.random.default_rng(31 + MP)
+    L, N_, K = MP - 5, 128, 512
+    xf = np.zeros((MP, K), np.float32)
+    xf[:L] = g.standard_normal((L, K))
+    hi = torch.from_numpy(xf).to(torch.bfloat16)
+    lo = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16)
+    x2 = torch.stack([hi, lo]).to(gpu_device)
+    w = torch.from_numpy(g.standard_normal((N_, K)).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu_device)
+    out = torch.zeros(2, MP, N_, dtype=torch.bfloat16, device=gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, N_, K, 2), dtype=torch.uint8, device=gpu_device)
+    a = N.GemmArgs()
+    a.x = x2[0].data_ptr(); a.x_lo = x2[1].data_ptr(); a.ldx = K; a.rows_padded = MP
+    a.w = w.data_ptr(); a.n = N_; a.k = K; a.epilogue = N.EPI_STORE_BF16; a.split_k = 2
+    a.out_bf16 = out[0].data_ptr(); a.out_lo = out[1].data_ptr(); a.ld_out_bf16 = N_
+    a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+    N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "gemm")
+    torch.cuda.synchronize()
+    ref = (hi.double() + lo.double()).numpy() @ bf16_f32(w).T.astype(np.float64)
+    got = out[0].double().cpu().numpy() + out[1].double().cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(ref).max()
+    # hi-only would be ~100x worse: the low half is really used
+    ref_hi = hi.double().numpy() @ bf16_f32(w).T.astype(np.float64)
+    assert np.abs(ref_hi - ref).max() > 10 * np.abs(got - ref).max()
+
+
+def test_gemm_shapes_share_one_workspace(gpu_device):
+    """Regression: a split-K GEMM with few column tiles followed by one with many
+    tiles on the same workspace (the layer sequence QKV -> gate/up). The first
+    one's partials must not land on the second one's tile counters."""
+    g = np.random.default_rng(21)
+    MP, L, K = 32, 25, 1024
+    x = _rows(MP, L, K, g, gpu_device)
+    w_small = torch.from_numpy(g.standard_normal((1536, K)).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu_device)
+    w_big = torch.from_numpy(g.standard_normal((4096, K)).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, 4096, K, 4), dtype=torch.uint8, device=gpu_device)
+    out_s = torch.zeros(MP, 1536, device=gpu_device)
+    out_b = torch.zeros(MP, 4096, device=gpu_device)
+    for _ in range(2):
+        _gemm(x, w_small, N.EPI_STORE_F32, 4, ws, out_f32=out_s)
+        _gemm(x, w_big, N.EPI_STORE_F32, 4, ws, out_f32=out_b)
+    torch.cuda.synchronize()
+    xf = bf16_f32(x).astype(np.float64)
+    np.testing.assert_allclose(out_s.cpu().numpy(), xf @ bf16_f32(w_small).T, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(out_b.cpu().numpy(), xf @ bf16_f32(w_big).T, rtol=1e-4, atol=1e-4)
 
 
 @pytest.mark.parametrize("split", [1, 4])
@@ -221,11 +271,11 @@ def _lmhead(x, E, dev, logits=None, ss=None):
     MP = x.shape[0]
     lib = N.lib()
     cand = torch.zeros(lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=dev)
-    N.check(lib.dtree_lmhead_argmax(x.data_ptr(), x.shape[1], MP, E.data_ptr(), E.shape[0], E.shape[1],
+    N.check(lib.dtree_lmhead_argmax(x.data_ptr(), None, x.shape[1], MP, E.data_ptr(), E.shape[0], E.shape[1],
                                     ss.data_ptr() if ss is not None else None, ss.shape[0] if ss is not None else 0,
                                     1e-6, logits.data_ptr() if logits is not None else None, cand.data_ptr(),
                                     stream()))
-    return cand, lib.dtree_lmhead_candidate_blocks(E.shape[0])
+    return cand, lib.dtree_lmhead_candidate_blocks(E.shape[0], MP)
 
 
 def _walk(cand, nblocks, desc, dev):

@@ -45,7 +45,7 @@ def test_argument_validation_without_gpu():
     assert b"null" in lib.dtree_last_error()
     a.x = 16; a.w = 16; a.n = 40; a.k = 64; a.ldx = 64; a.rows_padded = 32
     assert lib.dtree_gemm_bf16(C.byref(a), None) == -1
-    assert b"multiple of 32" in lib.dtree_last_error()
+    assert b"multiple of 64" in lib.dtree_last_error()
     a.n = 64; a.rows_padded = 48
     assert lib.dtree_gemm_bf16(C.byref(a), None) == -1
     assert b"rows_padded" in lib.dtree_last_error()
@@ -58,10 +58,11 @@ def test_argument_validation_without_gpu():
 
 def test_workspace_queries():
     lib = N.lib()
-    # split-K 1 needs only tile counters
-    assert lib.dtree_gemm_workspace_bytes(32, 2560, 4096, 1) == 80 * 4 + 256
+    # split-K 1 needs only the fixed tile-counter region
+    assert lib.dtree_gemm_workspace_bytes(32, 2560, 4096, 1) == 65536
     # split-K 8: counters + 80 tiles * 8 splits * 32x32 fp32
-    assert lib.dtree_gemm_workspace_bytes(32, 2560, 4096, 8) == 80 * 4 + 80 * 8 * 32 * 32 * 4 + 256
-    assert lib.dtree_lmhead_candidate_blocks(151936) == 1024
-    assert lib.dtree_lmhead_candidate_blocks(4096) == 128
+    assert lib.dtree_gemm_workspace_bytes(32, 2560, 4096, 8) == 65536 + 80 * 8 * 32 * 32 * 4
+    assert lib.dtree_lmhead_candidate_blocks(151936, 32) == 1024
+    assert lib.dtree_lmhead_candidate_blocks(4096, 32) == 64
+    assert lib.dtree_lmhead_candidate_blocks(4096, 128) == 128
     assert lib.dtree_attention_workspace_bytes(32, 128, 1024) > 32 * 9 * 32 * 128 * 4
