@@ -33,7 +33,7 @@ struct AttnParams {
   const float* rope_cos; const float* rope_sin;
   uint16_t* kp; uint16_t* vp; const int* page_table;
   const DtreeStepDesc* desc;
-  uint16_t* out; uint16_t* out_lo; int ld_out;
+  uint16_t* out; uint16_t* out_lo; int ld_out; int out_tiled;
   int Hq, Hkv, max_chunks;
   float scale_log2;
   int write_cache;
@@ -283,29 +283,28 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
 #pragma unroll
   for (int db = 0; db < ND; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) part[(size_t)c * D + 32 * db + acc_row(r, h)] = o[db][r];
+    for (int r = 0; r < 16; ++r) st_coherent(part + (size_t)c * D + 32 * db + acc_row(r, h), o[db][r]);
   if (h == 0) {
-    part[32 * D + c] = m_run;
-    part[32 * D + 32 + c] = l_tot;
+    st_coherent(part + 32 * D + c, m_run);
+    st_coherent(part + 32 * D + 32 + c, l_tot);
   }
-  fence_release();
+  wait_stores_done();
   __syncthreads();
   int last = 0;
-  if (lane == 0) last = atomicAdd(&p.counters[hq], 1) == nprefix;
+  if (lane == 0) last = arrive(&p.counters[hq]) == nprefix;
   last = __shfl(last, 0);
   if (!last) return;
-  fence_acquire();
-  if (lane == 0) p.counters[hq] = 0;
+  if (lane == 0) reset_counter(&p.counters[hq]);
 
   const int nc = nprefix + 1;
   const float* base = p.part + (size_t)hq * p.max_chunks * stride;
   if (lane < 32) {
     float M = kNeg;
-    for (int k = 0; k < nc; ++k) M = fmaxf(M, __builtin_nontemporal_load(base + k * stride + 32 * D + lane));
+    for (int k = 0; k < nc; ++k) M = fmaxf(M, ld_coherent(base + k * stride + 32 * D + lane));
     float tot = 0.f;
     for (int k = 0; k < nc; ++k) {
-      const float mk = __builtin_nontemporal_load(base + k * stride + 32 * D + lane);
-      const float lk = __builtin_nontemporal_load(base + k * stride + 32 * D + 32 + lane);
+      const float mk = ld_coherent(base + k * stride + 32 * D + lane);
+      const float lk = ld_coherent(base + k * stride + 32 * D + 32 + lane);
       const float wk = exp2f(mk - M);
       wts[k * 32 + lane] = wk;
       tot += lk * wk;
@@ -318,8 +317,8 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
     for (int d = lane; d < D; d += 64) {
       float acc = 0.f;
       if (q < L)
-        for (int k = 0; k < nc; ++k) acc += wts[k * 32 + q] * __builtin_nontemporal_load(base + k * stride + (size_t)q * D + d);
-      const size_t oi = (size_t)q * p.ld_out + hq * D + d;
+        for (int k = 0; k < nc; ++k) acc += wts[k * 32 + q] * ld_coherent(base + k * stride + (size_t)q * D + d);
+      const size_t oi = p.out_tiled ? tiled_index(q, hq * D + d, p.ld_out) : (size_t)q * p.ld_out + hq * D + d;
       const uint16_t hi = f2bf(acc);
       p.out[oi] = hi;
       if (p.out_lo) p.out_lo[oi] = f2bf(acc - bf2f(hi));
@@ -360,6 +359,10 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
   p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
   p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
+                    (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * a->head_dim && a->ld_out % 64 == 0),
+                "attention: tiled out needs ld_out == num_heads * head_dim");
+  p.out_tiled = a->out_layout == DTREE_W_TILED;
   p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.max_chunks = max_chunks;
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.counters = reinterpret_cast<int*>(a->workspace);

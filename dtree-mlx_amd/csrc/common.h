@@ -63,8 +63,33 @@ __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 *
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
-// Agent-scope release/acquire around split-K / split-KV partials.
-__device__ __forceinline__ void fence_release() { __threadfence(); }
-__device__ __forceinline__ void fence_acquire() { __threadfence(); }
+// Element (row r, column k) of a DTREE_W_TILED matrix with `width` columns:
+// [rows/32][width/64][4][64][8], lane l = r%32 + 32*((k%64)/32) of load i.
+__device__ __forceinline__ size_t tiled_index(int r, int k, int width) {
+  const int l = (r & 31) + 32 * ((k & 63) >> 5);
+  const int i = (k & 31) >> 3, e = k & 7;
+  return (((size_t)(r >> 5) * (width >> 6) + (k >> 6)) * 4 + i) * 512 + (size_t)l * 8 + e;
+}
+
+// Cross-workgroup hand-off of partial results without cache maintenance.
+// A device-scope __threadfence() writes back and invalidates the whole L2 of
+// the XCD (buffer_wbl2 / buffer_inv) and costs tens of microseconds when every
+// workgroup issues it. Partials are instead written and read with
+// agent-coherent (sc1) accesses; the producer waits for its stores to be
+// acknowledged (s_waitcnt) before the workgroup's counter increment, and the
+// last workgroup to arrive reads every partial coherently.
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores_done() { __builtin_amdgcn_s_waitcnt(0); }
+__device__ __forceinline__ int arrive(int* counter) {
+  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_counter(int* counter) {
+  __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 }  // namespace dtree

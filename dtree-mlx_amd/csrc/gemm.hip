@@ -40,12 +40,17 @@ struct GemmParams {
   int S, kb_per_split, ntiles;
   const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
   float* out_f32; int ld_out_f32;
-  uint16_t* out_bf16; uint16_t* out_lo; int ld_out_bf16;
+  uint16_t* out_bf16; uint16_t* out_lo; int ld_out_bf16; int out_tiled;
   const uint16_t* next_norm;
   float* ss_out;
   uint16_t* hidden_out; int ld_hidden;
   float* part; int* counters;
 };
+
+// Index of element (m, col) of a bf16 output with `ld` columns.
+__device__ __forceinline__ size_t out_index(int tiled, int m, int col, int ld) {
+  return tiled ? tiled_index(m, col, ld) : (size_t)m * ld + col;
+}
 
 // Split v into bf16 hi + bf16 lo (lo = bf16(v - hi)).
 __device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, size_t idx, float v) {
@@ -56,12 +61,17 @@ __device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, size_t i
 
 // Partial product of one tile (32*NB columns) over K blocks [kb0, kb1); the
 // waves' tiles are summed into red[0 .. MB*32*32*NB) laid out [row][col].
-template <int MB, int NB, int U, bool LO>
+// TILED: W is stored in the kernel's consumption order (DTREE_W_TILED), so
+// every load instruction of a wave reads one contiguous kilobyte.
+template <int MB, int NB, int U, bool LO, bool TILED>
 __device__ __forceinline__ void wg_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ xlo, int ldx,
                                         const uint16_t* __restrict__ w, int K, int tile, int kb0, int kb1,
                                         float* red) {
   constexpr int TN = 32 * NB;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // Wave index in a scalar register: the K loop below is then uniform
+  // control flow with scalar branches instead of an exec-masked loop.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 31, h = lane >> 5;
   f32x16_t acc[NB][MB];
 #pragma unroll
@@ -71,53 +81,76 @@ __device__ __forceinline__ void wg_tile(const uint16_t* __restrict__ x, const ui
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[nb][mb][r] = 0.f;
 
-  const uint16_t* wp = w + (size_t)(tile * TN + c) * K + 32 * h;
-  const size_t wnb = (size_t)32 * K;  // next 32-row weight block
-  const uint16_t* xp = x + (size_t)c * ldx + 32 * h;
-  const uint16_t* xq = LO ? xlo + (size_t)c * ldx + 32 * h : nullptr;
-  int kb = kb0 + wave;
-  for (; kb < kb1; kb += kWaves * U) {
-    u32x4_t wv[U][NB][4];
-    u32x4_t xv[U][MB][4];
-    u32x4_t xl[U][MB][4];
+  // Row-major: lane (c, h) reads row tile*TN + nb*32 + c, K offset 64*kk + 32h.
+  // Tiled ([N/32][K/64][4][64][8]): the 32-row x 64-K block (r32, kk) is 2048
+  // contiguous elements; load i of lane l reads elements (64*i + l)*8 .. +8
+  // of it, which hold the same K values as the row-major load.
+  const int nkb = K >> 6;
+  const uint16_t* wp = TILED ? w + (size_t)tile * NB * nkb * 2048 + lane * 8 : w + (size_t)(tile * TN + c) * K + 32 * h;
+  const size_t wnb = TILED ? (size_t)nkb * 2048 : (size_t)32 * K;  // next 32-row weight block
+  const size_t wkb = TILED ? 2048 : 64;                            // next K block
+  const int wi = TILED ? 512 : 8;                     // next 16-byte load of a lane
+  // Activations use the same layout as the weights (tiled: [MP/32][K/64]
+  // blocks of 2048 elements, so each activation load is one contiguous KB too).
+  const uint16_t* xp = TILED ? x + lane * 8 : x + (size_t)c * ldx + 32 * h;
+  const uint16_t* xq = LO ? (TILED ? xlo + lane * 8 : xlo + (size_t)c * ldx + 32 * h) : nullptr;
+  const size_t xmb = TILED ? (size_t)nkb * 2048 : (size_t)32 * ldx;  // next 32-row activation block
+  // Software pipeline over this wave's n K blocks (kb0 + wave + 4j): while
+  // block j is multiplied, block j+1's weights are already in flight in the
+  // other register set. Per block the activations are loaded first and the
+  // weight prefetch second, so waiting for the activations (loads retire in
+  // issue order) never waits for the prefetch. The loop runs whole pairs of
+  // blocks (A then B register set) plus an optional single tail block, so
+  // every prefetch is used on every path and cannot be sunk out of place; a
+  // prefetch past the end re-reads a 64-byte slice of the (L2-resident)
+  // activations instead of weights.
+  const int kfirst = kb0 + wave;
+  const int n = kfirst < kb1 ? (kb1 - kfirst + kWaves - 1) / kWaves : 0;
+  if (n > 0) {
+    u32x4_t wa[NB][4], wb[NB][4];
+    auto load_w = [&](u32x4_t (&dst)[NB][4], int j) {
+      const bool real = j < n;
+      const int kk = kfirst + kWaves * j;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kk = kb + kWaves * u;
-      if (U == 1 || kk < kb1) {
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint16_t* src = real ? wp + nb * wnb + (size_t)kk * wkb : xp;
+        const int step = real ? wi : 8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[nb][i] = ld_u32x4_stream(src + step * i);
+      }
+    };
+    auto step = [&](const u32x4_t (&wc)[NB][4], u32x4_t (&wn)[NB][4], int j, bool prefetch) {
+      const int kk = kfirst + kWaves * j;
+      u32x4_t xv[MB][4], xl[MB][4];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const size_t off = (size_t)mb * xmb + (size_t)kk * wkb + (size_t)wi * i;
+          xv[mb][i] = ld_u32x4(xp + off);
+          if (LO) xl[mb][i] = ld_u32x4(xq + off);
+        }
+      // Fixed issue order: activations, then the weight prefetch, then MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
+      if (prefetch) load_w(wn, j + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) wv[u][nb][i] = ld_u32x4_stream(wp + nb * wnb + (size_t)kk * 64 + 8 * i);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kk = kb + kWaves * u;
-      if (U == 1 || kk < kb1) {
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            xv[u][mb][i] = ld_u32x4(xp + (size_t)mb * 32 * ldx + (size_t)kk * 64 + 8 * i);
-            if (LO) xl[u][mb][i] = ld_u32x4(xq + (size_t)mb * 32 * ldx + (size_t)kk * 64 + 8 * i);
+          for (int mb = 0; mb < MB; ++mb) {
+            acc[nb][mb] = mfma32(xv[mb][i], wc[nb][i], acc[nb][mb]);
+            if (LO) acc[nb][mb] = mfma32(xl[mb][i], wc[nb][i], acc[nb][mb]);
           }
-      }
+    };
+    load_w(wa, 0);
+    int j = 0;
+    for (; j + 2 <= n; j += 2) {
+      step(wa, wb, j, true);      // block j+1 is always real here
+      step(wb, wa, j + 1, true);  // block j+2 may be past the end (dummy)
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kk = kb + kWaves * u;
-      if (U == 1 || kk < kb1) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
-              acc[nb][mb] = mfma32(xv[u][mb][i], wv[u][nb][i], acc[nb][mb]);
-              if (LO) acc[nb][mb] = mfma32(xl[u][mb][i], wv[u][nb][i], acc[nb][mb]);
-            }
-      }
-    }
+    if (j < n) step(wa, wb, j, false);
   }
 
   // Waves 1..3 park their tiles in LDS; wave 0 adds them in wave order, so
@@ -167,7 +200,7 @@ __device__ __forceinline__ void row_scale(const float* ss_in, int ss_tiles, floa
   }
 }
 
-template <int MB, int NB, int U, bool LO, int EPI>
+template <int MB, int NB, int U, bool LO, bool TILED, int EPI>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int MP = MB * 32;
   constexpr int TN = 32 * NB;
@@ -190,24 +223,23 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   const int kb0 = s * p.kb_per_split;
   const int kb1 = min(kb0 + p.kb_per_split, nkb);
 
-  wg_tile<MB, NB, U, LO>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, kb0, kb1, red);
+  wg_tile<MB, NB, U, LO, TILED>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, kb0, kb1, red);
 
   if (p.S > 1) {
     float* mine = p.part + ((size_t)tile * p.S + s) * TE;
-    for (int e = threadIdx.x; e < TE; e += kThreads) mine[e] = red[e];
-    fence_release();
+    for (int e = threadIdx.x; e < TE; e += kThreads) st_coherent(mine + e, red[e]);
+    wait_stores_done();
     __syncthreads();
-    if (threadIdx.x == 0) is_last = (atomicAdd(&p.counters[tile], 1) == p.S - 1);
+    if (threadIdx.x == 0) is_last = (arrive(&p.counters[tile]) == p.S - 1);
     __syncthreads();
     if (!is_last) return;
-    fence_acquire();
     const float* all = p.part + (size_t)tile * p.S * TE;
     for (int e = threadIdx.x; e < TE; e += kThreads) {
       float v = 0.f;
-      for (int q = 0; q < p.S; ++q) v += __builtin_nontemporal_load(all + (size_t)q * TE + e);
+      for (int q = 0; q < p.S; ++q) v += ld_coherent(all + (size_t)q * TE + e);
       red[e] = v;
     }
-    if (threadIdx.x == 0) p.counters[tile] = 0;
+    if (threadIdx.x == 0) reset_counter(&p.counters[tile]);
   }
   row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs);
   __syncthreads();
@@ -222,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   } else if constexpr (EPI == DTREE_EPI_STORE_BF16) {
     for (int e = threadIdx.x; e < TE; e += kThreads) {
       const int m = e / TN, n = e % TN;
-      split_store(p.out_bf16, p.out_lo, (size_t)m * p.ld_out_bf16 + tile * TN + n, red[e] * rs[m]);
+      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * TN + n, p.ld_out_bf16), red[e] * rs[m]);
     }
   } else if constexpr (EPI == DTREE_EPI_RESIDUAL) {
     const int n = threadIdx.x % TN;
@@ -233,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       float* xp = p.out_f32 + (size_t)m * p.ld_out_f32 + col;
       const float xv = *xp + red[e];
       *xp = xv;
-      split_store(p.out_bf16, p.out_lo, (size_t)m * p.ld_out_bf16 + col, xv * g);
+      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, col, p.ld_out_bf16), xv * g);
       if (p.hidden_out) p.hidden_out[(size_t)m * p.ld_hidden + col] = f2bf(xv);
       float sq = xv * xv;
 #pragma unroll
@@ -247,7 +279,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       const int sb = f >> 4, j = f & 15;
       const float gt = red[m * TN + sb * 32 + j] * rs[m];
       const float up = red[m * TN + sb * 32 + 16 + j] * rs[m];
-      split_store(p.out_bf16, p.out_lo, (size_t)m * p.ld_out_bf16 + tile * (TN / 2) + f, silu_f(gt) * up);
+      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * (TN / 2) + f, p.ld_out_bf16),
+                  silu_f(gt) * up);
     }
   }
 }
@@ -269,7 +302,7 @@ __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi)
   }
 }
 
-template <int MB, int NB, int U, bool LO>
+template <int MB, int NB, int U, bool LO, bool TILED>
 __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   constexpr int MP = MB * 32;
   constexpr int TN = 32 * NB;
@@ -289,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   const int n = threadIdx.x % TN;
   for (int tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     __syncthreads();
-    wg_tile<MB, NB, U, LO>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, 0, nkb, red);
+    wg_tile<MB, NB, U, LO, TILED>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, 0, nkb, red);
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int e = threadIdx.x + i * kThreads;
@@ -333,28 +366,46 @@ static int auto_split(int ntiles, int nkb) {
   return s;
 }
 
-template <int MB, bool LO>
+template <int MB, bool LO, bool TILED>
 static void launch_gemm_lo(const GemmParams& p, int epi, int blocks, hipStream_t st) {
   constexpr int NB = Cfg<MB>::NB, U = Cfg<MB>::U;
   switch (epi) {
-    case DTREE_EPI_STORE_F32: gemm_kernel<MB, NB, U, LO, DTREE_EPI_STORE_F32><<<blocks, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_RESIDUAL: gemm_kernel<MB, NB, U, LO, DTREE_EPI_RESIDUAL><<<blocks, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_SWIGLU: gemm_kernel<MB, NB, U, LO, DTREE_EPI_SWIGLU><<<blocks, kThreads, 0, st>>>(p); break;
-    default: gemm_kernel<MB, NB, U, LO, DTREE_EPI_STORE_BF16><<<blocks, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_STORE_F32:
+      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_STORE_F32><<<blocks, kThreads, 0, st>>>(p);
+      break;
+    case DTREE_EPI_RESIDUAL:
+      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_RESIDUAL><<<blocks, kThreads, 0, st>>>(p);
+      break;
+    case DTREE_EPI_SWIGLU:
+      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_SWIGLU><<<blocks, kThreads, 0, st>>>(p);
+      break;
+    default:
+      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_STORE_BF16><<<blocks, kThreads, 0, st>>>(p);
+      break;
   }
 }
 
 template <int MB>
-static void launch_gemm(const GemmParams& p, int epi, int blocks, hipStream_t st) {
-  if (p.x_lo) launch_gemm_lo<MB, true>(p, epi, blocks, st);
-  else launch_gemm_lo<MB, false>(p, epi, blocks, st);
+static void launch_gemm(const GemmParams& p, int epi, int blocks, hipStream_t st, bool tiled) {
+  if (p.x_lo) {
+    if (tiled) launch_gemm_lo<MB, true, true>(p, epi, blocks, st);
+    else launch_gemm_lo<MB, true, false>(p, epi, blocks, st);
+  } else {
+    if (tiled) launch_gemm_lo<MB, false, true>(p, epi, blocks, st);
+    else launch_gemm_lo<MB, false, false>(p, epi, blocks, st);
+  }
 }
 
 template <int MB>
-static void launch_lm(const LmParams& p, int grid, hipStream_t st) {
+static void launch_lm(const LmParams& p, int grid, hipStream_t st, bool tiled) {
   constexpr int NB = Cfg<MB>::NB, U = Cfg<MB>::U;
-  if (p.x_lo) lmhead_kernel<MB, NB, U, true><<<grid, kThreads, 0, st>>>(p);
-  else lmhead_kernel<MB, NB, U, false><<<grid, kThreads, 0, st>>>(p);
+  if (p.x_lo) {
+    if (tiled) lmhead_kernel<MB, NB, U, true, true><<<grid, kThreads, 0, st>>>(p);
+    else lmhead_kernel<MB, NB, U, true, false><<<grid, kThreads, 0, st>>>(p);
+  } else {
+    if (tiled) lmhead_kernel<MB, NB, U, false, true><<<grid, kThreads, 0, st>>>(p);
+    else lmhead_kernel<MB, NB, U, false, false><<<grid, kThreads, 0, st>>>(p);
+  }
 }
 
 // Workspace = a fixed counter region (so GEMMs of different shapes can share
@@ -410,17 +461,27 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   p.inv_norm_dim = a->norm_dim > 0 ? 1.0f / (float)a->norm_dim : 1.f; p.eps = a->eps;
   p.out_f32 = a->out_f32; p.ld_out_f32 = a->ld_out_f32;
   p.out_bf16 = a->out_bf16; p.out_lo = a->out_lo; p.ld_out_bf16 = a->ld_out_bf16;
+  p.out_tiled = a->out_layout == DTREE_W_TILED;
   p.next_norm = a->next_norm; p.ss_out = a->ss_out;
   p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
   const size_t nt8 = (size_t)((ntiles + 7) / 8) * 8;
   p.counters = reinterpret_cast<int*>(a->workspace);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kCounterBytes);
   const int blocks = S == 1 ? ntiles : (int)(nt8 * S);
+  const bool tiled = a->w_layout == DTREE_W_TILED;
+  DTREE_REQUIRE(a->w_layout == DTREE_W_ROWMAJOR || tiled, "gemm: unknown w_layout");
+  DTREE_REQUIRE(a->x_layout == a->w_layout, "gemm: x_layout must equal w_layout (both row-major or both tiled)");
+  DTREE_REQUIRE(!tiled || (a->ldx == a->k && a->rows_padded % 32 == 0), "gemm: tiled x needs ldx == k");
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR || a->out_layout == DTREE_W_TILED, "gemm: unknown out_layout");
+  if (a->out_layout == DTREE_W_TILED && a->out_bf16) {
+    const int width = epi == DTREE_EPI_SWIGLU ? a->n / 2 : a->n;
+    DTREE_REQUIRE(a->ld_out_bf16 == width && width % 64 == 0, "gemm: tiled out needs ld_out_bf16 == width, width % 64");
+  }
   switch (a->rows_padded) {
-    case 32: launch_gemm<1>(p, epi, blocks, stream); break;
-    case 64: launch_gemm<2>(p, epi, blocks, stream); break;
-    case 96: launch_gemm<3>(p, epi, blocks, stream); break;
-    default: launch_gemm<4>(p, epi, blocks, stream); break;
+    case 32: launch_gemm<1>(p, epi, blocks, stream, tiled); break;
+    case 64: launch_gemm<2>(p, epi, blocks, stream, tiled); break;
+    case 96: launch_gemm<3>(p, epi, blocks, stream, tiled); break;
+    default: launch_gemm<4>(p, epi, blocks, stream, tiled); break;
   }
   DTREE_LAUNCH_CHECK("gemm launch");
   return DTREE_OK;
@@ -435,8 +496,10 @@ extern "C" int dtree_lmhead_candidate_blocks(int32_t vocab, int32_t rows_padded)
   return lmhead_grid(vocab / tn);
 }
 
-extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int32_t ldx, int32_t rows_padded,
-                                   const uint16_t* emb, int32_t vocab, int32_t hidden, const float* ss_in,
+extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int32_t x_layout, int32_t ldx,
+                                   int32_t rows_padded,
+                                   const uint16_t* emb, int32_t emb_layout, int32_t vocab, int32_t hidden,
+                                   const float* ss_in,
                                    int32_t ss_tiles, float eps, float* logits, void* candidates,
                                    hipStream_t stream) {
   DTREE_REQUIRE(x && emb && candidates, "lmhead: null pointer");
@@ -450,11 +513,15 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
   p.ss_in = ss_in; p.ss_tiles = ss_tiles; p.inv_norm_dim = 1.0f / (float)hidden; p.eps = eps;
   p.logits = logits; p.cand = reinterpret_cast<int2*>(candidates);
   const int grid = lmhead_grid(p.ntiles);
+  DTREE_REQUIRE(emb_layout == DTREE_W_ROWMAJOR || emb_layout == DTREE_W_TILED, "lmhead: unknown emb_layout");
+  DTREE_REQUIRE(x_layout == emb_layout, "lmhead: x_layout must equal emb_layout");
+  DTREE_REQUIRE(emb_layout != DTREE_W_TILED || ldx == hidden, "lmhead: tiled x needs ldx == hidden");
+  const bool tiled = emb_layout == DTREE_W_TILED;
   switch (rows_padded) {
-    case 32: launch_lm<1>(p, grid, stream); break;
-    case 64: launch_lm<2>(p, grid, stream); break;
-    case 96: launch_lm<3>(p, grid, stream); break;
-    default: launch_lm<4>(p, grid, stream); break;
+    case 32: launch_lm<1>(p, grid, stream, tiled); break;
+    case 64: launch_lm<2>(p, grid, stream, tiled); break;
+    case 96: launch_lm<3>(p, grid, stream, tiled); break;
+    default: launch_lm<4>(p, grid, stream, tiled); break;
   }
   DTREE_LAUNCH_CHECK("lmhead launch");
   return DTREE_OK;

@@ -25,9 +25,10 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const DtreeStepDesc* de
 
 // x[m][:] = E[tokens[m]] (rows >= L zero), xg = bf16(x * g), ss[tile][m].
 // Blocks [0, H/256) gather; the remaining blocks fill the RoPE table.
-__global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, const uint16_t* emb, int V, int H,
+__global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, const uint16_t* emb, int tiled, int V,
+                                                    int H,
                                                     const uint16_t* g, int MP, float* x, uint16_t* xg,
-                                                    uint16_t* xg_lo, float* ss,
+                                                    uint16_t* xg_lo, int xg_tiled, float* ss,
                                                     int half, float base, float* cos_out, float* sin_out,
                                                     int gather_blocks) {
   if ((int)blockIdx.x >= gather_blocks) {
@@ -43,14 +44,16 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
     float v = 0.f;
     if (in && m < L) {
       const int tok = desc->tokens[m];
-      if (tok >= 0 && tok < V) v = bf2f(emb[(size_t)tok * H + col]);  // out-of-range ids embed as zero
+      if (tok >= 0 && tok < V)  // out-of-range ids embed as zero
+        v = bf2f(emb[tiled ? tiled_index(tok, col, H) : (size_t)tok * H + col]);
     }
     if (in) {
       x[(size_t)m * H + col] = v;
       const float vg = v * gw;
       const uint16_t hi = f2bf(vg);
-      xg[(size_t)m * H + col] = hi;
-      if (xg_lo) xg_lo[(size_t)m * H + col] = f2bf(vg - bf2f(hi));
+      const size_t xi = xg_tiled ? tiled_index(m, col, H) : (size_t)m * H + col;
+      xg[xi] = hi;
+      if (xg_lo) xg_lo[xi] = f2bf(vg - bf2f(hi));
     }
     float sq = v * v;
 #pragma unroll
@@ -192,9 +195,27 @@ __global__ __launch_bounds__(256) void rownorm_kernel(const float* x, int ldx, i
   for (int m = 0; m < MP; ++m) out[(size_t)m * ld_out + col] = f2bf(x[(size_t)m * ldx + col] * rs[m] * gw);
 }
 
+__global__ __launch_bounds__(256) void tile_weight_kernel(const uint16_t* src, uint16_t* dst, int n, int k) {
+  const size_t total = (size_t)n * k / 8;
+  for (size_t v = (size_t)blockIdx.x * 256 + threadIdx.x; v < total; v += (size_t)gridDim.x * 256) {
+    const int r = (int)(v / (k / 8)), k0 = (int)(v % (k / 8)) * 8;  // 8 consecutive columns of one row
+    *reinterpret_cast<u32x4_t*>(dst + tiled_index(r, k0, k)) = *reinterpret_cast<const u32x4_t*>(src + (size_t)r * k + k0);
+  }
+}
+
 }  // namespace dtree
 
 using namespace dtree;
+
+extern "C" int dtree_tile_weight(const uint16_t* src, uint16_t* dst, int32_t n, int32_t k, hipStream_t stream) {
+  DTREE_REQUIRE(src && dst && src != dst, "tile_weight: pointers");
+  DTREE_REQUIRE(n > 0 && k > 0 && n % 32 == 0 && k % 64 == 0, "tile_weight: n % 32 and k % 64");
+  const size_t total = (size_t)n * k / 8;
+  const int grid = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+  tile_weight_kernel<<<grid, 256, 0, stream>>>(src, dst, n, k);
+  DTREE_LAUNCH_CHECK("tile_weight launch");
+  return DTREE_OK;
+}
 
 extern "C" int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, int32_t head_dim, float rope_base,
                                 float* rope_cos, float* rope_sin, hipStream_t stream) {
@@ -208,13 +229,17 @@ extern "C" int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, 
   return DTREE_OK;
 }
 
-extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t vocab, int32_t hidden,
+extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t embed_layout, int32_t vocab,
+                           int32_t hidden,
                            const uint16_t* norm_w, int32_t rows_padded, float* x, uint16_t* xg, uint16_t* xg_lo,
-                           float* ss, int32_t head_dim, float rope_base,
+                           int32_t xg_layout, float* ss, int32_t head_dim, float rope_base,
                            float* rope_cos, float* rope_sin, hipStream_t stream) {
   DTREE_REQUIRE(desc && embed && norm_w && x && xg && ss, "embed: null pointer");
   DTREE_REQUIRE(hidden > 0 && hidden % 32 == 0, "embed: hidden must be a multiple of 32");
   DTREE_REQUIRE(vocab > 0, "embed: vocab");
+  DTREE_REQUIRE(embed_layout == DTREE_W_ROWMAJOR || (embed_layout == DTREE_W_TILED && hidden % 64 == 0 && vocab % 32 == 0),
+                "embed: layout");
+  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || (xg_layout == DTREE_W_TILED && hidden % 64 == 0), "embed: xg layout");
   DTREE_REQUIRE(rows_padded > 0 && rows_padded <= DTREE_MAX_NODES && rows_padded % 32 == 0, "embed: rows_padded");
   const int gather = (hidden + 255) / 256;
   int rope_blocks = 0;
@@ -222,7 +247,8 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
     DTREE_REQUIRE(head_dim > 0 && head_dim % 2 == 0, "embed: head_dim");
     rope_blocks = (rows_padded * head_dim / 2 + 255) / 256;
   }
-  embed_kernel<<<gather + rope_blocks, 256, 0, stream>>>(desc, embed, vocab, hidden, norm_w, rows_padded, x, xg, xg_lo, ss,
+  embed_kernel<<<gather + rope_blocks, 256, 0, stream>>>(desc, embed, embed_layout, vocab, hidden, norm_w, rows_padded,
+                                                          x, xg, xg_lo, xg_layout == DTREE_W_TILED, ss,
                                                           head_dim / 2, rope_base, rope_cos, rope_sin, gather);
   DTREE_LAUNCH_CHECK("embed launch");
   return DTREE_OK;

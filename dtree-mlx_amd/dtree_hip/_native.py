@@ -21,6 +21,9 @@ EPI_RESIDUAL = 1
 EPI_SWIGLU = 2
 EPI_STORE_BF16 = 3
 
+W_ROWMAJOR = 0
+W_TILED = 1
+
 
 class DtreeError(RuntimeError):
     pass
@@ -43,12 +46,13 @@ class StepDesc(C.Structure):
 
 class GemmArgs(C.Structure):
     _fields_ = [
-        ("x", C.c_void_p), ("x_lo", C.c_void_p), ("ldx", C.c_int32), ("rows_padded", C.c_int32),
-        ("w", C.c_void_p), ("n", C.c_int32), ("k", C.c_int32),
+        ("x", C.c_void_p), ("x_lo", C.c_void_p), ("x_layout", C.c_int32), ("ldx", C.c_int32),
+        ("rows_padded", C.c_int32),
+        ("w", C.c_void_p), ("w_layout", C.c_int32), ("n", C.c_int32), ("k", C.c_int32),
         ("epilogue", C.c_int32), ("split_k", C.c_int32),
         ("ss_in", C.c_void_p), ("ss_tiles", C.c_int32), ("norm_dim", C.c_int32), ("eps", C.c_float),
         ("out_f32", C.c_void_p), ("ld_out_f32", C.c_int32),
-        ("out_bf16", C.c_void_p), ("out_lo", C.c_void_p), ("ld_out_bf16", C.c_int32),
+        ("out_bf16", C.c_void_p), ("out_lo", C.c_void_p), ("out_layout", C.c_int32), ("ld_out_bf16", C.c_int32),
         ("next_norm", C.c_void_p), ("ss_out", C.c_void_p),
         ("hidden_out", C.c_void_p), ("ld_hidden", C.c_int32),
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
@@ -62,7 +66,7 @@ class AttnArgs(C.Structure):
         ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
         ("k_pages", C.c_void_p), ("v_pages", C.c_void_p), ("page_table", C.c_void_p),
         ("desc", C.c_void_p),
-        ("out", C.c_void_p), ("out_lo", C.c_void_p), ("ld_out", C.c_int32),
+        ("out", C.c_void_p), ("out_lo", C.c_void_p), ("ld_out", C.c_int32), ("out_layout", C.c_int32),
         ("num_heads", C.c_int32), ("num_kv_heads", C.c_int32), ("head_dim", C.c_int32),
         ("rows_padded", C.c_int32),
         ("scale", C.c_float),
@@ -81,13 +85,16 @@ SIGNATURES = {
     "dtree_step_desc_bytes": (_sz, []),
     "dtree_gemm_workspace_bytes": (_sz, [C.c_int, C.c_int, C.c_int, C.c_int]),
     "dtree_gemm_bf16": (C.c_int, [C.POINTER(GemmArgs), _vp]),
-    "dtree_embed": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _f32, _vp, _vp, _vp]),
+    "dtree_embed": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _vp, _vp,
+                              _vp]),
     "dtree_rope_table": (C.c_int, [_vp, _i32, _i32, _f32, _vp, _vp, _vp]),
     "dtree_attention_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "dtree_tree_attention": (C.c_int, [C.POINTER(AttnArgs), _vp]),
     "dtree_lmhead_candidates_bytes": (_sz, [_i32]),
     "dtree_lmhead_candidate_blocks": (C.c_int, [_i32, _i32]),
-    "dtree_lmhead_argmax": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _f32, _vp, _vp, _vp]),
+    "dtree_lmhead_argmax": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _i32, _f32, _vp, _vp,
+                                      _vp]),
+    "dtree_tile_weight": (C.c_int, [_vp, _vp, _i32, _i32, _vp]),
     "dtree_accept_walk": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "dtree_compact": (C.c_int, [_vp, _vp, _vp, _sz, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
     "dtree_rownorm": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _i32, _vp]),

@@ -99,7 +99,7 @@ class Qwen3TargetAdapter(MLXTargetAdapter):
 
     def embed_tokens(self, model: Qwen3TreeModel, tokens) -> torch.Tensor:
         ids = torch.as_tensor(tokens, device=model.weights.device).long()
-        return model.weights.embed[ids]
+        return model.weights.embed_rows(ids)
 
     def _rows(self, model, hidden_states):
         h = hidden_states.reshape(-1, hidden_states.shape[-1])

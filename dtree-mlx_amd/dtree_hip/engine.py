@@ -24,7 +24,7 @@ import torch
 from . import _native as N
 from .cache import PagedKVCache
 from .config import Qwen3Config
-from .weights import Qwen3Weights
+from .weights import W_TILED, Qwen3Weights, tile_weight
 
 
 def ancestor_bitsets(parents) -> np.ndarray:
@@ -197,7 +197,9 @@ class Qwen3TreeEngine:
         else:
             a.x = x.data_ptr()
         a.ldx = ldx; a.rows_padded = self.MP
-        a.w = w.data_ptr(); a.n = n; a.k = k
+        # Internal activations share the weights' layout (tiled: contiguous
+        # kilobyte loads for both GEMM operands).
+        a.w = w.data_ptr(); a.w_layout = self.w.layout; a.x_layout = self.w.layout; a.n = n; a.k = k
         a.epilogue = epi; a.split_k = self.split_k.get(name, 0)
         a.ss_in = ss_in.data_ptr() if ss_in is not None else None
         a.ss_tiles = self.cfg.hidden_size // 32 if ss_in is not None else 0
@@ -210,6 +212,7 @@ class Qwen3TreeEngine:
             else:
                 a.out_bf16 = out_bf16.data_ptr()
             a.ld_out_bf16 = out_bf16.shape[-1]
+            a.out_layout = self.w.layout
         a.next_norm = next_norm.data_ptr() if next_norm is not None else None
         a.ss_out = ss_out.data_ptr() if ss_out is not None else None
         a.hidden_out = hidden_out or None; a.ld_hidden = ld_hidden
@@ -230,6 +233,7 @@ class Qwen3TreeEngine:
         a.k_pages = cache.k_ptr(li); a.v_pages = cache.v_ptr(li); a.page_table = cache.page_table.data_ptr()
         a.desc = self.desc.data_ptr()
         a.out = self.attn[0].data_ptr(); a.out_lo = self.attn[1].data_ptr(); a.ld_out = self.attn.shape[-1]
+        a.out_layout = self.w.layout
         a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
         a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
         a.max_past_length = self.max_past; a.write_cache = 1 if write_cache else 0
@@ -243,9 +247,11 @@ class Qwen3TreeEngine:
         if cache.capacity < self.max_past + self.max_nodes:
             raise ValueError("cache capacity is smaller than max_past + max_nodes")
         N.check(self.lib.dtree_embed(
-            self.desc.data_ptr(), self.w.embed.data_ptr(), c.vocab_size, H, self.w.layers[0].input_norm.data_ptr(),
+            self.desc.data_ptr(), self.w.embed.data_ptr(), self.w.layout, c.vocab_size, H,
+            self.w.layers[0].input_norm.data_ptr(),
             self.MP,
-            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.ss.data_ptr(), c.head_dim, c.rope_theta,
+            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
+            c.head_dim, c.rope_theta,
             self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
         slot = {li: i for i, li in enumerate(self.layer_ids)}
         nL = c.num_hidden_layers
@@ -275,10 +281,16 @@ class Qwen3TreeEngine:
             if self.logits is None:
                 self.logits = torch.zeros(self.MP, c.vocab_size, dtype=torch.float32, device=self.dev)
             logits_ptr = self.logits.data_ptr()
-        xin = self.xg if x is None else x
+        if x is None:
+            xin = self.xg
+        elif self.w.layout == W_TILED:  # caller rows are row-major [MP, H]
+            self._lm_tiled = tile_weight(x)
+            xin = self._lm_tiled
+        else:
+            xin = x
         hi, lo = (xin[0].data_ptr(), xin[1].data_ptr()) if xin.dim() == 3 else (xin.data_ptr(), None)
         N.check(self.lib.dtree_lmhead_argmax(
-            hi, lo, xin.shape[-1], self.MP, self.w.embed.data_ptr(), c.vocab_size, c.hidden_size,
+            hi, lo, self.w.layout, xin.shape[-1], self.MP, self.w.embed.data_ptr(), self.w.layout, c.vocab_size, c.hidden_size,
             self.ss.data_ptr() if ss else None, c.hidden_size // 32 if ss else 0, c.rms_norm_eps,
             logits_ptr, self.cand.data_ptr(), st), "lm head")
 

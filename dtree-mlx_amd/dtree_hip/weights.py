@@ -10,6 +10,11 @@ Per layer (all bf16, nn.Linear [out, in] layout):
   input_norm, post_norm [H], q_norm, k_norm [head_dim]
 Global: embed [V, H] (tied LM head), final_norm [H].
 
+Linear weights and the embedding are stored in the GEMM's tiled layout
+(DTREE_W_TILED: [N/32][K/64][4][64][8], the order the kernel lanes consume, so
+every weight load instruction of a wavefront reads one contiguous kilobyte);
+``untile_weight`` restores nn.Linear order for host-side checks.
+
 Random init follows the synthetic workload: linear and embedding weights
 N(0, 0.02) in bf16, norm weights 1.
 """
@@ -21,6 +26,33 @@ import numpy as np
 import torch
 
 from .config import Qwen3Config
+
+
+W_ROWMAJOR, W_TILED = 0, 1
+
+
+def tile_weight(w: torch.Tensor) -> torch.Tensor:
+    """[n, k] row-major -> DTREE_W_TILED (same shape, permuted storage)."""
+    n, k = w.shape
+    if n % 32 or k % 64:
+        raise ValueError("tiled weights need n % 32 == 0 and k % 64 == 0")
+    t = w.reshape(n // 32, 32, k // 64, 2, 4, 8)        # r, c, b, h, i, e
+    return t.permute(0, 2, 4, 3, 1, 5).contiguous().reshape(n, k)  # r, b, i, (h, c), e
+
+
+def untile_weight(t: torch.Tensor) -> torch.Tensor:
+    n, k = t.shape
+    u = t.reshape(n // 32, k // 64, 4, 2, 32, 8)         # r, b, i, h, c, e
+    return u.permute(0, 4, 1, 3, 2, 5).contiguous().reshape(n, k)
+
+
+def tiled_rows(t: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """Rows of a tiled [n, k] matrix in row-major order (embedding lookups)."""
+    n, k = t.shape
+    v = t.reshape(n // 32, k // 64, 4, 2, 32, 8)
+    r = rows.long().reshape(-1)
+    g = v[r // 32, :, :, :, r % 32, :]                    # [R, b, i, h, e]
+    return g.permute(0, 1, 3, 2, 4).reshape(*rows.shape, k)
 
 
 def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
@@ -54,6 +86,7 @@ class Qwen3Weights:
     embed: torch.Tensor
     final_norm: torch.Tensor
     layers: list[LayerWeights] = field(default_factory=list)
+    layout: int = W_TILED
 
     @property
     def device(self) -> torch.device:
@@ -61,8 +94,9 @@ class Qwen3Weights:
 
     @classmethod
     def random(cls, cfg: Qwen3Config, seed: int = 0, device="cuda", std: float = 0.02,
-               norm_jitter: float = 0.0) -> "Qwen3Weights":
+               norm_jitter: float = 0.0, layout: int = W_TILED) -> "Qwen3Weights":
         """Seeded random init on `device` (norm weights 1, or 1 + N(0, jitter))."""
+        lay = tile_weight if layout == W_TILED else (lambda t: t)
         cfg.validate()
         dev = torch.device(device)
         gen = torch.Generator(device=dev)
@@ -80,26 +114,32 @@ class Qwen3Weights:
             return (1.0 + t).to(torch.bfloat16)
 
         H, F, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
-        embed = lin(cfg.vocab_size, H)
+        embed = lay(lin(cfg.vocab_size, H))
         layers = []
         for _ in range(cfg.num_hidden_layers):
-            wqkv = lin(cfg.qkv_dim, H)
-            wo = lin(H, cfg.q_dim)
+            wqkv = lay(lin(cfg.qkv_dim, H))
+            wo = lay(lin(H, cfg.q_dim))
             gate = lin(F, H)
             up = lin(F, H)
-            wd = lin(H, F)
+            wd = lay(lin(H, F))
             layers.append(LayerWeights(
                 input_norm=norm(H), wqkv=wqkv, q_norm=norm(D), k_norm=norm(D), wo=wo,
-                post_norm=norm(H), wgu=interleave_gate_up(gate, up), wd=wd))
+                post_norm=norm(H), wgu=lay(interleave_gate_up(gate, up)), wd=wd))
             del gate, up
-        return cls(cfg=cfg, embed=embed, final_norm=norm(H), layers=layers)
+        return cls(cfg=cfg, embed=embed, final_norm=norm(H), layers=layers, layout=layout)
 
     def to(self, device) -> "Qwen3Weights":
         mv = lambda t: t.to(device)  # noqa: E731
         return Qwen3Weights(
             cfg=self.cfg, embed=mv(self.embed), final_norm=mv(self.final_norm),
             layers=[LayerWeights(**{k: mv(getattr(lw, k)) for k in LayerWeights.__dataclass_fields__})
-                    for lw in self.layers])
+                    for lw in self.layers], layout=self.layout)
+
+    def rowmajor(self, t: torch.Tensor) -> torch.Tensor:
+        return untile_weight(t) if self.layout == W_TILED else t
+
+    def embed_rows(self, ids: torch.Tensor) -> torch.Tensor:
+        return tiled_rows(self.embed, ids) if self.layout == W_TILED else self.embed[ids.long()]
 
     def nbytes_linear(self) -> int:
         return sum(lw.wqkv.numel() + lw.wo.numel() + lw.wgu.numel() + lw.wd.numel()
@@ -113,12 +153,15 @@ class Qwen3Weights:
         def bits(t: torch.Tensor) -> np.ndarray:
             return t.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16)
 
+        def lin_bits(t: torch.Tensor) -> np.ndarray:
+            return bits(self.rowmajor(t))
+
         def get(layer, name):
             key = (layer, name)
             if key in cache:
                 return cache[key]
             if layer is None:
-                out = bits({"embed": self.embed, "final_norm": self.final_norm}[name])
+                out = lin_bits(self.embed) if name == "embed" else bits(self.final_norm)
                 if name == "embed":
                     cache[key] = out
                 return out
@@ -127,11 +170,13 @@ class Qwen3Weights:
             if name in ("q", "k", "v"):
                 lo = {"q": 0, "k": q, "v": q + kv}[name]
                 hi = lo + (q if name == "q" else kv)
-                return bits(lw.wqkv[lo:hi])
+                return bits(self.rowmajor(lw.wqkv)[lo:hi])
             if name in ("gate", "up"):
-                g, u = split_gate_up(lw.wgu)
+                g, u = split_gate_up(self.rowmajor(lw.wgu))
                 return bits(g if name == "gate" else u)
+            if name in ("o", "down"):
+                return lin_bits(lw.wo if name == "o" else lw.wd)
             return bits({"input_norm": lw.input_norm, "q_norm": lw.q_norm, "k_norm": lw.k_norm,
-                         "o": lw.wo, "post_norm": lw.post_norm, "down": lw.wd}[name])
+                         "post_norm": lw.post_norm}[name])
 
         return get

@@ -55,6 +55,19 @@ typedef struct DtreeStepDesc {
   int32_t posterior[DTREE_MAX_NODES];  /* out: target argmax per node         */
 } DtreeStepDesc;
 
+/*
+ * Weight layouts of an [n][k] bf16 matrix (nn.Linear layout).
+ *  DTREE_W_ROWMAJOR: plain [n][k].
+ *  DTREE_W_TILED:    [n/32][k/64][4][64][8]: block (r, b) holds rows 32r..32r+31
+ *                    and columns 64b..64b+63; element (i, l, e) of a block is
+ *                    row 32r + l%32, column 64b + 32*(l/32) + 8i + e. This is
+ *                    the order the GEMM lanes consume, so each 16-byte load
+ *                    instruction of a wavefront reads one contiguous kilobyte.
+ *                    dtree_tile_weight converts a row-major matrix.
+ */
+#define DTREE_W_ROWMAJOR 0
+#define DTREE_W_TILED 1
+
 /* GEMM epilogues (dtree_gemm_bf16). */
 #define DTREE_EPI_STORE_F32 0  /* out_f32[m][n] = rs[m] * acc                 */
 #define DTREE_EPI_RESIDUAL 1   /* x[m][n] += acc; xg = bf16(x*g_next); ss tile */
@@ -73,9 +86,11 @@ typedef struct DtreeStepDesc {
 typedef struct DtreeGemmArgs {
   const uint16_t* x;      /* bf16 [rows_padded][ldx], rows >= L are zero   */
   const uint16_t* x_lo;   /* optional low half: X = x + x_lo (both bf16)   */
+  int32_t x_layout;       /* DTREE_W_ROWMAJOR, or DTREE_W_TILED with ldx = k */
   int32_t ldx;
   int32_t rows_padded;    /* 32, 64, 96 or 128                             */
   const uint16_t* w;      /* bf16 [n][k] (nn.Linear layout)                */
+  int32_t w_layout;       /* DTREE_W_ROWMAJOR or DTREE_W_TILED             */
   int32_t n, k;           /* k % 64 == 0; n % 64 == 0 (% 32 above 64 rows) */
   int32_t epilogue;       /* DTREE_EPI_*                                   */
   int32_t split_k;        /* >= 1; 0 = choose automatically                */
@@ -86,6 +101,7 @@ typedef struct DtreeGemmArgs {
   float* out_f32; int32_t ld_out_f32;      /* STORE_F32 out / RESIDUAL x   */
   uint16_t* out_bf16;     /* RESIDUAL xg / SWIGLU / BF16 output (hi half)  */
   uint16_t* out_lo;       /* optional low half of out_bf16 (v - hi)        */
+  int32_t out_layout;     /* layout of out_bf16 / out_lo (TILED: ld = width) */
   int32_t ld_out_bf16;
   const uint16_t* next_norm;  /* RESIDUAL: weight of the following RMSNorm */
   float* ss_out;              /* RESIDUAL: [n/32][rows_padded] sum of x^2  */
@@ -104,16 +120,16 @@ int dtree_gemm_bf16(const DtreeGemmArgs* args, hipStream_t stream);
 
 /*
  * Embedding gather + first RMSNorm fold (adapters.py:580, qwen3_tree.py:47):
- * x[m] = E[tokens[m]] (fp32), xg = bf16(x * norm_w) (+ optional low half
+ * x[m] = E[tokens[m]] (fp32; E in DTREE_W_* layout embed_layout), xg = bf16(x * norm_w) (+ optional low half
  * xg_lo = bf16(x * norm_w - xg)), ss[t][m] = sum of x^2
  * over column tile t (32 columns); rows >= L and token ids outside
  * [0, vocab) embed as zero. Also fills the RoPE
  * table cos/sin [rows_padded][head_dim/2] for desc->positions
  * (mlx nn.RoPE, traditional=False, per-token offsets, qwen3_tree.py:22-27).
  */
-int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t vocab,
+int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t embed_layout, int32_t vocab,
                 int32_t hidden, const uint16_t* norm_w, int32_t rows_padded, float* x, uint16_t* xg,
-                uint16_t* xg_lo, float* ss, int32_t head_dim, float rope_base, float* rope_cos,
+                uint16_t* xg_lo, int32_t xg_layout, float* ss, int32_t head_dim, float rope_base, float* rope_cos,
                 float* rope_sin, hipStream_t stream);
 
 /* RoPE table only (used when q/k come from outside dtree_embed). */
@@ -139,6 +155,7 @@ typedef struct DtreeAttnArgs {
   uint16_t* k_pages; uint16_t* v_pages; const int32_t* page_table;
   const DtreeStepDesc* desc;
   uint16_t* out; uint16_t* out_lo; int32_t ld_out;  /* out_lo optional low half */
+  int32_t out_layout;       /* DTREE_W_ROWMAJOR or DTREE_W_TILED (ld_out = width) */
   int32_t num_heads, num_kv_heads, head_dim, rows_padded;
   float scale;
   int32_t max_past_length;  /* grid is sized for this P */
@@ -153,14 +170,15 @@ int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
 /*
  * Fused LM head + argmax (adapters.py:114-118, 489-492, first index on ties
  * as adapters.py:78-81): per row m, argmax_v rs[m] * (x[m] . E[v]).
+ * x = x + x_lo (split pair, x_lo optional); E in layout emb_layout.
  * Writes per-workgroup (value, index) candidates to `candidates`
  * ([grid][rows_padded] float2-like pairs); dtree_accept_walk reduces them.
  * logits (optional, [rows_padded][vocab] fp32) receives every logit.
  */
 size_t dtree_lmhead_candidates_bytes(int32_t rows_padded);
 int dtree_lmhead_candidate_blocks(int32_t vocab, int32_t rows_padded);
-int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int32_t ldx, int32_t rows_padded,
-                        const uint16_t* emb, int32_t vocab, int32_t hidden,
+int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int32_t x_layout, int32_t ldx, int32_t rows_padded,
+                        const uint16_t* emb, int32_t emb_layout, int32_t vocab, int32_t hidden,
                         const float* ss_in, int32_t ss_tiles, float eps,
                         float* logits, void* candidates, hipStream_t stream);
 
@@ -191,6 +209,10 @@ int dtree_compact(const DtreeStepDesc* desc, uint16_t* k_pages, uint16_t* v_page
 int dtree_rownorm(const float* x, int32_t ldx, int32_t rows_padded, int32_t hidden,
                   const float* ss_in, int32_t ss_tiles, const uint16_t* w, float eps,
                   uint16_t* out, int32_t ld_out, hipStream_t stream);
+
+/* Convert a row-major [n][k] bf16 matrix to DTREE_W_TILED (n % 32 == 0,
+ * k % 64 == 0; src and dst must not overlap). */
+int dtree_tile_weight(const uint16_t* src, uint16_t* dst, int32_t n, int32_t k, hipStream_t stream);
 
 /* HIP graph capture of a launch sequence (stands in for the mx.compile region
  * of qwen3_tree.py:38 and the per-step eval of dtree_runtime.py:480). */

@@ -10,6 +10,7 @@ import torch
 
 from dtree_hip import _native as N
 from dtree_hip.cache import PagedKVCache
+from dtree_hip.weights import tile_weight
 from oracle import qwen3 as oq
 from oracle import tree as otree
 
@@ -19,7 +20,12 @@ pytestmark = pytest.mark.gpu
 
 
 def _gemm(x, w, epi, split, ws, **kw):
+    """w is row-major; tiled=True hands the kernel its DTREE_W_TILED copy."""
     a = N.GemmArgs()
+    if kw.get("tiled"):  # tiled copies are freed stream-ordered, after the launch below
+        w = tile_weight(w)
+        x = tile_weight(x)
+        a.w_layout = a.x_layout = N.W_TILED
     a.x = x.data_ptr(); a.ldx = x.shape[1]; a.rows_padded = x.shape[0]
     a.w = w.data_ptr(); a.n = w.shape[0]; a.k = w.shape[1]
     a.epilogue = epi; a.split_k = split
@@ -50,7 +56,8 @@ def _rows(MP, L, K, g, dev, scale=1.0):
 
 @pytest.mark.parametrize("MP,L", [(32, 25), (32, 32), (64, 40), (96, 65), (128, 128)])
 @pytest.mark.parametrize("split", [1, 3, 8])
-def test_gemm_store_f32_rowscale(gpu_device, MP, L, split):
+@pytest.mark.parametrize("tiled", [False, True])
+def test_gemm_store_f32_rowscale(gpu_device, MP, L, split, tiled):
     g = np.random.default_rng(MP + split)
     N_, K = 256, 1024
     x = _rows(MP, L, K, g, gpu_device)
@@ -58,7 +65,7 @@ def test_gemm_store_f32_rowscale(gpu_device, MP, L, split):
     ss = torch.from_numpy(np.abs(g.standard_normal((5, MP))).astype(np.float32)).to(gpu_device)
     out = torch.zeros(MP, N_, device=gpu_device)
     ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, N_, K, split), dtype=torch.uint8, device=gpu_device)
-    _gemm(x, w, N.EPI_STORE_F32, split, ws, ss_in=ss, norm_dim=K, out_f32=out)
+    _gemm(x, w, N.EPI_STORE_F32, split, ws, ss_in=ss, norm_dim=K, out_f32=out, tiled=tiled)
     torch.cuda.synchronize()
     rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(0) / K + 1e-6)
     ref = (bf16_f32(x).astype(np.float64) @ bf16_f32(w).T.astype(np.float64)) * rs[:, None]
@@ -97,6 +104,15 @@ def test_gemm_split_pair_input_and_output(gpu_device, MP):
     # hi-only would be ~100x worse: the low half is really used
     ref_hi = hi.double().numpy() @ bf16_f32(w).T.astype(np.float64)
     assert np.abs(ref_hi - ref).max() > 10 * np.abs(got - ref).max()
+
+
+def test_tile_weight_kernel_matches_host_layout(gpu_device):
+    g = np.random.default_rng(41)
+    w = torch.from_numpy(g.standard_normal((96, 320)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    dst = torch.empty_like(w)
+    N.check(N.lib().dtree_tile_weight(w.data_ptr(), dst.data_ptr(), 96, 320, stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(dst, tile_weight(w))
 
 
 def test_gemm_shapes_share_one_workspace(gpu_device):
@@ -267,11 +283,14 @@ def test_tree_attention_gqa_small_and_deterministic(gpu_device):
     assert torch.equal(out, out2)
 
 
-def _lmhead(x, E, dev, logits=None, ss=None):
+def _lmhead(x, E, dev, logits=None, ss=None, layout=0):
     MP = x.shape[0]
     lib = N.lib()
     cand = torch.zeros(lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=dev)
-    N.check(lib.dtree_lmhead_argmax(x.data_ptr(), None, x.shape[1], MP, E.data_ptr(), E.shape[0], E.shape[1],
+    if layout == N.W_TILED:
+        x = tile_weight(x)
+    N.check(lib.dtree_lmhead_argmax(x.data_ptr(), None, layout, x.shape[1], MP, E.data_ptr(), layout, E.shape[0],
+                                    E.shape[1],
                                     ss.data_ptr() if ss is not None else None, ss.shape[0] if ss is not None else 0,
                                     1e-6, logits.data_ptr() if logits is not None else None, cand.data_ptr(),
                                     stream()))
@@ -288,13 +307,17 @@ def _walk(cand, nblocks, desc, dev):
 
 
 @pytest.mark.parametrize("V", [4096, 151936])
-def test_lmhead_argmax_and_logits(gpu_device, V):
+@pytest.mark.parametrize("tiled", [False, True])
+def test_lmhead_argmax_and_logits(gpu_device, V, tiled):
     g = np.random.default_rng(V)
     H, L = 2560, 25
     x = _rows(32, L, H, g, gpu_device)
     E = torch.from_numpy((g.standard_normal((V, H)) * 0.02).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
     logits = torch.zeros(32, V, device=gpu_device)
-    cand, nb = _lmhead(x, E, gpu_device, logits=logits)
+    if tiled:
+        cand, nb = _lmhead(x, tile_weight(E), gpu_device, logits=logits, layout=N.W_TILED)
+    else:
+        cand, nb = _lmhead(x, E, gpu_device, logits=logits)
     desc = device_desc([0] * L, [0] * L, [-1] + [0] * (L - 1), 0, gpu_device)
     _, _, post = _walk(cand, nb, desc, gpu_device)
     ref = bf16_f32(x)[:L] @ bf16_f32(E).T
