@@ -1,10 +1,17 @@
 // Ancestor-masked GQA tree attention over a paged bf16 KV prefix.
 //
-// One workgroup is one wavefront and owns (query head, key chunk): chunk 0 is
-// the tree itself (the L new keys, ancestor-or-self mask), chunks 1.. are
-// 128-key slices of the prefix (fully visible). Each chunk produces a
-// flash-decoding partial (row max, row sum, unnormalised output); the last
-// chunk of a head to finish (device-scope counter) merges them in chunk order.
+// Work split: the keys of one query head are cut into chunks. Chunk 0 is the
+// tree itself (the L new keys, ancestor-or-self mask); chunks 1.. are the
+// 64-key pages of the prefix (fully visible). A workgroup has four waves, one
+// chunk each, so workgroup `split` of a head owns chunks 4*split .. 4*split+3.
+// A wave owns exactly one chunk, so its softmax needs no running rescale: it
+// issues Q's loads, then all K and V of its page (32 KB in flight per wave),
+// scores both 32-key blocks, takes one max and accumulates P V.
+// The four waves merge in LDS; when a head needs more than one workgroup,
+// each writes a merged partial (row max, row sum, unnormalised output) and the
+// last one to arrive (device-scope counter) combines them, all 256 threads
+// with independent loads. The heads of one KV group run on one XCD
+// (blockIdx % 8), so their shared K/V reads meet in one L2.
 //
 // MFMA use (v_mfma_f32_32x32x16_bf16), with the tree rows (<= 32) as one
 // MFMA dimension:
@@ -22,8 +29,10 @@
 
 namespace dtree {
 
-constexpr int kChunkKeys = 128;  // prefix keys per chunk
-constexpr int kMaxChunks = 128;  // merge-weight capacity (prefix <= 16256)
+constexpr int kChunkKeys = DTREE_PAGE;  // prefix keys per chunk: one page
+constexpr int kWaves = 4;        // waves (chunks) per workgroup
+constexpr int kBlocks = kChunkKeys / 32;
+constexpr int kMaxChunks = 257;  // tree + 256 prefix pages (prefix <= 16384)
 constexpr float kNeg = -1e30f;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -34,7 +43,7 @@ struct AttnParams {
   uint16_t* kp; uint16_t* vp; const int* page_table;
   const DtreeStepDesc* desc;
   uint16_t* out; uint16_t* out_lo; int ld_out; int out_tiled;
-  int Hq, Hkv, max_chunks;
+  int Hq, Hkv, max_chunks, splits;
   float scale_log2;
   int write_cache;
   float* part; int* counters;
@@ -42,43 +51,72 @@ struct AttnParams {
 
 __device__ __forceinline__ int swap_bits23(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
 
-// Loads 64 values of row `row` (dims 16j + 8h + i) from an fp32 row, applies
-// an optional RMSNorm over D (with the partner lane^32) and RoPE.
+// Raw operands of one head row for lane (c, h), which owns dims 16j + 8h + i:
+// the fp32 values, the bf16 RMSNorm weights and the RoPE cos/sin of the first
+// half. Issuing all loads before any use lets a wave keep them in flight
+// together with the K/V loads that follow.
 template <int D>
-__device__ __forceinline__ void load_head_row(const float* src, const uint16_t* norm_w, float eps, bool rope,
-                                              const float* cosr, const float* sinr, int h,
-                                              float (&v)[D / 16][8]) {
+struct HeadRow {
+  f32x4_t x[D / 16][2];
+  u32x4_t nw[D / 16];
+  f32x4_t cs[D / 32][2], sn[D / 32][2];
+};
+
+template <int D>
+__device__ __forceinline__ void row_issue(HeadRow<D>& r, const float* src, const uint16_t* norm_w, const float* cosr,
+                                          const float* sinr, int h) {
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) {
+    r.x[j][0] = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h);
+    r.x[j][1] = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h + 4);
+    if (norm_w) r.nw[j] = ld_u32x4(norm_w + 16 * j + 8 * h);
+  }
+  if (cosr) {
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        r.cs[j][u] = *reinterpret_cast<const f32x4_t*>(cosr + 16 * j + 8 * h + 4 * u);
+        r.sn[j][u] = *reinterpret_cast<const f32x4_t*>(sinr + 16 * j + 8 * h + 4 * u);
+      }
+  }
+}
+
+// RMSNorm over D (sum of squares completed with the partner lane^32), then
+// RoPE on (dim d, dim d + D/2) pairs, which live in the same lane.
+template <int D>
+__device__ __forceinline__ void row_finish(const HeadRow<D>& r, bool norm, bool rope, float eps,
+                                           float (&v)[D / 16][8]) {
   constexpr int NJ = D / 16;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h);
-    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h + 4);
+  for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v[j][i] = a[i];
-      v[j][i + 4] = b[i];
+      v[j][i] = r.x[j][0][i];
+      v[j][i + 4] = r.x[j][1][i];
     }
-  }
-  if (norm_w) {
+  if (norm) {
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
     ss += __shfl_xor(ss, 32);
-    const float r = rsqrtf(ss * (1.0f / D) + eps);
+    const float rs = rsqrtf(ss * (1.0f / D) + eps);
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[j][i] *= r * bf2f(norm_w[16 * j + 8 * h + i]);
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t w = r.nw[j][i >> 1];
+        v[j][i] *= rs * __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+      }
   }
   if (rope) {
 #pragma unroll
     for (int j = 0; j < NJ / 2; ++j)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int d = 16 * j + 8 * h + i;
-        const float cs = cosr[d], sn = sinr[d];
+        const float cs = r.cs[j][i >> 2][i & 3], sn = r.sn[j][i >> 2][i & 3];
         const float x1 = v[j][i], x2 = v[j + NJ / 2][i];
         v[j][i] = x1 * cs - x2 * sn;
         v[j + NJ / 2][i] = x1 * sn + x2 * cs;
@@ -120,57 +158,233 @@ __device__ __forceinline__ void pv_step(const f32x16_t& p, int s2, const u32x4_t
   }
 }
 
-// Online-softmax update for one 32-key block; s[] already scaled (log2 units).
-template <int ND>
-__device__ __forceinline__ void softmax_block(f32x16_t& s, float& m_run, float& l_run, f32x16_t (&o)[ND]) {
+// Softmax numerators of NB 32-key blocks that start a chunk: every wave owns
+// exactly one chunk, so the running max starts here and no rescale exists.
+// s[] is already scaled (log2 units) and masked (kNeg).
+template <int NB>
+__device__ __forceinline__ void softmax_fresh(f32x16_t (&s)[NB], float& m_run, float& l_run) {
   float bmax = kNeg;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) bmax = fmaxf(bmax, s[r]);
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) bmax = fmaxf(bmax, s[b][r]);
   bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-  const float m_new = fmaxf(m_run, bmax);
-  const float alpha = exp2f(m_run - m_new);
   float lsum = 0.f;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    s[r] = exp2f(s[r] - m_new);
-    lsum += s[r];
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[b][r] = fast_exp2(s[b][r] - bmax);
+      lsum += s[b][r];
+    }
+  m_run = bmax;
+  l_run = lsum;
+}
+
+// Zeroes the bf16 elements of a V^T fragment whose key (first + e) is >= end:
+// keys past the prefix may hold stale or non-finite data, and 0 * NaN would
+// reach the output through the PV MFMA.
+__device__ __forceinline__ u32x4_t mask_keys(u32x4_t v, int first, int end) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo_ok = (first + 2 * i) < end ? 0xffffu : 0u;
+    const uint32_t hi_ok = (first + 2 * i + 1) < end ? 0xffff0000u : 0u;
+    v[i] &= lo_ok | hi_ok;
   }
-  l_run = l_run * alpha + lsum;
-#pragma unroll
-  for (int db = 0; db < ND; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-  m_run = m_new;
+  return v;
 }
 
 template <int D>
-__global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
-  constexpr int NJ = D / 16;  // 16-dim K steps of S^T
+__device__ __forceinline__ void q_fragments(const HeadRow<D>& qr, bool norm, float eps, u32x4_t (&qf)[D / 16],
+                                            u32x4_t (&ql)[D / 16]) {
+  float q[D / 16][8];
+  row_finish<D>(qr, norm, true, eps, q);
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) split8(q[j], qf[j], ql[j]);
+}
+
+// The tree chunk: q, k (norm + RoPE) and v of node c come from the fused qkv
+// row; k and v^T are staged in LDS (this wave's private region) for the MFMA
+// operand layouts, one 32-key block is scored with the ancestor-or-self mask,
+// and finally k/v are written to the cache rows P + c (one head per group).
+template <int D>
+__device__ __forceinline__ void tree_chunk(const AttnParams& p, int hq, int g, int G, int P, int L, int c, int h,
+                                           uint16_t* ks, uint16_t* vt, float& m_run, float& l_run,
+                                           f32x16_t (&o)[D / 32]) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  constexpr int KS = D + 8, VS = 32 + 8;
+  const int half_d = D / 2;
+  const float* row = p.qkv + (size_t)c * p.ld_qkv;
+  HeadRow<D> qr, kr, vr;
+  row_issue<D>(qr, row + hq * D, p.q_norm, p.rope_cos + c * half_d, p.rope_sin + c * half_d, h);
+  row_issue<D>(kr, row + (p.Hq + g) * D, p.k_norm, p.rope_cos + c * half_d, p.rope_sin + c * half_d, h);
+  row_issue<D>(vr, row + (p.Hq + p.Hkv + g) * D, nullptr, nullptr, nullptr, h);
+  const uint32_t anc = p.desc->ancestors[c][0];
+  u32x4_t qf[NJ], ql[NJ];
+  q_fragments<D>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  u32x4_t kf8[NJ], vf8[NJ];
+  {
+    float kv[NJ][8], vv[NJ][8];
+    row_finish<D>(kr, p.k_norm != nullptr, true, p.eps, kv);
+    row_finish<D>(vr, false, false, 0.f, vv);
+    pack_frag<D>(kv, kf8);
+    pack_frag<D>(vv, vf8);
+  }
+  if (c >= L) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) vf8[j] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    *reinterpret_cast<u32x4_t*>(&ks[c * KS + 16 * j + 8 * h]) = kf8[j];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t word = vf8[j][i >> 1];
+      vt[(16 * j + 8 * h + i) * VS + c] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
+    }
+  }
+  // Only this wave touches ks/vt, and a wave's LDS operations complete in
+  // order: waiting for them (and fencing the compiler) suffices.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int kr_row = swap_bits23(c);
+  f32x16_t s[1];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s[0][r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[kr_row * KS + 16 * j + 8 * h]);
+    s[0] = mfma32(a, qf[j], s[0]);
+    s[0] = mfma32(a, ql[j], s[0]);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int t = 16 * (r >> 3) + 8 * h + (r & 7);
+    const bool ok = c < L && t < L && ((anc >> t) & 1u);
+    s[0][r] = ok ? s[0][r] * p.scale_log2 : kNeg;
+  }
+  softmax_fresh<1>(s, m_run, l_run);
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    u32x4_t va[ND];
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+      va[db] = *reinterpret_cast<const u32x4_t*>(&vt[(32 * db + c) * VS + 16 * s2 + 8 * h]);
+    pv_step<ND>(s[0], s2, va, o);
+  }
+  if (p.write_cache && (hq % G) == 0 && c < L) {
+    const int pos = P + c;
+    const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
+    uint16_t* krow = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off) * D;
+    uint16_t* vcol = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      *reinterpret_cast<u32x4_t*>(krow + 16 * j + 8 * h) = kf8[j];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t word = vf8[j][i >> 1];
+        vcol[(size_t)(16 * j + 8 * h + i) * DTREE_PAGE] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
+      }
+    }
+  }
+}
+
+// One prefix chunk = one 64-key page. Q's loads go out first, then all K and V
+// of the page, so Q's norm/RoPE overlaps the K/V flight. Keys past the prefix
+// in the last page are masked (scores) and zeroed (V), since the page may hold
+// stale or non-finite data there.
+template <int D>
+__device__ __forceinline__ void prefix_chunk(const AttnParams& p, int hq, int g, int P, int chunk, int c, int h,
+                                             float& m_run, float& l_run, f32x16_t (&o)[D / 32]) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  const int half_d = D / 2;
+  HeadRow<D> qr;
+  row_issue<D>(qr, p.qkv + (size_t)c * p.ld_qkv + hq * D, p.q_norm, p.rope_cos + c * half_d,
+               p.rope_sin + c * half_d, h);
+  const int k_begin = (chunk - 1) * kChunkKeys;
+  const int k_end = min(k_begin + kChunkKeys, P);
+  const int page = p.page_table[k_begin / DTREE_PAGE];
+  const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + swap_bits23(c)) * D;
+  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE;
+  u32x4_t kf[kBlocks][NJ];
+  u32x4_t vf[kBlocks][2][ND];
+#pragma unroll
+  for (int b = 0; b < kBlocks; ++b) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) kf[b][j] = ld_u32x4_stream(kbase + (size_t)32 * b * D + 16 * j + 8 * h);
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int db = 0; db < ND; ++db)
+        vf[b][s2][db] = ld_u32x4_stream(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 32 * b + 16 * s2 + 8 * h);
+  }
+  u32x4_t qf[NJ], ql[NJ];
+  q_fragments<D>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+
+  f32x16_t s[kBlocks];
+#pragma unroll
+  for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+      s[b] = mfma32(kf[b][j], qf[j], s[b]);
+      s[b] = mfma32(kf[b][j], ql[j], s[b]);
+    }
+  const bool ragged = k_end - k_begin < kChunkKeys;
+#pragma unroll
+  for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = k_begin + 32 * b + 16 * (r >> 3) + 8 * h + (r & 7);
+      s[b][r] = (!ragged || key < k_end) ? s[b][r] * p.scale_log2 : kNeg;
+    }
+  softmax_fresh<kBlocks>(s, m_run, l_run);
+#pragma unroll
+  for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      u32x4_t va[ND];
+      const int first = k_begin + 32 * b + 16 * s2 + 8 * h;
+#pragma unroll
+      for (int db = 0; db < ND; ++db) va[db] = ragged ? mask_keys(vf[b][s2][db], first, k_end) : vf[b][s2][db];
+      pv_step<ND>(s[b], s2, va, o);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   constexpr int ND = D / 32;  // 32-dim blocks of O^T
   constexpr int KS = D + 8;   // padded LDS row of tree K
   constexpr int VS = 32 + 8;  // padded LDS row of tree V^T
-  __shared__ uint16_t ks[32 * KS];
-  __shared__ uint16_t vt[D * VS];
-  __shared__ float wts[kMaxChunks * 32];  // merge weights [chunk][query]; reused
+  constexpr int MS = 33;      // row stride of a wave's O^T in the LDS merge
+  constexpr int kWaveMerge = D * MS + 64;  // floats per wave: O^T, m, l
+  constexpr int kStage = (32 * KS + D * VS) * 2;
+  constexpr int kMerge = kWaves * kWaveMerge * 4;
+  __shared__ __align__(16) unsigned char lds[kStage > kMerge ? kStage : kMerge];
+  __shared__ int s_last;
+
+  // blockIdx -> (split, kv group, head in group): the G heads of one (split,
+  // group) pair share blockIdx % 8, i.e. one XCD.
+  const int G = p.Hq / p.Hkv;
+  const int bid = blockIdx.x;
+  const int pair = (bid / (8 * G)) * 8 + (bid & 7);
+  if (pair >= p.splits * p.Hkv) return;
+  const int g = pair % p.Hkv, split = pair / p.Hkv;
+  const int hq = g * G + (bid >> 3) % G;
 
   const int P = p.desc->past_length, L = p.desc->num_nodes;
-  const int nprefix = (P + kChunkKeys - 1) / kChunkKeys;
-  const int hq = blockIdx.x % p.Hq, chunk = blockIdx.x / p.Hq;
+  const int nchunks = 1 + (P + kChunkKeys - 1) / kChunkKeys;
   // A descriptor beyond the grid's capacity (P > max_past_length) or with more
   // than 32 rows leaves the output untouched instead of indexing past buffers.
-  if (chunk > nprefix || nprefix >= p.max_chunks || L > 32 || L < 1) return;
-  const int G = p.Hq / p.Hkv, g = hq / G;
-  const int lane = threadIdx.x, c = lane & 31, h = lane >> 5;
-  const int half_d = D / 2;
+  if (nchunks > p.max_chunks || L > 32 || L < 1) return;
+  const int nsplit = (nchunks + kWaves - 1) / kWaves;
+  if (split >= nsplit) return;
 
-  u32x4_t qf[NJ], ql[NJ];
-  {
-    float q[NJ][8];
-    load_head_row<D>(p.qkv + (size_t)c * p.ld_qkv + hq * D, p.q_norm, p.eps, true, p.rope_cos + c * half_d,
-                     p.rope_sin + c * half_d, h, q);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) split8(q[j], qf[j], ql[j]);
-  }
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int chunk = split * kWaves + wave;
 
   float m_run = kNeg, l_run = 0.f;
   f32x16_t o[ND];
@@ -180,149 +394,96 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
 
   if (chunk == 0) {
-    // The tree's own keys: build k (norm + RoPE) and v rows for node c.
-    float kr[NJ][8], vr[NJ][8];
-    load_head_row<D>(p.qkv + (size_t)c * p.ld_qkv + (p.Hq + g) * D, p.k_norm, p.eps, true,
-                     p.rope_cos + c * half_d, p.rope_sin + c * half_d, h, kr);
-    load_head_row<D>(p.qkv + (size_t)c * p.ld_qkv + (p.Hq + p.Hkv + g) * D, nullptr, 0.f, false, nullptr,
-                     nullptr, h, vr);
-    u32x4_t kf8[NJ], vf8[NJ];
-    pack_frag<D>(kr, kf8);
-    pack_frag<D>(vr, vf8);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      *reinterpret_cast<u32x4_t*>(&ks[c * KS + 16 * j + 8 * h]) = kf8[j];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t word = vf8[j][i >> 1];
-        vt[(16 * j + 8 * h + i) * VS + c] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
-      }
-    }
-    if (p.write_cache && (hq % G) == 0 && c < L) {
-      const int pos = P + c;
-      const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
-      uint16_t* krow = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off) * D;
-      uint16_t* vcol = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        *reinterpret_cast<u32x4_t*>(krow + 16 * j + 8 * h) = kf8[j];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t word = vf8[j][i >> 1];
-          vcol[(size_t)(16 * j + 8 * h + i) * DTREE_PAGE] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
-        }
-      }
-    }
-    __syncthreads();
-    const int kr_row = swap_bits23(c);
-    f32x16_t s;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[kr_row * KS + 16 * j + 8 * h]);
-      s = mfma32(a, qf[j], s);
-      s = mfma32(a, ql[j], s);
-    }
-    const uint32_t anc = p.desc->ancestors[c][0];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = 16 * (r >> 3) + 8 * h + (r & 7);
-      const bool ok = c < L && t < L && ((anc >> t) & 1u);
-      s[r] = ok ? s[r] * p.scale_log2 : kNeg;
-    }
-    softmax_block<ND>(s, m_run, l_run, o);
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      u32x4_t va[ND];
-#pragma unroll
-      for (int db = 0; db < ND; ++db)
-        va[db] = *reinterpret_cast<const u32x4_t*>(&vt[(32 * db + c) * VS + 16 * s2 + 8 * h]);
-      pv_step<ND>(s, s2, va, o);
-    }
-  } else {
-    const int k_begin = (chunk - 1) * kChunkKeys;
-    const int k_end = min(k_begin + kChunkKeys, P);
-    const int kr_off = swap_bits23(c);
-    for (int kb0 = k_begin; kb0 < k_end; kb0 += 32) {
-      const int page = p.page_table[kb0 / DTREE_PAGE];
-      const int off0 = kb0 % DTREE_PAGE;
-      const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off0 + kr_off) * D;
-      u32x4_t kf[NJ];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) kf[j] = ld_u32x4(kbase + 16 * j + 8 * h);
-      f32x16_t s;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        s = mfma32(kf[j], qf[j], s);
-        s = mfma32(kf[j], ql[j], s);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb0 + 16 * (r >> 3) + 8 * h + (r & 7);
-        s[r] = key < k_end ? s[r] * p.scale_log2 : kNeg;
-      }
-      softmax_block<ND>(s, m_run, l_run, o);
-      const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off0;
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        u32x4_t va[ND];
-#pragma unroll
-        for (int db = 0; db < ND; ++db) va[db] = ld_u32x4(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 16 * s2 + 8 * h);
-        pv_step<ND>(s, s2, va, o);
-      }
-    }
+    uint16_t* ks = reinterpret_cast<uint16_t*>(lds);
+    tree_chunk<D>(p, hq, g, G, P, L, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+  } else if (chunk < nchunks) {
+    prefix_chunk<D>(p, hq, g, P, chunk, c, h, m_run, l_run, o);
   }
 
-  // Partial for (head, chunk): O[q][d] unnormalised, m[q], l[q].
+  // LDS merge of the four waves. The first barrier retires the tree chunk's
+  // staging, which shares this memory.
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const size_t stride = (size_t)32 * D + 64;
-  float* part = p.part + ((size_t)hq * p.max_chunks + chunk) * stride;
+  __syncthreads();
+  float* mw = reinterpret_cast<float*>(lds) + wave * kWaveMerge;
 #pragma unroll
   for (int db = 0; db < ND; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) st_coherent(part + (size_t)c * D + 32 * db + acc_row(r, h), o[db][r]);
+    for (int r = 0; r < 16; ++r) mw[(32 * db + acc_row(r, h)) * MS + c] = o[db][r];
   if (h == 0) {
-    st_coherent(part + 32 * D + c, m_run);
-    st_coherent(part + 32 * D + 32 + c, l_tot);
+    mw[D * MS + c] = m_run;
+    mw[D * MS + 32 + c] = l_tot;
   }
-  wait_stores_done();
   __syncthreads();
-  int last = 0;
-  if (lane == 0) last = arrive(&p.counters[hq]) == nprefix;
-  last = __shfl(last, 0);
-  if (!last) return;
-  if (lane == 0) reset_counter(&p.counters[hq]);
 
-  const int nc = nprefix + 1;
-  const float* base = p.part + (size_t)hq * p.max_chunks * stride;
-  if (lane < 32) {
-    float M = kNeg;
-    for (int k = 0; k < nc; ++k) M = fmaxf(M, ld_coherent(base + k * stride + 32 * D + lane));
-    float tot = 0.f;
-    for (int k = 0; k < nc; ++k) {
-      const float mk = ld_coherent(base + k * stride + 32 * D + lane);
-      const float lk = ld_coherent(base + k * stride + 32 * D + 32 + lane);
-      const float wk = exp2f(mk - M);
-      wts[k * 32 + lane] = wk;
-      tot += lk * wk;
-    }
-    const float inv = tot > 0.f ? 1.0f / tot : 0.f;
-    for (int k = 0; k < nc; ++k) wts[k * 32 + lane] *= inv;
+  // Thread t combines query q = t/8, dims d0 .. d0+15 with d0 = 16 (t%8).
+  constexpr int kDims = 32 * D / (64 * kWaves);  // 16 for D = 128
+  const int t = threadIdx.x;
+  const int q = t >> 3, d0 = (t & 7) * kDims;
+  const float* m0 = reinterpret_cast<const float*>(lds);
+  float M = kNeg;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m0[w * kWaveMerge + D * MS + q]);
+  float acc[kDims];
+#pragma unroll
+  for (int i = 0; i < kDims; ++i) acc[i] = 0.f;
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float* mv = m0 + w * kWaveMerge;
+    const float wk = fast_exp2(mv[D * MS + q] - M);
+    tot += wk * mv[D * MS + 32 + q];
+#pragma unroll
+    for (int i = 0; i < kDims; ++i) acc[i] += wk * mv[(d0 + i) * MS + q];
   }
-  __syncthreads();
-  for (int q = 0; q < 32; ++q) {
-    for (int d = lane; d < D; d += 64) {
-      float acc = 0.f;
-      if (q < L)
-        for (int k = 0; k < nc; ++k) acc += wts[k * 32 + q] * ld_coherent(base + k * stride + (size_t)q * D + d);
-      const size_t oi = p.out_tiled ? tiled_index(q, hq * D + d, p.ld_out) : (size_t)q * p.ld_out + hq * D + d;
-      const uint16_t hi = f2bf(acc);
-      p.out[oi] = hi;
-      if (p.out_lo) p.out_lo[oi] = f2bf(acc - bf2f(hi));
+
+  if (nsplit > 1) {
+    // Workgroup partial, laid out [i][thread] so both the stores here and the
+    // loads of the combining workgroup are coalesced.
+    const size_t stride = (size_t)32 * D + 64;
+    float* part = p.part + ((size_t)hq * p.splits + split) * stride;
+#pragma unroll
+    for (int i = 0; i < kDims; ++i) st_coherent(part + (size_t)i * 64 * kWaves + t, acc[i]);
+    if ((t & 7) == 0) {
+      st_coherent(part + 32 * D + q, M);
+      st_coherent(part + 32 * D + 32 + q, tot);
     }
+    wait_stores_done();
+    __syncthreads();
+    if (t == 0) s_last = arrive(&p.counters[hq]) == nsplit - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (t == 0) reset_counter(&p.counters[hq]);
+
+    const float* base = p.part + (size_t)hq * p.splits * stride;
+    float Ms = kNeg;
+    for (int s = 0; s < nsplit; ++s) Ms = fmaxf(Ms, ld_coherent(base + s * stride + 32 * D + q));
+#pragma unroll
+    for (int i = 0; i < kDims; ++i) acc[i] = 0.f;
+    tot = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float* ps = base + s * stride;
+      float v[kDims];
+#pragma unroll
+      for (int i = 0; i < kDims; ++i) v[i] = ld_coherent(ps + (size_t)i * 64 * kWaves + t);
+      const float wk = fast_exp2(ld_coherent(ps + 32 * D + q) - Ms);
+      tot += wk * ld_coherent(ps + 32 * D + 32 + q);
+#pragma unroll
+      for (int i = 0; i < kDims; ++i) acc[i] += wk * v[i];
+    }
+  }
+
+  const float inv = (q < L && tot > 0.f) ? 1.0f / tot : 0.f;
+#pragma unroll
+  for (int i0 = 0; i0 < kDims; i0 += 8) {
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = q < L ? acc[i0 + i] * inv : 0.f;
+    u32x4_t hi, lo;
+    split8(y, hi, lo);
+    const int col = hq * D + d0 + i0;
+    const size_t oi = p.out_tiled ? tiled_index(q, col, p.ld_out) : (size_t)q * p.ld_out + col;
+    *reinterpret_cast<u32x4_t*>(p.out + oi) = hi;
+    if (p.out_lo) *reinterpret_cast<u32x4_t*>(p.out_lo + oi) = lo;
   }
 }
 
@@ -331,11 +492,13 @@ __global__ __launch_bounds__(64) void tree_attn_kernel(AttnParams p) {
 using namespace dtree;
 
 static int attn_max_chunks(int max_past) { return 1 + (max_past + kChunkKeys - 1) / kChunkKeys; }
+static int attn_splits(int max_past) { return (attn_max_chunks(max_past) + kWaves - 1) / kWaves; }
 
 extern "C" size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length) {
   if (num_heads <= 0 || head_dim <= 0 || max_past_length < 0) return 0;
   const size_t stride = (size_t)32 * head_dim + 64;
-  return 256 + (size_t)num_heads * sizeof(int) + (size_t)num_heads * attn_max_chunks(max_past_length) * stride * sizeof(float);
+  return (((size_t)num_heads * sizeof(int) + 255) & ~(size_t)255) +
+         (size_t)num_heads * attn_splits(max_past_length) * stride * sizeof(float);
 }
 
 extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
@@ -349,27 +512,33 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   DTREE_REQUIRE(a->max_past_length >= 0, "attention: max_past_length");
   DTREE_REQUIRE(a->ld_qkv >= (a->num_heads + 2 * a->num_kv_heads) * a->head_dim && a->ld_qkv % 4 == 0,
                 "attention: ld_qkv too small");
-  DTREE_REQUIRE(a->ld_out >= a->num_heads * a->head_dim, "attention: ld_out too small");
+  DTREE_REQUIRE(a->ld_out >= a->num_heads * a->head_dim && a->ld_out % 8 == 0,
+                "attention: ld_out below num_heads * head_dim or not a multiple of 8");
+  DTREE_REQUIRE(((uintptr_t)a->out & 15) == 0 && ((uintptr_t)a->out_lo & 15) == 0,
+                "attention: out and out_lo must be 16-byte aligned");
   const int max_chunks = attn_max_chunks(a->max_past_length);
-  DTREE_REQUIRE(max_chunks <= kMaxChunks, "attention: max_past_length beyond 16256");
+  DTREE_REQUIRE(max_chunks <= kMaxChunks, "attention: max_past_length beyond 16384");
   DTREE_REQUIRE(a->workspace_bytes >= dtree_attention_workspace_bytes(a->num_heads, a->head_dim, a->max_past_length),
                 "attention: workspace too small");
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
+                    (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * a->head_dim && a->ld_out % 64 == 0),
+                "attention: tiled out needs ld_out == num_heads * head_dim");
   AttnParams p{};
   p.qkv = a->qkv; p.ld_qkv = a->ld_qkv; p.q_norm = a->q_norm; p.k_norm = a->k_norm; p.eps = a->eps;
   p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
   p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
   p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
-  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
-                    (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * a->head_dim && a->ld_out % 64 == 0),
-                "attention: tiled out needs ld_out == num_heads * head_dim");
   p.out_tiled = a->out_layout == DTREE_W_TILED;
   p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.max_chunks = max_chunks;
+  p.splits = attn_splits(a->max_past_length);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.counters = reinterpret_cast<int*>(a->workspace);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) +
                                     (((size_t)a->num_heads * sizeof(int) + 255) & ~(size_t)255));
-  const int grid = a->num_heads * max_chunks;
-  tree_attn_kernel<128><<<grid, 64, 0, stream>>>(p);
+  const int G = p.Hq / p.Hkv;
+  const int pairs = p.splits * p.Hkv;
+  const int grid = ((pairs + 7) / 8) * 8 * G;
+  tree_attn_kernel<128><<<grid, 64 * kWaves, 0, stream>>>(p);
   DTREE_LAUNCH_CHECK("attention launch");
   return DTREE_OK;
 }

@@ -65,4 +65,7 @@ def test_workspace_queries():
     assert lib.dtree_lmhead_candidate_blocks(151936, 32) == 1024
     assert lib.dtree_lmhead_candidate_blocks(4096, 32) == 64
     assert lib.dtree_lmhead_candidate_blocks(4096, 128) == 128
-    assert lib.dtree_attention_workspace_bytes(32, 128, 1024) > 32 * 9 * 32 * 128 * 4
+    # attention: head counters (256-byte aligned) + one partial per head per
+    # 4-chunk workgroup; prefix 1024 = tree + 16 pages = 5 workgroups per head
+    assert lib.dtree_attention_workspace_bytes(32, 128, 1024) == 256 + 32 * 5 * (32 * 128 + 64) * 4
+    assert lib.dtree_attention_workspace_bytes(32, 128, 0) == 256 + 32 * 1 * (32 * 128 + 64) * 4
