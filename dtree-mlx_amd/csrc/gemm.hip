@@ -360,9 +360,13 @@ static int tile_cols(int rows_padded) { return rows_padded <= 64 ? 64 : 32; }
 
 static int lmhead_grid(int ntiles) { return ntiles < 1024 ? ntiles : 1024; }
 
+// Split-K only while the grid stays within one workgroup per CU (256) and
+// every split keeps at least 16 K blocks: each split costs a partial-tile
+// round trip through memory at the end, so splitting pays only where it
+// brings otherwise idle CUs into the weight stream.
 static int auto_split(int ntiles, int nkb) {
   int s = 1;
-  while (s * 2 * ntiles <= 1024 && nkb / (s * 2) >= 4) s *= 2;
+  while ((s + 1) * ntiles <= 256 && nkb / (s + 1) >= 16) ++s;
   return s;
 }
 
