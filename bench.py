@@ -176,6 +176,21 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int) -> dict:
     return out
 
 
+def copy_probe(mib: int) -> None:
+    """Five copies of `mib` MiB between two device buffers: each dispatch reads
+    and writes exactly mib MiB, which calibrates the profiler's FETCH_SIZE and
+    WRITE_SIZE counters against known traffic."""
+    import torch
+
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] copy probe: 5 x {mib} MiB")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -185,7 +200,13 @@ def main():
     ap.add_argument("--budget", type=int, default=24)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=108)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 5 device copies of MIB MiB (the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     a = ap.parse_args()
+    if a.copy_probe:
+        copy_probe(a.copy_probe)
+        return
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (the verify step is not sharded across GPUs); got --gpus {a.gpus}",
               file=sys.stderr)

@@ -20,14 +20,8 @@ DrHB/dtree-mlx checkout):
   SDPA, RoPE, RMSNorm, LM head + first-index argmax (``adapters.py:28-118,
   489-492``), KV compaction (``adapters.py:635-668``). Pinned by closed forms
   and special cases (chain tree == causal attention, star tree == prefix +
-  self, L=1 == decode attention, RoPE vs complex rotation, fp64 re-evaluation).
-- ``q4``     : 4-bit group-64 affine dequant + matmul (``adapters.py:63-71``;
-  MLX ``quantized_matmul`` semantics). Pinned by exact integer unpacking and
-  a dense fp64 matmul on the dequantised weight.
-- ``gdn``    : parent-indexed causal conv1d + SiLU and gated-delta recurrence
-  (``qwen35_tree_kernels.py:8-152``). Pinned by the numpy loops the reference
-  tests hold (``tests/test_qwen35_tree_kernels.py:17-98``), reproduced with the
-  same seeds, and by the chain-tree special case (sequential gated delta rule).
+  self, L=1 == decode attention, RoPE vs complex rotation, fp64 re-evaluation,
+  and a cross-check of the decoder layer against transformers' Qwen3).
 
 Parity unpinned (MLX internals that only an MLX import could pin): the exact
 rounding / accumulation order of ``mx.fast.scaled_dot_product_attention``,
