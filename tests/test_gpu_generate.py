@@ -1,0 +1,118 @@
+"""End-to-end DTree decoding on the GPU through the reference-shaped surface.
+
+``dtree_generate`` (dtree_runtime.py:293-586) drives the HIP target through the
+adapter methods of adapters.py (forward_with_hidden_states, embed_tokens,
+lm_head_logits / lm_head_argmax, forward_tree_with_hidden_states,
+compact_kv_caches) or the fused verify graph. At temperature 0, speculative
+decoding must emit the target's greedy continuation whatever the drafter
+proposes: every emitted token is checked against the fp32 oracle run over the
+emitted sequence itself (teacher forcing), to be its argmax within the 2e-2
+relative logit tolerance (and exactly its argmax on nearly every position).
+
+The drafter is scripted: it proposes a continuation through the tied
+LM head (hidden row = 24 * E[token], so the draft logits peak at that token)
+following the target's own sequential greedy decode on the GPU, and plants one wrong token at a depth that cycles over the steps, so the
+accepted lengths cover 1 .. the full chain."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qwen3 as oq
+
+from dtree_hip.adapters import load_target_model
+from dtree_hip.config import tiny_qwen3
+from dtree_hip.dtree_runtime import dtree_generate
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+BLOCK = 8
+
+
+def _oracle_teacher_forced(target, seq):
+    """fp32 oracle logits of every position of `seq` under a causal mask
+    (row i predicts seq[i + 1])."""
+    cfg = target.model.args
+    ocfg = oq.Qwen3Config(hidden=cfg.hidden_size, layers=cfg.num_hidden_layers, ffn=cfg.intermediate_size,
+                          heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+                          vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_base=cfg.rope_theta)
+    orc = oq.OracleQwen3(ocfg, target.model.weights.host_accessor())
+    nl, Hkv, D = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+    empty = oq.OracleCache(keys=[np.zeros((0, Hkv, D), np.float32)] * nl,
+                           values=[np.zeros((0, Hkv, D), np.float32)] * nl)
+    T = len(seq)
+    norm, _, _, _ = orc.forward_tree(np.asarray(seq, np.int64), np.arange(T), np.tril(np.ones((T, T), bool)), empty)
+    return orc.lm_head_logits(norm)
+
+
+def _gpu_sequential_greedy(target, prompt, n_new):
+    """The target's greedy continuation one token per forward (chain of 1)."""
+    cache = target.make_cache()
+    logits, _ = target.forward_with_hidden_states(torch.tensor(prompt)[None], cache, [0, 1])
+    out = [int(torch.argmax(logits[0, -1]).item())]
+    while len(out) < n_new:
+        logits, _ = target.forward_with_hidden_states(torch.tensor([out[-1]])[None], cache, [0, 1])
+        out.append(int(torch.argmax(logits[0, -1]).item()))
+    return out
+
+
+class ScriptedDrafter:
+    """Drafter with the interface dtree_generate uses (draft.py:312-367 shape):
+    mask_token_id, block_size, make_cache(), __call__(noise_embedding,
+    target_hidden, cache) -> hidden [1, block, H]."""
+
+    mask_token_id = 0
+    block_size = BLOCK
+
+    def __init__(self, target, seq):
+        self.target = target
+        self.seq = seq  # prompt + oracle continuation
+
+    def make_cache(self):
+        return {"pos": None, "calls": 0}
+
+    def __call__(self, noise_embedding, target_hidden, cache):
+        # The target hidden rows handed over are the committed tokens since the
+        # last call (the prompt first), so their running count is the root's position.
+        n = int(target_hidden.shape[1])
+        cache["pos"] = n if cache["pos"] is None else cache["pos"] + n
+        start = cache["pos"]
+        wrong = cache["calls"] % BLOCK  # 0: whole chain right, else the depth that is wrong
+        cache["calls"] += 1
+        V = self.target.model.args.vocab_size
+        toks = []
+        for d in range(BLOCK):
+            p = start + d
+            t = self.seq[p] if p < len(self.seq) else (7 * p) % V
+            if d == wrong and d > 0:
+                t = (t + 1) % V
+            toks.append(t)
+        E = self.target.model.weights.embed_rows(torch.tensor(toks, device="cuda")).float()
+        return (24.0 * E)[None]
+
+
+@pytest.mark.parametrize("verify_mode", ["parallel-greedy-argmax", "parallel-replay"])
+def test_dtree_generate_emits_greedy_tokens(gpu_device, verify_mode):
+    cfg = tiny_qwen3()
+    target = load_target_model(cfg, seed=0, max_past=256, device="cuda", layer_ids=[0, 1])
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(1, cfg.vocab_size, 40).tolist()
+    n_new = 40
+    plan = _gpu_sequential_greedy(target, prompt, n_new)
+    drafter = ScriptedDrafter(target, prompt + plan)
+    out, metrics = dtree_generate(target, drafter, prompt, max_new_tokens=n_new, temperature=0.0,
+                                  stop_token_ids=set(), layer_ids=[0, 1], speculative_tokens=BLOCK,
+                                  tree_budget=12, verify_mode=verify_mode, tree_topk=4)
+    gen = out[len(prompt):]
+    assert len(gen) == n_new
+    # Every emitted token is the oracle's argmax within the logit tolerance,
+    # given the tokens before it, and nearly all are its exact argmax.
+    logits = _oracle_teacher_forced(target, out[:-1])[len(prompt) - 1:]
+    scale = np.abs(logits).max(axis=-1)
+    chosen = logits[np.arange(n_new), gen]
+    assert np.all(chosen >= logits.max(axis=-1) - TOL * scale)
+    assert np.mean(np.argmax(logits, axis=-1) == np.asarray(gen)) >= 0.9
+    # The drafter proposed the target's own greedy path with one planted error
+    # per step, so acceptance lengths span single tokens to long chains.
+    acc = metrics["acceptance_lengths"]
+    assert max(acc) >= 5 and min(acc) == 1, acc
