@@ -9,10 +9,11 @@ proposes: every emitted token is checked against the fp32 oracle run over the
 emitted sequence itself (teacher forcing), to be its argmax within the 2e-2
 relative logit tolerance (and exactly its argmax on nearly every position).
 
-The drafter is scripted: it proposes a continuation through the tied
-LM head (hidden row = 24 * E[token], so the draft logits peak at that token)
-following the target's own sequential greedy decode on the GPU, and plants one wrong token at a depth that cycles over the steps, so the
-accepted lengths cover 1 .. the full chain."""
+The drafter is scripted: it proposes the target's own sequential greedy decode
+(computed on the GPU beforehand) through the tied LM head (hidden row =
+24 * E[token], so the draft logits peak at that token), and plants one wrong
+token at a depth that cycles over the steps, so the accepted lengths cover
+1 .. the full chain."""
 import numpy as np
 import pytest
 import torch
