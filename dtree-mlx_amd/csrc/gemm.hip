@@ -45,6 +45,8 @@ struct GemmParams {
   float* ss_out;
   uint16_t* hidden_out; int ld_hidden;
   float* part; int* counters;
+  // stream-K schedule: T = (n/64) * (k/64) units over G workgroups
+  int T, G; unsigned part_bytes;
 };
 
 // Index of element (m, col) of a bf16 output with `ld` columns.
@@ -185,19 +187,118 @@ __device__ __forceinline__ void wg_tile(const uint16_t* __restrict__ x, const ui
   __syncthreads();
 }
 
+// RMSNorm row scale rs[m] = rsqrt(sum_t ss_in[t][m] * inv_dim + eps) (1 when
+// ss_in is null) with every thread of the workgroup: thread (part, m) owns
+// tiles part, part + kThreads/MP, ...; ss_issue puts its first kSsBatch loads
+// in flight at once (issue them before other long loads: loads retire in
+// order), ss_finish adds the rest, and the parts are added in a fixed order.
+// ss_finish contains one barrier; callers barrier again before reading rs.
+constexpr int kSsBatch = 16;
+
 template <int MB>
-__device__ __forceinline__ void row_scale(const float* ss_in, int ss_tiles, float inv_dim, float eps,
-                                          float* rs) {
-  constexpr int MP = MB * 32;
-  if (threadIdx.x < MP) {
-    float v = 1.f;
-    if (ss_in) {
-      float s = 0.f;
-      for (int t = 0; t < ss_tiles; ++t) s += ss_in[t * MP + threadIdx.x];
-      v = rsqrtf(s * inv_dim + eps);
-    }
-    rs[threadIdx.x] = v;
+__device__ __forceinline__ void ss_issue(const float* ss_in, int ss_tiles, float (&v)[kSsBatch]) {
+  constexpr int MP = MB * 32, TPR = kThreads / MP;
+  const int m = threadIdx.x % MP, part = threadIdx.x / MP;
+#pragma unroll
+  for (int i = 0; i < kSsBatch; ++i) {
+    const int t = part + i * TPR;
+    v[i] = (ss_in && t < ss_tiles) ? ss_in[(size_t)t * MP + m] : 0.f;
   }
+}
+
+template <int MB>
+__device__ __forceinline__ void ss_finish(const float* ss_in, int ss_tiles, float inv_dim, float eps,
+                                          const float (&v)[kSsBatch], float* rs, float* scratch) {
+  constexpr int MP = MB * 32, TPR = kThreads / MP;
+  const int m = threadIdx.x % MP, part = threadIdx.x / MP;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kSsBatch; ++i) s += v[i];
+  if (ss_in) {
+    for (int base = kSsBatch * TPR; base < ss_tiles; base += kSsBatch * TPR) {
+      float w[kSsBatch];
+#pragma unroll
+      for (int i = 0; i < kSsBatch; ++i) {
+        const int t = base + part + i * TPR;
+        w[i] = t < ss_tiles ? ss_in[(size_t)t * MP + m] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < kSsBatch; ++i) s += w[i];
+    }
+  }
+  scratch[threadIdx.x] = s;
+  __syncthreads();
+  if (threadIdx.x < MP) {
+    float r = 1.f;
+    if (ss_in) {
+      float tot = 0.f;
+      for (int q = 0; q < TPR; ++q) tot += scratch[q * MP + threadIdx.x];
+      r = rsqrtf(tot * inv_dim + eps);
+    }
+    rs[threadIdx.x] = r;
+  }
+}
+
+template <int MB>
+__device__ __forceinline__ void row_scale(const float* ss_in, int ss_tiles, float inv_dim, float eps, float* rs,
+                                          float* scratch) {
+  float v[kSsBatch];
+  ss_issue<MB>(ss_in, ss_tiles, v);
+  ss_finish<MB>(ss_in, ss_tiles, inv_dim, eps, v, rs, scratch);
+}
+
+// Epilogue of one finished tile held in LDS as red[row * TN + col] (row scale
+// rs[] applied here). Element e of the tile: row e / TN, column e % TN; with
+// TN in {32, 64} and 256 threads a 32-column group of one row is held by 32
+// consecutive lanes.
+template <int MP, int TN, int EPI>
+__device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* red, const float* rs, int tile) {
+  constexpr int TE = MP * TN;
+  if constexpr (EPI == DTREE_EPI_STORE_F32) {
+    for (int e = threadIdx.x; e < TE; e += kThreads) {
+      const int m = e / TN, n = e % TN;
+      p.out_f32[(size_t)m * p.ld_out_f32 + tile * TN + n] = red[e] * rs[m];
+    }
+  } else if constexpr (EPI == DTREE_EPI_STORE_BF16) {
+    for (int e = threadIdx.x; e < TE; e += kThreads) {
+      const int m = e / TN, n = e % TN;
+      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * TN + n, p.ld_out_bf16), red[e] * rs[m]);
+    }
+  } else if constexpr (EPI == DTREE_EPI_RESIDUAL) {
+    constexpr int IT = TE / kThreads;
+    const int n = threadIdx.x % TN;
+    const int col = tile * TN + n;
+    const float g = bf2f(p.next_norm[col]);
+    // All residual loads first, so they are in flight together.
+    float xo[IT];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) xo[i] = p.out_f32[(size_t)((threadIdx.x + i * kThreads) / TN) * p.ld_out_f32 + col];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int e = threadIdx.x + i * kThreads;
+      const int m = e / TN;
+      float* xp = p.out_f32 + (size_t)m * p.ld_out_f32 + col;
+      const float xv = xo[i] + red[e];
+      *xp = xv;
+      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, col, p.ld_out_bf16), xv * g);
+      if (p.hidden_out) p.hidden_out[(size_t)m * p.ld_hidden + col] = f2bf(xv);
+      float sq = xv * xv;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+      if ((n & 31) == 0) p.ss_out[(size_t)(col >> 5) * MP + m] = sq;
+    }
+  } else if constexpr (EPI == DTREE_EPI_SWIGLU) {
+    // Each 32-column group = 16 gate rows then 16 up rows of 16 FFN features.
+    for (int e = threadIdx.x; e < MP * TN / 2; e += kThreads) {
+      const int m = e / (TN / 2), f = e % (TN / 2);
+      const int sb = f >> 4, j = f & 15;
+      const float gt = red[m * TN + sb * 32 + j] * rs[m];
+      const float up = red[m * TN + sb * 32 + 16 + j] * rs[m];
+      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * (TN / 2) + f, p.ld_out_bf16),
+                  silu_f(gt) * up);
+    }
+  }
+
 }
 
 template <int MB, int NB, int U, bool LO, bool TILED, int EPI>
@@ -207,6 +308,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int TE = MP * TN;  // tile elements
   __shared__ float red[(kWaves - 1) * TE];
   __shared__ float rs[MP];
+  __shared__ float rs_scratch[kThreads];
   __shared__ int is_last;
 
   int tile, s;
@@ -241,47 +343,207 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
     }
     if (threadIdx.x == 0) reset_counter(&p.counters[tile]);
   }
-  row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs);
+  row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs, rs_scratch);
   __syncthreads();
 
-  // Element e of the tile: row e / TN, column e % TN. With TN in {32, 64} and
-  // 256 threads, a 32-column group of one row is held by 32 consecutive lanes.
-  if constexpr (EPI == DTREE_EPI_STORE_F32) {
-    for (int e = threadIdx.x; e < TE; e += kThreads) {
-      const int m = e / TN, n = e % TN;
-      p.out_f32[(size_t)m * p.ld_out_f32 + tile * TN + n] = red[e] * rs[m];
-    }
-  } else if constexpr (EPI == DTREE_EPI_STORE_BF16) {
-    for (int e = threadIdx.x; e < TE; e += kThreads) {
-      const int m = e / TN, n = e % TN;
-      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * TN + n, p.ld_out_bf16), red[e] * rs[m]);
-    }
-  } else if constexpr (EPI == DTREE_EPI_RESIDUAL) {
-    const int n = threadIdx.x % TN;
-    const int col = tile * TN + n;
-    const float g = bf2f(p.next_norm[col]);
-    for (int e = threadIdx.x; e < TE; e += kThreads) {
-      const int m = e / TN;
-      float* xp = p.out_f32 + (size_t)m * p.ld_out_f32 + col;
-      const float xv = *xp + red[e];
-      *xp = xv;
-      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, col, p.ld_out_bf16), xv * g);
-      if (p.hidden_out) p.hidden_out[(size_t)m * p.ld_hidden + col] = f2bf(xv);
-      float sq = xv * xv;
+  tile_epilogue<MP, TN, EPI>(p, red, rs, tile);
+}
+
+
+// ---- stream-K GEMM for 32 rows (tiled operands) ------------------------------
+//
+// The weight stream of the whole launch is cut evenly across the grid: unit u
+// = (64-column block b = u / nkb, 64-wide K block kb = u % nkb), 8 KB of
+// weights; workgroup g owns units [g*T/G, (g+1)*T/G), one workgroup per CU, so
+// every CU streams the same number of bytes whatever the matrix shape. The
+// four waves take contiguous quarters of that range and keep kSkDepth units
+// (weights and activation hi/lo) in flight in registers. A wave's per-block
+// accumulator goes to LDS when its block changes; the workgroup then adds its
+// four waves per block and, when other workgroups share the block, publishes
+// one partial tile (agent-coherent stores to slot g + b, which is unique per
+// (workgroup, block) pair because ranges are ordered). The last workgroup to
+// arrive at a block sums the partials in workgroup order (deterministic) and
+// runs the shared tile epilogue.
+constexpr int kSkMaxBlocks = 4;  // 64-column blocks one workgroup may touch
+constexpr int kSkDepth = 4;      // units in flight per wave
+constexpr int kSkMaxGrid = 1024; // CU-count bound used for workspace sizing
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* part, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)bytes, 0x00020000);
+}
+// sc1: coherent across the XCDs' L2s (written through / read past them).
+constexpr int kSc1 = 16;
+
+template <bool LO, int EPI>
+__global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
+  constexpr int TN = 64, TE = 32 * TN;
+  __shared__ float acc_lds[kSkMaxBlocks * kWaves * TE];  // [local block][wave][row][col]
+  __shared__ float rs[32];
+  __shared__ float rs_scratch[kThreads];
+  __shared__ int last_flag[kSkMaxBlocks];
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x, G = p.G, T = p.T, nkb = p.k >> 6;
+  const int U0 = (int)((long long)g * T / G), U1 = (int)((long long)(g + 1) * T / G);
+  if (U0 >= U1) return;
+  const int b_first = U0 / nkb, b_last = (U1 - 1) / nkb;
+  const int nloc = b_last - b_first + 1;  // <= kSkMaxBlocks (host-checked)
+  if (nloc > kSkMaxBlocks) return;
+  // The row scale's loads go out before the weight stream (loads retire in
+  // order, so waiting for them later does not wait for the stream).
+  float ssv[kSsBatch];
+  ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
+  for (int e = threadIdx.x; e < nloc * kWaves * TE / 4; e += kThreads)
+    reinterpret_cast<f32x4_t*>(acc_lds)[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
+
+  // ---- stream this wave's quarter of the range ----
+  const int R = U1 - U0;
+  const int a0 = U0 + wave * R / kWaves, a1 = U0 + (wave + 1) * R / kWaves;
+  const uint16_t* xb = p.x + lane * 8;
+  const uint16_t* xlb = LO ? p.x_lo + lane * 8 : nullptr;
+  const uint16_t* wb = p.w + lane * 8;
+  u32x4_t wr[kSkDepth][2][4], xr[kSkDepth][2][4];
+  auto issue = [&](int s, int u) {
+    if (u < a1) {
+      const int b = u / nkb, kb = u - b * nkb;
+      const uint16_t* x0 = xb + (size_t)kb * 2048;
+      const uint16_t* w0 = wb + ((size_t)(2 * b) * nkb + kb) * 2048;
+      const uint16_t* w1 = w0 + (size_t)nkb * 2048;
 #pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
-      if ((n & 31) == 0) p.ss_out[(size_t)(col >> 5) * MP + m] = sq;
+      for (int i = 0; i < 4; ++i) {
+        xr[s][0][i] = ld_u32x4(x0 + 512 * i);
+        if (LO) xr[s][1][i] = ld_u32x4(xlb + (size_t)kb * 2048 + 512 * i);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wr[s][0][i] = ld_u32x4_stream(w0 + 512 * i);
+        wr[s][1][i] = ld_u32x4_stream(w1 + 512 * i);
+      }
     }
-  } else if constexpr (EPI == DTREE_EPI_SWIGLU) {
-    // Each 32-column group = 16 gate rows then 16 up rows of 16 FFN features.
-    for (int e = threadIdx.x; e < MP * TN / 2; e += kThreads) {
-      const int m = e / (TN / 2), f = e % (TN / 2);
-      const int sb = f >> 4, j = f & 15;
-      const float gt = red[m * TN + sb * 32 + j] * rs[m];
-      const float up = red[m * TN + sb * 32 + 16 + j] * rs[m];
-      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * (TN / 2) + f, p.ld_out_bf16),
-                  silu_f(gt) * up);
+  };
+  f32x16_t acc[2];
+  auto zero = [&]() {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
+  };
+  // Per-wave accumulator -> LDS [row][col] of (local block, wave); written
+  // once per pair because a wave's units of one block are contiguous.
+  auto dump = [&](int b) {
+    float* d = acc_lds + ((b - b_first) * kWaves + wave) * TE;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) d[acc_row(r, h) * TN + nb * 32 + c] = acc[nb][r];
+  };
+  zero();
+  int cur = a0 < a1 ? a0 / nkb : -1;
+#pragma unroll
+  for (int s = 0; s < kSkDepth; ++s) issue(s, a0 + s);
+  ss_finish<1>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, ssv, rs, rs_scratch);
+  for (int ub = a0; ub < a1; ub += kSkDepth) {
+#pragma unroll
+    for (int s = 0; s < kSkDepth; ++s) {
+      const int u = ub + s;
+      if (u < a1) {
+        const int b = u / nkb;
+        if (b != cur) {
+          dump(cur);
+          zero();
+          cur = b;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            acc[nb] = mfma32(xr[s][0][i], wr[s][nb][i], acc[nb]);
+            if (LO) acc[nb] = mfma32(xr[s][1][i], wr[s][nb][i], acc[nb]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(s, u + kSkDepth);
+      }
     }
+  }
+  if (cur >= 0) dump(cur);
+  __syncthreads();
+
+  // ---- per block: add the four waves; publish or finish ----
+  const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
+  const int t = threadIdx.x;  // owns tile elements 8t .. 8t+7
+  auto owner = [&](int u) { return (int)(((long long)(u + 1) * G + T - 1) / T) - 1; };
+  bool any_shared = false;
+  for (int j = 0; j < nloc; ++j) {
+    const int b = b_first + j;
+    const int gf = owner(b * nkb), gl = owner((b + 1) * nkb - 1);
+    f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(acc_lds + (j * kWaves + w) * TE + 8 * t);
+      s0 += src[0];
+      s1 += src[1];
+    }
+    if (gf == gl) {
+      // Sole owner: keep the sum in this block's wave-0 slot for the epilogue
+      // (each thread rewrites only the elements it just read).
+      f32x4_t* dst = reinterpret_cast<f32x4_t*>(acc_lds + (j * kWaves) * TE + 8 * t);
+      dst[0] = s0;
+      dst[1] = s1;
+    } else {
+      any_shared = true;
+      const int off = ((g + b) * TE + 8 * t) * 4;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, s0), prs, off, 0, kSc1);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, s1), prs, off + 16, 0, kSc1);
+    }
+  }
+  if (any_shared) wait_stores_done();
+  __syncthreads();
+  if (t < nloc) {
+    const int b = b_first + t;
+    const int gf = owner(b * nkb), gl = owner((b + 1) * nkb - 1);
+    int last = 1;
+    if (gf != gl) {
+      last = arrive(&p.counters[b]) == gl - gf;
+      if (last) reset_counter(&p.counters[b]);
+    }
+    last_flag[t] = last;
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nloc; ++j) {
+    if (!last_flag[j]) continue;  // uniform: flag in LDS
+    const int b = b_first + j;
+    const int gf = owner(b * nkb), gl = owner((b + 1) * nkb - 1);
+    float* red = acc_lds + (j * kWaves) * TE;
+    if (gf != gl) {
+      f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+      int q = gf;
+      for (; q + 4 <= gl + 1; q += 4) {
+        u32x4_t v[4][2];
+#pragma unroll
+        for (int z = 0; z < 4; ++z) {
+          const int off = ((q + z + b) * TE + 8 * t) * 4;
+          v[z][0] = __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kSc1);
+          v[z][1] = __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16, 0, kSc1);
+        }
+#pragma unroll
+        for (int z = 0; z < 4; ++z) {
+          s0 += __builtin_bit_cast(f32x4_t, v[z][0]);
+          s1 += __builtin_bit_cast(f32x4_t, v[z][1]);
+        }
+      }
+      for (; q <= gl; ++q) {
+        const int off = ((q + b) * TE + 8 * t) * 4;
+        s0 += __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kSc1));
+        s1 += __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16, 0, kSc1));
+      }
+      reinterpret_cast<f32x4_t*>(red + 8 * t)[0] = s0;
+      reinterpret_cast<f32x4_t*>(red + 8 * t)[1] = s1;
+    }
+    __syncthreads();
+    tile_epilogue<32, TN, EPI>(p, red, rs, b);
   }
 }
 
@@ -310,7 +572,8 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   constexpr int IT = TE / kThreads;  // rows handled per thread
   __shared__ float red[(kWaves - 1) * TE];
   __shared__ float rs[MP];
-  row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs);
+  __shared__ float rs_scratch[kThreads];
+  row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs, rs_scratch);
   float bv[IT];
   int bi[IT];
 #pragma unroll
@@ -417,6 +680,41 @@ static void launch_lm(const LmParams& p, int grid, hipStream_t st, bool tiled) {
 // by the split-K partial tiles.
 constexpr size_t kCounterBytes = 65536;  // 16384 column tiles
 
+// Stream-K grid: one workgroup per CU, more only when a workgroup's range
+// would touch more than kSkMaxBlocks column blocks.
+static int sk_grid(int T, int nkb, int cus) {
+  int G = T < cus ? T : cus;
+  const int need = (T + 3 * nkb - 1) / (3 * nkb);
+  return G > need ? G : need;
+}
+
+static size_t sk_workspace_bytes(int n, int k, int cus) {
+  const int nkb = k / 64, nblk = n / 64, T = nblk * nkb;
+  return kCounterBytes + (size_t)(sk_grid(T, nkb, cus) + nblk) * 32 * 64 * sizeof(float);
+}
+
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <bool LO>
+static void launch_sk(const GemmParams& p, int epi, hipStream_t st) {
+  switch (epi) {
+    case DTREE_EPI_STORE_F32: sk_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: sk_gemm_kernel<LO, DTREE_EPI_RESIDUAL><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: sk_gemm_kernel<LO, DTREE_EPI_SWIGLU><<<p.G, kThreads, 0, st>>>(p); break;
+    default: sk_gemm_kernel<LO, DTREE_EPI_STORE_BF16><<<p.G, kThreads, 0, st>>>(p); break;
+  }
+}
+
 }  // namespace dtree
 
 using namespace dtree;
@@ -427,7 +725,14 @@ extern "C" size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int 
   const int ntiles = (n + tn - 1) / tn, nkb = k / 64;
   const int S = split_k > 0 ? split_k : auto_split(ntiles, nkb);
   const size_t nt8 = (size_t)((ntiles + 7) / 8) * 8;
-  return kCounterBytes + (S > 1 ? nt8 * S * (size_t)rows_padded * tn * sizeof(float) : 0);
+  size_t need = kCounterBytes + (S > 1 ? nt8 * S * (size_t)rows_padded * tn * sizeof(float) : 0);
+  if (split_k <= 0 && rows_padded == 32) {
+    // The stream-K path (tiled operands) may serve this shape: size for the
+    // largest CU count it plans for.
+    const size_t sk = sk_workspace_bytes(n, k, kSkMaxGrid);
+    if (sk > need) need = sk;
+  }
+  return need;
 }
 
 extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
@@ -480,6 +785,19 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   if (a->out_layout == DTREE_W_TILED && a->out_bf16) {
     const int width = epi == DTREE_EPI_SWIGLU ? a->n / 2 : a->n;
     DTREE_REQUIRE(a->ld_out_bf16 == width && width % 64 == 0, "gemm: tiled out needs ld_out_bf16 == width, width % 64");
+  }
+  if (tiled && a->rows_padded == 32 && a->split_k <= 0) {
+    const int cus = device_cus();
+    const int nblk = a->n / 64;
+    p.T = nblk * nkb;
+    p.G = sk_grid(p.T, nkb, cus < kSkMaxGrid ? cus : kSkMaxGrid);
+    const size_t need_sk = sk_workspace_bytes(a->n, a->k, cus < kSkMaxGrid ? cus : kSkMaxGrid);
+    DTREE_REQUIRE(a->workspace_bytes >= need_sk, "gemm: workspace too small for the stream-K schedule");
+    p.part_bytes = (unsigned)(need_sk - kCounterBytes);
+    if (p.x_lo) launch_sk<true>(p, epi, stream);
+    else launch_sk<false>(p, epi, stream);
+    DTREE_LAUNCH_CHECK("gemm launch");
+    return DTREE_OK;
   }
   switch (a->rows_padded) {
     case 32: launch_gemm<1>(p, epi, blocks, stream, tiled); break;

@@ -187,6 +187,106 @@ def test_gemm_swiglu_epilogue(gpu_device):
     np.testing.assert_allclose(bf16_f32(act), ref, rtol=1e-2, atol=1e-3)
 
 
+# ---- stream-K path (32 rows, tiled operands, split_k = 0) -------------------
+# Shapes chosen for the schedule: one unit; one K block over many column
+# blocks (workgroups touching several blocks); one column block over 152 K
+# blocks (one block shared by 152 workgroups); and the Qwen3-4B layer shapes.
+SK_SHAPES = [(64, 64), (4096, 64), (19456, 64), (64, 9728), (256, 1024), (6144, 2560), (2560, 4096),
+             (19456, 2560), (2560, 9728)]
+
+
+def _sk_args(xt, xlo_t, wt, n, k, epi, ws):
+    a = N.GemmArgs()
+    a.x = xt.data_ptr(); a.x_lo = xlo_t.data_ptr() if xlo_t is not None else None
+    a.x_layout = a.w_layout = N.W_TILED; a.ldx = k; a.rows_padded = 32
+    a.w = wt.data_ptr(); a.n = n; a.k = k; a.epilogue = epi; a.split_k = 0
+    a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+    return a
+
+
+@pytest.mark.parametrize("n,k", SK_SHAPES)
+@pytest.mark.parametrize("lo", [False, True])
+def test_sk_gemm_store_f32(gpu_device, n, k, lo):
+    g = np.random.default_rng(n + k + lo)
+    L = 25
+    xf = np.zeros((32, k), np.float32)
+    xf[:L] = g.standard_normal((L, k))
+    hi = torch.from_numpy(xf).to(torch.bfloat16)
+    lo_t = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16) if lo else None
+    w = torch.from_numpy(g.standard_normal((n, k)).astype(np.float32) * 0.05).to(torch.bfloat16)
+    ss = torch.from_numpy(np.abs(g.standard_normal((3, 32))).astype(np.float32) + 0.5).to(gpu_device)
+    xt = tile_weight(hi.to(gpu_device))
+    xlt = tile_weight(lo_t.to(gpu_device)) if lo else None
+    wt = tile_weight(w.to(gpu_device))
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, n, k, 0), dtype=torch.uint8, device=gpu_device)
+    outs = []
+    for _ in range(2):
+        out = torch.zeros(32, n, device=gpu_device)
+        a = _sk_args(xt, xlt, wt, n, k, N.EPI_STORE_F32, ws)
+        a.ss_in = ss.data_ptr(); a.ss_tiles = 3; a.norm_dim = k; a.eps = 1e-6
+        a.out_f32 = out.data_ptr(); a.ld_out_f32 = n
+        N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "gemm")
+        outs.append(out)
+    torch.cuda.synchronize()
+    rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(0) / k + 1e-6)
+    xin = hi.double() + (lo_t.double() if lo else 0)
+    ref = (xin.numpy() @ bf16_f32(w).T.astype(np.float64)) * rs[:, None]
+    got = outs[0].cpu().numpy()
+    assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max())
+    assert torch.equal(outs[0], outs[1])  # fixed reduction order
+    assert int(ws[: (n // 64) * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
+
+
+@pytest.mark.parametrize("n,k", [(512, 768), (2560, 4096), (2560, 9728)])
+def test_sk_gemm_residual_epilogue(gpu_device, n, k):
+    g = np.random.default_rng(n + 3 * k)
+    L = 25
+    x = _rows(32, L, k, g, gpu_device)
+    w = torch.from_numpy(g.standard_normal((n, k)).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu_device)
+    res = torch.zeros(32, n)
+    res[:L] = torch.from_numpy(g.standard_normal((L, n)).astype(np.float32))
+    res = res.to(gpu_device)
+    res0 = res.clone()
+    gn = torch.from_numpy((1 + 0.1 * g.standard_normal(n)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    xg = torch.zeros(32, n, dtype=torch.bfloat16, device=gpu_device)
+    ss = torch.zeros(n // 32, 32, device=gpu_device)
+    hid = torch.zeros(32, n, dtype=torch.bfloat16, device=gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, n, k, 0), dtype=torch.uint8, device=gpu_device)
+    _gemm(x, w, N.EPI_RESIDUAL, 0, ws, out_f32=res, out_bf16=xg, next_norm=gn, ss_out=ss, hidden_out=hid,
+          tiled=True)
+    torch.cuda.synchronize()
+    ref = res0.cpu().numpy().astype(np.float64) + bf16_f32(x).astype(np.float64) @ bf16_f32(w).T.astype(np.float64)
+    got = res.cpu().numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+    assert np.all(got[L:] == 0)
+    assert torch.equal(xg.cpu(), (torch.from_numpy(got) * gn.float().cpu()).to(torch.bfloat16))
+    exp_ss = (got.astype(np.float64) ** 2).reshape(32, n // 32, 32).sum(-1).T
+    np.testing.assert_allclose(ss.cpu().numpy(), exp_ss, rtol=1e-5, atol=1e-5)
+    assert torch.equal(hid.cpu(), torch.from_numpy(got).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("F,k", [(384, 512), (9728, 2560)])
+def test_sk_gemm_swiglu_epilogue(gpu_device, F, k):
+    g = np.random.default_rng(F + k)
+    L = 25
+    x = _rows(32, L, k, g, gpu_device)
+    gate = torch.from_numpy(g.standard_normal((F, k)).astype(np.float32) * 0.05).to(torch.bfloat16)
+    up = torch.from_numpy(g.standard_normal((F, k)).astype(np.float32) * 0.05).to(torch.bfloat16)
+    from dtree_hip.weights import interleave_gate_up
+    wgu = interleave_gate_up(gate, up).to(gpu_device)
+    ss = torch.from_numpy(np.abs(g.standard_normal((3, 32))).astype(np.float32) + 0.5).to(gpu_device)
+    act = torch.zeros(32, F, dtype=torch.bfloat16, device=gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, 2 * F, k, 0), dtype=torch.uint8, device=gpu_device)
+    _gemm(x, wgu, N.EPI_SWIGLU, 0, ws, ss_in=ss, norm_dim=k, out_bf16=act, tiled=True)
+    torch.cuda.synchronize()
+    rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(0) / k + 1e-6)
+    xf = bf16_f32(x).astype(np.float64)
+    gt = (xf @ gate.float().numpy().T) * rs[:, None]
+    u = (xf @ up.float().numpy().T) * rs[:, None]
+    ref = gt / (1 + np.exp(-gt)) * u
+    np.testing.assert_allclose(bf16_f32(act), ref, rtol=1e-2, atol=1e-3)
+
+
 def _attention(qkv, cache, layer, desc, out, ws, Hq, Hkv, max_past, cos, sin, qn, kn, write=1):
     a = N.AttnArgs()
     a.qkv = qkv.data_ptr(); a.ld_qkv = qkv.shape[1]
