@@ -31,6 +31,10 @@ extern "C" int dtree_abi_version(void) { return DTREE_ABI_VERSION; }
 
 extern "C" size_t dtree_step_desc_bytes(void) { return sizeof(DtreeStepDesc); }
 
+extern "C" size_t dtree_gemm_args_bytes(void) { return sizeof(DtreeGemmArgs); }
+
+extern "C" size_t dtree_attn_args_bytes(void) { return sizeof(DtreeAttnArgs); }
+
 extern "C" int dtree_graph_begin(hipStream_t stream) {
   return hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
 }

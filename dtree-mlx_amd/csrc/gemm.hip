@@ -37,6 +37,7 @@ constexpr int kWaves = 4;
 struct GemmParams {
   const uint16_t* x; const uint16_t* x_lo; int ldx;
   const uint16_t* w; int n, k;
+  const uint16_t* w_sb;  // q4: (scale, bias) pairs
   int S, kb_per_split, ntiles;
   const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
   float* out_f32; int ld_out_f32;
@@ -367,6 +368,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 constexpr int kSkMaxBlocks = 4;  // 64-column blocks one workgroup may touch
 constexpr int kSkDepth = 4;      // units in flight per wave
 constexpr int kSkMaxGrid = 1024; // CU-count bound used for workspace sizing
+constexpr int kSkMaxKb = 64;     // q4: K groups whose activation sums one workgroup keeps
+
+// q4 nibble pair j of a repacked word -> two bf16 holding 128 + q (exact: the
+// bf16 with bits 0x4300 | q is 128 + q for q < 128), K order (2j, 2j+1).
+__device__ __forceinline__ u32x4_t q4_pairs(uint32_t w) {
+  return u32x4_t{(w & 0x000F000Fu) | 0x43004300u, ((w >> 4) & 0x000F000Fu) | 0x43004300u,
+                 ((w >> 8) & 0x000F000Fu) | 0x43004300u, ((w >> 12) & 0x000F000Fu) | 0x43004300u};
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* part, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)bytes, 0x00020000);
@@ -374,10 +383,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* part, unsigne
 // sc1: coherent across the XCDs' L2s (written through / read past them).
 constexpr int kSc1 = 16;
 
-template <bool LO, int EPI>
+template <bool LO, int EPI, bool Q4>
 __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   constexpr int TN = 64, TE = 32 * TN;
   __shared__ float acc_lds[kSkMaxBlocks * kWaves * TE];  // [local block][wave][row][col]
+  __shared__ float xsum_lds[Q4 ? kSkMaxKb * 32 : 1];      // q4: [local group][row] sum of x
   __shared__ float rs[32];
   __shared__ float rs_scratch[kThreads];
   __shared__ int last_flag[kSkMaxBlocks];
@@ -395,6 +405,32 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
   for (int e = threadIdx.x; e < nloc * kWaves * TE / 4; e += kThreads)
     reinterpret_cast<f32x4_t*>(acc_lds)[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // q4: per (group, row) sums of the activations over this workgroup's groups
+  // (the affine bias term and the 128 offset of the nibble encoding need them).
+  const int ngrp = (U1 - U0) < nkb ? (U1 - U0) : nkb;
+  const int kbase = (U1 - U0) < nkb ? U0 % nkb : 0;
+  if constexpr (Q4) {
+    for (int pr = threadIdx.x; pr < ngrp * 32; pr += kThreads) {
+      const int j = pr >> 5, m = pr & 31;
+      int kb = kbase + j;
+      if (kb >= nkb) kb -= nkb;
+      float sum = 0.f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const size_t off = (size_t)kb * 2048 + (size_t)(i * 64 + m + 32 * hh) * 8;
+          const u32x4_t v = ld_u32x4(p.x + off);
+          u32x4_t vl = u32x4_t{0u, 0u, 0u, 0u};
+          if (LO) vl = ld_u32x4(p.x_lo + off);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            sum += (__uint_as_float(v[q] << 16) + __uint_as_float(v[q] & 0xffff0000u)) +
+                   (__uint_as_float(vl[q] << 16) + __uint_as_float(vl[q] & 0xffff0000u));
+        }
+      xsum_lds[j * 32 + m] = sum;
+    }
+  }
   __syncthreads();
 
   // ---- stream this wave's quarter of the range ----
@@ -403,22 +439,36 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   const uint16_t* xb = p.x + lane * 8;
   const uint16_t* xlb = LO ? p.x_lo + lane * 8 : nullptr;
   const uint16_t* wb = p.w + lane * 8;
-  u32x4_t wr[kSkDepth][2][4], xr[kSkDepth][2][4];
+  const uint32_t* qb = reinterpret_cast<const uint32_t*>(p.w) + lane * 4;  // q4 words
+  const uint32_t* sbb = reinterpret_cast<const uint32_t*>(p.w_sb) + c;     // q4 (scale, bias)
+  // Ring of in-flight units: bf16 weights (2 blocks x 4 loads) or q4 words
+  // (2 blocks x 1 load) + (scale, bias) per block; activations hi/lo.
+  u32x4_t wr[kSkDepth][2][Q4 ? 1 : 4], xr[kSkDepth][2][4];
+  uint32_t sbr[kSkDepth][2];
   auto issue = [&](int s, int u) {
     if (u < a1) {
       const int b = u / nkb, kb = u - b * nkb;
       const uint16_t* x0 = xb + (size_t)kb * 2048;
-      const uint16_t* w0 = wb + ((size_t)(2 * b) * nkb + kb) * 2048;
-      const uint16_t* w1 = w0 + (size_t)nkb * 2048;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         xr[s][0][i] = ld_u32x4(x0 + 512 * i);
         if (LO) xr[s][1][i] = ld_u32x4(xlb + (size_t)kb * 2048 + 512 * i);
       }
+      if constexpr (Q4) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        wr[s][0][i] = ld_u32x4_stream(w0 + 512 * i);
-        wr[s][1][i] = ld_u32x4_stream(w1 + 512 * i);
+        for (int nb = 0; nb < 2; ++nb) {
+          const size_t blk = (size_t)(2 * b + nb) * nkb + kb;
+          wr[s][nb][0] = ld_u32x4_stream(qb + blk * 256);
+          sbr[s][nb] = sbb[blk * 32];
+        }
+      } else {
+        const uint16_t* w0 = wb + ((size_t)(2 * b) * nkb + kb) * 2048;
+        const uint16_t* w1 = w0 + (size_t)nkb * 2048;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wr[s][0][i] = ld_u32x4_stream(w0 + 512 * i);
+          wr[s][1][i] = ld_u32x4_stream(w1 + 512 * i);
+        }
       }
     }
   };
@@ -455,13 +505,40 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
           cur = b;
         }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (Q4) {
+          // One group: fresh MFMA sums of x (128 + q), then
+          // y += s * acc + (b - 128 s) * sum(x) per (row, column).
+          int j = u - b * nkb - kbase;
+          if (j < 0) j += nkb;
+          const float* xs = xsum_lds + j * 32 + 4 * h;
+          f32x4_t xsv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+          for (int q = 0; q < 4; ++q) xsv[q] = *reinterpret_cast<const f32x4_t*>(xs + 8 * q);
 #pragma unroll
           for (int nb = 0; nb < 2; ++nb) {
-            acc[nb] = mfma32(xr[s][0][i], wr[s][nb][i], acc[nb]);
-            if (LO) acc[nb] = mfma32(xr[s][1][i], wr[s][nb][i], acc[nb]);
+            f32x16_t au;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) au[r] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const u32x4_t bq = q4_pairs(wr[s][nb][0][i]);
+              au = mfma32(xr[s][0][i], bq, au);
+              if (LO) au = mfma32(xr[s][1][i], bq, au);
+            }
+            const float sc = __uint_as_float(sbr[s][nb] << 16);
+            const float cf = __uint_as_float(sbr[s][nb] & 0xffff0000u) - 128.f * sc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[nb][r] += sc * au[r] + cf * xsv[r >> 2][r & 3];
           }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+              acc[nb] = mfma32(xr[s][0][i], wr[s][nb][i], acc[nb]);
+              if (LO) acc[nb] = mfma32(xr[s][1][i], wr[s][nb][i], acc[nb]);
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
         issue(s, u + kSkDepth);
       }
@@ -684,7 +761,11 @@ constexpr size_t kCounterBytes = 65536;  // 16384 column tiles
 // would touch more than kSkMaxBlocks column blocks.
 static int sk_grid(int T, int nkb, int cus) {
   int G = T < cus ? T : cus;
-  const int need = (T + 3 * nkb - 1) / (3 * nkb);
+  int need = (T + 3 * nkb - 1) / (3 * nkb);  // <= kSkMaxBlocks column blocks per workgroup
+  if (nkb > kSkMaxKb) {                      // q4: <= kSkMaxKb groups per workgroup
+    const int need_q4 = (T + kSkMaxKb - 1) / kSkMaxKb;
+    if (need_q4 > need) need = need_q4;
+  }
   return G > need ? G : need;
 }
 
@@ -705,13 +786,13 @@ static int device_cus() {
   return cached[dev];
 }
 
-template <bool LO>
+template <bool LO, bool Q4>
 static void launch_sk(const GemmParams& p, int epi, hipStream_t st) {
   switch (epi) {
-    case DTREE_EPI_STORE_F32: sk_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<p.G, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_RESIDUAL: sk_gemm_kernel<LO, DTREE_EPI_RESIDUAL><<<p.G, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_SWIGLU: sk_gemm_kernel<LO, DTREE_EPI_SWIGLU><<<p.G, kThreads, 0, st>>>(p); break;
-    default: sk_gemm_kernel<LO, DTREE_EPI_STORE_BF16><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_STORE_F32: sk_gemm_kernel<LO, DTREE_EPI_STORE_F32, Q4><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: sk_gemm_kernel<LO, DTREE_EPI_RESIDUAL, Q4><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: sk_gemm_kernel<LO, DTREE_EPI_SWIGLU, Q4><<<p.G, kThreads, 0, st>>>(p); break;
+    default: sk_gemm_kernel<LO, DTREE_EPI_STORE_BF16, Q4><<<p.G, kThreads, 0, st>>>(p); break;
   }
 }
 
@@ -777,9 +858,18 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   p.counters = reinterpret_cast<int*>(a->workspace);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kCounterBytes);
   const int blocks = S == 1 ? ntiles : (int)(nt8 * S);
-  const bool tiled = a->w_layout == DTREE_W_TILED;
+  const bool q4 = a->w_layout == DTREE_W_Q4G64;
+  const bool tiled = a->w_layout == DTREE_W_TILED || q4;
   DTREE_REQUIRE(a->w_layout == DTREE_W_ROWMAJOR || tiled, "gemm: unknown w_layout");
-  DTREE_REQUIRE(a->x_layout == a->w_layout, "gemm: x_layout must equal w_layout (both row-major or both tiled)");
+  if (q4) {
+    DTREE_REQUIRE(a->x_layout == DTREE_W_TILED && a->rows_padded == 32 && a->split_k <= 0,
+                  "gemm: q4 weights need tiled 32-row activations and split_k 0");
+    DTREE_REQUIRE(a->w_scales && ((uintptr_t)a->w & 15) == 0 && ((uintptr_t)a->w_scales & 3) == 0,
+                  "gemm: q4 weights need w (16-byte aligned) and w_scales (4-byte aligned)");
+  } else {
+    DTREE_REQUIRE(a->x_layout == a->w_layout, "gemm: x_layout must equal w_layout (both row-major or both tiled)");
+  }
+  p.w_sb = a->w_scales;
   DTREE_REQUIRE(!tiled || (a->ldx == a->k && a->rows_padded % 32 == 0), "gemm: tiled x needs ldx == k");
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR || a->out_layout == DTREE_W_TILED, "gemm: unknown out_layout");
   if (a->out_layout == DTREE_W_TILED && a->out_bf16) {
@@ -794,8 +884,13 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     const size_t need_sk = sk_workspace_bytes(a->n, a->k, cus < kSkMaxGrid ? cus : kSkMaxGrid);
     DTREE_REQUIRE(a->workspace_bytes >= need_sk, "gemm: workspace too small for the stream-K schedule");
     p.part_bytes = (unsigned)(need_sk - kCounterBytes);
-    if (p.x_lo) launch_sk<true>(p, epi, stream);
-    else launch_sk<false>(p, epi, stream);
+    if (q4) {
+      if (p.x_lo) launch_sk<true, true>(p, epi, stream);
+      else launch_sk<false, true>(p, epi, stream);
+    } else {
+      if (p.x_lo) launch_sk<true, false>(p, epi, stream);
+      else launch_sk<false, false>(p, epi, stream);
+    }
     DTREE_LAUNCH_CHECK("gemm launch");
     return DTREE_OK;
   }

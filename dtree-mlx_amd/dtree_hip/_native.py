@@ -14,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
 MAX_NODES = 128
 MASK_WORDS = 4
 PAGE = 64
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 EPI_STORE_F32 = 0
 EPI_RESIDUAL = 1
@@ -23,6 +23,7 @@ EPI_STORE_BF16 = 3
 
 W_ROWMAJOR = 0
 W_TILED = 1
+W_Q4G64 = 2
 
 
 class DtreeError(RuntimeError):
@@ -56,6 +57,7 @@ class GemmArgs(C.Structure):
         ("next_norm", C.c_void_p), ("ss_out", C.c_void_p),
         ("hidden_out", C.c_void_p), ("ld_hidden", C.c_int32),
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("w_scales", C.c_void_p),
     ]
 
 
@@ -83,6 +85,8 @@ SIGNATURES = {
     "dtree_last_error": (C.c_char_p, []),
     "dtree_abi_version": (C.c_int, []),
     "dtree_step_desc_bytes": (_sz, []),
+    "dtree_gemm_args_bytes": (_sz, []),
+    "dtree_attn_args_bytes": (_sz, []),
     "dtree_gemm_workspace_bytes": (_sz, [C.c_int, C.c_int, C.c_int, C.c_int]),
     "dtree_gemm_bf16": (C.c_int, [C.POINTER(GemmArgs), _vp]),
     "dtree_embed": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _vp, _vp,
@@ -123,8 +127,10 @@ def lib() -> C.CDLL:
         fn.argtypes = args
     if h.dtree_abi_version() != ABI_VERSION:
         raise DtreeError("libdtree_hip.so ABI version mismatch; rebuild it")
-    if h.dtree_step_desc_bytes() != C.sizeof(StepDesc):
-        raise DtreeError("DtreeStepDesc layout mismatch between Python and the library")
+    for fn, struct in (("dtree_step_desc_bytes", StepDesc), ("dtree_gemm_args_bytes", GemmArgs),
+                       ("dtree_attn_args_bytes", AttnArgs)):
+        if getattr(h, fn)() != C.sizeof(struct):
+            raise DtreeError(f"{struct.__name__} layout mismatch between Python and the library")
     _LIB = h
     return h
 

@@ -28,7 +28,7 @@ import torch
 from .config import Qwen3Config
 
 
-W_ROWMAJOR, W_TILED = 0, 1
+W_ROWMAJOR, W_TILED, W_Q4G64 = 0, 1, 2
 
 
 def tile_weight(w: torch.Tensor) -> torch.Tensor:
@@ -66,6 +66,30 @@ def split_gate_up(wgu: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     F2, H = wgu.shape
     v = wgu.reshape(F2 // 32, 2, 16, H)
     return v[:, 0].reshape(F2 // 2, H), v[:, 1].reshape(F2 // 2, H)
+
+
+def q4_to_tiled(wq: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """MLX quantized layout -> DTREE_W_Q4G64.
+
+    In: wq [N, K/8] (uint32 bit patterns in an int32 tensor; element k of a row
+    is nibble k % 8 of word k // 8), scales / biases bf16 [N, K/64].
+    Out: words int32 [N/32, K/64, 64, 4] -- word (l, i) of block (r, b) holds
+    row 32r + l % 32, columns 64b + 32 (l // 32) + 8i + e, even e in bits
+    4 (e // 2), odd e in bits 16 + 4 (e // 2) -- and (scale, bias) bf16
+    [N/32, K/64, 32, 2]."""
+    n, kw = wq.shape
+    k = kw * 8
+    if n % 32 or k % 64:
+        raise ValueError("q4 weights need n % 32 == 0 and k % 64 == 0")
+    nkb = k // 64
+    w = (wq.to(torch.int64) & 0xFFFFFFFF).reshape(n // 32, 32, nkb, 2, 4).permute(0, 2, 3, 1, 4)  # r, b, h, c, i
+    out = torch.zeros_like(w)
+    for e in range(8):
+        out |= ((w >> (4 * e)) & 0xF) << ((e & 1) * 16 + 4 * (e >> 1))
+    out = torch.where(out >= 2 ** 31, out - 2 ** 32, out).to(torch.int32).reshape(n // 32, nkb, 64, 4)
+    sc = scales.reshape(n // 32, 32, nkb).permute(0, 2, 1)
+    bi = biases.reshape(n // 32, 32, nkb).permute(0, 2, 1)
+    return out.contiguous(), torch.stack([sc, bi], dim=-1).contiguous()
 
 
 @dataclass

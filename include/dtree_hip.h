@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define DTREE_ABI_VERSION 1
+#define DTREE_ABI_VERSION 2
 
 #define DTREE_OK 0
 #define DTREE_E_ARG (-1)      /* bad shape / pointer / enum */
@@ -64,9 +64,19 @@ typedef struct DtreeStepDesc {
  *                    the order the GEMM lanes consume, so each 16-byte load
  *                    instruction of a wavefront reads one contiguous kilobyte.
  *                    dtree_tile_weight converts a row-major matrix.
+ *  DTREE_W_Q4G64:    4-bit affine groups of 64 (the MLX quantized format of
+ *                    nn.QuantizedLinear, adapters.py:63-71, api.py:46-54:
+ *                    W[n][k] = scale[n][k/64] * q[n][k] + bias[n][k/64]),
+ *                    repacked: w = uint32 [n/32][k/64][64][4]; word (l, i) of
+ *                    block (r, b) holds q of row 32r + l%32 at columns
+ *                    64b + 32*(l/32) + 8i + e, e = 0..7, with even e in bits
+ *                    4*(e/2) and odd e in bits 16 + 4*(e/2); w_scales = bf16
+ *                    [n/32][k/64][32][2] (scale, bias) of row 32r + c, group b.
+ *                    Activations must be DTREE_W_TILED, 32 rows.
  */
 #define DTREE_W_ROWMAJOR 0
 #define DTREE_W_TILED 1
+#define DTREE_W_Q4G64 2
 
 /* GEMM epilogues (dtree_gemm_bf16). */
 #define DTREE_EPI_STORE_F32 0  /* out_f32[m][n] = rs[m] * acc                 */
@@ -89,8 +99,8 @@ typedef struct DtreeGemmArgs {
   int32_t x_layout;       /* DTREE_W_ROWMAJOR, or DTREE_W_TILED with ldx = k */
   int32_t ldx;
   int32_t rows_padded;    /* 32, 64, 96 or 128                             */
-  const uint16_t* w;      /* bf16 [n][k] (nn.Linear layout)                */
-  int32_t w_layout;       /* DTREE_W_ROWMAJOR or DTREE_W_TILED             */
+  const uint16_t* w;      /* bf16 [n][k] (nn.Linear layout); Q4G64: packed q */
+  int32_t w_layout;       /* DTREE_W_ROWMAJOR, DTREE_W_TILED or DTREE_W_Q4G64 */
   int32_t n, k;           /* k % 64 == 0; n % 64 == 0 (% 32 above 64 rows) */
   int32_t epilogue;       /* DTREE_EPI_*                                   */
   int32_t split_k;        /* >= 1; 0 = choose automatically                */
@@ -107,11 +117,16 @@ typedef struct DtreeGemmArgs {
   float* ss_out;              /* RESIDUAL: [n/32][rows_padded] sum of x^2  */
   uint16_t* hidden_out; int32_t ld_hidden; /* RESIDUAL: optional bf16 copy */
   void* workspace; size_t workspace_bytes; /* split-K partials + counters  */
+  const uint16_t* w_scales;   /* Q4G64: (scale, bias) pairs, else NULL     */
 } DtreeGemmArgs;
 
 const char* dtree_last_error(void);
 int dtree_abi_version(void);
 size_t dtree_step_desc_bytes(void);
+/* sizeof(DtreeGemmArgs) / sizeof(DtreeAttnArgs): lets bindings check their
+ * mirrored struct layouts. */
+size_t dtree_gemm_args_bytes(void);
+size_t dtree_attn_args_bytes(void);
 
 /* Workspace for dtree_gemm_bf16 (partials + tile counters). Counters must be
  * zero before the first call; every call leaves them zero again. */

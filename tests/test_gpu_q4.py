@@ -1,0 +1,140 @@
+"""q4 group-64 affine GEMM (DTREE_W_Q4G64, adapters.py:63-71 semantics) on the
+GPU against the float64 q4 oracle (oracle/q4.py), through the C-ABI.
+
+Weights are synthetic as in the q4 workload: nibbles uniform in [0, 15],
+scales |N(0, 0.02)| * 8, biases N(0, 0.01), scales/biases bf16. The kernel
+multiplies raw nibbles on MFMA (as 128 + q in bf16, exact) and applies
+s * acc + (b - 128 s) * sum(x) per group; its fp32 accumulation is the only
+rounding, so the bar is 2e-4 of the output's magnitude."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bf16_f32, stream
+from oracle import q4 as o4
+from oracle.qwen3 import bf16_to_f32
+
+from dtree_hip import _native as N
+from dtree_hip.weights import interleave_gate_up, q4_to_tiled, tile_weight
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(64, 64), (4096, 64), (64, 9728), (256, 1024), (6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)]
+
+
+def _to_torch(wq, s, b):
+    return (torch.from_numpy(np.ascontiguousarray(wq).view(np.int32)),
+            torch.from_numpy(np.ascontiguousarray(s).view(np.int16)).view(torch.bfloat16),
+            torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16))
+
+
+def _x(L, k, g, dev, lo):
+    xf = np.zeros((32, k), np.float32)
+    xf[:L] = g.standard_normal((L, k))
+    hi = torch.from_numpy(xf).to(torch.bfloat16)
+    lo_t = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16)
+    xin = hi.double() + (lo_t.double() if lo else 0)
+    return tile_weight(hi.to(dev)), (tile_weight(lo_t.to(dev)) if lo else None), xin.numpy()
+
+
+def _args(xt, xlt, wt, sb, n, k, epi, ws):
+    a = N.GemmArgs()
+    a.x = xt.data_ptr(); a.x_lo = xlt.data_ptr() if xlt is not None else None
+    a.x_layout = N.W_TILED; a.ldx = k; a.rows_padded = 32
+    a.w = wt.data_ptr(); a.w_layout = N.W_Q4G64; a.w_scales = sb.data_ptr()
+    a.n = n; a.k = k; a.epilogue = epi; a.split_k = 0
+    a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+    return a
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("lo", [False, True])
+def test_q4_gemm_store_f32(gpu_device, n, k, lo):
+    g = np.random.default_rng(n * 7 + k + lo)
+    wq, s, b = o4.random_q4(n, k, g)
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    wt, sb = wt.to(gpu_device), sb.to(gpu_device)
+    xt, xlt, xin = _x(25, k, g, gpu_device, lo)
+    ss = torch.from_numpy(np.abs(g.standard_normal((3, 32))).astype(np.float32) + 0.5).to(gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, n, k, 0), dtype=torch.uint8, device=gpu_device)
+    outs = []
+    for _ in range(2):
+        out = torch.zeros(32, n, device=gpu_device)
+        a = _args(xt, xlt, wt, sb, n, k, N.EPI_STORE_F32, ws)
+        a.ss_in = ss.data_ptr(); a.ss_tiles = 3; a.norm_dim = k; a.eps = 1e-6
+        a.out_f32 = out.data_ptr(); a.ld_out_f32 = n
+        N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 gemm")
+        outs.append(out)
+    torch.cuda.synchronize()
+    rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(0) / k + 1e-6)
+    ref = o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b)) * rs[:, None]
+    got = outs[0].cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    assert torch.equal(outs[0], outs[1])
+    assert int(ws[: (n // 64) * 4].view(torch.int32).abs().sum()) == 0
+
+
+def test_q4_gemm_residual_and_swiglu(gpu_device):
+    g = np.random.default_rng(77)
+    H, F, L = 512, 768, 25
+    # residual (o_proj / down_proj shape class): x += y, xg = split(x * g), ss
+    wq, s, b = o4.random_q4(H, F, g)
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    xt, xlt, xin = _x(L, F, g, gpu_device, True)
+    res = torch.zeros(32, H)
+    res[:L] = torch.from_numpy(g.standard_normal((L, H)).astype(np.float32))
+    res = res.to(gpu_device)
+    res0 = res.clone()
+    gn = torch.from_numpy((1 + 0.1 * g.standard_normal(H)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    xg = torch.zeros(32, H, dtype=torch.bfloat16, device=gpu_device)
+    ss = torch.zeros(H // 32, 32, device=gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, 2 * F, H, 0) + (1 << 20), dtype=torch.uint8,
+                     device=gpu_device)
+    a = _args(xt, xlt, wt.to(gpu_device), sb.to(gpu_device), H, F, N.EPI_RESIDUAL, ws)
+    a.out_f32 = res.data_ptr(); a.ld_out_f32 = H
+    a.out_bf16 = xg.data_ptr(); a.ld_out_bf16 = H; a.next_norm = gn.data_ptr(); a.ss_out = ss.data_ptr()
+    N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 residual")
+    torch.cuda.synchronize()
+    ref = res0.cpu().double().numpy() + o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b))
+    got = res.cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    assert torch.equal(xg.cpu(), (torch.from_numpy(got) * gn.float().cpu()).to(torch.bfloat16))
+    np.testing.assert_allclose(ss.cpu().numpy(), (got.astype(np.float64) ** 2).reshape(32, H // 32, 32).sum(-1).T,
+                               rtol=1e-5, atol=1e-5)
+
+    # SwiGLU: gate / up interleaved in 16-row groups, q4 on both
+    gq, gs, gb = o4.random_q4(F, H, g)
+    uq, us, ub = o4.random_q4(F, H, g)
+    wq2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int32)) for t in (gq, uq)])
+    s2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int16)) for t in (gs, us)])
+    b2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int16)) for t in (gb, ub)])
+    wt2, sb2 = q4_to_tiled(wq2, s2.view(torch.bfloat16), b2.view(torch.bfloat16))
+    xt, xlt, xin = _x(L, H, g, gpu_device, True)
+    rsq = torch.from_numpy(np.abs(g.standard_normal((2, 32))).astype(np.float32) + 0.5).to(gpu_device)
+    act = torch.zeros(32, F, dtype=torch.bfloat16, device=gpu_device)
+    a = _args(xt, xlt, wt2.to(gpu_device), sb2.to(gpu_device), 2 * F, H, N.EPI_SWIGLU, ws)
+    a.ss_in = rsq.data_ptr(); a.ss_tiles = 2; a.norm_dim = H; a.eps = 1e-6
+    a.out_bf16 = act.data_ptr(); a.ld_out_bf16 = F
+    N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 swiglu")
+    torch.cuda.synchronize()
+    rs = 1.0 / np.sqrt(rsq.cpu().numpy().sum(0) / H + 1e-6)
+    gt = o4.q4_matmul(xin, gq, bf16_to_f32(gs), bf16_to_f32(gb)) * rs[:, None]
+    up = o4.q4_matmul(xin, uq, bf16_to_f32(us), bf16_to_f32(ub)) * rs[:, None]
+    ref = gt / (1 + np.exp(-np.clip(gt, -80, 80))) * up
+    # bf16 output: 1e-2 relative, plus an absolute floor scaled to the output's
+    # magnitude (q4 activations here reach ~1e5)
+    assert np.all(np.abs(bf16_f32(act) - ref) <= 1e-2 * np.abs(ref) + 1e-5 * np.abs(ref).max())
+
+
+def test_q4_rejects_bad_arguments(gpu_device):
+    a = N.GemmArgs()
+    buf = torch.zeros(1 << 16, dtype=torch.uint8, device=gpu_device)
+    a.x = buf.data_ptr(); a.x_layout = N.W_TILED; a.ldx = 64; a.rows_padded = 32
+    a.w = buf.data_ptr(); a.w_layout = N.W_Q4G64; a.w_scales = None; a.n = 64; a.k = 64
+    a.epilogue = N.EPI_STORE_F32; a.out_f32 = buf.data_ptr(); a.ld_out_f32 = 64
+    a.workspace = buf.data_ptr(); a.workspace_bytes = buf.numel()
+    assert N.lib().dtree_gemm_bf16(C.byref(a), stream()) != 0  # no scales
+    a.w_scales = buf.data_ptr(); a.split_k = 2
+    assert N.lib().dtree_gemm_bf16(C.byref(a), stream()) != 0  # q4 is stream-K only
