@@ -31,14 +31,19 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(cfg, P: int, L: int) -> dict:
+def weight_bytes(params: int, quant: str) -> int:
+    """bf16: 2 B per weight; q4 group-64: half a byte plus a bf16 scale and bias per 64."""
+    return params * 2 if quant == "bf16" else params // 2 + params // 64 * 4
+
+
+def algorithmic_bytes(cfg, P: int, L: int, quant: str = "bf16") -> dict:
     """Minimum HBM bytes of one verify step (weights once, KV prefix read, tree KV write)."""
     H, F, V, D = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.head_dim
     nl = cfg.num_hidden_layers
-    lin = nl * cfg.layer_linear_params() * 2
-    lm = V * H * 2
+    lin = weight_bytes(nl * cfg.layer_linear_params(), quant)
+    lm = weight_bytes(V * H, quant)
     norms = (nl * (2 * H + 2 * D) + H) * 2
-    emb = L * H * 2
+    emb = weight_bytes(L * H, quant)
     kv_read = nl * 2 * cfg.num_key_value_heads * P * D * 2
     kv_write = nl * 2 * cfg.num_key_value_heads * L * D * 2
     total = lin + lm + norms + emb + kv_read + kv_write
@@ -98,7 +103,7 @@ def cpu_baseline(cfg, weights, cache, tree, P, sample_layers=4, min_seconds=15.0
                        f"the LM head, scaled linearly to one step ({t_step:.2f} s)")}
 
 
-def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int) -> dict:
+def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str = "bf16") -> dict:
     """Average launch duration of every kernel of the step, timed live with HIP
     events on the launch stream (torch's current stream), each kernel class
     rotating over the 36 layers' weights so every launch streams from HBM.
@@ -150,28 +155,30 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int) -> dict:
     us["lm_head"] = timed(lambda r: eng.launch_lm_head(st))
     keep.append(refs)
 
+    wb = lambda params: weight_bytes(params, quant)  # noqa: E731
     b = {
-        "qkv": qkv_n * H * 2 + L * H * 2 + L * qkv_n * 2,
-        "o": H * cfg.q_dim * 2 + L * cfg.q_dim * 2 + L * H * 2,
-        "gu": 2 * F * H * 2 + L * H * 2 + L * F * 2,
-        "down": H * F * 2 + L * F * 2 + L * H * 2,
+        "qkv": wb(qkv_n * H) + L * H * 2 + L * qkv_n * 2,
+        "o": wb(H * cfg.q_dim) + L * cfg.q_dim * 2 + L * H * 2,
+        "gu": wb(2 * F * H) + L * H * 2 + L * F * 2,
+        "down": wb(H * F) + L * F * 2 + L * H * 2,
         "attention": 2 * Hkv * P * D * 2 + 2 * Hkv * L * D * 2 + L * qkv_n * 2 + L * cfg.q_dim * 2,
-        "lm_head": V * H * 2 + L * H * 2,
+        "lm_head": wb(V * H) + L * H * 2,
     }
+    q4 = "true" if quant == "q4" else "false"
     out = {}
 
     def entry(kernel, n, t_us, nbytes):
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    out["qkv_gemm"] = entry("gemm_kernel<1, 2, 2, true, true, 0>", nl, us["qkv"], b["qkv"])
+    out["qkv_gemm"] = entry(f"sk_gemm_kernel<true, 0, {q4}>", nl, us["qkv"], b["qkv"])
     out["attention"] = entry("tree_attn_kernel<128>", nl, us["attention"], b["attention"])
     # o_proj and down_proj share one instantiation (residual epilogue): its
     # average launch is the mean of the two shapes, as the profiler reports.
-    out["residual_gemm"] = entry("gemm_kernel<1, 2, 2, true, true, 1>", 2 * nl, (us["o"] + us["down"]) / 2,
+    out["residual_gemm"] = entry(f"sk_gemm_kernel<true, 1, {q4}>", 2 * nl, (us["o"] + us["down"]) / 2,
                                  (b["o"] + b["down"]) / 2)
-    out["gate_up_gemm"] = entry("gemm_kernel<1, 2, 2, true, true, 2>", nl, us["gu"], b["gu"])
-    out["lm_head"] = entry("lmhead_kernel<1, 2, 2, true, true>", 1, us["lm_head"], b["lm_head"])
+    out["gate_up_gemm"] = entry(f"sk_gemm_kernel<true, 2, {q4}>", nl, us["gu"], b["gu"])
+    out["lm_head"] = entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"])
     out["residual_gemm"]["shapes_us"] = {"o_proj": us["o"], "down_proj": us["down"]}
     return out
 
@@ -198,6 +205,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--prefix", type=int, default=1024)
     ap.add_argument("--budget", type=int, default=24)
+    ap.add_argument("--quant", choices=["bf16", "q4"], default="bf16",
+                    help="q4: every linear layer and the tied LM head in 4-bit affine groups of 64")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=108)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -223,7 +232,10 @@ def main():
     cfg = QWEN3_4B
     P = a.prefix
     t0 = time.time()
-    w = Qwen3Weights.random(cfg, seed=0, device=dev)
+    if a.quant == "q4":
+        w = Qwen3Weights.random_q4(cfg, seed=0, device=dev)
+    else:
+        w = Qwen3Weights.random(cfg, seed=0, device=dev)
     model = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33])
     eng = model.engine
     cache = eng.new_cache()
@@ -261,18 +273,18 @@ def main():
     elapsed = time.perf_counter() - t_start
     ms = elapsed / a.steps * 1e3
     steps_per_s = a.steps / elapsed
-    ab = algorithmic_bytes(cfg, P, L)
+    ab = algorithmic_bytes(cfg, P, L, a.quant)
     gbps = ab["total"] / (ms * 1e-3) / 1e9
     log(f"[bench] {ms:.3f} ms/step  {steps_per_s:.1f} steps/s  {gbps:.0f} GB/s")
 
-    kernels = time_kernels(eng, cfg, w, cache, st, P, L, a.kernel_reps)
+    kernels = time_kernels(eng, cfg, w, cache, st, P, L, a.kernel_reps, a.quant)
     for name, kd in kernels.items():
         log(f"[bench] {name:10s} {kd['avg_launch_us']:7.1f} us/launch x {kd['launches_per_step']:2d}  "
             f"{kd['achieved_gbps']:6.0f} GB/s  ({kd['kernel']})")
     dom = max(kernels, key=lambda k: kernels[k]["avg_launch_us"] * kernels[k]["launches_per_step"])
     kd = kernels[dom]
     traffic = None
-    tf = ROOT / "profiles" / f"{dom}_traffic.json"
+    tf = ROOT / "profiles" / (f"{dom}_traffic.json" if a.quant == "bf16" else f"{dom}_q4_traffic.json")
     if tf.exists():
         try:
             traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
@@ -287,7 +299,8 @@ def main():
 
     mean_acc = sum(accepted_lens) / len(accepted_lens)
     out = {
-        "metric": "tree-verify steps/s + HBM GB/s (% of peak), 24-node tree, Qwen3-4B bf16",
+        "metric": ("tree-verify steps/s + HBM GB/s (% of peak), 24-node tree, Qwen3-4B bf16" if a.quant == "bf16"
+                   else "tree-verify steps/s + HBM GB/s (% of peak), 24-node tree, Qwen3-4B q4 group-64"),
         "value": round(steps_per_s, 3),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -297,10 +310,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: random-init weights N(0,0.02), uniform prefix ids, seeded Gumbel draft tree",
-        "config": {"workload": "Qwen3-4B-shaped bf16 tree-verify step (36 layers, LM-head argmax, walk, "
-                               "compaction)", "prefix": P, "tree_nodes": L, "draft_budget": a.budget,
+        "dtype": "bf16" if a.quant == "bf16" else "q4g64 weights, bf16 activations",
+        "data": ("synthetic: random-init weights N(0,0.02), uniform prefix ids, seeded Gumbel draft tree"
+                 if a.quant == "bf16" else
+                 "synthetic: q4 nibbles uniform 0..15, scales |N(0,0.02)|*8, biases N(0,0.01), uniform prefix ids, "
+                 "seeded Gumbel draft tree"),
+        "config": {"workload": (f"Qwen3-4B-shaped {'bf16' if a.quant == 'bf16' else 'q4 group-64'} tree-verify step "
+                                "(36 layers, LM-head argmax, walk, compaction)"),
+                   "prefix": P, "tree_nodes": L, "draft_budget": a.budget,
                    "layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size, "vocab": cfg.vocab_size},
         "hbm_gbps": round(gbps, 1),
         "hbm_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),

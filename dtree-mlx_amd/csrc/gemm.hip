@@ -377,6 +377,135 @@ __device__ __forceinline__ u32x4_t q4_pairs(uint32_t w) {
                  ((w >> 8) & 0x000F000Fu) | 0x43004300u, ((w >> 12) & 0x000F000Fu) | 0x43004300u};
 }
 
+// ---- q4 helpers for 32 rows ----------------------------------------------------
+// Activation sums per (K group, row) over groups [kb0, kb0 + ng) into
+// xsum[j * 32 + m] (j = group - kb0): the affine bias term and the 128 offset
+// of the nibble encoding need them.
+template <bool LO>
+__device__ __forceinline__ void q4_xsums(const uint16_t* x, const uint16_t* xlo, int kb0, int ng, int nkb,
+                                         float* xsum) {
+  for (int pr = threadIdx.x; pr < ng * 32; pr += kThreads) {
+    const int j = pr >> 5, m = pr & 31;
+    int kb = kb0 + j;
+    if (kb >= nkb) kb -= nkb;
+    float sum = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const size_t off = (size_t)kb * 2048 + (size_t)(i * 64 + m + 32 * hh) * 8;
+        const u32x4_t v = ld_u32x4(x + off);
+        u32x4_t vl = u32x4_t{0u, 0u, 0u, 0u};
+        if (LO) vl = ld_u32x4(xlo + off);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          sum += (__uint_as_float(v[q] << 16) + __uint_as_float(v[q] & 0xffff0000u)) +
+                 (__uint_as_float(vl[q] << 16) + __uint_as_float(vl[q] & 0xffff0000u));
+      }
+    xsum[j * 32 + m] = sum;
+  }
+}
+
+// One q4 group (64 K) of two 32-column blocks: fresh MFMA sums of x (128 + q),
+// then acc += s * sums + (b - 128 s) * sum(x) per (row, column).
+template <bool LO>
+__device__ __forceinline__ void q4_group(const u32x4_t (&xv)[2][4], const u32x4_t (&wq)[2], const uint32_t (&sb)[2],
+                                         const float* xs_group, int h, f32x16_t (&acc)[2]) {
+  f32x4_t xsv[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) xsv[q] = *reinterpret_cast<const f32x4_t*>(xs_group + 4 * h + 8 * q);
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    f32x16_t au;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) au[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4_t bq = q4_pairs(wq[nb][i]);
+      au = mfma32(xv[0][i], bq, au);
+      if (LO) au = mfma32(xv[1][i], bq, au);
+    }
+    const float sc = __uint_as_float(sb[nb] << 16);
+    const float cf = __uint_as_float(sb[nb] & 0xffff0000u) - 128.f * sc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[nb][r] += sc * au[r] + cf * xsv[r >> 2][r & 3];
+  }
+}
+
+// q4 counterpart of wg_tile for 32 rows and 64 columns (two 32-row blocks):
+// the tile over all K, waves interleaving groups, a 4-deep register ring of
+// (q4 words, scale/bias, activations), LDS reduction of the four waves into
+// red[row * 64 + col] in wave order. xsum holds every group's activation sums.
+template <bool LO>
+__device__ __forceinline__ void wg_tile_q4(const uint16_t* __restrict__ x, const uint16_t* __restrict__ xlo,
+                                           const uint32_t* __restrict__ wq, const uint32_t* __restrict__ wsb,
+                                           int K, int tile, const float* xsum, float* red) {
+  constexpr int TN = 64, TE = 32 * TN, D = 4;
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nkb = K >> 6;
+  const int n = wave < nkb ? (nkb - wave + kWaves - 1) / kWaves : 0;  // groups wave, wave + 4, ...
+  f32x16_t acc[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
+  u32x4_t wr[D][2], xr[D][2][4];
+  uint32_t sbr[D][2];
+  auto issue = [&](int s, int j) {
+    if (j < n) {
+      const int kb = wave + kWaves * j;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xr[s][0][i] = ld_u32x4(x + (size_t)kb * 2048 + lane * 8 + 512 * i);
+        if (LO) xr[s][1][i] = ld_u32x4(xlo + (size_t)kb * 2048 + lane * 8 + 512 * i);
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const size_t blk = (size_t)(2 * tile + nb) * nkb + kb;
+        wr[s][nb] = ld_u32x4_stream(wq + blk * 256 + lane * 4);
+        sbr[s][nb] = wsb[blk * 32 + c];
+      }
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < D; ++s) issue(s, s);
+  for (int j0 = 0; j0 < n; j0 += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int j = j0 + s;
+      if (j < n) {
+        __builtin_amdgcn_sched_barrier(0);
+        q4_group<LO>(xr[s], wr[s], sbr[s], xsum + (wave + kWaves * j) * 32, h, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(s, j + D);
+      }
+    }
+  }
+  if (wave > 0) {
+    float* my = red + (wave - 1) * TE;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) my[acc_row(r, h) * TN + nb * 32 + c] = acc[nb][r];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int wv = 0; wv < kWaves - 1; ++wv)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[nb][r] += red[wv * TE + acc_row(r, h) * TN + nb * 32 + c];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[acc_row(r, h) * TN + nb * 32 + c] = acc[nb][r];
+  }
+  __syncthreads();
+}
+
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* part, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)bytes, 0x00020000);
 }
@@ -409,28 +538,7 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   // (the affine bias term and the 128 offset of the nibble encoding need them).
   const int ngrp = (U1 - U0) < nkb ? (U1 - U0) : nkb;
   const int kbase = (U1 - U0) < nkb ? U0 % nkb : 0;
-  if constexpr (Q4) {
-    for (int pr = threadIdx.x; pr < ngrp * 32; pr += kThreads) {
-      const int j = pr >> 5, m = pr & 31;
-      int kb = kbase + j;
-      if (kb >= nkb) kb -= nkb;
-      float sum = 0.f;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const size_t off = (size_t)kb * 2048 + (size_t)(i * 64 + m + 32 * hh) * 8;
-          const u32x4_t v = ld_u32x4(p.x + off);
-          u32x4_t vl = u32x4_t{0u, 0u, 0u, 0u};
-          if (LO) vl = ld_u32x4(p.x_lo + off);
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            sum += (__uint_as_float(v[q] << 16) + __uint_as_float(v[q] & 0xffff0000u)) +
-                   (__uint_as_float(vl[q] << 16) + __uint_as_float(vl[q] & 0xffff0000u));
-        }
-      xsum_lds[j * 32 + m] = sum;
-    }
-  }
+  if constexpr (Q4) q4_xsums<LO>(p.x, p.x_lo, kbase, ngrp, nkb, xsum_lds);
   __syncthreads();
 
   // ---- stream this wave's quarter of the range ----
@@ -506,30 +614,10 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
         }
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (Q4) {
-          // One group: fresh MFMA sums of x (128 + q), then
-          // y += s * acc + (b - 128 s) * sum(x) per (row, column).
           int j = u - b * nkb - kbase;
           if (j < 0) j += nkb;
-          const float* xs = xsum_lds + j * 32 + 4 * h;
-          f32x4_t xsv[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) xsv[q] = *reinterpret_cast<const f32x4_t*>(xs + 8 * q);
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) {
-            f32x16_t au;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) au[r] = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const u32x4_t bq = q4_pairs(wr[s][nb][0][i]);
-              au = mfma32(xr[s][0][i], bq, au);
-              if (LO) au = mfma32(xr[s][1][i], bq, au);
-            }
-            const float sc = __uint_as_float(sbr[s][nb] << 16);
-            const float cf = __uint_as_float(sbr[s][nb] & 0xffff0000u) - 128.f * sc;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[nb][r] += sc * au[r] + cf * xsv[r >> 2][r & 3];
-          }
+          u32x4_t wq2[2] = {wr[s][0][0], wr[s][1][0]};
+          q4_group<LO>(xr[s], wq2, sbr[s], xsum_lds + j * 32, h, acc);
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
@@ -628,6 +716,7 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
 struct LmParams {
   const uint16_t* x; const uint16_t* x_lo; int ldx;
   const uint16_t* w; int vocab, k;
+  const uint16_t* w_sb;  // q4: (scale, bias) pairs
   int ntiles;
   const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
   float* logits;
@@ -641,7 +730,7 @@ __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi)
   }
 }
 
-template <int MB, int NB, int U, bool LO, bool TILED>
+template <int MB, int NB, int U, bool LO, bool TILED, bool Q4>
 __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   constexpr int MP = MB * 32;
   constexpr int TN = 32 * NB;
@@ -650,7 +739,10 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   __shared__ float red[(kWaves - 1) * TE];
   __shared__ float rs[MP];
   __shared__ float rs_scratch[kThreads];
+  __shared__ float xsum[Q4 ? kSkMaxKb * 32 : 1];
+  static_assert(!Q4 || (MB == 1 && NB == 2), "q4 LM head: 32 rows, 64-column tiles");
   row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs, rs_scratch);
+  if constexpr (Q4) q4_xsums<LO>(p.x, p.x_lo, 0, p.k >> 6, p.k >> 6, xsum);
   float bv[IT];
   int bi[IT];
 #pragma unroll
@@ -662,7 +754,11 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   const int n = threadIdx.x % TN;
   for (int tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     __syncthreads();
-    wg_tile<MB, NB, U, LO, TILED>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, 0, nkb, red);
+    if constexpr (Q4)
+      wg_tile_q4<LO>(p.x, p.x_lo, reinterpret_cast<const uint32_t*>(p.w), reinterpret_cast<const uint32_t*>(p.w_sb),
+                     p.k, tile, xsum, red);
+    else
+      wg_tile<MB, NB, U, LO, TILED>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, 0, nkb, red);
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int e = threadIdx.x + i * kThreads;
@@ -744,12 +840,17 @@ template <int MB>
 static void launch_lm(const LmParams& p, int grid, hipStream_t st, bool tiled) {
   constexpr int NB = Cfg<MB>::NB, U = Cfg<MB>::U;
   if (p.x_lo) {
-    if (tiled) lmhead_kernel<MB, NB, U, true, true><<<grid, kThreads, 0, st>>>(p);
-    else lmhead_kernel<MB, NB, U, true, false><<<grid, kThreads, 0, st>>>(p);
+    if (tiled) lmhead_kernel<MB, NB, U, true, true, false><<<grid, kThreads, 0, st>>>(p);
+    else lmhead_kernel<MB, NB, U, true, false, false><<<grid, kThreads, 0, st>>>(p);
   } else {
-    if (tiled) lmhead_kernel<MB, NB, U, false, true><<<grid, kThreads, 0, st>>>(p);
-    else lmhead_kernel<MB, NB, U, false, false><<<grid, kThreads, 0, st>>>(p);
+    if (tiled) lmhead_kernel<MB, NB, U, false, true, false><<<grid, kThreads, 0, st>>>(p);
+    else lmhead_kernel<MB, NB, U, false, false, false><<<grid, kThreads, 0, st>>>(p);
   }
+}
+
+static void launch_lm_q4(const LmParams& p, int grid, hipStream_t st) {
+  if (p.x_lo) lmhead_kernel<1, 2, 2, true, true, true><<<grid, kThreads, 0, st>>>(p);
+  else lmhead_kernel<1, 2, 2, false, true, true><<<grid, kThreads, 0, st>>>(p);
 }
 
 // Workspace = a fixed counter region (so GEMMs of different shapes can share
@@ -915,8 +1016,8 @@ extern "C" int dtree_lmhead_candidate_blocks(int32_t vocab, int32_t rows_padded)
 
 extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int32_t x_layout, int32_t ldx,
                                    int32_t rows_padded,
-                                   const uint16_t* emb, int32_t emb_layout, int32_t vocab, int32_t hidden,
-                                   const float* ss_in,
+                                   const uint16_t* emb, int32_t emb_layout, const uint16_t* emb_scales,
+                                   int32_t vocab, int32_t hidden, const float* ss_in,
                                    int32_t ss_tiles, float eps, float* logits, void* candidates,
                                    hipStream_t stream) {
   DTREE_REQUIRE(x && emb && candidates, "lmhead: null pointer");
@@ -926,11 +1027,21 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
   DTREE_REQUIRE(vocab > 0 && vocab % tn == 0, "lmhead: vocab must be a multiple of 64 (32 for > 64 rows)");
   DTREE_REQUIRE(hidden > 0 && hidden % 64 == 0 && ldx >= hidden, "lmhead: hidden must be a multiple of 64");
   LmParams p{};
-  p.x = x; p.x_lo = x_lo; p.ldx = ldx; p.w = emb; p.vocab = vocab; p.k = hidden; p.ntiles = vocab / tn;
+  p.x = x; p.x_lo = x_lo; p.ldx = ldx; p.w = emb; p.w_sb = emb_scales; p.vocab = vocab; p.k = hidden;
+  p.ntiles = vocab / tn;
   p.ss_in = ss_in; p.ss_tiles = ss_tiles; p.inv_norm_dim = 1.0f / (float)hidden; p.eps = eps;
   p.logits = logits; p.cand = reinterpret_cast<int2*>(candidates);
   const int grid = lmhead_grid(p.ntiles);
-  DTREE_REQUIRE(emb_layout == DTREE_W_ROWMAJOR || emb_layout == DTREE_W_TILED, "lmhead: unknown emb_layout");
+  DTREE_REQUIRE(emb_layout == DTREE_W_ROWMAJOR || emb_layout == DTREE_W_TILED || emb_layout == DTREE_W_Q4G64,
+                "lmhead: unknown emb_layout");
+  if (emb_layout == DTREE_W_Q4G64) {
+    DTREE_REQUIRE(x_layout == DTREE_W_TILED && ldx == hidden && rows_padded == 32 && hidden / 64 <= kSkMaxKb,
+                  "lmhead: q4 embedding needs tiled 32-row x and hidden <= 4096");
+    DTREE_REQUIRE(emb_scales && ((uintptr_t)emb & 15) == 0, "lmhead: q4 embedding needs emb_scales");
+    launch_lm_q4(p, grid, stream);
+    DTREE_LAUNCH_CHECK("lmhead launch");
+    return DTREE_OK;
+  }
   DTREE_REQUIRE(x_layout == emb_layout, "lmhead: x_layout must equal emb_layout");
   DTREE_REQUIRE(emb_layout != DTREE_W_TILED || ldx == hidden, "lmhead: tiled x needs ldx == hidden");
   const bool tiled = emb_layout == DTREE_W_TILED;

@@ -25,8 +25,23 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const DtreeStepDesc* de
 
 // x[m][:] = E[tokens[m]] (rows >= L zero), xg = bf16(x * g), ss[tile][m].
 // Blocks [0, H/256) gather; the remaining blocks fill the RoPE table.
-__global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, const uint16_t* emb, int tiled, int V,
-                                                    int H,
+// Element (row, col) of an embedding in DTREE_W_Q4G64 layout, dequantised:
+// scale * q + bias of the row's group col / 64.
+__device__ __forceinline__ float q4_element(const uint32_t* words, const uint32_t* sb, int row, int col, int H) {
+  const int nkb = H >> 6, kb = col >> 6, kk = col & 63;
+  const int l = (row & 31) + 32 * (kk >> 5), i = (kk & 31) >> 3, e = kk & 7;
+  const size_t blk = (size_t)(row >> 5) * nkb + kb;
+  const uint32_t w = words[(blk * 64 + l) * 4 + i];
+  const float q = (float)((w >> ((e & 1) * 16 + 4 * (e >> 1))) & 0xFu);
+  const uint32_t pr = sb[blk * 32 + (row & 31)];
+  return __uint_as_float(pr << 16) * q + __uint_as_float(pr & 0xffff0000u);
+}
+
+// Thread = one hidden column over all rows: x[m] = E[tokens[m]], xg = split(x * g),
+// ss = per-32-column sums of x^2. Rows go in batches of 32 whose loads are all
+// issued before any use.
+__global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, const uint16_t* emb, int layout,
+                                                    const uint16_t* emb_sb, int V, int H,
                                                     const uint16_t* g, int MP, float* x, uint16_t* xg,
                                                     uint16_t* xg_lo, int xg_tiled, float* ss,
                                                     int half, float base, float* cos_out, float* sin_out,
@@ -40,25 +55,40 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
   const bool in = col < H;
   const int L = min(desc->num_nodes, MP);
   const float gw = in ? bf2f(g[col]) : 0.f;
-  for (int m = 0; m < MP; ++m) {
-    float v = 0.f;
-    if (in && m < L) {
-      const int tok = desc->tokens[m];
-      if (tok >= 0 && tok < V)  // out-of-range ids embed as zero
-        v = bf2f(emb[tiled ? tiled_index(tok, col, H) : (size_t)tok * H + col]);
-    }
-    if (in) {
-      x[(size_t)m * H + col] = v;
-      const float vg = v * gw;
-      const uint16_t hi = f2bf(vg);
-      const size_t xi = xg_tiled ? tiled_index(m, col, H) : (size_t)m * H + col;
-      xg[xi] = hi;
-      if (xg_lo) xg_lo[xi] = f2bf(vg - bf2f(hi));
-    }
-    float sq = v * v;
+  for (int m0 = 0; m0 < MP; m0 += 32) {
+    float v[32];
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
-    if (in && n == 0) ss[(size_t)(col >> 5) * MP + m] = sq;
+    for (int j = 0; j < 32; ++j) {
+      const int m = m0 + j;
+      v[j] = 0.f;
+      if (in && m < L) {
+        const int tok = desc->tokens[m];
+        if (tok >= 0 && tok < V) {  // out-of-range ids embed as zero
+          if (layout == DTREE_W_Q4G64)
+            v[j] = q4_element(reinterpret_cast<const uint32_t*>(emb), reinterpret_cast<const uint32_t*>(emb_sb), tok,
+                              col, H);
+          else
+            v[j] = bf2f(emb[layout == DTREE_W_TILED ? tiled_index(tok, col, H) : (size_t)tok * H + col]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int m = m0 + j;
+      if (m >= MP) break;
+      if (in) {
+        x[(size_t)m * H + col] = v[j];
+        const float vg = v[j] * gw;
+        const uint16_t hi = f2bf(vg);
+        const size_t xi = xg_tiled ? tiled_index(m, col, H) : (size_t)m * H + col;
+        xg[xi] = hi;
+        if (xg_lo) xg_lo[xi] = f2bf(vg - bf2f(hi));
+      }
+      float sq = v[j] * v[j];
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+      if (in && n == 0) ss[(size_t)(col >> 5) * MP + m] = sq;
+    }
   }
 }
 
@@ -229,16 +259,19 @@ extern "C" int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, 
   return DTREE_OK;
 }
 
-extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t embed_layout, int32_t vocab,
-                           int32_t hidden,
+extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t embed_layout,
+                           const uint16_t* embed_scales, int32_t vocab, int32_t hidden,
                            const uint16_t* norm_w, int32_t rows_padded, float* x, uint16_t* xg, uint16_t* xg_lo,
                            int32_t xg_layout, float* ss, int32_t head_dim, float rope_base,
                            float* rope_cos, float* rope_sin, hipStream_t stream) {
   DTREE_REQUIRE(desc && embed && norm_w && x && xg && ss, "embed: null pointer");
   DTREE_REQUIRE(hidden > 0 && hidden % 32 == 0, "embed: hidden must be a multiple of 32");
   DTREE_REQUIRE(vocab > 0, "embed: vocab");
-  DTREE_REQUIRE(embed_layout == DTREE_W_ROWMAJOR || (embed_layout == DTREE_W_TILED && hidden % 64 == 0 && vocab % 32 == 0),
+  DTREE_REQUIRE(embed_layout == DTREE_W_ROWMAJOR ||
+                    ((embed_layout == DTREE_W_TILED || embed_layout == DTREE_W_Q4G64) && hidden % 64 == 0 &&
+                     vocab % 32 == 0),
                 "embed: layout");
+  DTREE_REQUIRE(embed_layout != DTREE_W_Q4G64 || embed_scales, "embed: q4 embedding needs embed_scales");
   DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || (xg_layout == DTREE_W_TILED && hidden % 64 == 0), "embed: xg layout");
   DTREE_REQUIRE(rows_padded > 0 && rows_padded <= DTREE_MAX_NODES && rows_padded % 32 == 0, "embed: rows_padded");
   const int gather = (hidden + 255) / 256;
@@ -247,9 +280,10 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
     DTREE_REQUIRE(head_dim > 0 && head_dim % 2 == 0, "embed: head_dim");
     rope_blocks = (rows_padded * head_dim / 2 + 255) / 256;
   }
-  embed_kernel<<<gather + rope_blocks, 256, 0, stream>>>(desc, embed, embed_layout, vocab, hidden, norm_w, rows_padded,
-                                                          x, xg, xg_lo, xg_layout == DTREE_W_TILED, ss,
-                                                          head_dim / 2, rope_base, rope_cos, rope_sin, gather);
+  embed_kernel<<<gather + rope_blocks, 256, 0, stream>>>(desc, embed, embed_layout, embed_scales, vocab, hidden,
+                                                          norm_w, rows_padded, x, xg, xg_lo,
+                                                          xg_layout == DTREE_W_TILED, ss, head_dim / 2, rope_base,
+                                                          rope_cos, rope_sin, gather);
   DTREE_LAUNCH_CHECK("embed launch");
   return DTREE_OK;
 }

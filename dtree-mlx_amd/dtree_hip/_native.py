@@ -89,15 +89,15 @@ SIGNATURES = {
     "dtree_attn_args_bytes": (_sz, []),
     "dtree_gemm_workspace_bytes": (_sz, [C.c_int, C.c_int, C.c_int, C.c_int]),
     "dtree_gemm_bf16": (C.c_int, [C.POINTER(GemmArgs), _vp]),
-    "dtree_embed": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _vp, _vp,
-                              _vp]),
+    "dtree_embed": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _vp,
+                              _vp, _vp]),
     "dtree_rope_table": (C.c_int, [_vp, _i32, _i32, _f32, _vp, _vp, _vp]),
     "dtree_attention_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "dtree_tree_attention": (C.c_int, [C.POINTER(AttnArgs), _vp]),
     "dtree_lmhead_candidates_bytes": (_sz, [_i32]),
     "dtree_lmhead_candidate_blocks": (C.c_int, [_i32, _i32]),
-    "dtree_lmhead_argmax": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _i32, _f32, _vp, _vp,
-                                      _vp]),
+    "dtree_lmhead_argmax": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _f32, _vp,
+                                      _vp, _vp]),
     "dtree_tile_weight": (C.c_int, [_vp, _vp, _i32, _i32, _vp]),
     "dtree_accept_walk": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "dtree_compact": (C.c_int, [_vp, _vp, _vp, _sz, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),

@@ -24,7 +24,7 @@ import torch
 from . import _native as N
 from .cache import PagedKVCache
 from .config import Qwen3Config
-from .weights import W_TILED, Qwen3Weights, tile_weight
+from .weights import W_TILED, Q4Linear, Qwen3Weights, tile_weight
 
 
 def ancestor_bitsets(parents) -> np.ndarray:
@@ -199,7 +199,11 @@ class Qwen3TreeEngine:
         a.ldx = ldx; a.rows_padded = self.MP
         # Internal activations share the weights' layout (tiled: contiguous
         # kilobyte loads for both GEMM operands).
-        a.w = w.data_ptr(); a.w_layout = self.w.layout; a.x_layout = self.w.layout; a.n = n; a.k = k
+        if isinstance(w, Q4Linear):  # q4 group-64 weights (w_scales = scale/bias pairs)
+            a.w = w.words.data_ptr(); a.w_scales = w.sb.data_ptr(); a.w_layout = N.W_Q4G64
+        else:
+            a.w = w.data_ptr(); a.w_layout = self.w.layout
+        a.x_layout = self.w.layout; a.n = n; a.k = k
         a.epilogue = epi; a.split_k = self.split_k.get(name, 0)
         a.ss_in = ss_in.data_ptr() if ss_in is not None else None
         a.ss_tiles = self.cfg.hidden_size // 32 if ss_in is not None else 0
@@ -218,6 +222,13 @@ class Qwen3TreeEngine:
         a.hidden_out = hidden_out or None; a.ld_hidden = ld_hidden
         a.workspace = self.gemm_ws.data_ptr(); a.workspace_bytes = self.gemm_ws.numel()
         return a
+
+    def _embedding(self):
+        """(pointer, layout, scale/bias pointer) of the tied embedding."""
+        e = self.w.embed
+        if isinstance(e, Q4Linear):
+            return e.words.data_ptr(), N.W_Q4G64, e.sb.data_ptr()
+        return e.data_ptr(), self.w.layout, None
 
     def _gemm(self, name, x, ldx, w, epi, st, **kw):
         a = self.gemm_args(name, x, ldx, w, epi, **kw)
@@ -246,8 +257,9 @@ class Qwen3TreeEngine:
         H = c.hidden_size
         if cache.capacity < self.max_past + self.max_nodes:
             raise ValueError("cache capacity is smaller than max_past + max_nodes")
+        emb, emb_layout, emb_sb = self._embedding()
         N.check(self.lib.dtree_embed(
-            self.desc.data_ptr(), self.w.embed.data_ptr(), self.w.layout, c.vocab_size, H,
+            self.desc.data_ptr(), emb, emb_layout, emb_sb, c.vocab_size, H,
             self.w.layers[0].input_norm.data_ptr(),
             self.MP,
             self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
@@ -289,8 +301,9 @@ class Qwen3TreeEngine:
         else:
             xin = x
         hi, lo = (xin[0].data_ptr(), xin[1].data_ptr()) if xin.dim() == 3 else (xin.data_ptr(), None)
+        emb, emb_layout, emb_sb = self._embedding()
         N.check(self.lib.dtree_lmhead_argmax(
-            hi, lo, self.w.layout, xin.shape[-1], self.MP, self.w.embed.data_ptr(), self.w.layout, c.vocab_size, c.hidden_size,
+            hi, lo, self.w.layout, xin.shape[-1], self.MP, emb, emb_layout, emb_sb, c.vocab_size, c.hidden_size,
             self.ss.data_ptr() if ss else None, c.hidden_size // 32 if ss else 0, c.rms_norm_eps,
             logits_ptr, self.cand.data_ptr(), st), "lm head")
 

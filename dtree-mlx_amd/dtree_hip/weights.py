@@ -93,6 +93,68 @@ def q4_to_tiled(wq: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) ->
 
 
 @dataclass
+class Q4Linear:
+    """A q4 group-64 linear layer in DTREE_W_Q4G64 layout (see q4_to_tiled)."""
+    words: torch.Tensor   # int32 [N/32, K/64, 64, 4]
+    sb: torch.Tensor      # bf16 [N/32, K/64, 32, 2] (scale, bias)
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return self.words.shape[0] * 32, self.words.shape[1] * 64
+
+    @property
+    def device(self) -> torch.device:
+        return self.words.device
+
+    def numel(self) -> int:
+        n, k = self.shape
+        return n * k
+
+    def nbytes(self) -> int:
+        return self.words.numel() * 4 + self.sb.numel() * 2
+
+    def to(self, device) -> "Q4Linear":
+        return Q4Linear(self.words.to(device), self.sb.to(device))
+
+
+def q4_random_mlx(n: int, k: int, gen: torch.Generator, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Synthetic q4 layer in MLX layout: nibbles uniform in [0, 15], scales
+    |N(0, 0.02)| * 8, biases N(0, 0.01) (bf16). Returns (wq int32 [n, k/8],
+    scales, biases)."""
+    q = torch.randint(0, 16, (n, k // 8, 8), generator=gen, device=device, dtype=torch.int64)
+    wq = (q << (4 * torch.arange(8, device=device, dtype=torch.int64))).sum(-1)
+    wq = torch.where(wq >= 2 ** 31, wq - 2 ** 32, wq).to(torch.int32)
+    sc = torch.empty(n, k // 64, device=device).normal_(0.0, 0.02, generator=gen).abs_().mul_(8.0)
+    bi = torch.empty(n, k // 64, device=device).normal_(0.0, 0.01, generator=gen)
+    return wq, sc.to(torch.bfloat16), bi.to(torch.bfloat16)
+
+
+def q4_unpack_tiled(lin: Q4Linear) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """DTREE_W_Q4G64 -> (q uint8 [N, K], scales [N, K/64], biases [N, K/64]) in nn.Linear order."""
+    w = lin.words.to(torch.int64) & 0xFFFFFFFF                # r, b, l, i
+    nr, nkb = w.shape[0], w.shape[1]
+    nib = torch.stack([(w >> ((e & 1) * 16 + 4 * (e >> 1))) & 0xF for e in range(8)], dim=-1)  # r, b, l, i, e
+    nib = nib.reshape(nr, nkb, 2, 32, 4, 8).permute(0, 3, 1, 2, 4, 5)  # r, c, b, h, i, e
+    q = nib.reshape(nr * 32, nkb * 64).to(torch.uint8)
+    sb = lin.sb.permute(0, 2, 1, 3).reshape(nr * 32, nkb, 2)
+    return q, sb[..., 0], sb[..., 1]
+
+
+def q4_dequant(lin: Q4Linear) -> torch.Tensor:
+    """float32 [N, K] = scale * q + bias per group of 64 (nn.Linear order)."""
+    q, sc, bi = q4_unpack_tiled(lin)
+    return q.float() * sc.float().repeat_interleave(64, dim=1) + bi.float().repeat_interleave(64, dim=1)
+
+
+def q4_rows(lin: Q4Linear, ids: torch.Tensor) -> torch.Tensor:
+    """Dequantised rows `ids` of a q4 matrix (embedding lookups), bf16."""
+    r = ids.long().reshape(-1)
+    sub = Q4Linear(lin.words[r // 32], lin.sb[r // 32])
+    full = q4_dequant(sub).reshape(len(r), 32, -1)
+    return full[torch.arange(len(r), device=full.device), r % 32].to(torch.bfloat16).reshape(*ids.shape, -1)
+
+
+@dataclass
 class LayerWeights:
     input_norm: torch.Tensor
     wqkv: torch.Tensor
@@ -111,10 +173,45 @@ class Qwen3Weights:
     final_norm: torch.Tensor
     layers: list[LayerWeights] = field(default_factory=list)
     layout: int = W_TILED
+    quant: str = "bf16"   # "bf16" or "q4" (every linear and the embedding, group 64)
 
     @property
     def device(self) -> torch.device:
         return self.embed.device
+
+    @classmethod
+    def random_q4(cls, cfg: Qwen3Config, seed: int = 0, device="cuda", norm_jitter: float = 0.0) -> "Qwen3Weights":
+        """Seeded q4 group-64 model (every linear layer and the tied embedding,
+        as quantize_model quantises them): nibbles uniform in [0, 15], scales
+        |N(0, 0.02)| * 8, biases N(0, 0.01). Activations stay tiled bf16."""
+        cfg.validate()
+        dev = torch.device(device)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+
+        def q4(rows, cols):
+            return Q4Linear(*q4_to_tiled(*q4_random_mlx(rows, cols, gen, dev)))
+
+        def norm(n):
+            if norm_jitter == 0.0:
+                return torch.ones(n, dtype=torch.bfloat16, device=dev)
+            t = torch.empty(n, dtype=torch.float32, device=dev).normal_(0.0, norm_jitter, generator=gen)
+            return (1.0 + t).to(torch.bfloat16)
+
+        H, F, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+        embed = q4(cfg.vocab_size, H)
+        layers = []
+        for _ in range(cfg.num_hidden_layers):
+            wqkv = q4(cfg.qkv_dim, H)
+            wo = q4(H, cfg.q_dim)
+            gq, gs, gb = q4_random_mlx(F, H, gen, dev)
+            uq, us, ub = q4_random_mlx(F, H, gen, dev)
+            wgu = Q4Linear(*q4_to_tiled(interleave_gate_up(gq, uq), interleave_gate_up(gs, us),
+                                        interleave_gate_up(gb, ub)))
+            wd = q4(H, F)
+            layers.append(LayerWeights(input_norm=norm(H), wqkv=wqkv, q_norm=norm(D), k_norm=norm(D), wo=wo,
+                                       post_norm=norm(H), wgu=wgu, wd=wd))
+        return cls(cfg=cfg, embed=embed, final_norm=norm(H), layers=layers, layout=W_TILED, quant="q4")
 
     @classmethod
     def random(cls, cfg: Qwen3Config, seed: int = 0, device="cuda", std: float = 0.02,
@@ -157,15 +254,22 @@ class Qwen3Weights:
         return Qwen3Weights(
             cfg=self.cfg, embed=mv(self.embed), final_norm=mv(self.final_norm),
             layers=[LayerWeights(**{k: mv(getattr(lw, k)) for k in LayerWeights.__dataclass_fields__})
-                    for lw in self.layers], layout=self.layout)
+                    for lw in self.layers], layout=self.layout, quant=self.quant)
 
-    def rowmajor(self, t: torch.Tensor) -> torch.Tensor:
+    def rowmajor(self, t) -> torch.Tensor:
+        """nn.Linear-order bf16 (or, for q4, dequantised fp32) matrix."""
+        if isinstance(t, Q4Linear):
+            return q4_dequant(t)
         return untile_weight(t) if self.layout == W_TILED else t
 
     def embed_rows(self, ids: torch.Tensor) -> torch.Tensor:
+        if isinstance(self.embed, Q4Linear):
+            return q4_rows(self.embed, ids)
         return tiled_rows(self.embed, ids) if self.layout == W_TILED else self.embed[ids.long()]
 
     def nbytes_linear(self) -> int:
+        if self.quant == "q4":
+            return sum(lw.wqkv.nbytes() + lw.wo.nbytes() + lw.wgu.nbytes() + lw.wd.nbytes() for lw in self.layers)
         return sum(lw.wqkv.numel() + lw.wo.numel() + lw.wgu.numel() + lw.wd.numel()
                    for lw in self.layers) * 2
 
@@ -175,6 +279,8 @@ class Qwen3Weights:
         cache: dict = {}
 
         def bits(t: torch.Tensor) -> np.ndarray:
+            if t.dtype == torch.float32:  # dequantised q4: handed over as fp32
+                return t.detach().to("cpu").contiguous().numpy()
             return t.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16)
 
         def lin_bits(t: torch.Tensor) -> np.ndarray:

@@ -135,15 +135,17 @@ int dtree_gemm_bf16(const DtreeGemmArgs* args, hipStream_t stream);
 
 /*
  * Embedding gather + first RMSNorm fold (adapters.py:580, qwen3_tree.py:47):
- * x[m] = E[tokens[m]] (fp32; E in DTREE_W_* layout embed_layout), xg = bf16(x * norm_w) (+ optional low half
+ * x[m] = E[tokens[m]] (fp32; E in DTREE_W_* layout embed_layout; DTREE_W_Q4G64
+ * dequantises the row with embed_scales, as quantize_model quantises the
+ * embedding, api.py:46-54), xg = bf16(x * norm_w) (+ optional low half
  * xg_lo = bf16(x * norm_w - xg)), ss[t][m] = sum of x^2
  * over column tile t (32 columns); rows >= L and token ids outside
  * [0, vocab) embed as zero. Also fills the RoPE
  * table cos/sin [rows_padded][head_dim/2] for desc->positions
  * (mlx nn.RoPE, traditional=False, per-token offsets, qwen3_tree.py:22-27).
  */
-int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t embed_layout, int32_t vocab,
-                int32_t hidden, const uint16_t* norm_w, int32_t rows_padded, float* x, uint16_t* xg,
+int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int32_t embed_layout,
+                const uint16_t* embed_scales, int32_t vocab, int32_t hidden, const uint16_t* norm_w, int32_t rows_padded, float* x, uint16_t* xg,
                 uint16_t* xg_lo, int32_t xg_layout, float* ss, int32_t head_dim, float rope_base, float* rope_cos,
                 float* rope_sin, hipStream_t stream);
 
@@ -185,16 +187,18 @@ int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
 /*
  * Fused LM head + argmax (adapters.py:114-118, 489-492, first index on ties
  * as adapters.py:78-81): per row m, argmax_v rs[m] * (x[m] . E[v]).
- * x = x + x_lo (split pair, x_lo optional); E in layout emb_layout.
- * Writes per-workgroup (value, index) candidates to `candidates`
+ * x = x + x_lo (split pair, x_lo optional); E in layout emb_layout
+ * (DTREE_W_Q4G64: the quantised tied embedding with its (scale, bias) pairs in
+ * emb_scales, 32 tiled rows, hidden <= 4096; adapters.py:28-85 is the
+ * reference's q4 LM-head argmax). Writes per-workgroup (value, index) candidates to `candidates`
  * ([grid][rows_padded] float2-like pairs); dtree_accept_walk reduces them.
  * logits (optional, [rows_padded][vocab] fp32) receives every logit.
  */
 size_t dtree_lmhead_candidates_bytes(int32_t rows_padded);
 int dtree_lmhead_candidate_blocks(int32_t vocab, int32_t rows_padded);
 int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int32_t x_layout, int32_t ldx, int32_t rows_padded,
-                        const uint16_t* emb, int32_t emb_layout, int32_t vocab, int32_t hidden,
-                        const float* ss_in, int32_t ss_tiles, float eps,
+                        const uint16_t* emb, int32_t emb_layout, const uint16_t* emb_scales, int32_t vocab,
+                        int32_t hidden, const float* ss_in, int32_t ss_tiles, float eps,
                         float* logits, void* candidates, hipStream_t stream);
 
 /*

@@ -389,8 +389,8 @@ def _lmhead(x, E, dev, logits=None, ss=None, layout=0):
     cand = torch.zeros(lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=dev)
     if layout == N.W_TILED:
         x = tile_weight(x)
-    N.check(lib.dtree_lmhead_argmax(x.data_ptr(), None, layout, x.shape[1], MP, E.data_ptr(), layout, E.shape[0],
-                                    E.shape[1],
+    N.check(lib.dtree_lmhead_argmax(x.data_ptr(), None, layout, x.shape[1], MP, E.data_ptr(), layout, None,
+                                    E.shape[0], E.shape[1],
                                     ss.data_ptr() if ss is not None else None, ss.shape[0] if ss is not None else 0,
                                     1e-6, logits.data_ptr() if logits is not None else None, cand.data_ptr(),
                                     stream()))

@@ -138,3 +138,71 @@ def test_q4_rejects_bad_arguments(gpu_device):
     assert N.lib().dtree_gemm_bf16(C.byref(a), stream()) != 0  # no scales
     a.w_scales = buf.data_ptr(); a.split_k = 2
     assert N.lib().dtree_gemm_bf16(C.byref(a), stream()) != 0  # q4 is stream-K only
+
+
+def test_q4_lmhead_argmax_and_logits(gpu_device):
+    """Fused q4 LM head (quantised tied embedding): logits against the q4
+    oracle, argmax first index on ties, including a tie across workgroups."""
+    g = np.random.default_rng(91)
+    V, H, L = 151936, 2560, 25
+    wq, s, b = o4.random_q4(V, H, g)
+    # two equal rows far apart -> equal logits; the smaller index must win.
+    # Their scales are the largest, so their norm is too and (Cauchy-Schwarz)
+    # row 3 = 4 E[5] peaks there.
+    from oracle.qwen3 import f32_to_bf16_bits
+    s[5] = f32_to_bf16_bits(np.full(s.shape[1], 0.5, np.float32))
+    wq[151900] = wq[5]; s[151900] = s[5]; b[151900] = b[5]
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    wt, sb = wt.to(gpu_device), sb.to(gpu_device)
+    xf = np.zeros((32, H), np.float32)
+    xf[:L] = g.standard_normal((L, H))
+    E5 = o4.dequantize(wq[5:6], bf16_to_f32(s[5:6]), bf16_to_f32(b[5:6]))[0]
+    xf[3] = E5.astype(np.float32) * 4.0  # row 3 peaks at tokens 5 and 151900
+    hi = torch.from_numpy(xf).to(torch.bfloat16)
+    lo = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16)
+    xt, xlt = tile_weight(hi.to(gpu_device)), tile_weight(lo.to(gpu_device))
+    lib = N.lib()
+    cand = torch.zeros(lib.dtree_lmhead_candidates_bytes(32), dtype=torch.uint8, device=gpu_device)
+    logits = torch.zeros(32, V, device=gpu_device)
+    N.check(lib.dtree_lmhead_argmax(xt.data_ptr(), xlt.data_ptr(), N.W_TILED, H, 32, wt.data_ptr(), N.W_Q4G64,
+                                    sb.data_ptr(), V, H, None, 0, 1e-6, logits.data_ptr(), cand.data_ptr(),
+                                    stream()), "q4 lmhead")
+    torch.cuda.synchronize()
+    xin = hi.double().numpy() + lo.double().numpy()
+    ref = np.concatenate([o4.q4_matmul(xin[:L], wq[r:r + 8192], bf16_to_f32(s[r:r + 8192]),
+                                       bf16_to_f32(b[r:r + 8192])) for r in range(0, V, 8192)], axis=1)
+    got = logits[:L].cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    c = cand.view(torch.int32).view(-1, 32, 2)[: lib.dtree_lmhead_candidate_blocks(V, 32)].cpu().numpy()
+    vals, idx = c[..., 0].view(np.float32), c[..., 1]
+    best = []
+    for m in range(L):
+        order = np.lexsort((idx[:, m], -vals[:, m]))
+        best.append(int(idx[order[0], m]))
+    exact = np.argmax(got, axis=-1)
+    assert best == exact.tolist()
+    assert best[3] == 5
+
+
+def test_q4_embedding_gather(gpu_device):
+    """dtree_embed on a q4 embedding: x rows = scale * q + bias of each token."""
+    from gpu_util import device_desc
+    g = np.random.default_rng(5)
+    V, H, L = 4096, 1024, 25
+    wq, s, b = o4.random_q4(V, H, g)
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    toks = g.integers(0, V, L).tolist()
+    desc = device_desc(toks, list(range(L)), [-1] + list(range(L - 1)), 0, gpu_device)
+    nw = torch.ones(H, dtype=torch.bfloat16, device=gpu_device)
+    x = torch.zeros(32, H, device=gpu_device)
+    xg = torch.zeros(32, H, dtype=torch.bfloat16, device=gpu_device)
+    ss = torch.zeros(H // 32, 32, device=gpu_device)
+    N.check(N.lib().dtree_embed(desc.data_ptr(), wt.to(gpu_device).data_ptr(), N.W_Q4G64,
+                                sb.to(gpu_device).data_ptr(), V, H, nw.data_ptr(), 32, x.data_ptr(),
+                                xg.data_ptr(), None, N.W_ROWMAJOR, ss.data_ptr(), 128, 1e6, None, None, stream()),
+            "q4 embed")
+    torch.cuda.synchronize()
+    ref = o4.dequantize(wq[toks], bf16_to_f32(s[toks]), bf16_to_f32(b[toks]))
+    got = x.cpu().numpy()
+    assert np.abs(got[:L] - ref).max() <= 1e-6 * np.abs(ref).max()
+    assert np.all(got[L:] == 0)

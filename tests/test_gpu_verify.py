@@ -31,9 +31,12 @@ def _oracle_cfg(cfg):
                           vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_base=cfg.rope_theta)
 
 
-def _run(cfg, P, layer_ids, dev, norm_jitter=0.0, log=print):
+def _run(cfg, P, layer_ids, dev, norm_jitter=0.0, log=print, quant="bf16"):
     t0 = time.time()
-    w = Qwen3Weights.random(cfg, seed=0, device=dev, norm_jitter=norm_jitter)
+    if quant == "q4":  # every linear layer and the tied embedding in 4-bit groups of 64
+        w = Qwen3Weights.random_q4(cfg, seed=0, device=dev, norm_jitter=norm_jitter)
+    else:
+        w = Qwen3Weights.random(cfg, seed=0, device=dev, norm_jitter=norm_jitter)
     model = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=layer_ids)
     eng = model.engine
     cache = eng.new_cache()
@@ -127,6 +130,13 @@ def test_verify_step_tiny_model(gpu_device):
     assert len(res.accepted) >= 1
 
 
+def test_verify_step_tiny_model_q4(gpu_device):
+    cfg = tiny_qwen3()
+    r = _run(cfg, P=100, layer_ids=[0, 1], dev=gpu_device, norm_jitter=0.1, quant="q4")
+    res = _check(r, [0, 1])
+    assert len(res.accepted) >= 1
+
+
 def test_verify_step_graph_replays_match_eager(gpu_device):
     cfg = tiny_qwen3(num_hidden_layers=3)
     w = Qwen3Weights.random(cfg, seed=0, device=gpu_device)
@@ -152,5 +162,14 @@ def test_verify_step_graph_replays_match_eager(gpu_device):
 def test_verify_step_qwen3_4b_prefix_1024(gpu_device):
     """Full-size verify step: 36 layers, hidden 2560, vocab 151936, P=1024, 25 nodes."""
     r = _run(QWEN3_4B, P=1024, layer_ids=[1, 9, 17, 25, 33], dev=gpu_device)
+    res = _check(r, [1, 9, 17, 25, 33])
+    print("accepted", res.accepted, "bonus", res.bonus_token)
+
+
+def test_verify_step_qwen3_4b_q4_prefix_1024(gpu_device):
+    """The q4 workload: the same full-size step with every linear layer and the
+    tied LM head quantised to 4-bit groups of 64 (scales |N(0, 0.02)| * 8,
+    biases N(0, 0.01)); the oracle runs on the dequantised weights."""
+    r = _run(QWEN3_4B, P=1024, layer_ids=[1, 9, 17, 25, 33], dev=gpu_device, quant="q4")
     res = _check(r, [1, 9, 17, 25, 33])
     print("accepted", res.accepted, "bonus", res.bonus_token)
