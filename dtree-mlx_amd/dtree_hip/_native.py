@@ -102,6 +102,11 @@ SIGNATURES = {
     "dtree_accept_walk": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "dtree_compact": (C.c_int, [_vp, _vp, _vp, _sz, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
     "dtree_rownorm": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _i32, _vp]),
+    "dtree_gdn_tree_conv": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "dtree_gdn_tree_recurrence": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
+                                            _vp]),
+    "dtree_gdn_commit": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                   _vp]),
     "dtree_graph_begin": (C.c_int, [_vp]),
     "dtree_graph_end": (C.c_int, [_vp, C.POINTER(C.c_void_p)]),
     "dtree_graph_launch": (C.c_int, [_vp, _vp]),

@@ -229,6 +229,44 @@ int dtree_rownorm(const float* x, int32_t ldx, int32_t rows_padded, int32_t hidd
                   const float* ss_in, int32_t ss_tiles, const uint16_t* w, float eps,
                   uint16_t* out, int32_t ld_out, hipStream_t stream);
 
+/*
+ * Qwen3.5 GatedDeltaNet tree primitives (qwen35_tree_kernels.py:8-152, the
+ * tree layer qwen35_tree.py:180-480), fp32, nodes in heap order (parent <
+ * child, root parent -1), num_nodes <= DTREE_MAX_NODES.
+ *
+ * Tree causal conv1d + SiLU (tree_conv1d_kernel): x [T][C] conv inputs,
+ * base_window [keep][C], weight [keep + 1][C] (newest tap last). Node t's
+ * input rows are its parent's window (the base for the root) followed by
+ * x[t]; out[t] = silu(sum_r rows[r] * weight[r]). windows ([T][keep][C],
+ * optional) receives each node's window; NULL keeps evaluation lazy.
+ */
+int dtree_gdn_tree_conv(const float* x, const float* base_window, const float* weight, const int32_t* parents,
+                        int32_t num_nodes, int32_t channels, int32_t keep, float* out, float* windows,
+                        hipStream_t stream);
+/*
+ * Tree gated-delta recurrence (tree_gated_delta_kernel): q, k [T][Hk][Dk],
+ * v [T][Hv][Dv], g (multiplicative decay) and beta [T][Hv], base state
+ * [Hv][Dv][Dk]; value head h reads key head h / (Hv / Hk). Per node:
+ * S = S_parent * g; S += ((v - S k) * beta) (outer) k; y[t] = S q.
+ * states ([T][Hv][Dv][Dk], optional) receives every node's state; NULL keeps
+ * the node states in LDS only (lazy). Dk in {32, 64, 128}.
+ */
+int dtree_gdn_tree_recurrence(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                              const float* state, const int32_t* parents, int32_t num_nodes, int32_t num_k_heads,
+                              int32_t num_v_heads, int32_t head_k_dim, int32_t head_v_dim, float* y, float* states,
+                              hipStream_t stream);
+/*
+ * Commit of an accepted root path (commit_qwen35_tree_path,
+ * qwen35_tree.py:708-732): window (optional) becomes the last keep rows of
+ * (window ++ x[path]) and state (optional) the path's replayed state, both in
+ * place. path / path_len are device pointers (DtreeStepDesc.accepted /
+ * n_accepted), so a captured graph can run it after dtree_accept_walk.
+ */
+int dtree_gdn_commit(const float* x, float* window, int32_t channels, int32_t keep, const float* q, const float* k,
+                     const float* v, const float* g, const float* beta, float* state, const int32_t* path,
+                     const int32_t* path_len, int32_t num_k_heads, int32_t num_v_heads, int32_t head_k_dim,
+                     int32_t head_v_dim, hipStream_t stream);
+
 /* Convert a row-major [n][k] bf16 matrix to DTREE_W_TILED (n % 32 == 0,
  * k % 64 == 0; src and dst must not overlap). */
 int dtree_tile_weight(const uint16_t* src, uint16_t* dst, int32_t n, int32_t k, hipStream_t stream);

@@ -1,0 +1,146 @@
+"""GatedDeltaNet tree primitives on the GPU against the float64 oracle
+(oracle/gdn.py), through the C-ABI: the reference kernel tests' own seeded
+inputs (tests/test_qwen35_tree_kernels.py, tolerance 1e-5 as there), the
+Qwen3.5 layer shapes (conv_dim 8192; 16 key / 32 value heads of 128) on 25- and
+65-node trees, and the lazy commit of an accepted path."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import random_tree, stream
+from oracle import gdn
+
+from dtree_hip import _native as N
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+
+
+def _conv(x, base, w, parents, dev, want_windows=True):
+    T, Cc = x.shape
+    keep = base.shape[0]
+    out = torch.zeros(T, Cc, device=dev)
+    win = torch.zeros(T, keep, Cc, device=dev) if want_windows else None
+    par = torch.tensor(parents, dtype=torch.int32, device=dev)
+    xs, bs, ws = _t(x, dev), _t(base, dev), _t(w, dev)  # held until the kernel has run
+    N.check(N.lib().dtree_gdn_tree_conv(xs.data_ptr(), bs.data_ptr(), ws.data_ptr(),
+                                        par.data_ptr(), T, Cc, keep, out.data_ptr(),
+                                        win.data_ptr() if win is not None else None, stream()), "gdn conv")
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), (win.cpu().numpy() if win is not None else None)
+
+
+def _delta(q, k, v, g, beta, state, parents, dev, want_states=True):
+    T, Hk, Dk = k.shape
+    Hv, Dv = v.shape[1], v.shape[2]
+    y = torch.zeros(T, Hv, Dv, device=dev)
+    st = torch.zeros(T, Hv, Dv, Dk, device=dev) if want_states else None
+    par = torch.tensor(parents, dtype=torch.int32, device=dev)
+    keep = [_t(a, dev) for a in (q, k, v, g, beta, state)]
+    N.check(N.lib().dtree_gdn_tree_recurrence(*[a.data_ptr() for a in keep], par.data_ptr(), T, Hk, Hv, Dk, Dv,
+                                              y.data_ptr(), st.data_ptr() if st is not None else None, stream()),
+            "gdn recurrence")
+    torch.cuda.synchronize()
+    return y.cpu().numpy(), (st.cpu().numpy() if st is not None else None)
+
+
+def test_reference_seeded_conv():
+    x = np.random.default_rng(0).normal(size=(1, 5, 8)).astype(np.float32)[0]
+    base = np.random.default_rng(1).normal(size=(1, 3, 8)).astype(np.float32)[0]
+    w = np.random.default_rng(2).normal(size=(4, 8)).astype(np.float32)
+    out, win = _conv(x, base, w, [-1, 0, 0, 1, 2], "cuda")
+    ro, rw = gdn.tree_conv1d(x, base, w, [-1, 0, 0, 1, 2])
+    np.testing.assert_allclose(out, ro, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(win, rw, atol=1e-5, rtol=1e-5)
+
+
+def test_reference_seeded_recurrence():
+    rng = np.random.default_rng(3)
+    q = rng.normal(size=(1, 5, 1, 32)).astype(np.float32)[0]
+    k = rng.normal(size=(1, 5, 1, 32)).astype(np.float32)[0]
+    v = rng.normal(size=(1, 5, 1, 8)).astype(np.float32)[0]
+    g = rng.normal(size=(1, 5, 1)).astype(np.float32)[0]
+    beta = rng.normal(size=(1, 5, 1)).astype(np.float32)[0]
+    state = rng.normal(size=(1, 1, 8, 32)).astype(np.float32)[0]
+    y, st = _delta(q, k, v, g, beta, state, [-1, 0, 0, 1, 2], "cuda")
+    ry, rs = gdn.tree_gated_delta(q, k, v, g, beta, state, [-1, 0, 0, 1, 2])
+    np.testing.assert_allclose(y, ry, atol=1e-5, rtol=1e-5)
+    np.testing.assert_allclose(st, rs, atol=1e-5, rtol=1e-5)
+
+
+def _layer_inputs(T, seed, Hk=16, Hv=32, D=128):
+    """Recurrence inputs at the Qwen3.5 GDN scales: q = rms(q) / D, k = rms(k) /
+    sqrt(D) (qwen35_tree.py:304-306), decay in (0, 1), beta = sigmoid."""
+    g_ = np.random.default_rng(seed)
+
+    def rms(a):
+        return a / np.sqrt((a * a).mean(-1, keepdims=True) + 1e-6)
+
+    q = rms(g_.normal(size=(T, Hk, D))) / D
+    k = rms(g_.normal(size=(T, Hk, D))) / np.sqrt(D)
+    v = g_.normal(size=(T, Hv, D))
+    g = np.exp(-np.exp(g_.normal(size=(T, Hv)) * 0.5) * 0.3)
+    beta = 1 / (1 + np.exp(-g_.normal(size=(T, Hv))))
+    state = g_.normal(size=(Hv, D, D)) * 0.1
+    return q, k, v, g, beta, state
+
+
+@pytest.mark.parametrize("T,seed", [(25, 0), (65, 1)])
+def test_layer_shapes_conv_and_recurrence(T, seed):
+    parents = random_tree(T, seed)
+    g_ = np.random.default_rng(100 + seed)
+    x = g_.normal(size=(T, 8192))
+    base = g_.normal(size=(3, 8192))
+    w = g_.normal(size=(4, 8192)) * 0.5
+    out, win = _conv(x, base, w, parents, "cuda")
+    ro, rw = gdn.tree_conv1d(x, base, w, parents)
+    np.testing.assert_allclose(out, ro, atol=2e-5, rtol=2e-5)
+    np.testing.assert_array_equal(win, rw.astype(np.float32))
+    q, k, v, g, beta, state = _layer_inputs(T, seed)
+    y, st = _delta(q, k, v, g, beta, state, parents, "cuda")
+    ry, rs = gdn.tree_gated_delta(q, k, v, g, beta, state, parents)
+    assert np.abs(y - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
+    assert np.abs(st - rs).max() <= 1e-5 * max(1.0, np.abs(rs).max())
+    # lazy mode (no node states / windows written) gives the same outputs
+    y2, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
+    out2, _ = _conv(x, base, w, parents, "cuda", want_windows=False)
+    assert np.array_equal(y, y2) and np.array_equal(out, out2)
+
+
+def test_commit_replays_accepted_path():
+    T = 25
+    parents = random_tree(T, 7)
+    # accepted = root path of the deepest node
+    depth = [0] * T
+    for t in range(1, T):
+        depth[t] = depth[parents[t]] + 1
+    path = gdn.root_path(parents, int(np.argmax(depth)))
+    g_ = np.random.default_rng(8)
+    x = g_.normal(size=(T, 8192))
+    base = g_.normal(size=(3, 8192))
+    q, k, v, g, beta, state = _layer_inputs(T, 9)
+    dev = "cuda"
+    win_d, st_d = _t(base, dev), _t(state, dev)
+    pbuf = torch.zeros(129, dtype=torch.int32, device=dev)
+    pbuf[: len(path)] = torch.tensor(path, dtype=torch.int32)
+    plen = torch.tensor([len(path)], dtype=torch.int32, device=dev)
+    keep = [_t(a, dev) for a in (x, q, k, v, g, beta)]
+    N.check(N.lib().dtree_gdn_commit(keep[0].data_ptr(), win_d.data_ptr(), 8192, 3, *[a.data_ptr() for a in keep[1:]],
+                                     st_d.data_ptr(), pbuf.data_ptr(), plen.data_ptr(), 16, 32, 128, 128, stream()),
+            "gdn commit")
+    torch.cuda.synchronize()
+    rw, rs = gdn.commit(x, base, q, k, v, g, beta, state, parents, path)
+    np.testing.assert_array_equal(win_d.cpu().numpy(), rw.astype(np.float32))
+    assert np.abs(st_d.cpu().numpy() - rs).max() <= 1e-5 * max(1.0, np.abs(rs).max())
+    # a one-node path (only the root accepted) shifts the window by one row
+    win1 = _t(base, dev)
+    plen.fill_(1)
+    N.check(N.lib().dtree_gdn_commit(keep[0].data_ptr(), win1.data_ptr(), 8192, 3, None, None, None, None, None, None,
+                                     pbuf.data_ptr(), plen.data_ptr(), 16, 32, 128, 128, stream()), "gdn commit")
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(win1.cpu().numpy(), np.concatenate([base[1:], x[path[:1]]]).astype(np.float32))
