@@ -22,6 +22,16 @@ DrHB/dtree-mlx checkout):
   and special cases (chain tree == causal attention, star tree == prefix +
   self, L=1 == decode attention, RoPE vs complex rotation, fp64 re-evaluation,
   and a cross-check of the decoder layer against transformers' Qwen3).
+- ``q4``     : MLX group-64 affine 4-bit format (``adapters.py:28-85``,
+  ``api.py:46-54``). Pinned by known-answer nibble vectors and the grouped
+  identity y = s (q . x) + b sum(x) per group.
+- ``gdn``    : GatedDeltaNet tree conv1d / tree recurrence / commit
+  (``qwen35_tree_kernels.py:8-152``, ``qwen35_tree.py:708-732``). Pinned by the
+  reference kernel tests' seeded vectors, the path-window closed form, the
+  chain decomposition and transformers' ``torch_recurrent_gated_delta_rule``.
+- ``qwen35`` : Qwen3.5 hybrid tree forward + commit (``qwen35_tree.py:180-732``).
+  Pinned end to end against transformers' Qwen3.5 text model: chain trees,
+  per-node root-path forwards, and commit + next step.
 
 Parity unpinned (MLX internals that only an MLX import could pin): the exact
 rounding / accumulation order of ``mx.fast.scaled_dot_product_attention``,
