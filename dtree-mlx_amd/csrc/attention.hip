@@ -1,9 +1,14 @@
 // Ancestor-masked GQA tree attention over a paged bf16 KV prefix.
 //
 // Work split: the keys of one query head are cut into chunks. Chunk 0 is the
-// tree itself (the L new keys, ancestor-or-self mask); chunks 1.. are the
-// 64-key pages of the prefix (fully visible). A workgroup has four waves, one
+// tree itself (the L new keys, ancestor-or-self mask); chunks 1.. are runs of
+// CK prefix keys (fully visible): a 64-key page for head_dim 128, half a page
+// for head_dim 256 (same registers per wave). A workgroup has four waves, one
 // chunk each, so workgroup `split` of a head owns chunks 4*split .. 4*split+3.
+//
+// Two head geometries are compiled: Qwen3 (head_dim 128, full RoPE) and the
+// gated attention of Qwen3.5 (head_dim 256, RoPE on the first 64 dims, q_proj
+// rows per head = [q | gate], output multiplied by sigmoid(gate)).
 // A wave owns exactly one chunk, so its softmax needs no running rescale: it
 // issues Q's loads, then all K and V of its page (32 KB in flight per wave),
 // scores both 32-key blocks, takes one max and accumulates P V.
@@ -29,15 +34,17 @@
 
 namespace dtree {
 
-constexpr int kChunkKeys = DTREE_PAGE;  // prefix keys per chunk: one page
-constexpr int kWaves = 4;        // waves (chunks) per workgroup
-constexpr int kBlocks = kChunkKeys / 32;
-constexpr int kMaxChunks = 257;  // tree + 256 prefix pages (prefix <= 16384)
+constexpr int kWaves = 4;          // waves (chunks) per workgroup
+constexpr int kMaxPast = 16384;    // longest prefix the grid is sized for
+constexpr int kMergeDims = 128;    // head dims merged per LDS pass
+// Prefix keys per chunk.
+__host__ __device__ constexpr int chunk_keys(int D) { return D <= 128 ? DTREE_PAGE : DTREE_PAGE / 2; }
 constexpr float kNeg = -1e30f;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
   const float* qkv; int ld_qkv;
+  int q_stride, k_off, v_off;  // qkv row: q of head h at h*q_stride (gate at +D), k / v of group g at k_off / v_off + g*D
   const uint16_t* q_norm; const uint16_t* k_norm; float eps;
   const float* rope_cos; const float* rope_sin;
   uint16_t* kp; uint16_t* vp; const int* page_table;
@@ -53,17 +60,17 @@ __device__ __forceinline__ int swap_bits23(int c) { return (c & ~12) | ((c & 4) 
 
 // Raw operands of one head row for lane (c, h), which owns dims 16j + 8h + i:
 // the fp32 values, the bf16 RMSNorm weights and the RoPE cos/sin of the first
-// half. Issuing all loads before any use lets a wave keep them in flight
-// together with the K/V loads that follow.
-template <int D>
+// half of the R rotated dims. Issuing all loads before any use lets a wave
+// keep them in flight together with the K/V loads that follow.
+template <int D, int R>
 struct HeadRow {
   f32x4_t x[D / 16][2];
   u32x4_t nw[D / 16];
-  f32x4_t cs[D / 32][2], sn[D / 32][2];
+  f32x4_t cs[R / 32][2], sn[R / 32][2];
 };
 
-template <int D>
-__device__ __forceinline__ void row_issue(HeadRow<D>& r, const float* src, const uint16_t* norm_w, const float* cosr,
+template <int D, int R>
+__device__ __forceinline__ void row_issue(HeadRow<D, R>& r, const float* src, const uint16_t* norm_w, const float* cosr,
                                           const float* sinr, int h) {
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) {
@@ -73,7 +80,7 @@ __device__ __forceinline__ void row_issue(HeadRow<D>& r, const float* src, const
   }
   if (cosr) {
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j)
+    for (int j = 0; j < R / 32; ++j)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         r.cs[j][u] = *reinterpret_cast<const f32x4_t*>(cosr + 16 * j + 8 * h + 4 * u);
@@ -83,9 +90,10 @@ __device__ __forceinline__ void row_issue(HeadRow<D>& r, const float* src, const
 }
 
 // RMSNorm over D (sum of squares completed with the partner lane^32), then
-// RoPE on (dim d, dim d + D/2) pairs, which live in the same lane.
-template <int D>
-__device__ __forceinline__ void row_finish(const HeadRow<D>& r, bool norm, bool rope, float eps,
+// RoPE on (dim d, dim d + R/2) pairs for d < R/2, which live in the same lane
+// (registers j and j + R/32); dims >= R pass through.
+template <int D, int R>
+__device__ __forceinline__ void row_finish(const HeadRow<D, R>& r, bool norm, bool rope, float eps,
                                            float (&v)[D / 16][8]) {
   constexpr int NJ = D / 16;
 #pragma unroll
@@ -112,14 +120,15 @@ __device__ __forceinline__ void row_finish(const HeadRow<D>& r, bool norm, bool 
       }
   }
   if (rope) {
+    constexpr int RJ = R / 32;
 #pragma unroll
-    for (int j = 0; j < NJ / 2; ++j)
+    for (int j = 0; j < RJ; ++j)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float cs = r.cs[j][i >> 2][i & 3], sn = r.sn[j][i >> 2][i & 3];
-        const float x1 = v[j][i], x2 = v[j + NJ / 2][i];
+        const float x1 = v[j][i], x2 = v[j + RJ][i];
         v[j][i] = x1 * cs - x2 * sn;
-        v[j + NJ / 2][i] = x1 * sn + x2 * cs;
+        v[j + RJ][i] = x1 * sn + x2 * cs;
       }
   }
 }
@@ -194,11 +203,11 @@ __device__ __forceinline__ u32x4_t mask_keys(u32x4_t v, int first, int end) {
   return v;
 }
 
-template <int D>
-__device__ __forceinline__ void q_fragments(const HeadRow<D>& qr, bool norm, float eps, u32x4_t (&qf)[D / 16],
+template <int D, int R>
+__device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, bool norm, float eps, u32x4_t (&qf)[D / 16],
                                             u32x4_t (&ql)[D / 16]) {
   float q[D / 16][8];
-  row_finish<D>(qr, norm, true, eps, q);
+  row_finish<D, R>(qr, norm, true, eps, q);
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) split8(q[j], qf[j], ql[j]);
 }
@@ -207,27 +216,38 @@ __device__ __forceinline__ void q_fragments(const HeadRow<D>& qr, bool norm, flo
 // row; k and v^T are staged in LDS (this wave's private region) for the MFMA
 // operand layouts, one 32-key block is scored with the ancestor-or-self mask,
 // and finally k/v are written to the cache rows P + c (one head per group).
-template <int D>
+// q, k and v are finished one after the other, so at most one raw head row is
+// live in registers (head_dim 256 rows are 128 floats per lane pair).
+template <int D, int R>
 __device__ __forceinline__ void tree_chunk(const AttnParams& p, int hq, int g, int G, int P, int L, int c, int h,
                                            uint16_t* ks, uint16_t* vt, float& m_run, float& l_run,
                                            f32x16_t (&o)[D / 32]) {
   constexpr int NJ = D / 16, ND = D / 32;
   constexpr int KS = D + 8, VS = 32 + 8;
-  const int half_d = D / 2;
+  constexpr int half_r = R / 2;
   const float* row = p.qkv + (size_t)c * p.ld_qkv;
-  HeadRow<D> qr, kr, vr;
-  row_issue<D>(qr, row + hq * D, p.q_norm, p.rope_cos + c * half_d, p.rope_sin + c * half_d, h);
-  row_issue<D>(kr, row + (p.Hq + g) * D, p.k_norm, p.rope_cos + c * half_d, p.rope_sin + c * half_d, h);
-  row_issue<D>(vr, row + (p.Hq + p.Hkv + g) * D, nullptr, nullptr, nullptr, h);
+  const float* cosr = p.rope_cos + c * half_r;
+  const float* sinr = p.rope_sin + c * half_r;
   const uint32_t anc = p.desc->ancestors[c][0];
   u32x4_t qf[NJ], ql[NJ];
-  q_fragments<D>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  {
+    HeadRow<D, R> qr;
+    row_issue<D, R>(qr, row + hq * p.q_stride, p.q_norm, cosr, sinr, h);
+    q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  }
   u32x4_t kf8[NJ], vf8[NJ];
   {
-    float kv[NJ][8], vv[NJ][8];
-    row_finish<D>(kr, p.k_norm != nullptr, true, p.eps, kv);
-    row_finish<D>(vr, false, false, 0.f, vv);
+    HeadRow<D, R> kr;
+    row_issue<D, R>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
+    float kv[NJ][8];
+    row_finish<D, R>(kr, p.k_norm != nullptr, true, p.eps, kv);
     pack_frag<D>(kv, kf8);
+  }
+  {
+    HeadRow<D, R> vr;
+    row_issue<D, R>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
+    float vv[NJ][8];
+    row_finish<D, R>(vr, false, false, 0.f, vv);
     pack_frag<D>(vv, vf8);
   }
   if (c >= L) {
@@ -288,27 +308,29 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, int hq, int g, i
   }
 }
 
-// One prefix chunk = one 64-key page. Q's loads go out first, then all K and V
-// of the page, so Q's norm/RoPE overlaps the K/V flight. Keys past the prefix
-// in the last page are masked (scores) and zeroed (V), since the page may hold
-// stale or non-finite data there.
-template <int D>
+// One prefix chunk = CK consecutive keys inside one page (the whole page for
+// head_dim 128, half of it for 256). Q's loads go out first, then all K and V
+// of the chunk, so Q's norm/RoPE overlaps the K/V flight. Keys past the prefix
+// in the last chunk are masked (scores) and zeroed (V), since the page may
+// hold stale or non-finite data there.
+template <int D, int R>
 __device__ __forceinline__ void prefix_chunk(const AttnParams& p, int hq, int g, int P, int chunk, int c, int h,
                                              float& m_run, float& l_run, f32x16_t (&o)[D / 32]) {
   constexpr int NJ = D / 16, ND = D / 32;
-  const int half_d = D / 2;
-  HeadRow<D> qr;
-  row_issue<D>(qr, p.qkv + (size_t)c * p.ld_qkv + hq * D, p.q_norm, p.rope_cos + c * half_d,
-               p.rope_sin + c * half_d, h);
-  const int k_begin = (chunk - 1) * kChunkKeys;
-  const int k_end = min(k_begin + kChunkKeys, P);
-  const int page = p.page_table[k_begin / DTREE_PAGE];
-  const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + swap_bits23(c)) * D;
-  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE;
-  u32x4_t kf[kBlocks][NJ];
-  u32x4_t vf[kBlocks][2][ND];
+  constexpr int CK = chunk_keys(D), NB = CK / 32;
+  constexpr int half_r = R / 2;
+  HeadRow<D, R> qr;
+  row_issue<D, R>(qr, p.qkv + (size_t)c * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + c * half_r,
+                  p.rope_sin + c * half_r, h);
+  const int k_begin = (chunk - 1) * CK;
+  const int k_end = min(k_begin + CK, P);
+  const int page = p.page_table[k_begin / DTREE_PAGE], po = k_begin % DTREE_PAGE;
+  const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po + swap_bits23(c)) * D;
+  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po;
+  u32x4_t kf[NB][NJ];
+  u32x4_t vf[NB][2][ND];
 #pragma unroll
-  for (int b = 0; b < kBlocks; ++b) {
+  for (int b = 0; b < NB; ++b) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) kf[b][j] = ld_u32x4_stream(kbase + (size_t)32 * b * D + 16 * j + 8 * h);
 #pragma unroll
@@ -318,31 +340,31 @@ __device__ __forceinline__ void prefix_chunk(const AttnParams& p, int hq, int g,
         vf[b][s2][db] = ld_u32x4_stream(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 32 * b + 16 * s2 + 8 * h);
   }
   u32x4_t qf[NJ], ql[NJ];
-  q_fragments<D>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
 
-  f32x16_t s[kBlocks];
+  f32x16_t s[NB];
 #pragma unroll
-  for (int b = 0; b < kBlocks; ++b)
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int b = 0; b < kBlocks; ++b) {
+    for (int b = 0; b < NB; ++b) {
       s[b] = mfma32(kf[b][j], qf[j], s[b]);
       s[b] = mfma32(kf[b][j], ql[j], s[b]);
     }
-  const bool ragged = k_end - k_begin < kChunkKeys;
+  const bool ragged = k_end - k_begin < CK;
 #pragma unroll
-  for (int b = 0; b < kBlocks; ++b)
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = k_begin + 32 * b + 16 * (r >> 3) + 8 * h + (r & 7);
       s[b][r] = (!ragged || key < k_end) ? s[b][r] * p.scale_log2 : kNeg;
     }
-  softmax_fresh<kBlocks>(s, m_run, l_run);
+  softmax_fresh<NB>(s, m_run, l_run);
 #pragma unroll
-  for (int b = 0; b < kBlocks; ++b)
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       u32x4_t va[ND];
@@ -353,15 +375,17 @@ __device__ __forceinline__ void prefix_chunk(const AttnParams& p, int hq, int g,
     }
 }
 
-template <int D>
+template <int D, int R, bool GATE>
 __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   constexpr int ND = D / 32;  // 32-dim blocks of O^T
   constexpr int KS = D + 8;   // padded LDS row of tree K
   constexpr int VS = 32 + 8;  // padded LDS row of tree V^T
   constexpr int MS = 33;      // row stride of a wave's O^T in the LDS merge
-  constexpr int kWaveMerge = D * MS + 64;  // floats per wave: O^T, m, l
+  constexpr int NP = D / kMergeDims;               // merge passes
+  constexpr int kWaveMerge = kMergeDims * MS + 64;  // floats per wave: O^T slice, m, l
   constexpr int kStage = (32 * KS + D * VS) * 2;
   constexpr int kMerge = kWaves * kWaveMerge * 4;
+  constexpr int CK = chunk_keys(D);
   __shared__ __align__(16) unsigned char lds[kStage > kMerge ? kStage : kMerge];
   __shared__ int s_last;
 
@@ -375,7 +399,7 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   const int hq = g * G + (bid >> 3) % G;
 
   const int P = p.desc->past_length, L = p.desc->num_nodes;
-  const int nchunks = 1 + (P + kChunkKeys - 1) / kChunkKeys;
+  const int nchunks = 1 + (P + CK - 1) / CK;
   // A descriptor beyond the grid's capacity (P > max_past_length) or with more
   // than 32 rows leaves the output untouched instead of indexing past buffers.
   if (nchunks > p.max_chunks || L > 32 || L < 1) return;
@@ -395,45 +419,50 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
 
   if (chunk == 0) {
     uint16_t* ks = reinterpret_cast<uint16_t*>(lds);
-    tree_chunk<D>(p, hq, g, G, P, L, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+    tree_chunk<D, R>(p, hq, g, G, P, L, c, h, ks, ks + 32 * KS, m_run, l_run, o);
   } else if (chunk < nchunks) {
-    prefix_chunk<D>(p, hq, g, P, chunk, c, h, m_run, l_run, o);
+    prefix_chunk<D, R>(p, hq, g, P, chunk, c, h, m_run, l_run, o);
   }
 
-  // LDS merge of the four waves. The first barrier retires the tree chunk's
-  // staging, which shares this memory.
+  // LDS merge of the four waves, 128 head dims per pass. The first barrier
+  // retires the tree chunk's staging, which shares this memory.
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  __syncthreads();
-  float* mw = reinterpret_cast<float*>(lds) + wave * kWaveMerge;
-#pragma unroll
-  for (int db = 0; db < ND; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mw[(32 * db + acc_row(r, h)) * MS + c] = o[db][r];
-  if (h == 0) {
-    mw[D * MS + c] = m_run;
-    mw[D * MS + 32 + c] = l_tot;
-  }
-  __syncthreads();
-
-  // Thread t combines query q = t/8, dims d0 .. d0+15 with d0 = 16 (t%8).
-  constexpr int kDims = 32 * D / (64 * kWaves);  // 16 for D = 128
+  // Thread t combines query q = t/8, dims pass*128 + d0 .. +15, d0 = 16 (t%8).
+  constexpr int kDims = 32 * D / (64 * kWaves);  // dims per thread: 16 per pass
   const int t = threadIdx.x;
-  const int q = t >> 3, d0 = (t & 7) * kDims;
+  const int q = t >> 3, d0 = (t & 7) * 16;
+  float* mw = reinterpret_cast<float*>(lds) + wave * kWaveMerge;
   const float* m0 = reinterpret_cast<const float*>(lds);
-  float M = kNeg;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m0[w * kWaveMerge + D * MS + q]);
   float acc[kDims];
+  float M = kNeg, tot = 0.f, wk[kWaves];
 #pragma unroll
-  for (int i = 0; i < kDims; ++i) acc[i] = 0.f;
-  float tot = 0.f;
+  for (int pass = 0; pass < NP; ++pass) {
+    __syncthreads();
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float* mv = m0 + w * kWaveMerge;
-    const float wk = fast_exp2(mv[D * MS + q] - M);
-    tot += wk * mv[D * MS + 32 + q];
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int i = 0; i < kDims; ++i) acc[i] += wk * mv[(d0 + i) * MS + q];
+      for (int r = 0; r < 16; ++r) mw[(32 * db + acc_row(r, h)) * MS + c] = o[4 * pass + db][r];
+    if (pass == 0 && h == 0) {
+      mw[kMergeDims * MS + c] = m_run;
+      mw[kMergeDims * MS + 32 + c] = l_tot;
+    }
+    __syncthreads();
+    if (pass == 0) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m0[w * kWaveMerge + kMergeDims * MS + q]);
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        wk[w] = fast_exp2(m0[w * kWaveMerge + kMergeDims * MS + q] - M);
+        tot += wk[w] * m0[w * kWaveMerge + kMergeDims * MS + 32 + q];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) a += wk[w] * m0[w * kWaveMerge + (d0 + i) * MS + q];
+      acc[16 * pass + i] = a;
+    }
   }
 
   if (nsplit > 1) {
@@ -465,22 +494,34 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
       float v[kDims];
 #pragma unroll
       for (int i = 0; i < kDims; ++i) v[i] = ld_coherent(ps + (size_t)i * 64 * kWaves + t);
-      const float wk = fast_exp2(ld_coherent(ps + 32 * D + q) - Ms);
-      tot += wk * ld_coherent(ps + 32 * D + 32 + q);
+      const float w = fast_exp2(ld_coherent(ps + 32 * D + q) - Ms);
+      tot += w * ld_coherent(ps + 32 * D + 32 + q);
 #pragma unroll
-      for (int i = 0; i < kDims; ++i) acc[i] += wk * v[i];
+      for (int i = 0; i < kDims; ++i) acc[i] += w * v[i];
     }
   }
 
   const float inv = (q < L && tot > 0.f) ? 1.0f / tot : 0.f;
 #pragma unroll
   for (int i0 = 0; i0 < kDims; i0 += 8) {
+    const int dd = (i0 / 16) * kMergeDims + d0 + (i0 % 16);  // head dim of acc[i0]
     float y[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = q < L ? acc[i0 + i] * inv : 0.f;
+    if (GATE && q < L) {
+      // o_proj input = attention * sigmoid(gate), gate = q_proj row dims D.. of the head
+      const float* gp = p.qkv + (size_t)q * p.ld_qkv + hq * p.q_stride + D + dd;
+      const f32x4_t g0 = *reinterpret_cast<const f32x4_t*>(gp);
+      const f32x4_t g1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        y[i] *= 1.0f / (1.0f + __expf(-g0[i]));
+        y[i + 4] *= 1.0f / (1.0f + __expf(-g1[i]));
+      }
+    }
     u32x4_t hi, lo;
     split8(y, hi, lo);
-    const int col = hq * D + d0 + i0;
+    const int col = hq * D + dd;
     const size_t oi = p.out_tiled ? tiled_index(q, col, p.ld_out) : (size_t)q * p.ld_out + col;
     *reinterpret_cast<u32x4_t*>(p.out + oi) = hi;
     if (p.out_lo) *reinterpret_cast<u32x4_t*>(p.out_lo + oi) = lo;
@@ -491,14 +532,17 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
 
 using namespace dtree;
 
-static int attn_max_chunks(int max_past) { return 1 + (max_past + kChunkKeys - 1) / kChunkKeys; }
-static int attn_splits(int max_past) { return (attn_max_chunks(max_past) + kWaves - 1) / kWaves; }
+static int attn_max_chunks(int head_dim, int max_past) {
+  const int ck = chunk_keys(head_dim);
+  return 1 + (max_past + ck - 1) / ck;
+}
+static int attn_splits(int head_dim, int max_past) { return (attn_max_chunks(head_dim, max_past) + kWaves - 1) / kWaves; }
 
 extern "C" size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length) {
   if (num_heads <= 0 || head_dim <= 0 || max_past_length < 0) return 0;
   const size_t stride = (size_t)32 * head_dim + 64;
   return (((size_t)num_heads * sizeof(int) + 255) & ~(size_t)255) +
-         (size_t)num_heads * attn_splits(max_past_length) * stride * sizeof(float);
+         (size_t)num_heads * attn_splits(head_dim, max_past_length) * stride * sizeof(float);
 }
 
 extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
@@ -506,31 +550,36 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   DTREE_REQUIRE(a->qkv && a->rope_cos && a->rope_sin && a->k_pages && a->v_pages && a->page_table && a->desc &&
                     a->out && a->workspace,
                 "attention: null pointer");
-  DTREE_REQUIRE(a->head_dim == 128, "attention: head_dim 128 is the compiled size");
+  const int D = a->head_dim;
+  const int R = a->rope_dims == 0 ? D : a->rope_dims;
+  const bool gated = a->gated != 0;
+  DTREE_REQUIRE((D == 128 && R == 128 && !gated) || (D == 256 && R == 64 && gated),
+                "attention: compiled geometries are head_dim 128 (full RoPE) and gated head_dim 256 (rope_dims 64)");
   DTREE_REQUIRE(a->rows_padded == 32, "attention: trees of up to 32 nodes (rows_padded 32)");
   DTREE_REQUIRE(a->num_kv_heads > 0 && a->num_heads % a->num_kv_heads == 0, "attention: num_heads % num_kv_heads");
-  DTREE_REQUIRE(a->max_past_length >= 0, "attention: max_past_length");
-  DTREE_REQUIRE(a->ld_qkv >= (a->num_heads + 2 * a->num_kv_heads) * a->head_dim && a->ld_qkv % 4 == 0,
+  DTREE_REQUIRE(a->max_past_length >= 0 && a->max_past_length <= kMaxPast, "attention: max_past_length beyond 16384");
+  const int q_stride = gated ? 2 * D : D;
+  DTREE_REQUIRE(a->ld_qkv >= a->num_heads * q_stride + 2 * a->num_kv_heads * D && a->ld_qkv % 4 == 0,
                 "attention: ld_qkv too small");
-  DTREE_REQUIRE(a->ld_out >= a->num_heads * a->head_dim && a->ld_out % 8 == 0,
+  DTREE_REQUIRE(a->ld_out >= a->num_heads * D && a->ld_out % 8 == 0,
                 "attention: ld_out below num_heads * head_dim or not a multiple of 8");
-  DTREE_REQUIRE(((uintptr_t)a->out & 15) == 0 && ((uintptr_t)a->out_lo & 15) == 0,
-                "attention: out and out_lo must be 16-byte aligned");
-  const int max_chunks = attn_max_chunks(a->max_past_length);
-  DTREE_REQUIRE(max_chunks <= kMaxChunks, "attention: max_past_length beyond 16384");
-  DTREE_REQUIRE(a->workspace_bytes >= dtree_attention_workspace_bytes(a->num_heads, a->head_dim, a->max_past_length),
+  DTREE_REQUIRE(((uintptr_t)a->out & 15) == 0 && ((uintptr_t)a->out_lo & 15) == 0 && ((uintptr_t)a->qkv & 15) == 0,
+                "attention: qkv, out and out_lo must be 16-byte aligned");
+  DTREE_REQUIRE(a->workspace_bytes >= dtree_attention_workspace_bytes(a->num_heads, D, a->max_past_length),
                 "attention: workspace too small");
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
-                    (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * a->head_dim && a->ld_out % 64 == 0),
+                    (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * D && a->ld_out % 64 == 0),
                 "attention: tiled out needs ld_out == num_heads * head_dim");
   AttnParams p{};
-  p.qkv = a->qkv; p.ld_qkv = a->ld_qkv; p.q_norm = a->q_norm; p.k_norm = a->k_norm; p.eps = a->eps;
+  p.qkv = a->qkv; p.ld_qkv = a->ld_qkv;
+  p.q_stride = q_stride; p.k_off = a->num_heads * q_stride; p.v_off = p.k_off + a->num_kv_heads * D;
+  p.q_norm = a->q_norm; p.k_norm = a->k_norm; p.eps = a->eps;
   p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
   p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
   p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
   p.out_tiled = a->out_layout == DTREE_W_TILED;
-  p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.max_chunks = max_chunks;
-  p.splits = attn_splits(a->max_past_length);
+  p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.max_chunks = attn_max_chunks(D, a->max_past_length);
+  p.splits = attn_splits(D, a->max_past_length);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.counters = reinterpret_cast<int*>(a->workspace);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) +
@@ -538,7 +587,10 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   const int G = p.Hq / p.Hkv;
   const int pairs = p.splits * p.Hkv;
   const int grid = ((pairs + 7) / 8) * 8 * G;
-  tree_attn_kernel<128><<<grid, 64 * kWaves, 0, stream>>>(p);
+  if (D == 128)
+    tree_attn_kernel<128, 128, false><<<grid, 64 * kWaves, 0, stream>>>(p);
+  else
+    tree_attn_kernel<256, 64, true><<<grid, 64 * kWaves, 0, stream>>>(p);
   DTREE_LAUNCH_CHECK("attention launch");
   return DTREE_OK;
 }

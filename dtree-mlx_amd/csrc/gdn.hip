@@ -70,6 +70,7 @@ struct GdnParams {
   float* state;        // [Hv][Dv][Dk] base state (commit: updated in place)
   const int* parents;  // tree kernel
   const int* path; const int* path_len;  // commit kernel (device)
+  const int* T_dev;    // optional device node count (<= T, which sizes LDS)
   int T, Hk, Hv, Dv, rpw;
   float* y;            // [T][Hv][Dv]
   float* states;       // optional [T][Hv][Dv][Dk]
@@ -102,7 +103,8 @@ __global__ __launch_bounds__(256) void gdn_tree_kernel(GdnParams p) {
   constexpr int LPR = DK / 4;
   extern __shared__ float lds[];
   __shared__ int par[kGdnMaxNodes];
-  const int T = p.T, rpw = p.rpw;
+  const int T = p.T_dev ? min(max(*p.T_dev, 0), p.T) : p.T;
+  const int rpw = p.rpw;
   const int nslices = p.Dv / rpw;
   const int h = blockIdx.x / nslices, row0 = (blockIdx.x % nslices) * rpw;
   const int hk = h / (p.Hv / p.Hk);
@@ -144,12 +146,16 @@ __global__ __launch_bounds__(256) void gdn_tree_kernel(GdnParams p) {
   }
 }
 
+// Path entries index the per-node buffers ([T] rows); an out-of-range entry
+// (a descriptor that no walk filled) is clamped so it can never read past them.
+__device__ __forceinline__ int clamp_node(int t, int T) { return min(max(t, 0), T - 1); }
+
 // Commit: replay the accepted path (path[0 .. *path_len), a root path) from the
 // base state, in place; the conv part moves the base window to the last keep
 // rows of (window ++ x along the path). Blocks [0, conv_blocks) do the conv
 // window, the rest the state rows.
 template <int DK>
-__global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const float* x, float* window, int C,
+__global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const float* x, int ldx, float* window, int C,
                                                          int keep, int conv_blocks) {
   constexpr int LPR = DK / 4;
   const int n = min(max(*p.path_len, 0), kGdnMaxNodes);
@@ -162,7 +168,7 @@ __global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const floa
     const int from_win = keep - from_path;
     for (int r = 0; r < keep; ++r) {
       const float val = r < from_win ? window[(size_t)(r + from_path) * C + c]
-                                     : x[(size_t)p.path[n - from_path + (r - from_win)] * C + c];
+                                     : x[(size_t)clamp_node(p.path[n - from_path + (r - from_win)], p.T) * ldx + c];
       window[(size_t)r * C + c] = val;
     }
     return;
@@ -177,13 +183,155 @@ __global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const floa
   float* sp = p.state + ((size_t)h * p.Dv + dv) * DK + 4 * lane4;
   f32x4_t s = *reinterpret_cast<const f32x4_t*>(sp);
   for (int i = 0; i < n; ++i) {
-    const int t = p.path[i];
+    const int t = clamp_node(p.path[i], p.T);
     const f32x4_t kk = *reinterpret_cast<const f32x4_t*>(p.k + ((size_t)t * p.Hk + hk) * DK + 4 * lane4);
     const f32x4_t qq = *reinterpret_cast<const f32x4_t*>(p.q + ((size_t)t * p.Hk + hk) * DK + 4 * lane4);
     gdn_step<LPR>(s, kk, qq, p.v[((size_t)t * p.Hv + h) * p.Dv + dv], p.g[(size_t)t * p.Hv + h],
                   p.beta[(size_t)t * p.Hv + h]);
   }
   *reinterpret_cast<f32x4_t*>(sp) = s;
+}
+
+// Layer prep (qwen35_tree.py:199-308 between the projections and the
+// recurrence): tree conv1d + SiLU of the projected conv input, split into
+// q | k | v, q = Dk^-1 rms_norm(q), k = Dk^-1/2 rms_norm(k) per key head
+// (eps 1e-6), and per (node, value head) g = exp(-exp(A_log) softplus(a +
+// dt_bias)), beta = sigmoid(b). Workgroup s < C / DK owns channels
+// s*DK .. s*DK + DK - 1 (one q or k head, or DK value channels), a thread per
+// channel; the conv outputs of all nodes are staged in LDS so that thread t
+// can reduce node t's head for the norm. The last workgroup computes g and
+// beta. Node count and parents come from the step descriptor.
+struct PrepParams {
+  const DtreeStepDesc* desc; int rows;  // rows = node capacity (sizes LDS)
+  const float* x; int ldx;  // conv input = proj columns [0, C)
+  const float* base; const float* w;
+  int C, key_dim, Hv, ab_col;  // b at proj column ab_col + h, a at ab_col + Hv + h
+  const float* A_log; const float* dt_bias;
+  float* q; float* k; float* v; float* g; float* beta;
+  float q_scale, k_scale;
+};
+
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+
+template <int KEEP, int DK>
+__global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
+  extern __shared__ float ob[];  // [L][DK + 1] conv outputs, then rs[L]
+  __shared__ int par[kGdnMaxNodes];
+  const int L = min(max(p.desc->num_nodes, 0), p.rows);
+  const int tid = threadIdx.x;
+  for (int t = tid; t < L; t += DK) par[t] = p.desc->parents[t];
+  __syncthreads();
+  const int nslices = p.C / DK;
+  if ((int)blockIdx.x == nslices) {
+    for (int e = tid; e < L * p.Hv; e += DK) {
+      const int t = e / p.Hv, h = e % p.Hv;
+      const float* row = p.x + (size_t)t * p.ldx + p.ab_col;
+      const float b = row[h], a = row[p.Hv + h];
+      p.g[(size_t)t * p.Hv + h] = __expf(-__expf(p.A_log[h]) * softplus_f(a + p.dt_bias[h]));
+      p.beta[(size_t)t * p.Hv + h] = 1.0f / (1.0f + __expf(-b));
+    }
+    return;
+  }
+  const int c0 = blockIdx.x * DK, c = c0 + tid;
+  float wk[KEEP + 1], bk[KEEP];
+#pragma unroll
+  for (int r = 0; r <= KEEP; ++r) wk[r] = p.w[(size_t)r * p.C + c];
+#pragma unroll
+  for (int r = 0; r < KEEP; ++r) bk[r] = p.base[(size_t)r * p.C + c];
+  for (int t = 0; t < L; ++t) {
+    // window of t = last KEEP + 1 rows of (base ++ x along the root path):
+    // val[i] is row KEEP - i (val[0] = x[t]).
+    float val[KEEP + 1];
+    int anc = t, nb = 0;
+#pragma unroll
+    for (int i = 0; i <= KEEP; ++i) {
+      if (anc >= 0) {
+        val[i] = p.x[(size_t)anc * p.ldx + c];
+        anc = par[anc];
+      } else {
+        val[i] = bk[KEEP - 1 - nb];
+        ++nb;
+      }
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i <= KEEP; ++i) acc += wk[KEEP - i] * val[i];
+    ob[t * (DK + 1) + tid] = silu_acc(acc);
+  }
+  const bool is_q = c0 < p.key_dim, is_k = !is_q && c0 < 2 * p.key_dim;
+  float* rs = ob + p.rows * (DK + 1);
+  __syncthreads();
+  if (is_q || is_k) {
+    // Node t's head; the padded row stride puts consecutive nodes on distinct banks.
+    for (int t = tid; t < L; t += DK) {
+      float ss = 0.f;
+      for (int j = 0; j < DK; ++j) {
+        const float o = ob[t * (DK + 1) + j];
+        ss += o * o;
+      }
+      rs[t] = rsqrtf(ss * (1.0f / DK) + 1e-6f) * (is_q ? p.q_scale : p.k_scale);
+    }
+    __syncthreads();
+  }
+  for (int t = 0; t < L; ++t) {
+    const float o = ob[t * (DK + 1) + tid];
+    if (is_q) p.q[(size_t)t * p.key_dim + c] = o * rs[t];
+    else if (is_k) p.k[(size_t)t * p.key_dim + (c - p.key_dim)] = o * rs[t];
+    else p.v[(size_t)t * (p.C - 2 * p.key_dim) + (c - 2 * p.key_dim)] = o;
+  }
+}
+
+// Gated RMSNorm of the recurrence output per (node, value head)
+// (RMSNormGated, qwen35_tree.py:322): o = rms_norm(y) * w * silu(z), written as
+// the split bf16 pair [hi, lo] the out_proj GEMM reads. 16 threads per
+// (node, head), 8 dims each; rows >= L are written as zero.
+template <int DV>
+__global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const DtreeStepDesc* desc, const float* __restrict__ y,
+                                                             const float* __restrict__ z, int ldz,
+                                                             const uint16_t* __restrict__ w, float eps, int Hv,
+                                                             int rows, uint16_t* out, uint16_t* out_lo, int tiled,
+                                                             int ld_out) {
+  constexpr int TPH = DV / 8;  // threads per (node, head)
+  const int L = desc->num_nodes;
+  const int gid = blockIdx.x * (256 / TPH) + threadIdx.x / TPH;
+  const int part = threadIdx.x % TPH;
+  if (gid >= rows * Hv) return;
+  const int t = gid / Hv, h = gid % Hv;
+  const int d0 = part * 8;
+  float o[8];
+  if (t < L) {
+    const float* yr = y + ((size_t)t * Hv + h) * DV + d0;
+    const f32x4_t y0 = *reinterpret_cast<const f32x4_t*>(yr), y1 = *reinterpret_cast<const f32x4_t*>(yr + 4);
+    const float* zr = z + (size_t)t * ldz + h * DV + d0;
+    const f32x4_t z0 = *reinterpret_cast<const f32x4_t*>(zr), z1 = *reinterpret_cast<const f32x4_t*>(zr + 4);
+    const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(w + d0);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += y0[i] * y0[i] + y1[i] * y1[i];
+#pragma unroll
+    for (int m = TPH / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+    const float r = rsqrtf(ss * (1.0f / DV) + eps);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float yi = i < 4 ? y0[i] : y1[i - 4];
+      const float zi = i < 4 ? z0[i] : z1[i - 4];
+      const uint32_t wb = wv[i >> 1];
+      const float wi = __uint_as_float((i & 1) ? (wb & 0xffff0000u) : (wb << 16));
+      o[i] = yi * r * wi * (zi / (1.0f + __expf(-zi)));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = 0.f;
+  }
+  float rr[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) rr[i] = o[i] - bf2f(f2bf(o[i]));
+  const u32x4_t hi{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]), pack_bf2(o[4], o[5]), pack_bf2(o[6], o[7])};
+  const u32x4_t lo{pack_bf2(rr[0], rr[1]), pack_bf2(rr[2], rr[3]), pack_bf2(rr[4], rr[5]), pack_bf2(rr[6], rr[7])};
+  const int col = h * DV + d0;
+  const size_t oi = tiled ? tiled_index(t, col, ld_out) : (size_t)t * ld_out + col;
+  *reinterpret_cast<u32x4_t*>(out + oi) = hi;
+  if (out_lo) *reinterpret_cast<u32x4_t*>(out_lo + oi) = lo;
 }
 
 // Rows per workgroup: the largest power of two <= 256 / (Dk / 4) and <= Dv
@@ -266,7 +414,7 @@ extern "C" int dtree_gdn_commit(const float* x, float* window, int32_t channels,
   while (rpw > 1 && head_v_dim % rpw) rpw >>= 1;
   GdnParams p{};
   p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.state = state; p.path = path; p.path_len = path_len;
-  p.Hk = num_k_heads; p.Hv = num_v_heads; p.Dv = head_v_dim; p.rpw = rpw;
+  p.T = kGdnMaxNodes; p.Hk = num_k_heads; p.Hv = num_v_heads; p.Dv = head_v_dim; p.rpw = rpw;
   const int conv_blocks = window ? (channels + 255) / 256 : 0;
   const int state_blocks = state ? num_v_heads * (head_v_dim / rpw) : 0;
   if (conv_blocks + state_blocks == 0) return DTREE_OK;
@@ -274,10 +422,111 @@ extern "C" int dtree_gdn_commit(const float* x, float* window, int32_t channels,
   // with 256 and let surplus state threads idle.
   const int threads = 256;
   switch (head_k_dim) {
-    case 32: gdn_commit_kernel<32><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, window, channels, keep, conv_blocks); break;
-    case 64: gdn_commit_kernel<64><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, window, channels, keep, conv_blocks); break;
-    default: gdn_commit_kernel<128><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, window, channels, keep, conv_blocks); break;
+    case 32: gdn_commit_kernel<32><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, channels, keep, conv_blocks); break;
+    case 64: gdn_commit_kernel<64><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, channels, keep, conv_blocks); break;
+    default: gdn_commit_kernel<128><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, channels, keep, conv_blocks); break;
   }
   DTREE_LAUNCH_CHECK("gdn_commit launch");
+  return DTREE_OK;
+}
+
+// ---- layer entry points (node count, parents and accepted path from the
+// device step descriptor, so one captured graph serves every step) ----------
+
+static int gdn_layer_check(const DtreeGdnArgs* a, const char* what) {
+  DTREE_REQUIRE(a && a->desc, std::string(what) + ": null args / desc");
+  DTREE_REQUIRE(a->rows_padded >= 1 && a->rows_padded <= kGdnMaxNodes, std::string(what) + ": rows_padded in [1, 128]");
+  DTREE_REQUIRE(a->num_k_heads > 0 && a->num_v_heads > 0 && a->num_v_heads % a->num_k_heads == 0,
+                std::string(what) + ": num_v_heads % num_k_heads");
+  DTREE_REQUIRE(a->head_k_dim == 128 && a->head_v_dim == 128, std::string(what) + ": head dims 128 are compiled");
+  DTREE_REQUIRE(a->conv_keep >= 1 && a->conv_keep <= kConvMaxKeep, std::string(what) + ": conv_keep in [1, 7]");
+  return DTREE_OK;
+}
+
+extern "C" size_t dtree_gdn_args_bytes(void) { return sizeof(DtreeGdnArgs); }
+
+extern "C" int dtree_gdn_layer_prep(const DtreeGdnArgs* a, hipStream_t stream) {
+  if (int rc = gdn_layer_check(a, "gdn_layer_prep")) return rc;
+  DTREE_REQUIRE(a->proj && a->window && a->conv_w && a->A_log && a->dt_bias && a->q && a->k && a->v && a->g && a->beta,
+                "gdn_layer_prep: null pointer");
+  const int key_dim = a->num_k_heads * a->head_k_dim, value_dim = a->num_v_heads * a->head_v_dim;
+  const int C = 2 * key_dim + value_dim;
+  DTREE_REQUIRE(a->ld_proj >= C + value_dim + 2 * a->num_v_heads, "gdn_layer_prep: ld_proj below C + z + b + a");
+  PrepParams p{};
+  p.desc = a->desc; p.rows = a->rows_padded;
+  p.x = a->proj; p.ldx = a->ld_proj; p.base = a->window; p.w = a->conv_w;
+  p.C = C; p.key_dim = key_dim; p.Hv = a->num_v_heads; p.ab_col = C + value_dim;
+  p.A_log = a->A_log; p.dt_bias = a->dt_bias;
+  p.q = a->q; p.k = a->k; p.v = a->v; p.g = a->g; p.beta = a->beta;
+  p.q_scale = 1.0f / (float)a->head_k_dim;
+  p.k_scale = 1.0f / sqrtf((float)a->head_k_dim);
+  const size_t lds = ((size_t)a->rows_padded * (128 + 1) + a->rows_padded) * sizeof(float);
+  const int grid = C / 128 + 1;
+  switch (a->conv_keep) {
+#define DTREE_PREP_CASE(K) \
+  case K: gdn_prep_kernel<K, 128><<<grid, 128, lds, stream>>>(p); break;
+    DTREE_PREP_CASE(1) DTREE_PREP_CASE(2) DTREE_PREP_CASE(3) DTREE_PREP_CASE(4) DTREE_PREP_CASE(5)
+    DTREE_PREP_CASE(6) DTREE_PREP_CASE(7)
+#undef DTREE_PREP_CASE
+  }
+  DTREE_LAUNCH_CHECK("gdn_layer_prep launch");
+  return DTREE_OK;
+}
+
+extern "C" int dtree_gdn_layer_recurrence(const DtreeGdnArgs* a, hipStream_t stream) {
+  if (int rc = gdn_layer_check(a, "gdn_layer_recurrence")) return rc;
+  DTREE_REQUIRE(a->q && a->k && a->v && a->g && a->beta && a->state && a->y, "gdn_layer_recurrence: null pointer");
+  size_t lds = 0;
+  const int rpw = gdn_rpw(a->rows_padded, a->head_k_dim, a->head_v_dim, &lds);
+  DTREE_REQUIRE(rpw > 0, "gdn_layer_recurrence: rows_padded too large for the LDS-resident node states");
+  GdnParams p{};
+  p.q = a->q; p.k = a->k; p.v = a->v; p.g = a->g; p.beta = a->beta; p.state = a->state;
+  p.parents = a->desc->parents; p.T_dev = &a->desc->num_nodes;
+  p.T = a->rows_padded; p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->head_v_dim; p.rpw = rpw;
+  p.y = a->y; p.states = nullptr;
+  const int grid = a->num_v_heads * (a->head_v_dim / rpw);
+  gdn_tree_kernel<128><<<grid, rpw * (128 / 4), lds, stream>>>(p);
+  DTREE_LAUNCH_CHECK("gdn_layer_recurrence launch");
+  return DTREE_OK;
+}
+
+extern "C" int dtree_gdn_layer_gated_norm(const DtreeGdnArgs* a, hipStream_t stream) {
+  if (int rc = gdn_layer_check(a, "gdn_layer_gated_norm")) return rc;
+  DTREE_REQUIRE(a->y && a->proj && a->norm_w && a->out, "gdn_layer_gated_norm: null pointer");
+  const int key_dim = a->num_k_heads * a->head_k_dim, value_dim = a->num_v_heads * a->head_v_dim;
+  const int C = 2 * key_dim + value_dim;
+  DTREE_REQUIRE(a->ld_proj >= C + value_dim && a->ld_proj % 4 == 0 && ((uintptr_t)a->proj & 15) == 0,
+                "gdn_layer_gated_norm: proj must be 16-byte aligned with ld_proj % 4 == 0");
+  DTREE_REQUIRE(((uintptr_t)a->out & 15) == 0 && ((uintptr_t)a->out_lo & 15) == 0 && ((uintptr_t)a->y & 15) == 0 &&
+                    ((uintptr_t)a->norm_w & 15) == 0,
+                "gdn_layer_gated_norm: y, norm_w, out and out_lo must be 16-byte aligned");
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ? (a->ld_out >= value_dim && a->ld_out % 8 == 0)
+                                                  : (a->out_layout == DTREE_W_TILED && a->ld_out == value_dim &&
+                                                     value_dim % 64 == 0 && a->rows_padded % 32 == 0),
+                "gdn_layer_gated_norm: out layout (tiled needs ld_out == value dim, rows_padded % 32 == 0)");
+  const int pairs = a->rows_padded * a->num_v_heads;
+  const int per_block = 256 / (128 / 8);
+  gdn_gated_norm_kernel<128><<<(pairs + per_block - 1) / per_block, 256, 0, stream>>>(
+      a->desc, a->y, a->proj + C, a->ld_proj, a->norm_w, a->eps, a->num_v_heads, a->rows_padded, a->out, a->out_lo,
+      a->out_layout == DTREE_W_TILED, a->ld_out);
+  DTREE_LAUNCH_CHECK("gdn_layer_gated_norm launch");
+  return DTREE_OK;
+}
+
+extern "C" int dtree_gdn_layer_commit(const DtreeGdnArgs* a, hipStream_t stream) {
+  if (int rc = gdn_layer_check(a, "gdn_layer_commit")) return rc;
+  DTREE_REQUIRE(a->proj && a->window && a->state && a->q && a->k && a->v && a->g && a->beta,
+                "gdn_layer_commit: null pointer");
+  const int C = 2 * a->num_k_heads * a->head_k_dim + a->num_v_heads * a->head_v_dim;
+  const int rpw = 256 / (128 / 4);
+  GdnParams p{};
+  p.q = a->q; p.k = a->k; p.v = a->v; p.g = a->g; p.beta = a->beta; p.state = a->state;
+  p.path = a->desc->accepted; p.path_len = &a->desc->n_accepted;
+  p.T = a->rows_padded; p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->head_v_dim; p.rpw = rpw;
+  const int conv_blocks = (C + 255) / 256;
+  const int state_blocks = a->num_v_heads * (a->head_v_dim / rpw);
+  gdn_commit_kernel<128><<<conv_blocks + state_blocks, 256, 0, stream>>>(p, a->proj, a->ld_proj, a->window, C,
+                                                                          a->conv_keep, conv_blocks);
+  DTREE_LAUNCH_CHECK("gdn_layer_commit launch");
   return DTREE_OK;
 }

@@ -14,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
 MAX_NODES = 128
 MASK_WORDS = 4
 PAGE = 64
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EPI_STORE_F32 = 0
 EPI_RESIDUAL = 1
@@ -75,6 +75,22 @@ class AttnArgs(C.Structure):
         ("max_past_length", C.c_int32),
         ("write_cache", C.c_int32),
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("rope_dims", C.c_int32), ("gated", C.c_int32),
+    ]
+
+
+class GdnArgs(C.Structure):
+    _fields_ = [
+        ("desc", C.c_void_p), ("rows_padded", C.c_int32),
+        ("num_k_heads", C.c_int32), ("num_v_heads", C.c_int32), ("head_k_dim", C.c_int32),
+        ("head_v_dim", C.c_int32), ("conv_keep", C.c_int32),
+        ("proj", C.c_void_p), ("ld_proj", C.c_int32),
+        ("window", C.c_void_p), ("conv_w", C.c_void_p), ("A_log", C.c_void_p), ("dt_bias", C.c_void_p),
+        ("state", C.c_void_p),
+        ("q", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p), ("g", C.c_void_p), ("beta", C.c_void_p),
+        ("y", C.c_void_p),
+        ("norm_w", C.c_void_p), ("eps", C.c_float),
+        ("out", C.c_void_p), ("out_lo", C.c_void_p), ("out_layout", C.c_int32), ("ld_out", C.c_int32),
     ]
 
 
@@ -107,6 +123,11 @@ SIGNATURES = {
                                             _vp]),
     "dtree_gdn_commit": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                    _vp]),
+    "dtree_gdn_args_bytes": (_sz, []),
+    "dtree_gdn_layer_prep": (C.c_int, [C.POINTER(GdnArgs), _vp]),
+    "dtree_gdn_layer_recurrence": (C.c_int, [C.POINTER(GdnArgs), _vp]),
+    "dtree_gdn_layer_gated_norm": (C.c_int, [C.POINTER(GdnArgs), _vp]),
+    "dtree_gdn_layer_commit": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_graph_begin": (C.c_int, [_vp]),
     "dtree_graph_end": (C.c_int, [_vp, C.POINTER(C.c_void_p)]),
     "dtree_graph_launch": (C.c_int, [_vp, _vp]),
@@ -133,7 +154,7 @@ def lib() -> C.CDLL:
     if h.dtree_abi_version() != ABI_VERSION:
         raise DtreeError("libdtree_hip.so ABI version mismatch; rebuild it")
     for fn, struct in (("dtree_step_desc_bytes", StepDesc), ("dtree_gemm_args_bytes", GemmArgs),
-                       ("dtree_attn_args_bytes", AttnArgs)):
+                       ("dtree_attn_args_bytes", AttnArgs), ("dtree_gdn_args_bytes", GdnArgs)):
         if getattr(h, fn)() != C.sizeof(struct):
             raise DtreeError(f"{struct.__name__} layout mismatch between Python and the library")
     _LIB = h

@@ -108,3 +108,43 @@ class PagedKVCache:
 
     def reset(self, offset: int = 0) -> None:
         self.offset = offset
+
+
+class Qwen35Cache:
+    """Committed state of a Qwen3.5 hybrid: a paged KV cache for the gated
+    attention layers and, per GatedDeltaNet layer, the conv window
+    [K - 1, conv_dim] and the recurrent state [Hv, Dv, Dk], both fp32 (the
+    ArraysCache entries [conv_state, state] of mlx-lm, qwen35_tree.py:85-101).
+    ``offset`` counts committed positions, as the KVCache offset does."""
+
+    def __init__(self, cfg, capacity: int, device="cuda", page_order: torch.Tensor | None = None):
+        self.cfg = cfg
+        self.attn_layers = cfg.attention_layers
+        self.gdn_layers = cfg.linear_layers
+        self.kv = PagedKVCache(len(self.attn_layers), cfg.num_key_value_heads, cfg.head_dim, capacity,
+                               device=device, page_order=page_order)
+        dev = torch.device(device)
+        nG = len(self.gdn_layers)
+        self.windows = torch.zeros(nG, cfg.linear_conv_kernel_dim - 1, cfg.conv_dim, dtype=torch.float32, device=dev)
+        self.states = torch.zeros(nG, cfg.linear_num_value_heads, cfg.linear_value_head_dim,
+                                  cfg.linear_key_head_dim, dtype=torch.float32, device=dev)
+        self.slot = {li: i for i, li in enumerate(self.attn_layers)}
+        self.slot.update({li: i for i, li in enumerate(self.gdn_layers)})
+
+    @property
+    def offset(self) -> int:
+        return self.kv.offset
+
+    @offset.setter
+    def offset(self, v: int) -> None:
+        self.kv.offset = v
+
+    @property
+    def capacity(self) -> int:
+        return self.kv.capacity
+
+    def reset(self, offset: int = 0) -> None:
+        self.kv.offset = offset
+        if offset == 0:
+            self.windows.zero_()
+            self.states.zero_()

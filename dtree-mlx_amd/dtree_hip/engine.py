@@ -72,12 +72,19 @@ class StepResult:
     posterior: list[int]
 
 
-class Qwen3TreeEngine:
-    def __init__(self, cfg: Qwen3Config, weights: Qwen3Weights, max_past: int, max_nodes: int = 32,
-                 layer_ids=(), split_k: dict | None = None):
+class TreeEngineBase:
+    """Buffers and launches shared by the Qwen3 and Qwen3.5 verify steps: the
+    device step descriptor, GEMM arguments, the LM head + argmax, the accept
+    walk, result readback and the HIP graph of the whole step. Subclasses
+    provide the layer stack (launch_forward), the cache and its compaction."""
+
+    max_nodes_limit = 32
+
+    def __init__(self, cfg, weights, max_past: int, max_nodes: int = 32, layer_ids=(), split_k: dict | None = None):
         cfg.validate()
-        if max_nodes > 32:
-            raise NotImplementedError("trees of up to 32 nodes (one 32-row MFMA block) for Qwen3 attention")
+        if max_nodes > self.max_nodes_limit:
+            raise NotImplementedError(
+                f"trees of up to {self.max_nodes_limit} nodes (one 32-row MFMA block) for tree attention")
         self.cfg = cfg
         self.w = weights
         self.lib = N.lib()
@@ -86,30 +93,24 @@ class Qwen3TreeEngine:
         self.max_nodes = max_nodes
         self.MP = 32
         self.layer_ids = list(layer_ids)
-        H, F, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+        H, V = cfg.hidden_size, cfg.vocab_size
         MP, dev = self.MP, self.dev
         f32, bf16 = torch.float32, torch.bfloat16
         # GEMM inputs are split pairs [hi, lo] of bf16 planes (value = hi + lo).
         self.x = torch.zeros(MP, H, dtype=f32, device=dev)
         self.xg = torch.zeros(2, MP, H, dtype=bf16, device=dev)
         self.ss = torch.zeros(H // 32, MP, dtype=f32, device=dev)
-        self.qkv = torch.zeros(MP, cfg.qkv_dim, dtype=f32, device=dev)
-        self.attn = torch.zeros(2, MP, cfg.q_dim, dtype=bf16, device=dev)
-        self.act = torch.zeros(2, MP, F, dtype=bf16, device=dev)
-        self.rope_cos = torch.zeros(MP, cfg.head_dim // 2, dtype=f32, device=dev)
-        self.rope_sin = torch.zeros(MP, cfg.head_dim // 2, dtype=f32, device=dev)
         self.norm_hidden = torch.zeros(MP, H, dtype=bf16, device=dev)
         nh = max(1, len(self.layer_ids))
         self.hidden = torch.zeros(MP, nh * H, dtype=bf16, device=dev)
         self.hidden_sel = torch.zeros(MP, nh * H, dtype=bf16, device=dev)
         self.logits = None
         self.split_k = dict(split_k or {})
+        self._alloc_layer_buffers()
         shapes = self._gemm_shapes()
         ws = max(self.lib.dtree_gemm_workspace_bytes(MP, n, k, self.split_k.get(name, 0))
                  for name, (n, k) in shapes.items())
         self.gemm_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
-        aws = self.lib.dtree_attention_workspace_bytes(cfg.num_attention_heads, cfg.head_dim, self.max_past)
-        self.attn_ws = torch.zeros(aws, dtype=torch.uint8, device=dev)
         self.n_cand = self.lib.dtree_lmhead_candidate_blocks(V, MP)
         self.cand = torch.zeros(self.lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=dev)
         self.desc_host = N.StepDesc()
@@ -126,16 +127,20 @@ class Qwen3TreeEngine:
         self.result_host = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32).pin_memory()
         self._graphs: dict = {}
 
-    # ---- sizes ---------------------------------------------------------------
-    def _gemm_shapes(self):
-        c = self.cfg
-        H, F = c.hidden_size, c.intermediate_size
-        return {"qkv": (c.qkv_dim, H), "o": (H, c.q_dim), "gu": (2 * F, H), "down": (H, F)}
+    def _alloc_layer_buffers(self) -> None:
+        raise NotImplementedError
 
-    def new_cache(self, page_order=None) -> PagedKVCache:
-        c = self.cfg
-        return PagedKVCache(c.num_hidden_layers, c.num_key_value_heads, c.head_dim,
-                            self.max_past + self.max_nodes, device=self.dev, page_order=page_order)
+    def _gemm_shapes(self) -> dict:
+        raise NotImplementedError
+
+    def new_cache(self, page_order=None):
+        raise NotImplementedError
+
+    def launch_forward(self, cache, st: int, norm_hidden: bool = False) -> None:
+        raise NotImplementedError
+
+    def launch_compact(self, cache, st: int, select_hidden: bool = True, aux: bool = False) -> None:
+        raise NotImplementedError
 
     @staticmethod
     def stream_handle(stream=None) -> int:
@@ -234,58 +239,6 @@ class Qwen3TreeEngine:
         a = self.gemm_args(name, x, ldx, w, epi, **kw)
         N.check(self.lib.dtree_gemm_bf16(C.byref(a), st), f"gemm {name}")
 
-    def _attention(self, li, cache: PagedKVCache, st, write_cache=True):
-        c = self.cfg
-        lw = self.w.layers[li]
-        a = N.AttnArgs()
-        a.qkv = self.qkv.data_ptr(); a.ld_qkv = self.qkv.shape[1]
-        a.q_norm = lw.q_norm.data_ptr(); a.k_norm = lw.k_norm.data_ptr(); a.eps = c.rms_norm_eps
-        a.rope_cos = self.rope_cos.data_ptr(); a.rope_sin = self.rope_sin.data_ptr()
-        a.k_pages = cache.k_ptr(li); a.v_pages = cache.v_ptr(li); a.page_table = cache.page_table.data_ptr()
-        a.desc = self.desc.data_ptr()
-        a.out = self.attn[0].data_ptr(); a.out_lo = self.attn[1].data_ptr(); a.ld_out = self.attn.shape[-1]
-        a.out_layout = self.w.layout
-        a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
-        a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
-        a.max_past_length = self.max_past; a.write_cache = 1 if write_cache else 0
-        a.workspace = self.attn_ws.data_ptr(); a.workspace_bytes = self.attn_ws.numel()
-        N.check(self.lib.dtree_tree_attention(C.byref(a), st), "tree attention")
-
-    def launch_forward(self, cache: PagedKVCache, st: int, norm_hidden: bool = False) -> None:
-        """embed + all layers; tree K/V rows land in the cache at [P, P+L)."""
-        c = self.cfg
-        H = c.hidden_size
-        if cache.capacity < self.max_past + self.max_nodes:
-            raise ValueError("cache capacity is smaller than max_past + max_nodes")
-        emb, emb_layout, emb_sb = self._embedding()
-        N.check(self.lib.dtree_embed(
-            self.desc.data_ptr(), emb, emb_layout, emb_sb, c.vocab_size, H,
-            self.w.layers[0].input_norm.data_ptr(),
-            self.MP,
-            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
-            c.head_dim, c.rope_theta,
-            self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
-        slot = {li: i for i, li in enumerate(self.layer_ids)}
-        nL = c.num_hidden_layers
-        for li in range(nL):
-            lw = self.w.layers[li]
-            nxt = self.w.layers[li + 1].input_norm if li + 1 < nL else self.w.final_norm
-            self._gemm("qkv", self.xg, H, lw.wqkv, N.EPI_STORE_F32, st, ss_in=self.ss, out_f32=self.qkv)
-            self._attention(li, cache, st)
-            self._gemm("o", self.attn, c.q_dim, lw.wo, N.EPI_RESIDUAL, st, out_f32=self.x, out_bf16=self.xg,
-                       next_norm=lw.post_norm, ss_out=self.ss)
-            self._gemm("gu", self.xg, H, lw.wgu, N.EPI_SWIGLU, st, ss_in=self.ss, out_bf16=self.act)
-            hid, ldh = 0, 0
-            if li in slot:
-                hid = self.hidden.data_ptr() + 2 * slot[li] * H
-                ldh = self.hidden.shape[1]
-            self._gemm("down", self.act, c.intermediate_size, lw.wd, N.EPI_RESIDUAL, st, out_f32=self.x,
-                       out_bf16=self.xg, next_norm=nxt, ss_out=self.ss, hidden_out=hid, ld_hidden=ldh)
-        if norm_hidden:
-            N.check(self.lib.dtree_rownorm(self.x.data_ptr(), H, self.MP, H, self.ss.data_ptr(), H // 32,
-                                           self.w.final_norm.data_ptr(), c.rms_norm_eps,
-                                           self.norm_hidden.data_ptr(), H, st), "rownorm")
-
     def launch_lm_head(self, st: int, x=None, ss=True, want_logits=False) -> None:
         c = self.cfg
         logits_ptr = None
@@ -311,15 +264,6 @@ class Qwen3TreeEngine:
         d = self.desc_aux if aux else self.desc
         N.check(self.lib.dtree_accept_walk(d.data_ptr(), self.cand.data_ptr(), self.n_cand, self.MP,
                                            self.result.data_ptr(), st), "accept walk")
-
-    def launch_compact(self, cache: PagedKVCache, st: int, select_hidden: bool = True, aux: bool = False) -> None:
-        c = self.cfg
-        d = self.desc_aux if aux else self.desc
-        N.check(self.lib.dtree_compact(
-            d.data_ptr(), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(), cache.layer_stride,
-            c.num_hidden_layers, c.num_key_value_heads, c.head_dim, cache.page_table.data_ptr(),
-            self.hidden.data_ptr() if select_hidden else None, self.hidden.shape[1],
-            self.hidden_sel.data_ptr() if select_hidden else None, st), "compact")
 
     def launch_verify(self, cache: PagedKVCache, st: int) -> None:
         self.launch_forward(cache, st)
@@ -416,3 +360,91 @@ class Qwen3TreeEngine:
             self.release_graphs()
         except Exception:
             pass
+
+
+class Qwen3TreeEngine(TreeEngineBase):
+    """Qwen3 tree-verify executor (module docstring)."""
+
+    def _alloc_layer_buffers(self) -> None:
+        c, MP, dev = self.cfg, self.MP, self.dev
+        f32, bf16 = torch.float32, torch.bfloat16
+        self.qkv = torch.zeros(MP, c.qkv_dim, dtype=f32, device=dev)
+        self.attn = torch.zeros(2, MP, c.q_dim, dtype=bf16, device=dev)
+        self.act = torch.zeros(2, MP, c.intermediate_size, dtype=bf16, device=dev)
+        self.rope_cos = torch.zeros(MP, c.head_dim // 2, dtype=f32, device=dev)
+        self.rope_sin = torch.zeros(MP, c.head_dim // 2, dtype=f32, device=dev)
+        aws = self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim, self.max_past)
+        self.attn_ws = torch.zeros(aws, dtype=torch.uint8, device=dev)
+
+    # ---- sizes ---------------------------------------------------------------
+    def _gemm_shapes(self):
+        c = self.cfg
+        H, F = c.hidden_size, c.intermediate_size
+        return {"qkv": (c.qkv_dim, H), "o": (H, c.q_dim), "gu": (2 * F, H), "down": (H, F)}
+
+    def new_cache(self, page_order=None) -> PagedKVCache:
+        c = self.cfg
+        return PagedKVCache(c.num_hidden_layers, c.num_key_value_heads, c.head_dim,
+                            self.max_past + self.max_nodes, device=self.dev, page_order=page_order)
+
+    def _attention(self, li, cache: PagedKVCache, st, write_cache=True):
+        c = self.cfg
+        lw = self.w.layers[li]
+        a = N.AttnArgs()
+        a.qkv = self.qkv.data_ptr(); a.ld_qkv = self.qkv.shape[1]
+        a.q_norm = lw.q_norm.data_ptr(); a.k_norm = lw.k_norm.data_ptr(); a.eps = c.rms_norm_eps
+        a.rope_cos = self.rope_cos.data_ptr(); a.rope_sin = self.rope_sin.data_ptr()
+        a.k_pages = cache.k_ptr(li); a.v_pages = cache.v_ptr(li); a.page_table = cache.page_table.data_ptr()
+        a.desc = self.desc.data_ptr()
+        a.out = self.attn[0].data_ptr(); a.out_lo = self.attn[1].data_ptr(); a.ld_out = self.attn.shape[-1]
+        a.out_layout = self.w.layout
+        a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
+        a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
+        a.max_past_length = self.max_past; a.write_cache = 1 if write_cache else 0
+        a.workspace = self.attn_ws.data_ptr(); a.workspace_bytes = self.attn_ws.numel()
+        N.check(self.lib.dtree_tree_attention(C.byref(a), st), "tree attention")
+
+    def launch_forward(self, cache: PagedKVCache, st: int, norm_hidden: bool = False) -> None:
+        """embed + all layers; tree K/V rows land in the cache at [P, P+L)."""
+        c = self.cfg
+        H = c.hidden_size
+        if cache.capacity < self.max_past + self.max_nodes:
+            raise ValueError("cache capacity is smaller than max_past + max_nodes")
+        emb, emb_layout, emb_sb = self._embedding()
+        N.check(self.lib.dtree_embed(
+            self.desc.data_ptr(), emb, emb_layout, emb_sb, c.vocab_size, H,
+            self.w.layers[0].input_norm.data_ptr(),
+            self.MP,
+            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
+            c.head_dim, c.rope_theta,
+            self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
+        slot = {li: i for i, li in enumerate(self.layer_ids)}
+        nL = c.num_hidden_layers
+        for li in range(nL):
+            lw = self.w.layers[li]
+            nxt = self.w.layers[li + 1].input_norm if li + 1 < nL else self.w.final_norm
+            self._gemm("qkv", self.xg, H, lw.wqkv, N.EPI_STORE_F32, st, ss_in=self.ss, out_f32=self.qkv)
+            self._attention(li, cache, st)
+            self._gemm("o", self.attn, c.q_dim, lw.wo, N.EPI_RESIDUAL, st, out_f32=self.x, out_bf16=self.xg,
+                       next_norm=lw.post_norm, ss_out=self.ss)
+            self._gemm("gu", self.xg, H, lw.wgu, N.EPI_SWIGLU, st, ss_in=self.ss, out_bf16=self.act)
+            hid, ldh = 0, 0
+            if li in slot:
+                hid = self.hidden.data_ptr() + 2 * slot[li] * H
+                ldh = self.hidden.shape[1]
+            self._gemm("down", self.act, c.intermediate_size, lw.wd, N.EPI_RESIDUAL, st, out_f32=self.x,
+                       out_bf16=self.xg, next_norm=nxt, ss_out=self.ss, hidden_out=hid, ld_hidden=ldh)
+        if norm_hidden:
+            N.check(self.lib.dtree_rownorm(self.x.data_ptr(), H, self.MP, H, self.ss.data_ptr(), H // 32,
+                                           self.w.final_norm.data_ptr(), c.rms_norm_eps,
+                                           self.norm_hidden.data_ptr(), H, st), "rownorm")
+
+    def launch_compact(self, cache: PagedKVCache, st: int, select_hidden: bool = True, aux: bool = False) -> None:
+        c = self.cfg
+        d = self.desc_aux if aux else self.desc
+        N.check(self.lib.dtree_compact(
+            d.data_ptr(), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(), cache.layer_stride,
+            c.num_hidden_layers, c.num_key_value_heads, c.head_dim, cache.page_table.data_ptr(),
+            self.hidden.data_ptr() if select_hidden else None, self.hidden.shape[1],
+            self.hidden_sel.data_ptr() if select_hidden else None, st), "compact")
+

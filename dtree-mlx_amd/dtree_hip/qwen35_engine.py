@@ -1,0 +1,194 @@
+"""Qwen3.5 hybrid tree-verify executor (forward_qwen35_tree_with_hidden_states
++ commit_qwen35_tree_path, qwen35_tree.py:629-732, on the HIP kernels).
+
+One step:
+  embed (+ first input RMSNorm fold, RoPE table for the 64 rotary dims)
+  GatedDeltaNet layer (qwen35_tree.py:329-480):
+    in_proj GEMM [qkv | z | b | a] (row scale = input RMSNorm)   -> proj fp32
+    prep: tree conv1d + SiLU, q/k RMS scaling, g, beta              -> q k v g beta
+    tree recurrence from the committed state (node states in LDS)  -> y
+    gated RMSNorm (y, z)                                           -> bf16 pair
+    out_proj GEMM + residual (+ post-attention RMSNorm fold)
+  gated attention layer (qwen35_tree.py:552-626):
+    QKV GEMM (q_proj [q | gate] per head, k_proj, v_proj)          -> fp32
+    tree attention (q/k norm, partial RoPE, cache append, mask, sigmoid gate)
+    o_proj GEMM + residual (+ post-attention RMSNorm fold)
+  MLP: gate/up GEMM + SwiGLU, down GEMM + residual (+ next RMSNorm fold)
+  LM head + argmax, accept walk, KV compaction of the attention layers and
+  the commit of every GatedDeltaNet layer along the accepted path.
+
+The reference keeps a pending state and commits it in compact_kv_caches
+(adapters.py:411-448); here the attention layers append the tree K/V at
+[P, P + L) during the forward (compaction moves the accepted rows to
+[P, P + n)), and the GatedDeltaNet layers keep their per-node inputs in
+per-layer buffers that the commit replays along the accepted path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _native as N
+from .cache import Qwen35Cache
+from .engine import TreeEngineBase
+from .weights import GdnLayerWeights
+
+
+class Qwen35TreeEngine(TreeEngineBase):
+
+    def _alloc_layer_buffers(self) -> None:
+        c, MP, dev = self.cfg, self.MP, self.dev
+        f32, bf16 = torch.float32, torch.bfloat16
+        nG = len(c.linear_layers)
+        Hv = c.linear_num_value_heads
+        # Per GatedDeltaNet layer: the projection and the prepped recurrence
+        # inputs of every node, kept until the commit after the walk.
+        self.proj = torch.zeros(nG, MP, c.in_proj_dim, dtype=f32, device=dev)
+        self.gq = torch.zeros(nG, MP, c.key_dim, dtype=f32, device=dev)
+        self.gk = torch.zeros(nG, MP, c.key_dim, dtype=f32, device=dev)
+        self.gv = torch.zeros(nG, MP, c.value_dim, dtype=f32, device=dev)
+        self.gg = torch.zeros(nG, MP, Hv, dtype=f32, device=dev)
+        self.gbeta = torch.zeros(nG, MP, Hv, dtype=f32, device=dev)
+        self.gy = torch.zeros(MP, c.value_dim, dtype=f32, device=dev)
+        self.gout = torch.zeros(2, MP, c.value_dim, dtype=bf16, device=dev)
+        self.qkv = torch.zeros(MP, c.attn_qkv_dim, dtype=f32, device=dev)
+        self.attn = torch.zeros(2, MP, c.q_dim, dtype=bf16, device=dev)
+        self.act = torch.zeros(2, MP, c.intermediate_size, dtype=bf16, device=dev)
+        self.rope_cos = torch.zeros(MP, c.rope_dims // 2, dtype=f32, device=dev)
+        self.rope_sin = torch.zeros(MP, c.rope_dims // 2, dtype=f32, device=dev)
+        aws = self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim, self.max_past)
+        self.attn_ws = torch.zeros(aws, dtype=torch.uint8, device=dev)
+
+    def _gemm_shapes(self):
+        c = self.cfg
+        H, F = c.hidden_size, c.intermediate_size
+        return {"in": (c.in_proj_dim, H), "out": (H, c.value_dim), "qkv": (c.attn_qkv_dim, H),
+                "o": (H, c.q_dim), "gu": (2 * F, H), "down": (H, F)}
+
+    def new_cache(self, page_order=None) -> Qwen35Cache:
+        return Qwen35Cache(self.cfg, self.max_past + self.max_nodes, device=self.dev, page_order=page_order)
+
+    # ---- launches ----------------------------------------------------------------
+    def gdn_args(self, li: int, cache: Qwen35Cache) -> N.GdnArgs:
+        c = self.cfg
+        gi = cache.slot[li]
+        lw: GdnLayerWeights = self.w.layers[li]
+        a = N.GdnArgs()
+        a.desc = self.desc.data_ptr(); a.rows_padded = self.MP
+        a.num_k_heads = c.linear_num_key_heads; a.num_v_heads = c.linear_num_value_heads
+        a.head_k_dim = c.linear_key_head_dim; a.head_v_dim = c.linear_value_head_dim
+        a.conv_keep = c.linear_conv_kernel_dim - 1
+        a.proj = self.proj[gi].data_ptr(); a.ld_proj = c.in_proj_dim
+        a.window = cache.windows[gi].data_ptr(); a.conv_w = lw.conv_w.data_ptr()
+        a.A_log = lw.A_log.data_ptr(); a.dt_bias = lw.dt_bias.data_ptr()
+        a.state = cache.states[gi].data_ptr()
+        a.q = self.gq[gi].data_ptr(); a.k = self.gk[gi].data_ptr(); a.v = self.gv[gi].data_ptr()
+        a.g = self.gg[gi].data_ptr(); a.beta = self.gbeta[gi].data_ptr()
+        a.y = self.gy.data_ptr()
+        a.norm_w = lw.gnorm.data_ptr(); a.eps = c.rms_norm_eps
+        a.out = self.gout[0].data_ptr(); a.out_lo = self.gout[1].data_ptr()
+        a.out_layout = self.w.layout; a.ld_out = c.value_dim
+        return a
+
+    def _attention(self, li, cache: Qwen35Cache, st, write_cache=True):
+        c = self.cfg
+        ai = cache.slot[li]
+        lw = self.w.layers[li]
+        kv = cache.kv
+        a = N.AttnArgs()
+        a.qkv = self.qkv.data_ptr(); a.ld_qkv = self.qkv.shape[1]
+        a.q_norm = lw.q_norm.data_ptr(); a.k_norm = lw.k_norm.data_ptr(); a.eps = c.rms_norm_eps
+        a.rope_cos = self.rope_cos.data_ptr(); a.rope_sin = self.rope_sin.data_ptr()
+        a.k_pages = kv.k_ptr(ai); a.v_pages = kv.v_ptr(ai); a.page_table = kv.page_table.data_ptr()
+        a.desc = self.desc.data_ptr()
+        a.out = self.attn[0].data_ptr(); a.out_lo = self.attn[1].data_ptr(); a.ld_out = self.attn.shape[-1]
+        a.out_layout = self.w.layout
+        a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
+        a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
+        a.max_past_length = self.max_past; a.write_cache = 1 if write_cache else 0
+        a.workspace = self.attn_ws.data_ptr(); a.workspace_bytes = self.attn_ws.numel()
+        a.rope_dims = c.rope_dims; a.gated = 1
+        N.check(self.lib.dtree_tree_attention(C.byref(a), st), "tree attention")
+
+    def launch_forward(self, cache: Qwen35Cache, st: int, norm_hidden: bool = False) -> None:
+        """embed + all layers; attention-layer tree K/V land in the cache at
+        [P, P + L); GatedDeltaNet per-node inputs stay in the layer buffers."""
+        c = self.cfg
+        H = c.hidden_size
+        if cache.capacity < self.max_past + self.max_nodes:
+            raise ValueError("cache capacity is smaller than max_past + max_nodes")
+        emb, emb_layout, emb_sb = self._embedding()
+        N.check(self.lib.dtree_embed(
+            self.desc.data_ptr(), emb, emb_layout, emb_sb, c.vocab_size, H,
+            self.w.layers[0].input_norm.data_ptr(), self.MP,
+            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
+            c.rope_dims, c.rope_theta, self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
+        slot = {li: i for i, li in enumerate(self.layer_ids)}
+        nL = c.num_hidden_layers
+        for li in range(nL):
+            lw = self.w.layers[li]
+            nxt = self.w.layers[li + 1].input_norm if li + 1 < nL else self.w.final_norm
+            if c.is_linear(li):
+                gi = cache.slot[li]
+                self._gemm("in", self.xg, H, lw.w_in, N.EPI_STORE_F32, st, ss_in=self.ss, out_f32=self.proj[gi])
+                ga = self.gdn_args(li, cache)
+                N.check(self.lib.dtree_gdn_layer_prep(C.byref(ga), st), "gdn prep")
+                N.check(self.lib.dtree_gdn_layer_recurrence(C.byref(ga), st), "gdn recurrence")
+                N.check(self.lib.dtree_gdn_layer_gated_norm(C.byref(ga), st), "gdn gated norm")
+                self._gemm("out", self.gout, c.value_dim, lw.w_out, N.EPI_RESIDUAL, st, out_f32=self.x,
+                           out_bf16=self.xg, next_norm=lw.post_norm, ss_out=self.ss)
+            else:
+                self._gemm("qkv", self.xg, H, lw.wqkv, N.EPI_STORE_F32, st, ss_in=self.ss, out_f32=self.qkv)
+                self._attention(li, cache, st)
+                self._gemm("o", self.attn, c.q_dim, lw.wo, N.EPI_RESIDUAL, st, out_f32=self.x, out_bf16=self.xg,
+                           next_norm=lw.post_norm, ss_out=self.ss)
+            self._gemm("gu", self.xg, H, lw.wgu, N.EPI_SWIGLU, st, ss_in=self.ss, out_bf16=self.act)
+            hid, ldh = 0, 0
+            if li in slot:
+                hid = self.hidden.data_ptr() + 2 * slot[li] * H
+                ldh = self.hidden.shape[1]
+            self._gemm("down", self.act, c.intermediate_size, lw.wd, N.EPI_RESIDUAL, st, out_f32=self.x,
+                       out_bf16=self.xg, next_norm=nxt, ss_out=self.ss, hidden_out=hid, ld_hidden=ldh)
+        if norm_hidden:
+            N.check(self.lib.dtree_rownorm(self.x.data_ptr(), H, self.MP, H, self.ss.data_ptr(), H // 32,
+                                           self.w.final_norm.data_ptr(), c.rms_norm_eps,
+                                           self.norm_hidden.data_ptr(), H, st), "rownorm")
+
+    def launch_compact(self, cache: Qwen35Cache, st: int, select_hidden: bool = True, aux: bool = False) -> None:
+        """commit_qwen35_tree_path: KV compaction of the attention layers (+ the
+        hidden-state select), then every GatedDeltaNet layer's window / state
+        replayed along desc.accepted."""
+        c = self.cfg
+        d = self.desc_aux if aux else self.desc
+        kv = cache.kv
+        N.check(self.lib.dtree_compact(
+            d.data_ptr(), kv.k_pages.data_ptr(), kv.v_pages.data_ptr(), kv.layer_stride, kv.layers,
+            c.num_key_value_heads, c.head_dim, kv.page_table.data_ptr(),
+            self.hidden.data_ptr() if select_hidden else None, self.hidden.shape[1],
+            self.hidden_sel.data_ptr() if select_hidden else None, st), "compact")
+        self._commit_gdn(cache, st, d)
+
+    def _commit_gdn(self, cache: Qwen35Cache, st: int, desc: torch.Tensor) -> None:
+        for li in cache.gdn_layers:
+            ga = self.gdn_args(li, cache)
+            ga.desc = desc.data_ptr()
+            N.check(self.lib.dtree_gdn_layer_commit(C.byref(ga), st), "gdn commit")
+
+    def prefill(self, cache: Qwen35Cache, tokens, chunk: int | None = None) -> None:
+        """Causal prefill through the tree path: chains of up to max_nodes
+        tokens, each fully accepted (KV rows stay where the forward wrote them,
+        GatedDeltaNet windows / states advance along the whole chain)."""
+        chunk = chunk or self.max_nodes
+        toks = [int(t) for t in tokens]
+        st = self.stream_handle()
+        for s in range(0, len(toks), chunk):
+            part = toks[s:s + chunk]
+            P = cache.offset
+            if P + len(part) > self.max_past:
+                raise ValueError("prefill beyond max_past")
+            n = len(part)
+            self.set_step(part, [P + i for i in range(n)], [-1] + list(range(n - 1)), P, accepted=list(range(n)))
+            self.launch_forward(cache, st)
+            self._commit_gdn(cache, st, self.desc)
+            cache.offset = P + n

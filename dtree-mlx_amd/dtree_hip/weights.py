@@ -310,3 +310,181 @@ class Qwen3Weights:
                          "post_norm": lw.post_norm}[name])
 
         return get
+
+
+@dataclass
+class GdnLayerWeights:
+    """One GatedDeltaNet layer (custom_qwen35_model.py:777-823 parameters).
+
+    w_in [in_proj_dim, H]: rows in_proj_qkv (conv_dim) | in_proj_z (value_dim)
+    | in_proj_b (Hv) | in_proj_a (Hv) | zero padding; conv_w fp32 [K, conv_dim]
+    (conv1d.weight[:, :, 0].T, newest tap last); A_log, dt_bias fp32 [Hv];
+    gnorm bf16 [Dv] (RMSNormGated weight); w_out [H, value_dim]."""
+    input_norm: torch.Tensor
+    w_in: torch.Tensor
+    conv_w: torch.Tensor
+    A_log: torch.Tensor
+    dt_bias: torch.Tensor
+    gnorm: torch.Tensor
+    w_out: torch.Tensor
+    post_norm: torch.Tensor
+    wgu: torch.Tensor
+    wd: torch.Tensor
+
+
+def _move(t, device):
+    return t.to(device)
+
+
+@dataclass
+class Qwen35Weights:
+    """Qwen3.5 hybrid weights: ``layers[i]`` is a GdnLayerWeights for
+    GatedDeltaNet layers and a LayerWeights for the gated attention layers
+    (wqkv rows: q_proj with [q | gate] per head, then k_proj, v_proj)."""
+    cfg: "Qwen35Config"
+    embed: torch.Tensor
+    final_norm: torch.Tensor
+    layers: list = field(default_factory=list)
+    layout: int = W_TILED
+    quant: str = "bf16"
+
+    @property
+    def device(self) -> torch.device:
+        return self.final_norm.device
+
+    @classmethod
+    def random(cls, cfg, seed: int = 0, device="cuda", std: float = 0.02, norm_jitter: float = 0.0,
+               quant: str = "bf16") -> "Qwen35Weights":
+        """Seeded random init: linear / embedding weights N(0, std) in bf16 (or
+        q4 group-64: nibbles uniform, scales |N(0, 0.02)| * 8, biases
+        N(0, 0.01)); norm weights 1 (+ N(0, jitter)); conv weights U(-0.5, 0.5)
+        rounded to bf16; A = U(1, 16), A_log = log A; dt_bias 1 (the init of
+        custom_qwen35_model.py:812-815 with A bounded away from 0)."""
+        from .config import Qwen35Config  # noqa: F401  (type of cfg)
+        cfg.validate()
+        if quant not in ("bf16", "q4"):
+            raise ValueError("quant must be 'bf16' or 'q4'")
+        dev = torch.device(device)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        H, F = cfg.hidden_size, cfg.intermediate_size
+
+        def lin_bf16(rows, cols):
+            t = torch.empty(rows, cols, dtype=torch.float32, device=dev)
+            t.normal_(0.0, std, generator=gen)
+            return t.to(torch.bfloat16)
+
+        def pad_rows(t, rows):
+            return torch.cat([t, t.new_zeros(rows - t.shape[0], *t.shape[1:])]) if rows > t.shape[0] else t
+
+        def lin(rows, cols, pad_to=None):
+            if quant == "q4":
+                wq, s, b = q4_random_mlx(rows, cols, gen, dev)
+                if pad_to:
+                    wq, s, b = pad_rows(wq, pad_to), pad_rows(s, pad_to), pad_rows(b, pad_to)
+                return Q4Linear(*q4_to_tiled(wq, s, b))
+            t = lin_bf16(rows, cols)
+            return tile_weight(pad_rows(t, pad_to) if pad_to else t)
+
+        def gate_up():
+            if quant == "q4":
+                gq, gs, gb = q4_random_mlx(F, H, gen, dev)
+                uq, us, ub = q4_random_mlx(F, H, gen, dev)
+                return Q4Linear(*q4_to_tiled(interleave_gate_up(gq, uq), interleave_gate_up(gs, us),
+                                            interleave_gate_up(gb, ub)))
+            return tile_weight(interleave_gate_up(lin_bf16(F, H), lin_bf16(F, H)))
+
+        def norm(n):
+            if norm_jitter == 0.0:
+                return torch.ones(n, dtype=torch.bfloat16, device=dev)
+            t = torch.empty(n, dtype=torch.float32, device=dev).normal_(0.0, norm_jitter, generator=gen)
+            return (1.0 + t).to(torch.bfloat16)
+
+        embed = lin(cfg.vocab_size, H)
+        layers = []
+        for i in range(cfg.num_hidden_layers):
+            if cfg.is_linear(i):
+                Hv = cfg.linear_num_value_heads
+                in_rows = cfg.conv_dim + cfg.value_dim + 2 * Hv
+                conv = torch.empty(cfg.linear_conv_kernel_dim, cfg.conv_dim, device=dev).uniform_(-0.5, 0.5,
+                                                                                                  generator=gen)
+                A = torch.empty(Hv, device=dev).uniform_(1.0, 16.0, generator=gen)
+                layers.append(GdnLayerWeights(
+                    input_norm=norm(H), w_in=lin(in_rows, H, pad_to=cfg.in_proj_dim),
+                    conv_w=conv.to(torch.bfloat16).float(), A_log=torch.log(A), dt_bias=torch.ones(Hv, device=dev),
+                    gnorm=norm(cfg.linear_value_head_dim), w_out=lin(H, cfg.value_dim), post_norm=norm(H),
+                    wgu=gate_up(), wd=lin(H, F)))
+            else:
+                layers.append(LayerWeights(
+                    input_norm=norm(H), wqkv=lin(cfg.attn_qkv_dim, H), q_norm=norm(cfg.head_dim),
+                    k_norm=norm(cfg.head_dim), wo=lin(H, cfg.q_dim), post_norm=norm(H), wgu=gate_up(),
+                    wd=lin(H, F)))
+        return cls(cfg=cfg, embed=embed, final_norm=norm(H), layers=layers, layout=W_TILED, quant=quant)
+
+    def rowmajor(self, t) -> torch.Tensor:
+        if isinstance(t, Q4Linear):
+            return q4_dequant(t)
+        return untile_weight(t) if self.layout == W_TILED else t
+
+    def embed_rows(self, ids: torch.Tensor) -> torch.Tensor:
+        if isinstance(self.embed, Q4Linear):
+            return q4_rows(self.embed, ids)
+        return tiled_rows(self.embed, ids)
+
+    def nbytes_linear(self) -> int:
+        def nb(t):
+            return t.nbytes() if isinstance(t, Q4Linear) else t.numel() * 2
+        total = 0
+        for lw in self.layers:
+            if isinstance(lw, GdnLayerWeights):
+                total += nb(lw.w_in) + nb(lw.w_out) + nb(lw.wgu) + nb(lw.wd)
+            else:
+                total += nb(lw.wqkv) + nb(lw.wo) + nb(lw.wgu) + nb(lw.wd)
+        return total
+
+    def host_accessor(self):
+        """(layer, name) -> numpy bf16 bits / fp32 arrays in nn.Linear layout,
+        with the names of oracle.qwen35.OracleQwen35."""
+        cfg = self.cfg
+        cache: dict = {}
+
+        def bits(t: torch.Tensor) -> np.ndarray:
+            if t.dtype == torch.float32:
+                return t.detach().to("cpu").contiguous().numpy()
+            return t.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16)
+
+        def get(layer, name):
+            key = (layer, name)
+            if key in cache:
+                return cache[key]
+            if layer is None:
+                out = bits(self.rowmajor(self.embed)) if name == "embed" else bits(self.final_norm)
+                cache[key] = out
+                return out
+            lw = self.layers[layer]
+            if name in ("gate", "up"):
+                g, u = split_gate_up(self.rowmajor(lw.wgu))
+                return bits(g if name == "gate" else u)
+            if name == "down":
+                return bits(self.rowmajor(lw.wd))
+            if name in ("input_norm", "post_norm"):
+                return bits(getattr(lw, name))
+            if isinstance(lw, GdnLayerWeights):
+                C, V, Hv = cfg.conv_dim, cfg.value_dim, cfg.linear_num_value_heads
+                if name in ("in_qkv", "in_z", "in_b", "in_a"):
+                    lo = {"in_qkv": 0, "in_z": C, "in_b": C + V, "in_a": C + V + Hv}[name]
+                    n = {"in_qkv": C, "in_z": V, "in_b": Hv, "in_a": Hv}[name]
+                    return bits(self.rowmajor(lw.w_in)[lo:lo + n])
+                if name == "out":
+                    return bits(self.rowmajor(lw.w_out))
+                t = {"conv": lw.conv_w, "A_log": lw.A_log, "dt_bias": lw.dt_bias, "gnorm": lw.gnorm}[name]
+                return bits(t)
+            q2, kv = 2 * cfg.q_dim, cfg.num_key_value_heads * cfg.head_dim
+            if name in ("q", "k", "v"):
+                lo = {"q": 0, "k": q2, "v": q2 + kv}[name]
+                return bits(self.rowmajor(lw.wqkv)[lo:lo + (q2 if name == "q" else kv)])
+            if name == "o":
+                return bits(self.rowmajor(lw.wo))
+            return bits({"q_norm": lw.q_norm, "k_norm": lw.k_norm}[name])
+
+        return get

@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define DTREE_ABI_VERSION 2
+#define DTREE_ABI_VERSION 3
 
 #define DTREE_OK 0
 #define DTREE_E_ARG (-1)      /* bad shape / pointer / enum */
@@ -158,12 +158,19 @@ int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, int32_t hea
  * (qwen3_tree.py:54-76 and the cache append at :146; mask semantics
  * dtree_runtime.py:190-191). Reads raw q/k/v (fp32, row m = tree node m) from
  * qkv[m][...] laid out as [q heads | k heads | v heads] * head_dim, applies
- * q_norm / k_norm (RMSNorm over head_dim, NULL = none), RoPE from the table,
- * writes the L new K/V rows into the cache at logical positions P..P+L-1,
- * and writes softmax(scale * q k^T + mask) v as bf16 out[m][h*head_dim + d]
- * (rows >= L zero). K pages: [page][kv_head][DTREE_PAGE][head_dim];
- * V pages (transposed): [page][kv_head][head_dim][DTREE_PAGE].
- * page_table maps logical page -> physical page.
+ * q_norm / k_norm (RMSNorm over head_dim, NULL = none), RoPE from the table
+ * (cos/sin [rows][rope_dims/2], pairs (d, d + rope_dims/2), dims >= rope_dims
+ * unrotated), writes the L new K/V rows into the cache at logical positions
+ * P..P+L-1, and writes softmax(scale * q k^T + mask) v as bf16
+ * out[m][h*head_dim + d] (rows >= L zero). K pages:
+ * [page][kv_head][DTREE_PAGE][head_dim]; V pages (transposed):
+ * [page][kv_head][head_dim][DTREE_PAGE]. page_table maps logical page ->
+ * physical page.
+ *
+ * gated = 1 is the Qwen3.5 gated attention (qwen35_tree.py:503-540): each q
+ * head occupies 2*head_dim columns of the qkv row, [q | gate], and the output
+ * is multiplied by sigmoid(gate). Compiled geometries: head_dim 128 with
+ * rope_dims 128 (or 0), gated 0; head_dim 256 with rope_dims 64, gated 1.
  */
 typedef struct DtreeAttnArgs {
   const float* qkv; int32_t ld_qkv;
@@ -178,6 +185,8 @@ typedef struct DtreeAttnArgs {
   int32_t max_past_length;  /* grid is sized for this P */
   int32_t write_cache;      /* 1: append the tree K/V rows to the cache */
   void* workspace; size_t workspace_bytes;
+  int32_t rope_dims;        /* rotated dims per head; 0 = head_dim */
+  int32_t gated;            /* 1: q heads are [q | gate] and out *= sigmoid(gate) */
 } DtreeAttnArgs;
 
 size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim,
@@ -266,6 +275,51 @@ int dtree_gdn_commit(const float* x, float* window, int32_t channels, int32_t ke
                      const float* v, const float* g, const float* beta, float* state, const int32_t* path,
                      const int32_t* path_len, int32_t num_k_heads, int32_t num_v_heads, int32_t head_k_dim,
                      int32_t head_v_dim, hipStream_t stream);
+
+/*
+ * Qwen3.5 GatedDeltaNet layer of the verify step (qwen35_tree.py:329-480 with
+ * the batched-kernel body :180-327), split into four launches that read the
+ * node count, parents and accepted path from the device step descriptor:
+ *
+ *  proj (fp32 [rows][ld_proj]) is the fused input projection of the
+ *  RMS-normalised hidden state: columns [conv input C = 2*Hk*Dk + Hv*Dv |
+ *  z (Hv*Dv) | b (Hv) | a (Hv)] (in_proj_qkv, in_proj_z, in_proj_b, in_proj_a).
+ *
+ *  dtree_gdn_layer_prep: tree conv1d + SiLU from the committed window, split
+ *    q | k | v, q = rms_norm(q) / Dk, k = rms_norm(k) / sqrt(Dk) (eps 1e-6,
+ *    :304-306), g = exp(-exp(A_log) softplus(a + dt_bias)), beta = sigmoid(b)
+ *    (:307-308) -> q, k [rows][Hk][Dk], v [rows][Hv][Dv], g, beta [rows][Hv].
+ *  dtree_gdn_layer_recurrence: tree gated-delta recurrence from the committed
+ *    state -> y [rows][Hv][Dv]; node states stay in LDS (lazy).
+ *  dtree_gdn_layer_gated_norm: out = rms_norm(y) * norm_w * silu(z) per value
+ *    head (:322) as bf16 [hi, lo] (out_lo optional) for out_proj; rows >= L zero.
+ *  dtree_gdn_layer_commit: commit_qwen35_tree_path (:708-732) for this layer:
+ *    replays desc->accepted[0 .. n_accepted) on window and state in place.
+ *
+ * The per-node buffers (proj, q, k, v, g, beta) must stay untouched between
+ * the layer's prep and its commit. Compiled for Dk = Dv = 128.
+ */
+typedef struct DtreeGdnArgs {
+  const DtreeStepDesc* desc;
+  int32_t rows_padded;               /* node capacity of the per-node buffers (<= 128) */
+  int32_t num_k_heads, num_v_heads, head_k_dim, head_v_dim;
+  int32_t conv_keep;                 /* conv kernel size - 1 */
+  const float* proj; int32_t ld_proj;
+  float* window;                     /* [conv_keep][C] committed conv window */
+  const float* conv_w;               /* [conv_keep + 1][C], newest tap last */
+  const float* A_log; const float* dt_bias;  /* [Hv] */
+  float* state;                      /* [Hv][Dv][Dk] committed state */
+  float* q; float* k; float* v; float* g; float* beta;
+  float* y;                          /* [rows][Hv][Dv] */
+  const uint16_t* norm_w; float eps; /* gated RMSNorm weight [Dv] (bf16) */
+  uint16_t* out; uint16_t* out_lo; int32_t out_layout; int32_t ld_out;
+} DtreeGdnArgs;
+
+size_t dtree_gdn_args_bytes(void);
+int dtree_gdn_layer_prep(const DtreeGdnArgs* args, hipStream_t stream);
+int dtree_gdn_layer_recurrence(const DtreeGdnArgs* args, hipStream_t stream);
+int dtree_gdn_layer_gated_norm(const DtreeGdnArgs* args, hipStream_t stream);
+int dtree_gdn_layer_commit(const DtreeGdnArgs* args, hipStream_t stream);
 
 /* Convert a row-major [n][k] bf16 matrix to DTREE_W_TILED (n % 32 == 0,
  * k % 64 == 0; src and dst must not overlap). */

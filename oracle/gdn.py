@@ -29,7 +29,8 @@ import numpy as np
 
 
 def silu(x):
-    return x / (1.0 + np.exp(-x))
+    with np.errstate(over="ignore"):  # exp(-x) -> inf gives the limit -0 for x -> -inf
+        return x / (1.0 + np.exp(-x))
 
 
 def tree_conv1d(x: np.ndarray, base: np.ndarray, w: np.ndarray, parents) -> tuple[np.ndarray, np.ndarray]:

@@ -1,0 +1,204 @@
+"""Qwen3.5 hybrid verify step on the GPU (GatedDeltaNet + gated attention
+layers, LM-head argmax, accept walk, KV compaction and the GatedDeltaNet
+commit) against the oracle (oracle/qwen35.py) on the same weights, committed
+state and tree.
+
+The oracle starts from the device's committed state after the prefill (KV
+prefix of the attention layers, conv windows and recurrent states of the
+GatedDeltaNet layers), so the check isolates one step; the prefill itself is
+checked against the oracle's chain commit separately.
+
+Bars: logits within 2e-2 relative (max |diff| per row <= 2e-2 x max |oracle
+logit| of that row); argmax tokens bit-exact on rows whose oracle top-2
+margin exceeds that tolerance; accepted path bit-exact when every row the
+walk reads has such a margin; compacted attention cache = the pre-compaction
+rows gathered at the accepted indices, bit for bit; committed windows and
+states within 2e-2 of the oracle's commit along the device's accepted path."""
+import time
+
+import numpy as np
+import pytest
+import torch
+
+from dtree_hip import Qwen35TreeEngine, Qwen35Weights, tiny_qwen35
+from dtree_hip.config import QWEN35_4B
+from dtree_hip.synthetic import acceptance_rewrite, make_tree, random_prefix
+from oracle import qwen35 as o35
+from oracle import tree as otree
+from oracle.qwen3 import bf16_to_f32
+
+from gpu_util import bf16_f32
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _oracle_cfg(c):
+    return o35.Qwen35Config(
+        hidden=c.hidden_size, layers=c.num_hidden_layers, ffn=c.intermediate_size, heads=c.num_attention_heads,
+        kv_heads=c.num_key_value_heads, head_dim=c.head_dim, rope_dims=c.rope_dims,
+        lin_k_heads=c.linear_num_key_heads, lin_v_heads=c.linear_num_value_heads, lin_k_dim=c.linear_key_head_dim,
+        lin_v_dim=c.linear_value_head_dim, conv_kernel=c.linear_conv_kernel_dim,
+        full_attention_interval=c.full_attention_interval, vocab=c.vocab_size, eps=c.rms_norm_eps,
+        rope_base=c.rope_theta)
+
+
+def _oracle_cache(cfg, cache, P):
+    """The device's committed state as an oracle cache (fp32)."""
+    layers = []
+    for li in range(cfg.num_hidden_layers):
+        s = cache.slot[li]
+        if cfg.is_linear(li):
+            layers.append((cache.windows[s].cpu().numpy().copy(), cache.states[s].cpu().double().numpy().copy()))
+        else:
+            layers.append((bf16_f32(cache.kv.logical_keys(s, P)), bf16_f32(cache.kv.logical_values(s, P))))
+    return o35.Qwen35Cache(layers=layers, offset=P)
+
+
+def _close(got, want, what):
+    err = np.abs(np.asarray(got, np.float64) - want).max()
+    assert err <= TOL * max(1.0, np.abs(want).max()), f"{what}: max err {err}"
+
+
+def _run(cfg, P, layer_ids, dev, norm_jitter=0.1, quant="bf16", log=print, check_prefill=False):
+    t0 = time.time()
+    w = Qwen35Weights.random(cfg, seed=0, device=dev, norm_jitter=norm_jitter, quant=quant)
+    eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=layer_ids)
+    cache = eng.new_cache()
+    prefix = random_prefix(P, cfg.vocab_size, seed=1)
+    eng.prefill(cache, prefix)
+    torch.cuda.synchronize()
+    assert cache.offset == P
+    orc = o35.OracleQwen35(_oracle_cfg(cfg), w.host_accessor())
+    if check_prefill:
+        oc = orc.new_cache()
+        chain = [-1] + list(range(P - 1))
+        _, _, pend = orc.forward_tree(np.asarray(prefix), np.arange(P), chain, oc)
+        orc.commit(oc, pend, chain, list(range(P)))
+        for li in cfg.linear_layers:
+            s = cache.slot[li]
+            _close(cache.windows[s].cpu().numpy(), oc.layers[li][0], f"prefill window {li}")
+            _close(cache.states[s].cpu().numpy(), oc.layers[li][1], f"prefill state {li}")
+        for li in cfg.attention_layers:
+            _close(bf16_f32(cache.kv.logical_keys(cache.slot[li], P)), oc.layers[li][0], f"prefill keys {li}")
+    st = eng.stream_handle()
+    tree = make_tree(root_token=prefix[-1] if P else 0, vocab=cfg.vocab_size, seed=2)
+
+    def argmax_at(tr):
+        eng.set_step(tr.tokens, tr.positions(P), tr.parents, P)
+        eng.launch_forward(cache, st)
+        eng.launch_lm_head(st)
+        eng.launch_walk(st)
+        return eng.read_result().posterior
+
+    path = acceptance_rewrite(tree, argmax_at, p=0.85, seed=3)
+    L = tree.size
+    log(f"setup {time.time() - t0:.1f}s  L={L} path={path}")
+
+    # dry forward: logits + tree K/V rows before compaction
+    eng.set_step(tree.tokens, tree.positions(P), tree.parents, P)
+    eng.launch_forward(cache, st)
+    eng.launch_lm_head(st, want_logits=True)
+    torch.cuda.synchronize()
+    logits = eng.logits[:L].cpu().numpy()
+    nA = len(cfg.attention_layers)
+    tree_k = [bf16_f32(cache.kv.logical_keys(a, P + L))[P:] for a in range(nA)]
+    tree_v = [bf16_f32(cache.kv.logical_values(a, P + L))[P:] for a in range(nA)]
+    hidden = bf16_f32(eng.hidden[:L]) if layer_ids else None
+    oc = _oracle_cache(cfg, cache, P)
+
+    # the real step: graph replay of forward + argmax + walk + compaction + commit
+    res = eng.verify(cache, tree.tokens, tree.positions(P), tree.parents, use_graph=True)
+    torch.cuda.synchronize()
+
+    t1 = time.time()
+    norm, vh, pend = orc.forward_tree(np.asarray(tree.tokens), np.asarray(tree.positions(P)), tree.parents, oc,
+                                      layer_ids)
+    E = w.host_accessor()(None, "embed")
+    ref = np.concatenate([norm @ bf16_to_f32(E[s:s + 16384]).T for s in range(0, E.shape[0], 16384)], axis=1)
+    log(f"oracle {time.time() - t1:.1f}s")
+    return dict(cfg=cfg, eng=eng, cache=cache, tree=tree, res=res, logits=logits, ref=ref, tree_k=tree_k,
+                tree_v=tree_v, hidden=hidden, vh=vh, P=P, L=L, orc=orc, oc=oc, pend=pend)
+
+
+def _check(r, layer_ids):
+    cfg, L, P = r["cfg"], r["L"], r["P"]
+    logits, ref, res, tree = r["logits"], r["ref"], r["res"], r["tree"]
+    scale = np.abs(ref).max(axis=-1)
+    err = np.abs(logits - ref).max(axis=-1)
+    assert np.all(err <= TOL * scale), f"logit rel err {float((err / scale).max()):.4f}"
+    srt = np.sort(ref, axis=-1)
+    confident = srt[:, -1] - srt[:, -2] > TOL * scale
+    o_post = np.argmax(ref, axis=-1)
+    post = np.array(res.posterior)
+    assert np.array_equal(post[confident], o_post[confident])
+    assert confident.mean() > 0.5
+    o_acc, o_bonus = otree.follow_verified_tree(tree.child_maps, o_post.tolist())
+    if all(confident[i] for i in o_acc):
+        assert res.accepted == o_acc and res.bonus_token == o_bonus
+    acc2, bonus2 = otree.follow_verified_tree(tree.child_maps, res.posterior)
+    assert res.accepted == acc2 and res.bonus_token == bonus2
+    cache, n = r["cache"], len(res.accepted)
+    assert cache.offset == P + n
+    # attention layers: compaction is a bit-exact gather; tree rows match the oracle
+    for a, li in enumerate(cfg.attention_layers):
+        kc = bf16_f32(cache.kv.logical_keys(a, P + n))[P:]
+        vc = bf16_f32(cache.kv.logical_values(a, P + n))[P:]
+        np.testing.assert_array_equal(kc, r["tree_k"][a][res.accepted])
+        np.testing.assert_array_equal(vc, r["tree_v"][a][res.accepted])
+        _close(r["tree_k"][a], r["pend"][li]["k"], f"tree keys {li}")
+        _close(r["tree_v"][a], r["pend"][li]["v"], f"tree values {li}")
+    # GatedDeltaNet layers: window / state = the oracle's commit along the same path
+    orc, oc = r["orc"], r["oc"]
+    orc.commit(oc, r["pend"], tree.parents, res.accepted)
+    for li in cfg.linear_layers:
+        s = cache.slot[li]
+        _close(cache.windows[s].cpu().numpy(), oc.layers[li][0], f"window {li}")
+        _close(cache.states[s].cpu().numpy(), oc.layers[li][1], f"state {li}")
+    if layer_ids:
+        hs = bf16_f32(r["eng"].hidden_sel[:n])
+        want = r["vh"][res.accepted]
+        assert np.abs(hs - want).max() <= TOL * np.abs(want).max()
+        assert np.abs(r["hidden"] - r["vh"]).max() <= TOL * np.abs(r["vh"]).max()
+    return res
+
+
+def test_qwen35_verify_step_tiny_model(gpu_device):
+    cfg = tiny_qwen35()
+    r = _run(cfg, P=100, layer_ids=[1, 3], dev=gpu_device, check_prefill=True)
+    res = _check(r, [1, 3])
+    assert len(res.accepted) >= 1
+
+
+def test_qwen35_verify_step_tiny_model_q4(gpu_device):
+    cfg = tiny_qwen35()
+    r = _run(cfg, P=70, layer_ids=[2], dev=gpu_device, quant="q4")
+    _check(r, [2])
+
+
+def test_qwen35_two_steps_graph_matches_eager(gpu_device):
+    """Two consecutive verify steps through the captured graph leave the same
+    committed state as the same steps launched eagerly."""
+    cfg = tiny_qwen35()
+    w = Qwen35Weights.random(cfg, seed=5, device=gpu_device, norm_jitter=0.1)
+    out = []
+    for use_graph in (True, False):
+        eng = Qwen35TreeEngine(cfg, w, max_past=128)
+        cache = eng.new_cache()
+        eng.prefill(cache, random_prefix(40, cfg.vocab_size, seed=6))
+        res = []
+        for step in range(2):
+            tree = make_tree(root_token=7 + step, vocab=cfg.vocab_size, seed=10 + step)
+            r = eng.verify(cache, tree.tokens, tree.positions(cache.offset), tree.parents, use_graph=use_graph)
+            res.append((r.accepted, r.bonus_token))
+        torch.cuda.synchronize()
+        out.append((res, cache.windows.cpu(), cache.states.cpu(), cache.offset))
+        eng.release_graphs()
+    assert out[0][0] == out[1][0] and out[0][3] == out[1][3]
+    assert torch.equal(out[0][1], out[1][1]) and torch.equal(out[0][2], out[1][2])
+
+
+def test_qwen35_4b_verify_step_prefix_2048(gpu_device):
+    """Qwen3.5-4B-shaped hybrid at a 2048-token prefix with a 24-node tree."""
+    r = _run(QWEN35_4B, P=2048, layer_ids=[1, 15, 30], dev=gpu_device, norm_jitter=0.0)
+    _check(r, [1, 15, 30])

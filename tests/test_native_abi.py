@@ -69,3 +69,38 @@ def test_workspace_queries():
     # 4-chunk workgroup; prefix 1024 = tree + 16 pages = 5 workgroups per head
     assert lib.dtree_attention_workspace_bytes(32, 128, 1024) == 256 + 32 * 5 * (32 * 128 + 64) * 4
     assert lib.dtree_attention_workspace_bytes(32, 128, 0) == 256 + 32 * 1 * (32 * 128 + 64) * 4
+    # head_dim 256 runs 32-key chunks: prefix 2048 = tree + 64 chunks = 17 workgroups per head
+    assert lib.dtree_attention_workspace_bytes(16, 256, 2048) == 256 + 16 * 17 * (32 * 256 + 64) * 4
+
+
+def test_struct_sizes_match_the_library():
+    lib = N.lib()
+    assert lib.dtree_gemm_args_bytes() == C.sizeof(N.GemmArgs)
+    assert lib.dtree_attn_args_bytes() == C.sizeof(N.AttnArgs)
+    assert lib.dtree_gdn_args_bytes() == C.sizeof(N.GdnArgs)
+
+
+def test_attention_and_gdn_layer_validation_without_gpu():
+    lib = N.lib()
+    att = N.AttnArgs()
+    for f in ("qkv", "rope_cos", "rope_sin", "k_pages", "v_pages", "page_table", "desc", "out", "workspace"):
+        setattr(att, f, 256)
+    att.num_heads, att.num_kv_heads, att.rows_padded = 16, 4, 32
+    att.head_dim, att.rope_dims, att.gated = 256, 256, 0  # head_dim 256 is compiled gated with rope_dims 64 only
+    assert lib.dtree_tree_attention(C.byref(att), None) == -1
+    assert b"geometries" in lib.dtree_last_error()
+    att.rope_dims, att.gated, att.ld_qkv = 64, 1, 16 * 512  # k / v columns missing
+    assert lib.dtree_tree_attention(C.byref(att), None) == -1
+    assert b"ld_qkv" in lib.dtree_last_error()
+    g = N.GdnArgs()
+    assert lib.dtree_gdn_layer_prep(C.byref(g), None) == -1
+    g.desc, g.rows_padded, g.num_k_heads, g.num_v_heads, g.conv_keep = 256, 32, 16, 32, 3
+    g.head_k_dim, g.head_v_dim = 64, 128
+    assert lib.dtree_gdn_layer_recurrence(C.byref(g), None) == -1
+    assert b"head dims" in lib.dtree_last_error()
+    g.head_k_dim = 128
+    for f in ("proj", "window", "conv_w", "A_log", "dt_bias", "q", "k", "v", "g", "beta"):
+        setattr(g, f, 256)
+    g.ld_proj = 8192 + 4096  # b and a columns missing
+    assert lib.dtree_gdn_layer_prep(C.byref(g), None) == -1
+    assert b"ld_proj" in lib.dtree_last_error()
