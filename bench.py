@@ -8,6 +8,12 @@ compaction, replayed as one HIP graph. Inputs (weights, KV prefix, tree) are
 resident in HBM before timing; each timed step uploads the 4.6 KB step
 descriptor, replays the graph and reads the walk result back.
 
+--model qwen35-4b runs the Qwen3.5-4B-shaped hybrid instead (32 layers: 24
+GatedDeltaNet + 8 gated attention, hidden 2560, prefix 2048 by default):
+GatedDeltaNet tree recurrence from the committed fp32 state, gated
+head_dim-256 tree attention, LM-head argmax, walk, KV compaction and the
+GatedDeltaNet commit along the accepted path, as one HIP graph.
+
 Prints ONE JSON line (rank 0). Progress goes to stderr.
 """
 from __future__ import annotations
@@ -172,7 +178,7 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
     out["qkv_gemm"] = entry(f"sk_gemm_kernel<true, 0, {q4}>", nl, us["qkv"], b["qkv"])
-    out["attention"] = entry("tree_attn_kernel<128>", nl, us["attention"], b["attention"])
+    out["attention"] = entry("tree_attn_kernel<128, 128, false>", nl, us["attention"], b["attention"])
     # o_proj and down_proj share one instantiation (residual epilogue): its
     # average launch is the mean of the two shapes, as the profiler reports.
     out["residual_gemm"] = entry(f"sk_gemm_kernel<true, 1, {q4}>", 2 * nl, (us["o"] + us["down"]) / 2,
@@ -181,6 +187,207 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
     out["lm_head"] = entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"])
     out["residual_gemm"]["shapes_us"] = {"o_proj": us["o"], "down_proj": us["down"]}
     return out
+
+
+def algorithmic_bytes35(cfg, P: int, L: int, quant: str = "bf16") -> dict:
+    """Minimum HBM bytes of one hybrid verify step: every weight once, the KV
+    prefix of the attention layers, the committed GatedDeltaNet windows and
+    states read and the committed ones written, tree KV rows written."""
+    H, F, V, D = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.head_dim
+    nG, nA = len(cfg.linear_layers), len(cfg.attention_layers)
+    Hv = cfg.linear_num_value_heads
+    gdn_params = (cfg.conv_dim + cfg.value_dim + 2 * Hv) * H + H * cfg.value_dim
+    attn_params = cfg.attn_qkv_dim * H + H * cfg.q_dim
+    mlp_params = 3 * H * F
+    lin = weight_bytes(nG * gdn_params + nA * attn_params + cfg.num_hidden_layers * mlp_params, quant)
+    small = nG * (cfg.linear_conv_kernel_dim * cfg.conv_dim * 4 + 2 * Hv * 4 + cfg.linear_value_head_dim * 2)
+    lm = weight_bytes(V * H, quant)
+    norms = (cfg.num_hidden_layers * 2 * H + nA * 2 * D + H) * 2
+    emb = weight_bytes(L * H, quant)
+    kv_read = nA * 2 * cfg.num_key_value_heads * P * D * 2
+    kv_write = nA * 2 * cfg.num_key_value_heads * L * D * 2
+    state = nG * (Hv * cfg.linear_value_head_dim * cfg.linear_key_head_dim
+                  + (cfg.linear_conv_kernel_dim - 1) * cfg.conv_dim) * 4
+    total = lin + small + lm + norms + emb + kv_read + kv_write + 2 * state
+    return dict(linear=lin, gdn_small=small, lm_head=lm, norms=norms, embed_rows=emb, kv_prefix_read=kv_read,
+                tree_kv_write=kv_write, gdn_state_read=state, gdn_state_write=state, total=total)
+
+
+def cpu_baseline35(cfg, weights, cache, tree, P, min_seconds=15.0):
+    """The oracle (fp32 numpy, GatedDeltaNet recurrence in fp64) of the same
+    hybrid step on the host cores, on a bounded sample: the first
+    GatedDeltaNet layer and the first attention layer (repeated), and a
+    quarter of the LM head, scaled linearly to the whole step."""
+    import numpy as np
+
+    from oracle import qwen35 as o35
+    from oracle.qwen3 import bf16_to_f32, rms_norm
+
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        cores = os.cpu_count() or 1
+    ocfg = o35.Qwen35Config(
+        hidden=cfg.hidden_size, layers=cfg.num_hidden_layers, ffn=cfg.intermediate_size,
+        heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+        rope_dims=cfg.rope_dims, lin_k_heads=cfg.linear_num_key_heads, lin_v_heads=cfg.linear_num_value_heads,
+        lin_k_dim=cfg.linear_key_head_dim, lin_v_dim=cfg.linear_value_head_dim,
+        conv_kernel=cfg.linear_conv_kernel_dim, full_attention_interval=cfg.full_attention_interval,
+        vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_base=cfg.rope_theta)
+    acc = weights.host_accessor()
+    lg, la = cfg.linear_layers[0], cfg.attention_layers[0]
+    gdn_names = ("input_norm", "in_qkv", "in_z", "in_b", "in_a", "conv", "A_log", "dt_bias", "gnorm", "out",
+                 "post_norm", "gate", "up", "down")
+    attn_names = ("input_norm", "q", "k", "v", "q_norm", "k_norm", "o", "post_norm", "gate", "up", "down")
+    W = {(lg, n): np.asarray(acc(lg, n)) for n in gdn_names}
+    W.update({(la, n): np.asarray(acc(la, n)) for n in attn_names})
+    orc = o35.OracleQwen35(ocfg, lambda li, n: W[(li, n)])
+    s = cache.slot
+    win = cache.windows[s[lg]].cpu().numpy()
+    state = cache.states[s[lg]].cpu().double().numpy()
+    kp = cache.kv.logical_keys(s[la], P).float().cpu().numpy()
+    vp = cache.kv.logical_values(s[la], P).float().cpu().numpy()
+    pos = np.asarray(tree.positions(P))
+    mask = o35.tree_mask(tree.parents, P)
+    x0 = bf16_to_f32(acc(None, "embed")[np.asarray(tree.tokens)])
+    tg, ta = [], []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        x, _ = orc.gdn_layer(lg, x0, win, state, tree.parents)
+        t1 = time.perf_counter()
+        x, _ = orc.attn_layer(la, x, kp, vp, pos, mask)
+        t2 = time.perf_counter()
+        tg.append(t1 - t0)
+        ta.append(t2 - t1)
+        if time.perf_counter() - t_start > min_seconds or len(tg) >= 200:
+            break
+    E = acc(None, "embed")
+    q = E.shape[0] // 4
+    Eq = bf16_to_f32(E[:q])
+    h = rms_norm(x, np.ones(cfg.hidden_size, np.float32), cfg.rms_norm_eps)
+    lm_t = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        np.argmax(h @ Eq.T, axis=-1)
+        lm_t.append(time.perf_counter() - t0)
+    t_g, t_a = float(np.median(tg)), float(np.median(ta))
+    t_step = (t_g * len(cfg.linear_layers) + t_a * len(cfg.attention_layers)
+              + float(np.median(lm_t)) * (E.shape[0] / q))
+    return {"value": 1.0 / t_step, "unit": "steps/s", "cores": int(cores), "kind": "port",
+            "sample": (f"oracle: 1 GatedDeltaNet + 1 attention layer x {len(tg)} passes (median "
+                       f"{t_g * 1e3:.1f} / {t_a * 1e3:.1f} ms) + 1/4 of the LM head, scaled linearly to one "
+                       f"step ({t_step:.2f} s)")}
+
+
+def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str = "bf16") -> dict:
+    """Average launch duration of every kernel class of the hybrid step (HIP
+    events on the launch stream), rotating over the layers of that class so
+    each launch streams its own weights. Runs after the timed region (the
+    residual GEMMs keep adding into the residual stream)."""
+    import ctypes as C
+
+    import torch
+
+    from dtree_hip import _native as N
+
+    H, F, V, D = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.head_dim
+    lib = eng.lib
+    gemm = lib.dtree_gemm_bf16
+    G, A = cfg.linear_layers, cfg.attention_layers
+    args = {"in": [], "out": [], "gdn": [], "qkv": [], "o": [], "gu": [], "down": []}
+    for li in G:
+        lw = w.layers[li]
+        gi = cache.slot[li]
+        args["in"].append(eng.gemm_args("in", eng.xg, H, lw.w_in, N.EPI_STORE_F32, ss_in=eng.ss,
+                                        out_f32=eng.proj[gi]))
+        args["out"].append(eng.gemm_args("out", eng.gout, cfg.value_dim, lw.w_out, N.EPI_RESIDUAL, out_f32=eng.x,
+                                         out_bf16=eng.xg, next_norm=lw.post_norm, ss_out=eng.ss))
+        args["gdn"].append(eng.gdn_args(li, cache))
+    for li in A:
+        lw = w.layers[li]
+        args["qkv"].append(eng.gemm_args("qkv", eng.xg, H, lw.wqkv, N.EPI_STORE_F32, ss_in=eng.ss,
+                                         out_f32=eng.qkv))
+        args["o"].append(eng.gemm_args("o", eng.attn, cfg.q_dim, lw.wo, N.EPI_RESIDUAL, out_f32=eng.x,
+                                       out_bf16=eng.xg, next_norm=lw.post_norm, ss_out=eng.ss))
+    for li in range(cfg.num_hidden_layers):
+        lw = w.layers[li]
+        nxt = w.layers[li + 1].input_norm if li + 1 < cfg.num_hidden_layers else w.final_norm
+        args["gu"].append(eng.gemm_args("gu", eng.xg, H, lw.wgu, N.EPI_SWIGLU, ss_in=eng.ss, out_bf16=eng.act))
+        args["down"].append(eng.gemm_args("down", eng.act, F, lw.wd, N.EPI_RESIDUAL, out_f32=eng.x,
+                                          out_bf16=eng.xg, next_norm=nxt, ss_out=eng.ss))
+    refs = {k: [C.byref(a) for a in v] for k, v in args.items()}
+
+    def timed(launch, n) -> float:
+        for r in range(n):
+            launch(r)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for r in range(reps):
+            launch(r % n)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    us = {k: timed(lambda r, k=k: gemm(refs[k][r], st), len(refs[k])) for k in ("in", "out", "qkv", "o", "gu",
+                                                                                   "down")}
+    g = refs["gdn"]
+    us["prep"] = timed(lambda r: lib.dtree_gdn_layer_prep(g[r], st), len(g))
+    us["recurrence"] = timed(lambda r: lib.dtree_gdn_layer_recurrence(g[r], st), len(g))
+    us["gated_norm"] = timed(lambda r: lib.dtree_gdn_layer_gated_norm(g[r], st), len(g))
+    us["commit"] = timed(lambda r: lib.dtree_gdn_layer_commit(g[r], st), len(g))
+    us["attention"] = timed(lambda r: eng._attention(A[r], cache, st), len(A))
+    us["lm_head"] = timed(lambda r: eng.launch_lm_head(st), 1)
+
+    wb = lambda params: weight_bytes(params, quant)  # noqa: E731
+    Hv, Dk, Dv = cfg.linear_num_value_heads, cfg.linear_key_head_dim, cfg.linear_value_head_dim
+    C_ = cfg.conv_dim
+    state_b = Hv * Dv * Dk * 4
+    b = {
+        "in": wb(cfg.in_proj_dim * H) + L * H * 2 + L * cfg.in_proj_dim * 4,
+        "out": wb(H * cfg.value_dim) + L * cfg.value_dim * 2 + L * H * 2,
+        "qkv": wb(cfg.attn_qkv_dim * H) + L * H * 2 + L * cfg.attn_qkv_dim * 4,
+        "o": wb(H * cfg.q_dim) + L * cfg.q_dim * 2 + L * H * 2,
+        "gu": wb(2 * F * H) + L * H * 2 + L * F * 2,
+        "down": wb(H * F) + L * F * 2 + L * H * 2,
+        "prep": L * (C_ + 2 * Hv) * 4 + cfg.linear_conv_kernel_dim * C_ * 4 + L * (C_ + 2 * Hv) * 4,
+        "recurrence": state_b + L * (2 * cfg.key_dim + cfg.value_dim + 2 * Hv) * 4 + L * cfg.value_dim * 4,
+        "gated_norm": 2 * L * cfg.value_dim * 4 + L * cfg.value_dim * 2,
+        "commit": 2 * state_b,
+        "attention": 2 * cfg.num_key_value_heads * P * D * 2 + 2 * cfg.num_key_value_heads * L * D * 2
+        + L * cfg.attn_qkv_dim * 4 + L * cfg.q_dim * 2,
+        "lm_head": wb(V * H) + L * H * 2,
+    }
+    q4 = "true" if quant == "q4" else "false"
+    nG, nA, nL = len(G), len(A), cfg.num_hidden_layers
+
+    def entry(kernel, n, t_us, nbytes):
+        return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
+                "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
+
+    # GEMMs of one epilogue share an instantiation: the profiler averages their shapes.
+    f32_n = nG + nA
+    res_n = nG + nA + nL
+    out = {
+        "store_f32_gemm": entry(f"sk_gemm_kernel<true, 0, {q4}>", f32_n, (nG * us["in"] + nA * us["qkv"]) / f32_n,
+                                (nG * b["in"] + nA * b["qkv"]) / f32_n),
+        "residual_gemm": entry(f"sk_gemm_kernel<true, 1, {q4}>", res_n,
+                               (nG * us["out"] + nA * us["o"] + nL * us["down"]) / res_n,
+                               (nG * b["out"] + nA * b["o"] + nL * b["down"]) / res_n),
+        "gate_up_gemm": entry(f"sk_gemm_kernel<true, 2, {q4}>", nL, us["gu"], b["gu"]),
+        "gdn_prep": entry("gdn_prep_kernel<3, 128>", nG, us["prep"], b["prep"]),
+        "gdn_recurrence": entry("gdn_tree_reg_kernel<32>", nG, us["recurrence"], b["recurrence"]),
+        "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
+        "gdn_commit": entry("gdn_commit_kernel<128>", nG, us["commit"], b["commit"]),
+        "attention": entry("tree_attn_kernel<256, 64, true>", nA, us["attention"], b["attention"]),
+        "lm_head": entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"]),
+    }
+    out["store_f32_gemm"]["shapes_us"] = {"in_proj": us["in"], "attn_qkv": us["qkv"]}
+    out["residual_gemm"]["shapes_us"] = {"out_proj": us["out"], "o_proj": us["o"], "down_proj": us["down"]}
+    return out
+
 
 
 def copy_probe(mib: int) -> None:
@@ -203,7 +410,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--prefix", type=int, default=1024)
+    ap.add_argument("--model", choices=["qwen3-4b", "qwen35-4b"], default="qwen3-4b",
+                    help="qwen35-4b: the Qwen3.5-4B-shaped GatedDeltaNet / attention hybrid")
+    ap.add_argument("--prefix", type=int, default=None, help="prefix tokens (default 1024; 2048 for qwen35-4b)")
     ap.add_argument("--budget", type=int, default=24)
     ap.add_argument("--quant", choices=["bf16", "q4"], default="bf16",
                     help="q4: every linear layer and the tied LM head in 4-bit affine groups of 64")
@@ -223,21 +432,24 @@ def main():
 
     import torch
 
-    from dtree_hip import Qwen3TreeModel, Qwen3Weights
-    from dtree_hip import _native as N
-    from dtree_hip.config import QWEN3_4B
+    from dtree_hip import Qwen35TreeEngine, Qwen35Weights, Qwen3TreeModel, Qwen3Weights
+    from dtree_hip.config import QWEN3_4B, QWEN35_4B
     from dtree_hip.synthetic import acceptance_rewrite, make_tree, random_prefix
 
     dev = torch.device("cuda:0")
-    cfg = QWEN3_4B
-    P = a.prefix
+    hybrid = a.model == "qwen35-4b"
+    cfg = QWEN35_4B if hybrid else QWEN3_4B
+    P = a.prefix if a.prefix is not None else (2048 if hybrid else 1024)
     t0 = time.time()
-    if a.quant == "q4":
-        w = Qwen3Weights.random_q4(cfg, seed=0, device=dev)
+    if hybrid:
+        w = Qwen35Weights.random(cfg, seed=0, device=dev, quant=a.quant)
+        eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 30])
     else:
-        w = Qwen3Weights.random(cfg, seed=0, device=dev)
-    model = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33])
-    eng = model.engine
+        if a.quant == "q4":
+            w = Qwen3Weights.random_q4(cfg, seed=0, device=dev)
+        else:
+            w = Qwen3Weights.random(cfg, seed=0, device=dev)
+        eng = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33]).engine
     cache = eng.new_cache()
     prefix = random_prefix(P, cfg.vocab_size, seed=1)
     eng.prefill(cache, prefix)
@@ -273,18 +485,19 @@ def main():
     elapsed = time.perf_counter() - t_start
     ms = elapsed / a.steps * 1e3
     steps_per_s = a.steps / elapsed
-    ab = algorithmic_bytes(cfg, P, L, a.quant)
+    ab = algorithmic_bytes35(cfg, P, L, a.quant) if hybrid else algorithmic_bytes(cfg, P, L, a.quant)
     gbps = ab["total"] / (ms * 1e-3) / 1e9
     log(f"[bench] {ms:.3f} ms/step  {steps_per_s:.1f} steps/s  {gbps:.0f} GB/s")
 
-    kernels = time_kernels(eng, cfg, w, cache, st, P, L, a.kernel_reps, a.quant)
+    kernels = (time_kernels35 if hybrid else time_kernels)(eng, cfg, w, cache, st, P, L, a.kernel_reps, a.quant)
     for name, kd in kernels.items():
         log(f"[bench] {name:10s} {kd['avg_launch_us']:7.1f} us/launch x {kd['launches_per_step']:2d}  "
             f"{kd['achieved_gbps']:6.0f} GB/s  ({kd['kernel']})")
     dom = max(kernels, key=lambda k: kernels[k]["avg_launch_us"] * kernels[k]["launches_per_step"])
     kd = kernels[dom]
     traffic = None
-    tf = ROOT / "profiles" / (f"{dom}_traffic.json" if a.quant == "bf16" else f"{dom}_q4_traffic.json")
+    tag = ("_qwen35" if hybrid else "") + ("_q4" if a.quant == "q4" else "")
+    tf = ROOT / "profiles" / f"{dom}{tag}_traffic.json"
     if tf.exists():
         try:
             traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
@@ -294,13 +507,19 @@ def main():
     cpu = None
     if not a.no_cpu_baseline:
         t0 = time.time()
-        cpu = cpu_baseline(cfg, w, cache, tree, P)
+        cpu = (cpu_baseline35 if hybrid else cpu_baseline)(cfg, w, cache, tree, P)
         log(f"[bench] cpu baseline {cpu['value']:.3f} steps/s ({time.time() - t0:.1f}s)")
 
     mean_acc = sum(accepted_lens) / len(accepted_lens)
+    model_name = "Qwen3.5-4B-shaped hybrid" if hybrid else "Qwen3-4B"
+    qname = "bf16" if a.quant == "bf16" else "q4 group-64"
+    if hybrid:
+        workload = (f"{model_name} {qname} tree-verify step (24 GatedDeltaNet + 8 gated attention layers, "
+                    "LM-head argmax, walk, KV compaction, GatedDeltaNet commit)")
+    else:
+        workload = f"{model_name} {qname} tree-verify step (36 layers, LM-head argmax, walk, compaction)"
     out = {
-        "metric": ("tree-verify steps/s + HBM GB/s (% of peak), 24-node tree, Qwen3-4B bf16" if a.quant == "bf16"
-                   else "tree-verify steps/s + HBM GB/s (% of peak), 24-node tree, Qwen3-4B q4 group-64"),
+        "metric": f"tree-verify steps/s + HBM GB/s (% of peak), 24-node tree, {model_name} {qname}",
         "value": round(steps_per_s, 3),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -315,8 +534,7 @@ def main():
                  if a.quant == "bf16" else
                  "synthetic: q4 nibbles uniform 0..15, scales |N(0,0.02)|*8, biases N(0,0.01), uniform prefix ids, "
                  "seeded Gumbel draft tree"),
-        "config": {"workload": (f"Qwen3-4B-shaped {'bf16' if a.quant == 'bf16' else 'q4 group-64'} tree-verify step "
-                                "(36 layers, LM-head argmax, walk, compaction)"),
+        "config": {"workload": workload,
                    "prefix": P, "tree_nodes": L, "draft_budget": a.budget,
                    "layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size, "vocab": cfg.vocab_size},
         "hbm_gbps": round(gbps, 1),

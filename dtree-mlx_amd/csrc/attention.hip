@@ -483,21 +483,41 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     if (!s_last) return;
     if (t == 0) reset_counter(&p.counters[hq]);
 
+    // Partials are read kSb splits at a time (all loads of a batch in flight
+    // together) with a running max: one memory round trip per batch instead
+    // of two per split.
+    constexpr int kSb = 128 / kDims;  // 8 splits per batch at head_dim 128, 4 at 256
     const float* base = p.part + (size_t)hq * p.splits * stride;
     float Ms = kNeg;
-    for (int s = 0; s < nsplit; ++s) Ms = fmaxf(Ms, ld_coherent(base + s * stride + 32 * D + q));
 #pragma unroll
     for (int i = 0; i < kDims; ++i) acc[i] = 0.f;
     tot = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* ps = base + s * stride;
-      float v[kDims];
+    for (int s0 = 0; s0 < nsplit; s0 += kSb) {
+      float v[kSb][kDims], mm[kSb], ll[kSb];
 #pragma unroll
-      for (int i = 0; i < kDims; ++i) v[i] = ld_coherent(ps + (size_t)i * 64 * kWaves + t);
-      const float w = fast_exp2(ld_coherent(ps + 32 * D + q) - Ms);
-      tot += w * ld_coherent(ps + 32 * D + 32 + q);
+      for (int b = 0; b < kSb; ++b) {
+        const bool ok = s0 + b < nsplit;
+        const float* ps = base + (size_t)(ok ? s0 + b : 0) * stride;
+        mm[b] = ok ? ld_coherent(ps + 32 * D + q) : kNeg;
+        ll[b] = ok ? ld_coherent(ps + 32 * D + 32 + q) : 0.f;
 #pragma unroll
-      for (int i = 0; i < kDims; ++i) acc[i] += w * v[i];
+        for (int i = 0; i < kDims; ++i) v[b][i] = ok ? ld_coherent(ps + (size_t)i * 64 * kWaves + t) : 0.f;
+      }
+      float gm = Ms;
+#pragma unroll
+      for (int b = 0; b < kSb; ++b) gm = fmaxf(gm, mm[b]);
+      const float r = fast_exp2(Ms - gm);
+      tot *= r;
+#pragma unroll
+      for (int i = 0; i < kDims; ++i) acc[i] *= r;
+#pragma unroll
+      for (int b = 0; b < kSb; ++b) {
+        const float w = fast_exp2(mm[b] - gm);
+        tot += w * ll[b];
+#pragma unroll
+        for (int i = 0; i < kDims; ++i) acc[i] += w * v[b][i];
+      }
+      Ms = gm;
     }
   }
 

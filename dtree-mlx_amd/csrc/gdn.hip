@@ -146,6 +146,127 @@ __global__ __launch_bounds__(256) void gdn_tree_kernel(GdnParams p) {
   }
 }
 
+// Sum over the 32 consecutive lanes of a row, three values at once (their
+// steps interleave, so the latency of one reduction covers all three): DPP
+// quad permutes, half-row and row mirrors, then a swizzle across the two
+// 16-lane rows. Every lane of the row ends with the sums.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float swz_xor16(float v) {
+  // bitmask mode: and_mask 0x1F, or_mask 0, xor_mask 0x10 (groups of 32 lanes)
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float row_sum32(float a) {
+  a += dpp<0xB1>(a);
+  a += dpp<0x4E>(a);
+  a += dpp<0x141>(a);
+  a += dpp<0x140>(a);
+  return a + swz_xor16(a);
+}
+
+__device__ __forceinline__ void row_sum32x3(float& a, float& b, float& c) {
+  a += dpp<0xB1>(a); b += dpp<0xB1>(b); c += dpp<0xB1>(c);     // lane ^ 1
+  a += dpp<0x4E>(a); b += dpp<0x4E>(b); c += dpp<0x4E>(c);     // lane ^ 2
+  a += dpp<0x141>(a); b += dpp<0x141>(b); c += dpp<0x141>(c);  // half-row mirror: other quad
+  a += dpp<0x140>(a); b += dpp<0x140>(b); c += dpp<0x140>(c);  // row mirror: other 8 lanes
+  a += swz_xor16(a); b += swz_xor16(b); c += swz_xor16(c);     // other 16-lane row
+}
+
+template <int TMAX>
+struct RegTree {
+  const GdnParams& p;
+  const float* qk;   // [TMAX][2][128]
+  const float* vgb;  // [TMAX][8 + 2]
+  const int* par;
+  int T, h, dv, rl, lane;
+  f32x4_t base;
+};
+
+// Node t of the register-resident recurrence. The recursion unrolls the node
+// loop in the source, so every index into s[] is a constant and the node
+// states stay in registers.
+template <int TMAX, int t>
+__device__ __forceinline__ void reg_tree_step(const RegTree<TMAX>& r, f32x4_t (&s)[TMAX]) {
+  if constexpr (t < TMAX) {
+    if (t >= r.T) return;
+    const int pa = __builtin_amdgcn_readfirstlane(r.par[t]);
+    f32x4_t sp = r.base;
+#pragma unroll
+    for (int j = 0; j < t; ++j) sp = pa == j ? s[j] : sp;
+    const f32x4_t kk = *reinterpret_cast<const f32x4_t*>(r.qk + (t * 2 + 1) * 128 + 4 * r.lane);
+    const f32x4_t qq = *reinterpret_cast<const f32x4_t*>(r.qk + (t * 2) * 128 + 4 * r.lane);
+    float sk = sp[0] * kk[0] + sp[1] * kk[1] + sp[2] * kk[2] + sp[3] * kk[3];
+    float sq = sp[0] * qq[0] + sp[1] * qq[1] + sp[2] * qq[2] + sp[3] * qq[3];
+    float kq = kk[0] * qq[0] + kk[1] * qq[1] + kk[2] * qq[2] + kk[3] * qq[3];
+    row_sum32x3(sk, sq, kq);
+    const float* vt = r.vgb + t * 10;
+    const float g = vt[8], b = vt[9];
+    const float delta = (vt[r.rl] - g * sk) * b;
+    s[t] = sp * g + kk * delta;
+    const GdnParams& p = r.p;
+    if (r.lane == 0) p.y[((size_t)t * p.Hv + r.h) * p.Dv + r.dv] = g * sq + delta * kq;
+    if (p.states)
+      *reinterpret_cast<f32x4_t*>(p.states + (((size_t)t * p.Hv + r.h) * p.Dv + r.dv) * 128 + 4 * r.lane) = s[t];
+    reg_tree_step<TMAX, t + 1>(r, s);
+  }
+}
+
+// Tree recurrence for trees of up to TMAX nodes with Dk = 128: a workgroup
+// owns one value head and 8 state rows (32 lanes x 4 elements per row), and
+// every node's state of those elements stays in registers (4 x TMAX), so LDS
+// holds only the node inputs and all workgroups of a launch are resident at
+// once. The parent's state is picked by a select chain on the wave-uniform
+// parent index. Per node one reduction yields S_p k, S_p q and k q:
+// kv = g (S_p k), delta = (v - kv) beta, y = g (S_p q) + delta (k q), and
+// S = g S_p + delta k, which equals the reference order of operations
+// (S = g S_p; S += delta k; y = S q) up to rounding.
+template <int TMAX>
+__global__ __launch_bounds__(256) void gdn_tree_reg_kernel(GdnParams p) {
+  constexpr int DK = 128, RPW = 8, NV = TMAX * 2 * DK / 4 / 256;  // staged f32x4 per thread
+  __shared__ __align__(16) float qk[TMAX][2][DK];
+  __shared__ float vgb[TMAX][RPW + 2];
+  __shared__ int par[TMAX];
+  const int T = p.T_dev ? min(max(*p.T_dev, 0), min(p.T, TMAX)) : min(p.T, TMAX);
+  const int nslices = p.Dv / RPW;
+  const int h = blockIdx.x / nslices, row0 = (blockIdx.x % nslices) * RPW;
+  const int hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x;
+  {
+    f32x4_t buf[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = tid + 256 * i, t = e >> 6, r = e & 63;  // r < 32: q, else k
+      if (t < T) {
+        const float* src = (r < 32 ? p.q : p.k) + ((size_t)t * p.Hk + hk) * DK + 4 * (r & 31);
+        buf[i] = *reinterpret_cast<const f32x4_t*>(src);
+      }
+    }
+    for (int e = tid; e < T * (RPW + 2); e += 256) {
+      const int t = e / (RPW + 2), r = e % (RPW + 2);
+      float val;
+      if (r < RPW) val = p.v[((size_t)t * p.Hv + h) * p.Dv + row0 + r];
+      else if (r == RPW) val = p.g[(size_t)t * p.Hv + h];
+      else val = p.beta[(size_t)t * p.Hv + h];
+      vgb[t][r] = val;
+    }
+    if (tid < T) par[tid] = p.parents[tid];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = tid + 256 * i, t = e >> 6, r = e & 63;
+      if (t < T) *reinterpret_cast<f32x4_t*>(&qk[t][r >> 5][4 * (r & 31)]) = buf[i];
+    }
+  }
+  const int rl = tid >> 5, lane = tid & 31;
+  const int dv = row0 + rl;
+  const f32x4_t base = *reinterpret_cast<const f32x4_t*>(p.state + ((size_t)h * p.Dv + dv) * DK + 4 * lane);
+  __syncthreads();
+  RegTree<TMAX> rt{p, &qk[0][0][0], &vgb[0][0], par, T, h, dv, rl, lane, base};
+  f32x4_t s[TMAX];
+  reg_tree_step<TMAX, 0>(rt, s);
+}
+
 // Path entries index the per-node buffers ([T] rows); an out-of-range entry
 // (a descriptor that no walk filled) is clamped so it can never read past them.
 __device__ __forceinline__ int clamp_node(int t, int T) { return min(max(t, 0), T - 1); }
@@ -183,11 +304,15 @@ __global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const floa
   float* sp = p.state + ((size_t)h * p.Dv + dv) * DK + 4 * lane4;
   f32x4_t s = *reinterpret_cast<const f32x4_t*>(sp);
   for (int i = 0; i < n; ++i) {
+    // The state update needs S k only (y is not replayed).
     const int t = clamp_node(p.path[i], p.T);
     const f32x4_t kk = *reinterpret_cast<const f32x4_t*>(p.k + ((size_t)t * p.Hk + hk) * DK + 4 * lane4);
-    const f32x4_t qq = *reinterpret_cast<const f32x4_t*>(p.q + ((size_t)t * p.Hk + hk) * DK + 4 * lane4);
-    gdn_step<LPR>(s, kk, qq, p.v[((size_t)t * p.Hv + h) * p.Dv + dv], p.g[(size_t)t * p.Hv + h],
-                  p.beta[(size_t)t * p.Hv + h]);
+    const float vv = p.v[((size_t)t * p.Hv + h) * p.Dv + dv];
+    const float gg = p.g[(size_t)t * p.Hv + h], bb = p.beta[(size_t)t * p.Hv + h];
+    s *= gg;
+    float kv = s[0] * kk[0] + s[1] * kk[1] + s[2] * kk[2] + s[3] * kk[3];
+    kv = LPR == 32 ? row_sum32(kv) : row_sum<LPR>(kv);
+    s += kk * ((vv - kv) * bb);
   }
   *reinterpret_cast<f32x4_t*>(sp) = s;
 }
@@ -215,7 +340,7 @@ __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log
 
 template <int KEEP, int DK>
 __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
-  extern __shared__ float ob[];  // [L][DK + 1] conv outputs, then rs[L]
+  extern __shared__ float ob[];  // [rows][DK + 1] conv outputs, rs[rows], then xin [rows][DK]
   __shared__ int par[kGdnMaxNodes];
   const int L = min(max(p.desc->num_nodes, 0), p.rows);
   const int tid = threadIdx.x;
@@ -238,6 +363,17 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
   for (int r = 0; r <= KEEP; ++r) wk[r] = p.w[(size_t)r * p.C + c];
 #pragma unroll
   for (int r = 0; r < KEEP; ++r) bk[r] = p.base[(size_t)r * p.C + c];
+  // This thread's channel of every node's conv input, staged in its own LDS
+  // column with all loads in flight at once (batches of 8).
+  float* xin = ob + p.rows * (DK + 2);
+  for (int t0 = 0; t0 < L; t0 += 8) {
+    float xv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = t0 + i < L ? p.x[(size_t)(t0 + i) * p.ldx + c] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (t0 + i < L) xin[(t0 + i) * DK + tid] = xv[i];
+  }
   for (int t = 0; t < L; ++t) {
     // window of t = last KEEP + 1 rows of (base ++ x along the root path):
     // val[i] is row KEEP - i (val[0] = x[t]).
@@ -246,7 +382,7 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
 #pragma unroll
     for (int i = 0; i <= KEEP; ++i) {
       if (anc >= 0) {
-        val[i] = p.x[(size_t)anc * p.ldx + c];
+        val[i] = xin[anc * DK + tid];
         anc = par[anc];
       } else {
         val[i] = bk[KEEP - 1 - nb];
@@ -259,7 +395,7 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
     ob[t * (DK + 1) + tid] = silu_acc(acc);
   }
   const bool is_q = c0 < p.key_dim, is_k = !is_q && c0 < 2 * p.key_dim;
-  float* rs = ob + p.rows * (DK + 1);
+  float* rs = ob + p.rows * (DK + 1);  // rows floats; xin starts at rows * (DK + 2)
   __syncthreads();
   if (is_q || is_k) {
     // Node t's head; the padded row stride puts consecutive nodes on distinct banks.
@@ -389,6 +525,11 @@ extern "C" int dtree_gdn_tree_recurrence(const float* q, const float* k, const f
   p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.state = const_cast<float*>(state); p.parents = parents;
   p.T = num_nodes; p.Hk = num_k_heads; p.Hv = num_v_heads; p.Dv = head_v_dim; p.rpw = rpw;
   p.y = y; p.states = states;
+  if (head_k_dim == 128 && num_nodes <= 32 && head_v_dim % 8 == 0) {
+    gdn_tree_reg_kernel<32><<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
+    DTREE_LAUNCH_CHECK("gdn_tree_recurrence launch");
+    return DTREE_OK;
+  }
   const int grid = num_v_heads * (head_v_dim / rpw);
   const int threads = rpw * (head_k_dim / 4);
   switch (head_k_dim) {
@@ -460,7 +601,7 @@ extern "C" int dtree_gdn_layer_prep(const DtreeGdnArgs* a, hipStream_t stream) {
   p.q = a->q; p.k = a->k; p.v = a->v; p.g = a->g; p.beta = a->beta;
   p.q_scale = 1.0f / (float)a->head_k_dim;
   p.k_scale = 1.0f / sqrtf((float)a->head_k_dim);
-  const size_t lds = ((size_t)a->rows_padded * (128 + 1) + a->rows_padded) * sizeof(float);
+  const size_t lds = ((size_t)a->rows_padded * (128 + 2) + (size_t)a->rows_padded * 128) * sizeof(float);
   const int grid = C / 128 + 1;
   switch (a->conv_keep) {
 #define DTREE_PREP_CASE(K) \
@@ -484,8 +625,13 @@ extern "C" int dtree_gdn_layer_recurrence(const DtreeGdnArgs* a, hipStream_t str
   p.parents = a->desc->parents; p.T_dev = &a->desc->num_nodes;
   p.T = a->rows_padded; p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->head_v_dim; p.rpw = rpw;
   p.y = a->y; p.states = nullptr;
-  const int grid = a->num_v_heads * (a->head_v_dim / rpw);
-  gdn_tree_kernel<128><<<grid, rpw * (128 / 4), lds, stream>>>(p);
+  if (a->rows_padded <= 32 && a->head_v_dim % 8 == 0) {
+    p.T = min(a->rows_padded, 32);
+    gdn_tree_reg_kernel<32><<<a->num_v_heads * (a->head_v_dim / 8), 256, 0, stream>>>(p);
+  } else {
+    const int grid = a->num_v_heads * (a->head_v_dim / rpw);
+    gdn_tree_kernel<128><<<grid, rpw * (128 / 4), lds, stream>>>(p);
+  }
   DTREE_LAUNCH_CHECK("gdn_layer_recurrence launch");
   return DTREE_OK;
 }
