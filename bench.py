@@ -177,15 +177,12 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    out["qkv_gemm"] = entry(f"sk_gemm_kernel<true, 0, {q4}>", nl, us["qkv"], b["qkv"])
+    out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant), nl, us["qkv"], b["qkv"])
     out["attention"] = entry("tree_attn_kernel<128, 128, false>", nl, us["attention"], b["attention"])
-    # o_proj and down_proj share one instantiation (residual epilogue): its
-    # average launch is the mean of the two shapes, as the profiler reports.
-    out["residual_gemm"] = entry(f"sk_gemm_kernel<true, 1, {q4}>", 2 * nl, (us["o"] + us["down"]) / 2,
-                                 (b["o"] + b["down"]) / 2)
-    out["gate_up_gemm"] = entry(f"sk_gemm_kernel<true, 2, {q4}>", nl, us["gu"], b["gu"])
+    out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant), nl, us["o"], b["o"])
+    out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant), nl, us["down"], b["down"])
+    out["gate_up_gemm"] = entry(gemm_kernel_name(2 * F, H, 2, quant), nl, us["gu"], b["gu"])
     out["lm_head"] = entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"])
-    out["residual_gemm"]["shapes_us"] = {"o_proj": us["o"], "down_proj": us["down"]}
     return out
 
 
@@ -367,16 +364,14 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    # GEMMs of one epilogue share an instantiation: the profiler averages their shapes.
-    f32_n = nG + nA
-    res_n = nG + nA + nL
+    kn = lambda n, k, epi: gemm_kernel_name(n, k, epi, quant)  # noqa: E731
     out = {
-        "store_f32_gemm": entry(f"sk_gemm_kernel<true, 0, {q4}>", f32_n, (nG * us["in"] + nA * us["qkv"]) / f32_n,
-                                (nG * b["in"] + nA * b["qkv"]) / f32_n),
-        "residual_gemm": entry(f"sk_gemm_kernel<true, 1, {q4}>", res_n,
-                               (nG * us["out"] + nA * us["o"] + nL * us["down"]) / res_n,
-                               (nG * b["out"] + nA * b["o"] + nL * b["down"]) / res_n),
-        "gate_up_gemm": entry(f"sk_gemm_kernel<true, 2, {q4}>", nL, us["gu"], b["gu"]),
+        "in_proj_gemm": entry(kn(cfg.in_proj_dim, H, 0), nG, us["in"], b["in"]),
+        "out_proj_gemm": entry(kn(H, cfg.value_dim, 1), nG, us["out"], b["out"]),
+        "attn_qkv_gemm": entry(kn(cfg.attn_qkv_dim, H, 0), nA, us["qkv"], b["qkv"]),
+        "o_gemm": entry(kn(H, cfg.q_dim, 1), nA, us["o"], b["o"]),
+        "gate_up_gemm": entry(kn(2 * F, H, 2), nL, us["gu"], b["gu"]),
+        "down_gemm": entry(kn(H, F, 1), nL, us["down"], b["down"]),
         "gdn_prep": entry("gdn_prep_kernel<3, 128>", nG, us["prep"], b["prep"]),
         "gdn_recurrence": entry("gdn_tree_reg_kernel<32>", nG, us["recurrence"], b["recurrence"]),
         "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
@@ -384,10 +379,17 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "attention": entry("tree_attn_kernel<256, 64, true>", nA, us["attention"], b["attention"]),
         "lm_head": entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"]),
     }
-    out["store_f32_gemm"]["shapes_us"] = {"in_proj": us["in"], "attn_qkv": us["qkv"]}
-    out["residual_gemm"]["shapes_us"] = {"out_proj": us["out"], "o_proj": us["o"], "down_proj": us["down"]}
     return out
 
+
+
+def gemm_kernel_name(n: int, k: int, epi: int, quant: str) -> str:
+    """Kernel the library picks for a 32-row tiled GEMM with split_k 0: one
+    workgroup per 32-column tile for bf16 when K <= 4096 and N <= 12800, the
+    stream-K schedule otherwise (gemm.hip, dtree_gemm_bf16)."""
+    if quant == "bf16" and k <= 4096 and n <= 12800:
+        return f"dp_gemm_kernel<true, {epi}>"
+    return f"sk_gemm_kernel<true, {epi}, {'true' if quant == 'q4' else 'false'}>"
 
 
 def copy_probe(mib: int) -> None:

@@ -219,9 +219,9 @@ __device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, bool norm, 
 // q, k and v are finished one after the other, so at most one raw head row is
 // live in registers (head_dim 256 rows are 128 floats per lane pair).
 template <int D, int R>
-__device__ __forceinline__ void tree_chunk(const AttnParams& p, int hq, int g, int G, int P, int L, int c, int h,
-                                           uint16_t* ks, uint16_t* vt, float& m_run, float& l_run,
-                                           f32x16_t (&o)[D / 32]) {
+__device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& qr, int hq, int g, int G, int P,
+                                           int L, int c, int h, uint16_t* ks, uint16_t* vt, float& m_run,
+                                           float& l_run, f32x16_t (&o)[D / 32]) {
   constexpr int NJ = D / 16, ND = D / 32;
   constexpr int KS = D + 8, VS = 32 + 8;
   constexpr int half_r = R / 2;
@@ -230,11 +230,8 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, int hq, int g, i
   const float* sinr = p.rope_sin + c * half_r;
   const uint32_t anc = p.desc->ancestors[c][0];
   u32x4_t qf[NJ], ql[NJ];
-  {
-    HeadRow<D, R> qr;
-    row_issue<D, R>(qr, row + hq * p.q_stride, p.q_norm, cosr, sinr, h);
-    q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
-  }
+  if constexpr (D > 128) row_issue<D, R>(qr, row + hq * p.q_stride, p.q_norm, cosr, sinr, h);
+  q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
   u32x4_t kf8[NJ], vf8[NJ];
   {
     HeadRow<D, R> kr;
@@ -314,17 +311,17 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, int hq, int g, i
 // in the last chunk are masked (scores) and zeroed (V), since the page may
 // hold stale or non-finite data there.
 template <int D, int R>
-__device__ __forceinline__ void prefix_chunk(const AttnParams& p, int hq, int g, int P, int chunk, int c, int h,
-                                             float& m_run, float& l_run, f32x16_t (&o)[D / 32]) {
+__device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>& qr, int page, int hq, int g, int P,
+                                             int chunk, int c, int h, float& m_run, float& l_run,
+                                             f32x16_t (&o)[D / 32]) {
   constexpr int NJ = D / 16, ND = D / 32;
   constexpr int CK = chunk_keys(D), NB = CK / 32;
-  constexpr int half_r = R / 2;
-  HeadRow<D, R> qr;
-  row_issue<D, R>(qr, p.qkv + (size_t)c * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + c * half_r,
-                  p.rope_sin + c * half_r, h);
+  if constexpr (D > 128)
+    row_issue<D, R>(qr, p.qkv + (size_t)c * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + c * (R / 2),
+                    p.rope_sin + c * (R / 2), h);
   const int k_begin = (chunk - 1) * CK;
   const int k_end = min(k_begin + CK, P);
-  const int page = p.page_table[k_begin / DTREE_PAGE], po = k_begin % DTREE_PAGE;
+  const int po = k_begin % DTREE_PAGE;
   const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po + swap_bits23(c)) * D;
   const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po;
   u32x4_t kf[NB][NJ];
@@ -398,6 +395,20 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   const int g = pair % p.Hkv, split = pair / p.Hkv;
   const int hq = g * G + (bid >> 3) % G;
 
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int chunk = split * kWaves + wave;
+  // Loads that do not depend on the step descriptor go out first, so their
+  // latency overlaps the descriptor read: this lane's q row (values, norm
+  // weights, RoPE) and the page of this wave's prefix chunk.
+  // (head_dim 256 issues its q row inside the chunk: live across the
+  // descriptor read it would spill.)
+  HeadRow<D, R> qr;
+  if constexpr (D <= 128)
+    row_issue<D, R>(qr, p.qkv + (size_t)c * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + c * (R / 2),
+                    p.rope_sin + c * (R / 2), h);
+  const int page = (chunk >= 1 && chunk < p.max_chunks) ? p.page_table[(chunk - 1) * CK / DTREE_PAGE] : 0;
+
   const int P = p.desc->past_length, L = p.desc->num_nodes;
   const int nchunks = 1 + (P + CK - 1) / CK;
   // A descriptor beyond the grid's capacity (P > max_past_length) or with more
@@ -405,10 +416,6 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   if (nchunks > p.max_chunks || L > 32 || L < 1) return;
   const int nsplit = (nchunks + kWaves - 1) / kWaves;
   if (split >= nsplit) return;
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
-  const int chunk = split * kWaves + wave;
 
   float m_run = kNeg, l_run = 0.f;
   f32x16_t o[ND];
@@ -419,9 +426,9 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
 
   if (chunk == 0) {
     uint16_t* ks = reinterpret_cast<uint16_t*>(lds);
-    tree_chunk<D, R>(p, hq, g, G, P, L, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+    tree_chunk<D, R>(p, qr, hq, g, G, P, L, c, h, ks, ks + 32 * KS, m_run, l_run, o);
   } else if (chunk < nchunks) {
-    prefix_chunk<D, R>(p, hq, g, P, chunk, c, h, m_run, l_run, o);
+    prefix_chunk<D, R>(p, qr, page, hq, g, P, chunk, c, h, m_run, l_run, o);
   }
 
   // LDS merge of the four waves, 128 head dims per pass. The first barrier

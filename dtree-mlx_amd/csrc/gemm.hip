@@ -532,14 +532,11 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   // order, so waiting for them later does not wait for the stream).
   float ssv[kSsBatch];
   ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
-  for (int e = threadIdx.x; e < nloc * kWaves * TE / 4; e += kThreads)
-    reinterpret_cast<f32x4_t*>(acc_lds)[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // q4: per (group, row) sums of the activations over this workgroup's groups
   // (the affine bias term and the 128 offset of the nibble encoding need them).
   const int ngrp = (U1 - U0) < nkb ? (U1 - U0) : nkb;
   const int kbase = (U1 - U0) < nkb ? U0 % nkb : 0;
   if constexpr (Q4) q4_xsums<LO>(p.x, p.x_lo, kbase, ngrp, nkb, xsum_lds);
-  __syncthreads();
 
   // ---- stream this wave's quarter of the range ----
   const int R = U1 - U0;
@@ -600,6 +597,10 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   int cur = a0 < a1 ? a0 / nkb : -1;
 #pragma unroll
   for (int s = 0; s < kSkDepth; ++s) issue(s, a0 + s);
+  // The accumulator slots are cleared while the first units are in flight.
+  for (int e = threadIdx.x; e < nloc * kWaves * TE / 4; e += kThreads)
+    reinterpret_cast<f32x4_t*>(acc_lds)[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
   ss_finish<1>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, ssv, rs, rs_scratch);
   for (int ub = a0; ub < a1; ub += kSkDepth) {
 #pragma unroll
@@ -897,6 +898,96 @@ static void launch_sk(const GemmParams& p, int epi, hipStream_t st) {
   }
 }
 
+
+// ---- data-parallel GEMM (32 tiled rows, bf16): no cross-workgroup sums ----
+// A workgroup owns one 32-column output tile over the whole K. Wave w streams
+// K blocks w, w + 4, ... through a kDpDepth-deep register ring (weights and
+// both activation planes of kDpDepth blocks in flight), the waves' partial
+// tiles are added in LDS in wave order (deterministic), and the shared tile
+// epilogue runs. Trades activation re-reads (from L2) for the stream-K
+// schedule's cross-workgroup publish / arrive / reduce tail.
+constexpr int kDpDepth = 4;
+
+template <bool LO, int EPI>
+__global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
+  constexpr int TN = 32, TE = 32 * TN;
+  __shared__ float red[kWaves * TE];
+  __shared__ float rs[32];
+  __shared__ float rs_scratch[kThreads];
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = blockIdx.x, nkb = p.k >> 6;
+  float ssv[kSsBatch];
+  ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
+  const uint16_t* xb = p.x + lane * 8;
+  const uint16_t* xlb = LO ? p.x_lo + lane * 8 : nullptr;
+  const uint16_t* wb = p.w + (size_t)tile * nkb * 2048 + lane * 8;
+  const int n = wave < nkb ? (nkb - wave + kWaves - 1) / kWaves : 0;
+  u32x4_t wr[kDpDepth][4], xr[kDpDepth][2][4];
+  auto issue = [&](int s, int j) {
+    if (j < n) {
+      const size_t off = (size_t)(wave + kWaves * j) * 2048;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xr[s][0][i] = ld_u32x4(xb + off + 512 * i);
+        if (LO) xr[s][1][i] = ld_u32x4(xlb + off + 512 * i);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[s][i] = ld_u32x4_stream(wb + off + 512 * i);
+    }
+  };
+  f32x16_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int s = 0; s < kDpDepth; ++s) issue(s, s);
+  ss_finish<1>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, ssv, rs, rs_scratch);
+  for (int jb = 0; jb < n; jb += kDpDepth) {
+#pragma unroll
+    for (int s = 0; s < kDpDepth; ++s) {
+      const int j = jb + s;
+      if (j < n) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc = mfma32(xr[s][0][i], wr[s][i], acc);
+          if (LO) acc = mfma32(xr[s][1][i], wr[s][i], acc);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(s, j + kDpDepth);
+      }
+    }
+  }
+  // Waves 1..3 park their tiles; wave 0 adds them in wave order into slot 0.
+  if (wave > 0) {
+    float* my = red + (wave - 1) * TE;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) my[acc_row(r, h) * TN + c] = acc[r];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 0; w < kWaves - 1; ++w)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += red[w * TE + acc_row(r, h) * TN + c];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[acc_row(r, h) * TN + c] = acc[r];
+  }
+  __syncthreads();
+  tile_epilogue<32, TN, EPI>(p, red, rs, tile);
+}
+
+template <bool LO>
+static void launch_dp(const GemmParams& p, int epi, hipStream_t st) {
+  const int grid = p.n / 32;
+  switch (epi) {
+    case DTREE_EPI_STORE_F32: dp_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<grid, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: dp_gemm_kernel<LO, DTREE_EPI_RESIDUAL><<<grid, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: dp_gemm_kernel<LO, DTREE_EPI_SWIGLU><<<grid, kThreads, 0, st>>>(p); break;
+    default: dp_gemm_kernel<LO, DTREE_EPI_STORE_BF16><<<grid, kThreads, 0, st>>>(p); break;
+  }
+}
+
 }  // namespace dtree
 
 using namespace dtree;
@@ -927,6 +1018,9 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0, "gemm: k must be a positive multiple of 64");
   DTREE_REQUIRE(a->ldx >= a->k && a->ldx % 8 == 0, "gemm: ldx must be >= k and a multiple of 8");
   const int ntiles = a->n / tn, nkb = a->k / 64;
+  DTREE_REQUIRE(a->split_k >= -2, "gemm: split_k must be >= -2");
+  DTREE_REQUIRE(a->split_k >= 0 || (a->w_layout != DTREE_W_ROWMAJOR && a->rows_padded == 32),
+                "gemm: split_k -1 / -2 need tiled weights and 32 rows");
   const int S = a->split_k > 0 ? a->split_k : auto_split(ntiles, nkb);
   DTREE_REQUIRE(S <= nkb, "gemm: split_k larger than the number of 64-wide K blocks");
   DTREE_REQUIRE((size_t)ntiles * sizeof(int) <= kCounterBytes, "gemm: n too large for the tile counter region");
@@ -977,7 +1071,19 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     const int width = epi == DTREE_EPI_SWIGLU ? a->n / 2 : a->n;
     DTREE_REQUIRE(a->ld_out_bf16 == width && width % 64 == 0, "gemm: tiled out needs ld_out_bf16 == width, width % 64");
   }
-  if (tiled && a->rows_padded == 32 && a->split_k <= 0) {
+  // One workgroup per 32-column tile over the whole K when asked (split_k -1)
+  // or, automatically, for the shapes where it beats the stream-K schedule on
+  // MI355X (K <= 4096 and N <= 12800, e.g. the fused QKV and o_proj at hidden
+  // 2560): no cross-workgroup reduction tail, at the price of re-reading the
+  // activations per tile and of fewer than 256 workgroups on narrow N.
+  const bool dp_auto = a->split_k == 0 && a->k <= 4096 && a->n <= 12800;
+  if (tiled && !q4 && a->rows_padded == 32 && (a->split_k == -1 || dp_auto)) {
+    if (p.x_lo) launch_dp<true>(p, epi, stream);
+    else launch_dp<false>(p, epi, stream);
+    DTREE_LAUNCH_CHECK("gemm launch");
+    return DTREE_OK;
+  }
+  if (tiled && a->rows_padded == 32 && (a->split_k == 0 || a->split_k == -2 || q4)) {
     const int cus = device_cus();
     const int nblk = a->n / 64;
     p.T = nblk * nkb;

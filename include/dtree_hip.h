@@ -103,7 +103,9 @@ typedef struct DtreeGemmArgs {
   int32_t w_layout;       /* DTREE_W_ROWMAJOR, DTREE_W_TILED or DTREE_W_Q4G64 */
   int32_t n, k;           /* k % 64 == 0; n % 64 == 0 (% 32 above 64 rows) */
   int32_t epilogue;       /* DTREE_EPI_*                                   */
-  int32_t split_k;        /* >= 1; 0 = choose automatically                */
+  int32_t split_k;        /* >= 1 split-K; 0 = automatic; tiled 32 rows only:
+                             -1 one workgroup per 32-column tile (bf16),
+                             -2 stream-K schedule                          */
   const float* ss_in;     /* [ss_tiles][rows_padded] or NULL               */
   int32_t ss_tiles;
   int32_t norm_dim;       /* divisor of the row mean square                */

@@ -187,26 +187,29 @@ def test_gemm_swiglu_epilogue(gpu_device):
     np.testing.assert_allclose(bf16_f32(act), ref, rtol=1e-2, atol=1e-3)
 
 
-# ---- stream-K path (32 rows, tiled operands, split_k = 0) -------------------
-# Shapes chosen for the schedule: one unit; one K block over many column
-# blocks (workgroups touching several blocks); one column block over 152 K
-# blocks (one block shared by 152 workgroups); and the Qwen3-4B layer shapes.
+# ---- 32-row tiled paths: stream-K (split_k -2) and one workgroup per tile
+# (split_k -1); split_k 0 picks one of them per shape.
+# Shapes chosen for the stream-K schedule: one unit; one K block over many
+# column blocks (workgroups touching several blocks); one column block over 152
+# K blocks (one block shared by 152 workgroups); and the Qwen3-4B layer shapes.
 SK_SHAPES = [(64, 64), (4096, 64), (19456, 64), (64, 9728), (256, 1024), (6144, 2560), (2560, 4096),
              (19456, 2560), (2560, 9728)]
+SCHEDULES = [-2, -1, 0]
 
 
-def _sk_args(xt, xlo_t, wt, n, k, epi, ws):
+def _sk_args(xt, xlo_t, wt, n, k, epi, ws, sched=0):
     a = N.GemmArgs()
     a.x = xt.data_ptr(); a.x_lo = xlo_t.data_ptr() if xlo_t is not None else None
     a.x_layout = a.w_layout = N.W_TILED; a.ldx = k; a.rows_padded = 32
-    a.w = wt.data_ptr(); a.n = n; a.k = k; a.epilogue = epi; a.split_k = 0
+    a.w = wt.data_ptr(); a.n = n; a.k = k; a.epilogue = epi; a.split_k = sched
     a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
     return a
 
 
 @pytest.mark.parametrize("n,k", SK_SHAPES)
 @pytest.mark.parametrize("lo", [False, True])
-def test_sk_gemm_store_f32(gpu_device, n, k, lo):
+@pytest.mark.parametrize("sched", SCHEDULES)
+def test_sk_gemm_store_f32(gpu_device, n, k, lo, sched):
     g = np.random.default_rng(n + k + lo)
     L = 25
     xf = np.zeros((32, k), np.float32)
@@ -222,7 +225,7 @@ def test_sk_gemm_store_f32(gpu_device, n, k, lo):
     outs = []
     for _ in range(2):
         out = torch.zeros(32, n, device=gpu_device)
-        a = _sk_args(xt, xlt, wt, n, k, N.EPI_STORE_F32, ws)
+        a = _sk_args(xt, xlt, wt, n, k, N.EPI_STORE_F32, ws, sched)
         a.ss_in = ss.data_ptr(); a.ss_tiles = 3; a.norm_dim = k; a.eps = 1e-6
         a.out_f32 = out.data_ptr(); a.ld_out_f32 = n
         N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "gemm")
@@ -238,7 +241,8 @@ def test_sk_gemm_store_f32(gpu_device, n, k, lo):
 
 
 @pytest.mark.parametrize("n,k", [(512, 768), (2560, 4096), (2560, 9728)])
-def test_sk_gemm_residual_epilogue(gpu_device, n, k):
+@pytest.mark.parametrize("sched", SCHEDULES)
+def test_sk_gemm_residual_epilogue(gpu_device, n, k, sched):
     g = np.random.default_rng(n + 3 * k)
     L = 25
     x = _rows(32, L, k, g, gpu_device)
@@ -252,7 +256,7 @@ def test_sk_gemm_residual_epilogue(gpu_device, n, k):
     ss = torch.zeros(n // 32, 32, device=gpu_device)
     hid = torch.zeros(32, n, dtype=torch.bfloat16, device=gpu_device)
     ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, n, k, 0), dtype=torch.uint8, device=gpu_device)
-    _gemm(x, w, N.EPI_RESIDUAL, 0, ws, out_f32=res, out_bf16=xg, next_norm=gn, ss_out=ss, hidden_out=hid,
+    _gemm(x, w, N.EPI_RESIDUAL, sched, ws, out_f32=res, out_bf16=xg, next_norm=gn, ss_out=ss, hidden_out=hid,
           tiled=True)
     torch.cuda.synchronize()
     ref = res0.cpu().numpy().astype(np.float64) + bf16_f32(x).astype(np.float64) @ bf16_f32(w).T.astype(np.float64)
@@ -266,7 +270,8 @@ def test_sk_gemm_residual_epilogue(gpu_device, n, k):
 
 
 @pytest.mark.parametrize("F,k", [(384, 512), (9728, 2560)])
-def test_sk_gemm_swiglu_epilogue(gpu_device, F, k):
+@pytest.mark.parametrize("sched", SCHEDULES)
+def test_sk_gemm_swiglu_epilogue(gpu_device, F, k, sched):
     g = np.random.default_rng(F + k)
     L = 25
     x = _rows(32, L, k, g, gpu_device)
@@ -277,7 +282,7 @@ def test_sk_gemm_swiglu_epilogue(gpu_device, F, k):
     ss = torch.from_numpy(np.abs(g.standard_normal((3, 32))).astype(np.float32) + 0.5).to(gpu_device)
     act = torch.zeros(32, F, dtype=torch.bfloat16, device=gpu_device)
     ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, 2 * F, k, 0), dtype=torch.uint8, device=gpu_device)
-    _gemm(x, wgu, N.EPI_SWIGLU, 0, ws, ss_in=ss, norm_dim=k, out_bf16=act, tiled=True)
+    _gemm(x, wgu, N.EPI_SWIGLU, sched, ws, ss_in=ss, norm_dim=k, out_bf16=act, tiled=True)
     torch.cuda.synchronize()
     rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(0) / k + 1e-6)
     xf = bf16_f32(x).astype(np.float64)
