@@ -5,8 +5,8 @@ Host side is Python on PyTorch-ROCm (device memory, streams); every verify
 computation runs in the hand-written HIP kernels of libdtree_hip.so, bound
 through the C ABI in include/dtree_hip.h.
 """
-from .adapters import (ADAPTERS, LoadedTargetModel, Qwen3TargetAdapter, Qwen3TreeModel, adapter_for_model_type,
-                       load_target_model)
+from .adapters import (ADAPTERS, LoadedTargetModel, Qwen35TargetAdapter, Qwen35TreeModel, Qwen3TargetAdapter,
+                       Qwen3TreeModel, adapter_for_model_type, load_target_model)
 from .cache import PagedKVCache, Qwen35Cache
 from .config import QWEN3_4B, QWEN35_4B, QWEN35_9B, Qwen35Config, Qwen3Config, tiny_qwen3, tiny_qwen35
 from .dtree_runtime import (build_dtree_tree, compile_dtree_tree, dtree_generate, follow_verified_tree,
@@ -20,5 +20,5 @@ __all__ = [
     "Qwen3TreeEngine", "Qwen3TreeModel", "Qwen3Weights", "StepResult", "adapter_for_model_type",
     "ancestor_bitsets", "build_dtree_tree", "compile_dtree_tree", "dtree_generate", "follow_verified_tree",
     "lazy_follow_tree_exact", "load_target_model", "sample_tokens", "tiny_qwen3",
-    "QWEN35_4B", "QWEN35_9B", "Qwen35Cache", "Qwen35Config", "Qwen35TreeEngine", "Qwen35Weights", "tiny_qwen35",
+    "Qwen35TargetAdapter", "Qwen35TreeModel", "QWEN35_4B", "QWEN35_9B", "Qwen35Cache", "Qwen35Config", "Qwen35TreeEngine", "Qwen35Weights", "tiny_qwen35",
 ]

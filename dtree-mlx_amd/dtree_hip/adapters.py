@@ -3,7 +3,8 @@
 Mirrors the reference's adapter boundary (adapters.py:88-213 protocol,
 Qwen3TargetAdapter adapters.py:451-668, LoadedTargetModel adapters.py:681-819)
 with torch tensors in place of mx.array. The tree-verify methods run the HIP
-kernels through Qwen3TreeEngine; nothing here computes on the CPU.
+kernels through Qwen3TreeEngine / Qwen35TreeEngine; nothing here computes on
+the CPU.
 """
 from __future__ import annotations
 
@@ -14,10 +15,11 @@ from typing import Any
 import numpy as np
 import torch
 
-from .cache import PagedKVCache
-from .config import QWEN3_4B, Qwen3Config
+from .cache import PagedKVCache, Qwen35Cache
+from .config import QWEN3_4B, QWEN35_4B, Qwen35Config, Qwen3Config
 from .engine import Qwen3TreeEngine
-from .weights import Qwen3Weights
+from .qwen35_engine import Qwen35TreeEngine
+from .weights import Qwen35Weights, Qwen3Weights
 
 
 class Qwen3TreeModel:
@@ -29,6 +31,44 @@ class Qwen3TreeModel:
         self.weights = weights
         self.engine = Qwen3TreeEngine(cfg, weights, max_past=max_past, max_nodes=max_nodes,
                                       layer_ids=layer_ids, split_k=split_k)
+
+    @property
+    def layers(self):
+        return self.weights.layers
+
+
+class _Qwen35TextModel:
+    """The text model's single-token path used by the lazy exact verifier
+    (Qwen3_5TextModel.forward_dflash, custom_qwen35_model.py:961-1097): one
+    forward per token that commits to the real cache."""
+
+    def __init__(self, owner: "Qwen35TreeModel"):
+        self._owner = owner
+
+    def forward_dflash(self, inputs, cache: Qwen35Cache, layer_ids, input_embeddings=None,
+                       return_rollback_records: bool = False):
+        if input_embeddings is not None or return_rollback_records:
+            raise NotImplementedError("forward_dflash takes token ids only here (no rollback records)")
+        eng = self._owner.engine
+        eng.set_layer_ids(layer_ids)
+        toks = _as_list(inputs)
+        eng.commit_chain(cache, toks, norm_hidden=True)
+        n = len(toks)
+        vh = (eng.hidden[:n].clone()[None] if layer_ids
+              else torch.zeros(1, n, 0, dtype=torch.bfloat16, device=eng.dev))
+        return eng.norm_hidden[:n].clone()[None], vh
+
+
+class Qwen35TreeModel:
+    """A Qwen3.5 hybrid target resident on one GPU (weights + verify engine)."""
+
+    def __init__(self, cfg: Qwen35Config, weights: Qwen35Weights, max_past: int = 4096, layer_ids=(),
+                 max_nodes: int = 32, split_k: dict | None = None):
+        self.args = cfg
+        self.weights = weights
+        self.engine = Qwen35TreeEngine(cfg, weights, max_past=max_past, max_nodes=max_nodes,
+                                       layer_ids=layer_ids, split_k=split_k)
+        self.model = _Qwen35TextModel(self)
 
     @property
     def layers(self):
@@ -220,7 +260,97 @@ class Qwen3TargetAdapter(MLXTargetAdapter):
         return res.accepted, res.bonus_token, vh
 
 
-ADAPTERS: dict[str, type[MLXTargetAdapter]] = {"qwen3": Qwen3TargetAdapter}
+class Qwen35TargetAdapter(Qwen3TargetAdapter):
+    """Qwen3.5 hybrid adapter (adapters.py:257-448): forward_tree leaves the
+    committed state untouched and keeps a pending tree state (here: the
+    attention layers' tree K/V rows at [P, P + L) beyond the offset and the
+    GatedDeltaNet layers' per-node inputs); compact_kv_caches commits it along
+    the accepted path and raises without one (adapters.py:433-448)."""
+
+    family = "qwen3_5"
+
+    def __init__(self):
+        self._pending_tree_state = None
+
+    def make_cache(self, model: Qwen35TreeModel, speculative_linear_cache: bool = False) -> Qwen35Cache:
+        del speculative_linear_cache
+        return model.engine.new_cache()
+
+    def forward_with_hidden_states(self, model: Qwen35TreeModel, inputs, cache: Qwen35Cache, layer_ids,
+                                   return_rollback_records: bool = False):
+        """Prefill as fully accepted chains of <= max_nodes tokens; returns the
+        last position's logits ([1, 1, V]) and every position's verifier hidden."""
+        eng = model.engine
+        eng.set_layer_ids(layer_ids)
+        toks = _as_list(inputs)
+        hid = []
+        n = 0
+        for s in range(0, len(toks), eng.max_nodes):
+            part = toks[s:s + eng.max_nodes]
+            eng.commit_chain(cache, part)
+            n = len(part)
+            if layer_ids:
+                hid.append(eng.hidden[:n].clone())
+        eng.launch_lm_head(eng.stream_handle(), want_logits=True)
+        logits = eng.logits[n - 1:n].clone()[None]
+        target_hidden = torch.cat(hid, 0)[None] if hid else torch.zeros(1, len(toks), 0, device=eng.dev)
+        if return_rollback_records:
+            return logits, target_hidden, {}
+        return logits, target_hidden
+
+    def forward_tree_with_hidden_states(self, model: Qwen35TreeModel, inputs, cache: Qwen35Cache, layer_ids,
+                                        parents, position_ids, attention_mask):
+        """adapters.py:411-431 (forward_qwen35_tree_with_hidden_states,
+        qwen35_tree.py:629-705): the offset stays at P; the tree is pending."""
+        eng = model.engine
+        eng.set_layer_ids(layer_ids)
+        toks = _as_list(inputs)
+        pos = _as_list(position_ids)
+        L, P = len(toks), cache.offset
+        if parents is None or len(parents) != L:
+            raise ValueError(f"tree parent list length must match verify length, got "
+                             f"{None if parents is None else len(parents)} vs {L}")
+        mask = attention_mask.cpu().numpy() if isinstance(attention_mask, torch.Tensor) else np.asarray(attention_mask)
+        anc = _mask_tree_bitsets(mask.astype(bool), P, L)
+        eng.set_step(toks, pos, list(parents), P, ancestors=anc)
+        eng.launch_forward(cache, eng.stream_handle(), norm_hidden=True)
+        self._pending_tree_state = (P, L, [int(p) for p in parents])
+        norm_hidden = eng.norm_hidden[:L].clone()[None]
+        vh = eng.hidden[:L].clone()[None] if layer_ids else torch.zeros(1, L, 0, dtype=torch.bfloat16, device=eng.dev)
+        return norm_hidden, vh
+
+    def compact_kv_caches(self, model: Qwen35TreeModel, cache: Qwen35Cache, past_length: int,
+                          keep_current_indices: list[int]) -> None:
+        """commit_qwen35_tree_path (qwen35_tree.py:708-732) on the HIP kernels:
+        KV compaction of the attention layers, then every GatedDeltaNet layer's
+        window / state replayed along the accepted path."""
+        if self._pending_tree_state is None:
+            raise RuntimeError("Qwen3.5 tree compaction requires pending tree state.")
+        P, L, parents = self._pending_tree_state
+        self._pending_tree_state = None
+        keep = [int(i) for i in keep_current_indices]
+        if not keep:
+            return
+        if keep[0] != 0 or any(parents[b] != a for a, b in zip(keep, keep[1:])):
+            raise ValueError("accepted indices must be a root path of the pending tree")
+        eng = model.engine
+        eng.set_step([0] * L, [0] * L, parents, P, aux=True, accepted=keep)
+        eng.launch_compact(cache, eng.stream_handle(), select_hidden=False, aux=True)
+        cache.offset = P + len(keep)
+
+    def cache_summary(self, cache: Qwen35Cache) -> str:
+        c = cache.cfg
+        parts = []
+        for i in range(c.num_hidden_layers):
+            if c.is_linear(i):
+                parts.append(f"{i}:ssm=(1, {c.linear_num_value_heads}, {c.linear_value_head_dim}, "
+                             f"{c.linear_key_head_dim})")
+            else:
+                parts.append(f"{i}:kv={cache.offset}")
+        return " ".join(parts)
+
+
+ADAPTERS: dict[str, type[MLXTargetAdapter]] = {"qwen3": Qwen3TargetAdapter, "qwen3_5": Qwen35TargetAdapter}
 
 
 def adapter_for_model_type(model_type: str):
@@ -283,18 +413,29 @@ class LoadedTargetModel:
         return out
 
 
-def load_target_model(spec: str | Qwen3Config = "random:qwen3-4b", seed: int = 0, max_past: int = 4096,
-                      device: str = "cuda", layer_ids=()) -> LoadedTargetModel:
+def load_target_model(spec: str | Qwen3Config | Qwen35Config = "random:qwen3-4b", seed: int = 0,
+                      max_past: int = 4096, device: str = "cuda", layer_ids=(), norm_jitter: float = 0.0,
+                      quant: str = "bf16") -> LoadedTargetModel:
     """Random-init target (no checkpoint download: weights ~ N(0, 0.02), seeded).
-    ``spec`` is "random:qwen3-4b" or a Qwen3Config."""
-    if isinstance(spec, Qwen3Config):
+    ``spec`` is "random:qwen3-4b", "random:qwen35-4b" or a Qwen3Config /
+    Qwen35Config (adapters.py:822-846 resolves a model name instead)."""
+    if isinstance(spec, (Qwen3Config, Qwen35Config)):
         cfg, name = spec, "random:custom"
     elif spec in ("random:qwen3-4b", "qwen3-4b"):
         cfg, name = QWEN3_4B, spec
+    elif spec in ("random:qwen35-4b", "qwen35-4b"):
+        cfg, name = QWEN35_4B, spec
     else:
-        raise NotImplementedError(f"Unsupported target {spec!r}: only random-init Qwen3 configs are available")
+        raise NotImplementedError(f"Unsupported target {spec!r}: only random-init Qwen3 / Qwen3.5 configs")
     cls = adapter_for_model_type(cfg.model_type)
-    weights = Qwen3Weights.random(cfg, seed=seed, device=device)
-    model = Qwen3TreeModel(cfg, weights, max_past=max_past, layer_ids=layer_ids)
+    if isinstance(cfg, Qwen35Config):
+        weights = Qwen35Weights.random(cfg, seed=seed, device=device, norm_jitter=norm_jitter, quant=quant)
+        model = Qwen35TreeModel(cfg, weights, max_past=max_past, layer_ids=layer_ids)
+    else:
+        if quant == "q4":
+            weights = Qwen3Weights.random_q4(cfg, seed=seed, device=device, norm_jitter=norm_jitter)
+        else:
+            weights = Qwen3Weights.random(cfg, seed=seed, device=device, norm_jitter=norm_jitter)
+        model = Qwen3TreeModel(cfg, weights, max_past=max_past, layer_ids=layer_ids)
     return LoadedTargetModel(requested_model=name, resolved_model_path=None, model=model, tokenizer=None,
                              adapter=cls())

@@ -175,20 +175,26 @@ class Qwen35TreeEngine(TreeEngineBase):
             ga.desc = desc.data_ptr()
             N.check(self.lib.dtree_gdn_layer_commit(C.byref(ga), st), "gdn commit")
 
+    def commit_chain(self, cache: Qwen35Cache, tokens, norm_hidden: bool = False) -> None:
+        """Forward a causal chain of <= max_nodes tokens and commit all of it:
+        the attention K/V rows stay where the forward wrote them, every
+        GatedDeltaNet window / state advances along the whole chain."""
+        n = len(tokens)
+        P = cache.offset
+        if not 1 <= n <= self.max_nodes:
+            raise ValueError(f"a chain holds 1..{self.max_nodes} tokens, got {n}")
+        if P + n > self.max_past:
+            raise ValueError("chain beyond max_past")
+        st = self.stream_handle()
+        self.set_step(tokens, [P + i for i in range(n)], [-1] + list(range(n - 1)), P, accepted=list(range(n)))
+        self.launch_forward(cache, st, norm_hidden=norm_hidden)
+        self._commit_gdn(cache, st, self.desc)
+        cache.offset = P + n
+
     def prefill(self, cache: Qwen35Cache, tokens, chunk: int | None = None) -> None:
-        """Causal prefill through the tree path: chains of up to max_nodes
-        tokens, each fully accepted (KV rows stay where the forward wrote them,
-        GatedDeltaNet windows / states advance along the whole chain)."""
+        """Causal prefill through the tree path: fully accepted chains of up to
+        max_nodes tokens."""
         chunk = chunk or self.max_nodes
         toks = [int(t) for t in tokens]
-        st = self.stream_handle()
         for s in range(0, len(toks), chunk):
-            part = toks[s:s + chunk]
-            P = cache.offset
-            if P + len(part) > self.max_past:
-                raise ValueError("prefill beyond max_past")
-            n = len(part)
-            self.set_step(part, [P + i for i in range(n)], [-1] + list(range(n - 1)), P, accepted=list(range(n)))
-            self.launch_forward(cache, st)
-            self._commit_gdn(cache, st, self.desc)
-            cache.offset = P + n
+            self.commit_chain(cache, toks[s:s + chunk])

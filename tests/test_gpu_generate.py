@@ -1,4 +1,6 @@
-"""End-to-end DTree decoding on the GPU through the reference-shaped surface.
+"""End-to-end DTree decoding on the GPU through the reference-shaped surface,
+for the Qwen3 target and the Qwen3.5 hybrid (lazy exact walk and full-tree
+verify).
 
 ``dtree_generate`` (dtree_runtime.py:293-586) drives the HIP target through the
 adapter methods of adapters.py (forward_with_hidden_states, embed_tokens,
@@ -11,7 +13,7 @@ relative logit tolerance (and exactly its argmax on nearly every position).
 
 The drafter is scripted: it proposes the target's own sequential greedy decode
 (computed on the GPU beforehand) through the tied LM head (hidden row =
-24 * E[token], so the draft logits peak at that token), and plants one wrong
+24 * (1024 / hidden) * E[token], so the draft logits peak at that token), and plants one wrong
 token at a depth that cycles over the steps, so the accepted lengths cover
 1 .. the full chain."""
 import numpy as np
@@ -19,9 +21,10 @@ import pytest
 import torch
 
 from oracle import qwen3 as oq
+from oracle import qwen35 as o35
 
 from dtree_hip.adapters import load_target_model
-from dtree_hip.config import tiny_qwen3
+from dtree_hip.config import Qwen35Config, tiny_qwen3, tiny_qwen35
 from dtree_hip.dtree_runtime import dtree_generate
 
 pytestmark = pytest.mark.gpu
@@ -34,6 +37,19 @@ def _oracle_teacher_forced(target, seq):
     """fp32 oracle logits of every position of `seq` under a causal mask
     (row i predicts seq[i + 1])."""
     cfg = target.model.args
+    if isinstance(cfg, Qwen35Config):
+        ocfg = o35.Qwen35Config(
+            hidden=cfg.hidden_size, layers=cfg.num_hidden_layers, ffn=cfg.intermediate_size,
+            heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+            rope_dims=cfg.rope_dims, lin_k_heads=cfg.linear_num_key_heads, lin_v_heads=cfg.linear_num_value_heads,
+            lin_k_dim=cfg.linear_key_head_dim, lin_v_dim=cfg.linear_value_head_dim,
+            conv_kernel=cfg.linear_conv_kernel_dim, full_attention_interval=cfg.full_attention_interval,
+            vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_base=cfg.rope_theta)
+        orc35 = o35.OracleQwen35(ocfg, target.model.weights.host_accessor())
+        T = len(seq)
+        norm, _, _ = orc35.forward_tree(np.asarray(seq, np.int64), np.arange(T), [-1] + list(range(T - 1)),
+                                        orc35.new_cache())
+        return orc35.lm_head_logits(norm)
     ocfg = oq.Qwen3Config(hidden=cfg.hidden_size, layers=cfg.num_hidden_layers, ffn=cfg.intermediate_size,
                           heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
                           vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_base=cfg.rope_theta)
@@ -89,13 +105,28 @@ class ScriptedDrafter:
                 t = (t + 1) % V
             toks.append(t)
         E = self.target.model.weights.embed_rows(torch.tensor(toks, device="cuda")).float()
-        return (24.0 * E)[None]
+        # peak logit 24 * 1024 * 0.02^2 ~ 9.8 whatever the hidden size, so the
+        # best-first tree follows the scripted chain
+        H = self.target.model.args.hidden_size
+        return (24.0 * 1024 / H * E)[None]
 
 
-@pytest.mark.parametrize("verify_mode", ["parallel-greedy-argmax", "parallel-replay"])
-def test_dtree_generate_emits_greedy_tokens(gpu_device, verify_mode):
-    cfg = tiny_qwen3()
-    target = load_target_model(cfg, seed=0, max_past=256, device="cuda", layer_ids=[0, 1])
+CASES = [("qwen3", "parallel-greedy-argmax", None), ("qwen3", "parallel-replay", None),
+         # Qwen3.5: the reference's default lazy exact walk, and the full-tree
+         # verify (DTREE_QWEN35_TREE_MODE=full_tree) fused and per method.
+         ("qwen3_5", "parallel-greedy-argmax", None), ("qwen3_5", "parallel-greedy-argmax", "full_tree"),
+         ("qwen3_5", "parallel-replay", "full_tree")]
+
+
+@pytest.mark.parametrize("family,verify_mode,tree_mode", CASES)
+def test_dtree_generate_emits_greedy_tokens(gpu_device, monkeypatch, family, verify_mode, tree_mode):
+    if tree_mode:
+        monkeypatch.setenv("DTREE_QWEN35_TREE_MODE", tree_mode)
+    else:
+        monkeypatch.delenv("DTREE_QWEN35_TREE_MODE", raising=False)
+    cfg = tiny_qwen3() if family == "qwen3" else tiny_qwen35()
+    target = load_target_model(cfg, seed=0, max_past=256, device="cuda", layer_ids=[0, 1],
+                               norm_jitter=0.0 if family == "qwen3" else 0.1)
     rng = np.random.default_rng(5)
     prompt = rng.integers(1, cfg.vocab_size, 40).tolist()
     n_new = 40
@@ -117,3 +148,4 @@ def test_dtree_generate_emits_greedy_tokens(gpu_device, verify_mode):
     # per step, so acceptance lengths span single tokens to long chains.
     acc = metrics["acceptance_lengths"]
     assert max(acc) >= 5 and min(acc) == 1, acc
+    assert target.model.args.model_type == target.adapter.family

@@ -137,3 +137,23 @@ def test_compile_tree_mask_semantics():
     assert vpos[0].tolist() == o_pos.tolist() == [P, *[P + d for d in depths]]
     assert np.array_equal(mask.numpy(), o_mask)
     assert mask[:, :P].all()
+
+
+def test_qwen35_compaction_requires_pending_tree_state():
+    """adapters.py:441-442: compact_kv_caches without a pending tree raises
+    (checked before any device work)."""
+    from dtree_hip.adapters import ADAPTERS, Qwen35TargetAdapter
+
+    ad = ADAPTERS["qwen3_5"]()
+    assert isinstance(ad, Qwen35TargetAdapter) and ad.family == "qwen3_5"
+    assert ad.supports_tree_verification()
+    with pytest.raises(RuntimeError, match="pending tree state"):
+        ad.compact_kv_caches(None, None, past_length=0, keep_current_indices=[0])
+    # an empty accepted list commits nothing but consumes the pending state
+    ad._pending_tree_state = (5, 3, [-1, 0, 1])
+    ad.compact_kv_caches(None, None, past_length=5, keep_current_indices=[])
+    assert ad._pending_tree_state is None
+    # accepted indices must be a root path of the pending tree
+    ad._pending_tree_state = (5, 3, [-1, 0, 0])
+    with pytest.raises(ValueError, match="root path"):
+        ad.compact_kv_caches(None, None, past_length=5, keep_current_indices=[0, 1, 2])
