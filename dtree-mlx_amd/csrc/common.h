@@ -56,6 +56,32 @@ __device__ __forceinline__ u32x4_t ld_u32x4_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
 }
 
+// ---- ranged buffer loads for register rings ------------------------------
+// A load through a raw buffer resource at a byte offset >= its size returns
+// zero without touching memory. A ring that refills its slots this way issues
+// the same number of loads on every path, whatever the remaining trip count,
+// so the compiler can wait for exactly the slot it consumes (vmcnt(N) with N
+// loads still in flight) instead of for every outstanding load, which it must
+// do when a refill is skipped on some path.
+constexpr unsigned kOob = 0x80000000u;  // offset past any buffer here (sizes < 2 GiB)
+constexpr int kNt = 2;                  // cache policy: nontemporal (read-once weights)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t buf_ld(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ u32x4_t buf_ld_stream(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kNt);
+}
+__device__ __forceinline__ uint32_t buf_ld32(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ float buf_ldf(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
 __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }

@@ -48,6 +48,8 @@ struct GemmParams {
   float* part; int* counters;
   // stream-K schedule: T = (n/64) * (k/64) units over G workgroups
   int T, G; unsigned part_bytes;
+  // ranged ring loads (32 tiled rows): bytes of w, w_sb and one x plane
+  unsigned w_bytes, sb_bytes, x_bytes;
 };
 
 // Index of element (m, col) of a bf16 output with `ld` columns.
@@ -200,10 +202,14 @@ template <int MB>
 __device__ __forceinline__ void ss_issue(const float* ss_in, int ss_tiles, float (&v)[kSsBatch]) {
   constexpr int MP = MB * 32, TPR = kThreads / MP;
   const int m = threadIdx.x % MP, part = threadIdx.x / MP;
+  // Ranged loads (zero past the statistics, or everywhere without them), so
+  // the same loads go out on every path and a later ring of loads can be
+  // waited on slot by slot.
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(ss_in, ss_in ? (unsigned)(ss_tiles * MP * 4) : 0u);
 #pragma unroll
   for (int i = 0; i < kSsBatch; ++i) {
     const int t = part + i * TPR;
-    v[i] = (ss_in && t < ss_tiles) ? ss_in[(size_t)t * MP + m] : 0.f;
+    v[i] = buf_ldf(r, t < ss_tiles ? (unsigned)((t * MP + m) * 4) : kOob);
   }
 }
 
@@ -252,8 +258,22 @@ __device__ __forceinline__ void row_scale(const float* ss_in, int ss_tiles, floa
 // rs[] applied here). Element e of the tile: row e / TN, column e % TN; with
 // TN in {32, 64} and 256 threads a 32-column group of one row is held by 32
 // consecutive lanes.
+// Residual rows of one output tile for the residual epilogue (thread t holds
+// elements t, t + kThreads, ... of the [MP][TN] tile) and, last, the next
+// RMSNorm weight of its column; all loads in flight together (callers issue
+// them before other waits to overlap the round trip).
+template <int MP, int TN>
+__device__ __forceinline__ void residual_issue(const GemmParams& p, int tile, float (&xo)[MP * TN / kThreads + 1]) {
+  const int col = tile * TN + threadIdx.x % TN;
+#pragma unroll
+  for (int i = 0; i < MP * TN / kThreads; ++i)
+    xo[i] = p.out_f32[(size_t)((threadIdx.x + i * kThreads) / TN) * p.ld_out_f32 + col];
+  xo[MP * TN / kThreads] = bf2f(p.next_norm[col]);  // the next RMSNorm's weight
+}
+
 template <int MP, int TN, int EPI>
-__device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* red, const float* rs, int tile) {
+__device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* red, const float* rs, int tile,
+                                              const float* xpre = nullptr) {
   constexpr int TE = MP * TN;
   if constexpr (EPI == DTREE_EPI_STORE_F32) {
     for (int e = threadIdx.x; e < TE; e += kThreads) {
@@ -269,11 +289,14 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* 
     constexpr int IT = TE / kThreads;
     const int n = threadIdx.x % TN;
     const int col = tile * TN + n;
-    const float g = bf2f(p.next_norm[col]);
-    // All residual loads first, so they are in flight together.
-    float xo[IT];
+    float xo[IT + 1];
+    if (xpre) {
 #pragma unroll
-    for (int i = 0; i < IT; ++i) xo[i] = p.out_f32[(size_t)((threadIdx.x + i * kThreads) / TN) * p.ld_out_f32 + col];
+      for (int i = 0; i <= IT; ++i) xo[i] = xpre[i];
+    } else {
+      residual_issue<MP, TN>(p, tile, xo);
+    }
+    const float g = xo[IT];
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int e = threadIdx.x + i * kThreads;
@@ -367,6 +390,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 // runs the shared tile epilogue.
 constexpr int kSkMaxBlocks = 4;  // 64-column blocks one workgroup may touch
 constexpr int kSkDepth = 4;      // units in flight per wave
+constexpr int kRedBatch = 8;     // partial tiles a last arriver loads per round
 constexpr int kSkMaxGrid = 1024; // CU-count bound used for workspace sizing
 constexpr int kSkMaxKb = 64;     // q4: K groups whose activation sums one workgroup keeps
 
@@ -509,8 +533,52 @@ __device__ __forceinline__ void wg_tile_q4(const uint16_t* __restrict__ x, const
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* part, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)bytes, 0x00020000);
 }
-// sc1: coherent across the XCDs' L2s (written through / read past them).
+// sc1: coherent across the XCDs' L2s (written through / read past them);
+// sc0: coherent within one XCD (read from its L2, past the CU's L1).
 constexpr int kSc1 = 16;
+constexpr int kSc0 = 1;
+
+// Stream-K ranges in XCD order. Workgroups are dispatched round-robin over
+// the XCDs (blockIdx % 8; each workgroup checks its own with HW_REG_XCC_ID),
+// so logical range g = (blockIdx % 8) * (G / 8) + blockIdx / 8 puts the
+// consecutive ranges that share a column block on one XCD. A partial tile
+// is always written through (sc1), and read from that XCD's L2 (sc0) when
+// its writers and reader are all confirmed on the same XCD.
+constexpr int kXcds = 8;
+constexpr int kForeign = 1 << 16;  // arrival increment of a workgroup off its XCD
+__device__ __forceinline__ int sk_logical(int bid, int G) {
+  return G % kXcds == 0 ? (bid % kXcds) * (G / kXcds) + bid / kXcds : bid;
+}
+__device__ __forceinline__ int xcc_id() {
+  return __builtin_amdgcn_s_getreg(20 | (3 << 11));  // HW_REG_XCC_ID, bits [3:0]
+}
+__device__ __forceinline__ int arrive_add(int* counter, int v) {
+  return __hip_atomic_fetch_add(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum of the partial tiles of workgroups gf..gl for block b (slot q + b),
+// elements 8t .. 8t+7: every partial in flight at once (kRedBatch per round;
+// ranged loads past the last return zero and add nothing), added in
+// workgroup order.
+template <int AUX>
+__device__ __forceinline__ void sum_partials(__amdgpu_buffer_rsrc_t prs, int b, int gf, int gl, int t, f32x4_t& s0,
+                                             f32x4_t& s1) {
+  constexpr int TE = 32 * 64;
+  for (int q = gf; q <= gl; q += kRedBatch) {
+    u32x4_t v[kRedBatch][2];
+#pragma unroll
+    for (int z = 0; z < kRedBatch; ++z) {
+      const unsigned off = q + z <= gl ? (unsigned)(((q + z + b) * TE + 8 * t) * 4) : kOob;
+      v[z][0] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0, AUX);
+      v[z][1] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(off + 16), 0, AUX);
+    }
+#pragma unroll
+    for (int z = 0; z < kRedBatch; ++z) {
+      s0 += __builtin_bit_cast(f32x4_t, v[z][0]);
+      s1 += __builtin_bit_cast(f32x4_t, v[z][1]);
+    }
+  }
+}
 
 template <bool LO, int EPI, bool Q4>
 __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
@@ -522,7 +590,12 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   __shared__ int last_flag[kSkMaxBlocks];
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = blockIdx.x, G = p.G, T = p.T, nkb = p.k >> 6;
+  const int G = p.G, T = p.T, nkb = p.k >> 6;
+  // Logical range g in XCD order (see sk_logical): the workgroups that share
+  // a column block run on one XCD; `native` confirms the placement.
+  const bool xcd_order = G % kXcds == 0;
+  const int g = sk_logical(blockIdx.x, G);
+  const bool native = xcd_order && xcc_id() == (int)(blockIdx.x % kXcds);
   const int U0 = (int)((long long)g * T / G), U1 = (int)((long long)(g + 1) * T / G);
   if (U0 >= U1) return;
   const int b_first = U0 / nkb, b_last = (U1 - 1) / nkb;
@@ -541,39 +614,37 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   // ---- stream this wave's quarter of the range ----
   const int R = U1 - U0;
   const int a0 = U0 + wave * R / kWaves, a1 = U0 + (wave + 1) * R / kWaves;
-  const uint16_t* xb = p.x + lane * 8;
-  const uint16_t* xlb = LO ? p.x_lo + lane * 8 : nullptr;
-  const uint16_t* wb = p.w + lane * 8;
-  const uint32_t* qb = reinterpret_cast<const uint32_t*>(p.w) + lane * 4;  // q4 words
-  const uint32_t* sbb = reinterpret_cast<const uint32_t*>(p.w_sb) + c;     // q4 (scale, bias)
+  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(p.x, p.x_bytes), xlrs = buf_rsrc(p.x_lo, LO ? p.x_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(p.w, p.w_bytes), sbrs = buf_rsrc(p.w_sb, Q4 ? p.sb_bytes : 0u);
   // Ring of in-flight units: bf16 weights (2 blocks x 4 loads) or q4 words
-  // (2 blocks x 1 load) + (scale, bias) per block; activations hi/lo.
+  // (2 blocks x 1 load) + (scale, bias) per block; activations hi/lo. A slot
+  // past the wave's range is refilled with ranged loads that return zero, so
+  // every refill issues the same loads (see kOob) and is never consumed.
   u32x4_t wr[kSkDepth][2][Q4 ? 1 : 4], xr[kSkDepth][2][4];
   uint32_t sbr[kSkDepth][2];
   auto issue = [&](int s, int u) {
-    if (u < a1) {
-      const int b = u / nkb, kb = u - b * nkb;
-      const uint16_t* x0 = xb + (size_t)kb * 2048;
+    const bool ok = u < a1;
+    const int b = u / nkb, kb = u - b * nkb;
+    const unsigned xo = ok ? (unsigned)(kb * 2048 + lane * 8) * 2u : kOob;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xr[s][0][i] = buf_ld(xrs, xo + 1024u * i);
+      if (LO) xr[s][1][i] = buf_ld(xlrs, xo + 1024u * i);
+    }
+    if constexpr (Q4) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const unsigned blk = (unsigned)((2 * b + nb) * nkb + kb);
+        wr[s][nb][0] = buf_ld_stream(wrs, ok ? (blk * 256u + lane * 4) * 4u : kOob);
+        sbr[s][nb] = buf_ld32(sbrs, ok ? (blk * 32u + c) * 4u : kOob);
+      }
+    } else {
+      const unsigned w0 = ok ? (unsigned)(((2 * b) * nkb + kb) * 2048 + lane * 8) * 2u : kOob;
+      const unsigned w1 = ok ? w0 + (unsigned)nkb * 4096u : kOob;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        xr[s][0][i] = ld_u32x4(x0 + 512 * i);
-        if (LO) xr[s][1][i] = ld_u32x4(xlb + (size_t)kb * 2048 + 512 * i);
-      }
-      if constexpr (Q4) {
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const size_t blk = (size_t)(2 * b + nb) * nkb + kb;
-          wr[s][nb][0] = ld_u32x4_stream(qb + blk * 256);
-          sbr[s][nb] = sbb[blk * 32];
-        }
-      } else {
-        const uint16_t* w0 = wb + ((size_t)(2 * b) * nkb + kb) * 2048;
-        const uint16_t* w1 = w0 + (size_t)nkb * 2048;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          wr[s][0][i] = ld_u32x4_stream(w0 + 512 * i);
-          wr[s][1][i] = ld_u32x4_stream(w1 + 512 * i);
-        }
+        wr[s][0][i] = buf_ld_stream(wrs, w0 + 1024u * i);
+        wr[s][1][i] = buf_ld_stream(wrs, w1 + 1024u * i);
       }
     }
   };
@@ -629,8 +700,8 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        issue(s, u + kSkDepth);
       }
+      issue(s, u + kSkDepth);
     }
   }
   if (cur >= 0) dump(cur);
@@ -669,10 +740,19 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   if (t < nloc) {
     const int b = b_first + t;
     const int gf = owner(b * nkb), gl = owner((b + 1) * nkb - 1);
-    int last = 1;
+    // last_flag: 0 not last; 1 last, partials read past L2 (sc1); 2 last,
+    // every contributor ran on this XCD, partials read from its L2 (sc0).
+    int last = 2;
     if (gf != gl) {
-      last = arrive(&p.counters[b]) == gl - gf;
-      if (last) reset_counter(&p.counters[b]);
+      // Arrival count in the low half, workgroups off their XCD in the high.
+      const int old = arrive_add(&p.counters[b], native ? 1 : 1 + kForeign);
+      last = 0;
+      if ((old & (kForeign - 1)) == gl - gf) {
+        const int Gx = G / kXcds;
+        const bool local = native && old < kForeign && gf / Gx == gl / Gx;
+        last = local ? 2 : 1;
+        reset_counter(&p.counters[b]);
+      }
     }
     last_flag[t] = last;
   }
@@ -683,33 +763,18 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
     const int b = b_first + j;
     const int gf = owner(b * nkb), gl = owner((b + 1) * nkb - 1);
     float* red = acc_lds + (j * kWaves) * TE;
+    // The residual rows go out with the partials: one round trip for both.
+    float xo[TE / kThreads + 1];
+    if constexpr (EPI == DTREE_EPI_RESIDUAL) residual_issue<32, TN>(p, b, xo);
     if (gf != gl) {
       f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
-      int q = gf;
-      for (; q + 4 <= gl + 1; q += 4) {
-        u32x4_t v[4][2];
-#pragma unroll
-        for (int z = 0; z < 4; ++z) {
-          const int off = ((q + z + b) * TE + 8 * t) * 4;
-          v[z][0] = __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kSc1);
-          v[z][1] = __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16, 0, kSc1);
-        }
-#pragma unroll
-        for (int z = 0; z < 4; ++z) {
-          s0 += __builtin_bit_cast(f32x4_t, v[z][0]);
-          s1 += __builtin_bit_cast(f32x4_t, v[z][1]);
-        }
-      }
-      for (; q <= gl; ++q) {
-        const int off = ((q + b) * TE + 8 * t) * 4;
-        s0 += __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kSc1));
-        s1 += __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16, 0, kSc1));
-      }
+      if (last_flag[j] == 2) sum_partials<kSc0>(prs, b, gf, gl, t, s0, s1);
+      else sum_partials<kSc1>(prs, b, gf, gl, t, s0, s1);
       reinterpret_cast<f32x4_t*>(red + 8 * t)[0] = s0;
       reinterpret_cast<f32x4_t*>(red + 8 * t)[1] = s1;
     }
     __syncthreads();
-    tile_epilogue<32, TN, EPI>(p, red, rs, b);
+    tile_epilogue<32, TN, EPI>(p, red, rs, b, EPI == DTREE_EPI_RESIDUAL ? xo : nullptr);
   }
 }
 
@@ -919,22 +984,22 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
   const int tile = blockIdx.x, nkb = p.k >> 6;
   float ssv[kSsBatch];
   ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
-  const uint16_t* xb = p.x + lane * 8;
-  const uint16_t* xlb = LO ? p.x_lo + lane * 8 : nullptr;
-  const uint16_t* wb = p.w + (size_t)tile * nkb * 2048 + lane * 8;
+  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(p.x, p.x_bytes), xlrs = buf_rsrc(p.x_lo, LO ? p.x_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(p.w, p.w_bytes);
+  const unsigned wtile = (unsigned)(tile * nkb * 2048) * 2u;
   const int n = wave < nkb ? (nkb - wave + kWaves - 1) / kWaves : 0;
   u32x4_t wr[kDpDepth][4], xr[kDpDepth][2][4];
+  // Slots past the wave's blocks are refilled with ranged loads that return
+  // zero (same loads on every path, see kOob) and are never consumed.
   auto issue = [&](int s, int j) {
-    if (j < n) {
-      const size_t off = (size_t)(wave + kWaves * j) * 2048;
+    const unsigned off = j < n ? (unsigned)((wave + kWaves * j) * 2048 + lane * 8) * 2u : kOob;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        xr[s][0][i] = ld_u32x4(xb + off + 512 * i);
-        if (LO) xr[s][1][i] = ld_u32x4(xlb + off + 512 * i);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wr[s][i] = ld_u32x4_stream(wb + off + 512 * i);
+    for (int i = 0; i < 4; ++i) {
+      xr[s][0][i] = buf_ld(xrs, off + 1024u * i);
+      if (LO) xr[s][1][i] = buf_ld(xlrs, off + 1024u * i);
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wr[s][i] = buf_ld_stream(wrs, j < n ? wtile + off + 1024u * i : kOob);
   };
   f32x16_t acc;
 #pragma unroll
@@ -954,10 +1019,13 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
           if (LO) acc = mfma32(xr[s][1][i], wr[s][i], acc);
         }
         __builtin_amdgcn_sched_barrier(0);
-        issue(s, j + kDpDepth);
       }
+      issue(s, j + kDpDepth);
     }
   }
+  // The residual rows are in flight during the wave reduction.
+  float xo[TE / kThreads + 1];
+  if constexpr (EPI == DTREE_EPI_RESIDUAL) residual_issue<32, TN>(p, tile, xo);
   // Waves 1..3 park their tiles; wave 0 adds them in wave order into slot 0.
   if (wave > 0) {
     float* my = red + (wave - 1) * TE;
@@ -974,7 +1042,7 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
     for (int r = 0; r < 16; ++r) red[acc_row(r, h) * TN + c] = acc[r];
   }
   __syncthreads();
-  tile_epilogue<32, TN, EPI>(p, red, rs, tile);
+  tile_epilogue<32, TN, EPI>(p, red, rs, tile, EPI == DTREE_EPI_RESIDUAL ? xo : nullptr);
 }
 
 template <bool LO>
@@ -1066,6 +1134,13 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   }
   p.w_sb = a->w_scales;
   DTREE_REQUIRE(!tiled || (a->ldx == a->k && a->rows_padded % 32 == 0), "gemm: tiled x needs ldx == k");
+  // Ranged ring loads address w, w_sb and the activation planes with 32-bit
+  // byte offsets below kOob.
+  const size_t w_bytes = q4 ? (size_t)a->n * a->k / 2 : (size_t)a->n * a->k * 2;
+  DTREE_REQUIRE(w_bytes < kOob, "gemm: weight matrix must be smaller than 2 GiB");
+  p.w_bytes = (unsigned)w_bytes;
+  p.sb_bytes = (unsigned)((size_t)a->n * (a->k / 64) * 4);
+  p.x_bytes = (unsigned)((size_t)32 * a->k * 2);
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR || a->out_layout == DTREE_W_TILED, "gemm: unknown out_layout");
   if (a->out_layout == DTREE_W_TILED && a->out_bf16) {
     const int width = epi == DTREE_EPI_SWIGLU ? a->n / 2 : a->n;
