@@ -92,6 +92,18 @@ __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 *
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
+// Per-row RMSNorm statistics (sums of x^2 over each 32-column tile) are laid
+// out [rows/32][tiles][32]: every 32-row block is one contiguous [tiles][32]
+// array, so kernels that work on one 32-row block address it directly.
+__device__ __forceinline__ size_t ss_index(int t, int m, int tiles) {
+  return ((size_t)(m >> 5) * tiles + t) * 32 + (m & 31);
+}
+// LM-head candidates (per workgroup, per row) are laid out [rows/32][blocks][32]
+// the same way.
+__device__ __forceinline__ size_t cand_index(int blk, int m, int blocks) {
+  return ((size_t)(m >> 5) * blocks + blk) * 32 + (m & 31);
+}
+
 // Element (row r, column k) of a DTREE_W_TILED matrix with `width` columns:
 // [rows/32][width/64][4][64][8], lane l = r%32 + 32*((k%64)/32) of load i.
 __device__ __forceinline__ size_t tiled_index(int r, int k, int width) {

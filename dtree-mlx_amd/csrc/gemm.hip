@@ -209,7 +209,7 @@ __device__ __forceinline__ void ss_issue(const float* ss_in, int ss_tiles, float
 #pragma unroll
   for (int i = 0; i < kSsBatch; ++i) {
     const int t = part + i * TPR;
-    v[i] = buf_ldf(r, t < ss_tiles ? (unsigned)((t * MP + m) * 4) : kOob);
+    v[i] = buf_ldf(r, t < ss_tiles ? (unsigned)(ss_index(t, m, ss_tiles) * 4) : kOob);
   }
 }
 
@@ -227,7 +227,7 @@ __device__ __forceinline__ void ss_finish(const float* ss_in, int ss_tiles, floa
 #pragma unroll
       for (int i = 0; i < kSsBatch; ++i) {
         const int t = base + part + i * TPR;
-        w[i] = t < ss_tiles ? ss_in[(size_t)t * MP + m] : 0.f;
+        w[i] = t < ss_tiles ? ss_in[ss_index(t, m, ss_tiles)] : 0.f;
       }
 #pragma unroll
       for (int i = 0; i < kSsBatch; ++i) s += w[i];
@@ -309,7 +309,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* 
       float sq = xv * xv;
 #pragma unroll
       for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
-      if ((n & 31) == 0) p.ss_out[(size_t)(col >> 5) * MP + m] = sq;
+      if ((n & 31) == 0) p.ss_out[ss_index(col >> 5, m, p.n >> 5)] = sq;
     }
   } else if constexpr (EPI == DTREE_EPI_SWIGLU) {
     // Each 32-column group = 16 gate rows then 16 up rows of 16 FFN features.
@@ -786,7 +786,8 @@ struct LmParams {
   int ntiles;
   const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
   float* logits;
-  int2* cand;  // [gridDim.x][MP] (value bits, index)
+  int2* cand;  // (value bits, index) per (row, workgroup), see cand_index
+  int cand_blocks;
 };
 
 __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
@@ -845,7 +846,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int m = (threadIdx.x + i * kThreads) / TN;
-      p.cand[(size_t)blockIdx.x * MP + m] = make_int2(__float_as_int(bv[i]), bi[i]);
+      p.cand[cand_index(blockIdx.x, m, p.cand_blocks)] = make_int2(__float_as_int(bv[i]), bi[i]);
     }
   }
 }
@@ -1124,6 +1125,31 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   const bool q4 = a->w_layout == DTREE_W_Q4G64;
   const bool tiled = a->w_layout == DTREE_W_TILED || q4;
   DTREE_REQUIRE(a->w_layout == DTREE_W_ROWMAJOR || tiled, "gemm: unknown w_layout");
+  if (q4 && a->rows_padded > 32) {
+    // q4 weights stream through the 32-row kernels, once per 32-row block:
+    // tiled activations, statistics and tiled outputs are contiguous per
+    // block; row-major outputs advance by 32 rows.
+    DTREE_REQUIRE(a->x_layout == DTREE_W_TILED, "gemm: q4 weights need tiled activations");
+    for (int r = 0; r < a->rows_padded / 32; ++r) {
+      DtreeGemmArgs b = *a;
+      b.rows_padded = 32;
+      const size_t xo = (size_t)r * 32 * a->k;
+      b.x = a->x + xo;
+      b.x_lo = a->x_lo ? a->x_lo + xo : nullptr;
+      if (a->out_f32) b.out_f32 = a->out_f32 + (size_t)r * 32 * a->ld_out_f32;
+      if (a->out_bf16) {
+        const size_t oo = (size_t)r * 32 * a->ld_out_bf16;  // tiled: ld_out_bf16 == width
+        b.out_bf16 = a->out_bf16 + oo;
+        b.out_lo = a->out_lo ? a->out_lo + oo : nullptr;
+      }
+      if (a->hidden_out) b.hidden_out = a->hidden_out + (size_t)r * 32 * a->ld_hidden;
+      if (a->ss_in) b.ss_in = a->ss_in + (size_t)r * a->ss_tiles * 32;
+      if (a->ss_out) b.ss_out = a->ss_out + (size_t)r * (a->n / 32) * 32;
+      const int rc = dtree_gemm_bf16(&b, stream);
+      if (rc) return rc;
+    }
+    return DTREE_OK;
+  }
   if (q4) {
     DTREE_REQUIRE(a->x_layout == DTREE_W_TILED && a->rows_padded == 32 && a->split_k <= 0,
                   "gemm: q4 weights need tiled 32-row activations and split_k 0");
@@ -1213,13 +1239,28 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
   p.ss_in = ss_in; p.ss_tiles = ss_tiles; p.inv_norm_dim = 1.0f / (float)hidden; p.eps = eps;
   p.logits = logits; p.cand = reinterpret_cast<int2*>(candidates);
   const int grid = lmhead_grid(p.ntiles);
+  p.cand_blocks = grid;
   DTREE_REQUIRE(emb_layout == DTREE_W_ROWMAJOR || emb_layout == DTREE_W_TILED || emb_layout == DTREE_W_Q4G64,
                 "lmhead: unknown emb_layout");
   if (emb_layout == DTREE_W_Q4G64) {
-    DTREE_REQUIRE(x_layout == DTREE_W_TILED && ldx == hidden && rows_padded == 32 && hidden / 64 <= kSkMaxKb,
-                  "lmhead: q4 embedding needs tiled 32-row x and hidden <= 4096");
+    DTREE_REQUIRE(x_layout == DTREE_W_TILED && ldx == hidden && hidden / 64 <= kSkMaxKb,
+                  "lmhead: q4 embedding needs tiled x and hidden <= 4096");
     DTREE_REQUIRE(emb_scales && ((uintptr_t)emb & 15) == 0, "lmhead: q4 embedding needs emb_scales");
-    launch_lm_q4(p, grid, stream);
+    DTREE_REQUIRE(vocab % 64 == 0, "lmhead: q4 embedding needs vocab % 64 == 0");
+    // One pass of the 32-row kernel per 32-row block (tiled x, statistics and
+    // candidates are contiguous per block; logits rows are row-major). The
+    // kernel walks 64-column tiles; the grid stays the candidate block count
+    // of this row count (workgroups past the tiles write empty candidates).
+    p.ntiles = vocab / 64;
+    for (int r = 0; r < rows_padded / 32; ++r) {
+      LmParams pb = p;
+      pb.x = x + (size_t)r * 32 * hidden;
+      pb.x_lo = x_lo ? x_lo + (size_t)r * 32 * hidden : nullptr;
+      pb.ss_in = ss_in ? ss_in + (size_t)r * ss_tiles * 32 : nullptr;
+      pb.logits = logits ? logits + (size_t)r * 32 * vocab : nullptr;
+      pb.cand = p.cand + (size_t)r * grid * 32;
+      launch_lm_q4(pb, grid, stream);
+    }
     DTREE_LAUNCH_CHECK("lmhead launch");
     return DTREE_OK;
   }

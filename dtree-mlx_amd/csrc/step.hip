@@ -23,7 +23,7 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const DtreeStepDesc* de
   rope_entry(desc, blockIdx.x * 256 + threadIdx.x, rows, half, base, cos_out, sin_out);
 }
 
-// x[m][:] = E[tokens[m]] (rows >= L zero), xg = bf16(x * g), ss[tile][m].
+// x[m][:] = E[tokens[m]] (rows >= L zero), xg = bf16(x * g), per-tile sums of x^2.
 // Blocks [0, H/256) gather; the remaining blocks fill the RoPE table.
 // Element (row, col) of an embedding in DTREE_W_Q4G64 layout, dequantised:
 // scale * q + bias of the row's group col / 64.
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
       float sq = v[j] * v[j];
 #pragma unroll
       for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
-      if (in && n == 0) ss[(size_t)(col >> 5) * MP + m] = sq;
+      if (in && n == 0) ss[ss_index(col >> 5, m, (H + 31) >> 5)] = sq;
     }
   }
 }
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void walk_kernel(DtreeStepDesc* desc, const in
     float v = -__builtin_huge_valf();
     int idx = 0x7fffffff;
     for (int b = lane; b < nblocks; b += 64) {
-      const int2 cv = cand[(size_t)b * MP + m];
+      const int2 cv = cand[cand_index(b, m, nblocks)];
       argmax_merge2(v, idx, __int_as_float(cv.x), cv.y);
     }
 #pragma unroll
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void rownorm_kernel(const float* x, int ldx, i
   __shared__ float rs[128];
   if ((int)threadIdx.x < MP) {
     float s = 0.f;
-    for (int t = 0; t < ss_tiles; ++t) s += ss[t * MP + threadIdx.x];
+    for (int t = 0; t < ss_tiles; ++t) s += ss[ss_index(t, threadIdx.x, ss_tiles)];
     rs[threadIdx.x] = rsqrtf(s / (float)H + eps);
   }
   __syncthreads();

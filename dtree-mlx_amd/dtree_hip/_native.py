@@ -14,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
 MAX_NODES = 128
 MASK_WORDS = 4
 PAGE = 64
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 EPI_STORE_F32 = 0
 EPI_RESIDUAL = 1

@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define DTREE_ABI_VERSION 3
+#define DTREE_ABI_VERSION 4
 
 #define DTREE_OK 0
 #define DTREE_E_ARG (-1)      /* bad shape / pointer / enum */
@@ -88,7 +88,10 @@ typedef struct DtreeStepDesc {
 /*
  * Skinny bf16 GEMM Y = X W^T for up to 128 rows (tree nodes), fp32 accumulate
  * on gfx950 MFMA 32x32x16. rs[m] is the RMSNorm row scale
- * rsqrt(sum_t ss_in[t][m] / norm_dim + eps) when ss_in != NULL, else 1.
+ * rsqrt(sum_t ss(t, m) / norm_dim + eps) when ss_in != NULL, else 1, where
+ * ss(t, m) = sum over columns 32t .. 32t+31 of row m's x^2, stored at
+ * ss_in[((m / 32) * ss_tiles + t) * 32 + m % 32] (every 32-row block is one
+ * contiguous [ss_tiles][32] array; for 32 rows this is [ss_tiles][32]).
  * Replaces the nn.Linear projections of the tree block
  * (qwen3_tree.py:50-52, 78, 82) with the RMSNorms of qwen3_tree.py:47, 81
  * folded in (norm weight folded into the producer's bf16 X, row scale here).
@@ -99,14 +102,15 @@ typedef struct DtreeGemmArgs {
   int32_t x_layout;       /* DTREE_W_ROWMAJOR, or DTREE_W_TILED with ldx = k */
   int32_t ldx;
   int32_t rows_padded;    /* 32, 64, 96 or 128                             */
-  const uint16_t* w;      /* bf16 [n][k] (nn.Linear layout); Q4G64: packed q */
+  const uint16_t* w;      /* bf16 [n][k] (nn.Linear layout); Q4G64: packed q
+                             (tiled x; above 32 rows one pass per 32 rows) */
   int32_t w_layout;       /* DTREE_W_ROWMAJOR, DTREE_W_TILED or DTREE_W_Q4G64 */
   int32_t n, k;           /* k % 64 == 0; n % 64 == 0 (% 32 above 64 rows) */
   int32_t epilogue;       /* DTREE_EPI_*                                   */
   int32_t split_k;        /* >= 1 split-K; 0 = automatic; tiled 32 rows only:
                              -1 one workgroup per 32-column tile (bf16),
                              -2 stream-K schedule                          */
-  const float* ss_in;     /* [ss_tiles][rows_padded] or NULL               */
+  const float* ss_in;     /* [rows_padded/32][ss_tiles][32] or NULL        */
   int32_t ss_tiles;
   int32_t norm_dim;       /* divisor of the row mean square                */
   float eps;
@@ -116,7 +120,7 @@ typedef struct DtreeGemmArgs {
   int32_t out_layout;     /* layout of out_bf16 / out_lo (TILED: ld = width) */
   int32_t ld_out_bf16;
   const uint16_t* next_norm;  /* RESIDUAL: weight of the following RMSNorm */
-  float* ss_out;              /* RESIDUAL: [n/32][rows_padded] sum of x^2  */
+  float* ss_out;              /* RESIDUAL: [rows_padded/32][n/32][32]      */
   uint16_t* hidden_out; int32_t ld_hidden; /* RESIDUAL: optional bf16 copy */
   void* workspace; size_t workspace_bytes; /* split-K partials + counters  */
   const uint16_t* w_scales;   /* Q4G64: (scale, bias) pairs, else NULL     */
@@ -200,9 +204,11 @@ int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
  * as adapters.py:78-81): per row m, argmax_v rs[m] * (x[m] . E[v]).
  * x = x + x_lo (split pair, x_lo optional); E in layout emb_layout
  * (DTREE_W_Q4G64: the quantised tied embedding with its (scale, bias) pairs in
- * emb_scales, 32 tiled rows, hidden <= 4096; adapters.py:28-85 is the
- * reference's q4 LM-head argmax). Writes per-workgroup (value, index) candidates to `candidates`
- * ([grid][rows_padded] float2-like pairs); dtree_accept_walk reduces them.
+ * emb_scales, tiled rows (one pass per 32 rows), hidden <= 4096;
+ * adapters.py:28-85 is the reference's q4 LM-head argmax). Statistics ss_in
+ * as for DtreeGemmArgs. Writes per-workgroup (value, index) candidates to
+ * `candidates` (pairs of row m, workgroup b at ((m / 32) * blocks + b) * 32 +
+ * m % 32, blocks = dtree_lmhead_candidate_blocks); dtree_accept_walk reduces them.
  * logits (optional, [rows_padded][vocab] fp32) receives every logit.
  */
 size_t dtree_lmhead_candidates_bytes(int32_t rows_padded);

@@ -31,7 +31,8 @@ def _gemm(x, w, epi, split, ws, **kw):
     a.epilogue = epi; a.split_k = split
     ss = kw.get("ss_in")
     a.ss_in = ss.data_ptr() if ss is not None else None
-    a.ss_tiles = ss.shape[0] if ss is not None else 0
+    # statistics [rows/32][tiles][32] (or [tiles][32] for 32 rows)
+    a.ss_tiles = (ss.shape[-2] if ss.dim() == 3 else ss.shape[0]) if ss is not None else 0
     a.norm_dim = kw.get("norm_dim", 1); a.eps = 1e-6
     for name in ("out_f32", "out_bf16"):
         t = kw.get(name)
@@ -62,12 +63,12 @@ def test_gemm_store_f32_rowscale(gpu_device, MP, L, split, tiled):
     N_, K = 256, 1024
     x = _rows(MP, L, K, g, gpu_device)
     w = torch.from_numpy(g.standard_normal((N_, K)).astype(np.float32) * 0.05).to(torch.bfloat16).to(gpu_device)
-    ss = torch.from_numpy(np.abs(g.standard_normal((5, MP))).astype(np.float32)).to(gpu_device)
+    ss = torch.from_numpy(np.abs(g.standard_normal((MP // 32, 5, 32))).astype(np.float32)).to(gpu_device)
     out = torch.zeros(MP, N_, device=gpu_device)
     ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, N_, K, split), dtype=torch.uint8, device=gpu_device)
     _gemm(x, w, N.EPI_STORE_F32, split, ws, ss_in=ss, norm_dim=K, out_f32=out, tiled=tiled)
     torch.cuda.synchronize()
-    rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(0) / K + 1e-6)
+    rs = 1.0 / np.sqrt(ss.cpu().numpy().sum(1).reshape(MP) / K + 1e-6)  # row m = 32 * block + lane
     ref = (bf16_f32(x).astype(np.float64) @ bf16_f32(w).T.astype(np.float64)) * rs[:, None]
     np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
     assert int(ws[: (N_ // 32) * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
@@ -402,9 +403,9 @@ def _lmhead(x, E, dev, logits=None, ss=None, layout=0):
     return cand, lib.dtree_lmhead_candidate_blocks(E.shape[0], MP)
 
 
-def _walk(cand, nblocks, desc, dev):
+def _walk(cand, nblocks, desc, dev, rows=32):
     res = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32, device=dev)
-    N.check(N.lib().dtree_accept_walk(desc.data_ptr(), cand.data_ptr(), nblocks, 32, res.data_ptr(), stream()))
+    N.check(N.lib().dtree_accept_walk(desc.data_ptr(), cand.data_ptr(), nblocks, rows, res.data_ptr(), stream()))
     torch.cuda.synchronize()
     r = res.cpu().numpy()
     n, bonus, L = int(r[0]), int(r[1]), int(r[2])
@@ -434,6 +435,38 @@ def test_lmhead_argmax_and_logits(gpu_device, V, tiled):
         if margin[m] > 1e-3:
             assert post[m] == want[m]
     assert post == list(np.argmax(logits.cpu().numpy()[:L], axis=-1))
+
+
+@pytest.mark.parametrize("tiled", [False, True])
+def test_lmhead_argmax_96_rows(gpu_device, tiled):
+    """65 tree rows (rows_padded 96, three 32-row blocks of candidates): every
+    row's argmax through the walk equals the fp64 product's where the top-2
+    margin is clear, and the RMSNorm statistics of every block apply."""
+    g = np.random.default_rng(965)
+    V, H, L, MP = 4096, 1024, 65, 96
+    x = _rows(MP, L, H, g, gpu_device)
+    E = torch.from_numpy((g.standard_normal((V, H)) * 0.02).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    ss_np = np.abs(g.standard_normal((MP // 32, H // 32, 32))).astype(np.float32) + 0.5
+    ss = torch.from_numpy(ss_np).to(gpu_device)
+    logits = torch.zeros(MP, V, device=gpu_device)
+    lib = N.lib()
+    cand = torch.zeros(lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=gpu_device)
+    xin, Ein = (tile_weight(x), tile_weight(E)) if tiled else (x, E)
+    lay = N.W_TILED if tiled else N.W_ROWMAJOR
+    N.check(lib.dtree_lmhead_argmax(xin.data_ptr(), None, lay, H, MP, Ein.data_ptr(), lay, None, V, H,
+                                    ss.data_ptr(), H // 32, 1e-6, logits.data_ptr(), cand.data_ptr(), stream()),
+            "lmhead 96")
+    nb = lib.dtree_lmhead_candidate_blocks(V, MP)
+    parents = [-1] + [(i - 1) // 2 for i in range(1, L)]
+    desc = device_desc([0] * L, list(range(L)), parents, 0, gpu_device)
+    _, _, post = _walk(cand, nb, desc, gpu_device, rows=MP)
+    rs = 1.0 / np.sqrt(ss_np.sum(1).reshape(MP) / H + 1e-6)
+    ref = (bf16_f32(x).astype(np.float64) @ bf16_f32(E).T.astype(np.float64)) * rs[:, None]
+    np.testing.assert_allclose(logits.cpu().numpy()[:L], ref[:L], rtol=1e-4, atol=1e-4)
+    assert post == list(np.argmax(logits.cpu().numpy()[:L], axis=-1))
+    srt = np.sort(ref[:L], axis=-1)
+    clear = srt[:, -1] - srt[:, -2] > 1e-3
+    assert np.array_equal(np.asarray(post)[clear], np.argmax(ref[:L], axis=-1)[clear])
 
 
 def test_lmhead_first_index_on_tie(gpu_device):

@@ -128,6 +128,69 @@ def test_q4_gemm_residual_and_swiglu(gpu_device):
     assert np.all(np.abs(bf16_f32(act) - ref) <= 1e-2 * np.abs(ref) + 1e-5 * np.abs(ref).max())
 
 
+def _x96(L, k, g, dev):
+    xf = np.zeros((96, k), np.float32)
+    xf[:L] = g.standard_normal((L, k))
+    hi = torch.from_numpy(xf).to(torch.bfloat16)
+    lo = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16)
+    return tile_weight(hi.to(dev)), tile_weight(lo.to(dev)), hi.double().numpy() + lo.double().numpy()
+
+
+def test_q4_gemm_96_rows(gpu_device):
+    """65 tree rows (rows_padded 96): q4 GEMMs run one pass per 32-row block.
+    Row-block-major statistics in and out, residual + next norm, SwiGLU into a
+    tiled output, against the q4 oracle on every row."""
+    g = np.random.default_rng(96)
+    H, F, L, MP = 512, 768, 65, 96
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, 2 * F, H, 0) + (1 << 20), dtype=torch.uint8,
+                     device=gpu_device)
+    # fp32 store with a row scale from [3][H/32][32] statistics
+    wq, s, b = o4.random_q4(F, H, g)
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    xt, xlt, xin = _x96(L, H, g, gpu_device)
+    ss_np = (np.abs(g.standard_normal((3, H // 32, 32))) + 0.5).astype(np.float32)
+    ss = torch.from_numpy(ss_np).to(gpu_device)
+    out = torch.zeros(MP, F, device=gpu_device)
+    a = _args(xt, xlt, wt.to(gpu_device), sb.to(gpu_device), F, H, N.EPI_STORE_F32, ws)
+    a.rows_padded = MP
+    a.ss_in = ss.data_ptr(); a.ss_tiles = H // 32; a.norm_dim = H; a.eps = 1e-6
+    a.out_f32 = out.data_ptr(); a.ld_out_f32 = F
+    N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 gemm 96 rows")
+    torch.cuda.synchronize()
+    rs = 1.0 / np.sqrt(ss_np.sum(1).reshape(MP) / H + 1e-6)
+    ref = o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b)) * rs[:, None]
+    got = out.cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    assert not got[L:].any()
+    # residual + next-norm statistics, tiled xg output
+    wq, s, b = o4.random_q4(H, F, g)
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    xt, xlt, xin = _x96(L, F, g, gpu_device)
+    res = torch.zeros(MP, H)
+    res[:L] = torch.from_numpy(g.standard_normal((L, H)).astype(np.float32))
+    res = res.to(gpu_device)
+    res0 = res.cpu().double().numpy()
+    gn = torch.from_numpy((1 + 0.1 * g.standard_normal(H)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    xg = torch.zeros(2, MP * H, dtype=torch.bfloat16, device=gpu_device)
+    sso = torch.zeros(3, H // 32, 32, device=gpu_device)
+    a = _args(xt, xlt, wt.to(gpu_device), sb.to(gpu_device), H, F, N.EPI_RESIDUAL, ws)
+    a.rows_padded = MP
+    a.out_f32 = res.data_ptr(); a.ld_out_f32 = H
+    a.out_bf16 = xg[0].data_ptr(); a.out_lo = xg[1].data_ptr(); a.ld_out_bf16 = H; a.out_layout = N.W_TILED
+    a.next_norm = gn.data_ptr(); a.ss_out = sso.data_ptr()
+    N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 residual 96 rows")
+    torch.cuda.synchronize()
+    ref = res0 + o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b))
+    got = res.cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    from dtree_hip.weights import untile_weight
+    xg_rows = untile_weight(xg[0].view(MP, H)).float() + untile_weight(xg[1].view(MP, H)).float()
+    want = torch.from_numpy(got) * gn.float().cpu()
+    assert torch.allclose(xg_rows.cpu(), want, rtol=2 ** -15, atol=1e-30)
+    exp_ss = (got.astype(np.float64) ** 2).reshape(3, 32, H // 32, 32).sum(-1).transpose(0, 2, 1)
+    np.testing.assert_allclose(sso.cpu().numpy(), exp_ss, rtol=1e-5, atol=1e-5)
+
+
 def test_q4_rejects_bad_arguments(gpu_device):
     a = N.GemmArgs()
     buf = torch.zeros(1 << 16, dtype=torch.uint8, device=gpu_device)
@@ -182,6 +245,36 @@ def test_q4_lmhead_argmax_and_logits(gpu_device):
     exact = np.argmax(got, axis=-1)
     assert best == exact.tolist()
     assert best[3] == 5
+
+
+def test_q4_lmhead_96_rows_through_walk(gpu_device):
+    """q4 LM head over 65 tree rows (one pass per 32-row block): the walk's
+    posterior over all 65 rows equals the argmax of the returned logits, which
+    match the q4 oracle."""
+    g = np.random.default_rng(965)
+    V, H, L, MP = 8192, 1024, 65, 96
+    wq, s, b = o4.random_q4(V, H, g)
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    xt, xlt, xin = _x96(L, H, g, gpu_device)
+    lib = N.lib()
+    cand = torch.zeros(lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=gpu_device)
+    logits = torch.zeros(MP, V, device=gpu_device)
+    N.check(lib.dtree_lmhead_argmax(xt.data_ptr(), xlt.data_ptr(), N.W_TILED, H, MP, wt.to(gpu_device).data_ptr(),
+                                    N.W_Q4G64, sb.to(gpu_device).data_ptr(), V, H, None, 0, 1e-6,
+                                    logits.data_ptr(), cand.data_ptr(), stream()), "q4 lmhead 96")
+    from gpu_util import device_desc
+    parents = [-1] + [(i - 1) // 3 for i in range(1, L)]
+    desc = device_desc([0] * L, list(range(L)), parents, 0, gpu_device)
+    res = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32, device=gpu_device)
+    N.check(lib.dtree_accept_walk(desc.data_ptr(), cand.data_ptr(), lib.dtree_lmhead_candidate_blocks(V, MP), MP,
+                                  res.data_ptr(), stream()), "walk 96")
+    torch.cuda.synchronize()
+    ref = o4.q4_matmul(xin[:L], wq, bf16_to_f32(s), bf16_to_f32(b))
+    got = logits[:L].cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    r = res.cpu().numpy()
+    post = list(r[3 + N.MAX_NODES:3 + N.MAX_NODES + L])
+    assert int(r[2]) == L and post == list(np.argmax(got, axis=-1))
 
 
 def test_q4_embedding_gather(gpu_device):
