@@ -1,10 +1,12 @@
 // Ancestor-masked GQA tree attention over a paged bf16 KV prefix.
 //
-// Work split: the keys of one query head are cut into chunks. Chunk 0 is the
-// tree itself (the L new keys, ancestor-or-self mask); chunks 1.. are runs of
-// CK prefix keys (fully visible): a 64-key page for head_dim 128, half a page
-// for head_dim 256 (same registers per wave). A workgroup has four waves, one
-// chunk each, so workgroup `split` of a head owns chunks 4*split .. 4*split+3.
+// Work split: a workgroup serves one 32-row block of tree queries (rows
+// 32*rb .. 32*rb+31) of one query head. The keys are cut into chunks: chunks
+// 0 .. NT-1 are the tree itself in 32-key blocks (NT = rows_padded / 32;
+// ancestor-or-self mask, word tc of each query's bitset), chunks NT.. are runs
+// of CK prefix keys (fully visible): a 64-key page for head_dim 128, half a
+// page for head_dim 256 (same registers per wave). A workgroup has four
+// waves, one chunk each, so workgroup `split` owns chunks 4*split .. 4*split+3.
 //
 // Two head geometries are compiled: Qwen3 (head_dim 128, full RoPE) and the
 // gated attention of Qwen3.5 (head_dim 256, RoPE on the first 64 dims, q_proj
@@ -51,6 +53,7 @@ struct AttnParams {
   const DtreeStepDesc* desc;
   uint16_t* out; uint16_t* out_lo; int ld_out; int out_tiled;
   int Hq, Hkv, max_chunks, splits;
+  int tree_chunks;  // 32-key tree chunks = 32-row query blocks = rows_padded / 32
   float scale_log2;
   int write_cache;
   float* part; int* counters;
@@ -212,25 +215,30 @@ __device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, bool norm, 
   for (int j = 0; j < D / 16; ++j) split8(q[j], qf[j], ql[j]);
 }
 
-// The tree chunk: q, k (norm + RoPE) and v of node c come from the fused qkv
-// row; k and v^T are staged in LDS (this wave's private region) for the MFMA
-// operand layouts, one 32-key block is scored with the ancestor-or-self mask,
-// and finally k/v are written to the cache rows P + c (one head per group).
+// Tree chunk tc: k (norm + RoPE) and v of nodes 32*tc .. 32*tc+31 come from
+// the fused qkv rows and are staged in LDS (this wave's private region) for
+// the MFMA operand layouts; the block's 32 query rows are scored against them
+// with word tc of their ancestor-or-self masks, and k/v are written to the
+// cache rows P + node (once: query block 0, first head of the group).
 // q, k and v are finished one after the other, so at most one raw head row is
 // live in registers (head_dim 256 rows are 128 floats per lane pair).
 template <int D, int R>
 __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& qr, int hq, int g, int G, int P,
-                                           int L, int c, int h, uint16_t* ks, uint16_t* vt, float& m_run,
-                                           float& l_run, f32x16_t (&o)[D / 32]) {
+                                           int L, int tc, int qrow, bool write_rows, int c, int h, uint16_t* ks,
+                                           uint16_t* vt, float& m_run, float& l_run, f32x16_t (&o)[D / 32]) {
   constexpr int NJ = D / 16, ND = D / 32;
   constexpr int KS = D + 8, VS = 32 + 8;
   constexpr int half_r = R / 2;
-  const float* row = p.qkv + (size_t)c * p.ld_qkv;
-  const float* cosr = p.rope_cos + c * half_r;
-  const float* sinr = p.rope_sin + c * half_r;
-  const uint32_t anc = p.desc->ancestors[c][0];
+  // Lane (c, h) stages key node 32*tc + c and owns query row qrow.
+  const int node = 32 * tc + c;
+  const float* row = p.qkv + (size_t)node * p.ld_qkv;
+  const float* cosr = p.rope_cos + node * half_r;
+  const float* sinr = p.rope_sin + node * half_r;
+  const uint32_t anc = p.desc->ancestors[qrow][tc];
   u32x4_t qf[NJ], ql[NJ];
-  if constexpr (D > 128) row_issue<D, R>(qr, row + hq * p.q_stride, p.q_norm, cosr, sinr, h);
+  if constexpr (D > 128)
+    row_issue<D, R>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * half_r,
+                    p.rope_sin + qrow * half_r, h);
   q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
   u32x4_t kf8[NJ], vf8[NJ];
   {
@@ -247,7 +255,7 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
     row_finish<D, R>(vr, false, false, 0.f, vv);
     pack_frag<D>(vv, vf8);
   }
-  if (c >= L) {
+  if (node >= L) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) vf8[j] = u32x4_t{0u, 0u, 0u, 0u};
   }
@@ -276,7 +284,7 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int t = 16 * (r >> 3) + 8 * h + (r & 7);
-    const bool ok = c < L && t < L && ((anc >> t) & 1u);
+    const bool ok = qrow < L && 32 * tc + t < L && ((anc >> t) & 1u);
     s[0][r] = ok ? s[0][r] * p.scale_log2 : kNeg;
   }
   softmax_fresh<1>(s, m_run, l_run);
@@ -288,8 +296,8 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
       va[db] = *reinterpret_cast<const u32x4_t*>(&vt[(32 * db + c) * VS + 16 * s2 + 8 * h]);
     pv_step<ND>(s[0], s2, va, o);
   }
-  if (p.write_cache && (hq % G) == 0 && c < L) {
-    const int pos = P + c;
+  if (p.write_cache && (hq % G) == 0 && write_rows && node < L) {
+    const int pos = P + node;
     const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
     uint16_t* krow = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off) * D;
     uint16_t* vcol = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off;
@@ -312,14 +320,14 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
 // hold stale or non-finite data there.
 template <int D, int R>
 __device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>& qr, int page, int hq, int g, int P,
-                                             int chunk, int c, int h, float& m_run, float& l_run,
+                                             int pc, int qrow, int c, int h, float& m_run, float& l_run,
                                              f32x16_t (&o)[D / 32]) {
   constexpr int NJ = D / 16, ND = D / 32;
   constexpr int CK = chunk_keys(D), NB = CK / 32;
   if constexpr (D > 128)
-    row_issue<D, R>(qr, p.qkv + (size_t)c * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + c * (R / 2),
-                    p.rope_sin + c * (R / 2), h);
-  const int k_begin = (chunk - 1) * CK;
+    row_issue<D, R>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * (R / 2),
+                    p.rope_sin + qrow * (R / 2), h);
+  const int k_begin = pc * CK;  // prefix chunk pc: keys pc*CK ..
   const int k_end = min(k_begin + CK, P);
   const int po = k_begin % DTREE_PAGE;
   const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po + swap_bits23(c)) * D;
@@ -372,7 +380,8 @@ __device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>&
     }
 }
 
-template <int D, int R, bool GATE>
+// TB: tree chunks the LDS staging is sized for (1 for 32 rows, 4 up to 128).
+template <int D, int R, bool GATE, int TB>
 __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   constexpr int ND = D / 32;  // 32-dim blocks of O^T
   constexpr int KS = D + 8;   // padded LDS row of tree K
@@ -383,13 +392,14 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   constexpr int kStage = (32 * KS + D * VS) * 2;
   constexpr int kMerge = kWaves * kWaveMerge * 4;
   constexpr int CK = chunk_keys(D);
-  __shared__ __align__(16) unsigned char lds[kStage > kMerge ? kStage : kMerge];
+  __shared__ __align__(16) unsigned char lds[TB * kStage > kMerge ? TB * kStage : kMerge];
   __shared__ int s_last;
 
-  // blockIdx -> (split, kv group, head in group): the G heads of one (split,
-  // group) pair share blockIdx % 8, i.e. one XCD.
-  const int G = p.Hq / p.Hkv;
-  const int bid = blockIdx.x;
+  // blockIdx -> (query block, split, kv group, head in group): the G heads of
+  // one (split, group) pair share blockIdx % 8, i.e. one XCD.
+  const int G = p.Hq / p.Hkv, NT = p.tree_chunks;
+  const int per_block = (int)gridDim.x / NT;  // workgroups per query block (a multiple of 8)
+  const int rb = blockIdx.x / per_block, bid = blockIdx.x % per_block;
   const int pair = (bid / (8 * G)) * 8 + (bid & 7);
   if (pair >= p.splits * p.Hkv) return;
   const int g = pair % p.Hkv, split = pair / p.Hkv;
@@ -398,6 +408,7 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int chunk = split * kWaves + wave;
+  const int qrow = 32 * rb + c;  // this lane's query row
   // Loads that do not depend on the step descriptor go out first, so their
   // latency overlaps the descriptor read: this lane's q row (values, norm
   // weights, RoPE) and the page of this wave's prefix chunk.
@@ -405,17 +416,32 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   // descriptor read it would spill.)
   HeadRow<D, R> qr;
   if constexpr (D <= 128)
-    row_issue<D, R>(qr, p.qkv + (size_t)c * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + c * (R / 2),
-                    p.rope_sin + c * (R / 2), h);
-  const int page = (chunk >= 1 && chunk < p.max_chunks) ? p.page_table[(chunk - 1) * CK / DTREE_PAGE] : 0;
+    row_issue<D, R>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * (R / 2),
+                    p.rope_sin + qrow * (R / 2), h);
+  const int page = (chunk >= NT && chunk < p.max_chunks) ? p.page_table[(chunk - NT) * CK / DTREE_PAGE] : 0;
 
   const int P = p.desc->past_length, L = p.desc->num_nodes;
-  const int nchunks = 1 + (P + CK - 1) / CK;
+  const int nchunks = NT + (P + CK - 1) / CK;
   // A descriptor beyond the grid's capacity (P > max_past_length) or with more
-  // than 32 rows leaves the output untouched instead of indexing past buffers.
-  if (nchunks > p.max_chunks || L > 32 || L < 1) return;
+  // rows than rows_padded leaves the output untouched instead of indexing past
+  // buffers.
+  if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;
   const int nsplit = (nchunks + kWaves - 1) / kWaves;
   if (split >= nsplit) return;
+  if (32 * rb >= L) {
+    // Query block past the tree: its output rows are zero (split 0 writes).
+    if (split == 0) {
+      const int q = threadIdx.x >> 3;
+      for (int dd = (threadIdx.x & 7) * 8; dd < D; dd += 64) {
+        const int col = hq * D + dd;
+        const int row = 32 * rb + q;
+        const size_t oi = p.out_tiled ? tiled_index(row, col, p.ld_out) : (size_t)row * p.ld_out + col;
+        *reinterpret_cast<u32x4_t*>(p.out + oi) = u32x4_t{0u, 0u, 0u, 0u};
+        if (p.out_lo) *reinterpret_cast<u32x4_t*>(p.out_lo + oi) = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+    return;
+  }
 
   float m_run = kNeg, l_run = 0.f;
   f32x16_t o[ND];
@@ -424,11 +450,14 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
 
-  if (chunk == 0) {
-    uint16_t* ks = reinterpret_cast<uint16_t*>(lds);
-    tree_chunk<D, R>(p, qr, hq, g, G, P, L, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+  if (chunk < NT) {
+    // Tree chunks are waves 0 .. NT-1 of split 0, each with its own staging.
+    if (32 * chunk < L) {
+      uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)chunk * kStage);
+      tree_chunk<D, R>(p, qr, hq, g, G, P, L, chunk, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+    }
   } else if (chunk < nchunks) {
-    prefix_chunk<D, R>(p, qr, page, hq, g, P, chunk, c, h, m_run, l_run, o);
+    prefix_chunk<D, R>(p, qr, page, hq, g, P, chunk - NT, qrow, c, h, m_run, l_run, o);
   }
 
   // LDS merge of the four waves, 128 head dims per pass. The first barrier
@@ -476,7 +505,8 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     // Workgroup partial, laid out [i][thread] so both the stores here and the
     // loads of the combining workgroup are coalesced.
     const size_t stride = (size_t)32 * D + 64;
-    float* part = p.part + ((size_t)hq * p.splits + split) * stride;
+    const int hb = hq * NT + rb;  // (head, query block)
+    float* part = p.part + ((size_t)hb * p.splits + split) * stride;
 #pragma unroll
     for (int i = 0; i < kDims; ++i) st_coherent(part + (size_t)i * 64 * kWaves + t, acc[i]);
     if ((t & 7) == 0) {
@@ -485,16 +515,16 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     }
     wait_stores_done();
     __syncthreads();
-    if (t == 0) s_last = arrive(&p.counters[hq]) == nsplit - 1;
+    if (t == 0) s_last = arrive(&p.counters[hb]) == nsplit - 1;
     __syncthreads();
     if (!s_last) return;
-    if (t == 0) reset_counter(&p.counters[hq]);
+    if (t == 0) reset_counter(&p.counters[hb]);
 
     // Partials are read kSb splits at a time (all loads of a batch in flight
     // together) with a running max: one memory round trip per batch instead
     // of two per split.
     constexpr int kSb = 128 / kDims;  // 8 splits per batch at head_dim 128, 4 at 256
-    const float* base = p.part + (size_t)hq * p.splits * stride;
+    const float* base = p.part + (size_t)hb * p.splits * stride;
     float Ms = kNeg;
 #pragma unroll
     for (int i = 0; i < kDims; ++i) acc[i] = 0.f;
@@ -528,16 +558,17 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     }
   }
 
-  const float inv = (q < L && tot > 0.f) ? 1.0f / tot : 0.f;
+  const int orow = 32 * rb + q;  // output row of thread t
+  const float inv = (orow < L && tot > 0.f) ? 1.0f / tot : 0.f;
 #pragma unroll
   for (int i0 = 0; i0 < kDims; i0 += 8) {
     const int dd = (i0 / 16) * kMergeDims + d0 + (i0 % 16);  // head dim of acc[i0]
     float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = q < L ? acc[i0 + i] * inv : 0.f;
-    if (GATE && q < L) {
+    for (int i = 0; i < 8; ++i) y[i] = orow < L ? acc[i0 + i] * inv : 0.f;
+    if (GATE && orow < L) {
       // o_proj input = attention * sigmoid(gate), gate = q_proj row dims D.. of the head
-      const float* gp = p.qkv + (size_t)q * p.ld_qkv + hq * p.q_stride + D + dd;
+      const float* gp = p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D + dd;
       const f32x4_t g0 = *reinterpret_cast<const f32x4_t*>(gp);
       const f32x4_t g1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
 #pragma unroll
@@ -549,7 +580,7 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     u32x4_t hi, lo;
     split8(y, hi, lo);
     const int col = hq * D + dd;
-    const size_t oi = p.out_tiled ? tiled_index(q, col, p.ld_out) : (size_t)q * p.ld_out + col;
+    const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
     *reinterpret_cast<u32x4_t*>(p.out + oi) = hi;
     if (p.out_lo) *reinterpret_cast<u32x4_t*>(p.out_lo + oi) = lo;
   }
@@ -559,17 +590,22 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
 
 using namespace dtree;
 
-static int attn_max_chunks(int head_dim, int max_past) {
+static int attn_max_chunks(int head_dim, int max_past, int nt) {
   const int ck = chunk_keys(head_dim);
-  return 1 + (max_past + ck - 1) / ck;
+  return nt + (max_past + ck - 1) / ck;
 }
-static int attn_splits(int head_dim, int max_past) { return (attn_max_chunks(head_dim, max_past) + kWaves - 1) / kWaves; }
+static int attn_splits(int head_dim, int max_past, int nt) {
+  return (attn_max_chunks(head_dim, max_past, nt) + kWaves - 1) / kWaves;
+}
 
-extern "C" size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length) {
-  if (num_heads <= 0 || head_dim <= 0 || max_past_length < 0) return 0;
+extern "C" size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length,
+                                                  int32_t rows_padded) {
+  if (num_heads <= 0 || head_dim <= 0 || max_past_length < 0 || rows_padded <= 0 || rows_padded % 32) return 0;
+  const int nt = rows_padded / 32;
   const size_t stride = (size_t)32 * head_dim + 64;
-  return (((size_t)num_heads * sizeof(int) + 255) & ~(size_t)255) +
-         (size_t)num_heads * attn_splits(head_dim, max_past_length) * stride * sizeof(float);
+  const size_t hb = (size_t)num_heads * nt;  // (head, query block) pairs
+  return ((hb * sizeof(int) + 255) & ~(size_t)255) +
+         hb * attn_splits(head_dim, max_past_length, nt) * stride * sizeof(float);
 }
 
 extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
@@ -582,7 +618,9 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   const bool gated = a->gated != 0;
   DTREE_REQUIRE((D == 128 && R == 128 && !gated) || (D == 256 && R == 64 && gated),
                 "attention: compiled geometries are head_dim 128 (full RoPE) and gated head_dim 256 (rope_dims 64)");
-  DTREE_REQUIRE(a->rows_padded == 32, "attention: trees of up to 32 nodes (rows_padded 32)");
+  DTREE_REQUIRE(a->rows_padded == 32 || a->rows_padded == 64 || a->rows_padded == 96 || a->rows_padded == 128,
+                "attention: rows_padded must be 32, 64, 96 or 128");
+  const int nt = a->rows_padded / 32;
   DTREE_REQUIRE(a->num_kv_heads > 0 && a->num_heads % a->num_kv_heads == 0, "attention: num_heads % num_kv_heads");
   DTREE_REQUIRE(a->max_past_length >= 0 && a->max_past_length <= kMaxPast, "attention: max_past_length beyond 16384");
   const int q_stride = gated ? 2 * D : D;
@@ -592,7 +630,8 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
                 "attention: ld_out below num_heads * head_dim or not a multiple of 8");
   DTREE_REQUIRE(((uintptr_t)a->out & 15) == 0 && ((uintptr_t)a->out_lo & 15) == 0 && ((uintptr_t)a->qkv & 15) == 0,
                 "attention: qkv, out and out_lo must be 16-byte aligned");
-  DTREE_REQUIRE(a->workspace_bytes >= dtree_attention_workspace_bytes(a->num_heads, D, a->max_past_length),
+  DTREE_REQUIRE(a->workspace_bytes >= dtree_attention_workspace_bytes(a->num_heads, D, a->max_past_length,
+                                                                      a->rows_padded),
                 "attention: workspace too small");
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
                     (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * D && a->ld_out % 64 == 0),
@@ -605,19 +644,24 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
   p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
   p.out_tiled = a->out_layout == DTREE_W_TILED;
-  p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.max_chunks = attn_max_chunks(D, a->max_past_length);
-  p.splits = attn_splits(D, a->max_past_length);
+  p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.tree_chunks = nt;
+  p.max_chunks = attn_max_chunks(D, a->max_past_length, nt);
+  p.splits = attn_splits(D, a->max_past_length, nt);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.counters = reinterpret_cast<int*>(a->workspace);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) +
-                                    (((size_t)a->num_heads * sizeof(int) + 255) & ~(size_t)255));
+                                    (((size_t)a->num_heads * nt * sizeof(int) + 255) & ~(size_t)255));
   const int G = p.Hq / p.Hkv;
   const int pairs = p.splits * p.Hkv;
-  const int grid = ((pairs + 7) / 8) * 8 * G;
-  if (D == 128)
-    tree_attn_kernel<128, 128, false><<<grid, 64 * kWaves, 0, stream>>>(p);
-  else
-    tree_attn_kernel<256, 64, true><<<grid, 64 * kWaves, 0, stream>>>(p);
+  const int grid = ((pairs + 7) / 8) * 8 * G * nt;  // nt query blocks of ((pairs+7)/8)*8*G workgroups
+  const bool one = nt == 1;
+  if (D == 128) {
+    if (one) tree_attn_kernel<128, 128, false, 1><<<grid, 64 * kWaves, 0, stream>>>(p);
+    else tree_attn_kernel<128, 128, false, 4><<<grid, 64 * kWaves, 0, stream>>>(p);
+  } else {
+    if (one) tree_attn_kernel<256, 64, true, 1><<<grid, 64 * kWaves, 0, stream>>>(p);
+    else tree_attn_kernel<256, 64, true, 4><<<grid, 64 * kWaves, 0, stream>>>(p);
+  }
   DTREE_LAUNCH_CHECK("attention launch");
   return DTREE_OK;
 }

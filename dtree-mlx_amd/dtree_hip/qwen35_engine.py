@@ -57,7 +57,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         self.act = torch.zeros(2, MP, c.intermediate_size, dtype=bf16, device=dev)
         self.rope_cos = torch.zeros(MP, c.rope_dims // 2, dtype=f32, device=dev)
         self.rope_sin = torch.zeros(MP, c.rope_dims // 2, dtype=f32, device=dev)
-        aws = self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim, self.max_past)
+        aws = self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim, self.max_past, self.MP)
         self.attn_ws = torch.zeros(aws, dtype=torch.uint8, device=dev)
 
     def _gemm_shapes(self):

@@ -177,6 +177,8 @@ int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, int32_t hea
  * head occupies 2*head_dim columns of the qkv row, [q | gate], and the output
  * is multiplied by sigmoid(gate). Compiled geometries: head_dim 128 with
  * rope_dims 128 (or 0), gated 0; head_dim 256 with rope_dims 64, gated 1.
+ * Trees of up to rows_padded (32, 64, 96 or 128) nodes; the ancestor bitset
+ * word w of a node covers nodes 32w .. 32w+31.
  */
 typedef struct DtreeAttnArgs {
   const float* qkv; int32_t ld_qkv;
@@ -186,7 +188,7 @@ typedef struct DtreeAttnArgs {
   const DtreeStepDesc* desc;
   uint16_t* out; uint16_t* out_lo; int32_t ld_out;  /* out_lo optional low half */
   int32_t out_layout;       /* DTREE_W_ROWMAJOR or DTREE_W_TILED (ld_out = width) */
-  int32_t num_heads, num_kv_heads, head_dim, rows_padded;
+  int32_t num_heads, num_kv_heads, head_dim, rows_padded;  /* rows: 32, 64, 96, 128 */
   float scale;
   int32_t max_past_length;  /* grid is sized for this P */
   int32_t write_cache;      /* 1: append the tree K/V rows to the cache */
@@ -196,7 +198,7 @@ typedef struct DtreeAttnArgs {
 } DtreeAttnArgs;
 
 size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim,
-                                       int32_t max_past_length);
+                                       int32_t max_past_length, int32_t rows_padded);
 int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
 
 /*

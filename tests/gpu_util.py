@@ -45,12 +45,16 @@ def read_desc(t: torch.Tensor) -> N.StepDesc:
 
 
 def tree_mask(parents, P: int) -> np.ndarray:
+    """[L, P + L] visibility: every prefix key, and each node's ancestors and
+    itself (walked from the parent list, independent of the bitset packing)."""
     L = len(parents)
-    anc = ancestor_bitsets(parents)
-    m = np.ones((L, P + L), bool)
+    m = np.zeros((L, P + L), bool)
+    m[:, :P] = True
     for i in range(L):
-        for j in range(L):
-            m[i, P + j] = bool((int(anc[i, j // 32]) >> (j % 32)) & 1)
+        j = i
+        while j >= 0:
+            m[i, P + j] = True
+            j = parents[j]
     return m
 
 

@@ -293,7 +293,7 @@ def test_sk_gemm_swiglu_epilogue(gpu_device, F, k, sched):
     np.testing.assert_allclose(bf16_f32(act), ref, rtol=1e-2, atol=1e-3)
 
 
-def _attention(qkv, cache, layer, desc, out, ws, Hq, Hkv, max_past, cos, sin, qn, kn, write=1):
+def _attention(qkv, cache, layer, desc, out, ws, Hq, Hkv, max_past, cos, sin, qn, kn, write=1, MP=32):
     a = N.AttnArgs()
     a.qkv = qkv.data_ptr(); a.ld_qkv = qkv.shape[1]
     a.q_norm = qn.data_ptr() if qn is not None else None
@@ -302,26 +302,26 @@ def _attention(qkv, cache, layer, desc, out, ws, Hq, Hkv, max_past, cos, sin, qn
     a.rope_cos = cos.data_ptr(); a.rope_sin = sin.data_ptr()
     a.k_pages = cache.k_ptr(layer); a.v_pages = cache.v_ptr(layer); a.page_table = cache.page_table.data_ptr()
     a.desc = desc.data_ptr(); a.out = out.data_ptr(); a.ld_out = out.shape[1]
-    a.num_heads = Hq; a.num_kv_heads = Hkv; a.head_dim = 128; a.rows_padded = 32
+    a.num_heads = Hq; a.num_kv_heads = Hkv; a.head_dim = 128; a.rows_padded = MP
     a.scale = 128 ** -0.5; a.max_past_length = max_past; a.write_cache = write
     a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
     N.check(N.lib().dtree_tree_attention(C.byref(a), stream()), "attention")
 
 
-def _attention_case(dev, P, parents, Hq=32, Hkv=8, seed=0, permute_pages=True, max_past=None):
+def _attention_case(dev, P, parents, Hq=32, Hkv=8, seed=0, permute_pages=True, max_past=None, MP=32):
     g = np.random.default_rng(seed)
     D = 128
     L = len(parents)
     max_past = max(P, 64) if max_past is None else max_past
-    n_pages = (max_past + 32 + 63) // 64
+    n_pages = (max_past + MP + 63) // 64
     order = torch.from_numpy(g.permutation(n_pages).astype(np.int32)) if permute_pages else None
-    cache = PagedKVCache(1, Hkv, D, max_past + 32, device=dev, page_order=order)
+    cache = PagedKVCache(1, Hkv, D, max_past + MP, device=dev, page_order=order)
     kpre = (g.standard_normal((P, Hkv, D)) * 0.5).astype(np.float32)
     vpre = (g.standard_normal((P, Hkv, D)) * 0.5).astype(np.float32)
     if P:
         cache.write_logical(0, torch.from_numpy(kpre), torch.from_numpy(vpre))
     cache.offset = P
-    qkv = np.zeros((32, (Hq + 2 * Hkv) * D), np.float32)
+    qkv = np.zeros((MP, (Hq + 2 * Hkv) * D), np.float32)
     qkv[:L] = g.standard_normal((L, (Hq + 2 * Hkv) * D)).astype(np.float32)
     qn = (1 + 0.1 * g.standard_normal(D)).astype(np.float32)
     kn = (1 + 0.1 * g.standard_normal(D)).astype(np.float32)
@@ -330,15 +330,16 @@ def _attention_case(dev, P, parents, Hq=32, Hkv=8, seed=0, permute_pages=True, m
         depth[i] = depth[parents[i]] + 1
     pos = [P + d for d in depth]
     desc = device_desc([0] * L, pos, parents, P, dev)
-    cos = torch.zeros(32, 64, device=dev)
-    sin = torch.zeros(32, 64, device=dev)
-    N.check(N.lib().dtree_rope_table(desc.data_ptr(), 32, D, 1e6, cos.data_ptr(), sin.data_ptr(), stream()))
+    cos = torch.zeros(MP, 64, device=dev)
+    sin = torch.zeros(MP, 64, device=dev)
+    N.check(N.lib().dtree_rope_table(desc.data_ptr(), MP, D, 1e6, cos.data_ptr(), sin.data_ptr(), stream()))
     qn_t = torch.from_numpy(qn).to(torch.bfloat16).to(dev)
     kn_t = torch.from_numpy(kn).to(torch.bfloat16).to(dev)
-    out = torch.zeros(32, Hq * D, dtype=torch.bfloat16, device=dev)
-    ws = torch.zeros(N.lib().dtree_attention_workspace_bytes(Hq, D, max_past), dtype=torch.uint8, device=dev)
+    # stale rows past the tree: the kernel must zero them
+    out = torch.full((MP, Hq * D), 7.0, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(N.lib().dtree_attention_workspace_bytes(Hq, D, max_past, MP), dtype=torch.uint8, device=dev)
     qkv_t = torch.from_numpy(qkv).to(dev)
-    _attention(qkv_t, cache, 0, desc, out, ws, Hq, Hkv, max_past, cos, sin, qn_t, kn_t)
+    _attention(qkv_t, cache, 0, desc, out, ws, Hq, Hkv, max_past, cos, sin, qn_t, kn_t, MP=MP)
     torch.cuda.synchronize()
 
     # oracle: q/k norm (bf16 norm weights), RoPE, masked SDPA over [prefix ; tree]
@@ -378,6 +379,26 @@ def test_tree_attention_matches_oracle(gpu_device, P, shape):
     np.testing.assert_array_equal(vc, oq.bf16_to_f32(oq.f32_to_bf16_bits(v)))
     Hq = 32
     assert int(ws[: Hq * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
+
+
+@pytest.mark.parametrize("P", [0, 129, 1000])
+@pytest.mark.parametrize("MP,L,shape", [(64, 40, "random"), (96, 65, "random"), (96, 65, "chain"),
+                                        (96, 65, "star"), (96, 33, "random"), (128, 128, "random")])
+def test_tree_attention_more_than_32_nodes(gpu_device, P, MP, L, shape):
+    """Trees of 33..128 nodes: query blocks of 32 rows, tree chunks of 32
+    keys masked by ancestor word w (nodes 32w..32w+31), cache rows appended
+    once, rows past the tree zero."""
+    parents = {"random": random_tree(L, seed=P + L), "chain": [-1] + list(range(L - 1)),
+               "star": [-1] + [0] * (L - 1)}[shape]
+    cache, out, ref, k, v, ws = _attention_case(gpu_device, P, parents, seed=P + L + MP, MP=MP)
+    got = bf16_f32(out)
+    assert np.abs(got[:L] - ref).max() <= 2e-2 * np.abs(ref).max()
+    assert np.all(got[L:] == 0)
+    kc = bf16_f32(cache.logical_keys(0, P + L))[P:]
+    vc = bf16_f32(cache.logical_values(0, P + L))[P:]
+    np.testing.assert_allclose(kc, k, rtol=1e-2, atol=1e-2)
+    np.testing.assert_array_equal(vc, oq.bf16_to_f32(oq.f32_to_bf16_bits(v)))
+    assert int(ws[: 32 * (MP // 32) * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
 
 
 def test_tree_attention_gqa_small_and_deterministic(gpu_device):

@@ -67,10 +67,14 @@ def test_workspace_queries():
     assert lib.dtree_lmhead_candidate_blocks(4096, 128) == 128
     # attention: head counters (256-byte aligned) + one partial per head per
     # 4-chunk workgroup; prefix 1024 = tree + 16 pages = 5 workgroups per head
-    assert lib.dtree_attention_workspace_bytes(32, 128, 1024) == 256 + 32 * 5 * (32 * 128 + 64) * 4
-    assert lib.dtree_attention_workspace_bytes(32, 128, 0) == 256 + 32 * 1 * (32 * 128 + 64) * 4
+    assert lib.dtree_attention_workspace_bytes(32, 128, 1024, 32) == 256 + 32 * 5 * (32 * 128 + 64) * 4
+    assert lib.dtree_attention_workspace_bytes(32, 128, 0, 32) == 256 + 32 * 1 * (32 * 128 + 64) * 4
     # head_dim 256 runs 32-key chunks: prefix 2048 = tree + 64 chunks = 17 workgroups per head
-    assert lib.dtree_attention_workspace_bytes(16, 256, 2048) == 256 + 16 * 17 * (32 * 256 + 64) * 4
+    assert lib.dtree_attention_workspace_bytes(16, 256, 2048, 32) == 256 + 16 * 17 * (32 * 256 + 64) * 4
+    # 96 rows: three 32-row query blocks per head, three tree chunks: prefix
+    # 1024 = 3 + 16 chunks = 5 workgroups per (head, block); 96 counters = 384 B -> 512
+    assert lib.dtree_attention_workspace_bytes(32, 128, 1024, 96) == 512 + 96 * 5 * (32 * 128 + 64) * 4
+    assert lib.dtree_attention_workspace_bytes(32, 128, 1024, 48) == 0
 
 
 def test_struct_sizes_match_the_library():
