@@ -1068,9 +1068,10 @@ extern "C" size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int 
   const int S = split_k > 0 ? split_k : auto_split(ntiles, nkb);
   const size_t nt8 = (size_t)((ntiles + 7) / 8) * 8;
   size_t need = kCounterBytes + (S > 1 ? nt8 * S * (size_t)rows_padded * tn * sizeof(float) : 0);
-  if (split_k <= 0 && rows_padded == 32) {
-    // The stream-K path (tiled operands) may serve this shape: size for the
-    // largest CU count it plans for.
+  if (split_k <= 0 && rows_padded % 32 == 0) {
+    // The stream-K path (tiled operands; q4 weights at any row count, one
+    // 32-row pass per block) may serve this shape: size for the largest CU
+    // count it plans for.
     const size_t sk = sk_workspace_bytes(n, k, kSkMaxGrid);
     if (sk > need) need = sk;
   }

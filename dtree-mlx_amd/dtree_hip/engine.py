@@ -78,20 +78,20 @@ class TreeEngineBase:
     walk, result readback and the HIP graph of the whole step. Subclasses
     provide the layer stack (launch_forward), the cache and its compaction."""
 
-    max_nodes_limit = 32
+    max_nodes_limit = N.MAX_NODES
 
     def __init__(self, cfg, weights, max_past: int, max_nodes: int = 32, layer_ids=(), split_k: dict | None = None):
         cfg.validate()
-        if max_nodes > self.max_nodes_limit:
-            raise NotImplementedError(
-                f"trees of up to {self.max_nodes_limit} nodes (one 32-row MFMA block) for tree attention")
+        if not 1 <= max_nodes <= self.max_nodes_limit:
+            raise NotImplementedError(f"trees of 1 .. {self.max_nodes_limit} nodes per verify step")
         self.cfg = cfg
         self.w = weights
         self.lib = N.lib()
         self.dev = weights.device
         self.max_past = int(max_past)
         self.max_nodes = max_nodes
-        self.MP = 32
+        # Tree rows padded to whole 32-row MFMA blocks (32, 64, 96 or 128).
+        self.MP = 32 * ((max_nodes + 31) // 32)
         self.layer_ids = list(layer_ids)
         H, V = cfg.hidden_size, cfg.vocab_size
         MP, dev = self.MP, self.dev
@@ -99,7 +99,8 @@ class TreeEngineBase:
         # GEMM inputs are split pairs [hi, lo] of bf16 planes (value = hi + lo).
         self.x = torch.zeros(MP, H, dtype=f32, device=dev)
         self.xg = torch.zeros(2, MP, H, dtype=bf16, device=dev)
-        self.ss = torch.zeros(H // 32, MP, dtype=f32, device=dev)
+        # RMSNorm statistics: per 32-row block, per 32-column tile, per row
+        self.ss = torch.zeros(MP // 32, H // 32, 32, dtype=f32, device=dev)
         self.norm_hidden = torch.zeros(MP, H, dtype=bf16, device=dev)
         nh = max(1, len(self.layer_ids))
         self.hidden = torch.zeros(MP, nh * H, dtype=bf16, device=dev)

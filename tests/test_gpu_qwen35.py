@@ -60,10 +60,10 @@ def _close(got, want, what):
     assert err <= TOL * max(1.0, np.abs(want).max()), f"{what}: max err {err}"
 
 
-def _run(cfg, P, layer_ids, dev, norm_jitter=0.1, quant="bf16", log=print, check_prefill=False):
+def _run(cfg, P, layer_ids, dev, norm_jitter=0.1, quant="bf16", log=print, check_prefill=False, budget=24):
     t0 = time.time()
     w = Qwen35Weights.random(cfg, seed=0, device=dev, norm_jitter=norm_jitter, quant=quant)
-    eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=layer_ids)
+    eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=layer_ids, max_nodes=budget + 1)
     cache = eng.new_cache()
     prefix = random_prefix(P, cfg.vocab_size, seed=1)
     eng.prefill(cache, prefix)
@@ -82,7 +82,7 @@ def _run(cfg, P, layer_ids, dev, norm_jitter=0.1, quant="bf16", log=print, check
         for li in cfg.attention_layers:
             _close(bf16_f32(cache.kv.logical_keys(cache.slot[li], P)), oc.layers[li][0], f"prefill keys {li}")
     st = eng.stream_handle()
-    tree = make_tree(root_token=prefix[-1] if P else 0, vocab=cfg.vocab_size, seed=2)
+    tree = make_tree(root_token=prefix[-1] if P else 0, vocab=cfg.vocab_size, seed=2, budget=budget)
 
     def argmax_at(tr):
         eng.set_step(tr.tokens, tr.positions(P), tr.parents, P)
@@ -121,20 +121,25 @@ def _run(cfg, P, layer_ids, dev, norm_jitter=0.1, quant="bf16", log=print, check
                 tree_v=tree_v, hidden=hidden, vh=vh, P=P, L=L, orc=orc, oc=oc, pend=pend)
 
 
-def _check(r, layer_ids):
+def _check(r, layer_ids, min_confident=0.5):
     cfg, L, P = r["cfg"], r["L"], r["P"]
     logits, ref, res, tree = r["logits"], r["ref"], r["res"], r["tree"]
     scale = np.abs(ref).max(axis=-1)
     err = np.abs(logits - ref).max(axis=-1)
     assert np.all(err <= TOL * scale), f"logit rel err {float((err / scale).max()):.4f}"
     srt = np.sort(ref, axis=-1)
-    confident = srt[:, -1] - srt[:, -2] > TOL * scale
+    margin = srt[:, -1] - srt[:, -2]
+    confident = margin > TOL * scale
+    # Where every logit of a row is within err of the oracle, a top-2 margin
+    # above 2 * err fixes the argmax whatever the logits' scale.
+    sure = margin > 2 * err
     o_post = np.argmax(ref, axis=-1)
     post = np.array(res.posterior)
     assert np.array_equal(post[confident], o_post[confident])
-    assert confident.mean() > 0.5
+    assert np.array_equal(post[sure], o_post[sure])
+    assert confident.mean() >= min_confident and sure.mean() > 0.5
     o_acc, o_bonus = otree.follow_verified_tree(tree.child_maps, o_post.tolist())
-    if all(confident[i] for i in o_acc):
+    if all(confident[i] or sure[i] for i in o_acc):
         assert res.accepted == o_acc and res.bonus_token == o_bonus
     acc2, bonus2 = otree.follow_verified_tree(tree.child_maps, res.posterior)
     assert res.accepted == acc2 and res.bonus_token == bonus2
@@ -176,6 +181,17 @@ def test_qwen35_verify_step_tiny_model_q4(gpu_device):
     _check(r, [2])
 
 
+@pytest.mark.parametrize("quant", ["bf16", "q4"])
+def test_qwen35_verify_step_65_nodes(gpu_device, quant):
+    """Draft budget 64 (a 65-node tree, 96 padded rows): attention over three
+    32-row query blocks and tree chunks, q4 GEMMs per 32-row block, the
+    GatedDeltaNet layer at 96 rows."""
+    cfg = tiny_qwen35()
+    r = _run(cfg, P=90, layer_ids=[1, 3], dev=gpu_device, quant=quant, budget=64)
+    assert r["L"] == 65 and r["eng"].MP == 96
+    _check(r, [1, 3])
+
+
 def test_qwen35_two_steps_graph_matches_eager(gpu_device):
     """Two consecutive verify steps through the captured graph leave the same
     committed state as the same steps launched eagerly."""
@@ -196,6 +212,19 @@ def test_qwen35_two_steps_graph_matches_eager(gpu_device):
         eng.release_graphs()
     assert out[0][0] == out[1][0] and out[0][3] == out[1][3]
     assert torch.equal(out[0][1], out[1][1]) and torch.equal(out[0][2], out[1][2])
+
+
+def test_qwen35_9b_q4_verify_step_prefix_8192_budget_64(gpu_device):
+    """Qwen3.5-9B-shaped hybrid (hidden 4096), q4 weights including the tied
+    LM head, 8192-token prefix, 65-node tree (draft budget 64)."""
+    from dtree_hip.config import QWEN35_9B
+    r = _run(QWEN35_9B, P=8192, layer_ids=[1, 15, 30], dev=gpu_device, norm_jitter=0.0, quant="q4", budget=64)
+    assert r["L"] == 65
+    # The synthetic q4 weights (nibbles 0..15, positive scales) give every
+    # embedding row a large common-mode term: at hidden 4096 the top-2 logit
+    # margins fall under 2e-2 of the largest logit, so the argmax bar is
+    # carried by the measured-error margin (`sure` rows) instead.
+    _check(r, [1, 15, 30], min_confident=0.0)
 
 
 def test_qwen35_4b_verify_step_prefix_2048(gpu_device):
