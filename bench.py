@@ -13,6 +13,9 @@ GatedDeltaNet + 8 gated attention, hidden 2560, prefix 2048 by default):
 GatedDeltaNet tree recurrence from the committed fp32 state, gated
 head_dim-256 tree attention, LM-head argmax, walk, KV compaction and the
 GatedDeltaNet commit along the accepted path, as one HIP graph.
+--model qwen35-9b runs the Qwen3.5-9B-shaped hybrid (hidden 4096, FFN 12288)
+with q4 weights, an 8192-token prefix and draft budget 64 (65-node trees) by
+default.
 
 Prints ONE JSON line (rank 0). Progress goes to stderr.
 """
@@ -178,7 +181,8 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
     out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant), nl, us["qkv"], b["qkv"])
-    out["attention"] = entry("tree_attn_kernel<128, 128, false>", nl, us["attention"], b["attention"])
+    out["attention"] = entry(f"tree_attn_kernel<128, 128, false, {1 if eng.MP == 32 else 4}>", nl, us["attention"],
+                             b["attention"])
     out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant), nl, us["o"], b["o"])
     out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant), nl, us["down"], b["down"])
     out["gate_up_gemm"] = entry(gemm_kernel_name(2 * F, H, 2, quant), nl, us["gu"], b["gu"])
@@ -373,10 +377,12 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "gate_up_gemm": entry(kn(2 * F, H, 2), nL, us["gu"], b["gu"]),
         "down_gemm": entry(kn(H, F, 1), nL, us["down"], b["down"]),
         "gdn_prep": entry("gdn_prep_kernel<3, 128>", nG, us["prep"], b["prep"]),
-        "gdn_recurrence": entry("gdn_tree_reg_kernel<32>", nG, us["recurrence"], b["recurrence"]),
+        "gdn_recurrence": entry(f"gdn_tree_reg_kernel<{32 if eng.MP == 32 else 96}>", nG,
+                                us["recurrence"], b["recurrence"]),
         "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
         "gdn_commit": entry("gdn_commit_kernel<128>", nG, us["commit"], b["commit"]),
-        "attention": entry("tree_attn_kernel<256, 64, true>", nA, us["attention"], b["attention"]),
+        "attention": entry(f"tree_attn_kernel<256, 64, true, {1 if eng.MP == 32 else 4}>", nA, us["attention"],
+                           b["attention"]),
         "lm_head": entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"]),
     }
     return out
@@ -412,12 +418,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--model", choices=["qwen3-4b", "qwen35-4b"], default="qwen3-4b",
-                    help="qwen35-4b: the Qwen3.5-4B-shaped GatedDeltaNet / attention hybrid")
-    ap.add_argument("--prefix", type=int, default=None, help="prefix tokens (default 1024; 2048 for qwen35-4b)")
-    ap.add_argument("--budget", type=int, default=24)
-    ap.add_argument("--quant", choices=["bf16", "q4"], default="bf16",
-                    help="q4: every linear layer and the tied LM head in 4-bit affine groups of 64")
+    ap.add_argument("--model", choices=["qwen3-4b", "qwen35-4b", "qwen35-9b"], default="qwen3-4b",
+                    help="qwen35-4b / qwen35-9b: the Qwen3.5-shaped GatedDeltaNet / attention hybrids")
+    ap.add_argument("--prefix", type=int, default=None,
+                    help="prefix tokens (default 1024; 2048 for qwen35-4b, 8192 for qwen35-9b)")
+    ap.add_argument("--budget", type=int, default=None, help="draft budget (default 24; 64 for qwen35-9b)")
+    ap.add_argument("--quant", choices=["bf16", "q4"], default=None,
+                    help="q4: every linear layer and the tied LM head in 4-bit affine groups of 64 "
+                         "(default bf16; q4 for qwen35-9b)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=108)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -435,23 +443,29 @@ def main():
     import torch
 
     from dtree_hip import Qwen35TreeEngine, Qwen35Weights, Qwen3TreeModel, Qwen3Weights
-    from dtree_hip.config import QWEN3_4B, QWEN35_4B
+    from dtree_hip.config import QWEN3_4B, QWEN35_4B, QWEN35_9B
     from dtree_hip.synthetic import acceptance_rewrite, make_tree, random_prefix
 
     dev = torch.device("cuda:0")
-    hybrid = a.model == "qwen35-4b"
-    cfg = QWEN35_4B if hybrid else QWEN3_4B
-    P = a.prefix if a.prefix is not None else (2048 if hybrid else 1024)
+    hybrid = a.model.startswith("qwen35")
+    big = a.model == "qwen35-9b"
+    cfg = {"qwen3-4b": QWEN3_4B, "qwen35-4b": QWEN35_4B, "qwen35-9b": QWEN35_9B}[a.model]
+    P = a.prefix if a.prefix is not None else {"qwen3-4b": 1024, "qwen35-4b": 2048, "qwen35-9b": 8192}[a.model]
+    if a.budget is None:
+        a.budget = 64 if big else 24
+    if a.quant is None:
+        a.quant = "q4" if big else "bf16"
+    max_nodes = a.budget + 1
     t0 = time.time()
     if hybrid:
         w = Qwen35Weights.random(cfg, seed=0, device=dev, quant=a.quant)
-        eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 30])
+        eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 30], max_nodes=max_nodes)
     else:
         if a.quant == "q4":
             w = Qwen3Weights.random_q4(cfg, seed=0, device=dev)
         else:
             w = Qwen3Weights.random(cfg, seed=0, device=dev)
-        eng = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33]).engine
+        eng = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33], max_nodes=max_nodes).engine
     cache = eng.new_cache()
     prefix = random_prefix(P, cfg.vocab_size, seed=1)
     eng.prefill(cache, prefix)
@@ -513,7 +527,8 @@ def main():
         log(f"[bench] cpu baseline {cpu['value']:.3f} steps/s ({time.time() - t0:.1f}s)")
 
     mean_acc = sum(accepted_lens) / len(accepted_lens)
-    model_name = "Qwen3.5-4B-shaped hybrid" if hybrid else "Qwen3-4B"
+    model_name = {"qwen3-4b": "Qwen3-4B", "qwen35-4b": "Qwen3.5-4B-shaped hybrid",
+                  "qwen35-9b": "Qwen3.5-9B-shaped hybrid"}[a.model]
     qname = "bf16" if a.quant == "bf16" else "q4 group-64"
     if hybrid:
         workload = (f"{model_name} {qname} tree-verify step (24 GatedDeltaNet + 8 gated attention layers, "
@@ -521,7 +536,7 @@ def main():
     else:
         workload = f"{model_name} {qname} tree-verify step (36 layers, LM-head argmax, walk, compaction)"
     out = {
-        "metric": f"tree-verify steps/s + HBM GB/s (% of peak), 24-node tree, {model_name} {qname}",
+        "metric": f"tree-verify steps/s + HBM GB/s (% of peak), {a.budget}-node tree, {model_name} {qname}",
         "value": round(steps_per_s, 3),
         "unit": "steps/s",
         "n_gpus": 1,

@@ -267,6 +267,10 @@ __global__ __launch_bounds__(256) void gdn_tree_reg_kernel(GdnParams p) {
   reg_tree_step<TMAX, 0>(rt, s);
 }
 
+// Largest tree of the register-resident recurrence (65-node trees of draft
+// budget 64 pad to 96 rows); larger trees use gdn_tree_kernel.
+constexpr int kRegTreeMax = 96;
+
 // Path entries index the per-node buffers ([T] rows); an out-of-range entry
 // (a descriptor that no walk filled) is clamped so it can never read past them.
 __device__ __forceinline__ int clamp_node(int t, int T) { return min(max(t, 0), T - 1); }
@@ -525,8 +529,9 @@ extern "C" int dtree_gdn_tree_recurrence(const float* q, const float* k, const f
   p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.state = const_cast<float*>(state); p.parents = parents;
   p.T = num_nodes; p.Hk = num_k_heads; p.Hv = num_v_heads; p.Dv = head_v_dim; p.rpw = rpw;
   p.y = y; p.states = states;
-  if (head_k_dim == 128 && num_nodes <= 32 && head_v_dim % 8 == 0) {
-    gdn_tree_reg_kernel<32><<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
+  if (head_k_dim == 128 && num_nodes <= kRegTreeMax && head_v_dim % 8 == 0) {
+    if (num_nodes <= 32) gdn_tree_reg_kernel<32><<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
+    else gdn_tree_reg_kernel<kRegTreeMax><<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
     DTREE_LAUNCH_CHECK("gdn_tree_recurrence launch");
     return DTREE_OK;
   }
@@ -628,6 +633,9 @@ extern "C" int dtree_gdn_layer_recurrence(const DtreeGdnArgs* a, hipStream_t str
   if (a->rows_padded <= 32 && a->head_v_dim % 8 == 0) {
     p.T = min(a->rows_padded, 32);
     gdn_tree_reg_kernel<32><<<a->num_v_heads * (a->head_v_dim / 8), 256, 0, stream>>>(p);
+  } else if (a->rows_padded <= kRegTreeMax && a->head_v_dim % 8 == 0) {
+    p.T = a->rows_padded;
+    gdn_tree_reg_kernel<kRegTreeMax><<<a->num_v_heads * (a->head_v_dim / 8), 256, 0, stream>>>(p);
   } else {
     const int grid = a->num_v_heads * (a->head_v_dim / rpw);
     gdn_tree_kernel<128><<<grid, rpw * (128 / 4), lds, stream>>>(p);

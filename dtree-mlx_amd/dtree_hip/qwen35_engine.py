@@ -36,6 +36,9 @@ from .weights import GdnLayerWeights
 
 
 class Qwen35TreeEngine(TreeEngineBase):
+    # The register-resident GatedDeltaNet recurrence holds trees of up to 96
+    # nodes (head dim 128); larger ones fit no recurrence kernel.
+    max_nodes_limit = 96
 
     def _alloc_layer_buffers(self) -> None:
         c, MP, dev = self.cfg, self.MP, self.dev

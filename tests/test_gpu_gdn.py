@@ -13,6 +13,7 @@ from gpu_util import random_tree, stream
 from oracle import gdn
 
 from dtree_hip import _native as N
+from dtree_hip._native import DtreeError
 
 pytestmark = pytest.mark.gpu
 
@@ -90,7 +91,7 @@ def _layer_inputs(T, seed, Hk=16, Hv=32, D=128):
     return q, k, v, g, beta, state
 
 
-@pytest.mark.parametrize("T,seed", [(25, 0), (65, 1)])
+@pytest.mark.parametrize("T,seed", [(25, 0), (65, 1), (96, 2)])
 def test_layer_shapes_conv_and_recurrence(T, seed):
     parents = random_tree(T, seed)
     g_ = np.random.default_rng(100 + seed)
@@ -110,6 +111,14 @@ def test_layer_shapes_conv_and_recurrence(T, seed):
     y2, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
     out2, _ = _conv(x, base, w, parents, "cuda", want_windows=False)
     assert np.array_equal(y, y2) and np.array_equal(out, out2)
+
+
+def test_recurrence_rejects_trees_past_96_nodes():
+    """Head dim 128: trees of up to 96 nodes run register-resident; larger ones
+    do not fit the LDS-resident fallback either and are rejected."""
+    q, k, v, g, beta, state = _layer_inputs(128, 3)
+    with pytest.raises(DtreeError, match="too large"):
+        _delta(q, k, v, g, beta, state, random_tree(128, 3), "cuda")
 
 
 def test_commit_replays_accepted_path():
