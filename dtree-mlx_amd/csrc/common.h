@@ -86,6 +86,32 @@ __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
+// ---- cross-lane reductions without LDS round trips -------------------------
+// DPP moves within 16-lane rows plus one ds_swizzle across the two rows of a
+// 32-lane half. Every lane of a 32-lane half ends with the half's total.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ int swz_xor16_i(int v) {
+  // bitmask mode: and_mask 0x1F, or_mask 0, xor_mask 0x10 (groups of 32 lanes)
+  return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+}
+__device__ __forceinline__ float swz_xor16(float v) {
+  return __builtin_bit_cast(float, swz_xor16_i(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float row_sum32(float a) {
+  a += dpp<0xB1>(a);   // lane ^ 1
+  a += dpp<0x4E>(a);   // lane ^ 2
+  a += dpp<0x141>(a);  // half-row mirror: the other quad of 8 lanes
+  a += dpp<0x140>(a);  // row mirror: the other 8 lanes of 16
+  return a + swz_xor16(a);  // the other 16-lane row
+}
+
 // Row of 32x32 MFMA accumulator register r held by a lane in half h (= lane/32):
 // D[row][col] with col = lane % 32.
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }

@@ -150,22 +150,6 @@ __global__ __launch_bounds__(256) void gdn_tree_kernel(GdnParams p) {
 // steps interleave, so the latency of one reduction covers all three): DPP
 // quad permutes, half-row and row mirrors, then a swizzle across the two
 // 16-lane rows. Every lane of the row ends with the sums.
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float swz_xor16(float v) {
-  // bitmask mode: and_mask 0x1F, or_mask 0, xor_mask 0x10 (groups of 32 lanes)
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-}
-__device__ __forceinline__ float row_sum32(float a) {
-  a += dpp<0xB1>(a);
-  a += dpp<0x4E>(a);
-  a += dpp<0x141>(a);
-  a += dpp<0x140>(a);
-  return a + swz_xor16(a);
-}
-
 __device__ __forceinline__ void row_sum32x3(float& a, float& b, float& c) {
   a += dpp<0xB1>(a); b += dpp<0xB1>(b); c += dpp<0xB1>(c);     // lane ^ 1
   a += dpp<0x4E>(a); b += dpp<0x4E>(b); c += dpp<0x4E>(c);     // lane ^ 2

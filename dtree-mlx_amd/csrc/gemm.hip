@@ -306,9 +306,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* 
       *xp = xv;
       split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, col, p.ld_out_bf16), xv * g);
       if (p.hidden_out) p.hidden_out[(size_t)m * p.ld_hidden + col] = f2bf(xv);
-      float sq = xv * xv;
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+      // sum of x^2 over this 32-column tile (the 32 lanes of a half-wave)
+      const float sq = row_sum32(xv * xv);
       if ((n & 31) == 0) p.ss_out[ss_index(col >> 5, m, p.n >> 5)] = sq;
     }
   } else if constexpr (EPI == DTREE_EPI_SWIGLU) {
@@ -796,6 +795,21 @@ __device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi)
     i = oi;
   }
 }
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
+  argmax_merge(v, i, dpp<CTRL>(v), dpp_i<CTRL>(i));
+}
+// (max, first index on ties) over TN lanes (32: each half-wave, 64: the wave).
+// The merge is a total order, so the result does not depend on the pairing.
+template <int TN>
+__device__ __forceinline__ void lane_argmax(float& v, int& i) {
+  argmax_dpp<0xB1>(v, i);
+  argmax_dpp<0x4E>(v, i);
+  argmax_dpp<0x141>(v, i);
+  argmax_dpp<0x140>(v, i);
+  argmax_merge(v, i, swz_xor16(v), swz_xor16_i(i));
+  if constexpr (TN == 64) argmax_merge(v, i, __shfl_xor(v, 32), __shfl_xor(i, 32));
+}
 
 template <int MB, int NB, int U, bool LO, bool TILED, bool Q4>
 __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
@@ -833,12 +847,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
       float v = red[e] * rs[m];
       int idx = tile * TN + n;
       if (p.logits) p.logits[(size_t)m * p.vocab + idx] = v;
-#pragma unroll
-      for (int o = TN / 2; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(v, o);
-        const int oi = __shfl_xor(idx, o);
-        argmax_merge(v, idx, ov, oi);
-      }
+      lane_argmax<TN>(v, idx);
       argmax_merge(bv[i], bi[i], v, idx);
     }
   }

@@ -84,9 +84,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
         xg[xi] = hi;
         if (xg_lo) xg_lo[xi] = f2bf(vg - bf2f(hi));
       }
-      float sq = v[j] * v[j];
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+      const float sq = row_sum32(v[j] * v[j]);  // this 32-column tile
       if (in && n == 0) ss[ss_index(col >> 5, m, (H + 31) >> 5)] = sq;
     }
   }
