@@ -38,7 +38,6 @@ namespace dtree {
 
 constexpr int kWaves = 4;          // waves (chunks) per workgroup
 constexpr int kMaxPast = 16384;    // longest prefix the grid is sized for
-constexpr int kMergeDims = 128;    // head dims merged per LDS pass
 // Prefix keys per chunk.
 __host__ __device__ constexpr int chunk_keys(int D) { return D <= 128 ? DTREE_PAGE : DTREE_PAGE / 2; }
 constexpr float kNeg = -1e30f;
@@ -72,16 +71,21 @@ struct HeadRow {
   f32x4_t cs[R / 32][2], sn[R / 32][2];
 };
 
-template <int D, int R>
+// AUX: also the norm weights and the RoPE cos/sin (q and k rows; v has
+// none). Without norm weights the loads read the row itself instead and
+// row_finish ignores them, so the loads never branch: the whole prologue
+// stays one basic block and its loads go out in one round trip.
+template <int D, int R, bool AUX>
 __device__ __forceinline__ void row_issue(HeadRow<D, R>& r, const float* src, const uint16_t* norm_w, const float* cosr,
                                           const float* sinr, int h) {
+  const uint16_t* nwp = norm_w ? norm_w : reinterpret_cast<const uint16_t*>(src);
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) {
     r.x[j][0] = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h);
     r.x[j][1] = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h + 4);
-    if (norm_w) r.nw[j] = ld_u32x4(norm_w + 16 * j + 8 * h);
+    if constexpr (AUX) r.nw[j] = ld_u32x4(nwp + 16 * j + 8 * h);
   }
-  if (cosr) {
+  if constexpr (AUX) {
 #pragma unroll
     for (int j = 0; j < R / 32; ++j)
 #pragma unroll
@@ -215,6 +219,92 @@ __device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, bool norm, 
   for (int j = 0; j < D / 16; ++j) split8(q[j], qf[j], ql[j]);
 }
 
+// ---- query rows staged once per workgroup (head_dim 128, full RoPE) --------
+// The four waves of a workgroup score the same 32 query rows of one head, so
+// the rows are loaded, normalised and rotated once: thread (row r = t / 8,
+// part j = t % 8) owns dims 8j .. 8j+7 and 64+8j .. 64+8j+7 (each RoPE pair
+// (d, d + 64) stays in one thread; the RMSNorm sum of squares is completed
+// over the row's 8 threads with DPP) and writes them to LDS, from which each
+// wave reads its MFMA fragments. Row stride kQsStride keeps those 32-byte
+// fragment reads apart in the LDS banks.
+constexpr int kQsStride = 128 + 4;  // floats
+struct QStage {
+  f32x4_t x[4];
+  u32x4_t nw[2];
+  f32x4_t cs[2], sn[2];
+};
+
+__device__ __forceinline__ void q_stage_issue(const AttnParams& p, int hq, int rb, QStage& q) {
+  const int t = threadIdx.x, r = t >> 3, j = t & 7;
+  const int row = 32 * rb + r;
+  const float* src = p.qkv + (size_t)row * p.ld_qkv + hq * p.q_stride + 8 * j;
+  q.x[0] = *reinterpret_cast<const f32x4_t*>(src);
+  q.x[1] = *reinterpret_cast<const f32x4_t*>(src + 4);
+  q.x[2] = *reinterpret_cast<const f32x4_t*>(src + 64);
+  q.x[3] = *reinterpret_cast<const f32x4_t*>(src + 68);
+  // without q_norm the weight loads read the row itself (ignored below)
+  const uint16_t* nwp = p.q_norm ? p.q_norm + 8 * j : reinterpret_cast<const uint16_t*>(src);
+  q.nw[0] = ld_u32x4(nwp);
+  q.nw[1] = ld_u32x4(nwp + 64);
+  const float* cr = p.rope_cos + row * 64 + 8 * j;
+  const float* sr = p.rope_sin + row * 64 + 8 * j;
+  q.cs[0] = *reinterpret_cast<const f32x4_t*>(cr);
+  q.cs[1] = *reinterpret_cast<const f32x4_t*>(cr + 4);
+  q.sn[0] = *reinterpret_cast<const f32x4_t*>(sr);
+  q.sn[1] = *reinterpret_cast<const f32x4_t*>(sr + 4);
+}
+
+__device__ __forceinline__ void q_stage_finish(const QStage& q, bool norm, float eps, float* qs) {
+  const int t = threadIdx.x, r = t >> 3, j = t & 7;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = q.x[0][i];
+    v[4 + i] = q.x[1][i];
+    v[8 + i] = q.x[2][i];
+    v[12 + i] = q.x[3][i];
+  }
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ss += v[i] * v[i];
+    ss += dpp<0xB1>(ss);   // lane ^ 1
+    ss += dpp<0x4E>(ss);   // lane ^ 2
+    ss += dpp<0x141>(ss);  // the other quad of the row's 8 lanes
+    const float rs = rsqrtf(ss * (1.0f / 128) + eps);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t w = q.nw[i >> 3][(i & 7) >> 1];
+      v[i] *= rs * __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float cs = q.cs[i >> 2][i & 3], sn = q.sn[i >> 2][i & 3];
+    const float x1 = v[i], x2 = v[8 + i];
+    v[i] = x1 * cs - x2 * sn;
+    v[8 + i] = x1 * sn + x2 * cs;
+  }
+  float* dst = qs + r * kQsStride + 8 * j;
+  *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+  *reinterpret_cast<f32x4_t*>(dst + 64) = f32x4_t{v[8], v[9], v[10], v[11]};
+  *reinterpret_cast<f32x4_t*>(dst + 68) = f32x4_t{v[12], v[13], v[14], v[15]};
+}
+
+// Lane (c, h)'s q fragments (dims 16j + 8h .. +7 of query row c) from the
+// staged rows, split hi / lo.
+__device__ __forceinline__ void q_frag_lds(const float* qs, int c, int h, u32x4_t (&qf)[8], u32x4_t (&ql)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float* src = qs + c * kQsStride + 16 * j + 8 * h;
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + 4);
+    const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    split8(v, qf[j], ql[j]);
+  }
+}
+
 // Tree chunk tc: k (norm + RoPE) and v of nodes 32*tc .. 32*tc+31 come from
 // the fused qkv rows and are staged in LDS (this wave's private region) for
 // the MFMA operand layouts; the block's 32 query rows are scored against them
@@ -223,9 +313,10 @@ __device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, bool norm, 
 // q, k and v are finished one after the other, so at most one raw head row is
 // live in registers (head_dim 256 rows are 128 floats per lane pair).
 template <int D, int R>
-__device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& qr, int hq, int g, int G, int P,
-                                           int L, int tc, int qrow, bool write_rows, int c, int h, uint16_t* ks,
-                                           uint16_t* vt, float& m_run, float& l_run, f32x16_t (&o)[D / 32]) {
+__device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs, int hq, int g,
+                                           int G, int P, int L, int tc, int qrow, bool write_rows, int c, int h,
+                                           uint16_t* ks, uint16_t* vt, float& m_run, float& l_run,
+                                           f32x16_t (&o)[D / 32]) {
   constexpr int NJ = D / 16, ND = D / 32;
   constexpr int KS = D + 8, VS = 32 + 8;
   constexpr int half_r = R / 2;
@@ -236,21 +327,24 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
   const float* sinr = p.rope_sin + node * half_r;
   const uint32_t anc = p.desc->ancestors[qrow][tc];
   u32x4_t qf[NJ], ql[NJ];
-  if constexpr (D > 128)
-    row_issue<D, R>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * half_r,
-                    p.rope_sin + qrow * half_r, h);
-  q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  if constexpr (D > 128) {
+    row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * half_r,
+                          p.rope_sin + qrow * half_r, h);
+    q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  } else {
+    q_frag_lds(qs, c, h, qf, ql);
+  }
   u32x4_t kf8[NJ], vf8[NJ];
   {
     HeadRow<D, R> kr;
-    row_issue<D, R>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
+    row_issue<D, R, true>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
     float kv[NJ][8];
     row_finish<D, R>(kr, p.k_norm != nullptr, true, p.eps, kv);
     pack_frag<D>(kv, kf8);
   }
   {
     HeadRow<D, R> vr;
-    row_issue<D, R>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
+    row_issue<D, R, false>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
     float vv[NJ][8];
     row_finish<D, R>(vr, false, false, 0.f, vv);
     pack_frag<D>(vv, vf8);
@@ -314,38 +408,48 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
 }
 
 // One prefix chunk = CK consecutive keys inside one page (the whole page for
-// head_dim 128, half of it for 256). Q's loads go out first, then all K and V
-// of the chunk, so Q's norm/RoPE overlaps the K/V flight. Keys past the prefix
-// in the last chunk are masked (scores) and zeroed (V), since the page may
-// hold stale or non-finite data there.
-template <int D, int R>
-__device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>& qr, int page, int hq, int g, int P,
-                                             int pc, int qrow, int c, int h, float& m_run, float& l_run,
-                                             f32x16_t (&o)[D / 32]) {
-  constexpr int NJ = D / 16, ND = D / 32;
-  constexpr int CK = chunk_keys(D), NB = CK / 32;
-  if constexpr (D > 128)
-    row_issue<D, R>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * (R / 2),
-                    p.rope_sin + qrow * (R / 2), h);
-  const int k_begin = pc * CK;  // prefix chunk pc: keys pc*CK ..
-  const int k_end = min(k_begin + CK, P);
-  const int po = k_begin % DTREE_PAGE;
-  const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po + swap_bits23(c)) * D;
-  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po;
+// head_dim 128, half of it for 256): its K and V fragments, loaded by
+// prefix_issue and consumed by prefix_chunk. Keys past the
+// prefix in the last chunk are masked (scores) and zeroed (V), since the page
+// may hold stale or non-finite data there.
+template <int D>
+struct ChunkKV {
+  static constexpr int NJ = D / 16, ND = D / 32, NB = chunk_keys(D) / 32;
   u32x4_t kf[NB][NJ];
   u32x4_t vf[NB][2][ND];
+};
+
+template <int D>
+__device__ __forceinline__ void prefix_issue(const AttnParams& p, ChunkKV<D>& kv, int page, int g, int pc, int c,
+                                             int h) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  constexpr int CK = chunk_keys(D), NB = CK / 32;
+  const int po = (pc * CK) % DTREE_PAGE;
+  const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po + swap_bits23(c)) * D;
+  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) kf[b][j] = ld_u32x4_stream(kbase + (size_t)32 * b * D + 16 * j + 8 * h);
+    for (int j = 0; j < NJ; ++j) kv.kf[b][j] = ld_u32x4_stream(kbase + (size_t)32 * b * D + 16 * j + 8 * h);
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int db = 0; db < ND; ++db)
-        vf[b][s2][db] = ld_u32x4_stream(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 32 * b + 16 * s2 + 8 * h);
+        kv.vf[b][s2][db] = ld_u32x4_stream(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 32 * b + 16 * s2 + 8 * h);
   }
+}
+
+template <int D, int R>
+__device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs,
+                                             const ChunkKV<D>& kv, int P, int pc, int c, int h, float& m_run,
+                                             float& l_run, f32x16_t (&o)[D / 32]) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  constexpr int CK = chunk_keys(D), NB = CK / 32;
+  const int k_begin = pc * CK;  // prefix chunk pc: keys pc*CK ..
+  const int k_end = min(k_begin + CK, P);
   u32x4_t qf[NJ], ql[NJ];
-  q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  if constexpr (D > 128) q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  else q_frag_lds(qs, c, h, qf, ql);
 
   f32x16_t s[NB];
 #pragma unroll
@@ -356,8 +460,8 @@ __device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>&
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      s[b] = mfma32(kf[b][j], qf[j], s[b]);
-      s[b] = mfma32(kf[b][j], ql[j], s[b]);
+      s[b] = mfma32(kv.kf[b][j], qf[j], s[b]);
+      s[b] = mfma32(kv.kf[b][j], ql[j], s[b]);
     }
   const bool ragged = k_end - k_begin < CK;
 #pragma unroll
@@ -375,9 +479,71 @@ __device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>&
       u32x4_t va[ND];
       const int first = k_begin + 32 * b + 16 * s2 + 8 * h;
 #pragma unroll
-      for (int db = 0; db < ND; ++db) va[db] = ragged ? mask_keys(vf[b][s2][db], first, k_end) : vf[b][s2][db];
+      for (int db = 0; db < ND; ++db)
+        va[db] = ragged ? mask_keys(kv.vf[b][s2][db], first, k_end) : kv.vf[b][s2][db];
       pv_step<ND>(s[b], s2, va, o);
     }
+}
+
+// Combine of a head's workgroup partials ([block][lane][16] floats, then m and
+// l of the 32 queries, per split) by the last workgroup to arrive: kSb splits
+// per round with every load of the round in flight (ranged loads past the
+// last split return zero) and a running max; AUX is the cache policy of the
+// loads (kSc0: all writers on this XCD, else kSc1).
+template <int D, int AUX>
+__device__ __forceinline__ void combine_splits(__amdgpu_buffer_rsrc_t prs, unsigned pbase, size_t stride, int nsplit,
+                                               int wave, int lane, int c, float& tot,
+                                               f32x16_t (&mine)[D / 32 / kWaves]) {
+  constexpr int NDW = D / 32 / kWaves;
+  constexpr int kSb = 8 / NDW;  // 8 splits per round at head_dim 128, 4 at 256
+  float Ms = kNeg;
+  tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < NDW; ++k)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mine[k][r] = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kSb) {
+    f32x4_t v[kSb][NDW][4];
+    float mm[kSb], ll[kSb];
+#pragma unroll
+    for (int b = 0; b < kSb; ++b) {
+      const bool ok = s0 + b < nsplit;
+      const unsigned so = ok ? pbase + (unsigned)((size_t)(s0 + b) * stride * sizeof(float)) : kOob;
+      const float mv = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(so + (32 * D + c) * 4), 0, AUX));
+      ll[b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(so + (32 * D + 32 + c) * 4),
+                                                                            0, AUX));
+      mm[b] = ok ? mv : kNeg;
+#pragma unroll
+      for (int k = 0; k < NDW; ++k)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq)
+          v[b][k][gq] = __builtin_bit_cast(
+              f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                           prs, (int)(so + (unsigned)(((wave + kWaves * k) * 64 + lane) * 64 + 16 * gq)), 0, AUX));
+    }
+    float gm = Ms;
+#pragma unroll
+    for (int b = 0; b < kSb; ++b) gm = fmaxf(gm, mm[b]);
+    const float rsc = fast_exp2(Ms - gm);
+    tot *= rsc;
+#pragma unroll
+    for (int k = 0; k < NDW; ++k)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mine[k][r] *= rsc;
+#pragma unroll
+    for (int b = 0; b < kSb; ++b) {
+      const float w = fast_exp2(mm[b] - gm);
+      tot += w * ll[b];
+#pragma unroll
+      for (int k = 0; k < NDW; ++k)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mine[k][4 * gq + i] += w * v[b][k][gq][i];
+    }
+    Ms = gm;
+  }
 }
 
 // TB: tree chunks the LDS staging is sized for (1 for 32 rows, 4 up to 128).
@@ -386,22 +552,29 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   constexpr int ND = D / 32;  // 32-dim blocks of O^T
   constexpr int KS = D + 8;   // padded LDS row of tree K
   constexpr int VS = 32 + 8;  // padded LDS row of tree V^T
-  constexpr int MS = 33;      // row stride of a wave's O^T in the LDS merge
-  constexpr int NP = D / kMergeDims;               // merge passes
-  constexpr int kWaveMerge = kMergeDims * MS + 64;  // floats per wave: O^T slice, m, l
-  constexpr int kStage = (32 * KS + D * VS) * 2;
-  constexpr int kMerge = kWaves * kWaveMerge * 4;
+  constexpr int kStage = (32 * KS + D * VS) * 2;   // one tree chunk's K / V^T staging
+  constexpr int kQs = D <= 128 ? 32 * kQsStride * 4 : 0;  // staged query rows
+  constexpr int kMl = kWaves * 64 * 4;               // merge: per wave, m and l of 32 queries
+  constexpr int kMerge = kMl + ND * kWaves * 4 * 64 * 16;  // + [block][wave][4][lane] f32x4
+  constexpr int kChunkLds = TB * kStage + kQs;
   constexpr int CK = chunk_keys(D);
-  __shared__ __align__(16) unsigned char lds[TB * kStage > kMerge ? TB * kStage : kMerge];
+  __shared__ __align__(16) unsigned char lds[kChunkLds > kMerge ? kChunkLds : kMerge];
   __shared__ int s_last;
 
+  // Every argument the prologue needs in scalar registers at once: one batch
+  // of argument loads and one wait, instead of a batch per basic block.
+  asm volatile("" ::"s"(p.qkv), "s"(p.ld_qkv), "s"(p.q_stride), "s"(p.q_norm), "s"(p.rope_cos), "s"(p.rope_sin),
+               "s"(p.kp), "s"(p.vp), "s"(p.page_table), "s"(p.desc), "s"(p.Hq), "s"(p.Hkv), "s"(p.max_chunks),
+               "s"(p.splits), "s"(p.tree_chunks), "s"(gridDim.x));
   // blockIdx -> (query block, split, kv group, head in group): the G heads of
   // one (split, group) pair share blockIdx % 8, i.e. one XCD.
   const int G = p.Hq / p.Hkv, NT = p.tree_chunks;
   const int per_block = (int)gridDim.x / NT;  // workgroups per query block (a multiple of 8)
   const int rb = blockIdx.x / per_block, bid = blockIdx.x % per_block;
   const int pair = (bid / (8 * G)) * 8 + (bid & 7);
-  if (pair >= p.splits * p.Hkv) return;
+  // Padding workgroups (pair past splits * Hkv) still name an in-range head
+  // and a chunk past max_chunks; they return after the loads below are out,
+  // which keeps the argument loads in one round trip.
   const int g = pair % p.Hkv, split = pair / p.Hkv;
   const int hq = g * G + (bid >> 3) % G;
 
@@ -410,16 +583,19 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   const int chunk = split * kWaves + wave;
   const int qrow = 32 * rb + c;  // this lane's query row
   // Loads that do not depend on the step descriptor go out first, so their
-  // latency overlaps the descriptor read: this lane's q row (values, norm
-  // weights, RoPE) and the page of this wave's prefix chunk.
-  // (head_dim 256 issues its q row inside the chunk: live across the
+  // latency overlaps the descriptor read: the workgroup's query rows (values,
+  // norm weights, RoPE; 10 loads per thread) and the page of this wave's
+  // prefix chunk. The chunk's K/V follow the descriptor check: issued before
+  // it, they delay the descriptor's own (scalar) load by microseconds.
+  // (head_dim 256 loads its q row per wave inside the chunk: live across the
   // descriptor read it would spill.)
+  const bool prefix_wave = chunk >= NT && chunk < p.max_chunks;
+  const int page = prefix_wave ? p.page_table[(chunk - NT) * CK / DTREE_PAGE] : 0;
   HeadRow<D, R> qr;
-  if constexpr (D <= 128)
-    row_issue<D, R>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * (R / 2),
-                    p.rope_sin + qrow * (R / 2), h);
-  const int page = (chunk >= NT && chunk < p.max_chunks) ? p.page_table[(chunk - NT) * CK / DTREE_PAGE] : 0;
+  QStage qst;
+  if constexpr (D <= 128) q_stage_issue(p, hq, rb, qst);
 
+  if (pair >= p.splits * p.Hkv) return;
   const int P = p.desc->past_length, L = p.desc->num_nodes;
   const int nchunks = NT + (P + CK - 1) / CK;
   // A descriptor beyond the grid's capacity (P > max_past_length) or with more
@@ -443,6 +619,12 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     return;
   }
 
+  float* qs = reinterpret_cast<float*>(lds + TB * kStage);
+  if constexpr (D <= 128) {
+    q_stage_finish(qst, p.q_norm != nullptr, p.eps, qs);
+    __syncthreads();
+  }
+
   float m_run = kNeg, l_run = 0.f;
   f32x16_t o[ND];
 #pragma unroll
@@ -454,135 +636,150 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     // Tree chunks are waves 0 .. NT-1 of split 0, each with its own staging.
     if (32 * chunk < L) {
       uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)chunk * kStage);
-      tree_chunk<D, R>(p, qr, hq, g, G, P, L, chunk, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+      tree_chunk<D, R>(p, qr, qs, hq, g, G, P, L, chunk, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
     }
   } else if (chunk < nchunks) {
-    prefix_chunk<D, R>(p, qr, page, hq, g, P, chunk - NT, qrow, c, h, m_run, l_run, o);
+    if constexpr (D > 128)
+      row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm,
+                            p.rope_cos + qrow * (R / 2), p.rope_sin + qrow * (R / 2), h);
+    ChunkKV<D> kv;
+    prefix_issue<D>(p, kv, page, g, chunk - NT, c, h);
+    prefix_chunk<D, R>(p, qr, qs, kv, P, chunk - NT, c, h, m_run, l_run, o);
   }
 
-  // LDS merge of the four waves, 128 head dims per pass. The first barrier
-  // retires the tree chunk's staging, which shares this memory.
+  // ---- merge the four waves ----
+  // o holds this wave's chunk for the 32 queries x D dims in MFMA layout:
+  // lane (c, h), register r of block db = dim 32 db + acc_row(r, h) of query
+  // c. Wave w completes blocks db = w, w + 4, ...: every wave rescales its o
+  // to the common max and hands the blocks it does not complete to their
+  // owners through LDS in 16-byte pieces.
+  constexpr int NDW = ND / kWaves;  // blocks a wave completes: 1 (head_dim 128), 2 (256)
+  float* ml = reinterpret_cast<float*>(lds);             // [wave][m | l][32]
+  f32x4_t* xch = reinterpret_cast<f32x4_t*>(lds + kMl);  // [block][wave][4][lane]
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  // Thread t combines query q = t/8, dims pass*128 + d0 .. +15, d0 = 16 (t%8).
-  constexpr int kDims = 32 * D / (64 * kWaves);  // dims per thread: 16 per pass
-  const int t = threadIdx.x;
-  const int q = t >> 3, d0 = (t & 7) * 16;
-  float* mw = reinterpret_cast<float*>(lds) + wave * kWaveMerge;
-  const float* m0 = reinterpret_cast<const float*>(lds);
-  float acc[kDims];
-  float M = kNeg, tot = 0.f, wk[kWaves];
+  __syncthreads();  // retires the chunk staging (tree K/V, query rows), which shares this memory
+  if (h == 0) {
+    ml[wave * 64 + c] = m_run;
+    ml[wave * 64 + 32 + c] = l_tot;
+  }
+  __syncthreads();
+  float M = kNeg, tot = 0.f, self = 0.f;
 #pragma unroll
-  for (int pass = 0; pass < NP; ++pass) {
-    __syncthreads();
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[w * 64 + c]);
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+  for (int w = 0; w < kWaves; ++w) {
+    const float f = fast_exp2(ml[w * 64 + c] - M);
+    tot += f * ml[w * 64 + 32 + c];
+    if (w == wave) self = f;
+  }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mw[(32 * db + acc_row(r, h)) * MS + c] = o[4 * pass + db][r];
-    if (pass == 0 && h == 0) {
-      mw[kMergeDims * MS + c] = m_run;
-      mw[kMergeDims * MS + 32 + c] = l_tot;
+  for (int db = 0; db < ND; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] *= self;
+    if (db % kWaves != wave) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        xch[((db * kWaves + wave) * 4 + gq) * 64 + lane] =
+            f32x4_t{o[db][4 * gq], o[db][4 * gq + 1], o[db][4 * gq + 2], o[db][4 * gq + 3]};
     }
-    __syncthreads();
-    if (pass == 0) {
+  }
+  __syncthreads();
+  f32x16_t mine[NDW];  // completed blocks wave + kWaves * k
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m0[w * kWaveMerge + kMergeDims * MS + q]);
+  for (int db = 0; db < ND; ++db) {
+    if (db % kWaves != wave) continue;
+    f32x16_t a = o[db];
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        wk[w] = fast_exp2(m0[w * kWaveMerge + kMergeDims * MS + q] - M);
-        tot += wk[w] * m0[w * kWaveMerge + kMergeDims * MS + 32 + q];
+    for (int w = 0; w < kWaves; ++w) {
+      if (w == wave) continue;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const f32x4_t x = xch[((db * kWaves + w) * 4 + gq) * 64 + lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[4 * gq + i] += x[i];
       }
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float a = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) a += wk[w] * m0[w * kWaveMerge + (d0 + i) * MS + q];
-      acc[16 * pass + i] = a;
-    }
+    mine[db / kWaves] = a;
   }
 
   if (nsplit > 1) {
-    // Workgroup partial, laid out [i][thread] so both the stores here and the
-    // loads of the combining workgroup are coalesced.
+    // Workgroup partial: [block][lane][16] floats (each lane moves its block
+    // values in 16-byte agent-coherent stores and loads), then m and l of the
+    // 32 queries.
     const size_t stride = (size_t)32 * D + 64;
     const int hb = hq * NT + rb;  // (head, query block)
-    float* part = p.part + ((size_t)hb * p.splits + split) * stride;
+    const __amdgpu_buffer_rsrc_t prs =
+        buf_rsrc(p.part, (unsigned)((size_t)p.Hq * NT * p.splits * stride * sizeof(float)));
+    const unsigned pbase = (unsigned)((size_t)hb * p.splits * stride * sizeof(float));
+    const unsigned mine_off = pbase + (unsigned)((size_t)split * stride * sizeof(float));
 #pragma unroll
-    for (int i = 0; i < kDims; ++i) st_coherent(part + (size_t)i * 64 * kWaves + t, acc[i]);
-    if ((t & 7) == 0) {
-      st_coherent(part + 32 * D + q, M);
-      st_coherent(part + 32 * D + 32 + q, tot);
+    for (int k = 0; k < NDW; ++k) {
+      const unsigned off = mine_off + (unsigned)(((wave + kWaves * k) * 64 + lane) * 64);
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4_t, f32x4_t{mine[k][4 * gq], mine[k][4 * gq + 1], mine[k][4 * gq + 2],
+                                                mine[k][4 * gq + 3]}),
+            prs, (int)(off + 16 * gq), 0, kSc1);
+    }
+    float* part = p.part + ((size_t)hb * p.splits + split) * stride;
+    if (wave == 0 && h == 0) {
+      st_coherent(part + 32 * D + c, M);
+      st_coherent(part + 32 * D + 32 + c, tot);
     }
     wait_stores_done();
     __syncthreads();
-    if (t == 0) s_last = arrive(&p.counters[hb]) == nsplit - 1;
+    if (threadIdx.x == 0) {
+      // arrival count in the low half, workgroups off their XCD in the high
+      const bool native = xcc_id() == (int)(blockIdx.x % kXcds);
+      const int old = arrive_add(&p.counters[hb], native ? 1 : 1 + kForeign);
+      int last = 0;
+      if ((old & (kForeign - 1)) == nsplit - 1) {
+        last = native && old < kForeign && p.Hkv % kXcds == 0 ? 2 : 1;
+        reset_counter(&p.counters[hb]);
+      }
+      s_last = last;
+    }
     __syncthreads();
     if (!s_last) return;
-    if (t == 0) reset_counter(&p.counters[hb]);
 
-    // Partials are read kSb splits at a time (all loads of a batch in flight
-    // together) with a running max: one memory round trip per batch instead
-    // of two per split.
-    constexpr int kSb = 128 / kDims;  // 8 splits per batch at head_dim 128, 4 at 256
-    const float* base = p.part + (size_t)hb * p.splits * stride;
-    float Ms = kNeg;
-#pragma unroll
-    for (int i = 0; i < kDims; ++i) acc[i] = 0.f;
-    tot = 0.f;
-    for (int s0 = 0; s0 < nsplit; s0 += kSb) {
-      float v[kSb][kDims], mm[kSb], ll[kSb];
-#pragma unroll
-      for (int b = 0; b < kSb; ++b) {
-        const bool ok = s0 + b < nsplit;
-        const float* ps = base + (size_t)(ok ? s0 + b : 0) * stride;
-        mm[b] = ok ? ld_coherent(ps + 32 * D + q) : kNeg;
-        ll[b] = ok ? ld_coherent(ps + 32 * D + 32 + q) : 0.f;
-#pragma unroll
-        for (int i = 0; i < kDims; ++i) v[b][i] = ok ? ld_coherent(ps + (size_t)i * 64 * kWaves + t) : 0.f;
-      }
-      float gm = Ms;
-#pragma unroll
-      for (int b = 0; b < kSb; ++b) gm = fmaxf(gm, mm[b]);
-      const float r = fast_exp2(Ms - gm);
-      tot *= r;
-#pragma unroll
-      for (int i = 0; i < kDims; ++i) acc[i] *= r;
-#pragma unroll
-      for (int b = 0; b < kSb; ++b) {
-        const float w = fast_exp2(mm[b] - gm);
-        tot += w * ll[b];
-#pragma unroll
-        for (int i = 0; i < kDims; ++i) acc[i] += w * v[b][i];
-      }
-      Ms = gm;
-    }
+    // Every split of this head ran on this XCD when all are confirmed on
+    // their expected XCD and the heads of a KV group's splits share one
+    // (Hkv % 8 == 0): the partials are then read from the local L2.
+    if (s_last == 2) combine_splits<D, kSc0>(prs, pbase, stride, nsplit, wave, lane, c, tot, mine);
+    else combine_splits<D, kSc1>(prs, pbase, stride, nsplit, wave, lane, c, tot, mine);
   }
 
-  const int orow = 32 * rb + q;  // output row of thread t
+  // Output: lane (c, h) holds, per completed block, 4 runs of 4 consecutive
+  // dims (registers 4g .. 4g+3 = dims 32 db + 8g + 4h .. +3) of query c.
+  const int orow = 32 * rb + c;
   const float inv = (orow < L && tot > 0.f) ? 1.0f / tot : 0.f;
 #pragma unroll
-  for (int i0 = 0; i0 < kDims; i0 += 8) {
-    const int dd = (i0 / 16) * kMergeDims + d0 + (i0 % 16);  // head dim of acc[i0]
-    float y[8];
+  for (int k = 0; k < NDW; ++k) {
+    const int db = wave + kWaves * k;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = orow < L ? acc[i0 + i] * inv : 0.f;
-    if (GATE && orow < L) {
-      // o_proj input = attention * sigmoid(gate), gate = q_proj row dims D.. of the head
-      const float* gp = p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D + dd;
-      const f32x4_t g0 = *reinterpret_cast<const f32x4_t*>(gp);
-      const f32x4_t g1 = *reinterpret_cast<const f32x4_t*>(gp + 4);
+    for (int gq = 0; gq < 4; ++gq) {
+      const int dim = 32 * db + 8 * gq + 4 * h;
+      float y[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        y[i] *= 1.0f / (1.0f + __expf(-g0[i]));
-        y[i + 4] *= 1.0f / (1.0f + __expf(-g1[i]));
+      for (int i = 0; i < 4; ++i) y[i] = orow < L ? mine[k][4 * gq + i] * inv : 0.f;
+      if (GATE && orow < L) {
+        // o_proj input = attention * sigmoid(gate), gate = q_proj row dims D.. of the head
+        const f32x4_t gt = *reinterpret_cast<const f32x4_t*>(p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D +
+                                                             dim);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
       }
+      float rl[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
+      const u32x2_t hi = {pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
+      const u32x2_t lo = {pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
+      const int col = hq * D + dim;
+      const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
+      *reinterpret_cast<u32x2_t*>(p.out + oi) = hi;
+      if (p.out_lo) *reinterpret_cast<u32x2_t*>(p.out_lo + oi) = lo;
     }
-    u32x4_t hi, lo;
-    split8(y, hi, lo);
-    const int col = hq * D + dd;
-    const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
-    *reinterpret_cast<u32x4_t*>(p.out + oi) = hi;
-    if (p.out_lo) *reinterpret_cast<u32x4_t*>(p.out_lo + oi) = lo;
   }
 }
 

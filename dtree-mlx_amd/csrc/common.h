@@ -10,6 +10,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
@@ -157,6 +158,22 @@ __device__ __forceinline__ int arrive(int* counter) {
 }
 __device__ __forceinline__ void reset_counter(int* counter) {
   __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int arrive_add(int* counter, int v) {
+  return __hip_atomic_fetch_add(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// XCD placement. Workgroups are dispatched round-robin over the 8 XCDs
+// (blockIdx % 8); a workgroup checks its own with HW_REG_XCC_ID. Cross-
+// workgroup exchanges write through (sc1) and read from the local L2 (sc0)
+// only when every party is confirmed on the same XCD; an arrival from a
+// workgroup off its expected XCD adds kForeign to the counter.
+constexpr int kXcds = 8;
+constexpr int kForeign = 1 << 16;
+constexpr int kSc0 = 1;   // cache policy sc0: coherent within one XCD (read from its L2)
+constexpr int kSc1 = 16;  // cache policy sc1: coherent across the XCDs' L2s (written through / read past them)
+__device__ __forceinline__ int xcc_id() {
+  return __builtin_amdgcn_s_getreg(20 | (3 << 11));  // HW_REG_XCC_ID, bits [3:0]
 }
 
 }  // namespace dtree

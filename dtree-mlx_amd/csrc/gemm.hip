@@ -532,27 +532,14 @@ __device__ __forceinline__ void wg_tile_q4(const uint16_t* __restrict__ x, const
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* part, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)bytes, 0x00020000);
 }
-// sc1: coherent across the XCDs' L2s (written through / read past them);
-// sc0: coherent within one XCD (read from its L2, past the CU's L1).
-constexpr int kSc1 = 16;
-constexpr int kSc0 = 1;
-
 // Stream-K ranges in XCD order. Workgroups are dispatched round-robin over
 // the XCDs (blockIdx % 8; each workgroup checks its own with HW_REG_XCC_ID),
 // so logical range g = (blockIdx % 8) * (G / 8) + blockIdx / 8 puts the
 // consecutive ranges that share a column block on one XCD. A partial tile
 // is always written through (sc1), and read from that XCD's L2 (sc0) when
 // its writers and reader are all confirmed on the same XCD.
-constexpr int kXcds = 8;
-constexpr int kForeign = 1 << 16;  // arrival increment of a workgroup off its XCD
 __device__ __forceinline__ int sk_logical(int bid, int G) {
   return G % kXcds == 0 ? (bid % kXcds) * (G / kXcds) + bid / kXcds : bid;
-}
-__device__ __forceinline__ int xcc_id() {
-  return __builtin_amdgcn_s_getreg(20 | (3 << 11));  // HW_REG_XCC_ID, bits [3:0]
-}
-__device__ __forceinline__ int arrive_add(int* counter, int v) {
-  return __hip_atomic_fetch_add(counter, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Sum of the partial tiles of workgroups gf..gl for block b (slot q + b),
