@@ -113,6 +113,29 @@ __device__ __forceinline__ float row_sum32(float a) {
   return a + swz_xor16(a);  // the other 16-lane row
 }
 
+// (max, first index on ties): a total order, so a reduction's result does not
+// depend on how candidates are paired.
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
+  argmax_merge(v, i, dpp<CTRL>(v), dpp_i<CTRL>(i));
+}
+// (max, first index on ties) over TN lanes (32: each half-wave, 64: the wave).
+template <int TN>
+__device__ __forceinline__ void lane_argmax(float& v, int& i) {
+  argmax_dpp<0xB1>(v, i);
+  argmax_dpp<0x4E>(v, i);
+  argmax_dpp<0x141>(v, i);
+  argmax_dpp<0x140>(v, i);
+  argmax_merge(v, i, swz_xor16(v), swz_xor16_i(i));
+  if constexpr (TN == 64) argmax_merge(v, i, __shfl_xor(v, 32), __shfl_xor(i, 32));
+}
+
 // Row of 32x32 MFMA accumulator register r held by a lane in half h (= lane/32):
 // D[row][col] with col = lane % 32.
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }

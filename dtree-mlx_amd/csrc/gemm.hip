@@ -776,27 +776,7 @@ struct LmParams {
   int cand_blocks;
 };
 
-__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) {
-    v = ov;
-    i = oi;
-  }
-}
-template <int CTRL>
-__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
-  argmax_merge(v, i, dpp<CTRL>(v), dpp_i<CTRL>(i));
-}
-// (max, first index on ties) over TN lanes (32: each half-wave, 64: the wave).
-// The merge is a total order, so the result does not depend on the pairing.
-template <int TN>
-__device__ __forceinline__ void lane_argmax(float& v, int& i) {
-  argmax_dpp<0xB1>(v, i);
-  argmax_dpp<0x4E>(v, i);
-  argmax_dpp<0x141>(v, i);
-  argmax_dpp<0x140>(v, i);
-  argmax_merge(v, i, swz_xor16(v), swz_xor16_i(i));
-  if constexpr (TN == 64) argmax_merge(v, i, __shfl_xor(v, 32), __shfl_xor(i, 32));
-}
+
 
 template <int MB, int NB, int U, bool LO, bool TILED, bool Q4>
 __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {

@@ -23,8 +23,6 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const DtreeStepDesc* de
   rope_entry(desc, blockIdx.x * 256 + threadIdx.x, rows, half, base, cos_out, sin_out);
 }
 
-// x[m][:] = E[tokens[m]] (rows >= L zero), xg = bf16(x * g), per-tile sums of x^2.
-// Blocks [0, H/256) gather; the remaining blocks fill the RoPE table.
 // Element (row, col) of an embedding in DTREE_W_Q4G64 layout, dequantised:
 // scale * q + bias of the row's group col / 64.
 __device__ __forceinline__ float q4_element(const uint32_t* words, const uint32_t* sb, int row, int col, int H) {
@@ -37,9 +35,11 @@ __device__ __forceinline__ float q4_element(const uint32_t* words, const uint32_
   return __uint_as_float(pr << 16) * q + __uint_as_float(pr & 0xffff0000u);
 }
 
-// Thread = one hidden column over all rows: x[m] = E[tokens[m]], xg = split(x * g),
-// ss = per-32-column sums of x^2. Rows go in batches of 32 whose loads are all
-// issued before any use.
+// Thread = 8 consecutive hidden columns of one row (one 16-byte load of the
+// embedding row): x[m] = E[tokens[m]] (rows >= L zero), xg = split(x * g), and
+// the row's sum of x^2 over each 32-column tile, added over the tile's 4
+// threads with DPP. Blocks [0, gather_blocks) gather; the remaining blocks
+// fill the RoPE table.
 __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, const uint16_t* emb, int layout,
                                                     const uint16_t* emb_sb, int V, int H,
                                                     const uint16_t* g, int MP, float* x, uint16_t* xg,
@@ -50,52 +50,55 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
     rope_entry(desc, (blockIdx.x - gather_blocks) * 256 + threadIdx.x, MP, half, base, cos_out, sin_out);
     return;
   }
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  const int n = threadIdx.x & 31;
-  const bool in = col < H;
+  const int per_row = H >> 3;
+  const int gt = blockIdx.x * 256 + threadIdx.x;
+  const bool in = gt < MP * per_row;
+  const int m = in ? gt / per_row : 0, col = in ? (gt % per_row) * 8 : 0;
   const int L = min(desc->num_nodes, MP);
-  const float gw = in ? bf2f(g[col]) : 0.f;
-  for (int m0 = 0; m0 < MP; m0 += 32) {
-    float v[32];
+  float v[8];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const int m = m0 + j;
-      v[j] = 0.f;
-      if (in && m < L) {
-        const int tok = desc->tokens[m];
-        if (tok >= 0 && tok < V) {  // out-of-range ids embed as zero
-          if (layout == DTREE_W_Q4G64)
-            v[j] = q4_element(reinterpret_cast<const uint32_t*>(emb), reinterpret_cast<const uint32_t*>(emb_sb), tok,
-                              col, H);
-          else
-            v[j] = bf2f(emb[layout == DTREE_W_TILED ? tiled_index(tok, col, H) : (size_t)tok * H + col]);
-        }
-      }
-    }
+  for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  if (in && m < L) {
+    const int tok = desc->tokens[m];
+    if (tok >= 0 && tok < V) {  // out-of-range ids embed as zero
+      if (layout == DTREE_W_Q4G64) {
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const int m = m0 + j;
-      if (m >= MP) break;
-      if (in) {
-        x[(size_t)m * H + col] = v[j];
-        const float vg = v[j] * gw;
-        const uint16_t hi = f2bf(vg);
-        const size_t xi = xg_tiled ? tiled_index(m, col, H) : (size_t)m * H + col;
-        xg[xi] = hi;
-        if (xg_lo) xg_lo[xi] = f2bf(vg - bf2f(hi));
+        for (int i = 0; i < 8; ++i)
+          v[i] = q4_element(reinterpret_cast<const uint32_t*>(emb), reinterpret_cast<const uint32_t*>(emb_sb), tok,
+                            col + i, H);
+      } else {
+        const u32x4_t w = ld_u32x4(emb + (layout == DTREE_W_TILED ? tiled_index(tok, col, H) : (size_t)tok * H + col));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
       }
-      const float sq = row_sum32(v[j] * v[j]);  // this 32-column tile
-      if (in && n == 0) ss[ss_index(col >> 5, m, (H + 31) >> 5)] = sq;
     }
   }
+  if (in) {
+    const u32x4_t gwv = ld_u32x4(g + col);
+    float y[8], r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      y[i] = v[i] * __uint_as_float((i & 1) ? (gwv[i >> 1] & 0xffff0000u) : (gwv[i >> 1] << 16));
+      r[i] = y[i] - bf2f(f2bf(y[i]));
+    }
+    float* xr = x + (size_t)m * H + col;
+    *reinterpret_cast<f32x4_t*>(xr) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(xr + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+    const size_t xi = xg_tiled ? tiled_index(m, col, H) : (size_t)m * H + col;
+    *reinterpret_cast<u32x4_t*>(xg + xi) =
+        u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])};
+    if (xg_lo)
+      *reinterpret_cast<u32x4_t*>(xg_lo + xi) =
+          u32x4_t{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+  }
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sq += v[i] * v[i];
+  sq += dpp<0xB1>(sq);  // the 4 threads of a 32-column tile (a lane quad; rows hold whole quads)
+  sq += dpp<0x4E>(sq);
+  if (in && (col & 31) == 0) ss[ss_index(col >> 5, m, H >> 5)] = sq;
 }
 
-__device__ __forceinline__ void argmax_merge2(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) {
-    v = ov;
-    i = oi;
-  }
-}
 
 // One workgroup: reduce the LM-head candidates per tree row (wavefront
 // butterflies, first index on ties), then walk the tree from the root while
@@ -104,53 +107,97 @@ __device__ __forceinline__ void argmax_merge2(float& v, int& i, float ov, int oi
 __global__ __launch_bounds__(256) void walk_kernel(DtreeStepDesc* desc, const int2* cand, int nblocks, int MP,
                                                    int* result) {
   __shared__ int post[DTREE_MAX_NODES];
+  __shared__ int par_s[DTREE_MAX_NODES], tok_s[DTREE_MAX_NODES];
   const int L = min(max(desc->num_nodes, 1), min(MP, DTREE_MAX_NODES));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int m = wave; m < L; m += 4) {
-    float v = -__builtin_huge_valf();
-    int idx = 0x7fffffff;
-    for (int b = lane; b < nblocks; b += 64) {
-      const int2 cv = cand[cand_index(b, m, nblocks)];
-      argmax_merge2(v, idx, __int_as_float(cv.x), cv.y);
+  // The walk reads parents and tokens from LDS (one load per node here).
+  for (int m = threadIdx.x; m < L; m += 256) {
+    par_s[m] = desc->parents[m];
+    tok_s[m] = desc->tokens[m];
+  }
+  // Candidates of one 32-row block are [blocks][32] pairs: thread t takes
+  // workgroups t, t + 256, ... with all 32 rows (256 contiguous bytes in 16-
+  // byte loads), then each row is reduced over the wave (DPP) and the four
+  // waves' results are merged in wave order.
+  __shared__ float red_v[4][32];
+  __shared__ int red_i[4][32];
+  for (int r0 = 0; r0 < L; r0 += 32) {
+    float v[32];
+    int ix[32];
+#pragma unroll
+    for (int m = 0; m < 32; ++m) {
+      v[m] = -__builtin_huge_valf();
+      ix[m] = 0x7fffffff;
+    }
+    for (int b = threadIdx.x; b < nblocks; b += 256) {
+      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(cand + cand_index(b, r0, nblocks));
+      u32x4_t w[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) w[k] = src[k];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        argmax_merge(v[2 * k], ix[2 * k], __uint_as_float(w[k][0]), (int)w[k][1]);
+        argmax_merge(v[2 * k + 1], ix[2 * k + 1], __uint_as_float(w[k][2]), (int)w[k][3]);
+      }
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(v, o);
-      const int oi = __shfl_xor(idx, o);
-      argmax_merge2(v, idx, ov, oi);
+    for (int m = 0; m < 32; ++m) {
+      lane_argmax<64>(v[m], ix[m]);
+      if (lane == 0) {
+        red_v[wave][m] = v[m];
+        red_i[wave][m] = ix[m];
+      }
     }
-    if (lane == 0) post[m] = idx;
+    __syncthreads();
+    if (threadIdx.x < 32 && r0 + (int)threadIdx.x < L) {
+      const int m = threadIdx.x;
+      float bv = red_v[0][m];
+      int bi = red_i[0][m];
+#pragma unroll
+      for (int w2 = 1; w2 < 4; ++w2) argmax_merge(bv, bi, red_v[w2][m], red_i[w2][m]);
+      post[r0 + m] = bi;
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc[DTREE_MAX_NODES];
-    int n = 1, cur = 0;
-    acc[0] = 0;
-    int nxt = post[0];
+  // The walk on wave 0: at each step every lane tests its nodes against
+  // (parent cur, token nxt) and a ballot picks the largest match, i.e. the
+  // last node inserted with that token (child_maps semantics). cur strictly
+  // increases, so the walk ends within L steps.
+  __shared__ int acc_s[DTREE_MAX_NODES];
+  __shared__ int walk_n;
+  if (wave == 0) {
+    int n = 1, cur = 0, nxt = post[0];
+    if (lane == 0) acc_s[0] = 0;
     for (;;) {
-      // child_maps[cur][token] keeps the last node inserted with that token.
       int found = -1;
-      for (int t = L - 1; t > cur; --t)
-        if (desc->parents[t] == cur && desc->tokens[t] == nxt) {
-          found = t;
-          break;
-        }
+      for (int base = ((L - 1) >> 6) << 6; base >= 0 && found < 0; base -= 64) {
+        const int t = base + lane;
+        const bool hit = t > cur && t < L && par_s[t] == cur && tok_s[t] == nxt;
+        const unsigned long long m = __ballot(hit);
+        if (m) found = base + 63 - __builtin_clzll(m);
+      }
       if (found < 0) break;
       cur = found;
-      acc[n++] = cur;
+      if (lane == 0) acc_s[n] = cur;
+      ++n;
       nxt = post[cur];
     }
-    desc->n_accepted = n;
-    desc->bonus_token = nxt;
-    for (int i = 0; i < n; ++i) desc->accepted[i] = acc[i];
-    if (result) {
-      result[0] = n;
-      result[1] = nxt;
-      result[2] = L;
-      for (int i = 0; i < n; ++i) result[3 + i] = acc[i];
+    if (lane == 0) {
+      walk_n = n;
+      desc->n_accepted = n;
+      desc->bonus_token = nxt;
+      if (result) {
+        result[0] = n;
+        result[1] = nxt;
+        result[2] = L;
+      }
     }
   }
   __syncthreads();
+  for (int i = threadIdx.x; i < walk_n; i += 256) {
+    desc->accepted[i] = acc_s[i];
+    if (result) result[3 + i] = acc_s[i];
+  }
   for (int m = threadIdx.x; m < L; m += 256) {
     desc->posterior[m] = post[m];
     if (result) result[3 + DTREE_MAX_NODES + m] = post[m];
@@ -158,50 +205,82 @@ __global__ __launch_bounds__(256) void walk_kernel(DtreeStepDesc* desc, const in
 }
 
 // Blocks [0, layers*Hkv): K rows of one (layer, kv head); next layers*Hkv
-// blocks: V^T columns; one more block: hidden-state select. Kept rows are
-// read into LDS before any is written, so the in-place move is safe.
+// blocks: V^T columns; kHidBlocks more blocks: hidden-state select. Kept rows are
+// read into LDS before any is written, so the in-place move is safe. The
+// page and slot of every source (P + accepted[j]) and destination (P + j)
+// position are looked up once per block; K rows move in 16-byte pieces, and
+// V^T (positions contiguous within a dim) is walked position-fastest, so a
+// wave's reads and writes of one dim touch one or two 128-byte lines.
+constexpr int kHidBlocks = 16;  // blocks of the compaction's hidden-state select
+
 __global__ __launch_bounds__(256) void compact_kernel(const DtreeStepDesc* desc, uint16_t* kp, uint16_t* vp,
                                                       size_t layer_stride, int layers, int Hkv, int D,
                                                       const int* page_table, const uint16_t* hid_in, int hid_w,
                                                       uint16_t* hid_out) {
-  __shared__ uint16_t buf[DTREE_MAX_NODES * 128];
+  __shared__ u32x4_t buf[DTREE_MAX_NODES * 16];  // 32 KB: n rows x 128 dims (bf16) per pass
   __shared__ int acc[DTREE_MAX_NODES];
+  __shared__ int src_row[DTREE_MAX_NODES], dst_row[DTREE_MAX_NODES];  // page * 64 + slot
   const int n = min(max(desc->n_accepted, 0), DTREE_MAX_NODES), P = desc->past_length, L = desc->num_nodes;
-  for (int i = threadIdx.x; i < n; i += 256) acc[i] = desc->accepted[i];
-  __syncthreads();
   const int nkv = layers * Hkv;
   const int b = blockIdx.x;
+  const int t = threadIdx.x;
+  if (t < n) {
+    const int a = desc->accepted[t];
+    acc[t] = a;
+    if (b < 2 * nkv) {
+      const int ps = P + a, pd = P + t;
+      src_row[t] = page_table[ps / DTREE_PAGE] * DTREE_PAGE + ps % DTREE_PAGE;
+      dst_row[t] = page_table[pd / DTREE_PAGE] * DTREE_PAGE + pd % DTREE_PAGE;
+    }
+  }
+  __syncthreads();
   if (b >= 2 * nkv) {
+    // hidden select over kHidBlocks blocks, 16-byte pieces (hid_w % 8 == 0)
     if (!hid_out) return;
-    for (int e = threadIdx.x; e < n * hid_w; e += 256) {
-      const int j = e / hid_w, col = e % hid_w;
-      hid_out[(size_t)j * hid_w + col] = hid_in[(size_t)acc[j] * hid_w + col];
+    const int nch = hid_w / 8;
+    for (int e = (b - 2 * nkv) * 256 + t; e < n * nch; e += kHidBlocks * 256) {
+      const int j = e / nch, ch = e % nch;
+      *reinterpret_cast<u32x4_t*>(hid_out + (size_t)j * hid_w + 8 * ch) =
+          *reinterpret_cast<const u32x4_t*>(hid_in + (size_t)acc[j] * hid_w + 8 * ch);
     }
     return;
   }
   if (n >= L) return;  // every tree row kept in place (adapters.py:654-655)
   const int layer = (b % nkv) / Hkv, g = (b % nkv) % Hkv;
-  const bool is_v = b >= nkv;
-  uint16_t* pool = (is_v ? vp : kp) + layer_stride * layer;
-  // One kept row = D values; rows staged through LDS in D/128 passes.
+  if (b < nkv) {
+    // K: row of position (page, slot) at ((page * Hkv + g) * 64 + slot) * D.
+    uint16_t* pool = kp + layer_stride * layer;
+    for (int d0 = 0; d0 < D; d0 += 128) {
+      const int dw = min(128, D - d0), nch = dw / 8;  // 16-byte pieces per row this pass
+      for (int e = t; e < n * nch; e += 256) {
+        const int j = e / nch, ch = e % nch, r = src_row[j];
+        const size_t idx = ((size_t)((r / DTREE_PAGE) * Hkv + g) * DTREE_PAGE + r % DTREE_PAGE) * D + d0 + 8 * ch;
+        buf[j * 16 + ch] = *reinterpret_cast<const u32x4_t*>(pool + idx);
+      }
+      __syncthreads();
+      for (int e = t; e < n * nch; e += 256) {
+        const int j = e / nch, ch = e % nch, r = dst_row[j];
+        const size_t idx = ((size_t)((r / DTREE_PAGE) * Hkv + g) * DTREE_PAGE + r % DTREE_PAGE) * D + d0 + 8 * ch;
+        *reinterpret_cast<u32x4_t*>(pool + idx) = buf[j * 16 + ch];
+      }
+      __syncthreads();
+    }
+    return;
+  }
+  // V^T: element (dim d, position (page, slot)) at ((page * Hkv + g) * D + d) * 64 + slot.
+  uint16_t* pool = vp + layer_stride * layer;
+  uint16_t* vb = reinterpret_cast<uint16_t*>(buf);
   for (int d0 = 0; d0 < D; d0 += 128) {
     const int dw = min(128, D - d0);
-    for (int e = threadIdx.x; e < n * dw; e += 256) {
-      const int j = e / dw, d = d0 + e % dw;
-      const int pos = P + acc[j];
-      const int page = page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
-      const size_t idx = is_v ? ((size_t)(page * Hkv + g) * D + d) * DTREE_PAGE + off
-                              : ((size_t)(page * Hkv + g) * DTREE_PAGE + off) * D + d;
-      buf[j * 128 + (d - d0)] = pool[idx];
+    for (int e = t; e < n * dw; e += 256) {
+      const int d = d0 + e / n, j = e % n, r = src_row[j];
+      vb[(d - d0) * n + j] =
+          pool[((size_t)((r / DTREE_PAGE) * Hkv + g) * D + d) * DTREE_PAGE + r % DTREE_PAGE];
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < n * dw; e += 256) {
-      const int j = e / dw, d = d0 + e % dw;
-      const int pos = P + j;
-      const int page = page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
-      const size_t idx = is_v ? ((size_t)(page * Hkv + g) * D + d) * DTREE_PAGE + off
-                              : ((size_t)(page * Hkv + g) * DTREE_PAGE + off) * D + d;
-      pool[idx] = buf[j * 128 + (d - d0)];
+    for (int e = t; e < n * dw; e += 256) {
+      const int d = d0 + e / n, j = e % n, r = dst_row[j];
+      pool[((size_t)((r / DTREE_PAGE) * Hkv + g) * D + d) * DTREE_PAGE + r % DTREE_PAGE] = vb[(d - d0) * n + j];
     }
     __syncthreads();
   }
@@ -272,7 +351,10 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
   DTREE_REQUIRE(embed_layout != DTREE_W_Q4G64 || embed_scales, "embed: q4 embedding needs embed_scales");
   DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || (xg_layout == DTREE_W_TILED && hidden % 64 == 0), "embed: xg layout");
   DTREE_REQUIRE(rows_padded > 0 && rows_padded <= DTREE_MAX_NODES && rows_padded % 32 == 0, "embed: rows_padded");
-  const int gather = (hidden + 255) / 256;
+  DTREE_REQUIRE(((uintptr_t)embed & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
+                    ((uintptr_t)xg & 15) == 0 && ((uintptr_t)xg_lo & 15) == 0,
+                "embed: embed, norm_w, x, xg and xg_lo must be 16-byte aligned");
+  const int gather = (rows_padded * (hidden / 8) + 255) / 256;
   int rope_blocks = 0;
   if (rope_cos && rope_sin) {
     DTREE_REQUIRE(head_dim > 0 && head_dim % 2 == 0, "embed: head_dim");
@@ -302,10 +384,12 @@ extern "C" int dtree_compact(const DtreeStepDesc* desc, uint16_t* k_pages, uint1
                              const uint16_t* hidden_in, int32_t hidden_width, uint16_t* hidden_out,
                              hipStream_t stream) {
   DTREE_REQUIRE(desc && page_table, "compact: null pointer");
-  DTREE_REQUIRE(layers >= 0 && num_kv_heads > 0 && head_dim > 0, "compact: shape");
+  DTREE_REQUIRE(layers >= 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 8 == 0, "compact: shape");
   DTREE_REQUIRE(layers == 0 || (k_pages && v_pages), "compact: null cache");
-  DTREE_REQUIRE(!hidden_out || (hidden_in && hidden_width > 0), "compact: hidden_in / hidden_width");
-  const int grid = 2 * layers * num_kv_heads + 1;
+  DTREE_REQUIRE(!hidden_out || (hidden_in && hidden_width > 0 && hidden_width % 8 == 0 &&
+                                 ((uintptr_t)hidden_in & 15) == 0 && ((uintptr_t)hidden_out & 15) == 0),
+                "compact: hidden_in / hidden_width (a multiple of 8, 16-byte aligned rows)");
+  const int grid = 2 * layers * num_kv_heads + kHidBlocks;
   compact_kernel<<<grid, 256, 0, stream>>>(desc, k_pages, v_pages, layer_stride, layers, num_kv_heads, head_dim,
                                            page_table, hidden_in, hidden_width, hidden_out);
   DTREE_LAUNCH_CHECK("compact launch");
