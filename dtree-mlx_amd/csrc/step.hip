@@ -115,38 +115,43 @@ __global__ __launch_bounds__(256) void walk_kernel(DtreeStepDesc* desc, const in
     par_s[m] = desc->parents[m];
     tok_s[m] = desc->tokens[m];
   }
-  // Candidates of one 32-row block are [blocks][32] pairs: thread t takes
-  // workgroups t, t + 256, ... with all 32 rows (256 contiguous bytes in 16-
-  // byte loads), then each row is reduced over the wave (DPP) and the four
-  // waves' results are merged in wave order.
+  // Candidates of one 32-row block are [blocks][32] pairs, 256 bytes per
+  // workgroup. Thread t = 16 s + j reads the 16 bytes of rows 2j, 2j + 1 of
+  // workgroups s, s + 16, ..., so each wave load covers 1 KB contiguous; the
+  // four lanes of a wave that share j, then the four waves, are merged
+  // ((max, first index) is a total order, so the pairing does not matter).
   __shared__ float red_v[4][32];
   __shared__ int red_i[4][32];
+  constexpr int kBatch = 32;  // loads in flight per thread
+  const int j = threadIdx.x & 15, s0 = threadIdx.x >> 4;
   for (int r0 = 0; r0 < L; r0 += 32) {
-    float v[32];
-    int ix[32];
+    const __amdgpu_buffer_rsrc_t crs = buf_rsrc(cand + cand_index(0, r0, nblocks), (unsigned)nblocks * 256u);
+    float v0 = -__builtin_huge_valf(), v1 = v0;
+    int i0 = 0x7fffffff, i1 = i0;
+    for (int b0 = s0; b0 < nblocks; b0 += 16 * kBatch) {
+      u32x4_t w[kBatch];
 #pragma unroll
-    for (int m = 0; m < 32; ++m) {
-      v[m] = -__builtin_huge_valf();
-      ix[m] = 0x7fffffff;
-    }
-    for (int b = threadIdx.x; b < nblocks; b += 256) {
-      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(cand + cand_index(b, r0, nblocks));
-      u32x4_t w[16];
+      for (int k = 0; k < kBatch; ++k) {
+        const int b = b0 + 16 * k;
+        w[k] = buf_ld(crs, b < nblocks ? (unsigned)(b * 256 + j * 16) : kOob);
+      }
 #pragma unroll
-      for (int k = 0; k < 16; ++k) w[k] = src[k];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        argmax_merge(v[2 * k], ix[2 * k], __uint_as_float(w[k][0]), (int)w[k][1]);
-        argmax_merge(v[2 * k + 1], ix[2 * k + 1], __uint_as_float(w[k][2]), (int)w[k][3]);
+      for (int k = 0; k < kBatch; ++k) {
+        if (b0 + 16 * k < nblocks) {
+          argmax_merge(v0, i0, __uint_as_float(w[k][0]), (int)w[k][1]);
+          argmax_merge(v1, i1, __uint_as_float(w[k][2]), (int)w[k][3]);
+        }
       }
     }
-#pragma unroll
-    for (int m = 0; m < 32; ++m) {
-      lane_argmax<64>(v[m], ix[m]);
-      if (lane == 0) {
-        red_v[wave][m] = v[m];
-        red_i[wave][m] = ix[m];
-      }
+    argmax_merge(v0, i0, swz_xor16(v0), swz_xor16_i(i0));
+    argmax_merge(v1, i1, swz_xor16(v1), swz_xor16_i(i1));
+    argmax_merge(v0, i0, __shfl_xor(v0, 32), __shfl_xor(i0, 32));
+    argmax_merge(v1, i1, __shfl_xor(v1, 32), __shfl_xor(i1, 32));
+    if (lane < 16) {
+      red_v[wave][2 * lane] = v0;
+      red_i[wave][2 * lane] = i0;
+      red_v[wave][2 * lane + 1] = v1;
+      red_i[wave][2 * lane + 1] = i1;
     }
     __syncthreads();
     if (threadIdx.x < 32 && r0 + (int)threadIdx.x < L) {
@@ -371,7 +376,7 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
 extern "C" int dtree_accept_walk(DtreeStepDesc* desc, const void* candidates, int32_t num_candidate_blocks,
                                  int32_t rows_padded, int32_t* result, hipStream_t stream) {
   DTREE_REQUIRE(desc && candidates, "accept_walk: null pointer");
-  DTREE_REQUIRE(num_candidate_blocks > 0, "accept_walk: num_candidate_blocks");
+  DTREE_REQUIRE(num_candidate_blocks > 0 && num_candidate_blocks <= (1 << 20), "accept_walk: num_candidate_blocks");
   DTREE_REQUIRE(rows_padded > 0 && rows_padded <= DTREE_MAX_NODES, "accept_walk: rows_padded");
   walk_kernel<<<1, 256, 0, stream>>>(desc, reinterpret_cast<const int2*>(candidates), num_candidate_blocks,
                                      rows_padded, result);
