@@ -389,7 +389,6 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 // runs the shared tile epilogue.
 constexpr int kSkMaxBlocks = 4;  // 64-column blocks one workgroup may touch
 constexpr int kSkDepth = 4;      // units in flight per wave
-constexpr int kRedBatch = 8;     // partial tiles a last arriver loads per round
 constexpr int kSkMaxGrid = 1024; // CU-count bound used for workspace sizing
 constexpr int kSkMaxKb = 64;     // q4: K groups whose activation sums one workgroup keeps
 
@@ -542,24 +541,26 @@ __device__ __forceinline__ int sk_logical(int bid, int G) {
   return G % kXcds == 0 ? (bid % kXcds) * (G / kXcds) + bid / kXcds : bid;
 }
 
-// Sum of the partial tiles of workgroups gf..gl for block b (slot q + b),
-// elements 8t .. 8t+7: every partial in flight at once (kRedBatch per round;
-// ranged loads past the last return zero and add nothing), added in
-// workgroup order.
+// One round of partial-tile loads for block b: the partials of workgroups
+// q0 .. min(q0 + kRedBatch, q_end) - 1 (slot q + b), elements 8t .. 8t+7, as
+// (16-byte, 16-byte) pairs; slots past the last read zero (ranged loads) and
+// are not added. Sole-owner blocks pass q_end = q0 and load nothing.
+constexpr int kRedBatch = 8;
 template <int AUX>
-__device__ __forceinline__ void sum_partials(__amdgpu_buffer_rsrc_t prs, int b, int gf, int gl, int t, f32x4_t& s0,
-                                             f32x4_t& s1) {
+__device__ __forceinline__ void partials_issue(__amdgpu_buffer_rsrc_t prs, int b, int q0, int q_end, int t,
+                                               u32x4_t (&v)[kRedBatch][2]) {
   constexpr int TE = 32 * 64;
-  for (int q = gf; q <= gl; q += kRedBatch) {
-    u32x4_t v[kRedBatch][2];
 #pragma unroll
-    for (int z = 0; z < kRedBatch; ++z) {
-      const unsigned off = q + z <= gl ? (unsigned)(((q + z + b) * TE + 8 * t) * 4) : kOob;
-      v[z][0] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0, AUX);
-      v[z][1] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(off + 16), 0, AUX);
-    }
+  for (int z = 0; z < kRedBatch; ++z) {
+    const unsigned off = q0 + z < q_end ? (unsigned)(((q0 + z + b) * TE + 8 * t) * 4) : kOob;
+    v[z][0] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0, AUX);
+    v[z][1] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(off + 16), 0, AUX);
+  }
+}
+__device__ __forceinline__ void partials_add(const u32x4_t (&v)[kRedBatch][2], int n, f32x4_t& s0, f32x4_t& s1) {
 #pragma unroll
-    for (int z = 0; z < kRedBatch; ++z) {
+  for (int z = 0; z < kRedBatch; ++z) {
+    if (z < n) {
       s0 += __builtin_bit_cast(f32x4_t, v[z][0]);
       s1 += __builtin_bit_cast(f32x4_t, v[z][1]);
     }
@@ -573,7 +574,7 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   __shared__ float xsum_lds[Q4 ? kSkMaxKb * 32 : 1];      // q4: [local group][row] sum of x
   __shared__ float rs[32];
   __shared__ float rs_scratch[kThreads];
-  __shared__ int last_flag[kSkMaxBlocks];
+  __shared__ int last_flag[kSkMaxBlocks], first_q[kSkMaxBlocks], pieces[kSkMaxBlocks];
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = p.G, T = p.T, nkb = p.k >> 6;
@@ -696,8 +697,18 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   // ---- per block: add the four waves; publish or finish ----
   const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
   const int t = threadIdx.x;  // owns tile elements 8t .. 8t+7
-  auto owner = [&](int u) { return (int)(((long long)(u + 1) * G + T - 1) / T) - 1; };
+  // Workgroup whose range holds unit u (T * G < 2^31, host-checked).
+  auto owner = [&](int u) { return (int)(((unsigned)(u + 1) * (unsigned)G + (unsigned)(T - 1)) / (unsigned)T) - 1; };
   bool any_shared = false;
+  // The residual rows of the first two blocks go out now (a workgroup spans
+  // at most two blocks at the usual shapes): their round trip overlaps the
+  // publish and the arrival below.
+  constexpr int IT = TE / kThreads;
+  float xo0[IT + 1], xo1[IT + 1];
+  if constexpr (EPI == DTREE_EPI_RESIDUAL) {
+    residual_issue<32, TN>(p, b_first, xo0);
+    if (nloc > 1) residual_issue<32, TN>(p, b_first + 1, xo1);
+  }
   for (int j = 0; j < nloc; ++j) {
     const int b = b_first + j;
     const int gf = owner(b * nkb), gl = owner((b + 1) * nkb - 1);
@@ -741,26 +752,54 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
       }
     }
     last_flag[t] = last;
+    first_q[t] = gf;
+    pieces[t] = last && gf != gl ? gl - gf + 1 : 0;
   }
   __syncthreads();
 
-  for (int j = 0; j < nloc; ++j) {
-    if (!last_flag[j]) continue;  // uniform: flag in LDS
-    const int b = b_first + j;
-    const int gf = owner(b * nkb), gl = owner((b + 1) * nkb - 1);
+  // The blocks this workgroup finishes, in order. The first round of the next
+  // block's partials is in flight during the current block's epilogue.
+  auto flag = [&](int j) { return __builtin_amdgcn_readfirstlane(last_flag[j]); };
+  auto next_last = [&](int j) {
+    for (++j; j < nloc && !flag(j); ++j) {}
+    return j;
+  };
+  u32x4_t pv[kRedBatch][2];
+  auto issue_partials = [&](int j, int q0) {
+    const int q_end = __builtin_amdgcn_readfirstlane(first_q[j]) + __builtin_amdgcn_readfirstlane(pieces[j]);
+    if (flag(j) == 2) partials_issue<kSc0>(prs, b_first + j, q0, q_end, t, pv);
+    else partials_issue<kSc1>(prs, b_first + j, q0, q_end, t, pv);
+  };
+  int j = next_last(-1);
+  if (j < nloc) issue_partials(j, __builtin_amdgcn_readfirstlane(first_q[j]));
+  while (j < nloc) {
+    const int np = __builtin_amdgcn_readfirstlane(pieces[j]);
+    const int jn = next_last(j);
     float* red = acc_lds + (j * kWaves) * TE;
-    // The residual rows go out with the partials: one round trip for both.
-    float xo[TE / kThreads + 1];
-    if constexpr (EPI == DTREE_EPI_RESIDUAL) residual_issue<32, TN>(p, b, xo);
-    if (gf != gl) {
+    if (np > 0) {
+      const int q0 = __builtin_amdgcn_readfirstlane(first_q[j]);
       f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
-      if (last_flag[j] == 2) sum_partials<kSc0>(prs, b, gf, gl, t, s0, s1);
-      else sum_partials<kSc1>(prs, b, gf, gl, t, s0, s1);
+      partials_add(pv, np < kRedBatch ? np : kRedBatch, s0, s1);
+      for (int q = kRedBatch; q < np; q += kRedBatch) {  // more than kRedBatch contributors
+        issue_partials(j, q0 + q);
+        partials_add(pv, np - q < kRedBatch ? np - q : kRedBatch, s0, s1);
+      }
       reinterpret_cast<f32x4_t*>(red + 8 * t)[0] = s0;
       reinterpret_cast<f32x4_t*>(red + 8 * t)[1] = s1;
     }
+    if (jn < nloc) issue_partials(jn, __builtin_amdgcn_readfirstlane(first_q[jn]));
     __syncthreads();
-    tile_epilogue<32, TN, EPI>(p, red, rs, b, EPI == DTREE_EPI_RESIDUAL ? xo : nullptr);
+    float xj[IT + 1];
+    if constexpr (EPI == DTREE_EPI_RESIDUAL) {
+      if (j >= 2) {
+        residual_issue<32, TN>(p, b_first + j, xj);
+      } else {
+#pragma unroll
+        for (int i = 0; i <= IT; ++i) xj[i] = j == 0 ? xo0[i] : xo1[i];
+      }
+    }
+    tile_epilogue<32, TN, EPI>(p, red, rs, b_first + j, EPI == DTREE_EPI_RESIDUAL ? xj : nullptr);
+    j = jn;
   }
 }
 
@@ -1166,6 +1205,7 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     const int nblk = a->n / 64;
     p.T = nblk * nkb;
     p.G = sk_grid(p.T, nkb, cus < kSkMaxGrid ? cus : kSkMaxGrid);
+    DTREE_REQUIRE((long long)p.T * p.G < (1LL << 31), "gemm: too many 64 x 64 units for the stream-K schedule");
     const size_t need_sk = sk_workspace_bytes(a->n, a->k, cus < kSkMaxGrid ? cus : kSkMaxGrid);
     DTREE_REQUIRE(a->workspace_bytes >= need_sk, "gemm: workspace too small for the stream-K schedule");
     p.part_bytes = (unsigned)(need_sk - kCounterBytes);
