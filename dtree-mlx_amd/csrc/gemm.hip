@@ -980,35 +980,52 @@ static void launch_sk(const GemmParams& p, int epi, hipStream_t st) {
 }
 
 
-// ---- data-parallel GEMM (32 tiled rows, bf16): no cross-workgroup sums ----
-// A workgroup owns one 32-column output tile over the whole K. Wave w streams
-// K blocks w, w + 4, ... through a kDpDepth-deep register ring (weights and
-// both activation planes of kDpDepth blocks in flight), the waves' partial
-// tiles are added in LDS in wave order (deterministic), and the shared tile
-// epilogue runs. Trades activation re-reads (from L2) for the stream-K
-// schedule's cross-workgroup publish / arrive / reduce tail.
+// ---- data-parallel GEMM (32 tiled rows, bf16) ------------------------------
+// A workgroup owns one 32-column output tile over the whole K (KS = 1) or
+// over one half of it (KS = 2). Wave w streams the K blocks w, w + 4, ... of
+// its range through a kDpDepth-deep register ring (weights and both
+// activation planes of kDpDepth blocks in flight), the waves' partial tiles
+// are added in LDS in wave order (deterministic), and the shared tile
+// epilogue runs. Each CU reads every activation block of its K range from L2
+// (about twice the bytes of its weights), so a CU's load bandwidth bounds
+// the one-workgroup-per-tile launch when N / 32 is well below the CU count;
+// KS = 2 puts twice the workgroups on the chip, each with half the bytes.
+// The two halves of a tile run as workgroups b and b + 8, which the
+// round-robin dispatch places on one XCD; each publishes its partial tile
+// (4 KB) written through, and the last to arrive adds the two (half 0 +
+// half 1: fp32 addition is commutative, so the sum does not depend on which
+// half arrives last) and runs the epilogue, reading its partner's tile from
+// its own L2 when both placements are confirmed (HW_REG_XCC_ID).
 constexpr int kDpDepth = 4;
 
-template <bool LO, int EPI>
+template <bool LO, int EPI, int KS>
 __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
   constexpr int TN = 32, TE = 32 * TN;
   __shared__ float red[kWaves * TE];
   __shared__ float rs[32];
   __shared__ float rs_scratch[kThreads];
+  __shared__ int last_s;
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = blockIdx.x, nkb = p.k >> 6;
+  const int nkb = p.k >> 6;
+  // KS = 2: blockIdx = 16 * (tile / 8) + 8 * half + tile % 8 (host: tiles % 8 == 0).
+  const int bid = blockIdx.x;
+  const int half = KS == 2 ? (bid >> 3) & 1 : 0;
+  const int tile = KS == 2 ? ((bid >> 4) << 3) + (bid & 7) : bid;
+  const int kb0 = KS == 2 ? half * ((nkb + 1) >> 1) : 0;
+  const int kb1 = KS == 2 ? (half ? nkb : (nkb + 1) >> 1) : nkb;
+  const int nk = kb1 - kb0;
   float ssv[kSsBatch];
   ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(p.x, p.x_bytes), xlrs = buf_rsrc(p.x_lo, LO ? p.x_bytes : 0u);
   const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(p.w, p.w_bytes);
   const unsigned wtile = (unsigned)(tile * nkb * 2048) * 2u;
-  const int n = wave < nkb ? (nkb - wave + kWaves - 1) / kWaves : 0;
+  const int n = wave < nk ? (nk - wave + kWaves - 1) / kWaves : 0;
   u32x4_t wr[kDpDepth][4], xr[kDpDepth][2][4];
   // Slots past the wave's blocks are refilled with ranged loads that return
   // zero (same loads on every path, see kOob) and are never consumed.
   auto issue = [&](int s, int j) {
-    const unsigned off = j < n ? (unsigned)((wave + kWaves * j) * 2048 + lane * 8) * 2u : kOob;
+    const unsigned off = j < n ? (unsigned)((kb0 + wave + kWaves * j) * 2048 + lane * 8) * 2u : kOob;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       xr[s][0][i] = buf_ld(xrs, off + 1024u * i);
@@ -1039,7 +1056,8 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
       issue(s, j + kDpDepth);
     }
   }
-  // The residual rows are in flight during the wave reduction.
+  // The residual rows are in flight during the wave reduction (and the
+  // partial exchange).
   float xo[TE / kThreads + 1];
   if constexpr (EPI == DTREE_EPI_RESIDUAL) residual_issue<32, TN>(p, tile, xo);
   // Waves 1..3 park their tiles; wave 0 adds them in wave order into slot 0.
@@ -1058,23 +1076,56 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
     for (int r = 0; r < 16; ++r) red[acc_row(r, h) * TN + c] = acc[r];
   }
   __syncthreads();
+  if constexpr (KS == 2) {
+    // Thread t holds elements 4t .. 4t+3 of the tile; slot 2 * tile + half.
+    const int t = threadIdx.x;
+    const bool native = xcc_id() == (bid & 7);
+    const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
+    const f32x4_t mine = reinterpret_cast<const f32x4_t*>(red)[t];
+    const int off = ((2 * tile + half) * TE + 4 * t) * 4;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, mine), prs, off, 0, kSc1);
+    wait_stores_done();
+    __syncthreads();
+    if (t == 0) {
+      const int old = arrive_add(&p.counters[tile], native ? 1 : 1 + kForeign);
+      int last = 0;
+      if ((old & (kForeign - 1)) == 1) {
+        last = native && old < kForeign ? 2 : 1;
+        reset_counter(&p.counters[tile]);
+      }
+      last_s = last;
+    }
+    __syncthreads();
+    const int last = __builtin_amdgcn_readfirstlane(last_s);
+    if (!last) return;
+    const int poff = ((2 * tile + (half ^ 1)) * TE + 4 * t) * 4;
+    const u32x4_t other = last == 2 ? __builtin_amdgcn_raw_buffer_load_b128(prs, poff, 0, kSc0)
+                                    : __builtin_amdgcn_raw_buffer_load_b128(prs, poff, 0, kSc1);
+    reinterpret_cast<f32x4_t*>(red)[t] = half ? __builtin_bit_cast(f32x4_t, other) + mine
+                                              : mine + __builtin_bit_cast(f32x4_t, other);
+    __syncthreads();
+  }
   tile_epilogue<32, TN, EPI>(p, red, rs, tile, EPI == DTREE_EPI_RESIDUAL ? xo : nullptr);
 }
 
-template <bool LO>
+template <bool LO, int KS>
 static void launch_dp(const GemmParams& p, int epi, hipStream_t st) {
-  const int grid = p.n / 32;
+  const int grid = KS * (p.n / 32);
   switch (epi) {
-    case DTREE_EPI_STORE_F32: dp_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<grid, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_RESIDUAL: dp_gemm_kernel<LO, DTREE_EPI_RESIDUAL><<<grid, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_SWIGLU: dp_gemm_kernel<LO, DTREE_EPI_SWIGLU><<<grid, kThreads, 0, st>>>(p); break;
-    default: dp_gemm_kernel<LO, DTREE_EPI_STORE_BF16><<<grid, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_STORE_F32: dp_gemm_kernel<LO, DTREE_EPI_STORE_F32, KS><<<grid, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: dp_gemm_kernel<LO, DTREE_EPI_RESIDUAL, KS><<<grid, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: dp_gemm_kernel<LO, DTREE_EPI_SWIGLU, KS><<<grid, kThreads, 0, st>>>(p); break;
+    default: dp_gemm_kernel<LO, DTREE_EPI_STORE_BF16, KS><<<grid, kThreads, 0, st>>>(p); break;
   }
 }
 
 }  // namespace dtree
 
 using namespace dtree;
+
+// The paired per-tile schedule: counters + one 32 x 32 fp32 partial per
+// (tile, half).
+static size_t dp_pair_workspace_bytes(int n) { return kCounterBytes + (size_t)(n / 32) * 2 * 32 * 32 * sizeof(float); }
 
 extern "C" size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int split_k) {
   if (rows_padded <= 0 || n <= 0 || k <= 0) return 0;
@@ -1089,6 +1140,8 @@ extern "C" size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int 
     // count it plans for.
     const size_t sk = sk_workspace_bytes(n, k, kSkMaxGrid);
     if (sk > need) need = sk;
+    const size_t pairs = dp_pair_workspace_bytes(n);
+    if (pairs > need) need = pairs;
   }
   return need;
 }
@@ -1103,9 +1156,9 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0, "gemm: k must be a positive multiple of 64");
   DTREE_REQUIRE(a->ldx >= a->k && a->ldx % 8 == 0, "gemm: ldx must be >= k and a multiple of 8");
   const int ntiles = a->n / tn, nkb = a->k / 64;
-  DTREE_REQUIRE(a->split_k >= -2, "gemm: split_k must be >= -2");
+  DTREE_REQUIRE(a->split_k >= -3, "gemm: split_k must be >= -3");
   DTREE_REQUIRE(a->split_k >= 0 || (a->w_layout != DTREE_W_ROWMAJOR && a->rows_padded == 32),
-                "gemm: split_k -1 / -2 need tiled weights and 32 rows");
+                "gemm: split_k -1 / -2 / -3 need tiled weights and 32 rows");
   const int S = a->split_k > 0 ? a->split_k : auto_split(ntiles, nkb);
   DTREE_REQUIRE(S <= nkb, "gemm: split_k larger than the number of 64-wide K blocks");
   DTREE_REQUIRE((size_t)ntiles * sizeof(int) <= kCounterBytes, "gemm: n too large for the tile counter region");
@@ -1193,10 +1246,25 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   // MI355X (K <= 4096 and N <= 12800, e.g. the fused QKV and o_proj at hidden
   // 2560): no cross-workgroup reduction tail, at the price of re-reading the
   // activations per tile and of fewer than 256 workgroups on narrow N.
+  // Of those, K = 4096 (o_proj, out_proj) runs two workgroups per tile: 11.8
+  // vs 15.8 us at N = 2560; at K = 2560 the halves are too short (QKV N =
+  // 6144: 16.7 vs 12.4 us).
   const bool dp_auto = a->split_k == 0 && a->k <= 4096 && a->n <= 12800;
+  const bool pairs_auto = dp_auto && a->k >= 4096 && a->n % 256 == 0;
+  if (tiled && !q4 && a->rows_padded == 32 && (a->split_k == -3 || pairs_auto)) {
+    // Two workgroups per tile, one per K half (see dp_gemm_kernel).
+    DTREE_REQUIRE(a->n % 256 == 0 && nkb >= 2, "gemm: split_k -3 needs n % 256 == 0 and k >= 128");
+    const size_t need_pairs = dp_pair_workspace_bytes(a->n);
+    DTREE_REQUIRE(a->workspace_bytes >= need_pairs, "gemm: workspace too small for the paired schedule");
+    p.part_bytes = (unsigned)(need_pairs - kCounterBytes);
+    if (p.x_lo) launch_dp<true, 2>(p, epi, stream);
+    else launch_dp<false, 2>(p, epi, stream);
+    DTREE_LAUNCH_CHECK("gemm launch");
+    return DTREE_OK;
+  }
   if (tiled && !q4 && a->rows_padded == 32 && (a->split_k == -1 || dp_auto)) {
-    if (p.x_lo) launch_dp<true>(p, epi, stream);
-    else launch_dp<false>(p, epi, stream);
+    if (p.x_lo) launch_dp<true, 1>(p, epi, stream);
+    else launch_dp<false, 1>(p, epi, stream);
     DTREE_LAUNCH_CHECK("gemm launch");
     return DTREE_OK;
   }
