@@ -56,6 +56,7 @@ struct AttnParams {
   float scale_log2;
   int write_cache;
   float* part; int* counters;
+  int sep_combine;  // partials are combined by attn_combine_kernel (long prefixes)
 };
 
 __device__ __forceinline__ int swap_bits23(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
@@ -727,6 +728,7 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
       st_coherent(part + 32 * D + c, M);
       st_coherent(part + 32 * D + 32 + c, tot);
     }
+    if (p.sep_combine) return;  // attn_combine_kernel (next launch) reads the partials
     wait_stores_done();
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -783,9 +785,126 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   }
 }
 
+// Combine of the workgroup partials for long prefixes, as a launch of its
+// own: with S splits the in-kernel last arriver reads S partial tiles of
+// 32 x D fp32 alone (544 KB at head_dim 256, P = 2048), which one CU's load
+// bandwidth turns into ~18 us. Here one workgroup per (head, query block,
+// 32-dim block) reads S x 4 KB: wave w takes splits w, w + 4, ... with a
+// running max, the four waves merge in LDS and wave 0 writes the block's
+// output (normalised, gated, bf16 pair). Splits and partial layout are the
+// main kernel's; with one split or a query block past the tree the main
+// kernel has written the output itself.
+template <int D, bool GATE>
+__global__ __launch_bounds__(64 * kWaves) void attn_combine_kernel(AttnParams p) {
+  constexpr int ND = D / 32;
+  constexpr int kB = 8;  // splits in flight per wave
+  const int NT = p.tree_chunks;
+  const int db = blockIdx.x % ND, hb = blockIdx.x / ND;  // hb = head * NT + query block
+  const int hq = hb / NT, rb = hb % NT;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  constexpr int CK = chunk_keys(D);
+  const int P = p.desc->past_length, L = p.desc->num_nodes;
+  const int nchunks = NT + (P + CK - 1) / CK;
+  if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;  // the main kernel's guards
+  const int nsplit = (nchunks + kWaves - 1) / kWaves;
+  if (nsplit <= 1 || 32 * rb >= L) return;
+  const size_t stride = (size_t)32 * D + 64;
+  const __amdgpu_buffer_rsrc_t prs =
+      buf_rsrc(p.part, (unsigned)((size_t)p.Hq * NT * p.splits * stride * sizeof(float)));
+  const unsigned pbase = (unsigned)((size_t)hb * p.splits * stride * sizeof(float));
+  float Ms = kNeg, tot = 0.f;
+  f32x4_t acc[4];
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) acc[gq] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = wave; s0 < nsplit; s0 += kWaves * kB) {
+    f32x4_t v[kB][4];
+    float mm[kB], ll[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const int sp = s0 + kWaves * b;
+      const unsigned so = sp < nsplit ? pbase + (unsigned)((size_t)sp * stride * sizeof(float)) : kOob;
+      const float mv = buf_ldf(prs, so + (32 * D + c) * 4);
+      ll[b] = buf_ldf(prs, so + (32 * D + 32 + c) * 4);
+      mm[b] = sp < nsplit ? mv : kNeg;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        v[b][gq] = __builtin_bit_cast(f32x4_t, buf_ld(prs, so + (unsigned)((db * 64 + lane) * 64 + 16 * gq)));
+    }
+    float gm = Ms;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) gm = fmaxf(gm, mm[b]);
+    const float rsc = fast_exp2(Ms - gm);
+    tot *= rsc;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) acc[gq] *= rsc;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const float w = fast_exp2(mm[b] - gm);  // 0 for splits past nsplit
+      tot += w * ll[b];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) acc[gq] += w * v[b][gq];
+    }
+    Ms = gm;
+  }
+  // Merge the four waves (in wave order) into wave 0.
+  __shared__ float ml[kWaves][2][64];
+  __shared__ f32x4_t xa[kWaves - 1][4][64];
+  ml[wave][0][lane] = Ms;
+  ml[wave][1][lane] = tot;
+  if (wave > 0) {
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) xa[wave - 1][gq][lane] = acc[gq];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float M = kNeg;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[w][0][lane]);
+  float T = 0.f;
+  f32x4_t o[4];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float f = fast_exp2(ml[w][0][lane] - M);
+    T += f * ml[w][1][lane];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4_t x = w == 0 ? acc[gq] : xa[w - 1][gq][lane];
+      o[gq] = w == 0 ? f * x : o[gq] + f * x;
+    }
+  }
+  // Output of query c, dims 32 db + 8 gq + 4 h .. +3 (MFMA accumulator layout).
+  const int orow = 32 * rb + c;
+  const float inv = (orow < L && T > 0.f) ? 1.0f / T : 0.f;
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) {
+    const int dim = 32 * db + 8 * gq + 4 * h;
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = orow < L ? o[gq][i] * inv : 0.f;
+    if (GATE && orow < L) {
+      const f32x4_t gt =
+          *reinterpret_cast<const f32x4_t*>(p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D + dim);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
+    }
+    float rl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
+    const u32x2_t hi = {pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
+    const u32x2_t lo = {pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
+    const int col = hq * D + dim;
+    const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
+    *reinterpret_cast<u32x2_t*>(p.out + oi) = hi;
+    if (p.out_lo) *reinterpret_cast<u32x2_t*>(p.out_lo + oi) = lo;
+  }
+}
+
 }  // namespace dtree
 
 using namespace dtree;
+
+constexpr size_t kSepCombineBytes = 128 * 1024;
 
 static int attn_max_chunks(int head_dim, int max_past, int nt) {
   const int ck = chunk_keys(head_dim);
@@ -852,6 +971,9 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   const int pairs = p.splits * p.Hkv;
   const int grid = ((pairs + 7) / 8) * 8 * G * nt;  // nt query blocks of ((pairs+7)/8)*8*G workgroups
   const bool one = nt == 1;
+  // Long prefixes combine in a launch of their own (attn_combine_kernel):
+  // when the last arriver alone would read more than 128 KB of partials.
+  p.sep_combine = (size_t)p.splits * 32 * D * sizeof(float) > kSepCombineBytes;
   if (D == 128) {
     if (one) tree_attn_kernel<128, 128, false, 1><<<grid, 64 * kWaves, 0, stream>>>(p);
     else tree_attn_kernel<128, 128, false, 4><<<grid, 64 * kWaves, 0, stream>>>(p);
@@ -860,5 +982,11 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
     else tree_attn_kernel<256, 64, true, 4><<<grid, 64 * kWaves, 0, stream>>>(p);
   }
   DTREE_LAUNCH_CHECK("attention launch");
+  if (p.sep_combine) {
+    const int cgrid = p.Hq * nt * (D / 32);
+    if (D == 128) attn_combine_kernel<128, false><<<cgrid, 64 * kWaves, 0, stream>>>(p);
+    else attn_combine_kernel<256, true><<<cgrid, 64 * kWaves, 0, stream>>>(p);
+    DTREE_LAUNCH_CHECK("attention combine launch");
+  }
   return DTREE_OK;
 }

@@ -410,6 +410,92 @@ def test_tree_attention_more_than_32_nodes(gpu_device, P, MP, L, shape):
     assert int(ws[: 32 * (MP // 32) * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
 
 
+@pytest.mark.parametrize("P,max_past", [(0, 64), (100, 128), (300, 2000), (1000, 4096), (4000, 4096)])
+def test_tree_attention_long_prefix_separate_combine(gpu_device, P, max_past):
+    """Grids sized for long prefixes combine the workgroup partials in a
+    launch of their own (more than 128 KB of partials per head); short
+    descriptors (one split) still write the output from the main kernel."""
+    parents = random_tree(25, seed=P + 3)
+    cache, out, ref, k, v, ws = _attention_case(gpu_device, P, parents, Hq=8, Hkv=2, seed=P + 1, max_past=max_past)
+    got = bf16_f32(out)
+    assert np.abs(got[:25] - ref).max() <= 2e-2 * np.abs(ref).max()
+    assert np.all(got[25:] == 0)
+    _, out2, *_ = _attention_case(gpu_device, P, parents, Hq=8, Hkv=2, seed=P + 1, max_past=max_past)
+    assert torch.equal(out, out2)
+
+
+def _gated_attention_case(dev, P, parents, max_past, Hq=8, Hkv=2, seed=0):
+    """Qwen3.5 gated attention: head_dim 256, per head [q | gate] in the QKV
+    row, q/k RMSNorm, RoPE on the first 64 dims (base 1e5), output times
+    sigmoid(gate) (qwen35_tree.py:503-540)."""
+    from oracle import qwen35 as o35
+    g = np.random.default_rng(seed)
+    D, RD, MP = 256, 64, 32
+    L = len(parents)
+    cache = PagedKVCache(1, Hkv, D, max_past + MP, device=dev,
+                         page_order=torch.from_numpy(g.permutation((max_past + MP + 63) // 64).astype(np.int32)))
+    kpre = (g.standard_normal((P, Hkv, D)) * 0.5).astype(np.float32)
+    vpre = (g.standard_normal((P, Hkv, D)) * 0.5).astype(np.float32)
+    if P:
+        cache.write_logical(0, torch.from_numpy(kpre), torch.from_numpy(vpre))
+    cache.offset = P
+    W = 2 * Hq * D + 2 * Hkv * D
+    qkv = np.zeros((MP, W), np.float32)
+    qkv[:L] = g.standard_normal((L, W)).astype(np.float32)
+    qn = (1 + 0.1 * g.standard_normal(D)).astype(np.float32)
+    kn = (1 + 0.1 * g.standard_normal(D)).astype(np.float32)
+    depth = [0] * L
+    for i in range(1, L):
+        depth[i] = depth[parents[i]] + 1
+    pos = [P + d for d in depth]
+    desc = device_desc([0] * L, pos, parents, P, dev)
+    cos = torch.zeros(MP, RD // 2, device=dev)
+    sin = torch.zeros(MP, RD // 2, device=dev)
+    N.check(N.lib().dtree_rope_table(desc.data_ptr(), MP, RD, 1e5, cos.data_ptr(), sin.data_ptr(), stream()))
+    qn_t = torch.from_numpy(qn).to(torch.bfloat16).to(dev)
+    kn_t = torch.from_numpy(kn).to(torch.bfloat16).to(dev)
+    out = torch.full((MP, Hq * D), 7.0, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(N.lib().dtree_attention_workspace_bytes(Hq, D, max_past, MP), dtype=torch.uint8, device=dev)
+    qkv_t = torch.from_numpy(qkv).to(dev)
+    a = N.AttnArgs()
+    a.qkv = qkv_t.data_ptr(); a.ld_qkv = W
+    a.q_norm = qn_t.data_ptr(); a.k_norm = kn_t.data_ptr(); a.eps = 1e-6
+    a.rope_cos = cos.data_ptr(); a.rope_sin = sin.data_ptr()
+    a.k_pages = cache.k_ptr(0); a.v_pages = cache.v_ptr(0); a.page_table = cache.page_table.data_ptr()
+    a.desc = desc.data_ptr(); a.out = out.data_ptr(); a.ld_out = Hq * D
+    a.num_heads = Hq; a.num_kv_heads = Hkv; a.head_dim = D; a.rows_padded = MP
+    a.scale = D ** -0.5; a.max_past_length = max_past; a.write_cache = 1
+    a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+    a.rope_dims = RD; a.gated = 1
+    N.check(N.lib().dtree_tree_attention(C.byref(a), stream()), "attention")
+    torch.cuda.synchronize()
+    qg = qkv[:L, : 2 * Hq * D].reshape(L, Hq, 2 * D)
+    q, gate = qg[..., :D], qg[..., D:].reshape(L, Hq * D)
+    k = qkv[:L, 2 * Hq * D:(2 * Hq + Hkv) * D].reshape(L, Hkv, D)
+    v = qkv[:L, (2 * Hq + Hkv) * D:].reshape(L, Hkv, D)
+    q = o35.partial_rope(oq.rms_norm(q, bf16_f32(qn_t), 1e-6), np.array(pos), RD, 1e5)
+    k = o35.partial_rope(oq.rms_norm(k, bf16_f32(kn_t), 1e-6), np.array(pos), RD, 1e5)
+    kp = oq.bf16_to_f32(oq.f32_to_bf16_bits(kpre))
+    vp = oq.bf16_to_f32(oq.f32_to_bf16_bits(vpre))
+    ref = oq.sdpa(q, np.concatenate([kp, k]), np.concatenate([vp, v]), tree_mask(parents, P), D ** -0.5)
+    ref = ref.reshape(L, Hq * D) / (1.0 + np.exp(-gate))
+    return out, ref
+
+
+@pytest.mark.parametrize("P,max_past", [(0, 64), (100, 128), (700, 2048), (2000, 2048)])
+def test_gated_attention_head_dim_256(gpu_device, P, max_past):
+    """The Qwen3.5 geometry directly against the oracle, with the in-kernel
+    combine (short grids) and the separate combine launch (max_past 2048:
+    17 splits of 32 KB per head)."""
+    parents = random_tree(25, seed=P + 7)
+    out, ref = _gated_attention_case(gpu_device, P, parents, max_past, seed=P + 2)
+    got = bf16_f32(out)
+    assert np.abs(got[:25] - ref).max() <= 2e-2 * np.abs(ref).max()
+    assert np.all(got[25:] == 0)
+    out2, _ = _gated_attention_case(gpu_device, P, parents, max_past, seed=P + 2)
+    assert torch.equal(out, out2)
+
+
 def test_tree_attention_gqa_small_and_deterministic(gpu_device):
     parents = random_tree(25, seed=5)
     cache, out, ref, *_ = _attention_case(gpu_device, 300, parents, Hq=8, Hkv=2, seed=4, max_past=2000)
