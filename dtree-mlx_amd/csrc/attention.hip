@@ -220,90 +220,151 @@ __device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, bool norm, 
   for (int j = 0; j < D / 16; ++j) split8(q[j], qf[j], ql[j]);
 }
 
-// ---- query rows staged once per workgroup (head_dim 128, full RoPE) --------
+// ---- query rows staged once per workgroup -----------------------------------
 // The four waves of a workgroup score the same 32 query rows of one head, so
 // the rows are loaded, normalised and rotated once: thread (row r = t / 8,
-// part j = t % 8) owns dims 8j .. 8j+7 and 64+8j .. 64+8j+7 (each RoPE pair
-// (d, d + 64) stays in one thread; the RMSNorm sum of squares is completed
-// over the row's 8 threads with DPP) and writes them to LDS, from which each
-// wave reads its MFMA fragments. Row stride kQsStride keeps those 32-byte
-// fragment reads apart in the LDS banks.
-constexpr int kQsStride = 128 + 4;  // floats
-struct QStage {
+// part j = t % 8) owns
+// * head_dim 128 (RoPE pairs (d, d + 64)): dims 8j .. 8j+7 and 64+8j .. +7;
+// * head_dim 256 (RoPE on dims 0..63, pairs (d, d + 32)): dims 4j .. 4j+3,
+//   32+4j .. +3 and the unrotated 64+24j .. 64+24j+23;
+// so each RoPE pair stays in one thread, and the RMSNorm sum of squares is
+// completed over the row's 8 threads with DPP. The rows go to LDS, from which
+// each wave reads its MFMA fragments. The row stride (D + 4 floats) keeps
+// those 32-byte fragment reads apart in the LDS banks.
+template <int D>
+__host__ __device__ constexpr int qs_stride() { return D + 4; }
+template <int D> struct QStage;
+template <> struct QStage<128> {
   f32x4_t x[4];
   u32x4_t nw[2];
   f32x4_t cs[2], sn[2];
 };
+template <> struct QStage<256> {
+  f32x4_t x[8];      // rotated pair halves [4j, +4), [32+4j, +4); then 64+24j .. +24
+  u32x2_t nwr[2];    // norm weights of the rotated dims
+  u32x4_t nwp[3];    // of the unrotated dims
+  f32x4_t cs, sn;    // RoPE entries 4j .. 4j+3
+};
 
-__device__ __forceinline__ void q_stage_issue(const AttnParams& p, int hq, int rb, QStage& q) {
+template <int D>
+__device__ __forceinline__ void q_stage_issue(const AttnParams& p, int hq, int rb, QStage<D>& q) {
   const int t = threadIdx.x, r = t >> 3, j = t & 7;
   const int row = 32 * rb + r;
-  const float* src = p.qkv + (size_t)row * p.ld_qkv + hq * p.q_stride + 8 * j;
-  q.x[0] = *reinterpret_cast<const f32x4_t*>(src);
-  q.x[1] = *reinterpret_cast<const f32x4_t*>(src + 4);
-  q.x[2] = *reinterpret_cast<const f32x4_t*>(src + 64);
-  q.x[3] = *reinterpret_cast<const f32x4_t*>(src + 68);
+  const float* src = p.qkv + (size_t)row * p.ld_qkv + hq * p.q_stride;
   // without q_norm the weight loads read the row itself (ignored below)
-  const uint16_t* nwp = p.q_norm ? p.q_norm + 8 * j : reinterpret_cast<const uint16_t*>(src);
-  q.nw[0] = ld_u32x4(nwp);
-  q.nw[1] = ld_u32x4(nwp + 64);
-  const float* cr = p.rope_cos + row * 64 + 8 * j;
-  const float* sr = p.rope_sin + row * 64 + 8 * j;
-  q.cs[0] = *reinterpret_cast<const f32x4_t*>(cr);
-  q.cs[1] = *reinterpret_cast<const f32x4_t*>(cr + 4);
-  q.sn[0] = *reinterpret_cast<const f32x4_t*>(sr);
-  q.sn[1] = *reinterpret_cast<const f32x4_t*>(sr + 4);
+  const uint16_t* nwb = p.q_norm ? p.q_norm : reinterpret_cast<const uint16_t*>(src);
+  if constexpr (D == 128) {
+    q.x[0] = *reinterpret_cast<const f32x4_t*>(src + 8 * j);
+    q.x[1] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 4);
+    q.x[2] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 64);
+    q.x[3] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 68);
+    q.nw[0] = ld_u32x4(nwb + 8 * j);
+    q.nw[1] = ld_u32x4(nwb + 8 * j + 64);
+    const float* cr = p.rope_cos + row * 64 + 8 * j;
+    const float* sr = p.rope_sin + row * 64 + 8 * j;
+    q.cs[0] = *reinterpret_cast<const f32x4_t*>(cr);
+    q.cs[1] = *reinterpret_cast<const f32x4_t*>(cr + 4);
+    q.sn[0] = *reinterpret_cast<const f32x4_t*>(sr);
+    q.sn[1] = *reinterpret_cast<const f32x4_t*>(sr + 4);
+  } else {
+    q.x[0] = *reinterpret_cast<const f32x4_t*>(src + 4 * j);
+    q.x[1] = *reinterpret_cast<const f32x4_t*>(src + 32 + 4 * j);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) q.x[2 + i] = *reinterpret_cast<const f32x4_t*>(src + 64 + 24 * j + 4 * i);
+    q.nwr[0] = *reinterpret_cast<const u32x2_t*>(nwb + 4 * j);
+    q.nwr[1] = *reinterpret_cast<const u32x2_t*>(nwb + 32 + 4 * j);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) q.nwp[i] = ld_u32x4(nwb + 64 + 24 * j + 8 * i);
+    q.cs = *reinterpret_cast<const f32x4_t*>(p.rope_cos + row * 32 + 4 * j);
+    q.sn = *reinterpret_cast<const f32x4_t*>(p.rope_sin + row * 32 + 4 * j);
+  }
 }
 
-__device__ __forceinline__ void q_stage_finish(const QStage& q, bool norm, float eps, float* qs) {
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+template <int D>
+__device__ __forceinline__ void q_stage_finish(const QStage<D>& q, bool norm, float eps, float* qs) {
   const int t = threadIdx.x, r = t >> 3, j = t & 7;
-  float v[16];
+  constexpr int NV = D / 8;  // values per thread
+  float v[NV];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[i] = q.x[0][i];
-    v[4 + i] = q.x[1][i];
-    v[8 + i] = q.x[2][i];
-    v[12 + i] = q.x[3][i];
-  }
+  for (int k = 0; k < NV / 4; ++k)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[4 * k + i] = q.x[k][i];
   if (norm) {
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) ss += v[i] * v[i];
+    for (int i = 0; i < NV; ++i) ss += v[i] * v[i];
     ss += dpp<0xB1>(ss);   // lane ^ 1
     ss += dpp<0x4E>(ss);   // lane ^ 2
     ss += dpp<0x141>(ss);  // the other quad of the row's 8 lanes
-    const float rs = rsqrtf(ss * (1.0f / 128) + eps);
+    const float rs = rsqrtf(ss * (1.0f / D) + eps);
+    if constexpr (D == 128) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t w = q.nw[i >> 3][(i & 7) >> 1];
-      v[i] *= rs * __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w = q.nw[i >> 3][(i & 7) >> 1];
+        v[i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t w = q.nwr[i >> 2][(i & 3) >> 1];
+        v[i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
+      }
+#pragma unroll
+      for (int i = 0; i < 24; ++i) {
+        const uint32_t w = q.nwp[i >> 3][(i & 7) >> 1];
+        v[8 + i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
+      }
     }
   }
+  constexpr int NR = D == 128 ? 8 : 4;  // rotated pairs per thread
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float cs = q.cs[i >> 2][i & 3], sn = q.sn[i >> 2][i & 3];
-    const float x1 = v[i], x2 = v[8 + i];
+  for (int i = 0; i < NR; ++i) {
+    float cs, sn;
+    if constexpr (D == 128) {
+      cs = q.cs[i >> 2][i & 3];
+      sn = q.sn[i >> 2][i & 3];
+    } else {
+      cs = q.cs[i];
+      sn = q.sn[i];
+    }
+    const float x1 = v[i], x2 = v[NR + i];
     v[i] = x1 * cs - x2 * sn;
-    v[8 + i] = x1 * sn + x2 * cs;
+    v[NR + i] = x1 * sn + x2 * cs;
   }
-  float* dst = qs + r * kQsStride + 8 * j;
-  *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{v[0], v[1], v[2], v[3]};
-  *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
-  *reinterpret_cast<f32x4_t*>(dst + 64) = f32x4_t{v[8], v[9], v[10], v[11]};
-  *reinterpret_cast<f32x4_t*>(dst + 68) = f32x4_t{v[12], v[13], v[14], v[15]};
+  float* dst = qs + r * qs_stride<D>();
+  if constexpr (D == 128) {
+    *reinterpret_cast<f32x4_t*>(dst + 8 * j) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 64) = f32x4_t{v[8], v[9], v[10], v[11]};
+    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 68) = f32x4_t{v[12], v[13], v[14], v[15]};
+  } else {
+    *reinterpret_cast<f32x4_t*>(dst + 4 * j) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(dst + 32 + 4 * j) = f32x4_t{v[4], v[5], v[6], v[7]};
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+      *reinterpret_cast<f32x4_t*>(dst + 64 + 24 * j + 4 * i) =
+          f32x4_t{v[8 + 4 * i], v[9 + 4 * i], v[10 + 4 * i], v[11 + 4 * i]};
+  }
 }
 
-// Lane (c, h)'s q fragments (dims 16j + 8h .. +7 of query row c) from the
+// Lane (c, h)'s q fragment j (dims 16j + 8h .. +7 of query row c) from the
 // staged rows, split hi / lo.
-__device__ __forceinline__ void q_frag_lds(const float* qs, int c, int h, u32x4_t (&qf)[8], u32x4_t (&ql)[8]) {
+template <int D>
+__device__ __forceinline__ void q_frag_one(const float* qs, int c, int h, int j, u32x4_t& qf, u32x4_t& ql) {
+  const float* src = qs + c * qs_stride<D>() + 16 * j + 8 * h;
+  const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
+  const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + 4);
+  const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  split8(v, qf, ql);
+}
+template <int D>
+__device__ __forceinline__ void q_frag_lds(const float* qs, int c, int h, u32x4_t (&qf)[D / 16],
+                                           u32x4_t (&ql)[D / 16]) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float* src = qs + c * kQsStride + 16 * j + 8 * h;
-    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
-    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + 4);
-    const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-    split8(v, qf[j], ql[j]);
-  }
+  for (int j = 0; j < D / 16; ++j) q_frag_one<D>(qs, c, h, j, qf[j], ql[j]);
 }
 
 // Tree chunk tc: k (norm + RoPE) and v of nodes 32*tc .. 32*tc+31 come from
@@ -313,7 +374,7 @@ __device__ __forceinline__ void q_frag_lds(const float* qs, int c, int h, u32x4_
 // cache rows P + node (once: query block 0, first head of the group).
 // q, k and v are finished one after the other, so at most one raw head row is
 // live in registers (head_dim 256 rows are 128 floats per lane pair).
-template <int D, int R>
+template <int D, int R, bool QS>
 __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs, int hq, int g,
                                            int G, int P, int L, int tc, int qrow, bool write_rows, int c, int h,
                                            uint16_t* ks, uint16_t* vt, float& m_run, float& l_run,
@@ -327,13 +388,16 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
   const float* cosr = p.rope_cos + node * half_r;
   const float* sinr = p.rope_sin + node * half_r;
   const uint32_t anc = p.desc->ancestors[qrow][tc];
-  u32x4_t qf[NJ], ql[NJ];
-  if constexpr (D > 128) {
+  // Staged head_dim-256 rows are read one fragment at a time in the QK^T
+  // loop (16 fragments would hold 128 registers).
+  constexpr bool PERJ = QS && D > 128;
+  u32x4_t qf[PERJ ? 1 : NJ], ql[PERJ ? 1 : NJ];
+  if constexpr (!QS) {
     row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * half_r,
                           p.rope_sin + qrow * half_r, h);
     q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
-  } else {
-    q_frag_lds(qs, c, h, qf, ql);
+  } else if constexpr (!PERJ) {
+    q_frag_lds<D>(qs, c, h, qf, ql);
   }
   u32x4_t kf8[NJ], vf8[NJ];
   {
@@ -373,8 +437,15 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[kr_row * KS + 16 * j + 8 * h]);
-    s[0] = mfma32(a, qf[j], s[0]);
-    s[0] = mfma32(a, ql[j], s[0]);
+    if constexpr (PERJ) {
+      u32x4_t f, l;
+      q_frag_one<D>(qs, c, h, j, f, l);
+      s[0] = mfma32(a, f, s[0]);
+      s[0] = mfma32(a, l, s[0]);
+    } else {
+      s[0] = mfma32(a, qf[j], s[0]);
+      s[0] = mfma32(a, ql[j], s[0]);
+    }
   }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -440,7 +511,7 @@ __device__ __forceinline__ void prefix_issue(const AttnParams& p, ChunkKV<D>& kv
   }
 }
 
-template <int D, int R>
+template <int D, int R, bool QS>
 __device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs,
                                              const ChunkKV<D>& kv, int P, int pc, int c, int h, float& m_run,
                                              float& l_run, f32x16_t (&o)[D / 32]) {
@@ -448,9 +519,10 @@ __device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>&
   constexpr int CK = chunk_keys(D), NB = CK / 32;
   const int k_begin = pc * CK;  // prefix chunk pc: keys pc*CK ..
   const int k_end = min(k_begin + CK, P);
-  u32x4_t qf[NJ], ql[NJ];
-  if constexpr (D > 128) q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
-  else q_frag_lds(qs, c, h, qf, ql);
+  constexpr bool PERJ = QS && D > 128;  // staged head_dim 256: one fragment at a time
+  u32x4_t qf[PERJ ? 1 : NJ], ql[PERJ ? 1 : NJ];
+  if constexpr (!QS) q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  else if constexpr (!PERJ) q_frag_lds<D>(qs, c, h, qf, ql);
 
   f32x16_t s[NB];
 #pragma unroll
@@ -458,12 +530,15 @@ __device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>&
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j)
+  for (int j = 0; j < NJ; ++j) {
+    u32x4_t f, l;
+    if constexpr (PERJ) q_frag_one<D>(qs, c, h, j, f, l);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      s[b] = mfma32(kv.kf[b][j], qf[j], s[b]);
-      s[b] = mfma32(kv.kf[b][j], ql[j], s[b]);
+      s[b] = mfma32(kv.kf[b][j], PERJ ? f : qf[PERJ ? 0 : j], s[b]);
+      s[b] = mfma32(kv.kf[b][j], PERJ ? l : ql[PERJ ? 0 : j], s[b]);
     }
+  }
   const bool ragged = k_end - k_begin < CK;
 #pragma unroll
   for (int b = 0; b < NB; ++b)
@@ -554,7 +629,10 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   constexpr int KS = D + 8;   // padded LDS row of tree K
   constexpr int VS = 32 + 8;  // padded LDS row of tree V^T
   constexpr int kStage = (32 * KS + D * VS) * 2;   // one tree chunk's K / V^T staging
-  constexpr int kQs = D <= 128 ? 32 * kQsStride * 4 : 0;  // staged query rows
+  // Query rows are staged in LDS except for head_dim 256 with four tree
+  // chunks (their K/V staging leaves no room).
+  constexpr bool QS = D <= 128 || TB == 1;
+  constexpr int kQs = QS ? 32 * qs_stride<D>() * 4 : 0;  // staged query rows
   constexpr int kMl = kWaves * 64 * 4;               // merge: per wave, m and l of 32 queries
   constexpr int kMerge = kMl + ND * kWaves * 4 * 64 * 16;  // + [block][wave][4][lane] f32x4
   constexpr int kChunkLds = TB * kStage + kQs;
@@ -588,13 +666,13 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   // norm weights, RoPE; 10 loads per thread) and the page of this wave's
   // prefix chunk. The chunk's K/V follow the descriptor check: issued before
   // it, they delay the descriptor's own (scalar) load by microseconds.
-  // (head_dim 256 loads its q row per wave inside the chunk: live across the
-  // descriptor read it would spill.)
+  // (head_dim 256 with four tree chunks loads its q row per wave inside the
+  // chunk: there is no LDS left to stage it.)
   const bool prefix_wave = chunk >= NT && chunk < p.max_chunks;
   const int page = prefix_wave ? p.page_table[(chunk - NT) * CK / DTREE_PAGE] : 0;
   HeadRow<D, R> qr;
-  QStage qst;
-  if constexpr (D <= 128) q_stage_issue(p, hq, rb, qst);
+  QStage<D> qst;
+  if constexpr (QS) q_stage_issue<D>(p, hq, rb, qst);
 
   if (pair >= p.splits * p.Hkv) return;
   const int P = p.desc->past_length, L = p.desc->num_nodes;
@@ -621,8 +699,8 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   }
 
   float* qs = reinterpret_cast<float*>(lds + TB * kStage);
-  if constexpr (D <= 128) {
-    q_stage_finish(qst, p.q_norm != nullptr, p.eps, qs);
+  if constexpr (QS) {
+    q_stage_finish<D>(qst, p.q_norm != nullptr, p.eps, qs);
     __syncthreads();
   }
 
@@ -637,15 +715,15 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     // Tree chunks are waves 0 .. NT-1 of split 0, each with its own staging.
     if (32 * chunk < L) {
       uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)chunk * kStage);
-      tree_chunk<D, R>(p, qr, qs, hq, g, G, P, L, chunk, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+      tree_chunk<D, R, QS>(p, qr, qs, hq, g, G, P, L, chunk, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
     }
   } else if (chunk < nchunks) {
-    if constexpr (D > 128)
+    if constexpr (!QS)
       row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm,
                             p.rope_cos + qrow * (R / 2), p.rope_sin + qrow * (R / 2), h);
     ChunkKV<D> kv;
     prefix_issue<D>(p, kv, page, g, chunk - NT, c, h);
-    prefix_chunk<D, R>(p, qr, qs, kv, P, chunk - NT, c, h, m_run, l_run, o);
+    prefix_chunk<D, R, QS>(p, qr, qs, kv, P, chunk - NT, c, h, m_run, l_run, o);
   }
 
   // ---- merge the four waves ----
