@@ -400,19 +400,31 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
     q_frag_lds<D>(qs, c, h, qf, ql);
   }
   u32x4_t kf8[NJ], vf8[NJ];
-  {
-    HeadRow<D, R> kr;
+  if constexpr (D <= 128) {
+    // Both raw rows in flight together: one round trip instead of two.
+    HeadRow<D, R> kr, vr;
     row_issue<D, R, true>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
-    float kv[NJ][8];
+    row_issue<D, R, false>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
+    float kv[NJ][8], vv[NJ][8];
     row_finish<D, R>(kr, p.k_norm != nullptr, true, p.eps, kv);
     pack_frag<D>(kv, kf8);
-  }
-  {
-    HeadRow<D, R> vr;
-    row_issue<D, R, false>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
-    float vv[NJ][8];
     row_finish<D, R>(vr, false, false, 0.f, vv);
     pack_frag<D>(vv, vf8);
+  } else {
+    {
+      HeadRow<D, R> kr;
+      row_issue<D, R, true>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
+      float kv[NJ][8];
+      row_finish<D, R>(kr, p.k_norm != nullptr, true, p.eps, kv);
+      pack_frag<D>(kv, kf8);
+    }
+    {
+      HeadRow<D, R> vr;
+      row_issue<D, R, false>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
+      float vv[NJ][8];
+      row_finish<D, R>(vr, false, false, 0.f, vv);
+      pack_frag<D>(vv, vf8);
+    }
   }
   if (node >= L) {
 #pragma unroll
