@@ -9,6 +9,8 @@ import ctypes as C
 import os
 from pathlib import Path
 
+import numpy as np
+
 LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
 
 MAX_NODES = 128
@@ -43,6 +45,16 @@ class StepDesc(C.Structure):
         ("accepted", C.c_int32 * MAX_NODES),
         ("posterior", C.c_int32 * MAX_NODES),
     ]
+
+
+# The same record as a numpy dtype (the host fills a pinned copy in place).
+STEP_DESC_DTYPE = np.dtype([
+    ("past_length", "<i4"), ("num_nodes", "<i4"), ("n_accepted", "<i4"), ("bonus_token", "<i4"),
+    ("tokens", "<i4", (MAX_NODES,)), ("positions", "<i4", (MAX_NODES,)), ("parents", "<i4", (MAX_NODES,)),
+    ("ancestors", "<u4", (MAX_NODES, MASK_WORDS)), ("accepted", "<i4", (MAX_NODES,)),
+    ("posterior", "<i4", (MAX_NODES,)),
+])
+assert STEP_DESC_DTYPE.itemsize == C.sizeof(StepDesc)
 
 
 class GemmArgs(C.Structure):

@@ -32,18 +32,19 @@ def ancestor_bitsets(parents) -> np.ndarray:
     L = len(parents)
     if L > N.MAX_NODES:
         raise ValueError(f"at most {N.MAX_NODES} tree nodes are supported, got {L}")
-    out = np.zeros((L, N.MASK_WORDS), dtype=np.uint32)
+    masks = [0] * L  # one Python integer per node: cheaper than L numpy row copies
     for i in range(L):
         p = int(parents[i])
         if i == 0:
             if p != -1:
                 raise ValueError(f"tree root parent must be -1, got {p}")
+            masks[0] = 1
         elif p < 0 or p >= i:
             raise ValueError(f"tree parent index must precede child, got parents[{i}]={p}")
         else:
-            out[i] = out[p]
-        out[i, i // 32] |= np.uint32(1 << (i % 32))
-    return out
+            masks[i] = masks[p] | (1 << i)
+    raw = b"".join(m.to_bytes(4 * N.MASK_WORDS, "little") for m in masks)
+    return np.frombuffer(raw, dtype="<u4").reshape(L, N.MASK_WORDS).copy()
 
 
 def mask_to_parents(tree_mask: np.ndarray) -> list[int]:
@@ -114,10 +115,14 @@ class TreeEngineBase:
         self.gemm_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
         self.n_cand = self.lib.dtree_lmhead_candidate_blocks(V, MP)
         self.cand = torch.zeros(self.lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=dev)
-        self.desc_host = N.StepDesc()
         self.desc_pinned = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8).pin_memory()
         self.desc = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8, device=dev)
         self.desc_aux_pinned = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8).pin_memory()
+        # record views of the pinned descriptors: the host fills them in place
+        self._desc_rec = self.desc_pinned.numpy().view(N.STEP_DESC_DTYPE)[0]
+        self._desc_aux_rec = self.desc_aux_pinned.numpy().view(N.STEP_DESC_DTYPE)[0]
+        for rec in (self._desc_rec, self._desc_aux_rec):
+            rec["parents"][:] = -1
         self.desc_aux = torch.zeros(C.sizeof(N.StepDesc), dtype=torch.uint8, device=dev)
         self._desc_event = torch.cuda.Event()
         self._aux_event = torch.cuda.Event()
@@ -161,33 +166,27 @@ class TreeEngineBase:
         if past_length < 0 or past_length > self.max_past:
             raise ValueError(f"past_length {past_length} outside [0, {self.max_past}]")
         anc = ancestor_bitsets(parents) if ancestors is None else np.asarray(ancestors, dtype=np.uint32)
-        d = self.desc_host
-        d.past_length = int(past_length)
-        d.num_nodes = L
-        d.n_accepted = 0 if accepted is None else len(accepted)
-        d.bonus_token = -1
-        if accepted is not None:
-            for i, a in enumerate(accepted):
-                d.accepted[i] = int(a)
-        for i in range(L):
-            tok = int(tokens[i])
-            if not 0 <= tok < self.cfg.vocab_size:
-                raise ValueError(f"token id {tok} outside the vocabulary")
-            d.tokens[i] = tok
-            d.positions[i] = int(positions[i])
-            d.parents[i] = int(parents[i])
-            for w in range(N.MASK_WORDS):
-                d.ancestors[i][w] = int(anc[i, w])
-        for i in range(L, N.MAX_NODES):
-            d.tokens[i] = 0
-            d.positions[i] = 0
-            d.parents[i] = -1
-            for w in range(N.MASK_WORDS):
-                d.ancestors[i][w] = 0
-        pinned, dst, ev = ((self.desc_aux_pinned, self.desc_aux, self._aux_event) if aux
-                           else (self.desc_pinned, self.desc, self._desc_event))
+        toks = np.asarray(tokens, dtype=np.int64).reshape(L)
+        bad = np.nonzero((toks < 0) | (toks >= self.cfg.vocab_size))[0]
+        if bad.size:
+            raise ValueError(f"token id {int(toks[bad[0]])} outside the vocabulary")
+        pinned, dst, ev, rec = ((self.desc_aux_pinned, self.desc_aux, self._aux_event, self._desc_aux_rec) if aux
+                                else (self.desc_pinned, self.desc, self._desc_event, self._desc_rec))
         ev.synchronize()  # the previous upload from this pinned buffer has finished
-        C.memmove(pinned.data_ptr(), C.addressof(d), C.sizeof(d))
+        rec["past_length"] = int(past_length)
+        rec["num_nodes"] = L
+        rec["n_accepted"] = 0 if accepted is None else len(accepted)
+        rec["bonus_token"] = -1
+        if accepted is not None and len(accepted):
+            rec["accepted"][: len(accepted)] = np.asarray(accepted, dtype=np.int64)
+        rec["tokens"][:L] = toks
+        rec["tokens"][L:] = 0
+        rec["positions"][:L] = np.asarray(positions, dtype=np.int64)
+        rec["positions"][L:] = 0
+        rec["parents"][:L] = np.asarray(parents, dtype=np.int64)
+        rec["parents"][L:] = -1
+        rec["ancestors"][:L] = anc
+        rec["ancestors"][L:] = 0
         s = torch.cuda.current_stream() if stream is None else stream
         with torch.cuda.stream(s):
             dst.copy_(pinned, non_blocking=True)
