@@ -27,6 +27,32 @@ from .config import Qwen3Config
 from .weights import W_TILED, Q4Linear, Qwen3Weights, tile_weight
 
 
+_HIP = None
+
+
+def _hip():
+    """The HIP runtime (already loaded by torch) for the per-step descriptor and
+    result copies: one call each instead of a tensor copy through the
+    dispatcher, on the step's critical path between two verify steps."""
+    global _HIP
+    if _HIP is None:
+        h = C.CDLL("libamdhip64.so")
+        h.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        h.hipMemcpyAsync.restype = C.c_int
+        h.hipStreamSynchronize.argtypes = [C.c_void_p]
+        h.hipStreamSynchronize.restype = C.c_int
+        _HIP = h
+    return _HIP
+
+
+_H2D, _D2H = 1, 2  # hipMemcpyHostToDevice, hipMemcpyDeviceToHost
+
+
+def _hip_check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what}: HIP error {rc}")
+
+
 def ancestor_bitsets(parents) -> np.ndarray:
     """[L, MASK_WORDS] uint32 ancestor-or-self bitsets (parents[i] < i, root -1)."""
     L = len(parents)
@@ -131,6 +157,7 @@ class TreeEngineBase:
         self.lm_in = torch.zeros(self.MP, H, dtype=bf16, device=dev)
         self.result = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32, device=dev)
         self.result_host = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32).pin_memory()
+        self._result_np = self.result_host.numpy()
         self._graphs: dict = {}
 
     def _alloc_layer_buffers(self) -> None:
@@ -188,9 +215,9 @@ class TreeEngineBase:
         rec["ancestors"][:L] = anc
         rec["ancestors"][L:] = 0
         s = torch.cuda.current_stream() if stream is None else stream
-        with torch.cuda.stream(s):
-            dst.copy_(pinned, non_blocking=True)
-            ev.record(s)
+        _hip_check(_hip().hipMemcpyAsync(dst.data_ptr(), pinned.data_ptr(), pinned.numel(), _H2D, s.cuda_stream),
+                   "step descriptor upload")
+        ev.record(s)
 
     # ---- launches ----------------------------------------------------------------
     def gemm_args(self, name, x, ldx, w, epi, *, ss_in=None, out_f32=None, out_bf16=None, next_norm=None,
@@ -285,13 +312,14 @@ class TreeEngineBase:
 
     def read_result(self, stream=None) -> StepResult:
         s = torch.cuda.current_stream() if stream is None else stream
-        with torch.cuda.stream(s):
-            self.result_host.copy_(self.result, non_blocking=True)
-        s.synchronize()
-        r = self.result_host.numpy()
+        h = _hip()
+        _hip_check(h.hipMemcpyAsync(self.result_host.data_ptr(), self.result.data_ptr(),
+                                    self.result_host.numel() * 4, _D2H, s.cuda_stream), "walk result copy")
+        _hip_check(h.hipStreamSynchronize(s.cuda_stream), "walk result wait")
+        r = self._result_np
         n, bonus, L = int(r[0]), int(r[1]), int(r[2])
-        return StepResult(accepted=[int(v) for v in r[3:3 + n]], bonus_token=bonus,
-                          posterior=[int(v) for v in r[3 + N.MAX_NODES:3 + N.MAX_NODES + L]])
+        return StepResult(accepted=r[3:3 + n].tolist(), bonus_token=bonus,
+                          posterior=r[3 + N.MAX_NODES:3 + N.MAX_NODES + L].tolist())
 
     def verify(self, cache: PagedKVCache, tokens, positions, parents, use_graph: bool = True,
                commit: bool = True) -> StepResult:
