@@ -700,6 +700,7 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   // Workgroup whose range holds unit u (T * G < 2^31, host-checked).
   auto owner = [&](int u) { return (int)(((unsigned)(u + 1) * (unsigned)G + (unsigned)(T - 1)) / (unsigned)T) - 1; };
   bool any_shared = false;
+  int sole = 0;  // bit j: this workgroup owns local block j alone
   // The residual rows of the first two blocks go out now (a workgroup spans
   // at most two blocks at the usual shapes): their round trip overlaps the
   // publish and the arrival below.
@@ -725,6 +726,7 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
       f32x4_t* dst = reinterpret_cast<f32x4_t*>(acc_lds + (j * kWaves) * TE + 8 * t);
       dst[0] = s0;
       dst[1] = s1;
+      sole |= 1 << j;
     } else {
       any_shared = true;
       const int off = ((g + b) * TE + 8 * t) * 4;
@@ -732,14 +734,38 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, s1), prs, off + 16, 0, kSc1);
     }
   }
+  // Epilogue of local block j (its tile summed in LDS): residual rows from the
+  // early loads for the first two blocks (selected by value, so the arrays
+  // stay in registers).
+#define DTREE_SK_EPILOGUE(j)                                                                \
+  do {                                                                                      \
+    float xj[IT + 1];                                                                       \
+    if constexpr (EPI == DTREE_EPI_RESIDUAL) {                                              \
+      if ((j) >= 2) {                                                                       \
+        residual_issue<32, TN>(p, b_first + (j), xj);                                       \
+      } else {                                                                              \
+        _Pragma("unroll") for (int i = 0; i <= IT; ++i) xj[i] = (j) == 0 ? xo0[i] : xo1[i]; \
+      }                                                                                     \
+    }                                                                                       \
+    tile_epilogue<32, TN, EPI>(p, acc_lds + ((j) * kWaves) * TE, rs, b_first + (j),         \
+                               EPI == DTREE_EPI_RESIDUAL ? xj : nullptr);                   \
+  } while (0)
+  // Blocks owned alone wait for nobody: their epilogues run while the shared
+  // blocks' partial stores are being acknowledged.
+  if (sole) {
+    __syncthreads();
+    for (int j = 0; j < nloc; ++j)
+      if ((sole >> j) & 1) DTREE_SK_EPILOGUE(j);
+  }
   if (any_shared) wait_stores_done();
   __syncthreads();
   if (t < nloc) {
     const int b = b_first + t;
     const int gf = owner(b * nkb), gl = owner((b + 1) * nkb - 1);
-    // last_flag: 0 not last; 1 last, partials read past L2 (sc1); 2 last,
-    // every contributor ran on this XCD, partials read from its L2 (sc0).
-    int last = 2;
+    // last_flag: 0 not last (or owned alone, finished above); 1 last, partials
+    // read past L2 (sc1); 2 last, every contributor ran on this XCD, partials
+    // read from its L2 (sc0).
+    int last = 0;
     if (gf != gl) {
       // Arrival count in the low half, workgroups off their XCD in the high.
       const int old = arrive_add(&p.counters[b], native ? 1 : 1 + kForeign);
@@ -789,18 +815,10 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
     }
     if (jn < nloc) issue_partials(jn, __builtin_amdgcn_readfirstlane(first_q[jn]));
     __syncthreads();
-    float xj[IT + 1];
-    if constexpr (EPI == DTREE_EPI_RESIDUAL) {
-      if (j >= 2) {
-        residual_issue<32, TN>(p, b_first + j, xj);
-      } else {
-#pragma unroll
-        for (int i = 0; i <= IT; ++i) xj[i] = j == 0 ? xo0[i] : xo1[i];
-      }
-    }
-    tile_epilogue<32, TN, EPI>(p, red, rs, b_first + j, EPI == DTREE_EPI_RESIDUAL ? xj : nullptr);
+    DTREE_SK_EPILOGUE(j);
     j = jn;
   }
+#undef DTREE_SK_EPILOGUE
 }
 
 // ---- LM head: persistent over vocab tiles, per-row running argmax --------
