@@ -104,40 +104,43 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
 // butterflies, first index on ties), then walk the tree from the root while
 // the target's argmax at the current node is the token of one of its
 // children (dtree_runtime.py:195-208).
-__global__ __launch_bounds__(256) void walk_kernel(DtreeStepDesc* desc, const int2* cand, int nblocks, int MP,
+constexpr int kWalkThreads = 1024;  // 16 waves, 16 candidate loads each in flight
+__global__ __launch_bounds__(kWalkThreads) void walk_kernel(DtreeStepDesc* desc, const int2* cand, int nblocks, int MP,
                                                    int* result) {
   __shared__ int post[DTREE_MAX_NODES];
   __shared__ int par_s[DTREE_MAX_NODES], tok_s[DTREE_MAX_NODES];
   const int L = min(max(desc->num_nodes, 1), min(MP, DTREE_MAX_NODES));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // The walk reads parents and tokens from LDS (one load per node here).
-  for (int m = threadIdx.x; m < L; m += 256) {
+  for (int m = threadIdx.x; m < L; m += kWalkThreads) {
     par_s[m] = desc->parents[m];
     tok_s[m] = desc->tokens[m];
   }
   // Candidates of one 32-row block are [blocks][32] pairs, 256 bytes per
   // workgroup. Thread t = 16 s + j reads the 16 bytes of rows 2j, 2j + 1 of
-  // workgroups s, s + 16, ..., so each wave load covers 1 KB contiguous; the
-  // four lanes of a wave that share j, then the four waves, are merged
-  // ((max, first index) is a total order, so the pairing does not matter).
-  __shared__ float red_v[4][32];
-  __shared__ int red_i[4][32];
-  constexpr int kBatch = 32;  // loads in flight per thread
+  // workgroups s, s + S, s + 2S, ... (S = threads / 16), so each wave load
+  // covers 1 KB contiguous; the four lanes of a wave that share j, then the
+  // waves, are merged ((max, first index) is a total order, so the pairing
+  // does not matter).
+  constexpr int kW = kWalkThreads / 64;
+  __shared__ float red_v[kW][32];
+  __shared__ int red_i[kW][32];
+  constexpr int kBatch = 16384 / kWalkThreads;  // loads in flight per thread (one batch covers 1024 workgroups)
   const int j = threadIdx.x & 15, s0 = threadIdx.x >> 4;
   for (int r0 = 0; r0 < L; r0 += 32) {
     const __amdgpu_buffer_rsrc_t crs = buf_rsrc(cand + cand_index(0, r0, nblocks), (unsigned)nblocks * 256u);
     float v0 = -__builtin_huge_valf(), v1 = v0;
     int i0 = 0x7fffffff, i1 = i0;
-    for (int b0 = s0; b0 < nblocks; b0 += 16 * kBatch) {
+    for (int b0 = s0; b0 < nblocks; b0 += (kWalkThreads / 16) * kBatch) {
       u32x4_t w[kBatch];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
-        const int b = b0 + 16 * k;
+        const int b = b0 + (kWalkThreads / 16) * k;
         w[k] = buf_ld(crs, b < nblocks ? (unsigned)(b * 256 + j * 16) : kOob);
       }
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
-        if (b0 + 16 * k < nblocks) {
+        if (b0 + (kWalkThreads / 16) * k < nblocks) {
           argmax_merge(v0, i0, __uint_as_float(w[k][0]), (int)w[k][1]);
           argmax_merge(v1, i1, __uint_as_float(w[k][2]), (int)w[k][3]);
         }
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(256) void walk_kernel(DtreeStepDesc* desc, const in
       float bv = red_v[0][m];
       int bi = red_i[0][m];
 #pragma unroll
-      for (int w2 = 1; w2 < 4; ++w2) argmax_merge(bv, bi, red_v[w2][m], red_i[w2][m]);
+      for (int w2 = 1; w2 < kW; ++w2) argmax_merge(bv, bi, red_v[w2][m], red_i[w2][m]);
       post[r0 + m] = bi;
     }
     __syncthreads();
@@ -199,11 +202,11 @@ __global__ __launch_bounds__(256) void walk_kernel(DtreeStepDesc* desc, const in
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < walk_n; i += 256) {
+  for (int i = threadIdx.x; i < walk_n; i += kWalkThreads) {
     desc->accepted[i] = acc_s[i];
     if (result) result[3 + i] = acc_s[i];
   }
-  for (int m = threadIdx.x; m < L; m += 256) {
+  for (int m = threadIdx.x; m < L; m += kWalkThreads) {
     desc->posterior[m] = post[m];
     if (result) result[3 + DTREE_MAX_NODES + m] = post[m];
   }
@@ -378,7 +381,7 @@ extern "C" int dtree_accept_walk(DtreeStepDesc* desc, const void* candidates, in
   DTREE_REQUIRE(desc && candidates, "accept_walk: null pointer");
   DTREE_REQUIRE(num_candidate_blocks > 0 && num_candidate_blocks <= (1 << 20), "accept_walk: num_candidate_blocks");
   DTREE_REQUIRE(rows_padded > 0 && rows_padded <= DTREE_MAX_NODES, "accept_walk: rows_padded");
-  walk_kernel<<<1, 256, 0, stream>>>(desc, reinterpret_cast<const int2*>(candidates), num_candidate_blocks,
+  walk_kernel<<<1, kWalkThreads, 0, stream>>>(desc, reinterpret_cast<const int2*>(candidates), num_candidate_blocks,
                                      rows_padded, result);
   DTREE_LAUNCH_CHECK("accept_walk launch");
   return DTREE_OK;
