@@ -410,27 +410,30 @@ def test_tree_attention_more_than_32_nodes(gpu_device, P, MP, L, shape):
     assert int(ws[: 32 * (MP // 32) * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
 
 
-@pytest.mark.parametrize("P,max_past", [(0, 64), (100, 128), (300, 2000), (1000, 4096), (4000, 4096)])
-def test_tree_attention_long_prefix_separate_combine(gpu_device, P, max_past):
+@pytest.mark.parametrize("P,max_past,MP,L", [(0, 64, 32, 25), (100, 128, 32, 25), (300, 2000, 32, 25),
+                                             (1000, 4096, 32, 25), (4000, 4096, 32, 25), (3000, 4096, 96, 65)])
+def test_tree_attention_long_prefix_separate_combine(gpu_device, P, max_past, MP, L):
     """Grids sized for long prefixes combine the workgroup partials in a
-    launch of their own (more than 128 KB of partials per head); short
-    descriptors (one split) still write the output from the main kernel."""
-    parents = random_tree(25, seed=P + 3)
-    cache, out, ref, k, v, ws = _attention_case(gpu_device, P, parents, Hq=8, Hkv=2, seed=P + 1, max_past=max_past)
+    launch of their own (more than 128 KB of partials per head), also for
+    several query blocks; short descriptors (one split) still write the
+    output from the main kernel."""
+    parents = random_tree(L, seed=P + 3)
+    cache, out, ref, k, v, ws = _attention_case(gpu_device, P, parents, Hq=8, Hkv=2, seed=P + 1, max_past=max_past,
+                                                MP=MP)
     got = bf16_f32(out)
-    assert np.abs(got[:25] - ref).max() <= 2e-2 * np.abs(ref).max()
-    assert np.all(got[25:] == 0)
-    _, out2, *_ = _attention_case(gpu_device, P, parents, Hq=8, Hkv=2, seed=P + 1, max_past=max_past)
+    assert np.abs(got[:L] - ref).max() <= 2e-2 * np.abs(ref).max()
+    assert np.all(got[L:] == 0)
+    _, out2, *_ = _attention_case(gpu_device, P, parents, Hq=8, Hkv=2, seed=P + 1, max_past=max_past, MP=MP)
     assert torch.equal(out, out2)
 
 
-def _gated_attention_case(dev, P, parents, max_past, Hq=8, Hkv=2, seed=0):
+def _gated_attention_case(dev, P, parents, max_past, Hq=8, Hkv=2, seed=0, MP=32):
     """Qwen3.5 gated attention: head_dim 256, per head [q | gate] in the QKV
     row, q/k RMSNorm, RoPE on the first 64 dims (base 1e5), output times
     sigmoid(gate) (qwen35_tree.py:503-540)."""
     from oracle import qwen35 as o35
     g = np.random.default_rng(seed)
-    D, RD, MP = 256, 64, 32
+    D, RD = 256, 64
     L = len(parents)
     cache = PagedKVCache(1, Hkv, D, max_past + MP, device=dev,
                          page_order=torch.from_numpy(g.permutation((max_past + MP + 63) // 64).astype(np.int32)))
@@ -482,17 +485,19 @@ def _gated_attention_case(dev, P, parents, max_past, Hq=8, Hkv=2, seed=0):
     return out, ref
 
 
-@pytest.mark.parametrize("P,max_past", [(0, 64), (100, 128), (700, 2048), (2000, 2048)])
-def test_gated_attention_head_dim_256(gpu_device, P, max_past):
-    """The Qwen3.5 geometry directly against the oracle, with the in-kernel
-    combine (short grids) and the separate combine launch (max_past 2048:
-    17 splits of 32 KB per head)."""
-    parents = random_tree(25, seed=P + 7)
-    out, ref = _gated_attention_case(gpu_device, P, parents, max_past, seed=P + 2)
+@pytest.mark.parametrize("P,max_past,MP,L", [(0, 64, 32, 25), (100, 128, 32, 25), (700, 2048, 32, 25),
+                                             (2000, 2048, 32, 25), (0, 64, 96, 65), (1500, 2048, 96, 65)])
+def test_gated_attention_head_dim_256(gpu_device, P, max_past, MP, L):
+    """The Qwen3.5 geometry directly against the oracle: staged query rows
+    (one query block) and per-wave rows (more than 32 nodes), with the
+    in-kernel combine (short grids) and the separate combine launch
+    (max_past 2048: 17 splits of 32 KB per head)."""
+    parents = random_tree(L, seed=P + 7)
+    out, ref = _gated_attention_case(gpu_device, P, parents, max_past, seed=P + 2, MP=MP)
     got = bf16_f32(out)
-    assert np.abs(got[:25] - ref).max() <= 2e-2 * np.abs(ref).max()
-    assert np.all(got[25:] == 0)
-    out2, _ = _gated_attention_case(gpu_device, P, parents, max_past, seed=P + 2)
+    assert np.abs(got[:L] - ref).max() <= 2e-2 * np.abs(ref).max()
+    assert np.all(got[L:] == 0)
+    out2, _ = _gated_attention_case(gpu_device, P, parents, max_past, seed=P + 2, MP=MP)
     assert torch.equal(out, out2)
 
 
