@@ -36,7 +36,15 @@ def _hip():
     dispatcher, on the step's critical path between two verify steps."""
     global _HIP
     if _HIP is None:
-        h = C.CDLL("libamdhip64.so")
+        h = None
+        for name in ("libamdhip64.so", "libamdhip64.so.7", "libamdhip64.so.6"):
+            try:
+                h = C.CDLL(name)
+                break
+            except OSError:
+                continue
+        if h is None:
+            raise RuntimeError("the HIP runtime (libamdhip64.so) is not loadable")
         h.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
         h.hipMemcpyAsync.restype = C.c_int
         h.hipStreamSynchronize.argtypes = [C.c_void_p]
