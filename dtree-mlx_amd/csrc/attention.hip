@@ -57,6 +57,7 @@ struct AttnParams {
   int write_cache;
   float* part; int* counters;
   int sep_combine;  // partials are combined by attn_combine_kernel (long prefixes)
+  int off_xcd;      // test hook: treat every workgroup as off its expected XCD
 };
 
 __device__ __forceinline__ int swap_bits23(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
@@ -823,7 +824,7 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     __syncthreads();
     if (threadIdx.x == 0) {
       // arrival count in the low half, workgroups off their XCD in the high
-      const bool native = xcc_id() == (int)(blockIdx.x % kXcds);
+      const bool native = !p.off_xcd && xcc_id() == (int)(blockIdx.x % kXcds);
       const int old = arrive_add(&p.counters[hb], native ? 1 : 1 + kForeign);
       int last = 0;
       if ((old & (kForeign - 1)) == nsplit - 1) {
@@ -1054,6 +1055,7 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   p.max_chunks = attn_max_chunks(D, a->max_past_length, nt);
   p.splits = attn_splits(D, a->max_past_length, nt);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
+  p.off_xcd = off_xcd_test();
   p.counters = reinterpret_cast<int*>(a->workspace);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) +
                                     (((size_t)a->num_heads * nt * sizeof(int) + 255) & ~(size_t)255));

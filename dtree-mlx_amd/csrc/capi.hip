@@ -1,5 +1,6 @@
 // C-ABI plumbing: per-thread error message, ABI queries, HIP graph capture.
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "common.h"
@@ -13,6 +14,14 @@ void set_error(const std::string& msg) { g_last_error = msg; }
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
   return code;
+}
+
+// Test hook: DTREE_TEST_OFF_XCD=1 makes the kernels treat every workgroup as
+// placed off its expected XCD, so the cross-XCD (sc1) exchange paths run even
+// though the dispatcher always places workgroups round-robin. Read per launch.
+bool off_xcd_test() {
+  const char* e = std::getenv("DTREE_TEST_OFF_XCD");
+  return e && e[0] == '1';
 }
 
 int hip_check(hipError_t e, const char* what) {

@@ -20,6 +20,7 @@ namespace dtree {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int hip_check(hipError_t e, const char* what);
+bool off_xcd_test();  // DTREE_TEST_OFF_XCD=1: exercise the cross-XCD exchange paths
 
 #define DTREE_REQUIRE(cond, msg)                         \
   do {                                                   \

@@ -50,6 +50,7 @@ struct GemmParams {
   int T, G; unsigned part_bytes;
   // ranged ring loads (32 tiled rows): bytes of w, w_sb and one x plane
   unsigned w_bytes, sb_bytes, x_bytes;
+  int off_xcd;  // test hook: treat every workgroup as off its expected XCD
 };
 
 // Index of element (m, col) of a bf16 output with `ld` columns.
@@ -582,7 +583,7 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   // a column block run on one XCD; `native` confirms the placement.
   const bool xcd_order = G % kXcds == 0;
   const int g = sk_logical(blockIdx.x, G);
-  const bool native = xcd_order && xcc_id() == (int)(blockIdx.x % kXcds);
+  const bool native = xcd_order && !p.off_xcd && xcc_id() == (int)(blockIdx.x % kXcds);
   const int U0 = (int)((long long)g * T / G), U1 = (int)((long long)(g + 1) * T / G);
   if (U0 >= U1) return;
   const int b_first = U0 / nkb, b_last = (U1 - 1) / nkb;
@@ -1097,7 +1098,7 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
   if constexpr (KS == 2) {
     // Thread t holds elements 4t .. 4t+3 of the tile; slot 2 * tile + half.
     const int t = threadIdx.x;
-    const bool native = xcc_id() == (bid & 7);
+    const bool native = !p.off_xcd && xcc_id() == (bid & 7);
     const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
     const f32x4_t mine = reinterpret_cast<const f32x4_t*>(red)[t];
     const int off = ((2 * tile + half) * TE + 4 * t) * 4;
@@ -1205,6 +1206,7 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   p.out_tiled = a->out_layout == DTREE_W_TILED;
   p.next_norm = a->next_norm; p.ss_out = a->ss_out;
   p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
+  p.off_xcd = off_xcd_test();
   const size_t nt8 = (size_t)((ntiles + 7) / 8) * 8;
   p.counters = reinterpret_cast<int*>(a->workspace);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kCounterBytes);

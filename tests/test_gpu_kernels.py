@@ -685,3 +685,39 @@ def test_walk_and_compaction_match_oracle(gpu_device, seed):
         # rows past the kept range are untouched unless overwritten by the move
         np.testing.assert_array_equal(bf16_f32(cache.logical_keys(li, P + L))[P + n:], before_k[li][P + n:])
     assert torch.equal(hsel[:n].cpu(), hid[acc].cpu())
+
+
+def test_cross_xcd_exchange_paths(gpu_device, monkeypatch):
+    """The dispatcher places workgroups round-robin over the XCDs, so the
+    exchanges normally read partials from the local L2. DTREE_TEST_OFF_XCD=1
+    makes every workgroup count as off its expected XCD: partials are then
+    read past the L2 (the path taken if placement ever differs) and must give
+    the same bits."""
+    L = 25
+
+    def gemms():
+        outs = []
+        for n, k, sched in [(19456 // 4, 2560, -2), (2560, 4096, -3), (2560, 9728, -2)]:
+            x = _rows(32, L, k, g, gpu_device)
+            w = torch.from_numpy(g.standard_normal((n, k)).astype(np.float32) * 0.05).to(torch.bfloat16)
+            w = w.to(gpu_device)
+            out = torch.zeros(32, n, device=gpu_device)
+            ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, n, k, 0), dtype=torch.uint8, device=gpu_device)
+            _gemm(x, w, N.EPI_STORE_F32, sched, ws, out_f32=out, tiled=True)
+            outs.append(out)
+        torch.cuda.synchronize()
+        return outs
+
+    g = np.random.default_rng(77)
+    native = gemms()
+    parents = random_tree(25, seed=9)
+    _, a_native, *_ = _attention_case(gpu_device, 1000, parents, seed=5)
+    monkeypatch.setenv("DTREE_TEST_OFF_XCD", "1")
+    g = np.random.default_rng(77)
+    off = gemms()
+    _, a_off, ref, *_ = _attention_case(gpu_device, 1000, parents, seed=5)
+    monkeypatch.delenv("DTREE_TEST_OFF_XCD")
+    for a, b in zip(native, off):
+        assert torch.equal(a, b)
+    assert torch.equal(a_native, a_off)
+    assert np.abs(bf16_f32(a_off)[:25] - ref).max() <= 2e-2 * np.abs(ref).max()
