@@ -392,10 +392,11 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
 def gemm_kernel_name(n: int, k: int, epi: int, quant: str) -> str:
     """Kernel the library picks for a 32-row tiled GEMM with split_k 0: for
     bf16 with K <= 4096 and N <= 12800 one workgroup per 32-column tile, two
-    (one per K half) at K = 4096 and N % 256 == 0; the stream-K schedule
-    otherwise (gemm.hip, dtree_gemm_bf16)."""
+    or three (one per part of K) at K = 4096 and N % 256 == 0; the stream-K
+    schedule otherwise (gemm.hip, dtree_gemm_bf16)."""
     if quant == "bf16" and k <= 4096 and n <= 12800:
-        return f"dp_gemm_kernel<true, {epi}, {2 if k >= 4096 and n % 256 == 0 else 1}>"
+        parts = (3 if (n // 32) * 3 <= 256 else 2) if k >= 4096 and n % 256 == 0 else 1  # 256 CUs
+        return f"dp_gemm_kernel<true, {epi}, {parts}>"
     return f"sk_gemm_kernel<true, {epi}, {'true' if quant == 'q4' else 'false'}>"
 
 

@@ -1027,12 +1027,11 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nkb = p.k >> 6;
-  // KS = 2: blockIdx = 16 * (tile / 8) + 8 * half + tile % 8 (host: tiles % 8 == 0).
+  // KS > 1: blockIdx = 8 KS (tile / 8) + 8 part + tile % 8 (host: tiles % 8 == 0).
   const int bid = blockIdx.x;
-  const int half = KS == 2 ? (bid >> 3) & 1 : 0;
-  const int tile = KS == 2 ? ((bid >> 4) << 3) + (bid & 7) : bid;
-  const int kb0 = KS == 2 ? half * ((nkb + 1) >> 1) : 0;
-  const int kb1 = KS == 2 ? (half ? nkb : (nkb + 1) >> 1) : nkb;
+  const int part = KS > 1 ? (bid >> 3) % KS : 0;
+  const int tile = KS > 1 ? (bid / (8 * KS)) * 8 + (bid & 7) : bid;
+  const int kb0 = part * nkb / KS, kb1 = (part + 1) * nkb / KS;
   const int nk = kb1 - kb0;
   float ssv[kSsBatch];
   ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
@@ -1095,20 +1094,20 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
     for (int r = 0; r < 16; ++r) red[acc_row(r, h) * TN + c] = acc[r];
   }
   __syncthreads();
-  if constexpr (KS == 2) {
-    // Thread t holds elements 4t .. 4t+3 of the tile; slot 2 * tile + half.
+  if constexpr (KS > 1) {
+    // Thread t holds elements 4t .. 4t+3 of the tile; slot KS * tile + part.
     const int t = threadIdx.x;
     const bool native = !p.off_xcd && xcc_id() == (bid & 7);
     const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
     const f32x4_t mine = reinterpret_cast<const f32x4_t*>(red)[t];
-    const int off = ((2 * tile + half) * TE + 4 * t) * 4;
+    const int off = ((KS * tile + part) * TE + 4 * t) * 4;
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, mine), prs, off, 0, kSc1);
     wait_stores_done();
     __syncthreads();
     if (t == 0) {
       const int old = arrive_add(&p.counters[tile], native ? 1 : 1 + kForeign);
       int last = 0;
-      if ((old & (kForeign - 1)) == 1) {
+      if ((old & (kForeign - 1)) == KS - 1) {
         last = native && old < kForeign ? 2 : 1;
         reset_counter(&p.counters[tile]);
       }
@@ -1117,11 +1116,19 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
     __syncthreads();
     const int last = __builtin_amdgcn_readfirstlane(last_s);
     if (!last) return;
-    const int poff = ((2 * tile + (half ^ 1)) * TE + 4 * t) * 4;
-    const u32x4_t other = last == 2 ? __builtin_amdgcn_raw_buffer_load_b128(prs, poff, 0, kSc0)
-                                    : __builtin_amdgcn_raw_buffer_load_b128(prs, poff, 0, kSc1);
-    reinterpret_cast<f32x4_t*>(red)[t] = half ? __builtin_bit_cast(f32x4_t, other) + mine
-                                              : mine + __builtin_bit_cast(f32x4_t, other);
+    // The parts in part order (own part from registers), so the sum does not
+    // depend on which part arrives last.
+    u32x4_t pv[KS];
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+      const int poff = q == part ? (int)kOob : ((KS * tile + q) * TE + 4 * t) * 4;
+      pv[q] = last == 2 ? __builtin_amdgcn_raw_buffer_load_b128(prs, poff, 0, kSc0)
+                        : __builtin_amdgcn_raw_buffer_load_b128(prs, poff, 0, kSc1);
+    }
+    f32x4_t sum = part == 0 ? mine : __builtin_bit_cast(f32x4_t, pv[0]);
+#pragma unroll
+    for (int q = 1; q < KS; ++q) sum += q == part ? mine : __builtin_bit_cast(f32x4_t, pv[q]);
+    reinterpret_cast<f32x4_t*>(red)[t] = sum;
     __syncthreads();
   }
   tile_epilogue<32, TN, EPI>(p, red, rs, tile, EPI == DTREE_EPI_RESIDUAL ? xo : nullptr);
@@ -1142,9 +1149,12 @@ static void launch_dp(const GemmParams& p, int epi, hipStream_t st) {
 
 using namespace dtree;
 
-// The paired per-tile schedule: counters + one 32 x 32 fp32 partial per
-// (tile, half).
-static size_t dp_pair_workspace_bytes(int n) { return kCounterBytes + (size_t)(n / 32) * 2 * 32 * 32 * sizeof(float); }
+// The split per-tile schedules: counters + one 32 x 32 fp32 partial per
+// (tile, part), at most kDpMaxParts parts.
+constexpr int kDpMaxParts = 3;
+static size_t dp_pair_workspace_bytes(int n) {
+  return kCounterBytes + (size_t)(n / 32) * kDpMaxParts * 32 * 32 * sizeof(float);
+}
 
 extern "C" size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int split_k) {
   if (rows_padded <= 0 || n <= 0 || k <= 0) return 0;
@@ -1175,9 +1185,9 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0, "gemm: k must be a positive multiple of 64");
   DTREE_REQUIRE(a->ldx >= a->k && a->ldx % 8 == 0, "gemm: ldx must be >= k and a multiple of 8");
   const int ntiles = a->n / tn, nkb = a->k / 64;
-  DTREE_REQUIRE(a->split_k >= -3, "gemm: split_k must be >= -3");
+  DTREE_REQUIRE(a->split_k >= -4, "gemm: split_k must be >= -4");
   DTREE_REQUIRE(a->split_k >= 0 || (a->w_layout != DTREE_W_ROWMAJOR && a->rows_padded == 32),
-                "gemm: split_k -1 / -2 / -3 need tiled weights and 32 rows");
+                "gemm: split_k -1 .. -4 need tiled weights and 32 rows");
   const int S = a->split_k > 0 ? a->split_k : auto_split(ntiles, nkb);
   DTREE_REQUIRE(S <= nkb, "gemm: split_k larger than the number of 64-wide K blocks");
   DTREE_REQUIRE((size_t)ntiles * sizeof(int) <= kCounterBytes, "gemm: n too large for the tile counter region");
@@ -1266,19 +1276,29 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   // MI355X (K <= 4096 and N <= 12800, e.g. the fused QKV and o_proj at hidden
   // 2560): no cross-workgroup reduction tail, at the price of re-reading the
   // activations per tile and of fewer than 256 workgroups on narrow N.
-  // Of those, K = 4096 (o_proj, out_proj) runs two workgroups per tile: 11.8
-  // vs 15.8 us at N = 2560; at K = 2560 the halves are too short (QKV N =
-  // 6144: 16.7 vs 12.4 us).
+  // Of those, K = 4096 (o_proj, out_proj) runs two or three workgroups per
+  // tile: 11.4 vs 15.8 us at N = 2560; at K = 2560 the parts are too short
+  // (QKV N = 6144: 16.7 vs 12.4 us).
   const bool dp_auto = a->split_k == 0 && a->k <= 4096 && a->n <= 12800;
   const bool pairs_auto = dp_auto && a->k >= 4096 && a->n % 256 == 0;
-  if (tiled && !q4 && a->rows_padded == 32 && (a->split_k == -3 || pairs_auto)) {
-    // Two workgroups per tile, one per K half (see dp_gemm_kernel).
-    DTREE_REQUIRE(a->n % 256 == 0 && nkb >= 2, "gemm: split_k -3 needs n % 256 == 0 and k >= 128");
+  if (tiled && !q4 && a->rows_padded == 32 && (a->split_k == -3 || a->split_k == -4 || pairs_auto)) {
+    // Two (-3) or three (-4) workgroups per tile, one per part of K (see
+    // dp_gemm_kernel).
+    // automatic: three parts while the grid stays within one workgroup per CU
+    // (o_proj: 240 workgroups, 11.4 us; two parts 11.9 us)
+    const int dp_parts = a->split_k == -4 ? 3 : a->split_k == -3 ? 2 : (a->n / 32) * 3 <= device_cus() ? 3 : 2;
+    DTREE_REQUIRE(a->n % 256 == 0 && nkb >= dp_parts,
+                  "gemm: split_k -3 / -4 need n % 256 == 0 and k >= 64 * parts");
     const size_t need_pairs = dp_pair_workspace_bytes(a->n);
     DTREE_REQUIRE(a->workspace_bytes >= need_pairs, "gemm: workspace too small for the paired schedule");
     p.part_bytes = (unsigned)(need_pairs - kCounterBytes);
-    if (p.x_lo) launch_dp<true, 2>(p, epi, stream);
-    else launch_dp<false, 2>(p, epi, stream);
+    if (dp_parts == 3) {
+      if (p.x_lo) launch_dp<true, 3>(p, epi, stream);
+      else launch_dp<false, 3>(p, epi, stream);
+    } else {
+      if (p.x_lo) launch_dp<true, 2>(p, epi, stream);
+      else launch_dp<false, 2>(p, epi, stream);
+    }
     DTREE_LAUNCH_CHECK("gemm launch");
     return DTREE_OK;
   }

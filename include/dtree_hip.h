@@ -110,8 +110,9 @@ typedef struct DtreeGemmArgs {
   int32_t split_k;        /* >= 1 split-K; 0 = automatic; tiled 32 rows only:
                              -1 one workgroup per 32-column tile (bf16),
                              -2 stream-K schedule,
-                             -3 two workgroups per 32-column tile, one per
-                                K half (bf16, n % 256 == 0, k >= 128)      */
+                             -3 / -4 two / three workgroups per 32-column
+                                tile, one per part of K (bf16,
+                                n % 256 == 0, k >= 64 * parts)             */
   const float* ss_in;     /* [rows_padded/32][ss_tiles][32] or NULL        */
   int32_t ss_tiles;
   int32_t norm_dim;       /* divisor of the row mean square                */

@@ -189,19 +189,20 @@ def test_gemm_swiglu_epilogue(gpu_device):
 
 
 # ---- 32-row tiled paths: stream-K (split_k -2), one workgroup per tile
-# (split_k -1) and two per tile, one per K half (split_k -3, n % 256 == 0 and
-# k >= 128); split_k 0 picks one of them per shape.
+# (split_k -1) and two or three per tile, one per part of K (split_k -3 / -4,
+# n % 256 == 0); split_k 0 picks one of them per shape.
 # Shapes chosen for the stream-K schedule: one unit; one K block over many
 # column blocks (workgroups touching several blocks); one column block over 152
 # K blocks (one block shared by 152 workgroups); and the Qwen3-4B layer shapes.
 SK_SHAPES = [(64, 64), (4096, 64), (19456, 64), (64, 9728), (256, 1024), (6144, 2560), (2560, 4096),
              (19456, 2560), (2560, 9728)]
-SCHEDULES = [-3, -2, -1, 0]
+SCHEDULES = [-4, -3, -2, -1, 0]
 
 
 def _skip_unsupported(n, k, sched):
-    if sched == -3 and (n % 256 or k < 128):
-        pytest.skip("the paired schedule needs n % 256 == 0 and k >= 128")
+    parts = {-3: 2, -4: 3}.get(sched)  # workgroups per 32-column tile
+    if parts and (n % 256 or k < 64 * parts):
+        pytest.skip("the split per-tile schedules need n % 256 == 0 and k >= 64 * parts")
 
 
 def _sk_args(xt, xlo_t, wt, n, k, epi, ws, sched=0):
