@@ -391,7 +391,6 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 constexpr int kSkMaxBlocks = 4;  // 64-column blocks one workgroup may touch
 constexpr int kSkDepth = 4;      // units in flight per wave
 constexpr int kSkMaxGrid = 1024; // CU-count bound used for workspace sizing
-constexpr int kSkMaxKb = 64;     // q4: K groups whose activation sums one workgroup keeps
 
 // q4 nibble pair j of a repacked word -> two bf16 holding 128 + q (exact: the
 // bf16 with bits 0x4300 | q is 128 + q for q < 128), K order (2j, 2j+1).
@@ -401,42 +400,23 @@ __device__ __forceinline__ u32x4_t q4_pairs(uint32_t w) {
 }
 
 // ---- q4 helpers for 32 rows ----------------------------------------------------
-// Activation sums per (K group, row) over groups [kb0, kb0 + ng) into
-// xsum[j * 32 + m] (j = group - kb0): the affine bias term and the 128 offset
-// of the nibble encoding need them.
-template <bool LO>
-__device__ __forceinline__ void q4_xsums(const uint16_t* x, const uint16_t* xlo, int kb0, int ng, int nkb,
-                                         float* xsum) {
-  for (int pr = threadIdx.x; pr < ng * 32; pr += kThreads) {
-    const int j = pr >> 5, m = pr & 31;
-    int kb = kb0 + j;
-    if (kb >= nkb) kb -= nkb;
-    float sum = 0.f;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const size_t off = (size_t)kb * 2048 + (size_t)(i * 64 + m + 32 * hh) * 8;
-        const u32x4_t v = ld_u32x4(x + off);
-        u32x4_t vl = u32x4_t{0u, 0u, 0u, 0u};
-        if (LO) vl = ld_u32x4(xlo + off);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          sum += (__uint_as_float(v[q] << 16) + __uint_as_float(v[q] & 0xffff0000u)) +
-                 (__uint_as_float(vl[q] << 16) + __uint_as_float(vl[q] & 0xffff0000u));
-      }
-    xsum[j * 32 + m] = sum;
-  }
-}
-
 // One q4 group (64 K) of two 32-column blocks: fresh MFMA sums of x (128 + q),
-// then acc += s * sums + (b - 128 s) * sum(x) per (row, column).
+// then acc += s * sums + (b - 128 s) * sum(x) per (row, column). sum(x) (the
+// affine bias term and the 128 offset of the nibble encoding need it) comes
+// from the same registers: an MFMA of the group's activations against bf16
+// ones gives sum_k x per row in the accumulator layout.
 template <bool LO>
-__device__ __forceinline__ void q4_group(const u32x4_t (&xv)[2][4], const u32x4_t (&wq)[2], const uint32_t (&sb)[2],
-                                         const float* xs_group, int h, f32x16_t (&acc)[2]) {
-  f32x4_t xsv[4];
+__device__ __forceinline__ void q4_group(const u32x4_t (&xv)[2][4], const u32x4_t (&wq)[2],
+                                            const uint32_t (&sb)[2], f32x16_t (&acc)[2]) {
+  const u32x4_t ones = u32x4_t{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  f32x16_t xs;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) xsv[q] = *reinterpret_cast<const f32x4_t*>(xs_group + 4 * h + 8 * q);
+  for (int r = 0; r < 16; ++r) xs[r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xs = mfma32(xv[0][i], ones, xs);
+    if (LO) xs = mfma32(xv[1][i], ones, xs);
+  }
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     f32x16_t au;
@@ -451,18 +431,18 @@ __device__ __forceinline__ void q4_group(const u32x4_t (&xv)[2][4], const u32x4_
     const float sc = __uint_as_float(sb[nb] << 16);
     const float cf = __uint_as_float(sb[nb] & 0xffff0000u) - 128.f * sc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[nb][r] += sc * au[r] + cf * xsv[r >> 2][r & 3];
+    for (int r = 0; r < 16; ++r) acc[nb][r] += sc * au[r] + cf * xs[r];
   }
 }
 
 // q4 counterpart of wg_tile for 32 rows and 64 columns (two 32-row blocks):
 // the tile over all K, waves interleaving groups, a 4-deep register ring of
 // (q4 words, scale/bias, activations), LDS reduction of the four waves into
-// red[row * 64 + col] in wave order. xsum holds every group's activation sums.
+// red[row * 64 + col] in wave order.
 template <bool LO>
 __device__ __forceinline__ void wg_tile_q4(const uint16_t* __restrict__ x, const uint16_t* __restrict__ xlo,
                                            const uint32_t* __restrict__ wq, const uint32_t* __restrict__ wsb,
-                                           int K, int tile, const float* xsum, float* red) {
+                                           int K, int tile, float* red) {
   constexpr int TN = 64, TE = 32 * TN, D = 4;
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -499,7 +479,7 @@ __device__ __forceinline__ void wg_tile_q4(const uint16_t* __restrict__ x, const
       const int j = j0 + s;
       if (j < n) {
         __builtin_amdgcn_sched_barrier(0);
-        q4_group<LO>(xr[s], wr[s], sbr[s], xsum + (wave + kWaves * j) * 32, h, acc);
+        q4_group<LO>(xr[s], wr[s], sbr[s], acc);
         __builtin_amdgcn_sched_barrier(0);
         issue(s, j + D);
       }
@@ -572,7 +552,6 @@ template <bool LO, int EPI, bool Q4>
 __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   constexpr int TN = 64, TE = 32 * TN;
   __shared__ float acc_lds[kSkMaxBlocks * kWaves * TE];  // [local block][wave][row][col]
-  __shared__ float xsum_lds[Q4 ? kSkMaxKb * 32 : 1];      // q4: [local group][row] sum of x
   __shared__ float rs[32];
   __shared__ float rs_scratch[kThreads];
   __shared__ int last_flag[kSkMaxBlocks], first_q[kSkMaxBlocks], pieces[kSkMaxBlocks];
@@ -593,11 +572,6 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   // order, so waiting for them later does not wait for the stream).
   float ssv[kSsBatch];
   ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
-  // q4: per (group, row) sums of the activations over this workgroup's groups
-  // (the affine bias term and the 128 offset of the nibble encoding need them).
-  const int ngrp = (U1 - U0) < nkb ? (U1 - U0) : nkb;
-  const int kbase = (U1 - U0) < nkb ? U0 % nkb : 0;
-  if constexpr (Q4) q4_xsums<LO>(p.x, p.x_lo, kbase, ngrp, nkb, xsum_lds);
 
   // ---- stream this wave's quarter of the range ----
   const int R = U1 - U0;
@@ -674,10 +648,8 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
         }
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (Q4) {
-          int j = u - b * nkb - kbase;
-          if (j < 0) j += nkb;
           u32x4_t wq2[2] = {wr[s][0][0], wr[s][1][0]};
-          q4_group<LO>(xr[s], wq2, sbr[s], xsum_lds + j * 32, h, acc);
+          q4_group<LO>(xr[s], wq2, sbr[s], acc);
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
@@ -845,10 +817,8 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   __shared__ float red[(kWaves - 1) * TE];
   __shared__ float rs[MP];
   __shared__ float rs_scratch[kThreads];
-  __shared__ float xsum[Q4 ? kSkMaxKb * 32 : 1];
   static_assert(!Q4 || (MB == 1 && NB == 2), "q4 LM head: 32 rows, 64-column tiles");
   row_scale<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, rs, rs_scratch);
-  if constexpr (Q4) q4_xsums<LO>(p.x, p.x_lo, 0, p.k >> 6, p.k >> 6, xsum);
   float bv[IT];
   int bi[IT];
 #pragma unroll
@@ -862,7 +832,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
     __syncthreads();
     if constexpr (Q4)
       wg_tile_q4<LO>(p.x, p.x_lo, reinterpret_cast<const uint32_t*>(p.w), reinterpret_cast<const uint32_t*>(p.w_sb),
-                     p.k, tile, xsum, red);
+                     p.k, tile, red);
     else
       wg_tile<MB, NB, U, LO, TILED>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, 0, nkb, red);
 #pragma unroll
@@ -963,11 +933,7 @@ constexpr size_t kCounterBytes = 65536;  // 16384 column tiles
 // would touch more than kSkMaxBlocks column blocks.
 static int sk_grid(int T, int nkb, int cus) {
   int G = T < cus ? T : cus;
-  int need = (T + 3 * nkb - 1) / (3 * nkb);  // <= kSkMaxBlocks column blocks per workgroup
-  if (nkb > kSkMaxKb) {                      // q4: <= kSkMaxKb groups per workgroup
-    const int need_q4 = (T + kSkMaxKb - 1) / kSkMaxKb;
-    if (need_q4 > need) need = need_q4;
-  }
+  const int need = (T + 3 * nkb - 1) / (3 * nkb);  // <= kSkMaxBlocks column blocks per workgroup
   return G > need ? G : need;
 }
 
@@ -1368,7 +1334,7 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
   DTREE_REQUIRE(emb_layout == DTREE_W_ROWMAJOR || emb_layout == DTREE_W_TILED || emb_layout == DTREE_W_Q4G64,
                 "lmhead: unknown emb_layout");
   if (emb_layout == DTREE_W_Q4G64) {
-    DTREE_REQUIRE(x_layout == DTREE_W_TILED && ldx == hidden && hidden / 64 <= kSkMaxKb,
+    DTREE_REQUIRE(x_layout == DTREE_W_TILED && ldx == hidden && hidden <= 4096,
                   "lmhead: q4 embedding needs tiled x and hidden <= 4096");
     DTREE_REQUIRE(emb_scales && ((uintptr_t)emb & 15) == 0, "lmhead: q4 embedding needs emb_scales");
     DTREE_REQUIRE(vocab % 64 == 0, "lmhead: q4 embedding needs vocab % 64 == 0");
