@@ -393,10 +393,13 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str) -> str:
     """Kernel the library picks for a 32-row tiled GEMM with split_k 0: for
     bf16 with K <= 4096 and N <= 12800 one workgroup per 32-column tile, two
     or three (one per part of K) at K = 4096 and N % 256 == 0; the stream-K
-    schedule otherwise (gemm.hip, dtree_gemm_bf16)."""
+    schedule otherwise, for q4 at two workgroups per CU when there are at
+    least 20 64 x 64 units per CU (gemm.hip, dtree_gemm_bf16)."""
     if quant == "bf16" and k <= 4096 and n <= 12800:
         parts = (3 if (n // 32) * 3 <= 256 else 2) if k >= 4096 and n % 256 == 0 else 1  # 256 CUs
         return f"dp_gemm_kernel<true, {epi}, {parts}>"
+    if quant == "q4" and (n // 64) * (k // 64) >= 20 * 256:
+        return f"sk2_gemm_kernel<true, {epi}>"
     return f"sk_gemm_kernel<true, {epi}, {'true' if quant == 'q4' else 'false'}>"
 
 

@@ -548,10 +548,11 @@ __device__ __forceinline__ void partials_add(const u32x4_t (&v)[kRedBatch][2], i
   }
 }
 
-template <bool LO, int EPI, bool Q4>
-__global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
+// RING units in flight per wave, at most MAXB column blocks per workgroup.
+template <bool LO, int EPI, bool Q4, int RING, int MAXB>
+__device__ __forceinline__ void sk_gemm_body(const GemmParams& p) {
   constexpr int TN = 64, TE = 32 * TN;
-  __shared__ float acc_lds[kSkMaxBlocks * kWaves * TE];  // [local block][wave][row][col]
+  __shared__ float acc_lds[MAXB * kWaves * TE];  // [local block][wave][row][col]
   __shared__ float rs[32];
   __shared__ float rs_scratch[kThreads];
   __shared__ int last_flag[kSkMaxBlocks], first_q[kSkMaxBlocks], pieces[kSkMaxBlocks];
@@ -566,8 +567,8 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   const int U0 = (int)((long long)g * T / G), U1 = (int)((long long)(g + 1) * T / G);
   if (U0 >= U1) return;
   const int b_first = U0 / nkb, b_last = (U1 - 1) / nkb;
-  const int nloc = b_last - b_first + 1;  // <= kSkMaxBlocks (host-checked)
-  if (nloc > kSkMaxBlocks) return;
+  const int nloc = b_last - b_first + 1;  // <= MAXB (host-checked)
+  if (nloc > MAXB) return;
   // The row scale's loads go out before the weight stream (loads retire in
   // order, so waiting for them later does not wait for the stream).
   float ssv[kSsBatch];
@@ -582,8 +583,8 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   // (2 blocks x 1 load) + (scale, bias) per block; activations hi/lo. A slot
   // past the wave's range is refilled with ranged loads that return zero, so
   // every refill issues the same loads (see kOob) and is never consumed.
-  u32x4_t wr[kSkDepth][2][Q4 ? 1 : 4], xr[kSkDepth][2][4];
-  uint32_t sbr[kSkDepth][2];
+  u32x4_t wr[RING][2][Q4 ? 1 : 4], xr[RING][2][4];
+  uint32_t sbr[RING][2];
   auto issue = [&](int s, int u) {
     const bool ok = u < a1;
     const int b = u / nkb, kb = u - b * nkb;
@@ -629,15 +630,15 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
   zero();
   int cur = a0 < a1 ? a0 / nkb : -1;
 #pragma unroll
-  for (int s = 0; s < kSkDepth; ++s) issue(s, a0 + s);
+  for (int s = 0; s < RING; ++s) issue(s, a0 + s);
   // The accumulator slots are cleared while the first units are in flight.
   for (int e = threadIdx.x; e < nloc * kWaves * TE / 4; e += kThreads)
     reinterpret_cast<f32x4_t*>(acc_lds)[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   __syncthreads();
   ss_finish<1>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, ssv, rs, rs_scratch);
-  for (int ub = a0; ub < a1; ub += kSkDepth) {
+  for (int ub = a0; ub < a1; ub += RING) {
 #pragma unroll
-    for (int s = 0; s < kSkDepth; ++s) {
+    for (int s = 0; s < RING; ++s) {
       const int u = ub + s;
       if (u < a1) {
         const int b = u / nkb;
@@ -661,7 +662,7 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      issue(s, u + kSkDepth);
+      issue(s, u + RING);
     }
   }
   if (cur >= 0) dump(cur);
@@ -792,6 +793,21 @@ __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
     j = jn;
   }
 #undef DTREE_SK_EPILOGUE
+}
+
+template <bool LO, int EPI, bool Q4>
+__global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
+  sk_gemm_body<LO, EPI, Q4, kSkDepth, kSkMaxBlocks>(p);
+}
+
+// q4 at two waves per SIMD: a 3-deep ring and at most two column blocks per
+// workgroup (half the accumulator LDS) let two workgroups share a CU. q4
+// units are issue-bound (nibble unpacking, MFMA chain and scale/bias
+// epilogue in one instruction stream), so a second wave per SIMD pays on
+// the large shapes.
+template <bool LO, int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void sk2_gemm_kernel(GemmParams p) {
+  sk_gemm_body<LO, EPI, true, 3, 2>(p);
 }
 
 // ---- LM head: persistent over vocab tiles, per-row running argmax --------
@@ -937,9 +953,20 @@ static int sk_grid(int T, int nkb, int cus) {
   return G > need ? G : need;
 }
 
+// q4 two-per-CU grid (sk2_gemm_kernel) for large unit counts: two
+// workgroups per CU, more only when a range would touch more than two
+// column blocks; 0 when the shape keeps one workgroup per CU.
+static int sk2_grid(int T, int nkb, int cus) {
+  if (T < 20 * cus) return 0;
+  const int G = T < 2 * cus ? T : 2 * cus;
+  const int need = (T + nkb - 1) / nkb;  // ranges of <= nkb units touch <= 2 blocks
+  return G > need ? G : need;
+}
+
 static size_t sk_workspace_bytes(int n, int k, int cus) {
   const int nkb = k / 64, nblk = n / 64, T = nblk * nkb;
-  return kCounterBytes + (size_t)(sk_grid(T, nkb, cus) + nblk) * 32 * 64 * sizeof(float);
+  const int g1 = sk_grid(T, nkb, cus), g2 = sk2_grid(T, nkb, cus);
+  return kCounterBytes + (size_t)((g1 > g2 ? g1 : g2) + nblk) * 32 * 64 * sizeof(float);
 }
 
 static int device_cus() {
@@ -952,6 +979,16 @@ static int device_cus() {
     cached[dev] = n;
   }
   return cached[dev];
+}
+
+template <bool LO>
+static void launch_sk2(const GemmParams& p, int epi, hipStream_t st) {
+  switch (epi) {
+    case DTREE_EPI_STORE_F32: sk2_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: sk2_gemm_kernel<LO, DTREE_EPI_RESIDUAL><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: sk2_gemm_kernel<LO, DTREE_EPI_SWIGLU><<<p.G, kThreads, 0, st>>>(p); break;
+    default: sk2_gemm_kernel<LO, DTREE_EPI_STORE_BF16><<<p.G, kThreads, 0, st>>>(p); break;
+  }
 }
 
 template <bool LO, bool Q4>
@@ -1278,12 +1315,16 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     const int cus = device_cus();
     const int nblk = a->n / 64;
     p.T = nblk * nkb;
-    p.G = sk_grid(p.T, nkb, cus < kSkMaxGrid ? cus : kSkMaxGrid);
+    const int g2 = q4 ? sk2_grid(p.T, nkb, cus < kSkMaxGrid ? cus : kSkMaxGrid) : 0;
+    p.G = g2 ? g2 : sk_grid(p.T, nkb, cus < kSkMaxGrid ? cus : kSkMaxGrid);
     DTREE_REQUIRE((long long)p.T * p.G < (1LL << 31), "gemm: too many 64 x 64 units for the stream-K schedule");
     const size_t need_sk = sk_workspace_bytes(a->n, a->k, cus < kSkMaxGrid ? cus : kSkMaxGrid);
     DTREE_REQUIRE(a->workspace_bytes >= need_sk, "gemm: workspace too small for the stream-K schedule");
     p.part_bytes = (unsigned)(need_sk - kCounterBytes);
-    if (q4) {
+    if (q4 && g2) {
+      if (p.x_lo) launch_sk2<true>(p, epi, stream);
+      else launch_sk2<false>(p, epi, stream);
+    } else if (q4) {
       if (p.x_lo) launch_sk<true, true>(p, epi, stream);
       else launch_sk<false, true>(p, epi, stream);
     } else {
