@@ -60,10 +60,11 @@ def algorithmic_bytes(cfg, P: int, L: int, quant: str = "bf16") -> dict:
                 tree_kv_write=kv_write, total=total)
 
 
-def cpu_baseline(cfg, weights, cache, tree, P, sample_layers=4, min_seconds=15.0):
-    """The fp32 numpy oracle of the same verify step, timed on the host cores on
-    a bounded sample: `sample_layers` of the 36 tree blocks (repeated) and a
-    quarter of the LM head, scaled linearly to the whole step."""
+def cpu_baseline(cfg, weights, cache, tree, P, warmup=2, steps=10):
+    """The fp32 numpy oracle of the same verify step (the CPU restatement:
+    every layer's tree block over the same KV prefix, the tied LM head and
+    argmax, the greedy walk and the KV compaction), timed on the host cores as
+    whole steps: `warmup` untimed steps, then the median of `steps` timed ones."""
     import numpy as np
 
     from oracle import qwen3 as oq
@@ -74,42 +75,44 @@ def cpu_baseline(cfg, weights, cache, tree, P, sample_layers=4, min_seconds=15.0
         cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:
         cores = os.cpu_count() or 1
+    t_setup = time.perf_counter()
     ocfg = oq.Qwen3Config(hidden=cfg.hidden_size, layers=cfg.num_hidden_layers, ffn=cfg.intermediate_size,
                           heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
                           vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_base=cfg.rope_theta)
     acc = weights.host_accessor()
     names = ("input_norm", "q", "k", "v", "q_norm", "k_norm", "o", "post_norm", "gate", "up", "down")
-    W = {(li, n): oq.bf16_to_f32(acc(li, n)) for li in range(sample_layers) for n in names}
+    W = {(li, n): oq.bf16_to_f32(acc(li, n)) for li in range(cfg.num_hidden_layers) for n in names}
+    W[(None, "embed")] = oq.bf16_to_f32(acc(None, "embed"))
+    W[(None, "final_norm")] = oq.bf16_to_f32(acc(None, "final_norm"))
     orc = oq.OracleQwen3(ocfg, lambda li, n: W[(li, n)])
     ids, pos, mask = otree.compile_tree(tree.tokens[0], P, tree.tokens[1:], tree.depths[1:], tree.visibility, P)
-    kp = [cache.logical_keys(li, P).float().cpu().numpy() for li in range(sample_layers)]
-    vp = [cache.logical_values(li, P).float().cpu().numpy() for li in range(sample_layers)]
-    x0 = oq.bf16_to_f32(acc(None, "embed")[ids])
-    per_layer = []
-    t_start = time.perf_counter()
-    while True:
-        x = x0
-        for li in range(sample_layers):
-            t0 = time.perf_counter()
-            x, _, _ = orc.layer_forward(li, x, kp[li], vp[li], pos, mask)
-            per_layer.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > min_seconds or len(per_layer) >= 400 * sample_layers:
-            break
-    E = acc(None, "embed")
-    q = E.shape[0] // 4
-    Eq = oq.bf16_to_f32(E[:q])
-    h = oq.rms_norm(x, np.ones(cfg.hidden_size, np.float32), cfg.rms_norm_eps)
-    lm_t = []
-    for _ in range(3):
+    kp = [cache.logical_keys(li, P).float().cpu().numpy() for li in range(cfg.num_hidden_layers)]
+    vp = [cache.logical_values(li, P).float().cpu().numpy() for li in range(cfg.num_hidden_layers)]
+    oc = oq.OracleCache(keys=kp, values=vp)
+    E = W[(None, "embed")]
+    t_setup = time.perf_counter() - t_setup
+
+    def step():
+        norm, vh, nk, nv = orc.forward_tree(ids, pos, mask, oc, [1, 9, 17, 25, 33])
+        post = np.argmax(norm @ E.T, axis=-1)
+        acc_idx, _ = otree.follow_verified_tree(tree.child_maps, post.tolist())
+        for li in range(cfg.num_hidden_layers):  # KV compaction: cache rows of the accepted path
+            np.concatenate([kp[li], nk[li][acc_idx]]), np.concatenate([vp[li], nv[li][acc_idx]])
+        return vh[acc_idx]
+
+    for _ in range(warmup):
+        step()
+    times = []
+    for _ in range(steps):
         t0 = time.perf_counter()
-        np.argmax(h @ Eq.T, axis=-1)
-        lm_t.append(time.perf_counter() - t0)
-    t_layer = float(np.median(per_layer))
-    t_step = t_layer * cfg.num_hidden_layers + float(np.median(lm_t)) * (E.shape[0] / q)
+        step()
+        times.append(time.perf_counter() - t0)
+    t_step = float(np.median(times))
     return {"value": 1.0 / t_step, "unit": "steps/s", "cores": int(cores), "kind": "port",
-            "sample": (f"fp32 numpy oracle: {sample_layers} of {cfg.num_hidden_layers} tree blocks x "
-                       f"{len(per_layer) // sample_layers} passes (median {t_layer * 1e3:.1f} ms/block) + 1/4 of "
-                       f"the LM head, scaled linearly to one step ({t_step:.2f} s)")}
+            "sample": (f"CPU restatement (fp32 numpy oracle of the whole verify step: {cfg.num_hidden_layers} tree "
+                       f"blocks, LM head + argmax, walk, KV compaction) on the same weights, prefix and tree; "
+                       f"{warmup} warm-up + median of {steps} whole steps ({t_step:.3f} s/step; setup "
+                       f"{t_setup:.0f} s)")}
 
 
 def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str = "bf16") -> dict:
@@ -418,6 +421,167 @@ def copy_probe(mib: int) -> None:
     log(f"[bench] copy probe: 5 x {mib} MiB")
 
 
+MODEL_NAMES = {"qwen3-4b": "Qwen3-4B", "qwen35-4b": "Qwen3.5-4B-shaped hybrid",
+               "qwen35-9b": "Qwen3.5-9B-shaped hybrid"}
+
+
+def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup: int, kernel_reps: int = 0,
+                 with_cpu: bool = False) -> dict:
+    """Builds the random-init model, prefills P tokens, builds the seeded tree
+    (acceptance pass at p = 0.85 on the device argmax) and times `steps`
+    verify steps (descriptor upload, graph replay, result read back) after
+    `warmup` untimed ones. Optionally times every kernel class and the CPU
+    restatement. Frees the model before returning."""
+    import torch
+
+    from dtree_hip import Qwen35TreeEngine, Qwen35Weights, Qwen3TreeModel, Qwen3Weights
+    from dtree_hip.config import QWEN3_4B, QWEN35_4B, QWEN35_9B
+    from dtree_hip.synthetic import acceptance_rewrite, make_tree, random_prefix
+
+    dev = torch.device("cuda:0")
+    hybrid = model.startswith("qwen35")
+    cfg = {"qwen3-4b": QWEN3_4B, "qwen35-4b": QWEN35_4B, "qwen35-9b": QWEN35_9B}[model]
+    max_nodes = budget + 1
+    t0 = time.time()
+    if hybrid:
+        w = Qwen35Weights.random(cfg, seed=0, device=dev, quant=quant)
+        eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 30], max_nodes=max_nodes)
+    else:
+        if quant == "q4":
+            w = Qwen3Weights.random_q4(cfg, seed=0, device=dev)
+        else:
+            w = Qwen3Weights.random(cfg, seed=0, device=dev)
+        eng = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33], max_nodes=max_nodes).engine
+    cache = eng.new_cache()
+    prefix = random_prefix(P, cfg.vocab_size, seed=1)
+    eng.prefill(cache, prefix)
+    torch.cuda.synchronize()
+    log(f"[bench] {model} {quant} P={P}: weights + prefill {time.time() - t0:.1f}s")
+    st = eng.stream_handle()
+    tree = make_tree(prefix[-1], cfg.vocab_size, budget=budget, depth=15, topk=4, seed=2)
+
+    def argmax_at(tr):
+        eng.set_step(tr.tokens, tr.positions(P), tr.parents, P)
+        eng.launch_forward(cache, st)
+        eng.launch_lm_head(st)
+        eng.launch_walk(st)
+        return eng.read_result().posterior
+
+    acceptance_rewrite(tree, argmax_at, p=0.85, seed=3)
+    L = tree.size
+    pos, par, toks = tree.positions(P), tree.parents, tree.tokens
+    log(f"[bench] tree L={L} max depth={max(tree.depths)}")
+    for _ in range(warmup):
+        res = eng.verify(cache, toks, pos, par, use_graph=True, commit=False)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup done, accepted={res.accepted}")
+    accepted_lens = []
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(steps):
+        res = eng.verify(cache, toks, pos, par, use_graph=True, commit=False)
+        accepted_lens.append(len(res.accepted))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ms = elapsed / steps * 1e3
+    ab = algorithmic_bytes35(cfg, P, L, quant) if hybrid else algorithmic_bytes(cfg, P, L, quant)
+    gbps = ab["total"] / (ms * 1e-3) / 1e9
+    mean_acc = sum(accepted_lens) / len(accepted_lens)
+    log(f"[bench] {model} {quant}: {ms:.3f} ms/step  {steps / elapsed:.1f} steps/s  {gbps:.0f} GB/s")
+    out = {"cfg": cfg, "P": P, "L": L, "ms": ms, "steps_per_s": steps / elapsed, "gbps": gbps,
+           "algorithmic_bytes": ab["total"], "mean_accepted": mean_acc, "accepted": res.accepted}
+    if kernel_reps:
+        out["kernels"] = (time_kernels35 if hybrid else time_kernels)(eng, cfg, w, cache, st, P, L, kernel_reps,
+                                                                      quant)
+    if with_cpu:
+        t0 = time.time()
+        out["cpu"] = (cpu_baseline35 if hybrid else cpu_baseline)(cfg, w, cache, tree, P)
+        log(f"[bench] cpu baseline {out['cpu']['value']:.3f} steps/s ({time.time() - t0:.1f}s)")
+    eng.release_graphs()
+    del eng, w, cache
+    import gc
+
+    gc.collect()
+    torch.cuda.empty_cache()
+    return out
+
+
+def attention_layer_bench(P: int = 512, sets: int = 128, reps: int = 1280) -> dict:
+    """One Qwen3-4B-shaped tree-attention layer (32 query / 8 KV heads,
+    head_dim 128, bf16 paged KV prefix of P positions ~ N(0, 0.5), 25-node
+    seeded tree), launched back to back over `sets` distinct layer-sized
+    buffer sets (their K/V prefixes together exceed the 256 MB MALL), timed
+    with HIP events on the launch stream."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from dtree_hip import _native as N
+    from dtree_hip.cache import PagedKVCache
+    from dtree_hip.engine import ancestor_bitsets
+    from dtree_hip.synthetic import make_tree
+
+    dev = torch.device("cuda:0")
+    lib = N.lib()
+    Hq, Hkv, D, MP = 32, 8, 128, 32
+    tree = make_tree(7, 151936, budget=24, depth=15, topk=4, seed=2)
+    L = tree.size
+    g = torch.Generator(device=dev).manual_seed(4)
+    cache = PagedKVCache(sets, Hkv, D, P + MP, device=dev)
+    cache.k_pages.normal_(0.0, 0.5, generator=g)
+    cache.v_pages.normal_(0.0, 0.5, generator=g)
+    qkv = torch.randn(sets, MP, (Hq + 2 * Hkv) * D, generator=g, device=dev)
+    qn = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    d = N.StepDesc()
+    d.past_length, d.num_nodes = P, L
+    anc = ancestor_bitsets(tree.parents)
+    for i in range(L):
+        d.tokens[i], d.positions[i], d.parents[i] = tree.tokens[i], tree.positions(P)[i], tree.parents[i]
+        for wd in range(N.MASK_WORDS):
+            d.ancestors[i][wd] = int(anc[i, wd])
+    N.check(lib.dtree_step_desc_validate(C.byref(d), MP, P, 151936), "attention bench descriptor")
+    desc = torch.frombuffer(bytearray(bytes(d)), dtype=torch.uint8).to(dev)
+    cos = torch.zeros(MP, D // 2, device=dev)
+    sin = torch.zeros(MP, D // 2, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    N.check(lib.dtree_rope_table(desc.data_ptr(), MP, D, 1e6, cos.data_ptr(), sin.data_ptr(), st), "rope table")
+    out = torch.zeros(2, MP, Hq * D, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(lib.dtree_attention_workspace_bytes(Hq, D, P, MP), dtype=torch.uint8, device=dev)
+    args = []
+    for s_ in range(sets):
+        a = N.AttnArgs()
+        a.qkv = qkv[s_].data_ptr(); a.ld_qkv = qkv.shape[-1]
+        a.q_norm = qn.data_ptr(); a.k_norm = qn.data_ptr(); a.eps = 1e-6
+        a.rope_cos = cos.data_ptr(); a.rope_sin = sin.data_ptr()
+        a.k_pages = cache.k_ptr(s_); a.v_pages = cache.v_ptr(s_); a.page_table = cache.page_table.data_ptr()
+        a.desc = desc.data_ptr()
+        a.out = out[0].data_ptr(); a.out_lo = out[1].data_ptr(); a.ld_out = Hq * D; a.out_layout = N.W_TILED
+        a.num_heads = Hq; a.num_kv_heads = Hkv; a.head_dim = D; a.rows_padded = MP; a.scale = D ** -0.5
+        a.max_past_length = P; a.write_cache = 0
+        a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+        args.append(a)
+    refs = [C.byref(a) for a in args]
+    for r in range(sets):
+        N.check(lib.dtree_tree_attention(refs[r], st), "attention")
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for r in range(reps):
+        lib.dtree_tree_attention(refs[r % sets], st)
+    e1.record()
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    # algorithmic bytes: Q (L x 32 heads x 128, bf16), K/V prefix + tree (P + L keys x 8 heads x 128 x 2),
+    # ancestor bitsets (4 B per node), output (L x 4096 bf16)
+    nbytes = L * Hq * D * 2 + 2 * Hkv * (P + L) * D * 2 + 4 * L + L * Hq * D * 2
+    del cache, qkv, out, ws
+    torch.cuda.empty_cache()
+    return {"workload": f"one Qwen3-4B tree-attention layer, prefix {P}, {L}-node tree, 32/8 heads, head_dim 128",
+            "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": int(nbytes),
+            "achieved_gbps": round(nbytes / (us * 1e-6) / 1e9, 1), "buffer_sets": sets, "launches": reps}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -432,6 +596,8 @@ def main():
                     help="q4: every linear layer and the tied LM head in 4-bit affine groups of 64 "
                          "(default bf16; q4 for qwen35-9b)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other workloads' lines (single attention layer, q4, Qwen3.5 hybrids)")
     ap.add_argument("--kernel-reps", type=int, default=108)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (the known-size kernel that scales the "
@@ -445,72 +611,17 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    import torch
-
-    from dtree_hip import Qwen35TreeEngine, Qwen35Weights, Qwen3TreeModel, Qwen3Weights
-    from dtree_hip.config import QWEN3_4B, QWEN35_4B, QWEN35_9B
-    from dtree_hip.synthetic import acceptance_rewrite, make_tree, random_prefix
-
-    dev = torch.device("cuda:0")
     hybrid = a.model.startswith("qwen35")
     big = a.model == "qwen35-9b"
-    cfg = {"qwen3-4b": QWEN3_4B, "qwen35-4b": QWEN35_4B, "qwen35-9b": QWEN35_9B}[a.model]
     P = a.prefix if a.prefix is not None else {"qwen3-4b": 1024, "qwen35-4b": 2048, "qwen35-9b": 8192}[a.model]
     if a.budget is None:
         a.budget = 64 if big else 24
     if a.quant is None:
         a.quant = "q4" if big else "bf16"
-    max_nodes = a.budget + 1
-    t0 = time.time()
-    if hybrid:
-        w = Qwen35Weights.random(cfg, seed=0, device=dev, quant=a.quant)
-        eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 30], max_nodes=max_nodes)
-    else:
-        if a.quant == "q4":
-            w = Qwen3Weights.random_q4(cfg, seed=0, device=dev)
-        else:
-            w = Qwen3Weights.random(cfg, seed=0, device=dev)
-        eng = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33], max_nodes=max_nodes).engine
-    cache = eng.new_cache()
-    prefix = random_prefix(P, cfg.vocab_size, seed=1)
-    eng.prefill(cache, prefix)
-    torch.cuda.synchronize()
-    log(f"[bench] weights + prefill {time.time() - t0:.1f}s")
-    st = eng.stream_handle()
-    tree = make_tree(prefix[-1], cfg.vocab_size, budget=a.budget, depth=15, topk=4, seed=2)
-
-    def argmax_at(tr):
-        eng.set_step(tr.tokens, tr.positions(P), tr.parents, P)
-        eng.launch_forward(cache, st)
-        eng.launch_lm_head(st)
-        eng.launch_walk(st)
-        return eng.read_result().posterior
-
-    acceptance_rewrite(tree, argmax_at, p=0.85, seed=3)
-    L = tree.size
-    pos, par, toks = tree.positions(P), tree.parents, tree.tokens
-    log(f"[bench] tree L={L} max depth={max(tree.depths)}")
-
-    for _ in range(a.warmup):
-        res = eng.verify(cache, toks, pos, par, use_graph=True, commit=False)
-    torch.cuda.synchronize()
-    log(f"[bench] warmup done, accepted={res.accepted}")
-
-    accepted_lens = []
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for _ in range(a.steps):
-        res = eng.verify(cache, toks, pos, par, use_graph=True, commit=False)
-        accepted_lens.append(len(res.accepted))
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t_start
-    ms = elapsed / a.steps * 1e3
-    steps_per_s = a.steps / elapsed
-    ab = algorithmic_bytes35(cfg, P, L, a.quant) if hybrid else algorithmic_bytes(cfg, P, L, a.quant)
-    gbps = ab["total"] / (ms * 1e-3) / 1e9
-    log(f"[bench] {ms:.3f} ms/step  {steps_per_s:.1f} steps/s  {gbps:.0f} GB/s")
-
-    kernels = (time_kernels35 if hybrid else time_kernels)(eng, cfg, w, cache, st, P, L, a.kernel_reps, a.quant)
+    r = run_workload(a.model, a.quant, P, a.budget, a.steps, a.warmup, kernel_reps=a.kernel_reps,
+                     with_cpu=not a.no_cpu_baseline)
+    cfg, L, ms, gbps = r["cfg"], r["L"], r["ms"], r["gbps"]
+    kernels = r["kernels"]
     for name, kd in kernels.items():
         log(f"[bench] {name:10s} {kd['avg_launch_us']:7.1f} us/launch x {kd['launches_per_step']:2d}  "
             f"{kd['achieved_gbps']:6.0f} GB/s  ({kd['kernel']})")
@@ -525,15 +636,25 @@ def main():
         except Exception:
             traffic = None
 
-    cpu = None
-    if not a.no_cpu_baseline:
+    configs = None
+    if not a.no_configs and a.model == "qwen3-4b" and a.quant == "bf16" and P == 1024 and a.budget == 24:
+        configs = {}
         t0 = time.time()
-        cpu = (cpu_baseline35 if hybrid else cpu_baseline)(cfg, w, cache, tree, P)
-        log(f"[bench] cpu baseline {cpu['value']:.3f} steps/s ({time.time() - t0:.1f}s)")
+        configs["attention_layer_p512"] = attention_layer_bench(P=512)
+        log(f"[bench] attention layer P=512: {configs['attention_layer_p512']}")
+        for key, (m, q, pp, bb) in {"qwen3_4b_q4_p1024": ("qwen3-4b", "q4", 1024, 24),
+                                    "qwen35_4b_bf16_p2048": ("qwen35-4b", "bf16", 2048, 24),
+                                    "qwen35_9b_q4_p8192_budget64": ("qwen35-9b", "q4", 8192, 64)}.items():
+            rr = run_workload(m, q, pp, bb, steps=30, warmup=5)
+            configs[key] = {"workload": f"{MODEL_NAMES[m]} {'bf16' if q == 'bf16' else 'q4 group-64'} tree-verify "
+                                        f"step, prefix {pp}, {rr['L']}-node tree",
+                            "ms_per_step": round(rr["ms"], 4), "steps_per_s": round(rr["steps_per_s"], 3),
+                            "hbm_gbps": round(rr["gbps"], 1), "hbm_frac_of_peak": round(rr["gbps"] / HBM_PEAK_GBPS, 4),
+                            "algorithmic_bytes_per_step": rr["algorithmic_bytes"],
+                            "mean_accepted": rr["mean_accepted"], "steps": 30}
+        log(f"[bench] other workloads {time.time() - t0:.1f}s")
 
-    mean_acc = sum(accepted_lens) / len(accepted_lens)
-    model_name = {"qwen3-4b": "Qwen3-4B", "qwen35-4b": "Qwen3.5-4B-shaped hybrid",
-                  "qwen35-9b": "Qwen3.5-9B-shaped hybrid"}[a.model]
+    model_name = MODEL_NAMES[a.model]
     qname = "bf16" if a.quant == "bf16" else "q4 group-64"
     if hybrid:
         workload = (f"{model_name} {qname} tree-verify step (24 GatedDeltaNet + 8 gated attention layers, "
@@ -542,7 +663,7 @@ def main():
         workload = f"{model_name} {qname} tree-verify step (36 layers, LM-head argmax, walk, compaction)"
     out = {
         "metric": f"tree-verify steps/s + HBM GB/s (% of peak), {a.budget}-node tree, {model_name} {qname}",
-        "value": round(steps_per_s, 3),
+        "value": round(r["steps_per_s"], 3),
         "unit": "steps/s",
         "n_gpus": 1,
         "steps": a.steps,
@@ -561,9 +682,9 @@ def main():
                    "layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size, "vocab": cfg.vocab_size},
         "hbm_gbps": round(gbps, 1),
         "hbm_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-        "algorithmic_bytes_per_step": ab["total"],
-        "tokens_per_s": round(steps_per_s * mean_acc, 2),
-        "mean_accepted": mean_acc,
+        "algorithmic_bytes_per_step": r["algorithmic_bytes"],
+        "tokens_per_s": round(r["steps_per_s"] * r["mean_accepted"], 2),
+        "mean_accepted": r["mean_accepted"],
         "roofline": {"kernel": f"{kd['kernel']} ({dom})", "bound": "hbm",
                      "achieved": round(kd["achieved_gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kd["achieved_gbps"] / HBM_PEAK_GBPS, 4), "traffic": traffic,
@@ -571,7 +692,8 @@ def main():
                      "algorithmic_bytes_per_launch": kd["algorithmic_bytes_per_launch"]},
         "kernels": {k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in kernels.items()},
-        "cpu_baseline": cpu,
+        "cpu_baseline": r.get("cpu"),
+        "configs": configs,
     }
     print(json.dumps(out), flush=True)
 

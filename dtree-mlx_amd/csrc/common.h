@@ -137,6 +137,12 @@ __device__ __forceinline__ void lane_argmax(float& v, int& i) {
   if constexpr (TN == 64) argmax_merge(v, i, __shfl_xor(v, 32), __shfl_xor(i, 32));
 }
 
+// Parent index of tree node t as a kernel may use it: parents precede their
+// children (dtree_runtime.py:125-130), so anything outside [0, t) (a tree the
+// host did not validate) is read as the root's parent -1, which keeps every
+// per-node access in bounds and every ancestor walk finite.
+__device__ __forceinline__ int valid_parent(int p, int t) { return (p >= 0 && p < t) ? p : -1; }
+
 // Row of 32x32 MFMA accumulator register r held by a lane in half h (= lane/32):
 // D[row][col] with col = lane % 32.
 __device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }

@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__
                                                        float* __restrict__ windows) {
   constexpr int keep = KEEP;
   __shared__ int par[kGdnMaxNodes];
-  for (int t = threadIdx.x; t < T; t += blockDim.x) par[t] = parents[t];
+  for (int t = threadIdx.x; t < T; t += blockDim.x) par[t] = valid_parent(parents[t], t);
   __syncthreads();
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void gdn_tree_kernel(GdnParams p) {
   float* vgb = qk + (size_t)T * 2 * DK;
   float* st = vgb + (size_t)T * (rpw + 2);
   const int nthr = blockDim.x;
-  for (int t = threadIdx.x; t < T; t += nthr) par[t] = p.parents[t];
+  for (int t = threadIdx.x; t < T; t += nthr) par[t] = valid_parent(p.parents[t], t);
   for (int e = threadIdx.x; e < T * 2 * DK; e += nthr) {
     const int t = e / (2 * DK), r = e % (2 * DK);
     const float* src = r < DK ? p.q : p.k;
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256) void gdn_tree_reg_kernel(GdnParams p) {
       else val = p.beta[(size_t)t * p.Hv + h];
       vgb[t][r] = val;
     }
-    if (tid < T) par[tid] = p.parents[tid];
+    if (tid < T) par[tid] = valid_parent(p.parents[tid], tid);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = tid + 256 * i, t = e >> 6, r = e & 63;
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
   __shared__ int par[kGdnMaxNodes];
   const int L = min(max(p.desc->num_nodes, 0), p.rows);
   const int tid = threadIdx.x;
-  for (int t = tid; t < L; t += DK) par[t] = p.desc->parents[t];
+  for (int t = tid; t < L; t += DK) par[t] = valid_parent(p.desc->parents[t], t);
   __syncthreads();
   const int nslices = p.C / DK;
   if ((int)blockIdx.x == nslices) {

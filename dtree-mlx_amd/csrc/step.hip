@@ -113,7 +113,7 @@ __global__ __launch_bounds__(kWalkThreads) void walk_kernel(DtreeStepDesc* desc,
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // The walk reads parents and tokens from LDS (one load per node here).
   for (int m = threadIdx.x; m < L; m += kWalkThreads) {
-    par_s[m] = desc->parents[m];
+    par_s[m] = valid_parent(desc->parents[m], m);
     tok_s[m] = desc->tokens[m];
   }
   // Candidates of one 32-row block are [blocks][32] pairs, 256 bytes per

@@ -18,6 +18,8 @@ MASK_WORDS = 4
 PAGE = 64
 ABI_VERSION = 4
 
+E_OK, E_ARG, E_HIP, E_TREE, E_WORKSPACE = 0, -1, -2, -3, -4
+
 EPI_STORE_F32 = 0
 EPI_RESIDUAL = 1
 EPI_SWIGLU = 2
@@ -113,6 +115,8 @@ SIGNATURES = {
     "dtree_last_error": (C.c_char_p, []),
     "dtree_abi_version": (C.c_int, []),
     "dtree_step_desc_bytes": (_sz, []),
+    "dtree_validate_parents": (C.c_int, [_vp, _i32]),
+    "dtree_step_desc_validate": (C.c_int, [_vp, _i32, _i32, _i32]),
     "dtree_gemm_args_bytes": (_sz, []),
     "dtree_attn_args_bytes": (_sz, []),
     "dtree_gemm_workspace_bytes": (_sz, [C.c_int, C.c_int, C.c_int, C.c_int]),

@@ -17,7 +17,7 @@ import torch
 
 from .cache import PagedKVCache, Qwen35Cache
 from .config import QWEN3_4B, QWEN35_4B, Qwen35Config, Qwen3Config
-from .engine import Qwen3TreeEngine
+from .engine import Qwen3TreeEngine, ancestor_bitsets
 from .qwen35_engine import Qwen35TreeEngine
 from .weights import Qwen35Weights, Qwen3Weights
 
@@ -252,9 +252,28 @@ class Qwen3TargetAdapter(MLXTargetAdapter):
     # ---- fused step (forward + LM-head argmax + walk + compaction) -----------
     def verify_tree(self, model: Qwen3TreeModel, inputs, cache: PagedKVCache, layer_ids, parents, position_ids,
                     attention_mask=None, child_maps=None):
+        """Forward + LM-head argmax + walk + compaction as one graph. The
+        device derives the ancestor masks from `parents` and walks the tree by
+        (parent, token); a given `attention_mask` / `child_maps` must describe
+        the same tree (the per-method path reads them instead), else ValueError."""
         eng = model.engine
         eng.set_layer_ids(layer_ids)
-        res = eng.verify(cache, _as_list(inputs), _as_list(position_ids), list(parents), use_graph=True)
+        toks, par = _as_list(inputs), [int(p) for p in parents]
+        L, P = len(toks), cache.offset
+        anc = ancestor_bitsets(par)
+        if attention_mask is not None:
+            mask = attention_mask.cpu().numpy() if isinstance(attention_mask, torch.Tensor) else np.asarray(attention_mask)
+            if not np.array_equal(_mask_tree_bitsets(mask.astype(bool), P, L), anc):
+                raise ValueError("attention_mask tree columns differ from the ancestor sets of `parents`")
+        if child_maps is not None:
+            if len(child_maps) != L:
+                raise ValueError(f"child_maps has {len(child_maps)} entries for {L} nodes")
+            expect: list[dict[int, int]] = [dict() for _ in range(L)]
+            for i in range(1, L):
+                expect[par[i]][toks[i]] = i
+            if [dict(m) for m in child_maps] != expect:
+                raise ValueError("child_maps differ from the (parent, token) children of the tree")
+        res = eng.verify(cache, toks, _as_list(position_ids), par, use_graph=True)
         n = len(res.accepted)
         vh = eng.hidden_sel[:n].clone()[None] if layer_ids else None
         return res.accepted, res.bonus_token, vh

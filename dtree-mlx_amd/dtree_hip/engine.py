@@ -16,6 +16,7 @@ so it can be captured once into a HIP graph and replayed for every step.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -167,6 +168,7 @@ class TreeEngineBase:
         self.result_host = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32).pin_memory()
         self._result_np = self.result_host.numpy()
         self._graphs: dict = {}
+        self._dead_graphs: list = []
 
     def _alloc_layer_buffers(self) -> None:
         raise NotImplementedError
@@ -362,11 +364,33 @@ class TreeEngineBase:
             cache.offset = P + len(part)
 
     # ---- HIP graph of the verify step ------------------------------------------
+    # A captured graph holds the raw device pointers of one cache (K/V pages,
+    # page table), so it is only ever replayed for that cache object: entries
+    # are keyed by id() and hold a weak reference that is checked on lookup
+    # (a new cache may reuse a dead one's id). When a cache dies its graph is
+    # queued and destroyed at the next launch, after the stream has drained
+    # (the finalizer itself may run at any point, e.g. during another capture).
+    def _graph_for(self, cache: PagedKVCache) -> int:
+        self._destroy_pending()
+        ent = self._graphs.get(id(cache))
+        if ent is not None:
+            ref, g = ent
+            if ref() is cache:
+                return g
+            self._graphs.pop(id(cache))
+            self._dead_graphs.append(g)
+            self._destroy_pending()
+        return self.capture_verify(cache)
+
+    def _destroy_pending(self) -> None:
+        if not self._dead_graphs:
+            return
+        torch.cuda.synchronize(self.dev)
+        while self._dead_graphs:
+            self.lib.dtree_graph_destroy(C.c_void_p(self._dead_graphs.pop()))
+
     def graph_launch(self, cache: PagedKVCache, st: int) -> None:
-        key = id(cache)
-        g = self._graphs.get(key)
-        if g is None:
-            g = self.capture_verify(cache)
+        g = self._graph_for(cache)
         N.check(self.lib.dtree_graph_launch(C.c_void_p(g), st), "graph launch")
 
     def capture_verify(self, cache: PagedKVCache) -> int:
@@ -383,13 +407,21 @@ class TreeEngineBase:
         ex = C.c_void_p()
         N.check(self.lib.dtree_graph_end(h, C.byref(ex)), "graph end")
         torch.cuda.current_stream().wait_stream(side)
-        self._graphs[id(cache)] = ex.value
+        key, graphs, dead = id(cache), self._graphs, self._dead_graphs
+
+        def on_cache_dead(_ref, key=key, graphs=graphs, dead=dead):
+            ent = graphs.get(key)
+            if ent is not None and ent[0] is _ref:
+                graphs.pop(key)
+                dead.append(ent[1])
+
+        self._graphs[key] = (weakref.ref(cache, on_cache_dead), ex.value)
         return ex.value
 
     def release_graphs(self) -> None:
-        for g in self._graphs.values():
-            self.lib.dtree_graph_destroy(C.c_void_p(g))
+        self._dead_graphs.extend(g for _, g in self._graphs.values())
         self._graphs.clear()
+        self._destroy_pending()
 
     def __del__(self):
         try:

@@ -132,6 +132,27 @@ typedef struct DtreeGemmArgs {
 const char* dtree_last_error(void);
 int dtree_abi_version(void);
 size_t dtree_step_desc_bytes(void);
+
+/*
+ * Host-side tree validation (host pointers; no device work). The kernels read
+ * trees from device memory and cannot report a malformed one synchronously:
+ * they only read a parent outside [0, i) as -1, which keeps every access in
+ * bounds, so a binder validates before the upload.
+ *
+ * dtree_validate_parents: parents[0] == -1 and 0 <= parents[i] < i (node
+ * order = heap-pop order, dtree_runtime.py:125-130), 1 <= num_nodes <= 128;
+ * else DTREE_E_TREE. Guards the raw-parent entries dtree_gdn_tree_conv and
+ * dtree_gdn_tree_recurrence.
+ * dtree_step_desc_validate: the input half of a DtreeStepDesc as
+ * compile_dtree_tree (dtree_runtime.py:166-192) produces it: 1 <= num_nodes
+ * <= max_nodes, 0 <= past_length <= max_past_length, topological parents,
+ * every ancestors[i] = ancestors[parents[i]] | bit i (bit 0 for the root),
+ * tokens in [0, vocab_size), positions >= 0, accepted[0 .. n_accepted) in
+ * [0, num_nodes). DTREE_E_TREE for the tree shape, DTREE_E_ARG otherwise.
+ */
+int dtree_validate_parents(const int32_t* parents, int32_t num_nodes);
+int dtree_step_desc_validate(const DtreeStepDesc* desc, int32_t max_nodes, int32_t max_past_length,
+                             int32_t vocab_size);
 /* sizeof(DtreeGemmArgs) / sizeof(DtreeAttnArgs): lets bindings check their
  * mirrored struct layouts. */
 size_t dtree_gemm_args_bytes(void);

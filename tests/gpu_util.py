@@ -65,3 +65,29 @@ def random_tree(L: int, seed: int) -> list[int]:
 
 def stream() -> int:
     return torch.cuda.current_stream().cuda_stream
+
+
+def compare_accepted_path(res, child_maps, oracle_post, decided, log=print) -> int:
+    """Accepted path of the device walk against the oracle's walk over the
+    oracle's own argmax (follow_verified_tree, dtree_runtime.py:195-208).
+
+    ``decided[i]`` says row i's argmax is pinned (its oracle top-2 margin
+    clears the logit tolerance). Both walks visit the same nodes up to and
+    including the first walked node whose row is not decided; past it the
+    device may legitimately take another branch. Asserts equality on that
+    prefix (and of the bonus token when the whole oracle path is decided) and
+    returns how many path nodes were compared."""
+    from oracle import tree as otree
+
+    o_acc, o_bonus = otree.follow_verified_tree(child_maps, [int(t) for t in oracle_post])
+    k = next((j for j, i in enumerate(o_acc) if not decided[i]), None)
+    if k is None:
+        assert res.accepted == o_acc and res.bonus_token == o_bonus, (res.accepted, o_acc)
+        compared = len(o_acc)
+    else:
+        assert res.accepted[:k + 1] == o_acc[:k + 1], (res.accepted, o_acc, k)
+        compared = k + 1
+    log(f"accepted path: device {res.accepted} bonus {res.bonus_token}; oracle {o_acc} bonus {o_bonus}; "
+        f"compared {compared} of {len(o_acc)} nodes" + ("" if k is None else f" (node {o_acc[k]} undecided)"))
+    assert compared >= 1
+    return compared

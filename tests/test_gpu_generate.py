@@ -149,3 +149,35 @@ def test_dtree_generate_emits_greedy_tokens(gpu_device, monkeypatch, family, ver
     acc = metrics["acceptance_lengths"]
     assert max(acc) >= 5 and min(acc) == 1, acc
     assert target.model.args.model_type == target.adapter.family
+
+
+def test_dtree_generate_twice_on_one_model(gpu_device, monkeypatch):
+    """Two decode calls on one resident model: each builds its own cache, and
+    the captured verify graph (which holds one cache's page pointers) must be
+    replayed only for the cache it was captured for, even when the second
+    cache reuses the first one's id after it is freed. Both runs must emit the
+    oracle's greedy continuation."""
+    import gc
+
+    monkeypatch.delenv("DTREE_QWEN35_TREE_MODE", raising=False)
+    cfg = tiny_qwen3()
+    target = load_target_model(cfg, seed=0, max_past=256, device="cuda", layer_ids=[0, 1])
+    rng = np.random.default_rng(11)
+    for run in range(2):
+        prompt = rng.integers(1, cfg.vocab_size, 30 + 7 * run).tolist()
+        n_new = 24
+        plan = _gpu_sequential_greedy(target, prompt, n_new)
+        drafter = ScriptedDrafter(target, prompt + plan)
+        out, metrics = dtree_generate(target, drafter, prompt, max_new_tokens=n_new, temperature=0.0,
+                                      stop_token_ids=set(), layer_ids=[0, 1], speculative_tokens=BLOCK,
+                                      tree_budget=12, verify_mode="parallel-greedy-argmax", tree_topk=4)
+        gc.collect()  # the first run's cache dies here; its graph is queued for destruction
+        gen = out[len(prompt):]
+        assert len(gen) == n_new
+        logits = _oracle_teacher_forced(target, out[:-1])[len(prompt) - 1:]
+        scale = np.abs(logits).max(axis=-1)
+        chosen = logits[np.arange(n_new), gen]
+        assert np.all(chosen >= logits.max(axis=-1) - TOL * scale), f"run {run}"
+        assert np.mean(np.argmax(logits, axis=-1) == np.asarray(gen)) >= 0.9, f"run {run}"
+    eng = target.model.engine
+    assert len(eng._graphs) <= 1

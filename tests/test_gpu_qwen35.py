@@ -10,8 +10,8 @@ checked against the oracle's chain commit separately.
 
 Bars: logits within 2e-2 relative (max |diff| per row <= 2e-2 x max |oracle
 logit| of that row); argmax tokens bit-exact on rows whose oracle top-2
-margin exceeds that tolerance; accepted path bit-exact when every row the
-walk reads has such a margin; compacted attention cache = the pre-compaction
+margin exceeds that tolerance; accepted path bit-exact up to and including the
+first walked node without such a margin; compacted attention cache = the pre-compaction
 rows gathered at the accepted indices, bit for bit; committed windows and
 states within 2e-2 of the oracle's commit along the device's accepted path."""
 import time
@@ -27,7 +27,7 @@ from oracle import qwen35 as o35
 from oracle import tree as otree
 from oracle.qwen3 import bf16_to_f32
 
-from gpu_util import bf16_f32
+from gpu_util import bf16_f32, compare_accepted_path
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
@@ -138,9 +138,7 @@ def _check(r, layer_ids, min_confident=0.5):
     assert np.array_equal(post[confident], o_post[confident])
     assert np.array_equal(post[sure], o_post[sure])
     assert confident.mean() >= min_confident and sure.mean() > 0.5
-    o_acc, o_bonus = otree.follow_verified_tree(tree.child_maps, o_post.tolist())
-    if all(confident[i] or sure[i] for i in o_acc):
-        assert res.accepted == o_acc and res.bonus_token == o_bonus
+    r["path_compared"] = compare_accepted_path(res, tree.child_maps, o_post, confident | sure)
     acc2, bonus2 = otree.follow_verified_tree(tree.child_maps, res.posterior)
     assert res.accepted == acc2 and res.bonus_token == bonus2
     cache, n = r["cache"], len(res.accepted)

@@ -4,8 +4,9 @@ and tree.
 
 Bars (north-star): logits within 2e-2 relative (max |diff| per row <= 2e-2 x
 max |oracle logit| of that row); argmax tokens bit-exact on rows whose oracle
-top-2 margin exceeds that tolerance; accepted path bit-exact when every row
-the walk reads has such a margin; compacted cache = the pre-compaction rows
+top-2 margin exceeds that tolerance; accepted path bit-exact up to and
+including the first walked node without such a margin (the whole path and
+the bonus token when every walked row has one); compacted cache = the pre-compaction rows
 gathered at the accepted indices, bit for bit."""
 import time
 
@@ -19,7 +20,7 @@ from dtree_hip.synthetic import acceptance_rewrite, make_tree, random_prefix
 from oracle import qwen3 as oq
 from oracle import tree as otree
 
-from gpu_util import bf16_f32
+from gpu_util import bf16_f32, compare_accepted_path
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
@@ -31,7 +32,26 @@ def _oracle_cfg(cfg):
                           vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_base=cfg.rope_theta)
 
 
-def _run(cfg, P, layer_ids, dev, norm_jitter=0.0, log=print, quant="bf16"):
+def _check_prefill(orc, cfg, prefix, prefix_k, prefix_v, layers, log=print):
+    """The device prefill's cache rows (32-row chained tree passes through the
+    same kernels, paged) against the oracle's causal forward over the prefix:
+    K and V of the first `layers` layers at every position."""
+    t0 = time.time()
+    P = len(prefix)
+    x = orc.embed(np.asarray(prefix, np.int64))
+    pos = np.arange(P)
+    causal = np.tril(np.ones((P, P), bool))
+    empty = np.zeros((0, cfg.num_key_value_heads, cfg.head_dim), np.float32)
+    for li in range(layers):
+        x, k, v = orc.layer_forward(li, x, empty, empty, pos, causal)
+        for got, want, what in ((prefix_k[li], k, "keys"), (prefix_v[li], v, "values")):
+            err = np.abs(got - want).max(axis=(1, 2))
+            bar = TOL * np.maximum(1.0, np.abs(want).max(axis=(1, 2)))
+            assert np.all(err <= bar), f"prefill {what} layer {li}: worst position {int(np.argmax(err / bar))}"
+    log(f"prefill K/V of {layers} layers at {P} positions match the oracle ({time.time() - t0:.1f}s)")
+
+
+def _run(cfg, P, layer_ids, dev, norm_jitter=0.0, log=print, quant="bf16", check_prefill_layers=0):
     t0 = time.time()
     if quant == "q4":  # every linear layer and the tied embedding in 4-bit groups of 64
         w = Qwen3Weights.random_q4(cfg, seed=0, device=dev, norm_jitter=norm_jitter)
@@ -76,6 +96,8 @@ def _run(cfg, P, layer_ids, dev, norm_jitter=0.0, log=print, quant="bf16"):
     # oracle on the same weights / prefix / tree
     t1 = time.time()
     orc = oq.OracleQwen3(_oracle_cfg(cfg), w.host_accessor())
+    if check_prefill_layers:
+        _check_prefill(orc, cfg, prefix, prefix_k, prefix_v, check_prefill_layers, log)
     oc = oq.OracleCache(keys=prefix_k, values=prefix_v)
     ids, pos, mask = otree.compile_tree(tree.tokens[0], P, tree.tokens[1:], tree.depths[1:], tree.visibility, P)
     norm, vh, nk, nv = orc.forward_tree(ids, pos, mask, oc, layer_ids)
@@ -99,9 +121,7 @@ def _check(r, layer_ids):
     post = np.array(res.posterior)
     assert np.array_equal(post[confident], o_post[confident])
     assert confident.mean() > 0.5
-    o_acc, o_bonus = otree.follow_verified_tree(tree.child_maps, o_post.tolist())
-    if all(confident[i] for i in o_acc):
-        assert res.accepted == o_acc and res.bonus_token == o_bonus
+    r["path_compared"] = compare_accepted_path(res, tree.child_maps, o_post, confident)
     # device walk == host walk on the device's own posterior
     acc2, bonus2 = otree.follow_verified_tree(tree.child_maps, res.posterior)
     assert res.accepted == acc2 and res.bonus_token == bonus2
@@ -125,7 +145,7 @@ def _check(r, layer_ids):
 
 def test_verify_step_tiny_model(gpu_device):
     cfg = tiny_qwen3()
-    r = _run(cfg, P=100, layer_ids=[0, 1], dev=gpu_device, norm_jitter=0.1)
+    r = _run(cfg, P=100, layer_ids=[0, 1], dev=gpu_device, norm_jitter=0.1, check_prefill_layers=2)
     res = _check(r, [0, 1])
     assert len(res.accepted) >= 1
 
@@ -161,7 +181,7 @@ def test_verify_step_graph_replays_match_eager(gpu_device):
 
 def test_verify_step_qwen3_4b_prefix_1024(gpu_device):
     """Full-size verify step: 36 layers, hidden 2560, vocab 151936, P=1024, 25 nodes."""
-    r = _run(QWEN3_4B, P=1024, layer_ids=[1, 9, 17, 25, 33], dev=gpu_device)
+    r = _run(QWEN3_4B, P=1024, layer_ids=[1, 9, 17, 25, 33], dev=gpu_device, check_prefill_layers=3)
     res = _check(r, [1, 9, 17, 25, 33])
     print("accepted", res.accepted, "bonus", res.bonus_token)
 

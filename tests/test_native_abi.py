@@ -108,3 +108,52 @@ def test_attention_and_gdn_layer_validation_without_gpu():
     g.ld_proj = 8192 + 4096  # b and a columns missing
     assert lib.dtree_gdn_layer_prep(C.byref(g), None) == -1
     assert b"ld_proj" in lib.dtree_last_error()
+
+
+def _desc(parents, tokens=None, P=10):
+    from dtree_hip import _native as N
+    from dtree_hip.engine import ancestor_bitsets
+
+    d = N.StepDesc()
+    L = len(parents)
+    d.past_length, d.num_nodes = P, L
+    anc = ancestor_bitsets(parents)
+    for i in range(L):
+        d.parents[i] = parents[i]
+        d.tokens[i] = (tokens or [3] * L)[i]
+        d.positions[i] = P + i
+        for w in range(N.MASK_WORDS):
+            d.ancestors[i][w] = int(anc[i, w])
+    return d
+
+
+def test_host_tree_validation():
+    """dtree_validate_parents / dtree_step_desc_validate (host only, no device
+    work): DTREE_E_TREE for non-topological parents, a wrong root, more nodes
+    than allowed or ancestor sets that are not the parent's plus the node;
+    DTREE_E_ARG for out-of-range tokens, past lengths and accepted indices."""
+    import ctypes as C
+
+    from dtree_hip import _native as N
+
+    lib = N.lib()
+    ok = (C.c_int32 * 5)(-1, 0, 0, 1, 2)
+    assert lib.dtree_validate_parents(ok, 5) == 0
+    for bad in ((0, 0, 0), (-1, 1, 0), (-1, 0, 2), (-1, -1, 0)):
+        arr = (C.c_int32 * 3)(*bad)
+        assert lib.dtree_validate_parents(arr, 3) == N.E_TREE, bad
+    assert lib.dtree_validate_parents(ok, 0) == N.E_TREE
+    d = _desc([-1, 0, 0, 1, 2])
+    assert lib.dtree_step_desc_validate(C.byref(d), 32, 100, 50) == 0
+    assert lib.dtree_step_desc_validate(C.byref(d), 4, 100, 50) == N.E_TREE      # more nodes than max_nodes
+    assert lib.dtree_step_desc_validate(C.byref(d), 32, 5, 50) == N.E_ARG        # past_length > max_past
+    d.ancestors[3][0] = 0b1001                                                    # node 3 without its parent 1
+    assert lib.dtree_step_desc_validate(C.byref(d), 32, 100, 50) == N.E_TREE
+    assert b"ancestors[3]" in lib.dtree_last_error()
+    d = _desc([-1, 0, 0], tokens=[1, 2, 50])
+    assert lib.dtree_step_desc_validate(C.byref(d), 32, 100, 50) == N.E_ARG
+    d = _desc([-1, 0, 0])
+    d.n_accepted, d.accepted[0], d.accepted[1] = 2, 0, 3
+    assert lib.dtree_step_desc_validate(C.byref(d), 32, 100, 50) == N.E_ARG
+    d.accepted[1] = 2
+    assert lib.dtree_step_desc_validate(C.byref(d), 32, 100, 50) == 0

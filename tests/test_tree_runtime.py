@@ -157,3 +157,31 @@ def test_qwen35_compaction_requires_pending_tree_state():
     ad._pending_tree_state = (5, 3, [-1, 0, 0])
     with pytest.raises(ValueError, match="root path"):
         ad.compact_kv_caches(None, None, past_length=5, keep_current_indices=[0, 1, 2])
+
+
+def test_dflash_prefix_match_and_chain_inputs():
+    """runtime.py:32-38 longest_prefix_match and the chain-shaped verify
+    inputs of the linear decode: parents -1, 0, 1, ..; positions start + i;
+    every prefix column visible, causal over the block."""
+    from dtree_hip.runtime import _chain_inputs, longest_prefix_match
+
+    assert longest_prefix_match([1, 2, 3], [1, 2, 4]) == 2
+    assert longest_prefix_match([1, 2], [1, 2, 3]) == 2
+    assert longest_prefix_match([5], [4]) == 0
+    assert longest_prefix_match([], [1]) == 0
+    ids, pos, parents, mask = _chain_inputs([9, 8, 7, 6], start=5)
+    assert ids.tolist() == [[9, 8, 7, 6]] and pos.tolist() == [[5, 6, 7, 8]]
+    assert parents == [-1, 0, 1, 2]
+    assert mask.shape == (4, 9) and bool(mask[:, :5].all())
+    for i in range(4):
+        for j in range(4):
+            assert bool(mask[i, 5 + j]) == (j <= i)
+
+
+def test_generator_rejects_unsupported_quantisation():
+    from dtree_hip.api import DFlashGenerator
+
+    with pytest.raises(NotImplementedError):
+        DFlashGenerator(target_model="random:qwen3-4b", target_quant_bits=8)
+    with pytest.raises(NotImplementedError):
+        DFlashGenerator(target_model="random:qwen3-4b", target_quant_bits=4, target_quant_group_size=32)
