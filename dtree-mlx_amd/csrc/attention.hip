@@ -1,47 +1,64 @@
-// Ancestor-masked GQA tree attention over a paged bf16 KV prefix.
+// Ancestor-masked GQA tree attention over a paged bf16 KV prefix, one
+// workgroup per (KV group, 32-row query block, key split).
 //
-// Work split: a workgroup serves one 32-row block of tree queries (rows
-// 32*rb .. 32*rb+31) of one query head. The keys are cut into chunks: chunks
-// 0 .. NT-1 are the tree itself in 32-key blocks (NT = rows_padded / 32;
-// ancestor-or-self mask, word tc of each query's bitset), chunks NT.. are runs
-// of CK prefix keys (fully visible): a 64-key page for head_dim 128, half a
-// page for head_dim 256 (same registers per wave). A workgroup has four
-// waves, one chunk each, so workgroup `split` owns chunks 4*split .. 4*split+3.
+// Work split
+//   * A KV group's G query heads read the same keys (GQA h -> h / G,
+//     qwen3_tree.py:69-76), so a workgroup owns one KV group: G waves, wave w
+//     computing query head g*G + w. Each K/V chunk is loaded from HBM once
+//     per workgroup into LDS and read by the G waves' MFMAs (for the Qwen3-4B
+//     step: 25 tree rows x 4 heads per chunk).
+//   * Keys are cut into chunks: 64-key prefix pages at head_dim 128 (32 keys,
+//     half a page, at 256), and 32-key tree chunks (tree chunk t = nodes
+//     32t .. 32t+31, masked with word t of each query's ancestor bitset).
+//     Split 0 of a (group, query block) takes the tree chunks 0 .. rb (later
+//     tree chunks hold no ancestor of a row of block rb); split s >= 1 takes
+//     the prefix chunks (s-1)*cps .. s*cps - 1 below P. The mapping depends on
+//     the grid only, so the first chunk's loads go out before the step
+//     descriptor (which holds P and L, so one grid serves every step up to
+//     max_past_length) is read; chunks run through two LDS buffers, the next
+//     chunk's loads in flight while the current one is multiplied, each wave
+//     keeping an online softmax.
+//   * Every split publishes one partial per head (unnormalised output, row
+//     max, row sum). The S workgroups of a (group, query block) then meet at
+//     a device-scope counter (all of them are resident: the grid never holds
+//     more workgroups than the GPU has CUs) and share the combine: unit
+//     (head, 32-dim block) u goes to workgroup u mod S, whose waves read the
+//     splits' 4 KB slices of that unit, merge them in LDS in wave order
+//     (deterministic) and write the output rows (normalised, optionally
+//     gated, as a bf16 hi / lo pair). The counter's second phase returns it
+//     to zero for the next launch. The wait is bounded: a workgroup that
+//     gives up sets the workspace's error word instead of hanging.
 //
-// Two head geometries are compiled: Qwen3 (head_dim 128, full RoPE) and the
-// gated attention of Qwen3.5 (head_dim 256, RoPE on the first 64 dims, q_proj
-// rows per head = [q | gate], output multiplied by sigmoid(gate)).
-// A wave owns exactly one chunk, so its softmax needs no running rescale: it
-// issues Q's loads, then all K and V of its page (32 KB in flight per wave),
-// scores both 32-key blocks, takes one max and accumulates P V.
-// The four waves merge in LDS; when a head needs more than one workgroup,
-// each writes a merged partial (row max, row sum, unnormalised output) and the
-// last one to arrive (device-scope counter) combines them, all 256 threads
-// with independent loads. The heads of one KV group run on one XCD
-// (blockIdx % 8), so their shared K/V reads meet in one L2.
-//
-// MFMA use (v_mfma_f32_32x32x16_bf16), with the tree rows (<= 32) as one
-// MFMA dimension:
-//   S^T = K Q^T : A = 32 keys x 16 dims, B = 16 dims x 32 queries. A lane owns
-//                 query column lane%32, so softmax statistics are lane-local
-//                 (16 registers + one exchange with lane^32).
-//   O^T = V^T P^T: A = V^T (32 dims x 16 keys), B = P^T taken straight from
-//                 the S^T registers. A-row rho of S^T is loaded from key
-//                 pi(rho) = rho with bits 2 and 3 swapped; then register r of
-//                 a lane in half h holds key 16*(r/8) + 8*h + r%8, i.e. eight
-//                 consecutive keys per PV step, which is one 16-byte read of
-//                 the transposed V page.
+// MFMA use (v_mfma_f32_32x32x16_f16, fp32 accumulate), tree rows as the
+// 32-wide B dimension. The cached bf16 K and V convert exactly to fp16 (fp16
+// keeps more significand bits; magnitudes above 65504 saturate), and q and the
+// probabilities round to fp16 (11 significant bits, against bf16's 8):
+//   S^T = K Q^T : A = 32 keys x 16 dims (LDS), B = 16 dims x 32 queries
+//                 (registers), so each lane owns one query column and its
+//                 softmax statistics stay lane-local (plus one exchange with
+//                 lane ^ 32).
+//   O^T = V^T P^T: A = V^T (32 dims x 16 keys, LDS), B = P^T straight from the
+//                 S^T registers: A-row rho of S^T is loaded from key rho with
+//                 bits 2 and 3 swapped, so register r of a lane in half h
+//                 holds key 16*(r/8) + 8*h + r%8, eight consecutive keys per
+//                 PV step.
 // K pages are [page][kv_head][64][D]; V pages are [page][kv_head][D][64].
+#include <cstdlib>
+
 #include "common.h"
 
 namespace dtree {
 
-constexpr int kWaves = 4;          // waves (chunks) per workgroup
-constexpr int kMaxPast = 16384;    // longest prefix the grid is sized for
-// Prefix keys per chunk.
+constexpr int kMaxPast = 16384;  // longest prefix the grid is sized for
 __host__ __device__ constexpr int chunk_keys(int D) { return D <= 128 ? DTREE_PAGE : DTREE_PAGE / 2; }
 constexpr float kNeg = -1e30f;
 constexpr float kLog2e = 1.4426950408889634f;
+// Workspace header: error word (bytes 0..3), then one counter per (group,
+// query block) from byte 64.
+constexpr int kWsHeader = 4096;
+constexpr int kMaxPairs = (kWsHeader - 64) / 4;
+constexpr int kSpinLimit = 1 << 21;  // counter polls (~1 us each) before a workgroup gives up
+constexpr int kCombineBatch = 4;     // split slices in flight per wave in the combine
 
 struct AttnParams {
   const float* qkv; int ld_qkv;
@@ -51,66 +68,83 @@ struct AttnParams {
   uint16_t* kp; uint16_t* vp; const int* page_table;
   const DtreeStepDesc* desc;
   uint16_t* out; uint16_t* out_lo; int ld_out; int out_tiled;
-  int Hq, Hkv, max_chunks, splits;
-  int tree_chunks;  // 32-key tree chunks = 32-row query blocks = rows_padded / 32
+  int Hq, Hkv, NT;       // NT: 32-row query blocks = 32-key tree chunks
+  int S, max_pchunks;    // splits per (group, query block); prefix chunks the grid is sized for
+  int cps;               // prefix chunks per split
+  int max_past;          // longest prefix the cache and page table hold
   float scale_log2;
   int write_cache;
-  float* part; int* counters;
-  int sep_combine;  // partials are combined by attn_combine_kernel (long prefixes)
-  int off_xcd;      // test hook: treat every workgroup as off its expected XCD
+  float* part; int* counters; int* err;
+  int off_xcd;  // test hook: treat every workgroup as off its expected XCD
 };
 
 __device__ __forceinline__ int swap_bits23(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
 
 // Raw operands of one head row for lane (c, h), which owns dims 16j + 8h + i:
 // the fp32 values, the bf16 RMSNorm weights and the RoPE cos/sin of the first
-// half of the R rotated dims. Issuing all loads before any use lets a wave
-// keep them in flight together with the K/V loads that follow.
+// half of the R rotated dims, all loads issued before any use.
 template <int D, int R>
 struct HeadRow {
   f32x4_t x[D / 16][2];
-  u32x4_t nw[D / 16];
-  f32x4_t cs[R / 32][2], sn[R / 32][2];
 };
 
-// AUX: also the norm weights and the RoPE cos/sin (q and k rows; v has
-// none). Without norm weights the loads read the row itself instead and
-// row_finish ignores them, so the loads never branch: the whole prologue
-// stays one basic block and its loads go out in one round trip.
-template <int D, int R, bool AUX>
-__device__ __forceinline__ void row_issue(HeadRow<D, R>& r, const float* src, const uint16_t* norm_w, const float* cosr,
-                                          const float* sinr, int h) {
-  const uint16_t* nwp = norm_w ? norm_w : reinterpret_cast<const uint16_t*>(src);
+// The block's 32 RoPE table rows (cos then sin, R/2 each) and the q_norm
+// weight, loaded once per workgroup and shared by its waves through LDS
+// (the waves' query heads use the same positions and weight).
+template <int D, int R, int NT_>
+struct QAux {
+  static constexpr int kRope = 32 * (R / 2) * 2;  // floats
+  static constexpr int kPieces = kRope / 4;       // 16-byte pieces
+  static constexpr int PT = (kPieces + NT_ - 1) / NT_;
+  static constexpr int kBytes = kRope * 4 + D * 2;
+  f32x4_t r[PT];
+  u32x4_t nw;
+
+  __device__ __forceinline__ void issue(const AttnParams& p, int rb, int t) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int e = t + i * NT_;
+      if (e < kPieces) {
+        const int half = e / (kPieces / 2), o = e % (kPieces / 2);  // cos rows, then sin rows
+        r[i] = *reinterpret_cast<const f32x4_t*>((half ? p.rope_sin : p.rope_cos) + 32 * rb * (R / 2) + 4 * o);
+      }
+    }
+    if (t < D / 8) nw = p.q_norm ? ld_u32x4(p.q_norm + 8 * t) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  __device__ __forceinline__ void commit(unsigned char* lds, int t) const {
+    f32x4_t* ro = reinterpret_cast<f32x4_t*>(lds);
+#pragma unroll
+    for (int i = 0; i < PT; ++i)
+      if (t + i * NT_ < kPieces) ro[t + i * NT_] = r[i];
+    if (t < D / 8) reinterpret_cast<u32x4_t*>(lds + kRope * 4)[t] = nw;
+  }
+};
+
+template <int D, int R>
+__device__ __forceinline__ void row_issue(HeadRow<D, R>& r, const float* src, int h) {
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) {
     r.x[j][0] = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h);
     r.x[j][1] = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h + 4);
-    if constexpr (AUX) r.nw[j] = ld_u32x4(nwp + 16 * j + 8 * h);
-  }
-  if constexpr (AUX) {
-#pragma unroll
-    for (int j = 0; j < R / 32; ++j)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        r.cs[j][u] = *reinterpret_cast<const f32x4_t*>(cosr + 16 * j + 8 * h + 4 * u);
-        r.sn[j][u] = *reinterpret_cast<const f32x4_t*>(sinr + 16 * j + 8 * h + 4 * u);
-      }
   }
 }
 
-// RMSNorm over D (sum of squares completed with the partner lane^32), then
-// RoPE on (dim d, dim d + R/2) pairs for d < R/2, which live in the same lane
-// (registers j and j + R/32); dims >= R pass through.
+// RMSNorm over D (sum of squares completed with the partner lane ^ 32), RoPE
+// on (d, d + R/2) for d < R/2 (registers j and j + R/32 of the same lane),
+// then the B-operand fragments in fp16.
 template <int D, int R>
-__device__ __forceinline__ void row_finish(const HeadRow<D, R>& r, bool norm, bool rope, float eps,
-                                           float (&v)[D / 16][8]) {
+__device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, const unsigned char* aux, bool norm, float eps,
+                                            int c, int h, u32x4_t (&qf)[D / 16]) {
   constexpr int NJ = D / 16;
+  const float* rope = reinterpret_cast<const float*>(aux);  // [cos | sin][32 rows][R/2]
+  const uint16_t* nwl = reinterpret_cast<const uint16_t*>(aux + 32 * (R / 2) * 2 * 4);
+  float v[NJ][8];
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v[j][i] = r.x[j][0][i];
-      v[j][i + 4] = r.x[j][1][i];
+      v[j][i] = qr.x[j][0][i];
+      v[j][i + 4] = qr.x[j][1][i];
     }
   if (norm) {
     float ss = 0.f;
@@ -121,178 +155,87 @@ __device__ __forceinline__ void row_finish(const HeadRow<D, R>& r, bool norm, bo
     ss += __shfl_xor(ss, 32);
     const float rs = rsqrtf(ss * (1.0f / D) + eps);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
+    for (int j = 0; j < NJ; ++j) {
+      const u32x4_t nw = *reinterpret_cast<const u32x4_t*>(nwl + 16 * j + 8 * h);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const uint32_t w = r.nw[j][i >> 1];
+        const uint32_t w = nw[i >> 1];
         v[j][i] *= rs * __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
       }
-  }
-  if (rope) {
-    constexpr int RJ = R / 32;
-#pragma unroll
-    for (int j = 0; j < RJ; ++j)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float cs = r.cs[j][i >> 2][i & 3], sn = r.sn[j][i >> 2][i & 3];
-        const float x1 = v[j][i], x2 = v[j + RJ][i];
-        v[j][i] = x1 * cs - x2 * sn;
-        v[j + RJ][i] = x1 * sn + x2 * cs;
-      }
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void pack_frag(const float (&v)[D / 16][8], u32x4_t (&f)[D / 16]) {
-#pragma unroll
-  for (int j = 0; j < D / 16; ++j)
-    f[j] = u32x4_t{pack_bf2(v[j][0], v[j][1]), pack_bf2(v[j][2], v[j][3]), pack_bf2(v[j][4], v[j][5]),
-                   pack_bf2(v[j][6], v[j][7])};
-}
-
-// v = hi + lo with hi = bf16(v), lo = bf16(v - hi): about 16 significant bits
-// through two bf16 MFMAs.
-__device__ __forceinline__ void split8(const float* v, u32x4_t& hi, u32x4_t& lo) {
-  float r[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = v[i] - bf2f(f2bf(v[i]));
-  hi = u32x4_t{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])};
-  lo = u32x4_t{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
-}
-
-// P.V step s2 of a 32-key block: B operand = probabilities of registers
-// 8*s2 .. 8*s2+7 (split hi/lo), A operand = V^T fragments.
-template <int ND>
-__device__ __forceinline__ void pv_step(const f32x16_t& p, int s2, const u32x4_t (&va)[ND], f32x16_t (&o)[ND]) {
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = p[8 * s2 + i];
-  u32x4_t ph, pl;
-  split8(v, ph, pl);
-#pragma unroll
-  for (int db = 0; db < ND; ++db) {
-    o[db] = mfma32(va[db], ph, o[db]);
-    o[db] = mfma32(va[db], pl, o[db]);
-  }
-}
-
-// Softmax numerators of NB 32-key blocks that start a chunk: every wave owns
-// exactly one chunk, so the running max starts here and no rescale exists.
-// s[] is already scaled (log2 units) and masked (kNeg).
-template <int NB>
-__device__ __forceinline__ void softmax_fresh(f32x16_t (&s)[NB], float& m_run, float& l_run) {
-  float bmax = kNeg;
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) bmax = fmaxf(bmax, s[b][r]);
-  bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-  float lsum = 0.f;
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[b][r] = fast_exp2(s[b][r] - bmax);
-      lsum += s[b][r];
     }
-  m_run = bmax;
-  l_run = lsum;
-}
-
-// Zeroes the bf16 elements of a V^T fragment whose key (first + e) is >= end:
-// keys past the prefix may hold stale or non-finite data, and 0 * NaN would
-// reach the output through the PV MFMA.
-__device__ __forceinline__ u32x4_t mask_keys(u32x4_t v, int first, int end) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo_ok = (first + 2 * i) < end ? 0xffffu : 0u;
-    const uint32_t hi_ok = (first + 2 * i + 1) < end ? 0xffff0000u : 0u;
-    v[i] &= lo_ok | hi_ok;
   }
-  return v;
-}
-
-template <int D, int R>
-__device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, bool norm, float eps, u32x4_t (&qf)[D / 16],
-                                            u32x4_t (&ql)[D / 16]) {
-  float q[D / 16][8];
-  row_finish<D, R>(qr, norm, true, eps, q);
+  constexpr int RJ = R / 32;
 #pragma unroll
-  for (int j = 0; j < D / 16; ++j) split8(q[j], qf[j], ql[j]);
+  for (int j = 0; j < RJ; ++j) {
+    const f32x4_t* cr = reinterpret_cast<const f32x4_t*>(rope + c * (R / 2) + 16 * j + 8 * h);
+    const f32x4_t* sr = reinterpret_cast<const f32x4_t*>(rope + (32 + c) * (R / 2) + 16 * j + 8 * h);
+    const f32x4_t cs0 = cr[0], cs1 = cr[1], sn0 = sr[0], sn1 = sr[1];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float cs = i < 4 ? cs0[i & 3] : cs1[i & 3], sn = i < 4 ? sn0[i & 3] : sn1[i & 3];
+      const float x1 = v[j][i], x2 = v[j + RJ][i];
+      v[j][i] = x1 * cs - x2 * sn;
+      v[j + RJ][i] = x1 * sn + x2 * cs;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    qf[j] = u32x4_t{pack_h2(v[j][0], v[j][1]), pack_h2(v[j][2], v[j][3]), pack_h2(v[j][4], v[j][5]),
+                    pack_h2(v[j][6], v[j][7])};
 }
 
-// ---- query rows staged once per workgroup -----------------------------------
-// The four waves of a workgroup score the same 32 query rows of one head, so
-// the rows are loaded, normalised and rotated once: thread (row r = t / 8,
-// part j = t % 8) owns
-// * head_dim 128 (RoPE pairs (d, d + 64)): dims 8j .. 8j+7 and 64+8j .. +7;
-// * head_dim 256 (RoPE on dims 0..63, pairs (d, d + 32)): dims 4j .. 4j+3,
-//   32+4j .. +3 and the unrotated 64+24j .. 64+24j+23;
-// so each RoPE pair stays in one thread, and the RMSNorm sum of squares is
-// completed over the row's 8 threads with DPP. The rows go to LDS, from which
-// each wave reads its MFMA fragments. The row stride (D + 4 floats) keeps
-// those 32-byte fragment reads apart in the LDS banks.
+// ---- tree K/V rows: 8 threads per node ------------------------------------
+// Thread part j of a node row owns, for head_dim 128 (RoPE pairs (d, d + 64)),
+// dims 8j .. 8j+7 and 64+8j .. +7; for head_dim 256 (RoPE on dims 0..63,
+// pairs (d, d + 32)) dims 4j .. 4j+3, 32+4j .. +3 and the unrotated
+// 64+24j .. 64+24j+23. Each RoPE pair stays in one thread; the RMSNorm sum
+// of squares is completed over the row's 8 threads with DPP.
 template <int D>
-__host__ __device__ constexpr int qs_stride() { return D + 4; }
-template <int D> struct QStage;
-template <> struct QStage<128> {
-  f32x4_t x[4];
-  u32x4_t nw[2];
-  f32x4_t cs[2], sn[2];
-};
-template <> struct QStage<256> {
-  f32x4_t x[8];      // rotated pair halves [4j, +4), [32+4j, +4); then 64+24j .. +24
-  u32x2_t nwr[2];    // norm weights of the rotated dims
-  u32x4_t nwp[3];    // of the unrotated dims
-  f32x4_t cs, sn;    // RoPE entries 4j .. 4j+3
+__device__ __forceinline__ int row8_dim(int j, int i) {
+  if constexpr (D == 128) return i < 8 ? 8 * j + i : 64 + 8 * j + (i - 8);
+  else return i < 4 ? 4 * j + i : (i < 8 ? 32 + 4 * j + (i - 4) : 64 + 24 * j + (i - 8));
+}
+
+template <int D>
+struct Row8 {
+  static constexpr int NV = D / 8;
+  f32x4_t x[NV / 4];
+  u32x2_t nw[NV / 4];
+  f32x4_t cs[D == 128 ? 2 : 1], sn[D == 128 ? 2 : 1];
 };
 
 template <int D>
-__device__ __forceinline__ void q_stage_issue(const AttnParams& p, int hq, int rb, QStage<D>& q) {
-  const int t = threadIdx.x, r = t >> 3, j = t & 7;
-  const int row = 32 * rb + r;
-  const float* src = p.qkv + (size_t)row * p.ld_qkv + hq * p.q_stride;
-  // without q_norm the weight loads read the row itself (ignored below)
-  const uint16_t* nwb = p.q_norm ? p.q_norm : reinterpret_cast<const uint16_t*>(src);
-  if constexpr (D == 128) {
-    q.x[0] = *reinterpret_cast<const f32x4_t*>(src + 8 * j);
-    q.x[1] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 4);
-    q.x[2] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 64);
-    q.x[3] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 68);
-    q.nw[0] = ld_u32x4(nwb + 8 * j);
-    q.nw[1] = ld_u32x4(nwb + 8 * j + 64);
-    const float* cr = p.rope_cos + row * 64 + 8 * j;
-    const float* sr = p.rope_sin + row * 64 + 8 * j;
-    q.cs[0] = *reinterpret_cast<const f32x4_t*>(cr);
-    q.cs[1] = *reinterpret_cast<const f32x4_t*>(cr + 4);
-    q.sn[0] = *reinterpret_cast<const f32x4_t*>(sr);
-    q.sn[1] = *reinterpret_cast<const f32x4_t*>(sr + 4);
-  } else {
-    q.x[0] = *reinterpret_cast<const f32x4_t*>(src + 4 * j);
-    q.x[1] = *reinterpret_cast<const f32x4_t*>(src + 32 + 4 * j);
+__device__ __forceinline__ void row8_issue(Row8<D>& r, const float* src, const uint16_t* norm_w, const float* cosr,
+                                           const float* sinr, int j, bool aux) {
+  const uint16_t* nwp = norm_w ? norm_w : reinterpret_cast<const uint16_t*>(src);
 #pragma unroll
-    for (int i = 0; i < 6; ++i) q.x[2 + i] = *reinterpret_cast<const f32x4_t*>(src + 64 + 24 * j + 4 * i);
-    q.nwr[0] = *reinterpret_cast<const u32x2_t*>(nwb + 4 * j);
-    q.nwr[1] = *reinterpret_cast<const u32x2_t*>(nwb + 32 + 4 * j);
+  for (int k = 0; k < Row8<D>::NV / 4; ++k) {
+    const int d0 = row8_dim<D>(j, 4 * k);
+    r.x[k] = *reinterpret_cast<const f32x4_t*>(src + d0);
+    if (aux) r.nw[k] = *reinterpret_cast<const u32x2_t*>(nwp + d0);
+  }
+  if (aux) {
+    if constexpr (D == 128) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) q.nwp[i] = ld_u32x4(nwb + 64 + 24 * j + 8 * i);
-    q.cs = *reinterpret_cast<const f32x4_t*>(p.rope_cos + row * 32 + 4 * j);
-    q.sn = *reinterpret_cast<const f32x4_t*>(p.rope_sin + row * 32 + 4 * j);
+      for (int u = 0; u < 2; ++u) {
+        r.cs[u] = *reinterpret_cast<const f32x4_t*>(cosr + 8 * j + 4 * u);
+        r.sn[u] = *reinterpret_cast<const f32x4_t*>(sinr + 8 * j + 4 * u);
+      }
+    } else {
+      r.cs[0] = *reinterpret_cast<const f32x4_t*>(cosr + 4 * j);
+      r.sn[0] = *reinterpret_cast<const f32x4_t*>(sinr + 4 * j);
+    }
   }
 }
 
-__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
 template <int D>
-__device__ __forceinline__ void q_stage_finish(const QStage<D>& q, bool norm, float eps, float* qs) {
-  const int t = threadIdx.x, r = t >> 3, j = t & 7;
-  constexpr int NV = D / 8;  // values per thread
-  float v[NV];
+__device__ __forceinline__ void row8_finish(const Row8<D>& r, bool norm, bool rope, float eps,
+                                            float (&v)[Row8<D>::NV]) {
+  constexpr int NV = Row8<D>::NV;
 #pragma unroll
   for (int k = 0; k < NV / 4; ++k)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[4 * k + i] = q.x[k][i];
+    for (int i = 0; i < 4; ++i) v[4 * k + i] = r.x[k][i];
   if (norm) {
     float ss = 0.f;
 #pragma unroll
@@ -301,681 +244,251 @@ __device__ __forceinline__ void q_stage_finish(const QStage<D>& q, bool norm, fl
     ss += dpp<0x4E>(ss);   // lane ^ 2
     ss += dpp<0x141>(ss);  // the other quad of the row's 8 lanes
     const float rs = rsqrtf(ss * (1.0f / D) + eps);
-    if constexpr (D == 128) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t w = q.nw[i >> 3][(i & 7) >> 1];
-        v[i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t w = q.nwr[i >> 2][(i & 3) >> 1];
-        v[i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
-      }
-#pragma unroll
-      for (int i = 0; i < 24; ++i) {
-        const uint32_t w = q.nwp[i >> 3][(i & 7) >> 1];
-        v[8 + i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
-      }
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t w = r.nw[i >> 2][(i & 3) >> 1];
+      v[i] *= rs * __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
     }
   }
-  constexpr int NR = D == 128 ? 8 : 4;  // rotated pairs per thread
+  if (rope) {
+    constexpr int NR = D == 128 ? 8 : 4;  // rotated pairs per thread
 #pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    float cs, sn;
-    if constexpr (D == 128) {
-      cs = q.cs[i >> 2][i & 3];
-      sn = q.sn[i >> 2][i & 3];
-    } else {
-      cs = q.cs[i];
-      sn = q.sn[i];
-    }
-    const float x1 = v[i], x2 = v[NR + i];
-    v[i] = x1 * cs - x2 * sn;
-    v[NR + i] = x1 * sn + x2 * cs;
-  }
-  float* dst = qs + r * qs_stride<D>();
-  if constexpr (D == 128) {
-    *reinterpret_cast<f32x4_t*>(dst + 8 * j) = f32x4_t{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
-    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 64) = f32x4_t{v[8], v[9], v[10], v[11]};
-    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 68) = f32x4_t{v[12], v[13], v[14], v[15]};
-  } else {
-    *reinterpret_cast<f32x4_t*>(dst + 4 * j) = f32x4_t{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4_t*>(dst + 32 + 4 * j) = f32x4_t{v[4], v[5], v[6], v[7]};
-#pragma unroll
-    for (int i = 0; i < 6; ++i)
-      *reinterpret_cast<f32x4_t*>(dst + 64 + 24 * j + 4 * i) =
-          f32x4_t{v[8 + 4 * i], v[9 + 4 * i], v[10 + 4 * i], v[11 + 4 * i]};
-  }
-}
-
-// Lane (c, h)'s q fragment j (dims 16j + 8h .. +7 of query row c) from the
-// staged rows, split hi / lo.
-template <int D>
-__device__ __forceinline__ void q_frag_one(const float* qs, int c, int h, int j, u32x4_t& qf, u32x4_t& ql) {
-  const float* src = qs + c * qs_stride<D>() + 16 * j + 8 * h;
-  const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
-  const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + 4);
-  const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-  split8(v, qf, ql);
-}
-template <int D>
-__device__ __forceinline__ void q_frag_lds(const float* qs, int c, int h, u32x4_t (&qf)[D / 16],
-                                           u32x4_t (&ql)[D / 16]) {
-#pragma unroll
-  for (int j = 0; j < D / 16; ++j) q_frag_one<D>(qs, c, h, j, qf[j], ql[j]);
-}
-
-// Tree chunk tc: k (norm + RoPE) and v of nodes 32*tc .. 32*tc+31 come from
-// the fused qkv rows and are staged in LDS (this wave's private region) for
-// the MFMA operand layouts; the block's 32 query rows are scored against them
-// with word tc of their ancestor-or-self masks, and k/v are written to the
-// cache rows P + node (once: query block 0, first head of the group).
-// q, k and v are finished one after the other, so at most one raw head row is
-// live in registers (head_dim 256 rows are 128 floats per lane pair).
-template <int D, int R, bool QS>
-__device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs, int hq, int g,
-                                           int G, int P, int L, int tc, int qrow, bool write_rows, int c, int h,
-                                           uint16_t* ks, uint16_t* vt, float& m_run, float& l_run,
-                                           f32x16_t (&o)[D / 32]) {
-  constexpr int NJ = D / 16, ND = D / 32;
-  constexpr int KS = D + 8, VS = 32 + 8;
-  constexpr int half_r = R / 2;
-  // Lane (c, h) stages key node 32*tc + c and owns query row qrow.
-  const int node = 32 * tc + c;
-  const float* row = p.qkv + (size_t)node * p.ld_qkv;
-  const float* cosr = p.rope_cos + node * half_r;
-  const float* sinr = p.rope_sin + node * half_r;
-  const uint32_t anc = p.desc->ancestors[qrow][tc];
-  // Staged head_dim-256 rows are read one fragment at a time in the QK^T
-  // loop (16 fragments would hold 128 registers).
-  constexpr bool PERJ = QS && D > 128;
-  u32x4_t qf[PERJ ? 1 : NJ], ql[PERJ ? 1 : NJ];
-  if constexpr (!QS) {
-    row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * half_r,
-                          p.rope_sin + qrow * half_r, h);
-    q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
-  } else if constexpr (!PERJ) {
-    q_frag_lds<D>(qs, c, h, qf, ql);
-  }
-  u32x4_t kf8[NJ], vf8[NJ];
-  if constexpr (D <= 128) {
-    // Both raw rows in flight together: one round trip instead of two.
-    HeadRow<D, R> kr, vr;
-    row_issue<D, R, true>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
-    row_issue<D, R, false>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
-    float kv[NJ][8], vv[NJ][8];
-    row_finish<D, R>(kr, p.k_norm != nullptr, true, p.eps, kv);
-    pack_frag<D>(kv, kf8);
-    row_finish<D, R>(vr, false, false, 0.f, vv);
-    pack_frag<D>(vv, vf8);
-  } else {
-    {
-      HeadRow<D, R> kr;
-      row_issue<D, R, true>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
-      float kv[NJ][8];
-      row_finish<D, R>(kr, p.k_norm != nullptr, true, p.eps, kv);
-      pack_frag<D>(kv, kf8);
-    }
-    {
-      HeadRow<D, R> vr;
-      row_issue<D, R, false>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
-      float vv[NJ][8];
-      row_finish<D, R>(vr, false, false, 0.f, vv);
-      pack_frag<D>(vv, vf8);
-    }
-  }
-  if (node >= L) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) vf8[j] = u32x4_t{0u, 0u, 0u, 0u};
-  }
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    *reinterpret_cast<u32x4_t*>(&ks[c * KS + 16 * j + 8 * h]) = kf8[j];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t word = vf8[j][i >> 1];
-      vt[(16 * j + 8 * h + i) * VS + c] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
-    }
-  }
-  // Only this wave touches ks/vt, and a wave's LDS operations complete in
-  // order: waiting for them (and fencing the compiler) suffices.
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  const int kr_row = swap_bits23(c);
-  f32x16_t s[1];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) s[0][r] = 0.f;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[kr_row * KS + 16 * j + 8 * h]);
-    if constexpr (PERJ) {
-      u32x4_t f, l;
-      q_frag_one<D>(qs, c, h, j, f, l);
-      s[0] = mfma32(a, f, s[0]);
-      s[0] = mfma32(a, l, s[0]);
-    } else {
-      s[0] = mfma32(a, qf[j], s[0]);
-      s[0] = mfma32(a, ql[j], s[0]);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int t = 16 * (r >> 3) + 8 * h + (r & 7);
-    const bool ok = qrow < L && 32 * tc + t < L && ((anc >> t) & 1u);
-    s[0][r] = ok ? s[0][r] * p.scale_log2 : kNeg;
-  }
-  softmax_fresh<1>(s, m_run, l_run);
-#pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2) {
-    u32x4_t va[ND];
-#pragma unroll
-    for (int db = 0; db < ND; ++db)
-      va[db] = *reinterpret_cast<const u32x4_t*>(&vt[(32 * db + c) * VS + 16 * s2 + 8 * h]);
-    pv_step<ND>(s[0], s2, va, o);
-  }
-  if (p.write_cache && (hq % G) == 0 && write_rows && node < L) {
-    const int pos = P + node;
-    const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
-    uint16_t* krow = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off) * D;
-    uint16_t* vcol = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      *reinterpret_cast<u32x4_t*>(krow + 16 * j + 8 * h) = kf8[j];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t word = vf8[j][i >> 1];
-        vcol[(size_t)(16 * j + 8 * h + i) * DTREE_PAGE] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
-      }
+    for (int i = 0; i < NR; ++i) {
+      const float cs = D == 128 ? r.cs[i >> 2][i & 3] : r.cs[0][i & 3];
+      const float sn = D == 128 ? r.sn[i >> 2][i & 3] : r.sn[0][i & 3];
+      const float x1 = v[i], x2 = v[NR + i];
+      v[i] = x1 * cs - x2 * sn;
+      v[NR + i] = x1 * sn + x2 * cs;
     }
   }
 }
 
-// One prefix chunk = CK consecutive keys inside one page (the whole page for
-// head_dim 128, half of it for 256): its K and V fragments, loaded by
-// prefix_issue and consumed by prefix_chunk. Keys past the
-// prefix in the last chunk are masked (scores) and zeroed (V), since the page
-// may hold stale or non-finite data there.
-template <int D>
-struct ChunkKV {
-  static constexpr int NJ = D / 16, ND = D / 32, NB = chunk_keys(D) / 32;
-  u32x4_t kf[NB][NJ];
-  u32x4_t vf[NB][2][ND];
+// Tree chunk tc into an LDS buffer (K rows [32][KS], V^T [D][VS], fp16 of
+// the bf16 cache values): k = RoPE(k_norm(k)), v raw, from the fused qkv rows
+// of nodes 32tc .. +31 (zero past the tree); the writer also appends the rows
+// to the paged cache at positions P + node (qwen3_tree.py:146). issue() only
+// reads the qkv rows, weights and RoPE table, so it can run before the step
+// descriptor arrives; commit() needs P and L.
+template <int D, int R, int TPS>
+struct TreeStage {
+  static constexpr int NTI = TPS >= 256 ? 1 : 256 / TPS;  // (node, part) units per thread
+  Row8<D> kr[NTI], vr[NTI];
+
+  __device__ __forceinline__ void issue(const AttnParams& p, int tc, int g, int ts) {
+#pragma unroll
+    for (int it = 0; it < NTI; ++it) {
+      const int e = ts + it * TPS;
+      if (e < 256) {
+        const int node = 32 * tc + (e >> 3), j = e & 7;
+        const float* row = p.qkv + (size_t)node * p.ld_qkv;
+        row8_issue<D>(kr[it], row + p.k_off + g * D, p.k_norm, p.rope_cos + node * (R / 2),
+                      p.rope_sin + node * (R / 2), j, true);
+        row8_issue<D>(vr[it], row + p.v_off + g * D, nullptr, nullptr, nullptr, j, false);
+      }
+    }
+  }
+
+  template <int KS, int VS>
+  __device__ __forceinline__ void commit(const AttnParams& p, int tc, int g, int P, int L, int ts, uint16_t* ks,
+                                         uint16_t* vt, bool write) {
+    constexpr int NV = D / 8;
+#pragma unroll
+    for (int it = 0; it < NTI; ++it) {
+      const int e = ts + it * TPS;
+      if (e >= 256) continue;
+      const int nl = e >> 3, j = e & 7;
+      const int node = 32 * tc + nl;
+      float kv[NV], vv[NV];
+      row8_finish<D>(kr[it], p.k_norm != nullptr, true, p.eps, kv);
+      row8_finish<D>(vr[it], false, false, 0.f, vv);
+      const bool live = node < L;
+      uint16_t kb[NV], vb[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        kb[i] = live ? f2bf(kv[i]) : (uint16_t)0;
+        vb[i] = live ? f2bf(vv[i]) : (uint16_t)0;
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        // the MFMA operands are the cached bf16 values, converted exactly to fp16
+        const int d = row8_dim<D>(j, i);
+        ks[nl * KS + d] = (uint16_t)(bf2_to_h2(kb[i]) & 0xffffu);
+        vt[d * VS + nl] = (uint16_t)(bf2_to_h2(vb[i]) & 0xffffu);
+      }
+      if (write && live) {
+        const int pos = P + node;
+        const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
+        uint16_t* krow = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off) * D;
+        uint16_t* vcol = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int d = row8_dim<D>(j, i);
+          krow[d] = kb[i];
+          vcol[(size_t)d * DTREE_PAGE] = vb[i];
+        }
+      }
+    }
+  }
 };
 
-template <int D>
-__device__ __forceinline__ void prefix_issue(const AttnParams& p, ChunkKV<D>& kv, int page, int g, int pc, int c,
-                                             int h) {
-  constexpr int NJ = D / 16, ND = D / 32;
-  constexpr int CK = chunk_keys(D), NB = CK / 32;
-  const int po = (pc * CK) % DTREE_PAGE;
-  const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po + swap_bits23(c)) * D;
-  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po;
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) kv.kf[b][j] = ld_u32x4_stream(kbase + (size_t)32 * b * D + 16 * j + 8 * h);
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int db = 0; db < ND; ++db)
-        kv.vf[b][s2][db] = ld_u32x4_stream(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 32 * b + 16 * s2 + 8 * h);
+// Prefix chunk pc (CK keys of one page) into an LDS buffer: K rows and V^T
+// columns in 16-byte pieces, every load of the workgroup's threads in flight
+// together; keys at or past P (stale rows of the last page) are zeroed.
+// Piece e = ts + i * TPS of K is key e / (D/8), dims 8 (e % (D/8)) .. +7: the
+// chunk's K rows are contiguous, so piece e is at byte 16 e. Piece e of V^T is
+// dim e / (CK/8), keys 8 (e % (CK/8)) .. +7 of the page row. issue() needs
+// only the chunk index (the page table is read there), commit() needs P.
+template <int D, int TPS>
+struct PrefixStage {
+  static constexpr int CK = chunk_keys(D);
+  static constexpr int PK = CK * D / 8 / TPS;  // 16-byte pieces of K (and of V^T) per thread
+  static constexpr int KPR = D / 8, VPR = CK / 8;  // pieces per K row / per V^T row
+  static_assert(TPS % KPR == 0 && TPS % VPR == 0, "the threads cover whole rows");
+  u32x4_t kv[PK], vv[PK];
+
+  // Physical page of chunk pc, read through the scalar cache (pc is uniform):
+  // waiting for it does not wait for the vector loads issued before it.
+  __device__ __forceinline__ static int page_of(const AttnParams& p, int pc) {
+    typedef const __attribute__((address_space(4))) int* const_int_ptr;  // constant address space: s_load
+    return ((const_int_ptr)(uintptr_t)p.page_table)[pc * CK / DTREE_PAGE];
   }
-}
-
-template <int D, int R, bool QS>
-__device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs,
-                                             const ChunkKV<D>& kv, int P, int pc, int c, int h, float& m_run,
-                                             float& l_run, f32x16_t (&o)[D / 32]) {
-  constexpr int NJ = D / 16, ND = D / 32;
-  constexpr int CK = chunk_keys(D), NB = CK / 32;
-  const int k_begin = pc * CK;  // prefix chunk pc: keys pc*CK ..
-  const int k_end = min(k_begin + CK, P);
-  constexpr bool PERJ = QS && D > 128;  // staged head_dim 256: one fragment at a time
-  u32x4_t qf[PERJ ? 1 : NJ], ql[PERJ ? 1 : NJ];
-  if constexpr (!QS) q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
-  else if constexpr (!PERJ) q_frag_lds<D>(qs, c, h, qf, ql);
-
-  f32x16_t s[NB];
+  __device__ __forceinline__ void issue(const AttnParams& p, int pc, int page, int g, int ts) {
+    const int po = (pc * CK) % DTREE_PAGE;
+    const __amdgpu_buffer_rsrc_t kr =
+        buf_rsrc(p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po) * D, (unsigned)(CK * D * 2));
+    const __amdgpu_buffer_rsrc_t vr =
+        buf_rsrc(p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po, (unsigned)(D * DTREE_PAGE * 2));
+    const int vrow0 = ts / VPR, vcol = 8 * (ts % VPR);
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+    for (int i = 0; i < PK; ++i) {
+      kv[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, 16 * (ts + i * TPS), 0, kNt);
+      vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, 2 * ((vrow0 + i * (TPS / VPR)) * DTREE_PAGE + vcol), 0, kNt);
+    }
+  }
+
+  template <int KS, int VS>
+  __device__ __forceinline__ void commit(int pc, int P, int ts, uint16_t* ks, uint16_t* vt) const {
+    const int kend = P - pc * CK;  // keys >= kend are past the prefix
+    const int krow0 = ts / KPR, kcol = 8 * (ts % KPR);
+    const int vrow0 = ts / VPR, vcol = 8 * (ts % VPR);
+#pragma unroll
+    for (int i = 0; i < PK; ++i) {
+      const int key = krow0 + i * (TPS / KPR);
+      *reinterpret_cast<u32x4_t*>(ks + key * KS + kcol) = key < kend ? bf8_to_h8(kv[i]) : u32x4_t{0u, 0u, 0u, 0u};
+      u32x4_t v = vv[i];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t lo_ok = (vcol + 2 * q) < kend ? 0xffffu : 0u;
+        const uint32_t hi_ok = (vcol + 2 * q + 1) < kend ? 0xffff0000u : 0u;
+        v[q] &= lo_ok | hi_ok;
+      }
+      *reinterpret_cast<u32x4_t*>(vt + (vrow0 + i * (TPS / VPR)) * VS + vcol) = bf8_to_h8(v);
+    }
+  }
+};
+
+// One chunk of NBK 32-key blocks from LDS for this wave's head: S^T = K Q^T,
+// scale and mask, online softmax update (running max m, lane-partial row sum
+// l, output rescaled when the max grows), O^T += V^T P^T. TREE: key k of
+// block 0 is tree node 32 tc + k, visible when bit k of the query's ancestor
+// word is set; else prefix keys >= kend are masked.
+template <int D, int NBK, int KS, int VS, bool TREE>
+__device__ __forceinline__ void attend_chunk(const uint16_t* ks, const uint16_t* vt, const u32x4_t (&qf)[D / 16],
+                                             float scale_log2, int kend, uint32_t anc,
+                                             bool qlive, int c, int h, float& m_run, float& l_run,
+                                             f32x16_t (&o)[D / 32]) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  f32x16_t s[NBK];
+#pragma unroll
+  for (int b = 0; b < NBK; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
+  const int krow = swap_bits23(c);
+  // K fragments are read one dims-step ahead of their MFMAs (not all at once:
+  // registers for two waves per SIMD).
+  u32x4_t a[2][NBK];
+#pragma unroll
+  for (int b = 0; b < NBK; ++b) a[0][b] = *reinterpret_cast<const u32x4_t*>(ks + (32 * b + krow) * KS + 8 * h);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    u32x4_t f, l;
-    if constexpr (PERJ) q_frag_one<D>(qs, c, h, j, f, l);
+    if (j + 1 < NJ) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      s[b] = mfma32(kv.kf[b][j], PERJ ? f : qf[PERJ ? 0 : j], s[b]);
-      s[b] = mfma32(kv.kf[b][j], PERJ ? l : ql[PERJ ? 0 : j], s[b]);
+      for (int b = 0; b < NBK; ++b)
+        a[(j + 1) & 1][b] = *reinterpret_cast<const u32x4_t*>(ks + (32 * b + krow) * KS + 16 * (j + 1) + 8 * h);
     }
-  }
-  const bool ragged = k_end - k_begin < CK;
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NBK; ++b) s[b] = mfma32_f16(a[j & 1][b], qf[j], s[b]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  float bmax = kNeg;
+#pragma unroll
+  for (int b = 0; b < NBK; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int key = k_begin + 32 * b + 16 * (r >> 3) + 8 * h + (r & 7);
-      s[b][r] = (!ragged || key < k_end) ? s[b][r] * p.scale_log2 : kNeg;
+      const int key = 32 * b + 16 * (r >> 3) + 8 * h + (r & 7);
+      const bool ok = TREE ? (qlive && key < kend && ((anc >> key) & 1u)) : key < kend;
+      s[b][r] = ok ? s[b][r] * scale_log2 : kNeg;
+      bmax = fmaxf(bmax, s[b][r]);
     }
-  softmax_fresh<NB>(s, m_run, l_run);
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      u32x4_t va[ND];
-      const int first = k_begin + 32 * b + 16 * s2 + 8 * h;
-#pragma unroll
-      for (int db = 0; db < ND; ++db)
-        va[db] = ragged ? mask_keys(kv.vf[b][s2][db], first, k_end) : kv.vf[b][s2][db];
-      pv_step<ND>(s[b], s2, va, o);
-    }
-}
-
-// Combine of a head's workgroup partials ([block][lane][16] floats, then m and
-// l of the 32 queries, per split) by the last workgroup to arrive: kSb splits
-// per round with every load of the round in flight (ranged loads past the
-// last split return zero) and a running max; AUX is the cache policy of the
-// loads (kSc0: all writers on this XCD, else kSc1).
-template <int D, int AUX>
-__device__ __forceinline__ void combine_splits(__amdgpu_buffer_rsrc_t prs, unsigned pbase, size_t stride, int nsplit,
-                                               int wave, int lane, int c, float& tot,
-                                               f32x16_t (&mine)[D / 32 / kWaves]) {
-  constexpr int NDW = D / 32 / kWaves;
-  constexpr int kSb = 8 / NDW;  // 8 splits per round at head_dim 128, 4 at 256
-  float Ms = kNeg;
-  tot = 0.f;
-#pragma unroll
-  for (int k = 0; k < NDW; ++k)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mine[k][r] = 0.f;
-  for (int s0 = 0; s0 < nsplit; s0 += kSb) {
-    f32x4_t v[kSb][NDW][4];
-    float mm[kSb], ll[kSb];
-#pragma unroll
-    for (int b = 0; b < kSb; ++b) {
-      const bool ok = s0 + b < nsplit;
-      const unsigned so = ok ? pbase + (unsigned)((size_t)(s0 + b) * stride * sizeof(float)) : kOob;
-      const float mv = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(so + (32 * D + c) * 4), 0, AUX));
-      ll[b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(so + (32 * D + 32 + c) * 4),
-                                                                            0, AUX));
-      mm[b] = ok ? mv : kNeg;
-#pragma unroll
-      for (int k = 0; k < NDW; ++k)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq)
-          v[b][k][gq] = __builtin_bit_cast(
-              f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                           prs, (int)(so + (unsigned)(((wave + kWaves * k) * 64 + lane) * 64 + 16 * gq)), 0, AUX));
-    }
-    float gm = Ms;
-#pragma unroll
-    for (int b = 0; b < kSb; ++b) gm = fmaxf(gm, mm[b]);
-    const float rsc = fast_exp2(Ms - gm);
-    tot *= rsc;
-#pragma unroll
-    for (int k = 0; k < NDW; ++k)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mine[k][r] *= rsc;
-#pragma unroll
-    for (int b = 0; b < kSb; ++b) {
-      const float w = fast_exp2(mm[b] - gm);
-      tot += w * ll[b];
-#pragma unroll
-      for (int k = 0; k < NDW; ++k)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) mine[k][4 * gq + i] += w * v[b][k][gq][i];
-    }
-    Ms = gm;
-  }
-}
-
-// TB: tree chunks the LDS staging is sized for (1 for 32 rows, 4 up to 128).
-template <int D, int R, bool GATE, int TB>
-__global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
-  constexpr int ND = D / 32;  // 32-dim blocks of O^T
-  constexpr int KS = D + 8;   // padded LDS row of tree K
-  constexpr int VS = 32 + 8;  // padded LDS row of tree V^T
-  constexpr int kStage = (32 * KS + D * VS) * 2;   // one tree chunk's K / V^T staging
-  // Query rows are staged in LDS except for head_dim 256 with four tree
-  // chunks (their K/V staging leaves no room).
-  constexpr bool QS = D <= 128 || TB == 1;
-  constexpr int kQs = QS ? 32 * qs_stride<D>() * 4 : 0;  // staged query rows
-  constexpr int kMl = kWaves * 64 * 4;               // merge: per wave, m and l of 32 queries
-  constexpr int kMerge = kMl + ND * kWaves * 4 * 64 * 16;  // + [block][wave][4][lane] f32x4
-  constexpr int kChunkLds = TB * kStage + kQs;
-  constexpr int CK = chunk_keys(D);
-  __shared__ __align__(16) unsigned char lds[kChunkLds > kMerge ? kChunkLds : kMerge];
-  __shared__ int s_last;
-
-  // Every argument the prologue needs in scalar registers at once: one batch
-  // of argument loads and one wait, instead of a batch per basic block.
-  asm volatile("" ::"s"(p.qkv), "s"(p.ld_qkv), "s"(p.q_stride), "s"(p.q_norm), "s"(p.rope_cos), "s"(p.rope_sin),
-               "s"(p.kp), "s"(p.vp), "s"(p.page_table), "s"(p.desc), "s"(p.Hq), "s"(p.Hkv), "s"(p.max_chunks),
-               "s"(p.splits), "s"(p.tree_chunks), "s"(gridDim.x));
-  // blockIdx -> (query block, split, kv group, head in group): the G heads of
-  // one (split, group) pair share blockIdx % 8, i.e. one XCD.
-  const int G = p.Hq / p.Hkv, NT = p.tree_chunks;
-  const int per_block = (int)gridDim.x / NT;  // workgroups per query block (a multiple of 8)
-  const int rb = blockIdx.x / per_block, bid = blockIdx.x % per_block;
-  const int pair = (bid / (8 * G)) * 8 + (bid & 7);
-  // Padding workgroups (pair past splits * Hkv) still name an in-range head
-  // and a chunk past max_chunks; they return after the loads below are out,
-  // which keeps the argument loads in one round trip.
-  const int g = pair % p.Hkv, split = pair / p.Hkv;
-  const int hq = g * G + (bid >> 3) % G;
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
-  const int chunk = split * kWaves + wave;
-  const int qrow = 32 * rb + c;  // this lane's query row
-  // Loads that do not depend on the step descriptor go out first, so their
-  // latency overlaps the descriptor read: the workgroup's query rows (values,
-  // norm weights, RoPE; 10 loads per thread) and the page of this wave's
-  // prefix chunk. The chunk's K/V follow the descriptor check: issued before
-  // it, they delay the descriptor's own (scalar) load by microseconds.
-  // (head_dim 256 with four tree chunks loads its q row per wave inside the
-  // chunk: there is no LDS left to stage it.)
-  const bool prefix_wave = chunk >= NT && chunk < p.max_chunks;
-  const int page = prefix_wave ? p.page_table[(chunk - NT) * CK / DTREE_PAGE] : 0;
-  HeadRow<D, R> qr;
-  QStage<D> qst;
-  if constexpr (QS) q_stage_issue<D>(p, hq, rb, qst);
-
-  if (pair >= p.splits * p.Hkv) return;
-  const int P = p.desc->past_length, L = p.desc->num_nodes;
-  const int nchunks = NT + (P + CK - 1) / CK;
-  // A descriptor beyond the grid's capacity (P > max_past_length) or with more
-  // rows than rows_padded leaves the output untouched instead of indexing past
-  // buffers.
-  if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;
-  const int nsplit = (nchunks + kWaves - 1) / kWaves;
-  if (split >= nsplit) return;
-  if (32 * rb >= L) {
-    // Query block past the tree: its output rows are zero (split 0 writes).
-    if (split == 0) {
-      const int q = threadIdx.x >> 3;
-      for (int dd = (threadIdx.x & 7) * 8; dd < D; dd += 64) {
-        const int col = hq * D + dd;
-        const int row = 32 * rb + q;
-        const size_t oi = p.out_tiled ? tiled_index(row, col, p.ld_out) : (size_t)row * p.ld_out + col;
-        *reinterpret_cast<u32x4_t*>(p.out + oi) = u32x4_t{0u, 0u, 0u, 0u};
-        if (p.out_lo) *reinterpret_cast<u32x4_t*>(p.out_lo + oi) = u32x4_t{0u, 0u, 0u, 0u};
-      }
-    }
-    return;
-  }
-
-  float* qs = reinterpret_cast<float*>(lds + TB * kStage);
-  if constexpr (QS) {
-    q_stage_finish<D>(qst, p.q_norm != nullptr, p.eps, qs);
-    __syncthreads();
-  }
-
-  float m_run = kNeg, l_run = 0.f;
-  f32x16_t o[ND];
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+  const float m_new = fmaxf(m_run, bmax);
+  const float alpha = fast_exp2(m_run - m_new);
+  l_run *= alpha;
 #pragma unroll
   for (int db = 0; db < ND; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
-
-  if (chunk < NT) {
-    // Tree chunks are waves 0 .. NT-1 of split 0, each with its own staging.
-    if (32 * chunk < L) {
-      uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)chunk * kStage);
-      tree_chunk<D, R, QS>(p, qr, qs, hq, g, G, P, L, chunk, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+#pragma unroll
+  for (int b = 0; b < NBK; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      // masked keys contribute nothing, also while every key so far is masked
+      const float e = s[b][r] > 0.5f * kNeg ? fast_exp2(s[b][r] - m_new) : 0.f;
+      s[b][r] = e;
+      l_run += e;
     }
-  } else if (chunk < nchunks) {
-    if constexpr (!QS)
-      row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm,
-                            p.rope_cos + qrow * (R / 2), p.rope_sin + qrow * (R / 2), h);
-    ChunkKV<D> kv;
-    prefix_issue<D>(p, kv, page, g, chunk - NT, c, h);
-    prefix_chunk<D, R, QS>(p, qr, qs, kv, P, chunk - NT, c, h, m_run, l_run, o);
-  }
-
-  // ---- merge the four waves ----
-  // o holds this wave's chunk for the 32 queries x D dims in MFMA layout:
-  // lane (c, h), register r of block db = dim 32 db + acc_row(r, h) of query
-  // c. Wave w completes blocks db = w, w + 4, ...: every wave rescales its o
-  // to the common max and hands the blocks it does not complete to their
-  // owners through LDS in 16-byte pieces.
-  constexpr int NDW = ND / kWaves;  // blocks a wave completes: 1 (head_dim 128), 2 (256)
-  float* ml = reinterpret_cast<float*>(lds);             // [wave][m | l][32]
-  f32x4_t* xch = reinterpret_cast<f32x4_t*>(lds + kMl);  // [block][wave][4][lane]
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  __syncthreads();  // retires the chunk staging (tree K/V, query rows), which shares this memory
-  if (h == 0) {
-    ml[wave * 64 + c] = m_run;
-    ml[wave * 64 + 32 + c] = l_tot;
-  }
-  __syncthreads();
-  float M = kNeg, tot = 0.f, self = 0.f;
+  m_run = m_new;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[w * 64 + c]);
+  for (int b = 0; b < NBK; ++b)
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float f = fast_exp2(ml[w * 64 + c] - M);
-    tot += f * ml[w * 64 + 32 + c];
-    if (w == wave) self = f;
-  }
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int r0 = 8 * s2;
+      const u32x4_t ph = {pack_h2(s[b][r0], s[b][r0 + 1]), pack_h2(s[b][r0 + 2], s[b][r0 + 3]),
+                          pack_h2(s[b][r0 + 4], s[b][r0 + 5]), pack_h2(s[b][r0 + 6], s[b][r0 + 7])};
 #pragma unroll
-  for (int db = 0; db < ND; ++db) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[db][r] *= self;
-    if (db % kWaves != wave) {
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq)
-        xch[((db * kWaves + wave) * 4 + gq) * 64 + lane] =
-            f32x4_t{o[db][4 * gq], o[db][4 * gq + 1], o[db][4 * gq + 2], o[db][4 * gq + 3]};
-    }
-  }
-  __syncthreads();
-  f32x16_t mine[NDW];  // completed blocks wave + kWaves * k
-#pragma unroll
-  for (int db = 0; db < ND; ++db) {
-    if (db % kWaves != wave) continue;
-    f32x16_t a = o[db];
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      if (w == wave) continue;
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const f32x4_t x = xch[((db * kWaves + w) * 4 + gq) * 64 + lane];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[4 * gq + i] += x[i];
+      for (int db = 0; db < ND; ++db) {
+        const u32x4_t va = *reinterpret_cast<const u32x4_t*>(vt + (32 * db + c) * VS + 32 * b + 16 * s2 + 8 * h);
+        o[db] = mfma32_f16(va, ph, o[db]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    mine[db / kWaves] = a;
-  }
-
-  if (nsplit > 1) {
-    // Workgroup partial: [block][lane][16] floats (each lane moves its block
-    // values in 16-byte agent-coherent stores and loads), then m and l of the
-    // 32 queries.
-    const size_t stride = (size_t)32 * D + 64;
-    const int hb = hq * NT + rb;  // (head, query block)
-    const __amdgpu_buffer_rsrc_t prs =
-        buf_rsrc(p.part, (unsigned)((size_t)p.Hq * NT * p.splits * stride * sizeof(float)));
-    const unsigned pbase = (unsigned)((size_t)hb * p.splits * stride * sizeof(float));
-    const unsigned mine_off = pbase + (unsigned)((size_t)split * stride * sizeof(float));
-#pragma unroll
-    for (int k = 0; k < NDW; ++k) {
-      const unsigned off = mine_off + (unsigned)(((wave + kWaves * k) * 64 + lane) * 64);
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(u32x4_t, f32x4_t{mine[k][4 * gq], mine[k][4 * gq + 1], mine[k][4 * gq + 2],
-                                                mine[k][4 * gq + 3]}),
-            prs, (int)(off + 16 * gq), 0, kSc1);
-    }
-    float* part = p.part + ((size_t)hb * p.splits + split) * stride;
-    if (wave == 0 && h == 0) {
-      st_coherent(part + 32 * D + c, M);
-      st_coherent(part + 32 * D + 32 + c, tot);
-    }
-    if (p.sep_combine) return;  // attn_combine_kernel (next launch) reads the partials
-    wait_stores_done();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      // arrival count in the low half, workgroups off their XCD in the high
-      const bool native = !p.off_xcd && xcc_id() == (int)(blockIdx.x % kXcds);
-      const int old = arrive_add(&p.counters[hb], native ? 1 : 1 + kForeign);
-      int last = 0;
-      if ((old & (kForeign - 1)) == nsplit - 1) {
-        last = native && old < kForeign && p.Hkv % kXcds == 0 ? 2 : 1;
-        reset_counter(&p.counters[hb]);
-      }
-      s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-
-    // Every split of this head ran on this XCD when all are confirmed on
-    // their expected XCD and the heads of a KV group's splits share one
-    // (Hkv % 8 == 0): the partials are then read from the local L2.
-    if (s_last == 2) combine_splits<D, kSc0>(prs, pbase, stride, nsplit, wave, lane, c, tot, mine);
-    else combine_splits<D, kSc1>(prs, pbase, stride, nsplit, wave, lane, c, tot, mine);
-  }
-
-  // Output: lane (c, h) holds, per completed block, 4 runs of 4 consecutive
-  // dims (registers 4g .. 4g+3 = dims 32 db + 8g + 4h .. +3) of query c.
-  const int orow = 32 * rb + c;
-  const float inv = (orow < L && tot > 0.f) ? 1.0f / tot : 0.f;
-#pragma unroll
-  for (int k = 0; k < NDW; ++k) {
-    const int db = wave + kWaves * k;
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const int dim = 32 * db + 8 * gq + 4 * h;
-      float y[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] = orow < L ? mine[k][4 * gq + i] * inv : 0.f;
-      if (GATE && orow < L) {
-        // o_proj input = attention * sigmoid(gate), gate = q_proj row dims D.. of the head
-        const f32x4_t gt = *reinterpret_cast<const f32x4_t*>(p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D +
-                                                             dim);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
-      }
-      float rl[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
-      const u32x2_t hi = {pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
-      const u32x2_t lo = {pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
-      const int col = hq * D + dim;
-      const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
-      *reinterpret_cast<u32x2_t*>(p.out + oi) = hi;
-      if (p.out_lo) *reinterpret_cast<u32x2_t*>(p.out_lo + oi) = lo;
-    }
-  }
 }
 
-// Combine of the workgroup partials for long prefixes, as a launch of its
-// own: with S splits the in-kernel last arriver reads S partial tiles of
-// 32 x D fp32 alone (544 KB at head_dim 256, P = 2048), which one CU's load
-// bandwidth turns into ~18 us. Here one workgroup per (head, query block,
-// 32-dim block) reads S x 4 KB: wave w takes splits w, w + 4, ... with a
-// running max, the four waves merge in LDS and wave 0 writes the block's
-// output (normalised, gated, bf16 pair). Splits and partial layout are the
-// main kernel's; with one split or a query block past the tree the main
-// kernel has written the output itself.
+// Prefix chunks [c0, c1) of split s >= 1: cps consecutive chunks, cut at the
+// np chunks of the prefix. The mapping depends on the grid only (not on P), so
+// a split can read its page table entry and issue its first K/V loads before
+// the step descriptor arrives.
+__device__ __forceinline__ void split_range(int s, int cps, int np, int& c0, int& c1) {
+  c0 = (s - 1) * cps;
+  c1 = min(c0 + cps, np);
+}
+
+// Output rows of one (head, 32-dim block) unit from lane (c, h)'s 16 values
+// (accumulator layout: register 4 gq + i = dim 32 db + 8 gq + 4 h + i of query
+// row 32 rb + c): normalised, gated, stored as the bf16 hi / lo pair.
 template <int D, bool GATE>
-__global__ __launch_bounds__(64 * kWaves) void attn_combine_kernel(AttnParams p) {
-  constexpr int ND = D / 32;
-  constexpr int kB = 8;  // splits in flight per wave
-  const int NT = p.tree_chunks;
-  const int db = blockIdx.x % ND, hb = blockIdx.x / ND;  // hb = head * NT + query block
-  const int hq = hb / NT, rb = hb % NT;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
-  constexpr int CK = chunk_keys(D);
-  const int P = p.desc->past_length, L = p.desc->num_nodes;
-  const int nchunks = NT + (P + CK - 1) / CK;
-  if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;  // the main kernel's guards
-  const int nsplit = (nchunks + kWaves - 1) / kWaves;
-  if (nsplit <= 1 || 32 * rb >= L) return;
-  const size_t stride = (size_t)32 * D + 64;
-  const __amdgpu_buffer_rsrc_t prs =
-      buf_rsrc(p.part, (unsigned)((size_t)p.Hq * NT * p.splits * stride * sizeof(float)));
-  const unsigned pbase = (unsigned)((size_t)hb * p.splits * stride * sizeof(float));
-  float Ms = kNeg, tot = 0.f;
-  f32x4_t acc[4];
-#pragma unroll
-  for (int gq = 0; gq < 4; ++gq) acc[gq] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int s0 = wave; s0 < nsplit; s0 += kWaves * kB) {
-    f32x4_t v[kB][4];
-    float mm[kB], ll[kB];
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const int sp = s0 + kWaves * b;
-      const unsigned so = sp < nsplit ? pbase + (unsigned)((size_t)sp * stride * sizeof(float)) : kOob;
-      const float mv = buf_ldf(prs, so + (32 * D + c) * 4);
-      ll[b] = buf_ldf(prs, so + (32 * D + 32 + c) * 4);
-      mm[b] = sp < nsplit ? mv : kNeg;
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq)
-        v[b][gq] = __builtin_bit_cast(f32x4_t, buf_ld(prs, so + (unsigned)((db * 64 + lane) * 64 + 16 * gq)));
-    }
-    float gm = Ms;
-#pragma unroll
-    for (int b = 0; b < kB; ++b) gm = fmaxf(gm, mm[b]);
-    const float rsc = fast_exp2(Ms - gm);
-    tot *= rsc;
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) acc[gq] *= rsc;
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const float w = fast_exp2(mm[b] - gm);  // 0 for splits past nsplit
-      tot += w * ll[b];
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) acc[gq] += w * v[b][gq];
-    }
-    Ms = gm;
-  }
-  // Merge the four waves (in wave order) into wave 0.
-  __shared__ float ml[kWaves][2][64];
-  __shared__ f32x4_t xa[kWaves - 1][4][64];
-  ml[wave][0][lane] = Ms;
-  ml[wave][1][lane] = tot;
-  if (wave > 0) {
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) xa[wave - 1][gq][lane] = acc[gq];
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  float M = kNeg;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[w][0][lane]);
-  float T = 0.f;
-  f32x4_t o[4];
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float f = fast_exp2(ml[w][0][lane] - M);
-    T += f * ml[w][1][lane];
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const f32x4_t x = w == 0 ? acc[gq] : xa[w - 1][gq][lane];
-      o[gq] = w == 0 ? f * x : o[gq] + f * x;
-    }
-  }
-  // Output of query c, dims 32 db + 8 gq + 4 h .. +3 (MFMA accumulator layout).
+__device__ __forceinline__ void write_unit(const AttnParams& p, int hq, int db, int rb, int L, int c, int h,
+                                           const float (&acc)[16], float inv) {
   const int orow = 32 * rb + c;
-  const float inv = (orow < L && T > 0.f) ? 1.0f / T : 0.f;
 #pragma unroll
   for (int gq = 0; gq < 4; ++gq) {
     const int dim = 32 * db + 8 * gq + 4 * h;
     float y[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = orow < L ? o[gq][i] * inv : 0.f;
+    for (int i = 0; i < 4; ++i) y[i] = orow < L ? acc[4 * gq + i] * inv : 0.f;
     if (GATE && orow < L) {
-      const f32x4_t gt =
-          *reinterpret_cast<const f32x4_t*>(p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D + dim);
+      // o_proj input = attention * sigmoid(gate), gate = q_proj row dims D.. of the head (qwen35_tree.py:540)
+      const f32x4_t gt = *reinterpret_cast<const f32x4_t*>(p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D + dim);
 #pragma unroll
       for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
     }
@@ -991,31 +504,345 @@ __global__ __launch_bounds__(64 * kWaves) void attn_combine_kernel(AttnParams p)
   }
 }
 
+template <int D, int R, bool GATE, int G>
+__global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  constexpr int CK = chunk_keys(D), NB = CK / 32;
+  constexpr int KS = D + 8;   // LDS K row stride (bf16 / fp16 elements)
+  constexpr int VS = CK + 8;  // LDS V^T row stride
+  constexpr int kStage = (CK * KS + D * VS) * 2;
+  constexpr int TPS = 64 * G;      // threads
+  constexpr int W = G;             // waves
+  constexpr int U = G * ND;        // combine units (head, 32-dim block)
+  constexpr int kComb = W * 64 * 5 * 16;  // [wave][4 f32x4 + (M, T) pad][lane]
+  constexpr int kLdsKV = 2 * kStage > kComb ? 2 * kStage : kComb;
+  __shared__ __align__(16) unsigned char lds[kLdsKV];
+  __shared__ __align__(16) unsigned char lds_aux[QAux<D, R, TPS>::kBytes];
+  __shared__ int s_flag;
+
+  const int pairs = p.Hkv * p.NT;
+  const int pair = blockIdx.x % pairs, s = blockIdx.x / pairs;
+  const int g = pair % p.Hkv, rb = pair / p.Hkv;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hw = wave;
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int ts = threadIdx.x;
+  const int hq = g * G + hw;
+  const int qrow = 32 * rb + c;
+  const int S = p.S;
+
+  // The step descriptor's P and L are read first; everything that does not
+  // depend on them (the query rows and their norm / RoPE, the first chunk:
+  // tree rows, or page table entry then K/V) goes out before they are used,
+  // so the latencies overlap.
+  u32x4_t qf[NJ];
+  HeadRow<D, R> qr;
+  row_issue<D, R>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, h);
+  QAux<D, R, TPS> qa;
+  qa.issue(p, rb, ts);
+  // RoPE rows and q_norm weight into LDS, then this wave's q fragments
+  auto build_q = [&]() {
+    qa.commit(lds_aux, ts);
+    __syncthreads();
+    q_fragments<D, R>(qr, lds_aux, p.q_norm != nullptr, p.eps, c, h, qf);
+  };
+  int P = 0, L = 0, np = 0;
+  // The descriptor is read after the chunk loads are issued (its scalar wait
+  // must not hold them back).
+  auto read_desc = [&]() {
+    P = p.desc->past_length;
+    L = p.desc->num_nodes;
+    np = (P + CK - 1) / CK;
+  };
+  // A descriptor beyond the grid's capacity leaves the output untouched (every
+  // workgroup returns, so none waits at the counter); a query block past the
+  // tree writes zero rows without an exchange.
+  auto bail = [&]() -> bool {
+    if (P < 0 || P > p.max_past || np > p.max_pchunks || L > 32 * p.NT || L < 1 || (np > 0 && S < 2)) return true;
+    if (32 * rb >= L) {
+      if (wave == 0) {
+        float z[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) z[i] = 0.f;
+        for (int u = s; u < U; u += S) write_unit<D, false>(p, g * G + u / ND, u % ND, rb, L, c, h, z, 0.f);
+      }
+      return true;
+    }
+    return false;
+  };
+
+  float m_run = kNeg, l_run = 0.f;
+  f32x16_t o[ND];
+  int n_items;
+  // Chunks run through two LDS buffers: chunk i + 1's loads are in flight
+  // while chunk i is multiplied.
+  auto buf_k = [&](int i) { return reinterpret_cast<uint16_t*>(lds + (i & 1) * kStage); };
+  auto buf_v = [&](int i) { return reinterpret_cast<uint16_t*>(lds + (i & 1) * kStage) + CK * KS; };
+  if (s == 0) {
+    // split 0: tree chunks 0 .. rb (later ones hold no ancestor of this block's rows)
+    n_items = min(rb, p.NT - 1) + 1;
+    TreeStage<D, R, TPS> st;
+    st.issue(p, 0, g, ts);
+    read_desc();
+    build_q();
+    if (bail()) return;
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+    for (int it = 0; it < n_items; ++it) {
+      st.template commit<KS, VS>(p, it, g, P, L, ts, buf_k(it), buf_v(it), p.write_cache && it == rb);
+      if (it + 1 < n_items) st.issue(p, it + 1, g, ts);
+      __syncthreads();
+      const uint32_t anc = p.desc->ancestors[qrow][it];
+      attend_chunk<D, 1, KS, VS, true>(buf_k(it), buf_v(it), qf, p.scale_log2, L - 32 * it, anc, qrow < L, c, h,
+                                       m_run, l_run, o);
+    }
+  } else {
+    // split s >= 1: prefix chunks c0 .. c0 + cps - 1 (cut at the prefix's np)
+    const int c0 = (s - 1) * p.cps;
+    const bool any = c0 < p.max_pchunks;
+    PrefixStage<D, TPS> st;
+    if (any) st.issue(p, c0, PrefixStage<D, TPS>::page_of(p, c0), g, ts);
+    read_desc();
+    build_q();
+    if (bail()) return;
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+    n_items = max(0, min(c0 + p.cps, np) - c0);
+    for (int it = 0; it < n_items; ++it) {
+      st.template commit<KS, VS>(c0 + it, P, ts, buf_k(it), buf_v(it));
+      if (it + 1 < n_items) st.issue(p, c0 + it + 1, PrefixStage<D, TPS>::page_of(p, c0 + it + 1), g, ts);
+      __syncthreads();
+      attend_chunk<D, NB, KS, VS, false>(buf_k(it), buf_v(it), qf, p.scale_log2, P - (c0 + it) * CK, 0u, true, c,
+                                         h, m_run, l_run, o);
+    }
+  }
+  __syncthreads();  // the LDS buffers are reused below
+
+  // ---- publish this split's partial, written through (sc1): per head
+  // [db][gq][lane] f32x4 (accumulator registers 4 gq .. 4 gq + 3 of block db:
+  // each store instruction of the wave writes one contiguous kilobyte), then
+  // m[32] and l[32] ----
+  constexpr int kHeadStride = ND * 64 * 16 + 64;  // floats per head
+  const size_t split_floats = (size_t)G * kHeadStride;
+  const unsigned part_bytes = (unsigned)((size_t)pairs * S * split_floats * sizeof(float));
+  const __amdgpu_buffer_rsrc_t prs = buf_rsrc(p.part, part_bytes);
+  const unsigned pair_base = (unsigned)((size_t)pair * S * split_floats * sizeof(float));
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (n_items > 0) {
+    const unsigned hb = pair_base + (unsigned)(((size_t)s * split_floats + (size_t)hw * kHeadStride) * 4);
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4_t, f32x4_t{o[db][4 * gq], o[db][4 * gq + 1], o[db][4 * gq + 2],
+                                                o[db][4 * gq + 3]}),
+            prs, (int)(hb + (unsigned)(((db * 4 + gq) * 64 + lane) * 16)), 0, kSc1);
+    if (h == 0) {
+      const unsigned mo = hb + (unsigned)(ND * 64 * 16 * 4);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, m_run), prs, (int)(mo + 4 * c), 0, kSc1);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, l_tot), prs, (int)(mo + 4 * (32 + c)), 0,
+                                            kSc1);
+    }
+  }
+  wait_stores_done();
+  __syncthreads();
+
+  // ---- meet the (group, query block)'s other splits ----
+  int* cnt = p.counters + pair;
+  if (threadIdx.x == 0) {
+    // arrivals in the low 16 bits; workgroups off their expected XCD add kForeign
+    const bool native = !p.off_xcd && xcc_id() == (int)(blockIdx.x % kXcds);
+    const int add = native ? 1 : 1 + kForeign;
+    int v = arrive_add(cnt, add) + add;
+    int it = 0;
+    while ((v & (kForeign - 1)) < S && it < kSpinLimit) {
+      __builtin_amdgcn_s_sleep(1);
+      v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ++it;
+    }
+    int flag;
+    if ((v & (kForeign - 1)) < S) {
+      __hip_atomic_fetch_or(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      flag = 0;
+    } else {
+      // all splits on this XCD (pairs % 8 == 0 puts a pair's splits on one
+      // XCD and none was foreign): read the partials from the local L2
+      flag = (v < kForeign && pairs % kXcds == 0) ? 2 : 1;
+    }
+    s_flag = flag;
+  }
+  __syncthreads();
+  const int flag = s_flag;
+
+  if (flag) {
+    // ---- combine: unit u = (head u / ND, dim block u % ND) ----
+    // k waves of one workgroup share a unit (k = the power of two <= W that
+    // spreads the U units over the S * W waves), wave wl of the group reading
+    // splits wl, wl + k, ...; groups of k waves take units gi, gi + S * W / k, ..
+    int k = 1;
+    while (2 * k <= W && 2 * k * U <= S * W) k *= 2;
+    const int gpw = W / k;                       // wave groups per workgroup
+    const int gi = s * gpw + wave / k, wl = wave % k;
+    const int stride = S * gpw;
+    const int rounds = (U + stride - 1) / stride;
+    f32x4_t* xc = reinterpret_cast<f32x4_t*>(lds);  // [wave][5][lane]
+    for (int rd = 0; rd < rounds; ++rd) {
+      const int u = gi + rd * stride;
+      const bool has_unit = u < U;
+      const int uh = has_unit ? u / ND : 0, udb = has_unit ? u % ND : 0;
+      float Ms = kNeg, T = 0.f;
+      f32x4_t acc[4];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) acc[gq] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int sp0 = wl; has_unit && sp0 < S; sp0 += k * kCombineBatch) {
+        f32x4_t v[kCombineBatch][4];
+        float mm[kCombineBatch], ll[kCombineBatch];
+#pragma unroll
+        for (int b = 0; b < kCombineBatch; ++b) {
+          const int sp = sp0 + k * b;
+          bool has = sp < S;
+          if (has && sp > 0) {
+            int a0, a1;
+            split_range(sp, p.cps, np, a0, a1);
+            has = a1 > a0;
+          }
+          const unsigned hb =
+              has ? pair_base + (unsigned)(((size_t)sp * split_floats + (size_t)uh * kHeadStride) * 4) : kOob;
+          const unsigned mo = hb + (has ? (unsigned)(ND * 64 * 16 * 4) : 0u);
+          float mv, lv;
+          if (flag == 2) {
+            mv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(mo + 4 * c), 0, kSc0));
+            lv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(mo + 4 * (32 + c)), 0, kSc0));
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+              v[b][gq] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                  prs, (int)(hb + (unsigned)(((udb * 4 + gq) * 64 + lane) * 16)), 0, kSc0));
+          } else {
+            mv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(mo + 4 * c), 0, kSc1));
+            lv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(mo + 4 * (32 + c)), 0, kSc1));
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+              v[b][gq] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                  prs, (int)(hb + (unsigned)(((udb * 4 + gq) * 64 + lane) * 16)), 0, kSc1));
+          }
+          mm[b] = has ? mv : kNeg;
+          ll[b] = has ? lv : 0.f;
+        }
+        float gm = Ms;
+#pragma unroll
+        for (int b = 0; b < kCombineBatch; ++b) gm = fmaxf(gm, mm[b]);
+        const float rsc = fast_exp2(Ms - gm);
+        T *= rsc;
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) acc[gq] *= rsc;
+#pragma unroll
+        for (int b = 0; b < kCombineBatch; ++b) {
+          const float w = mm[b] > 0.5f * kNeg ? fast_exp2(mm[b] - gm) : 0.f;
+          T += w * ll[b];
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) acc[gq] += w * v[b][gq];
+        }
+        Ms = gm;
+      }
+      // merge the group's k waves in wave order
+      if (k > 1) {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) xc[(wave * 5 + gq) * 64 + lane] = acc[gq];
+        xc[(wave * 5 + 4) * 64 + lane] = f32x4_t{Ms, T, 0.f, 0.f};
+        __syncthreads();
+      }
+      if (has_unit && wl == 0) {
+        float y[16], tot;
+        if (k > 1) {
+          float M = kNeg;
+          for (int w = wave; w < wave + k; ++w) M = fmaxf(M, xc[(w * 5 + 4) * 64 + lane][0]);
+          tot = 0.f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) y[i] = 0.f;
+          for (int w = wave; w < wave + k; ++w) {
+            const f32x4_t mt = xc[(w * 5 + 4) * 64 + lane];
+            const float f = mt[0] > 0.5f * kNeg ? fast_exp2(mt[0] - M) : 0.f;
+            tot += f * mt[1];
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const f32x4_t x = xc[(w * 5 + gq) * 64 + lane];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) y[4 * gq + i] += f * x[i];
+            }
+          }
+        } else {
+          tot = T;
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[4 * gq + i] = acc[gq][i];
+        }
+        const float inv = tot > 0.f ? 1.0f / tot : 0.f;
+        write_unit<D, GATE>(p, g * G + uh, udb, rb, L, c, h, y, inv);
+      }
+      if (k > 1) __syncthreads();
+    }
+  }
+
+  // second phase: the last workgroup to pass the combine returns the counter to zero
+  if (threadIdx.x == 0) {
+    const int old = arrive_add(cnt, 1);
+    if ((old & (kForeign - 1)) == 2 * S - 1) reset_counter(cnt);
+  }
+}
+
 }  // namespace dtree
 
 using namespace dtree;
 
-constexpr size_t kSepCombineBytes = 128 * 1024;
-
-static int attn_max_chunks(int head_dim, int max_past, int nt) {
+static int attn_max_pchunks(int head_dim, int max_past) {
   const int ck = chunk_keys(head_dim);
-  return nt + (max_past + ck - 1) / ck;
-}
-static int attn_splits(int head_dim, int max_past, int nt) {
-  return (attn_max_chunks(head_dim, max_past, nt) + kWaves - 1) / kWaves;
+  return (max_past + ck - 1) / ck;
 }
 
-extern "C" size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length,
-                                                  int32_t rows_padded) {
+// Prefix chunks per split and splits per (group, query block): kDefaultCps
+// chunks per split, plus the tree split, as many splits as
+// fit next to the other pairs in one resident grid (at most one workgroup per
+// CU; more chunks per split when the prefix needs it).
+// DTREE_ATTN_CHUNKS_PER_SPLIT=n asks for n instead (tuning).
+constexpr int kDefaultCps = 2;
+static void attn_splits(int head_dim, int max_past, int pairs, int cus, int& S, int& cps) {
+  const int npc = attn_max_pchunks(head_dim, max_past);
+  cps = kDefaultCps;
+  if (const char* e = std::getenv("DTREE_ATTN_CHUNKS_PER_SPLIT")) cps = std::max(1, std::atoi(e));
+  const int cap = cus / pairs;  // >= 2, checked by the caller
+  if (1 + (npc + cps - 1) / cps > cap) cps = (npc + cap - 2) / (cap - 1);
+  S = 1 + (npc + cps - 1) / cps;
+}
+
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+static size_t group_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length,
+                                              int32_t rows_padded) {
   if (num_heads <= 0 || head_dim <= 0 || max_past_length < 0 || rows_padded <= 0 || rows_padded % 32) return 0;
   const int nt = rows_padded / 32;
-  const size_t stride = (size_t)32 * head_dim + 64;
-  const size_t hb = (size_t)num_heads * nt;  // (head, query block) pairs
-  return ((hb * sizeof(int) + 255) & ~(size_t)255) +
-         hb * attn_splits(head_dim, max_past_length, nt) * stride * sizeof(float);
+  const size_t head_floats = (size_t)(head_dim / 32) * 64 * 16 + 64;
+  // splits never exceed one per prefix chunk plus the tree split
+  const size_t splits = 1 + (size_t)attn_max_pchunks(head_dim, max_past_length);
+  return kWsHeader + (size_t)num_heads * nt * splits * head_floats * sizeof(float);
 }
 
-extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
+static int group_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a, "attention: null args");
   DTREE_REQUIRE(a->qkv && a->rope_cos && a->rope_sin && a->k_pages && a->v_pages && a->page_table && a->desc &&
                     a->out && a->workspace,
@@ -1029,6 +856,8 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
                 "attention: rows_padded must be 32, 64, 96 or 128");
   const int nt = a->rows_padded / 32;
   DTREE_REQUIRE(a->num_kv_heads > 0 && a->num_heads % a->num_kv_heads == 0, "attention: num_heads % num_kv_heads");
+  const int G = a->num_heads / a->num_kv_heads;
+  DTREE_REQUIRE(G == 2 || G == 4 || (G == 8 && D == 128), "attention: GQA group of 2, 4 or 8 (8: head_dim 128)");
   DTREE_REQUIRE(a->max_past_length >= 0 && a->max_past_length <= kMaxPast, "attention: max_past_length beyond 16384");
   const int q_stride = gated ? 2 * D : D;
   DTREE_REQUIRE(a->ld_qkv >= a->num_heads * q_stride + 2 * a->num_kv_heads * D && a->ld_qkv % 4 == 0,
@@ -1037,12 +866,16 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
                 "attention: ld_out below num_heads * head_dim or not a multiple of 8");
   DTREE_REQUIRE(((uintptr_t)a->out & 15) == 0 && ((uintptr_t)a->out_lo & 15) == 0 && ((uintptr_t)a->qkv & 15) == 0,
                 "attention: qkv, out and out_lo must be 16-byte aligned");
-  DTREE_REQUIRE(a->workspace_bytes >= dtree_attention_workspace_bytes(a->num_heads, D, a->max_past_length,
+  DTREE_REQUIRE(a->workspace_bytes >= group_attention_workspace_bytes(a->num_heads, D, a->max_past_length,
                                                                       a->rows_padded),
                 "attention: workspace too small");
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
                     (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * D && a->ld_out % 64 == 0),
                 "attention: tiled out needs ld_out == num_heads * head_dim");
+  const int pairs = a->num_kv_heads * nt;
+  const int cus = device_cus();
+  DTREE_REQUIRE(pairs <= kMaxPairs && 2 * pairs <= cus,
+                "attention: num_kv_heads * rows_padded / 32 must leave two splits per pair within the CU count");
   AttnParams p{};
   p.qkv = a->qkv; p.ld_qkv = a->ld_qkv;
   p.q_stride = q_stride; p.k_off = a->num_heads * q_stride; p.v_off = p.k_off + a->num_kv_heads * D;
@@ -1051,34 +884,61 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
   p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
   p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
   p.out_tiled = a->out_layout == DTREE_W_TILED;
-  p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.tree_chunks = nt;
-  p.max_chunks = attn_max_chunks(D, a->max_past_length, nt);
-  p.splits = attn_splits(D, a->max_past_length, nt);
+  p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.NT = nt;
+  p.max_pchunks = attn_max_pchunks(D, a->max_past_length);
+  p.max_past = a->max_past_length;
+  attn_splits(D, a->max_past_length, pairs, cus, p.S, p.cps);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.off_xcd = off_xcd_test();
-  p.counters = reinterpret_cast<int*>(a->workspace);
-  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) +
-                                    (((size_t)a->num_heads * nt * sizeof(int) + 255) & ~(size_t)255));
-  const int G = p.Hq / p.Hkv;
-  const int pairs = p.splits * p.Hkv;
-  const int grid = ((pairs + 7) / 8) * 8 * G * nt;  // nt query blocks of ((pairs+7)/8)*8*G workgroups
-  const bool one = nt == 1;
-  // Long prefixes combine in a launch of their own (attn_combine_kernel):
-  // when the last arriver alone would read more than 128 KB of partials.
-  p.sep_combine = (size_t)p.splits * 32 * D * sizeof(float) > kSepCombineBytes;
+  p.err = reinterpret_cast<int*>(a->workspace);
+  p.counters = reinterpret_cast<int*>(reinterpret_cast<char*>(a->workspace) + 64);
+  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kWsHeader);
+  const int grid = pairs * p.S;
   if (D == 128) {
-    if (one) tree_attn_kernel<128, 128, false, 1><<<grid, 64 * kWaves, 0, stream>>>(p);
-    else tree_attn_kernel<128, 128, false, 4><<<grid, 64 * kWaves, 0, stream>>>(p);
+    if (G == 2) gqa_tree_attn_kernel<128, 128, false, 2><<<grid, 64 * 2, 0, stream>>>(p);
+    else if (G == 4) gqa_tree_attn_kernel<128, 128, false, 4><<<grid, 64 * 4, 0, stream>>>(p);
+    else gqa_tree_attn_kernel<128, 128, false, 8><<<grid, 64 * 8, 0, stream>>>(p);
   } else {
-    if (one) tree_attn_kernel<256, 64, true, 1><<<grid, 64 * kWaves, 0, stream>>>(p);
-    else tree_attn_kernel<256, 64, true, 4><<<grid, 64 * kWaves, 0, stream>>>(p);
+    if (G == 2) gqa_tree_attn_kernel<256, 64, true, 2><<<grid, 64 * 2, 0, stream>>>(p);
+    else gqa_tree_attn_kernel<256, 64, true, 4><<<grid, 64 * 4, 0, stream>>>(p);
   }
   DTREE_LAUNCH_CHECK("attention launch");
-  if (p.sep_combine) {
-    const int cgrid = p.Hq * nt * (D / 32);
-    if (D == 128) attn_combine_kernel<128, false><<<cgrid, 64 * kWaves, 0, stream>>>(p);
-    else attn_combine_kernel<256, true><<<cgrid, 64 * kWaves, 0, stream>>>(p);
-    DTREE_LAUNCH_CHECK("attention combine launch");
-  }
   return DTREE_OK;
+}
+
+// ---- entry points: per-head or per-KV-group kernel ----------------------------
+// Two designs cover the prefix range. The per-head kernel (attention_head.hip:
+// a workgroup per (query head, four chunks), last-arriver combine) has the
+// shorter fixed latency; the per-KV-group kernel above loads every K/V chunk
+// once for the group's G heads and wins once the prefix stream dominates.
+// Measured on MI355X (Qwen3-4B layer, 25-node tree, us per launch, per-head /
+// per-group): P 128: 11.1 / 24.6; 512: 15.8 / 19.1; 1024: 16.3 / 19.7;
+// 2048: 24.2 / 21.5; 4096: 36.0 / 25.7. The choice follows the prefix the grid
+// is sized for; DTREE_ATTN_KERNEL=head|group forces one (tests).
+namespace dtree {
+size_t head_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length,
+                                      int32_t rows_padded);
+int head_tree_attention(const DtreeAttnArgs* a, hipStream_t stream);
+}  // namespace dtree
+
+constexpr int kGroupKernelMinPast = 1536;
+
+static bool use_group_kernel(const DtreeAttnArgs* a) {
+  if (const char* e = std::getenv("DTREE_ATTN_KERNEL")) {
+    if (e[0] == 'g') return true;
+    if (e[0] == 'h') return false;
+  }
+  return a->max_past_length > kGroupKernelMinPast;
+}
+
+extern "C" size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length,
+                                                  int32_t rows_padded) {
+  const size_t a = group_attention_workspace_bytes(num_heads, head_dim, max_past_length, rows_padded);
+  const size_t b = dtree::head_attention_workspace_bytes(num_heads, head_dim, max_past_length, rows_padded);
+  return a > b ? a : b;
+}
+
+extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
+  DTREE_REQUIRE(a, "attention: null args");
+  return use_group_kernel(a) ? group_tree_attention(a, stream) : dtree::head_tree_attention(a, stream);
 }

@@ -1,0 +1,1088 @@
+// Ancestor-masked GQA tree attention over a paged bf16 KV prefix.
+//
+// Work split: a workgroup serves one 32-row block of tree queries (rows
+// 32*rb .. 32*rb+31) of one query head. The keys are cut into chunks: chunks
+// 0 .. NT-1 are the tree itself in 32-key blocks (NT = rows_padded / 32;
+// ancestor-or-self mask, word tc of each query's bitset), chunks NT.. are runs
+// of CK prefix keys (fully visible): a 64-key page for head_dim 128, half a
+// page for head_dim 256 (same registers per wave). A workgroup has four
+// waves, one chunk each, so workgroup `split` owns chunks 4*split .. 4*split+3.
+//
+// Two head geometries are compiled: Qwen3 (head_dim 128, full RoPE) and the
+// gated attention of Qwen3.5 (head_dim 256, RoPE on the first 64 dims, q_proj
+// rows per head = [q | gate], output multiplied by sigmoid(gate)).
+// A wave owns exactly one chunk, so its softmax needs no running rescale: it
+// issues Q's loads, then all K and V of its page (32 KB in flight per wave),
+// scores both 32-key blocks, takes one max and accumulates P V.
+// The four waves merge in LDS; when a head needs more than one workgroup,
+// each writes a merged partial (row max, row sum, unnormalised output) and the
+// last one to arrive (device-scope counter) combines them, all 256 threads
+// with independent loads. The heads of one KV group run on one XCD
+// (blockIdx % 8), so their shared K/V reads meet in one L2.
+//
+// MFMA use (v_mfma_f32_32x32x16_bf16), with the tree rows (<= 32) as one
+// MFMA dimension:
+//   S^T = K Q^T : A = 32 keys x 16 dims, B = 16 dims x 32 queries. A lane owns
+//                 query column lane%32, so softmax statistics are lane-local
+//                 (16 registers + one exchange with lane^32).
+//   O^T = V^T P^T: A = V^T (32 dims x 16 keys), B = P^T taken straight from
+//                 the S^T registers. A-row rho of S^T is loaded from key
+//                 pi(rho) = rho with bits 2 and 3 swapped; then register r of
+//                 a lane in half h holds key 16*(r/8) + 8*h + r%8, i.e. eight
+//                 consecutive keys per PV step, which is one 16-byte read of
+//                 the transposed V page.
+// K pages are [page][kv_head][64][D]; V pages are [page][kv_head][D][64].
+#include "common.h"
+
+namespace dtree {
+namespace head_attn {
+
+constexpr int kWaves = 4;          // waves (chunks) per workgroup
+constexpr int kMaxPast = 16384;    // longest prefix the grid is sized for
+// Prefix keys per chunk.
+__host__ __device__ constexpr int chunk_keys(int D) { return D <= 128 ? DTREE_PAGE : DTREE_PAGE / 2; }
+constexpr float kNeg = -1e30f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnParams {
+  const float* qkv; int ld_qkv;
+  int q_stride, k_off, v_off;  // qkv row: q of head h at h*q_stride (gate at +D), k / v of group g at k_off / v_off + g*D
+  const uint16_t* q_norm; const uint16_t* k_norm; float eps;
+  const float* rope_cos; const float* rope_sin;
+  uint16_t* kp; uint16_t* vp; const int* page_table;
+  const DtreeStepDesc* desc;
+  uint16_t* out; uint16_t* out_lo; int ld_out; int out_tiled;
+  int Hq, Hkv, max_chunks, splits;
+  int tree_chunks;  // 32-key tree chunks = 32-row query blocks = rows_padded / 32
+  float scale_log2;
+  int write_cache;
+  float* part; int* counters;
+  int sep_combine;  // partials are combined by attn_combine_kernel (long prefixes)
+  int off_xcd;      // test hook: treat every workgroup as off its expected XCD
+};
+
+__device__ __forceinline__ int swap_bits23(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
+
+// Raw operands of one head row for lane (c, h), which owns dims 16j + 8h + i:
+// the fp32 values, the bf16 RMSNorm weights and the RoPE cos/sin of the first
+// half of the R rotated dims. Issuing all loads before any use lets a wave
+// keep them in flight together with the K/V loads that follow.
+template <int D, int R>
+struct HeadRow {
+  f32x4_t x[D / 16][2];
+  u32x4_t nw[D / 16];
+  f32x4_t cs[R / 32][2], sn[R / 32][2];
+};
+
+// AUX: also the norm weights and the RoPE cos/sin (q and k rows; v has
+// none). Without norm weights the loads read the row itself instead and
+// row_finish ignores them, so the loads never branch: the whole prologue
+// stays one basic block and its loads go out in one round trip.
+template <int D, int R, bool AUX>
+__device__ __forceinline__ void row_issue(HeadRow<D, R>& r, const float* src, const uint16_t* norm_w, const float* cosr,
+                                          const float* sinr, int h) {
+  const uint16_t* nwp = norm_w ? norm_w : reinterpret_cast<const uint16_t*>(src);
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) {
+    r.x[j][0] = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h);
+    r.x[j][1] = *reinterpret_cast<const f32x4_t*>(src + 16 * j + 8 * h + 4);
+    if constexpr (AUX) r.nw[j] = ld_u32x4(nwp + 16 * j + 8 * h);
+  }
+  if constexpr (AUX) {
+#pragma unroll
+    for (int j = 0; j < R / 32; ++j)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        r.cs[j][u] = *reinterpret_cast<const f32x4_t*>(cosr + 16 * j + 8 * h + 4 * u);
+        r.sn[j][u] = *reinterpret_cast<const f32x4_t*>(sinr + 16 * j + 8 * h + 4 * u);
+      }
+  }
+}
+
+// RMSNorm over D (sum of squares completed with the partner lane^32), then
+// RoPE on (dim d, dim d + R/2) pairs for d < R/2, which live in the same lane
+// (registers j and j + R/32); dims >= R pass through.
+template <int D, int R>
+__device__ __forceinline__ void row_finish(const HeadRow<D, R>& r, bool norm, bool rope, float eps,
+                                           float (&v)[D / 16][8]) {
+  constexpr int NJ = D / 16;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[j][i] = r.x[j][0][i];
+      v[j][i + 4] = r.x[j][1][i];
+    }
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += v[j][i] * v[j][i];
+    ss += __shfl_xor(ss, 32);
+    const float rs = rsqrtf(ss * (1.0f / D) + eps);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t w = r.nw[j][i >> 1];
+        v[j][i] *= rs * __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+      }
+  }
+  if (rope) {
+    constexpr int RJ = R / 32;
+#pragma unroll
+    for (int j = 0; j < RJ; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float cs = r.cs[j][i >> 2][i & 3], sn = r.sn[j][i >> 2][i & 3];
+        const float x1 = v[j][i], x2 = v[j + RJ][i];
+        v[j][i] = x1 * cs - x2 * sn;
+        v[j + RJ][i] = x1 * sn + x2 * cs;
+      }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void pack_frag(const float (&v)[D / 16][8], u32x4_t (&f)[D / 16]) {
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j)
+    f[j] = u32x4_t{pack_bf2(v[j][0], v[j][1]), pack_bf2(v[j][2], v[j][3]), pack_bf2(v[j][4], v[j][5]),
+                   pack_bf2(v[j][6], v[j][7])};
+}
+
+// v = hi + lo with hi = bf16(v), lo = bf16(v - hi): about 16 significant bits
+// through two bf16 MFMAs.
+__device__ __forceinline__ void split8(const float* v, u32x4_t& hi, u32x4_t& lo) {
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = v[i] - bf2f(f2bf(v[i]));
+  hi = u32x4_t{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7])};
+  lo = u32x4_t{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+}
+
+// P.V step s2 of a 32-key block: B operand = probabilities of registers
+// 8*s2 .. 8*s2+7 (split hi/lo), A operand = V^T fragments.
+template <int ND>
+__device__ __forceinline__ void pv_step(const f32x16_t& p, int s2, const u32x4_t (&va)[ND], f32x16_t (&o)[ND]) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = p[8 * s2 + i];
+  u32x4_t ph, pl;
+  split8(v, ph, pl);
+#pragma unroll
+  for (int db = 0; db < ND; ++db) {
+    o[db] = mfma32(va[db], ph, o[db]);
+    o[db] = mfma32(va[db], pl, o[db]);
+  }
+}
+
+// Softmax numerators of NB 32-key blocks that start a chunk: every wave owns
+// exactly one chunk, so the running max starts here and no rescale exists.
+// s[] is already scaled (log2 units) and masked (kNeg).
+template <int NB>
+__device__ __forceinline__ void softmax_fresh(f32x16_t (&s)[NB], float& m_run, float& l_run) {
+  float bmax = kNeg;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) bmax = fmaxf(bmax, s[b][r]);
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+  float lsum = 0.f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[b][r] = fast_exp2(s[b][r] - bmax);
+      lsum += s[b][r];
+    }
+  m_run = bmax;
+  l_run = lsum;
+}
+
+// Zeroes the bf16 elements of a V^T fragment whose key (first + e) is >= end:
+// keys past the prefix may hold stale or non-finite data, and 0 * NaN would
+// reach the output through the PV MFMA.
+__device__ __forceinline__ u32x4_t mask_keys(u32x4_t v, int first, int end) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo_ok = (first + 2 * i) < end ? 0xffffu : 0u;
+    const uint32_t hi_ok = (first + 2 * i + 1) < end ? 0xffff0000u : 0u;
+    v[i] &= lo_ok | hi_ok;
+  }
+  return v;
+}
+
+template <int D, int R>
+__device__ __forceinline__ void q_fragments(const HeadRow<D, R>& qr, bool norm, float eps, u32x4_t (&qf)[D / 16],
+                                            u32x4_t (&ql)[D / 16]) {
+  float q[D / 16][8];
+  row_finish<D, R>(qr, norm, true, eps, q);
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) split8(q[j], qf[j], ql[j]);
+}
+
+// ---- query rows staged once per workgroup -----------------------------------
+// The four waves of a workgroup score the same 32 query rows of one head, so
+// the rows are loaded, normalised and rotated once: thread (row r = t / 8,
+// part j = t % 8) owns
+// * head_dim 128 (RoPE pairs (d, d + 64)): dims 8j .. 8j+7 and 64+8j .. +7;
+// * head_dim 256 (RoPE on dims 0..63, pairs (d, d + 32)): dims 4j .. 4j+3,
+//   32+4j .. +3 and the unrotated 64+24j .. 64+24j+23;
+// so each RoPE pair stays in one thread, and the RMSNorm sum of squares is
+// completed over the row's 8 threads with DPP. The rows go to LDS, from which
+// each wave reads its MFMA fragments. The row stride (D + 4 floats) keeps
+// those 32-byte fragment reads apart in the LDS banks.
+template <int D>
+__host__ __device__ constexpr int qs_stride() { return D + 4; }
+template <int D> struct QStage;
+template <> struct QStage<128> {
+  f32x4_t x[4];
+  u32x4_t nw[2];
+  f32x4_t cs[2], sn[2];
+};
+template <> struct QStage<256> {
+  f32x4_t x[8];      // rotated pair halves [4j, +4), [32+4j, +4); then 64+24j .. +24
+  u32x2_t nwr[2];    // norm weights of the rotated dims
+  u32x4_t nwp[3];    // of the unrotated dims
+  f32x4_t cs, sn;    // RoPE entries 4j .. 4j+3
+};
+
+template <int D>
+__device__ __forceinline__ void q_stage_issue(const AttnParams& p, int hq, int rb, QStage<D>& q) {
+  const int t = threadIdx.x, r = t >> 3, j = t & 7;
+  const int row = 32 * rb + r;
+  const float* src = p.qkv + (size_t)row * p.ld_qkv + hq * p.q_stride;
+  // without q_norm the weight loads read the row itself (ignored below)
+  const uint16_t* nwb = p.q_norm ? p.q_norm : reinterpret_cast<const uint16_t*>(src);
+  if constexpr (D == 128) {
+    q.x[0] = *reinterpret_cast<const f32x4_t*>(src + 8 * j);
+    q.x[1] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 4);
+    q.x[2] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 64);
+    q.x[3] = *reinterpret_cast<const f32x4_t*>(src + 8 * j + 68);
+    q.nw[0] = ld_u32x4(nwb + 8 * j);
+    q.nw[1] = ld_u32x4(nwb + 8 * j + 64);
+    const float* cr = p.rope_cos + row * 64 + 8 * j;
+    const float* sr = p.rope_sin + row * 64 + 8 * j;
+    q.cs[0] = *reinterpret_cast<const f32x4_t*>(cr);
+    q.cs[1] = *reinterpret_cast<const f32x4_t*>(cr + 4);
+    q.sn[0] = *reinterpret_cast<const f32x4_t*>(sr);
+    q.sn[1] = *reinterpret_cast<const f32x4_t*>(sr + 4);
+  } else {
+    q.x[0] = *reinterpret_cast<const f32x4_t*>(src + 4 * j);
+    q.x[1] = *reinterpret_cast<const f32x4_t*>(src + 32 + 4 * j);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) q.x[2 + i] = *reinterpret_cast<const f32x4_t*>(src + 64 + 24 * j + 4 * i);
+    q.nwr[0] = *reinterpret_cast<const u32x2_t*>(nwb + 4 * j);
+    q.nwr[1] = *reinterpret_cast<const u32x2_t*>(nwb + 32 + 4 * j);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) q.nwp[i] = ld_u32x4(nwb + 64 + 24 * j + 8 * i);
+    q.cs = *reinterpret_cast<const f32x4_t*>(p.rope_cos + row * 32 + 4 * j);
+    q.sn = *reinterpret_cast<const f32x4_t*>(p.rope_sin + row * 32 + 4 * j);
+  }
+}
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+template <int D>
+__device__ __forceinline__ void q_stage_finish(const QStage<D>& q, bool norm, float eps, float* qs) {
+  const int t = threadIdx.x, r = t >> 3, j = t & 7;
+  constexpr int NV = D / 8;  // values per thread
+  float v[NV];
+#pragma unroll
+  for (int k = 0; k < NV / 4; ++k)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[4 * k + i] = q.x[k][i];
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) ss += v[i] * v[i];
+    ss += dpp<0xB1>(ss);   // lane ^ 1
+    ss += dpp<0x4E>(ss);   // lane ^ 2
+    ss += dpp<0x141>(ss);  // the other quad of the row's 8 lanes
+    const float rs = rsqrtf(ss * (1.0f / D) + eps);
+    if constexpr (D == 128) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w = q.nw[i >> 3][(i & 7) >> 1];
+        v[i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t w = q.nwr[i >> 2][(i & 3) >> 1];
+        v[i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
+      }
+#pragma unroll
+      for (int i = 0; i < 24; ++i) {
+        const uint32_t w = q.nwp[i >> 3][(i & 7) >> 1];
+        v[8 + i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
+      }
+    }
+  }
+  constexpr int NR = D == 128 ? 8 : 4;  // rotated pairs per thread
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    float cs, sn;
+    if constexpr (D == 128) {
+      cs = q.cs[i >> 2][i & 3];
+      sn = q.sn[i >> 2][i & 3];
+    } else {
+      cs = q.cs[i];
+      sn = q.sn[i];
+    }
+    const float x1 = v[i], x2 = v[NR + i];
+    v[i] = x1 * cs - x2 * sn;
+    v[NR + i] = x1 * sn + x2 * cs;
+  }
+  float* dst = qs + r * qs_stride<D>();
+  if constexpr (D == 128) {
+    *reinterpret_cast<f32x4_t*>(dst + 8 * j) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 64) = f32x4_t{v[8], v[9], v[10], v[11]};
+    *reinterpret_cast<f32x4_t*>(dst + 8 * j + 68) = f32x4_t{v[12], v[13], v[14], v[15]};
+  } else {
+    *reinterpret_cast<f32x4_t*>(dst + 4 * j) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(dst + 32 + 4 * j) = f32x4_t{v[4], v[5], v[6], v[7]};
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+      *reinterpret_cast<f32x4_t*>(dst + 64 + 24 * j + 4 * i) =
+          f32x4_t{v[8 + 4 * i], v[9 + 4 * i], v[10 + 4 * i], v[11 + 4 * i]};
+  }
+}
+
+// Lane (c, h)'s q fragment j (dims 16j + 8h .. +7 of query row c) from the
+// staged rows, split hi / lo.
+template <int D>
+__device__ __forceinline__ void q_frag_one(const float* qs, int c, int h, int j, u32x4_t& qf, u32x4_t& ql) {
+  const float* src = qs + c * qs_stride<D>() + 16 * j + 8 * h;
+  const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
+  const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + 4);
+  const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  split8(v, qf, ql);
+}
+template <int D>
+__device__ __forceinline__ void q_frag_lds(const float* qs, int c, int h, u32x4_t (&qf)[D / 16],
+                                           u32x4_t (&ql)[D / 16]) {
+#pragma unroll
+  for (int j = 0; j < D / 16; ++j) q_frag_one<D>(qs, c, h, j, qf[j], ql[j]);
+}
+
+// Tree chunk tc: k (norm + RoPE) and v of nodes 32*tc .. 32*tc+31 come from
+// the fused qkv rows and are staged in LDS (this wave's private region) for
+// the MFMA operand layouts; the block's 32 query rows are scored against them
+// with word tc of their ancestor-or-self masks, and k/v are written to the
+// cache rows P + node (once: query block 0, first head of the group).
+// q, k and v are finished one after the other, so at most one raw head row is
+// live in registers (head_dim 256 rows are 128 floats per lane pair).
+template <int D, int R, bool QS>
+__device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs, int hq, int g,
+                                           int G, int P, int L, int tc, int qrow, bool write_rows, int c, int h,
+                                           uint16_t* ks, uint16_t* vt, float& m_run, float& l_run,
+                                           f32x16_t (&o)[D / 32]) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  constexpr int KS = D + 8, VS = 32 + 8;
+  constexpr int half_r = R / 2;
+  // Lane (c, h) stages key node 32*tc + c and owns query row qrow.
+  const int node = 32 * tc + c;
+  const float* row = p.qkv + (size_t)node * p.ld_qkv;
+  const float* cosr = p.rope_cos + node * half_r;
+  const float* sinr = p.rope_sin + node * half_r;
+  const uint32_t anc = p.desc->ancestors[qrow][tc];
+  // Staged head_dim-256 rows are read one fragment at a time in the QK^T
+  // loop (16 fragments would hold 128 registers).
+  constexpr bool PERJ = QS && D > 128;
+  u32x4_t qf[PERJ ? 1 : NJ], ql[PERJ ? 1 : NJ];
+  if constexpr (!QS) {
+    row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm, p.rope_cos + qrow * half_r,
+                          p.rope_sin + qrow * half_r, h);
+    q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  } else if constexpr (!PERJ) {
+    q_frag_lds<D>(qs, c, h, qf, ql);
+  }
+  u32x4_t kf8[NJ], vf8[NJ];
+  if constexpr (D <= 128) {
+    // Both raw rows in flight together: one round trip instead of two.
+    HeadRow<D, R> kr, vr;
+    row_issue<D, R, true>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
+    row_issue<D, R, false>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
+    float kv[NJ][8], vv[NJ][8];
+    row_finish<D, R>(kr, p.k_norm != nullptr, true, p.eps, kv);
+    pack_frag<D>(kv, kf8);
+    row_finish<D, R>(vr, false, false, 0.f, vv);
+    pack_frag<D>(vv, vf8);
+  } else {
+    {
+      HeadRow<D, R> kr;
+      row_issue<D, R, true>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
+      float kv[NJ][8];
+      row_finish<D, R>(kr, p.k_norm != nullptr, true, p.eps, kv);
+      pack_frag<D>(kv, kf8);
+    }
+    {
+      HeadRow<D, R> vr;
+      row_issue<D, R, false>(vr, row + p.v_off + g * D, nullptr, nullptr, nullptr, h);
+      float vv[NJ][8];
+      row_finish<D, R>(vr, false, false, 0.f, vv);
+      pack_frag<D>(vv, vf8);
+    }
+  }
+  if (node >= L) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) vf8[j] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    *reinterpret_cast<u32x4_t*>(&ks[c * KS + 16 * j + 8 * h]) = kf8[j];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t word = vf8[j][i >> 1];
+      vt[(16 * j + 8 * h + i) * VS + c] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
+    }
+  }
+  // Only this wave touches ks/vt, and a wave's LDS operations complete in
+  // order: waiting for them (and fencing the compiler) suffices.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int kr_row = swap_bits23(c);
+  f32x16_t s[1];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s[0][r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[kr_row * KS + 16 * j + 8 * h]);
+    if constexpr (PERJ) {
+      u32x4_t f, l;
+      q_frag_one<D>(qs, c, h, j, f, l);
+      s[0] = mfma32(a, f, s[0]);
+      s[0] = mfma32(a, l, s[0]);
+    } else {
+      s[0] = mfma32(a, qf[j], s[0]);
+      s[0] = mfma32(a, ql[j], s[0]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int t = 16 * (r >> 3) + 8 * h + (r & 7);
+    const bool ok = qrow < L && 32 * tc + t < L && ((anc >> t) & 1u);
+    s[0][r] = ok ? s[0][r] * p.scale_log2 : kNeg;
+  }
+  softmax_fresh<1>(s, m_run, l_run);
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    u32x4_t va[ND];
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+      va[db] = *reinterpret_cast<const u32x4_t*>(&vt[(32 * db + c) * VS + 16 * s2 + 8 * h]);
+    pv_step<ND>(s[0], s2, va, o);
+  }
+  if (p.write_cache && (hq % G) == 0 && write_rows && node < L) {
+    const int pos = P + node;
+    const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
+    uint16_t* krow = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off) * D;
+    uint16_t* vcol = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      *reinterpret_cast<u32x4_t*>(krow + 16 * j + 8 * h) = kf8[j];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t word = vf8[j][i >> 1];
+        vcol[(size_t)(16 * j + 8 * h + i) * DTREE_PAGE] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
+      }
+    }
+  }
+}
+
+// One prefix chunk = CK consecutive keys inside one page (the whole page for
+// head_dim 128, half of it for 256): its K and V fragments, loaded by
+// prefix_issue and consumed by prefix_chunk. Keys past the
+// prefix in the last chunk are masked (scores) and zeroed (V), since the page
+// may hold stale or non-finite data there.
+template <int D>
+struct ChunkKV {
+  static constexpr int NJ = D / 16, ND = D / 32, NB = chunk_keys(D) / 32;
+  u32x4_t kf[NB][NJ];
+  u32x4_t vf[NB][2][ND];
+};
+
+template <int D>
+__device__ __forceinline__ void prefix_issue(const AttnParams& p, ChunkKV<D>& kv, int page, int g, int pc, int c,
+                                             int h) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  constexpr int CK = chunk_keys(D), NB = CK / 32;
+  const int po = (pc * CK) % DTREE_PAGE;
+  const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po + swap_bits23(c)) * D;
+  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) kv.kf[b][j] = ld_u32x4_stream(kbase + (size_t)32 * b * D + 16 * j + 8 * h);
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int db = 0; db < ND; ++db)
+        kv.vf[b][s2][db] = ld_u32x4_stream(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 32 * b + 16 * s2 + 8 * h);
+  }
+}
+
+template <int D, int R, bool QS>
+__device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs,
+                                             const ChunkKV<D>& kv, int P, int pc, int c, int h, float& m_run,
+                                             float& l_run, f32x16_t (&o)[D / 32]) {
+  constexpr int NJ = D / 16, ND = D / 32;
+  constexpr int CK = chunk_keys(D), NB = CK / 32;
+  const int k_begin = pc * CK;  // prefix chunk pc: keys pc*CK ..
+  const int k_end = min(k_begin + CK, P);
+  constexpr bool PERJ = QS && D > 128;  // staged head_dim 256: one fragment at a time
+  u32x4_t qf[PERJ ? 1 : NJ], ql[PERJ ? 1 : NJ];
+  if constexpr (!QS) q_fragments<D, R>(qr, p.q_norm != nullptr, p.eps, qf, ql);
+  else if constexpr (!PERJ) q_frag_lds<D>(qs, c, h, qf, ql);
+
+  f32x16_t s[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    u32x4_t f, l;
+    if constexpr (PERJ) q_frag_one<D>(qs, c, h, j, f, l);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      s[b] = mfma32(kv.kf[b][j], PERJ ? f : qf[PERJ ? 0 : j], s[b]);
+      s[b] = mfma32(kv.kf[b][j], PERJ ? l : ql[PERJ ? 0 : j], s[b]);
+    }
+  }
+  const bool ragged = k_end - k_begin < CK;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = k_begin + 32 * b + 16 * (r >> 3) + 8 * h + (r & 7);
+      s[b][r] = (!ragged || key < k_end) ? s[b][r] * p.scale_log2 : kNeg;
+    }
+  softmax_fresh<NB>(s, m_run, l_run);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      u32x4_t va[ND];
+      const int first = k_begin + 32 * b + 16 * s2 + 8 * h;
+#pragma unroll
+      for (int db = 0; db < ND; ++db)
+        va[db] = ragged ? mask_keys(kv.vf[b][s2][db], first, k_end) : kv.vf[b][s2][db];
+      pv_step<ND>(s[b], s2, va, o);
+    }
+}
+
+// Combine of a head's workgroup partials ([block][lane][16] floats, then m and
+// l of the 32 queries, per split) by the last workgroup to arrive: kSb splits
+// per round with every load of the round in flight (ranged loads past the
+// last split return zero) and a running max; AUX is the cache policy of the
+// loads (kSc0: all writers on this XCD, else kSc1).
+template <int D, int AUX>
+__device__ __forceinline__ void combine_splits(__amdgpu_buffer_rsrc_t prs, unsigned pbase, size_t stride, int nsplit,
+                                               int wave, int lane, int c, float& tot,
+                                               f32x16_t (&mine)[D / 32 / kWaves]) {
+  constexpr int NDW = D / 32 / kWaves;
+  constexpr int kSb = 8 / NDW;  // 8 splits per round at head_dim 128, 4 at 256
+  float Ms = kNeg;
+  tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < NDW; ++k)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mine[k][r] = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kSb) {
+    f32x4_t v[kSb][NDW][4];
+    float mm[kSb], ll[kSb];
+#pragma unroll
+    for (int b = 0; b < kSb; ++b) {
+      const bool ok = s0 + b < nsplit;
+      const unsigned so = ok ? pbase + (unsigned)((size_t)(s0 + b) * stride * sizeof(float)) : kOob;
+      const float mv = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(so + (32 * D + c) * 4), 0, AUX));
+      ll[b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)(so + (32 * D + 32 + c) * 4),
+                                                                            0, AUX));
+      mm[b] = ok ? mv : kNeg;
+#pragma unroll
+      for (int k = 0; k < NDW; ++k)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq)
+          v[b][k][gq] = __builtin_bit_cast(
+              f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                           prs, (int)(so + (unsigned)(((wave + kWaves * k) * 64 + lane) * 64 + 16 * gq)), 0, AUX));
+    }
+    float gm = Ms;
+#pragma unroll
+    for (int b = 0; b < kSb; ++b) gm = fmaxf(gm, mm[b]);
+    const float rsc = fast_exp2(Ms - gm);
+    tot *= rsc;
+#pragma unroll
+    for (int k = 0; k < NDW; ++k)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mine[k][r] *= rsc;
+#pragma unroll
+    for (int b = 0; b < kSb; ++b) {
+      const float w = fast_exp2(mm[b] - gm);
+      tot += w * ll[b];
+#pragma unroll
+      for (int k = 0; k < NDW; ++k)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mine[k][4 * gq + i] += w * v[b][k][gq][i];
+    }
+    Ms = gm;
+  }
+}
+
+// TB: tree chunks the LDS staging is sized for (1 for 32 rows, 4 up to 128).
+template <int D, int R, bool GATE, int TB>
+__global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
+  constexpr int ND = D / 32;  // 32-dim blocks of O^T
+  constexpr int KS = D + 8;   // padded LDS row of tree K
+  constexpr int VS = 32 + 8;  // padded LDS row of tree V^T
+  constexpr int kStage = (32 * KS + D * VS) * 2;   // one tree chunk's K / V^T staging
+  // Query rows are staged in LDS except for head_dim 256 with four tree
+  // chunks (their K/V staging leaves no room).
+  constexpr bool QS = D <= 128 || TB == 1;
+  constexpr int kQs = QS ? 32 * qs_stride<D>() * 4 : 0;  // staged query rows
+  constexpr int kMl = kWaves * 64 * 4;               // merge: per wave, m and l of 32 queries
+  constexpr int kMerge = kMl + ND * kWaves * 4 * 64 * 16;  // + [block][wave][4][lane] f32x4
+  constexpr int kChunkLds = TB * kStage + kQs;
+  constexpr int CK = chunk_keys(D);
+  __shared__ __align__(16) unsigned char lds[kChunkLds > kMerge ? kChunkLds : kMerge];
+  __shared__ int s_last;
+
+  // Every argument the prologue needs in scalar registers at once: one batch
+  // of argument loads and one wait, instead of a batch per basic block.
+  asm volatile("" ::"s"(p.qkv), "s"(p.ld_qkv), "s"(p.q_stride), "s"(p.q_norm), "s"(p.rope_cos), "s"(p.rope_sin),
+               "s"(p.kp), "s"(p.vp), "s"(p.page_table), "s"(p.desc), "s"(p.Hq), "s"(p.Hkv), "s"(p.max_chunks),
+               "s"(p.splits), "s"(p.tree_chunks), "s"(gridDim.x));
+  // blockIdx -> (query block, split, kv group, head in group): the G heads of
+  // one (split, group) pair share blockIdx % 8, i.e. one XCD.
+  const int G = p.Hq / p.Hkv, NT = p.tree_chunks;
+  const int per_block = (int)gridDim.x / NT;  // workgroups per query block (a multiple of 8)
+  const int rb = blockIdx.x / per_block, bid = blockIdx.x % per_block;
+  const int pair = (bid / (8 * G)) * 8 + (bid & 7);
+  // Padding workgroups (pair past splits * Hkv) still name an in-range head
+  // and a chunk past max_chunks; they return after the loads below are out,
+  // which keeps the argument loads in one round trip.
+  const int g = pair % p.Hkv, split = pair / p.Hkv;
+  const int hq = g * G + (bid >> 3) % G;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int chunk = split * kWaves + wave;
+  const int qrow = 32 * rb + c;  // this lane's query row
+  // Loads that do not depend on the step descriptor go out first, so their
+  // latency overlaps the descriptor read: the workgroup's query rows (values,
+  // norm weights, RoPE; 10 loads per thread) and the page of this wave's
+  // prefix chunk. The chunk's K/V follow the descriptor check: issued before
+  // it, they delay the descriptor's own (scalar) load by microseconds.
+  // (head_dim 256 with four tree chunks loads its q row per wave inside the
+  // chunk: there is no LDS left to stage it.)
+  const bool prefix_wave = chunk >= NT && chunk < p.max_chunks;
+  const int page = prefix_wave ? p.page_table[(chunk - NT) * CK / DTREE_PAGE] : 0;
+  HeadRow<D, R> qr;
+  QStage<D> qst;
+  if constexpr (QS) q_stage_issue<D>(p, hq, rb, qst);
+
+  if (pair >= p.splits * p.Hkv) return;
+  const int P = p.desc->past_length, L = p.desc->num_nodes;
+  const int nchunks = NT + (P + CK - 1) / CK;
+  // A descriptor beyond the grid's capacity (P > max_past_length) or with more
+  // rows than rows_padded leaves the output untouched instead of indexing past
+  // buffers.
+  if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;
+  const int nsplit = (nchunks + kWaves - 1) / kWaves;
+  if (split >= nsplit) return;
+  if (32 * rb >= L) {
+    // Query block past the tree: its output rows are zero (split 0 writes).
+    if (split == 0) {
+      const int q = threadIdx.x >> 3;
+      for (int dd = (threadIdx.x & 7) * 8; dd < D; dd += 64) {
+        const int col = hq * D + dd;
+        const int row = 32 * rb + q;
+        const size_t oi = p.out_tiled ? tiled_index(row, col, p.ld_out) : (size_t)row * p.ld_out + col;
+        *reinterpret_cast<u32x4_t*>(p.out + oi) = u32x4_t{0u, 0u, 0u, 0u};
+        if (p.out_lo) *reinterpret_cast<u32x4_t*>(p.out_lo + oi) = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+    return;
+  }
+
+  float* qs = reinterpret_cast<float*>(lds + TB * kStage);
+  if constexpr (QS) {
+    q_stage_finish<D>(qst, p.q_norm != nullptr, p.eps, qs);
+    __syncthreads();
+  }
+
+  float m_run = kNeg, l_run = 0.f;
+  f32x16_t o[ND];
+#pragma unroll
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+
+  if (chunk < NT) {
+    // Tree chunks are waves 0 .. NT-1 of split 0, each with its own staging.
+    if (32 * chunk < L) {
+      uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)chunk * kStage);
+      tree_chunk<D, R, QS>(p, qr, qs, hq, g, G, P, L, chunk, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+    }
+  } else if (chunk < nchunks) {
+    if constexpr (!QS)
+      row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm,
+                            p.rope_cos + qrow * (R / 2), p.rope_sin + qrow * (R / 2), h);
+    ChunkKV<D> kv;
+    prefix_issue<D>(p, kv, page, g, chunk - NT, c, h);
+    prefix_chunk<D, R, QS>(p, qr, qs, kv, P, chunk - NT, c, h, m_run, l_run, o);
+  }
+
+  // ---- merge the four waves ----
+  // o holds this wave's chunk for the 32 queries x D dims in MFMA layout:
+  // lane (c, h), register r of block db = dim 32 db + acc_row(r, h) of query
+  // c. Wave w completes blocks db = w, w + 4, ...: every wave rescales its o
+  // to the common max and hands the blocks it does not complete to their
+  // owners through LDS in 16-byte pieces.
+  constexpr int NDW = ND / kWaves;  // blocks a wave completes: 1 (head_dim 128), 2 (256)
+  float* ml = reinterpret_cast<float*>(lds);             // [wave][m | l][32]
+  f32x4_t* xch = reinterpret_cast<f32x4_t*>(lds + kMl);  // [block][wave][4][lane]
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  __syncthreads();  // retires the chunk staging (tree K/V, query rows), which shares this memory
+  if (h == 0) {
+    ml[wave * 64 + c] = m_run;
+    ml[wave * 64 + 32 + c] = l_tot;
+  }
+  __syncthreads();
+  float M = kNeg, tot = 0.f, self = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[w * 64 + c]);
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float f = fast_exp2(ml[w * 64 + c] - M);
+    tot += f * ml[w * 64 + 32 + c];
+    if (w == wave) self = f;
+  }
+#pragma unroll
+  for (int db = 0; db < ND; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] *= self;
+    if (db % kWaves != wave) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        xch[((db * kWaves + wave) * 4 + gq) * 64 + lane] =
+            f32x4_t{o[db][4 * gq], o[db][4 * gq + 1], o[db][4 * gq + 2], o[db][4 * gq + 3]};
+    }
+  }
+  __syncthreads();
+  f32x16_t mine[NDW];  // completed blocks wave + kWaves * k
+#pragma unroll
+  for (int db = 0; db < ND; ++db) {
+    if (db % kWaves != wave) continue;
+    f32x16_t a = o[db];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      if (w == wave) continue;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const f32x4_t x = xch[((db * kWaves + w) * 4 + gq) * 64 + lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[4 * gq + i] += x[i];
+      }
+    }
+    mine[db / kWaves] = a;
+  }
+
+  if (nsplit > 1) {
+    // Workgroup partial: [block][lane][16] floats (each lane moves its block
+    // values in 16-byte agent-coherent stores and loads), then m and l of the
+    // 32 queries.
+    const size_t stride = (size_t)32 * D + 64;
+    const int hb = hq * NT + rb;  // (head, query block)
+    const __amdgpu_buffer_rsrc_t prs =
+        buf_rsrc(p.part, (unsigned)((size_t)p.Hq * NT * p.splits * stride * sizeof(float)));
+    const unsigned pbase = (unsigned)((size_t)hb * p.splits * stride * sizeof(float));
+    const unsigned mine_off = pbase + (unsigned)((size_t)split * stride * sizeof(float));
+#pragma unroll
+    for (int k = 0; k < NDW; ++k) {
+      const unsigned off = mine_off + (unsigned)(((wave + kWaves * k) * 64 + lane) * 64);
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4_t, f32x4_t{mine[k][4 * gq], mine[k][4 * gq + 1], mine[k][4 * gq + 2],
+                                                mine[k][4 * gq + 3]}),
+            prs, (int)(off + 16 * gq), 0, kSc1);
+    }
+    float* part = p.part + ((size_t)hb * p.splits + split) * stride;
+    if (wave == 0 && h == 0) {
+      st_coherent(part + 32 * D + c, M);
+      st_coherent(part + 32 * D + 32 + c, tot);
+    }
+    if (p.sep_combine) return;  // attn_combine_kernel (next launch) reads the partials
+    wait_stores_done();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      // arrival count in the low half, workgroups off their XCD in the high
+      const bool native = !p.off_xcd && xcc_id() == (int)(blockIdx.x % kXcds);
+      const int old = arrive_add(&p.counters[hb], native ? 1 : 1 + kForeign);
+      int last = 0;
+      if ((old & (kForeign - 1)) == nsplit - 1) {
+        last = native && old < kForeign && p.Hkv % kXcds == 0 ? 2 : 1;
+        reset_counter(&p.counters[hb]);
+      }
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+
+    // Every split of this head ran on this XCD when all are confirmed on
+    // their expected XCD and the heads of a KV group's splits share one
+    // (Hkv % 8 == 0): the partials are then read from the local L2.
+    if (s_last == 2) combine_splits<D, kSc0>(prs, pbase, stride, nsplit, wave, lane, c, tot, mine);
+    else combine_splits<D, kSc1>(prs, pbase, stride, nsplit, wave, lane, c, tot, mine);
+  }
+
+  // Output: lane (c, h) holds, per completed block, 4 runs of 4 consecutive
+  // dims (registers 4g .. 4g+3 = dims 32 db + 8g + 4h .. +3) of query c.
+  const int orow = 32 * rb + c;
+  const float inv = (orow < L && tot > 0.f) ? 1.0f / tot : 0.f;
+#pragma unroll
+  for (int k = 0; k < NDW; ++k) {
+    const int db = wave + kWaves * k;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int dim = 32 * db + 8 * gq + 4 * h;
+      float y[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = orow < L ? mine[k][4 * gq + i] * inv : 0.f;
+      if (GATE && orow < L) {
+        // o_proj input = attention * sigmoid(gate), gate = q_proj row dims D.. of the head
+        const f32x4_t gt = *reinterpret_cast<const f32x4_t*>(p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D +
+                                                             dim);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
+      }
+      float rl[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
+      const u32x2_t hi = {pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
+      const u32x2_t lo = {pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
+      const int col = hq * D + dim;
+      const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
+      *reinterpret_cast<u32x2_t*>(p.out + oi) = hi;
+      if (p.out_lo) *reinterpret_cast<u32x2_t*>(p.out_lo + oi) = lo;
+    }
+  }
+}
+
+// Combine of the workgroup partials for long prefixes, as a launch of its
+// own: with S splits the in-kernel last arriver reads S partial tiles of
+// 32 x D fp32 alone (544 KB at head_dim 256, P = 2048), which one CU's load
+// bandwidth turns into ~18 us. Here one workgroup per (head, query block,
+// 32-dim block) reads S x 4 KB: wave w takes splits w, w + 4, ... with a
+// running max, the four waves merge in LDS and wave 0 writes the block's
+// output (normalised, gated, bf16 pair). Splits and partial layout are the
+// main kernel's; with one split or a query block past the tree the main
+// kernel has written the output itself.
+template <int D, bool GATE>
+__global__ __launch_bounds__(64 * kWaves) void attn_combine_kernel(AttnParams p) {
+  constexpr int ND = D / 32;
+  constexpr int kB = 8;  // splits in flight per wave
+  const int NT = p.tree_chunks;
+  const int db = blockIdx.x % ND, hb = blockIdx.x / ND;  // hb = head * NT + query block
+  const int hq = hb / NT, rb = hb % NT;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  constexpr int CK = chunk_keys(D);
+  const int P = p.desc->past_length, L = p.desc->num_nodes;
+  const int nchunks = NT + (P + CK - 1) / CK;
+  if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;  // the main kernel's guards
+  const int nsplit = (nchunks + kWaves - 1) / kWaves;
+  if (nsplit <= 1 || 32 * rb >= L) return;
+  const size_t stride = (size_t)32 * D + 64;
+  const __amdgpu_buffer_rsrc_t prs =
+      buf_rsrc(p.part, (unsigned)((size_t)p.Hq * NT * p.splits * stride * sizeof(float)));
+  const unsigned pbase = (unsigned)((size_t)hb * p.splits * stride * sizeof(float));
+  float Ms = kNeg, tot = 0.f;
+  f32x4_t acc[4];
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) acc[gq] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = wave; s0 < nsplit; s0 += kWaves * kB) {
+    f32x4_t v[kB][4];
+    float mm[kB], ll[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const int sp = s0 + kWaves * b;
+      const unsigned so = sp < nsplit ? pbase + (unsigned)((size_t)sp * stride * sizeof(float)) : kOob;
+      const float mv = buf_ldf(prs, so + (32 * D + c) * 4);
+      ll[b] = buf_ldf(prs, so + (32 * D + 32 + c) * 4);
+      mm[b] = sp < nsplit ? mv : kNeg;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        v[b][gq] = __builtin_bit_cast(f32x4_t, buf_ld(prs, so + (unsigned)((db * 64 + lane) * 64 + 16 * gq)));
+    }
+    float gm = Ms;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) gm = fmaxf(gm, mm[b]);
+    const float rsc = fast_exp2(Ms - gm);
+    tot *= rsc;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) acc[gq] *= rsc;
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const float w = fast_exp2(mm[b] - gm);  // 0 for splits past nsplit
+      tot += w * ll[b];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) acc[gq] += w * v[b][gq];
+    }
+    Ms = gm;
+  }
+  // Merge the four waves (in wave order) into wave 0.
+  __shared__ float ml[kWaves][2][64];
+  __shared__ f32x4_t xa[kWaves - 1][4][64];
+  ml[wave][0][lane] = Ms;
+  ml[wave][1][lane] = tot;
+  if (wave > 0) {
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) xa[wave - 1][gq][lane] = acc[gq];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float M = kNeg;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[w][0][lane]);
+  float T = 0.f;
+  f32x4_t o[4];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float f = fast_exp2(ml[w][0][lane] - M);
+    T += f * ml[w][1][lane];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4_t x = w == 0 ? acc[gq] : xa[w - 1][gq][lane];
+      o[gq] = w == 0 ? f * x : o[gq] + f * x;
+    }
+  }
+  // Output of query c, dims 32 db + 8 gq + 4 h .. +3 (MFMA accumulator layout).
+  const int orow = 32 * rb + c;
+  const float inv = (orow < L && T > 0.f) ? 1.0f / T : 0.f;
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) {
+    const int dim = 32 * db + 8 * gq + 4 * h;
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = orow < L ? o[gq][i] * inv : 0.f;
+    if (GATE && orow < L) {
+      const f32x4_t gt =
+          *reinterpret_cast<const f32x4_t*>(p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D + dim);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
+    }
+    float rl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
+    const u32x2_t hi = {pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
+    const u32x2_t lo = {pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
+    const int col = hq * D + dim;
+    const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
+    *reinterpret_cast<u32x2_t*>(p.out + oi) = hi;
+    if (p.out_lo) *reinterpret_cast<u32x2_t*>(p.out_lo + oi) = lo;
+  }
+}
+
+}  // namespace head_attn
+}  // namespace dtree
+
+using namespace dtree::head_attn;
+
+constexpr size_t kSepCombineBytes = 128 * 1024;
+
+static int attn_max_chunks(int head_dim, int max_past, int nt) {
+  const int ck = chunk_keys(head_dim);
+  return nt + (max_past + ck - 1) / ck;
+}
+static int attn_splits(int head_dim, int max_past, int nt) {
+  return (attn_max_chunks(head_dim, max_past, nt) + kWaves - 1) / kWaves;
+}
+
+namespace dtree {
+size_t head_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32_t max_past_length,
+                                      int32_t rows_padded) {
+  if (num_heads <= 0 || head_dim <= 0 || max_past_length < 0 || rows_padded <= 0 || rows_padded % 32) return 0;
+  const int nt = rows_padded / 32;
+  const size_t stride = (size_t)32 * head_dim + 64;
+  const size_t hb = (size_t)num_heads * nt;  // (head, query block) pairs
+  return ((hb * sizeof(int) + 255) & ~(size_t)255) +
+         hb * attn_splits(head_dim, max_past_length, nt) * stride * sizeof(float);
+}
+
+int head_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
+  DTREE_REQUIRE(a, "attention: null args");
+  DTREE_REQUIRE(a->qkv && a->rope_cos && a->rope_sin && a->k_pages && a->v_pages && a->page_table && a->desc &&
+                    a->out && a->workspace,
+                "attention: null pointer");
+  const int D = a->head_dim;
+  const int R = a->rope_dims == 0 ? D : a->rope_dims;
+  const bool gated = a->gated != 0;
+  DTREE_REQUIRE((D == 128 && R == 128 && !gated) || (D == 256 && R == 64 && gated),
+                "attention: compiled geometries are head_dim 128 (full RoPE) and gated head_dim 256 (rope_dims 64)");
+  DTREE_REQUIRE(a->rows_padded == 32 || a->rows_padded == 64 || a->rows_padded == 96 || a->rows_padded == 128,
+                "attention: rows_padded must be 32, 64, 96 or 128");
+  const int nt = a->rows_padded / 32;
+  DTREE_REQUIRE(a->num_kv_heads > 0 && a->num_heads % a->num_kv_heads == 0, "attention: num_heads % num_kv_heads");
+  DTREE_REQUIRE(a->max_past_length >= 0 && a->max_past_length <= kMaxPast, "attention: max_past_length beyond 16384");
+  const int q_stride = gated ? 2 * D : D;
+  DTREE_REQUIRE(a->ld_qkv >= a->num_heads * q_stride + 2 * a->num_kv_heads * D && a->ld_qkv % 4 == 0,
+                "attention: ld_qkv too small");
+  DTREE_REQUIRE(a->ld_out >= a->num_heads * D && a->ld_out % 8 == 0,
+                "attention: ld_out below num_heads * head_dim or not a multiple of 8");
+  DTREE_REQUIRE(((uintptr_t)a->out & 15) == 0 && ((uintptr_t)a->out_lo & 15) == 0 && ((uintptr_t)a->qkv & 15) == 0,
+                "attention: qkv, out and out_lo must be 16-byte aligned");
+  DTREE_REQUIRE(a->workspace_bytes >= head_attention_workspace_bytes(a->num_heads, D, a->max_past_length,
+                                                                     a->rows_padded),
+                "attention: workspace too small");
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
+                    (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * D && a->ld_out % 64 == 0),
+                "attention: tiled out needs ld_out == num_heads * head_dim");
+  AttnParams p{};
+  p.qkv = a->qkv; p.ld_qkv = a->ld_qkv;
+  p.q_stride = q_stride; p.k_off = a->num_heads * q_stride; p.v_off = p.k_off + a->num_kv_heads * D;
+  p.q_norm = a->q_norm; p.k_norm = a->k_norm; p.eps = a->eps;
+  p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
+  p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
+  p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
+  p.out_tiled = a->out_layout == DTREE_W_TILED;
+  p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.tree_chunks = nt;
+  p.max_chunks = attn_max_chunks(D, a->max_past_length, nt);
+  p.splits = attn_splits(D, a->max_past_length, nt);
+  p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
+  p.off_xcd = off_xcd_test();
+  p.counters = reinterpret_cast<int*>(a->workspace);
+  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) +
+                                    (((size_t)a->num_heads * nt * sizeof(int) + 255) & ~(size_t)255));
+  const int G = p.Hq / p.Hkv;
+  const int pairs = p.splits * p.Hkv;
+  const int grid = ((pairs + 7) / 8) * 8 * G * nt;  // nt query blocks of ((pairs+7)/8)*8*G workgroups
+  const bool one = nt == 1;
+  // Long prefixes combine in a launch of their own (attn_combine_kernel):
+  // when the last arriver alone would read more than 128 KB of partials.
+  p.sep_combine = (size_t)p.splits * 32 * D * sizeof(float) > kSepCombineBytes;
+  if (D == 128) {
+    if (one) tree_attn_kernel<128, 128, false, 1><<<grid, 64 * kWaves, 0, stream>>>(p);
+    else tree_attn_kernel<128, 128, false, 4><<<grid, 64 * kWaves, 0, stream>>>(p);
+  } else {
+    if (one) tree_attn_kernel<256, 64, true, 1><<<grid, 64 * kWaves, 0, stream>>>(p);
+    else tree_attn_kernel<256, 64, true, 4><<<grid, 64 * kWaves, 0, stream>>>(p);
+  }
+  DTREE_LAUNCH_CHECK("attention launch");
+  if (p.sep_combine) {
+    const int cgrid = p.Hq * nt * (D / 32);
+    if (D == 128) attn_combine_kernel<128, false><<<cgrid, 64 * kWaves, 0, stream>>>(p);
+    else attn_combine_kernel<256, true><<<cgrid, 64 * kWaves, 0, stream>>>(p);
+    DTREE_LAUNCH_CHECK("attention combine launch");
+  }
+  return DTREE_OK;
+}
+}  // namespace dtree

@@ -13,6 +13,8 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 namespace dtree {
 
@@ -86,6 +88,29 @@ __device__ __forceinline__ float buf_ldf(__amdgpu_buffer_rsrc_t r, unsigned off)
 
 __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// fp16 operands (v_mfma_f32_32x32x16_f16), fp32 accumulate.
+__device__ __forceinline__ f32x16_t mfma32_f16(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                0, 0, 0);
+}
+
+// fp32 pair -> fp16 pair, round to nearest even.
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+}
+
+// bf16 pair -> fp16 pair. Exact for every bf16 value of magnitude in
+// [2^-14, 65504] (fp16 has more significand bits than bf16); smaller ones
+// round to fp16's 2^-24 grid, larger ones saturate to +-65504.
+__device__ __forceinline__ uint32_t bf2_to_h2(uint32_t w) {
+  const float lo = __builtin_amdgcn_fmed3f(__uint_as_float(w << 16), -65504.f, 65504.f);
+  const float hi = __builtin_amdgcn_fmed3f(__uint_as_float(w & 0xffff0000u), -65504.f, 65504.f);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+__device__ __forceinline__ u32x4_t bf8_to_h8(u32x4_t v) {
+  return u32x4_t{bf2_to_h2(v[0]), bf2_to_h2(v[1]), bf2_to_h2(v[2]), bf2_to_h2(v[3])};
 }
 
 // ---- cross-lane reductions without LDS round trips -------------------------

@@ -24,3 +24,12 @@ def gpu_device():
 
     _native.lib()  # fail loudly if the native library is missing
     return torch.device("cuda:0")
+
+
+@pytest.fixture(params=["head", "group"])
+def attn_kernel(request, monkeypatch):
+    """Both tree-attention designs (per query head, per KV group); the library
+    picks one by the prefix its grid is sized for, DTREE_ATTN_KERNEL forces it
+    here (read at every launch)."""
+    monkeypatch.setenv("DTREE_ATTN_KERNEL", request.param)
+    return request.param

@@ -367,7 +367,7 @@ def _attention_case(dev, P, parents, Hq=32, Hkv=8, seed=0, permute_pages=True, m
 
 @pytest.mark.parametrize("P", [0, 1, 100, 128, 129, 512, 1000])
 @pytest.mark.parametrize("shape", ["chain25", "star25", "random25", "single", "chain32"])
-def test_tree_attention_matches_oracle(gpu_device, P, shape):
+def test_tree_attention_matches_oracle(gpu_device, P, shape, attn_kernel):
     L = {"chain25": 25, "star25": 25, "random25": 25, "single": 1, "chain32": 32}[shape]
     if shape.startswith("chain"):
         parents = [-1] + list(range(L - 1))
@@ -394,7 +394,7 @@ def test_tree_attention_matches_oracle(gpu_device, P, shape):
 @pytest.mark.parametrize("P", [0, 129, 1000])
 @pytest.mark.parametrize("MP,L,shape", [(64, 40, "random"), (96, 65, "random"), (96, 65, "chain"),
                                         (96, 65, "star"), (96, 33, "random"), (128, 128, "random")])
-def test_tree_attention_more_than_32_nodes(gpu_device, P, MP, L, shape):
+def test_tree_attention_more_than_32_nodes(gpu_device, P, MP, L, shape, attn_kernel):
     """Trees of 33..128 nodes: query blocks of 32 rows, tree chunks of 32
     keys masked by ancestor word w (nodes 32w..32w+31), cache rows appended
     once, rows past the tree zero."""
@@ -413,7 +413,7 @@ def test_tree_attention_more_than_32_nodes(gpu_device, P, MP, L, shape):
 
 @pytest.mark.parametrize("P,max_past,MP,L", [(0, 64, 32, 25), (100, 128, 32, 25), (300, 2000, 32, 25),
                                              (1000, 4096, 32, 25), (4000, 4096, 32, 25), (3000, 4096, 96, 65)])
-def test_tree_attention_long_prefix_separate_combine(gpu_device, P, max_past, MP, L):
+def test_tree_attention_long_prefix_separate_combine(gpu_device, P, max_past, MP, L, attn_kernel):
     """Grids sized for long prefixes combine the workgroup partials in a
     launch of their own (more than 128 KB of partials per head), also for
     several query blocks; short descriptors (one split) still write the
@@ -488,7 +488,7 @@ def _gated_attention_case(dev, P, parents, max_past, Hq=8, Hkv=2, seed=0, MP=32)
 
 @pytest.mark.parametrize("P,max_past,MP,L", [(0, 64, 32, 25), (100, 128, 32, 25), (700, 2048, 32, 25),
                                              (2000, 2048, 32, 25), (0, 64, 96, 65), (1500, 2048, 96, 65)])
-def test_gated_attention_head_dim_256(gpu_device, P, max_past, MP, L):
+def test_gated_attention_head_dim_256(gpu_device, P, max_past, MP, L, attn_kernel):
     """The Qwen3.5 geometry directly against the oracle: staged query rows
     (one query block) and per-wave rows (more than 32 nodes), with the
     in-kernel combine (short grids) and the separate combine launch
@@ -502,7 +502,7 @@ def test_gated_attention_head_dim_256(gpu_device, P, max_past, MP, L):
     assert torch.equal(out, out2)
 
 
-def test_tree_attention_gqa_small_and_deterministic(gpu_device):
+def test_tree_attention_gqa_small_and_deterministic(gpu_device, attn_kernel):
     parents = random_tree(25, seed=5)
     cache, out, ref, *_ = _attention_case(gpu_device, 300, parents, Hq=8, Hkv=2, seed=4, max_past=2000)
     got = bf16_f32(out)
@@ -688,7 +688,7 @@ def test_walk_and_compaction_match_oracle(gpu_device, seed):
     assert torch.equal(hsel[:n].cpu(), hid[acc].cpu())
 
 
-def test_cross_xcd_exchange_paths(gpu_device, monkeypatch):
+def test_cross_xcd_exchange_paths(gpu_device, monkeypatch, attn_kernel):
     """The dispatcher places workgroups round-robin over the XCDs, so the
     exchanges normally read partials from the local L2. DTREE_TEST_OFF_XCD=1
     makes every workgroup count as off its expected XCD: partials are then

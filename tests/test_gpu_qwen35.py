@@ -166,7 +166,7 @@ def _check(r, layer_ids, min_confident=0.5):
     return res
 
 
-def test_qwen35_verify_step_tiny_model(gpu_device):
+def test_qwen35_verify_step_tiny_model(gpu_device, attn_kernel):
     cfg = tiny_qwen35()
     r = _run(cfg, P=100, layer_ids=[1, 3], dev=gpu_device, check_prefill=True)
     res = _check(r, [1, 3])
@@ -180,7 +180,7 @@ def test_qwen35_verify_step_tiny_model_q4(gpu_device):
 
 
 @pytest.mark.parametrize("quant", ["bf16", "q4"])
-def test_qwen35_verify_step_65_nodes(gpu_device, quant):
+def test_qwen35_verify_step_65_nodes(gpu_device, quant, attn_kernel):
     """Draft budget 64 (a 65-node tree, 96 padded rows): attention over three
     32-row query blocks and tree chunks, q4 GEMMs per 32-row block, the
     GatedDeltaNet layer at 96 rows."""

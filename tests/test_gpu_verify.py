@@ -143,7 +143,7 @@ def _check(r, layer_ids):
     return res
 
 
-def test_verify_step_tiny_model(gpu_device):
+def test_verify_step_tiny_model(gpu_device, attn_kernel):
     cfg = tiny_qwen3()
     r = _run(cfg, P=100, layer_ids=[0, 1], dev=gpu_device, norm_jitter=0.1, check_prefill_layers=2)
     res = _check(r, [0, 1])
@@ -157,7 +157,7 @@ def test_verify_step_tiny_model_q4(gpu_device):
     assert len(res.accepted) >= 1
 
 
-def test_verify_step_graph_replays_match_eager(gpu_device):
+def test_verify_step_graph_replays_match_eager(gpu_device, attn_kernel):
     cfg = tiny_qwen3(num_hidden_layers=3)
     w = Qwen3Weights.random(cfg, seed=0, device=gpu_device)
     model = Qwen3TreeModel(cfg, w, max_past=256, layer_ids=[1])

@@ -65,15 +65,28 @@ def test_workspace_queries():
     assert lib.dtree_lmhead_candidate_blocks(151936, 32) == 1024
     assert lib.dtree_lmhead_candidate_blocks(4096, 32) == 64
     assert lib.dtree_lmhead_candidate_blocks(4096, 128) == 128
-    # attention: head counters (256-byte aligned) + one partial per head per
-    # 4-chunk workgroup; prefix 1024 = tree + 16 pages = 5 workgroups per head
-    assert lib.dtree_attention_workspace_bytes(32, 128, 1024, 32) == 256 + 32 * 5 * (32 * 128 + 64) * 4
-    assert lib.dtree_attention_workspace_bytes(32, 128, 0, 32) == 256 + 32 * 1 * (32 * 128 + 64) * 4
-    # head_dim 256 runs 32-key chunks: prefix 2048 = tree + 64 chunks = 17 workgroups per head
-    assert lib.dtree_attention_workspace_bytes(16, 256, 2048, 32) == 256 + 16 * 17 * (32 * 256 + 64) * 4
-    # 96 rows: three 32-row query blocks per head, three tree chunks: prefix
-    # 1024 = 3 + 16 chunks = 5 workgroups per (head, block); 96 counters = 384 B -> 512
-    assert lib.dtree_attention_workspace_bytes(32, 128, 1024, 96) == 512 + 96 * 5 * (32 * 128 + 64) * 4
+    # attention: the larger of the two designs' workspaces.
+    # Per-head kernel: head counters (256-byte aligned) + one partial per head
+    # per 4-chunk workgroup (prefix 1024 = tree + 16 pages = 5 workgroups per head).
+    def head_ws(Hq, D, P, MP):
+        nt = MP // 32
+        ck = 64 if D == 128 else 32
+        splits = (nt + (P + ck - 1) // ck + 3) // 4
+        return ((Hq * nt * 4 + 255) // 256) * 256 + Hq * nt * splits * (32 * D + 64) * 4
+
+    # Per-KV-group kernel: 4 KB header (error word, counters) + at most one
+    # partial (32 rows x head_dim fp32 + row max / sum) per head, query block
+    # and split, with at most one split per prefix chunk plus the tree split.
+    def group_ws(Hq, D, P, MP):
+        nt = MP // 32
+        ck = 64 if D == 128 else 32
+        return 4096 + Hq * nt * (1 + (P + ck - 1) // ck) * ((D // 32) * 64 * 16 + 64) * 4
+
+    for Hq, D, P, MP in [(32, 128, 1024, 32), (32, 128, 0, 32), (16, 256, 2048, 32), (32, 128, 1024, 96),
+                         (16, 256, 8192, 96)]:
+        want = max(head_ws(Hq, D, P, MP), group_ws(Hq, D, P, MP))
+        assert lib.dtree_attention_workspace_bytes(Hq, D, P, MP) == want, (Hq, D, P, MP)
+    assert head_ws(32, 128, 1024, 32) == 256 + 32 * 5 * (32 * 128 + 64) * 4
     assert lib.dtree_attention_workspace_bytes(32, 128, 1024, 48) == 0
 
 
