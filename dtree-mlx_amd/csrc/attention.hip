@@ -44,6 +44,7 @@
 //                 PV step.
 // K pages are [page][kv_head][64][D]; V pages are [page][kv_head][D][64].
 #include <cstdlib>
+#include <mutex>
 
 #include "common.h"
 
@@ -941,4 +942,72 @@ extern "C" size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t hea
 extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a, "attention: null args");
   return use_group_kernel(a) ? group_tree_attention(a, stream) : dtree::head_tree_attention(a, stream);
+}
+
+// ---- allocation-free variant ---------------------------------------------------
+// For callers that cannot allocate device memory (code under graph capture,
+// serving loops, harnesses that forbid hipMalloc): the same kernels with their
+// workspace (error word, split counters, partials) in this file-scope device
+// array instead of a caller buffer. Each GPU holds its own copy until the
+// process ends; every call on a GPU shares it, so calls that overlap on one
+// GPU race.
+constexpr size_t kScratchBytes = 16u << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {nullptr};
+
+// Device address of this GPU's scratch array (the host-side name is only a
+// stand-in), looked up once per device with that device current.
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  int rc = hip_check(hipGetDevice(&dev), "attention (no alloc): hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= 64) return fail(DTREE_E_ARG, "attention (no alloc): device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    rc = hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "attention (no alloc): hipGetSymbolAddress");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return DTREE_OK;
+}
+
+// Zeroes the workspace header (error word and split counters of either
+// kernel) before each call: a fill kernel, so the call stays capturable.
+__global__ void zero_header_kernel(u32x4_t* p, int n16) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n16) p[i] = u32x4_t{0u, 0u, 0u, 0u};
+}
+}  // namespace
+
+extern "C" size_t dtree_tree_attention_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int dtree_tree_attention_noalloc(const DtreeAttnArgs* a, hipStream_t stream) {
+  DTREE_REQUIRE(a, "attention (no alloc): null args");
+  const bool group = use_group_kernel(a);
+  const size_t need = group ? group_attention_workspace_bytes(a->num_heads, a->head_dim, a->max_past_length,
+                                                              a->rows_padded)
+                            : dtree::head_attention_workspace_bytes(a->num_heads, a->head_dim, a->max_past_length,
+                                                                    a->rows_padded);
+  DTREE_REQUIRE(need > 0, "attention (no alloc): bad num_heads / head_dim / max_past_length / rows_padded");
+  if (need > kScratchBytes)
+    return fail(DTREE_E_WORKSPACE, "attention (no alloc): this shape needs " + std::to_string(need) +
+                                       " bytes of workspace, beyond the 16 MiB device scratch array");
+  void* ws = nullptr;
+  int rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  // The group kernel keeps its error word and counters in the first 4 KiB; the
+  // per-head kernel keeps one counter per (head, row block) at the start.
+  const size_t head_counters = (static_cast<size_t>(a->num_heads) * (a->rows_padded / 32) * 4 + 255) / 256 * 256;
+  const int n16 = static_cast<int>(std::min(need, std::max<size_t>(4096, head_counters)) / 16);
+  zero_header_kernel<<<(n16 + 255) / 256, 256, 0, stream>>>(reinterpret_cast<u32x4_t*>(ws), n16);
+  DTREE_LAUNCH_CHECK("attention (no alloc): header clear");
+  DtreeAttnArgs b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = need;
+  return group ? group_tree_attention(&b, stream) : dtree::head_tree_attention(&b, stream);
 }

@@ -126,6 +126,8 @@ SIGNATURES = {
     "dtree_rope_table": (C.c_int, [_vp, _i32, _i32, _f32, _vp, _vp, _vp]),
     "dtree_attention_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "dtree_tree_attention": (C.c_int, [C.POINTER(AttnArgs), _vp]),
+    "dtree_tree_attention_noalloc_max_bytes": (_sz, []),
+    "dtree_tree_attention_noalloc": (C.c_int, [C.POINTER(AttnArgs), _vp]),
     "dtree_lmhead_candidates_bytes": (_sz, [_i32]),
     "dtree_lmhead_candidate_blocks": (C.c_int, [_i32, _i32]),
     "dtree_lmhead_argmax": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _f32, _vp,

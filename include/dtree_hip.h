@@ -226,6 +226,23 @@ size_t dtree_attention_workspace_bytes(int32_t num_heads, int32_t head_dim,
 int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
 
 /*
+ * dtree_tree_attention without a caller workspace: the same kernels keep their
+ * workspace (error word, split counters, partials) in a file-scope device array
+ * of dtree_tree_attention_noalloc_max_bytes() (16 MiB) bytes, one per GPU, held
+ * until the process ends; args->workspace / workspace_bytes are ignored. A
+ * shape whose workspace (dtree_attention_workspace_bytes' formula for the
+ * kernel the shape selects) exceeds the array returns DTREE_E_WORKSPACE. Each
+ * call clears the array's header with a fill kernel on `stream`; calls that
+ * overlap on one GPU race (they share the array). No device memory is
+ * allocated or freed.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+size_t dtree_tree_attention_noalloc_max_bytes(void);
+int dtree_tree_attention_noalloc(const DtreeAttnArgs* args, hipStream_t stream);
+
+/*
  * Fused LM head + argmax (adapters.py:114-118, 489-492, first index on ties
  * as adapters.py:78-81): per row m, argmax_v rs[m] * (x[m] . E[v]).
  * x = x + x_lo (split pair, x_lo optional); E in layout emb_layout
