@@ -35,11 +35,42 @@ __device__ __forceinline__ float q4_element(const uint32_t* words, const uint32_
   return __uint_as_float(pr << 16) * q + __uint_as_float(pr & 0xffff0000u);
 }
 
+// Stores 8 consecutive columns of row m of the layer input: x = v (fp32),
+// xg = split(v * g) (bf16 hi, optional lo), and the row's sum of x^2 over the
+// 32-column tile, added over the tile's 4 threads (a lane quad) with DPP.
+// Every thread of the wavefront calls it (the DPP needs all lanes); `in`
+// marks the threads that own a column group.
+__device__ __forceinline__ void fold_store8(const float (&v)[8], bool in, int m, int col, const uint16_t* g, int H,
+                                            float* x, uint16_t* xg, uint16_t* xg_lo, int xg_tiled, float* ss) {
+  if (in) {
+    const u32x4_t gwv = ld_u32x4(g + col);
+    float y[8], r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      y[i] = v[i] * __uint_as_float((i & 1) ? (gwv[i >> 1] & 0xffff0000u) : (gwv[i >> 1] << 16));
+      r[i] = y[i] - bf2f(f2bf(y[i]));
+    }
+    float* xr = x + (size_t)m * H + col;
+    *reinterpret_cast<f32x4_t*>(xr) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(xr + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+    const size_t xi = xg_tiled ? tiled_index(m, col, H) : (size_t)m * H + col;
+    *reinterpret_cast<u32x4_t*>(xg + xi) =
+        u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])};
+    if (xg_lo)
+      *reinterpret_cast<u32x4_t*>(xg_lo + xi) =
+          u32x4_t{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+  }
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sq += v[i] * v[i];
+  sq += dpp<0xB1>(sq);  // the 4 threads of a 32-column tile (a lane quad; rows hold whole quads)
+  sq += dpp<0x4E>(sq);
+  if (in && (col & 31) == 0) ss[ss_index(col >> 5, m, H >> 5)] = sq;
+}
+
 // Thread = 8 consecutive hidden columns of one row (one 16-byte load of the
-// embedding row): x[m] = E[tokens[m]] (rows >= L zero), xg = split(x * g), and
-// the row's sum of x^2 over each 32-column tile, added over the tile's 4
-// threads with DPP. Blocks [0, gather_blocks) gather; the remaining blocks
-// fill the RoPE table.
+// embedding row): x[m] = E[tokens[m]] (rows >= L zero), then fold_store8.
+// Blocks [0, gather_blocks) gather; the remaining blocks fill the RoPE table.
 __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, const uint16_t* emb, int layout,
                                                     const uint16_t* emb_sb, int V, int H,
                                                     const uint16_t* g, int MP, float* x, uint16_t* xg,
@@ -73,30 +104,28 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
       }
     }
   }
-  if (in) {
-    const u32x4_t gwv = ld_u32x4(g + col);
-    float y[8], r[8];
+  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_tiled, ss);
+}
+
+// The same layer-input fold for rows handed over by the caller (the DFlash
+// drafter's noise embedding, draft.py:355-364): x[m] = rows[m] (bf16, rows
+// >= n_rows zero), then fold_store8.
+__global__ __launch_bounds__(256) void rows_in_kernel(const uint16_t* rows, int ld_rows, int n_rows, const uint16_t* g,
+                                                      int MP, int H, float* x, uint16_t* xg, uint16_t* xg_lo,
+                                                      int xg_tiled, float* ss) {
+  const int per_row = H >> 3;
+  const int gt = blockIdx.x * 256 + threadIdx.x;
+  const bool in = gt < MP * per_row;
+  const int m = in ? gt / per_row : 0, col = in ? (gt % per_row) * 8 : 0;
+  float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      y[i] = v[i] * __uint_as_float((i & 1) ? (gwv[i >> 1] & 0xffff0000u) : (gwv[i >> 1] << 16));
-      r[i] = y[i] - bf2f(f2bf(y[i]));
-    }
-    float* xr = x + (size_t)m * H + col;
-    *reinterpret_cast<f32x4_t*>(xr) = f32x4_t{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4_t*>(xr + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
-    const size_t xi = xg_tiled ? tiled_index(m, col, H) : (size_t)m * H + col;
-    *reinterpret_cast<u32x4_t*>(xg + xi) =
-        u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])};
-    if (xg_lo)
-      *reinterpret_cast<u32x4_t*>(xg_lo + xi) =
-          u32x4_t{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+  for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  if (in && m < n_rows) {
+    const u32x4_t w = ld_u32x4(rows + (size_t)m * ld_rows + col);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
   }
-  float sq = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) sq += v[i] * v[i];
-  sq += dpp<0xB1>(sq);  // the 4 threads of a 32-column tile (a lane quad; rows hold whole quads)
-  sq += dpp<0x4E>(sq);
-  if (in && (col & 31) == 0) ss[ss_index(col >> 5, m, H >> 5)] = sq;
+  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_tiled, ss);
 }
 
 
@@ -373,6 +402,25 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
                                                           xg_layout == DTREE_W_TILED, ss, head_dim / 2, rope_base,
                                                           rope_cos, rope_sin, gather);
   DTREE_LAUNCH_CHECK("embed launch");
+  return DTREE_OK;
+}
+
+extern "C" int dtree_rows_in(const uint16_t* rows, int32_t ld_rows, int32_t n_rows, const uint16_t* norm_w,
+                             int32_t rows_padded, int32_t hidden, float* x, uint16_t* xg, uint16_t* xg_lo,
+                             int32_t xg_layout, float* ss, hipStream_t stream) {
+  DTREE_REQUIRE(rows && norm_w && x && xg && ss, "rows_in: null pointer");
+  DTREE_REQUIRE(hidden > 0 && hidden % 64 == 0, "rows_in: hidden must be a multiple of 64");
+  DTREE_REQUIRE(rows_padded > 0 && rows_padded <= DTREE_MAX_NODES && rows_padded % 32 == 0, "rows_in: rows_padded");
+  DTREE_REQUIRE(n_rows >= 0 && n_rows <= rows_padded, "rows_in: n_rows");
+  DTREE_REQUIRE(ld_rows >= hidden && ld_rows % 8 == 0, "rows_in: ld_rows (>= hidden, a multiple of 8)");
+  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || xg_layout == DTREE_W_TILED, "rows_in: xg layout");
+  DTREE_REQUIRE(((uintptr_t)rows & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
+                    ((uintptr_t)xg & 15) == 0 && ((uintptr_t)xg_lo & 15) == 0,
+                "rows_in: rows, norm_w, x, xg and xg_lo must be 16-byte aligned");
+  const int grid = (rows_padded * (hidden / 8) + 255) / 256;
+  rows_in_kernel<<<grid, 256, 0, stream>>>(rows, ld_rows, n_rows, norm_w, rows_padded, hidden, x, xg, xg_lo,
+                                           xg_layout == DTREE_W_TILED, ss);
+  DTREE_LAUNCH_CHECK("rows_in launch");
   return DTREE_OK;
 }
 

@@ -16,7 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
 MAX_NODES = 128
 MASK_WORDS = 4
 PAGE = 64
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 E_OK, E_ARG, E_HIP, E_TREE, E_WORKSPACE = 0, -1, -2, -3, -4
 
@@ -136,6 +136,9 @@ SIGNATURES = {
     "dtree_accept_walk": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "dtree_compact": (C.c_int, [_vp, _vp, _vp, _sz, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
     "dtree_rownorm": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _i32, _vp]),
+    "dtree_rows_in": (C.c_int, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
+    "dtree_kv_append": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _f32, _i32, _i32, _f32, _i32, _i32, _vp, _vp, _vp, _i32,
+                                  _vp]),
     "dtree_gdn_tree_conv": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "dtree_gdn_tree_recurrence": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                                             _vp]),

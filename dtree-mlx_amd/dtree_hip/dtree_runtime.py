@@ -230,6 +230,8 @@ def dtree_generate(target, draft, prompt_tokens, max_new_tokens: int, temperatur
     if verify_mode == "parallel-greedy-argmax" and temperature >= 1e-5:
         raise ValueError("DTree parallel-greedy-argmax only supports temperature=0.")
 
+    from .runtime import trim_draft_cache
+
     target_cache = target.make_cache()
     draft_cache = draft.make_cache()
     profile_times = empty_dtree_profile() if profile else None
@@ -265,8 +267,7 @@ def dtree_generate(target, draft, prompt_tokens, max_new_tokens: int, temperatur
         noise = target.embed_tokens(torch.tensor(block)[None])
         draft_hidden = draft(noise_embedding=noise, target_hidden=target_hidden, cache=draft_cache)
         draft_logits = target.lm_head_logits(draft_hidden[:, 1:, :])
-        if hasattr(draft, "trim_cache"):
-            draft.trim_cache(draft_cache, block_size)
+        trim_draft_cache(draft_cache, block_size)
         add_profile_elapsed(profile_times, "draft_time_s", t0)
 
         t0 = profile_start(profile_times)

@@ -443,6 +443,9 @@ class Qwen3TreeEngine(TreeEngineBase):
         self.rope_sin = torch.zeros(MP, c.head_dim // 2, dtype=f32, device=dev)
         aws = self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim, self.max_past, self.MP)
         self.attn_ws = torch.zeros(aws, dtype=torch.uint8, device=dev)
+        # Prefix length the attention grid is sized for; the cache's page table
+        # must cover it (the kernels read page entries before P is known).
+        self.attn_max_past = self.max_past
 
     # ---- sizes ---------------------------------------------------------------
     def _gemm_shapes(self):
@@ -468,7 +471,7 @@ class Qwen3TreeEngine(TreeEngineBase):
         a.out_layout = self.w.layout
         a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
         a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
-        a.max_past_length = self.max_past; a.write_cache = 1 if write_cache else 0
+        a.max_past_length = self.attn_max_past; a.write_cache = 1 if write_cache else 0
         a.workspace = self.attn_ws.data_ptr(); a.workspace_bytes = self.attn_ws.numel()
         N.check(self.lib.dtree_tree_attention(C.byref(a), st), "tree attention")
 
@@ -486,13 +489,20 @@ class Qwen3TreeEngine(TreeEngineBase):
             self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
             c.head_dim, c.rope_theta,
             self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
+        self._launch_layers(cache, st, norm_hidden=norm_hidden)
+
+    def _launch_layers(self, cache: PagedKVCache, st: int, norm_hidden: bool = False, write_cache: bool = True) -> None:
+        """The decoder layers over the rows already in x / xg / ss (and the RoPE
+        table), then the optional final-norm output."""
+        c = self.cfg
+        H = c.hidden_size
         slot = {li: i for i, li in enumerate(self.layer_ids)}
         nL = c.num_hidden_layers
         for li in range(nL):
             lw = self.w.layers[li]
             nxt = self.w.layers[li + 1].input_norm if li + 1 < nL else self.w.final_norm
             self._gemm("qkv", self.xg, H, lw.wqkv, N.EPI_STORE_F32, st, ss_in=self.ss, out_f32=self.qkv)
-            self._attention(li, cache, st)
+            self._attention(li, cache, st, write_cache=write_cache)
             self._gemm("o", self.attn, c.q_dim, lw.wo, N.EPI_RESIDUAL, st, out_f32=self.x, out_bf16=self.xg,
                        next_norm=lw.post_norm, ss_out=self.ss)
             self._gemm("gu", self.xg, H, lw.wgu, N.EPI_SWIGLU, st, ss_in=self.ss, out_bf16=self.act)

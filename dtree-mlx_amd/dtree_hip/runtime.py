@@ -261,8 +261,6 @@ def dflash_generate(target, draft, prompt_tokens, max_new_tokens: int, temperatu
         draft_hidden = draft(noise_embedding=noise_embedding, target_hidden=target_hidden, cache=draft_cache)
         drafted = sample_tokens(target.lm_head_logits(draft_hidden[:, 1:, :]), temperature)
         trim_draft_cache(draft_cache, block_size)
-        if hasattr(draft, "trim_cache"):
-            draft.trim_cache(draft_cache, block_size)
         block_tokens[1:] = drafted[0].tolist()[: block_size - 1]
         add_profile_elapsed(profile_times, "draft_time_s", t0)
 

@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define DTREE_ABI_VERSION 4
+#define DTREE_ABI_VERSION 5
 
 #define DTREE_OK 0
 #define DTREE_E_ARG (-1)      /* bad shape / pointer / enum */
@@ -214,7 +214,9 @@ typedef struct DtreeAttnArgs {
   int32_t out_layout;       /* DTREE_W_ROWMAJOR or DTREE_W_TILED (ld_out = width) */
   int32_t num_heads, num_kv_heads, head_dim, rows_padded;  /* rows: 32, 64, 96, 128 */
   float scale;
-  int32_t max_past_length;  /* grid is sized for this P */
+  int32_t max_past_length;  /* grid is sized for this P; page_table must cover
+                               max_past_length positions (entries are read
+                               before P is known) */
   int32_t write_cache;      /* 1: append the tree K/V rows to the cache */
   void* workspace; size_t workspace_bytes;
   int32_t rope_dims;        /* rotated dims per head; 0 = head_dim */
@@ -288,6 +290,39 @@ int dtree_compact(const DtreeStepDesc* desc, uint16_t* k_pages, uint16_t* v_page
 int dtree_rownorm(const float* x, int32_t ldx, int32_t rows_padded, int32_t hidden,
                   const float* ss_in, int32_t ss_tiles, const uint16_t* w, float eps,
                   uint16_t* out, int32_t ld_out, hipStream_t stream);
+
+/*
+ * Layer input from caller rows instead of token ids: the DFlash drafter's
+ * noise embedding enters its first decoder layer (DFlashDraftModel.__call__,
+ * draft.py:349-364, input_layernorm at draft.py:294-295). rows: bf16
+ * [n_rows][ld_rows] row-major; rows >= n_rows read as zero. Outputs as
+ * dtree_embed: x (fp32 [rows_padded][hidden]), xg (+ optional xg_lo) =
+ * split(x * norm_w) in xg_layout, ss statistics.
+ */
+int dtree_rows_in(const uint16_t* rows, int32_t ld_rows, int32_t n_rows, const uint16_t* norm_w,
+                  int32_t rows_padded, int32_t hidden, float* x, uint16_t* xg, uint16_t* xg_lo,
+                  int32_t xg_layout, float* ss, hipStream_t stream);
+
+/*
+ * Context K/V append of the DFlash drafter (DFlashAttention.
+ * precompute_context_kv, draft.py:186-206): kv holds fp32 projections
+ * [n_rows][ld_kv] = [k heads | v heads] * head_dim of the prepared target
+ * hidden rows; row r becomes position first_position + r:
+ * k = RoPE(k_norm(k)) (k_norm NULL = none; head_dim 128, every dim rotated),
+ * v as is, both stored bf16 in the paged layout of dtree_tree_attention.
+ * window = 0: slot = position (mlx KVCache.update_and_fetch, draft.py:206).
+ * window > 0: the sink + window context cache (ContextOnlyDraftKVCache,
+ * draft.py:67-110, sink 64 / window 1024 there): positions below `sink` keep
+ * their slot, later ones go to ring slot sink + (position - sink) % window, so
+ * the slots always hold the sink and the newest `window` positions (a row
+ * that a later row of the same call replaces is skipped). The ring changes
+ * only the order of the keys, which unmasked attention does not see.
+ * capacity = positions covered by page_table; every slot written lies below.
+ */
+int dtree_kv_append(const float* kv, int32_t ld_kv, int32_t n_rows, int32_t first_position,
+                    const uint16_t* k_norm, float eps, int32_t num_kv_heads, int32_t head_dim,
+                    float rope_base, int32_t sink, int32_t window, uint16_t* k_pages, uint16_t* v_pages,
+                    const int32_t* page_table, int32_t capacity, hipStream_t stream);
 
 /*
  * Qwen3.5 GatedDeltaNet tree primitives (qwen35_tree_kernels.py:8-152, the

@@ -185,3 +185,40 @@ def test_generator_rejects_unsupported_quantisation():
         DFlashGenerator(target_model="random:qwen3-4b", target_quant_bits=8)
     with pytest.raises(NotImplementedError):
         DFlashGenerator(target_model="random:qwen3-4b", target_quant_bits=4, target_quant_group_size=32)
+
+
+def test_draft_config_and_cache_bookkeeping():
+    """Drafter host logic (draft.py:25-110, runtime.py:22-26): config fields,
+    target layer spread, cache offsets under trim in both modes."""
+    from dtree_hip.config import QWEN3_4B, QWEN35_4B
+    from dtree_hip.draft import DFlashDraftCache, DraftArgs, build_target_layer_ids, random_draft_config
+    from dtree_hip.runtime import trim_draft_cache
+
+    a = random_draft_config(QWEN3_4B, "dflash-b16")
+    assert (a.block_size, a.num_hidden_layers, a.num_attention_heads, a.num_key_value_heads) == (16, 5, 32, 8)
+    assert a.dflash_config["target_layer_ids"] == [1, 9, 17, 25, 33]
+    assert a.dflash_config["mask_token_id"] == QWEN3_4B.vocab_size - 1
+    assert random_draft_config(QWEN35_4B, "dflash-b16-l3").dflash_config["target_layer_ids"] == [1, 15, 29]
+    assert build_target_layer_ids(2, 5) == [1]
+    assert DraftArgs.from_dict({**a.__dict__, "unknown": 1}) == a
+    with pytest.raises(NotImplementedError):
+        random_draft_config(QWEN3_4B, "eagle")
+    with pytest.raises(NotImplementedError):
+        DraftArgs.from_dict({**a.__dict__, "attention_bias": True}).stack_config()
+
+    kv = DFlashDraftCache(3, 2, 128, "kv", max_past=256, block=32, device="cpu")
+    for lc in kv:
+        lc.offset = 40
+    trim_draft_cache(kv, 16)
+    assert kv.offset == 24 and kv.stored_length() == 24
+    trim_draft_cache(kv, 100)
+    assert kv.offset == 0
+    co = DFlashDraftCache(3, 2, 128, "context-only", max_past=256, block=32, device="cpu")
+    assert co.capacity == 64 + 1024
+    for lc in co:
+        lc.offset = 5000
+    trim_draft_cache(co, 16)
+    assert co.offset == 5000 and co.stored_length() == 1088
+    co.layers[1].offset = 4999
+    with pytest.raises(ValueError):
+        co.offset
