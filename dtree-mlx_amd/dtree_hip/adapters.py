@@ -279,6 +279,22 @@ class Qwen3TargetAdapter(MLXTargetAdapter):
         return res.accepted, res.bonus_token, vh
 
 
+    def verify_tree_from_logits(self, model, draft_logits, budget: int, topk, root_token: int, cache, layer_ids):
+        """build_dtree_tree + compile_dtree_tree on the device (the tree kernels
+        write the step descriptor), then the fused verify step; one readback.
+        Returns (node_token_ids, node_depths, parents, child_maps, accepted,
+        bonus_token, verifier_hidden). The device tree follows the reference
+        order rules exactly given its fp32 log-probs, whose logsumexp is
+        summed in another order than the host path's."""
+        eng = model.engine
+        eng.set_layer_ids(layer_ids)
+        res, (ids, depths, parents, child_maps) = eng.verify_from_logits(cache, draft_logits, budget, topk,
+                                                                         int(root_token))
+        n = len(res.accepted)
+        vh = eng.hidden_sel[:n].clone()[None] if layer_ids else None
+        return ids, depths, parents, child_maps, res.accepted, res.bonus_token, vh
+
+
 class Qwen35TargetAdapter(Qwen3TargetAdapter):
     """Qwen3.5 hybrid adapter (adapters.py:257-448): forward_tree leaves the
     committed state untouched and keeps a pending tree state (here: the
@@ -428,6 +444,12 @@ class LoadedTargetModel:
     def verify_tree(self, inputs, cache, layer_ids, parents, position_ids, attention_mask=None, child_maps=None):
         out = self.adapter.verify_tree(self.model, inputs, cache, layer_ids, parents, position_ids,
                                        attention_mask, child_maps)
+        self.last_verify_compacted = True
+        return out
+
+    def verify_tree_from_logits(self, draft_logits, budget: int, topk, root_token: int, cache, layer_ids):
+        out = self.adapter.verify_tree_from_logits(self.model, draft_logits, budget, topk, root_token, cache,
+                                                   layer_ids)
         self.last_verify_compacted = True
         return out
 

@@ -259,6 +259,10 @@ def dtree_generate(target, draft, prompt_tokens, max_new_tokens: int, temperatur
     verified_tree_nodes: list[int] = []
     qwen35_tree_mode = os.environ.get("DTREE_QWEN35_TREE_MODE")
     use_lazy = target.adapter.family == "qwen3_5" and qwen35_tree_mode != "full_tree"
+    # The fused greedy verify builds the tree on the device unless told otherwise
+    # (DTREE_TREE_BUILD=host keeps the host heap of build_dtree_tree).
+    device_tree = (not use_lazy and verify_mode == "parallel-greedy-argmax" and profile_times is None
+                   and hasattr(target, "verify_tree_from_logits") and os.environ.get("DTREE_TREE_BUILD") != "host")
 
     decode_start = time.perf_counter()
     while start < total_max_tokens:
@@ -270,22 +274,34 @@ def dtree_generate(target, draft, prompt_tokens, max_new_tokens: int, temperatur
         trim_draft_cache(draft_cache, block_size)
         add_profile_elapsed(profile_times, "draft_time_s", t0)
 
-        t0 = profile_start(profile_times)
-        node_ids, depths, parents, child_maps, vis, sub = build_dtree_tree(draft_logits[0], budget, topk=tree_topk)
-        add_profile_elapsed(profile_times, "tree_build_time_s", t0)
-        if profile_times is not None:
-            for k2, v in sub.items():
-                profile_times[k2] += v
+        if device_tree:
+            # Tree build, verify-input compile and the fused verify step on the
+            # device with one readback (tree kernels write the step descriptor).
+            t0 = profile_start(profile_times)
+            node_ids, depths, parents, child_maps, accepted, posterior_token, verifier_hidden = \
+                target.verify_tree_from_logits(draft_logits[0], budget, tree_topk, block[0], target_cache, layer_ids)
+            tree_tokens = [block[0], *node_ids]
+            add_profile_elapsed(profile_times, "verify_time_s", t0)
+        else:
+            t0 = profile_start(profile_times)
+            node_ids, depths, parents, child_maps, vis, sub = build_dtree_tree(draft_logits[0], budget,
+                                                                               topk=tree_topk)
+            add_profile_elapsed(profile_times, "tree_build_time_s", t0)
+            if profile_times is not None:
+                for k2, v in sub.items():
+                    profile_times[k2] += v
+
+            t0 = profile_start(profile_times)
+            tree_tokens = [block[0], *node_ids]
+            if not use_lazy:
+                ids, tree_tokens, pos, mask = compile_dtree_tree(block[0], start, node_ids, depths, vis, start,
+                                                                 ids_buf, pos_buf, mask_buf)
+            add_profile_elapsed(profile_times, "tree_compile_time_s", t0)
 
         t0 = profile_start(profile_times)
-        tree_tokens = [block[0], *node_ids]
-        if not use_lazy:
-            ids, tree_tokens, pos, mask = compile_dtree_tree(block[0], start, node_ids, depths, vis, start,
-                                                             ids_buf, pos_buf, mask_buf)
-        add_profile_elapsed(profile_times, "tree_compile_time_s", t0)
-
-        t0 = profile_start(profile_times)
-        if use_lazy:
+        if device_tree:
+            pass
+        elif use_lazy:
             accepted, posterior_token, verifier_hidden = lazy_follow_tree_exact(
                 target, target_cache, layer_ids, tree_tokens, child_maps, temperature, verify_mode, profile_times)
         elif verify_mode == "parallel-greedy-argmax" and profile_times is None and hasattr(target, "verify_tree"):
@@ -378,6 +394,7 @@ def dtree_generate(target, draft, prompt_tokens, max_new_tokens: int, temperatur
         "speculative_tokens": block_size,
         "tree_budget": budget,
         "verify_mode": verify_mode,
+        "tree_build": "device" if device_tree else "host",
     }
     if profile_times is not None:
         profiled = sum(profile_times[k] for k in DTREE_STAGE_ORDER)

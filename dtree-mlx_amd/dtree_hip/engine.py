@@ -169,6 +169,9 @@ class TreeEngineBase:
         self._result_np = self.result_host.numpy()
         self._graphs: dict = {}
         self._dead_graphs: list = []
+        self._tree_ws = None
+        self.tree_out = torch.zeros(1 + 3 * N.MAX_NODES, dtype=torch.int32, device=dev)
+        self.tree_out_host = torch.zeros(1 + 3 * N.MAX_NODES, dtype=torch.int32).pin_memory()
 
     def _alloc_layer_buffers(self) -> None:
         raise NotImplementedError
@@ -320,11 +323,71 @@ class TreeEngineBase:
         self.hidden_sel = torch.zeros(self.MP, nh * H, dtype=torch.bfloat16, device=self.dev)
         self.release_graphs()
 
-    def read_result(self, stream=None) -> StepResult:
+    # ---- draft tree on the device (dtree_runtime.py:82-192) ----------------------
+    def launch_tree_build(self, draft_logits: torch.Tensor, budget: int, topk: int | None, root_token: int,
+                          past_length: int, st: int) -> None:
+        """build_dtree_tree + compile_dtree_tree into the step descriptor: the
+        verify launches can follow on the stream without a host round trip."""
+        x = draft_logits
+        if x.dim() != 2 or x.dtype != torch.float32 or x.device != self.dev or not x.is_contiguous():
+            x = x.reshape(-1, x.shape[-1]).to(self.dev, torch.float32).contiguous()
+        D, V = x.shape
+        budget = max(int(budget), 0)
+        if 1 + budget > self.max_nodes:
+            raise ValueError(f"tree budget {budget} needs {1 + budget} nodes; the engine holds {self.max_nodes}")
+        if not 0 <= int(root_token) < self.cfg.vocab_size:
+            raise ValueError(f"root token {root_token} outside the vocabulary")
+        if past_length < 0 or past_length > self.max_past:
+            raise ValueError(f"past_length {past_length} outside [0, {self.max_past}]")
+        k = min(budget if topk is None else int(topk), V) if budget > 0 and D > 0 else 1
+        ws_ptr, ws_bytes = None, 0
+        if budget > 0 and D > 0:
+            need = self.lib.dtree_tree_build_workspace_bytes(D, V, k)
+            if self._tree_ws is None or self._tree_ws.numel() < need:
+                self._tree_ws = torch.zeros(need, dtype=torch.uint8, device=self.dev)
+            ws_ptr, ws_bytes = self._tree_ws.data_ptr(), self._tree_ws.numel()
+        self._desc_event.synchronize()  # no host upload into the descriptor is still in flight
+        N.check(self.lib.dtree_tree_build(x.data_ptr(), V, D, V, k, budget, int(root_token), int(past_length),
+                                          ws_ptr, ws_bytes, self.desc.data_ptr(), self.tree_out.data_ptr(), None,
+                                          None, st), "tree build")
+
+    def tree_lists(self, root_token: int):
+        """(node_token_ids, node_depths, parents, child_maps) of the last device
+        tree, from the copy read_result(tree=True) fetched."""
+        t = self.tree_out_host.numpy()
+        n, M = int(t[0]), N.MAX_NODES
+        ids = t[1:1 + n].tolist()
+        depths = t[1 + M:1 + M + n].tolist()
+        parents = [-1] + t[1 + 2 * M:1 + 2 * M + n].tolist()
+        child_maps: list[dict[int, int]] = [dict() for _ in range(n + 1)]
+        for i in range(1, n + 1):
+            child_maps[parents[i]][ids[i - 1]] = i
+        return ids, depths, parents, child_maps
+
+    def verify_from_logits(self, cache, draft_logits, budget: int, topk: int | None, root_token: int,
+                           use_graph: bool = True, commit: bool = True):
+        """Tree build on the device, then the verify step, then one readback of
+        the walk result and the tree. Returns (StepResult, tree lists)."""
+        P = cache.offset
+        st = self.stream_handle()
+        self.launch_tree_build(draft_logits, budget, topk, root_token, P, st)
+        if use_graph:
+            self.graph_launch(cache, st)
+        else:
+            self.launch_verify(cache, st)
+        res = self.read_result(tree=True)
+        if commit:
+            cache.offset = P + len(res.accepted)
+        return res, self.tree_lists(root_token)
+
+    def read_result(self, stream=None, tree: bool = False) -> StepResult:
         s = torch.cuda.current_stream() if stream is None else stream
         h = _hip()
         _hip_check(h.hipMemcpyAsync(self.result_host.data_ptr(), self.result.data_ptr(),
                                     self.result_host.numel() * 4, _D2H, s.cuda_stream), "walk result copy")
+        if tree:
+            _hip_check(h.hipMemcpyAsync(self.tree_out_host.data_ptr(), self.tree_out.data_ptr(),
+                                        self.tree_out_host.numel() * 4, _D2H, s.cuda_stream), "tree copy")
         _hip_check(h.hipStreamSynchronize(s.cuda_stream), "walk result wait")
         r = self._result_np
         n, bonus, L = int(r[0]), int(r[1]), int(r[2])

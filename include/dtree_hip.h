@@ -325,6 +325,30 @@ int dtree_kv_append(const float* kv, int32_t ld_kv, int32_t n_rows, int32_t firs
                     const int32_t* page_table, int32_t capacity, hipStream_t stream);
 
 /*
+ * Draft tree on the GPU (build_dtree_tree, dtree_runtime.py:82-163, and the
+ * verify inputs of compile_dtree_tree, dtree_runtime.py:166-192). logits:
+ * fp32 [depth][ld] draft logits (row d = depth d + 1); per row the top `topk`
+ * tokens by (logit desc, token id asc) with log-probs logit - logsumexp(row)
+ * (fp32); then the reference's best-first heap over cumulative log-probs
+ * (fp64, its operation order and tuple tie-break) pops `budget` nodes. The
+ * tree is written into `desc`: tokens = [root_token, nodes...], positions =
+ * past_length + depth, parents, ancestor bitsets, num_nodes = 1 + nodes,
+ * past_length, n_accepted = 0; rows past the tree cleared. tree_out
+ * (optional, int32 [1 + 3 * DTREE_MAX_NODES]): node count, then node tokens,
+ * depths and parents of nodes 1.. at offsets 1, 1 + DTREE_MAX_NODES,
+ * 1 + 2 * DTREE_MAX_NODES. topk_ids / topk_logprobs (optional, [depth][topk]
+ * int32 / fp32) receive the per-row top-k lists (row-wise argmax = column 0).
+ * Limits: depth <= 18, topk <= min(127, vocab),
+ * budget <= 127, vocab and ld multiples of 4, ceil(vocab / 8192) * topk <=
+ * 4096. budget = 0 or depth = 0 gives the root alone (no logits read).
+ */
+size_t dtree_tree_build_workspace_bytes(int32_t depth, int32_t vocab, int32_t topk);
+int dtree_tree_build(const float* logits, int32_t ld, int32_t depth, int32_t vocab, int32_t topk,
+                     int32_t budget, int32_t root_token, int32_t past_length, void* workspace,
+                     size_t workspace_bytes, DtreeStepDesc* desc, int32_t* tree_out, int32_t* topk_ids,
+                     float* topk_logprobs, hipStream_t stream);
+
+/*
  * Qwen3.5 GatedDeltaNet tree primitives (qwen35_tree_kernels.py:8-152, the
  * tree layer qwen35_tree.py:180-480), fp32, nodes in heap order (parent <
  * child, root parent -1), num_nodes <= DTREE_MAX_NODES.

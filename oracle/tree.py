@@ -4,7 +4,8 @@ Test infrastructure only (see ``oracle/__init__.py``).
 
 Restates, in numpy / pure Python:
 - ``build_tree``          <- ``dtree_runtime.py:82-163`` (best-first heap over
-  per-depth top-k ranks, cumulative log-prob scores).
+  per-depth top-k ranks, cumulative log-prob scores); ``heap_tree`` is its
+  heap half over given top-k lists.
 - ``brute_force_tree``    -- independent check of ``build_tree``: every rank
   tuple (r_1..r_d), r_i < k, d <= D, scored by sum_i lp[i-1, r_i] in fp64,
   sorted by (-score, ranks); the first ``budget`` tuples are the tree. This
@@ -41,9 +42,18 @@ def build_tree(draft_logits: np.ndarray, budget: int, topk: int | None = None):
     if budget <= 0 or draft_logits.shape[0] == 0:
         return [], [], [-1], [dict()], np.ones((1, 1), dtype=bool)
     k = min(budget, draft_logits.shape[-1]) if topk is None else min(topk, draft_logits.shape[-1])
-    depth_limit = draft_logits.shape[0]
     tok, lp = _topk_sorted(draft_logits, k)
+    return heap_tree(tok, lp, budget)
 
+
+def heap_tree(tok: np.ndarray, lp: np.ndarray, budget: int):
+    """The heap half of build_tree (dtree_runtime.py:112-160) over given per-depth
+    top-k token ids [D, k] and fp32 log-probs [D, k]."""
+    if budget <= 0 or tok.shape[0] == 0:
+        return [], [], [-1], [dict()], np.ones((1, 1), dtype=bool)
+    k = tok.shape[1]
+    depth_limit = tok.shape[0]
+    lp = np.asarray(lp, dtype=np.float32)
     first = float(lp[0, 0])
     heap = [(-first, (0,), 0, 1, 0, first)]
     node_ids: list[int] = []
