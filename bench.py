@@ -184,7 +184,7 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
     out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant), nl, us["qkv"], b["qkv"])
-    out["attention"] = entry(f"tree_attn_kernel<128, 128, false, {1 if eng.MP == 32 else 4}>", nl, us["attention"],
+    out["attention"] = entry(attention_kernel_name(eng.max_past, 128, 128, False, eng.MP), nl, us["attention"],
                              b["attention"])
     out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant), nl, us["o"], b["o"])
     out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant), nl, us["down"], b["down"])
@@ -384,12 +384,22 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
                                 us["recurrence"], b["recurrence"]),
         "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
         "gdn_commit": entry("gdn_commit_kernel<128>", nG, us["commit"], b["commit"]),
-        "attention": entry(f"tree_attn_kernel<256, 64, true, {1 if eng.MP == 32 else 4}>", nA, us["attention"],
+        "attention": entry(attention_kernel_name(eng.max_past, 256, 64, True, eng.MP), nA, us["attention"],
                            b["attention"]),
         "lm_head": entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"]),
     }
     return out
 
+
+
+def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -> str:
+    """Tree-attention kernel the library dispatches (attention.hip): the
+    per-KV-group design above a 1536-key prefix grid, the per-head one below;
+    DTREE_ATTN_KERNEL forces either."""
+    forced = os.environ.get("DTREE_ATTN_KERNEL")
+    group = forced == "group" or (forced != "head" and max_past > 1536)
+    g = "true" if gated else "false"
+    return f"gqa_tree_attn_kernel<{D}, {R}, {g}, 4>" if group else f"tree_attn_kernel<{D}, {R}, {g}, {1 if MP == 32 else 4}>"
 
 
 def gemm_kernel_name(n: int, k: int, epi: int, quant: str) -> str:
@@ -425,8 +435,80 @@ MODEL_NAMES = {"qwen3-4b": "Qwen3-4B", "qwen35-4b": "Qwen3.5-4B-shaped hybrid",
                "qwen35-9b": "Qwen3.5-9B-shaped hybrid"}
 
 
+def decode_step_bench(target_model, cache, P: int, budget: int, steps: int = 30) -> dict:
+    """Latency of the rest of a DTree decode step around the verify, at the
+    verify workload's shapes: the DFlash drafter call (Qwen3-4B-sized drafter,
+    5 layers; 16-row block after a 5-row context append, then the block trim),
+    the target's LM head over the 15 draft rows (fp32 logits), the draft tree
+    built on the device from those logits (3 launches) against the host heap
+    of build_dtree_tree, and the whole step: drafter + LM head + device tree +
+    verify graph + one readback. Random-init drafter: the acceptance it gets is
+    not meaningful, the latencies are."""
+    import torch
+
+    from dtree_hip.adapters import Qwen3TargetAdapter
+    from dtree_hip.draft import DFlashDraftModel, random_draft_config
+    from dtree_hip.dtree_runtime import build_dtree_tree
+    from dtree_hip.runtime import trim_draft_cache
+
+    eng = target_model.engine
+    cfg = target_model.args
+    dev = eng.dev
+    args = random_draft_config(cfg, "dflash-b16")
+    draft = DFlashDraftModel.random(args, seed=11, max_past=P + 64, device=dev)
+    dcache = draft.make_cache()
+    H = cfg.hidden_size
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    ctx0 = (torch.randn(1, P, 5 * H, generator=g, device=dev)).to(torch.bfloat16)
+    draft(noise_embedding=torch.zeros(1, 16, H, dtype=torch.bfloat16, device=dev), target_hidden=ctx0, cache=dcache)
+    trim_draft_cache(dcache, 16)
+    ctx = (torch.randn(1, 5, 5 * H, generator=g, device=dev)).to(torch.bfloat16)
+    noise = target_model.weights.embed_rows(torch.tensor([7] + [args.dflash_config["mask_token_id"]] * 15,
+                                                         device=dev))[None]
+    adapter = Qwen3TargetAdapter()
+    base_off = dcache.offset
+
+    def one_draft():
+        for lc in dcache:
+            lc.offset = base_off
+        h = draft(noise_embedding=noise, target_hidden=ctx, cache=dcache)
+        trim_draft_cache(dcache, 16)
+        return h
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            out = fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3, out
+
+    draft_ms, dh = timed(one_draft, steps)
+    lm_ms, logits = timed(lambda: adapter.lm_head_logits(target_model, dh[:, 1:, :]), steps)
+    x = logits[0].contiguous()
+    st = eng.stream_handle()
+    tb_ms, _ = timed(lambda: eng.launch_tree_build(x, budget, 4, 7, P, st), steps * 4)
+    host_ms, _ = timed(lambda: build_dtree_tree(x, budget, topk=4), steps)
+
+    def full():
+        h = one_draft()
+        lg = adapter.lm_head_logits(target_model, h[:, 1:, :])
+        return eng.verify_from_logits(cache, lg[0], budget, 4, 7, commit=False)
+
+    step_ms, _ = timed(full, steps)
+    del draft, dcache
+    return {"workload": "DTree decode step pieces around the verify (Qwen3-4B target, DFlash drafter sized for it, "
+                        f"prefix {P}, budget {budget}, top-4)",
+            "draft_call_ms": round(draft_ms, 4), "lm_head_15_rows_ms": round(lm_ms, 4),
+            "tree_build_device_ms": round(tb_ms, 4), "tree_build_host_ms": round(host_ms, 4),
+            "whole_step_ms": round(step_ms, 4), "steps": steps}
+
+
 def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup: int, kernel_reps: int = 0,
-                 with_cpu: bool = False) -> dict:
+                 with_cpu: bool = False, with_decode: bool = False) -> dict:
     """Builds the random-init model, prefills P tokens, builds the seeded tree
     (acceptance pass at p = 0.85 on the device argmax) and times `steps`
     verify steps (descriptor upload, graph replay, result read back) after
@@ -451,7 +533,8 @@ def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup
             w = Qwen3Weights.random_q4(cfg, seed=0, device=dev)
         else:
             w = Qwen3Weights.random(cfg, seed=0, device=dev)
-        eng = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33], max_nodes=max_nodes).engine
+        tmodel = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33], max_nodes=max_nodes)
+        eng = tmodel.engine
     cache = eng.new_cache()
     prefix = random_prefix(P, cfg.vocab_size, seed=1)
     eng.prefill(cache, prefix)
@@ -493,12 +576,18 @@ def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup
     if kernel_reps:
         out["kernels"] = (time_kernels35 if hybrid else time_kernels)(eng, cfg, w, cache, st, P, L, kernel_reps,
                                                                       quant)
+    if with_decode and not hybrid:
+        t0 = time.time()
+        out["decode"] = decode_step_bench(tmodel, cache, P, budget)
+        log(f"[bench] decode step pieces {out['decode']} ({time.time() - t0:.1f}s)")
     if with_cpu:
         t0 = time.time()
         out["cpu"] = (cpu_baseline35 if hybrid else cpu_baseline)(cfg, w, cache, tree, P)
         log(f"[bench] cpu baseline {out['cpu']['value']:.3f} steps/s ({time.time() - t0:.1f}s)")
     eng.release_graphs()
     del eng, w, cache
+    if not hybrid:
+        del tmodel
     import gc
 
     gc.collect()
@@ -619,7 +708,7 @@ def main():
     if a.quant is None:
         a.quant = "q4" if big else "bf16"
     r = run_workload(a.model, a.quant, P, a.budget, a.steps, a.warmup, kernel_reps=a.kernel_reps,
-                     with_cpu=not a.no_cpu_baseline)
+                     with_cpu=not a.no_cpu_baseline, with_decode=not a.no_configs)
     cfg, L, ms, gbps = r["cfg"], r["L"], r["ms"], r["gbps"]
     kernels = r["kernels"]
     for name, kd in kernels.items():
@@ -639,6 +728,8 @@ def main():
     configs = None
     if not a.no_configs and a.model == "qwen3-4b" and a.quant == "bf16" and P == 1024 and a.budget == 24:
         configs = {}
+        if "decode" in r:
+            configs["decode_step_qwen3_4b_p1024"] = r["decode"]
         t0 = time.time()
         configs["attention_layer_p512"] = attention_layer_bench(P=512)
         log(f"[bench] attention layer P=512: {configs['attention_layer_p512']}")
