@@ -435,6 +435,41 @@ MODEL_NAMES = {"qwen3-4b": "Qwen3-4B", "qwen35-4b": "Qwen3.5-4B-shaped hybrid",
                "qwen35-9b": "Qwen3.5-9B-shaped hybrid"}
 
 
+def prefill_bench(eng, P: int, reps: int = 3) -> dict:
+    """Prompt prefill of P random tokens into a fresh cache: the long-M path
+    (128 x 128 MFMA tiles, attention per 128-row chunk) against the chain
+    path (max_nodes-token tree passes). Algorithmic FLOPs: 2 * P * linear
+    parameters (the kernels do twice that: hi and lo activation planes)."""
+    import torch
+
+    from dtree_hip.synthetic import random_prefix
+
+    c = eng.cfg
+    toks = random_prefix(P, c.vocab_size, seed=7)
+    times = []
+    for _ in range(reps + 1):
+        cache = eng.new_cache()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.prefill_long(cache, toks)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        del cache
+    long_ms = min(times[1:]) * 1e3
+    cache = eng.new_cache()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.prefill(cache, toks, chunk=eng.max_nodes)
+    torch.cuda.synchronize()
+    chain_ms = (time.perf_counter() - t0) * 1e3
+    del cache
+    flops = 2.0 * P * c.layer_linear_params() * c.num_hidden_layers
+    return {"workload": f"Qwen3-4B bf16 prompt prefill, {P} tokens (36 layers, K/V into the paged cache)",
+            "long_path_ms": round(long_ms, 3), "chain_path_ms": round(chain_ms, 3),
+            "long_path_tflops_algorithmic": round(flops / (long_ms * 1e-3) / 1e12, 1),
+            "tokens_per_s": round(P / (long_ms * 1e-3), 1)}
+
+
 def decode_step_bench(target_model, cache, P: int, budget: int, steps: int = 30) -> dict:
     """Latency of the rest of a DTree decode step around the verify, at the
     verify workload's shapes: the DFlash drafter call (Qwen3-4B-sized drafter,
@@ -576,6 +611,10 @@ def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup
     if kernel_reps:
         out["kernels"] = (time_kernels35 if hybrid else time_kernels)(eng, cfg, w, cache, st, P, L, kernel_reps,
                                                                       quant)
+    if with_decode and not hybrid and quant == "bf16":
+        t0 = time.time()
+        out["prefill"] = prefill_bench(eng, P)
+        log(f"[bench] prefill {out['prefill']} ({time.time() - t0:.1f}s)")
     if with_decode and not hybrid:
         t0 = time.time()
         out["decode"] = decode_step_bench(tmodel, cache, P, budget)
@@ -730,6 +769,8 @@ def main():
         configs = {}
         if "decode" in r:
             configs["decode_step_qwen3_4b_p1024"] = r["decode"]
+        if "prefill" in r:
+            configs["prefill_qwen3_4b_p1024"] = r["prefill"]
         t0 = time.time()
         configs["attention_layer_p512"] = attention_layer_bench(P=512)
         log(f"[bench] attention layer P=512: {configs['attention_layer_p512']}")

@@ -1148,6 +1148,121 @@ static void launch_dp(const GemmParams& p, int epi, hipStream_t st) {
   }
 }
 
+// ---- long-M GEMM (prompt prefill): rows a multiple of 128 --------------------
+// Compute-bound: a workgroup owns a 128-row x 128-column output tile over the
+// whole K. Per 64-wide K block the workgroup stages the tile's activation
+// blocks (4 row blocks, hi and lo planes) and weight blocks (4 column blocks)
+// in LDS, 16 bytes per thread per 4 KB block, double-buffered with one barrier
+// per K block (the next block's loads are in flight during the current
+// block's MFMAs). Wave w computes rows 64 (w / 2) .. + 63 x columns
+// 64 (w % 2) .. + 63 as 2 x 2 MFMA 32 x 32 tiles: 32 MFMAs per K block with
+// both planes. The finished tile goes through LDS to the same epilogues as
+// the skinny GEMMs, applied to 128 rows.
+constexpr int kLongRows = 128, kLongCols = 128;
+
+template <bool LO, int EPI>
+__global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
+  constexpr int NPL = LO ? 2 : 1, ABLK = 4 * NPL, NBLK = ABLK + 4;
+  constexpr int STAGE = NBLK * 4096;                                    // bytes per stage
+  constexpr int SMEM = 2 * STAGE > kLongRows * kLongCols * 4 ? 2 * STAGE : kLongRows * kLongCols * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
+  __shared__ float rs[kLongRows];
+  const int t = threadIdx.x, lane = t & 63, c = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+  const int ntn = p.n / kLongCols;
+  const int mt = blockIdx.x / ntn, nt = blockIdx.x - mt * ntn;
+  const int nkb = p.k >> 6;
+  const int R = mt * kLongRows;
+  if (t < kLongRows) {
+    float r = 1.f;
+    if (p.ss_in) {
+      float s = 0.f;
+      for (int tt = 0; tt < p.ss_tiles; ++tt) s += p.ss_in[ss_index(tt, R + t, p.ss_tiles)];
+      r = rsqrtf(s * p.inv_norm_dim + p.eps);
+    }
+    rs[t] = r;
+  }
+  u32x4_t ld[NBLK];
+  auto load_stage = [&](int kb) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const size_t blk = ((size_t)((R >> 5) + rb) * nkb + kb) * 2048 + 8 * t;
+      ld[rb * NPL] = ld_u32x4(p.x + blk);
+      if (LO) ld[rb * NPL + NPL - 1] = ld_u32x4(p.x_lo + blk);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) ld[ABLK + cb] = ld_u32x4(p.w + ((size_t)(nt * 4 + cb) * nkb + kb) * 2048 + 8 * t);
+  };
+  auto store_stage = [&](int s) {
+#pragma unroll
+    for (int b = 0; b < NBLK; ++b) *reinterpret_cast<u32x4_t*>(smem + s * STAGE + b * 4096 + 16 * t) = ld[b];
+  };
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int s = kb & 1;
+    if (kb + 1 < nkb) load_stage(kb + 1);
+    const unsigned char* st = smem + s * STAGE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int fo = (64 * i + lane) * 16;
+      u32x4_t b[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(st + (ABLK + 2 * wc + j) * 4096 + fo);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const u32x4_t ah = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL) * 4096 + fo);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32(ah, b[j], acc[rb][j]);
+        if (LO) {
+          const u32x4_t al = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL + 1) * 4096 + fo);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32(al, b[j], acc[rb][j]);
+        }
+      }
+    }
+    if (kb + 1 < nkb) store_stage(s ^ 1);
+    __syncthreads();
+  }
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        red[(64 * wr + 32 * rb + acc_row(r, h)) * kLongCols + 64 * wc + 32 * j + c] = acc[rb][j][r];
+  __syncthreads();
+  // the epilogue of rows R .. R + 127: outputs shifted by R rows (32-row
+  // blocks are contiguous in both layouts; statistics are per 32-row block)
+  GemmParams q = p;
+  if (q.out_f32) q.out_f32 += (size_t)R * q.ld_out_f32;
+  if (q.out_bf16) q.out_bf16 += (size_t)R * q.ld_out_bf16;
+  if (q.out_lo) q.out_lo += (size_t)R * q.ld_out_bf16;
+  if (q.hidden_out) q.hidden_out += (size_t)R * q.ld_hidden;
+  if (q.ss_out) q.ss_out += (size_t)(R >> 5) * (q.n >> 5) * 32;
+  tile_epilogue<kLongRows, kLongCols, EPI>(q, red, rs, nt);
+}
+
+template <bool LO>
+static void launch_long(const GemmParams& p, int epi, int grid, hipStream_t st) {
+  switch (epi) {
+    case DTREE_EPI_STORE_F32: long_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<grid, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: long_gemm_kernel<LO, DTREE_EPI_RESIDUAL><<<grid, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: long_gemm_kernel<LO, DTREE_EPI_SWIGLU><<<grid, kThreads, 0, st>>>(p); break;
+    default: long_gemm_kernel<LO, DTREE_EPI_STORE_BF16><<<grid, kThreads, 0, st>>>(p); break;
+  }
+}
+
 }  // namespace dtree
 
 using namespace dtree;
@@ -1341,6 +1456,52 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     default: launch_gemm<4>(p, epi, blocks, stream, tiled); break;
   }
   DTREE_LAUNCH_CHECK("gemm launch");
+  return DTREE_OK;
+}
+
+extern "C" int dtree_gemm_long(const DtreeGemmArgs* a, hipStream_t stream) {
+  DTREE_REQUIRE(a, "gemm_long: null args");
+  DTREE_REQUIRE(a->x && a->w, "gemm_long: null x or w");
+  DTREE_REQUIRE(a->x_layout == DTREE_W_TILED && a->w_layout == DTREE_W_TILED,
+                "gemm_long: tiled bf16 activations and weights");
+  DTREE_REQUIRE(a->rows_padded >= kLongRows && a->rows_padded % kLongRows == 0 && a->rows_padded <= (1 << 20),
+                "gemm_long: rows_padded must be a positive multiple of 128");
+  DTREE_REQUIRE(a->n > 0 && a->n % kLongCols == 0, "gemm_long: n must be a positive multiple of 128");
+  DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0 && a->ldx == a->k, "gemm_long: k a multiple of 64, ldx == k");
+  const int epi = a->epilogue;
+  DTREE_REQUIRE(epi >= 0 && epi <= 3, "gemm_long: unknown epilogue");
+  if (epi == DTREE_EPI_STORE_F32 || epi == DTREE_EPI_RESIDUAL)
+    DTREE_REQUIRE(a->out_f32 && a->ld_out_f32 >= a->n, "gemm_long: out_f32 missing or ld too small");
+  if (epi == DTREE_EPI_RESIDUAL)
+    DTREE_REQUIRE(a->out_bf16 && a->next_norm && a->ss_out && a->ld_out_bf16 >= a->n,
+                  "gemm_long: residual epilogue needs out_bf16, next_norm, ss_out");
+  if (epi == DTREE_EPI_SWIGLU)
+    DTREE_REQUIRE(a->out_bf16 && a->ld_out_bf16 >= a->n / 2, "gemm_long: swiglu needs out_bf16 (n/2 wide)");
+  if (epi == DTREE_EPI_STORE_BF16) DTREE_REQUIRE(a->out_bf16 && a->ld_out_bf16 >= a->n, "gemm_long: out_bf16");
+  if (a->hidden_out) DTREE_REQUIRE(a->ld_hidden >= a->n, "gemm_long: ld_hidden too small");
+  if (a->ss_in) DTREE_REQUIRE(a->ss_tiles > 0 && a->norm_dim > 0, "gemm_long: ss_in needs ss_tiles and norm_dim");
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR || a->out_layout == DTREE_W_TILED, "gemm_long: unknown out_layout");
+  if (a->out_layout == DTREE_W_TILED && a->out_bf16) {
+    const int width = epi == DTREE_EPI_SWIGLU ? a->n / 2 : a->n;
+    DTREE_REQUIRE(a->ld_out_bf16 == width && width % 64 == 0,
+                  "gemm_long: tiled out needs ld_out_bf16 == width, width % 64");
+  }
+  DTREE_REQUIRE(((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->x_lo & 15) == 0 && ((uintptr_t)a->w & 15) == 0,
+                "gemm_long: x, x_lo and w must be 16-byte aligned");
+  GemmParams p{};
+  p.x = a->x; p.x_lo = a->x_lo; p.ldx = a->ldx; p.w = a->w; p.n = a->n; p.k = a->k;
+  p.ss_in = a->ss_in; p.ss_tiles = a->ss_tiles;
+  p.inv_norm_dim = a->norm_dim > 0 ? 1.0f / (float)a->norm_dim : 1.f; p.eps = a->eps;
+  p.out_f32 = a->out_f32; p.ld_out_f32 = a->ld_out_f32;
+  p.out_bf16 = a->out_bf16; p.out_lo = a->out_lo; p.ld_out_bf16 = a->ld_out_bf16;
+  p.out_tiled = a->out_layout == DTREE_W_TILED;
+  p.next_norm = a->next_norm; p.ss_out = a->ss_out;
+  p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
+  const long long grid = (long long)(a->rows_padded / kLongRows) * (a->n / kLongCols);
+  DTREE_REQUIRE(grid < (1LL << 31), "gemm_long: grid too large");
+  if (a->x_lo) launch_long<true>(p, epi, (int)grid, stream);
+  else launch_long<false>(p, epi, (int)grid, stream);
+  DTREE_LAUNCH_CHECK("gemm_long launch");
   return DTREE_OK;
 }
 

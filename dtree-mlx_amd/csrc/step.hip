@@ -107,6 +107,37 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
   fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_tiled, ss);
 }
 
+// Gather + fold for a token array of any length (prompt prefill): row m < n
+// embeds tokens[m], rows n .. MP - 1 are zero.
+__global__ __launch_bounds__(256) void embed_tokens_kernel(const int32_t* tokens, int n, const uint16_t* emb,
+                                                           int layout, const uint16_t* emb_sb, int V, int H,
+                                                           const uint16_t* g, int MP, float* x, uint16_t* xg,
+                                                           uint16_t* xg_lo, int xg_tiled, float* ss) {
+  const int per_row = H >> 3;
+  const long long gt = (long long)blockIdx.x * 256 + threadIdx.x;
+  const bool in = gt < (long long)MP * per_row;
+  const int m = in ? (int)(gt / per_row) : 0, col = in ? (int)(gt % per_row) * 8 : 0;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  if (in && m < n) {
+    const int tok = tokens[m];
+    if (tok >= 0 && tok < V) {
+      if (layout == DTREE_W_Q4G64) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = q4_element(reinterpret_cast<const uint32_t*>(emb), reinterpret_cast<const uint32_t*>(emb_sb), tok,
+                            col + i, H);
+      } else {
+        const u32x4_t w = ld_u32x4(emb + (layout == DTREE_W_TILED ? tiled_index(tok, col, H) : (size_t)tok * H + col));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+      }
+    }
+  }
+  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_tiled, ss);
+}
+
 // The same layer-input fold for rows handed over by the caller (the DFlash
 // drafter's noise embedding, draft.py:355-364): x[m] = rows[m] (bf16, rows
 // >= n_rows zero), then fold_store8.
@@ -402,6 +433,30 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
                                                           xg_layout == DTREE_W_TILED, ss, head_dim / 2, rope_base,
                                                           rope_cos, rope_sin, gather);
   DTREE_LAUNCH_CHECK("embed launch");
+  return DTREE_OK;
+}
+
+extern "C" int dtree_embed_tokens(const int32_t* tokens, int32_t n, const uint16_t* embed, int32_t embed_layout,
+                                  const uint16_t* embed_scales, int32_t vocab, int32_t hidden, const uint16_t* norm_w,
+                                  int32_t rows_padded, float* x, uint16_t* xg, uint16_t* xg_lo, int32_t xg_layout,
+                                  float* ss, hipStream_t stream) {
+  DTREE_REQUIRE(tokens && embed && norm_w && x && xg && ss, "embed_tokens: null pointer");
+  DTREE_REQUIRE(hidden > 0 && hidden % 64 == 0, "embed_tokens: hidden must be a multiple of 64");
+  DTREE_REQUIRE(vocab > 0 && vocab % 32 == 0, "embed_tokens: vocab");
+  DTREE_REQUIRE(embed_layout == DTREE_W_ROWMAJOR || embed_layout == DTREE_W_TILED || embed_layout == DTREE_W_Q4G64,
+                "embed_tokens: layout");
+  DTREE_REQUIRE(embed_layout != DTREE_W_Q4G64 || embed_scales, "embed_tokens: q4 embedding needs embed_scales");
+  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || xg_layout == DTREE_W_TILED, "embed_tokens: xg layout");
+  DTREE_REQUIRE(rows_padded > 0 && rows_padded % 32 == 0 && rows_padded <= (1 << 20) && n >= 0 && n <= rows_padded,
+                "embed_tokens: rows_padded (a multiple of 32) and n <= rows_padded");
+  DTREE_REQUIRE(((uintptr_t)embed & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
+                    ((uintptr_t)xg & 15) == 0 && ((uintptr_t)xg_lo & 15) == 0,
+                "embed_tokens: embed, norm_w, x, xg and xg_lo must be 16-byte aligned");
+  const long long threads = (long long)rows_padded * (hidden / 8);
+  embed_tokens_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
+      tokens, n, embed, embed_layout, embed_scales, vocab, hidden, norm_w, rows_padded, x, xg, xg_lo,
+      xg_layout == DTREE_W_TILED, ss);
+  DTREE_LAUNCH_CHECK("embed_tokens launch");
   return DTREE_OK;
 }
 

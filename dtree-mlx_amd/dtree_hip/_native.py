@@ -139,6 +139,8 @@ SIGNATURES = {
     "dtree_tree_build_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "dtree_tree_build": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _sz, _vp, _vp, _vp, _vp,
                                    _vp]),
+    "dtree_gemm_long": (C.c_int, [C.POINTER(GemmArgs), _vp]),
+    "dtree_embed_tokens": (C.c_int, [_vp, _i32, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "dtree_rows_in": (C.c_int, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp]),
     "dtree_kv_append": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _f32, _i32, _i32, _f32, _i32, _i32, _vp, _vp, _vp, _i32,
                                   _vp]),

@@ -178,12 +178,21 @@ class Qwen3TargetAdapter(MLXTargetAdapter):
 
     def forward_with_hidden_states(self, model: Qwen3TreeModel, inputs, cache: PagedKVCache, layer_ids,
                                    return_rollback_records: bool = False):
-        """Prefill through the tree kernels (causal chains of <= 32 tokens).
-        Returns the logits of the last position only ([1, 1, V]) and the
-        verifier hidden states of every position."""
+        """Causal forward over the prompt: the long-M GEMM path for 128 tokens
+        or more (bf16 weights), else chains of up to max_nodes tokens through
+        the tree kernels. Returns the logits of the last position only
+        ([1, 1, V], all the callers read) and the verifier hidden states of
+        every position."""
         eng = model.engine
         eng.set_layer_ids(layer_ids)
         toks = _as_list(inputs)
+        if len(toks) >= 128 and eng.supports_long_prefill():
+            logits, hidden = eng.prefill_long(cache, toks)
+            target_hidden = (hidden[None] if hidden is not None
+                             else torch.zeros(1, len(toks), 0, device=eng.dev))
+            if return_rollback_records:
+                return logits, target_hidden, {}
+            return logits, target_hidden
         hid = []
         for s in range(0, len(toks), eng.max_nodes):
             part = toks[s:s + eng.max_nodes]

@@ -415,9 +415,14 @@ class TreeEngineBase:
         self.launch_forward(cache, self.stream_handle(), norm_hidden=norm_hidden)
 
     def prefill(self, cache: PagedKVCache, tokens, chunk: int | None = None) -> None:
-        """Causal prefill through the tree path: chains of up to max_nodes tokens."""
-        chunk = chunk or self.max_nodes
+        """Causal prefill: the long-M path (prefill_long) for prompts of 128
+        tokens or more where the engine has one, else chains of up to
+        max_nodes tokens through the tree path."""
         toks = [int(t) for t in tokens]
+        if chunk is None and len(toks) >= 128 and getattr(self, "supports_long_prefill", lambda: False)():
+            self.prefill_long(cache, toks, want_logits=False)
+            return
+        chunk = chunk or self.max_nodes
         for s in range(0, len(toks), chunk):
             part = toks[s:s + chunk]
             P = cache.offset
@@ -579,6 +584,145 @@ class Qwen3TreeEngine(TreeEngineBase):
             N.check(self.lib.dtree_rownorm(self.x.data_ptr(), H, self.MP, H, self.ss.data_ptr(), H // 32,
                                            self.w.final_norm.data_ptr(), c.rms_norm_eps,
                                            self.norm_hidden.data_ptr(), H, st), "rownorm")
+
+    # ---- prompt prefill on the long-M GEMM (adapters.py:494-533) ---------------
+    PREFILL_SEGMENT = 1024  # prompt rows per pass through the layer stack (a multiple of 128)
+
+    def supports_long_prefill(self) -> bool:
+        return self.w.layout == W_TILED and not isinstance(self.w.layers[0].wqkv, Q4Linear)
+
+    def _prefill_buffers(self, rows: int) -> dict:
+        pf = getattr(self, "_pf", None)
+        if pf is not None and pf["rows"] >= rows and pf["nh"] == max(1, len(self.layer_ids)):
+            return pf
+        c, dev = self.cfg, self.dev
+        H, F, D = c.hidden_size, c.intermediate_size, c.head_dim
+        f32, bf16 = torch.float32, torch.bfloat16
+        nh = max(1, len(self.layer_ids))
+        pf = dict(rows=rows, nh=nh,
+                  tokens=torch.zeros(rows, dtype=torch.int32, device=dev),
+                  x=torch.zeros(rows, H, dtype=f32, device=dev),
+                  xg=torch.zeros(2, rows, H, dtype=bf16, device=dev),
+                  ss=torch.zeros(rows // 32, H // 32, 32, dtype=f32, device=dev),
+                  qkv=torch.zeros(rows, c.qkv_dim, dtype=f32, device=dev),
+                  attn=torch.zeros(2, rows, c.q_dim, dtype=bf16, device=dev),
+                  act=torch.zeros(2, rows, F, dtype=bf16, device=dev),
+                  hidden=torch.zeros(rows, nh * H, dtype=bf16, device=dev),
+                  cos=torch.zeros(rows, D // 2, dtype=f32, device=dev),
+                  sin=torch.zeros(rows, D // 2, dtype=f32, device=dev),
+                  descs=torch.zeros(rows // 128, C.sizeof(N.StepDesc), dtype=torch.uint8, device=dev),
+                  attn_ws=torch.zeros(self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, D,
+                                                                               self.max_past, 128),
+                                      dtype=torch.uint8, device=dev))
+        self._pf = pf
+        return pf
+
+    def _long_gemm(self, name, x, k, w, epi, rows, st, **kw):
+        a = self.gemm_args(name, x, k, w, epi, **kw)
+        a.rows_padded = rows
+        N.check(self.lib.dtree_gemm_long(C.byref(a), st), f"long gemm {name}")
+
+    def prefill_long(self, cache: PagedKVCache, tokens, want_logits: bool = True):
+        """Causal forward over the prompt with the long-M GEMM: per segment of
+        up to PREFILL_SEGMENT tokens, embed, then per layer the fused QKV GEMM,
+        attention per 128-row chunk (a chain "tree" over the cached prefix,
+        appending its K/V rows), o_proj, gate/up and down_proj. Returns the
+        fp32 logits of the last position ([1, 1, V]) if asked and the
+        verifier hidden rows of every position ([n, n_ids * H] bf16 or None)."""
+        if not self.supports_long_prefill():
+            raise NotImplementedError("the long-M prefill runs tiled bf16 weights")
+        c = self.cfg
+        H, D = c.hidden_size, c.head_dim
+        toks = [int(t) for t in tokens]
+        if not toks:
+            raise ValueError("empty prompt")
+        if any(t < 0 or t >= c.vocab_size for t in toks):
+            raise ValueError("token id outside the vocabulary")
+        if cache.offset + len(toks) > self.max_past:
+            raise ValueError(f"prefill of {len(toks)} tokens beyond max_past {self.max_past}")
+        st = self.stream_handle()
+        emb, emb_layout, emb_sb = self._embedding()
+        slot = {li: i for i, li in enumerate(self.layer_ids)}
+        hid_parts = []
+        seg = self.PREFILL_SEGMENT
+        last_block = None
+        for s0 in range(0, len(toks), seg):
+            part = toks[s0:s0 + seg]
+            n = len(part)
+            rows = 128 * ((n + 127) // 128)
+            pf = self._prefill_buffers(max(rows, seg if len(toks) > seg else rows))
+            P0 = cache.offset
+            pf["tokens"][:n].copy_(torch.tensor(part, dtype=torch.int32))
+            nch = rows // 128
+            recs = np.zeros(nch, dtype=N.STEP_DESC_DTYPE)
+            for ch in range(nch):
+                L = min(128, n - 128 * ch)
+                r = recs[ch]
+                r["past_length"] = P0 + 128 * ch
+                r["num_nodes"] = L
+                r["bonus_token"] = -1
+                r["positions"][:L] = np.arange(P0 + 128 * ch, P0 + 128 * ch + L)
+                r["parents"][:] = -1
+                r["parents"][1:L] = np.arange(L - 1)
+                r["ancestors"][:L] = ancestor_bitsets([-1] + list(range(L - 1)))
+            pf["descs"][:nch].copy_(torch.from_numpy(recs.view(np.uint8).reshape(nch, -1)))
+            N.check(self.lib.dtree_embed_tokens(
+                pf["tokens"].data_ptr(), n, emb, emb_layout, emb_sb, c.vocab_size, H,
+                self.w.layers[0].input_norm.data_ptr(), rows, pf["x"].data_ptr(), pf["xg"][0].data_ptr(),
+                pf["xg"][1].data_ptr(), self.w.layout, pf["ss"].data_ptr(), st), "embed tokens")
+            dstride = pf["descs"].shape[1]
+            for ch in range(nch):
+                N.check(self.lib.dtree_rope_table(pf["descs"].data_ptr() + ch * dstride, 128, D, c.rope_theta,
+                                                  pf["cos"][128 * ch].data_ptr(), pf["sin"][128 * ch].data_ptr(), st),
+                        "rope table")
+            nL = c.num_hidden_layers
+            for li in range(nL):
+                lw = self.w.layers[li]
+                nxt = self.w.layers[li + 1].input_norm if li + 1 < nL else self.w.final_norm
+                self._long_gemm("qkv", pf["xg"], H, lw.wqkv, N.EPI_STORE_F32, rows, st, ss_in=pf["ss"],
+                                out_f32=pf["qkv"])
+                for ch in range(nch):
+                    a = N.AttnArgs()
+                    a.qkv = pf["qkv"][128 * ch].data_ptr(); a.ld_qkv = c.qkv_dim
+                    a.q_norm = lw.q_norm.data_ptr(); a.k_norm = lw.k_norm.data_ptr(); a.eps = c.rms_norm_eps
+                    a.rope_cos = pf["cos"][128 * ch].data_ptr(); a.rope_sin = pf["sin"][128 * ch].data_ptr()
+                    a.k_pages = cache.k_ptr(li); a.v_pages = cache.v_ptr(li)
+                    a.page_table = cache.page_table.data_ptr()
+                    a.desc = pf["descs"].data_ptr() + ch * dstride
+                    a.out = pf["attn"][0, 128 * ch].data_ptr(); a.out_lo = pf["attn"][1, 128 * ch].data_ptr()
+                    a.ld_out = c.q_dim; a.out_layout = self.w.layout
+                    a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = D
+                    a.rows_padded = 128; a.scale = D ** -0.5
+                    a.max_past_length = self.max_past; a.write_cache = 1
+                    a.workspace = pf["attn_ws"].data_ptr(); a.workspace_bytes = pf["attn_ws"].numel()
+                    N.check(self.lib.dtree_tree_attention(C.byref(a), st), "prefill attention")
+                self._long_gemm("o", pf["attn"], c.q_dim, lw.wo, N.EPI_RESIDUAL, rows, st, out_f32=pf["x"],
+                                out_bf16=pf["xg"], next_norm=lw.post_norm, ss_out=pf["ss"])
+                self._long_gemm("gu", pf["xg"], H, lw.wgu, N.EPI_SWIGLU, rows, st, ss_in=pf["ss"], out_bf16=pf["act"])
+                hid, ldh = 0, 0
+                if li in slot:
+                    hid = pf["hidden"].data_ptr() + 2 * slot[li] * H
+                    ldh = pf["hidden"].shape[1]
+                self._long_gemm("down", pf["act"], c.intermediate_size, lw.wd, N.EPI_RESIDUAL, rows, st,
+                                out_f32=pf["x"], out_bf16=pf["xg"], next_norm=nxt, ss_out=pf["ss"],
+                                hidden_out=hid, ld_hidden=ldh)
+            cache.offset = P0 + n
+            if self.layer_ids:
+                hid_parts.append(pf["hidden"][:n].clone())
+            last_block = ((n - 1) // 32, (n - 1) % 32)
+        logits = None
+        if want_logits:
+            b, r = last_block
+            if self.logits is None:
+                self.logits = torch.zeros(self.MP, c.vocab_size, dtype=torch.float32, device=self.dev)
+            xo = b * 32 * H
+            N.check(self.lib.dtree_lmhead_argmax(
+                pf["xg"][0].data_ptr() + 2 * xo, pf["xg"][1].data_ptr() + 2 * xo, self.w.layout, H, 32, emb,
+                emb_layout, emb_sb, c.vocab_size, H, pf["ss"][b].data_ptr(), H // 32, c.rms_norm_eps,
+                self.logits.data_ptr(), self.cand.data_ptr(), st), "prefill lm head")
+            logits = self.logits[r:r + 1].clone()[None]
+        hidden = torch.cat(hid_parts, 0) if hid_parts else None
+        return logits, hidden
 
     def launch_compact(self, cache: PagedKVCache, st: int, select_hidden: bool = True, aux: bool = False) -> None:
         c = self.cfg

@@ -292,6 +292,22 @@ int dtree_rownorm(const float* x, int32_t ldx, int32_t rows_padded, int32_t hidd
                   uint16_t* out, int32_t ld_out, hipStream_t stream);
 
 /*
+ * Prompt prefill (forward_with_hidden_states, adapters.py:494-533: the
+ * target's causal forward over the prompt). dtree_gemm_long is the
+ * compute-bound GEMM for rows_padded = a multiple of 128 (any length):
+ * tiled bf16 activations (split pair optional) and tiled bf16 weights,
+ * n a multiple of 128, the four epilogues of dtree_gemm_bf16 with outputs,
+ * statistics and hidden rows laid out as there (per 32-row block).
+ * dtree_embed_tokens is dtree_embed for a device token array of any length
+ * (rows n .. rows_padded - 1 zero), without the RoPE table.
+ */
+int dtree_gemm_long(const DtreeGemmArgs* args, hipStream_t stream);
+int dtree_embed_tokens(const int32_t* tokens, int32_t n, const uint16_t* embed, int32_t embed_layout,
+                       const uint16_t* embed_scales, int32_t vocab, int32_t hidden, const uint16_t* norm_w,
+                       int32_t rows_padded, float* x, uint16_t* xg, uint16_t* xg_lo, int32_t xg_layout, float* ss,
+                       hipStream_t stream);
+
+/*
  * Layer input from caller rows instead of token ids: the DFlash drafter's
  * noise embedding enters its first decoder layer (DFlashDraftModel.__call__,
  * draft.py:349-364, input_layernorm at draft.py:294-295). rows: bf16
