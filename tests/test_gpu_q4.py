@@ -128,6 +128,97 @@ def test_q4_gemm_residual_and_swiglu(gpu_device):
     assert np.all(np.abs(bf16_f32(act) - ref) <= 1e-2 * np.abs(ref) + 1e-5 * np.abs(ref).max())
 
 
+def _q4_layer_case(epi, g, dev):
+    """Qwen3-4B layer shapes that take the two-workgroups-per-CU stream-K
+    kernel (sk2_gemm_kernel: at least 20 units per CU): down_proj with the
+    residual epilogue (N 2560, K 9728) and gate/up with SwiGLU (N 19456,
+    K 2560)."""
+    L = 25
+    if epi == N.EPI_RESIDUAL:
+        n, k = 2560, 9728
+        wq, s, b = o4.random_q4(n, k, g)
+        wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+        ref_w = [(wq, s, b)]
+    else:
+        F, k = 9728, 2560
+        n = 2 * F
+        gq, gs, gb = o4.random_q4(F, k, g)
+        uq, us, ub = o4.random_q4(F, k, g)
+        wq2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int32)) for t in (gq, uq)])
+        s2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int16)) for t in (gs, us)])
+        b2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int16)) for t in (gb, ub)])
+        wt, sb = q4_to_tiled(wq2, s2.view(torch.bfloat16), b2.view(torch.bfloat16))
+        ref_w = [(gq, gs, gb), (uq, us, ub)]
+    xt, xlt, xin = _x(L, k, g, dev, True)
+    return n, k, wt.to(dev), sb.to(dev), xt, xlt, xin, ref_w
+
+
+def _run_q4_layer(epi, n, k, wt, sb, xt, xlt, g_seed, dev):
+    g = np.random.default_rng(g_seed)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, n, k, 0), dtype=torch.uint8, device=dev)
+    a = _args(xt, xlt, wt, sb, n, k, epi, ws)
+    out = {}
+    if epi == N.EPI_RESIDUAL:
+        res = torch.zeros(32, n)
+        res[:25] = torch.from_numpy(g.standard_normal((25, n)).astype(np.float32))
+        out["res0"] = res.clone()
+        out["res"] = res.to(dev)
+        out["gn"] = torch.from_numpy((1 + 0.1 * g.standard_normal(n)).astype(np.float32)).to(torch.bfloat16).to(dev)
+        out["xg"] = torch.zeros(32, n, dtype=torch.bfloat16, device=dev)
+        out["ss"] = torch.zeros(n // 32, 32, device=dev)
+        a.out_f32 = out["res"].data_ptr(); a.ld_out_f32 = n
+        a.out_bf16 = out["xg"].data_ptr(); a.ld_out_bf16 = n
+        a.next_norm = out["gn"].data_ptr(); a.ss_out = out["ss"].data_ptr()
+    else:
+        out["rsq"] = torch.from_numpy(np.abs(g.standard_normal((k // 32, 32))).astype(np.float32) + 0.5).to(dev)
+        out["act"] = torch.zeros(32, n // 2, dtype=torch.bfloat16, device=dev)
+        a.ss_in = out["rsq"].data_ptr(); a.ss_tiles = k // 32; a.norm_dim = k; a.eps = 1e-6
+        a.out_bf16 = out["act"].data_ptr(); a.ld_out_bf16 = n // 2
+    N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 layer gemm")
+    torch.cuda.synchronize()
+    out["ws"] = ws
+    return out
+
+
+@pytest.mark.parametrize("epi", [N.EPI_RESIDUAL, N.EPI_SWIGLU])
+def test_q4_sk2_layer_shapes(gpu_device, epi):
+    g = np.random.default_rng(91 + epi)
+    n, k, wt, sb, xt, xlt, xin, ref_w = _q4_layer_case(epi, g, gpu_device)
+    runs = [_run_q4_layer(epi, n, k, wt, sb, xt, xlt, 5, gpu_device) for _ in range(2)]
+    if epi == N.EPI_RESIDUAL:
+        wq, s, b = ref_w[0]
+        ref = runs[0]["res0"].double().numpy() + o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b))
+        got = runs[0]["res"].cpu().numpy()
+        assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+        assert torch.equal(runs[0]["xg"].cpu(), (torch.from_numpy(got) * runs[0]["gn"].float().cpu()).to(torch.bfloat16))
+        for key in ("res", "xg", "ss"):
+            assert torch.equal(runs[0][key], runs[1][key]), key
+    else:
+        rs = 1.0 / np.sqrt(runs[0]["rsq"].cpu().numpy().sum(0) / k + 1e-6)
+        (gq, gs, gb), (uq, us, ub) = ref_w
+        gt = o4.q4_matmul(xin, gq, bf16_to_f32(gs), bf16_to_f32(gb)) * rs[:, None]
+        up = o4.q4_matmul(xin, uq, bf16_to_f32(us), bf16_to_f32(ub)) * rs[:, None]
+        ref = gt / (1 + np.exp(-np.clip(gt, -80, 80))) * up
+        assert np.all(np.abs(bf16_f32(runs[0]["act"]) - ref) <= 1e-2 * np.abs(ref) + 1e-5 * np.abs(ref).max())
+        assert torch.equal(runs[0]["act"], runs[1]["act"])
+    for r in runs:  # counters self-reset
+        assert int(r["ws"][: (n // 64) * 4].view(torch.int32).abs().sum()) == 0
+
+
+def test_q4_sk2_partials_read_past_the_l2(gpu_device, monkeypatch):
+    """DTREE_TEST_OFF_XCD=1 makes every workgroup count as off its expected
+    XCD, so the two-per-CU q4 kernel reads its partial tiles past the L2; the
+    bits must equal the native run's."""
+    g = np.random.default_rng(123)
+    n, k, wt, sb, xt, xlt, xin, _ = _q4_layer_case(N.EPI_RESIDUAL, g, gpu_device)
+    native = _run_q4_layer(N.EPI_RESIDUAL, n, k, wt, sb, xt, xlt, 6, gpu_device)
+    monkeypatch.setenv("DTREE_TEST_OFF_XCD", "1")
+    off = _run_q4_layer(N.EPI_RESIDUAL, n, k, wt, sb, xt, xlt, 6, gpu_device)
+    monkeypatch.delenv("DTREE_TEST_OFF_XCD")
+    for key in ("res", "xg", "ss"):
+        assert torch.equal(native[key], off[key]), key
+
+
 def _x96(L, k, g, dev):
     xf = np.zeros((96, k), np.float32)
     xf[:L] = g.standard_normal((L, k))
