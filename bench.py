@@ -402,16 +402,22 @@ def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -
     return f"gqa_tree_attn_kernel<{D}, {R}, {g}, 4>" if group else f"tree_attn_kernel<{D}, {R}, {g}, {1 if MP == 32 else 4}>"
 
 
-def gemm_kernel_name(n: int, k: int, epi: int, quant: str) -> str:
-    """Kernel the library picks for a 32-row tiled GEMM with split_k 0: for
-    bf16 with K <= 4096 and N <= 12800 one workgroup per 32-column tile, two
-    or three (one per part of K) at K = 4096 and N % 256 == 0; the stream-K
-    schedule otherwise, for q4 at two workgroups per CU when there are at
-    least 20 64 x 64 units per CU (gemm.hip, dtree_gemm_bf16)."""
-    if quant == "bf16" and k <= 4096 and n <= 12800:
-        parts = (3 if (n // 32) * 3 <= 256 else 2) if k >= 4096 and n % 256 == 0 else 1  # 256 CUs
-        return f"dp_gemm_kernel<true, {epi}, {parts}>"
-    if quant == "q4" and (n // 64) * (k // 64) >= 20 * 256:
+def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256) -> str:
+    """Kernel the library picks for a 32-row tiled GEMM with split_k 0
+    (gemm.hip, dtree_gemm_bf16). bf16: three workgroups per 32-column tile
+    (one per part of K) at K >= 4096 and N % 256 == 0 when 3 N / 32 fit the
+    CUs, two at K = 4096 when 2 N / 32 do; else one per tile at K <= 4096 and
+    N / 32 <= CUs; else stream-K. q4: stream-K, two workgroups per CU when
+    there are at least 20 64 x 64 units per CU."""
+    if quant == "bf16":
+        if k >= 4096 and n % 256 == 0:
+            if (n // 32) * 3 <= cus:
+                return f"dp_gemm_kernel<true, {epi}, 3>"
+            if k == 4096 and (n // 32) * 2 <= cus:
+                return f"dp_gemm_kernel<true, {epi}, 2>"
+        if k <= 4096 and n // 32 <= cus:
+            return f"dp_gemm_kernel<true, {epi}, 1>"
+    if quant == "q4" and (n // 64) * (k // 64) >= 20 * cus:
         return f"sk2_gemm_kernel<true, {epi}>"
     return f"sk_gemm_kernel<true, {epi}, {'true' if quant == 'q4' else 'false'}>"
 

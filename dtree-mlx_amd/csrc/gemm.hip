@@ -1389,22 +1389,28 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     const int width = epi == DTREE_EPI_SWIGLU ? a->n / 2 : a->n;
     DTREE_REQUIRE(a->ld_out_bf16 == width && width % 64 == 0, "gemm: tiled out needs ld_out_bf16 == width, width % 64");
   }
-  // One workgroup per 32-column tile over the whole K when asked (split_k -1)
-  // or, automatically, for the shapes where it beats the stream-K schedule on
-  // MI355X (K <= 4096 and N <= 12800, e.g. the fused QKV and o_proj at hidden
-  // 2560): no cross-workgroup reduction tail, at the price of re-reading the
-  // activations per tile and of fewer than 256 workgroups on narrow N.
-  // Of those, K = 4096 (o_proj, out_proj) runs two or three workgroups per
-  // tile: 11.4 vs 15.8 us at N = 2560; at K = 2560 the parts are too short
-  // (QKV N = 6144: 16.7 vs 12.4 us).
-  const bool dp_auto = a->split_k == 0 && a->k <= 4096 && a->n <= 12800;
-  const bool pairs_auto = dp_auto && a->k >= 4096 && a->n % 256 == 0;
+  // Automatic choice among the 32-row tiled schedules (split_k 0), from
+  // measurements on MI355X with the weights streamed from HBM:
+  // * K >= 4096 over N % 256 == 0: three workgroups per tile, one per part of
+  //   K, when N / 32 * 3 <= CUs (o_proj N = 2560: 11.3 vs 16.1 us stream-K;
+  //   down_proj N = 2560, K = 9728: 17.2 vs 20.2 us), else two at K = 4096
+  //   (N = 4096: 12.6 vs 14.8 us; at K = 12288 stream-K wins, 24.6 vs 26.2);
+  // * else K <= 4096 with at most one tile per CU: one workgroup per tile over
+  //   the whole K, no cross-workgroup reduction tail (QKV N = 6144: 12.5 vs
+  //   14.5 us stream-K);
+  // * else stream-K: more tiles than CUs (N = 10240: 18.2 vs 22.7 us one per
+  //   tile) or long K on narrow N.
+  const int auto_cus = device_cus();
+  const bool k_auto = a->split_k == 0 && tiled && !q4 && a->rows_padded == 32;
+  const bool pairs_auto = k_auto && a->k >= 4096 && a->n % 256 == 0 &&
+                          ((a->n / 32) * 3 <= auto_cus || (a->k == 4096 && (a->n / 32) * 2 <= auto_cus));
+  const bool dp_auto = k_auto && !pairs_auto && a->k <= 4096 && a->n / 32 <= auto_cus;
   if (tiled && !q4 && a->rows_padded == 32 && (a->split_k == -3 || a->split_k == -4 || pairs_auto)) {
     // Two (-3) or three (-4) workgroups per tile, one per part of K (see
     // dp_gemm_kernel).
     // automatic: three parts while the grid stays within one workgroup per CU
     // (o_proj: 240 workgroups, 11.4 us; two parts 11.9 us)
-    const int dp_parts = a->split_k == -4 ? 3 : a->split_k == -3 ? 2 : (a->n / 32) * 3 <= device_cus() ? 3 : 2;
+    const int dp_parts = a->split_k == -4 ? 3 : a->split_k == -3 ? 2 : (a->n / 32) * 3 <= auto_cus ? 3 : 2;
     DTREE_REQUIRE(a->n % 256 == 0 && nkb >= dp_parts,
                   "gemm: split_k -3 / -4 need n % 256 == 0 and k >= 64 * parts");
     const size_t need_pairs = dp_pair_workspace_bytes(a->n);
