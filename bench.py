@@ -371,7 +371,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    kn = lambda n, k, epi: gemm_kernel_name(n, k, epi, quant)  # noqa: E731
+    kn = lambda n, k, epi: gemm_kernel_name(n, k, epi, quant, rows=eng.MP)  # noqa: E731
     out = {
         "in_proj_gemm": entry(kn(cfg.in_proj_dim, H, 0), nG, us["in"], b["in"]),
         "out_proj_gemm": entry(kn(H, cfg.value_dim, 1), nG, us["out"], b["out"]),
@@ -402,13 +402,19 @@ def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -
     return f"gqa_tree_attn_kernel<{D}, {R}, {g}, 4>" if group else f"tree_attn_kernel<{D}, {R}, {g}, {1 if MP == 32 else 4}>"
 
 
-def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256) -> str:
-    """Kernel the library picks for a 32-row tiled GEMM with split_k 0
-    (gemm.hip, dtree_gemm_bf16). bf16: three workgroups per 32-column tile
-    (one per part of K) at K >= 4096 and N % 256 == 0 when 3 N / 32 fit the
-    CUs, two at K = 4096 when 2 N / 32 do; else one per tile at K <= 4096 and
-    N / 32 <= CUs; else stream-K. q4: stream-K, two workgroups per CU when
-    there are at least 20 64 x 64 units per CU."""
+def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows: int = 32) -> str:
+    """Kernel the library picks for a tiled GEMM with split_k 0 (gemm.hip,
+    dtree_gemm_bf16). q4 over 64-128 rows: the one-pass kernel, two 64-column
+    blocks per workgroup unless a 4-block tiling still covers half the CUs.
+    32 rows, bf16: three workgroups per 32-column tile (one per part of K) at
+    K >= 4096 and N % 256 == 0 when 3 N / 32 fit the CUs, two at K = 4096 when
+    2 N / 32 do; else one per tile at K <= 4096 and N / 32 <= CUs; else
+    stream-K. q4 at 32 rows: stream-K, two workgroups per CU when there are at
+    least 20 64 x 64 units per CU."""
+    if quant == "q4" and rows > 32:
+        nblk = n // 64
+        cw = 4 if nblk % 4 == 0 and 2 * (nblk // 4) >= cus else 2
+        return f"q4m_gemm_kernel<true, {epi}, {rows // 32}, {cw}>"
     if quant == "bf16":
         if k >= 4096 and n % 256 == 0:
             if (n // 32) * 3 <= cus:

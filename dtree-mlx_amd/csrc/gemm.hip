@@ -810,6 +810,240 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   sk_gemm_body<LO, EPI, true, 3, 2>(p);
 }
 
+// ---- q4 GEMM over 64-128 rows in one pass -------------------------------------
+//
+// For the 65-node trees of the 9B-shaped step (96 rows) the 32-row q4 kernels
+// stream and dequantise the weights once per 32-row block. This kernel makes
+// one pass: a workgroup owns a tile of CW 64-column blocks and one part of K,
+// with one wave per (K lane kl, row block rb, column block cb): 64 * MB * 4
+// threads (KI = 4 / CW K lanes). Per step the workgroup stages the next KI
+// groups' activations (all row blocks, hi and lo planes; 4 KB per row block
+// and plane) in LDS with coalesced 16-byte loads, double buffered and
+// prefetched a step ahead in registers, so each activation byte is loaded
+// once per workgroup and read from LDS by the CW waves that use it. A wave
+// holds one 32 x 64 accumulator, so two or three waves share each SIMD and
+// one wave's scale/bias arithmetic overlaps another's MFMAs. Per group a wave
+// dequantises its column block's q4 words (128 + q as bf16, exact), runs
+// the MFMAs of its row block, and takes sum(x) per row (for the affine bias
+// and the 128 offset) from an MFMA of the activations against bf16 ones, as
+// in the 32-row kernels. The K lanes are added in LDS in lane order; the
+// parts of a tile are added by the last part to arrive, in part order
+// (deterministic), which then runs the shared tile epilogue per 64-column
+// block.
+template <bool LO, int MB, int CW>
+struct Q4mShape {
+  static constexpr int KI = kWaves / CW;                 // K lanes
+  static constexpr int NPL = LO ? 2 : 1;                 // activation planes
+  static constexpr int MP = MB * 32;                     // rows
+  static constexpr int THREADS = kThreads * MB;          // one wave per (kl, rb, cb)
+  static constexpr int CHUNKS = KI * MB * NPL;           // 4 KB activation chunks per step
+  static constexpr int STAGE_BYTES = CHUNKS * 4096;
+  static constexpr int LOADS = STAGE_BYTES / (THREADS * 16);  // 16-byte pieces per thread per step
+  static constexpr int TILE_FLOATS = CW * MP * 64;       // one part's output tile
+  static constexpr int RED_BYTES = KI * TILE_FLOATS * 4;
+  static constexpr int LDS_BYTES = 2 * STAGE_BYTES > RED_BYTES ? 2 * STAGE_BYTES : RED_BYTES;
+};
+constexpr int kQ4mDepth = 2;  // weight groups in flight per wave
+
+template <bool LO, int EPI, int MB, int CW>
+__global__ __launch_bounds__(kThreads * MB) void q4m_gemm_kernel(GemmParams p) {
+  using Sh = Q4mShape<LO, MB, CW>;
+  constexpr int KI = Sh::KI, NPL = Sh::NPL, MP = Sh::MP, D = kQ4mDepth, NT = Sh::THREADS;
+  constexpr int TF = Sh::TILE_FLOATS;
+  static_assert(Sh::LOADS * NT * 16 == Sh::STAGE_BYTES, "staging pieces");
+  __shared__ __align__(16) unsigned char lds[Sh::LDS_BYTES];
+  __shared__ float rs[MP];
+  __shared__ float rs_scratch[NT];
+  __shared__ int s_last;
+  const int t = threadIdx.x, lane = t & 63, c = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int cw = wave % CW, rb = (wave / CW) % MB, kl = wave / (CW * MB);
+  const int nkb = p.k >> 6, nblk = p.n >> 6, P = p.S;
+  const int tile = blockIdx.x / P, part = blockIdx.x % P;
+  const int g0 = (int)((long long)part * nkb / P), g1 = (int)((long long)(part + 1) * nkb / P);
+  const int nsteps = (g1 - g0 + KI - 1) / KI;
+  const int cb = tile * CW + cw;
+  const bool cb_ok = cb < nblk;
+
+  // The row scale's loads go out first (loads retire in order). Threads past
+  // the first kThreads load and add tiles the final sum never reads.
+  float ssv[kSsBatch];
+  ss_issue<MB>(p.ss_in, p.ss_tiles, ssv);
+
+  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(p.x, p.x_bytes), xlrs = buf_rsrc(p.x_lo, LO ? p.x_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(p.w, p.w_bytes), sbrs = buf_rsrc(p.w_sb, p.sb_bytes);
+  // Activation staging: piece j of thread t is piece t + j * NT of the step,
+  // i.e. bytes 16 * (piece % 256) of chunk q = piece / 256 = (K lane kk, row
+  // block rq, plane pl). Groups past the part read zero (ranged loads) and
+  // are never used.
+  u32x4_t xpre[Sh::LOADS];
+  auto x_issue = [&](int st) {
+#pragma unroll
+    for (int j = 0; j < Sh::LOADS; ++j) {
+      const int piece = t + j * NT, q = piece >> 8, tq = piece & 255;
+      const int kk = q / (MB * NPL), rq = (q / NPL) % MB, pl = q % NPL;
+      const int kb = g0 + st * KI + kk;
+      const unsigned off = kb < g1 ? (unsigned)(rq * nkb + kb) * 4096u + 16u * tq : kOob;
+      xpre[j] = pl == 0 ? buf_ld(xrs, off) : buf_ld(xlrs, off);
+    }
+  };
+  auto x_store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < Sh::LOADS; ++j)
+      *reinterpret_cast<u32x4_t*>(lds + buf * Sh::STAGE_BYTES + 16 * (t + j * NT)) = xpre[j];
+  };
+  // Weight ring: group j of this wave is kb = g0 + kl + KI * j; two 32-column
+  // halves (nb) of q4 words (1 KB each) and their (scale, bias) words.
+  u32x4_t wr[D][2];
+  uint32_t sbr[D][2];
+  auto w_issue = [&](int s, int j) {
+    const int kb = g0 + kl + KI * j;
+    const bool ok = cb_ok && kb < g1;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const unsigned blk = (unsigned)((2 * cb + nb) * nkb + kb);
+      wr[s][nb] = buf_ld_stream(wrs, ok ? (blk * 256u + lane * 4) * 4u : kOob);
+      sbr[s][nb] = buf_ld32(sbrs, ok ? (blk * 32u + c) * 4u : kOob);
+    }
+  };
+  f32x16_t acc[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[nb][r] = 0.f;
+  const u32x4_t ones = u32x4_t{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  const int xbase = ((kl * MB + rb) * NPL) * 4096 + lane * 16;
+  auto compute = [&](int s, int buf) {
+    u32x4_t xv[NPL][4];
+#pragma unroll
+    for (int pl = 0; pl < NPL; ++pl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xv[pl][i] = *reinterpret_cast<const u32x4_t*>(lds + buf * Sh::STAGE_BYTES + xbase + pl * 4096 + i * 1024);
+    f32x16_t xs;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) xs[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int pl = 0; pl < NPL; ++pl) xs = mfma32(xv[pl][i], ones, xs);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      f32x16_t au;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) au[r] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4_t bq = q4_pairs(wr[s][nb][i]);
+#pragma unroll
+        for (int pl = 0; pl < NPL; ++pl) au = mfma32(xv[pl][i], bq, au);
+      }
+      const float sc = __uint_as_float(sbr[s][nb] << 16);
+      const float cf = __uint_as_float(sbr[s][nb] & 0xffff0000u) - 128.f * sc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[nb][r] += sc * au[r] + cf * xs[r];
+    }
+  };
+
+  x_issue(0);
+#pragma unroll
+  for (int s = 0; s < D; ++s) w_issue(s, s);
+  ss_finish<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, ssv, rs, rs_scratch);
+  x_store(0);
+  x_issue(1);
+  __syncthreads();
+  // Step st: compute from LDS buffer st & 1, refill the weight slot, store
+  // step st + 1 (prefetched one step ago) into the other buffer, prefetch
+  // st + 2. (Prefetching two steps ahead in a second register set measured
+  // no faster: the steps are bound by issue, not by load latency.)
+  for (int st0 = 0; st0 < nsteps; st0 += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int st = st0 + s;
+      if (st < nsteps) {
+        if (cb_ok && g0 + st * KI + kl < g1) {
+          __builtin_amdgcn_sched_barrier(0);
+          compute(s, s & 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        w_issue(s, st + D);
+        x_store((s + 1) & 1);
+        x_issue(st + 2);
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- K lanes, then parts ----
+  float* red = reinterpret_cast<float*>(lds);  // [kl][cb][row][64]
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      red[((kl * CW + cw) * MP + rb * 32 + acc_row(r, h)) * 64 + nb * 32 + c] = acc[nb][r];
+  __syncthreads();
+  if constexpr (KI > 1) {
+    for (int e4 = t; e4 < TF / 4; e4 += NT) {
+      f32x4_t v = reinterpret_cast<const f32x4_t*>(red)[e4];
+#pragma unroll
+      for (int k2 = 1; k2 < KI; ++k2) v += reinterpret_cast<const f32x4_t*>(red + k2 * TF)[e4];
+      reinterpret_cast<f32x4_t*>(red)[e4] = v;
+    }
+    __syncthreads();
+  }
+  const int nvalid = min(CW, nblk - tile * CW);  // column blocks of this tile inside n
+  if (P > 1) {
+    const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
+    const unsigned tile_base = (unsigned)tile * (unsigned)P * (unsigned)(TF * 4);
+    const unsigned mine = tile_base + (unsigned)part * (unsigned)(TF * 4);
+    const int nf4 = nvalid * MP * 16;  // valid floats / 4 (blocks are [cb][row][64])
+    for (int e4 = t; e4 < nf4; e4 += NT)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, reinterpret_cast<const f32x4_t*>(red)[e4]),
+                                             prs, (int)(mine + 16u * e4), 0, kSc1);
+    wait_stores_done();
+    __syncthreads();
+    if (t == 0) {
+      const int old = arrive(&p.counters[tile]);
+      s_last = old == P - 1;
+      if (s_last) reset_counter(&p.counters[tile]);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int e4 = t; e4 < nf4; e4 += NT) {
+      f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < P; ++q) {
+        if (q == part) {
+          v += reinterpret_cast<const f32x4_t*>(red)[e4];
+        } else {
+          v += __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               prs, (int)(tile_base + (unsigned)q * (TF * 4) + 16u * e4), 0, kSc1));
+        }
+      }
+      reinterpret_cast<f32x4_t*>(red)[e4] = v;
+    }
+    __syncthreads();
+  }
+  // The tile epilogue is written for kThreads threads: the first four waves
+  // run it per (64-column block, 32-row block), outputs shifted by the row
+  // block (32-row blocks are contiguous in both output layouts; statistics
+  // are per 32-row block), which keeps its residual preloads at 8 per thread.
+  if (t < kThreads) {
+    for (int j = 0; j < nvalid; ++j) {
+#pragma unroll 1
+      for (int r2 = 0; r2 < MB; ++r2) {
+        const int R = 32 * r2;
+        GemmParams q = p;
+        if (q.out_f32) q.out_f32 += (size_t)R * q.ld_out_f32;
+        if (q.out_bf16) q.out_bf16 += (size_t)R * q.ld_out_bf16;
+        if (q.out_lo) q.out_lo += (size_t)R * q.ld_out_bf16;
+        if (q.hidden_out) q.hidden_out += (size_t)R * q.ld_hidden;
+        if (q.ss_out) q.ss_out += (size_t)r2 * (q.n >> 5) * 32;
+        tile_epilogue<32, 64, EPI>(q, red + (j * MP + R) * 64, rs + R, tile * CW + j);
+      }
+    }
+  }
+}
+
 // ---- LM head: persistent over vocab tiles, per-row running argmax --------
 struct LmParams {
   const uint16_t* x; const uint16_t* x_lo; int ldx;
@@ -967,6 +1201,71 @@ static size_t sk_workspace_bytes(int n, int k, int cus) {
   const int nkb = k / 64, nblk = n / 64, T = nblk * nkb;
   const int g1 = sk_grid(T, nkb, cus), g2 = sk2_grid(T, nkb, cus);
   return kCounterBytes + (size_t)((g1 > g2 ? g1 : g2) + nblk) * 32 * 64 * sizeof(float);
+}
+
+// q4 one-pass plan for 64-128 rows (q4m_gemm_kernel): CW 64-column blocks per
+// workgroup (4 when the tiles still cover half the CUs, else 2), and K parts
+// so that tiles x parts stays within the CU count of the current device (one
+// workgroup per CU: the LDS staging and K-lane reduction take 64-128 KB).
+// Workspace sizing and launch both plan for the current device. DTREE_Q4M_CW and
+// DTREE_Q4M_PARTS override the choice; DTREE_Q4M=0 sends these shapes back to
+// one 32-row pass per row block.
+struct Q4mPlan {
+  int cw, parts, tiles;
+};
+static int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+static bool q4m_enabled() {
+  static const int on = env_int("DTREE_Q4M", 1);
+  return on != 0;
+}
+static Q4mPlan q4m_plan(int n, int k, int cus) {
+  const int nblk = n / 64, nkb = k / 64;
+  static const int cw_env = env_int("DTREE_Q4M_CW", 0), parts_env = env_int("DTREE_Q4M_PARTS", 0);
+  Q4mPlan pl{};
+  pl.cw = cw_env == 2 || cw_env == 4 ? cw_env : ((nblk % 4 == 0 && 2 * (nblk / 4) >= cus) ? 4 : 2);
+  pl.tiles = (nblk + pl.cw - 1) / pl.cw;
+  const int ki = kWaves / pl.cw;
+  int parts = parts_env > 0 ? parts_env : cus / pl.tiles;
+  const int max_parts = nkb / ki;  // at least one step of groups per part
+  if (parts > max_parts) parts = max_parts;
+  if (parts < 1) parts = 1;
+  pl.parts = parts;
+  return pl;
+}
+static size_t q4m_workspace_bytes(int rows, int n, int k, int cus) {
+  const Q4mPlan pl = q4m_plan(n, k, cus);
+  if (pl.parts <= 1) return kCounterBytes;
+  return kCounterBytes + (size_t)pl.tiles * pl.parts * pl.cw * rows * 64 * sizeof(float);
+}
+
+template <bool LO, int MB, int CW>
+static void launch_q4m_mb(const GemmParams& p, int epi, int grid, hipStream_t st) {
+  switch (epi) {
+    case DTREE_EPI_STORE_F32: q4m_gemm_kernel<LO, DTREE_EPI_STORE_F32, MB, CW><<<grid, kThreads * MB, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: q4m_gemm_kernel<LO, DTREE_EPI_RESIDUAL, MB, CW><<<grid, kThreads * MB, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: q4m_gemm_kernel<LO, DTREE_EPI_SWIGLU, MB, CW><<<grid, kThreads * MB, 0, st>>>(p); break;
+    default: q4m_gemm_kernel<LO, DTREE_EPI_STORE_BF16, MB, CW><<<grid, kThreads * MB, 0, st>>>(p); break;
+  }
+}
+template <bool LO, int CW>
+static void launch_q4m_cw(const GemmParams& p, int epi, int mb, int grid, hipStream_t st) {
+  switch (mb) {
+    case 2: launch_q4m_mb<LO, 2, CW>(p, epi, grid, st); break;
+    case 3: launch_q4m_mb<LO, 3, CW>(p, epi, grid, st); break;
+    default: launch_q4m_mb<LO, 4, CW>(p, epi, grid, st); break;
+  }
+}
+static void launch_q4m(const GemmParams& p, int epi, int mb, int cw, int grid, hipStream_t st) {
+  if (p.x_lo) {
+    if (cw == 4) launch_q4m_cw<true, 4>(p, epi, mb, grid, st);
+    else launch_q4m_cw<true, 2>(p, epi, mb, grid, st);
+  } else {
+    if (cw == 4) launch_q4m_cw<false, 4>(p, epi, mb, grid, st);
+    else launch_q4m_cw<false, 2>(p, epi, mb, grid, st);
+  }
 }
 
 static int device_cus() {
@@ -1290,6 +1589,11 @@ extern "C" size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int 
     const size_t pairs = dp_pair_workspace_bytes(n);
     if (pairs > need) need = pairs;
   }
+  if (split_k <= 0 && rows_padded > 32 && rows_padded % 32 == 0 && n % 64 == 0) {
+    // q4 weights at 64-128 rows take the one-pass kernel (q4m_gemm_kernel).
+    const size_t q4m = q4m_workspace_bytes(rows_padded, n, k, device_cus());
+    if (q4m > need) need = q4m;
+  }
   return need;
 }
 
@@ -1342,6 +1646,32 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   const bool q4 = a->w_layout == DTREE_W_Q4G64;
   const bool tiled = a->w_layout == DTREE_W_TILED || q4;
   DTREE_REQUIRE(a->w_layout == DTREE_W_ROWMAJOR || tiled, "gemm: unknown w_layout");
+  if (q4 && a->rows_padded > 32 && q4m_enabled()) {
+    // One pass over the q4 weights for every row block (q4m_gemm_kernel).
+    DTREE_REQUIRE(a->x_layout == DTREE_W_TILED && a->ldx == a->k && a->split_k <= 0,
+                  "gemm: q4 weights need tiled activations (ldx == k) and split_k 0");
+    DTREE_REQUIRE(a->n % 64 == 0, "gemm: q4 weights need n % 64 == 0");
+    DTREE_REQUIRE(a->w_scales && ((uintptr_t)a->w & 15) == 0 && ((uintptr_t)a->w_scales & 3) == 0,
+                  "gemm: q4 weights need w (16-byte aligned) and w_scales (4-byte aligned)");
+    DTREE_REQUIRE(((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->x_lo & 15) == 0,
+                  "gemm: q4 activations must be 16-byte aligned");
+    const size_t xb = (size_t)a->rows_padded * a->k * 2, wb = (size_t)a->n * a->k / 2;
+    DTREE_REQUIRE(xb < kOob && wb < kOob, "gemm: operands must be smaller than 2 GiB");
+    const int cus = device_cus();
+    const Q4mPlan pl = q4m_plan(a->n, a->k, cus);
+    DTREE_REQUIRE((size_t)pl.tiles * sizeof(int) <= kCounterBytes, "gemm: n too large for the tile counter region");
+    const size_t need_m = q4m_workspace_bytes(a->rows_padded, a->n, a->k, cus);
+    DTREE_REQUIRE(a->workspace_bytes >= need_m, "gemm: workspace too small for the q4 one-pass schedule");
+    p.w_sb = a->w_scales;
+    p.x_bytes = (unsigned)xb;
+    p.w_bytes = (unsigned)wb;
+    p.sb_bytes = (unsigned)((size_t)a->n * (a->k / 64) * 4);
+    p.S = pl.parts;
+    p.part_bytes = (unsigned)(need_m - kCounterBytes);
+    launch_q4m(p, epi, a->rows_padded / 32, pl.cw, pl.tiles * pl.parts, stream);
+    DTREE_LAUNCH_CHECK("gemm launch");
+    return DTREE_OK;
+  }
   if (q4 && a->rows_padded > 32) {
     // q4 weights stream through the 32-row kernels, once per 32-row block:
     // tiled activations, statistics and tiled outputs are contiguous per

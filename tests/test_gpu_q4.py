@@ -219,22 +219,30 @@ def test_q4_sk2_partials_read_past_the_l2(gpu_device, monkeypatch):
         assert torch.equal(native[key], off[key]), key
 
 
-def _x96(L, k, g, dev):
-    xf = np.zeros((96, k), np.float32)
+def _xrows(MP, L, k, g, dev, hi_only=False):
+    """MP tiled activation rows (L nonzero) as the split pair; the float64
+    input the kernel sees (hi + lo, or hi alone without the low plane)."""
+    xf = np.zeros((MP, k), np.float32)
     xf[:L] = g.standard_normal((L, k))
     hi = torch.from_numpy(xf).to(torch.bfloat16)
     lo = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16)
-    return tile_weight(hi.to(dev)), tile_weight(lo.to(dev)), hi.double().numpy() + lo.double().numpy()
+    xin = hi.double().numpy() + (0 if hi_only else lo.double().numpy())
+    return tile_weight(hi.to(dev)), tile_weight(lo.to(dev)), xin
+
+
+def _x96(L, k, g, dev):
+    return _xrows(96, L, k, g, dev)
 
 
 def test_q4_gemm_96_rows(gpu_device):
-    """65 tree rows (rows_padded 96): q4 GEMMs run one pass per 32-row block.
-    Row-block-major statistics in and out, residual + next norm, SwiGLU into a
-    tiled output, against the q4 oracle on every row."""
+    """65 tree rows (rows_padded 96): the q4 GEMM makes one pass over the
+    weights for all three row blocks (q4m_gemm_kernel). Row-block-major
+    statistics in and out, residual + next norm into a tiled output, against
+    the q4 oracle on every row."""
     g = np.random.default_rng(96)
     H, F, L, MP = 512, 768, 65, 96
-    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, 2 * F, H, 0) + (1 << 20), dtype=torch.uint8,
-                     device=gpu_device)
+    ws = torch.zeros(max(N.lib().dtree_gemm_workspace_bytes(MP, n, k, 0) for n, k in ((F, H), (H, F))),
+                     dtype=torch.uint8, device=gpu_device)
     # fp32 store with a row scale from [3][H/32][32] statistics
     wq, s, b = o4.random_q4(F, H, g)
     wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
@@ -280,6 +288,118 @@ def test_q4_gemm_96_rows(gpu_device):
     assert torch.allclose(xg_rows.cpu(), want, rtol=2 ** -15, atol=1e-30)
     exp_ss = (got.astype(np.float64) ** 2).reshape(3, 32, H // 32, 32).sum(-1).transpose(0, 2, 1)
     np.testing.assert_allclose(sso.cpu().numpy(), exp_ss, rtol=1e-5, atol=1e-5)
+
+
+# One-pass q4 GEMM over 64-128 rows (q4m_gemm_kernel). Shapes chosen for its
+# plans on a 256-CU device: (768, 512) two 64-column blocks per workgroup
+# over several K parts; (320, 1024) a ragged last tile (5 blocks in tiles of
+# 2); (32768, 128) four blocks per workgroup in two K parts; (4096, 4096) the
+# 9B out_proj class (two per workgroup, eight K parts); (12352, 256) 193
+# blocks (in_proj's ragged width) in two parts.
+Q4M_SHAPES = [(768, 512), (320, 1024), (32768, 128), (4096, 4096), (12352, 256)]
+
+
+@pytest.mark.parametrize("n,k", Q4M_SHAPES)
+@pytest.mark.parametrize("MP", [64, 96, 128])
+def test_q4_one_pass_store_f32(gpu_device, n, k, MP):
+    g = np.random.default_rng(n + k + MP)
+    L = MP - 31
+    lo = MP != 64  # both activation-plane variants
+    wq, s, b = o4.random_q4(n, k, g)
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    wt, sb = wt.to(gpu_device), sb.to(gpu_device)
+    xt, xlt, xin = _xrows(MP, L, k, g, gpu_device, hi_only=not lo)
+    ss_np = (np.abs(g.standard_normal((MP // 32, k // 32, 32))) + 0.5).astype(np.float32)
+    ss = torch.from_numpy(ss_np).to(gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, n, k, 0), dtype=torch.uint8, device=gpu_device)
+    outs = []
+    for _ in range(2):
+        out = torch.zeros(MP, n, device=gpu_device)
+        a = _args(xt, xlt if lo else None, wt, sb, n, k, N.EPI_STORE_F32, ws)
+        a.rows_padded = MP
+        a.ss_in = ss.data_ptr(); a.ss_tiles = k // 32; a.norm_dim = k; a.eps = 1e-6
+        a.out_f32 = out.data_ptr(); a.ld_out_f32 = n
+        print(f"q4 one pass n={n} k={k} rows={MP}", flush=True)
+        N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 one pass")
+        outs.append(out)
+    torch.cuda.synchronize()
+    rs = 1.0 / np.sqrt(ss_np.transpose(0, 2, 1).reshape(MP, k // 32).sum(1) / k + 1e-6)
+    ref = o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b)) * rs[:, None]
+    got = outs[0].cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    assert not got[L:].any()
+    assert torch.equal(outs[0], outs[1])  # fixed reduction order
+    assert int(ws[:65536].view(torch.int32).abs().sum()) == 0  # counters self-reset
+
+
+@pytest.mark.parametrize("epi", ["residual", "swiglu", "bf16"])
+@pytest.mark.parametrize("MP", [64, 96, 128])
+def test_q4_one_pass_epilogues(gpu_device, epi, MP):
+    """Residual + next-norm statistics + hidden capture, SwiGLU and the split
+    bf16 store over 64-128 rows, tiled bf16 outputs, against the q4 oracle."""
+    from dtree_hip.weights import untile_weight
+    g = np.random.default_rng(7 * MP + len(epi))
+    L = MP - 31
+    n, k = (640, 1024) if epi != "swiglu" else (1536, 512)
+    if epi == "swiglu":
+        F = n // 2
+        gq, gs, gb = o4.random_q4(F, k, g)
+        uq, us, ub = o4.random_q4(F, k, g)
+        wq2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int32)) for t in (gq, uq)])
+        s2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int16)) for t in (gs, us)])
+        b2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int16)) for t in (gb, ub)])
+        wt, sb = q4_to_tiled(wq2, s2.view(torch.bfloat16), b2.view(torch.bfloat16))
+    else:
+        wq, s, b = o4.random_q4(n, k, g)
+        wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    wt, sb = wt.to(gpu_device), sb.to(gpu_device)
+    xt, xlt, xin = _xrows(MP, L, k, g, gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, n, k, 0), dtype=torch.uint8, device=gpu_device)
+    width = n // 2 if epi == "swiglu" else n
+    outb = torch.zeros(2, MP * width, dtype=torch.bfloat16, device=gpu_device)
+    a = _args(xt, xlt, wt, sb, n, k, {"residual": N.EPI_RESIDUAL, "swiglu": N.EPI_SWIGLU,
+                                      "bf16": N.EPI_STORE_BF16}[epi], ws)
+    a.rows_padded = MP
+    a.out_bf16 = outb[0].data_ptr(); a.out_lo = outb[1].data_ptr(); a.ld_out_bf16 = width
+    a.out_layout = N.W_TILED
+    rs = np.ones(MP)
+    if epi != "residual":
+        ss_np = (np.abs(g.standard_normal((MP // 32, k // 32, 32))) + 0.5).astype(np.float32)
+        ss = torch.from_numpy(ss_np).to(gpu_device)
+        a.ss_in = ss.data_ptr(); a.ss_tiles = k // 32; a.norm_dim = k; a.eps = 1e-6
+        rs = 1.0 / np.sqrt(ss_np.transpose(0, 2, 1).reshape(MP, k // 32).sum(1) / k + 1e-6)
+    else:
+        res = torch.zeros(MP, n)
+        res[:L] = torch.from_numpy(g.standard_normal((L, n)).astype(np.float32))
+        res = res.to(gpu_device)
+        res0 = res.cpu().double().numpy()
+        gn = torch.from_numpy((1 + 0.1 * g.standard_normal(n)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+        sso = torch.zeros(MP // 32, n // 32, 32, device=gpu_device)
+        hid = torch.zeros(MP, n, dtype=torch.bfloat16, device=gpu_device)
+        a.out_f32 = res.data_ptr(); a.ld_out_f32 = n
+        a.next_norm = gn.data_ptr(); a.ss_out = sso.data_ptr(); a.hidden_out = hid.data_ptr(); a.ld_hidden = n
+    print(f"q4 one pass epilogue={epi} rows={MP}", flush=True)
+    N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 one pass")
+    torch.cuda.synchronize()
+    got_b = (untile_weight(outb[0].view(MP, width)).float() + untile_weight(outb[1].view(MP, width)).float()).cpu().numpy()
+    if epi == "residual":
+        ref = res0 + o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b))
+        got = res.cpu().numpy()
+        assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+        assert not got[L:].any()
+        np.testing.assert_allclose(got_b, got * bf16_f32(gn)[None], rtol=2 ** -15, atol=1e-30)
+        exp_ss = (got.astype(np.float64) ** 2).reshape(MP // 32, 32, n // 32, 32).sum(-1).transpose(0, 2, 1)
+        np.testing.assert_allclose(sso.cpu().numpy(), exp_ss, rtol=1e-5, atol=1e-5)
+        assert torch.equal(hid.cpu(), torch.from_numpy(got).to(torch.bfloat16))
+    elif epi == "swiglu":
+        gt = o4.q4_matmul(xin, gq, bf16_to_f32(gs), bf16_to_f32(gb)) * rs[:, None]
+        up = o4.q4_matmul(xin, uq, bf16_to_f32(us), bf16_to_f32(ub)) * rs[:, None]
+        ref = gt / (1 + np.exp(-np.clip(gt, -80, 80))) * up
+        assert np.abs(got_b - ref).max() <= 2e-4 * np.abs(ref).max()
+    else:
+        ref = o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b)) * rs[:, None]
+        assert np.abs(got_b - ref).max() <= 2e-4 * np.abs(ref).max()
+    assert int(ws[:65536].view(torch.int32).abs().sum()) == 0
 
 
 def test_q4_rejects_bad_arguments(gpu_device):
