@@ -380,7 +380,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "gate_up_gemm": entry(kn(2 * F, H, 2), nL, us["gu"], b["gu"]),
         "down_gemm": entry(kn(H, F, 1), nL, us["down"], b["down"]),
         "gdn_prep": entry("gdn_prep_kernel<3, 128>", nG, us["prep"], b["prep"]),
-        "gdn_recurrence": entry(f"gdn_tree_reg_kernel<{32 if eng.MP == 32 else 96}>", nG,
+        "gdn_recurrence": entry("gdn_tree_reg_kernel<32>" if eng.MP == 32 else "gdn_tree_dfs_kernel", nG,
                                 us["recurrence"], b["recurrence"]),
         "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
         "gdn_commit": entry("gdn_commit_kernel<128>", nG, us["commit"], b["commit"]),

@@ -131,6 +131,19 @@ __device__ __forceinline__ int swz_xor16_i(int v) {
 __device__ __forceinline__ float swz_xor16(float v) {
   return __builtin_bit_cast(float, swz_xor16_i(__builtin_bit_cast(int, v)));
 }
+// a + (the same lane's value in the other 16-lane row of its 32-lane half),
+// with v_permlane16_swap (a VALU lane exchange, no LDS round trip). Written
+// as one asm sequence: the compiler's own lowering of the builtin, when both
+// swapped registers hold the same value and the two results are added, adds
+// the first result to itself (checked on the device), so it is not used.
+// The s_nop covers the VALU-write to permlane-read hazard, as the compiler
+// places it.
+__device__ __forceinline__ float row_pair_sum(float a) {
+  float b;
+  asm volatile("v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\tv_add_f32 %0, %0, %1"
+               : "+v"(a), "=&v"(b));
+  return a;
+}
 __device__ __forceinline__ float row_sum32(float a) {
   a += dpp<0xB1>(a);   // lane ^ 1
   a += dpp<0x4E>(a);   // lane ^ 2

@@ -148,14 +148,15 @@ __global__ __launch_bounds__(256) void gdn_tree_kernel(GdnParams p) {
 
 // Sum over the 32 consecutive lanes of a row, three values at once (their
 // steps interleave, so the latency of one reduction covers all three): DPP
-// quad permutes, half-row and row mirrors, then a swizzle across the two
-// 16-lane rows. Every lane of the row ends with the sums.
+// quad permutes, half-row and row mirrors, then a lane swap across the two
+// 16-lane rows (v_permlane16_swap: VALU only, so the recurrence's critical
+// path has no LDS round trip). Every lane of the row ends with the sums.
 __device__ __forceinline__ void row_sum32x3(float& a, float& b, float& c) {
   a += dpp<0xB1>(a); b += dpp<0xB1>(b); c += dpp<0xB1>(c);     // lane ^ 1
   a += dpp<0x4E>(a); b += dpp<0x4E>(b); c += dpp<0x4E>(c);     // lane ^ 2
   a += dpp<0x141>(a); b += dpp<0x141>(b); c += dpp<0x141>(c);  // half-row mirror: other quad
   a += dpp<0x140>(a); b += dpp<0x140>(b); c += dpp<0x140>(c);  // row mirror: other 8 lanes
-  a += swz_xor16(a); b += swz_xor16(b); c += swz_xor16(c);     // other 16-lane row
+  a = row_pair_sum(a); b = row_pair_sum(b); c = row_pair_sum(c);  // other 16-lane row
 }
 
 template <int TMAX>
@@ -254,6 +255,258 @@ __global__ __launch_bounds__(256) void gdn_tree_reg_kernel(GdnParams p) {
 // Largest tree of the register-resident recurrence (65-node trees of draft
 // budget 64 pad to 96 rows); larger trees use gdn_tree_kernel.
 constexpr int kRegTreeMax = 96;
+
+// ---- depth-first recurrence for trees of 33-96 nodes ----------------------
+//
+// Keeping every node's state in registers (gdn_tree_reg_kernel<96>: 4 x 96
+// floats per thread) and the nodes' q / k in LDS (96 KB) leaves one
+// workgroup per CU, so the 512 workgroups of a Qwen3.5-9B-shaped layer run in
+// two rounds, and each node picks its parent's state through a select chain
+// over every earlier node. Visiting the nodes in depth-first preorder needs
+// far fewer states: a node with one child hands its state straight to that
+// child (the next node in preorder), so only nodes with two or more children
+// keep theirs, in a stack slot given by their number of branching ancestors
+// (slot 0 holds the committed state for the roots). Chains (prompt prefill)
+// use no slot at all. The stack is addressed by a wave-uniform index; node
+// inputs are staged in LDS by blocks of 8 preorder positions, two blocks
+// ahead (about 34 KB, so two workgroups share a CU).
+//
+// The order is rebuilt from the parent list by every workgroup (a few
+// microseconds of LDS work): ancestor bitsets by pointer doubling, depth =
+// |ancestors| - 1, subtree sizes, preorder(t) = depth(t) + the subtree sizes
+// of the earlier siblings of t and of each of its ancestors (children in
+// increasing index order; nodes with no valid parent are roots, ordered the
+// same way).
+constexpr int kDfsStack = 32;            // slots; at most 31 nested branching ancestors
+constexpr int kDfsWords = (kRegTreeMax + 31) / 32;
+
+// The stack as four 32-wide vectors (element e of slot j = vector e, lane j):
+// a wave-uniform index into one vector register tuple compiles to indexed
+// register moves (s_set_gpr_idx), so the stack stays in VGPRs.
+typedef float f32x32_t __attribute__((ext_vector_type(kDfsStack)));
+struct DfsStack {
+  f32x32_t e[4];
+  __device__ __forceinline__ f32x4_t get(int d) const { return f32x4_t{e[0][d], e[1][d], e[2][d], e[3][d]}; }
+  __device__ __forceinline__ void put(int d, f32x4_t v) {
+    e[0][d] = v[0];
+    e[1][d] = v[1];
+    e[2][d] = v[2];
+    e[3][d] = v[3];
+  }
+};
+
+// Depth-first preorder of the first T (<= kRegTreeMax) nodes. For position i:
+// order[i] = the node and meta[i] = node | (rslot + 1) << 8 | (wslot + 1) << 16
+// with rslot the stack slot its parent's state is read from (-1: the state
+// just computed) and wslot the slot its own state is kept in (-1: none).
+// Returns the largest slot used. Every thread of the workgroup calls it (it
+// holds barriers).
+__device__ int tree_preorder(const int* parents, int T, int* order, int* meta) {
+  __shared__ uint32_t anc[kRegTreeMax][kDfsWords];
+  __shared__ int par[kRegTreeMax], up[kRegTreeMax], sz[kRegTreeMax], esz[kRegTreeMax], dep[kRegTreeMax];
+  __shared__ int nch[kRegTreeMax], bd[kRegTreeMax];
+  __shared__ int s_max;
+  const int t = threadIdx.x;
+  if (t == 0) s_max = 0;
+  if (t < T) {
+    const int pa = valid_parent(parents[t], t);
+    par[t] = pa;
+    up[t] = pa;
+#pragma unroll
+    for (int w = 0; w < kDfsWords; ++w) anc[t][w] = (t >> 5) == w ? 1u << (t & 31) : 0u;
+  }
+  __syncthreads();
+  // pointer doubling: after round r, anc[t] holds t and its ancestors within
+  // distance 2^r - 1 and up[t] the ancestor at distance 2^r
+  for (int r = 0; (1 << r) < kRegTreeMax; ++r) {
+    uint32_t a[kDfsWords];
+    int u = -1;
+    if (t < T) {
+      u = up[t];
+#pragma unroll
+      for (int w = 0; w < kDfsWords; ++w) a[w] = anc[t][w];
+      if (u >= 0) {
+#pragma unroll
+        for (int w = 0; w < kDfsWords; ++w) a[w] |= anc[u][w];
+        u = up[u];
+      }
+    }
+    __syncthreads();
+    if (t < T) {
+#pragma unroll
+      for (int w = 0; w < kDfsWords; ++w) anc[t][w] = a[w];
+      up[t] = u;
+    }
+    __syncthreads();
+  }
+  if (t < T) {
+    int d = -1, n = 0, c = 0;
+#pragma unroll
+    for (int w = 0; w < kDfsWords; ++w) d += __popc(anc[t][w]);
+    for (int u = 0; u < T; ++u) {
+      n += (anc[u][t >> 5] >> (t & 31)) & 1u;
+      c += par[u] == t;
+    }
+    dep[t] = d;
+    sz[t] = n;
+    nch[t] = c;
+  }
+  __syncthreads();
+  if (t < T) {
+    const int pa = par[t];
+    int e = 0;
+    for (int u = 0; u < t; ++u) e += par[u] == pa ? sz[u] : 0;
+    esz[t] = e;
+    int b = 0;  // branching proper ancestors
+#pragma unroll
+    for (int w = 0; w < kDfsWords; ++w) {
+      uint32_t m = anc[t][w];
+      while (m) {
+        const int a = 32 * w + __ffs(m) - 1;
+        m &= m - 1;
+        b += a != t && nch[a] >= 2;
+      }
+    }
+    bd[t] = b;
+  }
+  __syncthreads();
+  if (t < T) {
+    int pre = dep[t];
+#pragma unroll
+    for (int w = 0; w < kDfsWords; ++w) {
+      uint32_t m = anc[t][w];
+      while (m) {
+        const int a = 32 * w + __ffs(m) - 1;
+        m &= m - 1;
+        pre += esz[a];
+      }
+    }
+    const int pa = par[t];
+    const int ws = nch[t] >= 2 ? bd[t] + 1 : -1;
+    const int rs = pa < 0 ? 0 : (nch[pa] >= 2 ? bd[pa] + 1 : -1);
+    order[pre] = t;
+    meta[pre] = t | (rs + 1) << 8 | (ws + 1) << 16;
+    atomicMax(&s_max, ws);
+  }
+  __syncthreads();
+  return s_max;
+}
+
+// The recurrence over the preorder: a workgroup owns one value head and 8
+// state rows (32 lanes x 4 elements per row) as in gdn_tree_reg_kernel, with
+// the same per-node arithmetic and one reduction for S_p k, S_p q and k q.
+// A tree with more than kDfsStack - 1 nested branching nodes writes NaN.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_tree_dfs_kernel(GdnParams p) {
+  constexpr int DK = 128, RPW = 8;
+  __shared__ int order[kRegTreeMax], meta[kRegTreeMax];
+  const int T = p.T_dev ? min(max(*p.T_dev, 0), min(p.T, kRegTreeMax)) : min(p.T, kRegTreeMax);
+  const int nslices = p.Dv / RPW;
+  const int h = blockIdx.x / nslices, row0 = (blockIdx.x % nslices) * RPW;
+  const int hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x, rl = tid >> 5, lane = tid & 31;
+  const int dv = row0 + rl;
+  DfsStack st;
+  f32x4_t cur = *reinterpret_cast<const f32x4_t*>(p.state + ((size_t)h * p.Dv + dv) * DK + 4 * lane);
+  st.put(0, cur);
+  const int top = tree_preorder(p.parents, T, order, meta);
+  if (top > kDfsStack - 1) {
+    for (int t = tid; t < T * RPW; t += 256)
+      p.y[((size_t)(t / RPW) * p.Hv + h) * p.Dv + row0 + t % RPW] = __builtin_nanf("");
+    return;
+  }
+  // Node inputs staged in LDS by blocks of 8 preorder positions, in a ring of
+  // 4 blocks filled two blocks ahead: k and q of the key head (256 floats per
+  // node, two 16-byte pieces per thread), v of the 8 rows, g and beta.
+  constexpr int NBK = 8, RING = 4;
+  __shared__ __align__(16) float kqs[RING * NBK][2][DK];
+  __shared__ float vgs[RING * NBK][RPW + 2];
+  const int nblocks = (T + NBK - 1) / NBK;
+  f32x4_t rk[2];
+  float rv = 0.f;
+  auto block_issue = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i, n = e >> 6, w = (e >> 5) & 1, c4 = e & 31;  // node, k|q, 16-byte piece
+      const int j = b * NBK + n;
+      if (b < nblocks && j < T) {
+        const int t = order[j];
+        const float* src = (w == 0 ? p.k : p.q) + ((size_t)t * p.Hk + hk) * DK + 4 * c4;
+        rk[i] = *reinterpret_cast<const f32x4_t*>(src);
+      }
+    }
+    if (tid < NBK * (RPW + 2)) {
+      const int n = tid / (RPW + 2), r = tid % (RPW + 2), j = b * NBK + n;
+      if (b < nblocks && j < T) {
+        const int t = order[j];
+        rv = r < RPW ? p.v[((size_t)t * p.Hv + h) * p.Dv + row0 + r]
+                     : (r == RPW ? p.g[(size_t)t * p.Hv + h] : p.beta[(size_t)t * p.Hv + h]);
+      }
+    }
+  };
+  auto block_store = [&](int b) {
+    const int base = (b % RING) * NBK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i, n = e >> 6, w = (e >> 5) & 1, c4 = e & 31;
+      *reinterpret_cast<f32x4_t*>(&kqs[base + n][w][4 * c4]) = rk[i];
+    }
+    if (tid < NBK * (RPW + 2)) vgs[base + tid / (RPW + 2)][tid % (RPW + 2)] = rv;
+  };
+  block_issue(0);
+  block_store(0);
+  block_issue(1);
+  block_store(1);
+  block_issue(2);
+  __syncthreads();
+  // One node's inputs from the ring (positions past T read stale entries that
+  // are never used), loaded a node ahead of its arithmetic.
+  struct NodeIn {
+    f32x4_t kk, qq;
+    float v, g, b;
+    int meta;
+  };
+  auto node_in = [&](int slot, int j) {
+    NodeIn r;
+    r.kk = *reinterpret_cast<const f32x4_t*>(&kqs[slot][0][4 * lane]);
+    r.qq = *reinterpret_cast<const f32x4_t*>(&kqs[slot][1][4 * lane]);
+    r.v = vgs[slot][rl];
+    r.g = vgs[slot][RPW];
+    r.b = vgs[slot][RPW + 1];
+    r.meta = meta[min(j, kRegTreeMax - 1)];
+    return r;
+  };
+  for (int b = 0; b < nblocks; ++b) {
+    const int base = (b % RING) * NBK;
+    const int jn = min(NBK, T - b * NBK);
+    NodeIn in = node_in(base, b * NBK);
+#pragma unroll
+    for (int n = 0; n < NBK; ++n) {
+      NodeIn nx;
+      if (n + 1 < NBK) nx = node_in(base + n + 1, b * NBK + n + 1);
+      if (n < jn) {
+        const int m = __builtin_amdgcn_readfirstlane(in.meta);
+        const int t = m & 255, rs = ((m >> 8) & 255) - 1, ws = ((m >> 16) & 255) - 1;
+        const f32x4_t kk = in.kk, qq = in.qq;
+        const f32x4_t sp = rs < 0 ? cur : st.get(rs);
+        float sk = sp[0] * kk[0] + sp[1] * kk[1] + sp[2] * kk[2] + sp[3] * kk[3];
+        float sq = sp[0] * qq[0] + sp[1] * qq[1] + sp[2] * qq[2] + sp[3] * qq[3];
+        float kqd = kk[0] * qq[0] + kk[1] * qq[1] + kk[2] * qq[2] + kk[3] * qq[3];
+        row_sum32x3(sk, sq, kqd);
+        const float delta = (in.v - in.g * sk) * in.b;
+        cur = sp * in.g + kk * delta;
+        if (ws >= 0) st.put(ws, cur);
+        if (lane == 0) p.y[((size_t)t * p.Hv + h) * p.Dv + dv] = in.g * sq + delta * kqd;
+        if (p.states)
+          *reinterpret_cast<f32x4_t*>(p.states + (((size_t)t * p.Hv + h) * p.Dv + dv) * DK + 4 * lane) = cur;
+      }
+      if (n + 1 < NBK) in = nx;
+    }
+    // block b + 2 (issued one block ago) into its ring slot, b + 3 out
+    block_store(b + 2);
+    block_issue(b + 3);
+    __syncthreads();
+  }
+}
 
 // Path entries index the per-node buffers ([T] rows); an out-of-range entry
 // (a descriptor that no walk filled) is clamped so it can never read past them.
@@ -515,7 +768,7 @@ extern "C" int dtree_gdn_tree_recurrence(const float* q, const float* k, const f
   p.y = y; p.states = states;
   if (head_k_dim == 128 && num_nodes <= kRegTreeMax && head_v_dim % 8 == 0) {
     if (num_nodes <= 32) gdn_tree_reg_kernel<32><<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
-    else gdn_tree_reg_kernel<kRegTreeMax><<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
+    else gdn_tree_dfs_kernel<<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
     DTREE_LAUNCH_CHECK("gdn_tree_recurrence launch");
     return DTREE_OK;
   }
@@ -619,7 +872,7 @@ extern "C" int dtree_gdn_layer_recurrence(const DtreeGdnArgs* a, hipStream_t str
     gdn_tree_reg_kernel<32><<<a->num_v_heads * (a->head_v_dim / 8), 256, 0, stream>>>(p);
   } else if (a->rows_padded <= kRegTreeMax && a->head_v_dim % 8 == 0) {
     p.T = a->rows_padded;
-    gdn_tree_reg_kernel<kRegTreeMax><<<a->num_v_heads * (a->head_v_dim / 8), 256, 0, stream>>>(p);
+    gdn_tree_dfs_kernel<<<a->num_v_heads * (a->head_v_dim / 8), 256, 0, stream>>>(p);
   } else {
     const int grid = a->num_v_heads * (a->head_v_dim / rpw);
     gdn_tree_kernel<128><<<grid, rpw * (128 / 4), lds, stream>>>(p);

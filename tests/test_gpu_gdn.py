@@ -113,9 +113,71 @@ def test_layer_shapes_conv_and_recurrence(T, seed):
     assert np.array_equal(y, y2) and np.array_equal(out, out2)
 
 
+def _chain_tree(T, depth, seed):
+    """Nodes 0 .. depth form a chain (the deepest node at depth `depth`); the
+    rest hang off random earlier nodes."""
+    g_ = np.random.default_rng(seed)
+    return [-1] + list(range(depth)) + [int(g_.integers(0, i)) for i in range(depth + 1, T)]
+
+
+def _caterpillar(n_branching):
+    """A path whose first n_branching nodes each also carry a leaf: node 2j is
+    path node j (children: leaf 2j + 1 and path node 2j + 2), so path node j
+    has j branching ancestors."""
+    par = [-1]
+    for j in range(n_branching):
+        par += [2 * j, 2 * j]
+    return par
+
+
+@pytest.mark.parametrize("parents", [
+    _chain_tree(40, 30, 70), _chain_tree(96, 21, 117), _chain_tree(65, 15, 80), _chain_tree(33, 1, 34),
+    list(range(-1, 95)),   # a 96-node chain (prompt prefill runs such chains): no stack slot
+    _caterpillar(31),      # 63 nodes, 31 nested branching nodes: the stack's last slot
+], ids=["chain30+9", "chain21+74", "chain15+49", "bushy33", "chain96", "caterpillar31"])
+def test_recurrence_depth_first_trees(parents):
+    """33-96 nodes run depth first, keeping the states of branching nodes on a
+    stack (gdn_tree_dfs_kernel): deep chains with side branches, a plain
+    96-node chain, a bushy tree and a caterpillar that fills the stack, against
+    the float64 oracle."""
+    T = len(parents)
+    q, k, v, g, beta, state = _layer_inputs(T, T)
+    y, st = _delta(q, k, v, g, beta, state, parents, "cuda")
+    ry, rs = gdn.tree_gated_delta(q, k, v, g, beta, state, parents)
+    assert np.abs(y - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
+    assert np.abs(st - rs).max() <= 1e-5 * max(1.0, np.abs(rs).max())
+
+
+def test_recurrence_forest_of_roots():
+    """Nodes without a valid parent (-1, or an index not below the node) start
+    from the committed state; the depth-first order visits each root's subtree
+    in turn."""
+    T = 48
+    parents = random_tree(T, 11)
+    for t in (5, 17, 30):
+        parents[t] = -1
+    parents[40] = 45  # not below the node: treated as a root
+    q, k, v, g, beta, state = _layer_inputs(T, 12)
+    y, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
+    ref_par = [p if 0 <= p < t else -1 for t, p in enumerate(parents)]
+    ry, _ = gdn.tree_gated_delta(q, k, v, g, beta, state, ref_par)
+    assert np.abs(y - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
+
+
+def test_recurrence_past_the_stack_writes_nan():
+    """32 nested branching nodes (a 65-node caterpillar) do not fit the
+    32-slot stack: every output is NaN, never a silently wrong value."""
+    parents = _caterpillar(32)
+    T = len(parents)
+    q, k, v, g, beta, state = _layer_inputs(T, 13)
+    y, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
+    assert np.isnan(y).all()
+
+
 def test_recurrence_rejects_trees_past_96_nodes():
-    """Head dim 128: trees of up to 96 nodes run register-resident; larger ones
-    do not fit the LDS-resident fallback either and are rejected."""
+    """Head dim 128: trees of up to 96 nodes run register-resident (up to 32
+    nodes) or depth first; larger ones do not fit the LDS-resident fallback
+    either and are rejected."""
     q, k, v, g, beta, state = _layer_inputs(128, 3)
     with pytest.raises(DtreeError, match="too large"):
         _delta(q, k, v, g, beta, state, random_tree(128, 3), "cuda")
