@@ -579,18 +579,29 @@ struct PrepParams {
 
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
+// One workgroup per (128-channel slice, block of kPrepNodes nodes), plus one
+// column of workgroups for g and beta. A thread owns one channel of the
+// block's nodes: it issues every conv input it needs at once (the node's row
+// and up to KEEP ancestors' rows of the projection output, or rows of the
+// committed window past the root path), runs the tree conv and SiLU, and for
+// q / k slices the head's sum of squares per node is a workgroup reduction
+// (wave sums through DPP and the lane swap, then LDS across the two waves).
+constexpr int kPrepNodes = 8;
+
 template <int KEEP, int DK>
 __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
-  extern __shared__ float ob[];  // [rows][DK + 1] conv outputs, rs[rows], then xin [rows][DK]
+  constexpr int NB = kPrepNodes, NW = DK / 64;
   __shared__ int par[kGdnMaxNodes];
+  __shared__ float wsum[NB][NW];
   const int L = min(max(p.desc->num_nodes, 0), p.rows);
+  const int t0 = blockIdx.y * NB;
+  if (t0 >= L) return;
   const int tid = threadIdx.x;
-  for (int t = tid; t < L; t += DK) par[t] = valid_parent(p.desc->parents[t], t);
-  __syncthreads();
   const int nslices = p.C / DK;
   if ((int)blockIdx.x == nslices) {
-    for (int e = tid; e < L * p.Hv; e += DK) {
-      const int t = e / p.Hv, h = e % p.Hv;
+    for (int e = tid; e < NB * p.Hv; e += DK) {
+      const int t = t0 + e / p.Hv, h = e % p.Hv;
+      if (t >= L) continue;
       const float* row = p.x + (size_t)t * p.ldx + p.ab_col;
       const float b = row[h], a = row[p.Hv + h];
       p.g[(size_t)t * p.Hv + h] = __expf(-__expf(p.A_log[h]) * softplus_f(a + p.dt_bias[h]));
@@ -598,63 +609,74 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
     }
     return;
   }
+  for (int t = tid; t < L; t += DK) par[t] = valid_parent(p.desc->parents[t], t);
   const int c0 = blockIdx.x * DK, c = c0 + tid;
   float wk[KEEP + 1], bk[KEEP];
 #pragma unroll
   for (int r = 0; r <= KEEP; ++r) wk[r] = p.w[(size_t)r * p.C + c];
 #pragma unroll
   for (int r = 0; r < KEEP; ++r) bk[r] = p.base[(size_t)r * p.C + c];
-  // This thread's channel of every node's conv input, staged in its own LDS
-  // column with all loads in flight at once (batches of 8).
-  float* xin = ob + p.rows * (DK + 2);
-  for (int t0 = 0; t0 < L; t0 += 8) {
-    float xv[8];
+  __syncthreads();
+  // window of node t = the last KEEP + 1 rows of (committed window ++ x along
+  // the root path): val[n][i] is row KEEP - i (val[n][0] = x[t])
+  float val[NB][KEEP + 1];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xv[i] = t0 + i < L ? p.x[(size_t)(t0 + i) * p.ldx + c] : 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (t0 + i < L) xin[(t0 + i) * DK + tid] = xv[i];
-  }
-  for (int t = 0; t < L; ++t) {
-    // window of t = last KEEP + 1 rows of (base ++ x along the root path):
-    // val[i] is row KEEP - i (val[0] = x[t]).
-    float val[KEEP + 1];
-    int anc = t, nb = 0;
+  for (int n = 0; n < NB; ++n) {
+    const int t = t0 + n;
+    int anc = t < L ? t : -1, nb = 0;
 #pragma unroll
     for (int i = 0; i <= KEEP; ++i) {
       if (anc >= 0) {
-        val[i] = xin[anc * DK + tid];
+        val[n][i] = p.x[(size_t)anc * p.ldx + c];
         anc = par[anc];
       } else {
-        val[i] = bk[KEEP - 1 - nb];
+        val[n][i] = bk[KEEP - 1 - min(nb, KEEP - 1)];
         ++nb;
       }
     }
+  }
+  float o[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i <= KEEP; ++i) acc += wk[KEEP - i] * val[i];
-    ob[t * (DK + 1) + tid] = silu_acc(acc);
+    for (int i = 0; i <= KEEP; ++i) acc += wk[KEEP - i] * val[n][i];
+    o[n] = silu_acc(acc);
   }
   const bool is_q = c0 < p.key_dim, is_k = !is_q && c0 < 2 * p.key_dim;
-  float* rs = ob + p.rows * (DK + 1);  // rows floats; xin starts at rows * (DK + 2)
-  __syncthreads();
+  float scale[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) scale[n] = 1.f;
   if (is_q || is_k) {
-    // Node t's head; the padded row stride puts consecutive nodes on distinct banks.
-    for (int t = tid; t < L; t += DK) {
-      float ss = 0.f;
-      for (int j = 0; j < DK; ++j) {
-        const float o = ob[t * (DK + 1) + j];
-        ss += o * o;
-      }
-      rs[t] = rsqrtf(ss * (1.0f / DK) + 1e-6f) * (is_q ? p.q_scale : p.k_scale);
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      float ss = o[n] * o[n];
+      ss += dpp<0xB1>(ss);
+      ss += dpp<0x4E>(ss);
+      ss += dpp<0x141>(ss);
+      ss += dpp<0x140>(ss);
+      ss = row_pair_sum(ss);                 // 32 lanes
+      ss += __shfl_xor(ss, 32);              // 64 lanes
+      if (lane == 0) wsum[n][wave] = ss;
     }
     __syncthreads();
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) tot += wsum[n][w2];
+      scale[n] = rsqrtf(tot * (1.0f / DK) + 1e-6f) * (is_q ? p.q_scale : p.k_scale);
+    }
   }
-  for (int t = 0; t < L; ++t) {
-    const float o = ob[t * (DK + 1) + tid];
-    if (is_q) p.q[(size_t)t * p.key_dim + c] = o * rs[t];
-    else if (is_k) p.k[(size_t)t * p.key_dim + (c - p.key_dim)] = o * rs[t];
-    else p.v[(size_t)t * (p.C - 2 * p.key_dim) + (c - 2 * p.key_dim)] = o;
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    const int t = t0 + n;
+    if (t >= L) break;
+    const float v = o[n] * scale[n];
+    if (is_q) p.q[(size_t)t * p.key_dim + c] = v;
+    else if (is_k) p.k[(size_t)t * p.key_dim + (c - p.key_dim)] = v;
+    else p.v[(size_t)t * (p.C - 2 * p.key_dim) + (c - 2 * p.key_dim)] = v;
   }
 }
 
@@ -843,11 +865,10 @@ extern "C" int dtree_gdn_layer_prep(const DtreeGdnArgs* a, hipStream_t stream) {
   p.q = a->q; p.k = a->k; p.v = a->v; p.g = a->g; p.beta = a->beta;
   p.q_scale = 1.0f / (float)a->head_k_dim;
   p.k_scale = 1.0f / sqrtf((float)a->head_k_dim);
-  const size_t lds = ((size_t)a->rows_padded * (128 + 2) + (size_t)a->rows_padded * 128) * sizeof(float);
-  const int grid = C / 128 + 1;
+  const dim3 grid(C / 128 + 1, (a->rows_padded + kPrepNodes - 1) / kPrepNodes);
   switch (a->conv_keep) {
 #define DTREE_PREP_CASE(K) \
-  case K: gdn_prep_kernel<K, 128><<<grid, 128, lds, stream>>>(p); break;
+  case K: gdn_prep_kernel<K, 128><<<grid, 128, 0, stream>>>(p); break;
     DTREE_PREP_CASE(1) DTREE_PREP_CASE(2) DTREE_PREP_CASE(3) DTREE_PREP_CASE(4) DTREE_PREP_CASE(5)
     DTREE_PREP_CASE(6) DTREE_PREP_CASE(7)
 #undef DTREE_PREP_CASE
