@@ -189,7 +189,7 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
     out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant), nl, us["o"], b["o"])
     out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant), nl, us["down"], b["down"])
     out["gate_up_gemm"] = entry(gemm_kernel_name(2 * F, H, 2, quant), nl, us["gu"], b["gu"])
-    out["lm_head"] = entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"])
+    out["lm_head"] = entry(lmhead_kernel_name(quant, eng.MP), 1, us["lm_head"], b["lm_head"])
     return out
 
 
@@ -386,7 +386,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "gdn_commit": entry("gdn_commit_kernel<128>", nG, us["commit"], b["commit"]),
         "attention": entry(attention_kernel_name(eng.max_past, 256, 64, True, eng.MP), nA, us["attention"],
                            b["attention"]),
-        "lm_head": entry(f"lmhead_kernel<1, 2, 2, true, true, {q4}>", 1, us["lm_head"], b["lm_head"]),
+        "lm_head": entry(lmhead_kernel_name(quant, eng.MP), 1, us["lm_head"], b["lm_head"]),
     }
     return out
 
@@ -400,6 +400,15 @@ def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -
     group = forced == "group" or (forced != "head" and max_past > 1536)
     g = "true" if gated else "false"
     return f"gqa_tree_attn_kernel<{D}, {R}, {g}, 4>" if group else f"tree_attn_kernel<{D}, {R}, {g}, {1 if MP == 32 else 4}>"
+
+
+def lmhead_kernel_name(quant: str, rows: int) -> str:
+    """LM-head kernel (gemm.hip, dtree_lmhead_argmax): the one-pass q4 kernel's
+    argmax epilogue for q4 over 64-128 rows, else the persistent LM head."""
+    if quant == "q4" and rows > 32:
+        return f"q4m_gemm_kernel<true, 16, {rows // 32}, 4>"
+    mb = rows // 32
+    return f"lmhead_kernel<{mb}, {2 if mb == 1 else (2 if mb == 2 else 1)}, {2 if mb == 1 else 1}, true, true, {'true' if quant == 'q4' else 'false'}>"
 
 
 def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows: int = 32) -> str:

@@ -51,6 +51,11 @@ struct GemmParams {
   // ranged ring loads (32 tiled rows): bytes of w, w_sb and one x plane
   unsigned w_bytes, sb_bytes, x_bytes;
   int off_xcd;  // test hook: treat every workgroup as off its expected XCD
+  // LM-head mode of the one-pass q4 kernel: optional fp32 logits [rows][n]
+  // and per-(workgroup, row) argmax candidates over lm_blocks workgroups
+  float* lm_logits;
+  int2* lm_cand;
+  int lm_blocks;
 };
 
 // Index of element (m, col) of a bf16 output with `ld` columns.
@@ -844,6 +849,10 @@ struct Q4mShape {
   static constexpr int LDS_BYTES = 2 * STAGE_BYTES > RED_BYTES ? 2 * STAGE_BYTES : RED_BYTES;
 };
 constexpr int kQ4mDepth = 2;  // weight groups in flight per wave
+// Epilogue of the one-pass q4 kernel as the fused LM head (not a GEMM
+// epilogue of the C ABI): row scale, optional fp32 logits, and per row the
+// (largest logit, first index) of the tile as the workgroup's candidate.
+constexpr int kEpiLmArgmax = 16;
 
 template <bool LO, int EPI, int MB, int CW>
 __global__ __launch_bounds__(kThreads * MB) void q4m_gemm_kernel(GemmParams p) {
@@ -864,6 +873,14 @@ __global__ __launch_bounds__(kThreads * MB) void q4m_gemm_kernel(GemmParams p) {
   const int nsteps = (g1 - g0 + KI - 1) / KI;
   const int cb = tile * CW + cw;
   const bool cb_ok = cb < nblk;
+  if constexpr (EPI == kEpiLmArgmax) {
+    // the candidate grid is wider than the vocab's tiles: the rest report
+    // empty candidates
+    if (tile * CW >= nblk) {
+      if (t < MP) p.lm_cand[cand_index(blockIdx.x, t, p.lm_blocks)] = make_int2(__float_as_int(-__builtin_huge_valf()), 0x7fffffff);
+      return;
+    }
+  }
 
   // The row scale's loads go out first (loads retire in order). Threads past
   // the first kThreads load and add tiles the final sum never reads.
@@ -1022,6 +1039,24 @@ __global__ __launch_bounds__(kThreads * MB) void q4m_gemm_kernel(GemmParams p) {
       reinterpret_cast<f32x4_t*>(red)[e4] = v;
     }
     __syncthreads();
+  }
+  if constexpr (EPI == kEpiLmArgmax) {
+    // 8 consecutive threads per row (NT = 8 * MP): each scans every 8th column
+    // of the tile, then the 8 lanes reduce (max, first index on ties).
+    const int m = t >> 3, q8 = t & 7;
+    float bv = -__builtin_huge_valf();
+    int bi = 0x7fffffff;
+    for (int cc = q8; cc < nvalid * 64; cc += 8) {
+      const float v = red[((cc >> 6) * MP + m) * 64 + (cc & 63)] * rs[m];
+      const int idx = tile * CW * 64 + cc;
+      if (p.lm_logits) p.lm_logits[(size_t)m * p.n + idx] = v;
+      argmax_merge(bv, bi, v, idx);
+    }
+    argmax_dpp<0xB1>(bv, bi);   // lane ^ 1
+    argmax_dpp<0x4E>(bv, bi);   // lane ^ 2
+    argmax_dpp<0x141>(bv, bi);  // half-row mirror: the other quad of the 8
+    if (q8 == 0) p.lm_cand[cand_index(blockIdx.x, m, p.lm_blocks)] = make_int2(__float_as_int(bv), bi);
+    return;
   }
   // The tile epilogue is written for kThreads threads: the first four waves
   // run it per (64-column block, 32-row block), outputs shifted by the row
@@ -1256,6 +1291,14 @@ static void launch_q4m_cw(const GemmParams& p, int epi, int mb, int grid, hipStr
     case 2: launch_q4m_mb<LO, 2, CW>(p, epi, grid, st); break;
     case 3: launch_q4m_mb<LO, 3, CW>(p, epi, grid, st); break;
     default: launch_q4m_mb<LO, 4, CW>(p, epi, grid, st); break;
+  }
+}
+template <bool LO>
+static void launch_q4m_lm(const GemmParams& p, int mb, int grid, hipStream_t st) {
+  switch (mb) {
+    case 2: q4m_gemm_kernel<LO, kEpiLmArgmax, 2, 4><<<grid, kThreads * 2, 0, st>>>(p); break;
+    case 3: q4m_gemm_kernel<LO, kEpiLmArgmax, 3, 4><<<grid, kThreads * 3, 0, st>>>(p); break;
+    default: q4m_gemm_kernel<LO, kEpiLmArgmax, 4, 4><<<grid, kThreads * 4, 0, st>>>(p); break;
   }
 }
 static void launch_q4m(const GemmParams& p, int epi, int mb, int cw, int grid, hipStream_t st) {
@@ -1876,6 +1919,27 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
                   "lmhead: q4 embedding needs tiled x and hidden <= 4096");
     DTREE_REQUIRE(emb_scales && ((uintptr_t)emb & 15) == 0, "lmhead: q4 embedding needs emb_scales");
     DTREE_REQUIRE(vocab % 64 == 0, "lmhead: q4 embedding needs vocab % 64 == 0");
+    if (rows_padded > 32 && q4m_enabled()) {
+      // One pass over the q4 embedding for every row block: the one-pass q4
+      // GEMM kernel with its LM-head epilogue, 4 64-column blocks per
+      // workgroup, one workgroup per candidate block (the ones past the
+      // vocab's tiles report empty candidates).
+      DTREE_REQUIRE((vocab / 64 + 3) / 4 <= grid, "lmhead: vocab too large for the q4 one-pass candidate grid");
+      DTREE_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)x_lo & 15) == 0 && ((uintptr_t)emb_scales & 3) == 0,
+                    "lmhead: q4 operands misaligned");
+      const size_t xb = (size_t)rows_padded * hidden * 2, wb = (size_t)vocab * hidden / 2;
+      DTREE_REQUIRE(xb < kOob && wb < kOob, "lmhead: operands must be smaller than 2 GiB");
+      GemmParams g{};
+      g.x = x; g.x_lo = x_lo; g.ldx = hidden; g.w = emb; g.w_sb = emb_scales; g.n = vocab; g.k = hidden;
+      g.S = 1;
+      g.ss_in = ss_in; g.ss_tiles = ss_tiles; g.inv_norm_dim = 1.0f / (float)hidden; g.eps = eps;
+      g.x_bytes = (unsigned)xb; g.w_bytes = (unsigned)wb; g.sb_bytes = (unsigned)((size_t)vocab * (hidden / 64) * 4);
+      g.lm_logits = logits; g.lm_cand = p.cand; g.lm_blocks = grid;
+      if (x_lo) launch_q4m_lm<true>(g, rows_padded / 32, grid, stream);
+      else launch_q4m_lm<false>(g, rows_padded / 32, grid, stream);
+      DTREE_LAUNCH_CHECK("lmhead launch");
+      return DTREE_OK;
+    }
     // One pass of the 32-row kernel per 32-row block (tiled x, statistics and
     // candidates are contiguous per block; logits rows are row-major). The
     // kernel walks 64-column tiles; the grid stays the candidate block count

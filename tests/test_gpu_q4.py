@@ -459,9 +459,9 @@ def test_q4_lmhead_argmax_and_logits(gpu_device):
 
 
 def test_q4_lmhead_96_rows_through_walk(gpu_device):
-    """q4 LM head over 65 tree rows (one pass per 32-row block): the walk's
-    posterior over all 65 rows equals the argmax of the returned logits, which
-    match the q4 oracle."""
+    """q4 LM head over 65 tree rows (one pass over the embedding for the three
+    row blocks): the walk's posterior over all 65 rows equals the argmax of
+    the returned logits, which match the q4 oracle."""
     g = np.random.default_rng(965)
     V, H, L, MP = 8192, 1024, 65, 96
     wq, s, b = o4.random_q4(V, H, g)
@@ -486,6 +486,58 @@ def test_q4_lmhead_96_rows_through_walk(gpu_device):
     r = res.cpu().numpy()
     post = list(r[3 + N.MAX_NODES:3 + N.MAX_NODES + L])
     assert int(r[2]) == L and post == list(np.argmax(got, axis=-1))
+
+
+@pytest.mark.parametrize("MP", [64, 96, 128])
+def test_q4_lmhead_one_pass_ties_ragged_vocab(gpu_device, MP):
+    """The one-pass q4 LM head (q4m_gemm_kernel's argmax epilogue) over 64-128
+    rows: a vocabulary whose last 256-column tile is ragged (42 64-column
+    blocks), the final RMSNorm row scale, no logits buffer, and an exact tie
+    between vocab rows 300 and 2600 (different tiles; identical words, scale
+    0, bias 20, activations >= 0, so the two are every row's maximum): the
+    walk's posterior is the first index, 300, on every row."""
+    from gpu_util import device_desc
+    from oracle.qwen3 import f32_to_bf16_bits
+    g = np.random.default_rng(MP + 5)
+    V, H, L = 2688, 512, MP - 31
+    wq, s, b = o4.random_q4(V, H, g)
+    wq[2600] = wq[300]
+    s[300] = s[2600] = 0
+    b[300] = b[2600] = f32_to_bf16_bits(np.float32([20.0]))[0]
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    wt, sb = wt.to(gpu_device), sb.to(gpu_device)
+    xf = np.zeros((MP, H), np.float32)
+    xf[:L] = np.abs(g.standard_normal((L, H)))
+    hi = torch.from_numpy(xf).to(torch.bfloat16)
+    lo = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16)
+    xt, xlt = tile_weight(hi.to(gpu_device)), tile_weight(lo.to(gpu_device))
+    xin = hi.double().numpy() + lo.double().numpy()
+    ss_np = (np.abs(g.standard_normal((MP // 32, H // 32, 32))) + 0.5).astype(np.float32)
+    ss = torch.from_numpy(ss_np).to(gpu_device)
+    rs = 1.0 / np.sqrt(ss_np.transpose(0, 2, 1).reshape(MP, H // 32).sum(1) / H + 1e-6)
+    lib = N.lib()
+    blocks = lib.dtree_lmhead_candidate_blocks(V, MP)
+    parents = [-1] + list(range(L - 1))
+    desc = device_desc([0] * L, list(range(L)), parents, 0, gpu_device)
+    posts = []
+    logits = torch.zeros(MP, V, device=gpu_device)
+    for want_logits in (False, True):
+        cand = torch.full((lib.dtree_lmhead_candidates_bytes(MP),), 0x55, dtype=torch.uint8, device=gpu_device)
+        print(f"q4 one-pass lm head rows={MP} logits={want_logits}", flush=True)
+        N.check(lib.dtree_lmhead_argmax(xt.data_ptr(), xlt.data_ptr(), N.W_TILED, H, MP, wt.data_ptr(), N.W_Q4G64,
+                                        sb.data_ptr(), V, H, ss.data_ptr(), H // 32, 1e-6,
+                                        logits.data_ptr() if want_logits else None, cand.data_ptr(), stream()),
+                "q4 lmhead one pass")
+        res = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32, device=gpu_device)
+        N.check(lib.dtree_accept_walk(desc.data_ptr(), cand.data_ptr(), blocks, MP, res.data_ptr(), stream()), "walk")
+        torch.cuda.synchronize()
+        r = res.cpu().numpy()
+        posts.append(list(r[3 + N.MAX_NODES:3 + N.MAX_NODES + L]))
+    assert posts[0] == posts[1] == [300] * L
+    ref = o4.q4_matmul(xin[:L], wq, bf16_to_f32(s), bf16_to_f32(b)) * rs[:L, None]
+    got = logits[:L].cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    assert np.array_equal(got[:, 300], got[:, 2600])
 
 
 def test_q4_embedding_gather(gpu_device):
