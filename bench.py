@@ -414,15 +414,24 @@ def lmhead_kernel_name(quant: str, rows: int) -> str:
 def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows: int = 32) -> str:
     """Kernel the library picks for a tiled GEMM with split_k 0 (gemm.hip,
     dtree_gemm_bf16). q4 over 64-128 rows: the one-pass kernel, two 64-column
-    blocks per workgroup unless a 4-block tiling still covers half the CUs.
+    blocks per workgroup unless a 4-block tiling still covers half the CUs,
+    three when that fills at least an eighth more of the CUs.
     32 rows, bf16: three workgroups per 32-column tile (one per part of K) at
     K >= 4096 and N % 256 == 0 when 3 N / 32 fit the CUs, two at K = 4096 when
     2 N / 32 do; else one per tile at K <= 4096 and N / 32 <= CUs; else
     stream-K. q4 at 32 rows: stream-K, two workgroups per CU when there are at
     least 20 64 x 64 units per CU."""
     if quant == "q4" and rows > 32:
-        nblk = n // 64
+        nblk, nkb = n // 64, k // 64
+
+        def plan(cw):
+            tiles = -(-nblk // cw)
+            parts = max(1, min(cus // tiles, nkb // (2 if cw == 2 else 1)))
+            return tiles * parts
+
         cw = 4 if nblk % 4 == 0 and 2 * (nblk // 4) >= cus else 2
+        if plan(3) >= plan(cw) + cus // 8:
+            cw = 3
         return f"q4m_gemm_kernel<true, {epi}, {rows // 32}, {cw}>"
     if quant == "bf16":
         if k >= 4096 and n % 256 == 0:

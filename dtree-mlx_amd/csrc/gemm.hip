@@ -820,11 +820,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 // For the 65-node trees of the 9B-shaped step (96 rows) the 32-row q4 kernels
 // stream and dequantise the weights once per 32-row block. This kernel makes
 // one pass: a workgroup owns a tile of CW 64-column blocks and one part of K,
-// with one wave per (K lane kl, row block rb, column block cb): 64 * MB * 4
-// threads (KI = 4 / CW K lanes). Per step the workgroup stages the next KI
-// groups' activations (all row blocks, hi and lo planes; 4 KB per row block
-// and plane) in LDS with coalesced 16-byte loads, double buffered and
-// prefetched a step ahead in registers, so each activation byte is loaded
+// with one wave per (K lane kl, row block rb, column block cb): 64 * CW * MB
+// * KI threads (KI = 2 K lanes for CW 2, else 1). Per step the workgroup
+// stages the next KI groups' activations (all row blocks, hi and lo planes;
+// 4 KB per row block and plane) in LDS with coalesced 16-byte loads, double
+// buffered and prefetched a step ahead in registers, so each activation byte is loaded
 // once per workgroup and read from LDS by the CW waves that use it. A wave
 // holds one 32 x 64 accumulator, so two or three waves share each SIMD and
 // one wave's scale/bias arithmetic overlaps another's MFMAs. Per group a wave
@@ -837,13 +837,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 // block.
 template <bool LO, int MB, int CW>
 struct Q4mShape {
-  static constexpr int KI = kWaves / CW;                 // K lanes
+  static constexpr int KI = CW == 2 ? 2 : 1;             // K lanes (CW 2, 3 or 4)
   static constexpr int NPL = LO ? 2 : 1;                 // activation planes
   static constexpr int MP = MB * 32;                     // rows
-  static constexpr int THREADS = kThreads * MB;          // one wave per (kl, rb, cb)
+  static constexpr int THREADS = 64 * CW * MB * KI;      // one wave per (kl, rb, cb); q4m_threads
   static constexpr int CHUNKS = KI * MB * NPL;           // 4 KB activation chunks per step
   static constexpr int STAGE_BYTES = CHUNKS * 4096;
-  static constexpr int LOADS = STAGE_BYTES / (THREADS * 16);  // 16-byte pieces per thread per step
+  static constexpr int PIECES = CHUNKS * 256;            // 16-byte staging pieces per step
+  static constexpr int LOADS = (PIECES + THREADS - 1) / THREADS;  // per thread
   static constexpr int TILE_FLOATS = CW * MP * 64;       // one part's output tile
   static constexpr int RED_BYTES = KI * TILE_FLOATS * 4;
   static constexpr int LDS_BYTES = 2 * STAGE_BYTES > RED_BYTES ? 2 * STAGE_BYTES : RED_BYTES;
@@ -854,12 +855,14 @@ constexpr int kQ4mDepth = 2;  // weight groups in flight per wave
 // (largest logit, first index) of the tile as the workgroup's candidate.
 constexpr int kEpiLmArgmax = 16;
 
+constexpr int q4m_threads(int mb, int cw) { return 64 * cw * mb * (cw == 2 ? 2 : 1); }
+
 template <bool LO, int EPI, int MB, int CW>
-__global__ __launch_bounds__(kThreads * MB) void q4m_gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParams p) {
   using Sh = Q4mShape<LO, MB, CW>;
   constexpr int KI = Sh::KI, NPL = Sh::NPL, MP = Sh::MP, D = kQ4mDepth, NT = Sh::THREADS;
   constexpr int TF = Sh::TILE_FLOATS;
-  static_assert(Sh::LOADS * NT * 16 == Sh::STAGE_BYTES, "staging pieces");
+  static_assert(EPI != kEpiLmArgmax || NT == 8 * MP, "LM-head epilogue: 8 threads per row");
   __shared__ __align__(16) unsigned char lds[Sh::LDS_BYTES];
   __shared__ float rs[MP];
   __shared__ float rs_scratch[NT];
@@ -897,7 +900,7 @@ __global__ __launch_bounds__(kThreads * MB) void q4m_gemm_kernel(GemmParams p) {
   auto x_issue = [&](int st) {
 #pragma unroll
     for (int j = 0; j < Sh::LOADS; ++j) {
-      const int piece = t + j * NT, q = piece >> 8, tq = piece & 255;
+      const int piece = min(t + j * NT, Sh::PIECES - 1), q = piece >> 8, tq = piece & 255;
       const int kk = q / (MB * NPL), rq = (q / NPL) % MB, pl = q % NPL;
       const int kb = g0 + st * KI + kk;
       const unsigned off = kb < g1 ? (unsigned)(rq * nkb + kb) * 4096u + 16u * tq : kOob;
@@ -907,7 +910,8 @@ __global__ __launch_bounds__(kThreads * MB) void q4m_gemm_kernel(GemmParams p) {
   auto x_store = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < Sh::LOADS; ++j)
-      *reinterpret_cast<u32x4_t*>(lds + buf * Sh::STAGE_BYTES + 16 * (t + j * NT)) = xpre[j];
+      if (Sh::LOADS * NT == Sh::PIECES || t + j * NT < Sh::PIECES)
+        *reinterpret_cast<u32x4_t*>(lds + buf * Sh::STAGE_BYTES + 16 * (t + j * NT)) = xpre[j];
   };
   // Weight ring: group j of this wave is kb = g0 + kl + KI * j; two 32-column
   // halves (nb) of q4 words (1 KB each) and their (scale, bias) words.
@@ -1259,15 +1263,25 @@ static bool q4m_enabled() {
 static Q4mPlan q4m_plan(int n, int k, int cus) {
   const int nblk = n / 64, nkb = k / 64;
   static const int cw_env = env_int("DTREE_Q4M_CW", 0), parts_env = env_int("DTREE_Q4M_PARTS", 0);
-  Q4mPlan pl{};
-  pl.cw = cw_env == 2 || cw_env == 4 ? cw_env : ((nblk % 4 == 0 && 2 * (nblk / 4) >= cus) ? 4 : 2);
-  pl.tiles = (nblk + pl.cw - 1) / pl.cw;
-  const int ki = kWaves / pl.cw;
-  int parts = parts_env > 0 ? parts_env : cus / pl.tiles;
-  const int max_parts = nkb / ki;  // at least one step of groups per part
-  if (parts > max_parts) parts = max_parts;
-  if (parts < 1) parts = 1;
-  pl.parts = parts;
+  auto plan_for = [&](int cw) {
+    Q4mPlan q{};
+    q.cw = cw;
+    q.tiles = (nblk + cw - 1) / cw;
+    const int ki = cw == 2 ? 2 : 1;
+    int parts = parts_env > 0 ? parts_env : cus / q.tiles;
+    const int max_parts = nkb / ki;  // at least one step of groups per part
+    if (parts > max_parts) parts = max_parts;
+    if (parts < 1) parts = 1;
+    q.parts = parts;
+    return q;
+  };
+  if (cw_env >= 2 && cw_env <= 4) return plan_for(cw_env);
+  Q4mPlan pl = plan_for((nblk % 4 == 0 && 2 * (nblk / 4) >= cus) ? 4 : 2);
+  // Three column blocks per workgroup when that fills at least an eighth more
+  // of the CUs (the 9B-shaped gate/up: 384 blocks are 192 tiles of 2 or 96 of
+  // 4 in two parts, 192 workgroups; 128 tiles of 3 in two parts fill 256).
+  const Q4mPlan p3 = plan_for(3);
+  if (p3.tiles * p3.parts >= pl.tiles * pl.parts + cus / 8) pl = p3;
   return pl;
 }
 static size_t q4m_workspace_bytes(int rows, int n, int k, int cus) {
@@ -1279,10 +1293,10 @@ static size_t q4m_workspace_bytes(int rows, int n, int k, int cus) {
 template <bool LO, int MB, int CW>
 static void launch_q4m_mb(const GemmParams& p, int epi, int grid, hipStream_t st) {
   switch (epi) {
-    case DTREE_EPI_STORE_F32: q4m_gemm_kernel<LO, DTREE_EPI_STORE_F32, MB, CW><<<grid, kThreads * MB, 0, st>>>(p); break;
-    case DTREE_EPI_RESIDUAL: q4m_gemm_kernel<LO, DTREE_EPI_RESIDUAL, MB, CW><<<grid, kThreads * MB, 0, st>>>(p); break;
-    case DTREE_EPI_SWIGLU: q4m_gemm_kernel<LO, DTREE_EPI_SWIGLU, MB, CW><<<grid, kThreads * MB, 0, st>>>(p); break;
-    default: q4m_gemm_kernel<LO, DTREE_EPI_STORE_BF16, MB, CW><<<grid, kThreads * MB, 0, st>>>(p); break;
+    case DTREE_EPI_STORE_F32: q4m_gemm_kernel<LO, DTREE_EPI_STORE_F32, MB, CW><<<grid, Q4mShape<LO, MB, CW>::THREADS, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: q4m_gemm_kernel<LO, DTREE_EPI_RESIDUAL, MB, CW><<<grid, Q4mShape<LO, MB, CW>::THREADS, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: q4m_gemm_kernel<LO, DTREE_EPI_SWIGLU, MB, CW><<<grid, Q4mShape<LO, MB, CW>::THREADS, 0, st>>>(p); break;
+    default: q4m_gemm_kernel<LO, DTREE_EPI_STORE_BF16, MB, CW><<<grid, Q4mShape<LO, MB, CW>::THREADS, 0, st>>>(p); break;
   }
 }
 template <bool LO, int CW>
@@ -1304,9 +1318,11 @@ static void launch_q4m_lm(const GemmParams& p, int mb, int grid, hipStream_t st)
 static void launch_q4m(const GemmParams& p, int epi, int mb, int cw, int grid, hipStream_t st) {
   if (p.x_lo) {
     if (cw == 4) launch_q4m_cw<true, 4>(p, epi, mb, grid, st);
+    else if (cw == 3) launch_q4m_cw<true, 3>(p, epi, mb, grid, st);
     else launch_q4m_cw<true, 2>(p, epi, mb, grid, st);
   } else {
     if (cw == 4) launch_q4m_cw<false, 4>(p, epi, mb, grid, st);
+    else if (cw == 3) launch_q4m_cw<false, 3>(p, epi, mb, grid, st);
     else launch_q4m_cw<false, 2>(p, epi, mb, grid, st);
   }
 }

@@ -295,8 +295,10 @@ def test_q4_gemm_96_rows(gpu_device):
 # over several K parts; (320, 1024) a ragged last tile (5 blocks in tiles of
 # 2); (32768, 128) four blocks per workgroup in two K parts; (4096, 4096) the
 # 9B out_proj class (two per workgroup, eight K parts); (12352, 256) 193
-# blocks (in_proj's ragged width) in two parts.
-Q4M_SHAPES = [(768, 512), (320, 1024), (32768, 128), (4096, 4096), (12352, 256)]
+# blocks (in_proj's ragged width) in two parts; (24576, 128) and (24448, 128)
+# three blocks per workgroup in two parts (the 9B gate/up plan), the second
+# with a ragged last tile (382 blocks).
+Q4M_SHAPES = [(768, 512), (320, 1024), (32768, 128), (4096, 4096), (12352, 256), (24576, 128), (24448, 128)]
 
 
 @pytest.mark.parametrize("n,k", Q4M_SHAPES)
