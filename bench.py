@@ -183,7 +183,7 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant), nl, us["qkv"], b["qkv"])
+    out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant, lo="qkv" not in eng.HI_ONLY), nl, us["qkv"], b["qkv"])
     out["attention"] = entry(attention_kernel_name(eng.max_past, 128, 128, False, eng.MP), nl, us["attention"],
                              b["attention"])
     out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant), nl, us["o"], b["o"])
@@ -371,11 +371,11 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    kn = lambda n, k, epi: gemm_kernel_name(n, k, epi, quant, rows=eng.MP)  # noqa: E731
+    kn = lambda n, k, epi, lo=True: gemm_kernel_name(n, k, epi, quant, rows=eng.MP, lo=lo)  # noqa: E731
     out = {
         "in_proj_gemm": entry(kn(cfg.in_proj_dim, H, 0), nG, us["in"], b["in"]),
         "out_proj_gemm": entry(kn(H, cfg.value_dim, 1), nG, us["out"], b["out"]),
-        "attn_qkv_gemm": entry(kn(cfg.attn_qkv_dim, H, 0), nA, us["qkv"], b["qkv"]),
+        "attn_qkv_gemm": entry(kn(cfg.attn_qkv_dim, H, 0, "qkv" not in eng.HI_ONLY), nA, us["qkv"], b["qkv"]),
         "o_gemm": entry(kn(H, cfg.q_dim, 1), nA, us["o"], b["o"]),
         "gate_up_gemm": entry(kn(2 * F, H, 2), nL, us["gu"], b["gu"]),
         "down_gemm": entry(kn(H, F, 1), nL, us["down"], b["down"]),
@@ -411,9 +411,11 @@ def lmhead_kernel_name(quant: str, rows: int) -> str:
     return f"lmhead_kernel<{mb}, {2 if mb == 1 else (2 if mb == 2 else 1)}, {2 if mb == 1 else 1}, true, true, {'true' if quant == 'q4' else 'false'}>"
 
 
-def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows: int = 32) -> str:
+def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows: int = 32,
+                     lo: bool = True) -> str:
     """Kernel the library picks for a tiled GEMM with split_k 0 (gemm.hip,
-    dtree_gemm_bf16). q4 over 64-128 rows: the one-pass kernel, two 64-column
+    dtree_gemm_bf16); `lo` False for a projection that reads only the high
+    activation plane (the first template argument). q4 over 64-128 rows: the one-pass kernel, two 64-column
     blocks per workgroup unless a 4-block tiling still covers half the CUs,
     three when that fills at least an eighth more of the CUs.
     32 rows, bf16: three workgroups per 32-column tile (one per part of K) at
@@ -421,6 +423,7 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows:
     2 N / 32 do; else one per tile at K <= 4096 and N / 32 <= CUs; else
     stream-K. q4 at 32 rows: stream-K, two workgroups per CU when there are at
     least 20 64 x 64 units per CU."""
+    L = "true" if lo else "false"
     if quant == "q4" and rows > 32:
         nblk, nkb = n // 64, k // 64
 
@@ -432,18 +435,18 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows:
         cw = 4 if nblk % 4 == 0 and 2 * (nblk // 4) >= cus else 2
         if plan(3) >= plan(cw) + cus // 8:
             cw = 3
-        return f"q4m_gemm_kernel<true, {epi}, {rows // 32}, {cw}>"
+        return f"q4m_gemm_kernel<{L}, {epi}, {rows // 32}, {cw}>"
     if quant == "bf16":
         if k >= 4096 and n % 256 == 0:
             if (n // 32) * 3 <= cus:
-                return f"dp_gemm_kernel<true, {epi}, 3>"
+                return f"dp_gemm_kernel<{L}, {epi}, 3>"
             if k == 4096 and (n // 32) * 2 <= cus:
-                return f"dp_gemm_kernel<true, {epi}, 2>"
+                return f"dp_gemm_kernel<{L}, {epi}, 2>"
         if k <= 4096 and n // 32 <= cus:
-            return f"dp_gemm_kernel<true, {epi}, 1>"
+            return f"dp_gemm_kernel<{L}, {epi}, 1>"
     if quant == "q4" and (n // 64) * (k // 64) >= 20 * cus:
-        return f"sk2_gemm_kernel<true, {epi}>"
-    return f"sk_gemm_kernel<true, {epi}, {'true' if quant == 'q4' else 'false'}>"
+        return f"sk2_gemm_kernel<{L}, {epi}>"
+    return f"sk_gemm_kernel<{L}, {epi}, {'true' if quant == 'q4' else 'false'}>"
 
 
 def copy_probe(mib: int) -> None:
