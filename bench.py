@@ -418,11 +418,11 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows:
     activation plane (the first template argument). q4 over 64-128 rows: the one-pass kernel, two 64-column
     blocks per workgroup unless a 4-block tiling still covers half the CUs,
     three when that fills at least an eighth more of the CUs.
-    32 rows, bf16: three workgroups per 32-column tile (one per part of K) at
-    K >= 4096 and N % 256 == 0 when 3 N / 32 fit the CUs, two at K = 4096 when
-    2 N / 32 do; else one per tile at K <= 4096 and N / 32 <= CUs; else
-    stream-K. q4 at 32 rows: stream-K, two workgroups per CU when there are at
-    least 20 64 x 64 units per CU."""
+    32 rows, bf16 or q4: three workgroups per 32-column tile (one per part of
+    K) at K >= 4096 and N % 256 == 0 when 3 N / 32 fit the CUs, two at K = 4096
+    when 2 N / 32 do; else one per tile at K <= 4096 and N / 32 <= CUs; else
+    stream-K (q4: two workgroups per CU when there are at least 20 64 x 64
+    units per CU)."""
     L = "true" if lo else "false"
     if quant == "q4" and rows > 32:
         nblk, nkb = n // 64, k // 64
@@ -436,14 +436,14 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows:
         if plan(3) >= plan(cw) + cus // 8:
             cw = 3
         return f"q4m_gemm_kernel<{L}, {epi}, {rows // 32}, {cw}>"
-    if quant == "bf16":
-        if k >= 4096 and n % 256 == 0:
-            if (n // 32) * 3 <= cus:
-                return f"dp_gemm_kernel<{L}, {epi}, 3>"
-            if k == 4096 and (n // 32) * 2 <= cus:
-                return f"dp_gemm_kernel<{L}, {epi}, 2>"
-        if k <= 4096 and n // 32 <= cus:
-            return f"dp_gemm_kernel<{L}, {epi}, 1>"
+    dp = "dp_gemm_kernel" if quant == "bf16" else "dpq_gemm_kernel"
+    if k >= 4096 and n % 256 == 0:
+        if (n // 32) * 3 <= cus:
+            return f"{dp}<{L}, {epi}, 3>"
+        if k == 4096 and (n // 32) * 2 <= cus:
+            return f"{dp}<{L}, {epi}, 2>"
+    if k <= 4096 and n // 32 <= cus:
+        return f"{dp}<{L}, {epi}, 1>"
     if quant == "q4" and (n // 64) * (k // 64) >= 20 * cus:
         return f"sk2_gemm_kernel<{L}, {epi}>"
     return f"sk_gemm_kernel<{L}, {epi}, {'true' if quant == 'q4' else 'false'}>"

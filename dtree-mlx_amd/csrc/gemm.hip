@@ -1360,7 +1360,7 @@ static void launch_sk(const GemmParams& p, int epi, hipStream_t st) {
 }
 
 
-// ---- data-parallel GEMM (32 tiled rows, bf16) ------------------------------
+// ---- data-parallel GEMM (32 tiled rows, bf16 or q4 weights) -----------------
 // A workgroup owns one 32-column output tile over the whole K (KS = 1) or
 // over one half of it (KS = 2). Wave w streams the K blocks w, w + 4, ... of
 // its range through a kDpDepth-deep register ring (weights and both
@@ -1378,9 +1378,16 @@ static void launch_sk(const GemmParams& p, int epi, hipStream_t st) {
 // its own L2 when both placements are confirmed (HW_REG_XCC_ID).
 constexpr int kDpDepth = 4;
 
-template <bool LO, int EPI, int KS>
-__global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
+// Q4: group-64 q4 weights (DTREE_W_Q4G64) in place of bf16. A K block is then
+// one quantisation group, 1 KB of nibbles (one 16-byte load per lane) and 32
+// scale/bias pairs per 32-column block; each group gets a fresh MFMA sum of
+// x (128 + q), folded in as acc += s * sum + (b - 128 s) * sum(x), with
+// sum(x) from an MFMA of the same activation registers against bf16 ones (as
+// q4_group).
+template <bool LO, int EPI, int KS, bool Q4>
+__device__ __forceinline__ void dp_gemm_body(const GemmParams& p) {
   constexpr int TN = 32, TE = 32 * TN;
+  constexpr int WL = Q4 ? 1 : 4;  // 16-byte weight loads per lane per K block
   __shared__ float red[kWaves * TE];
   __shared__ float rs[32];
   __shared__ float rs_scratch[kThreads];
@@ -1398,20 +1405,29 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
   ss_issue<1>(p.ss_in, p.ss_tiles, ssv);
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(p.x, p.x_bytes), xlrs = buf_rsrc(p.x_lo, LO ? p.x_bytes : 0u);
   const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(p.w, p.w_bytes);
-  const unsigned wtile = (unsigned)(tile * nkb * 2048) * 2u;
+  const __amdgpu_buffer_rsrc_t sbrs = buf_rsrc(p.w_sb, Q4 ? p.sb_bytes : 0u);
   const int n = wave < nk ? (nk - wave + kWaves - 1) / kWaves : 0;
-  u32x4_t wr[kDpDepth][4], xr[kDpDepth][2][4];
+  u32x4_t wr[kDpDepth][WL], xr[kDpDepth][2][4];
+  uint32_t sbr[kDpDepth];
   // Slots past the wave's blocks are refilled with ranged loads that return
   // zero (same loads on every path, see kOob) and are never consumed.
   auto issue = [&](int s, int j) {
-    const unsigned off = j < n ? (unsigned)((kb0 + wave + kWaves * j) * 2048 + lane * 8) * 2u : kOob;
+    const int kb = kb0 + wave + kWaves * j;
+    const unsigned off = j < n ? (unsigned)(kb * 2048 + lane * 8) * 2u : kOob;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       xr[s][0][i] = buf_ld(xrs, off + 1024u * i);
       if (LO) xr[s][1][i] = buf_ld(xlrs, off + 1024u * i);
     }
+    if constexpr (Q4) {
+      const unsigned blk = (unsigned)(tile * nkb + kb);
+      wr[s][0] = buf_ld_stream(wrs, j < n ? blk * 1024u + lane * 16u : kOob);
+      sbr[s] = buf_ld32(sbrs, j < n ? (blk * 32u + c) * 4u : kOob);
+    } else {
+      const unsigned wtile = (unsigned)(tile * nkb * 2048) * 2u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wr[s][i] = buf_ld_stream(wrs, j < n ? wtile + off + 1024u * i : kOob);
+      for (int i = 0; i < 4; ++i) wr[s][i] = buf_ld_stream(wrs, j < n ? wtile + off + 1024u * i : kOob);
+    }
   };
   f32x16_t acc;
 #pragma unroll
@@ -1425,10 +1441,33 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
       const int j = jb + s;
       if (j < n) {
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (Q4) {
+          const u32x4_t ones = u32x4_t{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+          f32x16_t xs, au;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc = mfma32(xr[s][0][i], wr[s][i], acc);
-          if (LO) acc = mfma32(xr[s][1][i], wr[s][i], acc);
+          for (int r = 0; r < 16; ++r) xs[r] = au[r] = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            xs = mfma32(xr[s][0][i], ones, xs);
+            if (LO) xs = mfma32(xr[s][1][i], ones, xs);
+          }
+          const uint32_t wq[4] = {wr[s][0][0], wr[s][0][1], wr[s][0][2], wr[s][0][3]};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const u32x4_t bq = q4_pairs(wq[i]);
+            au = mfma32(xr[s][0][i], bq, au);
+            if (LO) au = mfma32(xr[s][1][i], bq, au);
+          }
+          const float sc = __uint_as_float(sbr[s] << 16);
+          const float cf = __uint_as_float(sbr[s] & 0xffff0000u) - 128.f * sc;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[r] += sc * au[r] + cf * xs[r];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc = mfma32(xr[s][0][i], wr[s][i], acc);
+            if (LO) acc = mfma32(xr[s][1][i], wr[s][i], acc);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1495,15 +1534,40 @@ __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
   tile_epilogue<32, TN, EPI>(p, red, rs, tile, EPI == DTREE_EPI_RESIDUAL ? xo : nullptr);
 }
 
-template <bool LO, int KS>
+template <bool LO, int EPI, int KS>
+__global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
+  dp_gemm_body<LO, EPI, KS, false>(p);
+}
+
+template <bool LO, int EPI, int KS>
+__global__ __launch_bounds__(kThreads) void dpq_gemm_kernel(GemmParams p) {
+  dp_gemm_body<LO, EPI, KS, true>(p);
+}
+
+template <bool LO, int KS, bool Q4>
 static void launch_dp(const GemmParams& p, int epi, hipStream_t st) {
   const int grid = KS * (p.n / 32);
-  switch (epi) {
-    case DTREE_EPI_STORE_F32: dp_gemm_kernel<LO, DTREE_EPI_STORE_F32, KS><<<grid, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_RESIDUAL: dp_gemm_kernel<LO, DTREE_EPI_RESIDUAL, KS><<<grid, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_SWIGLU: dp_gemm_kernel<LO, DTREE_EPI_SWIGLU, KS><<<grid, kThreads, 0, st>>>(p); break;
-    default: dp_gemm_kernel<LO, DTREE_EPI_STORE_BF16, KS><<<grid, kThreads, 0, st>>>(p); break;
+  if constexpr (Q4) {
+    switch (epi) {
+      case DTREE_EPI_STORE_F32: dpq_gemm_kernel<LO, DTREE_EPI_STORE_F32, KS><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_RESIDUAL: dpq_gemm_kernel<LO, DTREE_EPI_RESIDUAL, KS><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_SWIGLU: dpq_gemm_kernel<LO, DTREE_EPI_SWIGLU, KS><<<grid, kThreads, 0, st>>>(p); break;
+      default: dpq_gemm_kernel<LO, DTREE_EPI_STORE_BF16, KS><<<grid, kThreads, 0, st>>>(p); break;
+    }
+  } else {
+    switch (epi) {
+      case DTREE_EPI_STORE_F32: dp_gemm_kernel<LO, DTREE_EPI_STORE_F32, KS><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_RESIDUAL: dp_gemm_kernel<LO, DTREE_EPI_RESIDUAL, KS><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_SWIGLU: dp_gemm_kernel<LO, DTREE_EPI_SWIGLU, KS><<<grid, kThreads, 0, st>>>(p); break;
+      default: dp_gemm_kernel<LO, DTREE_EPI_STORE_BF16, KS><<<grid, kThreads, 0, st>>>(p); break;
+    }
   }
+}
+template <int KS>
+static void launch_dp_any(const GemmParams& p, int epi, bool q4, hipStream_t st) {
+  const bool lo = p.x_lo != nullptr;
+  if (q4) lo ? launch_dp<true, KS, true>(p, epi, st) : launch_dp<false, KS, true>(p, epi, st);
+  else lo ? launch_dp<true, KS, false>(p, epi, st) : launch_dp<false, KS, false>(p, epi, st);
 }
 
 // ---- long-M GEMM (prompt prefill): rows a multiple of 128 --------------------
@@ -1789,12 +1853,16 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   //   14.5 us stream-K);
   // * else stream-K: more tiles than CUs (N = 10240: 18.2 vs 22.7 us one per
   //   tile) or long K on narrow N.
+  // q4 weights follow the same rule (dpq_gemm_kernel), measured against the
+  // stream-K q4 kernels: QKV (N 6144, K 2560, high plane only) 8.0 vs 12.1 us,
+  // o_proj 10.6 vs 15.3, down_proj 15.0 vs 18.4; gate/up (N 19456: 608 tiles)
+  // keeps the two-per-CU stream-K kernel (21.4 vs 23.5 us one per tile).
   const int auto_cus = device_cus();
-  const bool k_auto = a->split_k == 0 && tiled && !q4 && a->rows_padded == 32;
+  const bool k_auto = a->split_k == 0 && tiled && a->rows_padded == 32;
   const bool pairs_auto = k_auto && a->k >= 4096 && a->n % 256 == 0 &&
                           ((a->n / 32) * 3 <= auto_cus || (a->k == 4096 && (a->n / 32) * 2 <= auto_cus));
   const bool dp_auto = k_auto && !pairs_auto && a->k <= 4096 && a->n / 32 <= auto_cus;
-  if (tiled && !q4 && a->rows_padded == 32 && (a->split_k == -3 || a->split_k == -4 || pairs_auto)) {
+  if (tiled && a->rows_padded == 32 && (a->split_k == -3 || a->split_k == -4 || pairs_auto)) {
     // Two (-3) or three (-4) workgroups per tile, one per part of K (see
     // dp_gemm_kernel).
     // automatic: three parts while the grid stays within one workgroup per CU
@@ -1805,19 +1873,13 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     const size_t need_pairs = dp_pair_workspace_bytes(a->n);
     DTREE_REQUIRE(a->workspace_bytes >= need_pairs, "gemm: workspace too small for the paired schedule");
     p.part_bytes = (unsigned)(need_pairs - kCounterBytes);
-    if (dp_parts == 3) {
-      if (p.x_lo) launch_dp<true, 3>(p, epi, stream);
-      else launch_dp<false, 3>(p, epi, stream);
-    } else {
-      if (p.x_lo) launch_dp<true, 2>(p, epi, stream);
-      else launch_dp<false, 2>(p, epi, stream);
-    }
+    if (dp_parts == 3) launch_dp_any<3>(p, epi, q4, stream);
+    else launch_dp_any<2>(p, epi, q4, stream);
     DTREE_LAUNCH_CHECK("gemm launch");
     return DTREE_OK;
   }
-  if (tiled && !q4 && a->rows_padded == 32 && (a->split_k == -1 || dp_auto)) {
-    if (p.x_lo) launch_dp<true, 1>(p, epi, stream);
-    else launch_dp<false, 1>(p, epi, stream);
+  if (tiled && a->rows_padded == 32 && (a->split_k == -1 || dp_auto)) {
+    launch_dp_any<1>(p, epi, q4, stream);
     DTREE_LAUNCH_CHECK("gemm launch");
     return DTREE_OK;
   }

@@ -129,10 +129,10 @@ def test_q4_gemm_residual_and_swiglu(gpu_device):
 
 
 def _q4_layer_case(epi, g, dev):
-    """Qwen3-4B layer shapes that take the two-workgroups-per-CU stream-K
-    kernel (sk2_gemm_kernel: at least 20 units per CU): down_proj with the
-    residual epilogue (N 2560, K 9728) and gate/up with SwiGLU (N 19456,
-    K 2560)."""
+    """Qwen3-4B layer shapes: down_proj with the residual epilogue (N 2560,
+    K 9728; automatically three per-tile workgroups, one per part of K) and
+    gate/up with SwiGLU (N 19456, K 2560; automatically the two-per-CU
+    stream-K kernel, at least 20 units per CU)."""
     L = 25
     if epi == N.EPI_RESIDUAL:
         n, k = 2560, 9728
@@ -153,10 +153,11 @@ def _q4_layer_case(epi, g, dev):
     return n, k, wt.to(dev), sb.to(dev), xt, xlt, xin, ref_w
 
 
-def _run_q4_layer(epi, n, k, wt, sb, xt, xlt, g_seed, dev):
+def _run_q4_layer(epi, n, k, wt, sb, xt, xlt, g_seed, dev, split_k=0):
     g = np.random.default_rng(g_seed)
     ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(32, n, k, 0), dtype=torch.uint8, device=dev)
     a = _args(xt, xlt, wt, sb, n, k, epi, ws)
+    a.split_k = split_k
     out = {}
     if epi == N.EPI_RESIDUAL:
         res = torch.zeros(32, n)
@@ -180,11 +181,16 @@ def _run_q4_layer(epi, n, k, wt, sb, xt, xlt, g_seed, dev):
     return out
 
 
-@pytest.mark.parametrize("epi", [N.EPI_RESIDUAL, N.EPI_SWIGLU])
-def test_q4_sk2_layer_shapes(gpu_device, epi):
+# split_k 0: the automatic schedule (residual: dpq_gemm_kernel, three parts;
+# SwiGLU: sk2_gemm_kernel); -2 forces stream-K (sk2_gemm_kernel at these unit
+# counts); -1 / -4 force the per-tile q4 kernel with one / three parts of K.
+@pytest.mark.parametrize("epi,split_k", [(N.EPI_RESIDUAL, 0), (N.EPI_RESIDUAL, -2), (N.EPI_RESIDUAL, -1),
+                                         (N.EPI_SWIGLU, 0), (N.EPI_SWIGLU, -1), (N.EPI_SWIGLU, -4)])
+def test_q4_layer_shapes(gpu_device, epi, split_k):
     g = np.random.default_rng(91 + epi)
     n, k, wt, sb, xt, xlt, xin, ref_w = _q4_layer_case(epi, g, gpu_device)
-    runs = [_run_q4_layer(epi, n, k, wt, sb, xt, xlt, 5, gpu_device) for _ in range(2)]
+    print(f"q4 layer shape n={n} k={k} epi={epi} split_k={split_k}", flush=True)
+    runs = [_run_q4_layer(epi, n, k, wt, sb, xt, xlt, 5, gpu_device, split_k) for _ in range(2)]
     if epi == N.EPI_RESIDUAL:
         wq, s, b = ref_w[0]
         ref = runs[0]["res0"].double().numpy() + o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b))
@@ -205,15 +211,17 @@ def test_q4_sk2_layer_shapes(gpu_device, epi):
         assert int(r["ws"][: (n // 64) * 4].view(torch.int32).abs().sum()) == 0
 
 
-def test_q4_sk2_partials_read_past_the_l2(gpu_device, monkeypatch):
+@pytest.mark.parametrize("split_k", [0, -2])
+def test_q4_partials_read_past_the_l2(gpu_device, monkeypatch, split_k):
     """DTREE_TEST_OFF_XCD=1 makes every workgroup count as off its expected
-    XCD, so the two-per-CU q4 kernel reads its partial tiles past the L2; the
+    XCD, so the per-tile q4 kernel's parts (split_k 0) and the two-per-CU
+    stream-K kernel (split_k -2) read their partial tiles past the L2; the
     bits must equal the native run's."""
     g = np.random.default_rng(123)
     n, k, wt, sb, xt, xlt, xin, _ = _q4_layer_case(N.EPI_RESIDUAL, g, gpu_device)
-    native = _run_q4_layer(N.EPI_RESIDUAL, n, k, wt, sb, xt, xlt, 6, gpu_device)
+    native = _run_q4_layer(N.EPI_RESIDUAL, n, k, wt, sb, xt, xlt, 6, gpu_device, split_k)
     monkeypatch.setenv("DTREE_TEST_OFF_XCD", "1")
-    off = _run_q4_layer(N.EPI_RESIDUAL, n, k, wt, sb, xt, xlt, 6, gpu_device)
+    off = _run_q4_layer(N.EPI_RESIDUAL, n, k, wt, sb, xt, xlt, 6, gpu_device, split_k)
     monkeypatch.delenv("DTREE_TEST_OFF_XCD")
     for key in ("res", "xg", "ss"):
         assert torch.equal(native[key], off[key]), key
