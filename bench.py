@@ -404,8 +404,9 @@ def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -
 
 def lmhead_kernel_name(quant: str, rows: int) -> str:
     """LM-head kernel (gemm.hip, dtree_lmhead_argmax): the one-pass q4 kernel's
-    argmax epilogue for q4 over 64-128 rows, else the persistent LM head."""
-    if quant == "q4" and rows > 32:
+    argmax epilogue for a q4 embedding (vocabularies up to 262144), else the
+    persistent LM head."""
+    if quant == "q4":
         return f"q4m_gemm_kernel<true, 16, {rows // 32}, 4>"
     mb = rows // 32
     return f"lmhead_kernel<{mb}, {2 if mb == 1 else (2 if mb == 2 else 1)}, {2 if mb == 1 else 1}, true, true, {'true' if quant == 'q4' else 'false'}>"

@@ -1310,6 +1310,7 @@ static void launch_q4m_cw(const GemmParams& p, int epi, int mb, int grid, hipStr
 template <bool LO>
 static void launch_q4m_lm(const GemmParams& p, int mb, int grid, hipStream_t st) {
   switch (mb) {
+    case 1: q4m_gemm_kernel<LO, kEpiLmArgmax, 1, 4><<<grid, kThreads, 0, st>>>(p); break;
     case 2: q4m_gemm_kernel<LO, kEpiLmArgmax, 2, 4><<<grid, kThreads * 2, 0, st>>>(p); break;
     case 3: q4m_gemm_kernel<LO, kEpiLmArgmax, 3, 4><<<grid, kThreads * 3, 0, st>>>(p); break;
     default: q4m_gemm_kernel<LO, kEpiLmArgmax, 4, 4><<<grid, kThreads * 4, 0, st>>>(p); break;
@@ -1997,12 +1998,13 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
                   "lmhead: q4 embedding needs tiled x and hidden <= 4096");
     DTREE_REQUIRE(emb_scales && ((uintptr_t)emb & 15) == 0, "lmhead: q4 embedding needs emb_scales");
     DTREE_REQUIRE(vocab % 64 == 0, "lmhead: q4 embedding needs vocab % 64 == 0");
-    if (rows_padded > 32 && q4m_enabled()) {
+    if ((vocab / 64 + 3) / 4 <= grid && q4m_enabled()) {
       // One pass over the q4 embedding for every row block: the one-pass q4
       // GEMM kernel with its LM-head epilogue, 4 64-column blocks per
       // workgroup, one workgroup per candidate block (the ones past the
-      // vocab's tiles report empty candidates).
-      DTREE_REQUIRE((vocab / 64 + 3) / 4 <= grid, "lmhead: vocab too large for the q4 one-pass candidate grid");
+      // vocab's tiles report empty candidates). Also at 32 rows, where the
+      // activations staged once per K group in LDS serve the four column
+      // blocks (Qwen3-4B: 103 vs 172 us for the 32-row kernel below).
       DTREE_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)x_lo & 15) == 0 && ((uintptr_t)emb_scales & 3) == 0,
                     "lmhead: q4 operands misaligned");
       const size_t xb = (size_t)rows_padded * hidden * 2, wb = (size_t)vocab * hidden / 2;
@@ -2018,10 +2020,12 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
       DTREE_LAUNCH_CHECK("lmhead launch");
       return DTREE_OK;
     }
-    // One pass of the 32-row kernel per 32-row block (tiled x, statistics and
-    // candidates are contiguous per block; logits rows are row-major). The
-    // kernel walks 64-column tiles; the grid stays the candidate block count
-    // of this row count (workgroups past the tiles write empty candidates).
+    // Vocabularies past the one-pass grid (more than 4 x 64 x 1024 = 262144
+    // entries) or DTREE_Q4M=0: one pass of the 32-row kernel per 32-row block (tiled x,
+    // statistics and candidates are contiguous per block; logits rows are
+    // row-major). The kernel walks 64-column tiles; the grid stays the
+    // candidate block count of this row count (workgroups past the tiles
+    // write empty candidates).
     p.ntiles = vocab / 64;
     for (int r = 0; r < rows_padded / 32; ++r) {
       LmParams pb = p;

@@ -468,6 +468,51 @@ def test_q4_lmhead_argmax_and_logits(gpu_device):
     assert best[3] == 5
 
 
+@pytest.mark.parametrize("MP", [32, 96])
+def test_q4_lmhead_vocab_past_the_one_pass_grid(gpu_device, MP):
+    """A vocabulary of more than 4 x 64 x 1024 entries does not fit the one-pass
+    kernel's candidate grid: the 32-row kernel runs once per row block
+    instead. Logits and first-index argmax against the q4 oracle."""
+    g = np.random.default_rng(17 + MP)
+    V, H, L = 4 * 64 * 1024 + 128, 128, MP - 7
+    wq, s, b = o4.random_q4(V, H, g)
+    # Row 3's scales (2.0, twelve standard deviations past the random ones)
+    # give it the largest norm, so x = 4 E[3] peaks there (Cauchy-Schwarz);
+    # row V - 40 copies it: a tie across workgroups.
+    from oracle.qwen3 import f32_to_bf16_bits
+    s[3] = f32_to_bf16_bits(np.full(s.shape[1], 2.0, np.float32))
+    wq[V - 40] = wq[3]; s[V - 40] = s[3]; b[V - 40] = b[3]
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    wt, sb = wt.to(gpu_device), sb.to(gpu_device)
+    xf = np.zeros((MP, H), np.float32)
+    xf[:L] = g.standard_normal((L, H))
+    xf[1] = o4.dequantize(wq[3:4], bf16_to_f32(s[3:4]), bf16_to_f32(b[3:4]))[0].astype(np.float32) * 4.0
+    hi = torch.from_numpy(xf).to(torch.bfloat16)
+    lo = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16)
+    xt, xlt = tile_weight(hi.to(gpu_device)), tile_weight(lo.to(gpu_device))
+    lib = N.lib()
+    cand = torch.zeros(lib.dtree_lmhead_candidates_bytes(MP), dtype=torch.uint8, device=gpu_device)
+    logits = torch.zeros(MP, V, device=gpu_device)
+    print(f"q4 lmhead V={V} H={H} MP={MP}", flush=True)
+    N.check(lib.dtree_lmhead_argmax(xt.data_ptr(), xlt.data_ptr(), N.W_TILED, H, MP, wt.data_ptr(), N.W_Q4G64,
+                                    sb.data_ptr(), V, H, None, 0, 1e-6, logits.data_ptr(), cand.data_ptr(),
+                                    stream()), "q4 lmhead")
+    torch.cuda.synchronize()
+    xin = hi.double().numpy() + lo.double().numpy()
+    ref = o4.q4_matmul(xin[:L], wq, bf16_to_f32(s), bf16_to_f32(b))
+    got = logits[:L].cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    blocks = lib.dtree_lmhead_candidate_blocks(V, MP)
+    c = cand.view(torch.int32)[: (MP // 32) * blocks * 64].view(MP // 32, blocks, 32, 2).cpu().numpy()
+    best = []
+    for m in range(L):
+        cb = c[m // 32, :, m % 32]
+        vals, idx = cb[:, 0].view(np.float32), cb[:, 1]
+        best.append(int(idx[np.lexsort((idx, -vals))[0]]))
+    assert best == np.argmax(got, axis=-1).tolist()
+    assert best[1] == 3
+
+
 def test_q4_lmhead_96_rows_through_walk(gpu_device):
     """q4 LM head over 65 tree rows (one pass over the embedding for the three
     row blocks): the walk's posterior over all 65 rows equals the argmax of
