@@ -569,6 +569,7 @@ __global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const floa
 // beta. Node count and parents come from the step descriptor.
 struct PrepParams {
   const DtreeStepDesc* desc; int rows;  // rows = node capacity (sizes LDS)
+  int chain;  // > 0: a causal chain of `chain` rows (parent of t is t - 1), no desc
   const float* x; int ldx;  // conv input = proj columns [0, C)
   const float* base; const float* w;
   int C, key_dim, Hv, ab_col;  // b at proj column ab_col + h, a at ab_col + Hv + h
@@ -593,7 +594,7 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
   constexpr int NB = kPrepNodes, NW = DK / 64;
   __shared__ int par[kGdnMaxNodes];
   __shared__ float wsum[NB][NW];
-  const int L = min(max(p.desc->num_nodes, 0), p.rows);
+  const int L = p.chain > 0 ? p.chain : min(max(p.desc->num_nodes, 0), p.rows);
   const int t0 = blockIdx.y * NB;
   if (t0 >= L) return;
   const int tid = threadIdx.x;
@@ -609,7 +610,8 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
     }
     return;
   }
-  for (int t = tid; t < L; t += DK) par[t] = valid_parent(p.desc->parents[t], t);
+  if (p.chain == 0)
+    for (int t = tid; t < L; t += DK) par[t] = valid_parent(p.desc->parents[t], t);
   const int c0 = blockIdx.x * DK, c = c0 + tid;
   float wk[KEEP + 1], bk[KEEP];
 #pragma unroll
@@ -628,7 +630,7 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
     for (int i = 0; i <= KEEP; ++i) {
       if (anc >= 0) {
         val[n][i] = p.x[(size_t)anc * p.ldx + c];
-        anc = par[anc];
+        anc = p.chain > 0 ? anc - 1 : par[anc];
       } else {
         val[n][i] = bk[KEEP - 1 - min(nb, KEEP - 1)];
         ++nb;
@@ -683,15 +685,17 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
 // Gated RMSNorm of the recurrence output per (node, value head)
 // (RMSNormGated, qwen35_tree.py:322): o = rms_norm(y) * w * silu(z), written as
 // the split bf16 pair [hi, lo] the out_proj GEMM reads. 16 threads per
-// (node, head), 8 dims each; rows >= L are written as zero.
+// (node, head), 8 dims each; rows >= L are written as zero. chain > 0: L is
+// chain (a prompt chain, no desc).
 template <int DV>
-__global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const DtreeStepDesc* desc, const float* __restrict__ y,
+__global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const DtreeStepDesc* desc, int chain,
+                                                             const float* __restrict__ y,
                                                              const float* __restrict__ z, int ldz,
                                                              const uint16_t* __restrict__ w, float eps, int Hv,
                                                              int rows, uint16_t* out, uint16_t* out_lo, int tiled,
                                                              int ld_out) {
   constexpr int TPH = DV / 8;  // threads per (node, head)
-  const int L = desc->num_nodes;
+  const int L = chain > 0 ? chain : desc->num_nodes;
   const int gid = blockIdx.x * (256 / TPH) + threadIdx.x / TPH;
   const int part = threadIdx.x % TPH;
   if (gid >= rows * Hv) return;
@@ -731,6 +735,85 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const DtreeStepDesc
   const size_t oi = tiled ? tiled_index(t, col, ld_out) : (size_t)t * ld_out + col;
   *reinterpret_cast<u32x4_t*>(out + oi) = hi;
   if (out_lo) *reinterpret_cast<u32x4_t*>(out_lo + oi) = lo;
+}
+
+// ---- causal chain (prompt prefill) -------------------------------------------
+// The recurrence over T prompt tokens that continue the committed state
+// (gated_delta_update over the prompt, custom_qwen35_model.py:868-878): a
+// workgroup owns one value head and 8 state rows (32 lanes x 4 elements per
+// row, as gdn_tree_reg_kernel), walks the tokens in order with its state in
+// registers and the next kChainAhead tokens' inputs in flight, writes y per
+// token (the same step as the tree kernels) and leaves the final state in
+// `state`. Workgroups past state_blocks advance the committed conv window to
+// the last `keep` rows of (window ++ conv inputs) (custom_qwen35_model.py:
+// 849-851), one channel per thread; the prep launch before this one has read
+// the old window.
+constexpr int kChainAhead = 8;
+
+__global__ __launch_bounds__(256) void gdn_chain_scan_kernel(GdnParams p, const float* __restrict__ x, int ldx,
+                                                             float* window, int C, int keep, int state_blocks) {
+  const int T = p.T;
+  if ((int)blockIdx.x >= state_blocks) {
+    const int c = ((int)blockIdx.x - state_blocks) * 256 + threadIdx.x;
+    if (c >= C) return;
+    float old[kConvMaxKeep];
+#pragma unroll
+    for (int r = 0; r < kConvMaxKeep; ++r) old[r] = r < keep ? window[(size_t)r * C + c] : 0.f;
+#pragma unroll
+    for (int r = 0; r < kConvMaxKeep; ++r) {
+      if (r >= keep) break;
+      // row r of the new window = element T + r of (old window ++ x)
+      const int e = T + r;
+      float val = 0.f;
+      if (e < keep) {
+#pragma unroll
+        for (int j = 0; j < kConvMaxKeep; ++j) val = j == e ? old[j] : val;
+      } else {
+        val = x[(size_t)(e - keep) * ldx + c];
+      }
+      window[(size_t)r * C + c] = val;
+    }
+    return;
+  }
+  constexpr int DK = 128, RPW = 8, A = kChainAhead;
+  const int nslices = p.Dv / RPW;
+  const int h = blockIdx.x / nslices, row0 = (blockIdx.x % nslices) * RPW;
+  const int hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x, rl = tid >> 5, lane = tid & 31;
+  const int dv = row0 + rl;
+  float* sp = p.state + ((size_t)h * p.Dv + dv) * DK + 4 * lane;
+  f32x4_t s = *reinterpret_cast<const f32x4_t*>(sp);
+  f32x4_t rk[A], rq[A];
+  float rv[A], rg[A], rb[A];
+  auto load = [&](int a, int t) {
+    if (t < T) {
+      rk[a] = *reinterpret_cast<const f32x4_t*>(p.k + ((size_t)t * p.Hk + hk) * DK + 4 * lane);
+      rq[a] = *reinterpret_cast<const f32x4_t*>(p.q + ((size_t)t * p.Hk + hk) * DK + 4 * lane);
+      rv[a] = p.v[((size_t)t * p.Hv + h) * p.Dv + dv];
+      rg[a] = p.g[(size_t)t * p.Hv + h];
+      rb[a] = p.beta[(size_t)t * p.Hv + h];
+    }
+  };
+#pragma unroll
+  for (int a = 0; a < A; ++a) load(a, a);
+  for (int t0 = 0; t0 < T; t0 += A) {
+#pragma unroll
+    for (int a = 0; a < A; ++a) {
+      const int t = t0 + a;
+      if (t >= T) break;
+      const f32x4_t kk = rk[a], qq = rq[a];
+      const float v = rv[a], g = rg[a], b = rb[a];
+      load(a, t + A);
+      float sk = s[0] * kk[0] + s[1] * kk[1] + s[2] * kk[2] + s[3] * kk[3];
+      float sq = s[0] * qq[0] + s[1] * qq[1] + s[2] * qq[2] + s[3] * qq[3];
+      float kq = kk[0] * qq[0] + kk[1] * qq[1] + kk[2] * qq[2] + kk[3] * qq[3];
+      row_sum32x3(sk, sq, kq);
+      const float delta = (v - g * sk) * b;
+      s = s * g + kk * delta;
+      if (lane == 0) p.y[((size_t)t * p.Hv + h) * p.Dv + dv] = g * sq + delta * kq;
+    }
+  }
+  *reinterpret_cast<f32x4_t*>(sp) = s;
 }
 
 // Rows per workgroup: the largest power of two <= 256 / (Dk / 4) and <= Dv
@@ -919,7 +1002,7 @@ extern "C" int dtree_gdn_layer_gated_norm(const DtreeGdnArgs* a, hipStream_t str
   const int pairs = a->rows_padded * a->num_v_heads;
   const int per_block = 256 / (128 / 8);
   gdn_gated_norm_kernel<128><<<(pairs + per_block - 1) / per_block, 256, 0, stream>>>(
-      a->desc, a->y, a->proj + C, a->ld_proj, a->norm_w, a->eps, a->num_v_heads, a->rows_padded, a->out, a->out_lo,
+      a->desc, 0, a->y, a->proj + C, a->ld_proj, a->norm_w, a->eps, a->num_v_heads, a->rows_padded, a->out, a->out_lo,
       a->out_layout == DTREE_W_TILED, a->ld_out);
   DTREE_LAUNCH_CHECK("gdn_layer_gated_norm launch");
   return DTREE_OK;
@@ -940,5 +1023,67 @@ extern "C" int dtree_gdn_layer_commit(const DtreeGdnArgs* a, hipStream_t stream)
   gdn_commit_kernel<128><<<conv_blocks + state_blocks, 256, 0, stream>>>(p, a->proj, a->ld_proj, a->window, C,
                                                                           a->conv_keep, conv_blocks);
   DTREE_LAUNCH_CHECK("gdn_layer_commit launch");
+  return DTREE_OK;
+}
+
+// A GatedDeltaNet layer's core over a causal chain of num_tokens prompt tokens
+// that continue the committed window and state: conv + SiLU and the q / k / v
+// / g / beta prep, the recurrence (final state committed, conv window
+// advanced), and the gated RMSNorm into the out_proj input. desc is unused;
+// rows_padded is the row capacity of the per-row buffers.
+extern "C" int dtree_gdn_layer_chain(const DtreeGdnArgs* a, int32_t num_tokens, hipStream_t stream) {
+  DTREE_REQUIRE(a, "gdn_layer_chain: null args");
+  DTREE_REQUIRE(num_tokens >= 1 && num_tokens <= a->rows_padded, "gdn_layer_chain: num_tokens in [1, rows_padded]");
+  DTREE_REQUIRE(a->num_k_heads > 0 && a->num_v_heads > 0 && a->num_v_heads % a->num_k_heads == 0,
+                "gdn_layer_chain: num_v_heads % num_k_heads");
+  DTREE_REQUIRE(a->head_k_dim == 128 && a->head_v_dim == 128, "gdn_layer_chain: head dims 128 are compiled");
+  DTREE_REQUIRE(a->conv_keep >= 1 && a->conv_keep <= kConvMaxKeep, "gdn_layer_chain: conv_keep in [1, 7]");
+  DTREE_REQUIRE(a->proj && a->window && a->conv_w && a->A_log && a->dt_bias && a->state && a->q && a->k && a->v &&
+                    a->g && a->beta && a->y && a->norm_w && a->out,
+                "gdn_layer_chain: null pointer");
+  const int key_dim = a->num_k_heads * a->head_k_dim, value_dim = a->num_v_heads * a->head_v_dim;
+  const int C = 2 * key_dim + value_dim;
+  DTREE_REQUIRE(a->ld_proj >= C + value_dim + 2 * a->num_v_heads && a->ld_proj % 4 == 0 &&
+                    ((uintptr_t)a->proj & 15) == 0,
+                "gdn_layer_chain: proj must be 16-byte aligned, ld_proj >= C + z + b + a, ld_proj % 4 == 0");
+  DTREE_REQUIRE(((uintptr_t)a->q & 15) == 0 && ((uintptr_t)a->k & 15) == 0 && ((uintptr_t)a->state & 15) == 0 &&
+                    ((uintptr_t)a->out & 15) == 0 && ((uintptr_t)a->out_lo & 15) == 0 && ((uintptr_t)a->y & 15) == 0 &&
+                    ((uintptr_t)a->norm_w & 15) == 0,
+                "gdn_layer_chain: q, k, state, y, norm_w, out and out_lo must be 16-byte aligned");
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ? (a->ld_out >= value_dim && a->ld_out % 8 == 0)
+                                                  : (a->out_layout == DTREE_W_TILED && a->ld_out == value_dim &&
+                                                     value_dim % 64 == 0 && a->rows_padded % 32 == 0),
+                "gdn_layer_chain: out layout (tiled needs ld_out == value dim, rows_padded % 32 == 0)");
+  PrepParams pp{};
+  pp.desc = nullptr; pp.rows = a->rows_padded; pp.chain = num_tokens;
+  pp.x = a->proj; pp.ldx = a->ld_proj; pp.base = a->window; pp.w = a->conv_w;
+  pp.C = C; pp.key_dim = key_dim; pp.Hv = a->num_v_heads; pp.ab_col = C + value_dim;
+  pp.A_log = a->A_log; pp.dt_bias = a->dt_bias;
+  pp.q = a->q; pp.k = a->k; pp.v = a->v; pp.g = a->g; pp.beta = a->beta;
+  pp.q_scale = 1.0f / (float)a->head_k_dim;
+  pp.k_scale = 1.0f / sqrtf((float)a->head_k_dim);
+  const dim3 pgrid(C / 128 + 1, (num_tokens + kPrepNodes - 1) / kPrepNodes);
+  switch (a->conv_keep) {
+#define DTREE_PREP_CASE(K) \
+  case K: gdn_prep_kernel<K, 128><<<pgrid, 128, 0, stream>>>(pp); break;
+    DTREE_PREP_CASE(1) DTREE_PREP_CASE(2) DTREE_PREP_CASE(3) DTREE_PREP_CASE(4) DTREE_PREP_CASE(5)
+    DTREE_PREP_CASE(6) DTREE_PREP_CASE(7)
+#undef DTREE_PREP_CASE
+  }
+  DTREE_LAUNCH_CHECK("gdn_layer_chain prep launch");
+  GdnParams p{};
+  p.q = a->q; p.k = a->k; p.v = a->v; p.g = a->g; p.beta = a->beta; p.state = a->state;
+  p.T = num_tokens; p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->head_v_dim; p.y = a->y;
+  const int state_blocks = a->num_v_heads * (a->head_v_dim / 8);
+  const int conv_blocks = (C + 255) / 256;
+  gdn_chain_scan_kernel<<<state_blocks + conv_blocks, 256, 0, stream>>>(p, a->proj, a->ld_proj, a->window, C,
+                                                                         a->conv_keep, state_blocks);
+  DTREE_LAUNCH_CHECK("gdn_layer_chain scan launch");
+  const int pairs = a->rows_padded * a->num_v_heads;
+  const int per_block = 256 / (128 / 8);
+  gdn_gated_norm_kernel<128><<<(pairs + per_block - 1) / per_block, 256, 0, stream>>>(
+      nullptr, num_tokens, a->y, a->proj + C, a->ld_proj, a->norm_w, a->eps, a->num_v_heads, a->rows_padded, a->out,
+      a->out_lo, a->out_layout == DTREE_W_TILED, a->ld_out);
+  DTREE_LAUNCH_CHECK("gdn_layer_chain gated norm launch");
   return DTREE_OK;
 }

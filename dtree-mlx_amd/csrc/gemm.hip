@@ -282,9 +282,10 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* 
                                               const float* xpre = nullptr) {
   constexpr int TE = MP * TN;
   if constexpr (EPI == DTREE_EPI_STORE_F32) {
+    // (columns past p.n: the long-M GEMM's last tile when n % 128 == 64)
     for (int e = threadIdx.x; e < TE; e += kThreads) {
       const int m = e / TN, n = e % TN;
-      p.out_f32[(size_t)m * p.ld_out_f32 + tile * TN + n] = red[e] * rs[m];
+      if (tile * TN + n < p.n) p.out_f32[(size_t)m * p.ld_out_f32 + tile * TN + n] = red[e] * rs[m];
     }
   } else if constexpr (EPI == DTREE_EPI_STORE_BF16) {
     for (int e = threadIdx.x; e < TE; e += kThreads) {
@@ -1593,7 +1594,7 @@ __global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
   const int t = threadIdx.x, lane = t & 63, c = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wr = wave >> 1, wc = wave & 1;
-  const int ntn = p.n / kLongCols;
+  const int ntn = (p.n + kLongCols - 1) / kLongCols;  // the last tile may hold 64 columns (STORE_F32)
   const int mt = blockIdx.x / ntn, nt = blockIdx.x - mt * ntn;
   const int nkb = p.k >> 6;
   const int R = mt * kLongRows;
@@ -1615,7 +1616,9 @@ __global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
       if (LO) ld[rb * NPL + NPL - 1] = ld_u32x4(p.x_lo + blk);
     }
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) ld[ABLK + cb] = ld_u32x4(p.w + ((size_t)(nt * 4 + cb) * nkb + kb) * 2048 + 8 * t);
+    for (int cb = 0; cb < 4; ++cb)
+      ld[ABLK + cb] = (nt * 4 + cb) * 32 < p.n ? ld_u32x4(p.w + ((size_t)(nt * 4 + cb) * nkb + kb) * 2048 + 8 * t)
+                                               : u32x4_t{0u, 0u, 0u, 0u};
   };
   auto store_stage = [&](int s) {
 #pragma unroll
@@ -1924,9 +1927,10 @@ extern "C" int dtree_gemm_long(const DtreeGemmArgs* a, hipStream_t stream) {
                 "gemm_long: tiled bf16 activations and weights");
   DTREE_REQUIRE(a->rows_padded >= kLongRows && a->rows_padded % kLongRows == 0 && a->rows_padded <= (1 << 20),
                 "gemm_long: rows_padded must be a positive multiple of 128");
-  DTREE_REQUIRE(a->n > 0 && a->n % kLongCols == 0, "gemm_long: n must be a positive multiple of 128");
-  DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0 && a->ldx == a->k, "gemm_long: k a multiple of 64, ldx == k");
   const int epi = a->epilogue;
+  DTREE_REQUIRE(a->n > 0 && (a->n % kLongCols == 0 || (a->n % 64 == 0 && epi == DTREE_EPI_STORE_F32)),
+                "gemm_long: n must be a positive multiple of 128 (of 64 with the fp32 store epilogue)");
+  DTREE_REQUIRE(a->k > 0 && a->k % 64 == 0 && a->ldx == a->k, "gemm_long: k a multiple of 64, ldx == k");
   DTREE_REQUIRE(epi >= 0 && epi <= 3, "gemm_long: unknown epilogue");
   if (epi == DTREE_EPI_STORE_F32 || epi == DTREE_EPI_RESIDUAL)
     DTREE_REQUIRE(a->out_f32 && a->ld_out_f32 >= a->n, "gemm_long: out_f32 missing or ld too small");
@@ -1955,7 +1959,7 @@ extern "C" int dtree_gemm_long(const DtreeGemmArgs* a, hipStream_t stream) {
   p.out_tiled = a->out_layout == DTREE_W_TILED;
   p.next_norm = a->next_norm; p.ss_out = a->ss_out;
   p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
-  const long long grid = (long long)(a->rows_padded / kLongRows) * (a->n / kLongCols);
+  const long long grid = (long long)(a->rows_padded / kLongRows) * ((a->n + kLongCols - 1) / kLongCols);
   DTREE_REQUIRE(grid < (1LL << 31), "gemm_long: grid too large");
   if (a->x_lo) launch_long<true>(p, epi, (int)grid, stream);
   else launch_long<false>(p, epi, (int)grid, stream);

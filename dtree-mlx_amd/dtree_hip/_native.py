@@ -154,6 +154,7 @@ SIGNATURES = {
     "dtree_gdn_layer_recurrence": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_gated_norm": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_commit": (C.c_int, [C.POINTER(GdnArgs), _vp]),
+    "dtree_gdn_layer_chain": (C.c_int, [C.POINTER(GdnArgs), C.c_int32, _vp]),
     "dtree_graph_begin": (C.c_int, [_vp]),
     "dtree_graph_end": (C.c_int, [_vp, C.POINTER(C.c_void_p)]),
     "dtree_graph_launch": (C.c_int, [_vp, _vp]),

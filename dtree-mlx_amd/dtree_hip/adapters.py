@@ -322,11 +322,21 @@ class Qwen35TargetAdapter(Qwen3TargetAdapter):
 
     def forward_with_hidden_states(self, model: Qwen35TreeModel, inputs, cache: Qwen35Cache, layer_ids,
                                    return_rollback_records: bool = False):
-        """Prefill as fully accepted chains of <= max_nodes tokens; returns the
-        last position's logits ([1, 1, V]) and every position's verifier hidden."""
+        """Prefill (adapters.py:290-307, forward_dflash over the prompt): the
+        long-M GEMM path for 128 tokens or more (bf16 weights), else fully
+        accepted chains of <= max_nodes tokens through the tree kernels; the
+        cache commits either way. Returns the last position's logits
+        ([1, 1, V]) and every position's verifier hidden."""
         eng = model.engine
         eng.set_layer_ids(layer_ids)
         toks = _as_list(inputs)
+        if len(toks) >= 128 and eng.supports_long_prefill():
+            logits, hidden = eng.prefill_long(cache, toks)
+            target_hidden = (hidden[None] if hidden is not None
+                             else torch.zeros(1, len(toks), 0, device=eng.dev))
+            if return_rollback_records:
+                return logits, target_hidden, {}
+            return logits, target_hidden
         hid = []
         n = 0
         for s in range(0, len(toks), eng.max_nodes):

@@ -287,6 +287,54 @@ class TreeEngineBase:
         a = self.gemm_args(name, x, ldx, w, epi, **kw)
         N.check(self.lib.dtree_gemm_bf16(C.byref(a), st), f"gemm {name}")
 
+    # ---- prompt prefill on the long-M GEMM: pieces shared by both models -------
+    PREFILL_SEGMENT = 1024  # prompt rows per pass through the layer stack (a multiple of 128)
+
+    def _long_gemm(self, name, x, k, w, epi, rows, st, **kw):
+        a = self.gemm_args(name, x, k, w, epi, **kw)
+        a.rows_padded = rows
+        N.check(self.lib.dtree_gemm_long(C.byref(a), st), f"long gemm {name}")
+
+    def _prefill_chunks(self, pf: dict, P0: int, n: int, rows: int, rope_dims: int, st: int) -> int:
+        """Step descriptors of a segment's 128-row causal chunks (chain trees
+        over the cached prefix: chunk ch holds positions P0 + 128 ch ..) and
+        their RoPE tables over rope_dims dims; returns the descriptor stride."""
+        nch = rows // 128
+        recs = np.zeros(nch, dtype=N.STEP_DESC_DTYPE)
+        for ch in range(nch):
+            L = min(128, n - 128 * ch)
+            r = recs[ch]
+            r["past_length"] = P0 + 128 * ch
+            r["num_nodes"] = L
+            r["bonus_token"] = -1
+            r["positions"][:L] = np.arange(P0 + 128 * ch, P0 + 128 * ch + L)
+            r["parents"][:] = -1
+            r["parents"][1:L] = np.arange(L - 1)
+            r["ancestors"][:L] = ancestor_bitsets([-1] + list(range(L - 1)))
+        pf["descs"][:nch].copy_(torch.from_numpy(recs.view(np.uint8).reshape(nch, -1)))
+        dstride = pf["descs"].shape[1]
+        for ch in range(nch):
+            N.check(self.lib.dtree_rope_table(pf["descs"].data_ptr() + ch * dstride, 128, rope_dims,
+                                              self.cfg.rope_theta, pf["cos"][128 * ch].data_ptr(),
+                                              pf["sin"][128 * ch].data_ptr(), st), "rope table")
+        return dstride
+
+    def _prefill_logits(self, pf: dict, n: int, st: int) -> torch.Tensor:
+        """fp32 logits [1, 1, V] of a segment's last row (its xg / ss rows hold
+        the final RMSNorm's input)."""
+        c = self.cfg
+        H = c.hidden_size
+        emb, emb_layout, emb_sb = self._embedding()
+        b, r = (n - 1) // 32, (n - 1) % 32
+        if self.logits is None:
+            self.logits = torch.zeros(self.MP, c.vocab_size, dtype=torch.float32, device=self.dev)
+        xo = b * 32 * H
+        N.check(self.lib.dtree_lmhead_argmax(
+            pf["xg"][0].data_ptr() + 2 * xo, pf["xg"][1].data_ptr() + 2 * xo, self.w.layout, H, 32, emb,
+            emb_layout, emb_sb, c.vocab_size, H, pf["ss"][b].data_ptr(), H // 32, c.rms_norm_eps,
+            self.logits.data_ptr(), self.cand.data_ptr(), st), "prefill lm head")
+        return self.logits[r:r + 1].clone()[None]
+
     def launch_lm_head(self, st: int, x=None, ss=True, want_logits=False) -> None:
         c = self.cfg
         logits_ptr = None
@@ -594,8 +642,6 @@ class Qwen3TreeEngine(TreeEngineBase):
                                            self.norm_hidden.data_ptr(), H, st), "rownorm")
 
     # ---- prompt prefill on the long-M GEMM (adapters.py:494-533) ---------------
-    PREFILL_SEGMENT = 1024  # prompt rows per pass through the layer stack (a multiple of 128)
-
     def supports_long_prefill(self) -> bool:
         return self.w.layout == W_TILED and not isinstance(self.w.layers[0].wqkv, Q4Linear)
 
@@ -625,11 +671,6 @@ class Qwen3TreeEngine(TreeEngineBase):
         self._pf = pf
         return pf
 
-    def _long_gemm(self, name, x, k, w, epi, rows, st, **kw):
-        a = self.gemm_args(name, x, k, w, epi, **kw)
-        a.rows_padded = rows
-        N.check(self.lib.dtree_gemm_long(C.byref(a), st), f"long gemm {name}")
-
     def prefill_long(self, cache: PagedKVCache, tokens, want_logits: bool = True):
         """Causal forward over the prompt with the long-M GEMM: per segment of
         up to PREFILL_SEGMENT tokens, embed, then per layer the fused QKV GEMM,
@@ -653,7 +694,6 @@ class Qwen3TreeEngine(TreeEngineBase):
         slot = {li: i for i, li in enumerate(self.layer_ids)}
         hid_parts = []
         seg = self.PREFILL_SEGMENT
-        last_block = None
         for s0 in range(0, len(toks), seg):
             part = toks[s0:s0 + seg]
             n = len(part)
@@ -662,27 +702,11 @@ class Qwen3TreeEngine(TreeEngineBase):
             P0 = cache.offset
             pf["tokens"][:n].copy_(torch.tensor(part, dtype=torch.int32))
             nch = rows // 128
-            recs = np.zeros(nch, dtype=N.STEP_DESC_DTYPE)
-            for ch in range(nch):
-                L = min(128, n - 128 * ch)
-                r = recs[ch]
-                r["past_length"] = P0 + 128 * ch
-                r["num_nodes"] = L
-                r["bonus_token"] = -1
-                r["positions"][:L] = np.arange(P0 + 128 * ch, P0 + 128 * ch + L)
-                r["parents"][:] = -1
-                r["parents"][1:L] = np.arange(L - 1)
-                r["ancestors"][:L] = ancestor_bitsets([-1] + list(range(L - 1)))
-            pf["descs"][:nch].copy_(torch.from_numpy(recs.view(np.uint8).reshape(nch, -1)))
             N.check(self.lib.dtree_embed_tokens(
                 pf["tokens"].data_ptr(), n, emb, emb_layout, emb_sb, c.vocab_size, H,
                 self.w.layers[0].input_norm.data_ptr(), rows, pf["x"].data_ptr(), pf["xg"][0].data_ptr(),
                 pf["xg"][1].data_ptr(), self.w.layout, pf["ss"].data_ptr(), st), "embed tokens")
-            dstride = pf["descs"].shape[1]
-            for ch in range(nch):
-                N.check(self.lib.dtree_rope_table(pf["descs"].data_ptr() + ch * dstride, 128, D, c.rope_theta,
-                                                  pf["cos"][128 * ch].data_ptr(), pf["sin"][128 * ch].data_ptr(), st),
-                        "rope table")
+            dstride = self._prefill_chunks(pf, P0, n, rows, D, st)
             nL = c.num_hidden_layers
             for li in range(nL):
                 lw = self.w.layers[li]
@@ -717,18 +741,7 @@ class Qwen3TreeEngine(TreeEngineBase):
             cache.offset = P0 + n
             if self.layer_ids:
                 hid_parts.append(pf["hidden"][:n].clone())
-            last_block = ((n - 1) // 32, (n - 1) % 32)
-        logits = None
-        if want_logits:
-            b, r = last_block
-            if self.logits is None:
-                self.logits = torch.zeros(self.MP, c.vocab_size, dtype=torch.float32, device=self.dev)
-            xo = b * 32 * H
-            N.check(self.lib.dtree_lmhead_argmax(
-                pf["xg"][0].data_ptr() + 2 * xo, pf["xg"][1].data_ptr() + 2 * xo, self.w.layout, H, 32, emb,
-                emb_layout, emb_sb, c.vocab_size, H, pf["ss"][b].data_ptr(), H // 32, c.rms_norm_eps,
-                self.logits.data_ptr(), self.cand.data_ptr(), st), "prefill lm head")
-            logits = self.logits[r:r + 1].clone()[None]
+        logits = self._prefill_logits(pf, n, st) if want_logits else None
         hidden = torch.cat(hid_parts, 0) if hid_parts else None
         return logits, hidden
 

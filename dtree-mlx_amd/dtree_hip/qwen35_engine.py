@@ -32,7 +32,7 @@ import torch
 from . import _native as N
 from .cache import Qwen35Cache
 from .engine import TreeEngineBase
-from .weights import GdnLayerWeights
+from .weights import W_TILED, GdnLayerWeights, Q4Linear
 
 
 class Qwen35TreeEngine(TreeEngineBase):
@@ -201,3 +201,152 @@ class Qwen35TreeEngine(TreeEngineBase):
         toks = [int(t) for t in tokens]
         for s in range(0, len(toks), chunk):
             self.commit_chain(cache, toks[s:s + chunk])
+
+    # ---- prompt prefill on the long-M GEMM (forward_dflash,
+    # custom_qwen35_model.py:961-1097, via adapters.py:290-307) ---------------------
+    def supports_long_prefill(self) -> bool:
+        return self.w.layout == W_TILED and not isinstance(self.w.layers[0].wgu, Q4Linear)
+
+    def _prefill_buffers(self, rows: int) -> dict:
+        pf = getattr(self, "_pf", None)
+        if pf is not None and pf["rows"] >= rows and pf["nh"] == max(1, len(self.layer_ids)):
+            return pf
+        self._pf = None  # release the smaller set first
+        c, dev = self.cfg, self.dev
+        H, F = c.hidden_size, c.intermediate_size
+        Hv = c.linear_num_value_heads
+        f32, bf16 = torch.float32, torch.bfloat16
+        nh = max(1, len(self.layer_ids))
+        pf = dict(rows=rows, nh=nh,
+                  tokens=torch.zeros(rows, dtype=torch.int32, device=dev),
+                  x=torch.zeros(rows, H, dtype=f32, device=dev),
+                  xg=torch.zeros(2, rows, H, dtype=bf16, device=dev),
+                  ss=torch.zeros(rows // 32, H // 32, 32, dtype=f32, device=dev),
+                  proj=torch.zeros(rows, c.in_proj_dim, dtype=f32, device=dev),
+                  q=torch.zeros(rows, c.key_dim, dtype=f32, device=dev),
+                  k=torch.zeros(rows, c.key_dim, dtype=f32, device=dev),
+                  v=torch.zeros(rows, c.value_dim, dtype=f32, device=dev),
+                  g=torch.zeros(rows, Hv, dtype=f32, device=dev),
+                  beta=torch.zeros(rows, Hv, dtype=f32, device=dev),
+                  y=torch.zeros(rows, c.value_dim, dtype=f32, device=dev),
+                  gout=torch.zeros(2, rows, c.value_dim, dtype=bf16, device=dev),
+                  qkv=torch.zeros(rows, c.attn_qkv_dim, dtype=f32, device=dev),
+                  attn=torch.zeros(2, rows, c.q_dim, dtype=bf16, device=dev),
+                  act=torch.zeros(2, rows, F, dtype=bf16, device=dev),
+                  hidden=torch.zeros(rows, nh * H, dtype=bf16, device=dev),
+                  cos=torch.zeros(rows, c.rope_dims // 2, dtype=f32, device=dev),
+                  sin=torch.zeros(rows, c.rope_dims // 2, dtype=f32, device=dev),
+                  descs=torch.zeros(rows // 128, C.sizeof(N.StepDesc), dtype=torch.uint8, device=dev),
+                  attn_ws=torch.zeros(self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim,
+                                                                               self.max_past, 128),
+                                      dtype=torch.uint8, device=dev))
+        self._pf = pf
+        return pf
+
+    def _chain_gdn_args(self, li: int, cache: Qwen35Cache, pf: dict, rows: int) -> N.GdnArgs:
+        c = self.cfg
+        gi = cache.slot[li]
+        lw: GdnLayerWeights = self.w.layers[li]
+        a = N.GdnArgs()
+        a.desc = None; a.rows_padded = rows
+        a.num_k_heads = c.linear_num_key_heads; a.num_v_heads = c.linear_num_value_heads
+        a.head_k_dim = c.linear_key_head_dim; a.head_v_dim = c.linear_value_head_dim
+        a.conv_keep = c.linear_conv_kernel_dim - 1
+        a.proj = pf["proj"].data_ptr(); a.ld_proj = c.in_proj_dim
+        a.window = cache.windows[gi].data_ptr(); a.conv_w = lw.conv_w.data_ptr()
+        a.A_log = lw.A_log.data_ptr(); a.dt_bias = lw.dt_bias.data_ptr()
+        a.state = cache.states[gi].data_ptr()
+        a.q = pf["q"].data_ptr(); a.k = pf["k"].data_ptr(); a.v = pf["v"].data_ptr()
+        a.g = pf["g"].data_ptr(); a.beta = pf["beta"].data_ptr(); a.y = pf["y"].data_ptr()
+        a.norm_w = lw.gnorm.data_ptr(); a.eps = c.rms_norm_eps
+        a.out = pf["gout"][0].data_ptr(); a.out_lo = pf["gout"][1].data_ptr()
+        a.out_layout = self.w.layout; a.ld_out = c.value_dim
+        return a
+
+    def prefill_long(self, cache: Qwen35Cache, tokens, want_logits: bool = True):
+        """Causal forward over the prompt with the long-M GEMM, committing as it
+        goes (forward_dflash over the prompt): per segment of up to
+        PREFILL_SEGMENT tokens, embed, then per GatedDeltaNet layer the in_proj
+        GEMM, the chain prep + recurrence + gated norm (dtree_gdn_layer_chain:
+        the committed window and state advance over the segment) and out_proj;
+        per attention layer the fused QKV GEMM, gated attention per 128-row
+        chunk (appending its K/V rows) and o_proj; then the MLP. Returns the
+        fp32 logits of the last position ([1, 1, V]) if asked and the verifier
+        hidden rows of every position ([n, n_ids * H] bf16 or None)."""
+        if not self.supports_long_prefill():
+            raise NotImplementedError("the long-M prefill runs tiled bf16 weights")
+        c = self.cfg
+        H, D = c.hidden_size, c.head_dim
+        toks = [int(t) for t in tokens]
+        if not toks:
+            raise ValueError("empty prompt")
+        if any(t < 0 or t >= c.vocab_size for t in toks):
+            raise ValueError("token id outside the vocabulary")
+        if cache.offset + len(toks) > self.max_past:
+            raise ValueError(f"prefill of {len(toks)} tokens beyond max_past {self.max_past}")
+        st = self.stream_handle()
+        emb, emb_layout, emb_sb = self._embedding()
+        slot = {li: i for i, li in enumerate(self.layer_ids)}
+        hid_parts = []
+        seg = self.PREFILL_SEGMENT
+        kv = cache.kv
+        for s0 in range(0, len(toks), seg):
+            part = toks[s0:s0 + seg]
+            n = len(part)
+            rows = 128 * ((n + 127) // 128)
+            pf = self._prefill_buffers(max(rows, seg if len(toks) > seg else rows))
+            P0 = cache.offset
+            pf["tokens"][:n].copy_(torch.tensor(part, dtype=torch.int32))
+            nch = rows // 128
+            N.check(self.lib.dtree_embed_tokens(
+                pf["tokens"].data_ptr(), n, emb, emb_layout, emb_sb, c.vocab_size, H,
+                self.w.layers[0].input_norm.data_ptr(), rows, pf["x"].data_ptr(), pf["xg"][0].data_ptr(),
+                pf["xg"][1].data_ptr(), self.w.layout, pf["ss"].data_ptr(), st), "embed tokens")
+            dstride = self._prefill_chunks(pf, P0, n, rows, c.rope_dims, st)
+            nL = c.num_hidden_layers
+            for li in range(nL):
+                lw = self.w.layers[li]
+                nxt = self.w.layers[li + 1].input_norm if li + 1 < nL else self.w.final_norm
+                if c.is_linear(li):
+                    self._long_gemm("in", pf["xg"], H, lw.w_in, N.EPI_STORE_F32, rows, st, ss_in=pf["ss"],
+                                    out_f32=pf["proj"])
+                    ga = self._chain_gdn_args(li, cache, pf, rows)
+                    N.check(self.lib.dtree_gdn_layer_chain(C.byref(ga), n, st), "gdn chain")
+                    self._long_gemm("out", pf["gout"], c.value_dim, lw.w_out, N.EPI_RESIDUAL, rows, st,
+                                    out_f32=pf["x"], out_bf16=pf["xg"], next_norm=lw.post_norm, ss_out=pf["ss"])
+                else:
+                    ai = cache.slot[li]
+                    self._long_gemm("qkv", pf["xg"], H, lw.wqkv, N.EPI_STORE_F32, rows, st, ss_in=pf["ss"],
+                                    out_f32=pf["qkv"])
+                    for ch in range(nch):
+                        a = N.AttnArgs()
+                        a.qkv = pf["qkv"][128 * ch].data_ptr(); a.ld_qkv = c.attn_qkv_dim
+                        a.q_norm = lw.q_norm.data_ptr(); a.k_norm = lw.k_norm.data_ptr(); a.eps = c.rms_norm_eps
+                        a.rope_cos = pf["cos"][128 * ch].data_ptr(); a.rope_sin = pf["sin"][128 * ch].data_ptr()
+                        a.k_pages = kv.k_ptr(ai); a.v_pages = kv.v_ptr(ai); a.page_table = kv.page_table.data_ptr()
+                        a.desc = pf["descs"].data_ptr() + ch * dstride
+                        a.out = pf["attn"][0, 128 * ch].data_ptr(); a.out_lo = pf["attn"][1, 128 * ch].data_ptr()
+                        a.ld_out = c.q_dim; a.out_layout = self.w.layout
+                        a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads
+                        a.head_dim = D; a.rows_padded = 128; a.scale = D ** -0.5
+                        a.max_past_length = self.max_past; a.write_cache = 1
+                        a.workspace = pf["attn_ws"].data_ptr(); a.workspace_bytes = pf["attn_ws"].numel()
+                        a.rope_dims = c.rope_dims; a.gated = 1
+                        N.check(self.lib.dtree_tree_attention(C.byref(a), st), "prefill attention")
+                    self._long_gemm("o", pf["attn"], c.q_dim, lw.wo, N.EPI_RESIDUAL, rows, st, out_f32=pf["x"],
+                                    out_bf16=pf["xg"], next_norm=lw.post_norm, ss_out=pf["ss"])
+                self._long_gemm("gu", pf["xg"], H, lw.wgu, N.EPI_SWIGLU, rows, st, ss_in=pf["ss"],
+                                out_bf16=pf["act"])
+                hid, ldh = 0, 0
+                if li in slot:
+                    hid = pf["hidden"].data_ptr() + 2 * slot[li] * H
+                    ldh = pf["hidden"].shape[1]
+                self._long_gemm("down", pf["act"], c.intermediate_size, lw.wd, N.EPI_RESIDUAL, rows, st,
+                                out_f32=pf["x"], out_bf16=pf["xg"], next_norm=nxt, ss_out=pf["ss"],
+                                hidden_out=hid, ld_hidden=ldh)
+            cache.offset = P0 + n
+            if self.layer_ids:
+                hid_parts.append(pf["hidden"][:n].clone())
+        logits = self._prefill_logits(pf, n, st) if want_logits else None
+        hidden = torch.cat(hid_parts, 0) if hid_parts else None
+        return logits, hidden

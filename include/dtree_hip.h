@@ -296,7 +296,8 @@ int dtree_rownorm(const float* x, int32_t ldx, int32_t rows_padded, int32_t hidd
  * target's causal forward over the prompt). dtree_gemm_long is the
  * compute-bound GEMM for rows_padded = a multiple of 128 (any length):
  * tiled bf16 activations (split pair optional) and tiled bf16 weights,
- * n a multiple of 128, the four epilogues of dtree_gemm_bf16 with outputs,
+ * n a multiple of 128 (of 64 with DTREE_EPI_STORE_F32: the Qwen3.5 in_proj),
+ * the four epilogues of dtree_gemm_bf16 with outputs,
  * statistics and hidden rows laid out as there (per 32-row block).
  * dtree_embed_tokens is dtree_embed for a device token array of any length
  * (rows n .. rows_padded - 1 zero), without the RoPE table.
@@ -446,6 +447,17 @@ int dtree_gdn_layer_prep(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_recurrence(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_gated_norm(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_commit(const DtreeGdnArgs* args, hipStream_t stream);
+/* One GatedDeltaNet layer over a causal chain of num_tokens prompt tokens that
+ * continue the committed window and state (prompt prefill): conv + SiLU and
+ * the q / k / v / g / beta prep, the recurrence (y per token; the final state
+ * and the last conv_keep conv inputs become the committed state and window),
+ * and the gated RMSNorm into out / out_lo. Replaces GatedDeltaNet.__call__
+ * over the prompt (custom_qwen35_model.py:823-878, reached from
+ * forward_dflash, custom_qwen35_model.py:961-1097, through
+ * Qwen35TargetAdapter.forward_with_hidden_states, adapters.py:290-307).
+ * desc is unused; rows_padded is the row capacity of q, k, v, g, beta, y,
+ * proj and out (num_tokens <= rows_padded). */
+int dtree_gdn_layer_chain(const DtreeGdnArgs* args, int32_t num_tokens, hipStream_t stream);
 
 /* Convert a row-major [n][k] bf16 matrix to DTREE_W_TILED (n % 32 == 0,
  * k % 64 == 0; src and dst must not overlap). */
