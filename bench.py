@@ -469,7 +469,7 @@ MODEL_NAMES = {"qwen3-4b": "Qwen3-4B", "qwen35-4b": "Qwen3.5-4B-shaped hybrid",
                "qwen35-9b": "Qwen3.5-9B-shaped hybrid"}
 
 
-def prefill_bench(eng, P: int, reps: int = 3, hybrid: bool = False) -> dict:
+def prefill_bench(eng, P: int, reps: int = 3, hybrid: bool = False, label: str = "Qwen3-4B bf16") -> dict:
     """Prompt prefill of P random tokens into a fresh cache: the long-M path
     (128 x 128 MFMA tiles, attention per 128-row chunk; for the hybrid the
     GatedDeltaNet layers as a chain recurrence over the prompt) against the
@@ -504,11 +504,11 @@ def prefill_bench(eng, P: int, reps: int = 3, hybrid: bool = False) -> dict:
         params = (nG * (c.in_proj_dim * c.hidden_size + c.hidden_size * c.value_dim)
                   + nA * (c.attn_qkv_dim * c.hidden_size + c.hidden_size * c.q_dim)
                   + c.num_hidden_layers * 3 * c.hidden_size * c.intermediate_size)
-        what = (f"Qwen3.5-4B-shaped hybrid bf16 prompt prefill, {P} tokens (24 GatedDeltaNet layers: chain "
-                "recurrence, committed window and state; 8 attention layers: K/V into the paged cache)")
+        what = (f"{label} prompt prefill, {P} tokens ({nG} GatedDeltaNet layers: chain recurrence, committed "
+                f"window and state; {nA} attention layers: K/V into the paged cache)")
     else:
         params = c.layer_linear_params() * c.num_hidden_layers
-        what = f"Qwen3-4B bf16 prompt prefill, {P} tokens (36 layers, K/V into the paged cache)"
+        what = f"{label} prompt prefill, {P} tokens ({c.num_hidden_layers} layers, K/V into the paged cache)"
     flops = 2.0 * P * params
     return {"workload": what,
             "long_path_ms": round(long_ms, 3), "chain_path_ms": round(chain_ms, 3),
@@ -657,9 +657,10 @@ def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup
     if kernel_reps:
         out["kernels"] = (time_kernels35 if hybrid else time_kernels)(eng, cfg, w, cache, st, P, L, kernel_reps,
                                                                       quant)
-    if (with_decode or with_prefill) and quant == "bf16":
+    if (with_decode and quant == "bf16") or with_prefill:
         t0 = time.time()
-        out["prefill"] = prefill_bench(eng, P, hybrid=hybrid)
+        label = f"{MODEL_NAMES[model]} {'bf16' if quant == 'bf16' else 'q4 group-64'}"
+        out["prefill"] = prefill_bench(eng, P, reps=1 if P > 4096 else 3, hybrid=hybrid, label=label)
         log(f"[bench] prefill {out['prefill']} ({time.time() - t0:.1f}s)")
     if with_decode and not hybrid:
         t0 = time.time()
@@ -823,9 +824,8 @@ def main():
         for key, (m, q, pp, bb) in {"qwen3_4b_q4_p1024": ("qwen3-4b", "q4", 1024, 24),
                                     "qwen35_4b_bf16_p2048": ("qwen35-4b", "bf16", 2048, 24),
                                     "qwen35_9b_q4_p8192_budget64": ("qwen35-9b", "q4", 8192, 64)}.items():
-            rr = run_workload(m, q, pp, bb, steps=30, warmup=5, with_prefill=m == "qwen35-4b")
-            if "prefill" in rr:
-                configs["prefill_qwen35_4b_p2048"] = rr["prefill"]
+            rr = run_workload(m, q, pp, bb, steps=30, warmup=5, with_prefill=True)
+            configs["prefill_" + key.replace("_budget64", "")] = rr["prefill"]
             configs[key] = {"workload": f"{MODEL_NAMES[m]} {'bf16' if q == 'bf16' else 'q4 group-64'} tree-verify "
                                         f"step, prefix {pp}, {rr['L']}-node tree",
                             "ms_per_step": round(rr["ms"], 4), "steps_per_s": round(rr["steps_per_s"], 3),

@@ -1584,10 +1584,16 @@ static void launch_dp_any(const GemmParams& p, int epi, bool q4, hipStream_t st)
 // the skinny GEMMs, applied to 128 rows.
 constexpr int kLongRows = 128, kLongCols = 128;
 
-template <bool LO, int EPI>
-__global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
-  constexpr int NPL = LO ? 2 : 1, ABLK = 4 * NPL, NBLK = ABLK + 4;
-  constexpr int STAGE = NBLK * 4096;                                    // bytes per stage
+// Q4: group-64 q4 weights (DTREE_W_Q4G64). A K block is one quantisation
+// group: per 32-column block 1 KB of nibbles and 32 (scale, bias) words are
+// staged; each wave's 32 x 32 tiles take a fresh MFMA sum of x (128 + q) per
+// group and fold it in as acc += s * sum + (b - 128 s) * sum(x), with sum(x)
+// per row block from an MFMA of the staged activations against bf16 ones.
+template <bool LO, int EPI, bool Q4>
+__device__ __forceinline__ void long_gemm_body(const GemmParams& p) {
+  constexpr int NPL = LO ? 2 : 1, ABLK = 4 * NPL;
+  constexpr int WBYTES = Q4 ? 4 * 1024 + 4 * 128 : 4 * 4096;            // weight bytes per stage
+  constexpr int STAGE = ABLK * 4096 + WBYTES;                           // bytes per stage
   constexpr int SMEM = 2 * STAGE > kLongRows * kLongCols * 4 ? 2 * STAGE : kLongRows * kLongCols * 4;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
   __shared__ float rs[kLongRows];
@@ -1607,7 +1613,12 @@ __global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
     }
     rs[t] = r;
   }
-  u32x4_t ld[NBLK];
+  // Staged per thread: ABLK activation pieces, then the weight pieces (bf16:
+  // 4 x 16 bytes; q4: 16 bytes of nibbles, and for t < 32 16 bytes of
+  // scale / bias words).
+  constexpr int NW = Q4 ? 2 : 4;
+  u32x4_t ld[ABLK + NW];
+  const uint32_t* wsb = reinterpret_cast<const uint32_t*>(p.w_sb);
   auto load_stage = [&](int kb) {
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
@@ -1615,14 +1626,35 @@ __global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
       ld[rb * NPL] = ld_u32x4(p.x + blk);
       if (LO) ld[rb * NPL + NPL - 1] = ld_u32x4(p.x_lo + blk);
     }
+    if constexpr (Q4) {
+      const int cb = nt * 4 + (t >> 6);  // this thread's 32-column block
+      ld[ABLK] = cb * 32 < p.n ? ld_u32x4(reinterpret_cast<const uint32_t*>(p.w) + ((size_t)cb * nkb + kb) * 256 +
+                                          4 * (t & 63))
+                               : u32x4_t{0u, 0u, 0u, 0u};
+      if (t < 32) {
+        const int sbb = nt * 4 + (t >> 3);
+        ld[ABLK + 1] = sbb * 32 < p.n ? ld_u32x4(wsb + ((size_t)sbb * nkb + kb) * 32 + 4 * (t & 7))
+                                      : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    } else {
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-      ld[ABLK + cb] = (nt * 4 + cb) * 32 < p.n ? ld_u32x4(p.w + ((size_t)(nt * 4 + cb) * nkb + kb) * 2048 + 8 * t)
-                                               : u32x4_t{0u, 0u, 0u, 0u};
+      for (int cb = 0; cb < 4; ++cb)
+        ld[ABLK + cb] = (nt * 4 + cb) * 32 < p.n ? ld_u32x4(p.w + ((size_t)(nt * 4 + cb) * nkb + kb) * 2048 + 8 * t)
+                                                 : u32x4_t{0u, 0u, 0u, 0u};
+    }
   };
   auto store_stage = [&](int s) {
+    unsigned char* st = smem + s * STAGE;
 #pragma unroll
-    for (int b = 0; b < NBLK; ++b) *reinterpret_cast<u32x4_t*>(smem + s * STAGE + b * 4096 + 16 * t) = ld[b];
+    for (int b = 0; b < ABLK; ++b) *reinterpret_cast<u32x4_t*>(st + b * 4096 + 16 * t) = ld[b];
+    if constexpr (Q4) {
+      // nibbles [block][lane] 16 bytes each, then (scale, bias) words [block][32]
+      *reinterpret_cast<u32x4_t*>(st + ABLK * 4096 + 16 * t) = ld[ABLK];
+      if (t < 32) *reinterpret_cast<u32x4_t*>(st + ABLK * 4096 + 4096 + 16 * t) = ld[ABLK + 1];
+    } else {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) *reinterpret_cast<u32x4_t*>(st + (ABLK + b) * 4096 + 16 * t) = ld[ABLK + b];
+    }
   };
   f32x16_t acc[2][2];
 #pragma unroll
@@ -1638,21 +1670,65 @@ __global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
     const int s = kb & 1;
     if (kb + 1 < nkb) load_stage(kb + 1);
     const unsigned char* st = smem + s * STAGE;
+    if constexpr (Q4) {
+      const u32x4_t ones = u32x4_t{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+      u32x4_t wq[2];
+      float sc[2], cf[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int fo = (64 * i + lane) * 16;
-      u32x4_t b[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(st + (ABLK + 2 * wc + j) * 4096 + fo);
+      for (int j = 0; j < 2; ++j) {
+        const int cb = 2 * wc + j;
+        wq[j] = *reinterpret_cast<const u32x4_t*>(st + ABLK * 4096 + cb * 1024 + 16 * lane);
+        const uint32_t sbw = *reinterpret_cast<const uint32_t*>(st + ABLK * 4096 + 4096 + (cb * 32 + c) * 4);
+        sc[j] = __uint_as_float(sbw << 16);
+        cf[j] = __uint_as_float(sbw & 0xffff0000u) - 128.f * sc[j];
+      }
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        const u32x4_t ah = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL) * 4096 + fo);
+        u32x4_t xa[4][NPL];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32(ah, b[j], acc[rb][j]);
-        if (LO) {
-          const u32x4_t al = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL + 1) * 4096 + fo);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32(al, b[j], acc[rb][j]);
+          for (int pl = 0; pl < NPL; ++pl)
+            xa[i][pl] = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL + pl) * 4096 + (64 * i + lane) * 16);
+        f32x16_t xs;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xs[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int pl = 0; pl < NPL; ++pl) xs = mfma32(xa[i][pl], ones, xs);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          f32x16_t au;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) au[r] = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const u32x4_t bq = q4_pairs(wq[j][i]);
+#pragma unroll
+            for (int pl = 0; pl < NPL; ++pl) au = mfma32(xa[i][pl], bq, au);
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[rb][j][r] += sc[j] * au[r] + cf[j] * xs[r];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int fo = (64 * i + lane) * 16;
+        u32x4_t b[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(st + (ABLK + 2 * wc + j) * 4096 + fo);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          const u32x4_t ah = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL) * 4096 + fo);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32(ah, b[j], acc[rb][j]);
+          if (LO) {
+            const u32x4_t al = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL + 1) * 4096 + fo);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32(al, b[j], acc[rb][j]);
+          }
         }
       }
     }
@@ -1679,8 +1755,27 @@ __global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
   tile_epilogue<kLongRows, kLongCols, EPI>(q, red, rs, nt);
 }
 
+template <bool LO, int EPI>
+__global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
+  long_gemm_body<LO, EPI, false>(p);
+}
+
+template <bool LO, int EPI>
+__global__ __launch_bounds__(kThreads) void longq_gemm_kernel(GemmParams p) {
+  long_gemm_body<LO, EPI, true>(p);
+}
+
 template <bool LO>
-static void launch_long(const GemmParams& p, int epi, int grid, hipStream_t st) {
+static void launch_long(const GemmParams& p, int epi, int grid, bool q4, hipStream_t st) {
+  if (q4) {
+    switch (epi) {
+      case DTREE_EPI_STORE_F32: longq_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_RESIDUAL: longq_gemm_kernel<LO, DTREE_EPI_RESIDUAL><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_SWIGLU: longq_gemm_kernel<LO, DTREE_EPI_SWIGLU><<<grid, kThreads, 0, st>>>(p); break;
+      default: longq_gemm_kernel<LO, DTREE_EPI_STORE_BF16><<<grid, kThreads, 0, st>>>(p); break;
+    }
+    return;
+  }
   switch (epi) {
     case DTREE_EPI_STORE_F32: long_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<grid, kThreads, 0, st>>>(p); break;
     case DTREE_EPI_RESIDUAL: long_gemm_kernel<LO, DTREE_EPI_RESIDUAL><<<grid, kThreads, 0, st>>>(p); break;
@@ -1923,8 +2018,11 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
 extern "C" int dtree_gemm_long(const DtreeGemmArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a, "gemm_long: null args");
   DTREE_REQUIRE(a->x && a->w, "gemm_long: null x or w");
-  DTREE_REQUIRE(a->x_layout == DTREE_W_TILED && a->w_layout == DTREE_W_TILED,
-                "gemm_long: tiled bf16 activations and weights");
+  const bool q4 = a->w_layout == DTREE_W_Q4G64;
+  DTREE_REQUIRE(a->x_layout == DTREE_W_TILED && (a->w_layout == DTREE_W_TILED || q4),
+                "gemm_long: tiled bf16 activations, tiled bf16 or q4 group-64 weights");
+  DTREE_REQUIRE(!q4 || (a->w_scales && ((uintptr_t)a->w_scales & 15) == 0),
+                "gemm_long: q4 weights need w_scales (16-byte aligned)");
   DTREE_REQUIRE(a->rows_padded >= kLongRows && a->rows_padded % kLongRows == 0 && a->rows_padded <= (1 << 20),
                 "gemm_long: rows_padded must be a positive multiple of 128");
   const int epi = a->epilogue;
@@ -1961,8 +2059,9 @@ extern "C" int dtree_gemm_long(const DtreeGemmArgs* a, hipStream_t stream) {
   p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
   const long long grid = (long long)(a->rows_padded / kLongRows) * ((a->n + kLongCols - 1) / kLongCols);
   DTREE_REQUIRE(grid < (1LL << 31), "gemm_long: grid too large");
-  if (a->x_lo) launch_long<true>(p, epi, (int)grid, stream);
-  else launch_long<false>(p, epi, (int)grid, stream);
+  p.w_sb = a->w_scales;
+  if (a->x_lo) launch_long<true>(p, epi, (int)grid, q4, stream);
+  else launch_long<false>(p, epi, (int)grid, q4, stream);
   DTREE_LAUNCH_CHECK("gemm_long launch");
   return DTREE_OK;
 }

@@ -643,7 +643,7 @@ class Qwen3TreeEngine(TreeEngineBase):
 
     # ---- prompt prefill on the long-M GEMM (adapters.py:494-533) ---------------
     def supports_long_prefill(self) -> bool:
-        return self.w.layout == W_TILED and not isinstance(self.w.layers[0].wqkv, Q4Linear)
+        return self.w.layout == W_TILED  # bf16 or q4 group-64 weights
 
     def _prefill_buffers(self, rows: int) -> dict:
         pf = getattr(self, "_pf", None)
@@ -679,7 +679,7 @@ class Qwen3TreeEngine(TreeEngineBase):
         fp32 logits of the last position ([1, 1, V]) if asked and the
         verifier hidden rows of every position ([n, n_ids * H] bf16 or None)."""
         if not self.supports_long_prefill():
-            raise NotImplementedError("the long-M prefill runs tiled bf16 weights")
+            raise NotImplementedError("the long-M prefill runs tiled weights")
         c = self.cfg
         H, D = c.hidden_size, c.head_dim
         toks = [int(t) for t in tokens]

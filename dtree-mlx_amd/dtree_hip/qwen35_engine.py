@@ -32,7 +32,7 @@ import torch
 from . import _native as N
 from .cache import Qwen35Cache
 from .engine import TreeEngineBase
-from .weights import W_TILED, GdnLayerWeights, Q4Linear
+from .weights import W_TILED, GdnLayerWeights
 
 
 class Qwen35TreeEngine(TreeEngineBase):
@@ -205,7 +205,7 @@ class Qwen35TreeEngine(TreeEngineBase):
     # ---- prompt prefill on the long-M GEMM (forward_dflash,
     # custom_qwen35_model.py:961-1097, via adapters.py:290-307) ---------------------
     def supports_long_prefill(self) -> bool:
-        return self.w.layout == W_TILED and not isinstance(self.w.layers[0].wgu, Q4Linear)
+        return self.w.layout == W_TILED  # bf16 or q4 group-64 weights
 
     def _prefill_buffers(self, rows: int) -> dict:
         pf = getattr(self, "_pf", None)
@@ -274,7 +274,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         fp32 logits of the last position ([1, 1, V]) if asked and the verifier
         hidden rows of every position ([n, n_ids * H] bf16 or None)."""
         if not self.supports_long_prefill():
-            raise NotImplementedError("the long-M prefill runs tiled bf16 weights")
+            raise NotImplementedError("the long-M prefill runs tiled weights")
         c = self.cfg
         H, D = c.hidden_size, c.head_dim
         toks = [int(t) for t in tokens]

@@ -295,7 +295,8 @@ int dtree_rownorm(const float* x, int32_t ldx, int32_t rows_padded, int32_t hidd
  * Prompt prefill (forward_with_hidden_states, adapters.py:494-533: the
  * target's causal forward over the prompt). dtree_gemm_long is the
  * compute-bound GEMM for rows_padded = a multiple of 128 (any length):
- * tiled bf16 activations (split pair optional) and tiled bf16 weights,
+ * tiled bf16 activations (split pair optional) and tiled bf16 or q4
+ * group-64 weights (DTREE_W_Q4G64 with w_scales 16-byte aligned),
  * n a multiple of 128 (of 64 with DTREE_EPI_STORE_F32: the Qwen3.5 in_proj),
  * the four epilogues of dtree_gemm_bf16 with outputs,
  * statistics and hidden rows laid out as there (per 32-row block).

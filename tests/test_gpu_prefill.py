@@ -3,13 +3,14 @@
 * dtree_gemm_long (128 x 128 MFMA tiles over any multiple of 128 rows) in
   every epilogue, with and without the low activation plane, tiled and
   row-major outputs, against a float64 product (2e-4 of the output scale,
-  as the skinny GEMMs).
+  as the skinny GEMMs); with q4 group-64 weights against the float64 q4
+  product (the fp32 store, a 64-column last tile, residual and SwiGLU).
 * Qwen3TreeEngine.prefill_long on the tiny model against the oracle's causal
   forward: every cached K / V row of every layer, the verifier hidden rows
   and the last position's logits within the 2e-2 bar; one segment with a
   ragged last 128-row chunk, several segments, and a prompt that continues
-  a prefix the chain path wrote; the adapter's forward_with_hidden_states
-  taking the long path.
+  a prefix the chain path wrote; q4 group-64 weights; the adapter's
+  forward_with_hidden_states taking the long path.
 """
 import ctypes as C
 
@@ -17,13 +18,14 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import q4 as o4
 from oracle import qwen3 as oq
 
 from dtree_hip import _native as N
 from dtree_hip import Qwen3TreeModel, Qwen3Weights, tiny_qwen3
 from dtree_hip.adapters import load_target_model
 from dtree_hip.synthetic import random_prefix
-from dtree_hip.weights import interleave_gate_up, tile_weight
+from dtree_hip.weights import interleave_gate_up, q4_to_tiled, tile_weight
 
 pytestmark = pytest.mark.gpu
 
@@ -117,6 +119,82 @@ def test_gemm_long_matches_float64(gpu_device, rows, L, epi, lo, out_tiled):
     assert np.all(got[L:] == 0) if epi != "residual" else True
 
 
+def _q4_torch(wq, s, b):
+    return (torch.from_numpy(np.ascontiguousarray(wq).view(np.int32)),
+            torch.from_numpy(np.ascontiguousarray(s).view(np.int16)).view(torch.bfloat16),
+            torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16))
+
+
+@pytest.mark.parametrize("rows,L", [(128, 100), (256, 200)])
+@pytest.mark.parametrize("epi", ["f32", "f32_tail", "residual", "swiglu"])
+@pytest.mark.parametrize("lo", [False, True])
+def test_gemm_long_q4_matches_float64(gpu_device, rows, L, epi, lo):
+    """dtree_gemm_long with q4 group-64 weights (the nibble trick and the
+    per-group scale / bias fix-up on 128 x 128 tiles) against the float64 q4
+    product; f32_tail: n % 128 == 64."""
+    g = np.random.default_rng(rows + L + 5 * lo + len(epi))
+    dev = gpu_device
+    k = 384
+    n = {"f32": 512, "f32_tail": 320, "residual": 512, "swiglu": 768}[epi]
+    xf = np.zeros((rows, k), np.float32)
+    xf[:L] = g.standard_normal((L, k))
+    hi = torch.from_numpy(xf).to(torch.bfloat16)
+    lo_t = (torch.from_numpy(xf) - hi.float()).to(torch.bfloat16)
+    xin = _bf(hi) + (_bf(lo_t) if lo else 0.0)
+    if epi == "swiglu":
+        F = n // 2
+        gq, gs, gb = o4.random_q4(F, k, g)
+        uq, us, ub = o4.random_q4(F, k, g)
+        wq2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int32)) for t in (gq, uq)])
+        s2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int16)) for t in (gs, us)])
+        b2 = interleave_gate_up(*[torch.from_numpy(np.ascontiguousarray(t).view(np.int16)) for t in (gb, ub)])
+        wt, sb = q4_to_tiled(wq2, s2.view(torch.bfloat16), b2.view(torch.bfloat16))
+        gate = o4.q4_matmul(xin, gq, oq.bf16_to_f32(gs), oq.bf16_to_f32(gb))
+        up = o4.q4_matmul(xin, uq, oq.bf16_to_f32(us), oq.bf16_to_f32(ub))
+    else:
+        wq, ws, wb = o4.random_q4(n, k, g)
+        wt, sb = q4_to_tiled(*_q4_torch(wq, ws, wb))
+        y = o4.q4_matmul(xin, wq, oq.bf16_to_f32(ws), oq.bf16_to_f32(wb))
+    wt, sb = wt.to(dev), sb.to(dev)
+    a = N.GemmArgs()
+    xt, xlt = tile_weight(hi.to(dev)), tile_weight(lo_t.to(dev))
+    a.x = xt.data_ptr(); a.x_lo = xlt.data_ptr() if lo else None
+    a.x_layout = N.W_TILED; a.ldx = k; a.rows_padded = rows
+    a.w = wt.data_ptr(); a.w_scales = sb.data_ptr(); a.w_layout = N.W_Q4G64; a.n = n; a.k = k
+    a.out_layout = N.W_ROWMAJOR
+    width = n // 2 if epi == "swiglu" else n
+    out_f32 = torch.zeros(rows, n, device=dev)
+    out_bf = torch.zeros(2, rows, width, dtype=torch.bfloat16, device=dev)
+    a.out_f32 = out_f32.data_ptr(); a.ld_out_f32 = n
+    a.out_bf16 = out_bf[0].data_ptr(); a.out_lo = out_bf[1].data_ptr(); a.ld_out_bf16 = width
+    rs = np.ones(rows)
+    if epi != "residual":
+        ss = torch.from_numpy(np.abs(g.standard_normal((rows // 32, k // 32, 32))).astype(np.float32) + 0.5).to(dev)
+        a.ss_in = ss.data_ptr(); a.ss_tiles = k // 32; a.norm_dim = k; a.eps = 1e-6
+        rs = 1.0 / np.sqrt(ss.cpu().numpy().transpose(0, 2, 1).reshape(rows, k // 32).sum(1) / k + 1e-6)
+    res0 = np.zeros((rows, n), np.float32)
+    gn = torch.ones(n, dtype=torch.bfloat16, device=dev)
+    ss_out = torch.zeros(rows // 32, n // 32, 32, device=dev)
+    if epi == "residual":
+        res0[:L] = g.standard_normal((L, n))
+        out_f32.copy_(torch.from_numpy(res0))
+        a.next_norm = gn.data_ptr(); a.ss_out = ss_out.data_ptr()
+    a.epilogue = {"f32": N.EPI_STORE_F32, "f32_tail": N.EPI_STORE_F32, "residual": N.EPI_RESIDUAL,
+                  "swiglu": N.EPI_SWIGLU}[epi]
+    print(f"q4 long gemm rows={rows} n={n} k={k} epi={epi} lo={lo}", flush=True)
+    N.check(N.lib().dtree_gemm_long(C.byref(a), _stream()), "gemm_long q4")
+    torch.cuda.synchronize()
+    if epi == "swiglu":
+        gt, upv = gate * rs[:, None], up * rs[:, None]
+        ref = gt / (1 + np.exp(-np.clip(gt, -80, 80))) * upv
+        got = _bf(out_bf[0]) + _bf(out_bf[1])
+    elif epi == "residual":
+        ref, got = res0.astype(np.float64) + y, out_f32.cpu().numpy()
+    else:
+        ref, got = y * rs[:, None], out_f32.cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-4 * max(1.0, np.abs(ref).max())
+
+
 def _oracle(cfg, w):
     ocfg = oq.Qwen3Config(hidden=cfg.hidden_size, layers=cfg.num_hidden_layers, ffn=cfg.intermediate_size,
                           heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
@@ -168,6 +246,30 @@ def test_prefill_long_matches_oracle(gpu_device, attn_kernel, T, segment, head):
         _check_rows(cache.logical_keys(li, T).float().cpu().numpy(), ks[li], f"keys layer {li}")
         _check_rows(cache.logical_values(li, T).float().cpu().numpy(), vs[li], f"values layer {li}")
     _check_rows(hidden.float().cpu().numpy(), hid[head:], "verifier hidden")
+    lg = logits[0, 0].cpu().numpy()
+    assert np.abs(lg - last_logits).max() <= TOL * np.abs(last_logits).max()
+
+
+def test_prefill_long_q4_matches_oracle(gpu_device):
+    """The long-M prefill with q4 group-64 weights (every linear layer and the
+    tied embedding) against the oracle on the dequantised weights."""
+    cfg = tiny_qwen3()
+    w = Qwen3Weights.random_q4(cfg, seed=0, device=gpu_device, norm_jitter=0.1)
+    layer_ids = [0, 1]
+    eng = Qwen3TreeModel(cfg, w, max_past=364, layer_ids=layer_ids).engine
+    eng.PREFILL_SEGMENT = 256
+    T = 300
+    toks = random_prefix(T, cfg.vocab_size, seed=T)
+    cache = eng.new_cache()
+    logits, hidden = eng.prefill_long(cache, toks)
+    torch.cuda.synchronize()
+    assert cache.offset == T
+    orc = _oracle(cfg, w)
+    ks, vs, hid, last_logits = _oracle_causal(orc, cfg, toks, layer_ids)
+    for li in range(cfg.num_hidden_layers):
+        _check_rows(cache.logical_keys(li, T).float().cpu().numpy(), ks[li], f"keys layer {li}")
+        _check_rows(cache.logical_values(li, T).float().cpu().numpy(), vs[li], f"values layer {li}")
+    _check_rows(hidden.float().cpu().numpy(), hid, "verifier hidden")
     lg = logits[0, 0].cpu().numpy()
     assert np.abs(lg - last_logits).max() <= TOL * np.abs(last_logits).max()
 

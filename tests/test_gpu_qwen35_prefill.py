@@ -14,8 +14,8 @@ the oracle.
   causal forward + commit: every GatedDeltaNet layer's committed window and
   state, every attention layer's cached K/V rows, the verifier hidden rows
   and the last position's logits (2e-2 bar); one segment, several segments,
-  a prompt continuing a prefix the chain path wrote, and the adapter taking
-  the long path.
+  a prompt continuing a prefix the chain path wrote, q4 group-64 weights,
+  and the adapter taking the long path.
 """
 import ctypes as C
 
@@ -195,6 +195,28 @@ def test_qwen35_prefill_long_matches_oracle(gpu_device, attn_kernel, T, segment,
     _, oc, vh, last_logits = _oracle_prefill(cfg, w, toks, layer_ids)
     _check_cache(cfg, cache, oc, T)
     _close(bf16_f32(hidden), vh[head:], "verifier hidden")
+    lg = logits[0, 0].cpu().numpy()
+    assert np.abs(lg - last_logits).max() <= TOL * np.abs(last_logits).max()
+
+
+def test_qwen35_prefill_long_q4_matches_oracle(gpu_device):
+    """The hybrid's long-M prefill with q4 group-64 weights (every linear
+    layer and the tied embedding) against the oracle on the dequantised
+    weights."""
+    cfg = tiny_qwen35()
+    w = Qwen35Weights.random(cfg, seed=0, device=gpu_device, norm_jitter=0.1, quant="q4")
+    layer_ids = [1, 3]
+    eng = Qwen35TreeEngine(cfg, w, max_past=364, layer_ids=layer_ids, max_nodes=25)
+    eng.PREFILL_SEGMENT = 256
+    T = 300
+    toks = random_prefix(T, cfg.vocab_size, seed=T)
+    cache = eng.new_cache()
+    logits, hidden = eng.prefill_long(cache, toks)
+    torch.cuda.synchronize()
+    assert cache.offset == T
+    _, oc, vh, last_logits = _oracle_prefill(cfg, w, toks, layer_ids)
+    _check_cache(cfg, cache, oc, T)
+    _close(bf16_f32(hidden), vh, "verifier hidden")
     lg = logits[0, 0].cpu().numpy()
     assert np.abs(lg - last_logits).max() <= TOL * np.abs(last_logits).max()
 
