@@ -317,15 +317,31 @@ struct TreeStage {
         vt[d * VS + nl] = (uint16_t)(bf2_to_h2(vb[i]) & 0xffffu);
       }
       if (write && live) {
+        // Buffer stores over the layer's cache pages: per lane one row offset
+        // plus the j-dependent part of the dim (dim = A(i) + B(i) j, B 4 / 8
+        // or 24), the constant A(i) part in the scalar offset, so no per-dim
+        // 64-bit address is held across the chunk loop. K dims come in runs of
+        // four consecutive dims (8-byte stores); V^T is one 2-byte store per
+        // dim (stride DTREE_PAGE).
         const int pos = P + node;
         const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
-        uint16_t* krow = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off) * D;
-        uint16_t* vcol = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off;
+        const int slot = page * p.Hkv + g;
+        // (one resource for the whole layer cache, uniform across the lanes;
+        // a layer's pages stay below 2 GiB)
+        const __amdgpu_buffer_rsrc_t kr = buf_rsrc(p.kp, 0x7ffffff0u);
+        const __amdgpu_buffer_rsrc_t vr = buf_rsrc(p.vp, 0x7ffffff0u);
+        const int kbase = (slot * DTREE_PAGE + off) * D * 2, vbase = (slot * D * DTREE_PAGE + off) * 2;
+#pragma unroll
+        for (int i = 0; i < NV; i += 4) {
+          const int a = row8_dim<D>(0, i), b = row8_dim<D>(1, i) - a;  // dim = a + b j
+          const u32x2_t w = {(uint32_t)kb[i] | ((uint32_t)kb[i + 1] << 16),
+                             (uint32_t)kb[i + 2] | ((uint32_t)kb[i + 3] << 16)};
+          __builtin_amdgcn_raw_buffer_store_b64(w, kr, kbase + 2 * b * j, 2 * a, 0);
+        }
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-          const int d = row8_dim<D>(j, i);
-          krow[d] = kb[i];
-          vcol[(size_t)d * DTREE_PAGE] = vb[i];
+          const int a = row8_dim<D>(0, i), b = row8_dim<D>(1, i) - a;
+          __builtin_amdgcn_raw_buffer_store_b16(vb[i], vr, vbase + 2 * DTREE_PAGE * b * j, 2 * DTREE_PAGE * a, 0);
         }
       }
     }
@@ -393,8 +409,22 @@ struct PrefixStage {
 // l, output rescaled when the max grows), O^T += V^T P^T. TREE: key k of
 // block 0 is tree node 32 tc + k, visible when bit k of the query's ancestor
 // word is set; else prefix keys >= kend are masked.
-template <int D, int NBK, int KS, int VS, bool TREE>
-__device__ __forceinline__ void attend_chunk(const uint16_t* ks, const uint16_t* vt, const u32x4_t (&qf)[D / 16],
+// The query fragments come from QF: q(j) returns fragment j, from registers
+// (QRegs) or, at head_dim 256 where registers run out, from the wave's copy in
+// LDS (QLds, read one dims-step ahead like the K fragments).
+template <int D>
+struct QRegs {
+  const u32x4_t (&qf)[D / 16];
+  __device__ __forceinline__ u32x4_t operator()(int j) const { return qf[j]; }
+};
+struct QLds {
+  const u32x4_t* q;  // this wave's fragments: [j][lane]
+  int lane;
+  __device__ __forceinline__ u32x4_t operator()(int j) const { return q[j * 64 + lane]; }
+};
+
+template <int D, int NBK, int KS, int VS, bool TREE, typename QF>
+__device__ __forceinline__ void attend_chunk(const uint16_t* ks, const uint16_t* vt, const QF& qf,
                                              float scale_log2, int kend, uint32_t anc,
                                              bool qlive, int c, int h, float& m_run, float& l_run,
                                              f32x16_t (&o)[D / 32]) {
@@ -405,20 +435,22 @@ __device__ __forceinline__ void attend_chunk(const uint16_t* ks, const uint16_t*
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
   const int krow = swap_bits23(c);
-  // K fragments are read one dims-step ahead of their MFMAs (not all at once:
-  // registers for two waves per SIMD).
-  u32x4_t a[2][NBK];
+  // K (and q) fragments are read one dims-step ahead of their MFMAs (not all
+  // at once: registers for two waves per SIMD).
+  u32x4_t a[2][NBK], qn[2];
 #pragma unroll
   for (int b = 0; b < NBK; ++b) a[0][b] = *reinterpret_cast<const u32x4_t*>(ks + (32 * b + krow) * KS + 8 * h);
+  qn[0] = qf(0);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     if (j + 1 < NJ) {
 #pragma unroll
       for (int b = 0; b < NBK; ++b)
         a[(j + 1) & 1][b] = *reinterpret_cast<const u32x4_t*>(ks + (32 * b + krow) * KS + 16 * (j + 1) + 8 * h);
+      qn[(j + 1) & 1] = qf(j + 1);
     }
 #pragma unroll
-    for (int b = 0; b < NBK; ++b) s[b] = mfma32_f16(a[j & 1][b], qf[j], s[b]);
+    for (int b = 0; b < NBK; ++b) s[b] = mfma32_f16(a[j & 1][b], qn[j & 1], s[b]);
     __builtin_amdgcn_sched_barrier(0);
   }
   float bmax = kNeg;
@@ -520,6 +552,14 @@ __global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
   __shared__ __align__(16) unsigned char lds[kLdsKV];
   __shared__ __align__(16) unsigned char lds_aux[QAux<D, R, TPS>::kBytes];
   __shared__ int s_flag;
+  // head_dim 256, split 0: each wave's query fragments live in LDS
+  // ([wave][j][lane], 16 KB per wave) instead of 64 registers, which the tree
+  // chunk loop (which also appends the tree K/V to the cache) otherwise
+  // spills, reloading addresses from scratch on every chunk. The prefix
+  // splits keep them in registers (their loop has room, and 16 more LDS reads
+  // per chunk would cost more there).
+  constexpr bool QL = D == 256;
+  __shared__ __align__(16) u32x4_t q_lds[QL ? W * NJ * 64 : 1];
 
   const int pairs = p.Hkv * p.NT;
   const int pair = blockIdx.x % pairs, s = blockIdx.x / pairs;
@@ -542,11 +582,19 @@ __global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
   QAux<D, R, TPS> qa;
   qa.issue(p, rb, ts);
   // RoPE rows and q_norm weight into LDS, then this wave's q fragments
-  auto build_q = [&]() {
+  auto build_q = [&](bool to_lds) {
     qa.commit(lds_aux, ts);
     __syncthreads();
     q_fragments<D, R>(qr, lds_aux, p.q_norm != nullptr, p.eps, c, h, qf);
+    if constexpr (QL) {
+      if (to_lds) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) q_lds[(wave * NJ + j) * 64 + lane] = qf[j];
+      }
+    }
   };
+  const QRegs<D> q_regs{qf};
+  const QLds q_mem{q_lds + wave * NJ * 64, lane};
   int P = 0, L = 0, np = 0;
   // The descriptor is read after the chunk loads are issued (its scalar wait
   // must not hold them back).
@@ -585,7 +633,7 @@ __global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
     TreeStage<D, R, TPS> st;
     st.issue(p, 0, g, ts);
     read_desc();
-    build_q();
+    build_q(true);
     if (bail()) return;
 #pragma unroll
     for (int db = 0; db < ND; ++db)
@@ -596,8 +644,12 @@ __global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
       if (it + 1 < n_items) st.issue(p, it + 1, g, ts);
       __syncthreads();
       const uint32_t anc = p.desc->ancestors[qrow][it];
-      attend_chunk<D, 1, KS, VS, true>(buf_k(it), buf_v(it), qf, p.scale_log2, L - 32 * it, anc, qrow < L, c, h,
-                                       m_run, l_run, o);
+      if constexpr (QL)
+        attend_chunk<D, 1, KS, VS, true>(buf_k(it), buf_v(it), q_mem, p.scale_log2, L - 32 * it, anc, qrow < L, c,
+                                         h, m_run, l_run, o);
+      else
+        attend_chunk<D, 1, KS, VS, true>(buf_k(it), buf_v(it), q_regs, p.scale_log2, L - 32 * it, anc, qrow < L, c,
+                                         h, m_run, l_run, o);
     }
   } else {
     // split s >= 1: prefix chunks c0 .. c0 + cps - 1 (cut at the prefix's np)
@@ -606,7 +658,7 @@ __global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
     PrefixStage<D, TPS> st;
     if (any) st.issue(p, c0, PrefixStage<D, TPS>::page_of(p, c0), g, ts);
     read_desc();
-    build_q();
+    build_q(false);
     if (bail()) return;
 #pragma unroll
     for (int db = 0; db < ND; ++db)
@@ -617,7 +669,7 @@ __global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
       st.template commit<KS, VS>(c0 + it, P, ts, buf_k(it), buf_v(it));
       if (it + 1 < n_items) st.issue(p, c0 + it + 1, PrefixStage<D, TPS>::page_of(p, c0 + it + 1), g, ts);
       __syncthreads();
-      attend_chunk<D, NB, KS, VS, false>(buf_k(it), buf_v(it), qf, p.scale_log2, P - (c0 + it) * CK, 0u, true, c,
+      attend_chunk<D, NB, KS, VS, false>(buf_k(it), buf_v(it), q_regs, p.scale_log2, P - (c0 + it) * CK, 0u, true, c,
                                          h, m_run, l_run, o);
     }
   }
