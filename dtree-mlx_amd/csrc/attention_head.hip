@@ -2,11 +2,16 @@
 //
 // Work split: a workgroup serves one 32-row block of tree queries (rows
 // 32*rb .. 32*rb+31) of one query head. The keys are cut into chunks: chunks
-// 0 .. NT-1 are the tree itself in 32-key blocks (NT = rows_padded / 32;
-// ancestor-or-self mask, word tc of each query's bitset), chunks NT.. are runs
-// of CK prefix keys (fully visible): a 64-key page for head_dim 128, half a
-// page for head_dim 256 (same registers per wave). A workgroup has four
-// waves, one chunk each, so workgroup `split` owns chunks 4*split .. 4*split+3.
+// 0 .. npre-1 are runs of CK prefix keys (fully visible): a 64-key page for
+// head_dim 128, half a page for head_dim 256 (same registers per wave);
+// chunks npre .. npre+NT-1 are the tree itself in 32-key blocks (NT =
+// rows_padded / 32; tree chunk tc is masked by word tc of each query's
+// ancestor-or-self bitset). A workgroup has four waves, one chunk each, so
+// workgroup `split` owns chunks 4*split .. 4*split+3. The tree chunks come
+// last: the wave that also normalises, stages and appends the tree rows then
+// shares its workgroup with the fewest prefix chunks (at a 1024-key prefix
+// the tree is the fifth workgroup's only chunk and the other four hold four
+// pages each), so that workgroup is not the last to publish its partial.
 //
 // Two head geometries are compiled: Qwen3 (head_dim 128, full RoPE) and the
 // gated attention of Qwen3.5 (head_dim 256, RoPE on the first 64 dims, q_proj
@@ -682,15 +687,15 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   // it, they delay the descriptor's own (scalar) load by microseconds.
   // (head_dim 256 with four tree chunks loads its q row per wave inside the
   // chunk: there is no LDS left to stage it.)
-  const bool prefix_wave = chunk >= NT && chunk < p.max_chunks;
-  const int page = prefix_wave ? p.page_table[(chunk - NT) * CK / DTREE_PAGE] : 0;
+  const bool prefix_wave = chunk < p.max_chunks - NT;  // a prefix chunk at the longest prefix
+  const int page = prefix_wave ? p.page_table[chunk * CK / DTREE_PAGE] : 0;
   HeadRow<D, R> qr;
   QStage<D> qst;
   if constexpr (QS) q_stage_issue<D>(p, hq, rb, qst);
 
   if (pair >= p.splits * p.Hkv) return;
   const int P = p.desc->past_length, L = p.desc->num_nodes;
-  const int nchunks = NT + (P + CK - 1) / CK;
+  const int npre = (P + CK - 1) / CK, nchunks = NT + npre;
   // A descriptor beyond the grid's capacity (P > max_past_length) or with more
   // rows than rows_padded leaves the output untouched instead of indexing past
   // buffers.
@@ -725,19 +730,20 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
 
-  if (chunk < NT) {
-    // Tree chunks are waves 0 .. NT-1 of split 0, each with its own staging.
-    if (32 * chunk < L) {
-      uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)chunk * kStage);
-      tree_chunk<D, R, QS>(p, qr, qs, hq, g, G, P, L, chunk, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+  const int tc = chunk - npre;  // tree chunk index
+  if (tc >= 0 && tc < NT) {
+    // Tree chunks are the last NT chunks, each with its own staging.
+    if (32 * tc < L) {
+      uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)tc * kStage);
+      tree_chunk<D, R, QS>(p, qr, qs, hq, g, G, P, L, tc, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
     }
-  } else if (chunk < nchunks) {
+  } else if (chunk < npre) {
     if constexpr (!QS)
       row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm,
                             p.rope_cos + qrow * (R / 2), p.rope_sin + qrow * (R / 2), h);
     ChunkKV<D> kv;
-    prefix_issue<D>(p, kv, page, g, chunk - NT, c, h);
-    prefix_chunk<D, R, QS>(p, qr, qs, kv, P, chunk - NT, c, h, m_run, l_run, o);
+    prefix_issue<D>(p, kv, page, g, chunk, c, h);
+    prefix_chunk<D, R, QS>(p, qr, qs, kv, P, chunk, c, h, m_run, l_run, o);
   }
 
   // ---- merge the four waves ----
