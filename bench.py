@@ -340,6 +340,10 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
     g = refs["gdn"]
     us["prep"] = timed(lambda r: lib.dtree_gdn_layer_prep(g[r], st), len(g))
     us["recurrence"] = timed(lambda r: lib.dtree_gdn_layer_recurrence(g[r], st), len(g))
+    # trees of up to 32 nodes run prep and recurrence as one launch in the step
+    fused = eng.MP == 32
+    if fused:
+        us["prep_recurrence"] = timed(lambda r: lib.dtree_gdn_layer_prep_recurrence(g[r], st), len(g))
     us["gated_norm"] = timed(lambda r: lib.dtree_gdn_layer_gated_norm(g[r], st), len(g))
     us["commit"] = timed(lambda r: lib.dtree_gdn_layer_commit(g[r], st), len(g))
     us["attention"] = timed(lambda r: eng._attention(A[r], cache, st), len(A))
@@ -388,6 +392,16 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
                            b["attention"]),
         "lm_head": entry(lmhead_kernel_name(quant, eng.MP), 1, us["lm_head"], b["lm_head"]),
     }
+    if fused:
+        for k in ("gdn_prep", "gdn_recurrence"):
+            out[k]["launches_per_step"] = 0
+            out[k]["note"] = "timed alone; the step runs it inside gdn_prep_recurrence"
+        # the recurrence's bytes (its inputs are now the raw conv / b / a columns,
+        # of the same size), the conv taps and window, and q / k / v / g / beta
+        # written for the commit
+        out["gdn_prep_recurrence"] = entry("gdn_prep_reg_kernel<3>", nG, us["prep_recurrence"],
+                                           b["recurrence"] + (2 * cfg.linear_conv_kernel_dim - 1) * C_ * 4
+                                           + L * (C_ + 2 * Hv) * 4)
     return out
 
 

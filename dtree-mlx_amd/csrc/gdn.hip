@@ -682,6 +682,163 @@ __global__ __launch_bounds__(DK) void gdn_prep_kernel(PrepParams p) {
   }
 }
 
+// Prep and the register-resident recurrence in one launch, for trees of up to
+// 32 nodes with Dk = Dv = 128 (the verify step's 25-node trees): each
+// workgroup of gdn_tree_reg_kernel computes the inputs it reads itself
+// instead of loading them from a prep launch. Its threads load, in one round,
+// the raw conv inputs of its key head's q and k channels and of its 8 value
+// rows for every node, the parents, the conv taps and committed window of
+// their channels, b / a of its value head and its committed state; then run
+// the tree conv + SiLU (the same window and tap order as gdn_prep_kernel), the
+// q / k RMS scaling (a thread holds 4 channels of one node; the 32 lanes of a
+// half-wave hold the node's head) and g / beta into the LDS rows the node loop
+// reads. The 32 workgroups of a key head repeat its q / k conv (256 channels x
+// nodes x taps). k, v, g and beta go out as gdn_prep_kernel writes them, for
+// the commit after the accept walk: k and q once per key head, g and beta once
+// per value head, v by every workgroup for its rows.
+template <int KEEP>
+__global__ __launch_bounds__(256, 2) void gdn_prep_reg_kernel(GdnParams p, PrepParams pp) {
+  constexpr int TMAX = 32, DK = 128, RPW = 8, NI = TMAX / 4;  // nodes per thread (4 waves)
+  __shared__ __align__(16) float qk[TMAX][2][DK];
+  __shared__ __align__(16) float raw[TMAX][2][DK];
+  __shared__ float vraw[TMAX][RPW];
+  __shared__ float vgb[TMAX][RPW + 2];
+  __shared__ int par[TMAX];
+  const int T = p.T_dev ? min(max(*p.T_dev, 0), min(p.T, TMAX)) : min(p.T, TMAX);
+  const int nslices = p.Dv / RPW;
+  const int h = blockIdx.x / nslices, row0 = (blockIdx.x % nslices) * RPW;
+  const int hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x, lane64 = tid & 63, wave = tid >> 6;
+  // q / k staging: thread (wave, lane) holds channels ch .. ch+3 of plane
+  // (0 = q, 1 = k) for nodes wave, wave + 4, ...
+  const int plane = lane64 >> 5, ch = 4 * (lane64 & 31);
+  const int cq = plane * pp.key_dim + hk * DK + ch;  // conv column of those channels
+  // v staging: thread tid < 8 T owns node tid / 8, value row row0 + tid % 8
+  const int vt = tid >> 3, vj = tid & 7;
+  const int cv = 2 * pp.key_dim + h * DK + row0 + vj;
+  const int rl = tid >> 5, lane = tid & 31;
+  const int dv = row0 + rl;
+  f32x4_t base, wk[KEEP + 1], bk[KEEP];
+  float wvk[KEEP + 1], bvk[KEEP];
+  {
+    f32x4_t xr[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int t = wave + 4 * i;
+      if (t < T) xr[i] = *reinterpret_cast<const f32x4_t*>(pp.x + (size_t)t * pp.ldx + cq);
+    }
+    f32x4_t vr;
+    if (tid < 2 * T)
+      vr = *reinterpret_cast<const f32x4_t*>(pp.x + (size_t)(tid >> 1) * pp.ldx + 2 * pp.key_dim + h * DK + row0 +
+                                             4 * (tid & 1));
+    float bb = 0.f, aa = 0.f;
+    if (tid < T) {
+      const float* row = pp.x + (size_t)tid * pp.ldx + pp.ab_col;
+      bb = row[h];
+      aa = row[pp.Hv + h];
+      par[tid] = valid_parent(p.parents[tid], tid);
+    }
+#pragma unroll
+    for (int r = 0; r <= KEEP; ++r) wk[r] = *reinterpret_cast<const f32x4_t*>(pp.w + (size_t)r * pp.C + cq);
+#pragma unroll
+    for (int r = 0; r < KEEP; ++r) bk[r] = *reinterpret_cast<const f32x4_t*>(pp.base + (size_t)r * pp.C + cq);
+#pragma unroll
+    for (int r = 0; r <= KEEP; ++r) wvk[r] = pp.w[(size_t)r * pp.C + cv];
+#pragma unroll
+    for (int r = 0; r < KEEP; ++r) bvk[r] = pp.base[(size_t)r * pp.C + cv];
+    const float alog = pp.A_log[h], dtb = pp.dt_bias[h];
+    base = *reinterpret_cast<const f32x4_t*>(p.state + ((size_t)h * p.Dv + dv) * DK + 4 * lane);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int t = wave + 4 * i;
+      if (t < T) *reinterpret_cast<f32x4_t*>(&raw[t][plane][ch]) = xr[i];
+    }
+    if (tid < 2 * T) *reinterpret_cast<f32x4_t*>(&vraw[tid >> 1][4 * (tid & 1)]) = vr;
+    if (tid < T) {
+      vgb[tid][RPW] = __expf(-__expf(alog) * softplus_f(aa + dtb));
+      vgb[tid][RPW + 1] = 1.0f / (1.0f + __expf(-bb));
+    }
+  }
+  __syncthreads();
+  // q / k: window of node t = the last KEEP + 1 rows of (committed window ++
+  // conv inputs along the root path), newest tap first, as gdn_prep_kernel.
+  const float qks = plane ? pp.k_scale : pp.q_scale;
+#pragma unroll 1
+  for (int i = 0; i < NI; ++i) {
+    const int t = wave + 4 * i;  // wave-uniform
+    if (t >= T) break;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    int anc = t, nb = 0;
+#pragma unroll
+    for (int i2 = 0; i2 <= KEEP; ++i2) {
+      f32x4_t val;
+      if (anc >= 0) {
+        val = *reinterpret_cast<const f32x4_t*>(&raw[anc][plane][ch]);
+        anc = par[anc];
+      } else {
+        // window row KEEP - 1 - min(nb, KEEP - 1), selected over constant
+        // indices (a runtime index would put the rows in scratch memory)
+        const int wr = KEEP - 1 - min(nb, KEEP - 1);
+        val = bk[0];
+#pragma unroll
+        for (int r = 1; r < KEEP; ++r) val = wr == r ? bk[r] : val;
+        ++nb;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += wk[KEEP - i2][e] * val[e];
+    }
+    f32x4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = silu_acc(acc[e]);
+    const float ss = row_sum32(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
+    const float sc = rsqrtf(ss * (1.0f / DK) + 1e-6f) * qks;
+    *reinterpret_cast<f32x4_t*>(&qk[t][plane][ch]) = o * sc;
+  }
+  // v of (node vt, row row0 + vj)
+  if (vt < T) {
+    float acc = 0.f;
+    int anc = vt, nb = 0;
+#pragma unroll
+    for (int i2 = 0; i2 <= KEEP; ++i2) {
+      float val;
+      if (anc >= 0) {
+        val = vraw[anc][vj];
+        anc = par[anc];
+      } else {
+        const int wr = KEEP - 1 - min(nb, KEEP - 1);
+        val = bvk[0];
+#pragma unroll
+        for (int r = 1; r < KEEP; ++r) val = wr == r ? bvk[r] : val;
+        ++nb;
+      }
+      acc += wvk[KEEP - i2] * val;
+    }
+    const float o = silu_acc(acc);
+    vgb[vt][vj] = o;
+    pp.v[(size_t)vt * (pp.C - 2 * pp.key_dim) + (cv - 2 * pp.key_dim)] = o;
+  }
+  __syncthreads();
+  // the commit's inputs (k, v, g, beta) and q, once each
+  if (row0 == 0) {
+    if (tid < T) {
+      pp.g[(size_t)tid * p.Hv + h] = vgb[tid][RPW];
+      pp.beta[(size_t)tid * p.Hv + h] = vgb[tid][RPW + 1];
+    }
+    if (h % (p.Hv / p.Hk) == 0) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int t = wave + 4 * i;
+        if (t >= T) break;
+        float* dst = (plane ? pp.k : pp.q) + (size_t)t * pp.key_dim + hk * DK + ch;
+        *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(&qk[t][plane][ch]);
+      }
+    }
+  }
+  RegTree<TMAX> rt{p, &qk[0][0][0], &vgb[0][0], par, T, h, dv, rl, lane, base};
+  f32x4_t s[TMAX];
+  reg_tree_step<TMAX, 0>(rt, s);
+}
+
 // Gated RMSNorm of the recurrence output per (node, value head)
 // (RMSNormGated, qwen35_tree.py:322): o = rms_norm(y) * w * silu(z), written as
 // the split bf16 pair [hi, lo] the out_proj GEMM reads. 16 threads per
@@ -982,6 +1139,51 @@ extern "C" int dtree_gdn_layer_recurrence(const DtreeGdnArgs* a, hipStream_t str
     gdn_tree_kernel<128><<<grid, rpw * (128 / 4), lds, stream>>>(p);
   }
   DTREE_LAUNCH_CHECK("gdn_layer_recurrence launch");
+  return DTREE_OK;
+}
+
+// dtree_gdn_layer_prep then dtree_gdn_layer_recurrence, as one launch
+// (gdn_prep_reg_kernel) for trees of up to 32 nodes with 16-byte aligned
+// projection rows, taps and window; otherwise the two launches.
+extern "C" int dtree_gdn_layer_prep_recurrence(const DtreeGdnArgs* a, hipStream_t stream) {
+  if (int rc = gdn_layer_check(a, "gdn_layer_prep_recurrence")) return rc;
+  const int key_dim = a->num_k_heads * a->head_k_dim, value_dim = a->num_v_heads * a->head_v_dim;
+  const int C = 2 * key_dim + value_dim;
+  const bool fits = a->rows_padded <= 32 && a->head_k_dim == 128 && a->head_v_dim == 128 && a->conv_keep >= 1 &&
+                    a->conv_keep <= kConvMaxKeep && a->ld_proj % 4 == 0 && C % 4 == 0 &&
+                    (((uintptr_t)a->proj | (uintptr_t)a->conv_w | (uintptr_t)a->window | (uintptr_t)a->state |
+                      (uintptr_t)a->q | (uintptr_t)a->k) & 15) == 0;
+  if (!fits) {
+    const int rc = dtree_gdn_layer_prep(a, stream);
+    return rc ? rc : dtree_gdn_layer_recurrence(a, stream);
+  }
+  DTREE_REQUIRE(a->proj && a->window && a->conv_w && a->A_log && a->dt_bias && a->q && a->k && a->v && a->g &&
+                    a->beta && a->state && a->y,
+                "gdn_layer_prep_recurrence: null pointer");
+  DTREE_REQUIRE(a->ld_proj >= C + value_dim + 2 * a->num_v_heads,
+                "gdn_layer_prep_recurrence: ld_proj below C + z + b + a");
+  PrepParams pp{};
+  pp.desc = a->desc; pp.rows = a->rows_padded;
+  pp.x = a->proj; pp.ldx = a->ld_proj; pp.base = a->window; pp.w = a->conv_w;
+  pp.C = C; pp.key_dim = key_dim; pp.Hv = a->num_v_heads; pp.ab_col = C + value_dim;
+  pp.A_log = a->A_log; pp.dt_bias = a->dt_bias;
+  pp.q = a->q; pp.k = a->k; pp.v = a->v; pp.g = a->g; pp.beta = a->beta;
+  pp.q_scale = 1.0f / (float)a->head_k_dim;
+  pp.k_scale = 1.0f / sqrtf((float)a->head_k_dim);
+  GdnParams p{};
+  p.q = a->q; p.k = a->k; p.v = a->v; p.g = a->g; p.beta = a->beta; p.state = a->state;
+  p.parents = a->desc->parents; p.T_dev = &a->desc->num_nodes;
+  p.T = a->rows_padded; p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->head_v_dim; p.rpw = 8;
+  p.y = a->y; p.states = nullptr;
+  const int grid = a->num_v_heads * (a->head_v_dim / 8);
+  switch (a->conv_keep) {
+#define DTREE_PREP_REG_CASE(K) \
+  case K: gdn_prep_reg_kernel<K><<<grid, 256, 0, stream>>>(p, pp); break;
+    DTREE_PREP_REG_CASE(1) DTREE_PREP_REG_CASE(2) DTREE_PREP_REG_CASE(3) DTREE_PREP_REG_CASE(4)
+    DTREE_PREP_REG_CASE(5) DTREE_PREP_REG_CASE(6) DTREE_PREP_REG_CASE(7)
+#undef DTREE_PREP_REG_CASE
+  }
+  DTREE_LAUNCH_CHECK("gdn_layer_prep_recurrence launch");
   return DTREE_OK;
 }
 

@@ -152,6 +152,7 @@ SIGNATURES = {
     "dtree_gdn_args_bytes": (_sz, []),
     "dtree_gdn_layer_prep": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_recurrence": (C.c_int, [C.POINTER(GdnArgs), _vp]),
+    "dtree_gdn_layer_prep_recurrence": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_gated_norm": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_commit": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_chain": (C.c_int, [C.POINTER(GdnArgs), C.c_int32, _vp]),

@@ -136,8 +136,8 @@ class Qwen35TreeEngine(TreeEngineBase):
                 gi = cache.slot[li]
                 self._gemm("in", self.xg, H, lw.w_in, N.EPI_STORE_F32, st, ss_in=self.ss, out_f32=self.proj[gi])
                 ga = self.gdn_args(li, cache)
-                N.check(self.lib.dtree_gdn_layer_prep(C.byref(ga), st), "gdn prep")
-                N.check(self.lib.dtree_gdn_layer_recurrence(C.byref(ga), st), "gdn recurrence")
+                # one launch for trees of up to 32 nodes, else prep + recurrence
+                N.check(self.lib.dtree_gdn_layer_prep_recurrence(C.byref(ga), st), "gdn prep + recurrence")
                 N.check(self.lib.dtree_gdn_layer_gated_norm(C.byref(ga), st), "gdn gated norm")
                 self._gemm("out", self.gout, c.value_dim, lw.w_out, N.EPI_RESIDUAL, st, out_f32=self.x,
                            out_bf16=self.xg, next_norm=lw.post_norm, ss_out=self.ss)

@@ -446,6 +446,12 @@ typedef struct DtreeGdnArgs {
 size_t dtree_gdn_args_bytes(void);
 int dtree_gdn_layer_prep(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_recurrence(const DtreeGdnArgs* args, hipStream_t stream);
+/* dtree_gdn_layer_prep followed by dtree_gdn_layer_recurrence (the same
+ * outputs: q, k, v, g, beta and y), as one launch when rows_padded <= 32, the
+ * head dims are 128 and proj (ld_proj % 4 == 0), conv_w, window, state, q and
+ * k are 16-byte aligned; otherwise the two launches. Replaces
+ * qwen35_tree.py:199-320 between the projections and the gated norm. */
+int dtree_gdn_layer_prep_recurrence(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_gated_norm(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_commit(const DtreeGdnArgs* args, hipStream_t stream);
 /* One GatedDeltaNet layer over a causal chain of num_tokens prompt tokens that

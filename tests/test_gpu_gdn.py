@@ -215,3 +215,61 @@ def test_commit_replays_accepted_path():
                                      pbuf.data_ptr(), plen.data_ptr(), 16, 32, 128, 128, stream()), "gdn commit")
     torch.cuda.synchronize()
     np.testing.assert_array_equal(win1.cpu().numpy(), np.concatenate([base[1:], x[path[:1]]]).astype(np.float32))
+
+
+@pytest.mark.parametrize("T,seed", [(25, 3), (32, 4), (1, 5), (17, 6)])
+def test_layer_prep_and_recurrence_in_one_launch(gpu_device, T, seed):
+    """dtree_gdn_layer_prep_recurrence (one launch for trees of up to 32 nodes)
+    against dtree_gdn_layer_prep + dtree_gdn_layer_recurrence on the same
+    inputs: v, g and beta bit for bit (same conv window, tap order and
+    formulas), q and k to the rounding of the RMS sum's order, y to 1e-5 of its
+    scale. Both read the node count and parents from the step descriptor."""
+    from gpu_util import device_desc
+
+    dev = gpu_device
+    g_ = np.random.default_rng(seed)
+    Hk, Hv, D, keep, MP = 16, 32, 128, 3, 32
+    key_dim, value_dim = Hk * D, Hv * D
+    conv_c = 2 * key_dim + value_dim
+    ld = conv_c + value_dim + 2 * Hv
+    parents = random_tree(T, seed)
+    desc = device_desc([0] * T, [5] * T, parents, 100, dev)
+    proj = torch.zeros(MP, ld, device=dev)
+    proj[:T] = torch.from_numpy(g_.normal(size=(T, ld)).astype(np.float32)).to(dev)
+    window = torch.from_numpy(g_.normal(size=(keep, conv_c)).astype(np.float32)).to(dev)
+    conv_w = torch.from_numpy((g_.normal(size=(keep + 1, conv_c)) * 0.5).astype(np.float32)).to(dev)
+    A_log = torch.from_numpy(g_.uniform(0, 2.7, size=Hv).astype(np.float32)).to(dev)
+    dt_bias = torch.ones(Hv, device=dev)
+    state = torch.from_numpy((g_.normal(size=(Hv, D, D)) * 0.1).astype(np.float32)).to(dev)
+
+    def run(fused):
+        out = {n: torch.full((MP, w), 7.0, device=dev) for n, w in
+               (("q", key_dim), ("k", key_dim), ("v", value_dim), ("g", Hv), ("beta", Hv), ("y", value_dim))}
+        a = N.GdnArgs()
+        a.desc = desc.data_ptr(); a.rows_padded = MP
+        a.num_k_heads = Hk; a.num_v_heads = Hv; a.head_k_dim = D; a.head_v_dim = D; a.conv_keep = keep
+        a.proj = proj.data_ptr(); a.ld_proj = ld
+        a.window = window.data_ptr(); a.conv_w = conv_w.data_ptr()
+        a.A_log = A_log.data_ptr(); a.dt_bias = dt_bias.data_ptr(); a.state = state.data_ptr()
+        a.q = out["q"].data_ptr(); a.k = out["k"].data_ptr(); a.v = out["v"].data_ptr()
+        a.g = out["g"].data_ptr(); a.beta = out["beta"].data_ptr(); a.y = out["y"].data_ptr()
+        lib = N.lib()
+        if fused:
+            N.check(lib.dtree_gdn_layer_prep_recurrence(C.byref(a), stream()), "prep + recurrence")
+        else:
+            N.check(lib.dtree_gdn_layer_prep(C.byref(a), stream()), "prep")
+            N.check(lib.dtree_gdn_layer_recurrence(C.byref(a), stream()), "recurrence")
+        torch.cuda.synchronize()
+        return {n: t[:T].cpu().numpy() for n, t in out.items()}
+
+    window0, state0 = window.clone(), state.clone()
+    sep, fus, fus2 = run(False), run(True), run(True)
+    for n in ("v", "g", "beta"):
+        assert np.array_equal(sep[n], fus[n]), n
+    for n in ("q", "k"):
+        np.testing.assert_allclose(fus[n], sep[n], rtol=1e-5, atol=1e-7, err_msg=n)
+    assert np.abs(fus["y"] - sep["y"]).max() <= 1e-5 * max(1.0, np.abs(sep["y"]).max())
+    for n in fus:
+        assert np.array_equal(fus[n], fus2[n]), n  # repeatable
+    # the committed window and state are read, not written
+    assert torch.equal(window, window0) and torch.equal(state, state0) and np.isfinite(fus["y"]).all()
