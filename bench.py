@@ -345,7 +345,9 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
     if fused:
         us["prep_recurrence"] = timed(lambda r: lib.dtree_gdn_layer_prep_recurrence(g[r], st), len(g))
     us["gated_norm"] = timed(lambda r: lib.dtree_gdn_layer_gated_norm(g[r], st), len(g))
-    us["commit"] = timed(lambda r: lib.dtree_gdn_layer_commit(g[r], st), len(g))
+    # every layer's commit in one launch, as the step runs it
+    g_all = (N.GdnArgs * len(args["gdn"]))(*args["gdn"])
+    us["commit"] = timed(lambda r: lib.dtree_gdn_layers_commit(g_all, len(args["gdn"]), st), 1)
     us["attention"] = timed(lambda r: eng._attention(A[r], cache, st), len(A))
     us["lm_head"] = timed(lambda r: eng.launch_lm_head(st), 1)
 
@@ -387,7 +389,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "gdn_recurrence": entry("gdn_tree_reg_kernel<32>" if eng.MP == 32 else "gdn_tree_dfs_kernel", nG,
                                 us["recurrence"], b["recurrence"]),
         "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
-        "gdn_commit": entry("gdn_commit_kernel<128>", nG, us["commit"], b["commit"]),
+        "gdn_commit": entry("gdn_commit_layers_kernel<128>", 1, us["commit"], nG * b["commit"]),
         "attention": entry(attention_kernel_name(eng.max_past, 256, 64, True, eng.MP), nA, us["attention"],
                            b["attention"]),
         "lm_head": entry(lmhead_kernel_name(quant, eng.MP), 1, us["lm_head"], b["lm_head"]),

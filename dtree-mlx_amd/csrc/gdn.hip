@@ -517,8 +517,8 @@ __device__ __forceinline__ int clamp_node(int t, int T) { return min(max(t, 0), 
 // rows of (window ++ x along the path). Blocks [0, conv_blocks) do the conv
 // window, the rest the state rows.
 template <int DK>
-__global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const float* x, int ldx, float* window, int C,
-                                                         int keep, int conv_blocks) {
+__device__ __forceinline__ void gdn_commit_body(const GdnParams& p, const float* x, int ldx, float* window, int C,
+                                                int keep, int conv_blocks) {
   constexpr int LPR = DK / 4;
   const int n = min(max(*p.path_len, 0), kGdnMaxNodes);
   if ((int)blockIdx.x < conv_blocks) {
@@ -556,6 +556,36 @@ __global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const floa
     s += kk * ((vv - kv) * bb);
   }
   *reinterpret_cast<f32x4_t*>(sp) = s;
+}
+
+template <int DK>
+__global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const float* x, int ldx, float* window, int C,
+                                                         int keep, int conv_blocks) {
+  gdn_commit_body<DK>(p, x, ldx, window, C, keep, conv_blocks);
+}
+
+// The commits of several GatedDeltaNet layers of one step in one launch: row
+// blockIdx.y of the grid is layer blockIdx.y of the batch (its projection
+// rows, window, state and k / v / g / beta); the layers share the accepted
+// path and the shapes. Each layer reads and rewrites its whole committed state
+// (2 MB at 32 value heads of 128 x 128), so the batch is one stream of those
+// bytes instead of one short launch per layer.
+constexpr int kCommitMaxLayers = 32;
+struct CommitLayer {
+  const float* x; float* window; float* state;
+  const float* k; const float* v; const float* g; const float* beta;
+};
+struct CommitBatch {
+  CommitLayer l[kCommitMaxLayers];
+};
+
+template <int DK>
+__global__ __launch_bounds__(256) void gdn_commit_layers_kernel(GdnParams p, CommitBatch b, int ldx, int C, int keep,
+                                                                int conv_blocks) {
+  const CommitLayer& ly = b.l[blockIdx.y];
+  GdnParams q = p;
+  q.state = ly.state; q.k = ly.k; q.v = ly.v; q.g = ly.g; q.beta = ly.beta;
+  gdn_commit_body<DK>(q, ly.x, ldx, ly.window, C, keep, conv_blocks);
 }
 
 // Layer prep (qwen35_tree.py:199-308 between the projections and the
@@ -1225,6 +1255,39 @@ extern "C" int dtree_gdn_layer_commit(const DtreeGdnArgs* a, hipStream_t stream)
   gdn_commit_kernel<128><<<conv_blocks + state_blocks, 256, 0, stream>>>(p, a->proj, a->ld_proj, a->window, C,
                                                                           a->conv_keep, conv_blocks);
   DTREE_LAUNCH_CHECK("gdn_layer_commit launch");
+  return DTREE_OK;
+}
+
+extern "C" int dtree_gdn_layers_commit(const DtreeGdnArgs* a, int32_t num_layers, hipStream_t stream) {
+  DTREE_REQUIRE(a && num_layers >= 1, "gdn_layers_commit: null args or no layers");
+  for (int i = 0; i < num_layers; ++i) {
+    if (int rc = gdn_layer_check(&a[i], "gdn_layers_commit")) return rc;
+    DTREE_REQUIRE(a[i].proj && a[i].window && a[i].state && a[i].k && a[i].v && a[i].g && a[i].beta,
+                  "gdn_layers_commit: null pointer");
+    DTREE_REQUIRE(a[i].desc == a[0].desc && a[i].rows_padded == a[0].rows_padded &&
+                      a[i].num_k_heads == a[0].num_k_heads && a[i].num_v_heads == a[0].num_v_heads &&
+                      a[i].conv_keep == a[0].conv_keep && a[i].ld_proj == a[0].ld_proj,
+                  "gdn_layers_commit: layers must share the step descriptor, node capacity, heads, conv and ld_proj");
+  }
+  const int C = 2 * a[0].num_k_heads * a[0].head_k_dim + a[0].num_v_heads * a[0].head_v_dim;
+  const int rpw = 256 / (128 / 4);
+  GdnParams p{};
+  p.path = a[0].desc->accepted; p.path_len = &a[0].desc->n_accepted;
+  p.T = a[0].rows_padded; p.Hk = a[0].num_k_heads; p.Hv = a[0].num_v_heads; p.Dv = a[0].head_v_dim; p.rpw = rpw;
+  const int conv_blocks = (C + 255) / 256;
+  const int state_blocks = a[0].num_v_heads * (a[0].head_v_dim / rpw);
+  for (int l0 = 0; l0 < num_layers; l0 += kCommitMaxLayers) {
+    const int nl = min(num_layers - l0, kCommitMaxLayers);
+    CommitBatch b{};
+    for (int i = 0; i < nl; ++i) {
+      const DtreeGdnArgs& x = a[l0 + i];
+      b.l[i] = CommitLayer{x.proj, x.window, x.state, x.k, x.v, x.g, x.beta};
+    }
+    gdn_commit_layers_kernel<128><<<dim3(conv_blocks + state_blocks, nl), 256, 0, stream>>>(p, b, a[0].ld_proj, C,
+                                                                                          a[0].conv_keep,
+                                                                                          conv_blocks);
+    DTREE_LAUNCH_CHECK("gdn_layers_commit launch");
+  }
   return DTREE_OK;
 }
 

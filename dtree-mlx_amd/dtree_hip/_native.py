@@ -153,6 +153,7 @@ SIGNATURES = {
     "dtree_gdn_layer_prep": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_recurrence": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_prep_recurrence": (C.c_int, [C.POINTER(GdnArgs), _vp]),
+    "dtree_gdn_layers_commit": (C.c_int, [C.POINTER(GdnArgs), _i32, _vp]),
     "dtree_gdn_layer_gated_norm": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_commit": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_chain": (C.c_int, [C.POINTER(GdnArgs), C.c_int32, _vp]),

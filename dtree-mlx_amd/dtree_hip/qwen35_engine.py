@@ -173,10 +173,15 @@ class Qwen35TreeEngine(TreeEngineBase):
         self._commit_gdn(cache, st, d)
 
     def _commit_gdn(self, cache: Qwen35Cache, st: int, desc: torch.Tensor) -> None:
-        for li in cache.gdn_layers:
-            ga = self.gdn_args(li, cache)
-            ga.desc = desc.data_ptr()
-            N.check(self.lib.dtree_gdn_layer_commit(C.byref(ga), st), "gdn commit")
+        """Every GatedDeltaNet layer's commit in one launch (dtree_gdn_layers_commit)."""
+        layers = list(cache.gdn_layers)
+        if not layers:
+            return
+        arr = (N.GdnArgs * len(layers))()
+        for i, li in enumerate(layers):
+            arr[i] = self.gdn_args(li, cache)
+            arr[i].desc = desc.data_ptr()
+        N.check(self.lib.dtree_gdn_layers_commit(arr, len(layers), st), "gdn commit")
 
     def commit_chain(self, cache: Qwen35Cache, tokens, norm_hidden: bool = False) -> None:
         """Forward a causal chain of <= max_nodes tokens and commit all of it:

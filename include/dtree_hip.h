@@ -454,6 +454,12 @@ int dtree_gdn_layer_recurrence(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_prep_recurrence(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_gated_norm(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_commit(const DtreeGdnArgs* args, hipStream_t stream);
+/* dtree_gdn_layer_commit for num_layers layers (args[0 .. num_layers)) in one
+ * launch: the layers of one verify step share desc (the accepted path),
+ * rows_padded, heads, conv_keep and ld_proj; each has its own proj, window,
+ * state, k, v, g and beta. Replaces the per-layer loop of
+ * commit_qwen35_tree_path (qwen35_tree.py:708-732). */
+int dtree_gdn_layers_commit(const DtreeGdnArgs* args, int32_t num_layers, hipStream_t stream);
 /* One GatedDeltaNet layer over a causal chain of num_tokens prompt tokens that
  * continue the committed window and state (prompt prefill): conv + SiLU and
  * the q / k / v / g / beta prep, the recurrence (y per token; the final state

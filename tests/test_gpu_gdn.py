@@ -273,3 +273,51 @@ def test_layer_prep_and_recurrence_in_one_launch(gpu_device, T, seed):
         assert np.array_equal(fus[n], fus2[n]), n  # repeatable
     # the committed window and state are read, not written
     assert torch.equal(window, window0) and torch.equal(state, state0) and np.isfinite(fus["y"]).all()
+
+
+def test_layers_commit_in_one_launch(gpu_device):
+    """dtree_gdn_layers_commit over three layers against dtree_gdn_layer_commit
+    per layer (the same body on each layer's window and state): bit for bit."""
+    from gpu_util import device_desc
+
+    dev = gpu_device
+    g_ = np.random.default_rng(11)
+    Hk, Hv, D, keep, MP, nl = 16, 32, 128, 3, 32, 3
+    key_dim, value_dim = Hk * D, Hv * D
+    conv_c = 2 * key_dim + value_dim
+    ld = conv_c + value_dim + 2 * Hv
+    parents = random_tree(25, 7)
+    desc = device_desc([0] * 25, [5] * 25, parents, 100, dev, accepted=[0, 3, 9, 14])
+
+    def t(*shape, scale=1.0):
+        return torch.from_numpy((g_.normal(size=shape) * scale).astype(np.float32)).to(dev)
+
+    layers = [dict(proj=t(MP, ld), window=t(keep, conv_c), state=t(Hv, D, D, scale=0.1), q=t(MP, key_dim),
+                   k=t(MP, key_dim, scale=0.1), v=t(MP, value_dim), g=torch.rand(MP, Hv, device=dev),
+                   beta=torch.rand(MP, Hv, device=dev)) for _ in range(nl)]
+
+    def args(ly):
+        a = N.GdnArgs()
+        a.desc = desc.data_ptr(); a.rows_padded = MP
+        a.num_k_heads = Hk; a.num_v_heads = Hv; a.head_k_dim = D; a.head_v_dim = D; a.conv_keep = keep
+        a.proj = ly["proj"].data_ptr(); a.ld_proj = ld
+        a.window = ly["window"].data_ptr(); a.state = ly["state"].data_ptr()
+        for n in ("q", "k", "v", "g", "beta"):
+            setattr(a, n, ly[n].data_ptr())
+        return a
+
+    before = [{n: ly[n].clone() for n in ("window", "state")} for ly in layers]
+    for ly in layers:
+        N.check(N.lib().dtree_gdn_layer_commit(C.byref(args(ly)), stream()), "commit")
+    torch.cuda.synchronize()
+    one = [{n: ly[n].clone() for n in ("window", "state")} for ly in layers]
+    for ly, b in zip(layers, before):
+        for n in ("window", "state"):
+            ly[n].copy_(b[n])
+    arr = (N.GdnArgs * nl)(*[args(ly) for ly in layers])
+    N.check(N.lib().dtree_gdn_layers_commit(arr, nl, stream()), "layers commit")
+    torch.cuda.synchronize()
+    for ly, o, b in zip(layers, one, before):
+        for n in ("window", "state"):
+            assert torch.equal(ly[n], o[n]), n
+        assert not torch.equal(ly["state"], b["state"])  # the commit did advance the state
