@@ -275,14 +275,16 @@ def test_layer_prep_and_recurrence_in_one_launch(gpu_device, T, seed):
     assert torch.equal(window, window0) and torch.equal(state, state0) and np.isfinite(fus["y"]).all()
 
 
-def test_layers_commit_in_one_launch(gpu_device):
-    """dtree_gdn_layers_commit over three layers against dtree_gdn_layer_commit
-    per layer (the same body on each layer's window and state): bit for bit."""
+@pytest.mark.parametrize("nl", [3, 34])
+def test_layers_commit_in_one_launch(gpu_device, nl):
+    """dtree_gdn_layers_commit against dtree_gdn_layer_commit per layer (the
+    same body on each layer's window and state): bit for bit. 34 layers take
+    two launches (32 layers per launch)."""
     from gpu_util import device_desc
 
     dev = gpu_device
-    g_ = np.random.default_rng(11)
-    Hk, Hv, D, keep, MP, nl = 16, 32, 128, 3, 32, 3
+    g_ = np.random.default_rng(11 + nl)
+    Hk, Hv, D, keep, MP = 16, 32, 128, 3, 32
     key_dim, value_dim = Hk * D, Hv * D
     conv_c = 2 * key_dim + value_dim
     ld = conv_c + value_dim + 2 * Hv
