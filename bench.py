@@ -340,8 +340,9 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
     g = refs["gdn"]
     us["prep"] = timed(lambda r: lib.dtree_gdn_layer_prep(g[r], st), len(g))
     us["recurrence"] = timed(lambda r: lib.dtree_gdn_layer_recurrence(g[r], st), len(g))
-    # trees of up to 32 nodes run prep and recurrence as one launch in the step
-    fused = eng.MP == 32
+    # trees of up to 32 nodes with 128-dim heads run prep and recurrence as one
+    # launch in the step (dtree_gdn_layer_prep_recurrence)
+    fused = eng.MP == 32 and cfg.linear_key_head_dim == 128 and cfg.linear_value_head_dim == 128
     if fused:
         us["prep_recurrence"] = timed(lambda r: lib.dtree_gdn_layer_prep_recurrence(g[r], st), len(g))
     us["gated_norm"] = timed(lambda r: lib.dtree_gdn_layer_gated_norm(g[r], st), len(g))
@@ -385,7 +386,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "o_gemm": entry(kn(H, cfg.q_dim, 1), nA, us["o"], b["o"]),
         "gate_up_gemm": entry(kn(2 * F, H, 2), nL, us["gu"], b["gu"]),
         "down_gemm": entry(kn(H, F, 1), nL, us["down"], b["down"]),
-        "gdn_prep": entry("gdn_prep_kernel<3, 128>", nG, us["prep"], b["prep"]),
+        "gdn_prep": entry(f"gdn_prep_kernel<{cfg.linear_conv_kernel_dim - 1}, 128>", nG, us["prep"], b["prep"]),
         "gdn_recurrence": entry("gdn_tree_reg_kernel<32>" if eng.MP == 32 else "gdn_tree_dfs_kernel", nG,
                                 us["recurrence"], b["recurrence"]),
         "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
@@ -401,7 +402,8 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         # the recurrence's bytes (its inputs are now the raw conv / b / a columns,
         # of the same size), the conv taps and window, and q / k / v / g / beta
         # written for the commit
-        out["gdn_prep_recurrence"] = entry("gdn_prep_reg_kernel<3>", nG, us["prep_recurrence"],
+        out["gdn_prep_recurrence"] = entry(f"gdn_prep_reg_kernel<{cfg.linear_conv_kernel_dim - 1}>", nG,
+                                           us["prep_recurrence"],
                                            b["recurrence"] + (2 * cfg.linear_conv_kernel_dim - 1) * C_ * 4
                                            + L * (C_ + 2 * Hv) * 4)
     return out
