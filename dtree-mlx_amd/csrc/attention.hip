@@ -654,9 +654,12 @@ __global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
   } else {
     // split s >= 1: prefix chunks c0 .. c0 + cps - 1 (cut at the prefix's np)
     const int c0 = (s - 1) * p.cps;
-    const bool any = c0 < p.max_pchunks;
+    // The first chunk's loads go out on every path (a split past the prefix
+    // chunks loads the last one and never commits it), so waiting for the
+    // query rows issued before them does not become a wait for every load.
+    const int cfirst = min(c0, p.max_pchunks - 1);  // splits s >= 1 exist only with prefix chunks
     PrefixStage<D, TPS> st;
-    if (any) st.issue(p, c0, PrefixStage<D, TPS>::page_of(p, c0), g, ts);
+    st.issue(p, cfirst, PrefixStage<D, TPS>::page_of(p, cfirst), g, ts);
     read_desc();
     build_q(false);
     if (bail()) return;
