@@ -184,7 +184,7 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
     out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant, lo="qkv" not in eng.HI_ONLY), nl, us["qkv"], b["qkv"])
-    out["attention"] = entry(attention_kernel_name(eng.max_past, 128, 128, False, eng.MP), nl, us["attention"],
+    out["attention"] = entry(attention_kernel_name(eng.attn_grid_past(P), 128, 128, False, eng.MP), nl, us["attention"],
                              b["attention"])
     out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant), nl, us["o"], b["o"])
     out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant), nl, us["down"], b["down"])
@@ -348,6 +348,9 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
     us["gated_norm"] = timed(lambda r: lib.dtree_gdn_layer_gated_norm(g[r], st), len(g))
     # every layer's commit in one launch, as the step runs it
     g_all = (N.GdnArgs * len(args["gdn"]))(*args["gdn"])
+    for i, li in enumerate(G):  # into the spare pair, as the step's commit writes
+        g_all[i].window_out = cache.windows_next[cache.slot[li]].data_ptr()
+        g_all[i].state_out = cache.states_next[cache.slot[li]].data_ptr()
     us["commit"] = timed(lambda r: lib.dtree_gdn_layers_commit(g_all, len(args["gdn"]), st), 1)
     us["attention"] = timed(lambda r: eng._attention(A[r], cache, st), len(A))
     us["lm_head"] = timed(lambda r: eng.launch_lm_head(st), 1)
@@ -391,7 +394,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
                                 us["recurrence"], b["recurrence"]),
         "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
         "gdn_commit": entry("gdn_commit_layers_kernel<128>", 1, us["commit"], nG * b["commit"]),
-        "attention": entry(attention_kernel_name(eng.max_past, 256, 64, True, eng.MP), nA, us["attention"],
+        "attention": entry(attention_kernel_name(eng.attn_grid_past(P), 256, 64, True, eng.MP), nA, us["attention"],
                            b["attention"]),
         "lm_head": entry(lmhead_kernel_name(quant, eng.MP), 1, us["lm_head"], b["lm_head"]),
     }
@@ -607,7 +610,8 @@ def decode_step_bench(target_model, cache, P: int, budget: int, steps: int = 30)
 
 
 def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup: int, kernel_reps: int = 0,
-                 with_cpu: bool = False, with_decode: bool = False, with_prefill: bool = False) -> dict:
+                 with_cpu: bool = False, with_decode: bool = False, with_prefill: bool = False,
+                 max_past: int | None = None) -> dict:
     """Builds the random-init model, prefills P tokens, builds the seeded tree
     (acceptance pass at p = 0.85 on the device argmax) and times `steps`
     verify steps (descriptor upload, graph replay, result read back) after
@@ -623,16 +627,17 @@ def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup
     hybrid = model.startswith("qwen35")
     cfg = {"qwen3-4b": QWEN3_4B, "qwen35-4b": QWEN35_4B, "qwen35-9b": QWEN35_9B}[model]
     max_nodes = budget + 1
+    max_past = P + 64 if max_past is None else max_past
     t0 = time.time()
     if hybrid:
         w = Qwen35Weights.random(cfg, seed=0, device=dev, quant=quant)
-        eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 30], max_nodes=max_nodes)
+        eng = Qwen35TreeEngine(cfg, w, max_past=max_past, layer_ids=[1, 9, 17, 25, 30], max_nodes=max_nodes)
     else:
         if quant == "q4":
             w = Qwen3Weights.random_q4(cfg, seed=0, device=dev)
         else:
             w = Qwen3Weights.random(cfg, seed=0, device=dev)
-        tmodel = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=[1, 9, 17, 25, 33], max_nodes=max_nodes)
+        tmodel = Qwen3TreeModel(cfg, w, max_past=max_past, layer_ids=[1, 9, 17, 25, 33], max_nodes=max_nodes)
         eng = tmodel.engine
     cache = eng.new_cache()
     prefix = random_prefix(P, cfg.vocab_size, seed=1)
@@ -653,18 +658,29 @@ def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup
     L = tree.size
     pos, par, toks = tree.positions(P), tree.parents, tree.tokens
     log(f"[bench] tree L={L} max depth={max(tree.depths)}")
-    for _ in range(warmup):
+    # commit=False: every step verifies the same tree against the same
+    # committed state (the hybrid's commit writes the cache's spare state
+    # buffers), so each replay is the seeded step and accepts the same path.
+    first = eng.verify(cache, toks, pos, par, use_graph=True, commit=False)
+    for _ in range(max(warmup - 1, 0)):
         res = eng.verify(cache, toks, pos, par, use_graph=True, commit=False)
+        if res.accepted != first.accepted:
+            raise RuntimeError(f"warmup step accepted {res.accepted}, the first step {first.accepted}")
     torch.cuda.synchronize()
-    log(f"[bench] warmup done, accepted={res.accepted}")
-    accepted_lens = []
+    log(f"[bench] warmup done, accepted={first.accepted}")
+    results = []
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for _ in range(steps):
-        res = eng.verify(cache, toks, pos, par, use_graph=True, commit=False)
-        accepted_lens.append(len(res.accepted))
+        results.append(eng.verify(cache, toks, pos, par, use_graph=True, commit=False))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
+    for i, r in enumerate(results):
+        if r.accepted != first.accepted or r.bonus_token != first.bonus_token:
+            raise RuntimeError(f"timed step {i} accepted {r.accepted} (bonus {r.bonus_token}), the first step "
+                               f"{first.accepted} (bonus {first.bonus_token})")
+    res = results[-1]
+    accepted_lens = [len(r.accepted) for r in results]
     ms = elapsed / steps * 1e3
     ab = algorithmic_bytes35(cfg, P, L, quant) if hybrid else algorithmic_bytes(cfg, P, L, quant)
     gbps = ab["total"] / (ms * 1e-3) / 1e9
@@ -697,6 +713,100 @@ def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup
     gc.collect()
     torch.cuda.empty_cache()
     return out
+
+
+def lazy_hop_bench(P: int = 2048, hops: int = 40, warmup: int = 5) -> dict:
+    """The reference's default Qwen3.5 verifier (lazy_follow_tree_exact,
+    dtree_runtime.py:211-290) walks the tree one token at a time; one hop is
+    text_model.forward_dflash over one token (every layer, committing the
+    GatedDeltaNet state and the attention K/V), the LM-head argmax and the
+    host read of the token. Timed here on the Qwen3.5-4B-shaped hybrid with q4
+    group-64 weights after a P-token prefill, hop after hop as the walk runs
+    them (the prefix grows by one per hop)."""
+    import torch
+
+    from dtree_hip.adapters import Qwen35TargetAdapter, Qwen35TreeModel
+    from dtree_hip.config import QWEN35_4B
+    from dtree_hip.synthetic import random_prefix
+    from dtree_hip.weights import Qwen35Weights
+
+    dev = torch.device("cuda:0")
+    cfg = QWEN35_4B
+    layer_ids = [1, 9, 17, 25, 30]
+    w = Qwen35Weights.random(cfg, seed=0, device=dev, quant="q4")
+    model = Qwen35TreeModel(cfg, w, max_past=P + hops + warmup + 64, layer_ids=layer_ids)
+    adapter = Qwen35TargetAdapter()
+    cache = adapter.make_cache(model)
+    model.engine.prefill(cache, random_prefix(P, cfg.vocab_size, seed=1))
+    text = model.model
+    tok = 7
+
+    def hop(t):
+        norm_hidden, _ = text.forward_dflash(torch.tensor([[t]]), cache, layer_ids)
+        return int(adapter.lm_head_argmax(model, norm_hidden).reshape(-1)[0].item())
+
+    for _ in range(warmup):
+        tok = hop(tok)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(hops):
+        tok = hop(tok)
+    ms = (time.perf_counter() - t0) / hops * 1e3
+    model.engine.release_graphs()
+    del model, w, cache
+    torch.cuda.empty_cache()
+    return {"workload": f"Qwen3.5-4B-shaped hybrid q4 group-64, lazy exact verifier: one single-token hop "
+                        f"(forward_dflash over 1 token with commit, LM-head argmax, host read) at prefix {P}",
+            "ms_per_hop": round(ms, 4), "hops": hops,
+            "reference_m2max_ms_per_hop": 14.38}
+
+
+def dflash_block_bench(P: int = 1024, block: int = 16, steps: int = 30, warmup: int = 5) -> dict:
+    """DFlash linear verification in the parallel-greedy-argmax mode
+    (runtime.py:302-354): a drafted block of 16 tokens verified in one
+    forward as a chain, LM-head argmax of every row, the longest matching
+    prefix and its commit, on the Qwen3-4B-shaped bf16 target at prefix P.
+    Each timed call starts from the same prefix (the offset is reset; the
+    rows past it are rewritten by the next call)."""
+    import torch
+
+    from dtree_hip import Qwen3TreeModel, Qwen3Weights
+    from dtree_hip.adapters import LoadedTargetModel, Qwen3TargetAdapter
+    from dtree_hip.config import QWEN3_4B
+    from dtree_hip.runtime import verify_block_parallel_greedy_argmax
+    from dtree_hip.synthetic import random_prefix
+
+    dev = torch.device("cuda:0")
+    cfg = QWEN3_4B
+    layer_ids = [1, 9, 17, 25, 33]
+    w = Qwen3Weights.random(cfg, seed=0, device=dev)
+    model = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=layer_ids, max_nodes=block)
+    target = LoadedTargetModel(requested_model="random:qwen3-4b", resolved_model_path=None, model=model,
+                               tokenizer=None, adapter=Qwen3TargetAdapter())
+    cache = target.make_cache()
+    model.engine.prefill(cache, random_prefix(P, cfg.vocab_size, seed=1))
+    blk = random_prefix(block, cfg.vocab_size, seed=9)
+    acc = []
+
+    def one():
+        cache.offset = P
+        n, post, _ = verify_block_parallel_greedy_argmax(target, cache, blk, block, 0.0, layer_ids)
+        acc.append(n)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    model.engine.release_graphs()
+    del model, w, cache, target
+    torch.cuda.empty_cache()
+    return {"workload": f"DFlash parallel-greedy-argmax block verify (Qwen3-4B bf16 target, {block}-token block as a "
+                        f"chain, LM-head argmax, prefix match, commit) at prefix {P}",
+            "ms_per_step": round(ms, 4), "steps": steps, "accepted_last": acc[-1]}
 
 
 def attention_layer_bench(P: int = 512, sets: int = 128, reps: int = 1280) -> dict:
@@ -839,6 +949,17 @@ def main():
         t0 = time.time()
         configs["attention_layer_p512"] = attention_layer_bench(P=512)
         log(f"[bench] attention layer P=512: {configs['attention_layer_p512']}")
+        # the same step on an engine sized for the generator's default max_past
+        rr = run_workload("qwen3-4b", "bf16", 1024, 24, steps=30, warmup=5, max_past=4096, kernel_reps=54)
+        configs["qwen3_4b_bf16_p1024_max_past_4096"] = {
+            "workload": "Qwen3-4B bf16 tree-verify step, prefix 1024, 25-node tree, engine and cache sized for "
+                        "max_past 4096 (DFlashGenerator's default)",
+            "ms_per_step": round(rr["ms"], 4), "steps_per_s": round(rr["steps_per_s"], 3),
+            "attention": {k: (round(v, 2) if isinstance(v, float) else v)
+                          for k, v in rr["kernels"]["attention"].items()}, "steps": 30}
+        log(f"[bench] max_past 4096: {configs['qwen3_4b_bf16_p1024_max_past_4096']}")
+        configs["dflash_block_verify_qwen3_4b_p1024"] = dflash_block_bench()
+        log(f"[bench] dflash block verify: {configs['dflash_block_verify_qwen3_4b_p1024']}")
         for key, (m, q, pp, bb) in {"qwen3_4b_q4_p1024": ("qwen3-4b", "q4", 1024, 24),
                                     "qwen35_4b_bf16_p2048": ("qwen35-4b", "bf16", 2048, 24),
                                     "qwen35_9b_q4_p8192_budget64": ("qwen35-9b", "q4", 8192, 64)}.items():
@@ -849,7 +970,10 @@ def main():
                             "ms_per_step": round(rr["ms"], 4), "steps_per_s": round(rr["steps_per_s"], 3),
                             "hbm_gbps": round(rr["gbps"], 1), "hbm_frac_of_peak": round(rr["gbps"] / HBM_PEAK_GBPS, 4),
                             "algorithmic_bytes_per_step": rr["algorithmic_bytes"],
-                            "mean_accepted": rr["mean_accepted"], "steps": 30}
+                            "tokens_per_s": round(rr["steps_per_s"] * rr["mean_accepted"], 2),
+                            "mean_accepted": rr["mean_accepted"], "accepted": rr["accepted"], "steps": 30}
+        configs["lazy_hop_qwen35_4b_q4_p2048"] = lazy_hop_bench()
+        log(f"[bench] lazy hop: {configs['lazy_hop_qwen35_4b_q4_p2048']}")
         log(f"[bench] other workloads {time.time() - t0:.1f}s")
 
     model_name = MODEL_NAMES[a.model]

@@ -59,6 +59,14 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWsHeader = 4096;
 constexpr int kMaxPairs = (kWsHeader - 64) / 4;
 constexpr int kSpinLimit = 1 << 21;  // counter polls (~1 us each) before a workgroup gives up
+
+// DTREE_TEST_SPIN_LIMIT=n lowers the poll bound (read at every launch), so
+// tests can make the wait give up from the host while every workgroup still
+// runs to its end.
+static int spin_limit() {
+  const char* e = std::getenv("DTREE_TEST_SPIN_LIMIT");
+  return e && e[0] ? std::max(0, std::atoi(e)) : kSpinLimit;
+}
 constexpr int kCombineBatch = 4;     // split slices in flight per wave in the combine
 
 struct AttnParams {
@@ -76,6 +84,7 @@ struct AttnParams {
   float scale_log2;
   int write_cache;
   float* part; int* counters; int* err;
+  int spin_limit;  // counter polls before a workgroup gives up
   int off_xcd;  // test hook: treat every workgroup as off its expected XCD
 };
 
@@ -716,7 +725,7 @@ __global__ __launch_bounds__(64 * G) void gqa_tree_attn_kernel(AttnParams p) {
     const int add = native ? 1 : 1 + kForeign;
     int v = arrive_add(cnt, add) + add;
     int it = 0;
-    while ((v & (kForeign - 1)) < S && it < kSpinLimit) {
+    while ((v & (kForeign - 1)) < S && it < p.spin_limit) {
       __builtin_amdgcn_s_sleep(1);
       v = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       ++it;
@@ -946,6 +955,7 @@ static int group_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   attn_splits(D, a->max_past_length, pairs, cus, p.S, p.cps);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.off_xcd = off_xcd_test();
+  p.spin_limit = spin_limit();
   p.err = reinterpret_cast<int*>(a->workspace);
   p.counters = reinterpret_cast<int*>(reinterpret_cast<char*>(a->workspace) + 64);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kWsHeader);
@@ -1031,6 +1041,17 @@ int scratch_for_current_device(void** out) {
   return DTREE_OK;
 }
 
+// Moves a workspace's error word into *status (OR) and clears it.
+__global__ void attn_status_kernel(int* err, int* status) {
+  if (threadIdx.x == 0) {
+    const int e = *err;
+    if (e) {
+      *status |= e;
+      *err = 0;
+    }
+  }
+}
+
 // Zeroes the workspace header (error word and split counters of either
 // kernel) before each call: a fill kernel, so the call stays capturable.
 __global__ void zero_header_kernel(u32x4_t* p, int n16) {
@@ -1057,7 +1078,7 @@ extern "C" int dtree_tree_attention_noalloc(const DtreeAttnArgs* a, hipStream_t 
   if (rc) return rc;
   // The group kernel keeps its error word and counters in the first 4 KiB; the
   // per-head kernel keeps one counter per (head, row block) at the start.
-  const size_t head_counters = (static_cast<size_t>(a->num_heads) * (a->rows_padded / 32) * 4 + 255) / 256 * 256;
+  const size_t head_counters = (64 + static_cast<size_t>(a->num_heads) * (a->rows_padded / 32) * 4 + 255) / 256 * 256;
   const int n16 = static_cast<int>(std::min(need, std::max<size_t>(4096, head_counters)) / 16);
   zero_header_kernel<<<(n16 + 255) / 256, 256, 0, stream>>>(reinterpret_cast<u32x4_t*>(ws), n16);
   DTREE_LAUNCH_CHECK("attention (no alloc): header clear");
@@ -1065,4 +1086,16 @@ extern "C" int dtree_tree_attention_noalloc(const DtreeAttnArgs* a, hipStream_t 
   b.workspace = ws;
   b.workspace_bytes = need;
   return group ? group_tree_attention(&b, stream) : dtree::head_tree_attention(&b, stream);
+}
+
+extern "C" int dtree_attention_status(void* workspace, int32_t* status, hipStream_t stream) {
+  DTREE_REQUIRE(status, "attention status: null status");
+  void* ws = workspace;
+  if (!ws) {
+    int rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+  }
+  attn_status_kernel<<<1, 64, 0, stream>>>(reinterpret_cast<int*>(ws), status);
+  DTREE_LAUNCH_CHECK("attention status launch");
+  return DTREE_OK;
 }

@@ -1020,7 +1020,9 @@ size_t head_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32
   const int nt = rows_padded / 32;
   const size_t stride = (size_t)32 * head_dim + 64;
   const size_t hb = (size_t)num_heads * nt;  // (head, query block) pairs
-  return ((hb * sizeof(int) + 255) & ~(size_t)255) +
+  // header: error word (bytes 0..3, shared layout with the per-group
+  // kernel's workspace, never set by this kernel), counters from byte 64
+  return ((64 + hb * sizeof(int) + 255) & ~(size_t)255) +
          hb * attn_splits(head_dim, max_past_length, nt) * stride * sizeof(float);
 }
 
@@ -1065,9 +1067,9 @@ int head_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   p.splits = attn_splits(D, a->max_past_length, nt);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.off_xcd = off_xcd_test();
-  p.counters = reinterpret_cast<int*>(a->workspace);
+  p.counters = reinterpret_cast<int*>(reinterpret_cast<char*>(a->workspace) + 64);
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) +
-                                    (((size_t)a->num_heads * nt * sizeof(int) + 255) & ~(size_t)255));
+                                    ((64 + (size_t)a->num_heads * nt * sizeof(int) + 255) & ~(size_t)255));
   const int G = p.Hq / p.Hkv;
   const int pairs = p.splits * p.Hkv;
   const int grid = ((pairs + 7) / 8) * 8 * G * nt;  // nt query blocks of ((pairs+7)/8)*8*G workgroups

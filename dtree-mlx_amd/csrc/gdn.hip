@@ -74,6 +74,7 @@ struct GdnParams {
   int T, Hk, Hv, Dv, rpw;
   float* y;            // [T][Hv][Dv]
   float* states;       // optional [T][Hv][Dv][Dk]
+  float* state_out;    // commit: destination of the new state (nullptr: in place)
 };
 
 // Sum over the LPR lanes that share a row (lanes are consecutive).
@@ -513,25 +514,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 __device__ __forceinline__ int clamp_node(int t, int T) { return min(max(t, 0), T - 1); }
 
 // Commit: replay the accepted path (path[0 .. *path_len), a root path) from the
-// base state, in place; the conv part moves the base window to the last keep
-// rows of (window ++ x along the path). Blocks [0, conv_blocks) do the conv
+// base state; the conv part moves the base window to the last keep rows of
+// (window ++ x along the path). The results go to window_out / p.state_out,
+// or back in place when those are null. Blocks [0, conv_blocks) do the conv
 // window, the rest the state rows.
 template <int DK>
-__device__ __forceinline__ void gdn_commit_body(const GdnParams& p, const float* x, int ldx, float* window, int C,
-                                                int keep, int conv_blocks) {
+__device__ __forceinline__ void gdn_commit_body(const GdnParams& p, const float* x, int ldx, const float* window,
+                                                float* window_out, int C, int keep, int conv_blocks) {
   constexpr int LPR = DK / 4;
   const int n = min(max(*p.path_len, 0), kGdnMaxNodes);
   if ((int)blockIdx.x < conv_blocks) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= C || n == 0) return;
-    // New window = the last keep rows of (window ++ x[path]). In place: row r
+    float* wout = window_out ? window_out : const_cast<float*>(window);
+    if (c >= C || (n == 0 && wout == window)) return;
+    // New window = the last keep rows of (window ++ x[path]). In place, row r
     // takes old row r + from_path (not yet overwritten) or a path input.
     const int from_path = min(n, keep);
     const int from_win = keep - from_path;
     for (int r = 0; r < keep; ++r) {
       const float val = r < from_win ? window[(size_t)(r + from_path) * C + c]
                                      : x[(size_t)clamp_node(p.path[n - from_path + (r - from_win)], p.T) * ldx + c];
-      window[(size_t)r * C + c] = val;
+      wout[(size_t)r * C + c] = val;
     }
     return;
   }
@@ -542,8 +545,8 @@ __device__ __forceinline__ void gdn_commit_body(const GdnParams& p, const float*
   const int rl = threadIdx.x / LPR, lane4 = threadIdx.x % LPR;
   if (rl >= rpw) return;  // surplus threads of the 256-thread launch
   const int dv = row0 + rl;
-  float* sp = p.state + ((size_t)h * p.Dv + dv) * DK + 4 * lane4;
-  f32x4_t s = *reinterpret_cast<const f32x4_t*>(sp);
+  const size_t so = ((size_t)h * p.Dv + dv) * DK + 4 * lane4;
+  f32x4_t s = *reinterpret_cast<const f32x4_t*>(p.state + so);
   for (int i = 0; i < n; ++i) {
     // The state update needs S k only (y is not replayed).
     const int t = clamp_node(p.path[i], p.T);
@@ -555,13 +558,13 @@ __device__ __forceinline__ void gdn_commit_body(const GdnParams& p, const float*
     kv = LPR == 32 ? row_sum32(kv) : row_sum<LPR>(kv);
     s += kk * ((vv - kv) * bb);
   }
-  *reinterpret_cast<f32x4_t*>(sp) = s;
+  *reinterpret_cast<f32x4_t*>((p.state_out ? p.state_out : p.state) + so) = s;
 }
 
 template <int DK>
-__global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const float* x, int ldx, float* window, int C,
-                                                         int keep, int conv_blocks) {
-  gdn_commit_body<DK>(p, x, ldx, window, C, keep, conv_blocks);
+__global__ __launch_bounds__(256) void gdn_commit_kernel(GdnParams p, const float* x, int ldx, const float* window,
+                                                         float* window_out, int C, int keep, int conv_blocks) {
+  gdn_commit_body<DK>(p, x, ldx, window, window_out, C, keep, conv_blocks);
 }
 
 // The commits of several GatedDeltaNet layers of one step in one launch: row
@@ -574,6 +577,7 @@ constexpr int kCommitMaxLayers = 32;
 struct CommitLayer {
   const float* x; float* window; float* state;
   const float* k; const float* v; const float* g; const float* beta;
+  float* window_out; float* state_out;  // nullptr: in place
 };
 struct CommitBatch {
   CommitLayer l[kCommitMaxLayers];
@@ -584,8 +588,8 @@ __global__ __launch_bounds__(256) void gdn_commit_layers_kernel(GdnParams p, Com
                                                                 int conv_blocks) {
   const CommitLayer& ly = b.l[blockIdx.y];
   GdnParams q = p;
-  q.state = ly.state; q.k = ly.k; q.v = ly.v; q.g = ly.g; q.beta = ly.beta;
-  gdn_commit_body<DK>(q, ly.x, ldx, ly.window, C, keep, conv_blocks);
+  q.state = ly.state; q.k = ly.k; q.v = ly.v; q.g = ly.g; q.beta = ly.beta; q.state_out = ly.state_out;
+  gdn_commit_body<DK>(q, ly.x, ldx, ly.window, ly.window_out, C, keep, conv_blocks);
 }
 
 // Layer prep (qwen35_tree.py:199-308 between the projections and the
@@ -1097,9 +1101,9 @@ extern "C" int dtree_gdn_commit(const float* x, float* window, int32_t channels,
   // with 256 and let surplus state threads idle.
   const int threads = 256;
   switch (head_k_dim) {
-    case 32: gdn_commit_kernel<32><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, channels, keep, conv_blocks); break;
-    case 64: gdn_commit_kernel<64><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, channels, keep, conv_blocks); break;
-    default: gdn_commit_kernel<128><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, channels, keep, conv_blocks); break;
+    case 32: gdn_commit_kernel<32><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, nullptr, channels, keep, conv_blocks); break;
+    case 64: gdn_commit_kernel<64><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, nullptr, channels, keep, conv_blocks); break;
+    default: gdn_commit_kernel<128><<<conv_blocks + state_blocks, threads, 0, stream>>>(p, x, channels, window, nullptr, channels, keep, conv_blocks); break;
   }
   DTREE_LAUNCH_CHECK("gdn_commit launch");
   return DTREE_OK;
@@ -1119,6 +1123,27 @@ static int gdn_layer_check(const DtreeGdnArgs* a, const char* what) {
 }
 
 extern "C" size_t dtree_gdn_args_bytes(void) { return sizeof(DtreeGdnArgs); }
+
+static_assert(DTREE_GDN_MAX_NESTED_BRANCHES == kDfsStack - 1, "the header's limit is the stack's");
+
+extern "C" int dtree_gdn_tree_check(const int32_t* parents, int32_t num_nodes) {
+  if (int rc = dtree_validate_parents(parents, num_nodes)) return rc;
+  if (num_nodes <= 32) return DTREE_OK;  // the register-resident recurrence holds any such tree
+  // nesting of a branching node = its branching ancestors + 1 (parents precede children)
+  int nch[DTREE_MAX_NODES] = {0}, nest[DTREE_MAX_NODES] = {0};
+  for (int i = 1; i < num_nodes; ++i) ++nch[parents[i]];
+  int deepest = 0;
+  for (int i = 0; i < num_nodes; ++i) {
+    const int above = i == 0 ? 0 : nest[parents[i]];
+    nest[i] = above + (nch[i] >= 2 ? 1 : 0);
+    if (nch[i] >= 2) deepest = std::max(deepest, nest[i]);
+  }
+  if (deepest > DTREE_GDN_MAX_NESTED_BRANCHES)
+    return fail(DTREE_E_TREE, "GatedDeltaNet tree recurrence: " + std::to_string(deepest) +
+                                  " nested branching nodes, beyond the " +
+                                  std::to_string(DTREE_GDN_MAX_NESTED_BRANCHES) + " its state stack holds");
+  return DTREE_OK;
+}
 
 extern "C" int dtree_gdn_layer_prep(const DtreeGdnArgs* a, hipStream_t stream) {
   if (int rc = gdn_layer_check(a, "gdn_layer_prep")) return rc;
@@ -1240,10 +1265,29 @@ extern "C" int dtree_gdn_layer_gated_norm(const DtreeGdnArgs* a, hipStream_t str
   return DTREE_OK;
 }
 
+// A commit's destination: both buffers given (and each either the source
+// itself or disjoint from it) or neither (in place).
+static int commit_dest_check(const DtreeGdnArgs* a, const char* what) {
+  const size_t C = 2 * (size_t)a->num_k_heads * a->head_k_dim + (size_t)a->num_v_heads * a->head_v_dim;
+  const size_t wb = (size_t)a->conv_keep * C * sizeof(float);
+  const size_t sb = (size_t)a->num_v_heads * a->head_v_dim * a->head_k_dim * sizeof(float);
+  auto disjoint = [](const void* x, const void* y, size_t n) {
+    const char* p = static_cast<const char*>(x);
+    const char* q = static_cast<const char*>(y);
+    return p == q || p + n <= q || q + n <= p;
+  };
+  if ((a->window_out == nullptr) != (a->state_out == nullptr))
+    return ::dtree::fail(DTREE_E_ARG, std::string(what) + ": window_out and state_out are given together or not at all");
+  if (a->window_out && !(disjoint(a->window, a->window_out, wb) && disjoint(a->state, a->state_out, sb)))
+    return ::dtree::fail(DTREE_E_ARG, std::string(what) + ": a commit destination partly overlaps its source");
+  return DTREE_OK;
+}
+
 extern "C" int dtree_gdn_layer_commit(const DtreeGdnArgs* a, hipStream_t stream) {
   if (int rc = gdn_layer_check(a, "gdn_layer_commit")) return rc;
   DTREE_REQUIRE(a->proj && a->window && a->state && a->q && a->k && a->v && a->g && a->beta,
                 "gdn_layer_commit: null pointer");
+  if (int rc = commit_dest_check(a, "gdn_layer_commit")) return rc;
   const int C = 2 * a->num_k_heads * a->head_k_dim + a->num_v_heads * a->head_v_dim;
   const int rpw = 256 / (128 / 4);
   GdnParams p{};
@@ -1252,7 +1296,9 @@ extern "C" int dtree_gdn_layer_commit(const DtreeGdnArgs* a, hipStream_t stream)
   p.T = a->rows_padded; p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->head_v_dim; p.rpw = rpw;
   const int conv_blocks = (C + 255) / 256;
   const int state_blocks = a->num_v_heads * (a->head_v_dim / rpw);
-  gdn_commit_kernel<128><<<conv_blocks + state_blocks, 256, 0, stream>>>(p, a->proj, a->ld_proj, a->window, C,
+  p.state_out = a->state_out;
+  gdn_commit_kernel<128><<<conv_blocks + state_blocks, 256, 0, stream>>>(p, a->proj, a->ld_proj, a->window,
+                                                                          a->window_out, C,
                                                                           a->conv_keep, conv_blocks);
   DTREE_LAUNCH_CHECK("gdn_layer_commit launch");
   return DTREE_OK;
@@ -1264,6 +1310,7 @@ extern "C" int dtree_gdn_layers_commit(const DtreeGdnArgs* a, int32_t num_layers
     if (int rc = gdn_layer_check(&a[i], "gdn_layers_commit")) return rc;
     DTREE_REQUIRE(a[i].proj && a[i].window && a[i].state && a[i].k && a[i].v && a[i].g && a[i].beta,
                   "gdn_layers_commit: null pointer");
+    if (int rc = commit_dest_check(&a[i], "gdn_layers_commit")) return rc;
     DTREE_REQUIRE(a[i].desc == a[0].desc && a[i].rows_padded == a[0].rows_padded &&
                       a[i].num_k_heads == a[0].num_k_heads && a[i].num_v_heads == a[0].num_v_heads &&
                       a[i].conv_keep == a[0].conv_keep && a[i].ld_proj == a[0].ld_proj,
@@ -1281,7 +1328,7 @@ extern "C" int dtree_gdn_layers_commit(const DtreeGdnArgs* a, int32_t num_layers
     CommitBatch b{};
     for (int i = 0; i < nl; ++i) {
       const DtreeGdnArgs& x = a[l0 + i];
-      b.l[i] = CommitLayer{x.proj, x.window, x.state, x.k, x.v, x.g, x.beta};
+      b.l[i] = CommitLayer{x.proj, x.window, x.state, x.k, x.v, x.g, x.beta, x.window_out, x.state_out};
     }
     gdn_commit_layers_kernel<128><<<dim3(conv_blocks + state_blocks, nl), 256, 0, stream>>>(p, b, a[0].ld_proj, C,
                                                                                           a[0].conv_keep,

@@ -16,7 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
 MAX_NODES = 128
 MASK_WORDS = 4
 PAGE = 64
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 E_OK, E_ARG, E_HIP, E_TREE, E_WORKSPACE = 0, -1, -2, -3, -4
 
@@ -105,6 +105,7 @@ class GdnArgs(C.Structure):
         ("y", C.c_void_p),
         ("norm_w", C.c_void_p), ("eps", C.c_float),
         ("out", C.c_void_p), ("out_lo", C.c_void_p), ("out_layout", C.c_int32), ("ld_out", C.c_int32),
+        ("window_out", C.c_void_p), ("state_out", C.c_void_p),
     ]
 
 
@@ -128,6 +129,7 @@ SIGNATURES = {
     "dtree_tree_attention": (C.c_int, [C.POINTER(AttnArgs), _vp]),
     "dtree_tree_attention_noalloc_max_bytes": (_sz, []),
     "dtree_tree_attention_noalloc": (C.c_int, [C.POINTER(AttnArgs), _vp]),
+    "dtree_attention_status": (C.c_int, [_vp, _vp, _vp]),
     "dtree_lmhead_candidates_bytes": (_sz, [_i32]),
     "dtree_lmhead_candidate_blocks": (C.c_int, [_i32, _i32]),
     "dtree_lmhead_argmax": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _f32, _vp,
@@ -150,6 +152,7 @@ SIGNATURES = {
     "dtree_gdn_commit": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                    _vp]),
     "dtree_gdn_args_bytes": (_sz, []),
+    "dtree_gdn_tree_check": (C.c_int, [_vp, _i32]),
     "dtree_gdn_layer_prep": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_recurrence": (C.c_int, [C.POINTER(GdnArgs), _vp]),
     "dtree_gdn_layer_prep_recurrence": (C.c_int, [C.POINTER(GdnArgs), _vp]),

@@ -390,7 +390,7 @@ class Qwen35TargetAdapter(Qwen3TargetAdapter):
         eng = model.engine
         eng.set_step([0] * L, [0] * L, parents, P, aux=True, accepted=keep)
         eng.launch_compact(cache, eng.stream_handle(), select_hidden=False, aux=True)
-        cache.offset = P + len(keep)
+        eng._keep_commit(cache, P, len(keep))
 
     def cache_summary(self, cache: Qwen35Cache) -> str:
         c = cache.cfg

@@ -115,7 +115,14 @@ class Qwen35Cache:
     attention layers and, per GatedDeltaNet layer, the conv window
     [K - 1, conv_dim] and the recurrent state [Hv, Dv, Dk], both fp32 (the
     ArraysCache entries [conv_state, state] of mlx-lm, qwen35_tree.py:85-101).
-    ``offset`` counts committed positions, as the KVCache offset does."""
+    ``offset`` counts committed positions, as the KVCache offset does.
+
+    The windows and states are held twice: ``windows`` / ``states`` are the
+    committed ones, ``windows_next`` / ``states_next`` the spare that a tree
+    commit writes (it reads the committed state and the accepted path).
+    ``flip()`` makes the spare the committed state. A verify step that is not
+    kept (``commit=False``) therefore leaves the state it started from
+    untouched and can be replayed as it is."""
 
     def __init__(self, cfg, capacity: int, device="cuda", page_order: torch.Tensor | None = None):
         self.cfg = cfg
@@ -125,11 +132,35 @@ class Qwen35Cache:
                                device=device, page_order=page_order)
         dev = torch.device(device)
         nG = len(self.gdn_layers)
-        self.windows = torch.zeros(nG, cfg.linear_conv_kernel_dim - 1, cfg.conv_dim, dtype=torch.float32, device=dev)
-        self.states = torch.zeros(nG, cfg.linear_num_value_heads, cfg.linear_value_head_dim,
-                                  cfg.linear_key_head_dim, dtype=torch.float32, device=dev)
+        self._windows = torch.zeros(2, nG, cfg.linear_conv_kernel_dim - 1, cfg.conv_dim, dtype=torch.float32,
+                                    device=dev)
+        self._states = torch.zeros(2, nG, cfg.linear_num_value_heads, cfg.linear_value_head_dim,
+                                   cfg.linear_key_head_dim, dtype=torch.float32, device=dev)
+        self.parity = 0
         self.slot = {li: i for i, li in enumerate(self.attn_layers)}
         self.slot.update({li: i for i, li in enumerate(self.gdn_layers)})
+
+    @property
+    def windows(self) -> torch.Tensor:
+        """Committed conv windows [nG, K - 1, conv_dim]."""
+        return self._windows[self.parity]
+
+    @property
+    def states(self) -> torch.Tensor:
+        """Committed recurrent states [nG, Hv, Dv, Dk]."""
+        return self._states[self.parity]
+
+    @property
+    def windows_next(self) -> torch.Tensor:
+        return self._windows[1 - self.parity]
+
+    @property
+    def states_next(self) -> torch.Tensor:
+        return self._states[1 - self.parity]
+
+    def flip(self) -> None:
+        """Keep the last commit: its output becomes the committed state."""
+        self.parity = 1 - self.parity
 
     @property
     def offset(self) -> int:
@@ -146,5 +177,5 @@ class Qwen35Cache:
     def reset(self, offset: int = 0) -> None:
         self.kv.offset = offset
         if offset == 0:
-            self.windows.zero_()
-            self.states.zero_()
+            self._windows.zero_()
+            self._states.zero_()

@@ -364,7 +364,7 @@ class DFlashDraftEngine(Qwen3TreeEngine):
                                           self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "rope table")
         write = cache.mode == "kv"
         # the context-only store's page table covers its sink + window only
-        self.attn_max_past = self.max_past if write else cache.capacity
+        self.attn_max_past = self.attn_grid_past(P) if write else cache.capacity
         self._launch_layers(cache.store, st, norm_hidden=True, write_cache=write)
         if write:
             for lc in cache.layers:

@@ -172,9 +172,12 @@ class TreeEngineBase:
         self._desc_event.record()
         self._aux_event.record()
         self.lm_in = torch.zeros(self.MP, H, dtype=bf16, device=dev)
-        self.result = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32, device=dev)
-        self.result_host = torch.zeros(3 + 2 * N.MAX_NODES, dtype=torch.int32).pin_memory()
+        # walk result [n, bonus, L, accepted[MAX], posterior[MAX]] + the attention
+        # status word (dtree_attention_status), read back together
+        self.result = torch.zeros(4 + 2 * N.MAX_NODES, dtype=torch.int32, device=dev)
+        self.result_host = torch.zeros(4 + 2 * N.MAX_NODES, dtype=torch.int32).pin_memory()
         self._result_np = self.result_host.numpy()
+        self._step_past = 0  # P of the step the descriptor holds (host copy)
         self._graphs: dict = {}
         self._dead_graphs: list = []
         self._tree_ws = None
@@ -221,6 +224,8 @@ class TreeEngineBase:
         pinned, dst, ev, rec = ((self.desc_aux_pinned, self.desc_aux, self._aux_event, self._desc_aux_rec) if aux
                                 else (self.desc_pinned, self.desc, self._desc_event, self._desc_rec))
         ev.synchronize()  # the previous upload from this pinned buffer has finished
+        if not aux:
+            self._step_past = int(past_length)
         rec["past_length"] = int(past_length)
         rec["num_nodes"] = L
         rec["n_accepted"] = 0 if accepted is None else len(accepted)
@@ -356,6 +361,14 @@ class TreeEngineBase:
             self.ss.data_ptr() if ss else None, c.hidden_size // 32 if ss else 0, c.rms_norm_eps,
             logits_ptr, self.cand.data_ptr(), st), "lm head")
 
+    STATUS_SLOT = 3 + 2 * N.MAX_NODES
+
+    def launch_attention_status(self, ws: torch.Tensor, st: int) -> None:
+        """ORs the attention workspace's error word into the result's status
+        slot (checked by read_result) and clears it."""
+        N.check(self.lib.dtree_attention_status(ws.data_ptr(), self.result.data_ptr() + 4 * self.STATUS_SLOT, st),
+                "attention status")
+
     def launch_walk(self, st: int, aux: bool = False) -> None:
         d = self.desc_aux if aux else self.desc
         N.check(self.lib.dtree_accept_walk(d.data_ptr(), self.cand.data_ptr(), self.n_cand, self.MP,
@@ -403,6 +416,7 @@ class TreeEngineBase:
                 self._tree_ws = torch.zeros(need, dtype=torch.uint8, device=self.dev)
             ws_ptr, ws_bytes = self._tree_ws.data_ptr(), self._tree_ws.numel()
         self._desc_event.synchronize()  # no host upload into the descriptor is still in flight
+        self._step_past = int(past_length)
         N.check(self.lib.dtree_tree_build(x.data_ptr(), V, D, V, k, budget, int(root_token), int(past_length),
                                           ws_ptr, ws_bytes, self.desc.data_ptr(), self.tree_out.data_ptr(), None,
                                           None, st), "tree build")
@@ -433,8 +447,13 @@ class TreeEngineBase:
             self.launch_verify(cache, st)
         res = self.read_result(tree=True)
         if commit:
-            cache.offset = P + len(res.accepted)
+            self._keep_commit(cache, P, len(res.accepted))
         return res, self.tree_lists(root_token)
+
+    def _keep_commit(self, cache, past_length: int, n_accepted: int) -> None:
+        """The host keeps a verify step's commit: the offset advances over the
+        accepted rows that compaction moved to [P, P + n)."""
+        cache.offset = past_length + n_accepted
 
     def read_result(self, stream=None, tree: bool = False) -> StepResult:
         s = torch.cuda.current_stream() if stream is None else stream
@@ -446,6 +465,10 @@ class TreeEngineBase:
                                         self.tree_out_host.numel() * 4, _D2H, s.cuda_stream), "tree copy")
         _hip_check(h.hipStreamSynchronize(s.cuda_stream), "walk result wait")
         r = self._result_np
+        if r[self.STATUS_SLOT]:
+            self.result[self.STATUS_SLOT:].zero_()
+            raise N.DtreeError("tree attention: a split's bounded wait gave up (DTREE_E_ATTN_WAIT); this step's "
+                               "attention output is incomplete and must be recomputed")
         n, bonus, L = int(r[0]), int(r[1]), int(r[2])
         return StepResult(accepted=r[3:3 + n].tolist(), bonus_token=bonus,
                           posterior=r[3 + N.MAX_NODES:3 + N.MAX_NODES + L].tolist())
@@ -463,7 +486,7 @@ class TreeEngineBase:
             self.launch_verify(cache, st)
         res = self.read_result()
         if commit:
-            cache.offset = P + len(res.accepted)
+            self._keep_commit(cache, P, len(res.accepted))
         return res
 
     def forward_only(self, cache: PagedKVCache, tokens, positions, parents, norm_hidden=False) -> None:
@@ -494,14 +517,31 @@ class TreeEngineBase:
     # (a new cache may reuse a dead one's id). When a cache dies its graph is
     # queued and destroyed at the next launch, after the stream has drained
     # (the finalizer itself may run at any point, e.g. during another capture).
+    # Prefix lengths an attention grid is sized for: the step's P rounded up
+    # to one of these (never past max_past), so the attention design and its
+    # split count follow the prefix the step has, not the longest prefix the
+    # engine may grow to (a 1024-key step of an engine sized for 4096 keys
+    # runs the 1024-key grid). Graphs are kept per grid size.
+    ATTN_GRID_PAST = (256, 512, 1024, 1536, 2048, 3072, 4096, 6144, 8192, 12288, 16384)
+
+    def attn_grid_past(self, past_length: int) -> int:
+        for b in self.ATTN_GRID_PAST:
+            if past_length <= b:
+                return min(b, self.max_past)
+        return self.max_past
+
+    def _graph_key(self, cache):
+        return (id(cache), self.attn_grid_past(self._step_past))
+
     def _graph_for(self, cache: PagedKVCache) -> int:
         self._destroy_pending()
-        ent = self._graphs.get(id(cache))
+        key = self._graph_key(cache)
+        ent = self._graphs.get(key)
         if ent is not None:
             ref, g = ent
             if ref() is cache:
                 return g
-            self._graphs.pop(id(cache))
+            self._graphs.pop(key)
             self._dead_graphs.append(g)
             self._destroy_pending()
         return self.capture_verify(cache)
@@ -531,7 +571,7 @@ class TreeEngineBase:
         ex = C.c_void_p()
         N.check(self.lib.dtree_graph_end(h, C.byref(ex)), "graph end")
         torch.cuda.current_stream().wait_stream(side)
-        key, graphs, dead = id(cache), self._graphs, self._dead_graphs
+        key, graphs, dead = self._graph_key(cache), self._graphs, self._dead_graphs
 
         def on_cache_dead(_ref, key=key, graphs=graphs, dead=dead):
             ent = graphs.get(key)
@@ -567,8 +607,9 @@ class Qwen3TreeEngine(TreeEngineBase):
         self.rope_sin = torch.zeros(MP, c.head_dim // 2, dtype=f32, device=dev)
         aws = self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim, self.max_past, self.MP)
         self.attn_ws = torch.zeros(aws, dtype=torch.uint8, device=dev)
-        # Prefix length the attention grid is sized for; the cache's page table
-        # must cover it (the kernels read page entries before P is known).
+        # Prefix length the attention grid is sized for (launch_forward sets it
+        # from the step's P); the cache's page table must cover it (the
+        # kernels read page entries before P is known).
         self.attn_max_past = self.max_past
 
     # ---- sizes ---------------------------------------------------------------
@@ -613,7 +654,9 @@ class Qwen3TreeEngine(TreeEngineBase):
             self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
             c.head_dim, c.rope_theta,
             self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
+        self.attn_max_past = self.attn_grid_past(self._step_past)
         self._launch_layers(cache, st, norm_hidden=norm_hidden)
+        self.launch_attention_status(self.attn_ws, st)
 
     def _launch_layers(self, cache: PagedKVCache, st: int, norm_hidden: bool = False, write_cache: bool = True) -> None:
         """The decoder layers over the rows already in x / xg / ss (and the RoPE
@@ -725,7 +768,7 @@ class Qwen3TreeEngine(TreeEngineBase):
                     a.ld_out = c.q_dim; a.out_layout = self.w.layout
                     a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = D
                     a.rows_padded = 128; a.scale = D ** -0.5
-                    a.max_past_length = self.max_past; a.write_cache = 1
+                    a.max_past_length = self.attn_grid_past(P0 + 128 * ch); a.write_cache = 1
                     a.workspace = pf["attn_ws"].data_ptr(); a.workspace_bytes = pf["attn_ws"].numel()
                     N.check(self.lib.dtree_tree_attention(C.byref(a), st), "prefill attention")
                 self._long_gemm("o", pf["attn"], c.q_dim, lw.wo, N.EPI_RESIDUAL, rows, st, out_f32=pf["x"],
@@ -741,6 +784,7 @@ class Qwen3TreeEngine(TreeEngineBase):
             cache.offset = P0 + n
             if self.layer_ids:
                 hid_parts.append(pf["hidden"][:n].clone())
+        self.launch_attention_status(pf["attn_ws"], st)
         logits = self._prefill_logits(pf, n, st) if want_logits else None
         hidden = torch.cat(hid_parts, 0) if hid_parts else None
         return logits, hidden

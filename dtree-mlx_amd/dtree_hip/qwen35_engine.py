@@ -69,6 +69,16 @@ class Qwen35TreeEngine(TreeEngineBase):
         return {"in": (c.in_proj_dim, H), "out": (H, c.value_dim), "qkv": (c.attn_qkv_dim, H),
                 "o": (H, c.q_dim), "gu": (2 * F, H), "down": (H, F)}
 
+    def set_step(self, tokens, positions, parents, past_length: int, stream=None, ancestors=None,
+                 aux: bool = False, accepted=None) -> None:
+        # Trees past 32 nodes run the depth-first recurrence, whose state stack
+        # holds a bounded nesting of branching nodes: reject deeper ones here.
+        if len(parents) > 32:
+            arr = (C.c_int32 * len(parents))(*[int(p) for p in parents])
+            N.check(self.lib.dtree_gdn_tree_check(arr, len(parents)), "GatedDeltaNet tree")
+        super().set_step(tokens, positions, parents, past_length, stream=stream, ancestors=ancestors, aux=aux,
+                         accepted=accepted)
+
     def new_cache(self, page_order=None) -> Qwen35Cache:
         return Qwen35Cache(self.cfg, self.max_past + self.max_nodes, device=self.dev, page_order=page_order)
 
@@ -109,7 +119,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         a.out_layout = self.w.layout
         a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
         a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
-        a.max_past_length = self.max_past; a.write_cache = 1 if write_cache else 0
+        a.max_past_length = self.attn_grid_past(self._step_past); a.write_cache = 1 if write_cache else 0
         a.workspace = self.attn_ws.data_ptr(); a.workspace_bytes = self.attn_ws.numel()
         a.rope_dims = c.rope_dims; a.gated = 1
         N.check(self.lib.dtree_tree_attention(C.byref(a), st), "tree attention")
@@ -157,6 +167,7 @@ class Qwen35TreeEngine(TreeEngineBase):
             N.check(self.lib.dtree_rownorm(self.x.data_ptr(), H, self.MP, H, self.ss.data_ptr(), H // 32,
                                            self.w.final_norm.data_ptr(), c.rms_norm_eps,
                                            self.norm_hidden.data_ptr(), H, st), "rownorm")
+        self.launch_attention_status(self.attn_ws, st)
 
     def launch_compact(self, cache: Qwen35Cache, st: int, select_hidden: bool = True, aux: bool = False) -> None:
         """commit_qwen35_tree_path: KV compaction of the attention layers (+ the
@@ -173,7 +184,9 @@ class Qwen35TreeEngine(TreeEngineBase):
         self._commit_gdn(cache, st, d)
 
     def _commit_gdn(self, cache: Qwen35Cache, st: int, desc: torch.Tensor) -> None:
-        """Every GatedDeltaNet layer's commit in one launch (dtree_gdn_layers_commit)."""
+        """Every GatedDeltaNet layer's commit in one launch
+        (dtree_gdn_layers_commit), from the committed windows / states into
+        the cache's spare pair; cache.flip() keeps it."""
         layers = list(cache.gdn_layers)
         if not layers:
             return
@@ -181,7 +194,19 @@ class Qwen35TreeEngine(TreeEngineBase):
         for i, li in enumerate(layers):
             arr[i] = self.gdn_args(li, cache)
             arr[i].desc = desc.data_ptr()
+            gi = cache.slot[li]
+            arr[i].window_out = cache.windows_next[gi].data_ptr()
+            arr[i].state_out = cache.states_next[gi].data_ptr()
         N.check(self.lib.dtree_gdn_layers_commit(arr, len(layers), st), "gdn commit")
+
+    def _graph_key(self, cache: Qwen35Cache):
+        # The graph reads the committed pair and writes the spare one, so each
+        # buffer parity has its own graph (and each attention grid size).
+        return (id(cache), cache.parity, self.attn_grid_past(self._step_past))
+
+    def _keep_commit(self, cache: Qwen35Cache, past_length: int, n_accepted: int) -> None:
+        cache.offset = past_length + n_accepted
+        cache.flip()
 
     def commit_chain(self, cache: Qwen35Cache, tokens, norm_hidden: bool = False) -> None:
         """Forward a causal chain of <= max_nodes tokens and commit all of it:
@@ -197,7 +222,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         self.set_step(tokens, [P + i for i in range(n)], [-1] + list(range(n - 1)), P, accepted=list(range(n)))
         self.launch_forward(cache, st, norm_hidden=norm_hidden)
         self._commit_gdn(cache, st, self.desc)
-        cache.offset = P + n
+        self._keep_commit(cache, P, n)
 
     def prefill(self, cache: Qwen35Cache, tokens, chunk: int | None = None) -> None:
         """Causal prefill through the tree path: fully accepted chains of up to
@@ -334,7 +359,7 @@ class Qwen35TreeEngine(TreeEngineBase):
                         a.ld_out = c.q_dim; a.out_layout = self.w.layout
                         a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads
                         a.head_dim = D; a.rows_padded = 128; a.scale = D ** -0.5
-                        a.max_past_length = self.max_past; a.write_cache = 1
+                        a.max_past_length = self.attn_grid_past(P0 + 128 * ch); a.write_cache = 1
                         a.workspace = pf["attn_ws"].data_ptr(); a.workspace_bytes = pf["attn_ws"].numel()
                         a.rope_dims = c.rope_dims; a.gated = 1
                         N.check(self.lib.dtree_tree_attention(C.byref(a), st), "prefill attention")
@@ -352,6 +377,7 @@ class Qwen35TreeEngine(TreeEngineBase):
             cache.offset = P0 + n
             if self.layer_ids:
                 hid_parts.append(pf["hidden"][:n].clone())
+        self.launch_attention_status(pf["attn_ws"], st)
         logits = self._prefill_logits(pf, n, st) if want_logits else None
         hidden = torch.cat(hid_parts, 0) if hid_parts else None
         return logits, hidden

@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define DTREE_ABI_VERSION 5
+#define DTREE_ABI_VERSION 6
 
 #define DTREE_OK 0
 #define DTREE_E_ARG (-1)      /* bad shape / pointer / enum */
@@ -243,6 +243,19 @@ int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
  */
 size_t dtree_tree_attention_noalloc_max_bytes(void);
 int dtree_tree_attention_noalloc(const DtreeAttnArgs* args, hipStream_t stream);
+/* Status of the attention launches on a workspace, in stream order: the
+ * per-KV-group kernel's splits meet at a bounded wait, and a split that gives
+ * up (another split was not resident for ~2 s, e.g. when work on another
+ * stream holds CUs) sets the workspace's error word and leaves its share of
+ * the output unwritten. This ORs that word into *status (device memory; 1 =
+ * a wait gave up since the last query) and clears it. workspace = NULL reads
+ * the allocation-free entry's device scratch of the current GPU, which
+ * dtree_tree_attention_noalloc clears before each call: query it after each
+ * such call. A step whose status is set must be recomputed; the wait's
+ * counters return to zero by themselves, so the next launch is sound. The
+ * reference's scaled_dot_product_attention (qwen3_tree.py:69-76) has no such
+ * failure mode; this is the error row of the boundary for it. */
+int dtree_attention_status(void* workspace, int32_t* status, hipStream_t stream);
 
 /*
  * Fused LM head + argmax (adapters.py:114-118, 489-492, first index on ties
@@ -422,7 +435,8 @@ int dtree_gdn_commit(const float* x, float* window, int32_t channels, int32_t ke
  *  dtree_gdn_layer_gated_norm: out = rms_norm(y) * norm_w * silu(z) per value
  *    head (:322) as bf16 [hi, lo] (out_lo optional) for out_proj; rows >= L zero.
  *  dtree_gdn_layer_commit: commit_qwen35_tree_path (:708-732) for this layer:
- *    replays desc->accepted[0 .. n_accepted) on window and state in place.
+ *    replays desc->accepted[0 .. n_accepted) on window and state (in place,
+ *    or into window_out / state_out).
  *
  * The per-node buffers (proj, q, k, v, g, beta) must stay untouched between
  * the layer's prep and its commit. Compiled for Dk = Dv = 128.
@@ -441,9 +455,24 @@ typedef struct DtreeGdnArgs {
   float* y;                          /* [rows][Hv][Dv] */
   const uint16_t* norm_w; float eps; /* gated RMSNorm weight [Dv] (bf16) */
   uint16_t* out; uint16_t* out_lo; int32_t out_layout; int32_t ld_out;
+  /* Commit destination (dtree_gdn_layer_commit / dtree_gdn_layers_commit):
+   * the new window and state go to window_out / state_out, read from window /
+   * state. NULL (both) commits in place. A second buffer lets a verify step
+   * run its commit without touching the state it started from, so it can be
+   * replayed (the host flips the two buffers when it keeps the commit). */
+  float* window_out; float* state_out;
 } DtreeGdnArgs;
 
 size_t dtree_gdn_args_bytes(void);
+/* Host check of a tree for the recurrence (the reference's tree kernel,
+ * qwen35_tree_kernels.py:8-83, takes any tree): trees of more than 32 nodes
+ * run depth first with a register stack of the states of branching nodes,
+ * which holds at most DTREE_GDN_MAX_NESTED_BRANCHES nested ones; DTREE_E_TREE
+ * for a tree beyond that (or malformed parents), else DTREE_OK. Trees of up
+ * to 32 nodes always pass. The device tree build (depth <= 18) never exceeds
+ * it; call this for caller-built trees before the recurrence. */
+#define DTREE_GDN_MAX_NESTED_BRANCHES 31
+int dtree_gdn_tree_check(const int32_t* parents, int32_t num_nodes);
 int dtree_gdn_layer_prep(const DtreeGdnArgs* args, hipStream_t stream);
 int dtree_gdn_layer_recurrence(const DtreeGdnArgs* args, hipStream_t stream);
 /* dtree_gdn_layer_prep followed by dtree_gdn_layer_recurrence (the same

@@ -73,6 +73,41 @@ def tree_gated_delta(q, k, v, g, beta, state, parents) -> tuple[np.ndarray, np.n
     return y, states
 
 
+def chain_conv1d(x: np.ndarray, base: np.ndarray, w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """tree_conv1d for a chain (parents t - 1) without the per-node windows:
+    input row j of node t is row t + j of (base ++ x). -> (out [T, C], the
+    last node's window [Keep, C])."""
+    x = np.asarray(x, np.float64)
+    base = np.asarray(base, np.float64)
+    w = np.asarray(w, np.float64)
+    keep = base.shape[0]
+    rows = np.concatenate([base, x], axis=0)
+    T = x.shape[0]
+    acc = np.zeros_like(x)
+    for j in range(keep + 1):
+        acc += rows[j:j + T] * w[j]
+    return silu(acc), rows[T:T + keep]
+
+
+def chain_gated_delta(q, k, v, g, beta, state) -> tuple[np.ndarray, np.ndarray]:
+    """tree_gated_delta for a chain, keeping only the running state:
+    -> (y [T, Hv, Dv], the last node's state [Hv, Dv, Dk])."""
+    q, k, v, g, beta = (np.asarray(a, np.float64) for a in (q, k, v, g, beta))
+    S = np.array(state, np.float64)
+    T, Hk, _ = k.shape
+    Hv, Dv = v.shape[1], v.shape[2]
+    grp = Hv // Hk
+    y = np.zeros((T, Hv, Dv))
+    for t in range(T):
+        S *= g[t][:, None, None]
+        kk = k[t][np.arange(Hv) // grp]
+        qq = q[t][np.arange(Hv) // grp]
+        delta = (v[t] - np.einsum("hvd,hd->hv", S, kk)) * beta[t][:, None]
+        S += delta[:, :, None] * kk[:, None, :]
+        y[t] = np.einsum("hvd,hd->hv", S, qq)
+    return y, S
+
+
 def root_path(parents, t: int) -> list[int]:
     path = []
     while t >= 0:

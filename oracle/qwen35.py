@@ -249,6 +249,35 @@ class OracleQwen35:
         vh = np.concatenate(sel, axis=-1) if sel else np.zeros((x.shape[0], 0), np.float32)
         return norm, vh, pending
 
+    def chain_prefill(self, ids, layers: int):
+        """The first `layers` layers over a causal chain of prompt tokens from
+        an empty cache, committing all of it: forward_tree + commit of the whole
+        chain, with the chain forms of the conv and the recurrence (no per-node
+        states kept, so long prompts fit). Returns (x after those layers, the
+        committed cache of those layers: (window, state) or (keys, values))."""
+        c = self.cfg
+        ids = np.asarray(ids)
+        T = len(ids)
+        pos = np.arange(T)
+        x = self.embed(ids)
+        out = []
+        for li in range(layers):
+            if c.is_linear(li):
+                xin, z, a, b = self.gdn_prep(li, x)
+                conv_out, win = gdn.chain_conv1d(xin, np.zeros((c.conv_kernel - 1, c.conv_dim)),
+                                                 np.asarray(self.w(li, "conv"), np.float64))
+                q, k, v, g, beta = self.gdn_inputs(li, conv_out, a, b)
+                y, state = gdn.chain_gated_delta(q, k, v, g, beta,
+                                                 np.zeros((c.lin_v_heads, c.lin_v_dim, c.lin_k_dim)))
+                o = self.gated_norm(li, y, z.reshape(T, c.lin_v_heads, c.lin_v_dim)).reshape(T, -1)
+                x = self.mlp(li, x + o @ self.w(li, "out").T)
+                out.append((win.astype(np.float32), state))
+            else:
+                empty = np.zeros((0, c.kv_heads, c.head_dim), np.float32)
+                x, pend = self.attn_layer(li, x, empty, empty, pos, np.tril(np.ones((T, T), bool)))
+                out.append((pend["k"], pend["v"]))
+        return x, out
+
     def commit(self, cache: Qwen35Cache, pending: list, parents, accepted) -> None:
         """commit_qwen35_tree_path: accepted = root path (accepted[0] = 0)."""
         if not accepted:

@@ -2,8 +2,10 @@
 from __future__ import annotations
 
 import ctypes as C
+import warnings
 
 import numpy as np
+import pytest
 import torch
 
 from dtree_hip import _native as N
@@ -87,7 +89,22 @@ def compare_accepted_path(res, child_maps, oracle_post, decided, log=print) -> i
     else:
         assert res.accepted[:k + 1] == o_acc[:k + 1], (res.accepted, o_acc, k)
         compared = k + 1
-    log(f"accepted path: device {res.accepted} bonus {res.bonus_token}; oracle {o_acc} bonus {o_bonus}; "
-        f"compared {compared} of {len(o_acc)} nodes" + ("" if k is None else f" (node {o_acc[k]} undecided)"))
-    assert compared >= 1
+    msg = (f"accepted path: device {res.accepted} bonus {res.bonus_token}; oracle {o_acc} bonus {o_bonus}; "
+           f"compared {compared} of {len(o_acc)} nodes" + ("" if k is None else f" (node {o_acc[k]} undecided)"))
+    log(msg)
+    # a record pytest -q shows in its warnings summary
+    warnings.warn(PathParityRecord(msg), stacklevel=2)
+    assert compared >= 1, msg
     return compared
+
+
+class PathParityRecord(UserWarning):
+    """How many accepted-path nodes a parity test compared bit for bit."""
+
+
+def require_path_compared(compared: int, what: str) -> None:
+    """Full-size steps: a path comparison that covered the root alone (its row
+    undecided, or the oracle walk stopping there) proves nothing; mark the
+    test xfail with the reason instead of passing it."""
+    if compared < 2:
+        pytest.xfail(f"{what}: the accepted-path comparison covered only {compared} node(s) (the root)")

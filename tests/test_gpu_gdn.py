@@ -166,12 +166,29 @@ def test_recurrence_forest_of_roots():
 
 def test_recurrence_past_the_stack_writes_nan():
     """32 nested branching nodes (a 65-node caterpillar) do not fit the
-    32-slot stack: every output is NaN, never a silently wrong value."""
+    32-slot stack: the kernel, called on such a tree anyway, writes NaN,
+    never a silently wrong value (the host check dtree_gdn_tree_check rejects
+    the tree before launch: tests/test_native_abi.py, and the hybrid engine
+    below)."""
     parents = _caterpillar(32)
     T = len(parents)
     q, k, v, g, beta, state = _layer_inputs(T, 13)
     y, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
     assert np.isnan(y).all()
+
+
+def test_hybrid_engine_rejects_trees_past_the_stack(gpu_device):
+    """The hybrid engine checks caller trees of more than 32 nodes on the host
+    (dtree_gdn_tree_check) and raises before any launch."""
+    from dtree_hip import Qwen35TreeEngine, Qwen35Weights, tiny_qwen35
+    cfg = tiny_qwen35()
+    w = Qwen35Weights.random(cfg, seed=5, device=gpu_device)
+    eng = Qwen35TreeEngine(cfg, w, max_past=64, max_nodes=96)
+    par = _caterpillar(32)
+    with pytest.raises(DtreeError, match="nested branching"):
+        eng.set_step([3] * len(par), [10] * len(par), par, 10)
+    ok = _caterpillar(31)
+    eng.set_step([3] * len(ok), [10] * len(ok), ok, 10)
 
 
 def test_recurrence_rejects_trees_past_96_nodes():
@@ -323,3 +340,17 @@ def test_layers_commit_in_one_launch(gpu_device, nl):
         for n in ("window", "state"):
             assert torch.equal(ly[n], o[n]), n
         assert not torch.equal(ly["state"], b["state"])  # the commit did advance the state
+    # into separate destinations: the same results, the sources untouched
+    for ly, b in zip(layers, before):
+        for n in ("window", "state"):
+            ly[n].copy_(b[n])
+    dst = [{n: torch.full_like(ly[n], float("nan")) for n in ("window", "state")} for ly in layers]
+    arr = (N.GdnArgs * nl)(*[args(ly) for ly in layers])
+    for i, d in enumerate(dst):
+        arr[i].window_out = d["window"].data_ptr(); arr[i].state_out = d["state"].data_ptr()
+    N.check(N.lib().dtree_gdn_layers_commit(arr, nl, stream()), "layers commit into spare buffers")
+    torch.cuda.synchronize()
+    for ly, d, o, b in zip(layers, dst, one, before):
+        for n in ("window", "state"):
+            assert torch.equal(d[n], o[n]), n
+            assert torch.equal(ly[n], b[n]), n

@@ -388,7 +388,65 @@ def test_tree_attention_matches_oracle(gpu_device, P, shape, attn_kernel):
     np.testing.assert_allclose(kc, k, rtol=1e-2, atol=1e-2)
     np.testing.assert_array_equal(vc, oq.bf16_to_f32(oq.f32_to_bf16_bits(v)))
     Hq = 32
-    assert int(ws[: Hq * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
+    assert int(ws[: 64 + Hq * 4].view(torch.int32).abs().sum()) == 0  # error word clear, counters self-reset
+
+
+@pytest.mark.parametrize("P,max_past,noalloc", [(1000, 1024, False), (1000, 1024, True), (3000, 4096, False)])
+def test_group_attention_give_up_is_reported(gpu_device, monkeypatch, P, max_past, noalloc):
+    """The per-KV-group kernel's bounded split wait, made to give up from the
+    host (DTREE_TEST_SPIN_LIMIT=0: a split that is not the last to arrive
+    stops waiting at once; every workgroup still runs to its end):
+    dtree_attention_status reports it and clears the word, the counters are
+    back at zero, and the next launch with the normal bound is correct and
+    reports nothing. Also through the allocation-free entry point (whose
+    16 MiB scratch holds the grid for 1024 keys)."""
+    monkeypatch.setenv("DTREE_ATTN_KERNEL", "group")
+    parents = random_tree(25, seed=3)
+    cache, out, ref, k, v, ws = _attention_case(gpu_device, P, parents, seed=5, max_past=max_past)
+    lib = N.lib()
+    status = torch.zeros(1, dtype=torch.int32, device=gpu_device)
+    ws_ptr = None if noalloc else ws.data_ptr()
+
+    def launch():
+        a = N.AttnArgs()
+        qkv = launch.qkv
+        a.qkv = qkv.data_ptr(); a.ld_qkv = qkv.shape[1]
+        a.q_norm = None; a.k_norm = None; a.eps = 1e-6
+        a.rope_cos = launch.cos.data_ptr(); a.rope_sin = launch.sin.data_ptr()
+        a.k_pages = cache.k_ptr(0); a.v_pages = cache.v_ptr(0); a.page_table = cache.page_table.data_ptr()
+        a.desc = launch.desc.data_ptr(); a.out = out.data_ptr(); a.ld_out = out.shape[1]
+        a.num_heads = 32; a.num_kv_heads = 8; a.head_dim = 128; a.rows_padded = 32
+        a.scale = 128 ** -0.5; a.max_past_length = max_past; a.write_cache = 0
+        a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+        f = lib.dtree_tree_attention_noalloc if noalloc else lib.dtree_tree_attention
+        N.check(f(C.byref(a), stream()), "attention")
+        N.check(lib.dtree_attention_status(ws_ptr, status.data_ptr(), stream()), "attention status")
+        torch.cuda.synchronize()
+
+    g = np.random.default_rng(9)
+    launch.qkv = torch.from_numpy(g.standard_normal((32, (32 + 16) * 128)).astype(np.float32)).to(gpu_device)
+    depth = [0] * 25
+    for i in range(1, 25):
+        depth[i] = depth[parents[i]] + 1
+    launch.desc = device_desc([0] * 25, [P + d for d in depth], parents, P, gpu_device)
+    launch.cos = torch.zeros(32, 64, device=gpu_device)
+    launch.sin = torch.zeros(32, 64, device=gpu_device)
+    N.check(lib.dtree_rope_table(launch.desc.data_ptr(), 32, 128, 1e6, launch.cos.data_ptr(), launch.sin.data_ptr(),
+                                 stream()))
+    launch()
+    assert int(status.item()) == 0
+    want = out.clone()
+    monkeypatch.setenv("DTREE_TEST_SPIN_LIMIT", "0")
+    out.fill_(7.0)
+    launch()
+    assert int(status.item()) == 1, "a give-up was not reported"
+    monkeypatch.delenv("DTREE_TEST_SPIN_LIMIT")
+    status.zero_()
+    launch()
+    assert int(status.item()) == 0  # the word was cleared, nothing new
+    assert torch.equal(out, want)
+    if not noalloc:
+        assert int(ws[:4096].view(torch.int32).abs().sum()) == 0  # error word and counters at zero
 
 
 @pytest.mark.parametrize("P", [0, 129, 1000])
@@ -408,7 +466,7 @@ def test_tree_attention_more_than_32_nodes(gpu_device, P, MP, L, shape, attn_ker
     vc = bf16_f32(cache.logical_values(0, P + L))[P:]
     np.testing.assert_allclose(kc, k, rtol=1e-2, atol=1e-2)
     np.testing.assert_array_equal(vc, oq.bf16_to_f32(oq.f32_to_bf16_bits(v)))
-    assert int(ws[: 32 * (MP // 32) * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
+    assert int(ws[: 64 + 32 * (MP // 32) * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
 
 
 @pytest.mark.parametrize("P,max_past,MP,L", [(0, 64, 32, 25), (100, 128, 32, 25), (300, 2000, 32, 25),

@@ -27,7 +27,7 @@ from oracle import qwen35 as o35
 from oracle import tree as otree
 from oracle.qwen3 import bf16_to_f32
 
-from gpu_util import bf16_f32, compare_accepted_path
+from gpu_util import bf16_f32, compare_accepted_path, require_path_compared
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
@@ -60,7 +60,27 @@ def _close(got, want, what):
     assert err <= TOL * max(1.0, np.abs(want).max()), f"{what}: max err {err}"
 
 
-def _run(cfg, P, layer_ids, dev, norm_jitter=0.1, quant="bf16", log=print, check_prefill=False, budget=24):
+def _check_long_prefill(orc, cfg, cache, prefix, layers, log=print):
+    """The long-M prefill at full size against the oracle's causal chain
+    (chain_prefill: forward + commit of the whole prompt) over the first
+    `layers` layers: each GatedDeltaNet layer's committed window and state and
+    each attention layer's K / V at every position."""
+    t0 = time.time()
+    P = len(prefix)
+    _, want = orc.chain_prefill(prefix, layers)
+    for li in range(layers):
+        s = cache.slot[li]
+        if cfg.is_linear(li):
+            _close(cache.windows[s].cpu().numpy(), want[li][0], f"prefill window {li}")
+            _close(cache.states[s].cpu().numpy(), want[li][1], f"prefill state {li}")
+        else:
+            _close(bf16_f32(cache.kv.logical_keys(s, P)), want[li][0], f"prefill keys {li}")
+            _close(bf16_f32(cache.kv.logical_values(s, P)), want[li][1], f"prefill values {li}")
+    log(f"long prefill: {layers} layers' committed state at P={P} match the oracle ({time.time() - t0:.1f}s)")
+
+
+def _run(cfg, P, layer_ids, dev, norm_jitter=0.1, quant="bf16", log=print, check_prefill=False, budget=24,
+         check_long_prefill_layers=0):
     t0 = time.time()
     w = Qwen35Weights.random(cfg, seed=0, device=dev, norm_jitter=norm_jitter, quant=quant)
     eng = Qwen35TreeEngine(cfg, w, max_past=P + 64, layer_ids=layer_ids, max_nodes=budget + 1)
@@ -81,6 +101,8 @@ def _run(cfg, P, layer_ids, dev, norm_jitter=0.1, quant="bf16", log=print, check
             _close(cache.states[s].cpu().numpy(), oc.layers[li][1], f"prefill state {li}")
         for li in cfg.attention_layers:
             _close(bf16_f32(cache.kv.logical_keys(cache.slot[li], P)), oc.layers[li][0], f"prefill keys {li}")
+    if check_long_prefill_layers:
+        _check_long_prefill(orc, cfg, cache, prefix, check_long_prefill_layers, log)
     st = eng.stream_handle()
     tree = make_tree(root_token=prefix[-1] if P else 0, vocab=cfg.vocab_size, seed=2, budget=budget)
 
@@ -212,6 +234,43 @@ def test_qwen35_two_steps_graph_matches_eager(gpu_device):
     assert torch.equal(out[0][1], out[1][1]) and torch.equal(out[0][2], out[1][2])
 
 
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_qwen35_uncommitted_step_leaves_state(gpu_device, use_graph):
+    """verify(commit=False) leaves the committed windows and states bit for bit
+    as they were (its commit goes to the spare pair), so replays accept the
+    same path; a kept step afterwards commits exactly what a kept step alone
+    would have."""
+    cfg = tiny_qwen35()
+    w = Qwen35Weights.random(cfg, seed=5, device=gpu_device, norm_jitter=0.1)
+    tree = make_tree(root_token=7, vocab=cfg.vocab_size, seed=10)
+    out = []
+    for preview in (3, 0):
+        eng = Qwen35TreeEngine(cfg, w, max_past=128)
+        cache = eng.new_cache()
+        eng.prefill(cache, random_prefix(40, cfg.vocab_size, seed=6))
+        torch.cuda.synchronize()
+        P = cache.offset
+        win0, st0 = cache.windows.clone(), cache.states.clone()
+        first = None
+        for _ in range(preview):
+            r = eng.verify(cache, tree.tokens, tree.positions(P), tree.parents, use_graph=use_graph, commit=False)
+            torch.cuda.synchronize()
+            assert cache.offset == P
+            assert torch.equal(cache.windows, win0) and torch.equal(cache.states, st0)
+            first = first or r
+            assert (r.accepted, r.bonus_token) == (first.accepted, first.bonus_token)
+        r = eng.verify(cache, tree.tokens, tree.positions(P), tree.parents, use_graph=use_graph, commit=True)
+        torch.cuda.synchronize()
+        if first is not None:
+            assert (r.accepted, r.bonus_token) == (first.accepted, first.bonus_token)
+        assert cache.offset == P + len(r.accepted)
+        assert not torch.equal(cache.states, st0)
+        out.append((r.accepted, cache.windows.cpu(), cache.states.cpu()))
+        eng.release_graphs()
+    assert out[0][0] == out[1][0]
+    assert torch.equal(out[0][1], out[1][1]) and torch.equal(out[0][2], out[1][2])
+
+
 def test_qwen35_9b_q4_verify_step_prefix_8192_budget_64(gpu_device):
     """Qwen3.5-9B-shaped hybrid (hidden 4096), q4 weights including the tied
     LM head, 8192-token prefix, 65-node tree (draft budget 64)."""
@@ -223,9 +282,11 @@ def test_qwen35_9b_q4_verify_step_prefix_8192_budget_64(gpu_device):
     # margins fall under 2e-2 of the largest logit, so the argmax bar is
     # carried by the measured-error margin (`sure` rows) instead.
     _check(r, [1, 15, 30], min_confident=0.0)
+    require_path_compared(r["path_compared"], "Qwen3.5-9B-shaped q4 P=8192")
 
 
 def test_qwen35_4b_verify_step_prefix_2048(gpu_device):
     """Qwen3.5-4B-shaped hybrid at a 2048-token prefix with a 24-node tree."""
-    r = _run(QWEN35_4B, P=2048, layer_ids=[1, 15, 30], dev=gpu_device, norm_jitter=0.0)
+    r = _run(QWEN35_4B, P=2048, layer_ids=[1, 15, 30], dev=gpu_device, norm_jitter=0.0, check_long_prefill_layers=4)
     _check(r, [1, 15, 30])
+    require_path_compared(r["path_compared"], "Qwen3.5-4B-shaped bf16 P=2048")

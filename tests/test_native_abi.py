@@ -66,13 +66,14 @@ def test_workspace_queries():
     assert lib.dtree_lmhead_candidate_blocks(4096, 32) == 64
     assert lib.dtree_lmhead_candidate_blocks(4096, 128) == 128
     # attention: the larger of the two designs' workspaces.
-    # Per-head kernel: head counters (256-byte aligned) + one partial per head
-    # per 4-chunk workgroup (prefix 1024 = tree + 16 pages = 5 workgroups per head).
+    # Per-head kernel: a 64-byte header (error word) and the head counters,
+    # 256-byte aligned, + one partial per head per 4-chunk workgroup (prefix
+    # 1024 = tree + 16 pages = 5 workgroups per head).
     def head_ws(Hq, D, P, MP):
         nt = MP // 32
         ck = 64 if D == 128 else 32
         splits = (nt + (P + ck - 1) // ck + 3) // 4
-        return ((Hq * nt * 4 + 255) // 256) * 256 + Hq * nt * splits * (32 * D + 64) * 4
+        return ((64 + Hq * nt * 4 + 255) // 256) * 256 + Hq * nt * splits * (32 * D + 64) * 4
 
     # Per-KV-group kernel: 4 KB header (error word, counters) + at most one
     # partial (32 rows x head_dim fp32 + row max / sum) per head, query block
@@ -87,6 +88,7 @@ def test_workspace_queries():
         want = max(head_ws(Hq, D, P, MP), group_ws(Hq, D, P, MP))
         assert lib.dtree_attention_workspace_bytes(Hq, D, P, MP) == want, (Hq, D, P, MP)
     assert head_ws(32, 128, 1024, 32) == 256 + 32 * 5 * (32 * 128 + 64) * 4
+    assert head_ws(64, 128, 1024, 32) == 512 + 64 * 5 * (32 * 128 + 64) * 4
     assert lib.dtree_attention_workspace_bytes(32, 128, 1024, 48) == 0
 
 
@@ -121,6 +123,15 @@ def test_attention_and_gdn_layer_validation_without_gpu():
     g.ld_proj = 8192 + 4096  # b and a columns missing
     assert lib.dtree_gdn_layer_prep(C.byref(g), None) == -1
     assert b"ld_proj" in lib.dtree_last_error()
+    # commit destinations: both or neither, and never a partial overlap
+    g.ld_proj = 8192 + 4096 + 64
+    g.state = 1 << 32
+    g.window_out = 1 << 33
+    assert lib.dtree_gdn_layer_commit(C.byref(g), None) == -1
+    assert b"together" in lib.dtree_last_error()
+    g.state_out = (1 << 32) + 4096
+    assert lib.dtree_gdn_layer_commit(C.byref(g), None) == -1
+    assert b"overlaps" in lib.dtree_last_error()
 
 
 def _desc(parents, tokens=None, P=10):
@@ -170,3 +181,30 @@ def test_host_tree_validation():
     assert lib.dtree_step_desc_validate(C.byref(d), 32, 100, 50) == N.E_ARG
     d.accepted[1] = 2
     assert lib.dtree_step_desc_validate(C.byref(d), 32, 100, 50) == 0
+
+
+def test_gdn_tree_check_bounds_the_nested_branching():
+    """dtree_gdn_tree_check: trees of more than 32 nodes run the depth-first
+    recurrence, whose state stack holds 31 nested branching nodes. A
+    caterpillar (path node j also carries a leaf, so it has j branching
+    ancestors) with 31 branching nodes passes, with 32 it is DTREE_E_TREE;
+    32-node trees always pass; malformed parents are DTREE_E_TREE too."""
+    lib = N.lib()
+
+    def check(par):
+        arr = (C.c_int32 * len(par))(*par)
+        return lib.dtree_gdn_tree_check(arr, len(par))
+
+    def caterpillar(n):
+        par = [-1]
+        for j in range(n):
+            par += [2 * j, 2 * j]
+        return par
+
+    assert check(caterpillar(31)) == 0
+    assert check(caterpillar(32)) == -3
+    assert b"nested branching" in lib.dtree_last_error()
+    assert check(caterpillar(15) + [30]) == 0  # 32 nodes: the register-resident recurrence
+    assert check([-1] + list(range(95))) == 0  # a 96-node chain has no branching node
+    assert check([-1, 0, 5]) == -3  # parent after the child
+

@@ -109,3 +109,33 @@ def test_commit_takes_last_accepted_node():
     np.testing.assert_array_equal(win, wins[3])
     np.testing.assert_array_equal(S, states[3])
     np.testing.assert_array_equal(win, np.stack([x[0], x[1], x[3]]))
+
+
+def test_chain_forms_equal_the_tree_forms_on_a_chain():
+    """chain_conv1d / chain_gated_delta (the memory-light forms used for long
+    prompts) against tree_conv1d / tree_gated_delta with chain parents, on
+    grouped heads and a nonzero base window and state; a planted off-by-one in
+    the conv rows (the window shifted by one) must fail."""
+    rng = np.random.default_rng(7)
+    T, Hk, Hv, Dk, Dv, C, keep = 23, 2, 4, 16, 8, 12, 3
+    x = rng.normal(size=(T, C))
+    base = rng.normal(size=(keep, C))
+    w = rng.normal(size=(keep + 1, C))
+    chain = [-1] + list(range(T - 1))
+    out, win = gdn.tree_conv1d(x, base, w, chain)
+    cout, cwin = gdn.chain_conv1d(x, base, w)
+    np.testing.assert_allclose(cout, out, rtol=1e-12, atol=1e-12)
+    np.testing.assert_array_equal(cwin, win[-1])
+    bad, _ = gdn.chain_conv1d(np.concatenate([x[1:], x[:1]]), base, w)
+    assert np.abs(bad - out).max() > 1e-3
+    q = rng.normal(size=(T, Hk, Dk))
+    k = rng.normal(size=(T, Hk, Dk)) / 4
+    v = rng.normal(size=(T, Hv, Dv))
+    g = rng.uniform(0.5, 1.0, size=(T, Hv))
+    beta = rng.uniform(0.0, 1.0, size=(T, Hv))
+    state = rng.normal(size=(Hv, Dv, Dk))
+    y, states = gdn.tree_gated_delta(q, k, v, g, beta, state, chain)
+    cy, cs = gdn.chain_gated_delta(q, k, v, g, beta, state)
+    np.testing.assert_allclose(cy, y, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(cs, states[-1], rtol=1e-12, atol=1e-12)
+

@@ -182,3 +182,24 @@ def test_commit_then_next_step_equals_one_forward(models):
     norm, _, _ = orc.forward_tree(nxt, cache.offset + np.arange(3), [-1, 0, 1], cache)
     ref = _hf_hidden(hf, np.concatenate([prefix, toks[accepted], nxt]))[-3:]
     _close(norm, ref)
+
+
+def test_chain_prefill_equals_forward_and_commit(models):
+    """chain_prefill (chain conv / recurrence, the form used for long prompts)
+    == forward_tree over the chain + commit of every token: the hidden rows
+    after the layers and every committed window, state, key and value."""
+    orc, _ = models
+    toks = np.random.default_rng(8).integers(0, CFG.vocab, 14)
+    chain = [-1] + list(range(13))
+    cache = orc.new_cache()
+    _, _, pend = orc.forward_tree(toks, np.arange(14), chain, cache)
+    orc.commit(cache, pend, chain, list(range(14)))
+    x, layers = orc.chain_prefill(toks, CFG.layers)
+    for li, (a, b) in enumerate(layers):
+        _close(a, cache.layers[li][0], 1e-5)
+        _close(b, cache.layers[li][1], 1e-5)
+    # hidden rows: forward_tree's normalised output equals the final norm of x
+    from oracle.qwen3 import rms_norm
+    norm, _, _ = orc.forward_tree(toks, np.arange(14), chain, orc.new_cache())
+    _close(rms_norm(x, orc.w(None, "final_norm"), CFG.eps), norm, 1e-5)
+
