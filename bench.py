@@ -849,7 +849,7 @@ def attention_layer_bench(P: int = 512, sets: int = 128, reps: int = 1280) -> di
     sin = torch.zeros(MP, D // 2, device=dev)
     st = torch.cuda.current_stream().cuda_stream
     N.check(lib.dtree_rope_table(desc.data_ptr(), MP, D, 1e6, cos.data_ptr(), sin.data_ptr(), st), "rope table")
-    out = torch.zeros(2, MP, Hq * D, dtype=torch.bfloat16, device=dev)
+    out = torch.zeros(2, MP, Hq * D, dtype=torch.float16, device=dev)
     ws = torch.zeros(lib.dtree_attention_workspace_bytes(Hq, D, P, MP), dtype=torch.uint8, device=dev)
     args = []
     for s_ in range(sets):
@@ -859,7 +859,7 @@ def attention_layer_bench(P: int = 512, sets: int = 128, reps: int = 1280) -> di
         a.rope_cos = cos.data_ptr(); a.rope_sin = sin.data_ptr()
         a.k_pages = cache.k_ptr(s_); a.v_pages = cache.v_ptr(s_); a.page_table = cache.page_table.data_ptr()
         a.desc = desc.data_ptr()
-        a.out = out[0].data_ptr(); a.out_lo = out[1].data_ptr(); a.ld_out = Hq * D; a.out_layout = N.W_TILED
+        a.out = out[0].data_ptr(); a.out_lo = None; a.ld_out = Hq * D; a.out_layout = N.W_TILED_F16
         a.num_heads = Hq; a.num_kv_heads = Hkv; a.head_dim = D; a.rows_padded = MP; a.scale = D ** -0.5
         a.max_past_length = P; a.write_cache = 0
         a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()

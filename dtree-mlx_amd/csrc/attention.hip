@@ -77,6 +77,7 @@ struct AttnParams {
   uint16_t* kp; uint16_t* vp; const int* page_table;
   const DtreeStepDesc* desc;
   uint16_t* out; uint16_t* out_lo; int ld_out; int out_tiled;
+  int out_h16;  // DTREE_W_TILED_F16 output: one fp16 plane
   int Hq, Hkv, NT;       // NT: 32-row query blocks = 32-key tree chunks
   int S, max_pchunks;    // splits per (group, query block); prefix chunks the grid is sized for
   int cps;               // prefix chunks per split
@@ -534,15 +535,9 @@ __device__ __forceinline__ void write_unit(const AttnParams& p, int hq, int db, 
 #pragma unroll
       for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
     }
-    float rl[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
-    const u32x2_t hi = {pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
-    const u32x2_t lo = {pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
     const int col = hq * D + dim;
     const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
-    *reinterpret_cast<u32x2_t*>(p.out + oi) = hi;
-    if (p.out_lo) *reinterpret_cast<u32x2_t*>(p.out_lo + oi) = lo;
+    store_act4(p.out, p.out_lo, oi, y, p.out_h16);
   }
 }
 
@@ -935,7 +930,8 @@ static int group_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
                                                                       a->rows_padded),
                 "attention: workspace too small");
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
-                    (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * D && a->ld_out % 64 == 0),
+                    ((a->out_layout == DTREE_W_TILED || a->out_layout == DTREE_W_TILED_F16) &&
+                     a->ld_out == a->num_heads * D && a->ld_out % 64 == 0),
                 "attention: tiled out needs ld_out == num_heads * head_dim");
   const int pairs = a->num_kv_heads * nt;
   const int cus = device_cus();
@@ -947,8 +943,9 @@ static int group_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   p.q_norm = a->q_norm; p.k_norm = a->k_norm; p.eps = a->eps;
   p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
   p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
-  p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
-  p.out_tiled = a->out_layout == DTREE_W_TILED;
+  p.out_tiled = a->out_layout == DTREE_W_TILED || a->out_layout == DTREE_W_TILED_F16;
+  p.out_h16 = a->out_layout == DTREE_W_TILED_F16;
+  p.out = a->out; p.out_lo = p.out_h16 ? nullptr : a->out_lo; p.ld_out = a->ld_out;  // fp16: one plane
   p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.NT = nt;
   p.max_pchunks = attn_max_pchunks(D, a->max_past_length);
   p.max_past = a->max_past_length;

@@ -57,6 +57,7 @@ struct AttnParams {
   uint16_t* kp; uint16_t* vp; const int* page_table;
   const DtreeStepDesc* desc;
   uint16_t* out; uint16_t* out_lo; int ld_out; int out_tiled;
+  int out_h16;  // DTREE_W_TILED_F16 output: one fp16 plane
   int Hq, Hkv, max_chunks, splits;
   int tree_chunks;  // 32-key tree chunks = 32-row query blocks = rows_padded / 32
   float scale_log2;
@@ -870,15 +871,9 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
       }
-      float rl[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
-      const u32x2_t hi = {pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
-      const u32x2_t lo = {pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
       const int col = hq * D + dim;
       const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
-      *reinterpret_cast<u32x2_t*>(p.out + oi) = hi;
-      if (p.out_lo) *reinterpret_cast<u32x2_t*>(p.out_lo + oi) = lo;
+      store_act4(p.out, p.out_lo, oi, y, p.out_h16);
     }
   }
 }
@@ -986,15 +981,9 @@ __global__ __launch_bounds__(64 * kWaves) void attn_combine_kernel(AttnParams p)
 #pragma unroll
       for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
     }
-    float rl[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
-    const u32x2_t hi = {pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
-    const u32x2_t lo = {pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
     const int col = hq * D + dim;
     const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
-    *reinterpret_cast<u32x2_t*>(p.out + oi) = hi;
-    if (p.out_lo) *reinterpret_cast<u32x2_t*>(p.out_lo + oi) = lo;
+    store_act4(p.out, p.out_lo, oi, y, p.out_h16);
   }
 }
 
@@ -1052,7 +1041,8 @@ int head_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
                                                                      a->rows_padded),
                 "attention: workspace too small");
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ||
-                    (a->out_layout == DTREE_W_TILED && a->ld_out == a->num_heads * D && a->ld_out % 64 == 0),
+                    ((a->out_layout == DTREE_W_TILED || a->out_layout == DTREE_W_TILED_F16) &&
+                     a->ld_out == a->num_heads * D && a->ld_out % 64 == 0),
                 "attention: tiled out needs ld_out == num_heads * head_dim");
   AttnParams p{};
   p.qkv = a->qkv; p.ld_qkv = a->ld_qkv;
@@ -1060,8 +1050,9 @@ int head_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   p.q_norm = a->q_norm; p.k_norm = a->k_norm; p.eps = a->eps;
   p.rope_cos = a->rope_cos; p.rope_sin = a->rope_sin;
   p.kp = a->k_pages; p.vp = a->v_pages; p.page_table = a->page_table; p.desc = a->desc;
-  p.out = a->out; p.out_lo = a->out_lo; p.ld_out = a->ld_out;
-  p.out_tiled = a->out_layout == DTREE_W_TILED;
+  p.out_tiled = a->out_layout == DTREE_W_TILED || a->out_layout == DTREE_W_TILED_F16;
+  p.out_h16 = a->out_layout == DTREE_W_TILED_F16;
+  p.out = a->out; p.out_lo = p.out_h16 ? nullptr : a->out_lo; p.ld_out = a->ld_out;  // fp16: one plane
   p.Hq = a->num_heads; p.Hkv = a->num_kv_heads; p.tree_chunks = nt;
   p.max_chunks = attn_max_chunks(D, a->max_past_length, nt);
   p.splits = attn_splits(D, a->max_past_length, nt);

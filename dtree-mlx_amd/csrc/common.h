@@ -100,6 +100,48 @@ __device__ __forceinline__ f32x16_t mfma32_f16(u32x4_t a, u32x4_t b, f32x16_t c)
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
 }
+__device__ __forceinline__ uint16_t f2h(float f) { return (uint16_t)(pack_h2(f, 0.f) & 0xffffu); }
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+
+// Activations for the next GEMM, 4 or 8 consecutive values at element oi:
+// DTREE_W_TILED_F16 (h16) -> one fp16 plane; else bf16 hi + bf16 lo (lo =
+// bf16(v - hi), skipped when lo is null).
+__device__ __forceinline__ void store_act4(uint16_t* hi, uint16_t* lo, size_t oi, const float (&y)[4], bool h16) {
+  if (h16) {
+    *reinterpret_cast<u32x2_t*>(hi + oi) = u32x2_t{pack_h2(y[0], y[1]), pack_h2(y[2], y[3])};
+    return;
+  }
+  float rl[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) rl[i] = y[i] - bf2f(f2bf(y[i]));
+  *reinterpret_cast<u32x2_t*>(hi + oi) = u32x2_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
+  if (lo) *reinterpret_cast<u32x2_t*>(lo + oi) = u32x2_t{pack_bf2(rl[0], rl[1]), pack_bf2(rl[2], rl[3])};
+}
+__device__ __forceinline__ void store_act8(uint16_t* hi, uint16_t* lo, size_t oi, const float (&y)[8], bool h16) {
+  if (h16) {
+    *reinterpret_cast<u32x4_t*>(hi + oi) =
+        u32x4_t{pack_h2(y[0], y[1]), pack_h2(y[2], y[3]), pack_h2(y[4], y[5]), pack_h2(y[6], y[7])};
+    return;
+  }
+  float rr[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) rr[i] = y[i] - bf2f(f2bf(y[i]));
+  *reinterpret_cast<u32x4_t*>(hi + oi) =
+      u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])};
+  if (lo)
+    *reinterpret_cast<u32x4_t*>(lo + oi) =
+        u32x4_t{pack_bf2(rr[0], rr[1]), pack_bf2(rr[2], rr[3]), pack_bf2(rr[4], rr[5]), pack_bf2(rr[6], rr[7])};
+}
+
+// 8 consecutive elements of one 16-byte load as fp32: fp16 (h16: the
+// DTREE_W_TILED_F16 layout) or bf16 (every other layout).
+__device__ __forceinline__ void unpack8(u32x4_t w, bool h16, float (&v)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t b = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
+    v[i] = h16 ? h2f((uint16_t)b) : __uint_as_float(b << 16);
+  }
+}
 
 // bf16 pair -> fp16 pair. Exact for every bf16 value of magnitude in
 // [2^-14, 65504] (fp16 has more significand bits than bf16); smaller ones

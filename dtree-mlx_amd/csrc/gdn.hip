@@ -883,7 +883,7 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const DtreeStepDesc
                                                              const float* __restrict__ y,
                                                              const float* __restrict__ z, int ldz,
                                                              const uint16_t* __restrict__ w, float eps, int Hv,
-                                                             int rows, uint16_t* out, uint16_t* out_lo, int tiled,
+                                                             int rows, uint16_t* out, uint16_t* out_lo, int layout,
                                                              int ld_out) {
   constexpr int TPH = DV / 8;  // threads per (node, head)
   const int L = chain > 0 ? chain : desc->num_nodes;
@@ -917,15 +917,9 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const DtreeStepDesc
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = 0.f;
   }
-  float rr[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) rr[i] = o[i] - bf2f(f2bf(o[i]));
-  const u32x4_t hi{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]), pack_bf2(o[4], o[5]), pack_bf2(o[6], o[7])};
-  const u32x4_t lo{pack_bf2(rr[0], rr[1]), pack_bf2(rr[2], rr[3]), pack_bf2(rr[4], rr[5]), pack_bf2(rr[6], rr[7])};
   const int col = h * DV + d0;
-  const size_t oi = tiled ? tiled_index(t, col, ld_out) : (size_t)t * ld_out + col;
-  *reinterpret_cast<u32x4_t*>(out + oi) = hi;
-  if (out_lo) *reinterpret_cast<u32x4_t*>(out_lo + oi) = lo;
+  const size_t oi = layout != DTREE_W_ROWMAJOR ? tiled_index(t, col, ld_out) : (size_t)t * ld_out + col;
+  store_act8(out, out_lo, oi, o, layout == DTREE_W_TILED_F16);
 }
 
 // ---- causal chain (prompt prefill) -------------------------------------------
@@ -1253,14 +1247,15 @@ extern "C" int dtree_gdn_layer_gated_norm(const DtreeGdnArgs* a, hipStream_t str
                     ((uintptr_t)a->norm_w & 15) == 0,
                 "gdn_layer_gated_norm: y, norm_w, out and out_lo must be 16-byte aligned");
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ? (a->ld_out >= value_dim && a->ld_out % 8 == 0)
-                                                  : (a->out_layout == DTREE_W_TILED && a->ld_out == value_dim &&
+                                                  : ((a->out_layout == DTREE_W_TILED || a->out_layout == DTREE_W_TILED_F16) &&
+                                                     a->ld_out == value_dim &&
                                                      value_dim % 64 == 0 && a->rows_padded % 32 == 0),
                 "gdn_layer_gated_norm: out layout (tiled needs ld_out == value dim, rows_padded % 32 == 0)");
   const int pairs = a->rows_padded * a->num_v_heads;
   const int per_block = 256 / (128 / 8);
   gdn_gated_norm_kernel<128><<<(pairs + per_block - 1) / per_block, 256, 0, stream>>>(
       a->desc, 0, a->y, a->proj + C, a->ld_proj, a->norm_w, a->eps, a->num_v_heads, a->rows_padded, a->out, a->out_lo,
-      a->out_layout == DTREE_W_TILED, a->ld_out);
+      a->out_layout, a->ld_out);
   DTREE_LAUNCH_CHECK("gdn_layer_gated_norm launch");
   return DTREE_OK;
 }
@@ -1363,7 +1358,8 @@ extern "C" int dtree_gdn_layer_chain(const DtreeGdnArgs* a, int32_t num_tokens, 
                     ((uintptr_t)a->norm_w & 15) == 0,
                 "gdn_layer_chain: q, k, state, y, norm_w, out and out_lo must be 16-byte aligned");
   DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR ? (a->ld_out >= value_dim && a->ld_out % 8 == 0)
-                                                  : (a->out_layout == DTREE_W_TILED && a->ld_out == value_dim &&
+                                                  : ((a->out_layout == DTREE_W_TILED || a->out_layout == DTREE_W_TILED_F16) &&
+                                                     a->ld_out == value_dim &&
                                                      value_dim % 64 == 0 && a->rows_padded % 32 == 0),
                 "gdn_layer_chain: out layout (tiled needs ld_out == value dim, rows_padded % 32 == 0)");
   PrepParams pp{};
@@ -1395,7 +1391,7 @@ extern "C" int dtree_gdn_layer_chain(const DtreeGdnArgs* a, int32_t num_tokens, 
   const int per_block = 256 / (128 / 8);
   gdn_gated_norm_kernel<128><<<(pairs + per_block - 1) / per_block, 256, 0, stream>>>(
       nullptr, num_tokens, a->y, a->proj + C, a->ld_proj, a->norm_w, a->eps, a->num_v_heads, a->rows_padded, a->out,
-      a->out_lo, a->out_layout == DTREE_W_TILED, a->ld_out);
+      a->out_lo, a->out_layout, a->ld_out);
   DTREE_LAUNCH_CHECK("gdn_layer_chain gated norm launch");
   return DTREE_OK;
 }

@@ -26,7 +26,12 @@
 //     partials stay in that XCD's L2.
 //   * Epilogues fuse the RMSNorm row scale (norm weight folded into the
 //     producer's X), residual add, SwiGLU, and the per-32-column sum of
-//     squares the next RMSNorm needs; they emit split hi/lo outputs.
+//     squares the next RMSNorm needs; they emit split hi/lo outputs (one
+//     fp16 plane for the DTREE_W_TILED_F16 layout).
+//   * H (DTREE_W_TILED_F16): fp16 weights and one fp16 activation plane run
+//     the fp16 MFMA once per weight fragment; the other tiled paths keep bf16
+//     weights with the activation pair (two bf16 MFMAs) and q4 dequantises to
+//     bf16.
 #include "common.h"
 
 namespace dtree {
@@ -42,6 +47,7 @@ struct GemmParams {
   const float* ss_in; int ss_tiles; float inv_norm_dim; float eps;
   float* out_f32; int ld_out_f32;
   uint16_t* out_bf16; uint16_t* out_lo; int ld_out_bf16; int out_tiled;
+  int out_h16;  // outputs in DTREE_W_TILED_F16: one fp16 plane
   const uint16_t* next_norm;
   float* ss_out;
   uint16_t* hidden_out; int ld_hidden;
@@ -63,8 +69,13 @@ __device__ __forceinline__ size_t out_index(int tiled, int m, int col, int ld) {
   return tiled ? tiled_index(m, col, ld) : (size_t)m * ld + col;
 }
 
-// Split v into bf16 hi + bf16 lo (lo = bf16(v - hi)).
-__device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, size_t idx, float v) {
+// An activation for the next GEMM: one fp16 value (h16: DTREE_W_TILED_F16), or
+// bf16 hi + bf16 lo (lo = bf16(v - hi)).
+__device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, size_t idx, float v, int h16) {
+  if (h16) {
+    hi[idx] = f2h(v);
+    return;
+  }
   const uint16_t h = f2bf(v);
   hi[idx] = h;
   if (lo) lo[idx] = f2bf(v - bf2f(h));
@@ -74,7 +85,7 @@ __device__ __forceinline__ void split_store(uint16_t* hi, uint16_t* lo, size_t i
 // waves' tiles are summed into red[0 .. MB*32*32*NB) laid out [row][col].
 // TILED: W is stored in the kernel's consumption order (DTREE_W_TILED), so
 // every load instruction of a wave reads one contiguous kilobyte.
-template <int MB, int NB, int U, bool LO, bool TILED>
+template <int MB, int NB, int U, bool LO, bool TILED, bool H = false>
 __device__ __forceinline__ void wg_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ xlo, int ldx,
                                         const uint16_t* __restrict__ w, int K, int tile, int kb0, int kb1,
                                         float* red) {
@@ -151,8 +162,12 @@ __device__ __forceinline__ void wg_tile(const uint16_t* __restrict__ x, const ui
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
-            acc[nb][mb] = mfma32(xv[mb][i], wc[nb][i], acc[nb][mb]);
-            if (LO) acc[nb][mb] = mfma32(xl[mb][i], wc[nb][i], acc[nb][mb]);
+            if constexpr (H) {  // fp16 weights, one fp16 activation plane
+              acc[nb][mb] = mfma32_f16(xv[mb][i], wc[nb][i], acc[nb][mb]);
+            } else {
+              acc[nb][mb] = mfma32(xv[mb][i], wc[nb][i], acc[nb][mb]);
+              if (LO) acc[nb][mb] = mfma32(xl[mb][i], wc[nb][i], acc[nb][mb]);
+            }
           }
     };
     load_w(wa, 0);
@@ -290,7 +305,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* 
   } else if constexpr (EPI == DTREE_EPI_STORE_BF16) {
     for (int e = threadIdx.x; e < TE; e += kThreads) {
       const int m = e / TN, n = e % TN;
-      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * TN + n, p.ld_out_bf16), red[e] * rs[m]);
+      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * TN + n, p.ld_out_bf16), red[e] * rs[m],
+                  p.out_h16);
     }
   } else if constexpr (EPI == DTREE_EPI_RESIDUAL) {
     constexpr int IT = TE / kThreads;
@@ -311,7 +327,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* 
       float* xp = p.out_f32 + (size_t)m * p.ld_out_f32 + col;
       const float xv = xo[i] + red[e];
       *xp = xv;
-      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, col, p.ld_out_bf16), xv * g);
+      split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, col, p.ld_out_bf16), xv * g, p.out_h16);
       if (p.hidden_out) p.hidden_out[(size_t)m * p.ld_hidden + col] = f2bf(xv);
       // sum of x^2 over this 32-column tile (the 32 lanes of a half-wave)
       const float sq = row_sum32(xv * xv);
@@ -325,13 +341,13 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* 
       const float gt = red[m * TN + sb * 32 + j] * rs[m];
       const float up = red[m * TN + sb * 32 + 16 + j] * rs[m];
       split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * (TN / 2) + f, p.ld_out_bf16),
-                  silu_f(gt) * up);
+                  silu_f(gt) * up, p.out_h16);
     }
   }
 
 }
 
-template <int MB, int NB, int U, bool LO, bool TILED, int EPI>
+template <int MB, int NB, int U, bool LO, bool TILED, int EPI, bool H = false>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int MP = MB * 32;
   constexpr int TN = 32 * NB;
@@ -355,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   const int kb0 = s * p.kb_per_split;
   const int kb1 = min(kb0 + p.kb_per_split, nkb);
 
-  wg_tile<MB, NB, U, LO, TILED>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, kb0, kb1, red);
+  wg_tile<MB, NB, U, LO, TILED, H>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, kb0, kb1, red);
 
   if (p.S > 1) {
     float* mine = p.part + ((size_t)tile * p.S + s) * TE;
@@ -555,7 +571,7 @@ __device__ __forceinline__ void partials_add(const u32x4_t (&v)[kRedBatch][2], i
 }
 
 // RING units in flight per wave, at most MAXB column blocks per workgroup.
-template <bool LO, int EPI, bool Q4, int RING, int MAXB>
+template <bool LO, int EPI, bool Q4, int RING, int MAXB, bool H = false>
 __device__ __forceinline__ void sk_gemm_body(const GemmParams& p) {
   constexpr int TN = 64, TE = 32 * TN;
   __shared__ float acc_lds[MAXB * kWaves * TE];  // [local block][wave][row][col]
@@ -662,8 +678,12 @@ __device__ __forceinline__ void sk_gemm_body(const GemmParams& p) {
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
-              acc[nb] = mfma32(xr[s][0][i], wr[s][nb][i], acc[nb]);
-              if (LO) acc[nb] = mfma32(xr[s][1][i], wr[s][nb][i], acc[nb]);
+              if constexpr (H) {
+                acc[nb] = mfma32_f16(xr[s][0][i], wr[s][nb][i], acc[nb]);
+              } else {
+                acc[nb] = mfma32(xr[s][0][i], wr[s][nb][i], acc[nb]);
+                if (LO) acc[nb] = mfma32(xr[s][1][i], wr[s][nb][i], acc[nb]);
+              }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -801,9 +821,9 @@ __device__ __forceinline__ void sk_gemm_body(const GemmParams& p) {
 #undef DTREE_SK_EPILOGUE
 }
 
-template <bool LO, int EPI, bool Q4>
+template <bool LO, int EPI, bool Q4, bool H = false>
 __global__ __launch_bounds__(kThreads) void sk_gemm_kernel(GemmParams p) {
-  sk_gemm_body<LO, EPI, Q4, kSkDepth, kSkMaxBlocks>(p);
+  sk_gemm_body<LO, EPI, Q4, kSkDepth, kSkMaxBlocks, H>(p);
 }
 
 // q4 at two waves per SIMD: a 3-deep ring and at most two column blocks per
@@ -1098,7 +1118,7 @@ struct LmParams {
 
 
 
-template <int MB, int NB, int U, bool LO, bool TILED, bool Q4>
+template <int MB, int NB, int U, bool LO, bool TILED, bool Q4, bool H = false>
 __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
   constexpr int MP = MB * 32;
   constexpr int TN = 32 * NB;
@@ -1124,7 +1144,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(LmParams p) {
       wg_tile_q4<LO>(p.x, p.x_lo, reinterpret_cast<const uint32_t*>(p.w), reinterpret_cast<const uint32_t*>(p.w_sb),
                      p.k, tile, red);
     else
-      wg_tile<MB, NB, U, LO, TILED>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, 0, nkb, red);
+      wg_tile<MB, NB, U, LO, TILED, H>(p.x, p.x_lo, p.ldx, p.w, p.k, tile, 0, nkb, red);
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int e = threadIdx.x + i * kThreads;
@@ -1167,28 +1187,30 @@ static int auto_split(int ntiles, int nkb) {
   return s;
 }
 
-template <int MB, bool LO, bool TILED>
+template <int MB, bool LO, bool TILED, bool H = false>
 static void launch_gemm_lo(const GemmParams& p, int epi, int blocks, hipStream_t st) {
   constexpr int NB = Cfg<MB>::NB, U = Cfg<MB>::U;
   switch (epi) {
     case DTREE_EPI_STORE_F32:
-      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_STORE_F32><<<blocks, kThreads, 0, st>>>(p);
+      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_STORE_F32, H><<<blocks, kThreads, 0, st>>>(p);
       break;
     case DTREE_EPI_RESIDUAL:
-      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_RESIDUAL><<<blocks, kThreads, 0, st>>>(p);
+      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_RESIDUAL, H><<<blocks, kThreads, 0, st>>>(p);
       break;
     case DTREE_EPI_SWIGLU:
-      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_SWIGLU><<<blocks, kThreads, 0, st>>>(p);
+      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_SWIGLU, H><<<blocks, kThreads, 0, st>>>(p);
       break;
     default:
-      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_STORE_BF16><<<blocks, kThreads, 0, st>>>(p);
+      gemm_kernel<MB, NB, U, LO, TILED, DTREE_EPI_STORE_BF16, H><<<blocks, kThreads, 0, st>>>(p);
       break;
   }
 }
 
 template <int MB>
-static void launch_gemm(const GemmParams& p, int epi, int blocks, hipStream_t st, bool tiled) {
-  if (p.x_lo) {
+static void launch_gemm(const GemmParams& p, int epi, int blocks, hipStream_t st, bool tiled, bool h16) {
+  if (h16) {
+    launch_gemm_lo<MB, false, true, true>(p, epi, blocks, st);
+  } else if (p.x_lo) {
     if (tiled) launch_gemm_lo<MB, true, true>(p, epi, blocks, st);
     else launch_gemm_lo<MB, true, false>(p, epi, blocks, st);
   } else {
@@ -1198,9 +1220,11 @@ static void launch_gemm(const GemmParams& p, int epi, int blocks, hipStream_t st
 }
 
 template <int MB>
-static void launch_lm(const LmParams& p, int grid, hipStream_t st, bool tiled) {
+static void launch_lm(const LmParams& p, int grid, hipStream_t st, bool tiled, bool h16) {
   constexpr int NB = Cfg<MB>::NB, U = Cfg<MB>::U;
-  if (p.x_lo) {
+  if (h16) {
+    lmhead_kernel<MB, NB, U, false, true, false, true><<<grid, kThreads, 0, st>>>(p);
+  } else if (p.x_lo) {
     if (tiled) lmhead_kernel<MB, NB, U, true, true, false><<<grid, kThreads, 0, st>>>(p);
     else lmhead_kernel<MB, NB, U, true, false, false><<<grid, kThreads, 0, st>>>(p);
   } else {
@@ -1351,13 +1375,13 @@ static void launch_sk2(const GemmParams& p, int epi, hipStream_t st) {
   }
 }
 
-template <bool LO, bool Q4>
+template <bool LO, bool Q4, bool H = false>
 static void launch_sk(const GemmParams& p, int epi, hipStream_t st) {
   switch (epi) {
-    case DTREE_EPI_STORE_F32: sk_gemm_kernel<LO, DTREE_EPI_STORE_F32, Q4><<<p.G, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_RESIDUAL: sk_gemm_kernel<LO, DTREE_EPI_RESIDUAL, Q4><<<p.G, kThreads, 0, st>>>(p); break;
-    case DTREE_EPI_SWIGLU: sk_gemm_kernel<LO, DTREE_EPI_SWIGLU, Q4><<<p.G, kThreads, 0, st>>>(p); break;
-    default: sk_gemm_kernel<LO, DTREE_EPI_STORE_BF16, Q4><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_STORE_F32: sk_gemm_kernel<LO, DTREE_EPI_STORE_F32, Q4, H><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_RESIDUAL: sk_gemm_kernel<LO, DTREE_EPI_RESIDUAL, Q4, H><<<p.G, kThreads, 0, st>>>(p); break;
+    case DTREE_EPI_SWIGLU: sk_gemm_kernel<LO, DTREE_EPI_SWIGLU, Q4, H><<<p.G, kThreads, 0, st>>>(p); break;
+    default: sk_gemm_kernel<LO, DTREE_EPI_STORE_BF16, Q4, H><<<p.G, kThreads, 0, st>>>(p); break;
   }
 }
 
@@ -1386,7 +1410,7 @@ constexpr int kDpDepth = 4;
 // x (128 + q), folded in as acc += s * sum + (b - 128 s) * sum(x), with
 // sum(x) from an MFMA of the same activation registers against bf16 ones (as
 // q4_group).
-template <bool LO, int EPI, int KS, bool Q4>
+template <bool LO, int EPI, int KS, bool Q4, bool H = false>
 __device__ __forceinline__ void dp_gemm_body(const GemmParams& p) {
   constexpr int TN = 32, TE = 32 * TN;
   constexpr int WL = Q4 ? 1 : 4;  // 16-byte weight loads per lane per K block
@@ -1467,8 +1491,12 @@ __device__ __forceinline__ void dp_gemm_body(const GemmParams& p) {
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            acc = mfma32(xr[s][0][i], wr[s][i], acc);
-            if (LO) acc = mfma32(xr[s][1][i], wr[s][i], acc);
+            if constexpr (H) {
+              acc = mfma32_f16(xr[s][0][i], wr[s][i], acc);
+            } else {
+              acc = mfma32(xr[s][0][i], wr[s][i], acc);
+              if (LO) acc = mfma32(xr[s][1][i], wr[s][i], acc);
+            }
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1536,9 +1564,9 @@ __device__ __forceinline__ void dp_gemm_body(const GemmParams& p) {
   tile_epilogue<32, TN, EPI>(p, red, rs, tile, EPI == DTREE_EPI_RESIDUAL ? xo : nullptr);
 }
 
-template <bool LO, int EPI, int KS>
+template <bool LO, int EPI, int KS, bool H = false>
 __global__ __launch_bounds__(kThreads) void dp_gemm_kernel(GemmParams p) {
-  dp_gemm_body<LO, EPI, KS, false>(p);
+  dp_gemm_body<LO, EPI, KS, false, H>(p);
 }
 
 template <bool LO, int EPI, int KS>
@@ -1546,7 +1574,7 @@ __global__ __launch_bounds__(kThreads) void dpq_gemm_kernel(GemmParams p) {
   dp_gemm_body<LO, EPI, KS, true>(p);
 }
 
-template <bool LO, int KS, bool Q4>
+template <bool LO, int KS, bool Q4, bool H = false>
 static void launch_dp(const GemmParams& p, int epi, hipStream_t st) {
   const int grid = KS * (p.n / 32);
   if constexpr (Q4) {
@@ -1558,15 +1586,16 @@ static void launch_dp(const GemmParams& p, int epi, hipStream_t st) {
     }
   } else {
     switch (epi) {
-      case DTREE_EPI_STORE_F32: dp_gemm_kernel<LO, DTREE_EPI_STORE_F32, KS><<<grid, kThreads, 0, st>>>(p); break;
-      case DTREE_EPI_RESIDUAL: dp_gemm_kernel<LO, DTREE_EPI_RESIDUAL, KS><<<grid, kThreads, 0, st>>>(p); break;
-      case DTREE_EPI_SWIGLU: dp_gemm_kernel<LO, DTREE_EPI_SWIGLU, KS><<<grid, kThreads, 0, st>>>(p); break;
-      default: dp_gemm_kernel<LO, DTREE_EPI_STORE_BF16, KS><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_STORE_F32: dp_gemm_kernel<LO, DTREE_EPI_STORE_F32, KS, H><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_RESIDUAL: dp_gemm_kernel<LO, DTREE_EPI_RESIDUAL, KS, H><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_SWIGLU: dp_gemm_kernel<LO, DTREE_EPI_SWIGLU, KS, H><<<grid, kThreads, 0, st>>>(p); break;
+      default: dp_gemm_kernel<LO, DTREE_EPI_STORE_BF16, KS, H><<<grid, kThreads, 0, st>>>(p); break;
     }
   }
 }
 template <int KS>
-static void launch_dp_any(const GemmParams& p, int epi, bool q4, hipStream_t st) {
+static void launch_dp_any(const GemmParams& p, int epi, bool q4, bool h16, hipStream_t st) {
+  if (h16) return launch_dp<false, KS, false, true>(p, epi, st);
   const bool lo = p.x_lo != nullptr;
   if (q4) lo ? launch_dp<true, KS, true>(p, epi, st) : launch_dp<false, KS, true>(p, epi, st);
   else lo ? launch_dp<true, KS, false>(p, epi, st) : launch_dp<false, KS, false>(p, epi, st);
@@ -1589,7 +1618,7 @@ constexpr int kLongRows = 128, kLongCols = 128;
 // staged; each wave's 32 x 32 tiles take a fresh MFMA sum of x (128 + q) per
 // group and fold it in as acc += s * sum + (b - 128 s) * sum(x), with sum(x)
 // per row block from an MFMA of the staged activations against bf16 ones.
-template <bool LO, int EPI, bool Q4>
+template <bool LO, int EPI, bool Q4, bool H = false>
 __device__ __forceinline__ void long_gemm_body(const GemmParams& p) {
   constexpr int NPL = LO ? 2 : 1, ABLK = 4 * NPL;
   constexpr int WBYTES = Q4 ? 4 * 1024 + 4 * 128 : 4 * 4096;            // weight bytes per stage
@@ -1722,8 +1751,13 @@ __device__ __forceinline__ void long_gemm_body(const GemmParams& p) {
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
           const u32x4_t ah = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL) * 4096 + fo);
+          if constexpr (H) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32(ah, b[j], acc[rb][j]);
+            for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32_f16(ah, b[j], acc[rb][j]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[rb][j] = mfma32(ah, b[j], acc[rb][j]);
+          }
           if (LO) {
             const u32x4_t al = *reinterpret_cast<const u32x4_t*>(st + ((2 * wr + rb) * NPL + 1) * 4096 + fo);
 #pragma unroll
@@ -1755,9 +1789,9 @@ __device__ __forceinline__ void long_gemm_body(const GemmParams& p) {
   tile_epilogue<kLongRows, kLongCols, EPI>(q, red, rs, nt);
 }
 
-template <bool LO, int EPI>
+template <bool LO, int EPI, bool H = false>
 __global__ __launch_bounds__(kThreads) void long_gemm_kernel(GemmParams p) {
-  long_gemm_body<LO, EPI, false>(p);
+  long_gemm_body<LO, EPI, false, H>(p);
 }
 
 template <bool LO, int EPI>
@@ -1766,7 +1800,16 @@ __global__ __launch_bounds__(kThreads) void longq_gemm_kernel(GemmParams p) {
 }
 
 template <bool LO>
-static void launch_long(const GemmParams& p, int epi, int grid, bool q4, hipStream_t st) {
+static void launch_long(const GemmParams& p, int epi, int grid, bool q4, bool h16, hipStream_t st) {
+  if (h16) {
+    switch (epi) {
+      case DTREE_EPI_STORE_F32: long_gemm_kernel<false, DTREE_EPI_STORE_F32, true><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_RESIDUAL: long_gemm_kernel<false, DTREE_EPI_RESIDUAL, true><<<grid, kThreads, 0, st>>>(p); break;
+      case DTREE_EPI_SWIGLU: long_gemm_kernel<false, DTREE_EPI_SWIGLU, true><<<grid, kThreads, 0, st>>>(p); break;
+      default: long_gemm_kernel<false, DTREE_EPI_STORE_BF16, true><<<grid, kThreads, 0, st>>>(p); break;
+    }
+    return;
+  }
   if (q4) {
     switch (epi) {
       case DTREE_EPI_STORE_F32: longq_gemm_kernel<LO, DTREE_EPI_STORE_F32><<<grid, kThreads, 0, st>>>(p); break;
@@ -1849,15 +1892,20 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   if (a->ss_in) DTREE_REQUIRE(a->ss_tiles > 0 && a->norm_dim > 0, "gemm: ss_in needs ss_tiles and norm_dim");
   const size_t need = dtree_gemm_workspace_bytes(a->rows_padded, a->n, a->k, S);
   DTREE_REQUIRE(a->workspace && a->workspace_bytes >= need, "gemm: workspace too small");
+  // fp16 path: fp16 weights and one fp16 activation plane, both TILED_F16
+  const bool h16 = a->x_layout == DTREE_W_TILED_F16;
+  DTREE_REQUIRE(h16 == (a->w_layout == DTREE_W_TILED_F16),
+                "gemm: DTREE_W_TILED_F16 weights and activations go together (q4 weights take DTREE_W_TILED x)");
 
   GemmParams p{};
-  p.x = a->x; p.x_lo = a->x_lo; p.ldx = a->ldx; p.w = a->w; p.n = a->n; p.k = a->k;
+  p.x = a->x; p.x_lo = h16 ? nullptr : a->x_lo; p.ldx = a->ldx; p.w = a->w; p.n = a->n; p.k = a->k;
   p.S = S; p.kb_per_split = (nkb + S - 1) / S; p.ntiles = ntiles;
   p.ss_in = a->ss_in; p.ss_tiles = a->ss_tiles;
   p.inv_norm_dim = a->norm_dim > 0 ? 1.0f / (float)a->norm_dim : 1.f; p.eps = a->eps;
   p.out_f32 = a->out_f32; p.ld_out_f32 = a->ld_out_f32;
-  p.out_bf16 = a->out_bf16; p.out_lo = a->out_lo; p.ld_out_bf16 = a->ld_out_bf16;
-  p.out_tiled = a->out_layout == DTREE_W_TILED;
+  p.out_tiled = a->out_layout == DTREE_W_TILED || a->out_layout == DTREE_W_TILED_F16;
+  p.out_h16 = a->out_layout == DTREE_W_TILED_F16;
+  p.out_bf16 = a->out_bf16; p.out_lo = p.out_h16 ? nullptr : a->out_lo; p.ld_out_bf16 = a->ld_out_bf16;
   p.next_norm = a->next_norm; p.ss_out = a->ss_out;
   p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
   p.off_xcd = off_xcd_test();
@@ -1866,7 +1914,7 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kCounterBytes);
   const int blocks = S == 1 ? ntiles : (int)(nt8 * S);
   const bool q4 = a->w_layout == DTREE_W_Q4G64;
-  const bool tiled = a->w_layout == DTREE_W_TILED || q4;
+  const bool tiled = a->w_layout == DTREE_W_TILED || q4 || h16;
   DTREE_REQUIRE(a->w_layout == DTREE_W_ROWMAJOR || tiled, "gemm: unknown w_layout");
   if (q4 && a->rows_padded > 32 && q4m_enabled()) {
     // One pass over the q4 weights for every row block (q4m_gemm_kernel).
@@ -1936,8 +1984,10 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   p.w_bytes = (unsigned)w_bytes;
   p.sb_bytes = (unsigned)((size_t)a->n * (a->k / 64) * 4);
   p.x_bytes = (unsigned)((size_t)32 * a->k * 2);
-  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR || a->out_layout == DTREE_W_TILED, "gemm: unknown out_layout");
-  if (a->out_layout == DTREE_W_TILED && a->out_bf16) {
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR || a->out_layout == DTREE_W_TILED ||
+                    a->out_layout == DTREE_W_TILED_F16,
+                "gemm: unknown out_layout");
+  if (p.out_tiled && a->out_bf16) {
     const int width = epi == DTREE_EPI_SWIGLU ? a->n / 2 : a->n;
     DTREE_REQUIRE(a->ld_out_bf16 == width && width % 64 == 0, "gemm: tiled out needs ld_out_bf16 == width, width % 64");
   }
@@ -1972,13 +2022,13 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     const size_t need_pairs = dp_pair_workspace_bytes(a->n);
     DTREE_REQUIRE(a->workspace_bytes >= need_pairs, "gemm: workspace too small for the paired schedule");
     p.part_bytes = (unsigned)(need_pairs - kCounterBytes);
-    if (dp_parts == 3) launch_dp_any<3>(p, epi, q4, stream);
-    else launch_dp_any<2>(p, epi, q4, stream);
+    if (dp_parts == 3) launch_dp_any<3>(p, epi, q4, h16, stream);
+    else launch_dp_any<2>(p, epi, q4, h16, stream);
     DTREE_LAUNCH_CHECK("gemm launch");
     return DTREE_OK;
   }
   if (tiled && a->rows_padded == 32 && (a->split_k == -1 || dp_auto)) {
-    launch_dp_any<1>(p, epi, q4, stream);
+    launch_dp_any<1>(p, epi, q4, h16, stream);
     DTREE_LAUNCH_CHECK("gemm launch");
     return DTREE_OK;
   }
@@ -1998,6 +2048,8 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     } else if (q4) {
       if (p.x_lo) launch_sk<true, true>(p, epi, stream);
       else launch_sk<false, true>(p, epi, stream);
+    } else if (h16) {
+      launch_sk<false, false, true>(p, epi, stream);
     } else {
       if (p.x_lo) launch_sk<true, false>(p, epi, stream);
       else launch_sk<false, false>(p, epi, stream);
@@ -2006,10 +2058,10 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     return DTREE_OK;
   }
   switch (a->rows_padded) {
-    case 32: launch_gemm<1>(p, epi, blocks, stream, tiled); break;
-    case 64: launch_gemm<2>(p, epi, blocks, stream, tiled); break;
-    case 96: launch_gemm<3>(p, epi, blocks, stream, tiled); break;
-    default: launch_gemm<4>(p, epi, blocks, stream, tiled); break;
+    case 32: launch_gemm<1>(p, epi, blocks, stream, tiled, h16); break;
+    case 64: launch_gemm<2>(p, epi, blocks, stream, tiled, h16); break;
+    case 96: launch_gemm<3>(p, epi, blocks, stream, tiled, h16); break;
+    default: launch_gemm<4>(p, epi, blocks, stream, tiled, h16); break;
   }
   DTREE_LAUNCH_CHECK("gemm launch");
   return DTREE_OK;
@@ -2019,8 +2071,10 @@ extern "C" int dtree_gemm_long(const DtreeGemmArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(a, "gemm_long: null args");
   DTREE_REQUIRE(a->x && a->w, "gemm_long: null x or w");
   const bool q4 = a->w_layout == DTREE_W_Q4G64;
-  DTREE_REQUIRE(a->x_layout == DTREE_W_TILED && (a->w_layout == DTREE_W_TILED || q4),
-                "gemm_long: tiled bf16 activations, tiled bf16 or q4 group-64 weights");
+  const bool h16 = a->x_layout == DTREE_W_TILED_F16;
+  DTREE_REQUIRE((a->x_layout == DTREE_W_TILED && (a->w_layout == DTREE_W_TILED || q4)) ||
+                    (h16 && a->w_layout == DTREE_W_TILED_F16),
+                "gemm_long: tiled bf16 activations with tiled bf16 or q4 group-64 weights, or TILED_F16 both");
   DTREE_REQUIRE(!q4 || (a->w_scales && ((uintptr_t)a->w_scales & 15) == 0),
                 "gemm_long: q4 weights need w_scales (16-byte aligned)");
   DTREE_REQUIRE(a->rows_padded >= kLongRows && a->rows_padded % kLongRows == 0 && a->rows_padded <= (1 << 20),
@@ -2040,8 +2094,10 @@ extern "C" int dtree_gemm_long(const DtreeGemmArgs* a, hipStream_t stream) {
   if (epi == DTREE_EPI_STORE_BF16) DTREE_REQUIRE(a->out_bf16 && a->ld_out_bf16 >= a->n, "gemm_long: out_bf16");
   if (a->hidden_out) DTREE_REQUIRE(a->ld_hidden >= a->n, "gemm_long: ld_hidden too small");
   if (a->ss_in) DTREE_REQUIRE(a->ss_tiles > 0 && a->norm_dim > 0, "gemm_long: ss_in needs ss_tiles and norm_dim");
-  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR || a->out_layout == DTREE_W_TILED, "gemm_long: unknown out_layout");
-  if (a->out_layout == DTREE_W_TILED && a->out_bf16) {
+  DTREE_REQUIRE(a->out_layout == DTREE_W_ROWMAJOR || a->out_layout == DTREE_W_TILED ||
+                    a->out_layout == DTREE_W_TILED_F16,
+                "gemm_long: unknown out_layout");
+  if (a->out_layout != DTREE_W_ROWMAJOR && a->out_bf16) {
     const int width = epi == DTREE_EPI_SWIGLU ? a->n / 2 : a->n;
     DTREE_REQUIRE(a->ld_out_bf16 == width && width % 64 == 0,
                   "gemm_long: tiled out needs ld_out_bf16 == width, width % 64");
@@ -2049,19 +2105,20 @@ extern "C" int dtree_gemm_long(const DtreeGemmArgs* a, hipStream_t stream) {
   DTREE_REQUIRE(((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->x_lo & 15) == 0 && ((uintptr_t)a->w & 15) == 0,
                 "gemm_long: x, x_lo and w must be 16-byte aligned");
   GemmParams p{};
-  p.x = a->x; p.x_lo = a->x_lo; p.ldx = a->ldx; p.w = a->w; p.n = a->n; p.k = a->k;
+  p.x = a->x; p.x_lo = h16 ? nullptr : a->x_lo; p.ldx = a->ldx; p.w = a->w; p.n = a->n; p.k = a->k;
   p.ss_in = a->ss_in; p.ss_tiles = a->ss_tiles;
   p.inv_norm_dim = a->norm_dim > 0 ? 1.0f / (float)a->norm_dim : 1.f; p.eps = a->eps;
   p.out_f32 = a->out_f32; p.ld_out_f32 = a->ld_out_f32;
-  p.out_bf16 = a->out_bf16; p.out_lo = a->out_lo; p.ld_out_bf16 = a->ld_out_bf16;
-  p.out_tiled = a->out_layout == DTREE_W_TILED;
+  p.out_tiled = a->out_layout == DTREE_W_TILED || a->out_layout == DTREE_W_TILED_F16;
+  p.out_h16 = a->out_layout == DTREE_W_TILED_F16;
+  p.out_bf16 = a->out_bf16; p.out_lo = p.out_h16 ? nullptr : a->out_lo; p.ld_out_bf16 = a->ld_out_bf16;
   p.next_norm = a->next_norm; p.ss_out = a->ss_out;
   p.hidden_out = a->hidden_out; p.ld_hidden = a->ld_hidden;
   const long long grid = (long long)(a->rows_padded / kLongRows) * ((a->n + kLongCols - 1) / kLongCols);
   DTREE_REQUIRE(grid < (1LL << 31), "gemm_long: grid too large");
   p.w_sb = a->w_scales;
-  if (a->x_lo) launch_long<true>(p, epi, (int)grid, q4, stream);
-  else launch_long<false>(p, epi, (int)grid, q4, stream);
+  if (p.x_lo) launch_long<true>(p, epi, (int)grid, q4, h16, stream);
+  else launch_long<false>(p, epi, (int)grid, q4, h16, stream);
   DTREE_LAUNCH_CHECK("gemm_long launch");
   return DTREE_OK;
 }
@@ -2094,7 +2151,8 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
   p.logits = logits; p.cand = reinterpret_cast<int2*>(candidates);
   const int grid = lmhead_grid(p.ntiles);
   p.cand_blocks = grid;
-  DTREE_REQUIRE(emb_layout == DTREE_W_ROWMAJOR || emb_layout == DTREE_W_TILED || emb_layout == DTREE_W_Q4G64,
+  DTREE_REQUIRE(emb_layout == DTREE_W_ROWMAJOR || emb_layout == DTREE_W_TILED || emb_layout == DTREE_W_TILED_F16 ||
+                    emb_layout == DTREE_W_Q4G64,
                 "lmhead: unknown emb_layout");
   if (emb_layout == DTREE_W_Q4G64) {
     DTREE_REQUIRE(x_layout == DTREE_W_TILED && ldx == hidden && hidden <= 4096,
@@ -2143,13 +2201,15 @@ extern "C" int dtree_lmhead_argmax(const uint16_t* x, const uint16_t* x_lo, int3
     return DTREE_OK;
   }
   DTREE_REQUIRE(x_layout == emb_layout, "lmhead: x_layout must equal emb_layout");
-  DTREE_REQUIRE(emb_layout != DTREE_W_TILED || ldx == hidden, "lmhead: tiled x needs ldx == hidden");
-  const bool tiled = emb_layout == DTREE_W_TILED;
+  const bool h16 = emb_layout == DTREE_W_TILED_F16;
+  const bool tiled = emb_layout == DTREE_W_TILED || h16;
+  DTREE_REQUIRE(!tiled || ldx == hidden, "lmhead: tiled x needs ldx == hidden");
+  if (h16) p.x_lo = nullptr;  // one fp16 plane
   switch (rows_padded) {
-    case 32: launch_lm<1>(p, grid, stream, tiled); break;
-    case 64: launch_lm<2>(p, grid, stream, tiled); break;
-    case 96: launch_lm<3>(p, grid, stream, tiled); break;
-    default: launch_lm<4>(p, grid, stream, tiled); break;
+    case 32: launch_lm<1>(p, grid, stream, tiled, h16); break;
+    case 64: launch_lm<2>(p, grid, stream, tiled, h16); break;
+    case 96: launch_lm<3>(p, grid, stream, tiled, h16); break;
+    default: launch_lm<4>(p, grid, stream, tiled, h16); break;
   }
   DTREE_LAUNCH_CHECK("lmhead launch");
   return DTREE_OK;

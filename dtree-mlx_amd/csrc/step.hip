@@ -36,29 +36,24 @@ __device__ __forceinline__ float q4_element(const uint32_t* words, const uint32_
 }
 
 // Stores 8 consecutive columns of row m of the layer input: x = v (fp32),
-// xg = split(v * g) (bf16 hi, optional lo), and the row's sum of x^2 over the
+// xg = v * g in xg's layout (DTREE_W_TILED_F16: one fp16 plane; else bf16 hi,
+// optional lo), and the row's sum of x^2 over the
 // 32-column tile, added over the tile's 4 threads (a lane quad) with DPP.
 // Every thread of the wavefront calls it (the DPP needs all lanes); `in`
 // marks the threads that own a column group.
 __device__ __forceinline__ void fold_store8(const float (&v)[8], bool in, int m, int col, const uint16_t* g, int H,
-                                            float* x, uint16_t* xg, uint16_t* xg_lo, int xg_tiled, float* ss) {
+                                            float* x, uint16_t* xg, uint16_t* xg_lo, int xg_layout, float* ss) {
   if (in) {
     const u32x4_t gwv = ld_u32x4(g + col);
-    float y[8], r[8];
+    float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 8; ++i)
       y[i] = v[i] * __uint_as_float((i & 1) ? (gwv[i >> 1] & 0xffff0000u) : (gwv[i >> 1] << 16));
-      r[i] = y[i] - bf2f(f2bf(y[i]));
-    }
     float* xr = x + (size_t)m * H + col;
     *reinterpret_cast<f32x4_t*>(xr) = f32x4_t{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f32x4_t*>(xr + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
-    const size_t xi = xg_tiled ? tiled_index(m, col, H) : (size_t)m * H + col;
-    *reinterpret_cast<u32x4_t*>(xg + xi) =
-        u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])};
-    if (xg_lo)
-      *reinterpret_cast<u32x4_t*>(xg_lo + xi) =
-          u32x4_t{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3]), pack_bf2(r[4], r[5]), pack_bf2(r[6], r[7])};
+    const size_t xi = xg_layout != DTREE_W_ROWMAJOR ? tiled_index(m, col, H) : (size_t)m * H + col;
+    store_act8(xg, xg_lo, xi, y, xg_layout == DTREE_W_TILED_F16);
   }
   float sq = 0.f;
 #pragma unroll
@@ -74,7 +69,7 @@ __device__ __forceinline__ void fold_store8(const float (&v)[8], bool in, int m,
 __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, const uint16_t* emb, int layout,
                                                     const uint16_t* emb_sb, int V, int H,
                                                     const uint16_t* g, int MP, float* x, uint16_t* xg,
-                                                    uint16_t* xg_lo, int xg_tiled, float* ss,
+                                                    uint16_t* xg_lo, int xg_layout, float* ss,
                                                     int half, float base, float* cos_out, float* sin_out,
                                                     int gather_blocks) {
   if ((int)blockIdx.x >= gather_blocks) {
@@ -98,13 +93,13 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
           v[i] = q4_element(reinterpret_cast<const uint32_t*>(emb), reinterpret_cast<const uint32_t*>(emb_sb), tok,
                             col + i, H);
       } else {
-        const u32x4_t w = ld_u32x4(emb + (layout == DTREE_W_TILED ? tiled_index(tok, col, H) : (size_t)tok * H + col));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+        const bool tl = layout != DTREE_W_ROWMAJOR;  // tiled bf16, or tiled fp16 (TILED_F16)
+        unpack8(ld_u32x4(emb + (tl ? tiled_index(tok, col, H) : (size_t)tok * H + col)), layout == DTREE_W_TILED_F16,
+                v);
       }
     }
   }
-  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_tiled, ss);
+  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_layout, ss);
 }
 
 // Gather + fold for a token array of any length (prompt prefill): row m < n
@@ -112,7 +107,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const DtreeStepDesc* desc, c
 __global__ __launch_bounds__(256) void embed_tokens_kernel(const int32_t* tokens, int n, const uint16_t* emb,
                                                            int layout, const uint16_t* emb_sb, int V, int H,
                                                            const uint16_t* g, int MP, float* x, uint16_t* xg,
-                                                           uint16_t* xg_lo, int xg_tiled, float* ss) {
+                                                           uint16_t* xg_lo, int xg_layout, float* ss) {
   const int per_row = H >> 3;
   const long long gt = (long long)blockIdx.x * 256 + threadIdx.x;
   const bool in = gt < (long long)MP * per_row;
@@ -129,13 +124,13 @@ __global__ __launch_bounds__(256) void embed_tokens_kernel(const int32_t* tokens
           v[i] = q4_element(reinterpret_cast<const uint32_t*>(emb), reinterpret_cast<const uint32_t*>(emb_sb), tok,
                             col + i, H);
       } else {
-        const u32x4_t w = ld_u32x4(emb + (layout == DTREE_W_TILED ? tiled_index(tok, col, H) : (size_t)tok * H + col));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+        const bool tl = layout != DTREE_W_ROWMAJOR;  // tiled bf16, or tiled fp16 (TILED_F16)
+        unpack8(ld_u32x4(emb + (tl ? tiled_index(tok, col, H) : (size_t)tok * H + col)), layout == DTREE_W_TILED_F16,
+                v);
       }
     }
   }
-  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_tiled, ss);
+  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_layout, ss);
 }
 
 // The same layer-input fold for rows handed over by the caller (the DFlash
@@ -143,7 +138,7 @@ __global__ __launch_bounds__(256) void embed_tokens_kernel(const int32_t* tokens
 // >= n_rows zero), then fold_store8.
 __global__ __launch_bounds__(256) void rows_in_kernel(const uint16_t* rows, int ld_rows, int n_rows, const uint16_t* g,
                                                       int MP, int H, float* x, uint16_t* xg, uint16_t* xg_lo,
-                                                      int xg_tiled, float* ss) {
+                                                      int xg_layout, float* ss) {
   const int per_row = H >> 3;
   const int gt = blockIdx.x * 256 + threadIdx.x;
   const bool in = gt < MP * per_row;
@@ -156,7 +151,7 @@ __global__ __launch_bounds__(256) void rows_in_kernel(const uint16_t* rows, int 
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
   }
-  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_tiled, ss);
+  fold_store8(v, in, m, col, g, H, x, xg, xg_lo, xg_layout, ss);
 }
 
 
@@ -370,11 +365,25 @@ __global__ __launch_bounds__(256) void rownorm_kernel(const float* x, int ldx, i
   for (int m = 0; m < MP; ++m) out[(size_t)m * ld_out + col] = f2bf(x[(size_t)m * ldx + col] * rs[m] * gw);
 }
 
+// bf16 row-major -> tiled, bf16 or (H) fp16 elements: every bf16 of
+// magnitude 2^-17 .. 65504 converts to fp16 exactly; smaller ones round to
+// fp16's 2^-24 grid (nearest even), larger ones saturate to +-65504.
+template <bool H>
 __global__ __launch_bounds__(256) void tile_weight_kernel(const uint16_t* src, uint16_t* dst, int n, int k) {
   const size_t total = (size_t)n * k / 8;
   for (size_t v = (size_t)blockIdx.x * 256 + threadIdx.x; v < total; v += (size_t)gridDim.x * 256) {
     const int r = (int)(v / (k / 8)), k0 = (int)(v % (k / 8)) * 8;  // 8 consecutive columns of one row
-    *reinterpret_cast<u32x4_t*>(dst + tiled_index(r, k0, k)) = *reinterpret_cast<const u32x4_t*>(src + (size_t)r * k + k0);
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(src + (size_t)r * k + k0);
+    if constexpr (H) {
+      float f[8];
+      unpack8(w, false, f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = __builtin_amdgcn_fmed3f(f[i], -65504.f, 65504.f);
+      *reinterpret_cast<u32x4_t*>(dst + tiled_index(r, k0, k)) =
+          u32x4_t{pack_h2(f[0], f[1]), pack_h2(f[2], f[3]), pack_h2(f[4], f[5]), pack_h2(f[6], f[7])};
+    } else {
+      *reinterpret_cast<u32x4_t*>(dst + tiled_index(r, k0, k)) = w;
+    }
   }
 }
 
@@ -387,8 +396,18 @@ extern "C" int dtree_tile_weight(const uint16_t* src, uint16_t* dst, int32_t n, 
   DTREE_REQUIRE(n > 0 && k > 0 && n % 32 == 0 && k % 64 == 0, "tile_weight: n % 32 and k % 64");
   const size_t total = (size_t)n * k / 8;
   const int grid = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
-  tile_weight_kernel<<<grid, 256, 0, stream>>>(src, dst, n, k);
+  tile_weight_kernel<false><<<grid, 256, 0, stream>>>(src, dst, n, k);
   DTREE_LAUNCH_CHECK("tile_weight launch");
+  return DTREE_OK;
+}
+
+extern "C" int dtree_tile_weight_f16(const uint16_t* src, uint16_t* dst, int32_t n, int32_t k, hipStream_t stream) {
+  DTREE_REQUIRE(src && dst && src != dst, "tile_weight_f16: pointers");
+  DTREE_REQUIRE(n > 0 && k > 0 && n % 32 == 0 && k % 64 == 0, "tile_weight_f16: n % 32 and k % 64");
+  const size_t total = (size_t)n * k / 8;
+  const int grid = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+  tile_weight_kernel<true><<<grid, 256, 0, stream>>>(src, dst, n, k);
+  DTREE_LAUNCH_CHECK("tile_weight_f16 launch");
   return DTREE_OK;
 }
 
@@ -413,11 +432,13 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
   DTREE_REQUIRE(hidden > 0 && hidden % 32 == 0, "embed: hidden must be a multiple of 32");
   DTREE_REQUIRE(vocab > 0, "embed: vocab");
   DTREE_REQUIRE(embed_layout == DTREE_W_ROWMAJOR ||
-                    ((embed_layout == DTREE_W_TILED || embed_layout == DTREE_W_Q4G64) && hidden % 64 == 0 &&
-                     vocab % 32 == 0),
+                    ((embed_layout == DTREE_W_TILED || embed_layout == DTREE_W_TILED_F16 ||
+                      embed_layout == DTREE_W_Q4G64) && hidden % 64 == 0 && vocab % 32 == 0),
                 "embed: layout");
   DTREE_REQUIRE(embed_layout != DTREE_W_Q4G64 || embed_scales, "embed: q4 embedding needs embed_scales");
-  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || (xg_layout == DTREE_W_TILED && hidden % 64 == 0), "embed: xg layout");
+  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR ||
+                    ((xg_layout == DTREE_W_TILED || xg_layout == DTREE_W_TILED_F16) && hidden % 64 == 0),
+                "embed: xg layout");
   DTREE_REQUIRE(rows_padded > 0 && rows_padded <= DTREE_MAX_NODES && rows_padded % 32 == 0, "embed: rows_padded");
   DTREE_REQUIRE(((uintptr_t)embed & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
                     ((uintptr_t)xg & 15) == 0 && ((uintptr_t)xg_lo & 15) == 0,
@@ -430,7 +451,7 @@ extern "C" int dtree_embed(const DtreeStepDesc* desc, const uint16_t* embed, int
   }
   embed_kernel<<<gather + rope_blocks, 256, 0, stream>>>(desc, embed, embed_layout, embed_scales, vocab, hidden,
                                                           norm_w, rows_padded, x, xg, xg_lo,
-                                                          xg_layout == DTREE_W_TILED, ss, head_dim / 2, rope_base,
+                                                          xg_layout, ss, head_dim / 2, rope_base,
                                                           rope_cos, rope_sin, gather);
   DTREE_LAUNCH_CHECK("embed launch");
   return DTREE_OK;
@@ -443,10 +464,12 @@ extern "C" int dtree_embed_tokens(const int32_t* tokens, int32_t n, const uint16
   DTREE_REQUIRE(tokens && embed && norm_w && x && xg && ss, "embed_tokens: null pointer");
   DTREE_REQUIRE(hidden > 0 && hidden % 64 == 0, "embed_tokens: hidden must be a multiple of 64");
   DTREE_REQUIRE(vocab > 0 && vocab % 32 == 0, "embed_tokens: vocab");
-  DTREE_REQUIRE(embed_layout == DTREE_W_ROWMAJOR || embed_layout == DTREE_W_TILED || embed_layout == DTREE_W_Q4G64,
+  DTREE_REQUIRE(embed_layout == DTREE_W_ROWMAJOR || embed_layout == DTREE_W_TILED ||
+                    embed_layout == DTREE_W_TILED_F16 || embed_layout == DTREE_W_Q4G64,
                 "embed_tokens: layout");
   DTREE_REQUIRE(embed_layout != DTREE_W_Q4G64 || embed_scales, "embed_tokens: q4 embedding needs embed_scales");
-  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || xg_layout == DTREE_W_TILED, "embed_tokens: xg layout");
+  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || xg_layout == DTREE_W_TILED || xg_layout == DTREE_W_TILED_F16,
+                "embed_tokens: xg layout");
   DTREE_REQUIRE(rows_padded > 0 && rows_padded % 32 == 0 && rows_padded <= (1 << 20) && n >= 0 && n <= rows_padded,
                 "embed_tokens: rows_padded (a multiple of 32) and n <= rows_padded");
   DTREE_REQUIRE(((uintptr_t)embed & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
@@ -455,7 +478,7 @@ extern "C" int dtree_embed_tokens(const int32_t* tokens, int32_t n, const uint16
   const long long threads = (long long)rows_padded * (hidden / 8);
   embed_tokens_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
       tokens, n, embed, embed_layout, embed_scales, vocab, hidden, norm_w, rows_padded, x, xg, xg_lo,
-      xg_layout == DTREE_W_TILED, ss);
+      xg_layout, ss);
   DTREE_LAUNCH_CHECK("embed_tokens launch");
   return DTREE_OK;
 }
@@ -468,13 +491,14 @@ extern "C" int dtree_rows_in(const uint16_t* rows, int32_t ld_rows, int32_t n_ro
   DTREE_REQUIRE(rows_padded > 0 && rows_padded <= DTREE_MAX_NODES && rows_padded % 32 == 0, "rows_in: rows_padded");
   DTREE_REQUIRE(n_rows >= 0 && n_rows <= rows_padded, "rows_in: n_rows");
   DTREE_REQUIRE(ld_rows >= hidden && ld_rows % 8 == 0, "rows_in: ld_rows (>= hidden, a multiple of 8)");
-  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || xg_layout == DTREE_W_TILED, "rows_in: xg layout");
+  DTREE_REQUIRE(xg_layout == DTREE_W_ROWMAJOR || xg_layout == DTREE_W_TILED || xg_layout == DTREE_W_TILED_F16,
+                "rows_in: xg layout");
   DTREE_REQUIRE(((uintptr_t)rows & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)x & 15) == 0 &&
                     ((uintptr_t)xg & 15) == 0 && ((uintptr_t)xg_lo & 15) == 0,
                 "rows_in: rows, norm_w, x, xg and xg_lo must be 16-byte aligned");
   const int grid = (rows_padded * (hidden / 8) + 255) / 256;
   rows_in_kernel<<<grid, 256, 0, stream>>>(rows, ld_rows, n_rows, norm_w, rows_padded, hidden, x, xg, xg_lo,
-                                           xg_layout == DTREE_W_TILED, ss);
+                                           xg_layout, ss);
   DTREE_LAUNCH_CHECK("rows_in launch");
   return DTREE_OK;
 }

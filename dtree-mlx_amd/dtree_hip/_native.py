@@ -16,7 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
 MAX_NODES = 128
 MASK_WORDS = 4
 PAGE = 64
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 E_OK, E_ARG, E_HIP, E_TREE, E_WORKSPACE = 0, -1, -2, -3, -4
 
@@ -27,6 +27,7 @@ EPI_STORE_BF16 = 3
 
 W_ROWMAJOR = 0
 W_TILED = 1
+W_TILED_F16 = 3  # tiled fp16 weights + one fp16 activation plane
 W_Q4G64 = 2
 
 
@@ -135,6 +136,7 @@ SIGNATURES = {
     "dtree_lmhead_argmax": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _f32, _vp,
                                       _vp, _vp]),
     "dtree_tile_weight": (C.c_int, [_vp, _vp, _i32, _i32, _vp]),
+    "dtree_tile_weight_f16": (C.c_int, [_vp, _vp, _i32, _i32, _vp]),
     "dtree_accept_walk": (C.c_int, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "dtree_compact": (C.c_int, [_vp, _vp, _vp, _sz, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
     "dtree_rownorm": (C.c_int, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _f32, _vp, _i32, _vp]),

@@ -45,7 +45,7 @@ from . import _native as N
 from .cache import PagedKVCache
 from .config import Qwen3Config
 from .engine import Qwen3TreeEngine
-from .weights import Q4Linear, Qwen3Weights, q4_random_mlx, q4_to_tiled, tile_weight
+from .weights import Q4Linear, Qwen3Weights, fp16_exact_bf16, q4_random_mlx, q4_to_tiled, tile_weight_f16
 
 CONTEXT_SINK = 64      # ContextOnlyDraftKVCache defaults, draft.py:68
 CONTEXT_WINDOW = 1024
@@ -156,7 +156,7 @@ class DFlashWeights:
         elif quant == "bf16":
             stack = Qwen3Weights.random(scfg, seed=seed, device=dev, std=std, norm_jitter=norm_jitter)
             t = torch.empty(args.hidden_size, n_in, dtype=torch.float32, device=dev).normal_(0.0, std, generator=gen)
-            fc = tile_weight(t.to(torch.bfloat16))
+            fc = tile_weight_f16(fp16_exact_bf16(t))
         else:
             raise NotImplementedError(f"draft weights {quant!r}: bf16 or q4")
         if norm_jitter:
@@ -262,9 +262,9 @@ class DFlashDraftEngine(Qwen3TreeEngine):
         c, CT, dev = self.cfg, self.CTX_ROWS, self.dev
         bf16, f32 = torch.bfloat16, torch.float32
         self.th_rm = torch.zeros(CT, self.n_in, dtype=bf16, device=dev)
-        self.th_t = torch.zeros(CT, self.n_in, dtype=bf16, device=dev)
+        self.th_t = torch.zeros(CT, self.n_in, dtype=self.act_dtype, device=dev)
         self.x_ctx = torch.zeros(CT, c.hidden_size, dtype=f32, device=dev)
-        self.ctx_g = torch.zeros(2, CT, c.hidden_size, dtype=bf16, device=dev)
+        self.ctx_g = torch.zeros(2, CT, c.hidden_size, dtype=self.act_dtype, device=dev)
         self.ss_ctx = torch.zeros(CT // 32, c.hidden_size // 32, 32, dtype=f32, device=dev)
         self.kv = torch.zeros(CT, 2 * c.kv_dim, dtype=f32, device=dev)
         self.noise = torch.zeros(self.MP, c.hidden_size, dtype=bf16, device=dev)
@@ -295,7 +295,8 @@ class DFlashDraftEngine(Qwen3TreeEngine):
         self.th_rm[:n].copy_(rows)
         if rp > n:
             self.th_rm[n:rp].zero_()
-        N.check(self.lib.dtree_tile_weight(self.th_rm.data_ptr(), self.th_t.data_ptr(), rp, self.n_in, st),
+        tile = self.lib.dtree_tile_weight_f16 if self.h16 else self.lib.dtree_tile_weight
+        N.check(tile(self.th_rm.data_ptr(), self.th_t.data_ptr(), rp, self.n_in, st),
                 "tile target hidden")
         self.x_ctx[:rp].zero_()
         self._ctx_gemm("fc", rp, self.th_t[:rp], self.n_in, self.dw.fc, N.EPI_RESIDUAL, st, out_f32=self.x_ctx,
@@ -358,7 +359,7 @@ class DFlashDraftEngine(Qwen3TreeEngine):
         self.noise[:L].copy_(noise)
         N.check(self.lib.dtree_rows_in(
             self.noise.data_ptr(), c.hidden_size, L, self.w.layers[0].input_norm.data_ptr(), self.MP, c.hidden_size,
-            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(), st),
+            self.x.data_ptr(), self.xg[0].data_ptr(), self.lo_ptr(self.xg), self.w.layout, self.ss.data_ptr(), st),
             "rows in")
         N.check(self.lib.dtree_rope_table(self.desc.data_ptr(), self.MP, c.head_dim, c.rope_theta,
                                           self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "rope table")

@@ -25,7 +25,7 @@ import torch
 from . import _native as N
 from .cache import PagedKVCache
 from .config import Qwen3Config
-from .weights import W_TILED, Q4Linear, Qwen3Weights, tile_weight
+from .weights import W_TILED, W_TILED_F16, Q4Linear, Qwen3Weights, tile_weight, tile_weight_f16
 
 
 _HIP = None
@@ -140,9 +140,13 @@ class TreeEngineBase:
         H, V = cfg.hidden_size, cfg.vocab_size
         MP, dev = self.MP, self.dev
         f32, bf16 = torch.float32, torch.bfloat16
-        # GEMM inputs are split pairs [hi, lo] of bf16 planes (value = hi + lo).
+        # GEMM inputs: with DTREE_W_TILED_F16 weights one fp16 plane (plane 0
+        # of the plane buffers; plane 1 stays unused), else split pairs
+        # [hi, lo] of bf16 planes (value = hi + lo).
+        self.h16 = weights.layout == W_TILED_F16
+        self.act_dtype = torch.float16 if self.h16 else bf16
         self.x = torch.zeros(MP, H, dtype=f32, device=dev)
-        self.xg = torch.zeros(2, MP, H, dtype=bf16, device=dev)
+        self.xg = torch.zeros(2, MP, H, dtype=self.act_dtype, device=dev)
         # RMSNorm statistics: per 32-row block, per 32-column tile, per row
         self.ss = torch.zeros(MP // 32, H // 32, 32, dtype=f32, device=dev)
         self.norm_hidden = torch.zeros(MP, H, dtype=bf16, device=dev)
@@ -250,8 +254,8 @@ class TreeEngineBase:
                   ss_out=None, hidden_out=0, ld_hidden=0) -> N.GemmArgs:
         n, k = w.shape
         a = N.GemmArgs()
-        if x.dim() == 3:  # split pair [hi, lo]
-            a.x = x[0].data_ptr(); a.x_lo = None if name in self.HI_ONLY else x[1].data_ptr()
+        if x.dim() == 3:  # plane buffers: [fp16] (tiled) or split pair [hi, lo]
+            a.x = x[0].data_ptr(); a.x_lo = None if name in self.HI_ONLY else self.lo_ptr(x)
         else:
             a.x = x.data_ptr()
         a.ldx = ldx; a.rows_padded = self.MP
@@ -270,7 +274,7 @@ class TreeEngineBase:
             a.out_f32 = out_f32.data_ptr(); a.ld_out_f32 = out_f32.shape[1]
         if out_bf16 is not None:
             if out_bf16.dim() == 3:
-                a.out_bf16 = out_bf16[0].data_ptr(); a.out_lo = out_bf16[1].data_ptr()
+                a.out_bf16 = out_bf16[0].data_ptr(); a.out_lo = self.lo_ptr(out_bf16)
             else:
                 a.out_bf16 = out_bf16.data_ptr()
             a.ld_out_bf16 = out_bf16.shape[-1]
@@ -280,6 +284,10 @@ class TreeEngineBase:
         a.hidden_out = hidden_out or None; a.ld_hidden = ld_hidden
         a.workspace = self.gemm_ws.data_ptr(); a.workspace_bytes = self.gemm_ws.numel()
         return a
+
+    def lo_ptr(self, t: torch.Tensor, offset_bytes: int = 0):
+        """Low plane of a plane buffer: none on the fp16 path (one plane)."""
+        return None if self.h16 else t[1].data_ptr() + offset_bytes
 
     def _embedding(self):
         """(pointer, layout, scale/bias pointer) of the tied embedding."""
@@ -335,7 +343,7 @@ class TreeEngineBase:
             self.logits = torch.zeros(self.MP, c.vocab_size, dtype=torch.float32, device=self.dev)
         xo = b * 32 * H
         N.check(self.lib.dtree_lmhead_argmax(
-            pf["xg"][0].data_ptr() + 2 * xo, pf["xg"][1].data_ptr() + 2 * xo, self.w.layout, H, 32, emb,
+            pf["xg"][0].data_ptr() + 2 * xo, self.lo_ptr(pf["xg"], 2 * xo), self.w.layout, H, 32, emb,
             emb_layout, emb_sb, c.vocab_size, H, pf["ss"][b].data_ptr(), H // 32, c.rms_norm_eps,
             self.logits.data_ptr(), self.cand.data_ptr(), st), "prefill lm head")
         return self.logits[r:r + 1].clone()[None]
@@ -349,12 +357,12 @@ class TreeEngineBase:
             logits_ptr = self.logits.data_ptr()
         if x is None:
             xin = self.xg
-        elif self.w.layout == W_TILED:  # caller rows are row-major [MP, H]
-            self._lm_tiled = tile_weight(x)
+        elif self.w.layout in (W_TILED, W_TILED_F16):  # caller rows are row-major [MP, H]
+            self._lm_tiled = tile_weight_f16(x) if self.h16 else tile_weight(x)
             xin = self._lm_tiled
         else:
             xin = x
-        hi, lo = (xin[0].data_ptr(), xin[1].data_ptr()) if xin.dim() == 3 else (xin.data_ptr(), None)
+        hi, lo = (xin[0].data_ptr(), self.lo_ptr(xin)) if xin.dim() == 3 else (xin.data_ptr(), None)
         emb, emb_layout, emb_sb = self._embedding()
         N.check(self.lib.dtree_lmhead_argmax(
             hi, lo, self.w.layout, xin.shape[-1], self.MP, emb, emb_layout, emb_sb, c.vocab_size, c.hidden_size,
@@ -601,8 +609,8 @@ class Qwen3TreeEngine(TreeEngineBase):
         c, MP, dev = self.cfg, self.MP, self.dev
         f32, bf16 = torch.float32, torch.bfloat16
         self.qkv = torch.zeros(MP, c.qkv_dim, dtype=f32, device=dev)
-        self.attn = torch.zeros(2, MP, c.q_dim, dtype=bf16, device=dev)
-        self.act = torch.zeros(2, MP, c.intermediate_size, dtype=bf16, device=dev)
+        self.attn = torch.zeros(2, MP, c.q_dim, dtype=self.act_dtype, device=dev)
+        self.act = torch.zeros(2, MP, c.intermediate_size, dtype=self.act_dtype, device=dev)
         self.rope_cos = torch.zeros(MP, c.head_dim // 2, dtype=f32, device=dev)
         self.rope_sin = torch.zeros(MP, c.head_dim // 2, dtype=f32, device=dev)
         aws = self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim, self.max_past, self.MP)
@@ -632,7 +640,7 @@ class Qwen3TreeEngine(TreeEngineBase):
         a.rope_cos = self.rope_cos.data_ptr(); a.rope_sin = self.rope_sin.data_ptr()
         a.k_pages = cache.k_ptr(li); a.v_pages = cache.v_ptr(li); a.page_table = cache.page_table.data_ptr()
         a.desc = self.desc.data_ptr()
-        a.out = self.attn[0].data_ptr(); a.out_lo = self.attn[1].data_ptr(); a.ld_out = self.attn.shape[-1]
+        a.out = self.attn[0].data_ptr(); a.out_lo = self.lo_ptr(self.attn); a.ld_out = self.attn.shape[-1]
         a.out_layout = self.w.layout
         a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
         a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
@@ -651,7 +659,7 @@ class Qwen3TreeEngine(TreeEngineBase):
             self.desc.data_ptr(), emb, emb_layout, emb_sb, c.vocab_size, H,
             self.w.layers[0].input_norm.data_ptr(),
             self.MP,
-            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
+            self.x.data_ptr(), self.xg[0].data_ptr(), self.lo_ptr(self.xg), self.w.layout, self.ss.data_ptr(),
             c.head_dim, c.rope_theta,
             self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
         self.attn_max_past = self.attn_grid_past(self._step_past)
@@ -686,7 +694,7 @@ class Qwen3TreeEngine(TreeEngineBase):
 
     # ---- prompt prefill on the long-M GEMM (adapters.py:494-533) ---------------
     def supports_long_prefill(self) -> bool:
-        return self.w.layout == W_TILED  # bf16 or q4 group-64 weights
+        return self.w.layout in (W_TILED, W_TILED_F16)  # bf16 or q4 group-64 weights
 
     def _prefill_buffers(self, rows: int) -> dict:
         pf = getattr(self, "_pf", None)
@@ -699,11 +707,11 @@ class Qwen3TreeEngine(TreeEngineBase):
         pf = dict(rows=rows, nh=nh,
                   tokens=torch.zeros(rows, dtype=torch.int32, device=dev),
                   x=torch.zeros(rows, H, dtype=f32, device=dev),
-                  xg=torch.zeros(2, rows, H, dtype=bf16, device=dev),
+                  xg=torch.zeros(2, rows, H, dtype=self.act_dtype, device=dev),
                   ss=torch.zeros(rows // 32, H // 32, 32, dtype=f32, device=dev),
                   qkv=torch.zeros(rows, c.qkv_dim, dtype=f32, device=dev),
-                  attn=torch.zeros(2, rows, c.q_dim, dtype=bf16, device=dev),
-                  act=torch.zeros(2, rows, F, dtype=bf16, device=dev),
+                  attn=torch.zeros(2, rows, c.q_dim, dtype=self.act_dtype, device=dev),
+                  act=torch.zeros(2, rows, F, dtype=self.act_dtype, device=dev),
                   hidden=torch.zeros(rows, nh * H, dtype=bf16, device=dev),
                   cos=torch.zeros(rows, D // 2, dtype=f32, device=dev),
                   sin=torch.zeros(rows, D // 2, dtype=f32, device=dev),
@@ -748,7 +756,7 @@ class Qwen3TreeEngine(TreeEngineBase):
             N.check(self.lib.dtree_embed_tokens(
                 pf["tokens"].data_ptr(), n, emb, emb_layout, emb_sb, c.vocab_size, H,
                 self.w.layers[0].input_norm.data_ptr(), rows, pf["x"].data_ptr(), pf["xg"][0].data_ptr(),
-                pf["xg"][1].data_ptr(), self.w.layout, pf["ss"].data_ptr(), st), "embed tokens")
+                self.lo_ptr(pf["xg"]), self.w.layout, pf["ss"].data_ptr(), st), "embed tokens")
             dstride = self._prefill_chunks(pf, P0, n, rows, D, st)
             nL = c.num_hidden_layers
             for li in range(nL):
@@ -764,7 +772,8 @@ class Qwen3TreeEngine(TreeEngineBase):
                     a.k_pages = cache.k_ptr(li); a.v_pages = cache.v_ptr(li)
                     a.page_table = cache.page_table.data_ptr()
                     a.desc = pf["descs"].data_ptr() + ch * dstride
-                    a.out = pf["attn"][0, 128 * ch].data_ptr(); a.out_lo = pf["attn"][1, 128 * ch].data_ptr()
+                    a.out = pf["attn"][0, 128 * ch].data_ptr()
+                    a.out_lo = self.lo_ptr(pf["attn"], 2 * 128 * ch * c.q_dim)
                     a.ld_out = c.q_dim; a.out_layout = self.w.layout
                     a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = D
                     a.rows_padded = 128; a.scale = D ** -0.5

@@ -32,7 +32,7 @@ import torch
 from . import _native as N
 from .cache import Qwen35Cache
 from .engine import TreeEngineBase
-from .weights import W_TILED, GdnLayerWeights
+from .weights import W_TILED, W_TILED_F16, GdnLayerWeights
 
 
 class Qwen35TreeEngine(TreeEngineBase):
@@ -54,10 +54,10 @@ class Qwen35TreeEngine(TreeEngineBase):
         self.gg = torch.zeros(nG, MP, Hv, dtype=f32, device=dev)
         self.gbeta = torch.zeros(nG, MP, Hv, dtype=f32, device=dev)
         self.gy = torch.zeros(MP, c.value_dim, dtype=f32, device=dev)
-        self.gout = torch.zeros(2, MP, c.value_dim, dtype=bf16, device=dev)
+        self.gout = torch.zeros(2, MP, c.value_dim, dtype=self.act_dtype, device=dev)
         self.qkv = torch.zeros(MP, c.attn_qkv_dim, dtype=f32, device=dev)
-        self.attn = torch.zeros(2, MP, c.q_dim, dtype=bf16, device=dev)
-        self.act = torch.zeros(2, MP, c.intermediate_size, dtype=bf16, device=dev)
+        self.attn = torch.zeros(2, MP, c.q_dim, dtype=self.act_dtype, device=dev)
+        self.act = torch.zeros(2, MP, c.intermediate_size, dtype=self.act_dtype, device=dev)
         self.rope_cos = torch.zeros(MP, c.rope_dims // 2, dtype=f32, device=dev)
         self.rope_sin = torch.zeros(MP, c.rope_dims // 2, dtype=f32, device=dev)
         aws = self.lib.dtree_attention_workspace_bytes(c.num_attention_heads, c.head_dim, self.max_past, self.MP)
@@ -100,7 +100,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         a.g = self.gg[gi].data_ptr(); a.beta = self.gbeta[gi].data_ptr()
         a.y = self.gy.data_ptr()
         a.norm_w = lw.gnorm.data_ptr(); a.eps = c.rms_norm_eps
-        a.out = self.gout[0].data_ptr(); a.out_lo = self.gout[1].data_ptr()
+        a.out = self.gout[0].data_ptr(); a.out_lo = self.lo_ptr(self.gout)
         a.out_layout = self.w.layout; a.ld_out = c.value_dim
         return a
 
@@ -115,7 +115,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         a.rope_cos = self.rope_cos.data_ptr(); a.rope_sin = self.rope_sin.data_ptr()
         a.k_pages = kv.k_ptr(ai); a.v_pages = kv.v_ptr(ai); a.page_table = kv.page_table.data_ptr()
         a.desc = self.desc.data_ptr()
-        a.out = self.attn[0].data_ptr(); a.out_lo = self.attn[1].data_ptr(); a.ld_out = self.attn.shape[-1]
+        a.out = self.attn[0].data_ptr(); a.out_lo = self.lo_ptr(self.attn); a.ld_out = self.attn.shape[-1]
         a.out_layout = self.w.layout
         a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads; a.head_dim = c.head_dim
         a.rows_padded = self.MP; a.scale = c.head_dim ** -0.5
@@ -135,7 +135,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         N.check(self.lib.dtree_embed(
             self.desc.data_ptr(), emb, emb_layout, emb_sb, c.vocab_size, H,
             self.w.layers[0].input_norm.data_ptr(), self.MP,
-            self.x.data_ptr(), self.xg[0].data_ptr(), self.xg[1].data_ptr(), self.w.layout, self.ss.data_ptr(),
+            self.x.data_ptr(), self.xg[0].data_ptr(), self.lo_ptr(self.xg), self.w.layout, self.ss.data_ptr(),
             c.rope_dims, c.rope_theta, self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), st), "embed")
         slot = {li: i for i, li in enumerate(self.layer_ids)}
         nL = c.num_hidden_layers
@@ -235,7 +235,7 @@ class Qwen35TreeEngine(TreeEngineBase):
     # ---- prompt prefill on the long-M GEMM (forward_dflash,
     # custom_qwen35_model.py:961-1097, via adapters.py:290-307) ---------------------
     def supports_long_prefill(self) -> bool:
-        return self.w.layout == W_TILED  # bf16 or q4 group-64 weights
+        return self.w.layout in (W_TILED, W_TILED_F16)  # bf16 or q4 group-64 weights
 
     def _prefill_buffers(self, rows: int) -> dict:
         pf = getattr(self, "_pf", None)
@@ -250,7 +250,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         pf = dict(rows=rows, nh=nh,
                   tokens=torch.zeros(rows, dtype=torch.int32, device=dev),
                   x=torch.zeros(rows, H, dtype=f32, device=dev),
-                  xg=torch.zeros(2, rows, H, dtype=bf16, device=dev),
+                  xg=torch.zeros(2, rows, H, dtype=self.act_dtype, device=dev),
                   ss=torch.zeros(rows // 32, H // 32, 32, dtype=f32, device=dev),
                   proj=torch.zeros(rows, c.in_proj_dim, dtype=f32, device=dev),
                   q=torch.zeros(rows, c.key_dim, dtype=f32, device=dev),
@@ -259,10 +259,10 @@ class Qwen35TreeEngine(TreeEngineBase):
                   g=torch.zeros(rows, Hv, dtype=f32, device=dev),
                   beta=torch.zeros(rows, Hv, dtype=f32, device=dev),
                   y=torch.zeros(rows, c.value_dim, dtype=f32, device=dev),
-                  gout=torch.zeros(2, rows, c.value_dim, dtype=bf16, device=dev),
+                  gout=torch.zeros(2, rows, c.value_dim, dtype=self.act_dtype, device=dev),
                   qkv=torch.zeros(rows, c.attn_qkv_dim, dtype=f32, device=dev),
-                  attn=torch.zeros(2, rows, c.q_dim, dtype=bf16, device=dev),
-                  act=torch.zeros(2, rows, F, dtype=bf16, device=dev),
+                  attn=torch.zeros(2, rows, c.q_dim, dtype=self.act_dtype, device=dev),
+                  act=torch.zeros(2, rows, F, dtype=self.act_dtype, device=dev),
                   hidden=torch.zeros(rows, nh * H, dtype=bf16, device=dev),
                   cos=torch.zeros(rows, c.rope_dims // 2, dtype=f32, device=dev),
                   sin=torch.zeros(rows, c.rope_dims // 2, dtype=f32, device=dev),
@@ -289,7 +289,7 @@ class Qwen35TreeEngine(TreeEngineBase):
         a.q = pf["q"].data_ptr(); a.k = pf["k"].data_ptr(); a.v = pf["v"].data_ptr()
         a.g = pf["g"].data_ptr(); a.beta = pf["beta"].data_ptr(); a.y = pf["y"].data_ptr()
         a.norm_w = lw.gnorm.data_ptr(); a.eps = c.rms_norm_eps
-        a.out = pf["gout"][0].data_ptr(); a.out_lo = pf["gout"][1].data_ptr()
+        a.out = pf["gout"][0].data_ptr(); a.out_lo = self.lo_ptr(pf["gout"])
         a.out_layout = self.w.layout; a.ld_out = c.value_dim
         return a
 
@@ -331,7 +331,7 @@ class Qwen35TreeEngine(TreeEngineBase):
             N.check(self.lib.dtree_embed_tokens(
                 pf["tokens"].data_ptr(), n, emb, emb_layout, emb_sb, c.vocab_size, H,
                 self.w.layers[0].input_norm.data_ptr(), rows, pf["x"].data_ptr(), pf["xg"][0].data_ptr(),
-                pf["xg"][1].data_ptr(), self.w.layout, pf["ss"].data_ptr(), st), "embed tokens")
+                self.lo_ptr(pf["xg"]), self.w.layout, pf["ss"].data_ptr(), st), "embed tokens")
             dstride = self._prefill_chunks(pf, P0, n, rows, c.rope_dims, st)
             nL = c.num_hidden_layers
             for li in range(nL):
@@ -355,7 +355,8 @@ class Qwen35TreeEngine(TreeEngineBase):
                         a.rope_cos = pf["cos"][128 * ch].data_ptr(); a.rope_sin = pf["sin"][128 * ch].data_ptr()
                         a.k_pages = kv.k_ptr(ai); a.v_pages = kv.v_ptr(ai); a.page_table = kv.page_table.data_ptr()
                         a.desc = pf["descs"].data_ptr() + ch * dstride
-                        a.out = pf["attn"][0, 128 * ch].data_ptr(); a.out_lo = pf["attn"][1, 128 * ch].data_ptr()
+                        a.out = pf["attn"][0, 128 * ch].data_ptr()
+                        a.out_lo = self.lo_ptr(pf["attn"], 2 * 128 * ch * c.q_dim)
                         a.ld_out = c.q_dim; a.out_layout = self.w.layout
                         a.num_heads = c.num_attention_heads; a.num_kv_heads = c.num_key_value_heads
                         a.head_dim = D; a.rows_padded = 128; a.scale = D ** -0.5

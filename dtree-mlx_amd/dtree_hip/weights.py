@@ -28,7 +28,7 @@ import torch
 from .config import Qwen3Config
 
 
-W_ROWMAJOR, W_TILED, W_Q4G64 = 0, 1, 2
+W_ROWMAJOR, W_TILED, W_Q4G64, W_TILED_F16 = 0, 1, 2, 3
 
 
 def tile_weight(w: torch.Tensor) -> torch.Tensor:
@@ -40,7 +40,26 @@ def tile_weight(w: torch.Tensor) -> torch.Tensor:
     return t.permute(0, 2, 4, 3, 1, 5).contiguous().reshape(n, k)  # r, b, i, (h, c), e
 
 
+def tile_weight_f16(w: torch.Tensor) -> torch.Tensor:
+    """[n, k] row-major (bf16 or any float) -> DTREE_W_TILED_F16: tile_weight's
+    order with fp16 elements (nearest even, saturating at +-65504; every bf16
+    of magnitude 2^-17 .. 65504 converts exactly)."""
+    if w.dtype != torch.float16:
+        w = w.float().clamp(-65504.0, 65504.0).to(torch.float16)
+    return tile_weight(w)
+
+
+def fp16_exact_bf16(t: torch.Tensor) -> torch.Tensor:
+    """bf16 weights that fp16 holds exactly: magnitudes below 2^-17 (3e-4 of
+    an N(0, 0.02) draw) become zero; every other bf16 up to 65504 converts to
+    fp16 without rounding, so the bf16 model and its DTREE_W_TILED_F16 copy
+    are the same matrix."""
+    t = t.to(torch.bfloat16)
+    return torch.where(t.abs() < 2.0 ** -17, torch.zeros_like(t), t)
+
+
 def untile_weight(t: torch.Tensor) -> torch.Tensor:
+    """Inverse permutation of tile_weight / tile_weight_f16 (element type kept)."""
     n, k = t.shape
     u = t.reshape(n // 32, k // 64, 4, 2, 32, 8)         # r, b, i, h, c, e
     return u.permute(0, 4, 1, 3, 2, 5).contiguous().reshape(n, k)
@@ -215,9 +234,11 @@ class Qwen3Weights:
 
     @classmethod
     def random(cls, cfg: Qwen3Config, seed: int = 0, device="cuda", std: float = 0.02,
-               norm_jitter: float = 0.0, layout: int = W_TILED) -> "Qwen3Weights":
-        """Seeded random init on `device` (norm weights 1, or 1 + N(0, jitter))."""
-        lay = tile_weight if layout == W_TILED else (lambda t: t)
+               norm_jitter: float = 0.0, layout: int = W_TILED_F16) -> "Qwen3Weights":
+        """Seeded random init on `device` (norm weights 1, or 1 + N(0, jitter));
+        linear weights N(0, std) as fp16-exact bf16 (fp16_exact_bf16), stored
+        in `layout` (the fp16 tiled copy by default)."""
+        lay = {W_TILED_F16: tile_weight_f16, W_TILED: tile_weight}.get(layout, lambda t: t)
         cfg.validate()
         dev = torch.device(device)
         gen = torch.Generator(device=dev)
@@ -226,7 +247,7 @@ class Qwen3Weights:
         def lin(rows, cols):
             t = torch.empty(rows, cols, dtype=torch.float32, device=dev)
             t.normal_(0.0, std, generator=gen)
-            return t.to(torch.bfloat16)
+            return fp16_exact_bf16(t)
 
         def norm(n):
             if norm_jitter == 0.0:
@@ -260,12 +281,16 @@ class Qwen3Weights:
         """nn.Linear-order bf16 (or, for q4, dequantised fp32) matrix."""
         if isinstance(t, Q4Linear):
             return q4_dequant(t)
+        if self.layout == W_TILED_F16:  # exact: the weights are fp16_exact_bf16
+            return untile_weight(t).to(torch.bfloat16)
         return untile_weight(t) if self.layout == W_TILED else t
 
     def embed_rows(self, ids: torch.Tensor) -> torch.Tensor:
         if isinstance(self.embed, Q4Linear):
             return q4_rows(self.embed, ids)
-        return tiled_rows(self.embed, ids) if self.layout == W_TILED else self.embed[ids.long()]
+        if self.layout in (W_TILED, W_TILED_F16):
+            return tiled_rows(self.embed, ids).to(torch.bfloat16)
+        return self.embed[ids.long()]
 
     def nbytes_linear(self) -> int:
         if self.quant == "q4":
@@ -281,6 +306,8 @@ class Qwen3Weights:
         def bits(t: torch.Tensor) -> np.ndarray:
             if t.dtype == torch.float32:  # dequantised q4: handed over as fp32
                 return t.detach().to("cpu").contiguous().numpy()
+            if t.dtype == torch.float16:  # a DTREE_W_TILED_F16 weight: exact in bf16 (fp16_exact_bf16)
+                t = t.to(torch.bfloat16)
             return t.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16)
 
         def lin_bits(t: torch.Tensor) -> np.ndarray:
@@ -372,7 +399,7 @@ class Qwen35Weights:
         def lin_bf16(rows, cols):
             t = torch.empty(rows, cols, dtype=torch.float32, device=dev)
             t.normal_(0.0, std, generator=gen)
-            return t.to(torch.bfloat16)
+            return fp16_exact_bf16(t)
 
         def pad_rows(t, rows):
             return torch.cat([t, t.new_zeros(rows - t.shape[0], *t.shape[1:])]) if rows > t.shape[0] else t
@@ -384,7 +411,7 @@ class Qwen35Weights:
                     wq, s, b = pad_rows(wq, pad_to), pad_rows(s, pad_to), pad_rows(b, pad_to)
                 return Q4Linear(*q4_to_tiled(wq, s, b))
             t = lin_bf16(rows, cols)
-            return tile_weight(pad_rows(t, pad_to) if pad_to else t)
+            return tile_weight_f16(pad_rows(t, pad_to) if pad_to else t)
 
         def gate_up():
             if quant == "q4":
@@ -392,7 +419,7 @@ class Qwen35Weights:
                 uq, us, ub = q4_random_mlx(F, H, gen, dev)
                 return Q4Linear(*q4_to_tiled(interleave_gate_up(gq, uq), interleave_gate_up(gs, us),
                                             interleave_gate_up(gb, ub)))
-            return tile_weight(interleave_gate_up(lin_bf16(F, H), lin_bf16(F, H)))
+            return tile_weight_f16(interleave_gate_up(lin_bf16(F, H), lin_bf16(F, H)))
 
         def norm(n):
             if norm_jitter == 0.0:
@@ -419,17 +446,22 @@ class Qwen35Weights:
                     input_norm=norm(H), wqkv=lin(cfg.attn_qkv_dim, H), q_norm=norm(cfg.head_dim),
                     k_norm=norm(cfg.head_dim), wo=lin(H, cfg.q_dim), post_norm=norm(H), wgu=gate_up(),
                     wd=lin(H, F)))
-        return cls(cfg=cfg, embed=embed, final_norm=norm(H), layers=layers, layout=W_TILED, quant=quant)
+        # bf16 weights are held as the fp16 tiled copy; q4 keeps tiled bf16
+        # activations (its random residual stream leaves the fp16 range)
+        return cls(cfg=cfg, embed=embed, final_norm=norm(H), layers=layers,
+                   layout=W_TILED_F16 if quant == "bf16" else W_TILED, quant=quant)
 
     def rowmajor(self, t) -> torch.Tensor:
         if isinstance(t, Q4Linear):
             return q4_dequant(t)
+        if self.layout == W_TILED_F16:
+            return untile_weight(t).to(torch.bfloat16)
         return untile_weight(t) if self.layout == W_TILED else t
 
     def embed_rows(self, ids: torch.Tensor) -> torch.Tensor:
         if isinstance(self.embed, Q4Linear):
             return q4_rows(self.embed, ids)
-        return tiled_rows(self.embed, ids)
+        return tiled_rows(self.embed, ids).to(torch.bfloat16)
 
     def nbytes_linear(self) -> int:
         def nb(t):
@@ -451,6 +483,8 @@ class Qwen35Weights:
         def bits(t: torch.Tensor) -> np.ndarray:
             if t.dtype == torch.float32:
                 return t.detach().to("cpu").contiguous().numpy()
+            if t.dtype == torch.float16:  # a DTREE_W_TILED_F16 weight: exact in bf16 (fp16_exact_bf16)
+                t = t.to(torch.bfloat16)
             return t.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16)
 
         def get(layer, name):

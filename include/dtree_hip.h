@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define DTREE_ABI_VERSION 6
+#define DTREE_ABI_VERSION 7
 
 #define DTREE_OK 0
 #define DTREE_E_ARG (-1)      /* bad shape / pointer / enum */
@@ -73,10 +73,25 @@ typedef struct DtreeStepDesc {
  *                    4*(e/2) and odd e in bits 16 + 4*(e/2); w_scales = bf16
  *                    [n/32][k/64][32][2] (scale, bias) of row 32r + c, group b.
  *                    Activations must be DTREE_W_TILED, 32 rows.
+ *  DTREE_W_TILED_F16: DTREE_W_TILED's order with fp16 elements: bf16 weights
+ *                    converted once (dtree_tile_weight_f16; exact for every
+ *                    bf16 of magnitude 2^-17 .. 65504), and activations as ONE
+ *                    fp16 plane (11 significant bits: no low half). The GEMM
+ *                    then runs one fp16 MFMA per weight fragment and each CU
+ *                    loads half the activation bytes of the bf16 pair. Both
+ *                    operands must be TILED_F16. The format holds values up to
+ *                    65504: models whose activations stay in that range (the
+ *                    bf16 workloads here: |x| < 50); q4 models, whose random
+ *                    residual stream reaches 1e12, keep DTREE_W_TILED.
+ *
+ * Activations between kernels (GEMM inputs and the *_bf16 / out outputs)
+ * take the layout code of their consumer: ROWMAJOR and TILED are bf16 with an
+ * optional low half (x = hi + lo), TILED_F16 is one fp16 plane (lo ignored).
  */
 #define DTREE_W_ROWMAJOR 0
 #define DTREE_W_TILED 1
 #define DTREE_W_Q4G64 2
+#define DTREE_W_TILED_F16 3
 
 /* GEMM epilogues (dtree_gemm_bf16). */
 #define DTREE_EPI_STORE_F32 0  /* out_f32[m][n] = rs[m] * acc                 */
@@ -99,12 +114,13 @@ typedef struct DtreeStepDesc {
 typedef struct DtreeGemmArgs {
   const uint16_t* x;      /* bf16 [rows_padded][ldx], rows >= L are zero   */
   const uint16_t* x_lo;   /* optional low half: X = x + x_lo (both bf16)   */
-  int32_t x_layout;       /* DTREE_W_ROWMAJOR, or DTREE_W_TILED with ldx = k */
+  int32_t x_layout;       /* DTREE_W_ROWMAJOR, or DTREE_W_TILED / _F16 with ldx = k */
   int32_t ldx;
   int32_t rows_padded;    /* 32, 64, 96 or 128                             */
   const uint16_t* w;      /* bf16 [n][k] (nn.Linear layout); Q4G64: packed q
                              (tiled x; above 32 rows one pass per 32 rows) */
-  int32_t w_layout;       /* DTREE_W_ROWMAJOR, DTREE_W_TILED or DTREE_W_Q4G64 */
+  int32_t w_layout;       /* DTREE_W_ROWMAJOR, DTREE_W_TILED, DTREE_W_TILED_F16
+                             (with x_layout TILED_F16) or DTREE_W_Q4G64     */
   int32_t n, k;           /* k % 64 == 0; n % 64 == 0 (% 32 above 64 rows) */
   int32_t epilogue;       /* DTREE_EPI_*                                   */
   int32_t split_k;        /* >= 1 split-K; 0 = automatic; tiled 32 rows only:
@@ -504,6 +520,11 @@ int dtree_gdn_layer_chain(const DtreeGdnArgs* args, int32_t num_tokens, hipStrea
 /* Convert a row-major [n][k] bf16 matrix to DTREE_W_TILED (n % 32 == 0,
  * k % 64 == 0; src and dst must not overlap). */
 int dtree_tile_weight(const uint16_t* src, uint16_t* dst, int32_t n, int32_t k, hipStream_t stream);
+/* The same to DTREE_W_TILED_F16: the elements become fp16 (round to nearest
+ * even; exact from 2^-17 to 65504 in magnitude, saturating at +-65504). The
+ * weight load of a bf16 checkpoint for the fp16 GEMM path; also the tiling of
+ * bf16 caller rows (LM-head inputs, the drafter's target hidden rows) for it. */
+int dtree_tile_weight_f16(const uint16_t* src, uint16_t* dst, int32_t n, int32_t k, hipStream_t stream);
 
 /* HIP graph capture of a launch sequence (stands in for the mx.compile region
  * of qwen3_tree.py:38 and the per-step eval of dtree_runtime.py:480). */

@@ -76,34 +76,60 @@ def _gpu_sequential_greedy(target, prompt, n_new):
 class ScriptedDrafter:
     """Drafter with the interface dtree_generate uses (draft.py:312-367 shape):
     mask_token_id, block_size, make_cache(), __call__(noise_embedding,
-    target_hidden, cache) -> hidden [1, block, H]."""
+    target_hidden, cache) -> hidden [1, block, H].
+
+    It proposes the target's own greedy continuation of the sequence actually
+    committed so far, with one planted wrong token per step. It rebuilds that
+    sequence from what it is handed (the count of committed rows since its
+    last call, which are the root and accepted tokens of its previous block,
+    and the new root token, read from the noise embedding's first row), so a
+    step whose verify resolves a near-tie of the tiny random model the other
+    way than the precomputed sequential decode (both within the logit
+    tolerance) costs that step's acceptance only; the proposals then follow
+    the new prefix (a fresh sequential greedy decode from it)."""
 
     mask_token_id = 0
     block_size = BLOCK
 
     def __init__(self, target, seq):
         self.target = target
-        self.seq = seq  # prompt + oracle continuation
+        self.seq = seq  # prompt + the target's sequential greedy continuation
+        V = target.model.args.vocab_size
+        self._emb = target.model.weights.embed_rows(torch.arange(V, device="cuda"))
 
     def make_cache(self):
-        return {"pos": None, "calls": 0}
+        return {"actual": None, "block": None, "calls": 0, "plan": list(self.seq)}
+
+    def _root_token(self, noise_embedding) -> int:
+        hit = (self._emb == noise_embedding[0, 0].to(self._emb.dtype)).all(-1).nonzero()
+        return int(hit[0, 0]) if hit.numel() else -1
 
     def __call__(self, noise_embedding, target_hidden, cache):
-        # The target hidden rows handed over are the committed tokens since the
-        # last call (the prompt first), so their running count is the root's position.
+        # Committed rows since the last call: the prompt first, then the root
+        # and the accepted draft tokens of the previous block.
         n = int(target_hidden.shape[1])
-        cache["pos"] = n if cache["pos"] is None else cache["pos"] + n
-        start = cache["pos"]
+        if cache["actual"] is None:
+            cache["actual"] = list(self.seq[:n])
+        else:
+            cache["actual"] += cache["block"][:n]
+        root = self._root_token(noise_embedding)
+        prefix = cache["actual"] + [root]
+        start = len(prefix) - 1
+        plan = cache["plan"]
+        if plan[:len(prefix)] != prefix:  # a near-tie went the other way: follow the actual prefix
+            plan = prefix + _gpu_sequential_greedy(self.target, prefix, BLOCK)
+            cache["plan"] = plan
         wrong = cache["calls"] % BLOCK  # 0: whole chain right, else the depth that is wrong
         cache["calls"] += 1
         V = self.target.model.args.vocab_size
         toks = []
         for d in range(BLOCK):
             p = start + d
-            t = self.seq[p] if p < len(self.seq) else (7 * p) % V
+            t = plan[p] if p < len(plan) else (7 * p) % V
             if d == wrong and d > 0:
                 t = (t + 1) % V
             toks.append(t)
+        cache["block"] = toks
         E = self.target.model.weights.embed_rows(torch.tensor(toks, device="cuda")).float()
         # peak logit 24 * 1024 * 0.02^2 ~ 9.8 whatever the hidden size, so the
         # best-first tree follows the scripted chain
