@@ -183,13 +183,13 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant, lo="qkv" not in eng.HI_ONLY), nl, us["qkv"], b["qkv"])
+    out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant, lo="qkv" not in eng.HI_ONLY, h16=eng.h16), nl, us["qkv"], b["qkv"])
     out["attention"] = entry(attention_kernel_name(eng.attn_grid_past(P), 128, 128, False, eng.MP), nl, us["attention"],
                              b["attention"])
-    out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant), nl, us["o"], b["o"])
-    out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant), nl, us["down"], b["down"])
-    out["gate_up_gemm"] = entry(gemm_kernel_name(2 * F, H, 2, quant), nl, us["gu"], b["gu"])
-    out["lm_head"] = entry(lmhead_kernel_name(quant, eng.MP), 1, us["lm_head"], b["lm_head"])
+    out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant, h16=eng.h16), nl, us["o"], b["o"])
+    out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant, h16=eng.h16), nl, us["down"], b["down"])
+    out["gate_up_gemm"] = entry(gemm_kernel_name(2 * F, H, 2, quant, h16=eng.h16), nl, us["gu"], b["gu"])
+    out["lm_head"] = entry(lmhead_kernel_name(quant, eng.MP, eng.h16), 1, us["lm_head"], b["lm_head"])
     return out
 
 
@@ -381,7 +381,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    kn = lambda n, k, epi, lo=True: gemm_kernel_name(n, k, epi, quant, rows=eng.MP, lo=lo)  # noqa: E731
+    kn = lambda n, k, epi, lo=True: gemm_kernel_name(n, k, epi, quant, rows=eng.MP, lo=lo, h16=eng.h16)  # noqa: E731
     out = {
         "in_proj_gemm": entry(kn(cfg.in_proj_dim, H, 0), nG, us["in"], b["in"]),
         "out_proj_gemm": entry(kn(H, cfg.value_dim, 1), nG, us["out"], b["out"]),
@@ -396,7 +396,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "gdn_commit": entry("gdn_commit_layers_kernel<128>", 1, us["commit"], nG * b["commit"]),
         "attention": entry(attention_kernel_name(eng.attn_grid_past(P), 256, 64, True, eng.MP), nA, us["attention"],
                            b["attention"]),
-        "lm_head": entry(lmhead_kernel_name(quant, eng.MP), 1, us["lm_head"], b["lm_head"]),
+        "lm_head": entry(lmhead_kernel_name(quant, eng.MP, eng.h16), 1, us["lm_head"], b["lm_head"]),
     }
     if fused:
         for k in ("gdn_prep", "gdn_recurrence"):
@@ -423,21 +423,26 @@ def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -
     return f"gqa_tree_attn_kernel<{D}, {R}, {g}, 4>" if group else f"tree_attn_kernel<{D}, {R}, {g}, {1 if MP == 32 else 4}>"
 
 
-def lmhead_kernel_name(quant: str, rows: int) -> str:
+def lmhead_kernel_name(quant: str, rows: int, h16: bool = False) -> str:
     """LM-head kernel (gemm.hip, dtree_lmhead_argmax): the one-pass q4 kernel's
     argmax epilogue for a q4 embedding (vocabularies up to 262144), else the
-    persistent LM head."""
+    persistent LM head (`h16`: fp16 tiled embedding and one fp16 activation
+    plane)."""
     if quant == "q4":
         return f"q4m_gemm_kernel<true, 16, {rows // 32}, 4>"
     mb = rows // 32
-    return f"lmhead_kernel<{mb}, {2 if mb == 1 else (2 if mb == 2 else 1)}, {2 if mb == 1 else 1}, true, true, {'true' if quant == 'q4' else 'false'}>"
+    lo, h = ("false", ", true") if h16 else ("true", "")
+    return (f"lmhead_kernel<{mb}, {2 if mb == 1 else (2 if mb == 2 else 1)}, {2 if mb == 1 else 1}, {lo}, true, "
+            f"{'true' if quant == 'q4' else 'false'}{h}>")
 
 
 def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows: int = 32,
-                     lo: bool = True) -> str:
+                     lo: bool = True, h16: bool = False) -> str:
     """Kernel the library picks for a tiled GEMM with split_k 0 (gemm.hip,
     dtree_gemm_bf16); `lo` False for a projection that reads only the high
-    activation plane (the first template argument). q4 over 64-128 rows: the one-pass kernel, two 64-column
+    activation plane (the first template argument); `h16` for fp16 tiled
+    weights with one fp16 activation plane (no low plane, the last template
+    argument true). q4 over 64-128 rows: the one-pass kernel, two 64-column
     blocks per workgroup unless a 4-block tiling still covers half the CUs,
     three when that fills at least an eighth more of the CUs.
     32 rows, bf16 or q4: three workgroups per 32-column tile (one per part of
@@ -445,7 +450,8 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows:
     when 2 N / 32 do; else one per tile at K <= 4096 and N / 32 <= CUs; else
     stream-K (q4: two workgroups per CU when there are at least 20 64 x 64
     units per CU)."""
-    L = "true" if lo else "false"
+    L = "true" if lo and not h16 else "false"
+    h = ", true" if h16 else ""
     if quant == "q4" and rows > 32:
         nblk, nkb = n // 64, k // 64
 
@@ -461,14 +467,14 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows:
     dp = "dp_gemm_kernel" if quant == "bf16" else "dpq_gemm_kernel"
     if k >= 4096 and n % 256 == 0:
         if (n // 32) * 3 <= cus:
-            return f"{dp}<{L}, {epi}, 3>"
+            return f"{dp}<{L}, {epi}, 3{h}>"
         if k == 4096 and (n // 32) * 2 <= cus:
-            return f"{dp}<{L}, {epi}, 2>"
+            return f"{dp}<{L}, {epi}, 2{h}>"
     if k <= 4096 and n // 32 <= cus:
-        return f"{dp}<{L}, {epi}, 1>"
+        return f"{dp}<{L}, {epi}, 1{h}>"
     if quant == "q4" and (n // 64) * (k // 64) >= 20 * cus:
         return f"sk2_gemm_kernel<{L}, {epi}>"
-    return f"sk_gemm_kernel<{L}, {epi}, {'true' if quant == 'q4' else 'false'}>"
+    return f"sk_gemm_kernel<{L}, {epi}, {'true' if quant == 'q4' else 'false'}{h}>"
 
 
 def copy_probe(mib: int) -> None:

@@ -17,6 +17,7 @@ import torch
 from dtree_hip import Qwen3TreeModel, Qwen3Weights, tiny_qwen3
 from dtree_hip.config import QWEN3_4B
 from dtree_hip.synthetic import acceptance_rewrite, make_tree, random_prefix
+from dtree_hip.weights import W_TILED, W_TILED_F16
 from oracle import qwen3 as oq
 from oracle import tree as otree
 
@@ -51,12 +52,13 @@ def _check_prefill(orc, cfg, prefix, prefix_k, prefix_v, layers, log=print):
     log(f"prefill K/V of {layers} layers at {P} positions match the oracle ({time.time() - t0:.1f}s)")
 
 
-def _run(cfg, P, layer_ids, dev, norm_jitter=0.0, log=print, quant="bf16", check_prefill_layers=0):
+def _run(cfg, P, layer_ids, dev, norm_jitter=0.0, log=print, quant="bf16", check_prefill_layers=0,
+         layout=W_TILED_F16):
     t0 = time.time()
     if quant == "q4":  # every linear layer and the tied embedding in 4-bit groups of 64
         w = Qwen3Weights.random_q4(cfg, seed=0, device=dev, norm_jitter=norm_jitter)
     else:
-        w = Qwen3Weights.random(cfg, seed=0, device=dev, norm_jitter=norm_jitter)
+        w = Qwen3Weights.random(cfg, seed=0, device=dev, norm_jitter=norm_jitter, layout=layout)
     model = Qwen3TreeModel(cfg, w, max_past=P + 64, layer_ids=layer_ids)
     eng = model.engine
     cache = eng.new_cache()
@@ -150,6 +152,16 @@ def _check(r, layer_ids):
 def test_verify_step_tiny_model(gpu_device, attn_kernel):
     cfg = tiny_qwen3()
     r = _run(cfg, P=100, layer_ids=[0, 1], dev=gpu_device, norm_jitter=0.1, check_prefill_layers=2)
+    res = _check(r, [0, 1])
+    assert len(res.accepted) >= 1
+
+
+def test_verify_step_tiny_model_bf16_pairs(gpu_device):
+    """bf16 weights in DTREE_W_TILED with the bf16 hi + lo activation pair
+    (the layout for checkpoints whose activations exceed fp16's range)."""
+    cfg = tiny_qwen3()
+    r = _run(cfg, P=100, layer_ids=[0, 1], dev=gpu_device, norm_jitter=0.1, check_prefill_layers=2, layout=W_TILED)
+    assert not r["eng"].h16
     res = _check(r, [0, 1])
     assert len(res.accepted) >= 1
 
