@@ -40,6 +40,45 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def graph_timed(lib, st: int, launch, n: int, reps: int) -> float:
+    """Average device time of one launch: `reps` launches (launch(r % n,
+    stream), rotating over n argument sets) captured into one HIP graph on a
+    side stream and replayed on `st` between two HIP events. Launching from
+    the host instead would time the host's launch rate for kernels shorter
+    than one ctypes + HIP launch (~10 us), as the step's graph never does."""
+    import ctypes as C
+
+    import torch
+
+    from dtree_hip import _native as N
+
+    for r in range(n):
+        launch(r, st)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    h = side.cuda_stream
+    N.check(lib.dtree_graph_begin(h), "graph begin")
+    try:
+        for r in range(reps):
+            launch(r % n, h)
+    finally:
+        ex = C.c_void_p()
+        rc = lib.dtree_graph_end(h, C.byref(ex))
+    N.check(rc, "graph end")
+    torch.cuda.current_stream().wait_stream(side)
+    try:
+        N.check(lib.dtree_graph_launch(ex, st), "graph launch")  # warm replay
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        N.check(lib.dtree_graph_launch(ex, st), "graph launch")
+        e1.record()
+        e1.synchronize()
+    finally:
+        lib.dtree_graph_destroy(ex)
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
 def weight_bytes(params: int, quant: str) -> int:
     """bf16: 2 B per weight; q4 group-64: half a byte plus a bf16 scale and bias per 64."""
     return params * 2 if quant == "bf16" else params // 2 + params // 64 * 4
@@ -150,21 +189,12 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
     keep = [args]
 
     def timed(launch) -> float:
-        for r in range(nl):
-            launch(r)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for r in range(reps):
-            launch(r % nl)
-        e1.record()
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / reps
+        return graph_timed(lib, st, launch, nl, reps)
 
     refs = {k: [C.byref(args[li][k]) for li in range(nl)] for k in ("qkv", "o", "gu", "down")}
-    us = {k: timed(lambda r, k=k: gemm(refs[k][r], st)) for k in refs}
-    us["attention"] = timed(lambda r: eng._attention(r, cache, st))
-    us["lm_head"] = timed(lambda r: eng.launch_lm_head(st))
+    us = {k: timed(lambda r, s, k=k: gemm(refs[k][r], s)) for k in refs}
+    us["attention"] = timed(lambda r, s: eng._attention(r, cache, s))
+    us["lm_head"] = timed(lambda r, s: eng.launch_lm_head(s))
     keep.append(refs)
 
     wb = lambda params: weight_bytes(params, quant)  # noqa: E731
@@ -324,36 +354,27 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
     refs = {k: [C.byref(a) for a in v] for k, v in args.items()}
 
     def timed(launch, n) -> float:
-        for r in range(n):
-            launch(r)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for r in range(reps):
-            launch(r % n)
-        e1.record()
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / reps
+        return graph_timed(lib, st, launch, n, reps)
 
-    us = {k: timed(lambda r, k=k: gemm(refs[k][r], st), len(refs[k])) for k in ("in", "out", "qkv", "o", "gu",
-                                                                                   "down")}
+    us = {k: timed(lambda r, s, k=k: gemm(refs[k][r], s), len(refs[k])) for k in ("in", "out", "qkv", "o", "gu",
+                                                                                     "down")}
     g = refs["gdn"]
-    us["prep"] = timed(lambda r: lib.dtree_gdn_layer_prep(g[r], st), len(g))
-    us["recurrence"] = timed(lambda r: lib.dtree_gdn_layer_recurrence(g[r], st), len(g))
+    us["prep"] = timed(lambda r, s: lib.dtree_gdn_layer_prep(g[r], s), len(g))
+    us["recurrence"] = timed(lambda r, s: lib.dtree_gdn_layer_recurrence(g[r], s), len(g))
     # trees of up to 32 nodes with 128-dim heads run prep and recurrence as one
     # launch in the step (dtree_gdn_layer_prep_recurrence)
     fused = eng.MP == 32 and cfg.linear_key_head_dim == 128 and cfg.linear_value_head_dim == 128
     if fused:
-        us["prep_recurrence"] = timed(lambda r: lib.dtree_gdn_layer_prep_recurrence(g[r], st), len(g))
-    us["gated_norm"] = timed(lambda r: lib.dtree_gdn_layer_gated_norm(g[r], st), len(g))
+        us["prep_recurrence"] = timed(lambda r, s: lib.dtree_gdn_layer_prep_recurrence(g[r], s), len(g))
+    us["gated_norm"] = timed(lambda r, s: lib.dtree_gdn_layer_gated_norm(g[r], s), len(g))
     # every layer's commit in one launch, as the step runs it
     g_all = (N.GdnArgs * len(args["gdn"]))(*args["gdn"])
     for i, li in enumerate(G):  # into the spare pair, as the step's commit writes
         g_all[i].window_out = cache.windows_next[cache.slot[li]].data_ptr()
         g_all[i].state_out = cache.states_next[cache.slot[li]].data_ptr()
-    us["commit"] = timed(lambda r: lib.dtree_gdn_layers_commit(g_all, len(args["gdn"]), st), 1)
-    us["attention"] = timed(lambda r: eng._attention(A[r], cache, st), len(A))
-    us["lm_head"] = timed(lambda r: eng.launch_lm_head(st), 1)
+    us["commit"] = timed(lambda r, s: lib.dtree_gdn_layers_commit(g_all, len(args["gdn"]), s), 1)
+    us["attention"] = timed(lambda r, s: eng._attention(A[r], cache, s), len(A))
+    us["lm_head"] = timed(lambda r, s: eng.launch_lm_head(s), 1)
 
     wb = lambda params: weight_bytes(params, quant)  # noqa: E731
     Hv, Dk, Dv = cfg.linear_num_value_heads, cfg.linear_key_head_dim, cfg.linear_value_head_dim

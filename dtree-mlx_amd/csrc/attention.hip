@@ -335,24 +335,26 @@ struct TreeStage {
         // dim (stride DTREE_PAGE).
         const int pos = P + node;
         const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
-        const int slot = page * p.Hkv + g;
         // (one resource for the whole layer cache, uniform across the lanes;
         // a layer's pages stay below 2 GiB)
         const __amdgpu_buffer_rsrc_t kr = buf_rsrc(p.kp, 0x7ffffff0u);
         const __amdgpu_buffer_rsrc_t vr = buf_rsrc(p.vp, 0x7ffffff0u);
-        const int kbase = (slot * DTREE_PAGE + off) * D * 2, vbase = (slot * D * DTREE_PAGE + off) * 2;
+        const int blk = (page * p.Hkv + g) * DTREE_PAGE * D * 2;  // byte offset of the (page, head) block
+        // The dims' offsets are computed here, next to their stores: j is
+        // made opaque so they are not hoisted out of the chunk loop, where
+        // NV of them would stay live across the MFMA registers.
+        int jj = j;
+        asm volatile("" : "+v"(jj));
 #pragma unroll
         for (int i = 0; i < NV; i += 4) {
-          const int a = row8_dim<D>(0, i), b = row8_dim<D>(1, i) - a;  // dim = a + b j
+          // four consecutive dims from a multiple of 4: one 8-byte run of K
           const u32x2_t w = {(uint32_t)kb[i] | ((uint32_t)kb[i + 1] << 16),
                              (uint32_t)kb[i + 2] | ((uint32_t)kb[i + 3] << 16)};
-          __builtin_amdgcn_raw_buffer_store_b64(w, kr, kbase + 2 * b * j, 2 * a, 0);
+          __builtin_amdgcn_raw_buffer_store_b64(w, kr, blk + 2 * kv_k_off(off, row8_dim<D>(jj, i), D), 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int a = row8_dim<D>(0, i), b = row8_dim<D>(1, i) - a;
-          __builtin_amdgcn_raw_buffer_store_b16(vb[i], vr, vbase + 2 * DTREE_PAGE * b * j, 2 * DTREE_PAGE * a, 0);
-        }
+        for (int i = 0; i < NV; ++i)
+          __builtin_amdgcn_raw_buffer_store_b16(vb[i], vr, blk + 2 * kv_v_off(off, row8_dim<D>(jj, i), D), 0, 0);
       }
     }
   }
@@ -361,16 +363,21 @@ struct TreeStage {
 // Prefix chunk pc (CK keys of one page) into an LDS buffer: K rows and V^T
 // columns in 16-byte pieces, every load of the workgroup's threads in flight
 // together; keys at or past P (stale rows of the last page) are zeroed.
-// Piece e = ts + i * TPS of K is key e / (D/8), dims 8 (e % (D/8)) .. +7: the
-// chunk's K rows are contiguous, so piece e is at byte 16 e. Piece e of V^T is
-// dim e / (CK/8), keys 8 (e % (CK/8)) .. +7 of the page row. issue() needs
-// only the chunk index (the page table is read there), commit() needs P.
+// The page block stores K and V in MFMA-fragment order (kv_k_off /
+// kv_v_off), and the chunk's K and its V are each one contiguous run of
+// kilobytes (from key half po / 32, resp. key step po / 16). Wavefront f's
+// kilobyte of K is fragment (key half f / NJ, dim step j = f % NJ): lane rem
+// holds key 32 (f / NJ) + pi(rem % 32) of the chunk, dims 16 j + 8 (rem / 32)
+// .. +7. Its kilobyte of V is key step f / ND, dim block db = f % ND: dim
+// 32 db + rem % 32, keys 16 (f / ND) + 8 (rem / 32) .. +7 of the chunk.
+// issue() needs only the chunk index (the page table is read there), commit()
+// needs P.
 template <int D, int TPS>
 struct PrefixStage {
   static constexpr int CK = chunk_keys(D);
+  static constexpr int NJ = D / 16, ND = D / 32;
   static constexpr int PK = CK * D / 8 / TPS;  // 16-byte pieces of K (and of V^T) per thread
-  static constexpr int KPR = D / 8, VPR = CK / 8;  // pieces per K row / per V^T row
-  static_assert(TPS % KPR == 0 && TPS % VPR == 0, "the threads cover whole rows");
+  static_assert(PK * TPS == CK * D / 8 && TPS % 64 == 0, "whole wavefronts cover the chunk");
   u32x4_t kv[PK], vv[PK];
 
   // Physical page of chunk pc, read through the scalar cache (pc is uniform):
@@ -379,37 +386,41 @@ struct PrefixStage {
     typedef const __attribute__((address_space(4))) int* const_int_ptr;  // constant address space: s_load
     return ((const_int_ptr)(uintptr_t)p.page_table)[pc * CK / DTREE_PAGE];
   }
+  // The wave index (ts / 64) is uniform: the kilobyte each wavefront load
+  // reads is a scalar; only the lane's 16-byte slot in it is per lane.
   __device__ __forceinline__ void issue(const AttnParams& p, int pc, int page, int g, int ts) {
     const int po = (pc * CK) % DTREE_PAGE;
-    const __amdgpu_buffer_rsrc_t kr =
-        buf_rsrc(p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po) * D, (unsigned)(CK * D * 2));
-    const __amdgpu_buffer_rsrc_t vr =
-        buf_rsrc(p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po, (unsigned)(D * DTREE_PAGE * 2));
-    const int vrow0 = ts / VPR, vcol = 8 * (ts % VPR);
+    const size_t blk = (size_t)(page * p.Hkv + g) * DTREE_PAGE * D;
+    const __amdgpu_buffer_rsrc_t kr = buf_rsrc(p.kp + blk, (unsigned)(DTREE_PAGE * D * 2));
+    const __amdgpu_buffer_rsrc_t vr = buf_rsrc(p.vp + blk, (unsigned)(DTREE_PAGE * D * 2));
+    const int w = __builtin_amdgcn_readfirstlane(ts >> 6), lo = 16 * (ts & 63);
 #pragma unroll
     for (int i = 0; i < PK; ++i) {
-      kv[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, 16 * (ts + i * TPS), 0, kNt);
-      vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, 2 * ((vrow0 + i * (TPS / VPR)) * DTREE_PAGE + vcol), 0, kNt);
+      const int f = w + i * (TPS / 64);  // this wavefront's kilobyte of the chunk
+      kv[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, lo, 1024 * ((po / 32) * NJ + f), kNt);
+      vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, lo, 1024 * ((po / 16) * ND + f), kNt);
     }
   }
 
   template <int KS, int VS>
   __device__ __forceinline__ void commit(int pc, int P, int ts, uint16_t* ks, uint16_t* vt) const {
     const int kend = P - pc * CK;  // keys >= kend are past the prefix
-    const int krow0 = ts / KPR, kcol = 8 * (ts % KPR);
-    const int vrow0 = ts / VPR, vcol = 8 * (ts % VPR);
+    const int w = __builtin_amdgcn_readfirstlane(ts >> 6), rem = ts & 63;
+    const int kl = kv_pi(rem & 31), hl = 8 * (rem >> 5);  // the lane's key row (pi) and 8-element half
 #pragma unroll
     for (int i = 0; i < PK; ++i) {
-      const int key = krow0 + i * (TPS / KPR);
+      const int f = w + i * (TPS / 64);
+      const int key = 32 * (f / NJ) + kl, kcol = 16 * (f % NJ) + hl;
       *reinterpret_cast<u32x4_t*>(ks + key * KS + kcol) = key < kend ? bf8_to_h8(kv[i]) : u32x4_t{0u, 0u, 0u, 0u};
+      const int dim = 32 * (f % ND) + (rem & 31), k0 = 16 * (f / ND) + hl;
       u32x4_t v = vv[i];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint32_t lo_ok = (vcol + 2 * q) < kend ? 0xffffu : 0u;
-        const uint32_t hi_ok = (vcol + 2 * q + 1) < kend ? 0xffff0000u : 0u;
+        const uint32_t lo_ok = (k0 + 2 * q) < kend ? 0xffffu : 0u;
+        const uint32_t hi_ok = (k0 + 2 * q + 1) < kend ? 0xffff0000u : 0u;
         v[q] &= lo_ok | hi_ok;
       }
-      *reinterpret_cast<u32x4_t*>(vt + (vrow0 + i * (TPS / VPR)) * VS + vcol) = bf8_to_h8(v);
+      *reinterpret_cast<u32x4_t*>(vt + dim * VS + k0) = bf8_to_h8(v);
     }
   }
 };

@@ -485,15 +485,16 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
   if (p.write_cache && (hq % G) == 0 && write_rows && node < L) {
     const int pos = P + node;
     const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
-    uint16_t* krow = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + off) * D;
-    uint16_t* vcol = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + off;
+    uint16_t* kblk = p.kp + (size_t)(page * p.Hkv + g) * DTREE_PAGE * D;
+    uint16_t* vblk = p.vp + (size_t)(page * p.Hkv + g) * DTREE_PAGE * D;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      *reinterpret_cast<u32x4_t*>(krow + 16 * j + 8 * h) = kf8[j];
+      // dims 16j + 8h .. +7 of this key are one 16-byte run of the K block
+      *reinterpret_cast<u32x4_t*>(kblk + kv_k_off(off, 16 * j + 8 * h, D)) = kf8[j];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const uint32_t word = vf8[j][i >> 1];
-        vcol[(size_t)(16 * j + 8 * h + i) * DTREE_PAGE] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
+        vblk[kv_v_off(off, 16 * j + 8 * h + i, D)] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
       }
     }
   }
@@ -516,18 +517,22 @@ __device__ __forceinline__ void prefix_issue(const AttnParams& p, ChunkKV<D>& kv
                                              int h) {
   constexpr int NJ = D / 16, ND = D / 32;
   constexpr int CK = chunk_keys(D), NB = CK / 32;
+  // The page block stores every fragment as one contiguous kilobyte in lane
+  // order (kv_k_off / kv_v_off): K fragment (j, key half) and V fragment (key
+  // step, dim block) are each one fully coalesced 16-byte load per lane.
   const int po = (pc * CK) % DTREE_PAGE;
-  const uint16_t* kbase = p.kp + ((size_t)(page * p.Hkv + g) * DTREE_PAGE + po + swap_bits23(c)) * D;
-  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * D * DTREE_PAGE + po;
+  const int lane = 32 * h + c;
+  const uint16_t* kbase = p.kp + (size_t)(page * p.Hkv + g) * DTREE_PAGE * D + 8 * lane;
+  const uint16_t* vbase = p.vp + (size_t)(page * p.Hkv + g) * DTREE_PAGE * D + 8 * lane;
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) kv.kf[b][j] = ld_u32x4_stream(kbase + (size_t)32 * b * D + 16 * j + 8 * h);
+    for (int j = 0; j < NJ; ++j) kv.kf[b][j] = ld_u32x4_stream(kbase + (size_t)((po / 32 + b) * NJ + j) * 512);
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int db = 0; db < ND; ++db)
-        kv.vf[b][s2][db] = ld_u32x4_stream(vbase + (size_t)(32 * db + c) * DTREE_PAGE + 32 * b + 16 * s2 + 8 * h);
+        kv.vf[b][s2][db] = ld_u32x4_stream(vbase + (size_t)((po / 16 + 2 * b + s2) * ND + db) * 512);
   }
 }
 

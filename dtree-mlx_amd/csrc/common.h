@@ -35,6 +35,27 @@ bool off_xcd_test();  // DTREE_TEST_OFF_XCD=1: exercise the cross-XCD exchange p
     if (_rc) return _rc;         \
   } while (0)
 
+// ---- KV cache pages ------------------------------------------------------------
+// One (page, kv head) block holds DTREE_PAGE = 64 positions x D dims of K and
+// of V, bf16, each in the order the attention MFMAs read them, so that one
+// 16-byte load per lane of a wavefront reads one contiguous kilobyte:
+// * K: the A operand of S^T = K Q^T (32 keys x 16 dims per fragment, lane
+//   (r, h) = 32 h + r holds dims 8h .. 8h+7 of its key). Fragment (key half b,
+//   dim step j) is the kilobyte b * (D/16) + j, so the 32 keys of a half page
+//   are one contiguous run; lane r of it holds slot 32 b + pi(r), pi = swap
+//   bits 2 and 3, the key order in which the S^T registers of a lane half form
+//   runs of eight consecutive keys for the P.V step.
+// * V: the A operand of O^T = V^T P^T (32 dims x 16 keys per fragment, lane
+//   (r, h) holds slots 8h .. 8h+7 of its dim). Fragment (key step st of 16
+//   slots, dim block db) is the kilobyte st * (D/32) + db.
+__host__ __device__ __forceinline__ int kv_pi(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+__host__ __device__ __forceinline__ int kv_k_off(int slot, int d, int D) {
+  return ((((slot >> 5) * (D >> 4) + (d >> 4)) * 64 + ((d >> 3) & 1) * 32 + kv_pi(slot & 31)) << 3) + (d & 7);
+}
+__host__ __device__ __forceinline__ int kv_v_off(int slot, int d, int D) {
+  return ((((slot >> 4) * (D >> 5) + (d >> 5)) * 64 + ((slot >> 3) & 1) * 32 + (d & 31)) << 3) + (slot & 7);
+}
+
 // ---- numeric helpers ---------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 

@@ -50,12 +50,12 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
   const float cs = (float)cos(ang), sn = (float)sin(ang);
   const float y1 = k1 * cs - k2 * sn, y2 = k1 * sn + k2 * cs;
   const int page = page_table[slot / DTREE_PAGE], off = slot % DTREE_PAGE;
-  uint16_t* kdst = kp + ((size_t)(page * Hkv + g) * DTREE_PAGE + off) * kHeadDim;
-  kdst[lane] = f2bf(y1);
-  kdst[lane + 64] = f2bf(y2);
-  uint16_t* vdst = vp + (size_t)(page * Hkv + g) * kHeadDim * DTREE_PAGE + off;
-  vdst[(size_t)lane * DTREE_PAGE] = f2bf(vrow[lane]);
-  vdst[(size_t)(lane + 64) * DTREE_PAGE] = f2bf(vrow[lane + 64]);
+  // (page, head) block in the attention kernels' fragment order (kv_k_off / kv_v_off)
+  const size_t blk = (size_t)(page * Hkv + g) * DTREE_PAGE * kHeadDim;
+  kp[blk + kv_k_off(off, lane, kHeadDim)] = f2bf(y1);
+  kp[blk + kv_k_off(off, lane + 64, kHeadDim)] = f2bf(y2);
+  vp[blk + kv_v_off(off, lane, kHeadDim)] = f2bf(vrow[lane]);
+  vp[blk + kv_v_off(off, lane + 64, kHeadDim)] = f2bf(vrow[lane + 64]);
 }
 
 }  // namespace

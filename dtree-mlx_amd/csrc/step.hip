@@ -311,39 +311,39 @@ __global__ __launch_bounds__(256) void compact_kernel(const DtreeStepDesc* desc,
   if (n >= L) return;  // every tree row kept in place (adapters.py:654-655)
   const int layer = (b % nkv) / Hkv, g = (b % nkv) % Hkv;
   if (b < nkv) {
-    // K: row of position (page, slot) at ((page * Hkv + g) * 64 + slot) * D.
+    // K of position (page, slot): dims 8c .. 8c+7 are one 16-byte run at
+    // kv_k_off(slot, 8c) in the (page, head) block.
     uint16_t* pool = kp + layer_stride * layer;
     for (int d0 = 0; d0 < D; d0 += 128) {
       const int dw = min(128, D - d0), nch = dw / 8;  // 16-byte pieces per row this pass
       for (int e = t; e < n * nch; e += 256) {
         const int j = e / nch, ch = e % nch, r = src_row[j];
-        const size_t idx = ((size_t)((r / DTREE_PAGE) * Hkv + g) * DTREE_PAGE + r % DTREE_PAGE) * D + d0 + 8 * ch;
+        const size_t idx = (size_t)((r / DTREE_PAGE) * Hkv + g) * DTREE_PAGE * D + kv_k_off(r % DTREE_PAGE, d0 + 8 * ch, D);
         buf[j * 16 + ch] = *reinterpret_cast<const u32x4_t*>(pool + idx);
       }
       __syncthreads();
       for (int e = t; e < n * nch; e += 256) {
         const int j = e / nch, ch = e % nch, r = dst_row[j];
-        const size_t idx = ((size_t)((r / DTREE_PAGE) * Hkv + g) * DTREE_PAGE + r % DTREE_PAGE) * D + d0 + 8 * ch;
+        const size_t idx = (size_t)((r / DTREE_PAGE) * Hkv + g) * DTREE_PAGE * D + kv_k_off(r % DTREE_PAGE, d0 + 8 * ch, D);
         *reinterpret_cast<u32x4_t*>(pool + idx) = buf[j * 16 + ch];
       }
       __syncthreads();
     }
     return;
   }
-  // V^T: element (dim d, position (page, slot)) at ((page * Hkv + g) * D + d) * 64 + slot.
+  // V of (dim d, position (page, slot)) at kv_v_off(slot, d) of the (page, head) block.
   uint16_t* pool = vp + layer_stride * layer;
   uint16_t* vb = reinterpret_cast<uint16_t*>(buf);
   for (int d0 = 0; d0 < D; d0 += 128) {
     const int dw = min(128, D - d0);
     for (int e = t; e < n * dw; e += 256) {
       const int d = d0 + e / n, j = e % n, r = src_row[j];
-      vb[(d - d0) * n + j] =
-          pool[((size_t)((r / DTREE_PAGE) * Hkv + g) * D + d) * DTREE_PAGE + r % DTREE_PAGE];
+      vb[(d - d0) * n + j] = pool[(size_t)((r / DTREE_PAGE) * Hkv + g) * DTREE_PAGE * D + kv_v_off(r % DTREE_PAGE, d, D)];
     }
     __syncthreads();
     for (int e = t; e < n * dw; e += 256) {
       const int d = d0 + e / n, j = e % n, r = dst_row[j];
-      pool[((size_t)((r / DTREE_PAGE) * Hkv + g) * D + d) * DTREE_PAGE + r % DTREE_PAGE] = vb[(d - d0) * n + j];
+      pool[(size_t)((r / DTREE_PAGE) * Hkv + g) * DTREE_PAGE * D + kv_v_off(r % DTREE_PAGE, d, D)] = vb[(d - d0) * n + j];
     }
     __syncthreads();
   }
@@ -519,7 +519,7 @@ extern "C" int dtree_compact(const DtreeStepDesc* desc, uint16_t* k_pages, uint1
                              const uint16_t* hidden_in, int32_t hidden_width, uint16_t* hidden_out,
                              hipStream_t stream) {
   DTREE_REQUIRE(desc && page_table, "compact: null pointer");
-  DTREE_REQUIRE(layers >= 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 8 == 0, "compact: shape");
+  DTREE_REQUIRE(layers >= 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 32 == 0, "compact: shape (head_dim a multiple of 32)");
   DTREE_REQUIRE(layers == 0 || (k_pages && v_pages), "compact: null cache");
   DTREE_REQUIRE(!hidden_out || (hidden_in && hidden_width > 0 && hidden_width % 8 == 0 &&
                                  ((uintptr_t)hidden_in & 15) == 0 && ((uintptr_t)hidden_out & 15) == 0),

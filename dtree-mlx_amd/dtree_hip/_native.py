@@ -16,7 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libdtree_hip.so"
 MAX_NODES = 128
 MASK_WORDS = 4
 PAGE = 64
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 E_OK, E_ARG, E_HIP, E_TREE, E_WORKSPACE = 0, -1, -2, -3, -4
 

@@ -1,9 +1,12 @@
 """Paged bf16 KV cache for the tree-verify kernels.
 
 Layout (all layers in one allocation each, so compaction is one launch):
-  k_pages [layers, n_pages, kv_heads, PAGE, head_dim]
-  v_pages [layers, n_pages, kv_heads, head_dim, PAGE]   (V^T inside a page, so
-          the P.V MFMA reads eight consecutive keys per 16-byte load)
+  k_pages, v_pages [layers, n_pages, kv_heads, PAGE * head_dim]: one block of
+          PAGE positions x head_dim dims per (page, kv head), each in the
+          order the attention MFMAs read their operands, so a wavefront's
+          16-byte-per-lane load of one operand fragment is one contiguous
+          kilobyte (``k_block_index`` / ``v_block_index``; the kernels use the
+          same formulas, kv_k_off / kv_v_off in csrc/common.h).
   page_table [n_pages] int32: logical page -> physical page.
 
 Logical position t of a layer lives in physical page page_table[t // PAGE] at
@@ -12,9 +15,41 @@ offset of mlx-lm that dtree_runtime / the adapters read).
 """
 from __future__ import annotations
 
+import functools
+
 import torch
 
 from ._native import PAGE
+
+
+def _pi(r: torch.Tensor) -> torch.Tensor:
+    """Swap bits 2 and 3 (an involution on 0..31)."""
+    return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1)
+
+
+@functools.lru_cache(maxsize=None)
+def _block_index(head_dim: int, which: str) -> torch.Tensor:
+    slot = torch.arange(PAGE).view(PAGE, 1)
+    d = torch.arange(head_dim).view(1, head_dim)
+    if which == "k":
+        # S^T = K Q^T fragment (key half b = slot // 32, dim step j = d // 16):
+        # kilobyte b * (head_dim // 16) + j, lane 32 * ((d // 8) % 2) + pi(slot % 32), element d % 8
+        off = ((((slot >> 5) * (head_dim >> 4) + (d >> 4)) * 64 + ((d >> 3) & 1) * 32 + _pi(slot & 31)) << 3) + (d & 7)
+    else:
+        # O^T = V^T P^T fragment (key step st = slot // 16, dim block db = d // 32):
+        # kilobyte st * (head_dim // 32) + db, lane 32 * ((slot // 8) % 2) + d % 32, element slot % 8
+        off = ((((slot >> 4) * (head_dim >> 5) + (d >> 5)) * 64 + ((slot >> 3) & 1) * 32 + (d & 31)) << 3) + (slot & 7)
+    return off
+
+
+def k_block_index(head_dim: int) -> torch.Tensor:
+    """[PAGE, head_dim] int64: element offset of K (slot, dim) inside a (page, kv head) block."""
+    return _block_index(head_dim, "k")
+
+
+def v_block_index(head_dim: int) -> torch.Tensor:
+    """[PAGE, head_dim] int64: element offset of V (slot, dim) inside a (page, kv head) block."""
+    return _block_index(head_dim, "v")
 
 
 class LayerCacheView:
@@ -46,8 +81,10 @@ class PagedKVCache:
         self.n_pages = (capacity + PAGE - 1) // PAGE
         self.capacity = self.n_pages * PAGE
         dev = torch.device(device)
-        self.k_pages = torch.zeros(layers, self.n_pages, kv_heads, PAGE, head_dim, dtype=torch.bfloat16, device=dev)
-        self.v_pages = torch.zeros(layers, self.n_pages, kv_heads, head_dim, PAGE, dtype=torch.bfloat16, device=dev)
+        if head_dim % 32:
+            raise ValueError("head_dim must be a multiple of 32 (the cache's 32-dim fragment blocks)")
+        self.k_pages = torch.zeros(layers, self.n_pages, kv_heads, PAGE * head_dim, dtype=torch.bfloat16, device=dev)
+        self.v_pages = torch.zeros(layers, self.n_pages, kv_heads, PAGE * head_dim, dtype=torch.bfloat16, device=dev)
         if page_order is None:
             page_order = torch.arange(self.n_pages, dtype=torch.int32)
         if sorted(page_order.tolist()) != list(range(self.n_pages)):
@@ -81,30 +118,34 @@ class PagedKVCache:
         n = (length + PAGE - 1) // PAGE
         return self.page_table[:n].long()
 
+    def _logical(self, pages: torch.Tensor, T: int, which: str) -> torch.Tensor:
+        pg = pages[self._pages_for(T)]  # [np, Hkv, PAGE * D]
+        idx = _block_index(self.head_dim, which).to(pg.device).reshape(-1)
+        rows = pg[:, :, idx].view(-1, self.kv_heads, PAGE, self.head_dim)
+        return rows.permute(0, 2, 1, 3).reshape(-1, self.kv_heads, self.head_dim)[:T]
+
     def logical_keys(self, layer: int, length: int | None = None) -> torch.Tensor:
         """[T, kv_heads, head_dim] bf16, logical order."""
-        T = self.offset if length is None else length
-        pg = self.k_pages[layer][self._pages_for(T)]  # [np, Hkv, PAGE, D]
-        return pg.permute(0, 2, 1, 3).reshape(-1, self.kv_heads, self.head_dim)[:T]
+        return self._logical(self.k_pages[layer], self.offset if length is None else length, "k")
 
     def logical_values(self, layer: int, length: int | None = None) -> torch.Tensor:
-        T = self.offset if length is None else length
-        pg = self.v_pages[layer][self._pages_for(T)]  # [np, Hkv, D, PAGE]
-        return pg.permute(0, 3, 1, 2).reshape(-1, self.kv_heads, self.head_dim)[:T]
+        return self._logical(self.v_pages[layer], self.offset if length is None else length, "v")
 
     def write_logical(self, layer: int, keys: torch.Tensor, values: torch.Tensor, start: int = 0) -> None:
         """Store [T, kv_heads, head_dim] rows at logical positions start..start+T-1."""
         T = keys.shape[0]
         if start + T > self.capacity:
             raise ValueError("cache capacity exceeded")
-        keys = keys.to(self.k_pages.device, torch.bfloat16)
-        values = values.to(self.v_pages.device, torch.bfloat16)
-        pos = torch.arange(start, start + T, device=self.k_pages.device)
-        page = self.page_table.long()[pos // PAGE]
+        dev = self.k_pages.device
+        keys = keys.to(dev, torch.bfloat16)
+        values = values.to(dev, torch.bfloat16)
+        pos = torch.arange(start, start + T, device=dev)
+        page = self.page_table.long()[pos // PAGE].view(T, 1, 1)
         slot = pos % PAGE
-        self.k_pages[layer][page, :, slot, :] = keys
-        # v_pages[layer][page, h, d, slot] = values[t, h, d]
-        self.v_pages[layer].permute(0, 3, 1, 2)[page, slot, :, :] = values
+        head = torch.arange(self.kv_heads, device=dev).view(1, -1, 1)
+        for pages, rows, which in ((self.k_pages[layer], keys, "k"), (self.v_pages[layer], values, "v")):
+            off = _block_index(self.head_dim, which).to(dev)[slot].view(T, 1, self.head_dim)
+            pages[page, head, off] = rows
 
     def reset(self, offset: int = 0) -> None:
         self.offset = offset

@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define DTREE_ABI_VERSION 7
+#define DTREE_ABI_VERSION 8
 
 #define DTREE_OK 0
 #define DTREE_E_ARG (-1)      /* bad shape / pointer / enum */
@@ -208,10 +208,15 @@ int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, int32_t hea
  * (cos/sin [rows][rope_dims/2], pairs (d, d + rope_dims/2), dims >= rope_dims
  * unrotated), writes the L new K/V rows into the cache at logical positions
  * P..P+L-1, and writes softmax(scale * q k^T + mask) v as bf16
- * out[m][h*head_dim + d] (rows >= L zero). K pages:
- * [page][kv_head][DTREE_PAGE][head_dim]; V pages (transposed):
- * [page][kv_head][head_dim][DTREE_PAGE]. page_table maps logical page ->
- * physical page.
+ * out[m][h*head_dim + d] (rows >= L zero). K and V pages are
+ * [page][kv_head][DTREE_PAGE * head_dim] bf16 blocks (head_dim a multiple of
+ * 32) in the order the attention's 32x32x16 MFMAs read their operands, so
+ * that each operand fragment is one contiguous kilobyte in lane order. With
+ * pi(r) = r with bits 2 and 3 swapped, element (slot s, dim d) of a block is
+ *   K: ((((s/32)*(head_dim/16) + d/16)*64 + ((d/8)%2)*32 + pi(s%32)) * 8) + d%8
+ *   V: ((((s/16)*(head_dim/32) + d/32)*64 + ((s/8)%2)*32 + d%32) * 8) + s%8
+ * (8 consecutive dims of one key, resp. 8 consecutive slots of one dim, are
+ * one 16-byte run). page_table maps logical page -> physical page.
  *
  * gated = 1 is the Qwen3.5 gated attention (qwen35_tree.py:503-540): each q
  * head occupies 2*head_dim columns of the qkv row, [q | gate], and the output
