@@ -411,7 +411,7 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "gate_up_gemm": entry(kn(2 * F, H, 2), nL, us["gu"], b["gu"]),
         "down_gemm": entry(kn(H, F, 1), nL, us["down"], b["down"]),
         "gdn_prep": entry(f"gdn_prep_kernel<{cfg.linear_conv_kernel_dim - 1}, 128>", nG, us["prep"], b["prep"]),
-        "gdn_recurrence": entry("gdn_tree_reg_kernel<32>" if eng.MP == 32 else "gdn_tree_dfs_kernel", nG,
+        "gdn_recurrence": entry(gdn_recurrence_name(eng.MP, 0), nG,
                                 us["recurrence"], b["recurrence"]),
         "gdn_gated_norm": entry("gdn_gated_norm_kernel<128>", nG, us["gated_norm"], b["gated_norm"]),
         "gdn_commit": entry("gdn_commit_layers_kernel<128>", 1, us["commit"], nG * b["commit"]),
@@ -426,12 +426,23 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         # the recurrence's bytes (its inputs are now the raw conv / b / a columns,
         # of the same size), the conv taps and window, and q / k / v / g / beta
         # written for the commit
-        out["gdn_prep_recurrence"] = entry(f"gdn_prep_reg_kernel<{cfg.linear_conv_kernel_dim - 1}>", nG,
+        out["gdn_prep_recurrence"] = entry(gdn_recurrence_name(eng.MP, cfg.linear_conv_kernel_dim - 1), nG,
                                            us["prep_recurrence"],
                                            b["recurrence"] + (2 * cfg.linear_conv_kernel_dim - 1) * C_ * 4
                                            + L * (C_ + 2 * Hv) * 4)
     return out
 
+
+
+def gdn_recurrence_name(rows: int, keep: int) -> str:
+    """GatedDeltaNet tree recurrence kernel (gdn.hip): the matrix form for up
+    to 32 rows (with the input prep fused when keep > 0; DTREE_GDN_KERNEL=reg
+    keeps the node-by-node kernels), else the depth-first kernel."""
+    if rows <= 32:
+        if os.environ.get("DTREE_GDN_KERNEL") == "reg":
+            return f"gdn_prep_reg_kernel<{keep}>" if keep else "gdn_tree_reg_kernel<32>"
+        return f"gdn_tree_chunk_kernel<{keep}>"
+    return "gdn_tree_dfs_kernel"
 
 
 def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -> str:

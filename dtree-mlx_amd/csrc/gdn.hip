@@ -15,6 +15,9 @@
 // per row = Dk / 4 (4 fp32 state elements each, dot products by butterflies
 // over the row's lanes). Node inputs (q, k, v, g, beta) and the node states of
 // the workgroup's rows live in LDS; nodes run in index order (parent < child).
+#include <cstdlib>
+#include <string>
+
 #include "common.h"
 
 namespace dtree {
@@ -23,6 +26,8 @@ constexpr int kConvMaxKeep = 7;
 constexpr int kGdnMaxNodes = DTREE_MAX_NODES;
 
 __device__ __forceinline__ float silu_acc(float a) { return a / (1.0f + __expf(-a)); }
+// SiLU with the hardware reciprocal (within 1 ulp) in place of the IEEE division.
+__device__ __forceinline__ float silu_fast(float a) { return a * __builtin_amdgcn_rcpf(1.0f + __expf(-a)); }
 
 template <int KEEP>
 __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__ x, const float* __restrict__ base,
@@ -873,6 +878,461 @@ __global__ __launch_bounds__(256, 2) void gdn_prep_reg_kernel(GdnParams p, PrepP
   reg_tree_step<TMAX, 0>(rt, s);
 }
 
+// ---- matrix form of the tree recurrence (trees of up to 32 nodes) ----------
+//
+// Unrolling S_t = g_t S_p(t) + delta_t k_t^T from the committed state S_0
+// along the root path of t gives, with D[t][a] = the product of g_b over the
+// path from a (exclusive) to t (inclusive) and gamma_t = the product over the
+// whole path,
+//   g_t S_p(t) = gamma_t S_0 + sum_{a strict ancestor of t} D[t][a] delta_a k_a^T.
+// The recurrence's per-node values are therefore
+//   delta_t = beta_t (v_t - gamma_t (S_0 k_t)) - sum_a L[t][a] delta_a,
+//             L[t][a] = beta_t D[t][a] (k_a . k_t)  (a strict ancestor of t),
+//   y_t     = gamma_t (S_0 q_t) + sum_a U[t][a] delta_a,
+//             U[t][a] = D[t][a] (k_a . q_t)  (a ancestor or t itself, D[t][t] = 1),
+// i.e. Delta = (I + L)^-1 R with R_t = beta_t (v_t - gamma_t S_0 k_t), and
+// Y = diag(gamma) (S_0 Q^T)^T + U (I + L)^-1 R. In node order (parents before
+// children) L is strictly lower triangular and L^(d+1) = 0 for a tree whose
+// deepest node has d strict ancestors, so
+//   (I + L)^-1 = (I - L)(I + L^2)(I + L^4) ... (I + L^(2^(K-1))),  2^K > d:
+// ceil(log2(d + 1)) squarings and products of 32 x 32 matrices instead of a
+// substitution over the nodes. Everything is fp32 on v_mfma_f32_16x16x4_f32:
+// the Gram matrices k.k and q.k, S_0 k and S_0 q, the powers and products, and
+// Y. D is formed by walking each node's parent chain (products of g, so any
+// real g is handled as by the node-by-node recurrence).
+//
+// A workgroup owns one value head and 16 value rows (S_0 rows [16][128]); it
+// loads its key head's k and q rows of every node, and computes the shared
+// 32 x 32 matrices itself (the 8 workgroups of a value head repeat them). Node
+// states are not formed: the commit replays the accepted path from S_0.
+constexpr int kChunkRows = 16;
+constexpr int kChunkThreads = 512;  // 8 waves: two per SIMD for the serial VALU phases
+
+__device__ __forceinline__ f32x4_t mfma16_f32(float a, float b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// acc += sum over k < 16 NJ of A[m][k] Bt[n][k] for a 16 x 16 tile (A, Bt row
+// pointers at the tile's first row, row stride LS floats, 16-byte aligned
+// rows). Lane l supplies row l % 16 of both; step s of dim group j contracts
+// k = 16 j + 4 (l / 16) + s, so each operand is one 16-byte LDS read per four
+// MFMAs. Output: lane l, register i holds (m, n) = (4 (l / 16) + i, l % 16).
+template <int LS, int NJ>
+__device__ __forceinline__ f32x4_t tile16_dot(const float* A, const float* Bt, int lane, f32x4_t acc) {
+  const float* ar = A + (lane & 15) * LS + 4 * (lane >> 4);
+  const float* br = Bt + (lane & 15) * LS + 4 * (lane >> 4);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(ar + 16 * j);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(br + 16 * j);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc = mfma16_f32(a[s], b[s], acc);
+  }
+  return acc;
+}
+
+// N independent tiles of tile16_dot (zero-initialised), their MFMA chains
+// interleaved step by step.
+template <int LS, int NJ, int N>
+__device__ __forceinline__ void tile16_dot_n(const float* const (&A)[N], const float* const (&Bt)[N], int lane,
+                                             f32x4_t (&acc)[N]) {
+  const float* ar[N];
+  const float* br[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    ar[n] = A[n] + (lane & 15) * LS + 4 * (lane >> 4);
+    br[n] = Bt[n] + (lane & 15) * LS + 4 * (lane >> 4);
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    f32x4_t a[N], b[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      a[n] = *reinterpret_cast<const f32x4_t*>(ar[n] + 16 * j);
+      b[n] = *reinterpret_cast<const f32x4_t*>(br[n] + 16 * j);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int n = 0; n < N; ++n) acc[n] = mfma16_f32(a[n][s], b[n][s], acc[n]);
+  }
+}
+
+// 32 x 32 matrices in LDS, row-major with stride 36 floats (16-byte aligned
+// rows; 16 rows of a tile read 16 bytes each from distinct banks), kept with
+// their transposes so both product operands are row reads.
+constexpr int kMS = 36;
+struct Mat32 {
+  float* a;  // [32][kMS] row-major
+  float* t;  // [32][kMS] transposed
+};
+
+// C = A B (+ C0 when given) for 32 x 32 matrices: wave w computes tile
+// (w / 2, w % 2) and stores it in both orientations.
+__device__ __forceinline__ void mat32_mul(Mat32 A, Mat32 B, const float* C0, Mat32 C, int wave, int lane) {
+  const int bm = wave >> 1, bn = wave & 1;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if (C0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = C0[(16 * bm + 4 * (lane >> 4) + i) * kMS + 16 * bn + (lane & 15)];
+  }
+  acc = tile16_dot<kMS, 2>(A.a + 16 * bm * kMS, B.t + 16 * bn * kMS, lane, acc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 16 * bm + 4 * (lane >> 4) + i, n = 16 * bn + (lane & 15);
+    C.a[m * kMS + n] = acc[i];
+    C.t[n * kMS + m] = acc[i];
+  }
+}
+
+// Input staging of the fused form: one round of loads (the raw conv inputs of
+// the key head's q and k channels and of the 16 value rows for every node, the
+// parents, the conv taps and committed window rows of those channels, b / a of
+// the value head, the committed state rows), then the tree conv + SiLU (window
+// of node t = the last KEEP + 1 rows of committed window ++ conv inputs along
+// the root path, newest tap first, as gdn_prep_kernel), the q / k RMS scaling
+// and g / beta, straight into the LDS rows of the matrix form. k and q are
+// written out by row block 0 of the first value head of a key head, g and beta
+// by row block 0 of each value head, v by every workgroup for its rows.
+template <int KEEP, int LS>
+__device__ __forceinline__ void chunk_prep(const GdnParams& p, const PrepParams& pp, int T, int h, int hk, int r0,
+                                           int tid, float (*kq)[32][LS], float (*s0)[LS], float (*vv)[kChunkRows],
+                                           float* gg, float* bb, int* par) {
+  constexpr int TM = 32, DK = 128, R = kChunkRows, NW = kChunkThreads / 64, NI = TM / NW;
+  __shared__ __align__(16) float raw[TM][2][DK];
+  __shared__ __align__(16) float vraw[TM][R];
+  const int lane64 = tid & 63, wave = tid >> 6;
+  // q / k: thread (wave, lane) holds channels ch .. ch+3 of plane (0 = q,
+  // 1 = k) for nodes wave, wave + 8, ...
+  const int plane = lane64 >> 5, ch = 4 * (lane64 & 31);
+  const int cq = plane * pp.key_dim + hk * DK + ch;  // conv column of those channels
+  // v: thread owns value row r0 + vj of node tid / 16
+  const int vj = tid & 15;
+  const int cv = 2 * pp.key_dim + h * DK + r0 + vj;
+  f32x4_t wk[KEEP + 1], bk[KEEP];
+  float wvk[KEEP + 1], bvk[KEEP];
+  {
+    f32x4_t xr[NI], sb;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {  // rows past the tree are zero (their conv stays finite)
+      const int t = wave + NW * i;
+      xr[i] = t < T ? *reinterpret_cast<const f32x4_t*>(pp.x + (size_t)t * pp.ldx + cq) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    f32x4_t vr = {0.f, 0.f, 0.f, 0.f};
+    if (tid < 4 * T)
+      vr = *reinterpret_cast<const f32x4_t*>(pp.x + (size_t)(tid >> 2) * pp.ldx + 2 * pp.key_dim + h * DK + r0 +
+                                             4 * (tid & 3));
+    float b_ = 0.f, a_ = 0.f;
+    if (tid < T) {
+      const float* row = pp.x + (size_t)tid * pp.ldx + pp.ab_col;
+      b_ = row[h];
+      a_ = row[pp.Hv + h];
+    }
+    if (tid < TM) par[tid] = tid < T ? valid_parent(p.parents[tid], tid) : -1;
+#pragma unroll
+    for (int r = 0; r <= KEEP; ++r) wk[r] = *reinterpret_cast<const f32x4_t*>(pp.w + (size_t)r * pp.C + cq);
+#pragma unroll
+    for (int r = 0; r < KEEP; ++r) bk[r] = *reinterpret_cast<const f32x4_t*>(pp.base + (size_t)r * pp.C + cq);
+#pragma unroll
+    for (int r = 0; r <= KEEP; ++r) wvk[r] = pp.w[(size_t)r * pp.C + cv];
+#pragma unroll
+    for (int r = 0; r < KEEP; ++r) bvk[r] = pp.base[(size_t)r * pp.C + cv];
+    sb = *reinterpret_cast<const f32x4_t*>(p.state + ((size_t)h * p.Dv + r0 + (tid >> 5)) * DK + 4 * (tid & 31));
+    const float alog = pp.A_log[h], dtb = pp.dt_bias[h];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) *reinterpret_cast<f32x4_t*>(&raw[wave + NW * i][plane][ch]) = xr[i];
+    if (tid < 4 * TM) *reinterpret_cast<f32x4_t*>(&vraw[tid >> 2][4 * (tid & 3)]) = vr;
+    if (tid < TM) {
+      const bool live = tid < T;
+      gg[tid] = live ? __expf(-__expf(alog) * softplus_f(a_ + dtb)) : 0.f;
+      bb[tid] = live ? 1.0f / (1.0f + __expf(-b_)) : 0.f;
+    }
+    *reinterpret_cast<f32x4_t*>(&s0[tid >> 5][4 * (tid & 31)]) = sb;
+  }
+  __syncthreads();
+  // conv rows of node t: itself and its first KEEP ancestors (-1 past the root)
+  __shared__ int anc_tab[TM][KEEP + 1];
+  if (tid < TM) {
+    int a = tid < T ? tid : -1;
+#pragma unroll
+    for (int i2 = 0; i2 <= KEEP; ++i2) {
+      anc_tab[tid][i2] = a;
+      if (a >= 0) a = par[a];
+    }
+  }
+  __syncthreads();
+  const float qks = plane ? pp.k_scale : pp.q_scale;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    // every node computed without a branch (so the unrolled nodes interleave);
+    // rows past the tree are set to zero after
+    const int t = wave + NW * i;  // wave-uniform
+    f32x4_t o;
+    {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      int nb = 0;
+#pragma unroll
+      for (int i2 = 0; i2 <= KEEP; ++i2) {
+        const int anc = anc_tab[t][i2];
+        f32x4_t val;
+        if (anc >= 0) {
+          val = *reinterpret_cast<const f32x4_t*>(&raw[anc][plane][ch]);
+        } else {
+          // window row KEEP - 1 - min(nb, KEEP - 1), selected over constant
+          // indices (a runtime index would put the rows in scratch memory)
+          const int wr = KEEP - 1 - min(nb, KEEP - 1);
+          val = bk[0];
+#pragma unroll
+          for (int r = 1; r < KEEP; ++r) val = wr == r ? bk[r] : val;
+          ++nb;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += wk[KEEP - i2][e] * val[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = silu_fast(acc[e]);
+      const float ss = row_sum32(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
+      o *= rsqrtf(ss * (1.0f / DK) + 1e-6f) * qks;
+    }
+    if (t >= T) o = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    *reinterpret_cast<f32x4_t*>(&kq[plane ^ 1][t][ch]) = o;  // kq[0] = k rows, kq[1] = q rows
+  }
+  {
+    const int t = tid >> 4;
+    float o;
+    {
+      float acc = 0.f;
+      int nb = 0;
+#pragma unroll
+      for (int i2 = 0; i2 <= KEEP; ++i2) {
+        const int anc = anc_tab[t][i2];
+        float val;
+        if (anc >= 0) {
+          val = vraw[anc][vj];
+        } else {
+          const int wr = KEEP - 1 - min(nb, KEEP - 1);
+          val = bvk[0];
+#pragma unroll
+          for (int r = 1; r < KEEP; ++r) val = wr == r ? bvk[r] : val;
+          ++nb;
+        }
+        acc += wvk[KEEP - i2] * val;
+      }
+      o = silu_acc(acc);  // v, g and beta equal gdn_prep_kernel's bit for bit
+    }
+    vv[t][vj] = t < T ? o : 0.f;
+  }
+  __syncthreads();
+}
+
+// The fused form's outputs for the commit (k, v, g, beta and q, as
+// gdn_prep_kernel writes them), from the staged LDS rows. Issued after the
+// staging barrier and before the MFMA tiles, so no barrier waits for these
+// stores while they are in flight.
+template <int LS>
+__device__ __forceinline__ void chunk_prep_store(const GdnParams& p, const PrepParams& pp, int T, int h, int hk,
+                                                 int r0, int tid, const float (*kq)[32][LS],
+                                                 const float (*vv)[kChunkRows], const float* gg, const float* bb) {
+  constexpr int DK = 128, R = kChunkRows;
+  if (r0 == 0 && h % (p.Hv / p.Hk) == 0) {  // q and k once per key head
+#pragma unroll
+    for (int i = 0; i < 2048 / kChunkThreads; ++i) {
+      const int e = tid + kChunkThreads * i, m = e >> 10, t = (e >> 5) & 31, c = e & 31;
+      if (t < T)
+        *reinterpret_cast<f32x4_t*>((m ? pp.q : pp.k) + (size_t)t * pp.key_dim + hk * DK + 4 * c) =
+            *reinterpret_cast<const f32x4_t*>(&kq[m][t][4 * c]);
+    }
+  }
+  {  // v of this workgroup's rows
+    const int t = tid >> 4, r = tid & 15;
+    if (t < T) pp.v[(size_t)t * (pp.C - 2 * pp.key_dim) + h * DK + r0 + r] = vv[t][r];
+  }
+  if (r0 == 0 && tid < T) {  // g and beta once per value head
+    pp.g[(size_t)tid * p.Hv + h] = gg[tid];
+    pp.beta[(size_t)tid * p.Hv + h] = bb[tid];
+  }
+}
+
+// KEEP = 0: q, k, v, g and beta come from memory (gdn_prep_kernel's output).
+// KEEP > 0 (the conv window, 1 .. kConvMaxKeep): the workgroup computes them
+// from the in_proj rows as gdn_prep_reg_kernel does (tree conv + SiLU, q / k
+// RMS scaling, g and beta), and writes k, v, g, beta and q once each for the
+// commit.
+template <int KEEP>
+__global__ __launch_bounds__(kChunkThreads) void gdn_tree_chunk_kernel(GdnParams p, PrepParams pp) {
+  constexpr int DK = 128, TM = 32, R = kChunkRows, LS = DK + 4;
+  // Phase 1 (loads, Gram and S_0 products) uses kq and s0; phase 2 (the
+  // inverse) reuses their space for eight 32 x 32 matrices.
+  constexpr int kPhase1 = (2 * TM + R) * LS;  // floats
+  constexpr int kPhase2 = 8 * TM * kMS;
+  __shared__ __align__(16) float big[kPhase1 > kPhase2 ? kPhase1 : kPhase2];
+  __shared__ __align__(16) float um[TM][kMS];      // U
+  __shared__ __align__(16) float rt[R][kMS];       // R^T: [value row][node]
+  __shared__ float gkk[TM][TM + 1], gqk[TM][TM + 1];  // k_t . k_a, q_t . k_a
+  __shared__ float sk[TM][R + 1], sq[TM][R + 1];  // S_0 k_t, S_0 q_t per value row
+  __shared__ float dm[TM][TM + 1];                // D[t][a] for strict ancestors a, else 0
+  __shared__ float vv[TM][R], gam[TM], gg[TM], bb[TM];
+  __shared__ int par[TM], s_depth;
+  float(*kq)[TM][LS] = reinterpret_cast<float(*)[TM][LS]>(big);
+  float(*s0)[LS] = reinterpret_cast<float(*)[LS]>(big + 2 * TM * LS);
+  const int T = p.T_dev ? min(max(*p.T_dev, 0), min(p.T, TM)) : min(p.T, TM);
+  const int nblk = p.Dv / R;
+  const int h = blockIdx.x / nblk, r0 = (blockIdx.x % nblk) * R;
+  const int hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) s_depth = 0;  // ordered before the decays by the loads' barrier
+
+  if constexpr (KEEP == 0) {
+    // ---- loads: every load of the workgroup in flight together ----
+    constexpr int NK = 2048 / kChunkThreads;  // float4 of k and q rows per thread
+    f32x4_t kb[NK], sb;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {  // 2 x 32 rows x 32 float4
+      const int e = tid + kChunkThreads * i, m = e >> 10, t = (e >> 5) & 31, c = e & 31;
+      kb[i] = t < T ? *reinterpret_cast<const f32x4_t*>((m ? p.q : p.k) + ((size_t)t * p.Hk + hk) * DK + 4 * c)
+                    : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    sb = *reinterpret_cast<const f32x4_t*>(p.state + ((size_t)h * p.Dv + r0 + (tid >> 5)) * DK + 4 * (tid & 31));
+    {  // 32 nodes x 16 rows of v
+      const int t = tid >> 4, r = tid & 15;
+      vv[t][r] = t < T ? p.v[((size_t)t * p.Hv + h) * p.Dv + r0 + r] : 0.f;
+    }
+    if (tid < TM) {
+      const bool live = tid < T;
+      gg[tid] = live ? p.g[(size_t)tid * p.Hv + h] : 0.f;
+      bb[tid] = live ? p.beta[(size_t)tid * p.Hv + h] : 0.f;
+      par[tid] = live ? valid_parent(p.parents[tid], tid) : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int e = tid + kChunkThreads * i, m = e >> 10, t = (e >> 5) & 31, c = e & 31;
+      *reinterpret_cast<f32x4_t*>(&kq[m][t][4 * c]) = kb[i];
+    }
+    *reinterpret_cast<f32x4_t*>(&s0[tid >> 5][4 * (tid & 31)]) = sb;
+    __syncthreads();
+  } else {
+    chunk_prep<KEEP>(p, pp, T, h, hk, r0, tid, kq, s0, vv, gg, bb, par);
+    chunk_prep_store<LS>(p, pp, T, h, hk, r0, tid, kq, vv, gg, bb);
+  }
+
+  // ---- path decays D[t][a] along each node's parent chain (wave 3, which
+  // has the fewest MFMA tiles below; LDS operations of a wave are ordered) ----
+  if (wave == 3) {
+    for (int e = lane; e < TM * TM; e += 64) dm[e >> 5][e & 31] = 0.f;
+    const int t = lane;
+    if (t < T) {
+      float cum = gg[t];
+      int a = par[t], depth = 0;
+      for (; depth < TM && a >= 0; ++depth) {  // a < t strictly decreasing
+        dm[t][a] = cum;
+        cum *= gg[a];
+        a = par[a];
+      }
+      gam[t] = cum;
+      atomicMax(&s_depth, depth);
+    } else if (t < TM) {
+      gam[t] = 0.f;
+    }
+  }
+  // ---- Gram blocks (t-block >= a-block) and S_0 products on MFMA ----
+  {
+    // wave w computes tile w (and w + 8 for waves 0, 1, their MFMA chains
+    // interleaved)
+    auto operands = [&](int job, const float*& A, const float*& B) {
+      if (job < 6) {
+        const int bt = job % 3 == 0 ? 0 : 1, ba = job % 3 == 2 ? 1 : 0;  // (0,0), (1,0), (1,1)
+        A = &kq[job < 3 ? 0 : 1][16 * bt][0];
+        B = &kq[0][16 * ba][0];
+      } else {
+        A = &s0[0][0];
+        B = &kq[job < 8 ? 0 : 1][16 * ((job - 6) & 1)][0];
+      }
+    };
+    auto store = [&](int job, const f32x4_t& d) {
+      if (job < 6) {
+        const int bt = job % 3 == 0 ? 0 : 1, ba = job % 3 == 2 ? 1 : 0;
+        float(*dst)[TM + 1] = job < 3 ? gkk : gqk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[16 * bt + 4 * (lane >> 4) + i][16 * ba + (lane & 15)] = d[i];
+      } else {
+        const int nb = (job - 6) & 1;
+        float(*dst)[R + 1] = job < 8 ? sk : sq;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[16 * nb + (lane & 15)][4 * (lane >> 4) + i] = d[i];
+      }
+    };
+    const float *A0, *B0, *A1, *B1;
+    operands(wave, A0, B0);
+    if (wave < 2) {
+      operands(wave + 8, A1, B1);
+      f32x4_t d[2];
+      tile16_dot_n<LS, 8, 2>({A0, A1}, {B0, B1}, lane, d);
+      store(wave, d[0]);
+      store(wave + 8, d[1]);
+    } else {
+      f32x4_t d[1];
+      tile16_dot_n<LS, 8, 1>({A0}, {B0}, lane, d);
+      store(wave, d[0]);
+    }
+  }
+  __syncthreads();
+
+  // ---- L, P_0 = I - L, U and R^T ----
+  // eight [32][kMS] matrices: X0, X0^T, X1, X1^T (powers of L), P0, P0^T,
+  // P1, P1^T (running product); the index is a pointer offset (an array of
+  // Mat32 indexed at run time would live in scratch memory)
+  auto Xm = [&](int i) { return Mat32{big + (2 * i) * TM * kMS, big + (2 * i + 1) * TM * kMS}; };
+  auto Pmat = [&](int i) { return Mat32{big + (4 + 2 * i) * TM * kMS, big + (5 + 2 * i) * TM * kMS}; };
+  for (int e = tid; e < TM * TM; e += kChunkThreads) {
+    const int t = e >> 5, a = e & 31;
+    const float l = a < t ? bb[t] * dm[t][a] * gkk[t][a] : 0.f;
+    Xm(0).a[t * kMS + a] = l;
+    Xm(0).t[a * kMS + t] = l;
+    const float p0 = (t == a ? 1.f : 0.f) - l;
+    Pmat(0).a[t * kMS + a] = p0;
+    Pmat(0).t[a * kMS + t] = p0;
+    um[t][a] = a < t ? dm[t][a] * gqk[t][a] : (a == t && t < T ? gqk[t][t] : 0.f);
+  }
+  for (int e = tid; e < R * TM; e += kChunkThreads) {
+    const int r = e >> 5, t = e & 31;
+    rt[r][t] = t < T ? bb[t] * (vv[t][r] - gam[t] * sk[t][r]) : 0.f;
+  }
+  __syncthreads();
+
+  // ---- (I + L)^-1 = (I - L)(I + L^2)(I + L^4) ... ----
+  const int d = s_depth;
+  int cur = 0;
+  for (int pw = 1; pw < TM && (1 << pw) <= d; ++pw) {  // factors I + L^(2^pw) while 2^pw <= d
+    const Mat32 src = Xm((pw - 1) & 1), dst = Xm(pw & 1);
+    if (wave < 4) mat32_mul(src, src, nullptr, dst, wave, lane);  // X_pw = X_(pw-1)^2
+    __syncthreads();
+    if (wave < 4) mat32_mul(Pmat(cur), dst, Pmat(cur).a, Pmat(cur ^ 1), wave, lane);  // P += P X_pw
+    cur ^= 1;
+    __syncthreads();
+  }
+
+  // ---- Y = diag(gamma) S_0 q + U (I + L)^-1 R ----
+  const Mat32 M = Xm(0);  // M = U T (the powers are no longer needed)
+  if (wave < 4) mat32_mul(Mat32{&um[0][0], nullptr}, Pmat(cur), nullptr, M, wave, lane);
+  __syncthreads();
+  if (wave < 2) {
+    f32x4_t acc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * wave + 4 * (lane >> 4) + i;
+      acc[i] = gam[t] * sq[t][lane & 15];
+    }
+    acc = tile16_dot<kMS, 2>(M.a + 16 * wave * kMS, &rt[0][0], lane, acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * wave + 4 * (lane >> 4) + i, r = lane & 15;
+      if (t < T) p.y[((size_t)t * p.Hv + h) * p.Dv + r0 + r] = acc[i];
+    }
+  }
+}
+
+
 // Gated RMSNorm of the recurrence output per (node, value head)
 // (RMSNormGated, qwen35_tree.py:322): o = rms_norm(y) * w * silu(z), written as
 // the split bf16 pair [hi, lo] the out_proj GEMM reads. 16 threads per
@@ -1038,6 +1498,17 @@ extern "C" int dtree_gdn_tree_conv(const float* x, const float* base_window, con
   return DTREE_OK;
 }
 
+// Matrix-form recurrence (gdn_tree_chunk_kernel) for trees of up to 32 nodes
+// with 128-dim key heads; DTREE_GDN_KERNEL=reg keeps the node-by-node
+// register kernel (timing and cross-checks).
+static bool use_chunk_recurrence(int rows, int dk, int dv) {
+  static const bool reg = [] {
+    const char* e = std::getenv("DTREE_GDN_KERNEL");
+    return e && std::string(e) == "reg";
+  }();
+  return !reg && rows <= 32 && dk == 128 && dv % kChunkRows == 0;
+}
+
 extern "C" int dtree_gdn_tree_recurrence(const float* q, const float* k, const float* v, const float* g,
                                          const float* beta, const float* state, const int32_t* parents,
                                          int32_t num_nodes, int32_t num_k_heads, int32_t num_v_heads,
@@ -1056,6 +1527,11 @@ extern "C" int dtree_gdn_tree_recurrence(const float* q, const float* k, const f
   p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.state = const_cast<float*>(state); p.parents = parents;
   p.T = num_nodes; p.Hk = num_k_heads; p.Hv = num_v_heads; p.Dv = head_v_dim; p.rpw = rpw;
   p.y = y; p.states = states;
+  if (!states && use_chunk_recurrence(num_nodes, head_k_dim, head_v_dim)) {
+    gdn_tree_chunk_kernel<0><<<num_v_heads * (head_v_dim / kChunkRows), kChunkThreads, 0, stream>>>(p, PrepParams{});
+    DTREE_LAUNCH_CHECK("gdn_tree_recurrence launch");
+    return DTREE_OK;
+  }
   if (head_k_dim == 128 && num_nodes <= kRegTreeMax && head_v_dim % 8 == 0) {
     if (num_nodes <= 32) gdn_tree_reg_kernel<32><<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
     else gdn_tree_dfs_kernel<<<num_v_heads * (head_v_dim / 8), 256, 0, stream>>>(p);
@@ -1177,7 +1653,10 @@ extern "C" int dtree_gdn_layer_recurrence(const DtreeGdnArgs* a, hipStream_t str
   p.parents = a->desc->parents; p.T_dev = &a->desc->num_nodes;
   p.T = a->rows_padded; p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->head_v_dim; p.rpw = rpw;
   p.y = a->y; p.states = nullptr;
-  if (a->rows_padded <= 32 && a->head_v_dim % 8 == 0) {
+  if (use_chunk_recurrence(a->rows_padded, a->head_k_dim, a->head_v_dim)) {
+    p.T = min(a->rows_padded, 32);
+    gdn_tree_chunk_kernel<0><<<a->num_v_heads * (a->head_v_dim / kChunkRows), kChunkThreads, 0, stream>>>(p, PrepParams{});
+  } else if (a->rows_padded <= 32 && a->head_v_dim % 8 == 0) {
     p.T = min(a->rows_padded, 32);
     gdn_tree_reg_kernel<32><<<a->num_v_heads * (a->head_v_dim / 8), 256, 0, stream>>>(p);
   } else if (a->rows_padded <= kRegTreeMax && a->head_v_dim % 8 == 0) {
@@ -1224,6 +1703,19 @@ extern "C" int dtree_gdn_layer_prep_recurrence(const DtreeGdnArgs* a, hipStream_
   p.parents = a->desc->parents; p.T_dev = &a->desc->num_nodes;
   p.T = a->rows_padded; p.Hk = a->num_k_heads; p.Hv = a->num_v_heads; p.Dv = a->head_v_dim; p.rpw = 8;
   p.y = a->y; p.states = nullptr;
+  if (use_chunk_recurrence(a->rows_padded, a->head_k_dim, a->head_v_dim)) {
+    const int cgrid = a->num_v_heads * (a->head_v_dim / kChunkRows);
+    p.T = min(a->rows_padded, 32);
+    switch (a->conv_keep) {
+#define DTREE_PREP_CHUNK_CASE(K) \
+  case K: gdn_tree_chunk_kernel<K><<<cgrid, kChunkThreads, 0, stream>>>(p, pp); break;
+      DTREE_PREP_CHUNK_CASE(1) DTREE_PREP_CHUNK_CASE(2) DTREE_PREP_CHUNK_CASE(3) DTREE_PREP_CHUNK_CASE(4)
+      DTREE_PREP_CHUNK_CASE(5) DTREE_PREP_CHUNK_CASE(6) DTREE_PREP_CHUNK_CASE(7)
+#undef DTREE_PREP_CHUNK_CASE
+    }
+    DTREE_LAUNCH_CHECK("gdn_layer_prep_recurrence launch");
+    return DTREE_OK;
+  }
   const int grid = a->num_v_heads * (a->head_v_dim / 8);
   switch (a->conv_keep) {
 #define DTREE_PREP_REG_CASE(K) \

@@ -107,10 +107,46 @@ def test_layer_shapes_conv_and_recurrence(T, seed):
     ry, rs = gdn.tree_gated_delta(q, k, v, g, beta, state, parents)
     assert np.abs(y - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
     assert np.abs(st - rs).max() <= 1e-5 * max(1.0, np.abs(rs).max())
-    # lazy mode (no node states / windows written) gives the same outputs
+    # lazy mode (no node states / windows written) gives the same outputs; up
+    # to 32 nodes it runs the matrix form (gdn_tree_chunk_kernel), which sums
+    # in another order
     y2, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
     out2, _ = _conv(x, base, w, parents, "cuda", want_windows=False)
-    assert np.array_equal(y, y2) and np.array_equal(out, out2)
+    assert np.array_equal(out, out2)
+    if T <= 32:
+        assert np.abs(y2 - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
+    else:
+        assert np.array_equal(y, y2)
+
+
+def _star(T):
+    return [-1] + [0] * (T - 1)
+
+
+@pytest.mark.parametrize("parents,scale", [
+    (random_tree(25, 11), "model"), (random_tree(32, 12), "model"), (list(range(-1, 31)), "model"),
+    (_star(32), "model"), ([-1], "model"), (random_tree(17, 13), "strong_decay"),
+    (random_tree(25, 14), "no_decay"), (random_tree(25, 15), "signed"),
+], ids=["rand25", "rand32", "chain32", "star32", "root_only", "strong_decay", "no_decay", "signed_g_beta"])
+def test_matrix_form_recurrence(parents, scale):
+    """Trees of up to 32 nodes without node states run the matrix form
+    (gdn_tree_chunk_kernel: Gram matrices and S_0 products on MFMA, a forward
+    substitution per value row). Against the node-by-node float64 oracle on
+    model-scale inputs, a 32-deep chain and a 31-leaf star, decays that
+    vanish (g ~ 1e-30) or are exactly 1, and the reference kernel test's
+    signed g / beta (no positivity assumed)."""
+    T = len(parents)
+    q, k, v, g, beta, state = _layer_inputs(T, 500 + T)
+    if scale == "strong_decay":
+        g = np.where(np.arange(T)[:, None] % 3 == 1, 1e-30, g)
+    elif scale == "no_decay":
+        g = np.ones_like(g)
+    elif scale == "signed":
+        r = np.random.default_rng(7)
+        g, beta = r.normal(size=g.shape) * 0.9, r.normal(size=beta.shape)
+    y, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
+    ry, _ = gdn.tree_gated_delta(q, k, v, g, beta, state, parents)
+    assert np.abs(y - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
 
 
 def _chain_tree(T, depth, seed):
