@@ -54,19 +54,11 @@ constexpr int kMaxPast = 16384;  // longest prefix the grid is sized for
 __host__ __device__ constexpr int chunk_keys(int D) { return D <= 128 ? DTREE_PAGE : DTREE_PAGE / 2; }
 constexpr float kNeg = -1e30f;
 constexpr float kLog2e = 1.4426950408889634f;
-// Workspace header: error word (bytes 0..3), then one counter per (group,
-// query block) from byte 64.
-constexpr int kWsHeader = 4096;
+// Workspace header (kAttnWsHeader): error word (bytes 0..3), then one counter
+// per (group, query block) from byte 64; the per-head kernel's flag exchange
+// region follows, then this kernel's partials.
+constexpr int kWsHeader = (int)kAttnWsHeader;
 constexpr int kMaxPairs = (kWsHeader - 64) / 4;
-constexpr int kSpinLimit = 1 << 21;  // counter polls (~1 us each) before a workgroup gives up
-
-// DTREE_TEST_SPIN_LIMIT=n lowers the poll bound (read at every launch), so
-// tests can make the wait give up from the host while every workgroup still
-// runs to its end.
-static int spin_limit() {
-  const char* e = std::getenv("DTREE_TEST_SPIN_LIMIT");
-  return e && e[0] ? std::max(0, std::atoi(e)) : kSpinLimit;
-}
 constexpr int kCombineBatch = 4;     // split slices in flight per wave in the combine
 
 struct AttnParams {
@@ -910,7 +902,8 @@ static size_t group_attention_workspace_bytes(int32_t num_heads, int32_t head_di
   const size_t head_floats = (size_t)(head_dim / 32) * 64 * 16 + 64;
   // splits never exceed one per prefix chunk plus the tree split
   const size_t splits = 1 + (size_t)attn_max_pchunks(head_dim, max_past_length);
-  return kWsHeader + (size_t)num_heads * nt * splits * head_floats * sizeof(float);
+  return kWsHeader + attn_ll_bytes(num_heads, head_dim, rows_padded) +
+         (size_t)num_heads * nt * splits * head_floats * sizeof(float);
 }
 
 static int group_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
@@ -963,10 +956,11 @@ static int group_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   attn_splits(D, a->max_past_length, pairs, cus, p.S, p.cps);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.off_xcd = off_xcd_test();
-  p.spin_limit = spin_limit();
+  p.spin_limit = attn_spin_limit();
   p.err = reinterpret_cast<int*>(a->workspace);
   p.counters = reinterpret_cast<int*>(reinterpret_cast<char*>(a->workspace) + 64);
-  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kWsHeader);
+  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + kWsHeader +
+                                    attn_ll_bytes(a->num_heads, D, a->rows_padded));
   const int grid = pairs * p.S;
   if (D == 128) {
     if (G == 2) gqa_tree_attn_kernel<128, 128, false, 2><<<grid, 64 * 2, 0, stream>>>(p);
@@ -1024,12 +1018,13 @@ extern "C" int dtree_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) 
 // array instead of a caller buffer. Each GPU holds its own copy until the
 // process ends; every call on a GPU shares it, so calls that overlap on one
 // GPU race.
-constexpr size_t kScratchBytes = 16u << 20;
+constexpr size_t kScratchBytes = 32u << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[64] = {nullptr};
+long long g_ll_key[64] = {0};  // exchange placement of the last call per GPU (0: region never used)
 
 // Device address of this GPU's scratch array (the host-side name is only a
 // stand-in), looked up once per device with that device current.
@@ -1049,14 +1044,22 @@ int scratch_for_current_device(void** out) {
   return DTREE_OK;
 }
 
-// Moves a workspace's error word into *status (OR) and clears it.
+// Moves a workspace's error word into *status (OR) and clears it. After a
+// give-up it also moves every epoch of the per-head flag exchange (table
+// place and length in header words 2 and 3) far ahead, so no flag written by
+// the failed launch, however late, matches a later launch's.
 __global__ void attn_status_kernel(int* err, int* status) {
+  const int e = *err;
+  if (!e) return;
+  const int off = err[2], n = err[3];
+  if (off >= (int)kAttnWsHeader && n > 0) {
+    uint32_t* ep = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(err) + off);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ep[i] += 1u << 16;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const int e = *err;
-    if (e) {
-      *status |= e;
-      *err = 0;
-    }
+    *status |= e;
+    *err = 0;
   }
 }
 
@@ -1080,10 +1083,28 @@ extern "C" int dtree_tree_attention_noalloc(const DtreeAttnArgs* a, hipStream_t 
   DTREE_REQUIRE(need > 0, "attention (no alloc): bad num_heads / head_dim / max_past_length / rows_padded");
   if (need > kScratchBytes)
     return fail(DTREE_E_WORKSPACE, "attention (no alloc): this shape needs " + std::to_string(need) +
-                                       " bytes of workspace, beyond the 16 MiB device scratch array");
+                                       " bytes of workspace, beyond the 32 MiB device scratch array");
   void* ws = nullptr;
   int rc = scratch_for_current_device(&ws);
   if (rc) return rc;
+  {
+    // The per-head flag exchange keeps epochs and slots across calls, placed
+    // by (heads, head dim); a call with another placement than the last one
+    // on this GPU starts from a cleared region.
+    int dev = 0;
+    rc = hip_check(hipGetDevice(&dev), "attention (no alloc): hipGetDevice");
+    if (rc) return rc;
+    const size_t llb = attn_ll_bytes(a->num_heads, a->head_dim, a->rows_padded);
+    const long long key = ((long long)a->num_heads << 32) | ((long long)a->head_dim << 8) | (a->rows_padded == 32);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (llb > 0 && g_ll_key[dev] != key) {
+      const int m16 = static_cast<int>(llb / 16);
+      zero_header_kernel<<<(m16 + 255) / 256, 256, 0, stream>>>(
+          reinterpret_cast<u32x4_t*>(reinterpret_cast<char*>(ws) + kAttnWsHeader), m16);
+      DTREE_LAUNCH_CHECK("attention (no alloc): exchange clear");
+      g_ll_key[dev] = key;
+    }
+  }
   // The group kernel keeps its error word and counters in the first 4 KiB; the
   // per-head kernel keeps one counter per (head, row block) at the start.
   const size_t head_counters = (64 + static_cast<size_t>(a->num_heads) * (a->rows_padded / 32) * 4 + 255) / 256 * 256;

@@ -37,6 +37,8 @@
 //                 consecutive keys per PV step, which is one 16-byte read of
 //                 the transposed V page.
 // K pages are [page][kv_head][64][D]; V pages are [page][kv_head][D][64].
+#include <cstdlib>
+
 #include "common.h"
 
 namespace dtree {
@@ -46,6 +48,13 @@ constexpr int kWaves = 4;          // waves (chunks) per workgroup
 constexpr int kMaxPast = 16384;    // longest prefix the grid is sized for
 // Prefix keys per chunk.
 __host__ __device__ constexpr int chunk_keys(int D) { return D <= 128 ? DTREE_PAGE : DTREE_PAGE / 2; }
+// Workgroups (splits) of one (head, query block) for npre prefix chunks and NT
+// tree chunks: head_dim 128 gives the tree chunks a split of their own, then
+// four prefix chunks per split; head_dim 256 packs tree chunks after the
+// prefix chunks, four chunks per split.
+__host__ __device__ constexpr int head_nsplit(int D, int npre, int NT) {
+  return D == 128 ? 1 + (npre + kWaves - 1) / kWaves : (npre + NT + kWaves - 1) / kWaves;
+}
 constexpr float kNeg = -1e30f;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -65,6 +74,12 @@ struct AttnParams {
   float* part; int* counters;
   int sep_combine;  // partials are combined by attn_combine_kernel (long prefixes)
   int off_xcd;      // test hook: treat every workgroup as off its expected XCD
+  // Flag exchange (ll_exchange; rows_padded 32, up to kAttnLLSplits splits):
+  // per query head an epoch word and kAttnLLSplits slots.
+  int ll;
+  uint32_t* ll_epoch; unsigned char* ll_slots; unsigned ll_bytes;
+  int* err;         // workspace header: error word, then the epoch table's place
+  int spin_limit;   // polls before a waiting workgroup gives up
 };
 
 __device__ __forceinline__ int swap_bits23(int c) { return (c & ~12) | ((c & 4) << 1) | ((c & 8) >> 1); }
@@ -382,7 +397,9 @@ __device__ __forceinline__ void q_frag_lds(const float* qs, int c, int h, u32x4_
 // cache rows P + node (once: query block 0, first head of the group).
 // q, k and v are finished one after the other, so at most one raw head row is
 // live in registers (head_dim 256 rows are 128 floats per lane pair).
-template <int D, int R, bool QS>
+// STAGED: the workgroup has already staged (and appended) this chunk's rows
+// (tree_rows_stage); the wave only scores its queries against them.
+template <int D, int R, bool QS, bool STAGED = false>
 __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& qr, const float* qs, int hq, int g,
                                            int G, int P, int L, int tc, int qrow, bool write_rows, int c, int h,
                                            uint16_t* ks, uint16_t* vt, float& m_run, float& l_run,
@@ -408,7 +425,8 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
     q_frag_lds<D>(qs, c, h, qf, ql);
   }
   u32x4_t kf8[NJ], vf8[NJ];
-  if constexpr (D <= 128) {
+  if constexpr (STAGED) {
+  } else if constexpr (D <= 128) {
     // Both raw rows in flight together: one round trip instead of two.
     HeadRow<D, R> kr, vr;
     row_issue<D, R, true>(kr, row + p.k_off + g * D, p.k_norm, cosr, sinr, h);
@@ -434,17 +452,19 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
       pack_frag<D>(vv, vf8);
     }
   }
-  if (node >= L) {
+  if constexpr (!STAGED) {
+    if (node >= L) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) vf8[j] = u32x4_t{0u, 0u, 0u, 0u};
-  }
+      for (int j = 0; j < NJ; ++j) vf8[j] = u32x4_t{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    *reinterpret_cast<u32x4_t*>(&ks[c * KS + 16 * j + 8 * h]) = kf8[j];
+    for (int j = 0; j < NJ; ++j) {
+      *reinterpret_cast<u32x4_t*>(&ks[c * KS + 16 * j + 8 * h]) = kf8[j];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t word = vf8[j][i >> 1];
-      vt[(16 * j + 8 * h + i) * VS + c] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t word = vf8[j][i >> 1];
+        vt[(16 * j + 8 * h + i) * VS + c] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
+      }
     }
   }
   // Only this wave touches ks/vt, and a wave's LDS operations complete in
@@ -482,7 +502,7 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
       va[db] = *reinterpret_cast<const u32x4_t*>(&vt[(32 * db + c) * VS + 16 * s2 + 8 * h]);
     pv_step<ND>(s[0], s2, va, o);
   }
-  if (p.write_cache && (hq % G) == 0 && write_rows && node < L) {
+  if (!STAGED && p.write_cache && (hq % G) == 0 && write_rows && node < L) {
     const int pos = P + node;
     const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
     uint16_t* kblk = p.kp + (size_t)(page * p.Hkv + g) * DTREE_PAGE * D;
@@ -496,6 +516,113 @@ __device__ __forceinline__ void tree_chunk(const AttnParams& p, HeadRow<D, R>& q
         const uint32_t word = vf8[j][i >> 1];
         vblk[kv_v_off(off, 16 * j + 8 * h + i, D)] = (uint16_t)((i & 1) ? (word >> 16) : (word & 0xffff));
       }
+    }
+  }
+}
+
+// ---- tree rows prepared by the whole workgroup (head_dim 128) --------------
+// Split 0 of a head holds the tree chunks alone. Its 256 threads load,
+// normalise, rotate and stage the tree's k and v rows for the scoring waves
+// and append them to the cache, instead of one wave doing all of it after the
+// query staging: thread t owns node 32 tc + t / 8 and dims 8j .. 8j+7 and
+// 64+8j .. +7 (j = t % 8), so each RoPE pair (d, d + 64) stays in one thread
+// and the k RMSNorm sum is completed over the row's 8 threads with DPP (the
+// query staging's layout). Chunk 0's loads go out at the kernel's start,
+// before the step descriptor is read.
+struct TreeRows {
+  f32x4_t k[4], v[4];
+  u32x4_t nw[2];
+  f32x4_t cs[2], sn[2];
+};
+
+__device__ __forceinline__ void tree_rows_issue(const AttnParams& p, int g, int tc, TreeRows& t) {
+  constexpr int D = 128;
+  const int n = 32 * tc + (threadIdx.x >> 3), j = threadIdx.x & 7;
+  const float* kr = p.qkv + (size_t)n * p.ld_qkv + p.k_off + g * D;
+  const float* vr = p.qkv + (size_t)n * p.ld_qkv + p.v_off + g * D;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = (i >> 1) * 64 + 8 * j + 4 * (i & 1);
+    t.k[i] = *reinterpret_cast<const f32x4_t*>(kr + d);
+    t.v[i] = *reinterpret_cast<const f32x4_t*>(vr + d);
+  }
+  // without k_norm the weight loads read the row itself (ignored)
+  const uint16_t* nwb = p.k_norm ? p.k_norm : reinterpret_cast<const uint16_t*>(kr);
+  t.nw[0] = ld_u32x4(nwb + 8 * j);
+  t.nw[1] = ld_u32x4(nwb + 64 + 8 * j);
+  const float* cr = p.rope_cos + n * 64 + 8 * j;
+  const float* sr = p.rope_sin + n * 64 + 8 * j;
+  t.cs[0] = *reinterpret_cast<const f32x4_t*>(cr);
+  t.cs[1] = *reinterpret_cast<const f32x4_t*>(cr + 4);
+  t.sn[0] = *reinterpret_cast<const f32x4_t*>(sr);
+  t.sn[1] = *reinterpret_cast<const f32x4_t*>(sr + 4);
+}
+
+// k: RMSNorm (k_norm) then RoPE; v: zero past the tree. Both go to the
+// chunk's LDS staging as bf16 (K rows [32][D + 8], V^T [D][40]) and, when
+// this workgroup appends (query block 0, first head of the KV group), to the
+// cache rows P + node.
+__device__ __forceinline__ void tree_rows_stage(const AttnParams& p, const TreeRows& t, int g, bool append, int P,
+                                                int L, int tc, uint16_t* ks, uint16_t* vt) {
+  constexpr int D = 128, KS = D + 8, VS = 32 + 8;
+  const int r = threadIdx.x >> 3, j = threadIdx.x & 7, n = 32 * tc + r;
+  float k[16], v[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      k[4 * i + e] = t.k[i][e];
+      v[4 * i + e] = n < L ? t.v[i][e] : 0.f;
+    }
+  if (p.k_norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ss += k[i] * k[i];
+    ss += dpp<0xB1>(ss);   // lane ^ 1
+    ss += dpp<0x4E>(ss);   // lane ^ 2
+    ss += dpp<0x141>(ss);  // the other quad of the row's 8 lanes
+    const float rs = rsqrtf(ss * (1.0f / D) + p.eps);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t w = t.nw[i >> 3][(i & 7) >> 1];
+      k[i] *= rs * ((i & 1) ? bf_hi(w) : bf_lo(w));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float cs = t.cs[i >> 2][i & 3], sn = t.sn[i >> 2][i & 3];
+    const float x1 = k[i], x2 = k[8 + i];
+    k[i] = x1 * cs - x2 * sn;
+    k[8 + i] = x1 * sn + x2 * cs;
+  }
+  const u32x4_t k0{pack_bf2(k[0], k[1]), pack_bf2(k[2], k[3]), pack_bf2(k[4], k[5]), pack_bf2(k[6], k[7])};
+  const u32x4_t k1{pack_bf2(k[8], k[9]), pack_bf2(k[10], k[11]), pack_bf2(k[12], k[13]), pack_bf2(k[14], k[15])};
+  *reinterpret_cast<u32x4_t*>(&ks[r * KS + 8 * j]) = k0;
+  *reinterpret_cast<u32x4_t*>(&ks[r * KS + 64 + 8 * j]) = k1;
+  uint16_t vb[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const uint32_t w = pack_bf2(v[i], v[i + 1]);
+    vb[i] = (uint16_t)(w & 0xffffu);
+    vb[i + 1] = (uint16_t)(w >> 16);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    vt[(8 * j + i) * VS + r] = vb[i];
+    vt[(64 + 8 * j + i) * VS + r] = vb[8 + i];
+  }
+  if (append && n < L) {
+    const int pos = P + n;
+    const int page = p.page_table[pos / DTREE_PAGE], off = pos % DTREE_PAGE;
+    uint16_t* kblk = p.kp + (size_t)(page * p.Hkv + g) * DTREE_PAGE * D;
+    uint16_t* vblk = p.vp + (size_t)(page * p.Hkv + g) * DTREE_PAGE * D;
+    // dims 8j .. 8j+7 (and 64 + 8j ..) of a key are one 16-byte run of the K block
+    *reinterpret_cast<u32x4_t*>(kblk + kv_k_off(off, 8 * j, D)) = k0;
+    *reinterpret_cast<u32x4_t*>(kblk + kv_k_off(off, 64 + 8 * j, D)) = k1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      vblk[kv_v_off(off, 8 * j + i, D)] = vb[i];
+      vblk[kv_v_off(off, 64 + 8 * j + i, D)] = vb[8 + i];
     }
   }
 }
@@ -586,6 +713,190 @@ __device__ __forceinline__ void prefix_chunk(const AttnParams& p, HeadRow<D, R>&
     }
 }
 
+// ---- flag exchange between a head's splits (rows_padded 32) ----------------
+// Each split's merged result (row max M, row sum, unnormalised 32 x D output)
+// is published as (value, flag) pairs, flag = the launch's epoch + 1, with
+// write-through stores whose acknowledgement nobody waits for: a reader takes
+// a pair as valid once its flag matches, and an aligned 8-byte store is seen
+// whole or not at all. The output is cut into 4 * D / 32 units (32-dim block
+// db, 8-dim group gq: four consecutive dims of each query per lane); unit u is
+// combined by split u % S, which reads only its partners' pairs of that unit
+// and their row statistics, so no split waits for a counter, an
+// acknowledgement or a last arriver, and the combine's reads are spread over
+// the S workgroups.
+//
+// Waves 0 and 1 publish, waves 2 and 3 combine: a wave's memory operations
+// complete in issue order, so a wave that had just issued write-through
+// stores would wait for their acknowledgement (~2 us) before its poll loads
+// return. The merged blocks sit in LDS (xm: the merge's exchange slots,
+// block db in owner wave db % 4's slot) for both roles.
+//
+// Epochs: every split reads its head's epoch word E at its start and flags
+// its pairs E + 1. A combiner that has seen all partners' flags knows every
+// split of this launch has read E, so it raises the word to E + 1 (atomic
+// max) for the next launch; slots are stale only with older flags, since a
+// slot's place depends on the head count and head dim alone. The wait is
+// bounded: a combiner that gives up sets the error word, raises the epoch past
+// E + 1, leaves its units unwritten, and dtree_attention_status moves every
+// epoch of the table far ahead before the step is recomputed.
+template <int D, bool GATE>
+__device__ __forceinline__ void ll_exchange(const AttnParams& p, int hq, int split, int S, int wave, int lane, int c,
+                                            int h, float M, float tot, const f32x4_t* xm, uint32_t F, int L) {
+  constexpr int ND = D / 32, NU = 4 * ND;
+  constexpr unsigned kSlot = attn_ll_slot_bytes(D);
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(p.ll_slots, p.ll_bytes);
+  const unsigned base = (unsigned)hq * kAttnLLSplits * kSlot;
+  // merged values of unit u for this lane: block u / 4 in its owner's slot
+  auto own_unit = [&](int u) -> f32x4_t {
+    const int db = u >> 2, gq = u & 3;
+    return xm[((db * kWaves + db % kWaves) * 4 + gq) * 64 + lane];
+  };
+  if (wave < 2) {
+    // ---- publish: row statistics, then every unit another split combines ----
+    // Workgroups go round-robin over the 8 XCDs (workgroup i of a launch to
+    // XCD (i + s) % 8, s the dispatcher's position when the launch starts), so
+    // with Hkv % 8 == 0 a head's splits, which share blockIdx % 8, share one
+    // XCD: there the pairs go to the shared L2 with plain stores
+    // (acknowledged by the L2, which serves the partners' polls). Otherwise
+    // (or with the test hook) they are written through (sc1) to memory, where
+    // polls from another XCD find them. Were placement ever different, the
+    // polls would give up and the launch report the error.
+    const bool native = !p.off_xcd && p.Hkv % kXcds == 0;
+    const unsigned own = base + (unsigned)split * kSlot;
+    if (wave == 0 && h == 0) {
+      const u32x4_t st{__float_as_uint(M), F, __float_as_uint(tot), F};
+      if (native) __builtin_amdgcn_raw_buffer_store_b128(st, rs, (int)(own + 16u * c), 0, 0);
+      else __builtin_amdgcn_raw_buffer_store_b128(st, rs, (int)(own + 16u * c), 0, kSc1);
+    }
+#pragma unroll
+    for (int u = wave; u < NU; u += 2) {
+      if (u % S == split) continue;
+      const f32x4_t v = own_unit(u);
+      const float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+      const unsigned off = own + 512u + (unsigned)u * 2048u + (unsigned)lane * 32u;
+      const u32x4_t s0{__float_as_uint(v0), F, __float_as_uint(v1), F}, s1{__float_as_uint(v2), F,
+                                                                           __float_as_uint(v3), F};
+      if (native) {
+        __builtin_amdgcn_raw_buffer_store_b128(s0, rs, (int)off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(s1, rs, (int)(off + 16u), 0, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(s0, rs, (int)off, 0, kSc1);
+        __builtin_amdgcn_raw_buffer_store_b128(s1, rs, (int)(off + 16u), 0, kSc1);
+      }
+    }
+    return;
+  }
+  // ---- combine: units split, split + S, ...; wave 2 takes every other one ----
+  const unsigned partners = ((1u << S) - 1u) & ~(1u << split);
+  const int orow = c;  // query block 0 (rows_padded 32)
+  bool seen = false, gave_up = false;
+  // A wave's loads complete after its earlier stores, so the output stores
+  // wait until every unit of the wave is combined.
+  constexpr int kMaxU = NU / 4;  // units per combining wave at S >= 2
+  float yo[kMaxU][4];
+  int uo_dim[kMaxU];
+#pragma unroll
+  for (int i = 0; i < kMaxU; ++i) uo_dim[i] = -1;
+#pragma unroll
+  for (int i = 0; i < kMaxU; ++i) {
+    const int u = split + S * (wave - 2) + 2 * S * i;
+    if (u >= NU || gave_up) break;
+    float pm[kAttnLLSplits], pt[kAttnLLSplits];
+    f32x4_t pv[kAttnLLSplits];
+#pragma unroll
+    for (int q = 0; q < kAttnLLSplits; ++q) {
+      pm[q] = kNeg;
+      pt[q] = 0.f;
+      pv[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    if (p.spin_limit < 0) {  // test hook: give up before the first poll
+      gave_up = true;
+      break;
+    }
+    unsigned pend = partners;  // partners some lane of the wave still lacks
+    int it = 0;
+    while (true) {
+      u32x4_t a[kAttnLLSplits], b0[kAttnLLSplits], b1[kAttnLLSplits];
+#pragma unroll
+      for (int q = 0; q < kAttnLLSplits; ++q) {
+        const bool want = (pend >> q) & 1u;
+        const unsigned qs = base + (unsigned)q * kSlot;
+        const unsigned uo = qs + 512u + (unsigned)u * 2048u + (unsigned)lane * 32u;
+        a[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(want ? qs + 16u * c : kOob), 0, kSc1);
+        b0[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(want ? uo : kOob), 0, kSc1);
+        b1[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(want ? uo + 16u : kOob), 0, kSc1);
+      }
+      unsigned still = 0;
+#pragma unroll
+      for (int q = 0; q < kAttnLLSplits; ++q) {
+        if (!((pend >> q) & 1u)) continue;
+        const bool ok = a[q][1] == F && a[q][3] == F && b0[q][1] == F && b0[q][3] == F && b1[q][1] == F &&
+                        b1[q][3] == F;
+        if (ok) {
+          const uint32_t a0 = a[q][0], a2 = a[q][2], c0 = b0[q][0], c2 = b0[q][2], d0 = b1[q][0], d2 = b1[q][2];
+          pm[q] = __uint_as_float(a0);
+          pt[q] = __uint_as_float(a2);
+          pv[q] = f32x4_t{__uint_as_float(c0), __uint_as_float(c2), __uint_as_float(d0), __uint_as_float(d2)};
+        }
+        if (__builtin_amdgcn_ballot_w64(!ok)) still |= 1u << q;
+      }
+      pend = still;
+      if (!pend) break;
+      if (++it > p.spin_limit) {
+        gave_up = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      asm volatile("" ::: "memory");  // the next round's loads are issued again
+    }
+    if (gave_up) break;
+    seen = true;
+    // Splits in split order, so every combiner of the head forms the same
+    // row max and sum.
+    const f32x4_t mv = own_unit(u);
+    const float m4[4] = {mv[0], mv[1], mv[2], mv[3]};
+    float Mx = M;
+#pragma unroll
+    for (int q = 0; q < kAttnLLSplits; ++q)
+      if ((partners >> q) & 1u) Mx = fmaxf(Mx, pm[q]);
+    float T = 0.f, y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < kAttnLLSplits; ++q) {
+      if (q >= S) continue;
+      const bool me = q == split;
+      const float w = fast_exp2((me ? M : pm[q]) - Mx);
+      T += w * (me ? tot : pt[q]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] += w * (me ? m4[i] : pv[q][i]);
+    }
+    const float inv = (orow < L && T > 0.f) ? 1.0f / T : 0.f;
+    const int db = u >> 2, gq = u & 3;
+    const int dim = 32 * db + 8 * gq + 4 * h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = orow < L ? y[i] * inv : 0.f;
+    if (GATE && orow < L) {
+      const f32x4_t gt =
+          *reinterpret_cast<const f32x4_t*>(p.qkv + (size_t)orow * p.ld_qkv + hq * p.q_stride + D + dim);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] *= 1.0f / (1.0f + __expf(-gt[i]));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) yo[i][e] = y[e];
+    uo_dim[i] = dim;
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxU; ++i) {
+    if (uo_dim[i] < 0) continue;
+    const int col = hq * D + uo_dim[i];
+    const size_t oi = p.out_tiled ? tiled_index(orow, col, p.ld_out) : (size_t)orow * p.ld_out + col;
+    store_act4(p.out, p.out_lo, oi, yo[i], p.out_h16);
+  }
+  if (lane == 0 && (seen || gave_up)) {
+    __hip_atomic_fetch_max(p.ll_epoch + hq, gave_up ? F + 1u : F, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gave_up) __hip_atomic_fetch_or(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // Combine of a head's workgroup partials ([block][lane][16] floats, then m and
 // l of the 32 queries, per split) by the last workgroup to arrive: kSb splits
 // per round with every load of the round in flight (ranged loads past the
@@ -662,6 +973,7 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   constexpr int kMerge = kMl + ND * kWaves * 4 * 64 * 16;  // + [block][wave][4][lane] f32x4
   constexpr int kChunkLds = TB * kStage + kQs;
   constexpr int CK = chunk_keys(D);
+  constexpr bool TF = D == 128;  // tree chunks first, in a split of their own, staged by the workgroup
   __shared__ __align__(16) unsigned char lds[kChunkLds > kMerge ? kChunkLds : kMerge];
   __shared__ int s_last;
 
@@ -681,23 +993,37 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   // which keeps the argument loads in one round trip.
   const int g = pair % p.Hkv, split = pair / p.Hkv;
   const int hq = g * G + (bid >> 3) % G;
+  // The head's exchange epoch (flag exchange), read before anything of this
+  // launch can raise it.
+  const uint32_t ll_flag =
+      p.ll ? __hip_atomic_load(p.ll_epoch + hq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u : 0u;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
-  const int chunk = split * kWaves + wave;
   const int qrow = 32 * rb + c;  // this lane's query row
+  // Chunk roles. head_dim 128 (TF): split 0 holds the tree chunks alone (wave
+  // tc scores tree chunk tc; the whole workgroup stages them) and prefix chunk
+  // pc is wave pc % 4 of split 1 + pc / 4. head_dim 256: chunk split * 4 +
+  // wave, prefix chunks first, then the tree chunks.
+  const int chunk = split * kWaves + wave;
+  const int pc_fixed = TF ? (split - 1) * kWaves + wave : chunk;  // prefix chunk, if this wave has one
   // Loads that do not depend on the step descriptor go out first, so their
   // latency overlaps the descriptor read: the workgroup's query rows (values,
-  // norm weights, RoPE; 10 loads per thread) and the page of this wave's
-  // prefix chunk. The chunk's K/V follow the descriptor check: issued before
-  // it, they delay the descriptor's own (scalar) load by microseconds.
+  // norm weights, RoPE; 10 loads per thread), the page of this wave's prefix
+  // chunk and (TF, split 0) the first tree chunk's k / v rows. The prefix
+  // chunk's K/V follow the descriptor check: issued before it, they delay the
+  // descriptor's own (scalar) load by microseconds.
   // (head_dim 256 with four tree chunks loads its q row per wave inside the
   // chunk: there is no LDS left to stage it.)
-  const bool prefix_wave = chunk < p.max_chunks - NT;  // a prefix chunk at the longest prefix
-  const int page = prefix_wave ? p.page_table[chunk * CK / DTREE_PAGE] : 0;
+  const bool prefix_wave = (!TF || split > 0) && pc_fixed < p.max_chunks - NT;  // at the longest prefix
+  const int page = prefix_wave ? p.page_table[pc_fixed * CK / DTREE_PAGE] : 0;
   HeadRow<D, R> qr;
   QStage<D> qst;
   if constexpr (QS) q_stage_issue<D>(p, hq, rb, qst);
+  TreeRows trows;
+  if constexpr (TF) {
+    if (split == 0) tree_rows_issue(p, g, 0, trows);
+  }
 
   if (pair >= p.splits * p.Hkv) return;
   const int P = p.desc->past_length, L = p.desc->num_nodes;
@@ -706,7 +1032,7 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   // rows than rows_padded leaves the output untouched instead of indexing past
   // buffers.
   if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;
-  const int nsplit = (nchunks + kWaves - 1) / kWaves;
+  const int nsplit = head_nsplit(D, npre, NT);
   if (split >= nsplit) return;
   if (32 * rb >= L) {
     // Query block past the tree: its output rows are zero (split 0 writes).
@@ -724,10 +1050,21 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   }
 
   float* qs = reinterpret_cast<float*>(lds + TB * kStage);
-  if constexpr (QS) {
-    q_stage_finish<D>(qst, p.q_norm != nullptr, p.eps, qs);
-    __syncthreads();
+  if constexpr (QS) q_stage_finish<D>(qst, p.q_norm != nullptr, p.eps, qs);
+  if constexpr (TF) {
+    // Split 0 stages tree chunks 0 .. rb (later chunks hold no ancestor of
+    // this query block's rows); query block 0 stages and appends them all.
+    if (split == 0) {
+      const bool append = p.write_cache && (hq % G) == 0 && rb == 0;
+      const int last = rb == 0 ? NT - 1 : rb;
+      for (int tc = 0; tc <= last && 32 * tc < L; ++tc) {
+        if (tc > 0) tree_rows_issue(p, g, tc, trows);
+        uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)tc * kStage);
+        tree_rows_stage(p, trows, g, append, P, L, tc, ks, ks + 32 * KS);
+      }
+    }
   }
+  if constexpr (QS || TF) lds_barrier();
 
   float m_run = kNeg, l_run = 0.f;
   f32x16_t o[ND];
@@ -736,20 +1073,22 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
 
-  const int tc = chunk - npre;  // tree chunk index
+  const int tc = TF ? (split == 0 ? wave : -1) : chunk - npre;  // tree chunk index
+  const int pc = TF ? (split == 0 ? npre : pc_fixed) : chunk;   // prefix chunk index (npre: none)
   if (tc >= 0 && tc < NT) {
-    // Tree chunks are the last NT chunks, each with its own staging.
-    if (32 * tc < L) {
+    // Each tree chunk has its own staging.
+    if (32 * tc < L && (!TF || tc <= rb)) {
       uint16_t* ks = reinterpret_cast<uint16_t*>(lds + (size_t)tc * kStage);
-      tree_chunk<D, R, QS>(p, qr, qs, hq, g, G, P, L, tc, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run, o);
+      tree_chunk<D, R, QS, TF>(p, qr, qs, hq, g, G, P, L, tc, qrow, rb == 0, c, h, ks, ks + 32 * KS, m_run, l_run,
+                               o);
     }
-  } else if (chunk < npre) {
+  } else if (pc < npre) {
     if constexpr (!QS)
       row_issue<D, R, true>(qr, p.qkv + (size_t)qrow * p.ld_qkv + hq * p.q_stride, p.q_norm,
                             p.rope_cos + qrow * (R / 2), p.rope_sin + qrow * (R / 2), h);
     ChunkKV<D> kv;
-    prefix_issue<D>(p, kv, page, g, chunk, c, h);
-    prefix_chunk<D, R, QS>(p, qr, qs, kv, P, chunk, c, h, m_run, l_run, o);
+    prefix_issue<D>(p, kv, page, g, pc, c, h);
+    prefix_chunk<D, R, QS>(p, qr, qs, kv, P, pc, c, h, m_run, l_run, o);
   }
 
   // ---- merge the four waves ----
@@ -762,12 +1101,12 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
   float* ml = reinterpret_cast<float*>(lds);             // [wave][m | l][32]
   f32x4_t* xch = reinterpret_cast<f32x4_t*>(lds + kMl);  // [block][wave][4][lane]
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  __syncthreads();  // retires the chunk staging (tree K/V, query rows), which shares this memory
+  lds_barrier();  // retires the chunk staging (tree K/V, query rows), which shares this memory
   if (h == 0) {
     ml[wave * 64 + c] = m_run;
     ml[wave * 64 + 32 + c] = l_tot;
   }
-  __syncthreads();
+  lds_barrier();
   float M = kNeg, tot = 0.f, self = 0.f;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[w * 64 + c]);
@@ -788,7 +1127,7 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
             f32x4_t{o[db][4 * gq], o[db][4 * gq + 1], o[db][4 * gq + 2], o[db][4 * gq + 3]};
     }
   }
-  __syncthreads();
+  lds_barrier();
   f32x16_t mine[NDW];  // completed blocks wave + kWaves * k
 #pragma unroll
   for (int db = 0; db < ND; ++db) {
@@ -807,6 +1146,26 @@ __global__ __launch_bounds__(64 * kWaves) void tree_attn_kernel(AttnParams p) {
     mine[db / kWaves] = a;
   }
 
+  if (nsplit > 1 && p.ll && nsplit <= kAttnLLSplits) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      // where dtree_attention_status finds the epoch table after a give-up
+      p.err[2] = (int)(reinterpret_cast<const unsigned char*>(p.ll_epoch) - reinterpret_cast<const unsigned char*>(p.err));
+      p.err[3] = p.Hq;
+    }
+    // Owner waves put their merged blocks in their own (unused) exchange
+    // slots, where both exchange roles read them.
+#pragma unroll
+    for (int k = 0; k < NDW; ++k) {
+      const int db = wave + kWaves * k;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        xch[((db * kWaves + wave) * 4 + gq) * 64 + lane] =
+            f32x4_t{mine[k][4 * gq], mine[k][4 * gq + 1], mine[k][4 * gq + 2], mine[k][4 * gq + 3]};
+    }
+    lds_barrier();
+    ll_exchange<D, GATE>(p, hq, split, nsplit, wave, lane, c, h, M, tot, xch, ll_flag, L);
+    return;
+  }
   if (nsplit > 1) {
     // Workgroup partial: [block][lane][16] floats (each lane moves its block
     // values in 16-byte agent-coherent stores and loads), then m and l of the
@@ -903,9 +1262,9 @@ __global__ __launch_bounds__(64 * kWaves) void attn_combine_kernel(AttnParams p)
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   constexpr int CK = chunk_keys(D);
   const int P = p.desc->past_length, L = p.desc->num_nodes;
-  const int nchunks = NT + (P + CK - 1) / CK;
+  const int npre = (P + CK - 1) / CK, nchunks = NT + npre;
   if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;  // the main kernel's guards
-  const int nsplit = (nchunks + kWaves - 1) / kWaves;
+  const int nsplit = head_nsplit(D, npre, NT);
   if (nsplit <= 1 || 32 * rb >= L) return;
   const size_t stride = (size_t)32 * D + 64;
   const __amdgpu_buffer_rsrc_t prs =
@@ -1004,7 +1363,7 @@ static int attn_max_chunks(int head_dim, int max_past, int nt) {
   return nt + (max_past + ck - 1) / ck;
 }
 static int attn_splits(int head_dim, int max_past, int nt) {
-  return (attn_max_chunks(head_dim, max_past, nt) + kWaves - 1) / kWaves;
+  return head_nsplit(head_dim, attn_max_chunks(head_dim, max_past, nt) - nt, nt);
 }
 
 namespace dtree {
@@ -1014,9 +1373,11 @@ size_t head_attention_workspace_bytes(int32_t num_heads, int32_t head_dim, int32
   const int nt = rows_padded / 32;
   const size_t stride = (size_t)32 * head_dim + 64;
   const size_t hb = (size_t)num_heads * nt;  // (head, query block) pairs
-  // header: error word (bytes 0..3, shared layout with the per-group
-  // kernel's workspace, never set by this kernel), counters from byte 64
-  return ((64 + hb * sizeof(int) + 255) & ~(size_t)255) +
+  if (64 + hb * sizeof(int) > kAttnWsHeader) return 0;
+  // header (kAttnWsHeader: error word, epoch table place, counters from byte
+  // 64; shared layout with the per-group kernel), the flag exchange region,
+  // then the last-arriver / separate-combine partials
+  return kAttnWsHeader + attn_ll_bytes(num_heads, head_dim, rows_padded) +
          hb * attn_splits(head_dim, max_past_length, nt) * stride * sizeof(float);
 }
 
@@ -1063,9 +1424,12 @@ int head_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   p.splits = attn_splits(D, a->max_past_length, nt);
   p.scale_log2 = a->scale * kLog2e; p.write_cache = a->write_cache;
   p.off_xcd = off_xcd_test();
-  p.counters = reinterpret_cast<int*>(reinterpret_cast<char*>(a->workspace) + 64);
-  p.part = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) +
-                                    ((64 + (size_t)a->num_heads * nt * sizeof(int) + 255) & ~(size_t)255));
+  char* ws = reinterpret_cast<char*>(a->workspace);
+  const size_t ll_bytes = attn_ll_bytes(a->num_heads, D, a->rows_padded);
+  p.err = reinterpret_cast<int*>(ws);
+  p.counters = reinterpret_cast<int*>(ws + 64);
+  p.part = reinterpret_cast<float*>(ws + kAttnWsHeader + ll_bytes);
+  p.spin_limit = attn_spin_limit();
   const int G = p.Hq / p.Hkv;
   const int pairs = p.splits * p.Hkv;
   const int grid = ((pairs + 7) / 8) * 8 * G * nt;  // nt query blocks of ((pairs+7)/8)*8*G workgroups
@@ -1073,6 +1437,14 @@ int head_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   // Long prefixes combine in a launch of their own (attn_combine_kernel):
   // when the last arriver alone would read more than 128 KB of partials.
   p.sep_combine = (size_t)p.splits * 32 * D * sizeof(float) > kSepCombineBytes;
+  // Trees of up to 32 nodes whose splits fit the exchange slots combine
+  // through the flag exchange (the step's split count is checked again on
+  // the device); DTREE_ATTN_EXCHANGE=counter keeps the last-arriver combine.
+  const char* xe = std::getenv("DTREE_ATTN_EXCHANGE");
+  p.ll = ll_bytes > 0 && !p.sep_combine && !(xe && xe[0] == 'c');
+  p.ll_epoch = reinterpret_cast<uint32_t*>(ws + kAttnWsHeader);
+  p.ll_slots = reinterpret_cast<unsigned char*>(ws + kAttnWsHeader + attn_ll_epoch_bytes(a->num_heads));
+  p.ll_bytes = (unsigned)(ll_bytes - attn_ll_epoch_bytes(a->num_heads));
   if (D == 128) {
     if (one) tree_attn_kernel<128, 128, false, 1><<<grid, 64 * kWaves, 0, stream>>>(p);
     else tree_attn_kernel<128, 128, false, 4><<<grid, 64 * kWaves, 0, stream>>>(p);

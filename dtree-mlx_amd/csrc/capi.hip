@@ -1,4 +1,5 @@
 // C-ABI plumbing: per-thread error message, ABI queries, HIP graph capture.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <string>
@@ -22,6 +23,15 @@ int fail(int code, const std::string& msg) {
 bool off_xcd_test() {
   const char* e = std::getenv("DTREE_TEST_OFF_XCD");
   return e && e[0] == '1';
+}
+
+// Polls before a bounded cross-workgroup wait gives up (~1 us each, ~2 s in
+// all). DTREE_TEST_SPIN_LIMIT=n lowers the bound (read at every launch), so
+// tests can make a wait give up from the host while every workgroup still
+// runs to its end; -1 makes every wait give up before its first poll.
+int attn_spin_limit() {
+  const char* e = std::getenv("DTREE_TEST_SPIN_LIMIT");
+  return e && e[0] ? std::max(-1, std::atoi(e)) : (1 << 21);
 }
 
 int hip_check(hipError_t e, const char* what) {

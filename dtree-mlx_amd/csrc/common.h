@@ -23,6 +23,7 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int hip_check(hipError_t e, const char* what);
 bool off_xcd_test();  // DTREE_TEST_OFF_XCD=1: exercise the cross-XCD exchange paths
+int attn_spin_limit();  // polls of a bounded cross-workgroup wait (DTREE_TEST_SPIN_LIMIT lowers it)
 
 #define DTREE_REQUIRE(cond, msg)                         \
   do {                                                   \
@@ -284,6 +285,12 @@ __device__ __forceinline__ float ld_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_stores_done() { __builtin_amdgcn_s_waitcnt(0); }
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS (and
+// scalar) operations, not for its global loads and stores, which
+// __syncthreads() drains as a workgroup-scope fence. Loads issued before it
+// stay in flight; stores (e.g. cache rows nobody in the workgroup reads back)
+// retire in the background.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ int arrive(int* counter) {
   return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -305,6 +312,27 @@ constexpr int kSc0 = 1;   // cache policy sc0: coherent within one XCD (read fro
 constexpr int kSc1 = 16;  // cache policy sc1: coherent across the XCDs' L2s (written through / read past them)
 __device__ __forceinline__ int xcc_id() {
   return __builtin_amdgcn_s_getreg(20 | (3 << 11));  // HW_REG_XCC_ID, bits [3:0]
+}
+
+// Tree-attention workspace layout shared by both attention designs:
+//   [0, 4 KiB)           header: error word (bytes 0..3), the flag exchange's
+//                        epoch table location (bytes 8..15), split counters
+//                        from byte 64
+//   [4 KiB, + ll bytes)  flag exchange of the per-head kernel (rows_padded 32
+//                        only): one epoch word per query head, then
+//                        kAttnLLSplits slots per head; neither design's
+//                        partials ever land here, so a flag word only ever
+//                        holds a flag
+//   then                 the design's own partials
+// A slot is 512 bytes of (row max, flag, row sum, flag) for 32 query rows,
+// then one 2 KiB unit per (32-dim block, 8-dim group): 64 lanes x 32 bytes of
+// (value, flag) pairs.
+constexpr size_t kAttnWsHeader = 4096;
+constexpr int kAttnLLSplits = 8;
+__host__ __device__ constexpr unsigned attn_ll_slot_bytes(int D) { return 512u + 4u * (unsigned)(D / 32) * 2048u; }
+__host__ __device__ constexpr size_t attn_ll_epoch_bytes(int Hq) { return ((size_t)Hq * 4 + 255) & ~(size_t)255; }
+__host__ __device__ constexpr size_t attn_ll_bytes(int Hq, int D, int rows_padded) {
+  return rows_padded == 32 ? attn_ll_epoch_bytes(Hq) + (size_t)Hq * kAttnLLSplits * attn_ll_slot_bytes(D) : 0;
 }
 
 }  // namespace dtree

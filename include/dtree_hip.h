@@ -224,6 +224,14 @@ int dtree_rope_table(const DtreeStepDesc* desc, int32_t rows_padded, int32_t hea
  * rope_dims 128 (or 0), gated 0; head_dim 256 with rope_dims 64, gated 1.
  * Trees of up to rows_padded (32, 64, 96 or 128) nodes; the ancestor bitset
  * word w of a node covers nodes 32w .. 32w+31.
+ *
+ * workspace: dtree_attention_workspace_bytes(num_heads, head_dim,
+ * max_past_length, rows_padded) bytes, zeroed once before its first use and
+ * then kept as the launches leave it: its counters return to zero by
+ * themselves and, for 32-row trees, the per-head kernel's splits exchange
+ * their partial results through flagged slots whose epoch words carry over
+ * from launch to launch. One workspace serves one (num_heads, head_dim,
+ * rows_padded); zero it again before using it with another.
  */
 typedef struct DtreeAttnArgs {
   const float* qkv; int32_t ld_qkv;
@@ -251,13 +259,14 @@ int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
 /*
  * dtree_tree_attention without a caller workspace: the same kernels keep their
  * workspace (error word, split counters, partials) in a file-scope device array
- * of dtree_tree_attention_noalloc_max_bytes() (16 MiB) bytes, one per GPU, held
+ * of dtree_tree_attention_noalloc_max_bytes() (32 MiB) bytes, one per GPU, held
  * until the process ends; args->workspace / workspace_bytes are ignored. A
  * shape whose workspace (dtree_attention_workspace_bytes' formula for the
  * kernel the shape selects) exceeds the array returns DTREE_E_WORKSPACE. Each
- * call clears the array's header with a fill kernel on `stream`; calls that
- * overlap on one GPU race (they share the array). No device memory is
- * allocated or freed.
+ * call clears the array's header with a fill kernel on `stream` (and the
+ * flag-exchange region when num_heads, head_dim or rows_padded differ from
+ * the previous call on this GPU); calls that overlap on one GPU race (they
+ * share the array). No device memory is allocated or freed.
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc).
@@ -265,12 +274,15 @@ int dtree_tree_attention(const DtreeAttnArgs* args, hipStream_t stream);
 size_t dtree_tree_attention_noalloc_max_bytes(void);
 int dtree_tree_attention_noalloc(const DtreeAttnArgs* args, hipStream_t stream);
 /* Status of the attention launches on a workspace, in stream order: the
- * per-KV-group kernel's splits meet at a bounded wait, and a split that gives
- * up (another split was not resident for ~2 s, e.g. when work on another
- * stream holds CUs) sets the workspace's error word and leaves its share of
- * the output unwritten. This ORs that word into *status (device memory; 1 =
- * a wait gave up since the last query) and clears it. workspace = NULL reads
- * the allocation-free entry's device scratch of the current GPU, which
+ * per-KV-group kernel's splits meet at a bounded wait, and so do the per-head
+ * kernel's splits in its flag exchange (32-row trees); a split that gives up
+ * (another split was not resident for ~2 s, e.g. when work on another stream
+ * holds CUs) sets the workspace's error word and leaves its share of the
+ * output unwritten. This ORs that word into *status (device memory; 1 = a
+ * wait gave up since the last query) and clears it; after a give-up it also
+ * moves the exchange's epoch words far ahead, so no flag the failed launch
+ * wrote can match a later one. workspace = NULL reads the allocation-free
+ * entry's device scratch of the current GPU, which
  * dtree_tree_attention_noalloc clears before each call: query it after each
  * such call. A step whose status is set must be recomputed; the wait's
  * counters return to zero by themselves, so the next launch is sound. The

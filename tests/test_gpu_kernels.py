@@ -388,7 +388,8 @@ def test_tree_attention_matches_oracle(gpu_device, P, shape, attn_kernel):
     np.testing.assert_allclose(kc, k, rtol=1e-2, atol=1e-2)
     np.testing.assert_array_equal(vc, oq.bf16_to_f32(oq.f32_to_bf16_bits(v)))
     Hq = 32
-    assert int(ws[: 64 + Hq * 4].view(torch.int32).abs().sum()) == 0  # error word clear, counters self-reset
+    assert int(ws[:4].view(torch.int32).item()) == 0  # error word clear
+    assert int(ws[64: 64 + Hq * 4].view(torch.int32).abs().sum()) == 0  # counters self-reset
 
 
 @pytest.mark.parametrize("P,max_past,noalloc", [(1000, 1024, False), (1000, 1024, True), (3000, 4096, False)])
@@ -399,7 +400,7 @@ def test_group_attention_give_up_is_reported(gpu_device, monkeypatch, P, max_pas
     dtree_attention_status reports it and clears the word, the counters are
     back at zero, and the next launch with the normal bound is correct and
     reports nothing. Also through the allocation-free entry point (whose
-    16 MiB scratch holds the grid for 1024 keys)."""
+    32 MiB scratch holds the grid for 1024 keys)."""
     monkeypatch.setenv("DTREE_ATTN_KERNEL", "group")
     parents = random_tree(25, seed=3)
     cache, out, ref, k, v, ws = _attention_case(gpu_device, P, parents, seed=5, max_past=max_past)
@@ -447,6 +448,91 @@ def test_group_attention_give_up_is_reported(gpu_device, monkeypatch, P, max_pas
     assert torch.equal(out, want)
     if not noalloc:
         assert int(ws[:4096].view(torch.int32).abs().sum()) == 0  # error word and counters at zero
+
+
+@pytest.mark.parametrize("P,max_past", [(300, 300), (512, 512), (1000, 1024), (1500, 1536), (1750, 1792)])
+def test_head_attention_flag_exchange_matches_counter_combine(gpu_device, monkeypatch, P, max_past):
+    """The per-head kernel's flag exchange (2..8 splits; every split combines
+    the output units u with u % splits == split from its partners' (value,
+    flag) pairs) against the last-arriver combine (DTREE_ATTN_EXCHANGE=counter)
+    and the oracle; the launch raises every head's epoch by exactly one
+    (launches in a row on one workspace: the give-up test below)."""
+    monkeypatch.setenv("DTREE_ATTN_KERNEL", "head")
+    parents = random_tree(25, seed=P)
+    Hq = 32
+    monkeypatch.setenv("DTREE_ATTN_EXCHANGE", "counter")
+    _, out_cnt, ref, *_ = _attention_case(gpu_device, P, parents, seed=P + 3, max_past=max_past)
+    monkeypatch.delenv("DTREE_ATTN_EXCHANGE")
+    cache, out_ll, ref2, k, v, ws = _attention_case(gpu_device, P, parents, seed=P + 3, max_past=max_past)
+    np.testing.assert_array_equal(ref, ref2)
+    epochs = ws[4096: 4096 + 4 * Hq].view(torch.int32)
+    assert torch.all(epochs == 1), epochs
+    got = bf16_f32(out_ll)[:25]
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref).max() <= 2e-2 * scale
+    # same partials, same split-order sum: at most one bf16 rounding apart
+    diff = np.abs(got - bf16_f32(out_cnt)[:25])
+    assert diff.max() <= 2 ** -7 * np.abs(got).max(), diff.max()
+
+
+@pytest.mark.parametrize("noalloc", [False, True])
+def test_head_attention_give_up_is_reported(gpu_device, monkeypatch, noalloc):
+    """The flag exchange's bounded wait, made to give up before its first poll
+    (DTREE_TEST_SPIN_LIMIT=-1; every workgroup still runs to its end): the
+    status query reports it, clears the word and moves every head's epoch
+    2^16 ahead; the next launch with the normal bound is correct and reports
+    nothing. Also through the allocation-free entry point."""
+    monkeypatch.setenv("DTREE_ATTN_KERNEL", "head")
+    P, max_past, Hq = 1000, 1024, 32
+    parents = random_tree(25, seed=4)
+    cache, out, ref, k, v, ws = _attention_case(gpu_device, P, parents, seed=6, max_past=max_past)
+    lib = N.lib()
+    status = torch.zeros(1, dtype=torch.int32, device=gpu_device)
+    ws_ptr = None if noalloc else ws.data_ptr()
+    g = np.random.default_rng(10)
+    qkv = torch.from_numpy(g.standard_normal((32, (Hq + 16) * 128)).astype(np.float32)).to(gpu_device)
+    depth = [0] * 25
+    for i in range(1, 25):
+        depth[i] = depth[parents[i]] + 1
+    desc = device_desc([0] * 25, [P + d for d in depth], parents, P, gpu_device)
+    cos = torch.zeros(32, 64, device=gpu_device)
+    sin = torch.zeros(32, 64, device=gpu_device)
+    N.check(lib.dtree_rope_table(desc.data_ptr(), 32, 128, 1e6, cos.data_ptr(), sin.data_ptr(), stream()))
+
+    def launch():
+        a = N.AttnArgs()
+        a.qkv = qkv.data_ptr(); a.ld_qkv = qkv.shape[1]
+        a.q_norm = None; a.k_norm = None; a.eps = 1e-6
+        a.rope_cos = cos.data_ptr(); a.rope_sin = sin.data_ptr()
+        a.k_pages = cache.k_ptr(0); a.v_pages = cache.v_ptr(0); a.page_table = cache.page_table.data_ptr()
+        a.desc = desc.data_ptr(); a.out = out.data_ptr(); a.ld_out = out.shape[1]
+        a.num_heads = Hq; a.num_kv_heads = 8; a.head_dim = 128; a.rows_padded = 32
+        a.scale = 128 ** -0.5; a.max_past_length = max_past; a.write_cache = 0
+        a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel()
+        f = lib.dtree_tree_attention_noalloc if noalloc else lib.dtree_tree_attention
+        N.check(f(C.byref(a), stream()), "attention")
+        N.check(lib.dtree_attention_status(ws_ptr, status.data_ptr(), stream()), "attention status")
+        torch.cuda.synchronize()
+
+    launch()
+    assert int(status.item()) == 0
+    want = out.clone()
+    if not noalloc:
+        e0 = ws[4096: 4096 + 4 * Hq].view(torch.int32).clone()
+    monkeypatch.setenv("DTREE_TEST_SPIN_LIMIT", "-1")
+    out.fill_(7.0)
+    launch()
+    assert int(status.item()) == 1, "a give-up was not reported"
+    if not noalloc:
+        e1 = ws[4096: 4096 + 4 * Hq].view(torch.int32)
+        assert torch.all(e1 >= e0 + (1 << 16)), (e0, e1)
+    monkeypatch.delenv("DTREE_TEST_SPIN_LIMIT")
+    status.zero_()
+    launch()
+    assert int(status.item()) == 0  # the word was cleared, nothing new
+    assert torch.equal(out, want)
+    if not noalloc:
+        assert int(ws[:4].view(torch.int32).item()) == 0
 
 
 @pytest.mark.parametrize("P", [0, 129, 1000])

@@ -65,30 +65,41 @@ def test_workspace_queries():
     assert lib.dtree_lmhead_candidate_blocks(151936, 32) == 1024
     assert lib.dtree_lmhead_candidate_blocks(4096, 32) == 64
     assert lib.dtree_lmhead_candidate_blocks(4096, 128) == 128
-    # attention: the larger of the two designs' workspaces.
-    # Per-head kernel: a 64-byte header (error word) and the head counters,
-    # 256-byte aligned, + one partial per head per 4-chunk workgroup (prefix
-    # 1024 = tree + 16 pages = 5 workgroups per head).
+    # attention: the larger of the two designs' workspaces. Both start with a
+    # 4 KB header (error word, exchange-table place, counters) and, for 32-row
+    # trees, the per-head flag exchange region: one epoch word per head
+    # (256-byte aligned block), then 8 slots per head of 512 bytes of row
+    # statistics and 4 * D / 32 units of 2 KB of (value, flag) pairs.
+    def ll_bytes(Hq, D, MP):
+        if MP != 32:
+            return 0
+        return ((Hq * 4 + 255) // 256) * 256 + Hq * 8 * (512 + 4 * (D // 32) * 2048)
+
+    # Per-head kernel: + one partial per head per workgroup for the
+    # last-arriver / separate combine; head_dim 128 gives the tree chunks a
+    # workgroup of its own (prefix 1024 = 16 pages -> 1 + 4 workgroups per
+    # head), head_dim 256 packs four chunks per workgroup, tree chunks last.
     def head_ws(Hq, D, P, MP):
         nt = MP // 32
         ck = 64 if D == 128 else 32
-        splits = (nt + (P + ck - 1) // ck + 3) // 4
-        return ((64 + Hq * nt * 4 + 255) // 256) * 256 + Hq * nt * splits * (32 * D + 64) * 4
+        npre = (P + ck - 1) // ck
+        splits = 1 + (npre + 3) // 4 if D == 128 else (nt + npre + 3) // 4
+        return 4096 + ll_bytes(Hq, D, MP) + Hq * nt * splits * (32 * D + 64) * 4
 
-    # Per-KV-group kernel: 4 KB header (error word, counters) + at most one
-    # partial (32 rows x head_dim fp32 + row max / sum) per head, query block
-    # and split, with at most one split per prefix chunk plus the tree split.
+    # Per-KV-group kernel: + at most one partial (32 rows x head_dim fp32 +
+    # row max / sum) per head, query block and split, with at most one split
+    # per prefix chunk plus the tree split.
     def group_ws(Hq, D, P, MP):
         nt = MP // 32
         ck = 64 if D == 128 else 32
-        return 4096 + Hq * nt * (1 + (P + ck - 1) // ck) * ((D // 32) * 64 * 16 + 64) * 4
+        return 4096 + ll_bytes(Hq, D, MP) + Hq * nt * (1 + (P + ck - 1) // ck) * ((D // 32) * 64 * 16 + 64) * 4
 
     for Hq, D, P, MP in [(32, 128, 1024, 32), (32, 128, 0, 32), (16, 256, 2048, 32), (32, 128, 1024, 96),
                          (16, 256, 8192, 96)]:
         want = max(head_ws(Hq, D, P, MP), group_ws(Hq, D, P, MP))
         assert lib.dtree_attention_workspace_bytes(Hq, D, P, MP) == want, (Hq, D, P, MP)
-    assert head_ws(32, 128, 1024, 32) == 256 + 32 * 5 * (32 * 128 + 64) * 4
-    assert head_ws(64, 128, 1024, 32) == 512 + 64 * 5 * (32 * 128 + 64) * 4
+    assert head_ws(32, 128, 1024, 96) == 4096 + 32 * 3 * 5 * (32 * 128 + 64) * 4
+    assert ll_bytes(32, 128, 32) == 256 + 32 * 8 * 33280
     assert lib.dtree_attention_workspace_bytes(32, 128, 1024, 48) == 0
 
 
