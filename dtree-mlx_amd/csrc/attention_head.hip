@@ -773,15 +773,17 @@ __device__ __forceinline__ void ll_exchange(const AttnParams& p, int hq, int spl
       if (u % S == split) continue;
       const f32x4_t v = own_unit(u);
       const float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
-      const unsigned off = own + 512u + (unsigned)u * 2048u + (unsigned)lane * 32u;
+      // two contiguous kilobytes per unit (every store instruction writes
+      // whole cache lines): values 0, 1 of each lane, then values 2, 3
+      const unsigned off = own + 512u + (unsigned)u * 2048u + (unsigned)lane * 16u;
       const u32x4_t s0{__float_as_uint(v0), F, __float_as_uint(v1), F}, s1{__float_as_uint(v2), F,
                                                                            __float_as_uint(v3), F};
       if (native) {
         __builtin_amdgcn_raw_buffer_store_b128(s0, rs, (int)off, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(s1, rs, (int)(off + 16u), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(s1, rs, (int)(off + 1024u), 0, 0);
       } else {
         __builtin_amdgcn_raw_buffer_store_b128(s0, rs, (int)off, 0, kSc1);
-        __builtin_amdgcn_raw_buffer_store_b128(s1, rs, (int)(off + 16u), 0, kSc1);
+        __builtin_amdgcn_raw_buffer_store_b128(s1, rs, (int)(off + 1024u), 0, kSc1);
       }
     }
     return;
@@ -821,10 +823,10 @@ __device__ __forceinline__ void ll_exchange(const AttnParams& p, int hq, int spl
       for (int q = 0; q < kAttnLLSplits; ++q) {
         const bool want = (pend >> q) & 1u;
         const unsigned qs = base + (unsigned)q * kSlot;
-        const unsigned uo = qs + 512u + (unsigned)u * 2048u + (unsigned)lane * 32u;
+        const unsigned uo = qs + 512u + (unsigned)u * 2048u + (unsigned)lane * 16u;
         a[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(want ? qs + 16u * c : kOob), 0, kSc1);
         b0[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(want ? uo : kOob), 0, kSc1);
-        b1[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(want ? uo + 16u : kOob), 0, kSc1);
+        b1[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(want ? uo + 1024u : kOob), 0, kSc1);
       }
       unsigned still = 0;
 #pragma unroll

@@ -325,8 +325,8 @@ __device__ __forceinline__ int xcc_id() {
 //                        holds a flag
 //   then                 the design's own partials
 // A slot is 512 bytes of (row max, flag, row sum, flag) for 32 query rows,
-// then one 2 KiB unit per (32-dim block, 8-dim group): 64 lanes x 32 bytes of
-// (value, flag) pairs.
+// then one 2 KiB unit per (32-dim block, 8-dim group): two runs of 64 lanes x
+// 16 bytes of (value, flag) pairs (a lane's values 0, 1, then its 2, 3).
 constexpr size_t kAttnWsHeader = 4096;
 constexpr int kAttnLLSplits = 8;
 __host__ __device__ constexpr unsigned attn_ll_slot_bytes(int D) { return 512u + 4u * (unsigned)(D / 32) * 2048u; }
