@@ -1508,28 +1508,26 @@ __device__ __forceinline__ void dp_gemm_body(const GemmParams& p) {
   // partial exchange).
   float xo[TE / kThreads + 1];
   if constexpr (EPI == DTREE_EPI_RESIDUAL) residual_issue<32, TN>(p, tile, xo);
-  // Waves 1..3 park their tiles; wave 0 adds them in wave order into slot 0.
-  if (wave > 0) {
-    float* my = red + (wave - 1) * TE;
+  // Every wave parks its tile; thread t adds elements 4t .. 4t+3 of the four
+  // in wave order (the order the sum always had) into slot 0. The barriers
+  // wait for LDS only: the residual rows stay in flight.
+  {
+    float* my = red + wave * TE;
 #pragma unroll
     for (int r = 0; r < 16; ++r) my[acc_row(r, h) * TN + c] = acc[r];
   }
-  __syncthreads();
-  if (wave == 0) {
+  lds_barrier();
+  f32x4_t tsum = reinterpret_cast<const f32x4_t*>(red)[threadIdx.x];
 #pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] += red[w * TE + acc_row(r, h) * TN + c];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) red[acc_row(r, h) * TN + c] = acc[r];
-  }
-  __syncthreads();
+  for (int w = 1; w < kWaves; ++w) tsum += reinterpret_cast<const f32x4_t*>(red + w * TE)[threadIdx.x];
+  reinterpret_cast<f32x4_t*>(red)[threadIdx.x] = tsum;
+  lds_barrier();
   if constexpr (KS > 1) {
     // Thread t holds elements 4t .. 4t+3 of the tile; slot KS * tile + part.
     const int t = threadIdx.x;
     const bool native = !p.off_xcd && xcc_id() == (bid & 7);
     const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
-    const f32x4_t mine = reinterpret_cast<const f32x4_t*>(red)[t];
+    const f32x4_t mine = tsum;
     const int off = ((KS * tile + part) * TE + 4 * t) * 4;
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, mine), prs, off, 0, kSc1);
     wait_stores_done();
