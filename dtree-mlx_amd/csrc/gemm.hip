@@ -381,10 +381,24 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
     if (threadIdx.x == 0) is_last = (arrive(&p.counters[tile]) == p.S - 1);
     __syncthreads();
     if (!is_last) return;
-    const float* all = p.part + (size_t)tile * p.S * TE;
+    // Splits' loads kPb at a time (agent-coherent, past the L2), added in
+    // split order.
+    constexpr int kPb = 8;
+    const __amdgpu_buffer_rsrc_t prs =
+        buf_rsrc(p.part + (size_t)tile * p.S * TE, (unsigned)((size_t)p.S * TE * sizeof(float)));
     for (int e = threadIdx.x; e < TE; e += kThreads) {
       float v = 0.f;
-      for (int q = 0; q < p.S; ++q) v += ld_coherent(all + (size_t)q * TE + e);
+      for (int q0 = 0; q0 < p.S; q0 += kPb) {
+        float pv[kPb];
+#pragma unroll
+        for (int z = 0; z < kPb; ++z) {
+          const unsigned off = q0 + z < p.S ? (unsigned)(((q0 + z) * TE + e) * 4) : kOob;
+          pv[z] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (int)off, 0, kSc1));
+        }
+#pragma unroll
+        for (int z = 0; z < kPb; ++z)
+          if (q0 + z < p.S) v += pv[z];
+      }
       red[e] = v;
     }
     if (threadIdx.x == 0) reset_counter(&p.counters[tile]);
@@ -1051,14 +1065,24 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
     }
     __syncthreads();
     if (!s_last) return;
+    // The parts' loads go out kQ4mPb at a time, then are added in part order
+    // (deterministic); a load-then-add per part would serialise P round
+    // trips past the L2.
+    constexpr int kQ4mPb = 8;
     for (int e4 = t; e4 < nf4; e4 += NT) {
       f32x4_t v = {0.f, 0.f, 0.f, 0.f};
-      for (int q = 0; q < P; ++q) {
-        if (q == part) {
-          v += reinterpret_cast<const f32x4_t*>(red)[e4];
-        } else {
-          v += __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                               prs, (int)(tile_base + (unsigned)q * (TF * 4) + 16u * e4), 0, kSc1));
+      for (int q0 = 0; q0 < P; q0 += kQ4mPb) {
+        u32x4_t pv[kQ4mPb];
+#pragma unroll
+        for (int z = 0; z < kQ4mPb; ++z) {
+          const int q = q0 + z;
+          const unsigned off = q < P && q != part ? tile_base + (unsigned)q * (TF * 4) + 16u * e4 : kOob;
+          pv[z] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0, kSc1);
+        }
+#pragma unroll
+        for (int z = 0; z < kQ4mPb; ++z) {
+          const int q = q0 + z;
+          if (q < P) v += q == part ? reinterpret_cast<const f32x4_t*>(red)[e4] : __builtin_bit_cast(f32x4_t, pv[z]);
         }
       }
       reinterpret_cast<f32x4_t*>(red)[e4] = v;
