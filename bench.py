@@ -213,13 +213,15 @@ def time_kernels(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str =
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant, lo="qkv" not in eng.HI_ONLY, h16=eng.h16), nl, us["qkv"], b["qkv"])
+    lo = not eng.hi_only  # q4 models and fp16 weights read one activation plane
+    out["qkv_gemm"] = entry(gemm_kernel_name(qkv_n, H, 0, quant, lo=lo and "qkv" not in eng.HI_ONLY, h16=eng.h16),
+                            nl, us["qkv"], b["qkv"])
     out["attention"] = entry(attention_kernel_name(eng.attn_grid_past(P), 128, 128, False, eng.MP), nl, us["attention"],
                              b["attention"])
-    out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant, h16=eng.h16), nl, us["o"], b["o"])
-    out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant, h16=eng.h16), nl, us["down"], b["down"])
-    out["gate_up_gemm"] = entry(gemm_kernel_name(2 * F, H, 2, quant, h16=eng.h16), nl, us["gu"], b["gu"])
-    out["lm_head"] = entry(lmhead_kernel_name(quant, eng.MP, eng.h16), 1, us["lm_head"], b["lm_head"])
+    out["o_gemm"] = entry(gemm_kernel_name(H, cfg.q_dim, 1, quant, lo=lo, h16=eng.h16), nl, us["o"], b["o"])
+    out["down_gemm"] = entry(gemm_kernel_name(H, F, 1, quant, lo=lo, h16=eng.h16), nl, us["down"], b["down"])
+    out["gate_up_gemm"] = entry(gemm_kernel_name(2 * F, H, 2, quant, lo=lo, h16=eng.h16), nl, us["gu"], b["gu"])
+    out["lm_head"] = entry(lmhead_kernel_name(quant, eng.MP, eng.h16, lo=lo), 1, us["lm_head"], b["lm_head"])
     return out
 
 
@@ -402,11 +404,13 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         return {"kernel": kernel, "launches_per_step": n, "avg_launch_us": t_us,
                 "algorithmic_bytes_per_launch": int(nbytes), "achieved_gbps": nbytes / (t_us * 1e-6) / 1e9}
 
-    kn = lambda n, k, epi, lo=True: gemm_kernel_name(n, k, epi, quant, rows=eng.MP, lo=lo, h16=eng.h16)  # noqa: E731
+    kn = lambda n, k, epi, lo=not eng.hi_only: gemm_kernel_name(n, k, epi, quant, rows=eng.MP, lo=lo,  # noqa: E731
+                                                                h16=eng.h16)
     out = {
         "in_proj_gemm": entry(kn(cfg.in_proj_dim, H, 0), nG, us["in"], b["in"]),
         "out_proj_gemm": entry(kn(H, cfg.value_dim, 1), nG, us["out"], b["out"]),
-        "attn_qkv_gemm": entry(kn(cfg.attn_qkv_dim, H, 0, "qkv" not in eng.HI_ONLY), nA, us["qkv"], b["qkv"]),
+        "attn_qkv_gemm": entry(kn(cfg.attn_qkv_dim, H, 0, not eng.hi_only and "qkv" not in eng.HI_ONLY), nA, us["qkv"],
+                               b["qkv"]),
         "o_gemm": entry(kn(H, cfg.q_dim, 1), nA, us["o"], b["o"]),
         "gate_up_gemm": entry(kn(2 * F, H, 2), nL, us["gu"], b["gu"]),
         "down_gemm": entry(kn(H, F, 1), nL, us["down"], b["down"]),
@@ -417,7 +421,8 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
         "gdn_commit": entry("gdn_commit_layers_kernel<128>", 1, us["commit"], nG * b["commit"]),
         "attention": entry(attention_kernel_name(eng.attn_grid_past(P), 256, 64, True, eng.MP), nA, us["attention"],
                            b["attention"]),
-        "lm_head": entry(lmhead_kernel_name(quant, eng.MP, eng.h16), 1, us["lm_head"], b["lm_head"]),
+        "lm_head": entry(lmhead_kernel_name(quant, eng.MP, eng.h16, lo=not eng.hi_only), 1, us["lm_head"],
+                         b["lm_head"]),
     }
     if fused:
         for k in ("gdn_prep", "gdn_recurrence"):
@@ -455,13 +460,13 @@ def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -
     return f"gqa_tree_attn_kernel<{D}, {R}, {g}, 4>" if group else f"tree_attn_kernel<{D}, {R}, {g}, {1 if MP == 32 else 4}>"
 
 
-def lmhead_kernel_name(quant: str, rows: int, h16: bool = False) -> str:
+def lmhead_kernel_name(quant: str, rows: int, h16: bool = False, lo: bool = True) -> str:
     """LM-head kernel (gemm.hip, dtree_lmhead_argmax): the one-pass q4 kernel's
-    argmax epilogue for a q4 embedding (vocabularies up to 262144), else the
-    persistent LM head (`h16`: fp16 tiled embedding and one fp16 activation
-    plane)."""
+    argmax epilogue for a q4 embedding (vocabularies up to 262144; `lo` False:
+    the high activation plane alone), else the persistent LM head (`h16`: fp16
+    tiled embedding and one fp16 activation plane)."""
     if quant == "q4":
-        return f"q4m_gemm_kernel<true, 16, {rows // 32}, 4>"
+        return f"q4m_gemm_kernel<{'true' if lo else 'false'}, 16, {rows // 32}, 4>"
     mb = rows // 32
     lo, h = ("false", ", true") if h16 else ("true", "")
     return (f"lmhead_kernel<{mb}, {2 if mb == 1 else (2 if mb == 2 else 1)}, {2 if mb == 1 else 1}, {lo}, true, "

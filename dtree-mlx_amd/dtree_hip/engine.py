@@ -145,6 +145,10 @@ class TreeEngineBase:
         # [hi, lo] of bf16 planes (value = hi + lo).
         self.h16 = weights.layout == W_TILED_F16
         self.act_dtype = torch.float16 if self.h16 else bf16
+        # q4 group-64 models run on the high bf16 plane alone (bf16
+        # activations, as the reference's quantised matmuls take them): half
+        # the activation bytes and MFMA passes of the split pair.
+        self.hi_only = self.h16 or getattr(weights, "quant", "bf16") == "q4"
         self.x = torch.zeros(MP, H, dtype=f32, device=dev)
         self.xg = torch.zeros(2, MP, H, dtype=self.act_dtype, device=dev)
         # RMSNorm statistics: per 32-row block, per 32-column tile, per row
@@ -286,8 +290,9 @@ class TreeEngineBase:
         return a
 
     def lo_ptr(self, t: torch.Tensor, offset_bytes: int = 0):
-        """Low plane of a plane buffer: none on the fp16 path (one plane)."""
-        return None if self.h16 else t[1].data_ptr() + offset_bytes
+        """Low plane of a plane buffer: none on the fp16 path (one plane) and
+        for q4 models (the high bf16 plane alone)."""
+        return None if self.hi_only else t[1].data_ptr() + offset_bytes
 
     def _embedding(self):
         """(pointer, layout, scale/bias pointer) of the tied embedding."""

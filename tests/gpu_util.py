@@ -69,7 +69,7 @@ def stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def compare_accepted_path(res, child_maps, oracle_post, decided, log=print) -> int:
+def compare_accepted_path(res, child_maps, oracle_post, decided, log=print, note: str = "") -> int:
     """Accepted path of the device walk against the oracle's walk over the
     oracle's own argmax (follow_verified_tree, dtree_runtime.py:195-208).
 
@@ -78,7 +78,8 @@ def compare_accepted_path(res, child_maps, oracle_post, decided, log=print) -> i
     including the first walked node whose row is not decided; past it the
     device may legitimately take another branch. Asserts equality on that
     prefix (and of the bonus token when the whole oracle path is decided) and
-    returns how many path nodes were compared."""
+    returns how many path nodes were compared. ``note`` (e.g. the logit
+    error) is appended to the record."""
     from oracle import tree as otree
 
     o_acc, o_bonus = otree.follow_verified_tree(child_maps, [int(t) for t in oracle_post])
@@ -90,7 +91,8 @@ def compare_accepted_path(res, child_maps, oracle_post, decided, log=print) -> i
         assert res.accepted[:k + 1] == o_acc[:k + 1], (res.accepted, o_acc, k)
         compared = k + 1
     msg = (f"accepted path: device {res.accepted} bonus {res.bonus_token}; oracle {o_acc} bonus {o_bonus}; "
-           f"compared {compared} of {len(o_acc)} nodes" + ("" if k is None else f" (node {o_acc[k]} undecided)"))
+           f"compared {compared} of {len(o_acc)} nodes" + ("" if k is None else f" (node {o_acc[k]} undecided)")
+           + (f"; {note}" if note else ""))
     log(msg)
     # a record pytest -q shows in its warnings summary
     warnings.warn(PathParityRecord(msg), stacklevel=2)

@@ -160,7 +160,9 @@ def _check(r, layer_ids, min_confident=0.5):
     assert np.array_equal(post[confident], o_post[confident])
     assert np.array_equal(post[sure], o_post[sure])
     assert confident.mean() >= min_confident and sure.mean() > 0.5
-    r["path_compared"] = compare_accepted_path(res, tree.child_maps, o_post, confident | sure)
+    note = (f"max logit err {float((err / scale).max()):.4f} of the row max (bar {TOL}); "
+            f"{int(confident.sum())}/{len(confident)} rows confident, {int(sure.sum())} sure")
+    r["path_compared"] = compare_accepted_path(res, tree.child_maps, o_post, confident | sure, note=note)
     acc2, bonus2 = otree.follow_verified_tree(tree.child_maps, res.posterior)
     assert res.accepted == acc2 and res.bonus_token == bonus2
     cache, n = r["cache"], len(res.accepted)

@@ -127,7 +127,9 @@ def _check(r, layer_ids):
     assert np.array_equal(post[confident], o_post[confident])
     assert np.array_equal(post[sure], o_post[sure])
     assert confident.mean() > 0.5
-    r["path_compared"] = compare_accepted_path(res, tree.child_maps, o_post, confident | sure)
+    note = (f"max logit err {float((err / scale).max()):.4f} of the row max (bar {TOL}); "
+            f"{int(confident.sum())}/{len(confident)} rows confident, {int(sure.sum())} sure")
+    r["path_compared"] = compare_accepted_path(res, tree.child_maps, o_post, confident | sure, note=note)
     # device walk == host walk on the device's own posterior
     acc2, bonus2 = otree.follow_verified_tree(tree.child_maps, res.posterior)
     assert res.accepted == acc2 and res.bonus_token == bonus2
