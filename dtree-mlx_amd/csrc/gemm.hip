@@ -283,46 +283,50 @@ __device__ __forceinline__ void row_scale(const float* ss_in, int ss_tiles, floa
 // elements t, t + kThreads, ... of the [MP][TN] tile) and, last, the next
 // RMSNorm weight of its column; all loads in flight together (callers issue
 // them before other waits to overlap the round trip).
+// tid: the thread's index within the kThreads threads that run the
+// epilogue (threadIdx.x, or its offset inside a 256-thread group of a larger
+// workgroup).
 template <int MP, int TN>
-__device__ __forceinline__ void residual_issue(const GemmParams& p, int tile, float (&xo)[MP * TN / kThreads + 1]) {
-  const int col = tile * TN + threadIdx.x % TN;
+__device__ __forceinline__ void residual_issue(const GemmParams& p, int tile, float (&xo)[MP * TN / kThreads + 1],
+                                               int tid = threadIdx.x) {
+  const int col = tile * TN + tid % TN;
 #pragma unroll
   for (int i = 0; i < MP * TN / kThreads; ++i)
-    xo[i] = p.out_f32[(size_t)((threadIdx.x + i * kThreads) / TN) * p.ld_out_f32 + col];
+    xo[i] = p.out_f32[(size_t)((tid + i * kThreads) / TN) * p.ld_out_f32 + col];
   xo[MP * TN / kThreads] = bf2f(p.next_norm[col]);  // the next RMSNorm's weight
 }
 
 template <int MP, int TN, int EPI>
 __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* red, const float* rs, int tile,
-                                              const float* xpre = nullptr) {
+                                              const float* xpre = nullptr, int tid = threadIdx.x) {
   constexpr int TE = MP * TN;
   if constexpr (EPI == DTREE_EPI_STORE_F32) {
     // (columns past p.n: the long-M GEMM's last tile when n % 128 == 64)
-    for (int e = threadIdx.x; e < TE; e += kThreads) {
+    for (int e = tid; e < TE; e += kThreads) {
       const int m = e / TN, n = e % TN;
       if (tile * TN + n < p.n) p.out_f32[(size_t)m * p.ld_out_f32 + tile * TN + n] = red[e] * rs[m];
     }
   } else if constexpr (EPI == DTREE_EPI_STORE_BF16) {
-    for (int e = threadIdx.x; e < TE; e += kThreads) {
+    for (int e = tid; e < TE; e += kThreads) {
       const int m = e / TN, n = e % TN;
       split_store(p.out_bf16, p.out_lo, out_index(p.out_tiled, m, tile * TN + n, p.ld_out_bf16), red[e] * rs[m],
                   p.out_h16);
     }
   } else if constexpr (EPI == DTREE_EPI_RESIDUAL) {
     constexpr int IT = TE / kThreads;
-    const int n = threadIdx.x % TN;
+    const int n = tid % TN;
     const int col = tile * TN + n;
     float xo[IT + 1];
     if (xpre) {
 #pragma unroll
       for (int i = 0; i <= IT; ++i) xo[i] = xpre[i];
     } else {
-      residual_issue<MP, TN>(p, tile, xo);
+      residual_issue<MP, TN>(p, tile, xo, tid);
     }
     const float g = xo[IT];
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
-      const int e = threadIdx.x + i * kThreads;
+      const int e = tid + i * kThreads;
       const int m = e / TN;
       float* xp = p.out_f32 + (size_t)m * p.ld_out_f32 + col;
       const float xv = xo[i] + red[e];
@@ -335,7 +339,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmParams& p, const float* 
     }
   } else if constexpr (EPI == DTREE_EPI_SWIGLU) {
     // Each 32-column group = 16 gate rows then 16 up rows of 16 FFN features.
-    for (int e = threadIdx.x; e < MP * TN / 2; e += kThreads) {
+    for (int e = tid; e < MP * TN / 2; e += kThreads) {
       const int m = e / (TN / 2), f = e % (TN / 2);
       const int sb = f >> 4, j = f & 15;
       const float gt = red[m * TN + sb * 32 + j] * rs[m];
@@ -1107,23 +1111,40 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
     if (q8 == 0) p.lm_cand[cand_index(blockIdx.x, m, p.lm_blocks)] = make_int2(__float_as_int(bv), bi);
     return;
   }
-  // The tile epilogue is written for kThreads threads: the first four waves
-  // run it per (64-column block, 32-row block), outputs shifted by the row
-  // block (32-row blocks are contiguous in both output layouts; statistics
-  // are per 32-row block), which keeps its residual preloads at 8 per thread.
-  if (t < kThreads) {
-    for (int j = 0; j < nvalid; ++j) {
-#pragma unroll 1
-      for (int r2 = 0; r2 < MB; ++r2) {
-        const int R = 32 * r2;
-        GemmParams q = p;
-        if (q.out_f32) q.out_f32 += (size_t)R * q.ld_out_f32;
-        if (q.out_bf16) q.out_bf16 += (size_t)R * q.ld_out_bf16;
-        if (q.out_lo) q.out_lo += (size_t)R * q.ld_out_bf16;
-        if (q.hidden_out) q.hidden_out += (size_t)R * q.ld_hidden;
-        if (q.ss_out) q.ss_out += (size_t)r2 * (q.n >> 5) * 32;
-        tile_epilogue<32, 64, EPI>(q, red + (j * MP + R) * 64, rs + R, tile * CW + j);
+  // The tile epilogue is written for kThreads threads and one (64-column
+  // block, 32-row block) pair, outputs shifted by the row block (32-row
+  // blocks are contiguous in both output layouts; statistics are per 32-row
+  // block). The workgroup's 256-thread groups take the pairs in turn, each
+  // with the residual rows of all its pairs in flight before the first
+  // epilogue (a remainder of threads past the last full group idles).
+  constexpr int NG = NT / kThreads, NPAIR = CW * MB, PG = (NPAIR + NG - 1) / NG;
+  constexpr int EIT = 32 * 64 / kThreads;
+  const int grp = t / kThreads, gt = t % kThreads;
+  auto pair_params = [&](int r2) {
+    const int R = 32 * r2;
+    GemmParams q = p;
+    if (q.out_f32) q.out_f32 += (size_t)R * q.ld_out_f32;
+    if (q.out_bf16) q.out_bf16 += (size_t)R * q.ld_out_bf16;
+    if (q.out_lo) q.out_lo += (size_t)R * q.ld_out_bf16;
+    if (q.hidden_out) q.hidden_out += (size_t)R * q.ld_hidden;
+    if (q.ss_out) q.ss_out += (size_t)r2 * (q.n >> 5) * 32;
+    return q;
+  };
+  if (grp < NG) {
+    float xo[PG][EIT + 1];
+    if constexpr (EPI == DTREE_EPI_RESIDUAL) {
+#pragma unroll
+      for (int k = 0; k < PG; ++k) {
+        const int i = grp + NG * k, j = i / MB, r2 = i % MB;
+        if (i < NPAIR && j < nvalid) residual_issue<32, 64>(pair_params(r2), tile * CW + j, xo[k], gt);
       }
+    }
+#pragma unroll
+    for (int k = 0; k < PG; ++k) {
+      const int i = grp + NG * k, j = i / MB, r2 = i % MB;
+      if (i < NPAIR && j < nvalid)
+        tile_epilogue<32, 64, EPI>(pair_params(r2), red + (j * MP + 32 * r2) * 64, rs + 32 * r2, tile * CW + j,
+                                   EPI == DTREE_EPI_RESIDUAL ? xo[k] : nullptr, gt);
     }
   }
 }
