@@ -62,6 +62,7 @@ struct GemmParams {
   float* lm_logits;
   int2* lm_cand;
   int lm_blocks;
+  int spin;  // polls of a bounded wait for other workgroups (q4 one-pass K parts)
 };
 
 // Index of element (m, col) of a bf16 output with `ld` columns.
@@ -434,9 +435,15 @@ constexpr int kSkMaxGrid = 1024; // CU-count bound used for workspace sizing
 
 // q4 nibble pair j of a repacked word -> two bf16 holding 128 + q (exact: the
 // bf16 with bits 0x4300 | q is 128 + q for q < 128), K order (2j, 2j+1).
+// The mask and the exponent bits are brought into registers by (pure, hence
+// shared) asm moves: with both in registers each pair is one v_and_or_b32
+// (a VOP3 instruction, which takes no literal operand on this target) after
+// its shift, where literal operands cost a v_and and a v_or.
 __device__ __forceinline__ u32x4_t q4_pairs(uint32_t w) {
-  return u32x4_t{(w & 0x000F000Fu) | 0x43004300u, ((w >> 4) & 0x000F000Fu) | 0x43004300u,
-                 ((w >> 8) & 0x000F000Fu) | 0x43004300u, ((w >> 12) & 0x000F000Fu) | 0x43004300u};
+  uint32_t m, e;
+  asm("s_mov_b32 %0, 0x000f000f" : "=s"(m));
+  asm("v_mov_b32 %0, 0x43004300" : "=v"(e));
+  return u32x4_t{(w & m) | e, ((w >> 4) & m) | e, ((w >> 8) & m) | e, ((w >> 12) & m) | e};
 }
 
 // ---- q4 helpers for 32 rows ----------------------------------------------------
@@ -471,7 +478,7 @@ __device__ __forceinline__ void q4_group(const u32x4_t (&xv)[2][4], const u32x4_
     const float sc = __uint_as_float(sb[nb] << 16);
     const float cf = __uint_as_float(sb[nb] & 0xffff0000u) - 128.f * sc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[nb][r] += sc * au[r] + cf * xs[r];
+    for (int r = 0; r < 16; ++r) acc[nb][r] = fmaf(cf, xs[r], fmaf(sc, au[r], acc[nb][r]));
   }
 }
 
@@ -888,7 +895,11 @@ struct Q4mShape {
   static constexpr int RED_BYTES = KI * TILE_FLOATS * 4;
   static constexpr int LDS_BYTES = 2 * STAGE_BYTES > RED_BYTES ? 2 * STAGE_BYTES : RED_BYTES;
 };
-constexpr int kQ4mDepth = 2;  // weight groups in flight per wave
+constexpr int kQ4mDepth = 2;   // weight groups in flight per wave
+constexpr int kQ4mMaxParts = 8;  // K parts per tile (remote partials of a pair fit one round of 8 loads)
+constexpr int kQ4mSpin = 2048;   // polls (about a microsecond each) before an owner leaves its pairs to the last arriver
+constexpr int kQ4mCtrInts = 32;  // counter words per tile: published, released, 16 pair claims (+ padding)
+constexpr int kQ4mXAhead = 1;  // activation steps in flight per thread (register sets)
 // Epilogue of the one-pass q4 kernel as the fused LM head (not a GEMM
 // epilogue of the C ABI): row scale, optional fp32 logits, and per row the
 // (largest logit, first index) of the tile as the workgroup's candidate.
@@ -899,13 +910,12 @@ constexpr int q4m_threads(int mb, int cw) { return 64 * cw * mb * (cw == 2 ? 2 :
 template <bool LO, int EPI, int MB, int CW>
 __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParams p) {
   using Sh = Q4mShape<LO, MB, CW>;
-  constexpr int KI = Sh::KI, NPL = Sh::NPL, MP = Sh::MP, D = kQ4mDepth, NT = Sh::THREADS;
+  constexpr int KI = Sh::KI, NPL = Sh::NPL, MP = Sh::MP, D = kQ4mDepth, XA = kQ4mXAhead, NT = Sh::THREADS;
   constexpr int TF = Sh::TILE_FLOATS;
   static_assert(EPI != kEpiLmArgmax || NT == 8 * MP, "LM-head epilogue: 8 threads per row");
   __shared__ __align__(16) unsigned char lds[Sh::LDS_BYTES];
   __shared__ float rs[MP];
   __shared__ float rs_scratch[NT];
-  __shared__ int s_last;
   const int t = threadIdx.x, lane = t & 63, c = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int cw = wave % CW, rb = (wave / CW) % MB, kl = wave / (CW * MB);
@@ -935,22 +945,23 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
   // i.e. bytes 16 * (piece % 256) of chunk q = piece / 256 = (K lane kk, row
   // block rq, plane pl). Groups past the part read zero (ranged loads) and
   // are never used.
-  u32x4_t xpre[Sh::LOADS];
-  auto x_issue = [&](int st) {
+  // Step j's pieces live in register set j % XA until they are stored.
+  u32x4_t xpre[XA][Sh::LOADS];
+  auto x_issue = [&](int xs, int st) {
 #pragma unroll
     for (int j = 0; j < Sh::LOADS; ++j) {
       const int piece = min(t + j * NT, Sh::PIECES - 1), q = piece >> 8, tq = piece & 255;
       const int kk = q / (MB * NPL), rq = (q / NPL) % MB, pl = q % NPL;
       const int kb = g0 + st * KI + kk;
       const unsigned off = kb < g1 ? (unsigned)(rq * nkb + kb) * 4096u + 16u * tq : kOob;
-      xpre[j] = pl == 0 ? buf_ld(xrs, off) : buf_ld(xlrs, off);
+      xpre[xs][j] = pl == 0 ? buf_ld(xrs, off) : buf_ld(xlrs, off);
     }
   };
-  auto x_store = [&](int buf) {
+  auto x_store = [&](int xs, int buf) {
 #pragma unroll
     for (int j = 0; j < Sh::LOADS; ++j)
       if (Sh::LOADS * NT == Sh::PIECES || t + j * NT < Sh::PIECES)
-        *reinterpret_cast<u32x4_t*>(lds + buf * Sh::STAGE_BYTES + 16 * (t + j * NT)) = xpre[j];
+        *reinterpret_cast<u32x4_t*>(lds + buf * Sh::STAGE_BYTES + 16 * (t + j * NT)) = xpre[xs][j];
   };
   // Weight ring: group j of this wave is kb = g0 + kl + KI * j; two 32-column
   // halves (nb) of q4 words (1 KB each) and their (scale, bias) words.
@@ -1001,34 +1012,43 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
       const float sc = __uint_as_float(sbr[s][nb] << 16);
       const float cf = __uint_as_float(sbr[s][nb] & 0xffff0000u) - 128.f * sc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[nb][r] += sc * au[r] + cf * xs[r];
+      for (int r = 0; r < 16; ++r) acc[nb][r] = fmaf(cf, xs[r], fmaf(sc, au[r], acc[nb][r]));
     }
   };
 
-  x_issue(0);
+#pragma unroll
+  for (int a = 0; a < XA; ++a) x_issue(a, a);
 #pragma unroll
   for (int s = 0; s < D; ++s) w_issue(s, s);
   ss_finish<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, ssv, rs, rs_scratch);
-  x_store(0);
-  x_issue(1);
+  x_store(0, 0);
+  x_issue(0, XA);
   __syncthreads();
-  // Step st: compute from LDS buffer st & 1, refill the weight slot, store
-  // step st + 1 (prefetched one step ago) into the other buffer, prefetch
-  // st + 2. (Prefetching two steps ahead in a second register set measured
-  // no faster: the steps are bound by issue, not by load latency.)
-  for (int st0 = 0; st0 < nsteps; st0 += D) {
+  // Step st: compute from LDS buffer st & 1, store step st + 1 (issued XA
+  // steps ago) into the other buffer, issue step st + 1 + XA's activations,
+  // then refill the weight slot with group st + D. A wave's loads return in
+  // issue order, so storing step st + 1 waits for every load issued before
+  // it; with the activations issued ahead of each step's weights that is the
+  // weights of group st + D - XA - 1 = st (D = XA + 1), which the step's
+  // compute needs anyway, issued D steps ago. (Weights issued before the
+  // activations made every step wait for the weights issued one step
+  // earlier, however deep the ring; D = 3 with XA = 2 measured no faster and
+  // spills at 128 rows.) U = the loop's unroll, a multiple of D and XA so
+  // slots and register sets are compile-time.
+  constexpr int U = D % XA == 0 ? D : D * XA;
+  for (int st0 = 0; st0 < nsteps; st0 += U) {
 #pragma unroll
-    for (int s = 0; s < D; ++s) {
+    for (int s = 0; s < U; ++s) {
       const int st = st0 + s;
       if (st < nsteps) {
         if (cb_ok && g0 + st * KI + kl < g1) {
           __builtin_amdgcn_sched_barrier(0);
-          compute(s, s & 1);
+          compute(s % D, st & 1);
           __builtin_amdgcn_sched_barrier(0);
         }
-        w_issue(s, st + D);
-        x_store((s + 1) & 1);
-        x_issue(st + 2);
+        x_store((s + 1) % XA, (st + 1) & 1);
+        x_issue((s + 1) % XA, st + 1 + XA);
+        w_issue(s % D, st + D);
         __syncthreads();
       }
     }
@@ -1052,49 +1072,9 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
     __syncthreads();
   }
   const int nvalid = min(CW, nblk - tile * CW);  // column blocks of this tile inside n
-  if (P > 1) {
-    const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
-    const unsigned tile_base = (unsigned)tile * (unsigned)P * (unsigned)(TF * 4);
-    const unsigned mine = tile_base + (unsigned)part * (unsigned)(TF * 4);
-    const int nf4 = nvalid * MP * 16;  // valid floats / 4 (blocks are [cb][row][64])
-    for (int e4 = t; e4 < nf4; e4 += NT)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, reinterpret_cast<const f32x4_t*>(red)[e4]),
-                                             prs, (int)(mine + 16u * e4), 0, kSc1);
-    wait_stores_done();
-    __syncthreads();
-    if (t == 0) {
-      const int old = arrive(&p.counters[tile]);
-      s_last = old == P - 1;
-      if (s_last) reset_counter(&p.counters[tile]);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    // The parts' loads go out kQ4mPb at a time, then are added in part order
-    // (deterministic); a load-then-add per part would serialise P round
-    // trips past the L2.
-    constexpr int kQ4mPb = 8;
-    for (int e4 = t; e4 < nf4; e4 += NT) {
-      f32x4_t v = {0.f, 0.f, 0.f, 0.f};
-      for (int q0 = 0; q0 < P; q0 += kQ4mPb) {
-        u32x4_t pv[kQ4mPb];
-#pragma unroll
-        for (int z = 0; z < kQ4mPb; ++z) {
-          const int q = q0 + z;
-          const unsigned off = q < P && q != part ? tile_base + (unsigned)q * (TF * 4) + 16u * e4 : kOob;
-          pv[z] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0, kSc1);
-        }
-#pragma unroll
-        for (int z = 0; z < kQ4mPb; ++z) {
-          const int q = q0 + z;
-          if (q < P) v += q == part ? reinterpret_cast<const f32x4_t*>(red)[e4] : __builtin_bit_cast(f32x4_t, pv[z]);
-        }
-      }
-      reinterpret_cast<f32x4_t*>(red)[e4] = v;
-    }
-    __syncthreads();
-  }
   if constexpr (EPI == kEpiLmArgmax) {
-    // 8 consecutive threads per row (NT = 8 * MP): each scans every 8th column
+    // One part per tile (the host launches the LM head with S = 1). 8
+    // consecutive threads per row (NT = 8 * MP): each scans every 8th column
     // of the tile, then the 8 lanes reduce (max, first index on ties).
     const int m = t >> 3, q8 = t & 7;
     float bv = -__builtin_huge_valf();
@@ -1110,14 +1090,35 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
     argmax_dpp<0x141>(bv, bi);  // half-row mirror: the other quad of the 8
     if (q8 == 0) p.lm_cand[cand_index(blockIdx.x, m, p.lm_blocks)] = make_int2(__float_as_int(bv), bi);
     return;
-  }
-  // The tile epilogue is written for kThreads threads and one (64-column
-  // block, 32-row block) pair, outputs shifted by the row block (32-row
+  } else {
+  // The tile's output is cut into NPAIR (64-column block j, 32-row block r2)
+  // pairs, i = j * MB + r2, each 32 x 64 floats contiguous in red and in a
+  // published partial (blocks are [cb][row][64]).
+  constexpr int NPAIR = CW * MB;
+  static_assert(NPAIR <= 16, "pair masks and claim words");
+  unsigned valid = 0;
+#pragma unroll
+  for (int i = 0; i < NPAIR; ++i)
+    if (i / MB < nvalid) valid |= 1u << i;
+  // The m-th pair of a mask (m < popcount), by a scan over the static pairs.
+  auto nth_pair = [&](unsigned mask, int m) {
+    int res = 0;
+#pragma unroll
+    for (int i = 0; i < NPAIR; ++i)
+      if ((mask >> i) & 1u) {
+        if (m == 0) res = i;
+        --m;
+      }
+    return res;
+  };
+  auto pair_f4 = [&](int i) { return ((i / MB) * MP + 32 * (i % MB)) * 16; };  // f32x4 offset in red
+  // Epilogue of the pairs in `todo`. The tile epilogue is written for
+  // kThreads threads and one pair, outputs shifted by the row block (32-row
   // blocks are contiguous in both output layouts; statistics are per 32-row
-  // block). The workgroup's 256-thread groups take the pairs in turn, each
-  // with the residual rows of all its pairs in flight before the first
+  // block). The m-th pair of the mask goes to 256-thread group m % NG, each
+  // group with the residual rows of all its pairs in flight before its first
   // epilogue (a remainder of threads past the last full group idles).
-  constexpr int NG = NT / kThreads, NPAIR = CW * MB, PG = (NPAIR + NG - 1) / NG;
+  constexpr int NG = NT / kThreads, PG = (NPAIR + NG - 1) / NG;
   constexpr int EIT = 32 * 64 / kThreads;
   const int grp = t / kThreads, gt = t % kThreads;
   auto pair_params = [&](int r2) {
@@ -1130,22 +1131,186 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
     if (q.ss_out) q.ss_out += (size_t)r2 * (q.n >> 5) * 32;
     return q;
   };
-  if (grp < NG) {
+  auto epilogue = [&](unsigned todo) {
+    const int cnt = __builtin_popcount(todo);
+    if (grp >= NG) return;
     float xo[PG][EIT + 1];
     if constexpr (EPI == DTREE_EPI_RESIDUAL) {
 #pragma unroll
       for (int k = 0; k < PG; ++k) {
-        const int i = grp + NG * k, j = i / MB, r2 = i % MB;
-        if (i < NPAIR && j < nvalid) residual_issue<32, 64>(pair_params(r2), tile * CW + j, xo[k], gt);
+        const int m = grp + NG * k;
+        if (m < cnt) {
+          const int i = nth_pair(todo, m);
+          residual_issue<32, 64>(pair_params(i % MB), tile * CW + i / MB, xo[k], gt);
+        }
       }
     }
 #pragma unroll
     for (int k = 0; k < PG; ++k) {
-      const int i = grp + NG * k, j = i / MB, r2 = i % MB;
-      if (i < NPAIR && j < nvalid)
+      const int m = grp + NG * k;
+      if (m < cnt) {
+        const int i = nth_pair(todo, m), j = i / MB, r2 = i % MB;
         tile_epilogue<32, 64, EPI>(pair_params(r2), red + (j * MP + 32 * r2) * 64, rs + 32 * r2, tile * CW + j,
                                    EPI == DTREE_EPI_RESIDUAL ? xo[k] : nullptr, gt);
+      }
     }
+  };
+  if (P == 1) {
+    epilogue(valid);
+    return;
+  }
+  // ---- K parts: distributed combine ----
+  // Every part publishes its whole partial tile (written through), waits for
+  // the acknowledgement and counts itself on the tile's publication word.
+  // Pair i belongs to part i % P. An owner other than the last part to
+  // arrive polls the publication word (bounded) and, once every part has
+  // published, claims its pairs; the last arriver needs no wait. A pair's
+  // partials are added in part order (the sum does not depend on who adds
+  // them), then the pair's epilogue runs. The last arriver finally claims
+  // every pair it does not own, so pairs whose owner gave up waiting are
+  // still combined (by it); a claim word counts 1 or 2 claims, and the first
+  // claimer combines. Each part counts itself once more on the release word
+  // after its last use of the tile's words; the last to release clears them
+  // for the next launch. No part waits unboundedly: a give-up costs time,
+  // never a result.
+  const __amdgpu_buffer_rsrc_t prs = part_rsrc(p.part, p.part_bytes);
+  const unsigned tile_base = (unsigned)tile * (unsigned)P * (unsigned)(TF * 4);
+  {
+    const unsigned mine = tile_base + (unsigned)part * (unsigned)(TF * 4);
+    const int nf4 = nvalid * MP * 16;  // valid floats / 4
+    for (int e4 = t; e4 < nf4; e4 += NT)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, reinterpret_cast<const f32x4_t*>(red)[e4]),
+                                             prs, (int)(mine + 16u * e4), 0, kSc1);
+  }
+  wait_stores_done();
+  __syncthreads();
+  int* const ctr = p.counters + tile * kQ4mCtrInts;  // [0] published, [1] released, [2 + i] claims of pair i
+  unsigned own = 0;
+#pragma unroll
+  for (int i = 0; i < NPAIR; ++i)
+    if (i % P == part) own |= 1u << i;
+  own &= valid;
+  auto release = [&]() {
+    if (arrive(ctr + 1) == P - 1) {
+      reset_counter(ctr);
+      reset_counter(ctr + 1);
+#pragma unroll
+      for (int i = 0; i < NPAIR; ++i) reset_counter(ctr + 2 + i);
+    }
+  };
+  // Wave 0 runs the protocol: lane 0 arrives and polls, lane i claims pair i.
+  __shared__ unsigned s_todo, s_islast;
+  if (wave == 0) {
+    int last_l = 0, seen_l = 0;
+    if (lane == 0) {
+      last_l = arrive(ctr) == P - 1;
+      if (!last_l && own) {
+        for (int it = 0; it <= p.spin; ++it) {
+          if (it > 0) __builtin_amdgcn_s_sleep(1);
+          if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= P) {
+            seen_l = 1;
+            break;
+          }
+        }
+      }
+    }
+    const bool lst = __builtin_amdgcn_readfirstlane(last_l) != 0, seen = __builtin_amdgcn_readfirstlane(seen_l) != 0;
+    // The last arriver's own pairs: nobody else claims them (its closing
+    // claims skip them).
+    unsigned todo = lst ? own : 0u;
+    if (!lst && seen) {
+      const bool won = lane < NPAIR && ((own >> lane) & 1u) && arrive(ctr + 2 + lane) == 0;
+      todo = (unsigned)__builtin_amdgcn_ballot_w64(won);
+    }
+    if (lane == 0) {
+      if (!lst) release();  // after this wave's claims have returned
+      s_todo = todo;
+      s_islast = lst;
+    }
+  }
+  __syncthreads();
+  const bool last = s_islast != 0;
+  // Sum the partials of the pairs in `todo` into red, in part order. Items
+  // are (m-th pair of todo, f32x4 e4 of the pair's 512); a thread takes R =
+  // 8 / (P - 1) items per round, items t + (round * R + r) * NT, with all
+  // their remote partials in flight (8 loads, ranged loads for the rest).
+  auto sum_pairs = [&](unsigned todo) {
+    const int cnt = __builtin_popcount(todo), items = cnt * 512;
+    const int per = P - 1, R = 8 / per;  // P <= kQ4mMaxParts = 8
+    // slot z holds remote part qq(z) of item r(z) (wave-uniform tables)
+    int zr[8], zq[8];
+    {
+      int r = 0, qq = 0;
+#pragma unroll
+      for (int z = 0; z < 8; ++z) {
+        zr[z] = r;
+        zq[z] = qq < part ? qq : qq + 1;
+        if (++qq == per) {
+          qq = 0;
+          ++r;
+        }
+      }
+    }
+    for (int it0 = t; it0 < items; it0 += R * NT) {
+      int loc[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int item = it0 + r * NT;
+        loc[r] = r < R && item < items ? pair_f4(nth_pair(todo, item >> 9)) + (item & 511) : -1;
+      }
+      u32x4_t pv[8];
+#pragma unroll
+      for (int z = 0; z < 8; ++z) {
+        int l = -1;
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          if (zr[z] == r) l = loc[r];
+        const unsigned off = l >= 0 ? tile_base + (unsigned)zq[z] * (TF * 4) + 16u * (unsigned)l : kOob;
+        pv[z] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0, kSc1);
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        if (loc[r] < 0) continue;
+        const f32x4_t own_v = reinterpret_cast<const f32x4_t*>(red)[loc[r]];
+        f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+        bool added = false;
+#pragma unroll
+        for (int z = 0; z < 8; ++z) {
+          if (zr[z] != r) continue;
+          if (!added && zq[z] > part) {
+            v += own_v;
+            added = true;
+          }
+          v += __builtin_bit_cast(f32x4_t, pv[z]);
+        }
+        if (!added) v += own_v;
+        reinterpret_cast<f32x4_t*>(red)[loc[r]] = v;
+      }
+    }
+  };
+  unsigned todo = s_todo;
+  if (todo) {
+    sum_pairs(todo);
+    __syncthreads();
+    epilogue(todo);
+  }
+  if (!last) return;
+  __syncthreads();  // every thread has read s_todo
+  if (wave == 0) {
+    const bool won = lane < NPAIR && (((valid & ~own) >> lane) & 1u) && arrive(ctr + 2 + lane) == 0;
+    const unsigned got = (unsigned)__builtin_amdgcn_ballot_w64(won);
+    if (lane == 0) {
+      release();
+      s_todo = got;
+    }
+  }
+  __syncthreads();
+  todo = s_todo;
+  if (todo) {
+    sum_pairs(todo);
+    __syncthreads();
+    epilogue(todo);
+  }
   }
 }
 
@@ -1315,8 +1480,9 @@ static size_t sk_workspace_bytes(int n, int k, int cus) {
 // q4 one-pass plan for 64-128 rows (q4m_gemm_kernel): CW 64-column blocks per
 // workgroup (4 when the tiles still cover half the CUs, else 2), and K parts
 // so that tiles x parts stays within the CU count of the current device (one
-// workgroup per CU: the LDS staging and K-lane reduction take 64-128 KB).
-// Workspace sizing and launch both plan for the current device. DTREE_Q4M_CW and
+// workgroup per CU: the LDS staging and K-lane reduction take 64-128 KB), at
+// most kQ4mMaxParts (a tile's parts then run at once, so the owners' bounded
+// waits for each other's partials end early). Workspace sizing and launch both plan for the current device. DTREE_Q4M_CW and
 // DTREE_Q4M_PARTS override the choice; DTREE_Q4M=0 sends these shapes back to
 // one 32-row pass per row block.
 struct Q4mPlan {
@@ -1341,6 +1507,7 @@ static Q4mPlan q4m_plan(int n, int k, int cus) {
     int parts = parts_env > 0 ? parts_env : cus / q.tiles;
     const int max_parts = nkb / ki;  // at least one step of groups per part
     if (parts > max_parts) parts = max_parts;
+    if (parts > kQ4mMaxParts) parts = kQ4mMaxParts;
     if (parts < 1) parts = 1;
     q.parts = parts;
     return q;
@@ -1532,7 +1699,7 @@ __device__ __forceinline__ void dp_gemm_body(const GemmParams& p) {
           const float sc = __uint_as_float(sbr[s] << 16);
           const float cf = __uint_as_float(sbr[s] & 0xffff0000u) - 128.f * sc;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[r] += sc * au[r] + cf * xs[r];
+          for (int r = 0; r < 16; ++r) acc[r] = fmaf(cf, xs[r], fmaf(sc, au[r], acc[r]));
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -1781,7 +1948,7 @@ __device__ __forceinline__ void long_gemm_body(const GemmParams& p) {
             for (int pl = 0; pl < NPL; ++pl) au = mfma32(xa[i][pl], bq, au);
           }
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[rb][j][r] += sc[j] * au[r] + cf[j] * xs[r];
+          for (int r = 0; r < 16; ++r) acc[rb][j][r] = fmaf(cf[j], xs[r], fmaf(sc[j], au[r], acc[rb][j][r]));
         }
       }
     } else {
@@ -1972,7 +2139,8 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     DTREE_REQUIRE(xb < kOob && wb < kOob, "gemm: operands must be smaller than 2 GiB");
     const int cus = device_cus();
     const Q4mPlan pl = q4m_plan(a->n, a->k, cus);
-    DTREE_REQUIRE((size_t)pl.tiles * sizeof(int) <= kCounterBytes, "gemm: n too large for the tile counter region");
+    DTREE_REQUIRE((size_t)pl.tiles * kQ4mCtrInts * sizeof(int) <= kCounterBytes,
+                  "gemm: n too large for the tile counter region");
     const size_t need_m = q4m_workspace_bytes(a->rows_padded, a->n, a->k, cus);
     DTREE_REQUIRE(a->workspace_bytes >= need_m, "gemm: workspace too small for the q4 one-pass schedule");
     p.w_sb = a->w_scales;
@@ -1981,6 +2149,7 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
     p.sb_bytes = (unsigned)((size_t)a->n * (a->k / 64) * 4);
     p.S = pl.parts;
     p.part_bytes = (unsigned)(need_m - kCounterBytes);
+    p.spin = attn_spin_limit() < kQ4mSpin ? attn_spin_limit() : kQ4mSpin;
     launch_q4m(p, epi, a->rows_padded / 32, pl.cw, pl.tiles * pl.parts, stream);
     DTREE_LAUNCH_CHECK("gemm launch");
     return DTREE_OK;

@@ -342,6 +342,65 @@ def test_q4_one_pass_store_f32(gpu_device, n, k, MP):
     assert int(ws[:65536].view(torch.int32).abs().sum()) == 0  # counters self-reset
 
 
+# (n, k, rows): eight K parts with fewer pairs than parts (the 9B out_proj
+# class), two parts owning several pairs each (the 9B gate/up plan), four
+# parts, and eight parts over a ragged last tile.
+Q4M_PART_CASES = [(4096, 4096, 96), (24576, 128, 96), (768, 512, 64), (320, 1024, 128)]
+
+
+@pytest.mark.parametrize("n,k,MP", Q4M_PART_CASES)
+def test_q4_one_pass_parts_combine(gpu_device, monkeypatch, n, k, MP):
+    """The K parts of a one-pass tile combine in a distributed way: pair i
+    (64-column block, 32-row block) is added and finished by part i % P once
+    every part has published, or by the last part to arrive when its owner's
+    bounded wait gave up. Forced from the host (DTREE_TEST_SPIN_LIMIT=-1: no
+    owner polls, so the last arriver claims every pair; 0: one poll each),
+    every variant gives the same bits through the residual + next-norm +
+    hidden-capture epilogue, matches the q4 oracle, and leaves the tile
+    counters at zero."""
+    from dtree_hip.weights import untile_weight
+    g = np.random.default_rng(n + 3 * k + MP)
+    L = MP - 29
+    wq, s, b = o4.random_q4(n, k, g)
+    wt, sb = q4_to_tiled(*_to_torch(wq, s, b))
+    wt, sb = wt.to(gpu_device), sb.to(gpu_device)
+    xt, _, xin = _xrows(MP, L, k, g, gpu_device, hi_only=True)
+    res0 = torch.zeros(MP, n)
+    res0[:L] = torch.from_numpy(g.standard_normal((L, n)).astype(np.float32))
+    gn = torch.from_numpy((1 + 0.1 * g.standard_normal(n)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    ws = torch.zeros(N.lib().dtree_gemm_workspace_bytes(MP, n, k, 0), dtype=torch.uint8, device=gpu_device)
+    runs = []
+    for limit in (None, "-1", "0", None):
+        if limit is None:
+            monkeypatch.delenv("DTREE_TEST_SPIN_LIMIT", raising=False)
+        else:
+            monkeypatch.setenv("DTREE_TEST_SPIN_LIMIT", limit)
+        res = res0.clone().to(gpu_device)
+        outb = torch.zeros(MP * n, dtype=torch.bfloat16, device=gpu_device)
+        sso = torch.zeros(MP // 32, n // 32, 32, device=gpu_device)
+        hid = torch.zeros(MP, n, dtype=torch.bfloat16, device=gpu_device)
+        a = _args(xt, None, wt, sb, n, k, N.EPI_RESIDUAL, ws)
+        a.rows_padded = MP
+        a.out_f32 = res.data_ptr(); a.ld_out_f32 = n
+        a.out_bf16 = outb.data_ptr(); a.out_lo = None; a.ld_out_bf16 = n; a.out_layout = N.W_TILED
+        a.next_norm = gn.data_ptr(); a.ss_out = sso.data_ptr(); a.hidden_out = hid.data_ptr(); a.ld_hidden = n
+        print(f"q4 one pass parts n={n} k={k} rows={MP} spin limit={limit}", flush=True)
+        N.check(N.lib().dtree_gemm_bf16(C.byref(a), stream()), "q4 one pass parts")
+        torch.cuda.synchronize()
+        assert int(ws[:65536].view(torch.int32).abs().sum()) == 0  # counters cleared by the last release
+        runs.append((res.cpu(), outb.cpu(), sso.cpu(), hid.cpu()))
+    monkeypatch.delenv("DTREE_TEST_SPIN_LIMIT", raising=False)
+    for other in runs[1:]:
+        for x, y in zip(runs[0], other):
+            assert torch.equal(x, y)
+    got = runs[0][0].numpy()
+    ref = res0.double().numpy() + o4.q4_matmul(xin, wq, bf16_to_f32(s), bf16_to_f32(b))
+    assert np.abs(got - ref).max() <= 2e-4 * np.abs(ref).max()
+    assert not got[L:].any()
+    got_b = untile_weight(runs[0][1].view(MP, n)).float().numpy()
+    np.testing.assert_allclose(got_b, got * bf16_f32(gn)[None], rtol=2 ** -8, atol=1e-30)  # one bf16 plane
+
+
 @pytest.mark.parametrize("epi", ["residual", "swiglu", "bf16"])
 @pytest.mark.parametrize("MP", [64, 96, 128])
 def test_q4_one_pass_epilogues(gpu_device, epi, MP):
