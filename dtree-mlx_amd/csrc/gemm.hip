@@ -899,7 +899,6 @@ constexpr int kQ4mDepth = 2;   // weight groups in flight per wave
 constexpr int kQ4mMaxParts = 8;  // K parts per tile (remote partials of a pair fit one round of 8 loads)
 constexpr int kQ4mSpin = 2048;   // polls (about a microsecond each) before an owner leaves its pairs to the last arriver
 constexpr int kQ4mCtrInts = 32;  // counter words per tile: published, released, 16 pair claims (+ padding)
-constexpr int kQ4mXAhead = 1;  // activation steps in flight per thread (register sets)
 // Epilogue of the one-pass q4 kernel as the fused LM head (not a GEMM
 // epilogue of the C ABI): row scale, optional fp32 logits, and per row the
 // (largest logit, first index) of the tile as the workgroup's candidate.
@@ -910,7 +909,8 @@ constexpr int q4m_threads(int mb, int cw) { return 64 * cw * mb * (cw == 2 ? 2 :
 template <bool LO, int EPI, int MB, int CW>
 __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParams p) {
   using Sh = Q4mShape<LO, MB, CW>;
-  constexpr int KI = Sh::KI, NPL = Sh::NPL, MP = Sh::MP, D = kQ4mDepth, XA = kQ4mXAhead, NT = Sh::THREADS;
+  constexpr int KI = Sh::KI, NPL = Sh::NPL, MP = Sh::MP, D = kQ4mDepth, NT = Sh::THREADS;
+  static_assert(D == 2, "the loop's issue order assumes two weight groups in flight");
   constexpr int TF = Sh::TILE_FLOATS;
   static_assert(EPI != kEpiLmArgmax || NT == 8 * MP, "LM-head epilogue: 8 threads per row");
   __shared__ __align__(16) unsigned char lds[Sh::LDS_BYTES];
@@ -945,23 +945,22 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
   // i.e. bytes 16 * (piece % 256) of chunk q = piece / 256 = (K lane kk, row
   // block rq, plane pl). Groups past the part read zero (ranged loads) and
   // are never used.
-  // Step j's pieces live in register set j % XA until they are stored.
-  u32x4_t xpre[XA][Sh::LOADS];
-  auto x_issue = [&](int xs, int st) {
+  u32x4_t xpre[Sh::LOADS];
+  auto x_issue = [&](int st) {
 #pragma unroll
     for (int j = 0; j < Sh::LOADS; ++j) {
       const int piece = min(t + j * NT, Sh::PIECES - 1), q = piece >> 8, tq = piece & 255;
       const int kk = q / (MB * NPL), rq = (q / NPL) % MB, pl = q % NPL;
       const int kb = g0 + st * KI + kk;
       const unsigned off = kb < g1 ? (unsigned)(rq * nkb + kb) * 4096u + 16u * tq : kOob;
-      xpre[xs][j] = pl == 0 ? buf_ld(xrs, off) : buf_ld(xlrs, off);
+      xpre[j] = pl == 0 ? buf_ld(xrs, off) : buf_ld(xlrs, off);
     }
   };
-  auto x_store = [&](int xs, int buf) {
+  auto x_store = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < Sh::LOADS; ++j)
       if (Sh::LOADS * NT == Sh::PIECES || t + j * NT < Sh::PIECES)
-        *reinterpret_cast<u32x4_t*>(lds + buf * Sh::STAGE_BYTES + 16 * (t + j * NT)) = xpre[xs][j];
+        *reinterpret_cast<u32x4_t*>(lds + buf * Sh::STAGE_BYTES + 16 * (t + j * NT)) = xpre[j];
   };
   // Weight ring: group j of this wave is kb = g0 + kl + KI * j; two 32-column
   // halves (nb) of q4 words (1 KB each) and their (scale, bias) words.
@@ -1016,41 +1015,42 @@ __global__ __launch_bounds__(q4m_threads(MB, CW)) void q4m_gemm_kernel(GemmParam
     }
   };
 
-#pragma unroll
-  for (int a = 0; a < XA; ++a) x_issue(a, a);
-#pragma unroll
-  for (int s = 0; s < D; ++s) w_issue(s, s);
+  // Prologue in the loop's issue order (a step's activations, then a weight
+  // group), so the loads in flight at the loop's head are those of any
+  // later iteration: w(0), x(1), w(1).
+  x_issue(0);
+  w_issue(0, 0);
   ss_finish<MB>(p.ss_in, p.ss_tiles, p.inv_norm_dim, p.eps, ssv, rs, rs_scratch);
-  x_store(0, 0);
-  x_issue(0, XA);
-  __syncthreads();
-  // Step st: compute from LDS buffer st & 1, store step st + 1 (issued XA
-  // steps ago) into the other buffer, issue step st + 1 + XA's activations,
-  // then refill the weight slot with group st + D. A wave's loads return in
-  // issue order, so storing step st + 1 waits for every load issued before
-  // it; with the activations issued ahead of each step's weights that is the
-  // weights of group st + D - XA - 1 = st (D = XA + 1), which the step's
-  // compute needs anyway, issued D steps ago. (Weights issued before the
-  // activations made every step wait for the weights issued one step
-  // earlier, however deep the ring; D = 3 with XA = 2 measured no faster and
-  // spills at 128 rows.) U = the loop's unroll, a multiple of D and XA so
-  // slots and register sets are compile-time.
-  constexpr int U = D % XA == 0 ? D : D * XA;
-  for (int st0 = 0; st0 < nsteps; st0 += U) {
+  x_store(0);
+  x_issue(1);
 #pragma unroll
-    for (int s = 0; s < U; ++s) {
+  for (int s = 1; s < D; ++s) w_issue(s, s);
+  __syncthreads();
+  // Step st: compute from LDS buffer st & 1, store step st + 1's activations
+  // (issued a step ago) into the other buffer, issue step st + 2's, then
+  // refill the weight slot with group st + D. A wave's loads return in issue
+  // order: storing step st + 1 waits for the loads issued before it, i.e.
+  // up to the weights of group st + D - 2 = st (D = 2), which the step's
+  // compute needs anyway, issued two steps ago. Every step issues the same
+  // loads (ranged loads past the part return zero and are never used) so the
+  // loop body has one pattern of loads in flight; a step guarded as a whole
+  // made the compiler wait for every load (vmcnt(0)) inside the compute.
+  // (Weights issued before the activations made every step wait for the
+  // weights issued one step earlier; D = 3 with two activation steps in
+  // flight measured no faster and spills at 128 rows.)
+  for (int st0 = 0; st0 < nsteps; st0 += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
       const int st = st0 + s;
-      if (st < nsteps) {
-        if (cb_ok && g0 + st * KI + kl < g1) {
-          __builtin_amdgcn_sched_barrier(0);
-          compute(s % D, st & 1);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        x_store((s + 1) % XA, (st + 1) & 1);
-        x_issue((s + 1) % XA, st + 1 + XA);
-        w_issue(s % D, st + D);
-        __syncthreads();
+      if (cb_ok && g0 + st * KI + kl < g1) {
+        __builtin_amdgcn_sched_barrier(0);
+        compute(s, st & 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      x_store((st + 1) & 1);
+      x_issue(st + 2);
+      w_issue(s, st + D);
+      __syncthreads();
     }
   }
 
