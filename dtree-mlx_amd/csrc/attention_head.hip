@@ -1268,6 +1268,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_combine_kernel(AttnParams p)
   if (nchunks > p.max_chunks || L > 32 * NT || L < 1) return;  // the main kernel's guards
   const int nsplit = head_nsplit(D, npre, NT);
   if (nsplit <= 1 || 32 * rb >= L) return;
+  if (p.ll && nsplit <= kAttnLLSplits) return;  // the main kernel combined through the exchange
   const size_t stride = (size_t)32 * D + 64;
   const __amdgpu_buffer_rsrc_t prs =
       buf_rsrc(p.part, (unsigned)((size_t)p.Hq * NT * p.splits * stride * sizeof(float)));
@@ -1440,10 +1441,12 @@ int head_tree_attention(const DtreeAttnArgs* a, hipStream_t stream) {
   // when the last arriver alone would read more than 128 KB of partials.
   p.sep_combine = (size_t)p.splits * 32 * D * sizeof(float) > kSepCombineBytes;
   // Trees of up to 32 nodes whose splits fit the exchange slots combine
-  // through the flag exchange (the step's split count is checked again on
-  // the device); DTREE_ATTN_EXCHANGE=counter keeps the last-arriver combine.
+  // through the flag exchange. The step's split count decides on the device,
+  // so a grid sized for a long prefix (partials combined by the second launch)
+  // still takes the exchange at a short one, and the second launch then has
+  // nothing to do. DTREE_ATTN_EXCHANGE=counter keeps the last-arriver combine.
   const char* xe = std::getenv("DTREE_ATTN_EXCHANGE");
-  p.ll = ll_bytes > 0 && !p.sep_combine && !(xe && xe[0] == 'c');
+  p.ll = ll_bytes > 0 && !(xe && xe[0] == 'c');
   p.ll_epoch = reinterpret_cast<uint32_t*>(ws + kAttnWsHeader);
   p.ll_slots = reinterpret_cast<unsigned char*>(ws + kAttnWsHeader + attn_ll_epoch_bytes(a->num_heads));
   p.ll_bytes = (unsigned)(ll_bytes - attn_ll_epoch_bytes(a->num_heads));

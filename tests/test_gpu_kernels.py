@@ -450,13 +450,17 @@ def test_group_attention_give_up_is_reported(gpu_device, monkeypatch, P, max_pas
         assert int(ws[:4096].view(torch.int32).abs().sum()) == 0  # error word and counters at zero
 
 
-@pytest.mark.parametrize("P,max_past", [(300, 300), (512, 512), (1000, 1024), (1500, 1536), (1750, 1792)])
+@pytest.mark.parametrize("P,max_past", [(300, 300), (512, 512), (1000, 1024), (1500, 1536), (1750, 1792),
+                                        (1000, 4096)])
 def test_head_attention_flag_exchange_matches_counter_combine(gpu_device, monkeypatch, P, max_past):
     """The per-head kernel's flag exchange (2..8 splits; every split combines
     the output units u with u % splits == split from its partners' (value,
     flag) pairs) against the last-arriver combine (DTREE_ATTN_EXCHANGE=counter)
     and the oracle; the launch raises every head's epoch by exactly one
-    (launches in a row on one workspace: the give-up test below)."""
+    (launches in a row on one workspace: the give-up test below). The last
+    case's grid is sized for 4096 keys, whose partials would be combined by a
+    second launch: its 1000-key step still takes the exchange (five splits)
+    and the second launch finds nothing to do."""
     monkeypatch.setenv("DTREE_ATTN_KERNEL", "head")
     parents = random_tree(25, seed=P)
     Hq = 32
