@@ -441,13 +441,15 @@ def time_kernels35(eng, cfg, w, cache, st, P: int, L: int, reps: int, quant: str
 
 def gdn_recurrence_name(rows: int, keep: int) -> str:
     """GatedDeltaNet tree recurrence kernel (gdn.hip): the matrix form for up
-    to 32 rows (with the input prep fused when keep > 0; DTREE_GDN_KERNEL=reg
-    keeps the node-by-node kernels), else the depth-first kernel."""
+    to 32 rows (with the input prep fused when keep > 0) and in 32-node blocks
+    up to 96 rows; DTREE_GDN_KERNEL=reg keeps the node-by-node kernels, =dfs
+    the depth-first kernel past 32 rows."""
+    node_by_node = os.environ.get("DTREE_GDN_KERNEL") in ("reg", "dfs")
     if rows <= 32:
         if os.environ.get("DTREE_GDN_KERNEL") == "reg":
             return f"gdn_prep_reg_kernel<{keep}>" if keep else "gdn_tree_reg_kernel<32>"
         return f"gdn_tree_chunk_kernel<{keep}>"
-    return "gdn_tree_dfs_kernel"
+    return "gdn_tree_dfs_kernel" if node_by_node or rows > 96 else "gdn_tree_blocks_kernel"
 
 
 def attention_kernel_name(max_past: int, D: int, R: int, gated: bool, MP: int) -> str:

@@ -1333,6 +1333,221 @@ __global__ __launch_bounds__(kChunkThreads) void gdn_tree_chunk_kernel(GdnParams
 }
 
 
+// ---- matrix form in 32-node blocks (trees of 33-96 nodes) -----------------
+//
+// In node order (parents before children) I + L is block lower triangular
+// over 32-node blocks, so block b of Delta follows from the earlier blocks by
+// substitution, and Y needs the earlier blocks' Delta rows only:
+//   (I + L_bb) Delta_b = R_b - sum_{a < b} L_ba Delta_a,
+//   Y_b = diag(gamma_b) (S_0 Q_b^T)^T + U_bb Delta_b + sum_{a < b} U_ba Delta_a,
+// with L, U, R, gamma and D as in the 32-node form above. The diagonal block
+// is inverted by the same squaring, over the block's own ancestor depth; the
+// off-diagonal terms (a node's ancestors in earlier blocks) are VALU sums
+// over the finished Delta rows. A workgroup owns one value head and 16 value
+// rows, keeps the k rows of every node and the finished Delta rows in LDS and
+// stages one block's q rows at a time. Unlike the depth-first walk it has no
+// limit on nested branch points.
+constexpr int kBlkMax = 3;               // 32-node blocks
+constexpr int kBlkNodes = 32 * kBlkMax;  // 96 nodes
+
+__global__ __launch_bounds__(kChunkThreads) void gdn_tree_blocks_kernel(GdnParams p) {
+  constexpr int DK = 128, TM = 32, R = kChunkRows, LS = DK + 4, NM = kBlkNodes;
+  static_assert(kChunkThreads == TM * R, "one thread per (block node, value row)");
+  __shared__ __align__(16) float kall[NM][LS];  // k rows of every node
+  __shared__ __align__(16) float s0[R][LS];     // S_0 rows of this workgroup
+  // One block's q rows while its Gram products run, then the inverse's eight
+  // 32 x 32 matrices (X0, X0^T, X1, X1^T, P0, P0^T, P1, P1^T).
+  constexpr int kQb = TM * LS, kInv = 8 * TM * kMS;
+  __shared__ __align__(16) float big[kQb > kInv ? kQb : kInv];
+  __shared__ __align__(16) float um[TM][kMS];            // U_bb
+  __shared__ float gkk[TM][TM + 1], gqk[TM][TM + 1];     // k_t . k_a, q_t . k_a within the block
+  __shared__ float gko[TM][2 * TM + 1], gqo[TM][2 * TM + 1];  // the same against earlier blocks
+  __shared__ float sk[TM][R + 1], sq[TM][R + 1];         // S_0 k_t, S_0 q_t per value row
+  __shared__ float dm[TM][NM + 1];                       // D[t][a] for the block's nodes t
+  __shared__ float dl[NM][R + 1];                        // Delta rows of finished blocks
+  __shared__ float rhs[TM][R + 1], yb[TM][R + 1];
+  __shared__ float gam[NM], gg[NM], bb[NM];
+  __shared__ int par[NM], s_depth;
+  float(*qb)[LS] = reinterpret_cast<float(*)[LS]>(big);
+  const int T = p.T_dev ? min(max(*p.T_dev, 0), min(p.T, NM)) : min(p.T, NM);
+  const int nblk = p.Dv / R;
+  const int h = blockIdx.x / nblk, r0 = (blockIdx.x % nblk) * R;
+  const int hk = h / (p.Hv / p.Hk);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tr = tid >> 4, rr = tid & 15;  // (block node, value row) of this thread
+
+  // ---- k rows of every node, S_0 rows, g / beta / parents ----
+  {
+    constexpr int NK = NM * (DK / 4) / kChunkThreads;  // float4 per thread
+    f32x4_t kv[NK], sv;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int e = tid + kChunkThreads * i, t = e >> 5, c = e & 31;
+      kv[i] = t < T ? *reinterpret_cast<const f32x4_t*>(p.k + ((size_t)t * p.Hk + hk) * DK + 4 * c)
+                    : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    sv = *reinterpret_cast<const f32x4_t*>(p.state + ((size_t)h * p.Dv + r0 + (tid >> 5)) * DK + 4 * (tid & 31));
+    if (tid < NM) {
+      const bool live = tid < T;
+      gg[tid] = live ? p.g[(size_t)tid * p.Hv + h] : 0.f;
+      bb[tid] = live ? p.beta[(size_t)tid * p.Hv + h] : 0.f;
+      par[tid] = live ? valid_parent(p.parents[tid], tid) : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int e = tid + kChunkThreads * i, t = e >> 5, c = e & 31;
+      *reinterpret_cast<f32x4_t*>(&kall[t][4 * c]) = kv[i];
+    }
+    *reinterpret_cast<f32x4_t*>(&s0[tid >> 5][4 * (tid & 31)]) = sv;
+  }
+  auto Xm = [&](int i) { return Mat32{big + (2 * i) * TM * kMS, big + (2 * i + 1) * TM * kMS}; };
+  auto Pmat = [&](int i) { return Mat32{big + (4 + 2 * i) * TM * kMS, big + (5 + 2 * i) * TM * kMS}; };
+
+  const int B = (T + TM - 1) / TM;
+  // q rows of block b (in registers a block ahead) and v of this thread's
+  // (node, value row)
+  f32x4_t qv[2];
+  float vt = 0.f;
+  auto q_issue = [&](int n0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + kChunkThreads * i, t = e >> 5, c = e & 31;
+      qv[i] = n0 + t < T ? *reinterpret_cast<const f32x4_t*>(p.q + ((size_t)(n0 + t) * p.Hk + hk) * DK + 4 * c)
+                         : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    vt = n0 + tr < T ? p.v[((size_t)(n0 + tr) * p.Hv + h) * p.Dv + r0 + rr] : 0.f;
+  };
+  q_issue(0);
+  for (int b = 0; b < B; ++b) {
+    const int n0 = TM * b;  // first node of the block
+    const float vb = vt;
+    // ---- this block's q rows; D[t][.] cleared; the next block's q issued ----
+    {
+      for (int e = tid; e < TM * (NM + 1); e += kChunkThreads) dm[e / (NM + 1)][e % (NM + 1)] = 0.f;
+      if (tid == 0) s_depth = 0;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + kChunkThreads * i, t = e >> 5, c = e & 31;
+        *reinterpret_cast<f32x4_t*>(&qb[t][4 * c]) = qv[i];
+      }
+      if (b + 1 < B) q_issue(n0 + TM);
+    }
+    __syncthreads();
+    // ---- Gram tiles and S_0 products on MFMA (wave w: jobs w, w + 8, ...);
+    // the path decays of the block's nodes by the last wave's lanes ----
+    {
+      const int njobs = 12 + 8 * b;
+      for (int job = wave; job < njobs; job += kChunkThreads / 64) {
+        const float *A, *Bt;
+        int kind, th, ah;
+        if (job < 8) {  // 0-3 k.k, 4-7 q.k within the block
+          kind = job >> 2; th = (job >> 1) & 1; ah = job & 1;
+          A = kind ? &qb[16 * th][0] : &kall[n0 + 16 * th][0];
+          Bt = &kall[n0 + 16 * ah][0];
+        } else if (job < 12) {  // 8-9 S_0 k, 10-11 S_0 q
+          kind = job < 10 ? 2 : 3; th = job & 1; ah = 0;
+          A = &s0[0][0];
+          Bt = kind == 2 ? &kall[n0 + 16 * th][0] : &qb[16 * th][0];
+        } else {  // k.k and q.k against the earlier blocks' nodes
+          const int idx = (job - 12) % (4 * b);
+          kind = job - 12 < 4 * b ? 4 : 5; th = idx & 1; ah = idx >> 1;
+          A = kind == 5 ? &qb[16 * th][0] : &kall[n0 + 16 * th][0];
+          Bt = &kall[16 * ah][0];
+        }
+        const f32x4_t d = tile16_dot<LS, DK / 16>(A, Bt, lane, f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * (lane >> 4) + i, n = lane & 15;
+          if (kind == 0) gkk[16 * th + m][16 * ah + n] = d[i];
+          else if (kind == 1) gqk[16 * th + m][16 * ah + n] = d[i];
+          else if (kind == 2) sk[16 * th + n][m] = d[i];
+          else if (kind == 3) sq[16 * th + n][m] = d[i];
+          else if (kind == 4) gko[16 * th + m][16 * ah + n] = d[i];
+          else gqo[16 * th + m][16 * ah + n] = d[i];
+        }
+      }
+      if (wave == kChunkThreads / 64 - 1 && lane < TM) {
+        const int t = n0 + lane;
+        if (t < T) {
+          float cum = gg[t];
+          int a = par[t], inblk = 0;
+          for (int steps = 0; steps < NM && a >= 0; ++steps) {  // a < t strictly decreasing
+            dm[lane][a] = cum;
+            inblk += a >= n0;
+            cum *= gg[a];
+            a = par[a];
+          }
+          gam[t] = cum;
+          atomicMax(&s_depth, inblk);
+        } else {
+          gam[t] = 0.f;
+        }
+      }
+    }
+    __syncthreads();
+    // ---- L_bb, I - L_bb, U_bb; the right-hand side and Y's known terms ----
+    for (int e = tid; e < TM * TM; e += kChunkThreads) {
+      const int t = e >> 5, a = e & 31;
+      const bool live = n0 + t < T;
+      const float l = live && a < t ? bb[n0 + t] * dm[t][n0 + a] * gkk[t][a] : 0.f;
+      Xm(0).a[t * kMS + a] = l;
+      Xm(0).t[a * kMS + t] = l;
+      const float p0 = (t == a ? 1.f : 0.f) - l;
+      Pmat(0).a[t * kMS + a] = p0;
+      Pmat(0).t[a * kMS + t] = p0;
+      um[t][a] = !live ? 0.f : a < t ? dm[t][n0 + a] * gqk[t][a] : (a == t ? gqk[t][t] : 0.f);
+    }
+    {
+      const int t = n0 + tr;
+      float rv = 0.f, yv = 0.f;
+      if (t < T) {
+        float off_r = 0.f;
+        for (int a = 0; a < n0; ++a) {
+          const float w = dm[tr][a];
+          if (w != 0.f) {
+            off_r += w * gko[tr][a] * dl[a][rr];
+            yv += w * gqo[tr][a] * dl[a][rr];
+          }
+        }
+        rv = bb[t] * (vb - gam[t] * sk[tr][rr]) - bb[t] * off_r;
+        yv += gam[t] * sq[tr][rr];
+      }
+      rhs[tr][rr] = rv;
+      yb[tr][rr] = yv;
+    }
+    __syncthreads();
+    // ---- (I + L_bb)^-1 = (I - L)(I + L^2)(I + L^4) ... over the block's depth ----
+    const int d = s_depth;
+    int cur = 0;
+    for (int pw = 1; pw < TM && (1 << pw) <= d; ++pw) {
+      const Mat32 src = Xm((pw - 1) & 1), dst = Xm(pw & 1);
+      if (wave < 4) mat32_mul(src, src, nullptr, dst, wave, lane);
+      __syncthreads();
+      if (wave < 4) mat32_mul(Pmat(cur), dst, Pmat(cur).a, Pmat(cur ^ 1), wave, lane);
+      cur ^= 1;
+      __syncthreads();
+    }
+    // ---- Delta_b, then Y_b ----
+    {
+      const float* Pa = Pmat(cur).a;
+      float dv = 0.f;
+#pragma unroll 8
+      for (int a = 0; a < TM; ++a) dv += Pa[tr * kMS + a] * rhs[a][rr];
+      dl[n0 + tr][rr] = n0 + tr < T ? dv : 0.f;
+    }
+    __syncthreads();
+    {
+      const int t = n0 + tr;
+      float yv = yb[tr][rr];
+#pragma unroll 8
+      for (int a = 0; a < TM; ++a) yv += um[tr][a] * dl[n0 + a][rr];
+      if (t < T) p.y[((size_t)t * p.Hv + h) * p.Dv + r0 + rr] = yv;
+    }
+    __syncthreads();  // big, dm and the block's scratch are rewritten next
+  }
+}
+
+
 // Gated RMSNorm of the recurrence output per (node, value head)
 // (RMSNormGated, qwen35_tree.py:322): o = rms_norm(y) * w * silu(z), written as
 // the split bf16 pair [hi, lo] the out_proj GEMM reads. 16 threads per
@@ -1509,6 +1724,17 @@ static bool use_chunk_recurrence(int rows, int dk, int dv) {
   return !reg && rows <= 32 && dk == 128 && dv % kChunkRows == 0;
 }
 
+// Matrix form in 32-node blocks (gdn_tree_blocks_kernel) for 33-96 nodes;
+// DTREE_GDN_KERNEL=reg or dfs keeps the depth-first walk (timing and
+// cross-checks).
+static bool use_block_recurrence(int rows, int dk, int dv) {
+  static const bool node_by_node = [] {
+    const char* e = std::getenv("DTREE_GDN_KERNEL");
+    return e && (std::string(e) == "reg" || std::string(e) == "dfs");
+  }();
+  return !node_by_node && rows > 32 && rows <= kBlkNodes && dk == 128 && dv % kChunkRows == 0;
+}
+
 extern "C" int dtree_gdn_tree_recurrence(const float* q, const float* k, const float* v, const float* g,
                                          const float* beta, const float* state, const int32_t* parents,
                                          int32_t num_nodes, int32_t num_k_heads, int32_t num_v_heads,
@@ -1529,6 +1755,11 @@ extern "C" int dtree_gdn_tree_recurrence(const float* q, const float* k, const f
   p.y = y; p.states = states;
   if (!states && use_chunk_recurrence(num_nodes, head_k_dim, head_v_dim)) {
     gdn_tree_chunk_kernel<0><<<num_v_heads * (head_v_dim / kChunkRows), kChunkThreads, 0, stream>>>(p, PrepParams{});
+    DTREE_LAUNCH_CHECK("gdn_tree_recurrence launch");
+    return DTREE_OK;
+  }
+  if (!states && use_block_recurrence(num_nodes, head_k_dim, head_v_dim)) {
+    gdn_tree_blocks_kernel<<<num_v_heads * (head_v_dim / kChunkRows), kChunkThreads, 0, stream>>>(p);
     DTREE_LAUNCH_CHECK("gdn_tree_recurrence launch");
     return DTREE_OK;
   }
@@ -1656,6 +1887,9 @@ extern "C" int dtree_gdn_layer_recurrence(const DtreeGdnArgs* a, hipStream_t str
   if (use_chunk_recurrence(a->rows_padded, a->head_k_dim, a->head_v_dim)) {
     p.T = min(a->rows_padded, 32);
     gdn_tree_chunk_kernel<0><<<a->num_v_heads * (a->head_v_dim / kChunkRows), kChunkThreads, 0, stream>>>(p, PrepParams{});
+  } else if (use_block_recurrence(a->rows_padded, a->head_k_dim, a->head_v_dim)) {
+    p.T = min(a->rows_padded, kBlkNodes);
+    gdn_tree_blocks_kernel<<<a->num_v_heads * (a->head_v_dim / kChunkRows), kChunkThreads, 0, stream>>>(p);
   } else if (a->rows_padded <= 32 && a->head_v_dim % 8 == 0) {
     p.T = min(a->rows_padded, 32);
     gdn_tree_reg_kernel<32><<<a->num_v_heads * (a->head_v_dim / 8), 256, 0, stream>>>(p);

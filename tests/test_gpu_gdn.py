@@ -107,16 +107,13 @@ def test_layer_shapes_conv_and_recurrence(T, seed):
     ry, rs = gdn.tree_gated_delta(q, k, v, g, beta, state, parents)
     assert np.abs(y - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
     assert np.abs(st - rs).max() <= 1e-5 * max(1.0, np.abs(rs).max())
-    # lazy mode (no node states / windows written) gives the same outputs; up
-    # to 32 nodes it runs the matrix form (gdn_tree_chunk_kernel), which sums
-    # in another order
+    # lazy mode (no node states / windows written) gives the same outputs; it
+    # runs the matrix form (gdn_tree_chunk_kernel up to 32 nodes,
+    # gdn_tree_blocks_kernel up to 96), which sums in another order
     y2, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
     out2, _ = _conv(x, base, w, parents, "cuda", want_windows=False)
     assert np.array_equal(out, out2)
-    if T <= 32:
-        assert np.abs(y2 - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
-    else:
-        assert np.array_equal(y, y2)
+    assert np.abs(y2 - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
 
 
 def _star(T):
@@ -182,6 +179,38 @@ def test_recurrence_depth_first_trees(parents):
     ry, rs = gdn.tree_gated_delta(q, k, v, g, beta, state, parents)
     assert np.abs(y - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
     assert np.abs(st - rs).max() <= 1e-5 * max(1.0, np.abs(rs).max())
+    # without node states the same trees run the blocked matrix form
+    y2, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
+    assert np.abs(y2 - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
+
+
+@pytest.mark.parametrize("parents,scale", [
+    (random_tree(65, 21), "model"), (random_tree(96, 22), "model"), (list(range(-1, 95)), "model"),
+    (_star(96), "model"), (_caterpillar(32), "model"), (_caterpillar(47), "model"),
+    (_chain_tree(64, 40, 23), "model"), (random_tree(33, 24), "model"), (random_tree(80, 25), "strong_decay"),
+    (random_tree(70, 26), "no_decay"), (random_tree(65, 27), "signed"),
+], ids=["rand65", "rand96", "chain96", "star96", "caterpillar32", "caterpillar47", "chain40+23", "rand33",
+        "strong_decay", "no_decay", "signed_g_beta"])
+def test_blocked_matrix_form_recurrence(parents, scale):
+    """Trees of 33-96 nodes without node states run the matrix form in
+    32-node blocks (gdn_tree_blocks_kernel: each block's diagonal inverted by
+    squaring, earlier blocks entering through their finished Delta rows).
+    Against the node-by-node float64 oracle: random trees, a 96-deep chain
+    (31 in-block ancestors in every block), a 95-leaf star, caterpillars
+    past the depth-first walk's 31 nested branch points (no limit here),
+    vanishing, unit and signed decays."""
+    T = len(parents)
+    q, k, v, g, beta, state = _layer_inputs(T, 700 + T)
+    if scale == "strong_decay":
+        g = np.where(np.arange(T)[:, None] % 3 == 1, 1e-30, g)
+    elif scale == "no_decay":
+        g = np.ones_like(g)
+    elif scale == "signed":
+        r = np.random.default_rng(9)
+        g, beta = r.normal(size=g.shape) * 0.9, r.normal(size=beta.shape)
+    y, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
+    ry, _ = gdn.tree_gated_delta(q, k, v, g, beta, state, parents)
+    assert np.abs(y - ry).max() <= 1e-5 * max(1.0, np.abs(ry).max())
 
 
 def test_recurrence_forest_of_roots():
@@ -202,14 +231,15 @@ def test_recurrence_forest_of_roots():
 
 def test_recurrence_past_the_stack_writes_nan():
     """32 nested branching nodes (a 65-node caterpillar) do not fit the
-    32-slot stack: the kernel, called on such a tree anyway, writes NaN,
-    never a silently wrong value (the host check dtree_gdn_tree_check rejects
-    the tree before launch: tests/test_native_abi.py, and the hybrid engine
+    depth-first walk's 32-slot stack (the walk runs when node states are
+    asked for): the kernel, called on such a tree anyway, writes NaN, never a
+    silently wrong value (the host check dtree_gdn_tree_check rejects the
+    tree before launch: tests/test_native_abi.py, and the hybrid engine
     below)."""
     parents = _caterpillar(32)
     T = len(parents)
     q, k, v, g, beta, state = _layer_inputs(T, 13)
-    y, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=False)
+    y, _ = _delta(q, k, v, g, beta, state, parents, "cuda", want_states=True)
     assert np.isnan(y).all()
 
 
