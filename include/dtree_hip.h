@@ -175,7 +175,12 @@ size_t dtree_gemm_args_bytes(void);
 size_t dtree_attn_args_bytes(void);
 
 /* Workspace for dtree_gemm_bf16 (partials + tile counters). Counters must be
- * zero before the first call; every call leaves them zero again. */
+ * zero before the first call; every call leaves them zero again. Calls that
+ * share a workspace must not overlap (one stream, or ordered by events).
+ * With q4 weights over 64-128 rows the K parts of a tile wait for each other
+ * at a bounded wait (~2 ms) to combine their partials in a distributed way;
+ * a part that gives up leaves its share to the last part to arrive, so the
+ * result never depends on it. */
 size_t dtree_gemm_workspace_bytes(int rows_padded, int n, int k, int split_k);
 int dtree_gemm_bf16(const DtreeGemmArgs* args, hipStream_t stream);
 
