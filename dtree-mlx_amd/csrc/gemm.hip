@@ -1988,15 +1988,22 @@ __device__ __forceinline__ void long_gemm_body(const GemmParams& p) {
       for (int r = 0; r < 16; ++r)
         red[(64 * wr + 32 * rb + acc_row(r, h)) * kLongCols + 64 * wc + 32 * j + c] = acc[rb][j][r];
   __syncthreads();
-  // the epilogue of rows R .. R + 127: outputs shifted by R rows (32-row
-  // blocks are contiguous in both layouts; statistics are per 32-row block)
-  GemmParams q = p;
-  if (q.out_f32) q.out_f32 += (size_t)R * q.ld_out_f32;
-  if (q.out_bf16) q.out_bf16 += (size_t)R * q.ld_out_bf16;
-  if (q.out_lo) q.out_lo += (size_t)R * q.ld_out_bf16;
-  if (q.hidden_out) q.hidden_out += (size_t)R * q.ld_hidden;
-  if (q.ss_out) q.ss_out += (size_t)(R >> 5) * (q.n >> 5) * 32;
-  tile_epilogue<kLongRows, kLongCols, EPI>(q, red, rs, nt);
+  // The epilogue of rows R .. R + 127, one 32-row block at a time (outputs
+  // shifted by the block's first row: 32-row blocks are contiguous in both
+  // layouts; statistics are per 32-row block). In one 128-row piece the
+  // residual epilogue held 64 preloaded values per thread and took the kernel
+  // to 320 VGPRs, one workgroup per CU for the whole K loop.
+#pragma unroll 1
+  for (int r2 = 0; r2 < kLongRows / 32; ++r2) {
+    const int R2 = R + 32 * r2;
+    GemmParams q = p;
+    if (q.out_f32) q.out_f32 += (size_t)R2 * q.ld_out_f32;
+    if (q.out_bf16) q.out_bf16 += (size_t)R2 * q.ld_out_bf16;
+    if (q.out_lo) q.out_lo += (size_t)R2 * q.ld_out_bf16;
+    if (q.hidden_out) q.hidden_out += (size_t)R2 * q.ld_hidden;
+    if (q.ss_out) q.ss_out += (size_t)(R2 >> 5) * (q.n >> 5) * 32;
+    tile_epilogue<32, kLongCols, EPI>(q, red + 32 * r2 * kLongCols, rs + 32 * r2, nt);
+  }
 }
 
 template <bool LO, int EPI, bool H = false>
