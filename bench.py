@@ -34,6 +34,10 @@ for _p in (ROOT, ROOT / "dtree-mlx_amd"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBPS = 8000.0
+# Timed and warmup steps of every extra workload line: the headline's
+# defaults, since a 30-step run after 5 warmup steps reads 2-4 % slower
+# than a 100-step run of the same step in the same process.
+CONFIG_STEPS, CONFIG_WARMUP = 100, 10
 
 
 def log(*a):
@@ -486,9 +490,9 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows:
     three when that fills at least an eighth more of the CUs.
     32 rows, bf16 or q4: three workgroups per 32-column tile (one per part of
     K) at K >= 4096 and N % 256 == 0 when 3 N / 32 fit the CUs, two at K = 4096
-    when 2 N / 32 do; else one per tile at K <= 4096 and N / 32 <= CUs; else
-    stream-K (q4: two workgroups per CU when there are at least 20 64 x 64
-    units per CU)."""
+    when 2 N / 32 do; else one per tile at K <= 4096 and N / 32 <= CUs (q4:
+    at K <= 4096 whatever N); else stream-K (q4: two workgroups per CU when
+    there are at least 20 64 x 64 units per CU)."""
     L = "true" if lo and not h16 else "false"
     h = ", true" if h16 else ""
     if quant == "q4" and rows > 32:
@@ -509,7 +513,7 @@ def gemm_kernel_name(n: int, k: int, epi: int, quant: str, cus: int = 256, rows:
             return f"{dp}<{L}, {epi}, 3{h}>"
         if k == 4096 and (n // 32) * 2 <= cus:
             return f"{dp}<{L}, {epi}, 2{h}>"
-    if k <= 4096 and n // 32 <= cus:
+    if k <= 4096 and (n // 32 <= cus or quant == "q4"):
         return f"{dp}<{L}, {epi}, 1{h}>"
     if quant == "q4" and (n // 64) * (k // 64) >= 20 * cus:
         return f"sk2_gemm_kernel<{L}, {epi}>"
@@ -995,20 +999,21 @@ def main():
         configs["attention_layer_p512"] = attention_layer_bench(P=512)
         log(f"[bench] attention layer P=512: {configs['attention_layer_p512']}")
         # the same step on an engine sized for the generator's default max_past
-        rr = run_workload("qwen3-4b", "bf16", 1024, 24, steps=30, warmup=5, max_past=4096, kernel_reps=54)
+        rr = run_workload("qwen3-4b", "bf16", 1024, 24, steps=CONFIG_STEPS, warmup=CONFIG_WARMUP, max_past=4096,
+                          kernel_reps=54)
         configs["qwen3_4b_bf16_p1024_max_past_4096"] = {
             "workload": "Qwen3-4B bf16 tree-verify step, prefix 1024, 25-node tree, engine and cache sized for "
                         "max_past 4096 (DFlashGenerator's default)",
             "ms_per_step": round(rr["ms"], 4), "steps_per_s": round(rr["steps_per_s"], 3),
             "attention": {k: (round(v, 2) if isinstance(v, float) else v)
-                          for k, v in rr["kernels"]["attention"].items()}, "steps": 30}
+                          for k, v in rr["kernels"]["attention"].items()}, "steps": CONFIG_STEPS}
         log(f"[bench] max_past 4096: {configs['qwen3_4b_bf16_p1024_max_past_4096']}")
         configs["dflash_block_verify_qwen3_4b_p1024"] = dflash_block_bench()
         log(f"[bench] dflash block verify: {configs['dflash_block_verify_qwen3_4b_p1024']}")
         for key, (m, q, pp, bb) in {"qwen3_4b_q4_p1024": ("qwen3-4b", "q4", 1024, 24),
                                     "qwen35_4b_bf16_p2048": ("qwen35-4b", "bf16", 2048, 24),
                                     "qwen35_9b_q4_p8192_budget64": ("qwen35-9b", "q4", 8192, 64)}.items():
-            rr = run_workload(m, q, pp, bb, steps=30, warmup=5, with_prefill=True)
+            rr = run_workload(m, q, pp, bb, steps=CONFIG_STEPS, warmup=CONFIG_WARMUP, with_prefill=True)
             configs["prefill_" + key.replace("_budget64", "")] = rr["prefill"]
             configs[key] = {"workload": f"{MODEL_NAMES[m]} {'bf16' if q == 'bf16' else 'q4 group-64'} tree-verify "
                                         f"step, prefix {pp}, {rr['L']}-node tree",
@@ -1016,7 +1021,7 @@ def main():
                             "hbm_gbps": round(rr["gbps"], 1), "hbm_frac_of_peak": round(rr["gbps"] / HBM_PEAK_GBPS, 4),
                             "algorithmic_bytes_per_step": rr["algorithmic_bytes"],
                             "tokens_per_s": round(rr["steps_per_s"] * rr["mean_accepted"], 2),
-                            "mean_accepted": rr["mean_accepted"], "accepted": rr["accepted"], "steps": 30}
+                            "mean_accepted": rr["mean_accepted"], "accepted": rr["accepted"], "steps": CONFIG_STEPS}
         configs["lazy_hop_qwen35_4b_q4_p2048"] = lazy_hop_bench()
         log(f"[bench] lazy hop: {configs['lazy_hop_qwen35_4b_q4_p2048']}")
         log(f"[bench] other workloads {time.time() - t0:.1f}s")

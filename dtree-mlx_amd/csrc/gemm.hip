@@ -2223,13 +2223,16 @@ extern "C" int dtree_gemm_bf16(const DtreeGemmArgs* a, hipStream_t stream) {
   //   tile) or long K on narrow N.
   // q4 weights follow the same rule (dpq_gemm_kernel), measured against the
   // stream-K q4 kernels: QKV (N 6144, K 2560, high plane only) 8.0 vs 12.1 us,
-  // o_proj 10.6 vs 15.3, down_proj 15.0 vs 18.4; gate/up (N 19456: 608 tiles)
-  // keeps the two-per-CU stream-K kernel (21.4 vs 23.5 us one per tile).
+  // o_proj 10.6 vs 15.3, down_proj 15.0 vs 18.4; and at K <= 4096 they take
+  // one workgroup per tile also past the CU count: the Qwen3-4B q4 step with
+  // gate/up (N 19456: 608 tiles) one per tile runs 2.18 ms, 2.31 ms with the
+  // two-per-CU stream-K kernel (bf16 weights keep stream-K there: 2.88 vs
+  // 2.91 ms for the bf16 step).
   const int auto_cus = device_cus();
   const bool k_auto = a->split_k == 0 && tiled && a->rows_padded == 32;
   const bool pairs_auto = k_auto && a->k >= 4096 && a->n % 256 == 0 &&
                           ((a->n / 32) * 3 <= auto_cus || (a->k == 4096 && (a->n / 32) * 2 <= auto_cus));
-  const bool dp_auto = k_auto && !pairs_auto && a->k <= 4096 && a->n / 32 <= auto_cus;
+  const bool dp_auto = k_auto && !pairs_auto && a->k <= 4096 && (a->n / 32 <= auto_cus || q4);
   if (tiled && a->rows_padded == 32 && (a->split_k == -3 || a->split_k == -4 || pairs_auto)) {
     // Two (-3) or three (-4) workgroups per tile, one per part of K (see
     // dp_gemm_kernel).

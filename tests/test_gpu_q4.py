@@ -131,8 +131,8 @@ def test_q4_gemm_residual_and_swiglu(gpu_device):
 def _q4_layer_case(epi, g, dev):
     """Qwen3-4B layer shapes: down_proj with the residual epilogue (N 2560,
     K 9728; automatically three per-tile workgroups, one per part of K) and
-    gate/up with SwiGLU (N 19456, K 2560; automatically the two-per-CU
-    stream-K kernel, at least 20 units per CU)."""
+    gate/up with SwiGLU (N 19456, K 2560; automatically one workgroup per
+    tile, 608 of them; split_k -2 forces the two-per-CU stream-K kernel)."""
     L = 25
     if epi == N.EPI_RESIDUAL:
         n, k = 2560, 9728
@@ -182,10 +182,11 @@ def _run_q4_layer(epi, n, k, wt, sb, xt, xlt, g_seed, dev, split_k=0):
 
 
 # split_k 0: the automatic schedule (residual: dpq_gemm_kernel, three parts;
-# SwiGLU: sk2_gemm_kernel); -2 forces stream-K (sk2_gemm_kernel at these unit
-# counts); -1 / -4 force the per-tile q4 kernel with one / three parts of K.
+# SwiGLU: dpq_gemm_kernel, one workgroup per tile); -2 forces stream-K
+# (sk2_gemm_kernel at these unit counts); -1 / -4 force the per-tile q4 kernel
+# with one / three parts of K.
 @pytest.mark.parametrize("epi,split_k", [(N.EPI_RESIDUAL, 0), (N.EPI_RESIDUAL, -2), (N.EPI_RESIDUAL, -1),
-                                         (N.EPI_SWIGLU, 0), (N.EPI_SWIGLU, -1), (N.EPI_SWIGLU, -4)])
+                                         (N.EPI_SWIGLU, 0), (N.EPI_SWIGLU, -2), (N.EPI_SWIGLU, -4)])
 def test_q4_layer_shapes(gpu_device, epi, split_k):
     g = np.random.default_rng(91 + epi)
     n, k, wt, sb, xt, xlt, xin, ref_w = _q4_layer_case(epi, g, gpu_device)
