@@ -764,7 +764,7 @@ def run_workload(model: str, quant: str, P: int, budget: int, steps: int, warmup
     return out
 
 
-def lazy_hop_bench(P: int = 2048, hops: int = 40, warmup: int = 5) -> dict:
+def lazy_hop_bench(P: int = 2048, hops: int = CONFIG_STEPS, warmup: int = CONFIG_WARMUP) -> dict:
     """The reference's default Qwen3.5 verifier (lazy_follow_tree_exact,
     dtree_runtime.py:211-290) walks the tree one token at a time; one hop is
     text_model.forward_dflash over one token (every layer, committing the
