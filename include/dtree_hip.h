@@ -123,12 +123,13 @@ typedef struct DtreeGemmArgs {
                              (with x_layout TILED_F16) or DTREE_W_Q4G64     */
   int32_t n, k;           /* k % 64 == 0; n % 64 == 0 (% 32 above 64 rows) */
   int32_t epilogue;       /* DTREE_EPI_*                                   */
-  int32_t split_k;        /* >= 1 split-K; 0 = automatic; tiled 32 rows only:
-                             -1 one workgroup per 32-column tile (bf16),
+  int32_t split_k;        /* >= 1 split-K (bf16); 0 = automatic; tiled 32
+                             rows only, bf16 or Q4G64:
+                             -1 one workgroup per 32-column tile,
                              -2 stream-K schedule,
                              -3 / -4 two / three workgroups per 32-column
-                                tile, one per part of K (bf16,
-                                n % 256 == 0, k >= 64 * parts)             */
+                                tile, one per part of K
+                                (n % 256 == 0, k >= 64 * parts)            */
   const float* ss_in;     /* [rows_padded/32][ss_tiles][32] or NULL        */
   int32_t ss_tiles;
   int32_t norm_dim;       /* divisor of the row mean square                */
